@@ -1,0 +1,247 @@
+/*
+ * runit_hip.h — C ABI of the MI355X (gfx950) quantized-GEMV decode path.
+ *
+ * This library replaces the Metal kernel runtime of RunIT's `crates/kernels`
+ * crate for the decode hot path.  Every `rt_<name>` kernel entry point takes
+ * the same arguments, in the same order and with the same meaning, as the
+ * reference's `dispatch::<name>(ctx, ...)` Rust function; Metal `&Buffer`
+ * arguments become device pointers and `u32` dimensions stay `uint32_t`.
+ *
+ * Execution model (mirrors crates/kernels/src/context.rs:248-296):
+ *   - every kernel call only ENQUEUES work on the context's HIP stream
+ *     (the reference encodes onto one open command buffer);
+ *   - rt_flush() waits for all enqueued work (the reference's `flush()`).
+ *   - A context is not thread-safe (the reference's MetalContext is !Sync,
+ *     context.rs:158); use one context per host thread.
+ *
+ * Weights are raw GGUF block streams, row-major, each row = K/blk blocks:
+ *   Q8_0 34 B / 32 el, Q4_0 18 B / 32 el, Q4_K 144 B / 256 el,
+ *   Q6_K 210 B / 256 el  (crates/gguf/src/types.rs:158-191),
+ * decoded with the reference's own layouts (crates/engine/src/forward.rs).
+ *
+ * Pointer rules: every pointer must be a device pointer (rt_malloc or any
+ * hipMalloc'd memory).  f32 activation vectors must be 16-byte aligned and
+ * f16 ones 8-byte aligned (the reference reads x as float4 / half4).
+ * `output` may alias `residual` (forward.rs:1619,1702 pass the same buffer).
+ *
+ * Status codes map one-to-one onto crates/kernels/src/error.rs:4-21.
+ */
+#ifndef RUNIT_HIP_H
+#define RUNIT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* KernelError variants (crates/kernels/src/error.rs:4-21). */
+typedef enum rt_status {
+    RT_OK = 0,
+    RT_ERR_NO_DEVICE = 1,          /* KernelError::NoDevice */
+    RT_ERR_LIBRARY_LOAD = 2,       /* KernelError::LibraryLoad { path, reason } */
+    RT_ERR_PIPELINE_NOT_FOUND = 3, /* KernelError::PipelineNotFound(name) */
+    RT_ERR_PIPELINE_CREATE = 4,    /* KernelError::PipelineCreate { name, reason } */
+    RT_ERR_DISPATCH = 5,           /* KernelError::Dispatch(msg) */
+    RT_ERR_BUFFER_SIZE = 6         /* KernelError::BufferSize { expected, actual } */
+} rt_status;
+
+typedef struct rt_ctx rt_ctx;
+
+/* ───────────────────────── context / runtime ───────────────────────── */
+
+/* MetalContext::new() (context.rs:163-205): selects device 0, loads the
+ * gfx950 code object at `code_object_path` (NULL → runit_kernels.hsaco next
+ * to this library), resolves every kernel, creates one stream. */
+int rt_ctx_create(rt_ctx** out, const char* code_object_path);
+/* Drop for MetalContext (context.rs:299-304): flushes, then releases. */
+void rt_ctx_destroy(rt_ctx* ctx);
+/* MetalContext::flush() (context.rs:289-296): waits for all enqueued work. */
+int rt_flush(rt_ctx* ctx);
+/* Human-readable text of the last error on this context (KernelError's
+ * Display string); never NULL. */
+const char* rt_last_error(const rt_ctx* ctx);
+/* Text for an error raised before a context exists (rt_ctx_create). */
+const char* rt_global_last_error(void);
+/* Number of compute units of the context's device. */
+int rt_device_cu_count(const rt_ctx* ctx);
+/* Resolves a kernel by name, like the reference's PSO lookup
+ * (context.rs:207-212): RT_ERR_PIPELINE_NOT_FOUND if absent. */
+int rt_has_kernel(rt_ctx* ctx, const char* name);
+
+/* MetalContext::new_buffer (context.rs:215-220) — device memory.  MI355X
+ * memory is not CPU-visible here, so contents move with upload/download. */
+int rt_malloc(rt_ctx* ctx, size_t bytes, void** out);
+int rt_free(rt_ctx* ctx, void* ptr);
+/* Synchronous on the context stream (orders after enqueued kernels). */
+int rt_upload(rt_ctx* ctx, void* dst_dev, const void* src_host, size_t bytes);
+int rt_download(rt_ctx* ctx, void* dst_host, const void* src_dev, size_t bytes);
+int rt_memset(rt_ctx* ctx, void* dst_dev, int value, size_t bytes);
+int rt_copy_d2d(rt_ctx* ctx, void* dst_dev, const void* src_dev, size_t bytes);
+
+/* Stream timing (HIP events recorded on the context stream). */
+typedef struct rt_event rt_event;
+int rt_event_create(rt_ctx* ctx, rt_event** out);
+int rt_event_record(rt_ctx* ctx, rt_event* ev);
+int rt_event_elapsed_ms(rt_ctx* ctx, rt_event* start, rt_event* stop, float* ms);
+void rt_event_destroy(rt_event* ev);
+
+/* HIP-graph capture of a sequence of enqueued kernels (replaces the
+ * reference's single reusable command buffer for a whole decode step). */
+typedef struct rt_graph rt_graph;
+int rt_capture_begin(rt_ctx* ctx);
+int rt_capture_end(rt_ctx* ctx, rt_graph** out);
+int rt_graph_launch(rt_ctx* ctx, rt_graph* g);
+void rt_graph_destroy(rt_graph* g);
+
+/* ───────────────────────── Q8_0 GEMV family ─────────────────────────
+ * y[r] = Σ_k d_b·q[r,k]·x[k]; m = rows, k = reduction length (k % 32 == 0). */
+
+/* dispatch.rs:1280-1295  → gemv_q8_0.metal:56-82 */
+int rt_gemv_q8_0_f32in_f32out(rt_ctx* ctx, const void* weight, const float* input,
+                              float* output, uint32_t m, uint32_t k);
+/* dispatch.rs:1298-1314  → gemv_q8_0.metal:88-114 (output may alias residual) */
+int rt_gemv_q8_0_add_f32_f32in(rt_ctx* ctx, const void* weight, const float* input,
+                               float* output, const float* residual, uint32_t m, uint32_t k);
+/* dispatch.rs:1317-1332  → gemv_q8_0.metal:120-145 (f16 output, RNE) */
+int rt_gemv_q8_0_f32in(rt_ctx* ctx, const void* weight, const float* input,
+                       uint16_t* output, uint32_t m, uint32_t k);
+/* dispatch.rs:1335-1351  → gemv_q8_0.metal:151-176 (f16 in, f16 out) */
+int rt_gemv_q8_0_f16(rt_ctx* ctx, const void* weight, const uint16_t* input,
+                     uint16_t* output, uint32_t m, uint32_t k);
+/* dispatch.rs:1353-1370  → gemv_q8_0.metal:182-208 (f16 in/out/residual) */
+int rt_gemv_q8_0_add_f16(rt_ctx* ctx, const void* weight, const uint16_t* input,
+                         uint16_t* output, const uint16_t* residual, uint32_t m, uint32_t k);
+/* dispatch.rs:1372-1388  → gemv_q8_0.metal:214-240 (f16 in, f32 out/residual) */
+int rt_gemv_q8_0_add_f32res_f16(rt_ctx* ctx, const void* weight, const uint16_t* input,
+                                float* output, const float* residual, uint32_t m, uint32_t k);
+/* dispatch.rs:1083-1098 → gemv_multirow.metal:163-200 (same result as the
+ * non-_mr kernel; kept as its own entry point for drop-in call sites). */
+int rt_gemv_q8_0_f32in_f32out_mr(rt_ctx* ctx, const void* weight, const float* input,
+                                 float* output, uint32_t m, uint32_t k);
+/* dispatch.rs:1101-1117 → gemv_multirow.metal:205-243 */
+int rt_gemv_q8_0_add_f32_f32in_mr(rt_ctx* ctx, const void* weight, const float* input,
+                                  float* output, const float* residual, uint32_t m, uint32_t k);
+
+/* ───────────────────────── Q4_0 GEMV family ───────────────────────── */
+
+/* dispatch.rs:1456-1469 → gemv_q4_0.metal:75-104 */
+int rt_gemv_q4_0_f32in_f32out(rt_ctx* ctx, const void* weight, const float* input,
+                              float* output, uint32_t m, uint32_t k);
+/* dispatch.rs:1471-1484 → gemv_q4_0.metal:110-140 */
+int rt_gemv_q4_0_add_f32_f32in(rt_ctx* ctx, const void* weight, const float* input,
+                               float* output, const float* residual, uint32_t m, uint32_t k);
+/* dispatch.rs:1486-1499 → gemv_q4_0.metal:146-175 (f16 output) */
+int rt_gemv_q4_0_f32in(rt_ctx* ctx, const void* weight, const float* input,
+                       uint16_t* output, uint32_t m, uint32_t k);
+/* dispatch.rs:1501-1514 → gemv_q4_0.metal:181-210 */
+int rt_gemv_q4_0_f16(rt_ctx* ctx, const void* weight, const uint16_t* input,
+                     uint16_t* output, uint32_t m, uint32_t k);
+/* dispatch.rs:1516-1529 → gemv_q4_0.metal:216-246 */
+int rt_gemv_q4_0_add_f16(rt_ctx* ctx, const void* weight, const uint16_t* input,
+                         uint16_t* output, const uint16_t* residual, uint32_t m, uint32_t k);
+
+/* ───────────────────────── Q4_K GEMV family ───────────────────────── */
+
+/* dispatch.rs:1229-1249 → gemv_q4k.metal:186-211 (k % 256 == 0) */
+int rt_gemv_q4k_f32in_f32out(rt_ctx* ctx, const void* weight_q4k, const float* input,
+                             float* output, uint32_t m, uint32_t k);
+/* dispatch.rs:1251-1272 → gemv_q4k.metal:215-241 */
+int rt_gemv_q4k_add_f32_f32in(rt_ctx* ctx, const void* weight_q4k, const float* input,
+                              float* output, const float* residual, uint32_t m, uint32_t k);
+/* dispatch.rs:621 (gemv_q4k_f16) → gemv_q4k.metal:126-150 */
+int rt_gemv_q4k_f16(rt_ctx* ctx, const void* weight_q4k, const uint16_t* input,
+                    uint16_t* output, uint32_t m, uint32_t k);
+/* dispatch.rs:585 (gemv_q4k_add_f16) → gemv_q4k.metal:156-181 */
+int rt_gemv_q4k_add_f16(rt_ctx* ctx, const void* weight_q4k, const uint16_t* input,
+                        uint16_t* output, const uint16_t* residual, uint32_t m, uint32_t k);
+/* dispatch.rs:358 (gemv_q4k_add_f32res_f16) → gemv_q4k.metal:245-271 */
+int rt_gemv_q4k_add_f32res_f16(rt_ctx* ctx, const void* weight_q4k, const uint16_t* input,
+                               float* output, const float* residual, uint32_t m, uint32_t k);
+
+/* ───────────────────────── Q6_K GEMV (new) ─────────────────────────
+ * The reference has no Q6_K GEMV: it dequantises Q6_K to f16 on the CPU
+ * (forward.rs:513-557) and runs gemv_f16w_f32in_f32out(_mr) /
+ * gemv_add_f32_f16w(_mr).  These read the packed 210-byte blocks directly,
+ * with the reference's decode (forward.rs:921-950, one scale per 32). */
+int rt_gemv_q6k_f32in_f32out(rt_ctx* ctx, const void* weight_q6k, const float* input,
+                             float* output, uint32_t m, uint32_t k);
+int rt_gemv_q6k_add_f32_f32in(rt_ctx* ctx, const void* weight_q6k, const float* input,
+                              float* output, const float* residual, uint32_t m, uint32_t k);
+int rt_gemv_q6k_f32in(rt_ctx* ctx, const void* weight_q6k, const float* input,
+                      uint16_t* output, uint32_t m, uint32_t k);
+
+/* ───────────────────────── fused kernels ───────────────────────── */
+
+/* dispatch.rs:813-838 → fused_qkv.metal:72-119 */
+int rt_fused_qkv_q8_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                          const float* x_vec, float* out_q, float* out_k, float* out_v,
+                          uint32_t q_dim, uint32_t kv_dim, uint32_t k);
+/* dispatch.rs:842-871 → fused_qkv.metal:13-69; out = W·x + f32(bias_f16) */
+int rt_fused_qkv_bias_q8_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                               const float* x_vec, float* out_q, float* out_k, float* out_v,
+                               const uint16_t* bias_q, const uint16_t* bias_k,
+                               const uint16_t* bias_v, uint32_t q_dim, uint32_t kv_dim,
+                               uint32_t k);
+/* New: the Q4_0 twin of fused_qkv_bias_q8_0_f32 (same arguments). */
+int rt_fused_qkv_bias_q4_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                               const float* x_vec, float* out_q, float* out_k, float* out_v,
+                               const uint16_t* bias_q, const uint16_t* bias_k,
+                               const uint16_t* bias_v, uint32_t q_dim, uint32_t kv_dim,
+                               uint32_t k);
+/* dispatch.rs:903-921 → fused_ffn.metal:36-93; act = silu(Wg·x)·(Wu·x) */
+int rt_fused_ffn_q8_0_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                          const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);
+/* dispatch.rs:1531-1544 → gemv_q4_0.metal:254-311 */
+int rt_fused_ffn_q4_0_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                          const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);
+/* New: Q4_K gate+up+SiLU (same arguments). */
+int rt_fused_ffn_q4k_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                         const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);
+
+/* ───────────────────────── dequantisation ─────────────────────────
+ * Bit-exact restatements of the reference decoders, to f32:
+ *   Q8_0 forward.rs:951-963, Q4_0 :964-978, Q4_K :1026-1057 (+:359-369),
+ *   Q6_K :921-950.  n_blocks = number of GGUF blocks. */
+int rt_dequant_q8_0_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+int rt_dequant_q4_0_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+int rt_dequant_q4k_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+int rt_dequant_q6k_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+/* dispatch.rs:756-772 → dequant.metal:53-98 (Q4_K → f16, RNE). */
+int rt_dequant_q4k_f16(rt_ctx* ctx, const void* input, uint16_t* output, uint32_t n_blocks);
+
+/* ───────────────────────── batched Q8_0 GEMM (new) ─────────────────────────
+ * Y[M,N] = X[M,K] · W[N,K]ᵀ with W in Q8_0; X, Y f32 row-major.
+ * Replaces the reference's only M>1 path, gemm_f16 on f16-dequantised
+ * weights in verify_draft (forward.rs:2193-2271, gemm.metal:39-190). */
+int rt_gemm_q8_0_f32(rt_ctx* ctx, const void* weight, const float* x, float* y,
+                     uint32_t m_rows, uint32_t n, uint32_t k);
+
+/* ───────────────────────── argmax ───────────────────────── */
+
+/* greedy_argmax_f32 (crates/engine/src/sampler.rs:111-116) on the GPU:
+ * Rust max_by semantics — the LAST index of the maximum wins ties; a NaN
+ * compares Equal.  Writes one uint32 to result; n == 0 → 0. */
+int rt_argmax_f32(rt_ctx* ctx, const float* input, uint32_t* result, uint32_t n);
+/* dispatch.rs:1615-1631 → activation.metal:56-109 (f16 logits). */
+int rt_argmax_f16(rt_ctx* ctx, const uint16_t* input, uint32_t* result, uint32_t n);
+
+/* ───────────────────────── synthetic data (bench/tests) ─────────────────
+ * Seeded, counter-based generators: w ~ N(0, std) quantised per block with
+ * the documented quantisers; x ~ N(mean, std) in f32.  No reference
+ * counterpart (the reference reads GGUF files). */
+int rt_synth_normal_f32(rt_ctx* ctx, float* out, uint64_t n, uint64_t seed, float mean,
+                        float std);
+int rt_synth_normal_f16(rt_ctx* ctx, uint16_t* out, uint64_t n, uint64_t seed, float mean,
+                        float std);
+int rt_synth_q8_0(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
+int rt_synth_q4_0(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
+int rt_synth_q4k(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
+int rt_synth_q6k(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RUNIT_HIP_H */

@@ -1,0 +1,391 @@
+/*
+ * oracle.c — CPU restatement of RunIT's quantized-GEMV decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker and CPU baseline, never
+ * part of the shipped path.  Build flags: -O2 -ffp-contract=off (no FMA
+ * contraction, no fast-math) so f32 arithmetic rounds like the reference's
+ * Rust code.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ───────────────────────── f16 (half 2.7.1) ───────────────────────── */
+
+float ora_h2f(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else { /* subnormal: m·2^-24 */
+            float v = (float)m * 5.9604644775390625e-8f;
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t ora_f2h(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) { /* Inf / NaN (quiet, payload kept) */
+        if (ax == 0x7F800000u) return (uint16_t)(sign | 0x7C00u);
+        return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+    }
+    const int e = (int)(ax >> 23) - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        const uint32_t mant = (ax & 0x7FFFFFu) | 0x800000u;
+        const int shift = 14 - e;
+        uint32_t q = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = ((uint32_t)e << 10) | ((ax & 0x7FFFFFu) >> 13);
+    const uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++; /* may carry to Inf: correct */
+    return (uint16_t)(sign | q);
+}
+
+static float rd_h(const uint8_t* p) { return ora_h2f((uint16_t)(p[0] | (p[1] << 8))); }
+
+size_t ora_block_elems(int fmt) { return (fmt == ORA_Q4K || fmt == ORA_Q6K) ? 256 : 32; }
+size_t ora_block_bytes(int fmt) {
+    switch (fmt) {
+        case ORA_Q8_0: return 34;
+        case ORA_Q4_0: return 18;
+        case ORA_Q4K: return 144;
+        case ORA_Q6K: return 210;
+    }
+    return 0;
+}
+
+/* ───────────────────────── dequantisers ───────────────────────── */
+
+/* forward.rs:951-963: f32_vec.push(d * qs[i] as i8 as f32) */
+void ora_dequant_q8_0(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const uint8_t* blk = in + b * 34;
+        const float d = rd_h(blk);
+        for (int i = 0; i < 32; ++i) out[b * 32 + i] = d * (float)(int8_t)blk[2 + i];
+    }
+}
+
+/* forward.rs:964-978: byte = qs[i/2]; nibble = i%2==0 ? lo : hi;
+ * push(d * (nibble as i32 - 8) as f32) */
+void ora_dequant_q4_0(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const uint8_t* blk = in + b * 18;
+        const float d = rd_h(blk);
+        for (int i = 0; i < 32; ++i) {
+            const uint8_t byte = blk[2 + i / 2];
+            const int nib = (i % 2 == 0) ? (byte & 0x0F) : ((byte >> 4) & 0x0F);
+            out[b * 32 + i] = d * (float)(nib - 8);
+        }
+    }
+}
+
+/* get_scale_min_k4, forward.rs:359-369 */
+static void scale_min_k4(int j, const uint8_t* s, uint8_t* sc, uint8_t* m) {
+    if (j < 4) {
+        *sc = s[j] & 0x3F;
+        *m = s[j + 4] & 0x3F;
+    } else {
+        *sc = (uint8_t)((s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4));
+        *m = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+/* forward.rs:1026-1057 */
+void ora_dequant_q4k(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const uint8_t* blk = in + b * 144;
+        const float d = rd_h(blk), dmin = rd_h(blk + 2);
+        const uint8_t* scales = blk + 4;
+        const uint8_t* qs = blk + 16;
+        float* vals = out + b * 256;
+        for (int j = 0; j < 4; ++j) {
+            uint8_t sc_lo, m_lo, sc_hi, m_hi;
+            scale_min_k4(j, scales, &sc_lo, &m_lo);
+            scale_min_k4(j + 4, scales, &sc_hi, &m_hi);
+            const float d_lo = d * (float)sc_lo, m_lo2 = dmin * (float)m_lo;
+            const float d_hi = d * (float)sc_hi, m_hi2 = dmin * (float)m_hi;
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t bv = qs[j * 32 + l];
+                vals[j * 64 + l] = d_lo * (float)(bv & 0x0F) - m_lo2;
+                vals[j * 64 + l + 32] = d_hi * (float)(bv >> 4) - m_hi2;
+            }
+        }
+    }
+}
+
+/* forward.rs:921-950 (f32 variant; is = n_half/16, scales is+0,2,4,6) */
+void ora_dequant_q6k(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const uint8_t* blk = in + b * 210;
+        const uint8_t* ql = blk;
+        const uint8_t* qh = blk + 128;
+        const uint8_t* scales = blk + 192;
+        const float d = rd_h(blk + 208);
+        float* vals = out + b * 256;
+        for (int n_half = 0; n_half < 256; n_half += 128) {
+            for (int l = 0; l < 32; ++l) {
+                const int is = n_half / 16;
+                const int i0 = n_half / 2 + l, i1 = n_half / 2 + l + 32, ih = n_half / 4 + l;
+                const int q1 = ((ql[i0] & 0x0F) | (((qh[ih] >> 0) & 3) << 4)) - 32;
+                const int q2 = ((ql[i1] & 0x0F) | (((qh[ih] >> 2) & 3) << 4)) - 32;
+                const int q3 = ((ql[i0] >> 4) | (((qh[ih] >> 4) & 3) << 4)) - 32;
+                const int q4 = ((ql[i1] >> 4) | (((qh[ih] >> 6) & 3) << 4)) - 32;
+                vals[n_half + l + 0] = d * (float)(int8_t)scales[is + 0] * (float)q1;
+                vals[n_half + l + 32] = d * (float)(int8_t)scales[is + 2] * (float)q2;
+                vals[n_half + l + 64] = d * (float)(int8_t)scales[is + 4] * (float)q3;
+                vals[n_half + l + 96] = d * (float)(int8_t)scales[is + 6] * (float)q4;
+            }
+        }
+    }
+}
+
+void ora_dequant(int fmt, const uint8_t* in, size_t nblk, float* out) {
+    switch (fmt) {
+        case ORA_Q8_0: ora_dequant_q8_0(in, nblk, out); break;
+        case ORA_Q4_0: ora_dequant_q4_0(in, nblk, out); break;
+        case ORA_Q4K: ora_dequant_q4k(in, nblk, out); break;
+        case ORA_Q6K: ora_dequant_q6k(in, nblk, out); break;
+    }
+}
+
+/* dequant.metal:53-98: half(actual_scale * q - actual_min) */
+void ora_dequant_q4k_f16(const uint8_t* in, size_t nblk, uint16_t* out) {
+    float tmp[256];
+    for (size_t b = 0; b < nblk; ++b) {
+        ora_dequant_q4k(in + b * 144, 1, tmp);
+        for (int i = 0; i < 256; ++i) out[b * 256 + i] = ora_f2h(tmp[i]);
+    }
+}
+
+/* ───────────────────────── GEMV ───────────────────────── */
+
+void ora_gemv_packed(int fmt, const uint8_t* w, const float* x, size_t m_vec, size_t n,
+                     size_t k, double* y, double* sabs) {
+    const size_t be = ora_block_elems(fmt), bb = ora_block_bytes(fmt);
+    const size_t nb = k / be, rb = nb * bb;
+#pragma omp parallel
+    {
+        float* row = (float*)malloc(k * sizeof(float));
+#pragma omp for schedule(static)
+        for (long long r = 0; r < (long long)n; ++r) {
+            ora_dequant(fmt, w + (size_t)r * rb, nb, row);
+            for (size_t mv = 0; mv < m_vec; ++mv) {
+                const float* xv = x + mv * k;
+                double acc = 0.0, sa = 0.0;
+                for (size_t c = 0; c < k; ++c) {
+                    const double p = (double)row[c] * (double)xv[c];
+                    acc += p;
+                    sa += fabs(p);
+                }
+                y[mv * n + (size_t)r] = acc;
+                sabs[mv * n + (size_t)r] = sa;
+            }
+        }
+        free(row);
+    }
+}
+
+/* cpu_gemv (dispatch.rs:1705-1709): (0..k).map(|c| a[r*k+c] * x[c]).sum() */
+void ora_gemv_ref_f32(int fmt, const uint8_t* w, const float* x, size_t n, size_t k, float* y,
+                      int threads) {
+    const size_t be = ora_block_elems(fmt), bb = ora_block_bytes(fmt);
+    const size_t nb = k / be, rb = nb * bb;
+#ifdef _OPENMP
+    if (threads < 1) threads = 1;
+#pragma omp parallel num_threads(threads)
+#endif
+    {
+        float* row = (float*)malloc(k * sizeof(float));
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (long long r = 0; r < (long long)n; ++r) {
+            ora_dequant(fmt, w + (size_t)r * rb, nb, row);
+            float acc = 0.0f;
+            for (size_t c = 0; c < k; ++c) acc += row[c] * x[c];
+            y[r] = acc;
+        }
+        free(row);
+    }
+    (void)threads;
+}
+
+double ora_silu(double x) { return x / (1.0 + exp(-x)); }
+
+/* sampler.rs:111-116: iter().enumerate().max_by(partial_cmp or Equal) —
+ * the running best is replaced unless it compares Greater. */
+uint32_t ora_argmax_f32(const float* v, size_t n) {
+    if (n == 0) return 0;
+    size_t best = 0;
+    for (size_t i = 1; i < n; ++i) {
+        const float m = v[best], c = v[i];
+        const int greater = (m > c); /* partial_cmp == Some(Greater) */
+        if (!greater) best = i;
+    }
+    return (uint32_t)best;
+}
+
+/* ───────────────────────── synthetic data ───────────────────────── */
+
+static uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+float ora_synth_normal(uint64_t seed, uint64_t idx) {
+    const uint64_t h = splitmix64(seed ^ splitmix64(idx));
+    const float u1 = (float)((h >> 40) + 1) * 5.9604644775390625e-8f;
+    const float u2 = (float)(h & 0xFFFFFFull) * 5.9604644775390625e-8f;
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+}
+
+static int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+static void wr_h(uint8_t* p, uint16_t h) { p[0] = (uint8_t)(h & 255); p[1] = (uint8_t)(h >> 8); }
+
+void ora_quantize_q8_0(const float* w, size_t nblk, uint8_t* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const float* x = w + b * 32;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+        const float d = amax / 127.0f;
+        uint8_t* p = out + b * 34;
+        wr_h(p, ora_f2h(d));
+        for (int i = 0; i < 32; ++i) {
+            const int q = d > 0.0f ? (int)roundf(x[i] / d) : 0;
+            p[2 + i] = (uint8_t)(int8_t)clampi(q, -127, 127);
+        }
+    }
+}
+
+void ora_quantize_q4_0(const float* w, size_t nblk, uint8_t* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const float* x = w + b * 32;
+        float amax = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 32; ++i)
+            if (fabsf(x[i]) > amax) { amax = fabsf(x[i]); mx = x[i]; }
+        const float d = mx / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint8_t* p = out + b * 18;
+        wr_h(p, ora_f2h(d));
+        for (int i = 0; i < 16; ++i) {
+            const int n0 = clampi((int)(x[2 * i] * id + 8.5f), 0, 15);
+            const int n1 = clampi((int)(x[2 * i + 1] * id + 8.5f), 0, 15);
+            p[2 + i] = (uint8_t)(n0 | (n1 << 4));
+        }
+    }
+}
+
+void ora_quantize_q4k(const float* w, size_t nblk, uint8_t* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const float* x = w + b * 256;
+        float scl[8], mns[8], maxs = 0.0f, maxm = 0.0f;
+        for (int s = 0; s < 8; ++s) {
+            const int base = 64 * (s & 3) + 32 * (s >> 2);
+            float mn = 0.0f, mx = -3.0e38f;
+            for (int l = 0; l < 32; ++l) { mn = fminf(mn, x[base + l]); mx = fmaxf(mx, x[base + l]); }
+            mns[s] = -mn;
+            scl[s] = (mx - mn) / 15.0f;
+            maxs = fmaxf(maxs, scl[s]);
+            maxm = fmaxf(maxm, mns[s]);
+        }
+        const float d = maxs / 63.0f, dmin = maxm / 63.0f;
+        const uint16_t dh = ora_f2h(d), dmh = ora_f2h(dmin);
+        const float dq = ora_h2f(dh), dmq = ora_h2f(dmh);
+        int sc[8], m[8];
+        for (int s = 0; s < 8; ++s) {
+            sc[s] = clampi(d > 0.0f ? (int)roundf(scl[s] / d) : 0, 0, 63);
+            m[s] = clampi(dmin > 0.0f ? (int)roundf(mns[s] / dmin) : 0, 0, 63);
+        }
+        uint8_t* p = out + b * 144;
+        wr_h(p, dh);
+        wr_h(p + 2, dmh);
+        uint8_t* S = p + 4;
+        for (int j = 0; j < 4; ++j) {
+            S[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            S[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+            S[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+        }
+        uint8_t* qs = p + 16;
+        for (int j = 0; j < 4; ++j)
+            for (int l = 0; l < 32; ++l) {
+                int qq[2];
+                for (int hi = 0; hi < 2; ++hi) {
+                    const int s = j + 4 * hi;
+                    const float ds = dq * (float)sc[s], ms = dmq * (float)m[s];
+                    const int q = ds > 0.0f ? (int)roundf((x[64 * j + 32 * hi + l] + ms) / ds) : 0;
+                    qq[hi] = clampi(q, 0, 15);
+                }
+                qs[32 * j + l] = (uint8_t)(qq[0] | (qq[1] << 4));
+            }
+    }
+}
+
+void ora_quantize_q6k(const float* w, size_t nblk, uint8_t* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const float* x = w + b * 256;
+        float scl[8], dmax = 0.0f;
+        for (int g = 0; g < 8; ++g) {
+            const int base = 128 * (g >> 2) + 32 * (g & 3);
+            float amax = 0.0f, mx = 0.0f;
+            for (int l = 0; l < 32; ++l)
+                if (fabsf(x[base + l]) > amax) { amax = fabsf(x[base + l]); mx = x[base + l]; }
+            scl[g] = mx / -32.0f;
+            dmax = fmaxf(dmax, fabsf(scl[g]));
+        }
+        const float d = dmax / 127.0f;
+        const uint16_t dh = ora_f2h(d);
+        const float dq = ora_h2f(dh);
+        int sc[8], q[256];
+        for (int g = 0; g < 8; ++g) sc[g] = clampi(d > 0.0f ? (int)roundf(scl[g] / d) : 0, -127, 127);
+        for (int g = 0; g < 8; ++g) {
+            const int base = 128 * (g >> 2) + 32 * (g & 3);
+            const float ds = dq * (float)sc[g];
+            for (int l = 0; l < 32; ++l) {
+                const int v = ds != 0.0f ? (int)roundf(x[base + l] / ds) + 32 : 32;
+                q[base + l] = clampi(v, 0, 63);
+            }
+        }
+        uint8_t* p = out + b * 210;
+        uint8_t* ql = p;
+        uint8_t* qh = p + 128;
+        for (int h = 0; h < 256; h += 128)
+            for (int l = 0; l < 32; ++l) {
+                const int q1 = q[h + l], q2 = q[h + l + 32], q3 = q[h + l + 64], q4 = q[h + l + 96];
+                ql[h / 2 + l] = (uint8_t)((q1 & 15) | ((q3 & 15) << 4));
+                ql[h / 2 + l + 32] = (uint8_t)((q2 & 15) | ((q4 & 15) << 4));
+                qh[h / 4 + l] = (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+            }
+        for (int g = 0; g < 8; ++g) {
+            const int slot = 8 * (g >> 2) + 2 * (g & 3);
+            p[192 + slot] = (uint8_t)(int8_t)sc[g];
+            p[192 + slot + 1] = 0x5A;
+        }
+        wr_h(p + 208, dh);
+    }
+}

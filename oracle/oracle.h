@@ -1,0 +1,75 @@
+/*
+ * oracle.h — CPU restatement of RunIT's quantized-GEMV decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (runit_mac_amd/) links,
+ * imports or calls this code; only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py do, and only as the checker / CPU baseline.
+ *
+ * Each function cites the reference file:line it restates (paths relative to
+ * the RunIT_Mac repository).  Compiled with -ffp-contract=off so every f32
+ * product/difference rounds exactly as the reference's Rust code does.
+ */
+#ifndef RUNIT_ORACLE_H
+#define RUNIT_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORA_Q8_0 = 0, ORA_Q4_0 = 1, ORA_Q4K = 2, ORA_Q6K = 3 };
+
+/* half 2.7.1 crate (Cargo.lock): f16::to_f32 (exact) and f16::from_f32
+ * (IEEE binary16, round to nearest even) — used at forward.rs:958,577. */
+float ora_h2f(uint16_t h);
+uint16_t ora_f2h(float f);
+
+/* Block geometry (crates/gguf/src/types.rs:158-191). */
+size_t ora_block_elems(int fmt);
+size_t ora_block_bytes(int fmt);
+
+/* Dequantisers to f32. */
+void ora_dequant_q8_0(const uint8_t* in, size_t nblk, float* out); /* forward.rs:951-963 */
+void ora_dequant_q4_0(const uint8_t* in, size_t nblk, float* out); /* forward.rs:964-978 */
+void ora_dequant_q4k(const uint8_t* in, size_t nblk, float* out);  /* forward.rs:1026-1057, 359-369 */
+void ora_dequant_q6k(const uint8_t* in, size_t nblk, float* out);  /* forward.rs:921-950 */
+void ora_dequant(int fmt, const uint8_t* in, size_t nblk, float* out);
+/* dequant.metal:53-98 — Q4_K → f16 (f32 value, then RNE to half). */
+void ora_dequant_q4k_f16(const uint8_t* in, size_t nblk, uint16_t* out);
+
+/* cpu_gemv (crates/kernels/src/dispatch.rs:1705-1709) on packed weights,
+ * rows dequantised one at a time, accumulated in f64 (precedent:
+ * crates/engine/src/bin/test_gemv.rs:110-115).  Also returns the per-row
+ * tolerance base sabs[r] = Σ_k |w[r,k]·x[k]|.  x is m_vec × k (row-major),
+ * y and sabs are m_vec × n. */
+void ora_gemv_packed(int fmt, const uint8_t* w, const float* x, size_t m_vec, size_t n,
+                     size_t k, double* y, double* sabs);
+
+/* The reference's CPU path as it runs (f32): dequantise a row
+ * (forward.rs decoders) then cpu_gemv's sequential f32 sum
+ * (dispatch.rs:1705-1709).  Used as the timed CPU baseline; threads > 1 splits
+ * rows over OpenMP threads (the reference itself is single-threaded). */
+void ora_gemv_ref_f32(int fmt, const uint8_t* w, const float* x, size_t n, size_t k, float* y,
+                      int threads);
+
+/* cpu_silu (dispatch.rs:1684-1686) in f64. */
+double ora_silu(double x);
+
+/* greedy_argmax_f32 (crates/engine/src/sampler.rs:111-116): Rust max_by
+ * with partial_cmp().unwrap_or(Equal) — last maximal index, NaN = Equal,
+ * n == 0 → 0. */
+uint32_t ora_argmax_f32(const float* v, size_t n);
+
+/* Seeded synthetic data with the same definitions as the device generators
+ * (splitmix64 → Box–Muller), used to build golden fixtures on the CPU. */
+float ora_synth_normal(uint64_t seed, uint64_t idx);
+void ora_quantize_q8_0(const float* w, size_t nblk, uint8_t* out);
+void ora_quantize_q4_0(const float* w, size_t nblk, uint8_t* out);
+void ora_quantize_q4k(const float* w, size_t nblk, uint8_t* out);
+void ora_quantize_q6k(const float* w, size_t nblk, uint8_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

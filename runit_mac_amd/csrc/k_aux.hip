@@ -1,0 +1,340 @@
+// k_aux.hip — bit-exact dequantisation, argmax and seeded synthetic data.
+#include "rt_device.h"
+
+// ───────────────────────────── dequantisation ─────────────────────────────
+// One thread per element.  Every product/difference is written with the
+// _rn intrinsics so no FMA contraction changes the rounding: the results are
+// bit-identical to the reference's f32 CPU decoders.
+
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q8_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_el) return;
+    const uint8_t* blk = in + (i >> 5) * 34;
+    const float d = h2f(*(const uint16_t*)blk);
+    const int8_t q = (int8_t)blk[2 + (i & 31)];
+    out[i] = __fmul_rn(d, (float)q);  // forward.rs:951-963: d * qs[i] as i8 as f32
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q4_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_el) return;
+    const uint8_t* blk = in + (i >> 5) * 18;
+    const float d = h2f(*(const uint16_t*)blk);
+    const uint32_t e = i & 31;
+    const uint8_t byte = blk[2 + e / 2];
+    const int nib = (e & 1) ? (byte >> 4) : (byte & 15);
+    out[i] = __fmul_rn(d, (float)(nib - 8));  // forward.rs:964-978
+}
+
+RT_DEV void q4k_scale_min(uint32_t j, const uint8_t* s, uint32_t& sc, uint32_t& m) {
+    // get_scale_min_k4 (forward.rs:359-369)
+    if (j < 4) {
+        sc = s[j] & 63u;
+        m = s[j + 4] & 63u;
+    } else {
+        sc = (s[j + 4] & 15u) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+RT_DEV float q4k_value(const uint8_t* blk, uint32_t e) {
+    const float d = h2f(*(const uint16_t*)blk);
+    const float dmin = h2f(*(const uint16_t*)(blk + 2));
+    const uint32_t j = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+    uint32_t sc, m;
+    q4k_scale_min(j + 4 * hi, blk + 4, sc, m);
+    const uint8_t byte = blk[16 + 32 * j + l];
+    const uint32_t q = hi ? (byte >> 4) : (byte & 15u);
+    const float dsc = __fmul_rn(d, (float)sc);
+    const float mm = __fmul_rn(dmin, (float)m);
+    return __fsub_rn(__fmul_rn(dsc, (float)q), mm);  // forward.rs:1043-1053
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q4k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_el) return;
+    out[i] = q4k_value(in + (i >> 8) * 144, (uint32_t)(i & 255));
+}
+
+// dequant.metal:53-98 — Q4_K to f16 (value rounded to nearest-even half).
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q4k_f16(const uint8_t* __restrict__ in, uint16_t* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_el) return;
+    out[i] = f2h(q4k_value(in + (i >> 8) * 144, (uint32_t)(i & 255)));
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q6k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_el) return;
+    const uint8_t* blk = in + (i >> 8) * 210;
+    const uint32_t e = (uint32_t)(i & 255);
+    const uint32_t h = e & 128u, t = (e >> 5) & 3, l = e & 31;
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    const float d = h2f(*(const uint16_t*)(blk + 208));
+    const uint32_t qlb = ql[h / 2 + l + ((t & 1) ? 32 : 0)];
+    const uint32_t lo4 = (t < 2) ? (qlb & 15u) : (qlb >> 4);
+    const uint32_t hi2 = (qh[h / 4 + l] >> (2 * t)) & 3u;
+    const int q = (int)(lo4 | (hi2 << 4)) - 32;
+    const float s = (float)sc[h / 16 + 2 * t];
+    out[i] = __fmul_rn(__fmul_rn(d, s), (float)q);  // forward.rs:935-946
+}
+
+// ───────────────────────────── argmax ─────────────────────────────
+// greedy_argmax_f32 (sampler.rs:111-116) folds with Rust's max_by: the
+// running best m is replaced by x unless m > x (partial_cmp None → Equal).
+// Parallel form: each segment summarises to (value, index, absorbing), where
+// `absorbing` means the segment holds a NaN, after which the fold no longer
+// depends on anything before it.  combine(L, R) = R if R.absorbing or
+// !(L.value > R.value), else L — associative, so a tree reduction reproduces
+// the sequential fold exactly (last index wins ties).
+struct AmState { float v; uint32_t i; uint32_t abs; };
+
+RT_DEV AmState am_combine(AmState L, AmState R, bool rvalid) {
+    if (!rvalid) return L;
+    if (R.abs) return R;
+    if (L.v > R.v) return AmState{L.v, L.i, L.abs};
+    return AmState{R.v, R.i, L.abs};
+}
+
+template <typename T>
+RT_DEV float am_load(const T* p, uint32_t i);
+template <>
+RT_DEV float am_load<float>(const float* p, uint32_t i) { return p[i]; }
+template <>
+RT_DEV float am_load<uint16_t>(const uint16_t* p, uint32_t i) { return h2f(p[i]); }
+
+template <typename T>
+RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result, uint32_t n) {
+    // single workgroup of 1024 threads: thread t folds a contiguous slice
+    __shared__ float sv[1024];
+    __shared__ uint32_t si[1024], sa[1024], sok[1024];
+    const uint32_t t = threadIdx.x, nt = blockDim.x;
+    const uint32_t per = (n + nt - 1) / nt;
+    const uint32_t b = t * per, e = min(n, b + per);
+    AmState s{0.0f, 0u, 0u};
+    bool have = false;
+    for (uint32_t i = b; i < e; ++i) {
+        const float x = am_load<T>(in, i);
+        AmState r{x, i, (uint32_t)(x != x)};
+        s = have ? am_combine(s, r, true) : r;
+        have = true;
+    }
+    sv[t] = s.v; si[t] = s.i; sa[t] = s.abs; sok[t] = have ? 1u : 0u;
+    __syncthreads();
+    for (uint32_t st = 1; st < nt; st <<= 1) {
+        if ((t % (2 * st)) == 0 && t + st < nt) {
+            AmState L{sv[t], si[t], sa[t]}, R{sv[t + st], si[t + st], sa[t + st]};
+            const bool lok = sok[t] != 0, rok = sok[t + st] != 0;
+            AmState o = lok ? am_combine(L, R, rok) : R;
+            sv[t] = o.v; si[t] = o.i; sa[t] = o.abs; sok[t] = (lok || rok) ? 1u : 0u;
+        }
+        __syncthreads();
+    }
+    if (t == 0) result[0] = sok[0] ? si[0] : 0u;
+}
+
+extern "C" __global__ void __launch_bounds__(1024)
+k_argmax_f32(const float* in, uint32_t* result, uint32_t n) { argmax_body<float>(in, result, n); }
+extern "C" __global__ void __launch_bounds__(1024)
+k_argmax_f16(const uint16_t* in, uint32_t* result, uint32_t n) { argmax_body<uint16_t>(in, result, n); }
+
+// ───────────────────────────── synthetic data ─────────────────────────────
+// Counter-based: element `idx` of stream `seed` is one splitmix64 hash turned
+// into a standard normal by Box–Muller (cos branch), so any slice can be
+// generated independently and in parallel.
+
+RT_DEV uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+RT_DEV float synth_normal(uint64_t seed, uint64_t idx) {
+    const uint64_t h = splitmix64(seed ^ splitmix64(idx));
+    const float u1 = (float)((h >> 40) + 1) * 5.9604644775390625e-8f;  // (0, 1]
+    const float u2 = (float)(h & 0xFFFFFFull) * 5.9604644775390625e-8f;  // [0, 1)
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+k_synth_normal_f32(float* out, uint64_t n, uint64_t seed, float mean, float stdv) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = mean + stdv * synth_normal(seed, i);
+}
+extern "C" __global__ void __launch_bounds__(256)
+k_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, float mean, float stdv) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = f2h(mean + stdv * synth_normal(seed, i));
+}
+
+// Q8_0: d = max|w|/127 stored as f16; q = clamp(round(w/d), −127, 127) with
+// the unrounded d (round half away from zero).
+extern "C" __global__ void __launch_bounds__(256)
+k_synth_q8_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * blockDim.x) {
+        float w[32];
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            w[i] = stdv * synth_normal(seed, b * 32 + i);
+            amax = fmaxf(amax, fabsf(w[i]));
+        }
+        const float d = amax / 127.0f;
+        uint8_t* p = out + b * 34;
+        const uint16_t dh = f2h(d);
+        p[0] = dh & 255; p[1] = dh >> 8;
+        for (int i = 0; i < 32; ++i) {
+            int q = d > 0.0f ? (int)roundf(w[i] / d) : 0;
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            p[2 + i] = (uint8_t)(int8_t)q;
+        }
+    }
+}
+
+// Q4_0: d = m/−8 where m is the signed value of largest magnitude;
+// nib = clamp(int(w/d + 8.5), 0, 15); reference nibble order (2i low, 2i+1 high).
+extern "C" __global__ void __launch_bounds__(256)
+k_synth_q4_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * blockDim.x) {
+        float w[32];
+        float amax = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            w[i] = stdv * synth_normal(seed, b * 32 + i);
+            if (fabsf(w[i]) > amax) { amax = fabsf(w[i]); mx = w[i]; }
+        }
+        const float d = mx / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint8_t* p = out + b * 18;
+        const uint16_t dh = f2h(d);
+        p[0] = dh & 255; p[1] = dh >> 8;
+        for (int i = 0; i < 16; ++i) {
+            int n0 = (int)(w[2 * i] * id + 8.5f), n1 = (int)(w[2 * i + 1] * id + 8.5f);
+            n0 = n0 < 0 ? 0 : (n0 > 15 ? 15 : n0);
+            n1 = n1 < 0 ? 0 : (n1 > 15 ? 15 : n1);
+            p[2 + i] = (uint8_t)(n0 | (n1 << 4));
+        }
+    }
+}
+
+// Q4_K: scale index s ∈ 0..7 covers elements 64(s%4) + 32(s/4) + [0,32) —
+// the reference's (j, j+4) pairing.  Per s: min_s = max(0, −min w),
+// scale_s = (max w + min_s)/15; d = max scale/63, dmin = max min/63 (f16);
+// sc_s = round(scale_s/d), m_s = round(min_s/dmin) (6-bit);
+// q = clamp(round((w + dmin·m_s)/(d·sc_s)), 0, 15).
+extern "C" __global__ void __launch_bounds__(256)
+k_synth_q4k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * blockDim.x) {
+        float w[256];
+        for (int i = 0; i < 256; ++i) w[i] = stdv * synth_normal(seed, b * 256 + i);
+        float scl[8], mns[8], maxs = 0.0f, maxm = 0.0f;
+        for (int s = 0; s < 8; ++s) {
+            const int base = 64 * (s & 3) + 32 * (s >> 2);
+            float mn = 0.0f, mx = -3.0e38f;
+            for (int l = 0; l < 32; ++l) { mn = fminf(mn, w[base + l]); mx = fmaxf(mx, w[base + l]); }
+            mns[s] = -mn;
+            scl[s] = (mx - mn) / 15.0f;
+            maxs = fmaxf(maxs, scl[s]);
+            maxm = fmaxf(maxm, mns[s]);
+        }
+        const float d = maxs / 63.0f, dmin = maxm / 63.0f;
+        const uint16_t dh = f2h(d), dmh = f2h(dmin);
+        const float dq = h2f(dh), dmq = h2f(dmh);
+        uint32_t sc[8], m[8];
+        for (int s = 0; s < 8; ++s) {
+            int a = d > 0.0f ? (int)roundf(scl[s] / d) : 0;
+            int c = dmin > 0.0f ? (int)roundf(mns[s] / dmin) : 0;
+            sc[s] = a < 0 ? 0 : (a > 63 ? 63 : a);
+            m[s] = c < 0 ? 0 : (c > 63 ? 63 : c);
+        }
+        uint8_t* p = out + b * 144;
+        p[0] = dh & 255; p[1] = dh >> 8; p[2] = dmh & 255; p[3] = dmh >> 8;
+        uint8_t* S = p + 4;
+        for (int j = 0; j < 4; ++j) {
+            S[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            S[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+            S[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+        }
+        uint8_t* qs = p + 16;
+        for (int j = 0; j < 4; ++j) {
+            for (int l = 0; l < 32; ++l) {
+                uint32_t qq[2];
+                for (int hi = 0; hi < 2; ++hi) {
+                    const int s = j + 4 * hi;
+                    const float ds = dq * (float)sc[s], ms = dmq * (float)m[s];
+                    int q = ds > 0.0f ? (int)roundf((w[64 * j + 32 * hi + l] + ms) / ds) : 0;
+                    qq[hi] = q < 0 ? 0 : (q > 15 ? 15 : q);
+                }
+                qs[32 * j + l] = (uint8_t)(qq[0] | (qq[1] << 4));
+            }
+        }
+    }
+}
+
+// Q6_K: group g = 4·(h/128) + t covers elements h + 32t + [0,32) and uses
+// scale slot h/16 + 2t (the only slots the reference decoder reads).
+// scale_g = m_g/−32 (m_g: signed value of largest magnitude), d = max|scale|/127,
+// sc_g = round(scale_g/d), q = clamp(round(w/(d·sc_g)) + 32, 0, 63).
+// The odd scale slots, which the reference ignores, hold 0x5A.
+extern "C" __global__ void __launch_bounds__(256)
+k_synth_q6k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * blockDim.x) {
+        float w[256];
+        for (int i = 0; i < 256; ++i) w[i] = stdv * synth_normal(seed, b * 256 + i);
+        float scl[8], dmax = 0.0f;
+        for (int g = 0; g < 8; ++g) {
+            const int base = 128 * (g >> 2) + 32 * (g & 3);
+            float amax = 0.0f, mx = 0.0f;
+            for (int l = 0; l < 32; ++l)
+                if (fabsf(w[base + l]) > amax) { amax = fabsf(w[base + l]); mx = w[base + l]; }
+            scl[g] = mx / -32.0f;
+            dmax = fmaxf(dmax, fabsf(scl[g]));
+        }
+        const float d = dmax / 127.0f;
+        const uint16_t dh = f2h(d);
+        const float dq = h2f(dh);
+        int sc[8];
+        for (int g = 0; g < 8; ++g) {
+            int a = d > 0.0f ? (int)roundf(scl[g] / d) : 0;
+            sc[g] = a < -127 ? -127 : (a > 127 ? 127 : a);
+        }
+        int q[256];
+        for (int g = 0; g < 8; ++g) {
+            const int base = 128 * (g >> 2) + 32 * (g & 3);
+            const float ds = dq * (float)sc[g];
+            for (int l = 0; l < 32; ++l) {
+                int v = ds != 0.0f ? (int)roundf(w[base + l] / ds) + 32 : 32;
+                q[base + l] = v < 0 ? 0 : (v > 63 ? 63 : v);
+            }
+        }
+        uint8_t* p = out + b * 210;
+        uint8_t* ql = p;
+        uint8_t* qh = p + 128;
+        int8_t* S = (int8_t*)(p + 192);
+        for (int h = 0; h < 256; h += 128) {
+            for (int l = 0; l < 32; ++l) {
+                const int q1 = q[h + l], q2 = q[h + l + 32], q3 = q[h + l + 64], q4 = q[h + l + 96];
+                ql[h / 2 + l] = (uint8_t)((q1 & 15) | ((q3 & 15) << 4));
+                ql[h / 2 + l + 32] = (uint8_t)((q2 & 15) | ((q4 & 15) << 4));
+                qh[h / 4 + l] = (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+            }
+        }
+        for (int g = 0; g < 8; ++g) {
+            const int slot = 8 * (g >> 2) + 2 * (g & 3);
+            S[slot] = (int8_t)sc[g];
+            S[slot + 1] = (int8_t)0x5A;
+        }
+        p[208] = dh & 255; p[209] = dh >> 8;
+    }
+}

@@ -1,0 +1,252 @@
+// rt_device.h — device-side building blocks shared by every gfx950 kernel of
+// the quantized-GEMV decode path.
+//
+//  * f16 helpers (IEEE binary16 ↔ binary32, round-to-nearest-even).
+//  * Wave64 cross-lane sums built from DPP (quad_perm / row mirrors) and
+//    ds_swizzle, instead of Metal's 32-lane simd_sum.
+//  * The activation "limb" record: every 32-element block of the f32
+//    activation vector x is turned, once per workgroup, into a block-floating
+//    point integer form  x_i = 2^(E-22) · (65536·a_i + 256·b_i + c_i)  with
+//    signed int8 limbs a, b, c.  Weights are integers inside a GGUF block
+//    (int8, nibbles, 6-bit codes), so a block dot product becomes three exact
+//    v_dot4_i32_i8 chains; scales are applied once per 32 elements in f32.
+//    x is represented to 22 bits below the block's power-of-two bound, i.e.
+//    |x_i − x̂_i| ≤ 2^(E−23) ≤ 2^-22·max|x_block|.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define RT_DEV __device__ __forceinline__
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ───────────────────────────── f16 ─────────────────────────────
+
+RT_DEV float h2f(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xFFFFu));
+    return (float)h;  // exact
+}
+RT_DEV uint16_t f2h(float f) {
+    _Float16 h = (_Float16)f;  // IEEE round-to-nearest-even
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+// ───────────────────────────── cross-lane ─────────────────────────────
+
+// DPP controls (GCN/CDNA encoding).
+#define DPP_QUAD_PERM(a, b, c, d) ((a) | ((b) << 2) | ((c) << 4) | ((d) << 6))
+#define DPP_ROW_MIRROR 0x140
+#define DPP_ROW_HALF_MIRROR 0x141
+
+template <int CTRL>
+RT_DEV float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+RT_DEV int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+// ds_swizzle bit-mode: lane' = ((lane & and) | or) ^ xor, within 32 lanes.
+template <int XORM>
+RT_DEV float swz_xor_f(float v) {
+    constexpr int pat = 0x1F | (XORM << 10);
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), pat));
+}
+
+// Sum over aligned groups of `n` lanes (n ∈ {1,2,4,...,64}, wave-uniform).
+// Every lane of a group receives the group total.
+RT_DEV float group_sum(float v, int n) {
+    if (n >= 2) v += dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
+    if (n >= 4) v += dpp_f<DPP_QUAD_PERM(2, 3, 0, 1)>(v);
+    if (n >= 8) v += dpp_f<DPP_ROW_HALF_MIRROR>(v);
+    if (n >= 16) v += dpp_f<DPP_ROW_MIRROR>(v);
+    if (n >= 32) v += swz_xor_f<16>(v);
+    if (n >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+RT_DEV float max8(float v) {  // max over aligned groups of 8 lanes
+    v = fmaxf(v, dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_PERM(2, 3, 0, 1)>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
+    return v;
+}
+RT_DEV int sum8_i(int v) {
+    v += dpp_i<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
+    v += dpp_i<DPP_QUAD_PERM(2, 3, 0, 1)>(v);
+    v += dpp_i<DPP_ROW_HALF_MIRROR>(v);
+    return v;
+}
+RT_DEV int sum4_i(int v) {
+    v += dpp_i<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
+    v += dpp_i<DPP_QUAD_PERM(2, 3, 0, 1)>(v);
+    return v;
+}
+
+RT_DEV int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// ───────────────────────────── activation limbs ─────────────────────────────
+//
+// One record per 32 activations, 112 bytes (a stride of 28 dwords keeps eight
+// consecutive records' ds_read_b128 on distinct bank groups):
+//   limb[0][32] (×65536), limb[1][32] (×256), limb[2][32] (×1)  — int8
+//   e        : int16, block exponent E (x̂ = 2^(E-22)·(...))
+//   s[2][3]  : int16, Σ of each limb over elements 0-15 and 16-31
+//   pad      : int16
+struct __attribute__((aligned(16))) XRec {
+    uint32_t limb[3][8];
+    int16_t e;
+    int16_t s[2][3];
+    int16_t pad;
+};
+static_assert(sizeof(XRec) == 112, "XRec layout");
+
+constexpr int XREC_BYTES = 112;
+constexpr int XE_NONFINITE = 300;  // marks a block that holds Inf/NaN
+
+// Position of element j (0..31) of a block inside its record.  The Q4_0
+// layout of the reference packs element 2i in the low nibble and 2i+1 in the
+// high nibble of byte i (gemv_q4_0.metal:13-14, forward.rs:974-976); a dword
+// of nibbles therefore yields elements {0,2,4,6} (low) and {1,3,5,7} (high),
+// and its records store each 8-group as evens then odds.
+template <bool Q40PERM>
+RT_DEV int xpos(int j) {
+    if (!Q40PERM) return j;
+    return (j & ~7) | ((j & 1) << 2) | ((j >> 1) & 3);
+}
+
+template <typename XT>
+RT_DEV void load_x4(const XT* x, uint32_t idx, float v[4]);
+template <>
+RT_DEV void load_x4<float>(const float* x, uint32_t idx, float v[4]) {
+    f32x4 t = *(const f32x4*)(x + idx);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+}
+template <>
+RT_DEV void load_x4<uint16_t>(const uint16_t* x, uint32_t idx, float v[4]) {
+    uint2 t = *(const uint2*)(x + idx);
+    v[0] = h2f(t.x); v[1] = h2f(t.x >> 16); v[2] = h2f(t.y); v[3] = h2f(t.y >> 16);
+}
+
+// Builds records for x-blocks [xb0, xb0+nxb) into recs[0..nxb).  Eight lanes
+// per block, four activations per lane.  All threads of the workgroup must
+// call it (it is followed by a barrier in the callers).
+template <typename XT, bool Q40PERM>
+RT_DEV void stage_x_limbs(const XT* __restrict__ x, uint32_t xb0, uint32_t nxb,
+                          XRec* __restrict__ recs) {
+    const uint32_t total = nxb * 8;
+    for (uint32_t t = threadIdx.x; t < total; t += blockDim.x) {
+        const uint32_t b = t >> 3, q = t & 7;
+        float v[4];
+        load_x4<XT>(x, (xb0 + b) * 32 + q * 4, v);
+        float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        // NaN-propagating max over 8 lanes: a NaN turns into +Inf here.
+        if (a != a) a = __builtin_huge_valf();
+        a = max8(a);
+        int e;
+        const bool finite = a <= 3.40282347e38f;
+        if (!finite) {
+            e = XE_NONFINITE;
+        } else if (a == 0.0f) {
+            e = 0;
+        } else {
+            e = __builtin_amdgcn_frexp_expf(a);  // a < 2^e
+        }
+        int l0[4], l1[4], l2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int xi;
+            if (finite) {
+                xi = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v[i], 22 - e));
+            } else {
+                // Inf/NaN blocks: ±2^22 on non-finite elements, 0 elsewhere;
+                // with e = 300 their products overflow to ±Inf (or NaN).
+                const bool nf = !(fabsf(v[i]) <= 3.40282347e38f);
+                xi = nf ? ((v[i] < 0.0f) ? -(1 << 22) : (1 << 22)) : 0;
+            }
+            // balanced base-256 digits: xi = 65536·l0 + 256·l1 + l2
+            const int c = ((xi + 128) & 255) - 128;
+            const int r1 = (xi - c) >> 8;
+            const int bb = ((r1 + 128) & 255) - 128;
+            l0[i] = (r1 - bb) >> 8;
+            l1[i] = bb;
+            l2[i] = c;
+        }
+        XRec* rec = recs + b;
+        uint8_t* base = (uint8_t*)rec;
+        if (!Q40PERM) {
+            uint32_t w0 = (l0[0] & 255) | ((l0[1] & 255) << 8) | ((l0[2] & 255) << 16) |
+                          ((uint32_t)(l0[3] & 255) << 24);
+            uint32_t w1 = (l1[0] & 255) | ((l1[1] & 255) << 8) | ((l1[2] & 255) << 16) |
+                          ((uint32_t)(l1[3] & 255) << 24);
+            uint32_t w2 = (l2[0] & 255) | ((l2[1] & 255) << 8) | ((l2[2] & 255) << 16) |
+                          ((uint32_t)(l2[3] & 255) << 24);
+            rec->limb[0][q] = w0;
+            rec->limb[1][q] = w1;
+            rec->limb[2][q] = w2;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int pos = xpos<true>(q * 4 + i);
+                base[0 * 32 + pos] = (uint8_t)l0[i];
+                base[1 * 32 + pos] = (uint8_t)l1[i];
+                base[2 * 32 + pos] = (uint8_t)l2[i];
+            }
+        }
+        // Limb sums per 16-element half (lanes 0-3 → half 0, 4-7 → half 1).
+        int s0 = l0[0] + l0[1] + l0[2] + l0[3];
+        int s1 = l1[0] + l1[1] + l1[2] + l1[3];
+        int s2 = l2[0] + l2[1] + l2[2] + l2[3];
+        s0 = sum4_i(s0);
+        s1 = sum4_i(s1);
+        s2 = sum4_i(s2);
+        if ((q & 3) == 0) {
+            const int h = q >> 2;
+            rec->s[h][0] = (int16_t)s0;
+            rec->s[h][1] = (int16_t)s1;
+            rec->s[h][2] = (int16_t)s2;
+        }
+        if (q == 0) {
+            rec->e = (int16_t)e;
+            rec->pad = 0;
+        }
+    }
+}
+
+// Registers holding one record (all three limbs + meta).
+struct XRegs {
+    uint32_t l[3][8];
+    int e;
+    int s[3];  // full-block limb sums
+};
+RT_DEV void load_xregs(const XRec* rec, XRegs& r) {
+    const u32x4* p = (const u32x4*)rec;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        u32x4 a = p[2 * k], b = p[2 * k + 1];
+        r.l[k][0] = a.x; r.l[k][1] = a.y; r.l[k][2] = a.z; r.l[k][3] = a.w;
+        r.l[k][4] = b.x; r.l[k][5] = b.y; r.l[k][6] = b.z; r.l[k][7] = b.w;
+    }
+    u32x4 m = p[6];
+    r.e = (int)(int16_t)(m.x & 0xFFFF);
+    const int s00 = (int16_t)(m.x >> 16), s01 = (int16_t)(m.y & 0xFFFF),
+              s02 = (int16_t)(m.y >> 16);
+    const int s10 = (int16_t)(m.z & 0xFFFF), s11 = (int16_t)(m.z >> 16),
+              s12 = (int16_t)(m.w & 0xFFFF);
+    r.s[0] = s00 + s10;
+    r.s[1] = s01 + s11;
+    r.s[2] = s02 + s12;
+}
+
+// Σ over limbs of an exact limb-dot triple, as f32: 65536·t0 + 256·t1 + t2.
+RT_DEV float limb_combine(int t0, int t1, int t2) {
+    return __builtin_fmaf((float)t0, 65536.0f, (float)(t1 * 256 + t2));
+}

@@ -1,0 +1,651 @@
+// runtime.cpp — host side of the C ABI declared in include/runit_hip.h.
+//
+// The context loads one prebuilt gfx950 code object (runit_kernels.hsaco)
+// with hipModuleLoad, resolves every kernel up front (the reference builds
+// every pipeline state at MetalContext::new, context.rs:163-205), owns one
+// HIP stream, and launches with hipModuleLaunchKernel.  Kernel entry points
+// validate their arguments, pick a launch shape for the problem and enqueue;
+// nothing synchronises until rt_flush (context.rs:289-296).
+#include <hip/hip_runtime.h>
+#include <dlfcn.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/runit_hip.h"
+
+namespace {
+
+// Mirrors the kernel-side GemvArgs (k_gemv.hip); passed by value.
+struct GemvArgs {
+    const uint8_t* w[3];
+    void* out[3];
+    const void* aux[3];
+    const void* x;
+    uint32_t n[3];
+    uint32_t nvrows;
+    uint32_t K;
+    uint32_t lpr;
+    uint32_t xb_chunk;
+    uint64_t row_bytes;
+};
+
+constexpr uint32_t XREC_BYTES = 112;  // one activation record per 32 elements
+
+const char* const kKernelNames[] = {
+    "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_gemv_q8_0_f32_f16",
+    "k_gemv_q8_0_f16_f16", "k_gemv_q8_0_f16_f16add", "k_gemv_q8_0_f16_f32add",
+    "k_qkv_q8_0", "k_qkv_bias_q8_0", "k_ffn_q8_0",
+    "k_gemv_q4_0_f32_f32", "k_gemv_q4_0_f32_f32add", "k_gemv_q4_0_f32_f16",
+    "k_gemv_q4_0_f16_f16", "k_gemv_q4_0_f16_f16add", "k_qkv_bias_q4_0", "k_ffn_q4_0",
+    "k_gemv_q4k_f32_f32", "k_gemv_q4k_f32_f32add", "k_gemv_q4k_f16_f16",
+    "k_gemv_q4k_f16_f16add", "k_gemv_q4k_f16_f32add", "k_ffn_q4k",
+    "k_gemv_q6k_f32_f32", "k_gemv_q6k_f32_f32add", "k_gemv_q6k_f32_f16",
+    "k_dequant_q8_0_f32", "k_dequant_q4_0_f32", "k_dequant_q4k_f32", "k_dequant_q4k_f16",
+    "k_dequant_q6k_f32",
+    "k_argmax_f32", "k_argmax_f16",
+    "k_synth_normal_f32", "k_synth_normal_f16", "k_synth_q8_0", "k_synth_q4_0",
+    "k_synth_q4k", "k_synth_q6k",
+};
+
+struct Fmt {
+    uint32_t blk_el, blk_bytes, unit_el;
+    const char* name;
+};
+constexpr Fmt kQ8_0{32, 34, 32, "Q8_0"};
+constexpr Fmt kQ4_0{32, 18, 32, "Q4_0"};
+constexpr Fmt kQ4K{256, 144, 64, "Q4_K"};
+constexpr Fmt kQ6K{256, 210, 64, "Q6_K"};
+
+thread_local std::string g_global_error = "no error";
+
+}  // namespace
+
+struct rt_ctx {
+    int device = 0;
+    hipModule_t module = nullptr;
+    hipStream_t stream = nullptr;
+    std::unordered_map<std::string, hipFunction_t> fns;
+    int cu_count = 0;
+    size_t max_lds = 65536;
+    std::string err = "no error";
+    bool capturing = false;
+};
+struct rt_event { hipEvent_t ev; };
+struct rt_graph { hipGraph_t graph; hipGraphExec_t exec; };
+
+namespace {
+
+int fail(rt_ctx* c, int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (c) c->err = buf; else g_global_error = buf;
+    return code;
+}
+
+int hip_fail(rt_ctx* c, hipError_t e, const char* what) {
+    return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: %s", what, hipGetErrorString(e));
+}
+
+std::string default_code_object_path() {
+    Dl_info info;
+    if (dladdr((void*)&rt_ctx_create, &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t s = p.find_last_of('/');
+        return (s == std::string::npos ? std::string(".") : p.substr(0, s)) +
+               "/runit_kernels.hsaco";
+    }
+    return "runit_kernels.hsaco";
+}
+
+int launch(rt_ctx* c, const char* name, dim3 grid, dim3 block, size_t lds, void** params) {
+    auto it = c->fns.find(name);
+    if (it == c->fns.end())
+        return fail(c, RT_ERR_PIPELINE_NOT_FOUND, "pipeline function '%s' not found in code object",
+                    name);
+    hipError_t e = hipModuleLaunchKernel(it->second, grid.x, grid.y, grid.z, block.x, block.y,
+                                         block.z, (unsigned)lds, c->stream, params, nullptr);
+    if (e != hipSuccess) return hip_fail(c, e, name);
+    return RT_OK;
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// Lanes per row group: maximise the fraction of busy lane-steps over the
+// row's units; prefer wider groups on ties (fewer, more contiguous rows).
+uint32_t pick_lpr(uint32_t units) {
+    uint32_t best = 64;
+    double best_eff = -1.0;
+    for (uint32_t lpr : {64u, 32u, 16u, 8u, 4u}) {
+        const uint32_t steps = (units + lpr - 1) / lpr;
+        const double eff = (double)units / (double)(steps * lpr);
+        if (eff > best_eff + 1e-9) {
+            best_eff = eff;
+            best = lpr;
+        }
+    }
+    return best;
+}
+
+constexpr uint32_t RPL = 2;  // rows per lane group (template constant of every GEMV kernel)
+
+int gemv_launch(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a, bool x_f16) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (a.K == 0 || a.K % f.blk_el != 0)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: %s: k=%u must be a positive multiple of %u (%s)",
+                    kname, a.K, f.blk_el, f.name);
+    if (a.nvrows == 0) return RT_OK;
+    if (!a.x || !a.out[0] || !a.w[0])
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", kname);
+    if (!aligned(a.x, x_f16 ? 8 : 16))
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: %s: input must be %d-byte aligned", kname,
+                    x_f16 ? 8 : 16);
+    const uint32_t units = a.K / f.unit_el;
+    a.lpr = pick_lpr(units);
+    a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
+    const uint32_t nxb = a.K / 32;
+    const size_t lds_cap = std::min<size_t>(c->max_lds, 80 * 1024);
+    uint32_t chunk = (uint32_t)(lds_cap / XREC_BYTES) & ~7u;
+    if (chunk >= nxb) chunk = nxb;
+    a.xb_chunk = chunk;
+    const size_t lds = (size_t)chunk * XREC_BYTES;
+
+    const uint32_t vrows_per_wave = (64 / a.lpr) * RPL;
+    uint32_t waves = 4;
+    auto tiles = [&](uint32_t w) { return (a.nvrows + vrows_per_wave * w - 1) / (vrows_per_wave * w); };
+    while (waves > 1 && tiles(waves) < (uint32_t)(2 * c->cu_count)) waves /= 2;
+    const uint32_t ntiles = tiles(waves);
+    uint32_t resident = std::min<uint32_t>(32 / waves, (uint32_t)(160 * 1024 / std::max<size_t>(lds, 1)));
+    resident = std::max<uint32_t>(resident, 1);
+    const uint32_t grid = std::min<uint32_t>(ntiles, (uint32_t)c->cu_count * resident);
+    void* params[] = {&a};
+    return launch(c, kname, dim3(grid), dim3(64 * waves), lds, params);
+}
+
+GemvArgs plain_args(const void* w, const void* x, void* y, const void* aux, uint32_t m,
+                    uint32_t k) {
+    GemvArgs a{};
+    a.w[0] = (const uint8_t*)w;
+    a.out[0] = y;
+    a.aux[0] = aux;
+    a.x = x;
+    a.n[0] = m;
+    a.nvrows = m;
+    a.K = k;
+    return a;
+}
+
+int gemv_plain(rt_ctx* c, const char* kname, const Fmt& f, const void* w, const void* x,
+               void* y, const void* res, bool need_res, uint32_t m, uint32_t k, bool x_f16) {
+    if (need_res && !res)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null residual", kname);
+    return gemv_launch(c, kname, f, plain_args(w, x, y, res, m, k), x_f16);
+}
+
+int qkv_launch(rt_ctx* c, const char* kname, const Fmt& f, const void* wq, const void* wk,
+               const void* wv, const float* x, float* oq, float* ok, float* ov,
+               const uint16_t* bq, const uint16_t* bk, const uint16_t* bv, bool bias,
+               uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    if (!wq || !wk || !wv || !oq || !ok || !ov || (bias && (!bq || !bk || !bv)))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", kname);
+    GemvArgs a{};
+    a.w[0] = (const uint8_t*)wq; a.w[1] = (const uint8_t*)wk; a.w[2] = (const uint8_t*)wv;
+    a.out[0] = oq; a.out[1] = ok; a.out[2] = ov;
+    a.aux[0] = bq; a.aux[1] = bk; a.aux[2] = bv;
+    a.x = x;
+    a.n[0] = q_dim; a.n[1] = kv_dim; a.n[2] = kv_dim;
+    a.nvrows = q_dim + 2 * kv_dim;
+    a.K = k;
+    return gemv_launch(c, kname, f, a, false);
+}
+
+int ffn_launch(rt_ctx* c, const char* kname, const Fmt& f, const void* wg, const void* wu,
+               const float* x, float* act, uint32_t ff, uint32_t k) {
+    if (!wg || !wu || !act)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", kname);
+    GemvArgs a{};
+    a.w[0] = (const uint8_t*)wg; a.w[1] = (const uint8_t*)wu;
+    a.out[0] = act;
+    a.x = x;
+    a.n[0] = ff; a.n[1] = ff;
+    a.nvrows = 2 * ff;
+    a.K = k;
+    return gemv_launch(c, kname, f, a, false);
+}
+
+int elementwise_launch(rt_ctx* c, const char* kname, const void* in, void* out, uint64_t n_el) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (n_el == 0) return RT_OK;
+    if (!in || !out) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", kname);
+    const uint64_t blocks = (n_el + 255) / 256;
+    if (blocks > 0x7FFFFFFFull)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: too many elements", kname);
+    void* params[] = {&in, &out, &n_el};
+    return launch(c, kname, dim3((uint32_t)blocks), dim3(256), 0, params);
+}
+
+int synth_launch(rt_ctx* c, const char* kname, void* out, uint64_t n, uint64_t seed, float std,
+                 bool has_mean, float mean) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (n == 0) return RT_OK;
+    if (!out) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", kname);
+    const uint64_t want = (n + 255) / 256;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>(want, (uint64_t)c->cu_count * 16);
+    if (has_mean) {
+        void* params[] = {&out, &n, &seed, &mean, &std};
+        return launch(c, kname, dim3(grid), dim3(256), 0, params);
+    }
+    void* params[] = {&out, &n, &seed, &std};
+    return launch(c, kname, dim3(grid), dim3(256), 0, params);
+}
+
+}  // namespace
+
+extern "C" {
+
+// ───────────────────────────── context ─────────────────────────────
+
+int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
+    if (!out) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null out pointer");
+    *out = nullptr;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+        return fail(nullptr, RT_ERR_NO_DEVICE, "HIP device not found — is an MI355X visible?");
+    rt_ctx* c = new rt_ctx();
+    c->device = 0;
+    hipError_t e = hipSetDevice(0);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(nullptr, RT_ERR_NO_DEVICE, "HIP device not found: %s", hipGetErrorString(e));
+    }
+    hipDeviceGetAttribute(&c->cu_count, hipDeviceAttributeMultiprocessorCount, 0);
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, 0) == hipSuccess &&
+        lds > 0)
+        c->max_lds = (size_t)lds;
+    std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
+    e = hipModuleLoad(&c->module, path.c_str());
+    if (e != hipSuccess) {
+        delete c;
+        return fail(nullptr, RT_ERR_LIBRARY_LOAD, "failed to load code object from '%s': %s",
+                    path.c_str(), hipGetErrorString(e));
+    }
+    for (const char* n : kKernelNames) {
+        hipFunction_t f = nullptr;
+        e = hipModuleGetFunction(&f, c->module, n);
+        if (e != hipSuccess || !f) {
+            hipModuleUnload(c->module);
+            delete c;
+            return fail(nullptr, RT_ERR_PIPELINE_NOT_FOUND,
+                        "pipeline function '%s' not found in code object", n);
+        }
+        c->fns[n] = f;
+    }
+    e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        hipModuleUnload(c->module);
+        delete c;
+        return fail(nullptr, RT_ERR_PIPELINE_CREATE, "failed to create stream: %s",
+                    hipGetErrorString(e));
+    }
+    *out = c;
+    return RT_OK;
+}
+
+void rt_ctx_destroy(rt_ctx* c) {
+    if (!c) return;
+    if (c->stream) {
+        hipStreamSynchronize(c->stream);
+        hipStreamDestroy(c->stream);
+    }
+    if (c->module) hipModuleUnload(c->module);
+    delete c;
+}
+
+int rt_flush(rt_ctx* c) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "flush");
+    return RT_OK;
+}
+
+const char* rt_last_error(const rt_ctx* c) { return c ? c->err.c_str() : g_global_error.c_str(); }
+const char* rt_global_last_error(void) { return g_global_error.c_str(); }
+int rt_device_cu_count(const rt_ctx* c) { return c ? c->cu_count : 0; }
+
+int rt_has_kernel(rt_ctx* c, const char* name) {
+    if (!c || !name) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: null argument");
+    if (c->fns.count(name)) return RT_OK;
+    return fail(c, RT_ERR_PIPELINE_NOT_FOUND, "pipeline function '%s' not found in code object",
+                name);
+}
+
+int rt_malloc(rt_ctx* c, size_t bytes, void** out) {
+    if (!c || !out) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: null argument");
+    *out = nullptr;
+    hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+    if (e != hipSuccess) return hip_fail(c, e, "hipMalloc");
+    return RT_OK;
+}
+int rt_free(rt_ctx* c, void* p) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!p) return RT_OK;
+    hipError_t e = hipFree(p);
+    if (e != hipSuccess) return hip_fail(c, e, "hipFree");
+    return RT_OK;
+}
+static int copy_sync(rt_ctx* c, void* dst, const void* src, size_t n, hipMemcpyKind k,
+                     const char* what) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (n == 0) return RT_OK;
+    if (!dst || !src) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", what);
+    hipError_t e = hipMemcpyAsync(dst, src, n, k, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, what);
+    if (!c->capturing) {
+        e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, what);
+    }
+    return RT_OK;
+}
+int rt_upload(rt_ctx* c, void* d, const void* h, size_t n) {
+    return copy_sync(c, d, h, n, hipMemcpyHostToDevice, "upload");
+}
+int rt_download(rt_ctx* c, void* h, const void* d, size_t n) {
+    return copy_sync(c, h, d, n, hipMemcpyDeviceToHost, "download");
+}
+int rt_copy_d2d(rt_ctx* c, void* d, const void* s, size_t n) {
+    return copy_sync(c, d, s, n, hipMemcpyDeviceToDevice, "copy");
+}
+int rt_memset(rt_ctx* c, void* d, int v, size_t n) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (n == 0) return RT_OK;
+    hipError_t e = hipMemsetAsync(d, v, n, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "memset");
+    e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "memset");
+    return RT_OK;
+}
+
+int rt_event_create(rt_ctx* c, rt_event** out) {
+    if (!c || !out) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: null argument");
+    rt_event* ev = new rt_event();
+    hipError_t e = hipEventCreate(&ev->ev);
+    if (e != hipSuccess) {
+        delete ev;
+        return hip_fail(c, e, "hipEventCreate");
+    }
+    *out = ev;
+    return RT_OK;
+}
+int rt_event_record(rt_ctx* c, rt_event* ev) {
+    if (!c || !ev) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: null argument");
+    hipError_t e = hipEventRecord(ev->ev, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "hipEventRecord");
+    return RT_OK;
+}
+int rt_event_elapsed_ms(rt_ctx* c, rt_event* a, rt_event* b, float* ms) {
+    if (!c || !a || !b || !ms) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: null argument");
+    hipError_t e = hipEventSynchronize(b->ev);
+    if (e != hipSuccess) return hip_fail(c, e, "hipEventSynchronize");
+    e = hipEventElapsedTime(ms, a->ev, b->ev);
+    if (e != hipSuccess) return hip_fail(c, e, "hipEventElapsedTime");
+    return RT_OK;
+}
+void rt_event_destroy(rt_event* ev) {
+    if (!ev) return;
+    hipEventDestroy(ev->ev);
+    delete ev;
+}
+
+int rt_capture_begin(rt_ctx* c) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(c, e, "hipStreamBeginCapture");
+    c->capturing = true;
+    return RT_OK;
+}
+int rt_capture_end(rt_ctx* c, rt_graph** out) {
+    if (!c || !out) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: null argument");
+    *out = nullptr;
+    c->capturing = false;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(c->stream, &g);
+    if (e != hipSuccess) return hip_fail(c, e, "hipStreamEndCapture");
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(g);
+        return hip_fail(c, e, "hipGraphInstantiate");
+    }
+    *out = new rt_graph{g, x};
+    return RT_OK;
+}
+int rt_graph_launch(rt_ctx* c, rt_graph* g) {
+    if (!c || !g) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: null argument");
+    hipError_t e = hipGraphLaunch(g->exec, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "hipGraphLaunch");
+    return RT_OK;
+}
+void rt_graph_destroy(rt_graph* g) {
+    if (!g) return;
+    hipGraphExecDestroy(g->exec);
+    hipGraphDestroy(g->graph);
+    delete g;
+}
+
+// ───────────────────────────── Q8_0 ─────────────────────────────
+
+int rt_gemv_q8_0_f32in_f32out(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m,
+                              uint32_t k) {
+    return gemv_plain(c, "k_gemv_q8_0_f32_f32", kQ8_0, w, x, y, nullptr, false, m, k, false);
+}
+int rt_gemv_q8_0_add_f32_f32in(rt_ctx* c, const void* w, const float* x, float* y,
+                               const float* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q8_0_f32_f32add", kQ8_0, w, x, y, r, true, m, k, false);
+}
+int rt_gemv_q8_0_f32in(rt_ctx* c, const void* w, const float* x, uint16_t* y, uint32_t m,
+                       uint32_t k) {
+    return gemv_plain(c, "k_gemv_q8_0_f32_f16", kQ8_0, w, x, y, nullptr, false, m, k, false);
+}
+int rt_gemv_q8_0_f16(rt_ctx* c, const void* w, const uint16_t* x, uint16_t* y, uint32_t m,
+                     uint32_t k) {
+    return gemv_plain(c, "k_gemv_q8_0_f16_f16", kQ8_0, w, x, y, nullptr, false, m, k, true);
+}
+int rt_gemv_q8_0_add_f16(rt_ctx* c, const void* w, const uint16_t* x, uint16_t* y,
+                         const uint16_t* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q8_0_f16_f16add", kQ8_0, w, x, y, r, true, m, k, true);
+}
+int rt_gemv_q8_0_add_f32res_f16(rt_ctx* c, const void* w, const uint16_t* x, float* y,
+                                const float* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q8_0_f16_f32add", kQ8_0, w, x, y, r, true, m, k, true);
+}
+int rt_gemv_q8_0_f32in_f32out_mr(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m,
+                                 uint32_t k) {
+    return rt_gemv_q8_0_f32in_f32out(c, w, x, y, m, k);
+}
+int rt_gemv_q8_0_add_f32_f32in_mr(rt_ctx* c, const void* w, const float* x, float* y,
+                                  const float* r, uint32_t m, uint32_t k) {
+    return rt_gemv_q8_0_add_f32_f32in(c, w, x, y, r, m, k);
+}
+
+// ───────────────────────────── Q4_0 ─────────────────────────────
+
+int rt_gemv_q4_0_f32in_f32out(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m,
+                              uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4_0_f32_f32", kQ4_0, w, x, y, nullptr, false, m, k, false);
+}
+int rt_gemv_q4_0_add_f32_f32in(rt_ctx* c, const void* w, const float* x, float* y,
+                               const float* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4_0_f32_f32add", kQ4_0, w, x, y, r, true, m, k, false);
+}
+int rt_gemv_q4_0_f32in(rt_ctx* c, const void* w, const float* x, uint16_t* y, uint32_t m,
+                       uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4_0_f32_f16", kQ4_0, w, x, y, nullptr, false, m, k, false);
+}
+int rt_gemv_q4_0_f16(rt_ctx* c, const void* w, const uint16_t* x, uint16_t* y, uint32_t m,
+                     uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4_0_f16_f16", kQ4_0, w, x, y, nullptr, false, m, k, true);
+}
+int rt_gemv_q4_0_add_f16(rt_ctx* c, const void* w, const uint16_t* x, uint16_t* y,
+                         const uint16_t* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4_0_f16_f16add", kQ4_0, w, x, y, r, true, m, k, true);
+}
+
+// ───────────────────────────── Q4_K ─────────────────────────────
+
+int rt_gemv_q4k_f32in_f32out(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m,
+                             uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4k_f32_f32", kQ4K, w, x, y, nullptr, false, m, k, false);
+}
+int rt_gemv_q4k_add_f32_f32in(rt_ctx* c, const void* w, const float* x, float* y,
+                              const float* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4k_f32_f32add", kQ4K, w, x, y, r, true, m, k, false);
+}
+int rt_gemv_q4k_f16(rt_ctx* c, const void* w, const uint16_t* x, uint16_t* y, uint32_t m,
+                    uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4k_f16_f16", kQ4K, w, x, y, nullptr, false, m, k, true);
+}
+int rt_gemv_q4k_add_f16(rt_ctx* c, const void* w, const uint16_t* x, uint16_t* y,
+                        const uint16_t* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4k_f16_f16add", kQ4K, w, x, y, r, true, m, k, true);
+}
+int rt_gemv_q4k_add_f32res_f16(rt_ctx* c, const void* w, const uint16_t* x, float* y,
+                               const float* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q4k_f16_f32add", kQ4K, w, x, y, r, true, m, k, true);
+}
+
+// ───────────────────────────── Q6_K ─────────────────────────────
+
+int rt_gemv_q6k_f32in_f32out(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m,
+                             uint32_t k) {
+    return gemv_plain(c, "k_gemv_q6k_f32_f32", kQ6K, w, x, y, nullptr, false, m, k, false);
+}
+int rt_gemv_q6k_add_f32_f32in(rt_ctx* c, const void* w, const float* x, float* y,
+                              const float* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q6k_f32_f32add", kQ6K, w, x, y, r, true, m, k, false);
+}
+int rt_gemv_q6k_f32in(rt_ctx* c, const void* w, const float* x, uint16_t* y, uint32_t m,
+                      uint32_t k) {
+    return gemv_plain(c, "k_gemv_q6k_f32_f16", kQ6K, w, x, y, nullptr, false, m, k, false);
+}
+
+// ───────────────────────────── fused ─────────────────────────────
+
+int rt_fused_qkv_q8_0_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                          const float* x, float* oq, float* ok, float* ov, uint32_t q_dim,
+                          uint32_t kv_dim, uint32_t k) {
+    return qkv_launch(c, "k_qkv_q8_0", kQ8_0, wq, wk, wv, x, oq, ok, ov, nullptr, nullptr,
+                      nullptr, false, q_dim, kv_dim, k);
+}
+int rt_fused_qkv_bias_q8_0_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                               const float* x, float* oq, float* ok, float* ov,
+                               const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                               uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    return qkv_launch(c, "k_qkv_bias_q8_0", kQ8_0, wq, wk, wv, x, oq, ok, ov, bq, bk, bv, true,
+                      q_dim, kv_dim, k);
+}
+int rt_fused_qkv_bias_q4_0_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                               const float* x, float* oq, float* ok, float* ov,
+                               const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                               uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    return qkv_launch(c, "k_qkv_bias_q4_0", kQ4_0, wq, wk, wv, x, oq, ok, ov, bq, bk, bv, true,
+                      q_dim, kv_dim, k);
+}
+int rt_fused_ffn_q8_0_f32(rt_ctx* c, const void* wg, const void* wu, const float* x, float* act,
+                          uint32_t ff, uint32_t k) {
+    return ffn_launch(c, "k_ffn_q8_0", kQ8_0, wg, wu, x, act, ff, k);
+}
+int rt_fused_ffn_q4_0_f32(rt_ctx* c, const void* wg, const void* wu, const float* x, float* act,
+                          uint32_t ff, uint32_t k) {
+    return ffn_launch(c, "k_ffn_q4_0", kQ4_0, wg, wu, x, act, ff, k);
+}
+int rt_fused_ffn_q4k_f32(rt_ctx* c, const void* wg, const void* wu, const float* x, float* act,
+                         uint32_t ff, uint32_t k) {
+    return ffn_launch(c, "k_ffn_q4k", kQ4K, wg, wu, x, act, ff, k);
+}
+
+// ───────────────────────────── batched Q8_0 ─────────────────────────────
+
+int rt_gemm_q8_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (m_rows == 0 || n == 0) return RT_OK;
+    if (!w || !x || !y)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_q8_0_f32: null buffer");
+    if (k == 0 || k % 32 != 0 || (k * 4u) % 16 != 0)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: gemm_q8_0_f32: k=%u must be a positive multiple of 32",
+                    k);
+    for (uint32_t r = 0; r < m_rows; ++r) {
+        int st = rt_gemv_q8_0_f32in_f32out(c, w, x + (size_t)r * k, y + (size_t)r * n, n, k);
+        if (st != RT_OK) return st;
+    }
+    return RT_OK;
+}
+
+// ───────────────────────────── dequant ─────────────────────────────
+
+int rt_dequant_q8_0_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q8_0_f32", in, out, (uint64_t)nb * 32);
+}
+int rt_dequant_q4_0_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q4_0_f32", in, out, (uint64_t)nb * 32);
+}
+int rt_dequant_q4k_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q4k_f32", in, out, (uint64_t)nb * 256);
+}
+int rt_dequant_q6k_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q6k_f32", in, out, (uint64_t)nb * 256);
+}
+int rt_dequant_q4k_f16(rt_ctx* c, const void* in, uint16_t* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q4k_f16", in, out, (uint64_t)nb * 256);
+}
+
+// ───────────────────────────── argmax ─────────────────────────────
+
+static int argmax_launch(rt_ctx* c, const char* kname, const void* in, uint32_t* res, uint32_t n) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!res || (n && !in))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", kname);
+    void* params[] = {&in, &res, &n};
+    return launch(c, kname, dim3(1), dim3(1024), 0, params);
+}
+int rt_argmax_f32(rt_ctx* c, const float* in, uint32_t* res, uint32_t n) {
+    return argmax_launch(c, "k_argmax_f32", in, res, n);
+}
+int rt_argmax_f16(rt_ctx* c, const uint16_t* in, uint32_t* res, uint32_t n) {
+    return argmax_launch(c, "k_argmax_f16", in, res, n);
+}
+
+// ───────────────────────────── synth ─────────────────────────────
+
+int rt_synth_normal_f32(rt_ctx* c, float* out, uint64_t n, uint64_t seed, float mean, float std) {
+    return synth_launch(c, "k_synth_normal_f32", out, n, seed, std, true, mean);
+}
+int rt_synth_normal_f16(rt_ctx* c, uint16_t* out, uint64_t n, uint64_t seed, float mean,
+                        float std) {
+    return synth_launch(c, "k_synth_normal_f16", out, n, seed, std, true, mean);
+}
+int rt_synth_q8_0(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
+    return synth_launch(c, "k_synth_q8_0", out, nb, seed, std, false, 0.0f);
+}
+int rt_synth_q4_0(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
+    return synth_launch(c, "k_synth_q4_0", out, nb, seed, std, false, 0.0f);
+}
+int rt_synth_q4k(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
+    return synth_launch(c, "k_synth_q4k", out, nb, seed, std, false, 0.0f);
+}
+int rt_synth_q6k(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
+    return synth_launch(c, "k_synth_q6k", out, nb, seed, std, false, 0.0f);
+}
+
+}  // extern "C"

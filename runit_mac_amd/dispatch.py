@@ -1,0 +1,418 @@
+"""Python mirror of RunIT's `crates/kernels` dispatch API over the C ABI.
+
+The reference exposes `MetalContext` (crates/kernels/src/context.rs) and about
+80 `dispatch::<kernel>(ctx, &Buffer.., dims) -> Result<()>` functions
+(crates/kernels/src/dispatch.rs).  This module keeps those names, argument
+order and meaning, and the `KernelError` variants (crates/kernels/src/error.rs:
+4-21), on top of `librunit_hip.so` (include/runit_hip.h).  Every call only
+enqueues; `ctx.flush()` waits, as in the reference.
+
+There is no CPU fallback: if the native library or the gfx950 code object is
+missing, or no GPU is visible, constructing a context raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_size_t, c_uint32, c_uint64, c_void_p
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "lib", "librunit_hip.so")
+HSACO_PATH = os.path.join(_PKG, "lib", "runit_kernels.hsaco")
+
+
+# ───────────────────────────── errors (error.rs:4-21) ─────────────────────────────
+
+class KernelError(Exception):
+    """Base of the KernelError variants."""
+
+
+class NoDevice(KernelError):
+    pass
+
+
+class LibraryLoad(KernelError):
+    pass
+
+
+class PipelineNotFound(KernelError):
+    pass
+
+
+class PipelineCreate(KernelError):
+    pass
+
+
+class Dispatch(KernelError):
+    pass
+
+
+class BufferSize(KernelError):
+    pass
+
+
+_STATUS = {1: NoDevice, 2: LibraryLoad, 3: PipelineNotFound, 4: PipelineCreate, 5: Dispatch,
+           6: BufferSize}
+
+
+# ───────────────────────────── library loading ─────────────────────────────
+
+_lib = None
+
+# (name, argtypes) for every exported symbol; restype is c_int unless noted.
+_P, _U32, _U64, _F = c_void_p, c_uint32, c_uint64, c_float
+_SIGS = {
+    "rt_ctx_create": [POINTER(c_void_p), c_char_p],
+    "rt_flush": [_P],
+    "rt_device_cu_count": [_P],
+    "rt_has_kernel": [_P, c_char_p],
+    "rt_malloc": [_P, c_size_t, POINTER(c_void_p)],
+    "rt_free": [_P, _P],
+    "rt_upload": [_P, _P, _P, c_size_t],
+    "rt_download": [_P, _P, _P, c_size_t],
+    "rt_memset": [_P, _P, c_int, c_size_t],
+    "rt_copy_d2d": [_P, _P, _P, c_size_t],
+    "rt_event_create": [_P, POINTER(c_void_p)],
+    "rt_event_record": [_P, _P],
+    "rt_event_elapsed_ms": [_P, _P, _P, POINTER(c_float)],
+    "rt_capture_begin": [_P],
+    "rt_capture_end": [_P, POINTER(c_void_p)],
+    "rt_graph_launch": [_P, _P],
+    # GEMV family: (ctx, weight, input, output, [residual,] m, k)
+    **{n: [_P, _P, _P, _P, _U32, _U32] for n in (
+        "rt_gemv_q8_0_f32in_f32out", "rt_gemv_q8_0_f32in", "rt_gemv_q8_0_f16",
+        "rt_gemv_q8_0_f32in_f32out_mr",
+        "rt_gemv_q4_0_f32in_f32out", "rt_gemv_q4_0_f32in", "rt_gemv_q4_0_f16",
+        "rt_gemv_q4k_f32in_f32out", "rt_gemv_q4k_f16",
+        "rt_gemv_q6k_f32in_f32out", "rt_gemv_q6k_f32in")},
+    **{n: [_P, _P, _P, _P, _P, _U32, _U32] for n in (
+        "rt_gemv_q8_0_add_f32_f32in", "rt_gemv_q8_0_add_f16", "rt_gemv_q8_0_add_f32res_f16",
+        "rt_gemv_q8_0_add_f32_f32in_mr",
+        "rt_gemv_q4_0_add_f32_f32in", "rt_gemv_q4_0_add_f16",
+        "rt_gemv_q4k_add_f32_f32in", "rt_gemv_q4k_add_f16", "rt_gemv_q4k_add_f32res_f16",
+        "rt_gemv_q6k_add_f32_f32in")},
+    "rt_fused_qkv_q8_0_f32": [_P] + [_P] * 7 + [_U32] * 3,
+    "rt_fused_qkv_bias_q8_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
+    "rt_fused_qkv_bias_q4_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
+    **{n: [_P, _P, _P, _P, _P, _U32, _U32] for n in (
+        "rt_fused_ffn_q8_0_f32", "rt_fused_ffn_q4_0_f32", "rt_fused_ffn_q4k_f32")},
+    **{n: [_P, _P, _P, _U32] for n in (
+        "rt_dequant_q8_0_f32", "rt_dequant_q4_0_f32", "rt_dequant_q4k_f32",
+        "rt_dequant_q6k_f32", "rt_dequant_q4k_f16", "rt_argmax_f32", "rt_argmax_f16")},
+    "rt_gemm_q8_0_f32": [_P, _P, _P, _P, _U32, _U32, _U32],
+    "rt_synth_normal_f32": [_P, _P, _U64, _U64, _F, _F],
+    "rt_synth_normal_f16": [_P, _P, _U64, _U64, _F, _F],
+    **{n: [_P, _P, _U64, _U64, _F] for n in (
+        "rt_synth_q8_0", "rt_synth_q4_0", "rt_synth_q4k", "rt_synth_q6k")},
+}
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Loads librunit_hip.so and declares every entry point's signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise LibraryLoad(f"native library missing: {path} (run __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, argtypes in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = c_int
+    lib.rt_last_error.argtypes = [_P]
+    lib.rt_last_error.restype = c_char_p
+    lib.rt_global_last_error.argtypes = []
+    lib.rt_global_last_error.restype = c_char_p
+    lib.rt_ctx_destroy.argtypes = [_P]
+    lib.rt_ctx_destroy.restype = None
+    lib.rt_event_destroy.argtypes = [_P]
+    lib.rt_event_destroy.restype = None
+    lib.rt_graph_destroy.argtypes = [_P]
+    lib.rt_graph_destroy.restype = None
+    _lib = lib
+    return lib
+
+
+def _ptr(b) -> int | None:
+    if b is None:
+        return None
+    if isinstance(b, Buffer):
+        return b.ptr
+    return int(b)
+
+
+# ───────────────────────────── context / buffers ─────────────────────────────
+
+class Buffer:
+    """A device allocation (the analogue of a Metal `Buffer`)."""
+
+    def __init__(self, ctx: "HipContext", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = c_void_p()
+        ctx._check(ctx.lib.rt_malloc(ctx.handle, self.nbytes, ctypes.byref(p)))
+        self.ptr = p.value
+
+    def write(self, data, offset: int = 0) -> "Buffer":
+        arr = np.ascontiguousarray(data)
+        n = arr.nbytes
+        if offset + n > self.nbytes:
+            raise BufferSize(f"buffer size mismatch: expected {offset + n} bytes, got {self.nbytes}")
+        self.ctx._check(self.ctx.lib.rt_upload(self.ctx.handle, self.ptr + offset,
+                                               arr.ctypes.data, n))
+        return self
+
+    def read(self, dtype=np.uint8, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dt.itemsize
+        out = np.empty(count, dtype=dt)
+        if out.nbytes + offset > self.nbytes:
+            raise BufferSize(f"buffer size mismatch: expected {out.nbytes + offset} bytes, "
+                             f"got {self.nbytes}")
+        self.ctx._check(self.ctx.lib.rt_download(self.ctx.handle, out.ctypes.data,
+                                                 self.ptr + offset, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            self.ctx.lib.rt_free(self.ctx.handle, self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            if self.ptr and self.ctx.handle:
+                self.free()
+        except Exception:
+            pass
+
+
+class Graph:
+    def __init__(self, ctx: "HipContext", handle: int):
+        self.ctx, self.handle = ctx, handle
+
+    def launch(self) -> None:
+        self.ctx._check(self.ctx.lib.rt_graph_launch(self.ctx.handle, self.handle))
+
+    def __del__(self):
+        try:
+            if self.handle:
+                self.ctx.lib.rt_graph_destroy(self.handle)
+                self.handle = 0
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self, ctx: "HipContext"):
+        self.ctx = ctx
+        h = c_void_p()
+        ctx._check(ctx.lib.rt_event_create(ctx.handle, ctypes.byref(h)))
+        self.handle = h.value
+
+    def record(self) -> None:
+        self.ctx._check(self.ctx.lib.rt_event_record(self.ctx.handle, self.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = c_float()
+        self.ctx._check(self.ctx.lib.rt_event_elapsed_ms(self.ctx.handle, self.handle,
+                                                         end.handle, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                self.ctx.lib.rt_event_destroy(self.handle)
+                self.handle = 0
+        except Exception:
+            pass
+
+
+class HipContext:
+    """MetalContext analogue (context.rs:139-304): device, code object, stream."""
+
+    def __init__(self, code_object: str | None = None):
+        self.lib = load_library()
+        h = c_void_p()
+        path = (code_object or HSACO_PATH).encode()
+        st = self.lib.rt_ctx_create(ctypes.byref(h), path)
+        if st != 0:
+            raise _STATUS.get(st, KernelError)(self.lib.rt_global_last_error().decode())
+        self.handle = h.value
+
+    def _check(self, status: int) -> None:
+        if status != 0:
+            msg = self.lib.rt_last_error(self.handle).decode()
+            raise _STATUS.get(status, KernelError)(msg)
+
+    @property
+    def cu_count(self) -> int:
+        return int(self.lib.rt_device_cu_count(self.handle))
+
+    def new_buffer(self, nbytes: int) -> Buffer:
+        return Buffer(self, nbytes)
+
+    def buffer_from(self, data) -> Buffer:
+        arr = np.ascontiguousarray(data)
+        return Buffer(self, max(arr.nbytes, 1)).write(arr)
+
+    def flush(self) -> None:
+        self._check(self.lib.rt_flush(self.handle))
+
+    def has_kernel(self, name: str) -> None:
+        self._check(self.lib.rt_has_kernel(self.handle, name.encode()))
+
+    def event(self) -> Event:
+        return Event(self)
+
+    def capture_begin(self) -> None:
+        self._check(self.lib.rt_capture_begin(self.handle))
+
+    def capture_end(self) -> Graph:
+        g = c_void_p()
+        self._check(self.lib.rt_capture_end(self.handle, ctypes.byref(g)))
+        return Graph(self, g.value)
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.rt_ctx_destroy(self.handle)
+            self.handle = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+# ───────────────────────────── dispatch functions ─────────────────────────────
+# Same names and argument order as crates/kernels/src/dispatch.rs.
+
+def _call(ctx: HipContext, name: str, *args) -> None:
+    ctx._check(getattr(ctx.lib, name)(ctx.handle, *[_ptr(a) if isinstance(a, Buffer) else a
+                                                   for a in args]))
+
+
+def _gemv(name):
+    def f(ctx, weight, input, output, m, k):
+        _call(ctx, "rt_" + name, _ptr(weight), _ptr(input), _ptr(output), m, k)
+    f.__name__ = name
+    f.__doc__ = f"dispatch::{name}(ctx, weight, input, output, m, k)"
+    return f
+
+
+def _gemv_add(name):
+    def f(ctx, weight, input, output, residual, m, k):
+        _call(ctx, "rt_" + name, _ptr(weight), _ptr(input), _ptr(output), _ptr(residual), m, k)
+    f.__name__ = name
+    f.__doc__ = f"dispatch::{name}(ctx, weight, input, output, residual, m, k)"
+    return f
+
+
+gemv_q8_0_f32in_f32out = _gemv("gemv_q8_0_f32in_f32out")
+gemv_q8_0_f32in = _gemv("gemv_q8_0_f32in")
+gemv_q8_0_f16 = _gemv("gemv_q8_0_f16")
+gemv_q8_0_f32in_f32out_mr = _gemv("gemv_q8_0_f32in_f32out_mr")
+gemv_q8_0_add_f32_f32in = _gemv_add("gemv_q8_0_add_f32_f32in")
+gemv_q8_0_add_f16 = _gemv_add("gemv_q8_0_add_f16")
+gemv_q8_0_add_f32res_f16 = _gemv_add("gemv_q8_0_add_f32res_f16")
+gemv_q8_0_add_f32_f32in_mr = _gemv_add("gemv_q8_0_add_f32_f32in_mr")
+gemv_q4_0_f32in_f32out = _gemv("gemv_q4_0_f32in_f32out")
+gemv_q4_0_f32in = _gemv("gemv_q4_0_f32in")
+gemv_q4_0_f16 = _gemv("gemv_q4_0_f16")
+gemv_q4_0_add_f32_f32in = _gemv_add("gemv_q4_0_add_f32_f32in")
+gemv_q4_0_add_f16 = _gemv_add("gemv_q4_0_add_f16")
+gemv_q4k_f32in_f32out = _gemv("gemv_q4k_f32in_f32out")
+gemv_q4k_f16 = _gemv("gemv_q4k_f16")
+gemv_q4k_add_f32_f32in = _gemv_add("gemv_q4k_add_f32_f32in")
+gemv_q4k_add_f16 = _gemv_add("gemv_q4k_add_f16")
+gemv_q4k_add_f32res_f16 = _gemv_add("gemv_q4k_add_f32res_f16")
+gemv_q6k_f32in_f32out = _gemv("gemv_q6k_f32in_f32out")
+gemv_q6k_f32in = _gemv("gemv_q6k_f32in")
+gemv_q6k_add_f32_f32in = _gemv_add("gemv_q6k_add_f32_f32in")
+
+
+def fused_qkv_q8_0_f32(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, q_dim, kv_dim, k):
+    """dispatch.rs:813-838"""
+    _call(ctx, "rt_fused_qkv_q8_0_f32", *map(_ptr, (w_q, w_k, w_v, x_vec, out_q, out_k, out_v)),
+          q_dim, kv_dim, k)
+
+
+def fused_qkv_bias_q8_0_f32(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k,
+                            bias_v, q_dim, kv_dim, k):
+    """dispatch.rs:842-871"""
+    _call(ctx, "rt_fused_qkv_bias_q8_0_f32",
+          *map(_ptr, (w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k, bias_v)),
+          q_dim, kv_dim, k)
+
+
+def fused_qkv_bias_q4_0_f32(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k,
+                            bias_v, q_dim, kv_dim, k):
+    """Q4_0 twin of dispatch.rs:842-871 (new)."""
+    _call(ctx, "rt_fused_qkv_bias_q4_0_f32",
+          *map(_ptr, (w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k, bias_v)),
+          q_dim, kv_dim, k)
+
+
+def fused_ffn_q8_0_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
+    """dispatch.rs:903-921"""
+    _call(ctx, "rt_fused_ffn_q8_0_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
+
+
+def fused_ffn_q4_0_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
+    """dispatch.rs:1531-1544"""
+    _call(ctx, "rt_fused_ffn_q4_0_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
+
+
+def fused_ffn_q4k_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
+    """Q4_K twin of dispatch.rs:903-921 (new)."""
+    _call(ctx, "rt_fused_ffn_q4k_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
+
+
+def dequant_q4k_f16(ctx, input, output, n_blocks):
+    """dispatch.rs:756-772"""
+    _call(ctx, "rt_dequant_q4k_f16", _ptr(input), _ptr(output), n_blocks)
+
+
+def dequant_f32(ctx, fmt: str, input, output, n_blocks):
+    """Bit-exact dequantisation to f32 for fmt in {q8_0, q4_0, q4k, q6k}."""
+    _call(ctx, f"rt_dequant_{fmt}_f32", _ptr(input), _ptr(output), n_blocks)
+
+
+def gemm_q8_0_f32(ctx, weight, x, y, m_rows, n, k):
+    """Batched Y[M,N] = X[M,K]·W[N,K]ᵀ (new; replaces gemm_f16 in verify_draft)."""
+    _call(ctx, "rt_gemm_q8_0_f32", _ptr(weight), _ptr(x), _ptr(y), m_rows, n, k)
+
+
+def argmax_f32(ctx, input, result, n):
+    """greedy_argmax_f32 (sampler.rs:111-116) on the GPU."""
+    _call(ctx, "rt_argmax_f32", _ptr(input), _ptr(result), n)
+
+
+def argmax_f16(ctx, input, result, n):
+    """dispatch.rs:1615-1631"""
+    _call(ctx, "rt_argmax_f16", _ptr(input), _ptr(result), n)
+
+
+def synth_normal_f32(ctx, out, n, seed, mean=0.0, std=1.0):
+    _call(ctx, "rt_synth_normal_f32", _ptr(out), n, seed, mean, std)
+
+
+def synth_normal_f16(ctx, out, n, seed, mean=0.0, std=1.0):
+    _call(ctx, "rt_synth_normal_f16", _ptr(out), n, seed, mean, std)
+
+
+def synth_weights(ctx, fmt: str, out, n_blocks, seed, std=0.02):
+    """Seeded N(0, std) weights quantised per block (fmt in q8_0/q4_0/q4k/q6k)."""
+    _call(ctx, f"rt_synth_{fmt}", _ptr(out), n_blocks, seed, std)
+
+
+# Block geometry (crates/gguf/src/types.rs:158-191).
+BLOCK = {"q8_0": (32, 34), "q4_0": (32, 18), "q4k": (256, 144), "q6k": (256, 210)}
+
+
+def weight_bytes(fmt: str, n: int, k: int) -> int:
+    el, by = BLOCK[fmt]
+    return n * (k // el) * by

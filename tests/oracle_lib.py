@@ -1,0 +1,120 @@
+"""ctypes access to the CPU oracle (oracle/liboracle.so) — tests only."""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(REPO, "oracle")
+LIB = os.path.join(ORACLE_DIR, "liboracle.so")
+
+FMT = {"q8_0": 0, "q4_0": 1, "q4k": 2, "q6k": 3}
+BLOCK = {"q8_0": (32, 34), "q4_0": (32, 18), "q4k": (256, 144), "q6k": (256, 210)}
+
+
+def _load():
+    src = os.path.join(ORACLE_DIR, "oracle.c")
+    if not os.path.exists(LIB) or os.path.getmtime(LIB) < os.path.getmtime(src):
+        subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
+    return ctypes.CDLL(LIB)
+
+
+_lib = _load()
+_P, _S = ctypes.c_void_p, ctypes.c_size_t
+_lib.ora_h2f.argtypes = [ctypes.c_uint16]
+_lib.ora_h2f.restype = ctypes.c_float
+_lib.ora_f2h.argtypes = [ctypes.c_float]
+_lib.ora_f2h.restype = ctypes.c_uint16
+_lib.ora_dequant.argtypes = [ctypes.c_int, _P, _S, _P]
+_lib.ora_dequant_q4k_f16.argtypes = [_P, _S, _P]
+_lib.ora_gemv_packed.argtypes = [ctypes.c_int, _P, _P, _S, _S, _S, _P, _P]
+_lib.ora_gemv_ref_f32.argtypes = [ctypes.c_int, _P, _P, _S, _S, _P, ctypes.c_int]
+_lib.ora_silu.argtypes = [ctypes.c_double]
+_lib.ora_silu.restype = ctypes.c_double
+_lib.ora_argmax_f32.argtypes = [_P, _S]
+_lib.ora_argmax_f32.restype = ctypes.c_uint32
+_lib.ora_synth_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+_lib.ora_synth_normal.restype = ctypes.c_float
+for _n in ("q8_0", "q4_0", "q4k", "q6k"):
+    getattr(_lib, f"ora_quantize_{_n}").argtypes = [_P, _S, _P]
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data
+
+
+def h2f(h: int) -> float:
+    return _lib.ora_h2f(h)
+
+
+def f2h(f: float) -> int:
+    return _lib.ora_f2h(f)
+
+
+def dequant(fmt: str, packed: np.ndarray) -> np.ndarray:
+    el, by = BLOCK[fmt]
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    nblk = packed.size // by
+    out = np.empty(nblk * el, dtype=np.float32)
+    _lib.ora_dequant(FMT[fmt], _p(packed), nblk, _p(out))
+    return out
+
+
+def dequant_q4k_f16(packed: np.ndarray) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    nblk = packed.size // 144
+    out = np.empty(nblk * 256, dtype=np.uint16)
+    _lib.ora_dequant_q4k_f16(_p(packed), nblk, _p(out))
+    return out
+
+
+def gemv(fmt: str, packed: np.ndarray, x: np.ndarray, n: int, k: int):
+    """f64 reference y and Σ|w·x| per row; x may be (k,) or (m, k)."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = 1 if x.ndim == 1 else x.shape[0]
+    y = np.empty((m, n), dtype=np.float64)
+    s = np.empty((m, n), dtype=np.float64)
+    _lib.ora_gemv_packed(FMT[fmt], _p(packed), _p(x), m, n, k, _p(y), _p(s))
+    if x.ndim == 1:
+        return y[0], s[0]
+    return y, s
+
+
+def gemv_ref_f32(fmt: str, packed: np.ndarray, x: np.ndarray, n: int, k: int, threads: int = 1):
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(n, dtype=np.float32)
+    _lib.ora_gemv_ref_f32(FMT[fmt], _p(packed), _p(x), n, k, _p(y), threads)
+    return y
+
+
+def silu(x: float) -> float:
+    return _lib.ora_silu(x)
+
+
+def argmax(v: np.ndarray) -> int:
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    return int(_lib.ora_argmax_f32(_p(v), v.size))
+
+
+def synth_normal(seed: int, n: int, start: int = 0) -> np.ndarray:
+    return np.array([_lib.ora_synth_normal(seed, start + i) for i in range(n)], dtype=np.float32)
+
+
+def quantize(fmt: str, w: np.ndarray) -> np.ndarray:
+    el, by = BLOCK[fmt]
+    w = np.ascontiguousarray(w, dtype=np.float32).ravel()
+    nblk = w.size // el
+    out = np.zeros(nblk * by, dtype=np.uint8)
+    getattr(_lib, f"ora_quantize_{fmt}")(_p(w), nblk, _p(out))
+    return out
+
+
+def synth_weights(fmt: str, n: int, k: int, seed: int, std: float = 0.02) -> np.ndarray:
+    """Host twin of the device generator (libm transcendental functions)."""
+    w = (std * synth_normal(seed, n * k)).astype(np.float32)
+    return quantize(fmt, w)

@@ -1,0 +1,130 @@
+"""GPU parity of fused QKV(+bias), fused gate+up+SiLU, argmax and the batched
+Q8_0 GEMM, against the CPU oracle, through the C ABI."""
+import numpy as np
+import pytest
+
+import oracle_lib as ora
+from gpu_helpers import F32_EPS, REL, check_close, device_weights
+from runit_mac_amd import dispatch as d
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv_case(ctx, fmt, q_dim, kv_dim, k, bias, seed):
+    rng = np.random.default_rng(seed)
+    ws = [device_weights(ctx, fmt, n, k, seed=seed + i) for i, n in
+          enumerate((q_dim, kv_dim, kv_dim))]
+    x = rng.standard_normal(k).astype(np.float32)
+    xb = ctx.buffer_from(x)
+    outs = [ctx.new_buffer(4 * n) for n in (q_dim, kv_dim, kv_dim)]
+    biases = [(0.02 * rng.standard_normal(n)).astype(np.float16) for n in (q_dim, kv_dim, kv_dim)]
+    if bias:
+        fn = getattr(d, f"fused_qkv_bias_{fmt}_f32")
+        fn(ctx, ws[0][0], ws[1][0], ws[2][0], xb, *outs, *[ctx.buffer_from(b) for b in biases],
+           q_dim, kv_dim, k)
+    else:
+        d.fused_qkv_q8_0_f32(ctx, ws[0][0], ws[1][0], ws[2][0], xb, *outs, q_dim, kv_dim, k)
+    ctx.flush()
+    for i, n in enumerate((q_dim, kv_dim, kv_dim)):
+        yref, sabs = ora.gemv(fmt, ws[i][1], x, n, k)
+        if bias:
+            yref = yref + biases[i].astype(np.float64)  # fused_qkv.metal:68
+        check_close(outs[i].read(np.float32, n), yref, sabs, f"qkv[{i}] {fmt}",
+                    F32_EPS * np.abs(yref))
+
+
+@pytest.mark.parametrize("q_dim,kv_dim,k", [(896, 128, 896), (256, 64, 512), (100, 20, 256)])
+def test_fused_qkv_bias_q8_0(ctx, q_dim, kv_dim, k):
+    _qkv_case(ctx, "q8_0", q_dim, kv_dim, k, True, seed=q_dim)
+
+
+def test_fused_qkv_no_bias_q8_0(ctx):
+    _qkv_case(ctx, "q8_0", 896, 128, 896, False, seed=3)
+
+
+@pytest.mark.parametrize("q_dim,kv_dim,k", [(3584, 512, 3584), (256, 64, 512)])
+def test_fused_qkv_bias_q4_0(ctx, q_dim, kv_dim, k):
+    _qkv_case(ctx, "q4_0", q_dim, kv_dim, k, True, seed=q_dim + 1)
+
+
+def ffn_check(got, gate_ref, gate_s, up_ref, up_s, what):
+    """act = silu(g)·u with |g−g_ref| ≤ eg, |u−u_ref| ≤ eu: |silu'| ≤ 1.1 gives
+    |Δact| ≤ 1.1·eg·(|u|+eu) + (|silu(g)|+1.1·eg)·eu, plus f32 epilogue rounding."""
+    eg, eu = REL * gate_s, REL * up_s
+    sil = np.array([ora.silu(g) for g in gate_ref])
+    ref = sil * up_ref
+    tol = 1.1 * eg * (np.abs(up_ref) + eu) + (np.abs(sil) + 1.1 * eg) * eu + 4 * F32_EPS * np.abs(ref)
+    err = np.abs(got.astype(np.float64) - ref)
+    bad = ~(err <= tol)
+    assert not bad.any(), f"{what}: {int(bad.sum())} outside; worst {err[bad].max():.3e}"
+
+
+@pytest.mark.parametrize("fmt,ff,k", [("q8_0", 4864, 896), ("q8_0", 300, 512),
+                                      ("q4_0", 1000, 3584), ("q4_0", 77, 256),
+                                      ("q4k", 1000, 3584), ("q4k", 33, 512)])
+def test_fused_ffn(ctx, fmt, ff, k):
+    wg, rg = device_weights(ctx, fmt, ff, k, seed=ff + 1)
+    wu, ru = device_weights(ctx, fmt, ff, k, seed=ff + 2)
+    x = np.random.default_rng(ff).standard_normal(k).astype(np.float32)
+    act = ctx.new_buffer(4 * ff)
+    getattr(d, f"fused_ffn_{fmt}_f32")(ctx, wg, wu, ctx.buffer_from(x), act, ff, k)
+    ctx.flush()
+    g, gs = ora.gemv(fmt, rg, x, ff, k)
+    u, us = ora.gemv(fmt, ru, x, ff, k)
+    ffn_check(act.read(np.float32, ff), g, gs, u, us, f"ffn {fmt} {ff}x{k}")
+
+
+# ───────────────────────── argmax ─────────────────────────
+
+@pytest.mark.parametrize("n", [1, 5, 1000, 1024, 1025, 151936, 152064])
+def test_argmax_random(ctx, n):
+    v = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    res = ctx.new_buffer(4)
+    d.argmax_f32(ctx, ctx.buffer_from(v), res, n)
+    ctx.flush()
+    assert int(res.read(np.uint32, 1)[0]) == ora.argmax(v)
+
+
+def test_argmax_ties_and_nan_follow_rust_max_by(ctx):
+    nan = np.float32("nan")
+    rng = np.random.default_rng(0)
+    cases = [np.zeros(5000, np.float32), np.full(3000, -np.inf, np.float32)]
+    v = rng.standard_normal(70000).astype(np.float32)
+    v[[10, 5000, 69000]] = 9.0
+    cases.append(v)
+    for pos in (0, 17, 40000, 69999):
+        w = rng.standard_normal(70000).astype(np.float32)
+        w[pos] = nan
+        cases.append(w)
+    w = rng.standard_normal(50000).astype(np.float32)
+    w[[5, 30000]] = nan
+    w[20000] = 50.0
+    w[45000] = 7.0
+    cases.append(w)
+    res = ctx.new_buffer(4)
+    for c in cases:
+        d.argmax_f32(ctx, ctx.buffer_from(c), res, c.size)
+        ctx.flush()
+        assert int(res.read(np.uint32, 1)[0]) == ora.argmax(c)
+
+
+def test_argmax_f16(ctx):
+    v = np.random.default_rng(9).standard_normal(151936).astype(np.float16)
+    res = ctx.new_buffer(4)
+    d.argmax_f16(ctx, ctx.buffer_from(v), res, v.size)
+    ctx.flush()
+    assert int(res.read(np.uint32, 1)[0]) == ora.argmax(v.astype(np.float32))
+
+
+# ───────────────────────── batched Q8_0 GEMM ─────────────────────────
+
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("n,k", [(512, 1024), (130, 3584)])
+def test_gemm_q8_0(ctx, m, n, k):
+    wbuf, raw = device_weights(ctx, "q8_0", n, k, seed=m + n)
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    y = ctx.new_buffer(4 * m * n)
+    d.gemm_q8_0_f32(ctx, wbuf, ctx.buffer_from(x), y, m, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv("q8_0", raw, x, n, k)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm m={m}")

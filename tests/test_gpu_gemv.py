@@ -1,0 +1,203 @@
+"""GPU parity of the quantized GEMV family against the CPU oracle.
+
+Every call goes through the C ABI (librunit_hip.so) via the dispatch mirror.
+Tolerance (BASELINE): |y − y_ref| ≤ 1e-4·Σ|w_i·x_i| per row, y_ref in f64;
+f16 outputs additionally get one binary16 rounding (gpu_helpers.f16_extra);
+dequantisation is compared bit for bit.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as ora
+from gpu_helpers import (F32_EPS, check_close, device_normal, device_weights, f16_extra,
+                         f16_to_f64)
+from runit_mac_amd import dispatch as d
+
+pytestmark = pytest.mark.gpu
+
+FMTS = ["q8_0", "q4_0", "q4k", "q6k"]
+
+VARIANTS = {
+    "q8_0": ["f32in_f32out", "add_f32_f32in", "f32in", "f16", "add_f16", "add_f32res_f16",
+             "f32in_f32out_mr", "add_f32_f32in_mr"],
+    "q4_0": ["f32in_f32out", "add_f32_f32in", "f32in", "f16", "add_f16"],
+    "q4k": ["f32in_f32out", "add_f32_f32in", "f16", "add_f16", "add_f32res_f16"],
+    "q6k": ["f32in_f32out", "add_f32_f32in", "f32in"],
+}
+
+
+def run_variant(ctx, fmt, var, wbuf, wraw, n, k, seed):
+    """Runs dispatch.gemv_<fmt>_<var> on seeded inputs and checks it."""
+    rng = np.random.default_rng(seed)
+    x_f16_in = var in ("f16", "add_f16", "add_f32res_f16")
+    x32 = rng.standard_normal(k).astype(np.float32)
+    if x_f16_in:
+        x16 = x32.astype(np.float16)
+        x32 = x16.astype(np.float32)
+        xbuf = ctx.buffer_from(x16)
+    else:
+        xbuf = ctx.buffer_from(x32)
+    yref, sabs = ora.gemv(fmt, wraw, x32, n, k)
+    fn = getattr(d, f"gemv_{fmt}_{var}")
+    out_f16 = var in ("f32in", "f16", "add_f16")
+    ybuf = ctx.new_buffer(n * (2 if out_f16 else 4))
+    if var.startswith("add"):
+        res32 = rng.standard_normal(n).astype(np.float32)
+        if var == "add_f16":
+            res16 = res32.astype(np.float16)
+            res32 = res16.astype(np.float32)
+            rbuf = ctx.buffer_from(res16)
+        else:
+            rbuf = ctx.buffer_from(res32)
+        fn(ctx, wbuf, xbuf, ybuf, rbuf, n, k)
+        ref = yref + res32.astype(np.float64)
+    else:
+        fn(ctx, wbuf, xbuf, ybuf, n, k)
+        ref = yref
+    ctx.flush()
+    if out_f16:
+        got = f16_to_f64(ybuf.read(np.uint16, n))
+        check_close(got, ref, sabs, f"{fmt}/{var} {n}x{k}", f16_extra(ref, sabs))
+    else:
+        got = ybuf.read(np.float32, n)
+        check_close(got, ref, sabs, f"{fmt}/{var} {n}x{k}", F32_EPS * np.abs(ref))
+
+
+# ───────────────────────── dequantisation: bit-exact ─────────────────────────
+
+def _bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.array_equal(a.view(np.uint32)[~nan], b.view(np.uint32)[~nan]) and
+                np.array_equal(np.isnan(a), np.isnan(b)))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_dequant_bit_exact_synth(ctx, fmt):
+    el, by = d.BLOCK[fmt]
+    n, k = 48, 1024
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=101)
+    nblk = n * k // el
+    out = ctx.new_buffer(4 * n * k)
+    d.dequant_f32(ctx, fmt, wbuf, out, nblk)
+    ctx.flush()
+    assert _bits_equal(out.read(np.float32, n * k), ora.dequant(fmt, raw))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_dequant_bit_exact_random_bytes(ctx, fmt):
+    # arbitrary bit patterns: subnormal / Inf / NaN scales, every code value
+    el, by = d.BLOCK[fmt]
+    nblk = 333
+    raw = np.random.default_rng(7).integers(0, 256, nblk * by, dtype=np.uint8)
+    out = ctx.new_buffer(4 * nblk * el)
+    d.dequant_f32(ctx, fmt, ctx.buffer_from(raw), out, nblk)
+    ctx.flush()
+    assert _bits_equal(out.read(np.float32, nblk * el), ora.dequant(fmt, raw))
+
+
+def test_dequant_q4k_f16_bit_exact(ctx):
+    nblk = 257
+    raw = np.random.default_rng(8).integers(0, 256, nblk * 144, dtype=np.uint8)
+    out = ctx.new_buffer(2 * nblk * 256)
+    d.dequant_q4k_f16(ctx, ctx.buffer_from(raw), out, nblk)
+    ctx.flush()
+    got = out.read(np.uint16, nblk * 256)
+    ref = ora.dequant_q4k_f16(raw)
+    gn = np.isnan(got.view(np.float16))
+    rn = np.isnan(ref.view(np.float16))
+    assert np.array_equal(gn, rn) and np.array_equal(got[~gn], ref[~rn])
+
+
+# ───────────────────────── GEMV variants ─────────────────────────
+
+SHAPES = [(64, 256), (37, 512), (300, 768), (1, 2048), (129, 1536)]
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_gemv_variants(ctx, fmt, n, k):
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=1000 + n + k)
+    for i, var in enumerate(VARIANTS[fmt]):
+        run_variant(ctx, fmt, var, wbuf, raw, n, k, seed=17 * i + n)
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0"])
+@pytest.mark.parametrize("k", [32, 64, 96, 160])
+def test_gemv_small_and_odd_block_counts(ctx, fmt, k):
+    n = 77
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=5 + k)
+    run_variant(ctx, fmt, "f32in_f32out", wbuf, raw, n, k, seed=k)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_gemv_long_k_staged_in_chunks(ctx, fmt):
+    # K = 32768 → 1024 activation records = 112 KiB > the per-pass LDS budget,
+    # so the kernel restages the activations in several passes.
+    n, k = 96, 32768
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=77)
+    run_variant(ctx, fmt, "f32in_f32out", wbuf, raw, n, k, seed=3)
+    run_variant(ctx, fmt, "add_f32_f32in", wbuf, raw, n, k, seed=4)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_gemv_output_aliases_residual(ctx, fmt):
+    # forward.rs:1619,1702 pass the same buffer as output and residual
+    n, k = 513, 1024
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=9)
+    x = np.random.default_rng(1).standard_normal(k).astype(np.float32)
+    res = np.random.default_rng(2).standard_normal(n).astype(np.float32)
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    buf = ctx.buffer_from(res)
+    getattr(d, f"gemv_{fmt}_add_f32_f32in")(ctx, wbuf, ctx.buffer_from(x), buf, buf, n, k)
+    ctx.flush()
+    ref = yref + res
+    check_close(buf.read(np.float32, n), ref, sabs, f"{fmt} aliased", F32_EPS * np.abs(ref))
+
+
+def test_gemv_heavy_tailed_activations(ctx):
+    # activations with 100× outliers inside blocks (post-norm LLM activations
+    # have such channels): the limb form keeps 22 bits below the block max
+    n, k = 256, 4096
+    wbuf, raw = device_weights(ctx, "q8_0", n, k, seed=12)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(k).astype(np.float32)
+    x[rng.integers(0, k, 40)] *= 100.0
+    yref, sabs = ora.gemv("q8_0", raw, x, n, k)
+    y = ctx.new_buffer(4 * n)
+    d.gemv_q8_0_f32in_f32out(ctx, wbuf, ctx.buffer_from(x), y, n, k)
+    ctx.flush()
+    check_close(y.read(np.float32, n), yref, sabs, "heavy-tailed x")
+
+
+def test_gemv_zero_and_tiny_activations(ctx):
+    n, k = 64, 512
+    wbuf, raw = device_weights(ctx, "q4k", n, k, seed=13)
+    x = np.zeros(k, np.float32)
+    x[100:132] = np.float32(1e-40)  # subnormal block
+    x[300] = np.float32(3.0e-30)
+    yref, sabs = ora.gemv("q4k", raw, x, n, k)
+    y = ctx.new_buffer(4 * n)
+    d.gemv_q4k_f32in_f32out(ctx, wbuf, ctx.buffer_from(x), y, n, k)
+    ctx.flush()
+    check_close(y.read(np.float32, n), yref, sabs, "tiny x", 1e-44)
+
+
+def test_gemv_rejects_bad_k(ctx):
+    w = ctx.new_buffer(1024)
+    x = ctx.new_buffer(1024)
+    y = ctx.new_buffer(1024)
+    with pytest.raises(d.Dispatch):
+        d.gemv_q8_0_f32in_f32out(ctx, w, x, y, 4, 48)
+    with pytest.raises(d.Dispatch):
+        d.gemv_q4k_f32in_f32out(ctx, w, x, y, 4, 128)
+    with pytest.raises(d.Dispatch):  # misaligned activation pointer
+        d.gemv_q8_0_f32in_f32out(ctx, w, x.ptr + 4, y, 4, 64)
+    # m = 0 is a no-op, like a zero-width Metal dispatch
+    d.gemv_q8_0_f32in_f32out(ctx, w, x, y, 0, 64)
+    ctx.flush()
+
+
+def test_pipeline_lookup(ctx):
+    ctx.has_kernel("k_gemv_q8_0_f32_f32")
+    with pytest.raises(d.PipelineNotFound):
+        ctx.has_kernel("no_such_kernel")

@@ -1,0 +1,286 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+The reference's own tests hold no golden vectors for quantized GEMV, fused
+QKV/FFN, Q4_0, Q4_K or Q6_K numerics (its only kernel tests are f16 GEMV /
+attention / norm tests, crates/kernels/src/dispatch.rs:1777-2004).  So each
+oracle function is pinned here by checks that a plausible mistake would fail:
+hand-built known-answer blocks for every layout quirk of the reference, the
+reference's own zero-quant fixtures (crates/engine/tests/qwen2_load_test.rs:
+105-134), the closed-form GEMV cases of crates/engine/src/bin/test_gemv.rs:
+58-85 re-expressed with quantized blocks, an independent library routine
+(numpy's IEEE float16 conversion), brute-force dot products, invariants of the
+quantisers, and the Rust `max_by` fold semantics for argmax.
+"""
+import struct
+
+import numpy as np
+import pytest
+
+import oracle_lib as ora
+
+
+def h16(v: float) -> bytes:
+    return np.float16(v).tobytes()
+
+
+# ───────────────────────── f16 conversions ─────────────────────────
+
+def test_h2f_all_halves_match_numpy():
+    hs = np.arange(65536, dtype=np.uint16)
+    ref = hs.view(np.float16).astype(np.float32)
+    got = np.array([ora.h2f(int(h)) for h in hs], dtype=np.float32)
+    both_nan = np.isnan(ref) & np.isnan(got)
+    assert np.array_equal(ref.view(np.uint32)[~both_nan], got.view(np.uint32)[~both_nan])
+
+
+def test_f2h_round_to_nearest_even_matches_numpy():
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 20000),
+        # exact ties between adjacent halves, subnormal ties, overflow edge
+        (np.arange(1, 2000, dtype=np.float32) + 0.5) * np.float32(2.0 ** -10),
+        (np.arange(0, 1024, dtype=np.float32) + 0.5) * np.float32(2.0 ** -24),
+        np.array([65504, 65519.99, 65520, 65536, 1e-8, 2.0 ** -25, 2.0 ** -25 * 1.0001,
+                  -0.0, np.inf, -np.inf], dtype=np.float32),
+    ]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([ora.f2h(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(ref, got)
+
+
+# ───────────────────────── dequant known answers ─────────────────────────
+
+def test_q8_0_known_block():
+    # d = 1, q = i − 16  →  v = i − 16 ; second block d = 0.5 → halves
+    b1 = h16(1.0) + bytes((i - 16) & 255 for i in range(32))
+    b2 = h16(0.5) + bytes((i - 16) & 255 for i in range(32))
+    v = ora.dequant("q8_0", np.frombuffer(b1 + b2, np.uint8))
+    assert np.array_equal(v[:32], np.arange(32) - 16)
+    assert np.array_equal(v[32:], (np.arange(32) - 16) * 0.5)
+
+
+def test_q4_0_reference_nibble_order():
+    # byte i holds element 2i (low nibble) and 2i+1 (high nibble)
+    # (gemv_q4_0.metal:13-14, forward.rs:974-976) — not ggml's j / j+16 split.
+    qs = bytes(((2 * i) & 15) | (((2 * i + 1) & 15) << 4) for i in range(16))
+    v = ora.dequant("q4_0", np.frombuffer(h16(2.0) + qs, np.uint8))
+    expect = 2.0 * (((np.arange(32)) & 15) - 8)
+    assert np.array_equal(v, expect)
+    # a single byte 0x21 → elements [1−8, 2−8]
+    qs = bytes([0x21]) + bytes([0x88] * 15)
+    v = ora.dequant("q4_0", np.frombuffer(h16(1.0) + qs, np.uint8))
+    assert v[0] == -7 and v[1] == -6 and np.all(v[2:] == 0)
+
+
+def _q4k_block(d, dmin, sc, m, q):
+    """Packs a Q4_K block with 6-bit (sc, m) per scale index s (0..7) and
+    4-bit codes q[256] in the reference layout (element 64j+l low nibble,
+    64j+32+l high nibble of qs[32j+l])."""
+    S = [0] * 12
+    for j in range(4):
+        S[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        S[j + 4] = (m[j] & 63) | ((m[j + 4] >> 4) << 6)
+        S[j + 8] = (sc[j + 4] & 15) | ((m[j + 4] & 15) << 4)
+    qs = bytearray(128)
+    for j in range(4):
+        for l in range(32):
+            qs[32 * j + l] = q[64 * j + l] | (q[64 * j + 32 + l] << 4)
+    return h16(d) + h16(dmin) + bytes(S) + bytes(qs)
+
+
+def test_q4k_scale_pairing_j_and_j_plus_4():
+    # Only scale index 5 (= pair j=1, high nibbles) is non-zero: elements
+    # 96..127 get d·sc5·q; the reference pairs (j, j+4), ggml pairs (2j, 2j+1),
+    # which would light up elements 160..191 instead.
+    sc = [0, 0, 0, 0, 0, 37, 0, 0]
+    m = [0] * 8
+    q = [(i * 7) & 15 for i in range(256)]
+    v = ora.dequant("q4k", np.frombuffer(_q4k_block(0.25, 0.0, sc, m, q), np.uint8))
+    nz = np.nonzero(v)[0]
+    assert nz.min() >= 96 and nz.max() <= 127
+    for e in range(96, 128):
+        assert v[e] == np.float32(0.25 * 37) * np.float32(q[e])
+
+
+def test_q4k_six_bit_high_scales_and_mins():
+    # 6-bit values ≥ 16 in scale indices 4..7 exercise the split packing
+    # (low 4 bits in bytes 8..11, top 2 bits in bytes 0..7) of get_scale_min_k4
+    sc = [1, 2, 3, 4, 63, 17, 48, 33]
+    m = [5, 6, 7, 8, 62, 31, 16, 47]
+    q = [((i * 5) + 3) & 15 for i in range(256)]
+    d, dmin = 0.0625, 0.03125
+    v = ora.dequant("q4k", np.frombuffer(_q4k_block(d, dmin, sc, m, q), np.uint8))
+    for e in range(256):
+        s = (e // 64) + 4 * ((e // 32) & 1)
+        expect = np.float32(np.float32(d * sc[s]) * np.float32(q[e])) - np.float32(dmin * m[s])
+        assert v[e] == expect, e
+
+
+def test_q4k_zero_quant_fixture_from_reference_test():
+    # qwen2_load_test.rs:105-119: d = 1, dmin = 0, scales = 0, qs = 0
+    blk = bytearray(144)
+    blk[0:2] = h16(1.0)
+    v = ora.dequant("q4k", np.frombuffer(bytes(blk) * 3, np.uint8))
+    assert np.all(v == 0)
+
+
+def _q6k_block(d, sc16, q):
+    ql = bytearray(128)
+    qh = bytearray(64)
+    for h in (0, 128):
+        for l in range(32):
+            q1, q2, q3, q4 = q[h + l], q[h + l + 32], q[h + l + 64], q[h + l + 96]
+            ql[h // 2 + l] = (q1 & 15) | ((q3 & 15) << 4)
+            ql[h // 2 + l + 32] = (q2 & 15) | ((q4 & 15) << 4)
+            qh[h // 4 + l] = (q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6)
+    return bytes(ql) + bytes(qh) + bytes(s & 255 for s in sc16) + h16(d)
+
+
+def test_q6k_only_even_scale_slots_are_read():
+    # forward.rs:935 uses is = n_half/16 and slots is+0,2,4,6: the odd slots
+    # (which ggml would use for elements 16..31 of each 32) are ignored.
+    q = [(i * 11 + 5) % 64 for i in range(256)]
+    sc_a = [3, -7, 5, 9, -2, 4, 6, 1, -8, 2, 7, -5, 11, 3, -1, 6]
+    sc_b = list(sc_a)
+    for i in range(1, 16, 2):
+        sc_b[i] = 100 - i
+    va = ora.dequant("q6k", np.frombuffer(_q6k_block(0.5, sc_a, q), np.uint8))
+    vb = ora.dequant("q6k", np.frombuffer(_q6k_block(0.5, sc_b, q), np.uint8))
+    assert np.array_equal(va, vb)
+    for e in range(256):
+        h, t = (e // 128) * 128, (e % 128) // 32
+        s = sc_a[h // 16 + 2 * t]
+        assert va[e] == np.float32(np.float32(0.5 * s) * np.float32(q[e] - 32)), e
+
+
+def test_q6k_zero_quant_fixture_from_reference_test():
+    # qwen2_load_test.rs:121-134: d = 1, ql = qh = scales = 0 → d·0·(0−32) = −0.0
+    blk = bytearray(210)
+    blk[208:210] = h16(1.0)
+    v = ora.dequant("q6k", np.frombuffer(bytes(blk), np.uint8))
+    assert np.all(v == 0) and np.all(np.signbit(v))
+
+
+def test_q4k_f16_matches_f32_then_rne():
+    rng = np.random.default_rng(3)
+    raw = ora.synth_weights("q4k", 4, 256, seed=5)
+    v32 = ora.dequant("q4k", raw)
+    v16 = ora.dequant_q4k_f16(raw)
+    assert np.array_equal(v32.astype(np.float16).view(np.uint16), v16)
+    del rng
+
+
+# ───────────────────────── GEMV closed forms / brute force ─────────────────────────
+
+def _ones_blocks(fmt, n, k):
+    """Blocks whose every element decodes to exactly 1.0."""
+    if fmt == "q8_0":
+        blk = h16(1.0) + bytes([1] * 32)
+        nb = k // 32
+    elif fmt == "q4_0":
+        blk = h16(1.0) + bytes([0x99] * 16)  # nib 9 → 9 − 8 = 1
+        nb = k // 32
+    elif fmt == "q4k":
+        blk = _q4k_block(1.0, 0.0, [1] * 8, [0] * 8, [1] * 256)
+        nb = k // 256
+    else:
+        blk = _q6k_block(1.0, [1] * 16, [33] * 256)
+        nb = k // 256
+    return np.frombuffer(blk * (n * nb), np.uint8)
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k"])
+def test_gemv_all_ones_closed_form(fmt):
+    # test_gemv.rs:58-85: all-ones 32×32 · [1..32] = 528 per row; at K=256:
+    # Σ 1..256 = 32896.
+    k = 32 if fmt in ("q8_0", "q4_0") else 256
+    n = 5
+    w = _ones_blocks(fmt, n, k)
+    x = np.arange(1, k + 1, dtype=np.float32)
+    y, s = ora.gemv(fmt, w, x, n, k)
+    assert np.all(y == k * (k + 1) / 2)
+    assert np.all(s == k * (k + 1) / 2)
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k"])
+def test_gemv_brute_force(fmt):
+    n, k = 7, 512
+    w = ora.synth_weights(fmt, n, k, seed=11)
+    x = np.random.default_rng(2).standard_normal(k).astype(np.float32)
+    y, s = ora.gemv(fmt, w, x, n, k)
+    W = ora.dequant(fmt, w).reshape(n, k).astype(np.float64)
+    for r in range(n):
+        acc = 0.0
+        sa = 0.0
+        for c in range(k):
+            acc += W[r, c] * float(x[c])
+            sa += abs(W[r, c] * float(x[c]))
+        assert abs(acc - y[r]) <= 1e-12 * sa
+        assert abs(sa - s[r]) <= 1e-12 * sa
+    # identity-like: one-hot x picks a column exactly
+    e = np.zeros(k, np.float32)
+    e[37] = 1.0
+    y1, _ = ora.gemv(fmt, w, e, n, k)
+    assert np.array_equal(y1, W[:, 37])
+
+
+def test_gemv_ref_f32_is_sequential_f32_sum():
+    n, k = 3, 64
+    w = ora.synth_weights("q8_0", n, k, seed=4)
+    x = np.random.default_rng(5).standard_normal(k).astype(np.float32)
+    W = ora.dequant("q8_0", w).reshape(n, k)
+    y = ora.gemv_ref_f32("q8_0", w, x, n, k)
+    for r in range(n):
+        acc = np.float32(0.0)
+        for c in range(k):
+            acc = np.float32(acc + np.float32(W[r, c] * x[c]))
+        assert y[r] == acc
+
+
+# ───────────────────────── silu / argmax ─────────────────────────
+
+def test_silu_closed_forms():
+    assert ora.silu(0.0) == 0.0
+    assert abs(ora.silu(1.0) - 1.0 / (1.0 + np.exp(-1.0))) < 1e-15
+    assert abs(ora.silu(-30.0)) < 1e-11
+    assert abs(ora.silu(30.0) - 30.0) < 1e-11
+
+
+def test_argmax_rust_max_by_semantics():
+    nan = np.float32("nan")
+    cases = [
+        ([], 0),
+        ([5.0], 0),
+        ([1.0, 3.0, 3.0, 2.0], 2),             # ties → last maximal index
+        ([3.0, 1.0, 3.0], 2),
+        ([-np.inf, -np.inf], 1),
+        ([1.0, nan, 0.5], 2),                  # NaN compares Equal: replaced, then replaced
+        ([9.0, 1.0, nan], 2),                  # trailing NaN wins
+        ([nan, 2.0, 7.0, 3.0], 2),
+        ([4.0, nan, 1.0, 2.0, 2.0], 4),
+    ]
+    for vals, expect in cases:
+        assert ora.argmax(np.array(vals, np.float32)) == expect, vals
+
+
+# ───────────────────────── quantiser invariants ─────────────────────────
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k"])
+def test_quantizer_round_trip_error_bounded(fmt):
+    n_el = 256 * 16
+    w = (0.02 * ora.synth_normal(99, n_el)).astype(np.float32)
+    v = ora.dequant(fmt, ora.quantize(fmt, w))
+    err = np.abs(v - w)
+    el = 32 if fmt in ("q8_0", "q4_0") else 256
+    amax = np.abs(w).reshape(-1, el).max(axis=1).repeat(el)
+    # half a step plus the f16 rounding of the scale: Q8_0 step amax/127
+    # (q uses the unrounded d, so up to 127·2^-11 steps more), Q4_0 amax/8
+    # (plus one clamped step at +8), Q4_K ≈ range/15, Q6_K amax/32
+    bound = {"q8_0": 0.6 / 127, "q4_0": 1.01 / 8, "q4k": 0.2, "q6k": 0.08}[fmt]
+    assert np.all(err <= bound * amax + 1e-7)
+
+
+def test_synth_normal_moments():
+    z = ora.synth_normal(7, 20000)
+    assert abs(z.mean()) < 0.03 and abs(z.std() - 1.0) < 0.03
