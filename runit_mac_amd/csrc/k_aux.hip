@@ -64,7 +64,12 @@ extern "C" __global__ void __launch_bounds__(256)
 k_dequant_q4k_f16(const uint8_t* __restrict__ in, uint16_t* __restrict__ out, uint64_t n_el) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_el) return;
-    out[i] = f2h(q4k_value(in + (i >> 8) * 144, (uint32_t)(i & 255)));
+    float v = q4k_value(in + (i >> 8) * 144, (uint32_t)(i & 255));
+    // Materialise the f32 value before the f16 conversion: the reference
+    // rounds to f32 first, then to half (double rounding); without the
+    // barrier the compiler fuses d·q − m with the conversion (one rounding).
+    asm volatile("" : "+v"(v));
+    out[i] = f2h(v);
 }
 
 extern "C" __global__ void __launch_bounds__(256)
