@@ -240,6 +240,14 @@ int rt_synth_q4_0(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, floa
 int rt_synth_q4k(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
 int rt_synth_q6k(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
 
+/* ───────────────────────── calibration (bench only) ─────────────────────────
+ * Plain HBM streams of known size; no reference counterpart.  stream_read
+ * reads `bytes` (multiple of 16) and writes one dword per wave to `sink`
+ * (sink needs grid·4 dwords; pass sink_dwords); stream_copy copies `bytes`. */
+int rt_stream_read(rt_ctx* ctx, const void* src, size_t bytes, uint32_t* sink,
+                   size_t sink_dwords);
+int rt_stream_copy(rt_ctx* ctx, void* dst, const void* src, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -343,3 +343,37 @@ k_synth_q6k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
         p[208] = dh & 255; p[209] = dh >> 8;
     }
 }
+
+// ───────────────────────────── calibration ─────────────────────────────
+// Plain HBM streams of known size: the achievable-bandwidth reference for the
+// GEMV kernels and the scale for rocprof's FETCH_SIZE / WRITE_SIZE counters.
+
+// Reads n16 16-byte vectors (grid-stride, 4 in flight per thread) and writes
+// one xor-folded dword per workgroup so the loads cannot be elided.
+extern "C" __global__ void __launch_bounds__(256)
+k_stream_read(const u32x4* __restrict__ src, uint64_t n16, uint32_t* __restrict__ sink) {
+    uint32_t acc = 0;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        u32x4 a = __builtin_nontemporal_load(src + i);
+        u32x4 b = __builtin_nontemporal_load(src + i + stride);
+        u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+        u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^
+               d.z ^ d.w;
+    }
+    for (; i < n16; i += stride) {
+        u32x4 a = src[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o, 64);
+    if ((threadIdx.x & 63) == 0) sink[blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)] = acc;
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+k_stream_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst, uint64_t n16) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        dst[i] = src[i];
+}

@@ -82,99 +82,339 @@ RT_DEV void store_row(const GemvArgs& a, uint32_t vr, float v) {
     }
 }
 
-template <class F, int EPI, typename XT, int RPL>
-RT_DEV void gemv_body(const GemvArgs& a) {
-    extern __shared__ XRec xs[];
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t nwaves = blockDim.x >> 6;
-    const uint32_t lpr = a.lpr;
-    const uint32_t g = lane / lpr, j = lane % lpr;
-    const uint32_t groups = 64 / lpr;
-    const uint32_t vrows_per_wave = groups * RPL;
-    const uint32_t vrows_per_wg = nwaves * vrows_per_wave;
-    const uint32_t nxb = a.K / 32;
-    const uint32_t ntiles = (a.nvrows + vrows_per_wg - 1) / vrows_per_wg;
-    const XT* x = (const XT*)a.x;
-    const bool one_chunk = a.xb_chunk >= nxb;
-
-    if (one_chunk) {
-        stage_x_limbs<XT, F::Q40PERM>(x, 0, nxb, xs);
+// Reduction over a row group (TL lanes, possibly several waves) followed by
+// the epilogue in the group's first lane.
+template <int EPI, int RPL>
+RT_DEV void finish_rows(const GemvArgs& a, float* red, uint32_t tid, uint32_t TL, uint32_t grp,
+                        uint32_t kl, uint32_t vr0, float acc[RPL]) {
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) acc[i] = group_sum(acc[i], (int)min(TL, 64u));
+    if (TL > 64) {
+        // the row group spans TL/64 waves: combine their sums through LDS in a
+        // fixed order (deterministic)
+        const uint32_t wave = tid >> 6, wpr = TL / 64;
+        if ((tid & 63) == 0) {
+#pragma unroll
+            for (int i = 0; i < RPL; ++i) red[wave * RPL + i] = acc[i];
+        }
+        __syncthreads();
+        if (kl == 0) {
+#pragma unroll
+            for (int i = 0; i < RPL; ++i) {
+                float t = 0.0f;
+                for (uint32_t w = 0; w < wpr; ++w) t += red[(grp * wpr + w) * RPL + i];
+                acc[i] = t;
+            }
+        }
         __syncthreads();
     }
-
-    for (uint32_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const uint32_t vr0 = tile * vrows_per_wg + wave * vrows_per_wave + g * RPL;
-        const uint8_t* rowp[RPL];
+    if (kl == 0) {
+        if (EPI == EPI_FFN) {
 #pragma unroll
-        for (int i = 0; i < RPL; ++i) {
-            uint32_t vr = vr0 + i;
-            if (vr >= a.nvrows) vr = a.nvrows - 1;  // clamp loads; store is skipped
-            uint32_t mat, r;
-            vrow_map<EPI>(a, vr, mat, r);
-            rowp[i] = a.w[mat] + (size_t)r * a.row_bytes;
-        }
-        float acc[RPL];
-#pragma unroll
-        for (int i = 0; i < RPL; ++i) acc[i] = 0.0f;
-
-        for (uint32_t xc = 0; xc < nxb; xc += a.xb_chunk) {
-            const uint32_t nx = min(a.xb_chunk, nxb - xc);
-            if (!one_chunk) {
-                __syncthreads();
-                stage_x_limbs<XT, F::Q40PERM>(x, xc, nx, xs);
-                __syncthreads();
+            for (int i = 0; i + 1 < RPL; i += 2) {
+                const uint32_t vr = vr0 + i;
+                if (vr + 1 < a.nvrows) {
+                    // act[r] = silu(gate)·up  (fused_ffn.metal:90-92)
+                    ((float*)a.out[0])[vr >> 1] = silu_ref(acc[i]) * acc[i + 1];
+                }
             }
-            const uint32_t units = nx * 32 / F::UNIT_EL;
-            const uint32_t u0 = xc * 32 / F::UNIT_EL;
-            for (uint32_t uu = j; uu < units; uu += lpr) {
-                typename F::Raw raw[RPL];
+        } else {
 #pragma unroll
-                for (int i = 0; i < RPL; ++i) F::load(rowp[i], u0 + uu, raw[i]);
-                typename F::XU xu;
-                F::load_x(xs, uu, xu);
-#pragma unroll
-                for (int i = 0; i < RPL; ++i) acc[i] += F::dot(raw[i], xu);
+            for (int i = 0; i < RPL; ++i) {
+                if (vr0 + i < a.nvrows) store_row<EPI>(a, vr0 + i, acc[i]);
             }
         }
-#pragma unroll
-        for (int i = 0; i < RPL; ++i) acc[i] = group_sum(acc[i], (int)lpr);
+    }
+}
 
-        if (j == 0) {
-            if (EPI == EPI_FFN) {
+template <int EPI, int RPL>
+RT_DEV void tile_rows(const GemvArgs& a, uint32_t vr0, const uint8_t* rowp[RPL]) {
 #pragma unroll
-                for (int i = 0; i + 1 < RPL; i += 2) {
-                    const uint32_t vr = vr0 + i;
-                    if (vr + 1 < a.nvrows) {
-                        // act[r] = silu(gate)·up  (fused_ffn.metal:90-92)
-                        ((float*)a.out[0])[vr >> 1] = silu_ref(acc[i]) * acc[i + 1];
+    for (int i = 0; i < RPL; ++i) {
+        uint32_t vr = vr0 + i;
+        if (vr >= a.nvrows) vr = a.nvrows - 1;  // clamp loads; the store is skipped
+        uint32_t mat, r;
+        vrow_map<EPI>(a, vr, mat, r);
+        rowp[i] = a.w[mat] + (size_t)r * a.row_bytes;
+    }
+}
+
+// Whole-K path (all activation records fit in LDS).  Each lane walks a flat
+// sequence of (tile, step) items; a step is UNR units of RPL rows.  The weight
+// loads of item n+1 are issued before item n is computed (two register
+// buffers), and the loads of the first item are issued before the activation
+// staging, so the staging latency hides behind HBM latency.
+template <class F, int EPI, typename XT, int RPL, int UNR>
+RT_DEV void gemv_body_pipelined(const GemvArgs& a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    XRec* xs = (XRec*)smem;
+    float* red = (float*)(smem + (size_t)a.xb_chunk * sizeof(XRec));
+    const uint32_t tid = threadIdx.x;
+    const uint32_t TL = a.lpr;
+    const uint32_t grp = tid / TL, kl = tid % TL;
+    const uint32_t vrows_per_wg = (blockDim.x / TL) * RPL;
+    const uint32_t nxb = a.K / 32;
+    const uint32_t ntiles = (a.nvrows + vrows_per_wg - 1) / vrows_per_wg;
+    const uint32_t units = a.K / F::UNIT_EL;
+    const uint32_t nsteps = (units + UNR * TL - 1) / (UNR * TL);
+    const uint32_t my_tiles =
+        blockIdx.x < ntiles ? (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    const uint32_t nitems = my_tiles * nsteps;
+
+    typename F::Raw buf[2][UNR][RPL];
+    const uint8_t* rowp[RPL];
+
+    auto issue = [&](uint32_t item, typename F::Raw (&dst)[UNR][RPL]) {
+        const uint32_t tile = blockIdx.x + (item / nsteps) * gridDim.x;
+        const uint32_t step = item % nsteps;
+        const uint8_t* rp[RPL];
+        tile_rows<EPI, RPL>(a, tile * vrows_per_wg + grp * RPL, rp);
+#pragma unroll
+        for (int s = 0; s < UNR; ++s) {
+            const uint32_t uu = kl + (step * UNR + s) * TL;
+            if (uu < units) {
+#pragma unroll
+                for (int i = 0; i < RPL; ++i) F::load(rp[i], uu, dst[s][i]);
+            }
+        }
+    };
+
+    if (nitems > 0) issue(0, buf[0]);
+#ifndef RT_PROBE_NO_STAGE
+    stage_x_limbs<XT, F::Q40PERM>((const XT*)a.x, 0, nxb, xs);
+#endif
+    __syncthreads();
+    if (nitems == 0) return;
+    (void)rowp;
+
+    float acc[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) acc[i] = 0.0f;
+
+    // two-deep pipeline, unrolled by two so the buffers are addressed statically
+    for (uint32_t it = 0; it < nitems; it += 2) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const uint32_t item = it + half;
+            if (item < nitems) {
+                if (item + 1 < nitems) issue(item + 1, buf[half ^ 1]);
+                const uint32_t step = item % nsteps;
+#pragma unroll
+                for (int s = 0; s < UNR; ++s) {
+                    const uint32_t uu = kl + (step * UNR + s) * TL;
+                    if (uu < units) {
+                        typename F::XU xu;
+                        F::load_x(xs, uu, xu);
+#ifdef RT_PROBE_NO_DOT
+#pragma unroll
+                        for (int i = 0; i < RPL; ++i)
+                            acc[i] += __builtin_bit_cast(
+                                float, ((const uint32_t*)&buf[half][s][i])[1] ^ ((const uint32_t*)&xu)[0]);
+#else
+#pragma unroll
+                        for (int i = 0; i < RPL; ++i) acc[i] += F::dot(buf[half][s][i], xu);
+#endif
                     }
                 }
-            } else {
+                if (step == nsteps - 1) {
+                    const uint32_t tile = blockIdx.x + (item / nsteps) * gridDim.x;
+                    finish_rows<EPI, RPL>(a, red, tid, TL, grp, kl,
+                                          tile * vrows_per_wg + grp * RPL, acc);
 #pragma unroll
-                for (int i = 0; i < RPL; ++i) {
-                    if (vr0 + i < a.nvrows) store_row<EPI>(a, vr0 + i, acc[i]);
+                    for (int i = 0; i < RPL; ++i) acc[i] = 0.0f;
                 }
             }
         }
     }
 }
 
-#define RT_GEMV_KERNEL(NAME, FMT, EPI, XT, RPL)                                   \
-    extern "C" __global__ void __launch_bounds__(256) NAME(GemvArgs a) {         \
-        gemv_body<FMT, EPI, XT, RPL>(a);                                          \
+// Long-K path: the activation records are staged in chunks, once per tile.
+template <class F, int EPI, typename XT, int RPL, int UNR>
+RT_DEV void gemv_body_chunked(const GemvArgs& a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    XRec* xs = (XRec*)smem;
+    float* red = (float*)(smem + (size_t)a.xb_chunk * sizeof(XRec));
+    const uint32_t tid = threadIdx.x;
+    const uint32_t TL = a.lpr;
+    const uint32_t grp = tid / TL, kl = tid % TL;
+    const uint32_t vrows_per_wg = (blockDim.x / TL) * RPL;
+    const uint32_t nxb = a.K / 32;
+    const uint32_t ntiles = (a.nvrows + vrows_per_wg - 1) / vrows_per_wg;
+    const XT* x = (const XT*)a.x;
+
+    for (uint32_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const uint32_t vr0 = tile * vrows_per_wg + grp * RPL;
+        const uint8_t* rowp[RPL];
+        tile_rows<EPI, RPL>(a, vr0, rowp);
+        float acc[RPL];
+#pragma unroll
+        for (int i = 0; i < RPL; ++i) acc[i] = 0.0f;
+        for (uint32_t xc = 0; xc < nxb; xc += a.xb_chunk) {
+            const uint32_t nx = min(a.xb_chunk, nxb - xc);
+            __syncthreads();
+            stage_x_limbs<XT, F::Q40PERM>(x, xc, nx, xs);
+            __syncthreads();
+            const uint32_t units = nx * 32 / F::UNIT_EL;
+            const uint32_t u0 = xc * 32 / F::UNIT_EL;
+            for (uint32_t ub = kl; ub < units; ub += UNR * TL) {
+                typename F::Raw raw[UNR][RPL];
+#pragma unroll
+                for (int s = 0; s < UNR; ++s) {
+                    const uint32_t uu = ub + s * TL;
+                    if (uu < units) {
+#pragma unroll
+                        for (int i = 0; i < RPL; ++i) F::load(rowp[i], u0 + uu, raw[s][i]);
+                    }
+                }
+#pragma unroll
+                for (int s = 0; s < UNR; ++s) {
+                    const uint32_t uu = ub + s * TL;
+                    if (uu < units) {
+                        typename F::XU xu;
+                        F::load_x(xs, uu, xu);
+#pragma unroll
+                        for (int i = 0; i < RPL; ++i) acc[i] += F::dot(raw[s][i], xu);
+                    }
+                }
+            }
+        }
+        finish_rows<EPI, RPL>(a, red, tid, TL, grp, kl, vr0, acc);
+    }
+}
+
+// Matrix-core path (whole K in LDS).  Lane 4·slot + q works on row q of the
+// wave's current row quad and on unit `slot` (+16 per step) of that row, so
+// the 16 lanes of a row read 16 consecutive units (coalesced) and the four
+// lanes of a quad feed one 4×4×4 block of v_mfma_i32_4x4x4i8 (rt_formats.h).
+// Each lane walks a flat sequence of (tile, step) items and issues the loads
+// of item n+1 before computing item n; the first item's loads are issued
+// before the activation staging.
+template <class F, int EPI, typename XT, int RQ>
+RT_DEV void gemv_mq_body(const GemvArgs& a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    XRec* xs = (XRec*)smem;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t q = lane & 3, slot = lane >> 2;
+    const uint32_t lq = q < 3 ? q : 2;  // the A row of lane q = 3 is a don't-care
+    const uint32_t vrows_per_wg = nwaves * 4 * RQ;
+    const uint32_t ntiles = (a.nvrows + vrows_per_wg - 1) / vrows_per_wg;
+    const uint32_t units = a.K / F::UNIT_EL;
+    const uint32_t nsteps = (units + 15) / 16;
+    const uint32_t my_tiles =
+        blockIdx.x < ntiles ? (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    const uint32_t nitems = my_tiles * nsteps;
+
+    typename F::Raw buf[2][RQ];
+    auto issue = [&](uint32_t item, typename F::Raw (&dst)[RQ]) {
+        const uint32_t tile = blockIdx.x + (item / nsteps) * gridDim.x;
+        const uint32_t step = item % nsteps;
+        uint32_t u = slot + 16 * step;
+        if (u >= units) u = 0;  // clamped: loads stay in bounds, result is discarded
+#pragma unroll
+        for (int rq = 0; rq < RQ; ++rq) {
+            uint32_t vr = tile * vrows_per_wg + wave * 4 * RQ + 4 * rq + q;
+            if (vr >= a.nvrows) vr = a.nvrows - 1;
+            uint32_t mat, r;
+            vrow_map<EPI>(a, vr, mat, r);
+            F::load(a.w[mat] + (size_t)r * a.row_bytes, u, dst[rq]);
+        }
+    };
+
+    if (nitems > 0) issue(0, buf[0]);
+    stage_x_limbs<XT, F::Q40PERM>((const XT*)a.x, 0, a.K / 32, xs);
+    __syncthreads();
+    if (nitems == 0) return;
+
+    float acc[RQ];
+#pragma unroll
+    for (int rq = 0; rq < RQ; ++rq) acc[rq] = 0.0f;
+
+    for (uint32_t it = 0; it < nitems; it += 2) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const uint32_t item = it + half;
+            if (item < nitems) {  // wave-uniform
+                if (item + 1 < nitems) issue(item + 1, buf[half ^ 1]);
+                const uint32_t step = item % nsteps;
+                const uint32_t u = slot + 16 * step;
+                const bool valid = u < units;
+                const uint32_t uc = valid ? u : 0;
+#pragma unroll
+                for (int rq = 0; rq < RQ; ++rq) {
+                    const float v = F::mdot(buf[half][rq], xs, uc, lq);
+                    acc[rq] += valid ? v : 0.0f;
+                }
+                if (step == nsteps - 1) {
+                    const uint32_t tile = blockIdx.x + (item / nsteps) * gridDim.x;
+                    const uint32_t vbase = tile * vrows_per_wg + wave * 4 * RQ;
+#pragma unroll
+                    for (int rq = 0; rq < RQ; ++rq) {
+                        // sum over the 16 slots of the row: lane bits 2..5
+                        float v = acc[rq];
+                        v += swz_xor_f<4>(v);
+                        v += swz_xor_f<8>(v);
+                        v += swz_xor_f<16>(v);
+                        v += __shfl_xor(v, 32, 64);
+                        acc[rq] = 0.0f;
+                        const uint32_t vr = vbase + 4 * rq + q;
+                        if (EPI == EPI_FFN) {
+                            // quad holds (gate r, up r, gate r+1, up r+1)
+                            const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
+                            if (slot == 0 && (q & 1) == 0 && vr + 1 < a.nvrows)
+                                ((float*)a.out[0])[vr >> 1] = silu_ref(v) * up;
+                        } else {
+                            if (slot == 0 && vr < a.nvrows) store_row<EPI>(a, vr, v);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <class F, int EPI, typename XT, int RPL, int UNR>
+RT_DEV void gemv_body(const GemvArgs& a) {
+    if (a.xb_chunk >= a.K / 32)
+        gemv_body_pipelined<F, EPI, XT, RPL, UNR>(a);
+    else
+        gemv_body_chunked<F, EPI, XT, RPL, UNR>(a);
+}
+
+// MFMA kernels: whole-K launches use the matrix-core body, long-K launches
+// the chunked v_dot4 body.
+template <class F, int EPI, typename XT, int RQ, int RPL, int UNR>
+RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
+    if (a.xb_chunk >= a.K / 32)
+        gemv_mq_body<F, EPI, XT, RQ>(a);
+    else
+        gemv_body_chunked<F, EPI, XT, RPL, UNR>(a);
+}
+
+#define RT_GEMV_KERNEL(NAME, FMT, EPI, XT, UNR)                                   \
+    extern "C" __global__ void __launch_bounds__(512) NAME##_r1(GemvArgs a) {   \
+        gemv_mq_or_chunked<FMT, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);   \
+    }                                                                             \
+    extern "C" __global__ void __launch_bounds__(512) NAME##_r2(GemvArgs a) {   \
+        gemv_mq_or_chunked<FMT, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);   \
+    }
+
+// Single-block-unit fallback (rows with an odd number of 32-element blocks)
+#define RT_GEMV_KERNEL_S(NAME, FMT, EPI, XT, UNR)                                 \
+    extern "C" __global__ void __launch_bounds__(512) NAME##_s1(GemvArgs a) {    \
+        gemv_body<FMT, EPI, XT, (EPI == EPI_FFN ? 2 : 1), UNR>(a);                \
     }
 
 // Q8_0 (gemv_q8_0.metal, gemv_multirow.metal, fused_qkv.metal, fused_ffn.metal)
-RT_GEMV_KERNEL(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float, 2)
-RT_GEMV_KERNEL(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float, 2)
-RT_GEMV_KERNEL(k_gemv_q8_0_f32_f16, FmtQ8_0, EPI_F16, float, 2)
-RT_GEMV_KERNEL(k_gemv_q8_0_f16_f16, FmtQ8_0, EPI_F16, uint16_t, 2)
-RT_GEMV_KERNEL(k_gemv_q8_0_f16_f16add, FmtQ8_0, EPI_F16_ADD, uint16_t, 2)
-RT_GEMV_KERNEL(k_gemv_q8_0_f16_f32add, FmtQ8_0, EPI_F32_ADD, uint16_t, 2)
-RT_GEMV_KERNEL(k_qkv_q8_0, FmtQ8_0, EPI_QKV, float, 2)
-RT_GEMV_KERNEL(k_qkv_bias_q8_0, FmtQ8_0, EPI_QKV_BIAS, float, 2)
-RT_GEMV_KERNEL(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float, 2)
+RT_GEMV_KERNEL(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float, 1)
+RT_GEMV_KERNEL(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float, 1)
+RT_GEMV_KERNEL(k_gemv_q8_0_f32_f16, FmtQ8_0, EPI_F16, float, 1)
+RT_GEMV_KERNEL(k_gemv_q8_0_f16_f16, FmtQ8_0, EPI_F16, uint16_t, 1)
+RT_GEMV_KERNEL(k_gemv_q8_0_f16_f16add, FmtQ8_0, EPI_F16_ADD, uint16_t, 1)
+RT_GEMV_KERNEL(k_gemv_q8_0_f16_f32add, FmtQ8_0, EPI_F32_ADD, uint16_t, 1)
+RT_GEMV_KERNEL(k_qkv_q8_0, FmtQ8_0, EPI_QKV, float, 1)
+RT_GEMV_KERNEL(k_qkv_bias_q8_0, FmtQ8_0, EPI_QKV_BIAS, float, 1)
+RT_GEMV_KERNEL(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float, 1)
 // Q4_0 (gemv_q4_0.metal)
 RT_GEMV_KERNEL(k_gemv_q4_0_f32_f32, FmtQ4_0, EPI_F32, float, 2)
 RT_GEMV_KERNEL(k_gemv_q4_0_f32_f32add, FmtQ4_0, EPI_F32_ADD, float, 2)
@@ -183,14 +423,30 @@ RT_GEMV_KERNEL(k_gemv_q4_0_f16_f16, FmtQ4_0, EPI_F16, uint16_t, 2)
 RT_GEMV_KERNEL(k_gemv_q4_0_f16_f16add, FmtQ4_0, EPI_F16_ADD, uint16_t, 2)
 RT_GEMV_KERNEL(k_qkv_bias_q4_0, FmtQ4_0, EPI_QKV_BIAS, float, 2)
 RT_GEMV_KERNEL(k_ffn_q4_0, FmtQ4_0, EPI_FFN, float, 2)
+RT_GEMV_KERNEL_S(k_gemv_q8_0_f32_f32, FmtQ8_0S, EPI_F32, float, 2)
+RT_GEMV_KERNEL_S(k_gemv_q8_0_f32_f32add, FmtQ8_0S, EPI_F32_ADD, float, 2)
+RT_GEMV_KERNEL_S(k_gemv_q8_0_f32_f16, FmtQ8_0S, EPI_F16, float, 2)
+RT_GEMV_KERNEL_S(k_gemv_q8_0_f16_f16, FmtQ8_0S, EPI_F16, uint16_t, 2)
+RT_GEMV_KERNEL_S(k_gemv_q8_0_f16_f16add, FmtQ8_0S, EPI_F16_ADD, uint16_t, 2)
+RT_GEMV_KERNEL_S(k_gemv_q8_0_f16_f32add, FmtQ8_0S, EPI_F32_ADD, uint16_t, 2)
+RT_GEMV_KERNEL_S(k_qkv_q8_0, FmtQ8_0S, EPI_QKV, float, 2)
+RT_GEMV_KERNEL_S(k_qkv_bias_q8_0, FmtQ8_0S, EPI_QKV_BIAS, float, 2)
+RT_GEMV_KERNEL_S(k_ffn_q8_0, FmtQ8_0S, EPI_FFN, float, 2)
+RT_GEMV_KERNEL_S(k_gemv_q4_0_f32_f32, FmtQ4_0S, EPI_F32, float, 4)
+RT_GEMV_KERNEL_S(k_gemv_q4_0_f32_f32add, FmtQ4_0S, EPI_F32_ADD, float, 4)
+RT_GEMV_KERNEL_S(k_gemv_q4_0_f32_f16, FmtQ4_0S, EPI_F16, float, 4)
+RT_GEMV_KERNEL_S(k_gemv_q4_0_f16_f16, FmtQ4_0S, EPI_F16, uint16_t, 4)
+RT_GEMV_KERNEL_S(k_gemv_q4_0_f16_f16add, FmtQ4_0S, EPI_F16_ADD, uint16_t, 4)
+RT_GEMV_KERNEL_S(k_qkv_bias_q4_0, FmtQ4_0S, EPI_QKV_BIAS, float, 4)
+RT_GEMV_KERNEL_S(k_ffn_q4_0, FmtQ4_0S, EPI_FFN, float, 4)
 // Q4_K (gemv_q4k.metal)
-RT_GEMV_KERNEL(k_gemv_q4k_f32_f32, FmtQ4K, EPI_F32, float, 2)
-RT_GEMV_KERNEL(k_gemv_q4k_f32_f32add, FmtQ4K, EPI_F32_ADD, float, 2)
-RT_GEMV_KERNEL(k_gemv_q4k_f16_f16, FmtQ4K, EPI_F16, uint16_t, 2)
-RT_GEMV_KERNEL(k_gemv_q4k_f16_f16add, FmtQ4K, EPI_F16_ADD, uint16_t, 2)
-RT_GEMV_KERNEL(k_gemv_q4k_f16_f32add, FmtQ4K, EPI_F32_ADD, uint16_t, 2)
-RT_GEMV_KERNEL(k_ffn_q4k, FmtQ4K, EPI_FFN, float, 2)
+RT_GEMV_KERNEL(k_gemv_q4k_f32_f32, FmtQ4K, EPI_F32, float, 1)
+RT_GEMV_KERNEL(k_gemv_q4k_f32_f32add, FmtQ4K, EPI_F32_ADD, float, 1)
+RT_GEMV_KERNEL(k_gemv_q4k_f16_f16, FmtQ4K, EPI_F16, uint16_t, 1)
+RT_GEMV_KERNEL(k_gemv_q4k_f16_f16add, FmtQ4K, EPI_F16_ADD, uint16_t, 1)
+RT_GEMV_KERNEL(k_gemv_q4k_f16_f32add, FmtQ4K, EPI_F32_ADD, uint16_t, 1)
+RT_GEMV_KERNEL(k_ffn_q4k, FmtQ4K, EPI_FFN, float, 1)
 // Q6_K (new: the reference runs Q6_K through f16-dequantised weights)
-RT_GEMV_KERNEL(k_gemv_q6k_f32_f32, FmtQ6K, EPI_F32, float, 2)
-RT_GEMV_KERNEL(k_gemv_q6k_f32_f32add, FmtQ6K, EPI_F32_ADD, float, 2)
-RT_GEMV_KERNEL(k_gemv_q6k_f32_f16, FmtQ6K, EPI_F16, float, 2)
+RT_GEMV_KERNEL(k_gemv_q6k_f32_f32, FmtQ6K, EPI_F32, float, 1)
+RT_GEMV_KERNEL(k_gemv_q6k_f32_f32add, FmtQ6K, EPI_F32_ADD, float, 1)
+RT_GEMV_KERNEL(k_gemv_q6k_f32_f16, FmtQ6K, EPI_F16, float, 1)

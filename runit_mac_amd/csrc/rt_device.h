@@ -136,87 +136,98 @@ RT_DEV void load_x4<uint16_t>(const uint16_t* x, uint32_t idx, float v[4]) {
     v[0] = h2f(t.x); v[1] = h2f(t.x >> 16); v[2] = h2f(t.y); v[3] = h2f(t.y >> 16);
 }
 
+// Converts one 4-element slice (lane q of the 8 lanes of x-block b) into
+// limbs and writes them to the block's record.
+template <bool Q40PERM>
+RT_DEV void limb_slice(const float v[4], uint32_t q, XRec* __restrict__ rec) {
+    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    // NaN-propagating max over 8 lanes: a NaN turns into +Inf here.
+    if (a != a) a = __builtin_huge_valf();
+    a = max8(a);
+    int e;
+    const bool finite = a <= 3.40282347e38f;
+    if (!finite) {
+        e = XE_NONFINITE;
+    } else if (a == 0.0f) {
+        e = 0;
+    } else {
+        e = __builtin_amdgcn_frexp_expf(a);  // a < 2^e
+    }
+    int l0[4], l1[4], l2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int xi;
+        if (finite) {
+            xi = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v[i], 22 - e));
+        } else {
+            // Inf/NaN blocks: ±2^22 on non-finite elements, 0 elsewhere;
+            // with e = 300 their products overflow to ±Inf (or NaN).
+            const bool nf = !(fabsf(v[i]) <= 3.40282347e38f);
+            xi = nf ? ((v[i] < 0.0f) ? -(1 << 22) : (1 << 22)) : 0;
+        }
+        // balanced base-256 digits: xi = 65536·l0 + 256·l1 + l2
+        const int c = ((xi + 128) & 255) - 128;
+        const int r1 = (xi - c) >> 8;
+        const int bb = ((r1 + 128) & 255) - 128;
+        l0[i] = (r1 - bb) >> 8;
+        l1[i] = bb;
+        l2[i] = c;
+    }
+    uint8_t* base = (uint8_t*)rec;
+    if (!Q40PERM) {
+        rec->limb[0][q] = (l0[0] & 255) | ((l0[1] & 255) << 8) | ((l0[2] & 255) << 16) |
+                          ((uint32_t)(l0[3] & 255) << 24);
+        rec->limb[1][q] = (l1[0] & 255) | ((l1[1] & 255) << 8) | ((l1[2] & 255) << 16) |
+                          ((uint32_t)(l1[3] & 255) << 24);
+        rec->limb[2][q] = (l2[0] & 255) | ((l2[1] & 255) << 8) | ((l2[2] & 255) << 16) |
+                          ((uint32_t)(l2[3] & 255) << 24);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int pos = xpos<true>(q * 4 + i);
+            base[0 * 32 + pos] = (uint8_t)l0[i];
+            base[1 * 32 + pos] = (uint8_t)l1[i];
+            base[2 * 32 + pos] = (uint8_t)l2[i];
+        }
+    }
+    // Limb sums per 16-element half (lanes 0-3 → half 0, 4-7 → half 1).
+    int s0 = sum4_i(l0[0] + l0[1] + l0[2] + l0[3]);
+    int s1 = sum4_i(l1[0] + l1[1] + l1[2] + l1[3]);
+    int s2 = sum4_i(l2[0] + l2[1] + l2[2] + l2[3]);
+    if ((q & 3) == 0) {
+        const int h = q >> 2;
+        rec->s[h][0] = (int16_t)s0;
+        rec->s[h][1] = (int16_t)s1;
+        rec->s[h][2] = (int16_t)s2;
+    }
+    if (q == 0) {
+        rec->e = (int16_t)e;
+        rec->pad = 0;
+    }
+}
+
 // Builds records for x-blocks [xb0, xb0+nxb) into recs[0..nxb).  Eight lanes
-// per block, four activations per lane.  All threads of the workgroup must
-// call it (it is followed by a barrier in the callers).
+// per block, four activations per lane; each thread first issues the loads of
+// up to XSTAGE_UNR slices, then converts them (one memory round trip per
+// XSTAGE_UNR slices instead of one per slice).  All threads of the workgroup
+// call it; callers follow it with a barrier.
+constexpr int XSTAGE_UNR = 4;
 template <typename XT, bool Q40PERM>
 RT_DEV void stage_x_limbs(const XT* __restrict__ x, uint32_t xb0, uint32_t nxb,
                           XRec* __restrict__ recs) {
     const uint32_t total = nxb * 8;
-    for (uint32_t t = threadIdx.x; t < total; t += blockDim.x) {
-        const uint32_t b = t >> 3, q = t & 7;
-        float v[4];
-        load_x4<XT>(x, (xb0 + b) * 32 + q * 4, v);
-        float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        // NaN-propagating max over 8 lanes: a NaN turns into +Inf here.
-        if (a != a) a = __builtin_huge_valf();
-        a = max8(a);
-        int e;
-        const bool finite = a <= 3.40282347e38f;
-        if (!finite) {
-            e = XE_NONFINITE;
-        } else if (a == 0.0f) {
-            e = 0;
-        } else {
-            e = __builtin_amdgcn_frexp_expf(a);  // a < 2^e
-        }
-        int l0[4], l1[4], l2[4];
+    const uint32_t step = blockDim.x;
+    for (uint32_t t0 = threadIdx.x; t0 < total; t0 += XSTAGE_UNR * step) {
+        float v[XSTAGE_UNR][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int xi;
-            if (finite) {
-                xi = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v[i], 22 - e));
-            } else {
-                // Inf/NaN blocks: ±2^22 on non-finite elements, 0 elsewhere;
-                // with e = 300 their products overflow to ±Inf (or NaN).
-                const bool nf = !(fabsf(v[i]) <= 3.40282347e38f);
-                xi = nf ? ((v[i] < 0.0f) ? -(1 << 22) : (1 << 22)) : 0;
-            }
-            // balanced base-256 digits: xi = 65536·l0 + 256·l1 + l2
-            const int c = ((xi + 128) & 255) - 128;
-            const int r1 = (xi - c) >> 8;
-            const int bb = ((r1 + 128) & 255) - 128;
-            l0[i] = (r1 - bb) >> 8;
-            l1[i] = bb;
-            l2[i] = c;
+        for (int s = 0; s < XSTAGE_UNR; ++s) {
+            const uint32_t t = t0 + s * step;
+            if (t < total) load_x4<XT>(x, (xb0 + (t >> 3)) * 32 + (t & 7) * 4, v[s]);
         }
-        XRec* rec = recs + b;
-        uint8_t* base = (uint8_t*)rec;
-        if (!Q40PERM) {
-            uint32_t w0 = (l0[0] & 255) | ((l0[1] & 255) << 8) | ((l0[2] & 255) << 16) |
-                          ((uint32_t)(l0[3] & 255) << 24);
-            uint32_t w1 = (l1[0] & 255) | ((l1[1] & 255) << 8) | ((l1[2] & 255) << 16) |
-                          ((uint32_t)(l1[3] & 255) << 24);
-            uint32_t w2 = (l2[0] & 255) | ((l2[1] & 255) << 8) | ((l2[2] & 255) << 16) |
-                          ((uint32_t)(l2[3] & 255) << 24);
-            rec->limb[0][q] = w0;
-            rec->limb[1][q] = w1;
-            rec->limb[2][q] = w2;
-        } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int pos = xpos<true>(q * 4 + i);
-                base[0 * 32 + pos] = (uint8_t)l0[i];
-                base[1 * 32 + pos] = (uint8_t)l1[i];
-                base[2 * 32 + pos] = (uint8_t)l2[i];
-            }
-        }
-        // Limb sums per 16-element half (lanes 0-3 → half 0, 4-7 → half 1).
-        int s0 = l0[0] + l0[1] + l0[2] + l0[3];
-        int s1 = l1[0] + l1[1] + l1[2] + l1[3];
-        int s2 = l2[0] + l2[1] + l2[2] + l2[3];
-        s0 = sum4_i(s0);
-        s1 = sum4_i(s1);
-        s2 = sum4_i(s2);
-        if ((q & 3) == 0) {
-            const int h = q >> 2;
-            rec->s[h][0] = (int16_t)s0;
-            rec->s[h][1] = (int16_t)s1;
-            rec->s[h][2] = (int16_t)s2;
-        }
-        if (q == 0) {
-            rec->e = (int16_t)e;
-            rec->pad = 0;
+        for (int s = 0; s < XSTAGE_UNR; ++s) {
+            const uint32_t t = t0 + s * step;
+            if (t < total) limb_slice<Q40PERM>(v[s], t & 7, recs + (t >> 3));
         }
     }
 }

@@ -14,66 +14,225 @@
 #pragma once
 #include "rt_device.h"
 
+// Loads are always 4-byte aligned: the 34- and 18-byte blocks (and the
+// 210-byte Q6_K blocks) start on 2-byte boundaries, and 2-byte-aligned wide
+// loads stream markedly slower on gfx950 than aligned dword loads of the same
+// lines.  Misaligned fields are rebuilt in registers with v_alignbyte.
+RT_DEV uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t sh) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+template <int N>
+RT_DEV void load_dwords(const uint8_t* p, uint32_t (&w)[N]) {
+    // p is 4-byte aligned; N dwords as dwordx4 / dwordx2 / dword loads
+#pragma unroll
+    for (int i = 0; i + 4 <= N; i += 4) {
+        u32x4 v = *(const u32x4_a4*)(p + 4 * i);
+        w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+    }
+    constexpr int R = N & 3, B = N - R;
+    if (R == 3) {
+        typedef uint32_t u32x3_a4 __attribute__((ext_vector_type(3), aligned(4)));
+        u32x3_a4 v = *(const u32x3_a4*)(p + 4 * B);
+        w[B] = v.x; w[B + 1] = v.y; w[B + 2] = v.z;
+    } else if (R == 2) {
+        typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+        u32x2_a4 v = *(const u32x2_a4*)(p + 4 * B);
+        w[B] = v.x; w[B + 1] = v.y;
+    } else if (R == 1) {
+        w[B] = *(const uint32_t*)(p + 4 * B);
+    }
+}
+
+// ───────────────────────────── matrix-core dots ─────────────────────────────
+// v_mfma_i32_4x4x4i8 runs 16 independent 4×4×4 int8 products per wave.  For
+// block b (lanes 4b..4b+3): lane 4b+i supplies row i of A (4 int8), lane 4b+j
+// supplies column j of B, and lane 4b+j receives D[0..3][j] in its 4 result
+// registers.  The GEMV kernels put activation limb i in A and weight row j in
+// B, so lane 4b+q ends up holding the three limb dots of ITS OWN row q for
+// the unit in slot b; lane q = 3 feeds a don't-care A row.
+typedef int v4i __attribute__((ext_vector_type(4)));
+RT_DEV v4i mfma4(uint32_t a, uint32_t b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_4x4x4i8((int)a, (int)b, c, 0, 0, 0);
+}
+RT_DEV float comb4(v4i c) { return limb_combine(c[0], c[1], c[2]); }
+
+// Limb `lq` of a record (8 dwords) and its exponent / limb sums.
+struct XLimb {
+    uint32_t l[8];
+    int e;
+    int s[3];      // full-block sums
+    int sh[2][3];  // per-half sums
+};
+RT_DEV void load_xlimb(const XRec* rec, uint32_t lq, XLimb& x) {
+    const u32x4* p = (const u32x4*)rec;
+    u32x4 a = p[2 * lq], b = p[2 * lq + 1];
+    x.l[0] = a.x; x.l[1] = a.y; x.l[2] = a.z; x.l[3] = a.w;
+    x.l[4] = b.x; x.l[5] = b.y; x.l[6] = b.z; x.l[7] = b.w;
+    u32x4 m = p[6];
+    x.e = (int)(int16_t)(m.x & 0xFFFF);
+    x.sh[0][0] = (int16_t)(m.x >> 16);
+    x.sh[0][1] = (int16_t)(m.y & 0xFFFF);
+    x.sh[0][2] = (int16_t)(m.y >> 16);
+    x.sh[1][0] = (int16_t)(m.z & 0xFFFF);
+    x.sh[1][1] = (int16_t)(m.z >> 16);
+    x.sh[1][2] = (int16_t)(m.w & 0xFFFF);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) x.s[i] = x.sh[0][i] + x.sh[1][i];
+}
+
 // ───────────────────────────── Q8_0 ─────────────────────────────
 // Block: d:f16 @0, qs:int8[32] @2 (gemv_q8_0.metal:11-17; forward.rs:951-963).
+RT_DEV float q8_0_block_dot(uint32_t d, const uint32_t q[8], const XRegs& x) {
+    int t0 = 0, t1 = 0, t2 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        t0 = sdot4(q[i], x.l[0][i], t0);
+        t1 = sdot4(q[i], x.l[1][i], t1);
+        t2 = sdot4(q[i], x.l[2][i], t2);
+    }
+    return __builtin_amdgcn_ldexpf(h2f(d) * limb_combine(t0, t1, t2), x.e - 22);
+}
+
+// Unit = two consecutive blocks (68 bytes, 4-byte aligned when a row holds
+// an even number of blocks): 17 aligned dwords.
 struct FmtQ8_0 {
+    static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 34, UNIT_EL = 64;
+    static constexpr bool Q40PERM = false;
+    struct Raw { uint32_t w[17]; };
+    struct XU { XRegs x[2]; };
+    RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
+        load_dwords<17>(row + (size_t)u * 68, r.w);
+    }
+    RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) {
+        load_xregs(recs + 2 * uu, xu.x[0]);
+        load_xregs(recs + 2 * uu + 1, xu.x[1]);
+    }
+    RT_DEV static float dot(const Raw& r, const XU& xu) {
+        uint32_t qa[8], qb[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            qa[i] = alignb(r.w[i + 1], r.w[i], 2);  // bytes 2..33
+            qb[i] = r.w[9 + i];                     // bytes 36..67
+        }
+        return q8_0_block_dot(r.w[0], qa, xu.x[0]) + q8_0_block_dot(r.w[8] >> 16, qb, xu.x[1]);
+    }
+    // matrix-core form: recs = the unit's two records, lq = this lane's limb
+    RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
+        XLimb xa, xb;
+        load_xlimb(xs + 2 * uu, lq, xa);
+        load_xlimb(xs + 2 * uu + 1, lq, xb);
+        v4i ca = {0, 0, 0, 0}, cb = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ca = mfma4(xa.l[i], alignb(r.w[i + 1], r.w[i], 2), ca);  // bytes 2..33
+            cb = mfma4(xb.l[i], r.w[9 + i], cb);                     // bytes 36..67
+        }
+        return __builtin_amdgcn_ldexpf(h2f(r.w[0]) * comb4(ca), xa.e - 22) +
+               __builtin_amdgcn_ldexpf(h2f(r.w[8] >> 16) * comb4(cb), xb.e - 22);
+    }
+};
+
+// Single-block unit for rows with an odd number of blocks: 10 aligned dwords
+// from the block's 4-byte-aligned floor.
+struct FmtQ8_0S {
     static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 34, UNIT_EL = 32;
     static constexpr bool Q40PERM = false;
-    struct Raw { uint32_t d; uint32_t q[8]; };
+    struct Raw { uint32_t w[10]; uint32_t sh; };
     struct XU { XRegs x; };
     RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
-        const uint8_t* p = row + (size_t)u * 34;
-        r.d = *(const uint16_t*)p;
-        u32x4 a = *(const u32x4_a2*)(p + 2);
-        u32x4 b = *(const u32x4_a2*)(p + 18);
-        r.q[0] = a.x; r.q[1] = a.y; r.q[2] = a.z; r.q[3] = a.w;
-        r.q[4] = b.x; r.q[5] = b.y; r.q[6] = b.z; r.q[7] = b.w;
+        const uintptr_t p = (uintptr_t)(row + (size_t)u * 34);
+        r.sh = (uint32_t)(p & 3);
+        load_dwords<10>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
     }
     RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) { load_xregs(recs + uu, xu.x); }
     RT_DEV static float dot(const Raw& r, const XU& xu) {
-        int t0 = 0, t1 = 0, t2 = 0;
+        uint32_t q[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            t0 = sdot4(r.q[i], xu.x.l[0][i], t0);
-            t1 = sdot4(r.q[i], xu.x.l[1][i], t1);
-            t2 = sdot4(r.q[i], xu.x.l[2][i], t2);
-        }
-        return __builtin_amdgcn_ldexpf(h2f(r.d) * limb_combine(t0, t1, t2), xu.x.e - 22);
+        for (int i = 0; i < 8; ++i) q[i] = r.sh ? r.w[i + 1] : alignb(r.w[i + 1], r.w[i], 2);
+        const uint32_t d = alignb(r.w[1], r.w[0], r.sh);
+        return q8_0_block_dot(d, q, xu.x);
     }
 };
 
 // ───────────────────────────── Q4_0 ─────────────────────────────
 // Block: d:f16 @0, qs:u8[16] @2; element 2i = qs[i]&0xF, 2i+1 = qs[i]>>4,
 // value d·(nib−8) (gemv_q4_0.metal:10-15; forward.rs:964-978).
+RT_DEV float q4_0_block_dot(uint32_t d, const uint32_t q[4], const XRegs& x) {
+    // −8·Σx folded into the accumulators' start values
+    int t0 = -8 * x.s[0], t1 = -8 * x.s[1], t2 = -8 * x.s[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = q[i] & 0x0F0F0F0Fu;         // elements 8i+{0,2,4,6}
+        const uint32_t hi = (q[i] >> 4) & 0x0F0F0F0Fu;  // elements 8i+{1,3,5,7}
+        t0 = sdot4(lo, x.l[0][2 * i], t0);
+        t0 = sdot4(hi, x.l[0][2 * i + 1], t0);
+        t1 = sdot4(lo, x.l[1][2 * i], t1);
+        t1 = sdot4(hi, x.l[1][2 * i + 1], t1);
+        t2 = sdot4(lo, x.l[2][2 * i], t2);
+        t2 = sdot4(hi, x.l[2][2 * i + 1], t2);
+    }
+    return __builtin_amdgcn_ldexpf(h2f(d) * limb_combine(t0, t1, t2), x.e - 22);
+}
+
+// Unit = two consecutive blocks (36 bytes): 9 aligned dwords.
 struct FmtQ4_0 {
+    static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 18, UNIT_EL = 64;
+    static constexpr bool Q40PERM = true;
+    struct Raw { uint32_t w[9]; };
+    struct XU { XRegs x[2]; };
+    RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
+        load_dwords<9>(row + (size_t)u * 36, r.w);
+    }
+    RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) {
+        load_xregs(recs + 2 * uu, xu.x[0]);
+        load_xregs(recs + 2 * uu + 1, xu.x[1]);
+    }
+    RT_DEV static float dot(const Raw& r, const XU& xu) {
+        uint32_t qa[4], qb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qa[i] = alignb(r.w[i + 1], r.w[i], 2);  // bytes 2..17
+            qb[i] = r.w[5 + i];                     // bytes 20..35
+        }
+        return q4_0_block_dot(r.w[0], qa, xu.x[0]) + q4_0_block_dot(r.w[4] >> 16, qb, xu.x[1]);
+    }
+    RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
+        XLimb xa, xb;
+        load_xlimb(xs + 2 * uu, lq, xa);
+        load_xlimb(xs + 2 * uu + 1, lq, xb);
+        // −8·Σx folded into the accumulators' start values
+        v4i ca = {-8 * xa.s[0], -8 * xa.s[1], -8 * xa.s[2], 0};
+        v4i cb = {-8 * xb.s[0], -8 * xb.s[1], -8 * xb.s[2], 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t qa = alignb(r.w[i + 1], r.w[i], 2), qb = r.w[5 + i];
+            ca = mfma4(xa.l[2 * i], qa & 0x0F0F0F0Fu, ca);           // elements 8i+{0,2,4,6}
+            ca = mfma4(xa.l[2 * i + 1], (qa >> 4) & 0x0F0F0F0Fu, ca);  // elements 8i+{1,3,5,7}
+            cb = mfma4(xb.l[2 * i], qb & 0x0F0F0F0Fu, cb);
+            cb = mfma4(xb.l[2 * i + 1], (qb >> 4) & 0x0F0F0F0Fu, cb);
+        }
+        return __builtin_amdgcn_ldexpf(h2f(r.w[0]) * comb4(ca), xa.e - 22) +
+               __builtin_amdgcn_ldexpf(h2f(r.w[4] >> 16) * comb4(cb), xb.e - 22);
+    }
+};
+
+// Single-block unit for rows with an odd number of blocks.
+struct FmtQ4_0S {
     static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 18, UNIT_EL = 32;
     static constexpr bool Q40PERM = true;
-    struct Raw { uint32_t d; uint32_t q[4]; };
+    struct Raw { uint32_t w[6]; uint32_t sh; };
     struct XU { XRegs x; };
     RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
-        const uint8_t* p = row + (size_t)u * 18;
-        r.d = *(const uint16_t*)p;
-        u32x4 a = *(const u32x4_a2*)(p + 2);
-        r.q[0] = a.x; r.q[1] = a.y; r.q[2] = a.z; r.q[3] = a.w;
+        const uintptr_t p = (uintptr_t)(row + (size_t)u * 18);
+        r.sh = (uint32_t)(p & 3);
+        load_dwords<6>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
     }
     RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) { load_xregs(recs + uu, xu.x); }
     RT_DEV static float dot(const Raw& r, const XU& xu) {
-        int t0 = 0, t1 = 0, t2 = 0;
+        uint32_t q[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = r.q[i] & 0x0F0F0F0Fu;         // elements 8i+{0,2,4,6}
-            const uint32_t hi = (r.q[i] >> 4) & 0x0F0F0F0Fu;  // elements 8i+{1,3,5,7}
-            t0 = sdot4(lo, xu.x.l[0][2 * i], t0);
-            t0 = sdot4(hi, xu.x.l[0][2 * i + 1], t0);
-            t1 = sdot4(lo, xu.x.l[1][2 * i], t1);
-            t1 = sdot4(hi, xu.x.l[1][2 * i + 1], t1);
-            t2 = sdot4(lo, xu.x.l[2][2 * i], t2);
-            t2 = sdot4(hi, xu.x.l[2][2 * i + 1], t2);
-        }
-        t0 -= 8 * xu.x.s[0];
-        t1 -= 8 * xu.x.s[1];
-        t2 -= 8 * xu.x.s[2];
-        return __builtin_amdgcn_ldexpf(h2f(r.d) * limb_combine(t0, t1, t2), xu.x.e - 22);
+        for (int i = 0; i < 4; ++i) q[i] = r.sh ? r.w[i + 1] : alignb(r.w[i + 1], r.w[i], 2);
+        return q4_0_block_dot(alignb(r.w[1], r.w[0], r.sh), q, xu.x);
     }
 };
 
@@ -90,9 +249,10 @@ struct FmtQ4K {
     RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
         const uint32_t b = u >> 2, j = u & 3;
         const uint8_t* p = row + (size_t)b * 144;
-        const uint32_t* pw = (const uint32_t*)p;  // 144-byte blocks keep 4-byte alignment
-        r.dd = pw[0];
-        const uint32_t s0 = pw[1], s1 = pw[2], s2 = pw[3];
+        // 144-byte blocks keep 16-byte alignment: header = one dwordx4
+        const u32x4 hdr = *(const u32x4*)p;
+        r.dd = hdr.x;
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
         // bytes j, j+4, j+8 of the scale table, packed as (b0 | b1<<8 | b2<<16)
         const uint32_t sh = 8 * j;
         r.sc = ((s0 >> sh) & 255u) | (((s1 >> sh) & 255u) << 8) | (((s2 >> sh) & 255u) << 16);
@@ -132,6 +292,27 @@ struct FmtQ4K {
         return __builtin_amdgcn_ldexpf(vlo, xu.lo.e - 22) +
                __builtin_amdgcn_ldexpf(vhi, xu.hi.e - 22);
     }
+    RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
+        XLimb xl, xh;
+        load_xlimb(xs + 2 * uu, lq, xl);
+        load_xlimb(xs + 2 * uu + 1, lq, xh);
+        v4i cl = {0, 0, 0, 0}, ch = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            cl = mfma4(xl.l[i], r.q[i] & 0x0F0F0F0Fu, cl);
+            ch = mfma4(xh.l[i], (r.q[i] >> 4) & 0x0F0F0F0Fu, ch);
+        }
+        const uint32_t c0 = r.sc & 255u, c1 = (r.sc >> 8) & 255u, c2 = (r.sc >> 16) & 255u;
+        const uint32_t sc_lo = c0 & 63u, m_lo = c1 & 63u;
+        const uint32_t sc_hi = (c2 & 15u) | ((c0 >> 6) << 4);
+        const uint32_t m_hi = (c2 >> 4) | ((c1 >> 6) << 4);
+        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
+        const float vlo = d * (float)sc_lo * comb4(cl) -
+                          dmin * (float)m_lo * limb_combine(xl.s[0], xl.s[1], xl.s[2]);
+        const float vhi = d * (float)sc_hi * comb4(ch) -
+                          dmin * (float)m_hi * limb_combine(xh.s[0], xh.s[1], xh.s[2]);
+        return __builtin_amdgcn_ldexpf(vlo, xl.e - 22) + __builtin_amdgcn_ldexpf(vhi, xh.e - 22);
+    }
 };
 
 // ───────────────────────────── Q6_K ─────────────────────────────
@@ -146,20 +327,32 @@ struct FmtQ6K {
     struct Raw { uint32_t ql0[4], ql1[4], qh[4]; uint32_t sc01, sc23; uint32_t d; };
     struct XHalf { uint32_t l[3][4]; int e; int s[3]; };
     struct XU { XHalf t[4]; };
+    // 16 bytes at a 2-byte-aligned address, via 5 aligned dwords + alignbyte
+    RT_DEV static void load16(const uint8_t* q, uint32_t out[4]) {
+        const uintptr_t pa = (uintptr_t)q;
+        const uint32_t sh = (uint32_t)(pa & 3);
+        uint32_t w[5];
+        load_dwords<5>((const uint8_t*)(pa & ~(uintptr_t)3), w);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[i] = alignb(w[i + 1], w[i], sh);
+    }
     RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
         const uint32_t b = u >> 2, hsel = (u >> 1) & 1, lh = u & 1;
         const uint8_t* p = row + (size_t)b * 210;
         const uint32_t h = hsel * 128;
-        u32x4 a = *(const u32x4_a2*)(p + h / 2 + 16 * lh);
-        u32x4 c = *(const u32x4_a2*)(p + h / 2 + 32 + 16 * lh);
-        u32x4 e = *(const u32x4_a2*)(p + 128 + h / 4 + 16 * lh);
-        u32x2_a2 s = *(const u32x2_a2*)(p + 192 + h / 16);
-        r.ql0[0] = a.x; r.ql0[1] = a.y; r.ql0[2] = a.z; r.ql0[3] = a.w;
-        r.ql1[0] = c.x; r.ql1[1] = c.y; r.ql1[2] = c.z; r.ql1[3] = c.w;
-        r.qh[0] = e.x; r.qh[1] = e.y; r.qh[2] = e.z; r.qh[3] = e.w;
-        r.sc01 = s.x;  // bytes 0..3: sc[is+0], (odd), sc[is+2], (odd)
-        r.sc23 = s.y;  // bytes 4..7: sc[is+4], (odd), sc[is+6], (odd)
-        r.d = *(const uint16_t*)(p + 208);
+        load16(p + h / 2 + 16 * lh, r.ql0);
+        load16(p + h / 2 + 32 + 16 * lh, r.ql1);
+        load16(p + 128 + h / 4 + 16 * lh, r.qh);
+        // scales sc[h/16 .. h/16+7] and d (bytes 208-209): 5 aligned dwords
+        // from the floor of byte 192 + h/16
+        const uintptr_t ps = (uintptr_t)(p + 192 + h / 16);
+        const uint32_t sh = (uint32_t)(ps & 3);
+        uint32_t w[5];
+        load_dwords<5>((const uint8_t*)(ps & ~(uintptr_t)3), w);
+        r.sc01 = alignb(w[1], w[0], sh);  // bytes 0..3: sc[is+0], (odd), sc[is+2], (odd)
+        r.sc23 = alignb(w[2], w[1], sh);  // bytes 4..7: sc[is+4], (odd), sc[is+6], (odd)
+        // d sits 16 (h = 0) or 8 (h = 128) bytes after the scale window start
+        r.d = hsel ? alignb(w[3], w[2], sh) : alignb(w[4], w[4], sh);
     }
     RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) {
         // unit uu (chunk-relative) → super-block b = uu>>2, half, l-half
@@ -210,6 +403,39 @@ struct FmtQ6K {
             const int sc = (int)(int8_t)((scw >> (16 * (t & 1))) & 255u);
             acc += __builtin_amdgcn_ldexpf(d * (float)sc * limb_combine(z0, z1, z2),
                                            xu.t[t].e - 22);
+        }
+        return acc;
+    }
+    RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
+        const uint32_t b = uu >> 2, hsel = (uu >> 1) & 1, lh = uu & 1;
+        const XRec* base = xs + 8 * b + 4 * hsel;
+        const float d = h2f(r.d);
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const u32x4* p = (const u32x4*)(base + t);
+            const u32x4 lv = p[2 * lq + lh];
+            const u32x4 m = p[6];
+            const int e = (int)(int16_t)(m.x & 0xFFFF);
+            int s0, s1, s2;
+            if (lh == 0) {
+                s0 = (int16_t)(m.x >> 16); s1 = (int16_t)(m.y & 0xFFFF); s2 = (int16_t)(m.y >> 16);
+            } else {
+                s0 = (int16_t)(m.z & 0xFFFF); s1 = (int16_t)(m.z >> 16); s2 = (int16_t)(m.w & 0xFFFF);
+            }
+            // codes are 0..63; −32·Σx (over this 16-element half) seeds the accumulators
+            v4i c = {-32 * s0, -32 * s1, -32 * s2, 0};
+            const uint32_t xl[4] = {lv.x, lv.y, lv.z, lv.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t ql = (t & 1) ? r.ql1[k] : r.ql0[k];
+                const uint32_t lo4 = (t < 2) ? (ql & 0x0F0F0F0Fu) : ((ql >> 4) & 0x0F0F0F0Fu);
+                const uint32_t hi2 = (r.qh[k] >> (2 * t)) & 0x03030303u;
+                c = mfma4(xl[k], lo4 | (hi2 << 4), c);
+            }
+            const uint32_t scw = (t < 2) ? r.sc01 : r.sc23;
+            const int sc = (int)(int8_t)((scw >> (16 * (t & 1))) & 255u);
+            acc += __builtin_amdgcn_ldexpf(d * (float)sc * comb4(c), e - 22);
         }
         return acc;
     }

@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -37,33 +38,66 @@ struct GemvArgs {
 constexpr uint32_t XREC_BYTES = 112;  // one activation record per 32 elements
 
 const char* const kKernelNames[] = {
-    "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_gemv_q8_0_f32_f16",
-    "k_gemv_q8_0_f16_f16", "k_gemv_q8_0_f16_f16add", "k_gemv_q8_0_f16_f32add",
-    "k_qkv_q8_0", "k_qkv_bias_q8_0", "k_ffn_q8_0",
-    "k_gemv_q4_0_f32_f32", "k_gemv_q4_0_f32_f32add", "k_gemv_q4_0_f32_f16",
-    "k_gemv_q4_0_f16_f16", "k_gemv_q4_0_f16_f16add", "k_qkv_bias_q4_0", "k_ffn_q4_0",
-    "k_gemv_q4k_f32_f32", "k_gemv_q4k_f32_f32add", "k_gemv_q4k_f16_f16",
-    "k_gemv_q4k_f16_f16add", "k_gemv_q4k_f16_f32add", "k_ffn_q4k",
-    "k_gemv_q6k_f32_f32", "k_gemv_q6k_f32_f32add", "k_gemv_q6k_f32_f16",
+    "k_gemv_q8_0_f32_f32_r1", "k_gemv_q8_0_f32_f32_r2",
+    "k_gemv_q8_0_f32_f32add_r1", "k_gemv_q8_0_f32_f32add_r2",
+    "k_gemv_q8_0_f32_f16_r1", "k_gemv_q8_0_f32_f16_r2",
+    "k_gemv_q8_0_f16_f16_r1", "k_gemv_q8_0_f16_f16_r2",
+    "k_gemv_q8_0_f16_f16add_r1", "k_gemv_q8_0_f16_f16add_r2",
+    "k_gemv_q8_0_f16_f32add_r1", "k_gemv_q8_0_f16_f32add_r2",
+    "k_qkv_q8_0_r1", "k_qkv_q8_0_r2",
+    "k_qkv_bias_q8_0_r1", "k_qkv_bias_q8_0_r2",
+    "k_ffn_q8_0_r1", "k_ffn_q8_0_r2",
+    "k_gemv_q4_0_f32_f32_r1", "k_gemv_q4_0_f32_f32_r2",
+    "k_gemv_q4_0_f32_f32add_r1", "k_gemv_q4_0_f32_f32add_r2",
+    "k_gemv_q4_0_f32_f16_r1", "k_gemv_q4_0_f32_f16_r2",
+    "k_gemv_q4_0_f16_f16_r1", "k_gemv_q4_0_f16_f16_r2",
+    "k_gemv_q4_0_f16_f16add_r1", "k_gemv_q4_0_f16_f16add_r2",
+    "k_qkv_bias_q4_0_r1", "k_qkv_bias_q4_0_r2",
+    "k_ffn_q4_0_r1", "k_ffn_q4_0_r2",
+    "k_gemv_q4k_f32_f32_r1", "k_gemv_q4k_f32_f32_r2",
+    "k_gemv_q4k_f32_f32add_r1", "k_gemv_q4k_f32_f32add_r2",
+    "k_gemv_q4k_f16_f16_r1", "k_gemv_q4k_f16_f16_r2",
+    "k_gemv_q4k_f16_f16add_r1", "k_gemv_q4k_f16_f16add_r2",
+    "k_gemv_q4k_f16_f32add_r1", "k_gemv_q4k_f16_f32add_r2",
+    "k_ffn_q4k_r1", "k_ffn_q4k_r2",
+    "k_gemv_q6k_f32_f32_r1", "k_gemv_q6k_f32_f32_r2",
+    "k_gemv_q6k_f32_f32add_r1", "k_gemv_q6k_f32_f32add_r2",
+    "k_gemv_q6k_f32_f16_r1", "k_gemv_q6k_f32_f16_r2",
+    "k_gemv_q8_0_f32_f32_s1", "k_gemv_q8_0_f32_f32add_s1", "k_gemv_q8_0_f32_f16_s1",
+    "k_gemv_q8_0_f16_f16_s1", "k_gemv_q8_0_f16_f16add_s1", "k_gemv_q8_0_f16_f32add_s1",
+    "k_qkv_q8_0_s1", "k_qkv_bias_q8_0_s1", "k_ffn_q8_0_s1",
+    "k_gemv_q4_0_f32_f32_s1", "k_gemv_q4_0_f32_f32add_s1", "k_gemv_q4_0_f32_f16_s1",
+    "k_gemv_q4_0_f16_f16_s1", "k_gemv_q4_0_f16_f16add_s1", "k_qkv_bias_q4_0_s1", "k_ffn_q4_0_s1",
     "k_dequant_q8_0_f32", "k_dequant_q4_0_f32", "k_dequant_q4k_f32", "k_dequant_q4k_f16",
     "k_dequant_q6k_f32",
     "k_argmax_f32", "k_argmax_f16",
     "k_synth_normal_f32", "k_synth_normal_f16", "k_synth_q8_0", "k_synth_q4_0",
     "k_synth_q4k", "k_synth_q6k",
+    "k_stream_read", "k_stream_copy",
 };
 
 struct Fmt {
     uint32_t blk_el, blk_bytes, unit_el;
+    uint32_t unroll;  // UNR template constant of the format's kernels
     const char* name;
+    const Fmt* single;  // single-block-unit fallback for odd block counts
 };
-constexpr Fmt kQ8_0{32, 34, 32, "Q8_0"};
-constexpr Fmt kQ4_0{32, 18, 32, "Q4_0"};
-constexpr Fmt kQ4K{256, 144, 64, "Q4_K"};
-constexpr Fmt kQ6K{256, 210, 64, "Q6_K"};
+// Q8_0 / Q4_0 kernels take two blocks per unit (4-byte-aligned loads); rows
+// with an odd number of blocks use the one-block "_s1" kernels.
+constexpr Fmt kQ8_0S{32, 34, 32, 2, "Q8_0", nullptr};
+constexpr Fmt kQ4_0S{32, 18, 32, 4, "Q4_0", nullptr};
+constexpr Fmt kQ8_0{32, 34, 64, 1, "Q8_0", &kQ8_0S};
+constexpr Fmt kQ4_0{32, 18, 64, 2, "Q4_0", &kQ4_0S};
+constexpr Fmt kQ4K{256, 144, 64, 1, "Q4_K", nullptr};
+constexpr Fmt kQ6K{256, 210, 64, 1, "Q6_K", nullptr};
 
 thread_local std::string g_global_error = "no error";
 
 }  // namespace
+
+struct Plan {
+    uint32_t T, TL, rpl;
+};
 
 struct rt_ctx {
     int device = 0;
@@ -74,6 +108,10 @@ struct rt_ctx {
     size_t max_lds = 65536;
     std::string err = "no error";
     bool capturing = false;
+    // Tuning knob: RUNIT_GEMV_PLAN="T,TL,rpl" forces one launch plan for
+    // every GEMV-family call (sweeps only; validated at context creation).
+    Plan plan_override{};
+    uint32_t grid_per_cu = 0;  // RUNIT_GEMV_GRID_PER_CU: persistent-grid cap (sweeps only)
 };
 struct rt_event { hipEvent_t ev; };
 struct rt_graph { hipGraph_t graph; hipGraphExec_t exec; };
@@ -118,25 +156,50 @@ int launch(rt_ctx* c, const char* name, dim3 grid, dim3 block, size_t lds, void*
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-// Lanes per row group: maximise the fraction of busy lane-steps over the
-// row's units; prefer wider groups on ties (fewer, more contiguous rows).
-uint32_t pick_lpr(uint32_t units) {
-    uint32_t best = 64;
-    double best_eff = -1.0;
-    for (uint32_t lpr : {64u, 32u, 16u, 8u, 4u}) {
-        const uint32_t steps = (units + lpr - 1) / lpr;
-        const double eff = (double)units / (double)(steps * lpr);
-        if (eff > best_eff + 1e-9) {
-            best_eff = eff;
-            best = lpr;
+// Launch plan for one GEMV-family call.
+//   T   threads per workgroup (256, or 512 when K is long so the activation
+//       staging is shared by more lanes);
+//   TL  threads per row group: the smallest power of two ≥ 16 that covers a
+//       row in ≤ 2 unrolled steps with ≥ 85% busy lanes (row groups wider
+//       than a wave reduce across waves through LDS);
+//   rows per lane group: 2 (kernel suffix _r2) when that still leaves ≥ 2
+//       workgroups per CU, else 1 (_r1) to spread small-N problems wider.
+Plan plan_gemv(const rt_ctx* c, const Fmt& f, uint32_t nvrows, uint32_t K, bool paired) {
+    const uint32_t units = K / f.unit_el;
+    Plan p{};
+    if (c->plan_override.T) return c->plan_override;
+    p.T = (K / 32 >= 256) ? 512 : 256;
+    p.TL = 0;
+    for (uint32_t tl = 16; tl <= p.T; tl *= 2) {
+        const uint32_t steps = (units + tl - 1) / tl;
+        const double eff = (double)units / (double)(steps * tl);
+        if (steps <= 2 * f.unroll && eff >= 0.85) {
+            p.TL = tl;
+            break;
         }
     }
-    return best;
+    if (!p.TL) {
+        double best = -1.0;
+        for (uint32_t tl = 16; tl <= p.T; tl *= 2) {
+            const uint32_t steps = (units + tl - 1) / tl;
+            const double eff = (double)units / (double)(steps * tl);
+            if (eff > best + 1e-9) {
+                best = eff;
+                p.TL = tl;
+            }
+        }
+    }
+    const uint32_t groups = p.T / p.TL;
+    const uint32_t r2 = paired ? 4 : 2;
+    const uint32_t wgs_r2 = (nvrows + groups * r2 - 1) / (groups * r2);
+    p.rpl = (wgs_r2 >= (uint32_t)(2 * c->cu_count)) ? 2 : 1;
+    return p;
 }
 
-constexpr uint32_t RPL = 2;  // rows per lane group (template constant of every GEMV kernel)
-
-int gemv_launch(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a, bool x_f16) {
+int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x_f16,
+                bool paired = false) {
+    const bool single = fmt.single && (a.K % fmt.unit_el) != 0;
+    const Fmt& f = single ? *fmt.single : fmt;
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     if (a.K == 0 || a.K % f.blk_el != 0)
         return fail(c, RT_ERR_DISPATCH,
@@ -149,26 +212,44 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a, bool x_f
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: %s: input must be %d-byte aligned", kname,
                     x_f16 ? 8 : 16);
-    const uint32_t units = a.K / f.unit_el;
-    a.lpr = pick_lpr(units);
     a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
     const uint32_t nxb = a.K / 32;
-    const size_t lds_cap = std::min<size_t>(c->max_lds, 80 * 1024);
+    const size_t red_bytes = 8 * 4 * sizeof(float);
+    const size_t lds_cap = std::min<size_t>(c->max_lds, 80 * 1024) - red_bytes;
     uint32_t chunk = (uint32_t)(lds_cap / XREC_BYTES) & ~7u;
     if (chunk >= nxb) chunk = nxb;
     a.xb_chunk = chunk;
-    const size_t lds = (size_t)chunk * XREC_BYTES;
-
-    const uint32_t vrows_per_wave = (64 / a.lpr) * RPL;
-    uint32_t waves = 4;
-    auto tiles = [&](uint32_t w) { return (a.nvrows + vrows_per_wave * w - 1) / (vrows_per_wave * w); };
-    while (waves > 1 && tiles(waves) < (uint32_t)(2 * c->cu_count)) waves /= 2;
-    const uint32_t ntiles = tiles(waves);
-    uint32_t resident = std::min<uint32_t>(32 / waves, (uint32_t)(160 * 1024 / std::max<size_t>(lds, 1)));
-    resident = std::max<uint32_t>(resident, 1);
+    const size_t lds = (size_t)chunk * XREC_BYTES + red_bytes;
+    Plan p;
+    uint32_t rows_per_wg;
+    uint32_t resident;
+    if (chunk == nxb && !single) {
+        // Matrix-core path: a wave covers RQ quads of 4 rows, 16 lanes per
+        // row; persistent grid of `gpc` workgroups per CU.
+        p = Plan{256, 16, 1};
+        if (c->plan_override.T) p = Plan{c->plan_override.T, 16, c->plan_override.rpl};
+        rows_per_wg = (p.T / 64) * 4 * p.rpl;
+        resident = c->grid_per_cu ? c->grid_per_cu : 4;
+    } else {
+        // chunked (long-K) and single-block kernels: one row (FFN: one gate/up
+        // pair) per row group
+        p = plan_gemv(c, f, a.nvrows, a.K, paired);
+        p.rpl = 1;
+        rows_per_wg = (p.T / p.TL) * (paired ? 2 * p.rpl : p.rpl);
+        resident = std::min<uint32_t>(2048 / p.T, (uint32_t)(160 * 1024 / lds));
+        resident = std::max<uint32_t>(resident, 1);
+        if (c->grid_per_cu) resident = std::min<uint32_t>(resident, c->grid_per_cu);
+    }
+    a.lpr = p.TL;
+    const uint32_t ntiles = (a.nvrows + rows_per_wg - 1) / rows_per_wg;
     const uint32_t grid = std::min<uint32_t>(ntiles, (uint32_t)c->cu_count * resident);
+    char name[96];
+    if (single)
+        snprintf(name, sizeof name, "%s_s1", kname);
+    else
+        snprintf(name, sizeof name, "%s_r%u", kname, p.rpl);
     void* params[] = {&a};
-    return launch(c, kname, dim3(grid), dim3(64 * waves), lds, params);
+    return launch(c, name, dim3(grid), dim3(p.T), lds, params);
 }
 
 GemvArgs plain_args(const void* w, const void* x, void* y, const void* aux, uint32_t m,
@@ -219,7 +300,7 @@ int ffn_launch(rt_ctx* c, const char* kname, const Fmt& f, const void* wg, const
     a.n[0] = ff; a.n[1] = ff;
     a.nvrows = 2 * ff;
     a.K = k;
-    return gemv_launch(c, kname, f, a, false);
+    return gemv_launch(c, kname, f, a, false, true);
 }
 
 int elementwise_launch(rt_ctx* c, const char* kname, const void* in, void* out, uint64_t n_el) {
@@ -272,7 +353,16 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, 0) == hipSuccess &&
         lds > 0)
         c->max_lds = (size_t)lds;
-    std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
+    if (const char* ov = getenv("RUNIT_GEMV_PLAN")) {
+        unsigned T = 0, TL = 0, r = 0;
+        if (sscanf(ov, "%u,%u,%u", &T, &TL, &r) == 3 && (T == 64 || T == 128 || T == 256 || T == 512) &&
+            TL >= 1 && TL <= T && (TL & (TL - 1)) == 0 && (r == 1 || r == 2))
+            c->plan_override = Plan{T, TL, r};
+    }
+    if (const char* g = getenv("RUNIT_GEMV_GRID_PER_CU")) c->grid_per_cu = (uint32_t)atoi(g);
+    const char* env_co = getenv("RUNIT_CODE_OBJECT");
+    std::string path = code_object_path ? std::string(code_object_path)
+                                        : (env_co ? std::string(env_co) : default_code_object_path());
     e = hipModuleLoad(&c->module, path.c_str());
     if (e != hipSuccess) {
         delete c;
@@ -646,6 +736,29 @@ int rt_synth_q4k(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
 }
 int rt_synth_q6k(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
     return synth_launch(c, "k_synth_q6k", out, nb, seed, std, false, 0.0f);
+}
+
+// ───────────────────────────── calibration ─────────────────────────────
+
+int rt_stream_read(rt_ctx* c, const void* src, size_t bytes, uint32_t* sink, size_t sink_dwords) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!src || !sink || bytes % 16)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: stream_read: bad arguments");
+    uint32_t grid = (uint32_t)std::min<size_t>(sink_dwords / 4, (size_t)c->cu_count * 8);
+    if (grid == 0) return fail(c, RT_ERR_BUFFER_SIZE, "buffer size mismatch: expected 16 bytes, got %zu", sink_dwords * 4);
+    uint64_t n16 = bytes / 16;
+    void* params[] = {&src, &n16, &sink};
+    return launch(c, "k_stream_read", dim3(grid), dim3(256), 0, params);
+}
+
+int rt_stream_copy(rt_ctx* c, void* dst, const void* src, size_t bytes) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!src || !dst || bytes % 16)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: stream_copy: bad arguments");
+    uint64_t n16 = bytes / 16;
+    uint32_t grid = (uint32_t)std::min<uint64_t>((n16 + 255) / 256, (uint64_t)c->cu_count * 8);
+    void* params[] = {&src, &dst, &n16};
+    return launch(c, "k_stream_copy", dim3(grid), dim3(256), 0, params);
 }
 
 }  // extern "C"

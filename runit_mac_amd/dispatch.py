@@ -102,6 +102,8 @@ _SIGS = {
         "rt_dequant_q8_0_f32", "rt_dequant_q4_0_f32", "rt_dequant_q4k_f32",
         "rt_dequant_q6k_f32", "rt_dequant_q4k_f16", "rt_argmax_f32", "rt_argmax_f16")},
     "rt_gemm_q8_0_f32": [_P, _P, _P, _P, _U32, _U32, _U32],
+    "rt_stream_read": [_P, _P, c_size_t, _P, c_size_t],
+    "rt_stream_copy": [_P, _P, _P, c_size_t],
     "rt_synth_normal_f32": [_P, _P, _U64, _U64, _F, _F],
     "rt_synth_normal_f16": [_P, _P, _U64, _U64, _F, _F],
     **{n: [_P, _P, _U64, _U64, _F] for n in (
@@ -236,7 +238,7 @@ class HipContext:
     def __init__(self, code_object: str | None = None):
         self.lib = load_library()
         h = c_void_p()
-        path = (code_object or HSACO_PATH).encode()
+        path = (code_object or os.environ.get("RUNIT_CODE_OBJECT") or HSACO_PATH).encode()
         st = self.lib.rt_ctx_create(ctypes.byref(h), path)
         if st != 0:
             raise _STATUS.get(st, KernelError)(self.lib.rt_global_last_error().decode())
@@ -407,6 +409,16 @@ def synth_normal_f16(ctx, out, n, seed, mean=0.0, std=1.0):
 def synth_weights(ctx, fmt: str, out, n_blocks, seed, std=0.02):
     """Seeded N(0, std) weights quantised per block (fmt in q8_0/q4_0/q4k/q6k)."""
     _call(ctx, f"rt_synth_{fmt}", _ptr(out), n_blocks, seed, std)
+
+
+def stream_read(ctx, src, nbytes, sink, sink_dwords):
+    """Calibration: plain HBM read of nbytes."""
+    _call(ctx, "rt_stream_read", _ptr(src), nbytes, _ptr(sink), sink_dwords)
+
+
+def stream_copy(ctx, dst, src, nbytes):
+    """Calibration: plain HBM copy of nbytes."""
+    _call(ctx, "rt_stream_copy", _ptr(dst), _ptr(src), nbytes)
 
 
 # Block geometry (crates/gguf/src/types.rs:158-191).

@@ -198,6 +198,6 @@ def test_gemv_rejects_bad_k(ctx):
 
 
 def test_pipeline_lookup(ctx):
-    ctx.has_kernel("k_gemv_q8_0_f32_f32")
+    ctx.has_kernel("k_gemv_q8_0_f32_f32_r1")
     with pytest.raises(d.PipelineNotFound):
         ctx.has_kernel("no_such_kernel")
