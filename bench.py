@@ -42,6 +42,28 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+class Arena:
+    """One device allocation carved into 256-byte-aligned sub-buffers: model
+    weights live in one large allocation, as a loaded model's would."""
+
+    def __init__(self, ctx, nbytes):
+        self.buf = ctx.new_buffer(nbytes)
+        self.base, self.off, self.size = self.buf.ptr, 0, nbytes
+
+    def take(self, nbytes) -> int:
+        p = self.base + self.off
+        self.off += (nbytes + 255) & ~255
+        assert self.off <= self.size, "arena overflow"
+        return p
+
+    def free(self):
+        self.buf.free()
+
+
+def _arena_for(ctx, sizes, reps):
+    return Arena(ctx, reps * sum((b + 255) & ~255 for b in sizes) + 4096)
+
+
 class Workload:
     """A set of launches over rotating weight replicas."""
 
@@ -52,11 +74,12 @@ class Workload:
         wbytes = d.weight_bytes(fmt, n, k)
         self.wbytes_per_launch = nmat * wbytes
         self.reps = max(2, min(512, -(-WORKSET_BYTES // self.wbytes_per_launch)))
+        self.arena = _arena_for(ctx, [wbytes] * nmat, self.reps)
         self.w = []
         for r in range(self.reps):
             mats = []
             for j in range(nmat):
-                b = ctx.new_buffer(wbytes)
+                b = self.arena.take(wbytes)
                 d.synth_weights(ctx, fmt, b, n * k // el, seed * 1000 + r * 2 + j)
                 mats.append(b)
             self.w.append(mats)
@@ -104,9 +127,7 @@ class Workload:
             raise ValueError(self.kind)
 
     def free(self):
-        for mats in self.w:
-            for b in mats:
-                b.free()
+        self.arena.free()
         self.w = []
 
 
@@ -119,11 +140,12 @@ class QKVWorkload(Workload):
         dims = (q_dim, kv_dim, kv_dim)
         self.wbytes_per_launch = sum(d.weight_bytes(fmt, n, k) for n in dims)
         self.reps = max(2, min(512, -(-WORKSET_BYTES // self.wbytes_per_launch)))
+        self.arena = _arena_for(ctx, [d.weight_bytes(fmt, n, k) for n in dims], self.reps)
         self.w = []
         for r in range(self.reps):
             mats = []
             for j, n in enumerate(dims):
-                b = ctx.new_buffer(d.weight_bytes(fmt, n, k))
+                b = self.arena.take(d.weight_bytes(fmt, n, k))
                 d.synth_weights(ctx, fmt, b, n * k // el, seed * 1000 + r * 3 + j)
                 mats.append(b)
             self.w.append(mats)
@@ -145,6 +167,8 @@ class QKVWorkload(Workload):
 def time_workload(ctx, wl: Workload, steps: int, warmup: int) -> dict:
     """Graph of `reps` launches (one per replica), replayed; returns µs/launch."""
     launches = wl.reps
+    wl.launch(0)  # eager first call: sizes the context workspace before capture
+    ctx.flush()
     ctx.capture_begin()
     for r in range(launches):
         wl.launch(r)
@@ -223,6 +247,8 @@ def main():
         ("c3_q4_0_ffn_2x18944x3584", lambda: Workload(ctx, "c3_ffn", "q4_0", "ffn", 18944, 3584, seed=2)),
         ("c3_q4_0_down_3584x18944", lambda: Workload(ctx, "c3_down", "q4_0", "add", 3584, 18944, seed=3)),
         ("c3_q4_0_qkv_4608x3584", lambda: QKVWorkload(ctx, "c3_qkv", "q4_0", 3584, 512, 3584, seed=4)),
+        ("x_q4_0_plain_4608x3584", lambda: Workload(ctx, "xq4", "q4_0", "gemv", 4608, 3584, seed=12)),
+        ("x_q8_0_plain_4608x3584", lambda: Workload(ctx, "xq8", "q8_0", "gemv", 4608, 3584, seed=13)),
         ("c4_q4k_q_3584x3584", lambda: Workload(ctx, "c4_q", "q4k", "gemv", 3584, 3584, seed=5)),
         ("c4_q4k_ffn_2x18944x3584", lambda: Workload(ctx, "c4_ffn", "q4k", "ffn", 18944, 3584, seed=6)),
         ("c4_q6k_down_3584x18944", lambda: Workload(ctx, "c4_down", "q6k", "add", 3584, 18944, seed=7)),

@@ -22,6 +22,8 @@ struct GemvArgs {
     uint32_t nvrows;     // virtual rows covered by the launch
     uint32_t K;
     uint32_t lpr;        // lanes per row group (1..64, power of two)
+    uint32_t ksw;        // matrix-core path: waves sharing one row-quad group (K split)
+    uint32_t x_rec;      // x already holds activation records (built by k_act_limbs)
     uint32_t xb_chunk;   // activation records staged per LDS pass (multiple of 8)
     uint64_t row_bytes;
 };
@@ -55,6 +57,18 @@ RT_DEV void vrow_map(const GemvArgs& a, uint32_t vr, uint32_t& mat, uint32_t& r)
     }
 }
 
+// Matrix selection by value (select chains): indexing the by-value argument
+// arrays with a runtime index would move the whole argument block to scratch.
+template <typename T>
+RT_DEV T pick3(T a0, T a1, T a2, uint32_t m) {
+    return m == 0 ? a0 : (m == 1 ? a1 : a2);
+}
+RT_DEV const uint8_t* mat_w(const GemvArgs& a, uint32_t m) { return pick3(a.w[0], a.w[1], a.w[2], m); }
+RT_DEV void* mat_out(const GemvArgs& a, uint32_t m) { return pick3(a.out[0], a.out[1], a.out[2], m); }
+RT_DEV const void* mat_aux(const GemvArgs& a, uint32_t m) {
+    return pick3(a.aux[0], a.aux[1], a.aux[2], m);
+}
+
 RT_DEV float silu_ref(float g) {
     // x / (1 + exp(-x))  (fused_ffn.metal:24-26; dispatch.rs:1684-1686)
     return g / (1.0f + expf(-g));
@@ -76,9 +90,9 @@ RT_DEV void store_row(const GemvArgs& a, uint32_t vr, float v) {
         const float res = h2f(((const uint16_t*)a.aux[0])[r]);
         ((uint16_t*)a.out[0])[r] = f2h(v + res);
     } else if (EPI == EPI_QKV) {
-        ((float*)a.out[mat])[r] = v;
+        ((float*)mat_out(a, mat))[r] = v;
     } else if (EPI == EPI_QKV_BIAS) {
-        ((float*)a.out[mat])[r] = v + h2f(((const uint16_t*)a.aux[mat])[r]);
+        ((float*)mat_out(a, mat))[r] = v + h2f(((const uint16_t*)mat_aux(a, mat))[r]);
     }
 }
 
@@ -135,7 +149,7 @@ RT_DEV void tile_rows(const GemvArgs& a, uint32_t vr0, const uint8_t* rowp[RPL])
         if (vr >= a.nvrows) vr = a.nvrows - 1;  // clamp loads; the store is skipped
         uint32_t mat, r;
         vrow_map<EPI>(a, vr, mat, r);
-        rowp[i] = a.w[mat] + (size_t)r * a.row_bytes;
+        rowp[i] = mat_w(a, mat) + (size_t)r * a.row_bytes;
     }
 }
 
@@ -181,7 +195,7 @@ RT_DEV void gemv_body_pipelined(const GemvArgs& a) {
 
     if (nitems > 0) issue(0, buf[0]);
 #ifndef RT_PROBE_NO_STAGE
-    stage_x_limbs<XT, F::Q40PERM>((const XT*)a.x, 0, nxb, xs);
+    stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, nxb, xs);
 #endif
     __syncthreads();
     if (nitems == 0) return;
@@ -240,7 +254,6 @@ RT_DEV void gemv_body_chunked(const GemvArgs& a) {
     const uint32_t vrows_per_wg = (blockDim.x / TL) * RPL;
     const uint32_t nxb = a.K / 32;
     const uint32_t ntiles = (a.nvrows + vrows_per_wg - 1) / vrows_per_wg;
-    const XT* x = (const XT*)a.x;
 
     for (uint32_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const uint32_t vr0 = tile * vrows_per_wg + grp * RPL;
@@ -252,7 +265,7 @@ RT_DEV void gemv_body_chunked(const GemvArgs& a) {
         for (uint32_t xc = 0; xc < nxb; xc += a.xb_chunk) {
             const uint32_t nx = min(a.xb_chunk, nxb - xc);
             __syncthreads();
-            stage_x_limbs<XT, F::Q40PERM>(x, xc, nx, xs);
+            stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, xc, nx, xs);
             __syncthreads();
             const uint32_t units = nx * 32 / F::UNIT_EL;
             const uint32_t u0 = xc * 32 / F::UNIT_EL;
@@ -293,36 +306,43 @@ template <class F, int EPI, typename XT, int RQ>
 RT_DEV void gemv_mq_body(const GemvArgs& a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     XRec* xs = (XRec*)smem;
+    float* red = (float*)(smem + (size_t)(a.K / 32) * sizeof(XRec));  // [waves][RQ][4]
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
     const uint32_t q = lane & 3, slot = lane >> 2;
     const uint32_t lq = q < 3 ? q : 2;  // the A row of lane q = 3 is a don't-care
-    const uint32_t vrows_per_wg = nwaves * 4 * RQ;
+    // ksw waves share one group of RQ row quads and split its K steps
+    const uint32_t ksw = a.ksw;
+    const uint32_t wgrp = wave / ksw, wk = wave % ksw;
+    const uint32_t vrows_per_wg = (nwaves / ksw) * 4 * RQ;
     const uint32_t ntiles = (a.nvrows + vrows_per_wg - 1) / vrows_per_wg;
     const uint32_t units = a.K / F::UNIT_EL;
     const uint32_t nsteps = (units + 15) / 16;
+    const uint32_t spw = (nsteps + ksw - 1) / ksw;  // steps per wave per tile
     const uint32_t my_tiles =
         blockIdx.x < ntiles ? (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
-    const uint32_t nitems = my_tiles * nsteps;
+    const uint32_t nitems = my_tiles * spw;
 
     typename F::Raw buf[2][RQ];
     auto issue = [&](uint32_t item, typename F::Raw (&dst)[RQ]) {
-        const uint32_t tile = blockIdx.x + (item / nsteps) * gridDim.x;
-        const uint32_t step = item % nsteps;
+        const uint32_t tile = blockIdx.x + (item / spw) * gridDim.x;
+        const uint32_t step = wk + ksw * (item % spw);
         uint32_t u = slot + 16 * step;
         if (u >= units) u = 0;  // clamped: loads stay in bounds, result is discarded
 #pragma unroll
         for (int rq = 0; rq < RQ; ++rq) {
-            uint32_t vr = tile * vrows_per_wg + wave * 4 * RQ + 4 * rq + q;
+            uint32_t vr = tile * vrows_per_wg + wgrp * 4 * RQ + 4 * rq + q;
             if (vr >= a.nvrows) vr = a.nvrows - 1;
             uint32_t mat, r;
             vrow_map<EPI>(a, vr, mat, r);
-            F::load(a.w[mat] + (size_t)r * a.row_bytes, u, dst[rq]);
+            F::load(mat_w(a, mat) + (size_t)r * a.row_bytes, u, dst[rq]);
         }
     };
 
     if (nitems > 0) issue(0, buf[0]);
-    stage_x_limbs<XT, F::Q40PERM>((const XT*)a.x, 0, a.K / 32, xs);
+#ifndef RT_PROBE_NO_STAGE
+    stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, a.K / 32, xs);
+#endif
     __syncthreads();
     if (nitems == 0) return;
 
@@ -334,9 +354,9 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             const uint32_t item = it + half;
-            if (item < nitems) {  // wave-uniform
+            if (item < nitems) {  // uniform across the workgroup
                 if (item + 1 < nitems) issue(item + 1, buf[half ^ 1]);
-                const uint32_t step = item % nsteps;
+                const uint32_t step = wk + ksw * (item % spw);
                 const uint32_t u = slot + 16 * step;
                 const bool valid = u < units;
                 const uint32_t uc = valid ? u : 0;
@@ -345,9 +365,10 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                     const float v = F::mdot(buf[half][rq], xs, uc, lq);
                     acc[rq] += valid ? v : 0.0f;
                 }
-                if (step == nsteps - 1) {
-                    const uint32_t tile = blockIdx.x + (item / nsteps) * gridDim.x;
-                    const uint32_t vbase = tile * vrows_per_wg + wave * 4 * RQ;
+                if (item % spw == spw - 1) {
+                    const uint32_t tile = blockIdx.x + (item / spw) * gridDim.x;
+                    const uint32_t vbase = tile * vrows_per_wg + wgrp * 4 * RQ;
+                    float rsum[RQ];
 #pragma unroll
                     for (int rq = 0; rq < RQ; ++rq) {
                         // sum over the 16 slots of the row: lane bits 2..5
@@ -356,15 +377,40 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                         v += swz_xor_f<8>(v);
                         v += swz_xor_f<16>(v);
                         v += __shfl_xor(v, 32, 64);
+                        rsum[rq] = v;
                         acc[rq] = 0.0f;
-                        const uint32_t vr = vbase + 4 * rq + q;
-                        if (EPI == EPI_FFN) {
-                            // quad holds (gate r, up r, gate r+1, up r+1)
-                            const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
-                            if (slot == 0 && (q & 1) == 0 && vr + 1 < a.nvrows)
-                                ((float*)a.out[0])[vr >> 1] = silu_ref(v) * up;
-                        } else {
-                            if (slot == 0 && vr < a.nvrows) store_row<EPI>(a, vr, v);
+                    }
+                    if (ksw > 1) {
+                        // combine the K-split waves of the group in a fixed order
+                        if (slot == 0) {
+#pragma unroll
+                            for (int rq = 0; rq < RQ; ++rq) red[(wave * RQ + rq) * 4 + q] = rsum[rq];
+                        }
+                        __syncthreads();
+                        if (wk == 0) {
+#pragma unroll
+                            for (int rq = 0; rq < RQ; ++rq) {
+                                float t = 0.0f;
+                                for (uint32_t w = 0; w < ksw; ++w)
+                                    t += red[((wgrp * ksw + w) * RQ + rq) * 4 + q];
+                                rsum[rq] = t;
+                            }
+                        }
+                        __syncthreads();
+                    }
+                    if (wk == 0) {
+#pragma unroll
+                        for (int rq = 0; rq < RQ; ++rq) {
+                            const float v = rsum[rq];
+                            const uint32_t vr = vbase + 4 * rq + q;
+                            if (EPI == EPI_FFN) {
+                                // quad holds (gate r, up r, gate r+1, up r+1)
+                                const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
+                                if (slot == 0 && (q & 1) == 0 && vr + 1 < a.nvrows)
+                                    ((float*)a.out[0])[vr >> 1] = silu_ref(v) * up;
+                            } else {
+                                if (slot == 0 && vr < a.nvrows) store_row<EPI>(a, vr, v);
+                            }
                         }
                     }
                 }
@@ -450,3 +496,24 @@ RT_GEMV_KERNEL(k_ffn_q4k, FmtQ4K, EPI_FFN, float, 1)
 RT_GEMV_KERNEL(k_gemv_q6k_f32_f32, FmtQ6K, EPI_F32, float, 1)
 RT_GEMV_KERNEL(k_gemv_q6k_f32_f32add, FmtQ6K, EPI_F32_ADD, float, 1)
 RT_GEMV_KERNEL(k_gemv_q6k_f32_f16, FmtQ6K, EPI_F16, float, 1)
+
+// Activation pre-pass: builds the limb records of x (nxb records) in global
+// memory once, for launches whose K is too long to convert per workgroup.
+template <typename XT, bool Q40PERM>
+RT_DEV void act_limbs_body(const XT* __restrict__ x, XRec* __restrict__ out, uint32_t nxb) {
+    const uint32_t total = nxb * 8;
+    for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += gridDim.x * blockDim.x) {
+        float v[4];
+        load_x4<XT>(x, (t >> 3) * 32 + (t & 7) * 4, v);
+        limb_slice<Q40PERM>(v, t & 7, out + (t >> 3));
+    }
+}
+extern "C" __global__ void __launch_bounds__(256)
+k_act_limbs_f32(const float* x, XRec* out, uint32_t nxb) { act_limbs_body<float, false>(x, out, nxb); }
+extern "C" __global__ void __launch_bounds__(256)
+k_act_limbs_f32_q40(const float* x, XRec* out, uint32_t nxb) { act_limbs_body<float, true>(x, out, nxb); }
+extern "C" __global__ void __launch_bounds__(256)
+k_act_limbs_f16(const uint16_t* x, XRec* out, uint32_t nxb) { act_limbs_body<uint16_t, false>(x, out, nxb); }
+extern "C" __global__ void __launch_bounds__(256)
+k_act_limbs_f16_q40(const uint16_t* x, XRec* out, uint32_t nxb) { act_limbs_body<uint16_t, true>(x, out, nxb); }

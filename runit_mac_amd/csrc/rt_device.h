@@ -232,6 +232,25 @@ RT_DEV void stage_x_limbs(const XT* __restrict__ x, uint32_t xb0, uint32_t nxb,
     }
 }
 
+// Copies nxb pre-built records (global) into LDS.
+RT_DEV void copy_x_limbs(const XRec* __restrict__ src, uint32_t xb0, uint32_t nxb,
+                         XRec* __restrict__ recs) {
+    const u32x4* s = (const u32x4*)(src + xb0);
+    u32x4* d = (u32x4*)recs;
+    const uint32_t n16 = nxb * (sizeof(XRec) / 16);
+    for (uint32_t i = threadIdx.x; i < n16; i += blockDim.x) d[i] = s[i];
+}
+
+// Stages activations for x-blocks [xb0, xb0+nxb): from f32/f16 values, or
+// from records that an earlier kernel already built (x_rec).
+template <typename XT, bool Q40PERM>
+RT_DEV void stage_x(const void* x, bool x_rec, uint32_t xb0, uint32_t nxb, XRec* recs) {
+    if (x_rec)
+        copy_x_limbs((const XRec*)x, xb0, nxb, recs);
+    else
+        stage_x_limbs<XT, Q40PERM>((const XT*)x, xb0, nxb, recs);
+}
+
 // Registers holding one record (all three limbs + meta).
 struct XRegs {
     uint32_t l[3][8];

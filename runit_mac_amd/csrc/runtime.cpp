@@ -31,6 +31,8 @@ struct GemvArgs {
     uint32_t nvrows;
     uint32_t K;
     uint32_t lpr;
+    uint32_t ksw;
+    uint32_t x_rec;
     uint32_t xb_chunk;
     uint64_t row_bytes;
 };
@@ -74,6 +76,7 @@ const char* const kKernelNames[] = {
     "k_synth_normal_f32", "k_synth_normal_f16", "k_synth_q8_0", "k_synth_q4_0",
     "k_synth_q4k", "k_synth_q6k",
     "k_stream_read", "k_stream_copy",
+    "k_act_limbs_f32", "k_act_limbs_f32_q40", "k_act_limbs_f16", "k_act_limbs_f16_q40",
 };
 
 struct Fmt {
@@ -112,6 +115,12 @@ struct rt_ctx {
     // every GEMV-family call (sweeps only; validated at context creation).
     Plan plan_override{};
     uint32_t grid_per_cu = 0;  // RUNIT_GEMV_GRID_PER_CU: persistent-grid cap (sweeps only)
+    uint32_t ksw_override = 0;  // RUNIT_GEMV_KSW: K-split waves (sweeps only)
+    // Workspace for activation records built by the long-K pre-pass; grows on
+    // demand (stream-ordered, so one buffer serves every launch).
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    uint32_t prepass_k = 8192;  // RUNIT_PREPASS_K: K from which x is converted once
 };
 struct rt_event { hipEvent_t ev; };
 struct rt_graph { hipGraph_t graph; hipGraphExec_t exec; };
@@ -214,7 +223,39 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
                     x_f16 ? 8 : 16);
     a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
     const uint32_t nxb = a.K / 32;
-    const size_t red_bytes = 8 * 4 * sizeof(float);
+    if (!a.x_rec && a.K >= c->prepass_k) {
+        // convert the activations once into the context workspace
+        const size_t need = (size_t)nxb * XREC_BYTES;
+        if (c->capturing && need > c->ws_bytes)
+            return fail(c, RT_ERR_DISPATCH,
+                        "kernel dispatch error: %s: workspace must be sized before graph capture",
+                        kname);
+        if (need > c->ws_bytes) {
+            if (c->ws) {
+                hipError_t e = hipStreamSynchronize(c->stream);
+                if (e != hipSuccess) return hip_fail(c, e, "workspace sync");
+                (void)hipFree(c->ws);
+                c->ws = nullptr;
+                c->ws_bytes = 0;
+            }
+            hipError_t e = hipMalloc(&c->ws, need);
+            if (e != hipSuccess) return hip_fail(c, e, "workspace hipMalloc");
+            c->ws_bytes = need;
+        }
+        const bool q40 = f.blk_bytes == 18;
+        const char* pk = x_f16 ? (q40 ? "k_act_limbs_f16_q40" : "k_act_limbs_f16")
+                               : (q40 ? "k_act_limbs_f32_q40" : "k_act_limbs_f32");
+        const void* xin = a.x;
+        void* xout = c->ws;
+        uint32_t nx = nxb;
+        void* pp[] = {&xin, &xout, &nx};
+        const uint32_t pgrid = (nxb * 8 + 255) / 256;
+        int st = launch(c, pk, dim3(pgrid), dim3(256), 0, pp);
+        if (st != RT_OK) return st;
+        a.x = c->ws;
+        a.x_rec = 1;
+    }
+    const size_t red_bytes = 8 * 2 * 4 * sizeof(float);  // [waves ≤ 8][rows ≤ 2][4]
     const size_t lds_cap = std::min<size_t>(c->max_lds, 80 * 1024) - red_bytes;
     uint32_t chunk = (uint32_t)(lds_cap / XREC_BYTES) & ~7u;
     if (chunk >= nxb) chunk = nxb;
@@ -228,7 +269,19 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         // row; persistent grid of `gpc` workgroups per CU.
         p = Plan{256, 16, 1};
         if (c->plan_override.T) p = Plan{c->plan_override.T, 16, c->plan_override.rpl};
-        rows_per_wg = (p.T / 64) * 4 * p.rpl;
+        // split K over the waves of a workgroup while row-quad groups are
+        // scarcer than the resident waves (latency-bound small problems)
+        const uint32_t nwaves = p.T / 64;
+        const uint32_t quads = (a.nvrows + 4 * p.rpl - 1) / (4 * p.rpl);
+        const uint32_t nsteps = (a.K / f.unit_el + 15) / 16;
+        const uint32_t resident_waves = (uint32_t)c->cu_count * 16;
+        uint32_t ksw = 1;
+        while (ksw < nwaves && quads * ksw < resident_waves && (nsteps + ksw * 2 - 1) / (ksw * 2) >= 1 &&
+               ksw * 2 <= nsteps)
+            ksw *= 2;
+        if (c->ksw_override) ksw = std::min<uint32_t>(c->ksw_override, nwaves);
+        a.ksw = ksw;
+        rows_per_wg = (nwaves / ksw) * 4 * p.rpl;
         resident = c->grid_per_cu ? c->grid_per_cu : 4;
     } else {
         // chunked (long-K) and single-block kernels: one row (FFN: one gate/up
@@ -360,6 +413,11 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
             c->plan_override = Plan{T, TL, r};
     }
     if (const char* g = getenv("RUNIT_GEMV_GRID_PER_CU")) c->grid_per_cu = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_PREPASS_K")) c->prepass_k = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMV_KSW")) {
+        const int v = atoi(g);
+        if (v == 1 || v == 2 || v == 4 || v == 8) c->ksw_override = (uint32_t)v;
+    }
     const char* env_co = getenv("RUNIT_CODE_OBJECT");
     std::string path = code_object_path ? std::string(code_object_path)
                                         : (env_co ? std::string(env_co) : default_code_object_path());
@@ -397,6 +455,7 @@ void rt_ctx_destroy(rt_ctx* c) {
         hipStreamSynchronize(c->stream);
         hipStreamDestroy(c->stream);
     }
+    if (c->ws) hipFree(c->ws);
     if (c->module) hipModuleUnload(c->module);
     delete c;
 }
