@@ -240,6 +240,50 @@ int rt_synth_q4_0(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, floa
 int rt_synth_q4k(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
 int rt_synth_q6k(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
 
+/* ───────────────────────── decode-step glue ─────────────────────────
+ * The non-GEMV kernels of one decode step (forward.rs:1523-1771). */
+
+/* dispatch.rs:177-200 → norm.metal:126-154: y = x·rsqrt(mean(x²)+eps)·γ per
+ * row; y may alias x. */
+int rt_rms_norm_f32_f32_f32g(rt_ctx* ctx, const float* x, float* y, const float* gamma, float eps,
+                             uint32_t hidden, uint32_t num_rows);
+/* dispatch.rs:945-971 → fused_rope.metal:17-56 (pairs (d, d+head_dim/2)). */
+int rt_fused_rope_qk_f32(rt_ctx* ctx, float* q, float* k, uint32_t head_dim, uint32_t q_heads,
+                         uint32_t kv_heads, uint32_t pos, float theta);
+/* dispatch.rs:1183-1205 → activation.metal:30-45: cache[h][pos][d] = src[h][d]. */
+int rt_kv_copy_to_cache_f32(rt_ctx* ctx, const float* src, float* dst, uint32_t pos,
+                            uint32_t max_seq, uint32_t head_dim, uint32_t num_kv_heads);
+/* dispatch.rs:1575-1612 → attention.metal:248-308 (GQA, scale 1/sqrt(hd)).
+ * head_dim must be 64, 128 or 256. */
+int rt_decode_attention_f32(rt_ctx* ctx, const float* q, const float* k, const float* v,
+                            float* out, uint32_t batch, uint32_t kv_len, uint32_t num_heads,
+                            uint32_t num_kv_heads, uint32_t head_dim, uint32_t kv_head_stride);
+/* New: fused_rope_qk_f32 + kv_copy_to_cache_f32 (k and v, at pos) +
+ * decode_attention_f32 (kv_len = pos+1) in one launch; q/k/v are the raw
+ * projections, the caches are [num_kv_heads][max_seq][head_dim]. */
+int rt_decode_attention_rope_f32(rt_ctx* ctx, const float* q_raw, const float* k_raw,
+                                 const float* v_raw, float* k_cache, float* v_cache, float* out,
+                                 uint32_t pos, uint32_t max_seq, uint32_t num_heads,
+                                 uint32_t num_kv_heads, uint32_t head_dim, float theta);
+/* New: out = dequant(table row *token) for a Q8_0 [vocab, k] table; the token
+ * id is read from device memory (forward.rs:1494-1505 does this on the CPU). */
+int rt_embed_q8_0_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+/* New: rms_norm_f32_f32_f32g(x → x̂) fused into the following GEMV's
+ * activation staging (same arguments as the pair of calls, minus x̂). */
+int rt_rms_norm_fused_qkv_bias_q8_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k,
+                                        const void* w_v, const float* x, const float* gamma,
+                                        float eps, float* out_q, float* out_k, float* out_v,
+                                        const uint16_t* bias_q, const uint16_t* bias_k,
+                                        const uint16_t* bias_v, uint32_t q_dim, uint32_t kv_dim,
+                                        uint32_t k);
+int rt_rms_norm_fused_ffn_q8_0_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                                   const float* x, const float* gamma, float eps, float* act_out,
+                                   uint32_t ff_dim, uint32_t k);
+int rt_rms_norm_gemv_q8_0_f32in_f32out(rt_ctx* ctx, const void* weight, const float* x,
+                                       const float* gamma, float eps, float* output, uint32_t m,
+                                       uint32_t k);
+
 /* ───────────────────────── calibration (bench only) ─────────────────────────
  * Plain HBM streams of known size; no reference counterpart.  stream_read
  * reads `bytes` (multiple of 16) and writes one dword per wave to `sink`

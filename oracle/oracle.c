@@ -249,6 +249,64 @@ uint32_t ora_argmax_f32(const float* v, size_t n) {
     return (uint32_t)best;
 }
 
+/* ───────────────────────── decode glue ───────────────────────── */
+
+void ora_rms_norm(const float* x, const float* gamma, double eps, size_t hidden, size_t rows,
+                  double* y) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * hidden;
+        double ss = 0.0;
+        for (size_t i = 0; i < hidden; ++i) ss += (double)xr[i] * (double)xr[i];
+        const double inv = 1.0 / sqrt(ss / (double)hidden + eps);
+        for (size_t i = 0; i < hidden; ++i) y[r * hidden + i] = (double)xr[i] * inv * (double)gamma[i];
+    }
+}
+
+void ora_rope(double* v, size_t heads, size_t head_dim, uint32_t pos, float theta) {
+    const size_t half = head_dim / 2;
+    for (size_t d = 0; d < half; ++d) {
+        const float freq = 1.0f / powf(theta, (float)(2 * d) / (float)head_dim);
+        const float angle = (float)pos * freq;
+        const double c = cos((double)angle), s = sin((double)angle);
+        for (size_t h = 0; h < heads; ++h) {
+            double* x = v + h * head_dim;
+            const double r = x[d], i = x[d + half];
+            x[d] = r * c - i * s;
+            x[d + half] = r * s + i * c;
+        }
+    }
+}
+
+void ora_attention(const double* q, const float* k, const float* v, size_t num_heads,
+                   size_t num_kv_heads, size_t head_dim, size_t kv_len, size_t kv_stride,
+                   double scale, double* out) {
+    const size_t group = num_heads / num_kv_heads;
+    double* sc = (double*)malloc((kv_len ? kv_len : 1) * sizeof(double));
+    for (size_t h = 0; h < num_heads; ++h) {
+        const size_t kvh = h / group;
+        const double* qh = q + h * head_dim;
+        double m = -INFINITY;
+        for (size_t j = 0; j < kv_len; ++j) {
+            const float* kr = k + (kvh * kv_stride + j) * head_dim;
+            double dot = 0.0;
+            for (size_t d = 0; d < head_dim; ++d) dot += qh[d] * (double)kr[d];
+            sc[j] = dot * scale;
+            if (sc[j] > m) m = sc[j];
+        }
+        double l = 0.0;
+        for (size_t j = 0; j < kv_len; ++j) {
+            sc[j] = exp(sc[j] - m);
+            l += sc[j];
+        }
+        for (size_t d = 0; d < head_dim; ++d) {
+            double o = 0.0;
+            for (size_t j = 0; j < kv_len; ++j) o += sc[j] * (double)v[(kvh * kv_stride + j) * head_dim + d];
+            out[h * head_dim + d] = l > 0.0 ? o / l : 0.0;
+        }
+    }
+    free(sc);
+}
+
 /* ───────────────────────── synthetic data ───────────────────────── */
 
 static uint64_t splitmix64(uint64_t z) {

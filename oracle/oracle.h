@@ -61,6 +61,24 @@ double ora_silu(double x);
  * n == 0 → 0. */
 uint32_t ora_argmax_f32(const float* v, size_t n);
 
+/* cpu_rms_norm (dispatch.rs:1699-1702) / rms_norm_f32_f32_f32g in f64:
+ * y = x / sqrt(mean(x²) + eps) · γ, per row of `hidden`. */
+void ora_rms_norm(const float* x, const float* gamma, double eps, size_t hidden, size_t rows,
+                  double* y);
+
+/* fused_rope_qk_f32 (fused_rope.metal:28-55) on one vector of `heads` heads,
+ * in place (f64 data).  The angle is formed exactly as the kernel forms it in
+ * f32 — freq = 1/powf(θ, (2d)/hd), angle = f32(pos)·freq — and the rotation is
+ * evaluated in f64. */
+void ora_rope(double* v, size_t heads, size_t head_dim, uint32_t pos, float theta);
+
+/* Decode attention (attention.metal:248-308; cpu_attention dispatch.rs:
+ * 1712-1742 generalised to GQA): per query head h, kv head h/(H/KVH),
+ * softmax(q·k_j · scale) · v over j < kv_len, in f64.  K/V: [kvh][stride][hd]. */
+void ora_attention(const double* q, const float* k, const float* v, size_t num_heads,
+                   size_t num_kv_heads, size_t head_dim, size_t kv_len, size_t kv_stride,
+                   double scale, double* out);
+
 /* Seeded synthetic data with the same definitions as the device generators
  * (splitmix64 → Box–Muller), used to build golden fixtures on the CPU. */
 float ora_synth_normal(uint64_t seed, uint64_t idx);

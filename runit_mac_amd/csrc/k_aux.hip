@@ -94,18 +94,27 @@ k_dequant_q6k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint6
 // ───────────────────────────── argmax ─────────────────────────────
 // greedy_argmax_f32 (sampler.rs:111-116) folds with Rust's max_by: the
 // running best m is replaced by x unless m > x (partial_cmp None → Equal).
-// Parallel form: each segment summarises to (value, index, absorbing), where
-// `absorbing` means the segment holds a NaN, after which the fold no longer
-// depends on anything before it.  combine(L, R) = R if R.absorbing or
-// !(L.value > R.value), else L — associative, so a tree reduction reproduces
-// the sequential fold exactly (last index wins ties).
-struct AmState { float v; uint32_t i; uint32_t abs; };
+// Unrolled, that fold returns:
+//   * the index of the last NaN, if the last element is NaN;
+//   * otherwise the LAST index of the maximum of the elements after the last
+//     NaN (of all elements when there is no NaN).
+// Both parts are order-independent reductions inside a range, so each
+// workgroup reduces its contiguous range with coalesced loads to a state
+// (last NaN index P, best (value, index) after P), and the ranges are merged
+// in index order: merge(L, R) = R if R has a NaN, else (L.P, later-wins max of
+// L.best and R.best).  The last workgroup to finish (arrival counter, reset by
+// that workgroup) merges all states and writes the result.
+struct AmState {
+    int32_t nan_idx;  // last NaN index in the range, -1 if none
+    int32_t idx;      // index of the best element after nan_idx, -1 if none
+    float v;
+};
+constexpr uint32_t AM_WGS = 256;
+constexpr uint32_t AM_T = 256;
 
-RT_DEV AmState am_combine(AmState L, AmState R, bool rvalid) {
-    if (!rvalid) return L;
-    if (R.abs) return R;
-    if (L.v > R.v) return AmState{L.v, L.i, L.abs};
-    return AmState{R.v, R.i, L.abs};
+RT_DEV bool am_better(float v, int32_t i, float bv, int32_t bi) {
+    // later wins ties; the best so far is replaced unless it is strictly greater
+    return bi < 0 || v > bv || (v == bv && i > bi);
 }
 
 template <typename T>
@@ -116,39 +125,87 @@ template <>
 RT_DEV float am_load<uint16_t>(const uint16_t* p, uint32_t i) { return h2f(p[i]); }
 
 template <typename T>
-RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result, uint32_t n) {
-    // single workgroup of 1024 threads: thread t folds a contiguous slice
-    __shared__ float sv[1024];
-    __shared__ uint32_t si[1024], sa[1024], sok[1024];
-    const uint32_t t = threadIdx.x, nt = blockDim.x;
-    const uint32_t per = (n + nt - 1) / nt;
-    const uint32_t b = t * per, e = min(n, b + per);
-    AmState s{0.0f, 0u, 0u};
-    bool have = false;
-    for (uint32_t i = b; i < e; ++i) {
+RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result, uint32_t n,
+                        AmState* __restrict__ states, uint32_t* __restrict__ counter) {
+    __shared__ int32_t sn[AM_T / 64];
+    __shared__ AmState sb[AM_T / 64];
+    __shared__ bool last;
+    const uint32_t per = (n + gridDim.x - 1) / gridDim.x;
+    const uint32_t b0 = blockIdx.x * per, b1 = min(n, b0 + per);
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // pass 1: last NaN of the range
+    int32_t nl = -1;
+    for (uint32_t i = b0 + tid; i < b1; i += AM_T) {
         const float x = am_load<T>(in, i);
-        AmState r{x, i, (uint32_t)(x != x)};
-        s = have ? am_combine(s, r, true) : r;
-        have = true;
+        if (x != x) nl = (int32_t)i;
     }
-    sv[t] = s.v; si[t] = s.i; sa[t] = s.abs; sok[t] = have ? 1u : 0u;
+    for (int o = 32; o > 0; o >>= 1) nl = max(nl, __shfl_xor(nl, o, 64));
+    if (lane == 0) sn[wave] = nl;
     __syncthreads();
-    for (uint32_t st = 1; st < nt; st <<= 1) {
-        if ((t % (2 * st)) == 0 && t + st < nt) {
-            AmState L{sv[t], si[t], sa[t]}, R{sv[t + st], si[t + st], sa[t + st]};
-            const bool lok = sok[t] != 0, rok = sok[t + st] != 0;
-            AmState o = lok ? am_combine(L, R, rok) : R;
-            sv[t] = o.v; si[t] = o.i; sa[t] = o.abs; sok[t] = (lok || rok) ? 1u : 0u;
-        }
-        __syncthreads();
+    int32_t P = -1;
+    for (uint32_t w = 0; w < AM_T / 64; ++w) P = max(P, sn[w]);
+    // pass 2: best after P
+    float bv = 0.0f;
+    int32_t bi = -1;
+    const uint32_t s0 = (P >= 0) ? (uint32_t)P + 1 : b0;
+    for (uint32_t i = s0 + tid; i < b1; i += AM_T) {
+        const float x = am_load<T>(in, i);
+        if (am_better(x, (int32_t)i, bv, bi)) { bv = x; bi = (int32_t)i; }
     }
-    if (t == 0) result[0] = sok[0] ? si[0] : 0u;
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int32_t oi = __shfl_xor(bi, o, 64);
+        if (oi >= 0 && am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) sb[wave] = AmState{P, bi, bv};
+    __syncthreads();
+    if (tid == 0) {
+        AmState st{P, -1, 0.0f};
+        for (uint32_t w = 0; w < AM_T / 64; ++w)
+            if (sb[w].idx >= 0 && am_better(sb[w].v, sb[w].idx, st.v, st.idx)) {
+                st.v = sb[w].v;
+                st.idx = sb[w].idx;
+            }
+        states[blockIdx.x] = st;
+        __threadfence();
+        last = atomicAdd(counter, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last || tid != 0) return;
+    __threadfence();
+    // merge the ranges in index order
+    AmState acc{-1, -1, 0.0f};
+    bool have = false;
+    for (uint32_t g = 0; g < gridDim.x; ++g) {
+        const volatile AmState* vs = &states[g];
+        const AmState r{vs->nan_idx, vs->idx, vs->v};
+        if (!have) { acc = r; have = true; continue; }
+        if (r.nan_idx >= 0) {
+            acc = r;
+        } else if (r.idx >= 0 && am_better(r.v, r.idx, acc.v, acc.idx)) {
+            acc.v = r.v;
+            acc.idx = r.idx;
+        }
+    }
+    uint32_t res = 0;
+    if (n > 0) {
+        if (acc.nan_idx == (int32_t)n - 1 || acc.idx < 0)
+            res = acc.nan_idx >= 0 ? (uint32_t)acc.nan_idx : 0u;
+        else
+            res = (uint32_t)acc.idx;
+    }
+    result[0] = res;
+    *counter = 0;  // ready for the next call (also under graph replay)
 }
 
-extern "C" __global__ void __launch_bounds__(1024)
-k_argmax_f32(const float* in, uint32_t* result, uint32_t n) { argmax_body<float>(in, result, n); }
-extern "C" __global__ void __launch_bounds__(1024)
-k_argmax_f16(const uint16_t* in, uint32_t* result, uint32_t n) { argmax_body<uint16_t>(in, result, n); }
+extern "C" __global__ void __launch_bounds__(256)
+k_argmax_f32(const float* in, uint32_t* result, uint32_t n, AmState* states, uint32_t* counter) {
+    argmax_body<float>(in, result, n, states, counter);
+}
+extern "C" __global__ void __launch_bounds__(256)
+k_argmax_f16(const uint16_t* in, uint32_t* result, uint32_t n, AmState* states, uint32_t* counter) {
+    argmax_body<uint16_t>(in, result, n, states, counter);
+}
 
 // ───────────────────────────── synthetic data ─────────────────────────────
 // Counter-based: element `idx` of stream `seed` is one splitmix64 hash turned

@@ -24,6 +24,8 @@ struct GemvArgs {
     uint32_t lpr;        // lanes per row group (1..64, power of two)
     uint32_t ksw;        // matrix-core path: waves sharing one row-quad group (K split)
     uint32_t x_rec;      // x already holds activation records (built by k_act_limbs)
+    const float* gamma;  // non-null: RMSNorm(x)·γ is staged instead of x (f32 x, whole K)
+    float eps;
     uint32_t xb_chunk;   // activation records staged per LDS pass (multiple of 8)
     uint64_t row_bytes;
 };
@@ -195,7 +197,7 @@ RT_DEV void gemv_body_pipelined(const GemvArgs& a) {
 
     if (nitems > 0) issue(0, buf[0]);
 #ifndef RT_PROBE_NO_STAGE
-    stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, nxb, xs);
+    stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, nxb, xs, a.gamma, a.eps);
 #endif
     __syncthreads();
     if (nitems == 0) return;
@@ -341,7 +343,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
 
     if (nitems > 0) issue(0, buf[0]);
 #ifndef RT_PROBE_NO_STAGE
-    stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, a.K / 32, xs);
+    stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, a.K / 32, xs, a.gamma, a.eps);
 #endif
     __syncthreads();
     if (nitems == 0) return;

@@ -2,3 +2,4 @@
 // object (runit_kernels.hsaco) loaded by the host runtime with hipModuleLoad.
 #include "k_gemv.hip"
 #include "k_aux.hip"
+#include "k_decode.hip"

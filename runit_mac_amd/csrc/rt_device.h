@@ -241,12 +241,60 @@ RT_DEV void copy_x_limbs(const XRec* __restrict__ src, uint32_t xb0, uint32_t nx
     for (uint32_t i = threadIdx.x; i < n16; i += blockDim.x) d[i] = s[i];
 }
 
-// Stages activations for x-blocks [xb0, xb0+nxb): from f32/f16 values, or
-// from records that an earlier kernel already built (x_rec).
+// RMSNorm fused into the staging (rms_norm_f32_f32_f32g, norm.metal:126-154,
+// followed by the GEMV): x̂ = x · rsqrt(Σx²/K + eps) · γ, element by element in
+// f32 as the separate kernel computes it, then converted to limbs.  Every
+// workgroup recomputes Σx² over the whole vector (K is the hidden size).
+template <bool Q40PERM>
+RT_DEV void stage_x_norm(const float* __restrict__ x, const float* __restrict__ gamma, float eps,
+                         uint32_t K, XRec* __restrict__ recs) {
+    __shared__ float nred[16];
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x * 4; i < K; i += blockDim.x * 4) {
+        const f32x4 v = *(const f32x4*)(x + i);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (uint32_t w = 0; w < (blockDim.x >> 6); ++w) tot += nred[w];
+    const float rms = rsqrtf(tot / (float)K + eps);
+    const uint32_t total = (K / 32) * 8;
+    const uint32_t step = blockDim.x;
+    for (uint32_t t0 = threadIdx.x; t0 < total; t0 += XSTAGE_UNR * step) {
+        float v[XSTAGE_UNR][4];
+#pragma unroll
+        for (int s = 0; s < XSTAGE_UNR; ++s) {
+            const uint32_t t = t0 + s * step;
+            if (t < total) {
+                const uint32_t i = (t >> 3) * 32 + (t & 7) * 4;
+                const f32x4 a = *(const f32x4*)(x + i);
+                const f32x4 g = *(const f32x4*)(gamma + i);
+                v[s][0] = a.x * rms * g.x;
+                v[s][1] = a.y * rms * g.y;
+                v[s][2] = a.z * rms * g.z;
+                v[s][3] = a.w * rms * g.w;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < XSTAGE_UNR; ++s) {
+            const uint32_t t = t0 + s * step;
+            if (t < total) limb_slice<Q40PERM>(v[s], t & 7, recs + (t >> 3));
+        }
+    }
+}
+
+// Stages activations for x-blocks [xb0, xb0+nxb): from f32/f16 values, from
+// RMSNorm(x) (gamma != null, whole K only), or from records that an earlier
+// kernel already built (x_rec).
 template <typename XT, bool Q40PERM>
-RT_DEV void stage_x(const void* x, bool x_rec, uint32_t xb0, uint32_t nxb, XRec* recs) {
+RT_DEV void stage_x(const void* x, bool x_rec, uint32_t xb0, uint32_t nxb, XRec* recs,
+                    const float* gamma = nullptr, float eps = 0.0f) {
     if (x_rec)
         copy_x_limbs((const XRec*)x, xb0, nxb, recs);
+    else if (gamma)
+        stage_x_norm<Q40PERM>((const float*)x, gamma, eps, nxb * 32, recs);
     else
         stage_x_limbs<XT, Q40PERM>((const XT*)x, xb0, nxb, recs);
 }

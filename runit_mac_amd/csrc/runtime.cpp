@@ -33,11 +33,17 @@ struct GemvArgs {
     uint32_t lpr;
     uint32_t ksw;
     uint32_t x_rec;
+    const float* gamma;
+    float eps;
     uint32_t xb_chunk;
     uint64_t row_bytes;
 };
 
 constexpr uint32_t XREC_BYTES = 112;  // one activation record per 32 elements
+// argmax: 256 workgroup states of 12 bytes, then the arrival counter
+constexpr uint32_t kArgmaxWgs = 256;
+constexpr size_t kAuxCounterOff = 4096;
+constexpr size_t kAuxBytes = 8192;
 
 const char* const kKernelNames[] = {
     "k_gemv_q8_0_f32_f32_r1", "k_gemv_q8_0_f32_f32_r2",
@@ -77,6 +83,10 @@ const char* const kKernelNames[] = {
     "k_synth_q4k", "k_synth_q6k",
     "k_stream_read", "k_stream_copy",
     "k_act_limbs_f32", "k_act_limbs_f32_q40", "k_act_limbs_f16", "k_act_limbs_f16_q40",
+    "k_rms_norm_f32g", "k_rope_qk_f32", "k_kv_copy_f32",
+    "k_decode_attention_f32_hd64", "k_decode_attention_f32_hd128", "k_decode_attention_f32_hd256",
+    "k_attn_rope_f32_hd64", "k_attn_rope_f32_hd128", "k_attn_rope_f32_hd256",
+    "k_embed_q8_0_f32",
 };
 
 struct Fmt {
@@ -121,6 +131,9 @@ struct rt_ctx {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     uint32_t prepass_k = 8192;  // RUNIT_PREPASS_K: K from which x is converted once
+    // Small per-context device buffer: argmax range states + arrival counter
+    // (the counter is reset by the kernel that consumes it).
+    void* aux = nullptr;
 };
 struct rt_event { hipEvent_t ev; };
 struct rt_graph { hipGraph_t graph; hipGraphExec_t exec; };
@@ -205,6 +218,25 @@ Plan plan_gemv(const rt_ctx* c, const Fmt& f, uint32_t nvrows, uint32_t K, bool 
     return p;
 }
 
+// Grows the context workspace to `need` bytes (not during graph capture).
+int ensure_ws(rt_ctx* c, size_t need, const char* who) {
+    if (need <= c->ws_bytes) return RT_OK;
+    if (c->capturing)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: %s: workspace must be sized before graph capture", who);
+    if (c->ws) {
+        hipError_t e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "workspace sync");
+        (void)hipFree(c->ws);
+        c->ws = nullptr;
+        c->ws_bytes = 0;
+    }
+    hipError_t e = hipMalloc(&c->ws, need);
+    if (e != hipSuccess) return hip_fail(c, e, "workspace hipMalloc");
+    c->ws_bytes = need;
+    return RT_OK;
+}
+
 int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x_f16,
                 bool paired = false) {
     const bool single = fmt.single && (a.K % fmt.unit_el) != 0;
@@ -223,25 +255,11 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
                     x_f16 ? 8 : 16);
     a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
     const uint32_t nxb = a.K / 32;
-    if (!a.x_rec && a.K >= c->prepass_k) {
+    if (!a.x_rec && !a.gamma && a.K >= c->prepass_k) {
         // convert the activations once into the context workspace
         const size_t need = (size_t)nxb * XREC_BYTES;
-        if (c->capturing && need > c->ws_bytes)
-            return fail(c, RT_ERR_DISPATCH,
-                        "kernel dispatch error: %s: workspace must be sized before graph capture",
-                        kname);
-        if (need > c->ws_bytes) {
-            if (c->ws) {
-                hipError_t e = hipStreamSynchronize(c->stream);
-                if (e != hipSuccess) return hip_fail(c, e, "workspace sync");
-                (void)hipFree(c->ws);
-                c->ws = nullptr;
-                c->ws_bytes = 0;
-            }
-            hipError_t e = hipMalloc(&c->ws, need);
-            if (e != hipSuccess) return hip_fail(c, e, "workspace hipMalloc");
-            c->ws_bytes = need;
-        }
+        const int st0 = ensure_ws(c, need, kname);
+        if (st0 != RT_OK) return st0;
         const bool q40 = f.blk_bytes == 18;
         const char* pk = x_f16 ? (q40 ? "k_act_limbs_f16_q40" : "k_act_limbs_f16")
                                : (q40 ? "k_act_limbs_f32_q40" : "k_act_limbs_f32");
@@ -438,6 +456,14 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
         }
         c->fns[n] = f;
     }
+    e = hipMalloc(&c->aux, kAuxBytes);
+    if (e == hipSuccess) e = hipMemset(c->aux, 0, kAuxBytes);
+    if (e != hipSuccess) {
+        hipModuleUnload(c->module);
+        delete c;
+        return fail(nullptr, RT_ERR_PIPELINE_CREATE, "failed to allocate context buffer: %s",
+                    hipGetErrorString(e));
+    }
     e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         hipModuleUnload(c->module);
@@ -456,6 +482,7 @@ void rt_ctx_destroy(rt_ctx* c) {
         hipStreamDestroy(c->stream);
     }
     if (c->ws) hipFree(c->ws);
+    if (c->aux) hipFree(c->aux);
     if (c->module) hipModuleUnload(c->module);
     delete c;
 }
@@ -765,8 +792,11 @@ static int argmax_launch(rt_ctx* c, const char* kname, const void* in, uint32_t*
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     if (!res || (n && !in))
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", kname);
-    void* params[] = {&in, &res, &n};
-    return launch(c, kname, dim3(1), dim3(1024), 0, params);
+    void* states = c->aux;
+    void* counter = (char*)c->aux + kAuxCounterOff;
+    const uint32_t grid = std::max<uint32_t>(1, std::min<uint32_t>(kArgmaxWgs, (n + 4095) / 4096));
+    void* params[] = {&in, &res, &n, &states, &counter};
+    return launch(c, kname, dim3(grid), dim3(256), 0, params);
 }
 int rt_argmax_f32(rt_ctx* c, const float* in, uint32_t* res, uint32_t n) {
     return argmax_launch(c, "k_argmax_f32", in, res, n);
@@ -818,6 +848,180 @@ int rt_stream_copy(rt_ctx* c, void* dst, const void* src, size_t bytes) {
     uint32_t grid = (uint32_t)std::min<uint64_t>((n16 + 255) / 256, (uint64_t)c->cu_count * 8);
     void* params[] = {&src, &dst, &n16};
     return launch(c, "k_stream_copy", dim3(grid), dim3(256), 0, params);
+}
+
+}  // extern "C"
+
+// ───────────────────────────── decode-step glue ─────────────────────────────
+
+namespace {
+
+constexpr uint32_t kMaxNormK = 8192;  // whole-K staging limit of the norm-fused GEMVs
+
+// Norm-fused GEMV: whole-K launches fold the norm into the staging; longer K
+// runs rms_norm into the workspace, then the plain kernel.
+int norm_then(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a, bool paired,
+              const float* gamma, float eps) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!gamma) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null gamma", kname);
+    if (a.K <= kMaxNormK) {
+        a.gamma = gamma;
+        a.eps = eps;
+        return gemv_launch(c, kname, f, a, false, paired);
+    }
+    int st = ensure_ws(c, (size_t)a.K * sizeof(float), kname);
+    if (st != RT_OK) return st;
+    st = rt_rms_norm_f32_f32_f32g(c, (const float*)a.x, (float*)c->ws, gamma, eps, a.K, 1);
+    if (st != RT_OK) return st;
+    a.x = c->ws;
+    return gemv_launch(c, kname, f, a, false, paired);
+}
+
+}  // namespace
+
+extern "C" {
+
+int rt_rms_norm_f32_f32_f32g(rt_ctx* c, const float* x, float* y, const float* gamma, float eps,
+                             uint32_t hidden, uint32_t num_rows) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (num_rows == 0 || hidden == 0) return RT_OK;
+    if (!x || !y || !gamma)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: rms_norm: null buffer");
+    void* params[] = {&x, &y, &gamma, &eps, &hidden};
+    return launch(c, "k_rms_norm_f32g", dim3(num_rows), dim3(256), 0, params);
+}
+
+int rt_fused_rope_qk_f32(rt_ctx* c, float* q, float* k, uint32_t head_dim, uint32_t q_heads,
+                         uint32_t kv_heads, uint32_t pos, float theta) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (head_dim < 2 || head_dim % 2)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: rope: head_dim=%u must be even",
+                    head_dim);
+    const uint32_t heads = q_heads > kv_heads ? q_heads : kv_heads;
+    if (heads == 0) return RT_OK;
+    if ((q_heads && !q) || (kv_heads && !k))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: rope: null buffer");
+    const uint32_t half = head_dim / 2;
+    void* params[] = {&q, &k, &head_dim, &q_heads, &kv_heads, &pos, &theta};
+    return launch(c, "k_rope_qk_f32", dim3((half + 63) / 64, heads), dim3(64), 0, params);
+}
+
+int rt_kv_copy_to_cache_f32(rt_ctx* c, const float* src, float* dst, uint32_t pos,
+                            uint32_t max_seq, uint32_t head_dim, uint32_t num_kv_heads) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    const uint32_t n = head_dim * num_kv_heads;
+    if (n == 0) return RT_OK;
+    if (!src || !dst) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: kv_copy: null buffer");
+    if (pos >= max_seq)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: kv_copy: pos=%u ≥ max_seq=%u", pos,
+                    max_seq);
+    void* params[] = {&src, &dst, &pos, &max_seq, &head_dim, (void*)&n};
+    return launch(c, "k_kv_copy_f32", dim3((n + 255) / 256), dim3(256), 0, params);
+}
+
+static int attn_check(rt_ctx* c, uint32_t num_heads, uint32_t num_kv_heads, uint32_t head_dim) {
+    if (num_kv_heads == 0 || num_heads % num_kv_heads)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: attention: num_heads=%u not a multiple of "
+                    "num_kv_heads=%u", num_heads, num_kv_heads);
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: attention: head_dim=%u (supported: 64, 128, 256)",
+                    head_dim);
+    return RT_OK;
+}
+
+int rt_decode_attention_f32(rt_ctx* c, const float* q, const float* k, const float* v, float* out,
+                            uint32_t batch, uint32_t kv_len, uint32_t num_heads,
+                            uint32_t num_kv_heads, uint32_t head_dim, uint32_t kv_head_stride) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (batch == 0 || num_heads == 0) return RT_OK;
+    int st = attn_check(c, num_heads, num_kv_heads, head_dim);
+    if (st != RT_OK) return st;
+    if (!q || !k || !v || !out)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: attention: null buffer");
+    if (kv_len > kv_head_stride)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: attention: kv_len=%u > kv_head_stride=%u", kv_len,
+                    kv_head_stride);
+    const float scale = 1.0f / sqrtf((float)head_dim);  // dispatch.rs:1588
+    void* params[] = {&q, &k, &v, &out, &kv_len, &num_heads, &num_kv_heads,
+                      (void*)&scale, &kv_head_stride};
+    char kn[64];
+    snprintf(kn, sizeof kn, "k_decode_attention_f32_hd%u", head_dim);
+    return launch(c, kn, dim3(num_heads, batch), dim3(256), 0, params);
+}
+
+int rt_decode_attention_rope_f32(rt_ctx* c, const float* q_raw, const float* k_raw,
+                                 const float* v_raw, float* k_cache, float* v_cache, float* out,
+                                 uint32_t pos, uint32_t max_seq, uint32_t num_heads,
+                                 uint32_t num_kv_heads, uint32_t head_dim, float theta) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (num_heads == 0) return RT_OK;
+    int st = attn_check(c, num_heads, num_kv_heads, head_dim);
+    if (st != RT_OK) return st;
+    if (!q_raw || !k_raw || !v_raw || !k_cache || !v_cache || !out)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: attention: null buffer");
+    if (pos >= max_seq)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: attention: pos=%u ≥ max_seq=%u",
+                    pos, max_seq);
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    void* params[] = {&q_raw, &k_raw, &v_raw, &k_cache, &v_cache, &out, &pos, &max_seq,
+                      &num_heads, &num_kv_heads, &theta, (void*)&scale};
+    char kn[64];
+    snprintf(kn, sizeof kn, "k_attn_rope_f32_hd%u", head_dim);
+    return launch(c, kn, dim3(num_heads), dim3(256), 0, params);
+}
+
+int rt_embed_q8_0_f32(rt_ctx* c, const void* table, const uint32_t* token, float* out, uint32_t k) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (k == 0) return RT_OK;
+    if (k % 32)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: embed: k=%u not a multiple of 32", k);
+    if (!table || !token || !out)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: embed: null buffer");
+    void* params[] = {&table, &token, &out, &k};
+    return launch(c, "k_embed_q8_0_f32", dim3((k + 255) / 256), dim3(256), 0, params);
+}
+
+int rt_rms_norm_fused_qkv_bias_q8_0_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                                        const float* x, const float* gamma, float eps, float* oq,
+                                        float* ok, float* ov, const uint16_t* bq,
+                                        const uint16_t* bk, const uint16_t* bv, uint32_t q_dim,
+                                        uint32_t kv_dim, uint32_t k) {
+    if (!wq || !wk || !wv || !oq || !ok || !ov || !bq || !bk || !bv)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: k_qkv_bias_q8_0: null buffer");
+    GemvArgs a{};
+    a.w[0] = (const uint8_t*)wq; a.w[1] = (const uint8_t*)wk; a.w[2] = (const uint8_t*)wv;
+    a.out[0] = oq; a.out[1] = ok; a.out[2] = ov;
+    a.aux[0] = bq; a.aux[1] = bk; a.aux[2] = bv;
+    a.x = x;
+    a.n[0] = q_dim; a.n[1] = kv_dim; a.n[2] = kv_dim;
+    a.nvrows = q_dim + 2 * kv_dim;
+    a.K = k;
+    return norm_then(c, "k_qkv_bias_q8_0", kQ8_0, a, false, gamma, eps);
+}
+
+int rt_rms_norm_fused_ffn_q8_0_f32(rt_ctx* c, const void* wg, const void* wu, const float* x,
+                                   const float* gamma, float eps, float* act, uint32_t ff,
+                                   uint32_t k) {
+    if (!wg || !wu || !act)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: k_ffn_q8_0: null buffer");
+    GemvArgs a{};
+    a.w[0] = (const uint8_t*)wg; a.w[1] = (const uint8_t*)wu;
+    a.out[0] = act;
+    a.x = x;
+    a.n[0] = ff; a.n[1] = ff;
+    a.nvrows = 2 * ff;
+    a.K = k;
+    return norm_then(c, "k_ffn_q8_0", kQ8_0, a, true, gamma, eps);
+}
+
+int rt_rms_norm_gemv_q8_0_f32in_f32out(rt_ctx* c, const void* w, const float* x,
+                                       const float* gamma, float eps, float* y, uint32_t m,
+                                       uint32_t k) {
+    return norm_then(c, "k_gemv_q8_0_f32_f32", kQ8_0, plain_args(w, x, y, nullptr, m, k), false,
+                     gamma, eps);
 }
 
 }  // extern "C"

@@ -1,0 +1,212 @@
+"""One greedy decode step of a Qwen2-shape model over the dispatch API.
+
+This is the caller side of the hot path — the per-layer loop of RunIT's
+`Executor::forward` / `forward_greedy` (crates/engine/src/forward.rs:1470-1787,
+1795-1975) — restated over the C ABI so the GEMV kernels can be measured in
+a whole decode step.  Two kernel sequences are provided:
+
+* ``reference``: the reference's own sequence per layer — rms_norm,
+  fused_qkv_bias, fused_rope_qk, kv_copy ×2, decode_attention, gemv_add (o),
+  rms_norm, fused_ffn, gemv_add (down) — 10 launches per layer;
+* ``fused``: the same arithmetic in 5 launches per layer (RMSNorm folded into
+  the QKV / FFN / LM-head activation staging; RoPE and the KV-cache write
+  folded into attention), captured once into a HIP graph and replayed.
+
+Weights are synthetic (seeded N(0, 0.02) quantised per block, f16 biases
+N(0, 0.02), norms 1 + N(0, 0.02)); the KV cache is pre-filled with N(0, 1)
+for the positions before the decoded one.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import dispatch as d
+
+
+@dataclass(frozen=True)
+class DecodeConfig:
+    """Qwen2.5-0.5B shapes (config.rs:96-265 reads these from GGUF metadata)."""
+    layers: int = 24
+    hidden: int = 896
+    heads: int = 14
+    kv_heads: int = 2
+    head_dim: int = 64
+    ff: int = 4864
+    vocab: int = 151936
+    eps: float = 1e-6
+    theta: float = 1e6
+    max_seq: int = 1024
+
+    @property
+    def q_dim(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.kv_heads * self.head_dim
+
+    def weight_bytes(self) -> int:
+        """Q8_0 weight bytes read per token (each matrix once)."""
+        h, q, kv, ff = self.hidden, self.q_dim, self.kv_dim, self.ff
+        per_layer = sum(d.weight_bytes("q8_0", n, k) for n, k in
+                        ((q, h), (kv, h), (kv, h), (h, q), (ff, h), (ff, h), (h, ff)))
+        return self.layers * per_layer + d.weight_bytes("q8_0", self.vocab, h)
+
+    def step_bytes(self, kv_len: int) -> int:
+        """Algorithmic bytes of one step: weights + KV reads + f16 biases and
+        f32 norms (activations are a few KB and not counted)."""
+        kv = self.layers * 2 * self.kv_heads * kv_len * self.head_dim * 4
+        small = self.layers * ((self.q_dim + 2 * self.kv_dim) * 2 + 2 * self.hidden * 4)
+        return self.weight_bytes() + kv + small + self.hidden * 4
+
+
+class Arena:
+    """Bump allocator over one device allocation (256-byte aligned pieces)."""
+
+    def __init__(self, ctx: d.HipContext, nbytes: int):
+        self.buf = ctx.new_buffer(nbytes)
+        self.off = 0
+
+    def take(self, nbytes: int) -> int:
+        p = self.buf.ptr + self.off
+        self.off += (nbytes + 255) & ~255
+        if self.off > self.buf.nbytes:
+            raise d.BufferSize(f"buffer size mismatch: expected {self.off} bytes, "
+                               f"got {self.buf.nbytes}")
+        return p
+
+
+class DecodeModel:
+    """Synthetic Qwen2-shape model resident in one arena, plus the KV cache."""
+
+    def __init__(self, ctx: d.HipContext, cfg: DecodeConfig = DecodeConfig(), seed: int = 7):
+        self.ctx, self.cfg = ctx, cfg
+        c = cfg
+        h, q, kv, ff = c.hidden, c.q_dim, c.kv_dim, c.ff
+        wb = lambda n, k: d.weight_bytes("q8_0", n, k)  # noqa: E731
+        per_layer = (wb(q, h) + 2 * wb(kv, h) + wb(h, q) + 2 * wb(ff, h) + wb(h, ff)
+                     + 2 * (q + 2 * kv) + 8 * h + 2 * 4 * c.kv_heads * c.max_seq * c.head_dim
+                     + 16 * 256)
+        total = c.layers * per_layer + wb(c.vocab, h) + 16 * h + 64 * 1024 + \
+            4 * (c.vocab + 8 * ff + 8 * q)
+        self.arena = Arena(ctx, total)
+        a = self.arena
+        s = seed * 1000
+
+        def qw(n, k):
+            nonlocal s
+            p = a.take(wb(n, k))
+            d.synth_weights(ctx, "q8_0", p, n * k // 32, s)
+            s += 1
+            return p
+
+        def f32(n, mean, std):
+            nonlocal s
+            p = a.take(4 * n)
+            d.synth_normal_f32(ctx, p, n, s, mean, std)
+            s += 1
+            return p
+
+        def f16(n, std):
+            nonlocal s
+            p = a.take(2 * n)
+            d.synth_normal_f16(ctx, p, n, s, 0.0, std)
+            s += 1
+            return p
+
+        self.layers = []
+        for _ in range(c.layers):
+            L = dict(wq=qw(q, h), wk=qw(kv, h), wv=qw(kv, h), bq=f16(q, 0.02), bk=f16(kv, 0.02),
+                     bv=f16(kv, 0.02), wo=qw(h, q), wg=qw(ff, h), wu=qw(ff, h), wd=qw(h, ff),
+                     attn_norm=f32(h, 1.0, 0.02), ffn_norm=f32(h, 1.0, 0.02),
+                     kc=f32(c.kv_heads * c.max_seq * c.head_dim, 0.0, 1.0),
+                     vc=f32(c.kv_heads * c.max_seq * c.head_dim, 0.0, 1.0))
+            self.layers.append(L)
+        self.final_norm = f32(h, 1.0, 0.02)
+        self.embd = qw(c.vocab, h)  # token_embd, tied LM head (forward.rs:1271-1276)
+        # activations
+        self.x = a.take(4 * h)
+        self.xn = a.take(4 * h)
+        self.q = a.take(4 * q)
+        self.k = a.take(4 * kv)
+        self.v = a.take(4 * kv)
+        self.attn = a.take(4 * q)
+        self.act = a.take(4 * ff)
+        self.logits = a.take(4 * c.vocab)
+        self.token = a.take(256)
+        ctx.flush()
+
+    def set_token(self, tok: int) -> None:
+        d.load_library().rt_upload(self.ctx.handle, self.token,
+                                   np.array([tok], np.uint32).ctypes.data, 4)
+
+    def get_token(self) -> int:
+        out = np.zeros(1, np.uint32)
+        self.ctx._check(d.load_library().rt_download(self.ctx.handle, out.ctypes.data,
+                                                     self.token, 4))
+        return int(out[0])
+
+    def read(self, ptr: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        self.ctx._check(d.load_library().rt_download(self.ctx.handle, out.ctypes.data, ptr,
+                                                     out.nbytes))
+        return out
+
+    # ─────────────────────────── step sequences ───────────────────────────
+
+    def step_reference(self, pos: int) -> None:
+        """forward.rs:1494-1771, the reference's kernel sequence."""
+        ctx, c = self.ctx, self.cfg
+        h, q_dim, kv_dim = c.hidden, c.q_dim, c.kv_dim
+        d.embed_q8_0_f32(ctx, self.embd, self.token, self.x, h)
+        for L in self.layers:
+            d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, L["attn_norm"], c.eps, h, 1)
+            d.fused_qkv_bias_q8_0_f32(ctx, L["wq"], L["wk"], L["wv"], self.xn, self.q, self.k,
+                                      self.v, L["bq"], L["bk"], L["bv"], q_dim, kv_dim, h)
+            d.fused_rope_qk_f32(ctx, self.q, self.k, c.head_dim, c.heads, c.kv_heads, pos,
+                                c.theta)
+            d.kv_copy_to_cache_f32(ctx, self.k, L["kc"], pos, c.max_seq, c.head_dim, c.kv_heads)
+            d.kv_copy_to_cache_f32(ctx, self.v, L["vc"], pos, c.max_seq, c.head_dim, c.kv_heads)
+            d.decode_attention_f32(ctx, self.q, L["kc"], L["vc"], self.attn, 1, pos + 1, c.heads,
+                                   c.kv_heads, c.head_dim, c.max_seq)
+            d.gemv_q8_0_add_f32_f32in_mr(ctx, L["wo"], self.attn, self.x, self.x, h, q_dim)
+            d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, L["ffn_norm"], c.eps, h, 1)
+            d.fused_ffn_q8_0_f32(ctx, L["wg"], L["wu"], self.xn, self.act, c.ff, h)
+            d.gemv_q8_0_add_f32_f32in_mr(ctx, L["wd"], self.act, self.x, self.x, h, c.ff)
+        d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, self.final_norm, c.eps, h, 1)
+        d.gemv_q8_0_f32in_f32out_mr(ctx, self.embd, self.xn, self.logits, c.vocab, h)
+        d.argmax_f32(ctx, self.logits, self.token, c.vocab)
+
+    def step_fused(self, pos: int) -> None:
+        """Same arithmetic, 5 launches per layer."""
+        ctx, c = self.ctx, self.cfg
+        h, q_dim, kv_dim = c.hidden, c.q_dim, c.kv_dim
+        d.embed_q8_0_f32(ctx, self.embd, self.token, self.x, h)
+        for L in self.layers:
+            d.rms_norm_fused_qkv_bias_q8_0_f32(ctx, L["wq"], L["wk"], L["wv"], self.x,
+                                               L["attn_norm"], c.eps, self.q, self.k, self.v,
+                                               L["bq"], L["bk"], L["bv"], q_dim, kv_dim, h)
+            d.decode_attention_rope_f32(ctx, self.q, self.k, self.v, L["kc"], L["vc"], self.attn,
+                                        pos, c.max_seq, c.heads, c.kv_heads, c.head_dim, c.theta)
+            d.gemv_q8_0_add_f32_f32in(ctx, L["wo"], self.attn, self.x, self.x, h, q_dim)
+            d.rms_norm_fused_ffn_q8_0_f32(ctx, L["wg"], L["wu"], self.x, L["ffn_norm"], c.eps,
+                                          self.act, c.ff, h)
+            d.gemv_q8_0_add_f32_f32in(ctx, L["wd"], self.act, self.x, self.x, h, c.ff)
+        d.rms_norm_gemv_q8_0_f32in_f32out(ctx, self.embd, self.x, self.final_norm, c.eps,
+                                          self.logits, c.vocab, h)
+        d.argmax_f32(ctx, self.logits, self.token, c.vocab)
+
+    def capture(self, pos: int, fused: bool = True) -> d.Graph:
+        """One step captured as a HIP graph (the reference's single command
+        buffer per token, context.rs:248-296)."""
+        step = self.step_fused if fused else self.step_reference
+        step(pos)  # eager first run sizes any workspace before capture
+        self.ctx.flush()
+        self.ctx.capture_begin()
+        step(pos)
+        return self.ctx.capture_end()
+
+    def free(self) -> None:
+        self.arena.buf.free()

@@ -102,6 +102,15 @@ _SIGS = {
         "rt_dequant_q8_0_f32", "rt_dequant_q4_0_f32", "rt_dequant_q4k_f32",
         "rt_dequant_q6k_f32", "rt_dequant_q4k_f16", "rt_argmax_f32", "rt_argmax_f16")},
     "rt_gemm_q8_0_f32": [_P, _P, _P, _P, _U32, _U32, _U32],
+    "rt_rms_norm_f32_f32_f32g": [_P, _P, _P, _P, _F, _U32, _U32],
+    "rt_fused_rope_qk_f32": [_P, _P, _P, _U32, _U32, _U32, _U32, _F],
+    "rt_kv_copy_to_cache_f32": [_P, _P, _P, _U32, _U32, _U32, _U32],
+    "rt_decode_attention_f32": [_P, _P, _P, _P, _P] + [_U32] * 6,
+    "rt_decode_attention_rope_f32": [_P] + [_P] * 6 + [_U32] * 5 + [_F],
+    "rt_embed_q8_0_f32": [_P, _P, _P, _P, _U32],
+    "rt_rms_norm_fused_qkv_bias_q8_0_f32": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 + [_U32] * 3,
+    "rt_rms_norm_fused_ffn_q8_0_f32": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32],
+    "rt_rms_norm_gemv_q8_0_f32in_f32out": [_P, _P, _P, _P, _F, _P, _U32, _U32],
     "rt_stream_read": [_P, _P, c_size_t, _P, c_size_t],
     "rt_stream_copy": [_P, _P, _P, c_size_t],
     "rt_synth_normal_f32": [_P, _P, _U64, _U64, _F, _F],
@@ -409,6 +418,64 @@ def synth_normal_f16(ctx, out, n, seed, mean=0.0, std=1.0):
 def synth_weights(ctx, fmt: str, out, n_blocks, seed, std=0.02):
     """Seeded N(0, std) weights quantised per block (fmt in q8_0/q4_0/q4k/q6k)."""
     _call(ctx, f"rt_synth_{fmt}", _ptr(out), n_blocks, seed, std)
+
+
+# ───────────────────────────── decode-step glue ─────────────────────────────
+
+def rms_norm_f32_f32_f32g(ctx, x, y, gamma, eps, hidden, num_rows):
+    """dispatch.rs:177-200"""
+    _call(ctx, "rt_rms_norm_f32_f32_f32g", _ptr(x), _ptr(y), _ptr(gamma), eps, hidden, num_rows)
+
+
+def fused_rope_qk_f32(ctx, q, k, head_dim, q_heads, kv_heads, pos, theta):
+    """dispatch.rs:945-971"""
+    _call(ctx, "rt_fused_rope_qk_f32", _ptr(q), _ptr(k), head_dim, q_heads, kv_heads, pos, theta)
+
+
+def kv_copy_to_cache_f32(ctx, src, dst, pos, max_seq, head_dim, num_kv_heads):
+    """dispatch.rs:1183-1205"""
+    _call(ctx, "rt_kv_copy_to_cache_f32", _ptr(src), _ptr(dst), pos, max_seq, head_dim,
+          num_kv_heads)
+
+
+def decode_attention_f32(ctx, q, k, v, out, batch, kv_len, num_heads, num_kv_heads, head_dim,
+                         kv_head_stride):
+    """dispatch.rs:1575-1612"""
+    _call(ctx, "rt_decode_attention_f32", _ptr(q), _ptr(k), _ptr(v), _ptr(out), batch, kv_len,
+          num_heads, num_kv_heads, head_dim, kv_head_stride)
+
+
+def decode_attention_rope_f32(ctx, q_raw, k_raw, v_raw, k_cache, v_cache, out, pos, max_seq,
+                              num_heads, num_kv_heads, head_dim, theta):
+    """RoPE + KV-cache write + decode attention in one launch (new)."""
+    _call(ctx, "rt_decode_attention_rope_f32", *map(_ptr, (q_raw, k_raw, v_raw, k_cache, v_cache,
+                                                           out)),
+          pos, max_seq, num_heads, num_kv_heads, head_dim, theta)
+
+
+def embed_q8_0_f32(ctx, table, token, out, k):
+    """Q8_0 embedding row of the device-resident token id (new)."""
+    _call(ctx, "rt_embed_q8_0_f32", _ptr(table), _ptr(token), _ptr(out), k)
+
+
+def rms_norm_fused_qkv_bias_q8_0_f32(ctx, w_q, w_k, w_v, x, gamma, eps, out_q, out_k, out_v,
+                                     bias_q, bias_k, bias_v, q_dim, kv_dim, k):
+    """rms_norm_f32_f32_f32g + fused_qkv_bias_q8_0_f32 in one launch (new)."""
+    _call(ctx, "rt_rms_norm_fused_qkv_bias_q8_0_f32", _ptr(w_q), _ptr(w_k), _ptr(w_v), _ptr(x),
+          _ptr(gamma), eps, *map(_ptr, (out_q, out_k, out_v, bias_q, bias_k, bias_v)),
+          q_dim, kv_dim, k)
+
+
+def rms_norm_fused_ffn_q8_0_f32(ctx, w_gate, w_up, x, gamma, eps, act_out, ff_dim, k):
+    """rms_norm_f32_f32_f32g + fused_ffn_q8_0_f32 in one launch (new)."""
+    _call(ctx, "rt_rms_norm_fused_ffn_q8_0_f32", _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(gamma),
+          eps, _ptr(act_out), ff_dim, k)
+
+
+def rms_norm_gemv_q8_0_f32in_f32out(ctx, weight, x, gamma, eps, output, m, k):
+    """rms_norm_f32_f32_f32g + gemv_q8_0_f32in_f32out in one launch (new)."""
+    _call(ctx, "rt_rms_norm_gemv_q8_0_f32in_f32out", _ptr(weight), _ptr(x), _ptr(gamma), eps,
+          _ptr(output), m, k)
 
 
 def stream_read(ctx, src, nbytes, sink, sink_dwords):

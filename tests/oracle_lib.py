@@ -38,6 +38,9 @@ _lib.ora_argmax_f32.argtypes = [_P, _S]
 _lib.ora_argmax_f32.restype = ctypes.c_uint32
 _lib.ora_synth_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
 _lib.ora_synth_normal.restype = ctypes.c_float
+_lib.ora_rms_norm.argtypes = [_P, _P, ctypes.c_double, _S, _S, _P]
+_lib.ora_rope.argtypes = [_P, _S, _S, ctypes.c_uint32, ctypes.c_float]
+_lib.ora_attention.argtypes = [_P, _P, _P, _S, _S, _S, _S, _S, ctypes.c_double, _P]
 for _n in ("q8_0", "q4_0", "q4k", "q6k"):
     getattr(_lib, f"ora_quantize_{_n}").argtypes = [_P, _S, _P]
 
@@ -118,3 +121,31 @@ def synth_weights(fmt: str, n: int, k: int, seed: int, std: float = 0.02) -> np.
     """Host twin of the device generator (libm transcendental functions)."""
     w = (std * synth_normal(seed, n * k)).astype(np.float32)
     return quantize(fmt, w)
+
+
+def rms_norm(x: np.ndarray, gamma: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    gamma = np.ascontiguousarray(gamma, dtype=np.float32)
+    hidden = gamma.size
+    rows = x.size // hidden
+    y = np.empty(x.size, dtype=np.float64)
+    _lib.ora_rms_norm(_p(x), _p(gamma), eps, hidden, rows, _p(y))
+    return y.reshape(x.shape)
+
+
+def rope(v: np.ndarray, heads: int, head_dim: int, pos: int, theta: float) -> np.ndarray:
+    out = np.ascontiguousarray(v, dtype=np.float64).copy()
+    _lib.ora_rope(_p(out), heads, head_dim, pos, theta)
+    return out
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, num_heads: int, num_kv_heads: int,
+              head_dim: int, kv_len: int, kv_stride: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.float64)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.empty(num_heads * head_dim, dtype=np.float64)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+    _lib.ora_attention(_p(q), _p(k), _p(v), num_heads, num_kv_heads, head_dim, kv_len,
+                       kv_stride, scale, _p(out))
+    return out

@@ -1,0 +1,160 @@
+"""GPU parity of the decode-step glue (RMSNorm, RoPE, KV scatter, decode
+attention, fused variants, embedding) against the CPU oracle."""
+import numpy as np
+import pytest
+
+import oracle_lib as ora
+from gpu_helpers import F32_EPS, check_close, device_weights
+from runit_mac_amd import dispatch as d
+
+pytestmark = pytest.mark.gpu
+
+
+def test_rms_norm(ctx):
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((3, 896)).astype(np.float32) * 3
+    g = (1 + 0.02 * rng.standard_normal(896)).astype(np.float32)
+    y = ctx.new_buffer(x.nbytes)
+    d.rms_norm_f32_f32_f32g(ctx, ctx.buffer_from(x), y, ctx.buffer_from(g), 1e-6, 896, 3)
+    ctx.flush()
+    ref = ora.rms_norm(x, g, 1e-6).ravel()
+    got = y.read(np.float32, x.size)
+    # f32 Σx² over 896 terms and one rsqrt: a few ulps relative
+    assert np.all(np.abs(got - ref) <= 4e-6 * np.abs(ref) + 1e-7)
+    # in place (y aliases x), as the reference's QK-norm calls do
+    xb = ctx.buffer_from(x)
+    d.rms_norm_f32_f32_f32g(ctx, xb, xb, ctx.buffer_from(g), 1e-6, 896, 3)
+    ctx.flush()
+    assert np.all(np.abs(xb.read(np.float32, x.size) - ref) <= 4e-6 * np.abs(ref) + 1e-7)
+
+
+@pytest.mark.parametrize("pos", [0, 1, 511, 4095])
+def test_fused_rope(ctx, pos):
+    rng = np.random.default_rng(pos)
+    hd, qh, kvh, theta = 64, 14, 2, 1e6
+    q = rng.standard_normal(qh * hd).astype(np.float32)
+    k = rng.standard_normal(kvh * hd).astype(np.float32)
+    qb, kb = ctx.buffer_from(q), ctx.buffer_from(k)
+    d.fused_rope_qk_f32(ctx, qb, kb, hd, qh, kvh, pos, theta)
+    ctx.flush()
+    for buf, v, h in ((qb, q, qh), (kb, k, kvh)):
+        ref = ora.rope(v, h, hd, pos, theta)
+        got = buf.read(np.float32, v.size).astype(np.float64)
+        vv = v.reshape(h, hd).astype(np.float64)
+        mag = np.abs(np.concatenate([vv[:, :hd // 2], vv[:, :hd // 2]], axis=1)) + \
+            np.abs(np.concatenate([vv[:, hd // 2:], vv[:, hd // 2:]], axis=1))
+        # powf / sincosf of an f32 angle up to ~4e3 rad: ≤ ~1e-4 relative
+        assert np.all(np.abs(got - ref) <= 2e-4 * mag.ravel() + 1e-6)
+
+
+def test_kv_copy(ctx):
+    hd, kvh, max_seq, pos = 64, 2, 40, 17
+    src = np.random.default_rng(1).standard_normal(kvh * hd).astype(np.float32)
+    cache = np.zeros((kvh, max_seq, hd), np.float32)
+    cb = ctx.buffer_from(cache)
+    d.kv_copy_to_cache_f32(ctx, ctx.buffer_from(src), cb, pos, max_seq, hd, kvh)
+    ctx.flush()
+    cache[:, pos] = src.reshape(kvh, hd)
+    assert np.array_equal(cb.read(np.float32, cache.size), cache.ravel())
+
+
+def attn_tol(v, kvh_of, L, hd):
+    vmax = np.max(np.abs(v[:, :max(L, 1)]), axis=1)  # [kvh, hd]
+    return np.concatenate([1e-5 * vmax[kvh_of(h)] + 1e-6 for h in range(len(kvh_of.heads))])
+
+
+@pytest.mark.parametrize("kv_len", [0, 1, 7, 512, 5000])
+def test_decode_attention(ctx, kv_len):
+    rng = np.random.default_rng(kv_len)
+    H, KVH, hd, S = 14, 2, 64, max(kv_len, 1) + 3
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    k = rng.standard_normal((KVH, S, hd)).astype(np.float32)
+    v = rng.standard_normal((KVH, S, hd)).astype(np.float32)
+    out = ctx.new_buffer(4 * H * hd)
+    d.decode_attention_f32(ctx, ctx.buffer_from(q), ctx.buffer_from(k), ctx.buffer_from(v), out,
+                           1, kv_len, H, KVH, hd, S)
+    ctx.flush()
+    ref = ora.attention(q, k, v, H, KVH, hd, kv_len, S)
+    got = out.read(np.float32, H * hd).astype(np.float64)
+    vmax = np.abs(v).max()
+    # f32 scores / exp / weighted sums over ≤ 5000 positions
+    assert np.all(np.abs(got - ref) <= 2e-5 * vmax + 1e-6), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("pos", [0, 511, 4200])
+def test_decode_attention_rope_fused(ctx, pos):
+    rng = np.random.default_rng(pos + 1)
+    H, KVH, hd, max_seq, theta = 14, 2, 64, 4300, 1e6
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    k_new = rng.standard_normal(KVH * hd).astype(np.float32)
+    v_new = rng.standard_normal(KVH * hd).astype(np.float32)
+    kc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float32)
+    vc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float32)
+    kcb, vcb = ctx.buffer_from(kc), ctx.buffer_from(vc)
+    out = ctx.new_buffer(4 * H * hd)
+    d.decode_attention_rope_f32(ctx, ctx.buffer_from(q), ctx.buffer_from(k_new),
+                                ctx.buffer_from(v_new), kcb, vcb, out, pos, max_seq, H, KVH, hd,
+                                theta)
+    ctx.flush()
+    q_r = ora.rope(q, H, hd, pos, theta)
+    k_r = ora.rope(k_new, KVH, hd, pos, theta)
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[:, pos] = k_r.reshape(KVH, hd).astype(np.float32)
+    vc2[:, pos] = v_new.reshape(KVH, hd)
+    got_k = kcb.read(np.float32, kc.size).reshape(kc.shape)
+    got_v = vcb.read(np.float32, vc.size).reshape(vc.shape)
+    # cache: untouched except position pos (v exact, rotated k to RoPE tolerance)
+    mask = np.ones(max_seq, bool)
+    mask[pos] = False
+    assert np.array_equal(got_k[:, mask], kc[:, mask]) and np.array_equal(got_v, vc2)
+    assert np.all(np.abs(got_k[:, pos] - kc2[:, pos]) <= 2e-4 * 2 * np.abs(k_new).max() + 1e-6)
+    ref = ora.attention(q_r, kc2, vc2, H, KVH, hd, pos + 1, max_seq)
+    got = out.read(np.float32, H * hd).astype(np.float64)
+    # RoPE angle error (≤ ~1e-4 relative on q, k) moves the scores by ≲ 1e-3
+    # relative; the output stays within 2e-3·max|v|
+    assert np.all(np.abs(got - ref) <= 2e-3 * np.abs(vc2).max() + 1e-6), np.abs(got - ref).max()
+
+
+def test_embed_q8_0(ctx):
+    vocab, k = 1000, 896
+    tb, raw = device_weights(ctx, "q8_0", vocab, k, 5)
+    tok = ctx.buffer_from(np.array([777], np.uint32))
+    out = ctx.new_buffer(4 * k)
+    d.embed_q8_0_f32(ctx, tb, tok, out, k)
+    ctx.flush()
+    row = ora.dequant("q8_0", raw[777 * (k // 32) * 34:778 * (k // 32) * 34])
+    assert np.array_equal(out.read(np.float32, k).view(np.uint32), row.view(np.uint32))
+
+
+def test_rms_norm_fused_gemvs(ctx):
+    rng = np.random.default_rng(3)
+    h, q_dim, kv_dim, ff = 896, 896, 128, 4864
+    x = (3 * rng.standard_normal(h)).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(h)).astype(np.float32)
+    xn = ora.rms_norm(x, g, 1e-6).astype(np.float32)  # oracle input of the GEMVs (f64→f32)
+    xb, gb = ctx.buffer_from(x), ctx.buffer_from(g)
+    ws = [device_weights(ctx, "q8_0", n, h, 10 + i) for i, n in enumerate((q_dim, kv_dim, kv_dim))]
+    bias = [(0.02 * rng.standard_normal(n)).astype(np.float16) for n in (q_dim, kv_dim, kv_dim)]
+    outs = [ctx.new_buffer(4 * n) for n in (q_dim, kv_dim, kv_dim)]
+    d.rms_norm_fused_qkv_bias_q8_0_f32(ctx, ws[0][0], ws[1][0], ws[2][0], xb, gb, 1e-6, *outs,
+                                       *[ctx.buffer_from(b) for b in bias], q_dim, kv_dim, h)
+    wg, rg = device_weights(ctx, "q8_0", ff, h, 20)
+    wu, ru = device_weights(ctx, "q8_0", ff, h, 21)
+    act = ctx.new_buffer(4 * ff)
+    d.rms_norm_fused_ffn_q8_0_f32(ctx, wg, wu, xb, gb, 1e-6, act, ff, h)
+    wl, rl = device_weights(ctx, "q8_0", 5000, h, 22)
+    yl = ctx.new_buffer(4 * 5000)
+    d.rms_norm_gemv_q8_0_f32in_f32out(ctx, wl, xb, gb, 1e-6, yl, 5000, h)
+    ctx.flush()
+    # the f32-vs-f64 normalised input adds ≤ ~1e-6 relative per element,
+    # inside the 1e-4·Σ|w·x| bound
+    for i, n in enumerate((q_dim, kv_dim, kv_dim)):
+        y, s = ora.gemv("q8_0", ws[i][1], xn, n, h)
+        ref = y + bias[i].astype(np.float64)
+        check_close(outs[i].read(np.float32, n), ref, s, f"norm+qkv[{i}]", F32_EPS * np.abs(ref))
+    from test_gpu_fused import ffn_check
+    gr, gs = ora.gemv("q8_0", rg, xn, ff, h)
+    ur, us = ora.gemv("q8_0", ru, xn, ff, h)
+    ffn_check(act.read(np.float32, ff), gr, gs, ur, us, "norm+ffn")
+    y, s = ora.gemv("q8_0", rl, xn, 5000, h)
+    check_close(yl.read(np.float32, 5000), y, s, "norm+lm head")

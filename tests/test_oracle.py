@@ -284,3 +284,55 @@ def test_quantizer_round_trip_error_bounded(fmt):
 def test_synth_normal_moments():
     z = ora.synth_normal(7, 20000)
     assert abs(z.mean()) < 0.03 and abs(z.std() - 1.0) < 0.03
+
+
+# ───────────────────────── decode glue oracles ─────────────────────────
+
+def test_rms_norm_closed_forms():
+    # constant vector c: mean(x²) = c², so y = c/|c| · γ (eps → 0)
+    x = np.full(64, -3.0, np.float32)
+    g = np.linspace(0.5, 2.0, 64).astype(np.float32)
+    y = ora.rms_norm(x, g, 0.0)
+    assert np.allclose(y, -1.0 * g, rtol=0, atol=1e-12)
+    # scale invariance: rms_norm(a·x) = rms_norm(x) for a > 0 (eps = 0)
+    x = np.random.default_rng(0).standard_normal((3, 128)).astype(np.float32)
+    g = np.ones(128, np.float32)
+    assert np.allclose(ora.rms_norm(x, g, 0.0), ora.rms_norm(4 * x, g, 0.0), atol=1e-12)
+
+
+def test_rope_pos0_identity_and_pair_norms():
+    v = np.random.default_rng(1).standard_normal(4 * 64)
+    assert np.array_equal(ora.rope(v, 4, 64, 0, 1e6), v)
+    r = ora.rope(v, 4, 64, 511, 1e6).reshape(4, 64)
+    vv = v.reshape(4, 64)
+    # each (d, d+32) pair is rotated: its norm is preserved
+    assert np.allclose(r[:, :32] ** 2 + r[:, 32:] ** 2, vv[:, :32] ** 2 + vv[:, 32:] ** 2,
+                       rtol=1e-12)
+    # pair 0 has frequency 1: angle = pos exactly
+    c, s = np.cos(511.0), np.sin(511.0)
+    assert np.allclose(r[:, 0], vv[:, 0] * c - vv[:, 32] * s, rtol=1e-12)
+
+
+def test_attention_closed_forms_and_gqa_mapping():
+    rng = np.random.default_rng(2)
+    H, KVH, hd, L, S = 14, 2, 64, 37, 48
+    q = rng.standard_normal(H * hd)
+    k = rng.standard_normal((KVH, S, hd)).astype(np.float32)
+    v = rng.standard_normal((KVH, S, hd)).astype(np.float32)
+    out = ora.attention(q, k, v, H, KVH, hd, L, S).reshape(H, hd)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    for h in range(H):
+        kvh = h // (H // KVH)
+        s = (k[kvh, :L].astype(np.float64) @ q[h * hd:(h + 1) * hd]) * scale
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        assert np.allclose(out[h], p @ v[kvh, :L].astype(np.float64), rtol=1e-12, atol=1e-12)
+    # one position: the output is that value row
+    o1 = ora.attention(q, k, v, H, KVH, hd, 1, S).reshape(H, hd)
+    assert np.allclose(o1[0], v[0, 0]) and np.allclose(o1[H - 1], v[1, 0])
+    # equal keys: uniform weights → mean of the values
+    k2 = np.repeat(k[:, :1], S, axis=1)
+    o2 = ora.attention(q, k2, v, H, KVH, hd, L, S).reshape(H, hd)
+    assert np.allclose(o2[0], v[0, :L].astype(np.float64).mean(axis=0), atol=1e-12)
+    # kv_len = 0 → zeros (the reference's l = 0 case)
+    assert np.all(ora.attention(q, k, v, H, KVH, hd, 0, S) == 0)
