@@ -109,7 +109,6 @@ struct AmState {
     int32_t idx;      // index of the best element after nan_idx, -1 if none
     float v;
 };
-constexpr uint32_t AM_WGS = 256;
 constexpr uint32_t AM_T = 256;
 
 RT_DEV bool am_better(float v, int32_t i, float bv, int32_t bi) {
@@ -124,33 +123,62 @@ RT_DEV float am_load<float>(const float* p, uint32_t i) { return p[i]; }
 template <>
 RT_DEV float am_load<uint16_t>(const uint16_t* p, uint32_t i) { return h2f(p[i]); }
 
+RT_DEV AmState am_merge(AmState L, AmState R) {
+    // R's range follows L's: a NaN in R makes everything before it irrelevant
+    if (R.nan_idx >= 0) return R;
+    if (R.idx >= 0 && am_better(R.v, R.idx, L.v, L.idx)) return AmState{L.nan_idx, R.idx, R.v};
+    return L;
+}
+
+constexpr int AM_PER = 4;  // elements per thread per workgroup range
+
 template <typename T>
 RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result, uint32_t n,
                         AmState* __restrict__ states, uint32_t* __restrict__ counter) {
     __shared__ int32_t sn[AM_T / 64];
-    __shared__ AmState sb[AM_T / 64];
+    __shared__ AmState sb[AM_T];
     __shared__ bool last;
     const uint32_t per = (n + gridDim.x - 1) / gridDim.x;
     const uint32_t b0 = blockIdx.x * per, b1 = min(n, b0 + per);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // pass 1: last NaN of the range
+    // Ranges up to AM_PER·AM_T elements take one pass with all loads issued
+    // up front; longer ranges loop over such chunks.
+    constexpr uint32_t CH = AM_PER * AM_T;
     int32_t nl = -1;
-    for (uint32_t i = b0 + tid; i < b1; i += AM_T) {
-        const float x = am_load<T>(in, i);
-        if (x != x) nl = (int32_t)i;
+    for (uint32_t c0 = b0; c0 < b1; c0 += CH) {
+        float xv[AM_PER];
+#pragma unroll
+        for (int u = 0; u < AM_PER; ++u) {
+            const uint32_t i = c0 + tid + u * AM_T;
+            xv[u] = i < b1 ? am_load<T>(in, i) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < AM_PER; ++u) {
+            const uint32_t i = c0 + tid + u * AM_T;
+            if (i < b1 && xv[u] != xv[u]) nl = (int32_t)i;
+        }
     }
     for (int o = 32; o > 0; o >>= 1) nl = max(nl, __shfl_xor(nl, o, 64));
     if (lane == 0) sn[wave] = nl;
     __syncthreads();
     int32_t P = -1;
     for (uint32_t w = 0; w < AM_T / 64; ++w) P = max(P, sn[w]);
-    // pass 2: best after P
+    // best element after P (later index wins ties); the second read of the
+    // range hits the cache
     float bv = 0.0f;
     int32_t bi = -1;
-    const uint32_t s0 = (P >= 0) ? (uint32_t)P + 1 : b0;
-    for (uint32_t i = s0 + tid; i < b1; i += AM_T) {
-        const float x = am_load<T>(in, i);
-        if (am_better(x, (int32_t)i, bv, bi)) { bv = x; bi = (int32_t)i; }
+    for (uint32_t c0 = b0; c0 < b1; c0 += CH) {
+        float xv[AM_PER];
+#pragma unroll
+        for (int u = 0; u < AM_PER; ++u) {
+            const uint32_t i = c0 + tid + u * AM_T;
+            xv[u] = i < b1 ? am_load<T>(in, i) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < AM_PER; ++u) {
+            const int32_t i = (int32_t)(c0 + tid + u * AM_T);
+            if ((uint32_t)i < b1 && i > P && am_better(xv[u], i, bv, bi)) { bv = xv[u]; bi = i; }
+        }
     }
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, 64);
@@ -171,31 +199,31 @@ RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result,
         last = atomicAdd(counter, 1u) == gridDim.x - 1;
     }
     __syncthreads();
-    if (!last || tid != 0) return;
+    if (!last) return;
     __threadfence();
-    // merge the ranges in index order
-    AmState acc{-1, -1, 0.0f};
-    bool have = false;
-    for (uint32_t g = 0; g < gridDim.x; ++g) {
-        const volatile AmState* vs = &states[g];
-        const AmState r{vs->nan_idx, vs->idx, vs->v};
-        if (!have) { acc = r; have = true; continue; }
-        if (r.nan_idx >= 0) {
-            acc = r;
-        } else if (r.idx >= 0 && am_better(r.v, r.idx, acc.v, acc.idx)) {
-            acc.v = r.v;
-            acc.idx = r.idx;
+    // ordered tree merge of the workgroup states (merge is associative)
+    const uint32_t G = gridDim.x;
+    if (tid < G) {
+        const volatile AmState* vs = &states[tid];
+        sb[tid] = AmState{vs->nan_idx, vs->idx, vs->v};
+    }
+    __syncthreads();
+    for (uint32_t st = 1; st < G; st <<= 1) {
+        if ((tid % (2 * st)) == 0 && tid + st < G) sb[tid] = am_merge(sb[tid], sb[tid + st]);
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const AmState acc = sb[0];
+        uint32_t res = 0;
+        if (n > 0) {
+            if (acc.nan_idx == (int32_t)n - 1 || acc.idx < 0)
+                res = acc.nan_idx >= 0 ? (uint32_t)acc.nan_idx : 0u;
+            else
+                res = (uint32_t)acc.idx;
         }
+        result[0] = res;
+        *counter = 0;  // ready for the next call (also under graph replay)
     }
-    uint32_t res = 0;
-    if (n > 0) {
-        if (acc.nan_idx == (int32_t)n - 1 || acc.idx < 0)
-            res = acc.nan_idx >= 0 ? (uint32_t)acc.nan_idx : 0u;
-        else
-            res = (uint32_t)acc.idx;
-    }
-    result[0] = res;
-    *counter = 0;  // ready for the next call (also under graph replay)
 }
 
 extern "C" __global__ void __launch_bounds__(256)

@@ -119,8 +119,20 @@ RT_DEV void attend(const AttnIO& io, float* o, uint32_t kv_len, float scale, flo
     float m_run = -__builtin_huge_valf(), l_run = 0.0f;
     const uint32_t col = tid % C4, g = tid / C4;
     f32x4 o_run = {0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int PF = 16;  // value rows per thread fetched before the softmax
+    auto vrow = [&](uint32_t p) -> const float* {
+        return (io.v_last && p == kv_len - 1) ? io.v_last : io.vc + (size_t)p * HD;
+    };
     for (uint32_t c0 = 0; c0 < kv_len; c0 += ATT_CHUNK) {
         const uint32_t cn = min(ATT_CHUNK, kv_len - c0);
+        // value loads of this thread's first PF positions of the chunk go out
+        // with the key loads (one memory round trip for both)
+        f32x4 vpre[PF];
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const uint32_t j = g + u * G;
+            vpre[u] = ((const f32x4*)vrow(c0 + (j < cn ? j : 0)))[col];
+        }
         float mloc = -__builtin_huge_valf();
         for (uint32_t j = tid; j < cn; j += ATT_T) {
             const uint32_t p = c0 + j;
@@ -147,20 +159,23 @@ RT_DEV void attend(const AttnIO& io, float* o, uint32_t kv_len, float scale, flo
         const float resc = (m_run == -__builtin_huge_valf()) ? 0.0f : expf(m_run - m_new);
         l_run = l_run * resc + lsum;
         o_run = o_run * resc;
-        for (uint32_t j0 = g; j0 < cn; j0 += 8 * G) {
-            f32x4 vv[8];
-            float w[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < PF; ++u) {
+            const uint32_t j = g + u * G;
+            if (j < cn) o_run += sc[j] * vpre[u];
+        }
+        for (uint32_t j0 = g + PF * G; j0 < cn; j0 += PF * G) {
+            f32x4 vv[PF];
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
                 const uint32_t j = j0 + u * G;
-                const uint32_t jc = j < cn ? j : j0;
-                const uint32_t p = c0 + jc;
-                const float* vr = (io.v_last && p == kv_len - 1) ? io.v_last : io.vc + (size_t)p * HD;
-                vv[u] = ((const f32x4*)vr)[col];
-                w[u] = j < cn ? sc[jc] : 0.0f;
+                vv[u] = ((const f32x4*)vrow(c0 + (j < cn ? j : j0)))[col];
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) o_run += w[u] * vv[u];
+            for (int u = 0; u < PF; ++u) {
+                const uint32_t j = j0 + u * G;
+                if (j < cn) o_run += sc[j] * vv[u];
+            }
         }
         m_run = m_new;
         __syncthreads();  // sc[] reused by the next chunk

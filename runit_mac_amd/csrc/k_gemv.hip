@@ -76,6 +76,38 @@ RT_DEV float silu_ref(float g) {
     return g / (1.0f + expf(-g));
 }
 
+// Epilogue operand (residual or bias) of virtual row vr, loaded early so the
+// epilogue does not wait on a dependent load.
+template <int EPI>
+RT_DEV float load_aux(const GemvArgs& a, uint32_t vr) {
+    uint32_t mat, r;
+    vrow_map<EPI>(a, vr, mat, r);
+    if (EPI == EPI_F32_ADD) return ((const float*)a.aux[0])[r];
+    if (EPI == EPI_F16_ADD) return h2f(((const uint16_t*)a.aux[0])[r]);
+    if (EPI == EPI_QKV_BIAS) return h2f(((const uint16_t*)mat_aux(a, mat))[r]);
+    return 0.0f;
+}
+template <int EPI>
+constexpr bool has_aux() {
+    return EPI == EPI_F32_ADD || EPI == EPI_F16_ADD || EPI == EPI_QKV_BIAS;
+}
+// Stores v (+ the preloaded epilogue operand) for virtual row vr.  With an
+// output aliasing the residual, the value was read by this same lane first.
+template <int EPI>
+RT_DEV void store_row_pre(const GemvArgs& a, uint32_t vr, float v, float aux) {
+    uint32_t mat, r;
+    vrow_map<EPI>(a, vr, mat, r);
+    if (EPI == EPI_F32_ADD) {
+        ((float*)a.out[0])[r] = v + aux;
+    } else if (EPI == EPI_F16_ADD) {
+        ((uint16_t*)a.out[0])[r] = f2h(v + aux);
+    } else if (EPI == EPI_QKV_BIAS) {
+        ((float*)mat_out(a, mat))[r] = v + aux;
+    } else {
+        store_row<EPI>(a, vr, v);
+    }
+}
+
 template <int EPI>
 RT_DEV void store_row(const GemvArgs& a, uint32_t vr, float v) {
     uint32_t mat, r;
@@ -348,9 +380,9 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     __syncthreads();
     if (nitems == 0) return;
 
-    float acc[RQ];
+    float acc[RQ], aux[RQ];
 #pragma unroll
-    for (int rq = 0; rq < RQ; ++rq) acc[rq] = 0.0f;
+    for (int rq = 0; rq < RQ; ++rq) acc[rq] = aux[rq] = 0.0f;
 
     for (uint32_t it = 0; it < nitems; it += 2) {
 #pragma unroll
@@ -358,6 +390,14 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
             const uint32_t item = it + half;
             if (item < nitems) {  // uniform across the workgroup
                 if (item + 1 < nitems) issue(item + 1, buf[half ^ 1]);
+                if (has_aux<EPI>() && item % spw == 0 && slot == 0 && wk == 0) {
+                    const uint32_t tile = blockIdx.x + (item / spw) * gridDim.x;
+#pragma unroll
+                    for (int rq = 0; rq < RQ; ++rq) {
+                        const uint32_t vr = tile * vrows_per_wg + wgrp * 4 * RQ + 4 * rq + q;
+                        aux[rq] = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
+                    }
+                }
                 const uint32_t step = wk + ksw * (item % spw);
                 const uint32_t u = slot + 16 * step;
                 const bool valid = u < units;
@@ -411,7 +451,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                                 if (slot == 0 && (q & 1) == 0 && vr + 1 < a.nvrows)
                                     ((float*)a.out[0])[vr >> 1] = silu_ref(v) * up;
                             } else {
-                                if (slot == 0 && vr < a.nvrows) store_row<EPI>(a, vr, v);
+                                if (slot == 0 && vr < a.nvrows) store_row_pre<EPI>(a, vr, v, aux[rq]);
                             }
                         }
                     }

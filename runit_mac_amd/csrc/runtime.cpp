@@ -794,7 +794,9 @@ static int argmax_launch(rt_ctx* c, const char* kname, const void* in, uint32_t*
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", kname);
     void* states = c->aux;
     void* counter = (char*)c->aux + kAuxCounterOff;
-    const uint32_t grid = std::max<uint32_t>(1, std::min<uint32_t>(kArgmaxWgs, (n + 4095) / 4096));
+    // 1024 elements per workgroup up to 256 workgroups; longer inputs give
+    // each workgroup a longer range
+    const uint32_t grid = std::max<uint32_t>(1, std::min<uint32_t>(kArgmaxWgs, (n + 1023) / 1024));
     void* params[] = {&in, &res, &n, &states, &counter};
     return launch(c, kname, dim3(grid), dim3(256), 0, params);
 }
