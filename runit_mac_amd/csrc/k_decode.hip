@@ -82,191 +82,266 @@ k_kv_copy_f32(const float* src, float* dst, uint32_t pos, uint32_t max_seq, uint
 }
 
 // ───────────────────────────── attention ─────────────────────────────
-// One workgroup (256 threads) per (query head, batch row); decode attention
-// is latency-bound (a few hundred KB per layer), so each phase issues all of
-// its loads at once:
-//   scores : thread t takes positions t, t+256, ...; a key row is HD/4
-//            float4 loads, issued together;
-//   softmax: block max / block sum (chunks of ATT_CHUNK positions merged with
-//            the usual running max / sum / output rescaling, any kv_len);
-//   output : thread t owns float4 column (t % (HD/4)) for positions
-//            ≡ t / (HD/4) (mod 256/(HD/4)), loads unrolled by 8; the partial
-//            outputs are summed in LDS in a fixed order.
-// Same math as the online softmax of attention.metal:248-308 up to f32
-// rounding order.
-constexpr uint32_t ATT_CHUNK = 4096;
-constexpr uint32_t ATT_T = 256;
+//
+// Split-KV decode attention.  Decode attention reads a few hundred KB per
+// layer, so it is bound by memory latency, not bandwidth: the design keeps the
+// number of dependent memory round trips per workgroup at one per 64
+// positions and spreads the positions over many workgroups.
+//
+// Grid (nsplit, num_kv_heads · head_blocks, batch), 256 threads.  Workgroup
+// (s, kvh·HB + hb, b) takes positions [s·chunk, min(kv_len, (s+1)·chunk)) of
+// kv head kvh for the (up to ATT_GM) query heads of head block hb of that kv
+// head's group, so each K/V row is fetched once for all of them.  Per 64
+// positions:
+//   loads  : thread t holds a quarter of key row t/4 and HD/16 float4 of the
+//            value rows ≡ t/(HD/4) (mod 1024/HD), column t % (HD/4) — all
+//            issued together;
+//   scores : quarter dots reduced over 4 lanes, written to LDS;
+//   softmax: one wave per query head (64 lanes = 64 positions), running
+//            max / sum with rescaling (the online softmax of
+//            attention.metal:248-308);
+//   output : each thread accumulates its value rows weighted by the
+//            probabilities.
+// With nsplit > 1 each workgroup writes (m, l, o) for its heads; the last
+// workgroup of a (b, kvh, hb) group to arrive (arrival counter, reset by that
+// workgroup) merges the splits in split order.
+constexpr uint32_t ATT_GM = 8;    // query heads per workgroup
+constexpr uint32_t ATT_SUB = 64;  // positions per inner step
 
-struct AttnIO {
-    const float* q;       // this head's query (already rotated), hd floats
-    const float* kc;      // cache base of the kv head: [pos][hd]
-    const float* vc;
-    const float* k_last;  // if non-null: the key/value of position kv_len-1
-    const float* v_last;  //   come from these (not yet visible in the cache)
+struct AttnArgs {
+    const float* q;       // [batch][H][HD]; with rope: the raw query of the token
+    float* kc;            // cache [batch][KVH][stride][HD]
+    float* vc;
+    float* out;           // [batch][H][HD]
+    const float* k_new;   // rope: raw key / value of the token, [KVH][HD]
+    const float* v_new;
+    float* part;          // nsplit > 1: [batch][H][nsplit][HD] unnormalised outputs
+    float* ml;            //             [batch][H][nsplit][2] running max, sum
+    uint32_t* counters;   //             [batch][KVH][HB] arrival counters
+    uint32_t kv_len, stride, H, KVH, chunk, pos;
+    float scale, theta;
 };
 
-template <int HD>
-RT_DEV void attend(const AttnIO& io, float* o, uint32_t kv_len, float scale, float* qs, float* sc,
-                   float* red, f32x4* part) {
-    constexpr int C4 = HD / 4;            // float4 columns of a row
-    constexpr int G = ATT_T / C4;         // position groups in the output pass
-    const uint32_t tid = threadIdx.x;
-    for (uint32_t i = tid; i < HD; i += ATT_T) qs[i] = io.q[i];
+template <int HD, bool ROPE>
+RT_DEV void attn_split(const AttnArgs& a) {
+    constexpr uint32_t GM = ATT_GM, SUB = ATT_SUB;
+    constexpr uint32_t NQ = HD / 16;   // float4 per thread: K quarter row, V rows
+    constexpr uint32_t C4 = HD / 4;    // float4 columns of a row
+    constexpr uint32_t PG = 256 / C4;  // value position groups
+    static_assert(SUB == 64 && NQ * PG == SUB, "layout");
+    __shared__ f32x4 qs4[GM][C4];
+    __shared__ f32x4 ks4[C4], vs4[C4];
+    __shared__ float sc[GM][SUB];
+    __shared__ float m_run[GM], l_run[GM], resc[GM];
+    __shared__ f32x4 ored[4][GM][C4];
+    __shared__ uint32_t last_flag;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t s = blockIdx.x, nsp = gridDim.x, b = blockIdx.z;
+    const uint32_t G = a.H / a.KVH, HB = (G + GM - 1) / GM;
+    const uint32_t kvh = blockIdx.y / HB, hb = blockIdx.y % HB;
+    const uint32_t gh = min(GM, G - hb * GM);
+    const uint32_t h0 = kvh * G + hb * GM;  // first query head of the block
+    const size_t kvb = ((size_t)b * a.KVH + kvh) * a.stride * HD;
+    float* kc = a.kc + kvb;
+    float* vc = a.vc + kvb;
+    const uint32_t p_begin = s * a.chunk, p_end = min(a.kv_len, p_begin + a.chunk);
+    float* qsf = (float*)qs4;
+    if constexpr (ROPE) {
+        // fused_rope_qk_f32 (fused_rope.metal:28-55) on the block's query
+        // heads and on the kv head's key
+        constexpr uint32_t half = HD / 2;
+        for (uint32_t i = tid; i < (gh + 1) * half; i += 256) {
+            const uint32_t hh = i / half, d = i % half;
+            float c, sn;
+            rope_cs(d, HD, a.pos, a.theta, c, sn);
+            const float* src = hh < gh ? a.q + (size_t)(h0 + hh) * HD : a.k_new + (size_t)kvh * HD;
+            float* dst = hh < gh ? qsf + hh * HD : (float*)ks4;
+            const float r = src[d], im = src[d + half];
+            dst[d] = r * c - im * sn;
+            dst[d + half] = r * sn + im * c;
+        }
+        for (uint32_t d = tid; d < HD; d += 256) ((float*)vs4)[d] = a.v_new[(size_t)kvh * HD + d];
+    } else {
+        const float* q = a.q + ((size_t)b * a.H + h0) * HD;
+        for (uint32_t i = tid; i < gh * HD; i += 256) qsf[i] = q[i];
+    }
+    if (tid < GM) {
+        m_run[tid] = -__builtin_huge_valf();
+        l_run[tid] = 0.0f;
+    }
     __syncthreads();
-    f32x4 qv[C4];
+    if constexpr (ROPE) {
+        // kv_copy_to_cache_f32 (activation.metal:30-45) of the rotated key and
+        // the value, by the one workgroup whose range holds `pos`
+        if (hb == 0 && a.pos >= p_begin && a.pos < p_end)
+            for (uint32_t d = tid; d < HD; d += 256) {
+                kc[(size_t)a.pos * HD + d] = ((const float*)ks4)[d];
+                vc[(size_t)a.pos * HD + d] = ((const float*)vs4)[d];
+            }
+    }
+    f32x4 oacc[GM];
 #pragma unroll
-    for (int c = 0; c < C4; ++c) qv[c] = ((const f32x4*)qs)[c];
-    float m_run = -__builtin_huge_valf(), l_run = 0.0f;
-    const uint32_t col = tid % C4, g = tid / C4;
-    f32x4 o_run = {0.0f, 0.0f, 0.0f, 0.0f};
-    constexpr int PF = 16;  // value rows per thread fetched before the softmax
-    auto vrow = [&](uint32_t p) -> const float* {
-        return (io.v_last && p == kv_len - 1) ? io.v_last : io.vc + (size_t)p * HD;
-    };
-    for (uint32_t c0 = 0; c0 < kv_len; c0 += ATT_CHUNK) {
-        const uint32_t cn = min(ATT_CHUNK, kv_len - c0);
-        // value loads of this thread's first PF positions of the chunk go out
-        // with the key loads (one memory round trip for both)
-        f32x4 vpre[PF];
+    for (uint32_t h = 0; h < GM; ++h) oacc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t kp = tid >> 2, kq = tid & 3;      // key layout
+    const uint32_t vcol = tid % C4, vg = tid / C4;  // value layout
+    for (uint32_t p0 = p_begin; p0 < p_end; p0 += SUB) {
+        f32x4 kr[NQ], vr[NQ];
+        const uint32_t pk = p0 + kp;
+        const bool kvalid = pk < p_end;
+        const f32x4* krow = (const f32x4*)(kc + (size_t)(kvalid ? pk : p_begin) * HD) + kq * NQ;
 #pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            const uint32_t j = g + u * G;
-            vpre[u] = ((const f32x4*)vrow(c0 + (j < cn ? j : 0)))[col];
+        for (uint32_t i = 0; i < NQ; ++i) kr[i] = krow[i];
+#pragma unroll
+        for (uint32_t i = 0; i < NQ; ++i) {
+            const uint32_t pv = p0 + vg + i * PG;
+            vr[i] = ((const f32x4*)(vc + (size_t)(pv < p_end ? pv : p_begin) * HD))[vcol];
         }
-        float mloc = -__builtin_huge_valf();
-        for (uint32_t j = tid; j < cn; j += ATT_T) {
-            const uint32_t p = c0 + j;
-            const float* kr = (io.k_last && p == kv_len - 1) ? io.k_last : io.kc + (size_t)p * HD;
-            f32x4 kv[C4];
+        if constexpr (ROPE) {
+            // position `pos` comes from LDS (the cache write above may not be
+            // visible to this workgroup's loads, and other workgroups never
+            // read it)
+            if (pk == a.pos)
 #pragma unroll
-            for (int c = 0; c < C4; ++c) kv[c] = ((const f32x4*)kr)[c];
-            float dot = 0.0f;
+                for (uint32_t i = 0; i < NQ; ++i) kr[i] = ks4[kq * NQ + i];
 #pragma unroll
-            for (int c = 0; c < C4; ++c)
-                dot += qv[c].x * kv[c].x + qv[c].y * kv[c].y + qv[c].z * kv[c].z + qv[c].w * kv[c].w;
-            const float s = dot * scale;
-            sc[j] = s;
-            mloc = fmaxf(mloc, s);
+            for (uint32_t i = 0; i < NQ; ++i)
+                if (p0 + vg + i * PG == a.pos) vr[i] = vs4[vcol];
         }
-        const float m_new = fmaxf(m_run, block_max(mloc, red));
-        float lloc = 0.0f;
-        for (uint32_t j = tid; j < cn; j += ATT_T) {
-            const float pexp = expf(sc[j] - m_new);
-            sc[j] = pexp;
-            lloc += pexp;
-        }
-        const float lsum = block_sum(lloc, red);  // also orders sc[] writes before reads
-        const float resc = (m_run == -__builtin_huge_valf()) ? 0.0f : expf(m_run - m_new);
-        l_run = l_run * resc + lsum;
-        o_run = o_run * resc;
 #pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            const uint32_t j = g + u * G;
-            if (j < cn) o_run += sc[j] * vpre[u];
-        }
-        for (uint32_t j0 = g + PF * G; j0 < cn; j0 += PF * G) {
-            f32x4 vv[PF];
+        for (uint32_t h = 0; h < GM; ++h) {
+            if (h < gh) {
+                float dot = 0.0f;
 #pragma unroll
-            for (int u = 0; u < PF; ++u) {
-                const uint32_t j = j0 + u * G;
-                vv[u] = ((const f32x4*)vrow(c0 + (j < cn ? j : j0)))[col];
+                for (uint32_t i = 0; i < NQ; ++i) {
+                    const f32x4 qv = qs4[h][kq * NQ + i];
+                    dot += qv.x * kr[i].x + qv.y * kr[i].y + qv.z * kr[i].z + qv.w * kr[i].w;
+                }
+                dot = group_sum(dot, 4);
+                if (kq == 0) sc[h][kp] = kvalid ? dot * a.scale : -__builtin_huge_valf();
+            }
+        }
+        __syncthreads();
+        {
+            // wave w: query heads w and w + 4, interleaved
+            float sv[2], e[2], mx[2], sum[2];
+#pragma unroll
+            for (uint32_t u = 0; u < 2; ++u) {
+                const uint32_t h = w + 4 * u;
+                sv[u] = h < gh ? sc[h][lane] : -__builtin_huge_valf();
+                mx[u] = group_max(sv[u], 64);
             }
 #pragma unroll
-            for (int u = 0; u < PF; ++u) {
-                const uint32_t j = j0 + u * G;
-                if (j < cn) o_run += sc[j] * vv[u];
+            for (uint32_t u = 0; u < 2; ++u) {
+                const uint32_t h = w + 4 * u;
+                const float m_old = h < gh ? m_run[h] : 0.0f, m_new = fmaxf(m_old, mx[u]);
+                e[u] = (sv[u] == -__builtin_huge_valf()) ? 0.0f : expf(sv[u] - m_new);
+                sum[u] = group_sum(e[u], 64);
+                if (h < gh) {
+                    sc[h][lane] = e[u];
+                    if (lane == 0) {
+                        const float r =
+                            (m_old == -__builtin_huge_valf()) ? 0.0f : expf(m_old - m_new);
+                        resc[h] = r;
+                        l_run[h] = l_run[h] * r + sum[u];
+                        m_run[h] = m_new;
+                    }
+                }
             }
         }
-        m_run = m_new;
-        __syncthreads();  // sc[] reused by the next chunk
+        __syncthreads();
+#pragma unroll
+        for (uint32_t h = 0; h < GM; ++h) {
+            if (h < gh) {
+                f32x4 acc = oacc[h] * resc[h];
+#pragma unroll
+                for (uint32_t i = 0; i < NQ; ++i) acc += sc[h][vg + i * PG] * vr[i];
+                oacc[h] = acc;
+            }
+        }
+        __syncthreads();  // sc / resc reused by the next step
     }
-    part[g * C4 + col] = o_run;
+    // sum the value position groups: within the wave, then over the 4 waves
+#pragma unroll
+    for (uint32_t h = 0; h < GM; ++h) {
+        if (h < gh) {
+            f32x4 v = oacc[h];
+            if constexpr (C4 == 16) {
+                v.x += swz_xor_f<16>(v.x);
+                v.y += swz_xor_f<16>(v.y);
+                v.z += swz_xor_f<16>(v.z);
+                v.w += swz_xor_f<16>(v.w);
+            }
+            if constexpr (C4 <= 32) {
+                v.x += __shfl_xor(v.x, 32, 64);
+                v.y += __shfl_xor(v.y, 32, 64);
+                v.z += __shfl_xor(v.z, 32, 64);
+                v.w += __shfl_xor(v.w, 32, 64);
+            }
+            if (lane < C4) ored[w][h][lane] = v;
+        }
+    }
     __syncthreads();
-    const float inv_l = (l_run > 0.0f) ? (1.0f / l_run) : 0.0f;
-    if (tid < C4) {
-        f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int gg = 0; gg < G; ++gg) t += part[gg * C4 + tid];
-        ((f32x4*)o)[tid] = t * inv_l;
+    for (uint32_t i = tid; i < gh * C4; i += 256) {
+        const uint32_t h = i / C4, c = i % C4;
+        const f32x4 t = ored[0][h][c] + ored[1][h][c] + ored[2][h][c] + ored[3][h][c];
+        if (nsp == 1) {
+            const float l = l_run[h];
+            ((f32x4*)(a.out + ((size_t)b * a.H + h0 + h) * HD))[c] = t * (l > 0.0f ? 1.0f / l : 0.0f);
+        } else {
+            ((f32x4*)(a.part + (((size_t)b * a.H + h0 + h) * nsp + s) * HD))[c] = t;
+        }
     }
-}
-
-template <int HD>
-RT_DEV void attention_head(const float* Q, const float* K, const float* V, float* O,
-                           uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads, float scale,
-                           uint32_t kv_head_stride) {
-    __shared__ float qs[HD], sc[ATT_CHUNK], red[16];
-    __shared__ f32x4 part[ATT_T];
-    const uint32_t h = blockIdx.x, b = blockIdx.y;
-    const uint32_t kvh = h / (num_heads / num_kv_heads);
-    const size_t kv_base = ((size_t)b * num_kv_heads + kvh) * kv_head_stride * HD;
-    AttnIO io{Q + ((size_t)b * num_heads + h) * HD, K + kv_base, V + kv_base, nullptr, nullptr};
-    attend<HD>(io, O + ((size_t)b * num_heads + h) * HD, kv_len, scale, qs, sc, red, part);
+    if (nsp == 1) return;
+    if (tid < gh) {
+        float* mlp = a.ml + (((size_t)b * a.H + h0 + tid) * nsp + s) * 2;
+        mlp[0] = m_run[tid];
+        mlp[1] = l_run[tid];
+    }
+    __threadfence();
+    __syncthreads();
+    uint32_t* counter = a.counters + ((size_t)b * a.KVH + kvh) * HB + hb;
+    if (tid == 0) last_flag = atomicAdd(counter, 1u) == nsp - 1;
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();  // acquire: the other workgroups' partials are visible
+    // merge the splits in split order: o = Σ o_s·e^(m_s−M) / Σ l_s·e^(m_s−M)
+    for (uint32_t i = tid; i < gh * C4; i += 256) {
+        const uint32_t h = i / C4, c = i % C4;
+        const size_t row = ((size_t)b * a.H + h0 + h) * nsp;
+        const float* mlv = a.ml + row * 2;
+        float M = -__builtin_huge_valf();
+#pragma unroll 8
+        for (uint32_t j = 0; j < nsp; ++j) M = fmaxf(M, mlv[2 * j]);
+        float L = 0.0f;
+        f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+        for (uint32_t j = 0; j < nsp; ++j) {
+            const float f = expf(mlv[2 * j] - M);
+            L += mlv[2 * j + 1] * f;
+            o += ((const f32x4*)(a.part + (row + j) * HD))[c] * f;
+        }
+        ((f32x4*)(a.out + ((size_t)b * a.H + h0 + h) * HD))[c] = o * (L > 0.0f ? 1.0f / L : 0.0f);
+    }
+    if (tid == 0) *counter = 0;  // ready for the next call (also under graph replay)
 }
 
 // decode_attention_f32 (attention.metal:248-308; dispatch.rs:1575-1612).
 // K/V cache: [batch][num_kv_heads][kv_head_stride][head_dim].  Instantiated
 // for head_dim 64, 128 and 256 (the host checks).
-#define RT_ATTN_KERNEL(HD)                                                                        \
-    extern "C" __global__ void __launch_bounds__(256) k_decode_attention_f32_hd##HD(               \
-        const float* Q, const float* K, const float* V, float* O, uint32_t kv_len,                 \
-        uint32_t num_heads, uint32_t num_kv_heads, float scale, uint32_t kv_head_stride) {         \
-        attention_head<HD>(Q, K, V, O, kv_len, num_heads, num_kv_heads, scale, kv_head_stride);    \
+//
+// k_attn_rope_f32_hd*: one new token at position `pos` (batch 1) — equivalent
+// to fused_rope_qk_f32 on (q, k), kv_copy_to_cache_f32 of k and v at `pos`,
+// then decode_attention_f32 with kv_len = pos + 1.
+#define RT_ATTN_KERNELS(HD)                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) k_decode_attention_f32_hd##HD(AttnArgs a) { \
+        attn_split<HD, false>(a);                                                                  \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(256) k_attn_rope_f32_hd##HD(AttnArgs a) {        \
+        attn_split<HD, true>(a);                                                                   \
     }
-RT_ATTN_KERNEL(64)
-RT_ATTN_KERNEL(128)
-RT_ATTN_KERNEL(256)
-
-// Fused decode attention for one new token at position `pos` (new, for the
-// graph-captured decode step).  Equivalent to fused_rope_qk_f32 on (q, k),
-// kv_copy_to_cache_f32 of k and v at `pos`, then decode_attention_f32 with
-// kv_len = pos + 1.  The first query head of each group writes the rotated key
-// and the value into the cache; every workgroup takes position `pos` from its
-// own LDS copy, so no workgroup waits for another's cache write.
-template <int HD>
-RT_DEV void attn_rope_head(const float* q_raw, const float* k_raw, const float* v_raw,
-                           float* k_cache, float* v_cache, float* O, uint32_t pos,
-                           uint32_t max_seq, uint32_t num_heads, uint32_t num_kv_heads,
-                           float theta, float scale) {
-    __shared__ float qs[HD], ks[HD], vs[HD], qr[HD], sc[ATT_CHUNK], red[16];
-    __shared__ f32x4 part[ATT_T];
-    const uint32_t h = blockIdx.x, group = num_heads / num_kv_heads, kvh = h / group;
-    constexpr uint32_t half = HD / 2;
-    const float* q = q_raw + (size_t)h * HD;
-    const float* k = k_raw + (size_t)kvh * HD;
-    const float* v = v_raw + (size_t)kvh * HD;
-    for (uint32_t d = threadIdx.x; d < half; d += blockDim.x) {
-        float c, s;
-        rope_cs(d, HD, pos, theta, c, s);
-        const float q0 = q[d], q1 = q[d + half], k0 = k[d], k1 = k[d + half];
-        qr[d] = q0 * c - q1 * s;
-        qr[d + half] = q0 * s + q1 * c;
-        ks[d] = k0 * c - k1 * s;
-        ks[d + half] = k0 * s + k1 * c;
-    }
-    for (uint32_t d = threadIdx.x; d < HD; d += blockDim.x) vs[d] = v[d];
-    __syncthreads();
-    float* kc = k_cache + (size_t)kvh * max_seq * HD;
-    float* vc = v_cache + (size_t)kvh * max_seq * HD;
-    if (h % group == 0) {
-        for (uint32_t d = threadIdx.x; d < HD; d += blockDim.x) {
-            kc[(size_t)pos * HD + d] = ks[d];
-            vc[(size_t)pos * HD + d] = vs[d];
-        }
-    }
-    AttnIO io{qr, kc, vc, ks, vs};
-    attend<HD>(io, O + (size_t)h * HD, pos + 1, scale, qs, sc, red, part);
-}
-#define RT_ATTN_ROPE_KERNEL(HD)                                                                   \
-    extern "C" __global__ void __launch_bounds__(256) k_attn_rope_f32_hd##HD(                      \
-        const float* q_raw, const float* k_raw, const float* v_raw, float* k_cache,                \
-        float* v_cache, float* O, uint32_t pos, uint32_t max_seq, uint32_t num_heads,              \
-        uint32_t num_kv_heads, float theta, float scale) {                                         \
-        attn_rope_head<HD>(q_raw, k_raw, v_raw, k_cache, v_cache, O, pos, max_seq, num_heads,      \
-                           num_kv_heads, theta, scale);                                            \
-    }
-RT_ATTN_ROPE_KERNEL(64)
-RT_ATTN_ROPE_KERNEL(128)
-RT_ATTN_ROPE_KERNEL(256)
+RT_ATTN_KERNELS(64)
+RT_ATTN_KERNELS(128)
+RT_ATTN_KERNELS(256)
 
 // Q8_0 embedding row (the reference copies a dequantised token_embd row into
 // the residual stream on the CPU, forward.rs:1494-1505).  The token id is

@@ -373,31 +373,62 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
         }
     };
 
-    if (nitems > 0) issue(0, buf[0]);
-#ifndef RT_PROBE_NO_STAGE
-    stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, a.K / 32, xs, a.gamma, a.eps);
-#endif
-    __syncthreads();
-    if (nitems == 0) return;
-
     float acc[RQ], aux[RQ];
 #pragma unroll
     for (int rq = 0; rq < RQ; ++rq) acc[rq] = aux[rq] = 0.0f;
+    // (every lane loads, unconditionally: a load on only some control paths
+    // would make the compiler's wait for the x loads a wait for all loads)
+    auto load_tile_aux = [&](uint32_t item) {
+        if (has_aux<EPI>()) {
+            const uint32_t tile = blockIdx.x + (item / spw) * gridDim.x;
+#pragma unroll
+            for (int rq = 0; rq < RQ; ++rq) {
+                const uint32_t vr = tile * vrows_per_wg + wgrp * 4 * RQ + 4 * rq + q;
+                aux[rq] = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
+            }
+        }
+    };
+
+    // Memory order of the prologue: x (and γ), the first tile's epilogue
+    // operand, the weights of the first two items; the conversion of x then
+    // waits only for x.
+#ifdef RT_PROBE_TIMING
+    uint64_t tp[6];
+    tp[0] = __builtin_amdgcn_s_memtime();
+    const uint64_t rt0 = __builtin_amdgcn_s_memrealtime();
+#define RT_TP(i) tp[i] = __builtin_amdgcn_s_memtime()
+#else
+#define RT_TP(i)
+#endif
+    const uint32_t nxb = a.K / 32;
+    const bool one_pass = !a.x_rec && stage_one_pass(nxb);
+    XPre xp;
+#ifndef RT_PROBE_NO_STAGE
+    if (one_pass) stage_x_load<XT>((const XT*)a.x, a.gamma, nxb, xp);
+#endif
+    load_tile_aux(0);
+    issue(0, buf[0]);  // items past nitems load clamped addresses
+    issue(1, buf[1]);
+    RT_TP(1);
+#ifndef RT_PROBE_NO_STAGE
+    // (the host launches whole-K kernels either with x records or with a K
+    // that one pass covers)
+    if (one_pass)
+        stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
+    else
+        copy_x_limbs((const XRec*)a.x, 0, nxb, xs);
+#endif
+    RT_TP(2);
+    __syncthreads();
+    RT_TP(3);
+    if (nitems == 0) return;
 
     for (uint32_t it = 0; it < nitems; it += 2) {
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             const uint32_t item = it + half;
             if (item < nitems) {  // uniform across the workgroup
-                if (item + 1 < nitems) issue(item + 1, buf[half ^ 1]);
-                if (has_aux<EPI>() && item % spw == 0 && slot == 0 && wk == 0) {
-                    const uint32_t tile = blockIdx.x + (item / spw) * gridDim.x;
-#pragma unroll
-                    for (int rq = 0; rq < RQ; ++rq) {
-                        const uint32_t vr = tile * vrows_per_wg + wgrp * 4 * RQ + 4 * rq + q;
-                        aux[rq] = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
-                    }
-                }
+                if (item > 0 && item % spw == 0) load_tile_aux(item);
                 const uint32_t step = wk + ksw * (item % spw);
                 const uint32_t u = slot + 16 * step;
                 const bool valid = u < units;
@@ -407,6 +438,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                     const float v = F::mdot(buf[half][rq], xs, uc, lq);
                     acc[rq] += valid ? v : 0.0f;
                 }
+                if (item + 2 < nitems) issue(item + 2, buf[half]);
                 if (item % spw == spw - 1) {
                     const uint32_t tile = blockIdx.x + (item / spw) * gridDim.x;
                     const uint32_t vbase = tile * vrows_per_wg + wgrp * 4 * RQ;
@@ -459,6 +491,18 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
             }
         }
     }
+#ifdef RT_PROBE_TIMING
+    RT_TP(4);
+    __syncthreads();
+    RT_TP(5);
+    if (threadIdx.x == 0) {
+        uint32_t* o = (uint32_t*)a.out[0] + 5120 + blockIdx.x * 8;  // past the outputs
+        o[0] = (uint32_t)rt0;
+        for (int i = 1; i < 6; ++i) o[i] = (uint32_t)(tp[i] - tp[0]);
+        o[6] = (uint32_t)(__builtin_amdgcn_s_memrealtime() - rt0);
+        o[7] = nitems;
+    }
+#endif
 }
 
 template <class F, int EPI, typename XT, int RPL, int UNR>

@@ -71,6 +71,15 @@ RT_DEV float group_sum(float v, int n) {
     if (n >= 64) v += __shfl_xor(v, 32, 64);
     return v;
 }
+RT_DEV float group_max(float v, int n) {  // as group_sum, with max
+    if (n >= 2) v = fmaxf(v, dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v));
+    if (n >= 4) v = fmaxf(v, dpp_f<DPP_QUAD_PERM(2, 3, 0, 1)>(v));
+    if (n >= 8) v = fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
+    if (n >= 16) v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    if (n >= 32) v = fmaxf(v, swz_xor_f<16>(v));
+    if (n >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
 RT_DEV float max8(float v) {  // max over aligned groups of 8 lanes
     v = fmaxf(v, dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v));
     v = fmaxf(v, dpp_f<DPP_QUAD_PERM(2, 3, 0, 1)>(v));
@@ -137,73 +146,76 @@ RT_DEV void load_x4<uint16_t>(const uint16_t* x, uint32_t idx, float v[4]) {
 }
 
 // Converts one 4-element slice (lane q of the 8 lanes of x-block b) into
-// limbs and writes them to the block's record.
+// limbs and writes them to the block's record.  The 8 lanes of a block are
+// 8 consecutive, 8-aligned lanes, all active.  Straight-line code: the
+// non-finite cases are selects, and every lane stores whole dwords (limb
+// dword q of each limb plane, and meta dword q % 4, which lanes q and q + 4
+// write with the same value).
 template <bool Q40PERM>
 RT_DEV void limb_slice(const float v[4], uint32_t q, XRec* __restrict__ rec) {
-    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    // NaN-propagating max over 8 lanes: a NaN turns into +Inf here.
-    if (a != a) a = __builtin_huge_valf();
-    a = max8(a);
-    int e;
-    const bool finite = a <= 3.40282347e38f;
-    if (!finite) {
-        e = XE_NONFINITE;
-    } else if (a == 0.0f) {
-        e = 0;
-    } else {
-        e = __builtin_amdgcn_frexp_expf(a);  // a < 2^e
-    }
-    int l0[4], l1[4], l2[4];
+    constexpr float FMAX = 3.40282347e38f;
+    bool nf[4];
+    bool any_nf = false;
+    float a = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        int xi;
-        if (finite) {
-            xi = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v[i], 22 - e));
-        } else {
-            // Inf/NaN blocks: ±2^22 on non-finite elements, 0 elsewhere;
-            // with e = 300 their products overflow to ±Inf (or NaN).
-            const bool nf = !(fabsf(v[i]) <= 3.40282347e38f);
-            xi = nf ? ((v[i] < 0.0f) ? -(1 << 22) : (1 << 22)) : 0;
-        }
+        const float av = fabsf(v[i]);
+        nf[i] = !(av <= FMAX);  // ±Inf or NaN
+        any_nf |= nf[i];
+        a = fmaxf(a, av);
+    }
+    // a non-finite element makes the whole block non-finite
+    a = max8(any_nf ? __builtin_huge_valf() : a);
+    const bool finite = a <= FMAX;
+    const int ef = __builtin_amdgcn_frexp_expf(a);  // a < 2^ef
+    const int e = !finite ? XE_NONFINITE : (a == 0.0f ? 0 : ef);
+    int l[3][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // finite block: round(x · 2^(22-e)), |xi| ≤ 2^22.  Non-finite block:
+        // ±2^22 on non-finite elements (NaN as +), 0 elsewhere; with e = 300
+        // their products overflow to ±Inf (or NaN).
+        const int xf = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v[i], 22 - ef));
+        const int xn = nf[i] ? ((v[i] < 0.0f) ? -(1 << 22) : (1 << 22)) : 0;
+        const int xi = finite ? xf : xn;
         // balanced base-256 digits: xi = 65536·l0 + 256·l1 + l2
         const int c = ((xi + 128) & 255) - 128;
         const int r1 = (xi - c) >> 8;
         const int bb = ((r1 + 128) & 255) - 128;
-        l0[i] = (r1 - bb) >> 8;
-        l1[i] = bb;
-        l2[i] = c;
+        l[0][i] = (r1 - bb) >> 8;
+        l[1][i] = bb;
+        l[2][i] = c;
     }
-    uint8_t* base = (uint8_t*)rec;
-    if (!Q40PERM) {
-        rec->limb[0][q] = (l0[0] & 255) | ((l0[1] & 255) << 8) | ((l0[2] & 255) << 16) |
-                          ((uint32_t)(l0[3] & 255) << 24);
-        rec->limb[1][q] = (l1[0] & 255) | ((l1[1] & 255) << 8) | ((l1[2] & 255) << 16) |
-                          ((uint32_t)(l1[3] & 255) << 24);
-        rec->limb[2][q] = (l2[0] & 255) | ((l2[1] & 255) << 8) | ((l2[2] & 255) << 16) |
-                          ((uint32_t)(l2[3] & 255) << 24);
-    } else {
+    uint32_t* recw = (uint32_t*)rec;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int pos = xpos<true>(q * 4 + i);
-            base[0 * 32 + pos] = (uint8_t)l0[i];
-            base[1 * 32 + pos] = (uint8_t)l1[i];
-            base[2 * 32 + pos] = (uint8_t)l2[i];
+    for (int k = 0; k < 3; ++k) {
+        const uint32_t own = (uint32_t)(l[k][0] & 255) | ((uint32_t)(l[k][1] & 255) << 8) |
+                             ((uint32_t)(l[k][2] & 255) << 16) | ((uint32_t)l[k][3] << 24);
+        uint32_t w = own;
+        if (Q40PERM) {
+            // 8-group as evens then odds: lane 2m stores elements
+            // {8m, 8m+2, 8m+4, 8m+6}, lane 2m+1 stores {8m+1, 8m+3, 8m+5, 8m+7}
+            const uint32_t par = (uint32_t)dpp_i<DPP_QUAD_PERM(1, 0, 3, 2)>((int)own);
+            w = __builtin_amdgcn_perm(par, own, (q & 1) ? 0x03010705u : 0x06040200u);
         }
+        recw[8 * k + q] = w;
     }
-    // Limb sums per 16-element half (lanes 0-3 → half 0, 4-7 → half 1).
-    int s0 = sum4_i(l0[0] + l0[1] + l0[2] + l0[3]);
-    int s1 = sum4_i(l1[0] + l1[1] + l1[2] + l1[3]);
-    int s2 = sum4_i(l2[0] + l2[1] + l2[2] + l2[3]);
-    if ((q & 3) == 0) {
-        const int h = q >> 2;
-        rec->s[h][0] = (int16_t)s0;
-        rec->s[h][1] = (int16_t)s1;
-        rec->s[h][2] = (int16_t)s2;
+    // limb sums per 16-element half (lanes 0-3 → half 0, 4-7 → half 1)
+    int hs[2][3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int sq = sum4_i(l[k][0] + l[k][1] + l[k][2] + l[k][3]);
+        const int sm = dpp_i<DPP_ROW_HALF_MIRROR>(sq);  // the other half's sum
+        hs[0][k] = q < 4 ? sq : sm;
+        hs[1][k] = q < 4 ? sm : sq;
     }
-    if (q == 0) {
-        rec->e = (int16_t)e;
-        rec->pad = 0;
-    }
+    // meta dwords: (e, s00) (s01, s02) (s10, s11) (s12, pad)
+    const uint32_t m0 = (uint32_t)(e & 0xFFFF) | ((uint32_t)hs[0][0] << 16);
+    const uint32_t m1 = (uint32_t)(hs[0][1] & 0xFFFF) | ((uint32_t)hs[0][2] << 16);
+    const uint32_t m2 = (uint32_t)(hs[1][0] & 0xFFFF) | ((uint32_t)hs[1][1] << 16);
+    const uint32_t m3 = (uint32_t)(hs[1][2] & 0xFFFF);
+    const uint32_t qm = q & 3;
+    recw[24 + qm] = qm == 0 ? m0 : (qm == 1 ? m1 : (qm == 2 ? m2 : m3));
 }
 
 // Builds records for x-blocks [xb0, xb0+nxb) into recs[0..nxb).  Eight lanes
@@ -281,6 +293,81 @@ RT_DEV void stage_x_norm(const float* __restrict__ x, const float* __restrict__ 
         for (int s = 0; s < XSTAGE_UNR; ++s) {
             const uint32_t t = t0 + s * step;
             if (t < total) limb_slice<Q40PERM>(v[s], t & 7, recs + (t >> 3));
+        }
+    }
+}
+
+// Two-phase staging for the whole-K launches whose vector fits in one pass
+// (nxb·8 ≤ XSTAGE_UNR·blockDim slices): stage_x_load issues the loads of x
+// (and γ), the caller issues its weight loads, and stage_x_convert then
+// converts while those are in flight.
+//
+// Slice handled by this thread in round s: t = threadIdx.x + s·blockDim.x.
+// Threads past the end take slice q of block 0: their 8-lane groups rebuild
+// record 0 exactly as its owners do (the same values into the same words),
+// so no lane needs a branch.
+RT_DEV uint32_t stage_slice(int s, uint32_t total) {
+    const uint32_t t = threadIdx.x + s * blockDim.x;
+    return t < total ? t : (t & 7);
+}
+struct XPre {
+    float v[XSTAGE_UNR][4];
+    float g[XSTAGE_UNR][4];
+};
+RT_DEV bool stage_one_pass(uint32_t nxb) { return nxb * 8 <= XSTAGE_UNR * blockDim.x; }
+
+template <typename XT>
+RT_DEV void stage_x_load(const XT* __restrict__ x, const float* __restrict__ gamma, uint32_t nxb,
+                         XPre& p) {
+    const uint32_t total = nxb * 8;
+#pragma unroll
+    for (int s = 0; s < XSTAGE_UNR; ++s) {
+        // rounds past the vector are skipped (workgroup-uniform: no lane of a
+        // later load is conditional); lanes past the end load clamped addresses
+        if (s * blockDim.x >= total) break;
+        const uint32_t t = stage_slice(s, total);
+        const uint32_t i = (t >> 3) * 32 + (t & 7) * 4;
+        load_x4<XT>(x, i, p.v[s]);
+        if (gamma) {
+            const f32x4 g = *(const f32x4*)(gamma + i);
+            p.g[s][0] = g.x; p.g[s][1] = g.y; p.g[s][2] = g.z; p.g[s][3] = g.w;
+        }
+    }
+}
+
+// With γ: x̂ = x · rsqrt(Σx²/K + eps) · γ (rms_norm_f32_f32_f32g,
+// norm.metal:126-154), each product rounded in f32 as in stage_x_norm.
+template <bool Q40PERM>
+RT_DEV void stage_x_convert(XPre& p, const float* gamma, float eps, uint32_t nxb,
+                            XRec* __restrict__ recs) {
+    const uint32_t total = nxb * 8;
+    if (gamma) {
+        __shared__ float nred[16];
+        float ss = 0.0f;
+#pragma unroll
+        for (int s = 0; s < XSTAGE_UNR; ++s) {
+            const float sq = p.v[s][0] * p.v[s][0] + p.v[s][1] * p.v[s][1] +
+                             p.v[s][2] * p.v[s][2] + p.v[s][3] * p.v[s][3];
+            ss += (threadIdx.x + s * blockDim.x < total) ? sq : 0.0f;
+        }
+        ss = group_sum(ss, 64);
+        if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (uint32_t w = 0; w < (blockDim.x >> 6); ++w) tot += nred[w];
+        const float rms = rsqrtf(tot / (float)(nxb * 32) + eps);
+#pragma unroll
+        for (int s = 0; s < XSTAGE_UNR; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p.v[s][i] = p.v[s][i] * rms * p.g[s][i];
+    }
+#pragma unroll
+    for (int s = 0; s < XSTAGE_UNR; ++s) {
+        // rounds past the vector are skipped (workgroup-uniform); inside a
+        // round, lanes past the end convert a copy of block 0 (see stage_slice)
+        if (s * blockDim.x < total) {
+            const uint32_t t = stage_slice(s, total);
+            limb_slice<Q40PERM>(p.v[s], t & 7, recs + (t >> 3));
         }
     }
 }

@@ -98,10 +98,19 @@ RT_DEV float q8_0_block_dot(uint32_t d, const uint32_t q[8], const XRegs& x) {
 struct FmtQ8_0 {
     static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 34, UNIT_EL = 64;
     static constexpr bool Q40PERM = false;
-    struct Raw { uint32_t w[17]; };
+    // held as whole dwordx4 tuples: element-wise copies out of a load's
+    // destination would make the compiler wait for the load right away
+    struct Raw {
+        u32x4 v[4];
+        uint32_t t;
+        RT_DEV uint32_t operator[](int i) const { return i < 16 ? v[i >> 2][i & 3] : t; }
+    };
     struct XU { XRegs x[2]; };
     RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
-        load_dwords<17>(row + (size_t)u * 68, r.w);
+        const uint8_t* p = row + (size_t)u * 68;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.v[i] = *(const u32x4_a4*)(p + 16 * i);
+        r.t = *(const uint32_t*)(p + 64);
     }
     RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) {
         load_xregs(recs + 2 * uu, xu.x[0]);
@@ -111,10 +120,10 @@ struct FmtQ8_0 {
         uint32_t qa[8], qb[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            qa[i] = alignb(r.w[i + 1], r.w[i], 2);  // bytes 2..33
-            qb[i] = r.w[9 + i];                     // bytes 36..67
+            qa[i] = alignb(r[i + 1], r[i], 2);  // bytes 2..33
+            qb[i] = r[9 + i];                     // bytes 36..67
         }
-        return q8_0_block_dot(r.w[0], qa, xu.x[0]) + q8_0_block_dot(r.w[8] >> 16, qb, xu.x[1]);
+        return q8_0_block_dot(r[0], qa, xu.x[0]) + q8_0_block_dot(r[8] >> 16, qb, xu.x[1]);
     }
     // matrix-core form: recs = the unit's two records, lq = this lane's limb
     RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
@@ -124,11 +133,11 @@ struct FmtQ8_0 {
         v4i ca = {0, 0, 0, 0}, cb = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            ca = mfma4(xa.l[i], alignb(r.w[i + 1], r.w[i], 2), ca);  // bytes 2..33
-            cb = mfma4(xb.l[i], r.w[9 + i], cb);                     // bytes 36..67
+            ca = mfma4(xa.l[i], alignb(r[i + 1], r[i], 2), ca);  // bytes 2..33
+            cb = mfma4(xb.l[i], r[9 + i], cb);                     // bytes 36..67
         }
-        return __builtin_amdgcn_ldexpf(h2f(r.w[0]) * comb4(ca), xa.e - 22) +
-               __builtin_amdgcn_ldexpf(h2f(r.w[8] >> 16) * comb4(cb), xb.e - 22);
+        return __builtin_amdgcn_ldexpf(h2f(r[0]) * comb4(ca), xa.e - 22) +
+               __builtin_amdgcn_ldexpf(h2f(r[8] >> 16) * comb4(cb), xb.e - 22);
     }
 };
 

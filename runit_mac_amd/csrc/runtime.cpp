@@ -42,8 +42,11 @@ struct GemvArgs {
 constexpr uint32_t XREC_BYTES = 112;  // one activation record per 32 elements
 // argmax: 256 workgroup states of 12 bytes, then the arrival counter
 constexpr uint32_t kArgmaxWgs = 256;
+constexpr uint32_t kOnePassMaxK = 8192;  // 512 threads × 4 slices × 4 elements
 constexpr size_t kAuxCounterOff = 4096;
-constexpr size_t kAuxBytes = 8192;
+constexpr size_t kAuxAttnOff = 8192;  // attention arrival counters
+constexpr size_t kAuxBytes = 65536;
+constexpr uint32_t kAttnCounters = (kAuxBytes - kAuxAttnOff) / 4;
 
 const char* const kKernelNames[] = {
     "k_gemv_q8_0_f32_f32_r1", "k_gemv_q8_0_f32_f32_r2",
@@ -255,7 +258,11 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
                     x_f16 ? 8 : 16);
     a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
     const uint32_t nxb = a.K / 32;
-    if (!a.x_rec && !a.gamma && a.K >= c->prepass_k) {
+    // Whole-K matrix-core launches stage x in one pass of ≤ 4 slices of 4
+    // elements per thread (K ≤ 8192 at 512 threads); longer activations are
+    // converted once by the pre-pass.
+    const bool mq_shape = !single;
+    if (!a.x_rec && !a.gamma && (a.K >= c->prepass_k || (mq_shape && a.K > kOnePassMaxK))) {
         // convert the activations once into the context workspace
         const size_t need = (size_t)nxb * XREC_BYTES;
         const int st0 = ensure_ws(c, need, kname);
@@ -287,6 +294,7 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         // row; persistent grid of `gpc` workgroups per CU.
         p = Plan{256, 16, 1};
         if (c->plan_override.T) p = Plan{c->plan_override.T, 16, c->plan_override.rpl};
+        if (!a.x_rec && nxb * 8 > 4 * p.T) p.T = 512;  // one staging pass
         // split K over the waves of a workgroup while row-quad groups are
         // scarcer than the resident waves (latency-bound small problems)
         const uint32_t nwaves = p.T / 64;
@@ -933,6 +941,48 @@ static int attn_check(rt_ctx* c, uint32_t num_heads, uint32_t num_kv_heads, uint
     return RT_OK;
 }
 
+// Mirrors the device-side AttnArgs (k_decode.hip).
+struct AttnArgs {
+    const float* q;
+    float* kc;
+    float* vc;
+    float* out;
+    const float* k_new;
+    const float* v_new;
+    float* part;
+    float* ml;
+    uint32_t* counters;
+    uint32_t kv_len, stride, H, KVH, chunk, pos;
+    float scale, theta;
+};
+
+// Splits kv_len into ranges of a multiple of 64 positions so that the grid
+// holds about two workgroups per CU; sizes the partial-output workspace.
+static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch) {
+    const uint32_t G = a.H / a.KVH, HB = (G + 7) / 8;
+    const uint32_t groups = batch * a.KVH * HB;
+    const uint32_t max_split = std::max<uint32_t>(1, 2 * c->cu_count / groups);
+    const uint32_t n64 = std::max<uint32_t>(1, (a.kv_len + 63) / 64);
+    const uint32_t per = (n64 + max_split - 1) / max_split;
+    a.chunk = per * 64;
+    const uint32_t nsplit = a.kv_len ? (a.kv_len + a.chunk - 1) / a.chunk : 1;
+    if (nsplit > 1) {
+        if (groups > kAttnCounters)
+            return fail(c, RT_ERR_DISPATCH,
+                        "kernel dispatch error: attention: %u head groups exceed %u", groups,
+                        kAttnCounters);
+        const size_t rows = (size_t)batch * a.H * nsplit;
+        const size_t hd = (size_t)(strstr(kname, "hd256") ? 256 : strstr(kname, "hd128") ? 128 : 64);
+        int st = ensure_ws(c, rows * (hd + 2) * sizeof(float), kname);
+        if (st != RT_OK) return st;
+        a.part = (float*)c->ws;
+        a.ml = a.part + rows * hd;
+        a.counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
+    }
+    void* params[] = {&a};
+    return launch(c, kname, dim3(nsplit, a.KVH * HB, batch), dim3(256), 0, params);
+}
+
 int rt_decode_attention_f32(rt_ctx* c, const float* q, const float* k, const float* v, float* out,
                             uint32_t batch, uint32_t kv_len, uint32_t num_heads,
                             uint32_t num_kv_heads, uint32_t head_dim, uint32_t kv_head_stride) {
@@ -946,12 +996,19 @@ int rt_decode_attention_f32(rt_ctx* c, const float* q, const float* k, const flo
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: attention: kv_len=%u > kv_head_stride=%u", kv_len,
                     kv_head_stride);
-    const float scale = 1.0f / sqrtf((float)head_dim);  // dispatch.rs:1588
-    void* params[] = {&q, &k, &v, &out, &kv_len, &num_heads, &num_kv_heads,
-                      (void*)&scale, &kv_head_stride};
+    AttnArgs a{};
+    a.q = q;
+    a.kc = const_cast<float*>(k);  // read only without rope
+    a.vc = const_cast<float*>(v);
+    a.out = out;
+    a.kv_len = kv_len;
+    a.stride = kv_head_stride;
+    a.H = num_heads;
+    a.KVH = num_kv_heads;
+    a.scale = 1.0f / sqrtf((float)head_dim);  // dispatch.rs:1588
     char kn[64];
     snprintf(kn, sizeof kn, "k_decode_attention_f32_hd%u", head_dim);
-    return launch(c, kn, dim3(num_heads, batch), dim3(256), 0, params);
+    return attn_launch(c, kn, a, batch);
 }
 
 int rt_decode_attention_rope_f32(rt_ctx* c, const float* q_raw, const float* k_raw,
@@ -967,12 +1024,23 @@ int rt_decode_attention_rope_f32(rt_ctx* c, const float* q_raw, const float* k_r
     if (pos >= max_seq)
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: attention: pos=%u ≥ max_seq=%u",
                     pos, max_seq);
-    const float scale = 1.0f / sqrtf((float)head_dim);
-    void* params[] = {&q_raw, &k_raw, &v_raw, &k_cache, &v_cache, &out, &pos, &max_seq,
-                      &num_heads, &num_kv_heads, &theta, (void*)&scale};
+    AttnArgs a{};
+    a.q = q_raw;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.out = out;
+    a.k_new = k_raw;
+    a.v_new = v_raw;
+    a.kv_len = pos + 1;
+    a.stride = max_seq;
+    a.H = num_heads;
+    a.KVH = num_kv_heads;
+    a.pos = pos;
+    a.scale = 1.0f / sqrtf((float)head_dim);
+    a.theta = theta;
     char kn[64];
     snprintf(kn, sizeof kn, "k_attn_rope_f32_hd%u", head_dim);
-    return launch(c, kn, dim3(num_heads), dim3(256), 0, params);
+    return attn_launch(c, kn, a, 1);
 }
 
 int rt_embed_q8_0_f32(rt_ctx* c, const void* table, const uint32_t* token, float* out, uint32_t k) {

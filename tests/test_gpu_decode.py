@@ -58,11 +58,6 @@ def test_kv_copy(ctx):
     assert np.array_equal(cb.read(np.float32, cache.size), cache.ravel())
 
 
-def attn_tol(v, kvh_of, L, hd):
-    vmax = np.max(np.abs(v[:, :max(L, 1)]), axis=1)  # [kvh, hd]
-    return np.concatenate([1e-5 * vmax[kvh_of(h)] + 1e-6 for h in range(len(kvh_of.heads))])
-
-
 @pytest.mark.parametrize("kv_len", [0, 1, 7, 512, 5000])
 def test_decode_attention(ctx, kv_len):
     rng = np.random.default_rng(kv_len)
@@ -79,6 +74,31 @@ def test_decode_attention(ctx, kv_len):
     vmax = np.abs(v).max()
     # f32 scores / exp / weighted sums over ≤ 5000 positions
     assert np.all(np.abs(got - ref) <= 2e-5 * vmax + 1e-6), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("batch,H,KVH,hd,kv_len", [
+    (2, 14, 2, 64, 300),     # batch rows share no state
+    (1, 32, 2, 128, 1500),   # 16 query heads per kv head: two head blocks
+    (1, 40, 8, 128, 4097),   # 5 per kv head, a ragged last split
+    (1, 8, 8, 256, 65),      # MHA, head_dim 256
+    (1, 4, 1, 64, 20000),    # many splits, each longer than 64 positions
+])
+def test_decode_attention_shapes(ctx, batch, H, KVH, hd, kv_len):
+    rng = np.random.default_rng(H * kv_len + hd)
+    S = kv_len + 5
+    q = rng.standard_normal((batch, H * hd)).astype(np.float32)
+    k = rng.standard_normal((batch, KVH, S, hd)).astype(np.float32)
+    v = rng.standard_normal((batch, KVH, S, hd)).astype(np.float32)
+    out = ctx.new_buffer(4 * batch * H * hd)
+    qb, kb, vb = ctx.buffer_from(q), ctx.buffer_from(k), ctx.buffer_from(v)
+    for _ in range(2):  # the second call reuses the arrival counters
+        d.decode_attention_f32(ctx, qb, kb, vb, out, batch, kv_len, H, KVH, hd, S)
+        ctx.flush()
+        got = out.read(np.float32, batch * H * hd).reshape(batch, -1).astype(np.float64)
+        for bi in range(batch):
+            ref = ora.attention(q[bi], k[bi], v[bi], H, KVH, hd, kv_len, S)
+            assert np.all(np.abs(got[bi] - ref) <= 2e-5 * np.abs(v[bi]).max() + 1e-6), \
+                (bi, np.abs(got[bi] - ref).max())
 
 
 @pytest.mark.parametrize("pos", [0, 511, 4200])
