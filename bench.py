@@ -384,6 +384,8 @@ def gemv_specs(ctx, suite):
         for m in (1, 4, 8, 16, 32):
             specs.append((f"c5_gemm_q8_0_m{m}_18944x3584",
                           (lambda m=m: Workload(ctx, "c5", "q8_0", "gemm", 18944, 3584, m=m, seed=11))))
+            specs.append((f"c5_gemm_q8_0_m{m}_3584x18944",
+                          (lambda m=m: Workload(ctx, "c5", "q8_0", "gemm", 3584, 18944, m=m, seed=12))))
     return specs
 
 

@@ -194,18 +194,20 @@ RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result,
                 st.v = sb[w].v;
                 st.idx = sb[w].idx;
             }
-        states[blockIdx.x] = st;
-        __threadfence();
-        last = atomicAdd(counter, 1u) == gridDim.x - 1;
+        AmState* dst = &states[blockIdx.x];
+        dev_store(&dst->nan_idx, st.nan_idx);
+        dev_store(&dst->idx, st.idx);
+        dev_store(&dst->v, st.v);
+        dev_stores_done();
+        last = arrive(counter) == gridDim.x - 1;
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     // ordered tree merge of the workgroup states (merge is associative)
     const uint32_t G = gridDim.x;
     if (tid < G) {
-        const volatile AmState* vs = &states[tid];
-        sb[tid] = AmState{vs->nan_idx, vs->idx, vs->v};
+        const AmState* vs = &states[tid];
+        sb[tid] = AmState{dev_load(&vs->nan_idx), dev_load(&vs->idx), dev_load(&vs->v)};
     }
     __syncthreads();
     for (uint32_t st = 1; st < G; st <<= 1) {
@@ -222,7 +224,7 @@ RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result,
                 res = (uint32_t)acc.idx;
         }
         result[0] = res;
-        *counter = 0;  // ready for the next call (also under graph replay)
+        dev_store(counter, 0u);  // ready for the next call (also under graph replay)
     }
 }
 

@@ -288,22 +288,25 @@ RT_DEV void attn_split(const AttnArgs& a) {
             const float l = l_run[h];
             ((f32x4*)(a.out + ((size_t)b * a.H + h0 + h) * HD))[c] = t * (l > 0.0f ? 1.0f / l : 0.0f);
         } else {
-            ((f32x4*)(a.part + (((size_t)b * a.H + h0 + h) * nsp + s) * HD))[c] = t;
+            float* pp = a.part + (((size_t)b * a.H + h0 + h) * nsp + s) * HD + 4 * c;
+            dev_store(pp + 0, t.x);
+            dev_store(pp + 1, t.y);
+            dev_store(pp + 2, t.z);
+            dev_store(pp + 3, t.w);
         }
     }
     if (nsp == 1) return;
     if (tid < gh) {
         float* mlp = a.ml + (((size_t)b * a.H + h0 + tid) * nsp + s) * 2;
-        mlp[0] = m_run[tid];
-        mlp[1] = l_run[tid];
+        dev_store(mlp + 0, m_run[tid]);
+        dev_store(mlp + 1, l_run[tid]);
     }
-    __threadfence();
+    dev_stores_done();
     __syncthreads();
     uint32_t* counter = a.counters + ((size_t)b * a.KVH + kvh) * HB + hb;
-    if (tid == 0) last_flag = atomicAdd(counter, 1u) == nsp - 1;
+    if (tid == 0) last_flag = arrive(counter) == nsp - 1;
     __syncthreads();
     if (!last_flag) return;
-    __threadfence();  // acquire: the other workgroups' partials are visible
     // merge the splits in split order: o = Σ o_s·e^(m_s−M) / Σ l_s·e^(m_s−M)
     for (uint32_t i = tid; i < gh * C4; i += 256) {
         const uint32_t h = i / C4, c = i % C4;
@@ -311,18 +314,19 @@ RT_DEV void attn_split(const AttnArgs& a) {
         const float* mlv = a.ml + row * 2;
         float M = -__builtin_huge_valf();
 #pragma unroll 8
-        for (uint32_t j = 0; j < nsp; ++j) M = fmaxf(M, mlv[2 * j]);
+        for (uint32_t j = 0; j < nsp; ++j) M = fmaxf(M, dev_load(mlv + 2 * j));
         float L = 0.0f;
         f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 8
         for (uint32_t j = 0; j < nsp; ++j) {
-            const float f = expf(mlv[2 * j] - M);
-            L += mlv[2 * j + 1] * f;
-            o += ((const f32x4*)(a.part + (row + j) * HD))[c] * f;
+            const float f = expf(dev_load(mlv + 2 * j) - M);
+            L += dev_load(mlv + 2 * j + 1) * f;
+            const float* pj = a.part + (row + j) * HD + 4 * c;
+            o += f32x4{dev_load(pj), dev_load(pj + 1), dev_load(pj + 2), dev_load(pj + 3)} * f;
         }
         ((f32x4*)(a.out + ((size_t)b * a.H + h0 + h) * HD))[c] = o * (L > 0.0f ? 1.0f / L : 0.0f);
     }
-    if (tid == 0) *counter = 0;  // ready for the next call (also under graph replay)
+    if (tid == 0) dev_store(counter, 0u);  // ready for the next call (also under graph replay)
 }
 
 // decode_attention_f32 (attention.metal:248-308; dispatch.rs:1575-1612).

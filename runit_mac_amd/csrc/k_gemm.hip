@@ -1,0 +1,382 @@
+// k_gemm.hip — batched Q8_0 GEMM, Y[M,N] = X[M,K]·W[N,K]ᵀ, for M ≥ 2 (new:
+// the reference's only M > 1 path is gemm_f16 on f16-dequantised weights,
+// gemm.metal:39-190, called from verify_draft, forward.rs:2193-2271).
+//
+// One v_mfma_i32_16x16x32_i8 per (Q8_0 block, 4 activation rows, 16 weight
+// rows): its K of 32 is exactly one block, so the block's scales apply to the
+// MFMA's integer result.
+//   A (16×32): row 4·mm + limb = limb plane `limb` (0..2; row 3 is zero) of
+//              activation row 4g + mm, i.e. the same exact base-256 digits as
+//              the GEMV path (rt_device.h);
+//   B (32×16): the block's int8 quants of weight rows n0 .. n0+15, as stored;
+//   D (16×16): lane l holds D[4·(l/16) + r][l % 16], r = 0..3 — the three
+//              limb dots of activation row 4g + l/16 against weight row
+//              n0 + l%16 (r = 3 is zero).
+// The lane combines its limbs and adds ldexp(d · (65536·c0 + 256·c1 + c2),
+// E − 22) to its f32 accumulator, as the GEMV's matrix-core path does.
+//
+// Activations are prepared once per launch by k_gemm_x_prep into the A
+// operand order ([chunk][block][group][lane] 8-byte entries, one coalesced
+// dwordx2 per lane) plus the block exponents ([chunk][block][mm][group]).
+#include "rt_formats.h"
+
+typedef long i64_t;
+
+struct GemmArgs {
+    const uint8_t* w;     // N rows of nxb Q8_0 blocks
+    const uint2* aops;    // prepared activations
+    const int* etab;      // block exponents
+    float* y;             // [M][N]
+    uint32_t M, N, K, nxb, ksw;
+    uint64_t row_bytes;
+};
+
+// Activation preparation: thread t → (chunk row r, block b, slice q of 4
+// elements); 8 consecutive threads hold one block (limb_digits' lane group).
+// Rows past M are zero.
+template <int MG>
+RT_DEV void gemm_prep_body(const float* __restrict__ x, uint32_t M, uint32_t K, uint32_t nchunks,
+                           uint32_t* __restrict__ aops, int* __restrict__ etab) {
+    const uint32_t nxb = K / 32;
+    constexpr uint32_t ROWS = 4 * MG;
+    const uint64_t total = (uint64_t)nchunks * ROWS * nxb * 8;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t q = t & 7;
+        const uint64_t rb = t >> 3;  // (chunk row, block) pair
+        const uint32_t b = (uint32_t)(rb % nxb);
+        const uint32_t rr = (uint32_t)(rb / nxb);  // chunk·ROWS + row
+        const uint32_t ch = rr / ROWS, row = rr % ROWS;
+        const uint32_t m = ch * ROWS + row;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (m < M) {
+            const f32x4 xv = *(const f32x4*)(x + (size_t)m * K + (size_t)b * 32 + 4 * q);
+            v[0] = xv.x; v[1] = xv.y; v[2] = xv.z; v[3] = xv.w;
+        }
+        int e;
+        int l[3][4];
+        limb_digits(v, e, l);
+        const uint32_t g = row / 4, mm = row % 4;
+        const uint32_t cq = q / 2;  // 8-element chunk of the block = MFMA k-group
+        uint32_t* base = aops + (((size_t)ch * nxb + b) * MG + g) * 128;  // 64 lanes × 2 dwords
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lane = (4 * mm + k) + 16 * cq;
+            base[lane * 2 + (q & 1)] = k < 3 ? pack_i8x4(l[k]) : 0u;
+        }
+        if (q == 0) etab[(((size_t)ch * nxb + b) * 4 + mm) * MG + g] = e;
+    }
+}
+#define RT_GEMM_PREP(MG)                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) k_gemm_x_prep_mg##MG(                    \
+        const float* x, uint32_t M, uint32_t K, uint32_t nchunks, uint32_t* aops, int* etab) { \
+        gemm_prep_body<MG>(x, M, K, nchunks, aops, etab);                                      \
+    }
+RT_GEMM_PREP(1)
+RT_GEMM_PREP(2)
+RT_GEMM_PREP(4)
+RT_GEMM_PREP(8)
+
+template <int MG, int CT>
+struct GemmBlk {
+    uint32_t wq[CT][3];  // aligned dwords covering the lane's 8 quants
+    uint32_t wd[CT];     // aligned dword holding the block scale
+    uint2 A[MG];
+    int E[MG];
+};
+
+// Workgroup = ksw waves sharing one group of 16·CT weight rows and one chunk
+// of 4·MG activation rows; wave wk takes blocks wk, wk + ksw, ... and the
+// waves' partial sums are added in wave order.
+template <int MG, int CT, int DEPTH>
+RT_DEV void gemm_body(const GemmArgs& a) {
+    __shared__ float red[8][MG * CT][64];
+    const uint32_t lane = threadIdx.x & 63, wk = threadIdx.x >> 6, ksw = a.ksw;
+    const uint32_t j = lane & 15, c = lane >> 4;
+    const uint32_t ch = blockIdx.y, n0 = blockIdx.x * 16 * CT;
+    const uint32_t nxb = a.nxb;
+    const uint2* ap = a.aops + (size_t)ch * nxb * MG * 64;
+    const int* ep = a.etab + (size_t)ch * nxb * 4 * MG;
+    const uint8_t* wrow[CT];
+#pragma unroll
+    for (int t = 0; t < CT; ++t) {
+        const uint32_t n = min(n0 + 16 * t + j, a.N - 1);  // clamped rows are not stored
+        wrow[t] = a.w + (size_t)n * a.row_bytes;
+    }
+    auto load = [&](uint32_t b, GemmBlk<MG, CT>& k) {
+#pragma unroll
+        for (int t = 0; t < CT; ++t) {
+            const uint8_t* blk = wrow[t] + (size_t)b * 34;
+            const uintptr_t p = (uintptr_t)(blk + 2 + 8 * c);
+            const uint32_t* pq = (const uint32_t*)(p & ~(uintptr_t)3);
+            k.wq[t][0] = pq[0];
+            k.wq[t][1] = pq[1];
+            // the third dword is needed only for a 2-byte offset; otherwise it
+            // could lie past the end of the weights, so re-read the second
+            k.wq[t][2] = pq[(p & 3) ? 2 : 1];
+            k.wd[t] = *(const uint32_t*)((uintptr_t)blk & ~(uintptr_t)3);
+        }
+#ifdef RT_PROBE_GEMM_NOA
+#pragma unroll
+        for (int g = 0; g < MG; ++g) { k.A[g] = uint2{lane * 77u + b, b}; k.E[g] = (int)(b & 7); }
+#else
+#pragma unroll
+        for (int g = 0; g < MG; ++g) k.A[g] = ap[((size_t)b * MG + g) * 64 + lane];
+        const int* e = ep + ((size_t)b * 4 + c) * MG;
+#pragma unroll
+        for (int g = 0; g < MG; ++g) k.E[g] = e[g];
+#endif
+    };
+    float acc[MG][CT];
+#pragma unroll
+    for (int g = 0; g < MG; ++g)
+#pragma unroll
+        for (int t = 0; t < CT; ++t) acc[g][t] = 0.0f;
+    auto compute = [&](uint32_t b, const GemmBlk<MG, CT>& k) {
+#pragma unroll
+        for (int t = 0; t < CT; ++t) {
+            const uintptr_t blk = (uintptr_t)(wrow[t] + (size_t)b * 34);
+            const uint32_t sh = (uint32_t)((blk + 2) & 3);  // 0 or 2
+            const uint32_t q0 = alignb(k.wq[t][1], k.wq[t][0], sh);
+            const uint32_t q1 = alignb(k.wq[t][2], k.wq[t][1], sh);
+            const i64_t B = (i64_t)(((uint64_t)q1 << 32) | q0);
+            const float d = h2f((blk & 3) ? (k.wd[t] >> 16) : k.wd[t]);
+#pragma unroll
+            for (int g = 0; g < MG; ++g) {
+#ifdef RT_PROBE_GEMM_NOMFMA
+                acc[g][t] += d * (float)(q0 ^ q1 ^ k.A[g].x ^ k.A[g].y) + (float)k.E[g];
+#else
+                const i64_t A = (i64_t)(((uint64_t)k.A[g].y << 32) | k.A[g].x);
+                const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, v4i{0, 0, 0, 0}, 0, 0, 0);
+                acc[g][t] += __builtin_amdgcn_ldexpf(d * comb4(C), k.E[g] - 22);
+#endif
+            }
+        }
+    };
+    // DEPTH blocks in flight per wave; loads past the end are clamped (every
+    // lane issues the same loads, so waits stay partial)
+    GemmBlk<MG, CT> buf[DEPTH];
+    const uint32_t last = nxb - 1;
+#pragma unroll
+    for (int h = 0; h < DEPTH; ++h) load(min(wk + h * ksw, last), buf[h]);
+    for (uint32_t b0 = wk; b0 < nxb; b0 += DEPTH * ksw) {
+#pragma unroll
+        for (int h = 0; h < DEPTH; ++h) {
+            const uint32_t b = b0 + h * ksw;
+            if (b < nxb) {
+                compute(b, buf[h]);
+                load(min(b + DEPTH * ksw, last), buf[h]);
+            }
+        }
+    }
+    if (ksw > 1) {
+#pragma unroll
+        for (int g = 0; g < MG; ++g)
+#pragma unroll
+            for (int t = 0; t < CT; ++t) red[wk][g * CT + t][lane] = acc[g][t];
+        __syncthreads();
+        if (wk != 0) return;
+#pragma unroll
+        for (int g = 0; g < MG; ++g)
+#pragma unroll
+            for (int t = 0; t < CT; ++t) {
+                float s = 0.0f;
+                for (uint32_t w = 0; w < ksw; ++w) s += red[w][g * CT + t][lane];
+                acc[g][t] = s;
+            }
+    }
+#pragma unroll
+    for (int g = 0; g < MG; ++g)
+#pragma unroll
+        for (int t = 0; t < CT; ++t) {
+            const uint32_t m = ch * 4 * MG + 4 * g + c, n = n0 + 16 * t + j;
+            if (m < a.M && n < a.N) a.y[(size_t)m * a.N + n] = acc[g][t];
+        }
+}
+
+// DEPTH: blocks in flight per wave (registers per block grow with MG)
+#define RT_GEMM_KERNEL(MG, CT, DEPTH)                                                       \
+    extern "C" __global__ void __launch_bounds__(512) k_gemm_q8_0_mg##MG##_ct##CT(GemmArgs a) { \
+        gemm_body<MG, CT, DEPTH>(a);                                                        \
+    }
+RT_GEMM_KERNEL(1, 1, 8)
+RT_GEMM_KERNEL(2, 1, 8)
+RT_GEMM_KERNEL(4, 1, 4)
+RT_GEMM_KERNEL(8, 1, 4)
+RT_GEMM_KERNEL(1, 2, 8)
+RT_GEMM_KERNEL(2, 2, 6)
+RT_GEMM_KERNEL(4, 2, 4)
+RT_GEMM_KERNEL(8, 2, 3)
+
+// ───────────────────── LDS-staged variant (nxb % 8 == 0) ─────────────────────
+//
+// Workgroup of 4 waves = one tile of 64 weight rows (16 per wave).  The K
+// range is streamed in stages of NB blocks (8, or 4 for large batches, which
+// keeps the stage's activation operands small enough for 2+ workgroups per
+// CU): the 64 row segments (NB·34 contiguous bytes each, 16- or 8-byte
+// aligned), the stage's prepared activation operands and block exponents are
+// loaded with coalesced loads, written to LDS, and consumed from there; the
+// next stage's loads are in flight while the current one is computed (two
+// LDS buffers).
+//
+// Work items (row tile, K split, activation chunk) are spread over a
+// persistent grid.  With more than one K split, each item writes its partial
+// sums; the last item of a (tile, chunk) to finish (arrival counter, reset by
+// that item) adds the splits in split order and stores Y.
+constexpr uint32_t GB_ROWS = 64;  // weight rows per tile
+
+struct Gemm2Args {
+    const uint8_t* w;
+    const uint2* aops;
+    const int* etab;
+    float* y;
+    float* part;          // [chunk][split][chunk rows][N] partial sums (splits > 1)
+    uint32_t* counters;   // [chunk][tile]
+    uint32_t M, N, nxb, tiles, splits, kbs, nchunks;
+    uint64_t row_bytes;
+};
+
+template <int MG, int NB>
+RT_DEV void gemm2_body(const Gemm2Args& a) {
+    constexpr uint32_t SEG = NB * 34;                   // bytes of a row segment
+    constexpr uint32_t VB = NB == 8 ? 16 : 8;           // bytes per W load (alignment)
+    typedef typename std::conditional<NB == 8, u32x4, uint2>::type WV;
+    constexpr uint32_t WPR = SEG / VB;                  // W loads per row segment
+    constexpr uint32_t WV_N = GB_ROWS * WPR;            // W loads per stage
+    constexpr uint32_t AV4 = NB * MG * 64 * 8 / 16;     // dwordx4 of A per stage
+    constexpr uint32_t EV4 = NB * 4 * MG * 4 / 16;      // dwordx4 of E per stage
+    constexpr uint32_t WPT = (WV_N + 255) / 256;        // W loads per thread
+    constexpr uint32_t APT = (AV4 + 255) / 256;
+    static_assert(SEG % VB == 0, "segment alignment");
+    __shared__ WV lw[2][WV_N];
+    __shared__ u32x4 la[2][AV4];
+    __shared__ u32x4 le[2][EV4 > 0 ? EV4 : 1];
+    __shared__ uint32_t last_flag;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t j = lane & 15, c = lane >> 4;
+    const uint32_t nitems = a.tiles * a.splits * a.nchunks;
+
+    for (uint32_t item = blockIdx.x; item < nitems; item += gridDim.x) {
+        const uint32_t tile = item % a.tiles;
+        const uint32_t split = (item / a.tiles) % a.splits;
+        const uint32_t ch = item / (a.tiles * a.splits);
+        const uint32_t kb0 = split * a.kbs;
+        const uint32_t kb1 = min(a.nxb, kb0 + a.kbs);
+        const uint32_t nst = (kb1 - kb0) / NB;
+        const uint32_t row0 = tile * GB_ROWS;
+        const uint2* ap = a.aops + (size_t)ch * a.nxb * MG * 64;
+        const int* ep = a.etab + (size_t)ch * a.nxb * 4 * MG;
+
+        WV rw[WPT];
+        u32x4 ra[APT], re;
+        auto gload = [&](uint32_t st) {
+            const uint32_t b0 = kb0 + st * NB;
+#pragma unroll
+            for (uint32_t i = 0; i < WPT; ++i) {
+                uint32_t f = tid + 256 * i;
+                if (f >= WV_N) f = WV_N - 1;  // duplicate load, not stored
+                const uint32_t r = f / WPR, col = f % WPR;
+                const uint32_t n = min(row0 + r, a.N - 1);
+                rw[i] = *(const WV*)(a.w + (size_t)n * a.row_bytes + (size_t)b0 * 34 + col * VB);
+            }
+            const u32x4* as = (const u32x4*)(ap + (size_t)b0 * MG * 64);
+#pragma unroll
+            for (uint32_t i = 0; i < APT; ++i) ra[i] = as[min(tid + 256 * i, AV4 - 1)];
+            re = ((const u32x4*)(ep + (size_t)b0 * 4 * MG))[min(tid, EV4 - 1)];
+        };
+        auto lstore = [&](uint32_t buf) {
+#pragma unroll
+            for (uint32_t i = 0; i < WPT; ++i)
+                if (tid + 256 * i < WV_N) lw[buf][tid + 256 * i] = rw[i];
+#pragma unroll
+            for (uint32_t i = 0; i < APT; ++i)
+                if (tid + 256 * i < AV4) la[buf][tid + 256 * i] = ra[i];
+            if (tid < EV4) le[buf][tid] = re;
+        };
+        float acc[MG];
+#pragma unroll
+        for (int g = 0; g < MG; ++g) acc[g] = 0.0f;
+        const uint32_t wrow = (16 * wv + j) * SEG;  // this lane's row in a W buffer
+        auto compute = [&](uint32_t buf) {
+            const uint8_t* wb = (const uint8_t*)lw[buf];
+            const uint2* ab = (const uint2*)la[buf];
+            const int* eb = (const int*)le[buf];
+#pragma unroll 2
+            for (uint32_t blk = 0; blk < NB; ++blk) {
+                const uint32_t o = wrow + blk * 34 + 2 + 8 * c;  // LDS byte offset of the quants
+                const uint32_t* pw = (const uint32_t*)(wb + (o & ~3u));
+                const uint32_t sh = o & 3;
+                const uint32_t w0 = pw[0], w1 = pw[1], w2 = pw[(o & 3) ? 2 : 1];
+                const uint32_t q0 = alignb(w1, w0, sh), q1 = alignb(w2, w1, sh);
+                const i64_t B = (i64_t)(((uint64_t)q1 << 32) | q0);
+                const float d = h2f(*(const uint16_t*)(wb + wrow + blk * 34));
+                // all of the block's matrix-core products first, then their
+                // epilogues (independent MFMAs overlap in the pipeline)
+                v4i C[MG];
+#pragma unroll
+                for (int g = 0; g < MG; ++g) {
+                    const uint2 av = ab[(blk * MG + g) * 64 + lane];
+                    const i64_t A = (i64_t)(((uint64_t)av.y << 32) | av.x);
+                    C[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, v4i{0, 0, 0, 0}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int g = 0; g < MG; ++g)
+                    acc[g] += __builtin_amdgcn_ldexpf(d * comb4(C[g]), eb[(blk * 4 + c) * MG + g] - 22);
+            }
+        };
+        if (nst > 0) {
+            gload(0);
+            lstore(0);
+        }
+        __syncthreads();
+        for (uint32_t st = 0; st < nst; ++st) {
+            const bool more = st + 1 < nst;
+            if (more) gload(st + 1);
+            compute(st & 1);
+            if (more) lstore((st + 1) & 1);
+            __syncthreads();
+        }
+        // results: lane holds (activation row ch·4MG + 4g + c, weight row row0 + 16wv + j)
+        const uint32_t n = row0 + 16 * wv + j;
+        if (a.splits == 1) {
+#pragma unroll
+            for (int g = 0; g < MG; ++g) {
+                const uint32_t m = ch * 4 * MG + 4 * g + c;
+                if (m < a.M && n < a.N) a.y[(size_t)m * a.N + n] = acc[g];
+            }
+            continue;
+        }
+        const size_t crow = (size_t)4 * MG;  // rows of a chunk
+#pragma unroll
+        for (int g = 0; g < MG; ++g) {
+            const size_t pr = ((size_t)(ch * a.splits + split) * crow + 4 * g + c);
+            if (n < a.N) dev_store(a.part + pr * a.N + n, acc[g]);
+        }
+        dev_stores_done();
+        __syncthreads();
+        uint32_t* counter = a.counters + (size_t)ch * a.tiles + tile;
+        if (tid == 0) last_flag = arrive(counter) == a.splits - 1;
+        __syncthreads();
+        if (!last_flag) continue;
+        if (n < a.N) {
+#pragma unroll
+            for (int g = 0; g < MG; ++g) {
+                const uint32_t m = ch * 4 * MG + 4 * g + c;
+                float s = 0.0f;
+                for (uint32_t sp = 0; sp < a.splits; ++sp)
+                    s += dev_load(a.part + ((size_t)(ch * a.splits + sp) * crow + 4 * g + c) * a.N + n);
+                if (m < a.M) a.y[(size_t)m * a.N + n] = s;
+            }
+        }
+        if (tid == 0) dev_store(counter, 0u);  // ready for the next call (also under graph replay)
+        __syncthreads();
+    }
+}
+#define RT_GEMM2_KERNEL(MG, NB)                                                                \
+    extern "C" __global__ void __launch_bounds__(256) k_gemm2_q8_0_mg##MG(Gemm2Args a) {      \
+        gemm2_body<MG, NB>(a);                                                                 \
+    }
+RT_GEMM2_KERNEL(1, 8)
+RT_GEMM2_KERNEL(2, 8)
+RT_GEMM2_KERNEL(4, 4)
+RT_GEMM2_KERNEL(8, 4)

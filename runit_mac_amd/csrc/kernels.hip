@@ -3,3 +3,4 @@
 #include "k_gemv.hip"
 #include "k_aux.hip"
 #include "k_decode.hip"
+#include "k_gemm.hip"

@@ -102,6 +102,28 @@ RT_DEV int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// ───────────────────── cross-workgroup hand-off ─────────────────────
+//
+// Partial results that another workgroup (possibly on another XCD) combines
+// are written with device-scope stores (written through to the coherent
+// level instead of staying in this XCD's L2) and read back with device-scope
+// loads.  arrive() waits until this thread's stores have completed and then
+// counts the workgroup in; callers put a __syncthreads() between every
+// thread's dev_store()s and the one thread that calls arrive().  No L2
+// write-back or invalidate of whole caches is involved.
+template <typename T>
+RT_DEV void dev_store(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+RT_DEV T dev_load(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+RT_DEV void dev_stores_done() { __builtin_amdgcn_s_waitcnt(0); }
+RT_DEV uint32_t arrive(uint32_t* counter) {
+    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ───────────────────────────── activation limbs ─────────────────────────────
 //
 // One record per 32 activations, 112 bytes (a stride of 28 dwords keeps eight
@@ -151,8 +173,11 @@ RT_DEV void load_x4<uint16_t>(const uint16_t* x, uint32_t idx, float v[4]) {
 // non-finite cases are selects, and every lane stores whole dwords (limb
 // dword q of each limb plane, and meta dword q % 4, which lanes q and q + 4
 // write with the same value).
-template <bool Q40PERM>
-RT_DEV void limb_slice(const float v[4], uint32_t q, XRec* __restrict__ rec) {
+// Block exponent and balanced base-256 digits of one 4-element slice (lane q
+// of the 8 consecutive, 8-aligned, active lanes of an x-block): e is the
+// block's frexp exponent (XE_NONFINITE if it holds Inf/NaN, 0 if all zero)
+// and x_i ≈ 2^(e-22)·(65536·l[0][i] + 256·l[1][i] + l[2][i]).
+RT_DEV void limb_digits(const float v[4], int& e, int l[3][4]) {
     constexpr float FMAX = 3.40282347e38f;
     bool nf[4];
     bool any_nf = false;
@@ -168,8 +193,7 @@ RT_DEV void limb_slice(const float v[4], uint32_t q, XRec* __restrict__ rec) {
     a = max8(any_nf ? __builtin_huge_valf() : a);
     const bool finite = a <= FMAX;
     const int ef = __builtin_amdgcn_frexp_expf(a);  // a < 2^ef
-    const int e = !finite ? XE_NONFINITE : (a == 0.0f ? 0 : ef);
-    int l[3][4];
+    e = !finite ? XE_NONFINITE : (a == 0.0f ? 0 : ef);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         // finite block: round(x · 2^(22-e)), |xi| ≤ 2^22.  Non-finite block:
@@ -178,7 +202,6 @@ RT_DEV void limb_slice(const float v[4], uint32_t q, XRec* __restrict__ rec) {
         const int xf = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v[i], 22 - ef));
         const int xn = nf[i] ? ((v[i] < 0.0f) ? -(1 << 22) : (1 << 22)) : 0;
         const int xi = finite ? xf : xn;
-        // balanced base-256 digits: xi = 65536·l0 + 256·l1 + l2
         const int c = ((xi + 128) & 255) - 128;
         const int r1 = (xi - c) >> 8;
         const int bb = ((r1 + 128) & 255) - 128;
@@ -186,11 +209,26 @@ RT_DEV void limb_slice(const float v[4], uint32_t q, XRec* __restrict__ rec) {
         l[1][i] = bb;
         l[2][i] = c;
     }
+}
+RT_DEV uint32_t pack_i8x4(const int l[4]) {
+    return (uint32_t)(l[0] & 255) | ((uint32_t)(l[1] & 255) << 8) |
+           ((uint32_t)(l[2] & 255) << 16) | ((uint32_t)l[3] << 24);
+}
+
+// Converts one 4-element slice (lane q of the 8 lanes of x-block b) into
+// limbs and writes them to the block's record.  Straight-line code: the
+// non-finite cases are selects, and every lane stores whole dwords (limb
+// dword q of each limb plane, and meta dword q % 4, which lanes q and q + 4
+// write with the same value).
+template <bool Q40PERM>
+RT_DEV void limb_slice(const float v[4], uint32_t q, XRec* __restrict__ rec) {
+    int e;
+    int l[3][4];
+    limb_digits(v, e, l);
     uint32_t* recw = (uint32_t*)rec;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-        const uint32_t own = (uint32_t)(l[k][0] & 255) | ((uint32_t)(l[k][1] & 255) << 8) |
-                             ((uint32_t)(l[k][2] & 255) << 16) | ((uint32_t)l[k][3] << 24);
+        const uint32_t own = pack_i8x4(l[k]);
         uint32_t w = own;
         if (Q40PERM) {
             // 8-group as evens then odds: lane 2m stores elements

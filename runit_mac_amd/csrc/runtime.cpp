@@ -90,6 +90,10 @@ const char* const kKernelNames[] = {
     "k_decode_attention_f32_hd64", "k_decode_attention_f32_hd128", "k_decode_attention_f32_hd256",
     "k_attn_rope_f32_hd64", "k_attn_rope_f32_hd128", "k_attn_rope_f32_hd256",
     "k_embed_q8_0_f32",
+    "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
+    "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
+    "k_gemm_q8_0_mg1_ct2", "k_gemm_q8_0_mg2_ct2", "k_gemm_q8_0_mg4_ct2", "k_gemm_q8_0_mg8_ct2",
+    "k_gemm2_q8_0_mg1", "k_gemm2_q8_0_mg2", "k_gemm2_q8_0_mg4", "k_gemm2_q8_0_mg8",
 };
 
 struct Fmt {
@@ -129,6 +133,7 @@ struct rt_ctx {
     Plan plan_override{};
     uint32_t grid_per_cu = 0;  // RUNIT_GEMV_GRID_PER_CU: persistent-grid cap (sweeps only)
     uint32_t ksw_override = 0;  // RUNIT_GEMV_KSW: K-split waves (sweeps only)
+    bool gemm_direct = false;   // RUNIT_GEMM_DIRECT: force the unstaged GEMM kernel (tests)
     // Workspace for activation records built by the long-K pre-pass; grows on
     // demand (stream-ordered, so one buffer serves every launch).
     void* ws = nullptr;
@@ -440,6 +445,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     }
     if (const char* g = getenv("RUNIT_GEMV_GRID_PER_CU")) c->grid_per_cu = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_PREPASS_K")) c->prepass_k = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMM_DIRECT")) c->gemm_direct = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSW")) {
         const int v = atoi(g);
         if (v == 1 || v == 2 || v == 4 || v == 8) c->ksw_override = (uint32_t)v;
@@ -759,21 +765,108 @@ int rt_fused_ffn_q4k_f32(rt_ctx* c, const void* wg, const void* wu, const float*
 
 // ───────────────────────────── batched Q8_0 ─────────────────────────────
 
+// Mirror the device-side GemmArgs / Gemm2Args (k_gemm.hip).
+struct Gemm2Args {
+    const void* w;
+    const void* aops;
+    const int* etab;
+    float* y;
+    float* part;
+    uint32_t* counters;
+    uint32_t M, N, nxb, tiles, splits, kbs, nchunks;
+    uint64_t row_bytes;
+};
+struct GemmArgs {
+    const void* w;
+    const void* aops;
+    const int* etab;
+    float* y;
+    uint32_t M, N, K, nxb, ksw;
+    uint64_t row_bytes;
+};
+
 int rt_gemm_q8_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
                      uint32_t n, uint32_t k) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     if (m_rows == 0 || n == 0) return RT_OK;
     if (!w || !x || !y)
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_q8_0_f32: null buffer");
-    if (k == 0 || k % 32 != 0 || (k * 4u) % 16 != 0)
+    if (k == 0 || k % 32 != 0)
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: gemm_q8_0_f32: k=%u must be a positive multiple of 32",
                     k);
-    for (uint32_t r = 0; r < m_rows; ++r) {
-        int st = rt_gemv_q8_0_f32in_f32out(c, w, x + (size_t)r * k, y + (size_t)r * n, n, k);
+    if (!aligned(x, 16))
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: gemm_q8_0_f32: input must be 16-byte aligned");
+    if (m_rows == 1) return rt_gemv_q8_0_f32in_f32out(c, w, x, y, n, k);
+    const uint32_t cu = (uint32_t)c->cu_count;
+    // 4·MG activation rows per chunk (MG ∈ {1, 2, 4, 8}); longer batches
+    // take several chunks, each streaming W once
+    const uint32_t groups = (m_rows + 3) / 4;
+    const uint32_t MG = groups <= 1 ? 1 : groups <= 2 ? 2 : groups <= 4 ? 4 : 8;
+    const uint32_t nchunks = (m_rows + 4 * MG - 1) / (4 * MG);
+    const uint32_t nxb = k / 32;
+    const size_t a_bytes = (size_t)nchunks * nxb * MG * 64 * 8;
+    const size_t e_bytes = (size_t)nchunks * nxb * 4 * MG * sizeof(int);
+
+    // Plan.  LDS-staged kernel when rows stream in 272-byte, 16-byte-aligned
+    // segments: 64-row tiles, K in stages of 8 blocks, items (tile, K split,
+    // chunk) on a persistent grid of `cap` workgroups.  Otherwise the direct
+    // kernel: 16·CT weight rows per workgroup whose ksw waves split the blocks.
+    const bool staged = nxb % 8 == 0 && aligned(w, 16) && !c->gemm_direct;
+    const uint32_t tiles = (n + 63) / 64;
+    const uint32_t per_cu = MG == 4 ? 4 : 3;  // LDS-bound residency (34-52 KB per workgroup)
+    const uint32_t cap = cu * per_cu;
+    const uint32_t base = tiles * nchunks;
+    uint32_t splits = 1, kbs = nxb;
+    if (staged) {
+        double best = 1e30;
+        for (uint32_t sp = 1; sp <= std::min<uint32_t>(16, nxb / 8); ++sp) {
+            // rounds of items, each 1/sp of the K range, plus a small cost per split
+            const double rounds = (double)((base * sp + cap - 1) / cap);
+            const double t = rounds / sp + 0.02 * sp;
+            if (t < best - 1e-9) { best = t; splits = sp; }
+        }
+        kbs = ((nxb + splits - 1) / splits + 7) / 8 * 8;
+        splits = (nxb + kbs - 1) / kbs;
+        if (splits > 1 && base > kAttnCounters)
+            return fail(c, RT_ERR_DISPATCH,
+                        "kernel dispatch error: gemm_q8_0_f32: %u tiles exceed %u counters", base,
+                        kAttnCounters);
+    }
+    const size_t p_bytes = splits > 1 ? (size_t)splits * nchunks * 4 * MG * n * sizeof(float) : 0;
+    int st = ensure_ws(c, a_bytes + e_bytes + p_bytes, "gemm_q8_0_f32");
+    if (st != RT_OK) return st;
+    void* aops = c->ws;
+    int* etab = (int*)((char*)c->ws + a_bytes);
+    float* part = p_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes) : nullptr;
+    {
+        char pk[48];
+        snprintf(pk, sizeof pk, "k_gemm_x_prep_mg%u", MG);
+        const uint64_t threads = (uint64_t)nchunks * 4 * MG * nxb * 8;
+        const uint32_t grid = (uint32_t)std::min<uint64_t>((threads + 255) / 256, (uint64_t)cu * 16);
+        uint32_t M = m_rows, K = k, nc = nchunks;
+        void* pp[] = {(void*)&x, &M, &K, &nc, &aops, &etab};
+        st = launch(c, pk, dim3(grid), dim3(256), 0, pp);
         if (st != RT_OK) return st;
     }
-    return RT_OK;
+    if (staged) {
+        Gemm2Args a2{w, aops, etab, y, part, (uint32_t*)((char*)c->aux + kAuxAttnOff),
+                     m_rows, n, nxb, tiles, splits, kbs, nchunks, (uint64_t)nxb * 34};
+        char kn2[48];
+        snprintf(kn2, sizeof kn2, "k_gemm2_q8_0_mg%u", MG);
+        void* p2[] = {&a2};
+        return launch(c, kn2, dim3(std::min(base * splits, cap)), dim3(256), 0, p2);
+    }
+    const uint32_t CT = ((n + 31) / 32 >= 2 * cu) ? 2 : 1;
+    const uint32_t gx = (n + 16 * CT - 1) / (16 * CT);
+    uint32_t ksw = 1;
+    while (ksw < 8 && (uint64_t)gx * nchunks * ksw < 8ull * cu && ksw * 2 <= nxb) ksw *= 2;
+    GemmArgs a{w, aops, etab, y, m_rows, n, k, nxb, ksw, (uint64_t)nxb * 34};
+    char kn[48];
+    snprintf(kn, sizeof kn, "k_gemm_q8_0_mg%u_ct%u", MG, CT);
+    void* params[] = {&a};
+    return launch(c, kn, dim3(gx, nchunks), dim3(64 * ksw), 0, params);
 }
 
 // ───────────────────────────── dequant ─────────────────────────────

@@ -118,8 +118,8 @@ def test_argmax_f16(ctx):
 
 # ───────────────────────── batched Q8_0 GEMM ─────────────────────────
 
-@pytest.mark.parametrize("m", [1, 4, 8, 16, 32])
-@pytest.mark.parametrize("n,k", [(512, 1024), (130, 3584)])
+@pytest.mark.parametrize("m", [1, 2, 4, 5, 8, 13, 16, 32, 37])
+@pytest.mark.parametrize("n,k", [(512, 1024), (130, 3584), (33, 96), (1100, 32), (70, 8192)])
 def test_gemm_q8_0(ctx, m, n, k):
     wbuf, raw = device_weights(ctx, "q8_0", n, k, seed=m + n)
     x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
@@ -128,3 +128,31 @@ def test_gemm_q8_0(ctx, m, n, k):
     ctx.flush()
     yref, sabs = ora.gemv("q8_0", raw, x, n, k)
     check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm m={m}")
+    # a second call reuses the workspace; a smaller batch must not read stale rows
+    if m > 2:
+        y2 = ctx.new_buffer(4 * 2 * n)
+        d.gemm_q8_0_f32(ctx, wbuf, ctx.buffer_from(x[:2]), y2, 2, n, k)
+        ctx.flush()
+        check_close(y2.read(np.float32, 2 * n), yref[:2].ravel(), sabs[:2].ravel(), "gemm m=2")
+
+
+def test_gemm_q8_0_direct_kernel_matches_staged(ctx):
+    """The unstaged kernel (any K) on a shape the staged kernel also takes."""
+    import os
+    n, k, m = 300, 2048, 12
+    wbuf, raw = device_weights(ctx, "q8_0", n, k, seed=5)
+    x = np.random.default_rng(9).standard_normal((m, k)).astype(np.float32)
+    yref, sabs = ora.gemv("q8_0", raw, x, n, k)
+    os.environ["RUNIT_GEMM_DIRECT"] = "1"
+    try:
+        c2 = d.HipContext()
+    finally:
+        del os.environ["RUNIT_GEMM_DIRECT"]
+    try:
+        w2 = c2.buffer_from(raw)
+        y = c2.new_buffer(4 * m * n)
+        d.gemm_q8_0_f32(c2, w2, c2.buffer_from(x), y, m, n, k)
+        c2.flush()
+        check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), "gemm direct")
+    finally:
+        c2.close()
