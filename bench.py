@@ -286,6 +286,56 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
             "launches_reference": 1 + 10 * cfg.layers + 3}
 
 
+def measured_traffic(summary: str):
+    """HBM bytes per launch of a kernel, from its committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE, each scaled by a copy kernel's
+    reading); None when the summary is absent."""
+    import re
+    path = os.path.join(REPO, "profiles", summary)
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", open(path).read())
+    return int(m.group(1)) if m else None
+
+
+def profile_pass(ctx, launches: int = 24) -> None:
+    """Eager (not graph-captured) launches for hardware-counter runs
+    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the dominant kernel of the
+    decode step — the norm-fused gate+up+SiLU GEMV at the 0.5B shape — over
+    `launches` distinct weight replicas, then a plain copy kernel of known
+    size whose counters calibrate the byte counts."""
+    from runit_mac_amd.decode import DecodeConfig
+    cfg = DecodeConfig()
+    h, ff = cfg.hidden, cfg.ff
+    wb = d.weight_bytes("q8_0", ff, h)
+    arena = _arena_for(ctx, [wb, wb], launches)
+    mats = []
+    for r in range(launches):
+        g, u = arena.take(wb), arena.take(wb)
+        d.synth_weights(ctx, "q8_0", g, ff * h // 32, 100 + 2 * r)
+        d.synth_weights(ctx, "q8_0", u, ff * h // 32, 101 + 2 * r)
+        mats.append((g, u))
+    x = ctx.new_buffer(4 * h)
+    gamma = ctx.new_buffer(4 * h)
+    act = ctx.new_buffer(4 * ff)
+    d.synth_normal_f32(ctx, x, h, 5)
+    d.synth_normal_f32(ctx, gamma, h, 6, 1.0, 0.02)
+    ctx.flush()
+    for g, u in mats:
+        d.rms_norm_fused_ffn_q8_0_f32(ctx, g, u, x, gamma, cfg.eps, act, ff, h)
+    ctx.flush()
+    copy_bytes = 256 << 20
+    src, dst = ctx.new_buffer(copy_bytes), ctx.new_buffer(copy_bytes)
+    for _ in range(3):
+        d.stream_copy(ctx, dst, src, copy_bytes)
+    ctx.flush()
+    log(f"profile pass: {launches} x k_ffn_q8_0 ({2 * wb} weight bytes each), "
+        f"3 x k_stream_copy ({copy_bytes} bytes each)")
+    for b in (src, dst, x, gamma, act):
+        b.free()
+    arena.free()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -294,12 +344,18 @@ def main():
     ap.add_argument("--suite", default="all", choices=["all", "gemv", "quick", "decode"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run only GEMV workloads whose label contains this")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="eager launches of the dominant kernel + a calibration copy, for "
+                         "rocprofv3 --pmc runs; prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         sys.exit("bench.py measures one GPU only: this build has no multi-GPU path "
-                 "(see DESIGN.md on how the path would shard); run with --gpus 1")
+                 "(how the path would shard is a design note, not code); run with --gpus 1")
 
     ctx = d.HipContext()
+    if args.profile_pass:
+        profile_pass(ctx)
+        return
     line = {
         "metric": "quant GEMV HBM GB/s (% of peak) + decode tok/s, 0.5B Q8_0 & 7B Q4_K",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
@@ -329,7 +385,8 @@ def main():
                        "global_batch": 1, "kv_len": 512},
             "roofline": {"bound": "hbm", "kernel": "k_ffn_q8_0 (rms_norm + gate/up + SiLU)",
                          "achieved": round(ffn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(ffn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "frac": round(ffn_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("ffn_q8_0_0p5b_pmc_traffic.md"),
                          "bytes_per_launch": dec["ffn_bytes"],
                          "avg_launch_us": round(dec["ffn_us"], 3)},
             "decode": {"tok_s": round(tok_s, 2), "us_per_token": round(ms * 1e3, 1),
