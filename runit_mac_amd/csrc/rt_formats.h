@@ -146,12 +146,14 @@ struct FmtQ8_0 {
 struct FmtQ8_0S {
     static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 34, UNIT_EL = 32;
     static constexpr bool Q40PERM = false;
-    struct Raw { uint32_t w[10]; uint32_t sh; };
+    // 9 aligned dwords from the block's floor cover its 34 bytes at either
+    // 2-byte offset and never lie wholly past the block
+    struct Raw { uint32_t w[9]; uint32_t sh; };
     struct XU { XRegs x; };
     RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
         const uintptr_t p = (uintptr_t)(row + (size_t)u * 34);
         r.sh = (uint32_t)(p & 3);
-        load_dwords<10>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
+        load_dwords<9>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
     }
     RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) { load_xregs(recs + uu, xu.x); }
     RT_DEV static float dot(const Raw& r, const XU& xu) {
@@ -229,12 +231,14 @@ struct FmtQ4_0 {
 struct FmtQ4_0S {
     static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 18, UNIT_EL = 32;
     static constexpr bool Q40PERM = true;
-    struct Raw { uint32_t w[6]; uint32_t sh; };
+    // 5 aligned dwords from the block's floor cover its 18 bytes at either
+    // 2-byte offset and never lie wholly past the block
+    struct Raw { uint32_t w[5]; uint32_t sh; };
     struct XU { XRegs x; };
     RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
         const uintptr_t p = (uintptr_t)(row + (size_t)u * 18);
         r.sh = (uint32_t)(p & 3);
-        load_dwords<6>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
+        load_dwords<5>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
     }
     RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) { load_xregs(recs + uu, xu.x); }
     RT_DEV static float dot(const Raw& r, const XU& xu) {
@@ -357,7 +361,14 @@ struct FmtQ6K {
         const uintptr_t ps = (uintptr_t)(p + 192 + h / 16);
         const uint32_t sh = (uint32_t)(ps & 3);
         uint32_t w[5];
-        load_dwords<5>((const uint8_t*)(ps & ~(uintptr_t)3), w);
+        // dwords past the block's last byte (never used) re-read its last
+        // dword instead, so the window stays inside the weights
+        const uintptr_t wl = (uintptr_t)(p + 209) & ~(uintptr_t)3;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const uintptr_t a = (ps & ~(uintptr_t)3) + 4 * i;
+            w[i] = *(const uint32_t*)(a <= wl ? a : wl);
+        }
         r.sc01 = alignb(w[1], w[0], sh);  // bytes 0..3: sc[is+0], (odd), sc[is+2], (odd)
         r.sc23 = alignb(w[2], w[1], sh);  // bytes 4..7: sc[is+4], (odd), sc[is+6], (odd)
         // d sits 16 (h = 0) or 8 (h = 128) bytes after the scale window start
