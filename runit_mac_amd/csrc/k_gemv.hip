@@ -28,7 +28,26 @@ struct GemvArgs {
     float eps;
     uint32_t xb_chunk;   // activation records staged per LDS pass (multiple of 8)
     uint64_t row_bytes;
+    // matrix-core path, K split over workgroups: chunk ks of kc_units units
+    // goes to workgroups ≡ ks (mod ksplit); partial sums meet in `part`
+    uint32_t ksplit;     // 1: whole K per workgroup
+    uint32_t kc_units;
+    float* part;         // [ksplit][nvrows]
+    uint32_t* counters;  // [tiles] arrival counters (reset by the last arriver)
 };
+
+// Tiles one workgroup may own in a K-split launch (the host keeps the grid's
+// rounds below this).
+constexpr uint32_t kMaxSplitTiles = 256;
+
+// Items (weight loads of one step) in flight per wave in the matrix-core
+// body, for one and two row quads per wave.
+#ifndef GEMV_PF1
+#define GEMV_PF1 2
+#endif
+#ifndef GEMV_PF2
+#define GEMV_PF2 2
+#endif
 
 enum Epi : int {
     EPI_F32 = 0,      // y = v                     (f32 out)
@@ -336,30 +355,33 @@ RT_DEV void gemv_body_chunked(const GemvArgs& a) {
 // Each lane walks a flat sequence of (tile, step) items and issues the loads
 // of item n+1 before computing item n; the first item's loads are issued
 // before the activation staging.
-template <class F, int EPI, typename XT, int RQ>
+template <class F, int EPI, typename XT, int RQ, int PF>
 RT_DEV void gemv_mq_body(const GemvArgs& a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    XRec* xs = (XRec*)smem;
-    float* red = (float*)(smem + (size_t)(a.K / 32) * sizeof(XRec));  // [waves][RQ][4]
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
     const uint32_t q = lane & 3, slot = lane >> 2;
     const uint32_t lq = q < 3 ? q : 2;  // the A row of lane q = 3 is a don't-care
+    // K chunk of this workgroup (the whole K when ksplit = 1)
+    const uint32_t S = a.ksplit;
+    const uint32_t ks = blockIdx.x % S, wg = blockIdx.x / S, nwg = gridDim.x / S;
+    const uint32_t cu0 = ks * a.kc_units;  // first unit of the chunk
+    const uint32_t units = min(a.K / F::UNIT_EL - cu0, a.kc_units);
+    XRec* xs = (XRec*)smem;  // the chunk's records
+    float* red = (float*)(smem + (size_t)(a.kc_units * F::UNIT_EL / 32) * sizeof(XRec));
     // ksw waves share one group of RQ row quads and split its K steps
     const uint32_t ksw = a.ksw;
     const uint32_t wgrp = wave / ksw, wk = wave % ksw;
     const uint32_t vrows_per_wg = (nwaves / ksw) * 4 * RQ;
     const uint32_t ntiles = (a.nvrows + vrows_per_wg - 1) / vrows_per_wg;
-    const uint32_t units = a.K / F::UNIT_EL;
     const uint32_t nsteps = (units + 15) / 16;
     const uint32_t spw = (nsteps + ksw - 1) / ksw;  // steps per wave per tile
-    const uint32_t my_tiles =
-        blockIdx.x < ntiles ? (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    const uint32_t my_tiles = wg < ntiles ? (ntiles - wg + nwg - 1) / nwg : 0;
     const uint32_t nitems = my_tiles * spw;
 
-    typename F::Raw buf[2][RQ];
+    typename F::Raw buf[PF][RQ];  // PF items in flight per wave
     auto issue = [&](uint32_t item, typename F::Raw (&dst)[RQ]) {
-        const uint32_t tile = blockIdx.x + (item / spw) * gridDim.x;
+        const uint32_t tile = wg + (item / spw) * nwg;
         const uint32_t step = wk + ksw * (item % spw);
         uint32_t u = slot + 16 * step;
         if (u >= units) u = 0;  // clamped: loads stay in bounds, result is discarded
@@ -369,7 +391,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
             if (vr >= a.nvrows) vr = a.nvrows - 1;
             uint32_t mat, r;
             vrow_map<EPI>(a, vr, mat, r);
-            F::load(mat_w(a, mat) + (size_t)r * a.row_bytes, u, dst[rq]);
+            F::load(mat_w(a, mat) + (size_t)r * a.row_bytes, cu0 + u, dst[rq]);
         }
     };
 
@@ -380,7 +402,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     // would make the compiler's wait for the x loads a wait for all loads)
     auto load_tile_aux = [&](uint32_t item) {
         if (has_aux<EPI>()) {
-            const uint32_t tile = blockIdx.x + (item / spw) * gridDim.x;
+            const uint32_t tile = wg + (item / spw) * nwg;
 #pragma unroll
             for (int rq = 0; rq < RQ; ++rq) {
                 const uint32_t vr = tile * vrows_per_wg + wgrp * 4 * RQ + 4 * rq + q;
@@ -400,15 +422,17 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
 #else
 #define RT_TP(i)
 #endif
-    const uint32_t nxb = a.K / 32;
+    const uint32_t nxb = units * F::UNIT_EL / 32, xb0 = cu0 * F::UNIT_EL / 32;
     const bool one_pass = !a.x_rec && stage_one_pass(nxb);
     XPre xp;
 #ifndef RT_PROBE_NO_STAGE
-    if (one_pass) stage_x_load<XT>((const XT*)a.x, a.gamma, nxb, xp);
+    if (one_pass)
+        stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32, a.gamma ? a.gamma + (size_t)xb0 * 32 : nullptr,
+                         nxb, xp);
 #endif
     load_tile_aux(0);
-    issue(0, buf[0]);  // items past nitems load clamped addresses
-    issue(1, buf[1]);
+#pragma unroll
+    for (int h = 0; h < PF; ++h) issue(h, buf[h]);  // items past nitems load clamped addresses
     RT_TP(1);
 #ifndef RT_PROBE_NO_STAGE
     // (the host launches whole-K kernels either with x records or with a K
@@ -416,16 +440,16 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     if (one_pass)
         stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
     else
-        copy_x_limbs((const XRec*)a.x, 0, nxb, xs);
+        copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
 #endif
     RT_TP(2);
     __syncthreads();
     RT_TP(3);
     if (nitems == 0) return;
 
-    for (uint32_t it = 0; it < nitems; it += 2) {
+    for (uint32_t it = 0; it < nitems; it += PF) {
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
+        for (int half = 0; half < PF; ++half) {
             const uint32_t item = it + half;
             if (item < nitems) {  // uniform across the workgroup
                 if (item > 0 && item % spw == 0) load_tile_aux(item);
@@ -435,12 +459,21 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                 const uint32_t uc = valid ? u : 0;
 #pragma unroll
                 for (int rq = 0; rq < RQ; ++rq) {
+#ifdef RT_PROBE_MQ_NODOT
+                    // probe: consume the raw registers without the dot
+                    uint32_t fold = 0;
+                    const uint32_t* rw = (const uint32_t*)&buf[half][rq];
+#pragma unroll
+                    for (uint32_t i = 0; i < sizeof(typename F::Raw) / 4; ++i) fold ^= rw[i];
+                    const float v = (float)(fold & 0xFFFF);
+#else
                     const float v = F::mdot(buf[half][rq], xs, uc, lq);
+#endif
                     acc[rq] += valid ? v : 0.0f;
                 }
-                if (item + 2 < nitems) issue(item + 2, buf[half]);
+                if (item + PF < nitems) issue(item + PF, buf[half]);
                 if (item % spw == spw - 1) {
-                    const uint32_t tile = blockIdx.x + (item / spw) * gridDim.x;
+                    const uint32_t tile = wg + (item / spw) * nwg;
                     const uint32_t vbase = tile * vrows_per_wg + wgrp * 4 * RQ;
                     float rsum[RQ];
 #pragma unroll
@@ -472,7 +505,17 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                         }
                         __syncthreads();
                     }
-                    if (wk == 0) {
+                    if (S > 1) {
+                        // partial sums of this K chunk (the tiles are
+                        // finished after the loop)
+                        if (wk == 0 && slot == 0) {
+#pragma unroll
+                            for (int rq = 0; rq < RQ; ++rq) {
+                                const uint32_t vr = vbase + 4 * rq + q;
+                                if (vr < a.nvrows) dev_store(a.part + (size_t)ks * a.nvrows + vr, rsum[rq]);
+                            }
+                        }
+                    } else if (wk == 0) {
 #pragma unroll
                         for (int rq = 0; rq < RQ; ++rq) {
                             const float v = rsum[rq];
@@ -489,6 +532,39 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                     }
                 }
             }
+        }
+    }
+    if (S > 1) {
+        // K split: count this workgroup's chunk in for all its tiles at once
+        // (the arrivals' latencies overlap); the last chunk to arrive at a
+        // tile adds the chunks in order and runs the epilogue
+        __shared__ uint8_t last_of[kMaxSplitTiles];
+        dev_stores_done();
+        __syncthreads();
+        for (uint32_t t = tid; t < my_tiles; t += blockDim.x)
+            last_of[t] = arrive(a.counters + wg + t * nwg) == S - 1;
+        __syncthreads();
+        for (uint32_t t = 0; t < my_tiles; ++t) {
+            if (!last_of[t]) continue;  // uniform
+            const uint32_t tile = wg + t * nwg;
+            const uint32_t vt = tile * vrows_per_wg;
+            const uint32_t step_r = EPI == EPI_FFN ? 2 : 1;
+            for (uint32_t i = tid * step_r; i < vrows_per_wg; i += blockDim.x * step_r) {
+                const uint32_t vr = vt + i;
+                if (vr >= a.nvrows) break;
+                float v = 0.0f, v1 = 0.0f;
+                for (uint32_t c = 0; c < S; ++c) {
+                    v += dev_load(a.part + (size_t)c * a.nvrows + vr);
+                    if (EPI == EPI_FFN && vr + 1 < a.nvrows)
+                        v1 += dev_load(a.part + (size_t)c * a.nvrows + vr + 1);
+                }
+                if (EPI == EPI_FFN) {
+                    if (vr + 1 < a.nvrows) ((float*)a.out[0])[vr >> 1] = silu_ref(v) * v1;
+                } else {
+                    store_row<EPI>(a, vr, v);
+                }
+            }
+            if (tid == 0) dev_store(a.counters + tile, 0u);  // ready for the next call
         }
     }
 #ifdef RT_PROBE_TIMING
@@ -513,23 +589,25 @@ RT_DEV void gemv_body(const GemvArgs& a) {
         gemv_body_chunked<F, EPI, XT, RPL, UNR>(a);
 }
 
-// MFMA kernels: whole-K launches use the matrix-core body, long-K launches
-// the chunked v_dot4 body.
-template <class F, int EPI, typename XT, int RQ, int RPL, int UNR>
+// MFMA kernels: whole-K (or K-split) launches use the matrix-core body with
+// unit format FM; launches whose K exceeds the LDS budget without a split use
+// the chunked v_dot4 body with unit format FC.
+template <class FM, class FC, int EPI, typename XT, int RQ, int RPL, int UNR>
 RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
     if (a.xb_chunk >= a.K / 32)
-        gemv_mq_body<F, EPI, XT, RQ>(a);
+        gemv_mq_body<FM, EPI, XT, RQ, (RQ == 1 ? GEMV_PF1 : GEMV_PF2)>(a);
     else
-        gemv_body_chunked<F, EPI, XT, RPL, UNR>(a);
+        gemv_body_chunked<FC, EPI, XT, RPL, UNR>(a);
 }
 
-#define RT_GEMV_KERNEL(NAME, FMT, EPI, XT, UNR)                                   \
-    extern "C" __global__ void __launch_bounds__(512) NAME##_r1(GemvArgs a) {   \
-        gemv_mq_or_chunked<FMT, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);   \
-    }                                                                             \
-    extern "C" __global__ void __launch_bounds__(512) NAME##_r2(GemvArgs a) {   \
-        gemv_mq_or_chunked<FMT, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);   \
+#define RT_GEMV_KERNEL2(NAME, FMTM, FMTC, EPI, XT, UNR)                                 \
+    extern "C" __global__ void __launch_bounds__(512) NAME##_r1(GemvArgs a) {         \
+        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);  \
+    }                                                                                   \
+    extern "C" __global__ void __launch_bounds__(512) NAME##_r2(GemvArgs a) {         \
+        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);  \
     }
+#define RT_GEMV_KERNEL(NAME, FMT, EPI, XT, UNR) RT_GEMV_KERNEL2(NAME, FMT, FMT, EPI, XT, UNR)
 
 // Single-block-unit fallback (rows with an odd number of 32-element blocks)
 #define RT_GEMV_KERNEL_S(NAME, FMT, EPI, XT, UNR)                                 \
@@ -579,9 +657,10 @@ RT_GEMV_KERNEL(k_gemv_q4k_f16_f16add, FmtQ4K, EPI_F16_ADD, uint16_t, 1)
 RT_GEMV_KERNEL(k_gemv_q4k_f16_f32add, FmtQ4K, EPI_F32_ADD, uint16_t, 1)
 RT_GEMV_KERNEL(k_ffn_q4k, FmtQ4K, EPI_FFN, float, 1)
 // Q6_K (new: the reference runs Q6_K through f16-dequantised weights)
-RT_GEMV_KERNEL(k_gemv_q6k_f32_f32, FmtQ6K, EPI_F32, float, 1)
-RT_GEMV_KERNEL(k_gemv_q6k_f32_f32add, FmtQ6K, EPI_F32_ADD, float, 1)
-RT_GEMV_KERNEL(k_gemv_q6k_f32_f16, FmtQ6K, EPI_F16, float, 1)
+// (matrix-core path: one super-block per lane; chunked path: 64-element units)
+RT_GEMV_KERNEL2(k_gemv_q6k_f32_f32, FmtQ6KB, FmtQ6K, EPI_F32, float, 1)
+RT_GEMV_KERNEL2(k_gemv_q6k_f32_f32add, FmtQ6KB, FmtQ6K, EPI_F32_ADD, float, 1)
+RT_GEMV_KERNEL2(k_gemv_q6k_f32_f16, FmtQ6KB, FmtQ6K, EPI_F16, float, 1)
 
 // Activation pre-pass: builds the limb records of x (nxb records) in global
 // memory once, for launches whose K is too long to convert per workgroup.

@@ -460,3 +460,71 @@ struct FmtQ6K {
         return acc;
     }
 };
+
+// Q6_K for the matrix-core path: one whole 210-byte super-block (256
+// elements) per lane, loaded as 53 aligned dwords (13 dwordx4 + 1) from the
+// block's 4-byte floor.  The block starts 0 or 2 bytes past that floor (sh);
+// every field read below sits at a 4-byte multiple of the block start, so a
+// single alignbyte by sh rebuilds it.  Reference layout (forward.rs:921-950):
+// for half h ∈ {0, 128} and l ∈ 0..31, element h + 32t + l (t = 0..3) is
+//   ((ql[h/2 + l + 32·(t&1)] >> 4·(t>>1)) & 15) | (((qh[h/4 + l] >> 2t) & 3) << 4),
+// minus 32, times d · int8(sc[h/16 + 2t]) — one scale per 32-element record.
+struct FmtQ6KB {
+    static constexpr uint32_t BLK_EL = 256, BLK_BYTES = 210, UNIT_EL = 256;
+    static constexpr bool Q40PERM = false;
+    struct Raw { uint32_t w[53]; uint32_t sh; };
+    RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
+        const uintptr_t p = (uintptr_t)(row + (size_t)u * 210);
+        r.sh = (uint32_t)(p & 3);
+        load_dwords<53>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
+    }
+    // bytes [off, off+4) of the block, off a multiple of 4 below 208 (a
+    // constant once the callers' loops are unrolled)
+    RT_DEV static uint32_t get(const Raw& r, uint32_t off) {
+        return alignb(r.w[off / 4 + 1], r.w[off / 4], r.sh);
+    }
+    RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
+        const float d = h2f(r.w[52] >> (8 * r.sh));  // bytes 208-209
+        float acc = 0.0f;
+#pragma unroll 1
+        for (int hs = 0; hs < 2; ++hs) {  // (rolled: one half's limbs live at a time)
+            const XRec* rec = xs + 8 * uu + 4 * hs;
+            v4i c[4];
+            uint32_t xl[4][8];
+            int e[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const u32x4* p = (const u32x4*)(rec + t);
+                const u32x4 a = p[2 * lq], b = p[2 * lq + 1], m = p[6];
+                xl[t][0] = a.x; xl[t][1] = a.y; xl[t][2] = a.z; xl[t][3] = a.w;
+                xl[t][4] = b.x; xl[t][5] = b.y; xl[t][6] = b.z; xl[t][7] = b.w;
+                e[t] = (int)(int16_t)(m.x & 0xFFFF);
+                // codes are 0..63; −32·Σx over the record seeds the accumulators
+                const int s0 = (int16_t)(m.x >> 16) + (int16_t)(m.z & 0xFFFF);
+                const int s1 = (int16_t)(m.y & 0xFFFF) + (int16_t)(m.z >> 16);
+                const int s2 = (int16_t)(m.y >> 16) + (int16_t)(m.w & 0xFFFF);
+                c[t] = v4i{-32 * s0, -32 * s1, -32 * s2, 0};
+            }
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                // (both halves' offsets are constants; the rolled loop selects)
+                const uint32_t ql = hs ? get(r, 64 + 4 * g) : get(r, 4 * g);
+                const uint32_t ql32 = hs ? get(r, 96 + 4 * g) : get(r, 32 + 4 * g);
+                const uint32_t qh = hs ? get(r, 160 + 4 * g) : get(r, 128 + 4 * g);
+                c[0] = mfma4(xl[0][g], (ql & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u), c[0]);
+                c[1] = mfma4(xl[1][g], (ql32 & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u), c[1]);
+                c[2] = mfma4(xl[2][g], ((ql >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u), c[2]);
+                c[3] = mfma4(xl[3][g], ((ql32 >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u), c[3]);
+            }
+            // scales sc[8·hs + 2t]: bytes 192 + 8·hs + {0, 2, 4, 6}
+            const uint32_t sa = hs ? get(r, 200) : get(r, 192);
+            const uint32_t sb = hs ? get(r, 204) : get(r, 196);
+            const int sc[4] = {(int8_t)(sa & 255u), (int8_t)((sa >> 16) & 255u),
+                               (int8_t)(sb & 255u), (int8_t)((sb >> 16) & 255u)};
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                acc += __builtin_amdgcn_ldexpf(d * (float)sc[t] * comb4(c[t]), e[t] - 22);
+        }
+        return acc;
+    }
+};

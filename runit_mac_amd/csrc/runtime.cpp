@@ -37,12 +37,18 @@ struct GemvArgs {
     float eps;
     uint32_t xb_chunk;
     uint64_t row_bytes;
+    uint32_t ksplit;
+    uint32_t kc_units;
+    float* part;
+    uint32_t* counters;
 };
 
 constexpr uint32_t XREC_BYTES = 112;  // one activation record per 32 elements
 // argmax: 256 workgroup states of 12 bytes, then the arrival counter
 constexpr uint32_t kArgmaxWgs = 256;
 constexpr uint32_t kOnePassMaxK = 8192;  // 512 threads × 4 slices × 4 elements
+constexpr uint32_t kKSplitElems = 4096;  // K chunk of a split matrix-core launch
+constexpr uint32_t kMaxSplitTiles = 256;  // tiles per workgroup of a split launch (kernel LDS)
 constexpr size_t kAuxCounterOff = 4096;
 constexpr size_t kAuxAttnOff = 8192;  // attention arrival counters
 constexpr size_t kAuxBytes = 65536;
@@ -97,10 +103,12 @@ const char* const kKernelNames[] = {
 };
 
 struct Fmt {
-    uint32_t blk_el, blk_bytes, unit_el;
+    uint32_t blk_el, blk_bytes, unit_el;  // unit_el: elements per lane unit (v_dot4 path)
     uint32_t unroll;  // UNR template constant of the format's kernels
     const char* name;
     const Fmt* single;  // single-block-unit fallback for odd block counts
+    uint32_t mq_unit_el = 0;  // matrix-core path unit, if it differs from unit_el
+    uint32_t mq_units() const { return mq_unit_el ? mq_unit_el : unit_el; }
 };
 // Q8_0 / Q4_0 kernels take two blocks per unit (4-byte-aligned loads); rows
 // with an odd number of blocks use the one-block "_s1" kernels.
@@ -109,7 +117,7 @@ constexpr Fmt kQ4_0S{32, 18, 32, 4, "Q4_0", nullptr};
 constexpr Fmt kQ8_0{32, 34, 64, 1, "Q8_0", &kQ8_0S};
 constexpr Fmt kQ4_0{32, 18, 64, 2, "Q4_0", &kQ4_0S};
 constexpr Fmt kQ4K{256, 144, 64, 1, "Q4_K", nullptr};
-constexpr Fmt kQ6K{256, 210, 64, 1, "Q6_K", nullptr};
+constexpr Fmt kQ6K{256, 210, 64, 1, "Q6_K", nullptr, 256};  // matrix-core: one block per lane
 
 thread_local std::string g_global_error = "no error";
 
@@ -134,10 +142,14 @@ struct rt_ctx {
     uint32_t grid_per_cu = 0;  // RUNIT_GEMV_GRID_PER_CU: persistent-grid cap (sweeps only)
     uint32_t ksw_override = 0;  // RUNIT_GEMV_KSW: K-split waves (sweeps only)
     bool gemm_direct = false;   // RUNIT_GEMM_DIRECT: force the unstaged GEMM kernel (tests)
+    bool ksplit_enabled = true; // RUNIT_GEMV_KSPLIT=0: long K via the pre-pass instead (tests)
     // Workspace for activation records built by the long-K pre-pass; grows on
     // demand (stream-ordered, so one buffer serves every launch).
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    std::unordered_map<std::string, uint32_t> occ;  // occupancy cache
+    void* part = nullptr;  // K-split GEMV partial sums
+    size_t part_bytes = 0;
     uint32_t prepass_k = 8192;  // RUNIT_PREPASS_K: K from which x is converted once
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
@@ -186,6 +198,23 @@ int launch(rt_ctx* c, const char* name, dim3 grid, dim3 block, size_t lds, void*
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Resident workgroups per CU of a kernel at a block size and dynamic LDS
+// size (cached per context).
+uint32_t occupancy(rt_ctx* c, const char* name, uint32_t threads, size_t lds) {
+    const std::string key = std::string(name) + "/" + std::to_string(threads) + "/" +
+                            std::to_string(lds);
+    auto hit = c->occ.find(key);
+    if (hit != c->occ.end()) return hit->second;
+    auto it = c->fns.find(name);
+    int n = 0;
+    if (it == c->fns.end() ||
+        hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, it->second, (int)threads, lds) !=
+            hipSuccess || n < 1)
+        n = 1;
+    c->occ[key] = (uint32_t)n;
+    return (uint32_t)n;
+}
+
 // Launch plan for one GEMV-family call.
 //   T   threads per workgroup (256, or 512 when K is long so the activation
 //       staging is shared by more lanes);
@@ -226,23 +255,33 @@ Plan plan_gemv(const rt_ctx* c, const Fmt& f, uint32_t nvrows, uint32_t K, bool 
     return p;
 }
 
-// Grows the context workspace to `need` bytes (not during graph capture).
-int ensure_ws(rt_ctx* c, size_t need, const char* who) {
-    if (need <= c->ws_bytes) return RT_OK;
+// Grows a context buffer to `need` bytes (not during graph capture).
+int ensure_buf(rt_ctx* c, void*& buf, size_t& bytes, size_t need, const char* who) {
+    if (need <= bytes) return RT_OK;
     if (c->capturing)
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: %s: workspace must be sized before graph capture", who);
-    if (c->ws) {
+    if (buf) {
         hipError_t e = hipStreamSynchronize(c->stream);
         if (e != hipSuccess) return hip_fail(c, e, "workspace sync");
-        (void)hipFree(c->ws);
-        c->ws = nullptr;
-        c->ws_bytes = 0;
+        (void)hipFree(buf);
+        buf = nullptr;
+        bytes = 0;
     }
-    hipError_t e = hipMalloc(&c->ws, need);
+    hipError_t e = hipMalloc(&buf, need);
     if (e != hipSuccess) return hip_fail(c, e, "workspace hipMalloc");
-    c->ws_bytes = need;
+    bytes = need;
     return RT_OK;
+}
+// The activation workspace (pre-pass records, normalised x, GEMM operands,
+// attention partials) ...
+int ensure_ws(rt_ctx* c, size_t need, const char* who) {
+    return ensure_buf(c, c->ws, c->ws_bytes, need, who);
+}
+// ... and, separately, the partial sums of K-split GEMVs, whose activations
+// may live in the workspace.
+int ensure_part(rt_ctx* c, size_t need, const char* who) {
+    return ensure_buf(c, c->part, c->part_bytes, need, who);
 }
 
 int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x_f16,
@@ -263,11 +302,22 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
                     x_f16 ? 8 : 16);
     a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
     const uint32_t nxb = a.K / 32;
-    // Whole-K matrix-core launches stage x in one pass of ≤ 4 slices of 4
-    // elements per thread (K ≤ 8192 at 512 threads); longer activations are
-    // converted once by the pre-pass.
     const bool mq_shape = !single;
-    if (!a.x_rec && !a.gamma && (a.K >= c->prepass_k || (mq_shape && a.K > kOnePassMaxK))) {
+    const uint32_t mq_el = f.mq_units();
+    const uint32_t units = a.K / mq_el;
+    // Matrix-core launches stage x in one pass of ≤ 4 slices of 4 elements
+    // per thread (K ≤ 8192 at 512 threads).  Longer K is split over
+    // workgroups in chunks of kKSplitElems, each staged in one pass; the
+    // partial sums meet in the workspace.
+    uint32_t S = 1, kcu = units;
+    if (mq_shape && c->ksplit_enabled && !a.x_rec && !a.gamma && a.K > kOnePassMaxK) {
+        kcu = kKSplitElems / mq_el;
+        S = (units + kcu - 1) / kcu;
+    }
+    a.ksplit = S;
+    a.kc_units = kcu;
+    if (S == 1 && !a.x_rec && !a.gamma &&
+        (a.K >= c->prepass_k || (mq_shape && a.K > kOnePassMaxK))) {
         // convert the activations once into the context workspace
         const size_t need = (size_t)nxb * XREC_BYTES;
         const int st0 = ensure_ws(c, need, kname);
@@ -287,33 +337,49 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
     }
     const size_t red_bytes = 8 * 2 * 4 * sizeof(float);  // [waves ≤ 8][rows ≤ 2][4]
     const size_t lds_cap = std::min<size_t>(c->max_lds, 80 * 1024) - red_bytes;
+    // records staged per workgroup: the K chunk (split), else all of K if it
+    // fits, else LDS-sized chunks (v_dot4 path)
+    const uint32_t recs = S > 1 ? kcu * mq_el / 32 : nxb;
     uint32_t chunk = (uint32_t)(lds_cap / XREC_BYTES) & ~7u;
-    if (chunk >= nxb) chunk = nxb;
-    a.xb_chunk = chunk;
+    if (chunk >= recs) chunk = recs;
+    const bool mq = mq_shape && chunk == recs;
+    a.xb_chunk = mq ? nxb : chunk;  // the kernel takes the matrix-core body when ≥ K/32
     const size_t lds = (size_t)chunk * XREC_BYTES + red_bytes;
     Plan p;
     uint32_t rows_per_wg;
     uint32_t resident;
-    if (chunk == nxb && !single) {
+    if (mq) {
         // Matrix-core path: a wave covers RQ quads of 4 rows, 16 lanes per
         // row; persistent grid of `gpc` workgroups per CU.
         p = Plan{256, 16, 1};
         if (c->plan_override.T) p = Plan{c->plan_override.T, 16, c->plan_override.rpl};
-        if (!a.x_rec && nxb * 8 > 4 * p.T) p.T = 512;  // one staging pass
+        if (!a.x_rec && recs * 8 > 4 * p.T) p.T = 512;  // one staging pass
         // split K over the waves of a workgroup while row-quad groups are
         // scarcer than the resident waves (latency-bound small problems)
         const uint32_t nwaves = p.T / 64;
         const uint32_t quads = (a.nvrows + 4 * p.rpl - 1) / (4 * p.rpl);
-        const uint32_t nsteps = (a.K / f.unit_el + 15) / 16;
+        const uint32_t nsteps = (kcu + 15) / 16;
         const uint32_t resident_waves = (uint32_t)c->cu_count * 16;
         uint32_t ksw = 1;
-        while (ksw < nwaves && quads * ksw < resident_waves && (nsteps + ksw * 2 - 1) / (ksw * 2) >= 1 &&
-               ksw * 2 <= nsteps)
-            ksw *= 2;
+        while (ksw < nwaves && quads * S * ksw < resident_waves && ksw * 2 <= nsteps) ksw *= 2;
         if (c->ksw_override) ksw = std::min<uint32_t>(c->ksw_override, nwaves);
         a.ksw = ksw;
         rows_per_wg = (nwaves / ksw) * 4 * p.rpl;
         resident = c->grid_per_cu ? c->grid_per_cu : 4;
+        // never more than the kernel's occupancy allows (registers / LDS)
+        char rn[96];
+        snprintf(rn, sizeof rn, "%s_r%u", kname, p.rpl);
+        resident = std::max<uint32_t>(1, std::min(resident, occupancy(c, rn, p.T, lds)));
+        if (S > 1) {
+            const uint32_t ntiles = (a.nvrows + rows_per_wg - 1) / rows_per_wg;
+            if (ntiles > kAttnCounters)
+                return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: %u row tiles exceed %u",
+                            kname, ntiles, kAttnCounters);
+            const int st = ensure_part(c, (size_t)S * a.nvrows * sizeof(float), kname);
+            if (st != RT_OK) return st;
+            a.part = (float*)c->part;
+            a.counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
+        }
     } else {
         // chunked (long-K) and single-block kernels: one row (FFN: one gate/up
         // pair) per row group
@@ -326,7 +392,18 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
     }
     a.lpr = p.TL;
     const uint32_t ntiles = (a.nvrows + rows_per_wg - 1) / rows_per_wg;
-    const uint32_t grid = std::min<uint32_t>(ntiles, (uint32_t)c->cu_count * resident);
+    // persistent grid with the same number of tiles per workgroup: the
+    // fewest rounds the resident capacity allows, spread evenly (a grid of
+    // `cap` with ntiles slightly above it would leave most workgroups idle
+    // while a few run a second tile)
+    // (with a K split, each of the S chunks gets the same number of
+    // workgroups, and the grid is a multiple of S)
+    const uint32_t cap = (uint32_t)c->cu_count * resident;
+    const uint32_t rounds = (ntiles * S + cap - 1) / cap;
+    const uint32_t grid = (ntiles + rounds - 1) / rounds * S;
+    if (S > 1 && rounds > kMaxSplitTiles)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: %u tiles per workgroup exceed %u",
+                    kname, rounds, kMaxSplitTiles);
     char name[96];
     if (single)
         snprintf(name, sizeof name, "%s_s1", kname);
@@ -446,6 +523,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_GRID_PER_CU")) c->grid_per_cu = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_PREPASS_K")) c->prepass_k = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_DIRECT")) c->gemm_direct = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSW")) {
         const int v = atoi(g);
         if (v == 1 || v == 2 || v == 4 || v == 8) c->ksw_override = (uint32_t)v;
@@ -496,6 +574,7 @@ void rt_ctx_destroy(rt_ctx* c) {
         hipStreamDestroy(c->stream);
     }
     if (c->ws) hipFree(c->ws);
+    if (c->part) hipFree(c->part);
     if (c->aux) hipFree(c->aux);
     if (c->module) hipModuleUnload(c->module);
     delete c;

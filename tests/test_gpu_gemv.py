@@ -201,3 +201,88 @@ def test_pipeline_lookup(ctx):
     ctx.has_kernel("k_gemv_q8_0_f32_f32_r1")
     with pytest.raises(d.PipelineNotFound):
         ctx.has_kernel("no_such_kernel")
+
+
+# ───────────── K split over workgroups (K > 8192, matrix-core path) ─────────────
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_gemv_k_split_all_variants_twice(ctx, fmt):
+    """K = 18944 (the 7B down projection's K) with few rows: the launch splits
+    K into 4096-element chunks whose partial sums meet in the workspace.  Each
+    variant runs twice (the arrival counters must be reset by the first)."""
+    n, k = 200, 18944
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=91)
+    for var in VARIANTS[fmt]:
+        for rep in range(2):
+            run_variant(ctx, fmt, var, wbuf, raw, n, k, seed=5 + rep)
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0"])
+def test_gemv_k_split_output_aliases_residual(ctx, fmt):
+    n, k = 300, 12288
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=92)
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal(k).astype(np.float32)
+    y0 = rng.standard_normal(n).astype(np.float32)
+    yb = ctx.buffer_from(y0)
+    getattr(d, f"gemv_{fmt}_add_f32_f32in")(ctx, wbuf, ctx.buffer_from(x), yb, yb, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    check_close(yb.read(np.float32, n), yref + y0, sabs, f"{fmt} split aliased")
+
+
+def test_fused_k_split_ffn_and_qkv(ctx):
+    from test_gpu_fused import ffn_check
+    ff, k = 150, 18944
+    wg, rg = device_weights(ctx, "q4_0", ff, k, seed=93)
+    wu, ru = device_weights(ctx, "q4_0", ff, k, seed=94)
+    x = np.random.default_rng(9).standard_normal(k).astype(np.float32)
+    act = ctx.new_buffer(4 * ff)
+    d.fused_ffn_q4_0_f32(ctx, wg, wu, ctx.buffer_from(x), act, ff, k)
+    ctx.flush()
+    gr, gs = ora.gemv("q4_0", rg, x, ff, k)
+    ur, us = ora.gemv("q4_0", ru, x, ff, k)
+    ffn_check(act.read(np.float32, ff), gr, gs, ur, us, "split ffn q4_0")
+    qd, kd = 64, 32
+    ws = [device_weights(ctx, "q8_0", n, k, seed=95 + i) for i, n in enumerate((qd, kd, kd))]
+    bias = [np.random.default_rng(10 + i).standard_normal(n).astype(np.float16) for i, n in
+            enumerate((qd, kd, kd))]
+    outs = [ctx.new_buffer(4 * n) for n in (qd, kd, kd)]
+    d.fused_qkv_bias_q8_0_f32(ctx, ws[0][0], ws[1][0], ws[2][0], ctx.buffer_from(x), *outs,
+                              *[ctx.buffer_from(b) for b in bias], qd, kd, k)
+    ctx.flush()
+    for i, n in enumerate((qd, kd, kd)):
+        y, s = ora.gemv("q8_0", ws[i][1], x, n, k)
+        check_close(outs[i].read(np.float32, n), y + bias[i].astype(np.float64), s, f"split qkv {i}")
+
+
+def test_norm_then_gemv_long_k(ctx):
+    """RMSNorm into the workspace, then a K-split GEMV (partials kept apart)."""
+    n, k = 120, 16384
+    rng = np.random.default_rng(11)
+    x = (2 * rng.standard_normal(k)).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(k)).astype(np.float32)
+    xn = ora.rms_norm(x, g, 1e-6).astype(np.float32)
+    wbuf, raw = device_weights(ctx, "q8_0", n, k, seed=96)
+    y = ctx.new_buffer(4 * n)
+    d.rms_norm_gemv_q8_0_f32in_f32out(ctx, wbuf, ctx.buffer_from(x), ctx.buffer_from(g), 1e-6, y,
+                                      n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv("q8_0", raw, xn, n, k)
+    check_close(y.read(np.float32, n), yref, sabs, "norm then split gemv", F32_EPS * np.abs(yref))
+
+
+def test_long_k_prepass_path_without_split():
+    """The pre-pass + whole-K path (RUNIT_GEMV_KSPLIT=0) stays correct."""
+    import os
+    os.environ["RUNIT_GEMV_KSPLIT"] = "0"
+    try:
+        c2 = d.HipContext()
+    finally:
+        del os.environ["RUNIT_GEMV_KSPLIT"]
+    try:
+        for fmt in FMTS:
+            wbuf, raw = device_weights(c2, fmt, 96, 18944, seed=97)
+            run_variant(c2, fmt, "f32in_f32out", wbuf, raw, 96, 18944, seed=12)
+    finally:
+        c2.close()
