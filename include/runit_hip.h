@@ -44,7 +44,16 @@ typedef enum rt_status {
     RT_ERR_PIPELINE_NOT_FOUND = 3, /* KernelError::PipelineNotFound(name) */
     RT_ERR_PIPELINE_CREATE = 4,    /* KernelError::PipelineCreate { name, reason } */
     RT_ERR_DISPATCH = 5,           /* KernelError::Dispatch(msg) */
-    RT_ERR_BUFFER_SIZE = 6         /* KernelError::BufferSize { expected, actual } */
+    RT_ERR_BUFFER_SIZE = 6,        /* KernelError::BufferSize { expected, actual } */
+    /* GgufError variants (crates/gguf/src/error.rs:4-31), rt_gguf_* only */
+    RT_ERR_GGUF_IO = 16,             /* GgufError::Io */
+    RT_ERR_GGUF_MAGIC = 17,          /* GgufError::InvalidMagic */
+    RT_ERR_GGUF_VERSION = 18,        /* GgufError::UnsupportedVersion */
+    RT_ERR_GGUF_DTYPE = 19,          /* GgufError::UnknownDtype */
+    RT_ERR_GGUF_METADATA_TYPE = 20,  /* GgufError::UnknownMetadataType */
+    RT_ERR_GGUF_EOF = 21,            /* GgufError::UnexpectedEof */
+    RT_ERR_GGUF_UTF8 = 22,           /* GgufError::InvalidUtf8 */
+    RT_ERR_GGUF_DATA_OVERFLOW = 23   /* GgufError::DataRegionOverflow */
 } rt_status;
 
 typedef struct rt_ctx rt_ctx;
@@ -291,6 +300,43 @@ int rt_rms_norm_gemv_q8_0_f32in_f32out(rt_ctx* ctx, const void* weight, const fl
 int rt_stream_read(rt_ctx* ctx, const void* src, size_t bytes, uint32_t* sink,
                    size_t sink_dwords);
 int rt_stream_copy(rt_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* ───────────────────────── GGUF files ───────────────────────── */
+/* The wire format in front of the path: crates/gguf (parser.rs:22-57,
+ * types.rs:142-198) plus the engine's mmap loader (crates/engine/src/
+ * loader.rs:124-218).  rt_gguf_open parses header, metadata and tensor
+ * table of a GGUF v2/v3 file and maps it read-only; errors are the GgufError
+ * variants above, with the message in rt_gguf_last_error().  Metadata value
+ * types: 0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool, 8 string,
+ * 9 array, 10 u64, 11 i64, 12 f64.  Tensor dtypes are GgufDtype ids. */
+typedef struct rt_gguf rt_gguf;
+int rt_gguf_open(const char* path, rt_gguf** out);
+void rt_gguf_close(rt_gguf* g);
+const char* rt_gguf_last_error(void);
+uint32_t rt_gguf_version(const rt_gguf* g);
+uint64_t rt_gguf_alignment(const rt_gguf* g);
+/* absolute file offset of the (aligned) tensor data region */
+uint64_t rt_gguf_data_offset(const rt_gguf* g);
+uint64_t rt_gguf_tensor_count(const rt_gguf* g);
+/* index of a tensor by name, -1 if absent */
+int64_t rt_gguf_find_tensor(const rt_gguf* g, const char* name);
+/* name, shape (up to 8 dims), dtype, offset within the data region, bytes */
+int rt_gguf_tensor_info(const rt_gguf* g, uint64_t i, const char** name, uint32_t* n_dims,
+                        uint64_t dims[8], uint32_t* dtype, uint64_t* offset, uint64_t* bytes);
+/* host pointer to the tensor's bytes inside the mapping */
+const void* rt_gguf_tensor_data(const rt_gguf* g, uint64_t i);
+/* copies the tensor's bytes to device memory (dst_dev holds ≥ bytes) */
+int rt_gguf_upload(rt_ctx* ctx, const rt_gguf* g, uint64_t i, void* dst_dev);
+uint64_t rt_gguf_meta_count(const rt_gguf* g);
+int64_t rt_gguf_find_meta(const rt_gguf* g, const char* key);
+int rt_gguf_meta_info(const rt_gguf* g, uint64_t i, const char** key, uint32_t* type,
+                      uint32_t* elem_type, uint64_t* count);
+int rt_gguf_meta_int(const rt_gguf* g, uint64_t i, int64_t* out);
+int rt_gguf_meta_float(const rt_gguf* g, uint64_t i, double* out);
+const char* rt_gguf_meta_string(const rt_gguf* g, uint64_t i);
+int rt_gguf_meta_array_numbers(const rt_gguf* g, uint64_t i, double* out, uint64_t max);
+int rt_gguf_meta_array_string(const rt_gguf* g, uint64_t i, uint64_t k, const char** s,
+                              uint64_t* len);
 
 #ifdef __cplusplus
 }

@@ -59,7 +59,7 @@ def build_host() -> str:
     _run([
         "g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-unused-result",
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
-        os.path.join(CSRC, "runtime.cpp"), "-o", tmp,
+        os.path.join(CSRC, "runtime.cpp"), os.path.join(CSRC, "gguf.cpp"), "-o", tmp,
         f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl",
     ])
     os.replace(tmp, HOST_LIB)

@@ -81,7 +81,13 @@ class Arena:
 class DecodeModel:
     """Synthetic Qwen2-shape model resident in one arena, plus the KV cache."""
 
-    def __init__(self, ctx: d.HipContext, cfg: DecodeConfig = DecodeConfig(), seed: int = 7):
+    def __init__(self, ctx: d.HipContext, cfg: DecodeConfig = DecodeConfig(), seed: int = 7,
+                 gguf=None):
+        """Synthetic weights, or (gguf: a runit_mac_amd.gguf.GgufFile) the
+        file's tensors: Q8_0 matrices as stored, f32 norms, f32/f16 biases
+        converted to f16 (RNE, as upload_weight converts F32, forward.rs:
+        442-455), an absent bias as zeros, the LM head tied to token_embd when
+        output.weight is absent (forward.rs:1271-1276), and an empty KV cache."""
         self.ctx, self.cfg = ctx, cfg
         c = cfg
         h, q, kv, ff = c.hidden, c.q_dim, c.kv_dim, c.ff
@@ -89,43 +95,87 @@ class DecodeModel:
         per_layer = (wb(q, h) + 2 * wb(kv, h) + wb(h, q) + 2 * wb(ff, h) + wb(h, ff)
                      + 2 * (q + 2 * kv) + 8 * h + 2 * 4 * c.kv_heads * c.max_seq * c.head_dim
                      + 16 * 256)
-        total = c.layers * per_layer + wb(c.vocab, h) + 16 * h + 64 * 1024 + \
-            4 * (c.vocab + 8 * ff + 8 * q)
+        tied = gguf is None or "output.weight" not in gguf
+        total = c.layers * per_layer + wb(c.vocab, h) * (1 if tied else 2) + 16 * h + \
+            64 * 1024 + 4 * (c.vocab + 8 * ff + 8 * q)
         self.arena = Arena(ctx, total)
         a = self.arena
         s = seed * 1000
+        lib = d.load_library()
 
-        def qw(n, k):
+        def upload_host(p, arr):
+            arr = np.ascontiguousarray(arr)
+            ctx._check(lib.rt_upload(ctx.handle, p, arr.ctypes.data, arr.nbytes))
+
+        def tensor(name, n, k=None, dtypes=()):
+            t = gguf.tensor(name)
+            shape = (k, n) if k is not None else (n,)
+            if t.shape != shape or t.dtype_name not in dtypes:
+                raise ValueError(f"{name}: {t.dtype_name} {t.shape}, expected one of {dtypes} "
+                                 f"{shape}")
+            return t
+
+        def qw(n, k, name=None):
             nonlocal s
             p = a.take(wb(n, k))
-            d.synth_weights(ctx, "q8_0", p, n * k // 32, s)
-            s += 1
+            if gguf is not None:
+                tensor(name, n, k, ("Q8_0",))
+                gguf.upload(ctx, name, p)
+            else:
+                d.synth_weights(ctx, "q8_0", p, n * k // 32, s)
+                s += 1
             return p
 
-        def f32(n, mean, std):
+        def f32(n, mean, std, name=None):
             nonlocal s
             p = a.take(4 * n)
-            d.synth_normal_f32(ctx, p, n, s, mean, std)
-            s += 1
+            if gguf is not None and name is not None:
+                t = tensor(name, n, dtypes=("F32", "F16"))
+                raw = gguf.tensor_bytes(name)
+                v = raw.view(np.float32) if t.dtype_name == "F32" else \
+                    raw.view(np.float16).astype(np.float32)
+                upload_host(p, v)
+            elif gguf is not None:  # KV cache of a loaded model: empty
+                ctx._check(lib.rt_memset(ctx.handle, p, 0, 4 * n))
+            else:
+                d.synth_normal_f32(ctx, p, n, s, mean, std)
+                s += 1
             return p
 
-        def f16(n, std):
+        def f16(n, std, name=None):
             nonlocal s
             p = a.take(2 * n)
-            d.synth_normal_f16(ctx, p, n, s, 0.0, std)
-            s += 1
+            if gguf is not None:
+                if name in gguf:
+                    t = tensor(name, n, dtypes=("F32", "F16"))
+                    raw = gguf.tensor_bytes(name)
+                    v = raw.view(np.float16) if t.dtype_name == "F16" else \
+                        raw.view(np.float32).astype(np.float16)
+                else:
+                    v = np.zeros(n, np.float16)
+                upload_host(p, v)
+            else:
+                d.synth_normal_f16(ctx, p, n, s, 0.0, std)
+                s += 1
             return p
 
         self.layers = []
-        for _ in range(c.layers):
-            L = dict(wq=qw(q, h), wk=qw(kv, h), wv=qw(kv, h), bq=f16(q, 0.02), bk=f16(kv, 0.02),
-                     bv=f16(kv, 0.02), wo=qw(h, q), wg=qw(ff, h), wu=qw(ff, h), wd=qw(h, ff),
-                     attn_norm=f32(h, 1.0, 0.02), ffn_norm=f32(h, 1.0, 0.02),
+        for i in range(c.layers):
+            b = f"blk.{i}."
+            L = dict(wq=qw(q, h, b + "attn_q.weight"), wk=qw(kv, h, b + "attn_k.weight"),
+                     wv=qw(kv, h, b + "attn_v.weight"), bq=f16(q, 0.02, b + "attn_q.bias"),
+                     bk=f16(kv, 0.02, b + "attn_k.bias"), bv=f16(kv, 0.02, b + "attn_v.bias"),
+                     wo=qw(h, q, b + "attn_output.weight"), wg=qw(ff, h, b + "ffn_gate.weight"),
+                     wu=qw(ff, h, b + "ffn_up.weight"), wd=qw(h, ff, b + "ffn_down.weight"),
+                     attn_norm=f32(h, 1.0, 0.02, b + "attn_norm.weight"),
+                     ffn_norm=f32(h, 1.0, 0.02, b + "ffn_norm.weight"),
                      kc=f32(c.kv_heads * c.max_seq * c.head_dim, 0.0, 1.0),
                      vc=f32(c.kv_heads * c.max_seq * c.head_dim, 0.0, 1.0))
             self.layers.append(L)
-        self.final_norm = f32(h, 1.0, 0.02)
-        self.embd = qw(c.vocab, h)  # token_embd, tied LM head (forward.rs:1271-1276)
+        self.final_norm = f32(h, 1.0, 0.02, "output_norm.weight")
+        self.embd = qw(c.vocab, h, "token_embd.weight")
+        # LM head: tied to token_embd unless the file has output.weight
+        self.lm_head = self.embd if tied else qw(c.vocab, h, "output.weight")
         # activations
         self.x = a.take(4 * h)
         self.xn = a.take(4 * h)
@@ -137,6 +187,18 @@ class DecodeModel:
         self.logits = a.take(4 * c.vocab)
         self.token = a.take(256)
         ctx.flush()
+
+    @classmethod
+    def from_gguf(cls, ctx: d.HipContext, gguf, max_seq: int = 1024) -> "DecodeModel":
+        """A Qwen2-family model from a GGUF file (Q8_0 matrices), with the
+        dimensions of ModelConfig.from_metadata (config.rs:96-265)."""
+        from .gguf import ModelConfig
+        mc = ModelConfig.from_metadata(gguf.metadata, gguf.metadata_types)
+        cfg = DecodeConfig(layers=mc.num_hidden_layers, hidden=mc.hidden_size,
+                           heads=mc.num_attention_heads, kv_heads=mc.num_key_value_heads,
+                           head_dim=mc.head_dim, ff=mc.intermediate_size, vocab=mc.vocab_size,
+                           eps=mc.rms_norm_eps, theta=mc.rope_theta, max_seq=max_seq)
+        return cls(ctx, cfg, gguf=gguf)
 
     def set_token(self, tok: int) -> None:
         d.load_library().rt_upload(self.ctx.handle, self.token,
@@ -176,7 +238,7 @@ class DecodeModel:
             d.fused_ffn_q8_0_f32(ctx, L["wg"], L["wu"], self.xn, self.act, c.ff, h)
             d.gemv_q8_0_add_f32_f32in_mr(ctx, L["wd"], self.act, self.x, self.x, h, c.ff)
         d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, self.final_norm, c.eps, h, 1)
-        d.gemv_q8_0_f32in_f32out_mr(ctx, self.embd, self.xn, self.logits, c.vocab, h)
+        d.gemv_q8_0_f32in_f32out_mr(ctx, self.lm_head, self.xn, self.logits, c.vocab, h)
         d.argmax_f32(ctx, self.logits, self.token, c.vocab)
 
     def step_fused(self, pos: int) -> None:
@@ -194,7 +256,7 @@ class DecodeModel:
             d.rms_norm_fused_ffn_q8_0_f32(ctx, L["wg"], L["wu"], self.x, L["ffn_norm"], c.eps,
                                           self.act, c.ff, h)
             d.gemv_q8_0_add_f32_f32in(ctx, L["wd"], self.act, self.x, self.x, h, c.ff)
-        d.rms_norm_gemv_q8_0_f32in_f32out(ctx, self.embd, self.x, self.final_norm, c.eps,
+        d.rms_norm_gemv_q8_0_f32in_f32out(ctx, self.lm_head, self.x, self.final_norm, c.eps,
                                           self.logits, c.vocab, h)
         d.argmax_f32(ctx, self.logits, self.token, c.vocab)
 

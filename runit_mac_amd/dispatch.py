@@ -142,6 +142,35 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.rt_event_destroy.restype = None
     lib.rt_graph_destroy.argtypes = [_P]
     lib.rt_graph_destroy.restype = None
+    # GGUF reader: (name, argtypes, restype)
+    PU64 = POINTER(c_uint64)
+    for name, argtypes, restype in (
+            ("rt_gguf_open", [c_char_p, POINTER(c_void_p)], c_int),
+            ("rt_gguf_close", [_P], None),
+            ("rt_gguf_last_error", [], c_char_p),
+            ("rt_gguf_version", [_P], c_uint32),
+            ("rt_gguf_alignment", [_P], c_uint64),
+            ("rt_gguf_data_offset", [_P], c_uint64),
+            ("rt_gguf_tensor_count", [_P], c_uint64),
+            ("rt_gguf_find_tensor", [_P, c_char_p], ctypes.c_int64),
+            ("rt_gguf_tensor_info", [_P, c_uint64, POINTER(c_char_p), POINTER(c_uint32), PU64,
+                                     POINTER(c_uint32), PU64, PU64], c_int),
+            ("rt_gguf_tensor_data", [_P, c_uint64], c_void_p),
+            ("rt_gguf_upload", [_P, _P, c_uint64, _P], c_int),
+            ("rt_gguf_meta_count", [_P], c_uint64),
+            ("rt_gguf_find_meta", [_P, c_char_p], ctypes.c_int64),
+            ("rt_gguf_meta_info", [_P, c_uint64, POINTER(c_char_p), POINTER(c_uint32),
+                                   POINTER(c_uint32), PU64], c_int),
+            ("rt_gguf_meta_int", [_P, c_uint64, POINTER(ctypes.c_int64)], c_int),
+            ("rt_gguf_meta_float", [_P, c_uint64, POINTER(ctypes.c_double)], c_int),
+            ("rt_gguf_meta_string", [_P, c_uint64], c_char_p),
+            ("rt_gguf_meta_array_numbers", [_P, c_uint64, POINTER(ctypes.c_double), c_uint64],
+             c_int),
+            ("rt_gguf_meta_array_string", [_P, c_uint64, c_uint64, POINTER(c_void_p), PU64],
+             c_int)):
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
     _lib = lib
     return lib
 

@@ -44,7 +44,8 @@ def cpu_step(m: DecodeModel, tok: int, pos: int) -> np.ndarray:
         y, _ = ora.gemv("q8_0", rd8(L["wd"], h, c.ff), act.astype(np.float32), h, c.ff)
         x = x + y
     xn = ora.rms_norm(x.astype(np.float32), m.read(m.final_norm, h), c.eps)
-    logits, _ = ora.gemv("q8_0", emb, xn.astype(np.float32), c.vocab, h)
+    head = emb if m.lm_head == m.embd else rd8(m.lm_head, c.vocab, h)
+    logits, _ = ora.gemv("q8_0", head, xn.astype(np.float32), c.vocab, h)
     return logits
 
 
