@@ -181,6 +181,25 @@ int rt_gemv_q6k_add_f32_f32in(rt_ctx* ctx, const void* weight_q6k, const float* 
 int rt_gemv_q6k_f32in(rt_ctx* ctx, const void* weight_q6k, const float* input,
                       uint16_t* output, uint32_t m, uint32_t k);
 
+/* ───────────────────────── Q5_0 / Q5_K GEMV (new) ─────────────────────────
+ * The reference has no Q5 GEMVs: the loader dequantises Q5_0 (forward.rs:
+ * 900-920) and Q5_K (forward.rs:979-1012) on the CPU and runs the f16-weight
+ * GEMVs.  These read the packed 22-byte / 176-byte blocks directly, with the
+ * reference's decode (its Q5_K high-bit order: bit e%8 of qh[e/8] for
+ * element e).  Arguments as the Q4_K family. */
+int rt_gemv_q5_0_f32in_f32out(rt_ctx* ctx, const void* weight_q5_0, const float* input,
+                              float* output, uint32_t m, uint32_t k);
+int rt_gemv_q5_0_add_f32_f32in(rt_ctx* ctx, const void* weight_q5_0, const float* input,
+                               float* output, const float* residual, uint32_t m, uint32_t k);
+int rt_gemv_q5_0_f32in(rt_ctx* ctx, const void* weight_q5_0, const float* input,
+                       uint16_t* output, uint32_t m, uint32_t k);
+int rt_gemv_q5k_f32in_f32out(rt_ctx* ctx, const void* weight_q5k, const float* input,
+                             float* output, uint32_t m, uint32_t k);
+int rt_gemv_q5k_add_f32_f32in(rt_ctx* ctx, const void* weight_q5k, const float* input,
+                              float* output, const float* residual, uint32_t m, uint32_t k);
+int rt_gemv_q5k_f32in(rt_ctx* ctx, const void* weight_q5k, const float* input,
+                      uint16_t* output, uint32_t m, uint32_t k);
+
 /* ───────────────────────── fused kernels ───────────────────────── */
 
 /* dispatch.rs:813-838 → fused_qkv.metal:72-119 */
@@ -209,6 +228,23 @@ int rt_fused_ffn_q4_0_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
 int rt_fused_ffn_q4k_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
                          const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);
 
+/* New: Q5_0 / Q5_K twins of fused_qkv_bias_q8_0_f32 and fused_ffn_q8_0_f32
+ * (same arguments). */
+int rt_fused_qkv_bias_q5_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                               const float* x_vec, float* out_q, float* out_k, float* out_v,
+                               const uint16_t* bias_q, const uint16_t* bias_k,
+                               const uint16_t* bias_v, uint32_t q_dim, uint32_t kv_dim,
+                               uint32_t k);
+int rt_fused_qkv_bias_q5k_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                              const float* x_vec, float* out_q, float* out_k, float* out_v,
+                              const uint16_t* bias_q, const uint16_t* bias_k,
+                              const uint16_t* bias_v, uint32_t q_dim, uint32_t kv_dim,
+                              uint32_t k);
+int rt_fused_ffn_q5_0_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                          const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);
+int rt_fused_ffn_q5k_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                         const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);
+
 /* ───────────────────────── dequantisation ─────────────────────────
  * Bit-exact restatements of the reference decoders, to f32:
  *   Q8_0 forward.rs:951-963, Q4_0 :964-978, Q4_K :1026-1057 (+:359-369),
@@ -217,6 +253,9 @@ int rt_dequant_q8_0_f32(rt_ctx* ctx, const void* input, float* output, uint32_t 
 int rt_dequant_q4_0_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
 int rt_dequant_q4k_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
 int rt_dequant_q6k_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+/* New: Q5_0 forward.rs:900-920, Q5_K forward.rs:979-1012 (+:359-369). */
+int rt_dequant_q5_0_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+int rt_dequant_q5k_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
 /* dispatch.rs:756-772 → dequant.metal:53-98 (Q4_K → f16, RNE). */
 int rt_dequant_q4k_f16(rt_ctx* ctx, const void* input, uint16_t* output, uint32_t n_blocks);
 
@@ -248,6 +287,8 @@ int rt_synth_q8_0(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, floa
 int rt_synth_q4_0(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
 int rt_synth_q4k(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
 int rt_synth_q6k(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
+int rt_synth_q5_0(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
+int rt_synth_q5k(rt_ctx* ctx, void* out, uint64_t n_blocks, uint64_t seed, float std);
 
 /* ───────────────────────── decode-step glue ─────────────────────────
  * The non-GEMV kernels of one decode step (forward.rs:1523-1771). */

@@ -67,13 +67,17 @@ uint16_t ora_f2h(float f) {
 
 static float rd_h(const uint8_t* p) { return ora_h2f((uint16_t)(p[0] | (p[1] << 8))); }
 
-size_t ora_block_elems(int fmt) { return (fmt == ORA_Q4K || fmt == ORA_Q6K) ? 256 : 32; }
+size_t ora_block_elems(int fmt) {
+    return (fmt == ORA_Q4K || fmt == ORA_Q6K || fmt == ORA_Q5K) ? 256 : 32;
+}
 size_t ora_block_bytes(int fmt) {
     switch (fmt) {
         case ORA_Q8_0: return 34;
         case ORA_Q4_0: return 18;
         case ORA_Q4K: return 144;
         case ORA_Q6K: return 210;
+        case ORA_Q5_0: return 22;
+        case ORA_Q5K: return 176;
     }
     return 0;
 }
@@ -163,12 +167,63 @@ void ora_dequant_q6k(const uint8_t* in, size_t nblk, float* out) {
     }
 }
 
+/* forward.rs:900-920: d f16, qh[4], qs[16]; for j in 0..16:
+ * xh_0 = (qh[j/8] >> j%8) & 1, xh_1 = (qh[j/8+2] >> j%8) & 1,
+ * vals[j] = d·((qs[j]&15 | xh_0<<4) − 16), vals[j+16] = d·((qs[j]>>4 | xh_1<<4) − 16) */
+void ora_dequant_q5_0(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const uint8_t* blk = in + b * 22;
+        const float d = rd_h(blk);
+        const uint8_t* qh = blk + 2;
+        const uint8_t* qs = blk + 6;
+        for (int j = 0; j < 16; ++j) {
+            const int xh0 = (qh[j / 8] >> (j % 8)) & 1;
+            const int xh1 = (qh[j / 8 + 2] >> (j % 8)) & 1;
+            const int x0 = (qs[j] & 0x0F) | (xh0 << 4);
+            const int x1 = ((qs[j] >> 4) & 0x0F) | (xh1 << 4);
+            out[b * 32 + j] = d * (float)(x0 - 16);
+            out[b * 32 + j + 16] = d * (float)(x1 - 16);
+        }
+    }
+}
+
+/* forward.rs:979-1012: d, dmin f16, scales[12], qh[32], qs[128]; pair j
+ * uses (sc, m) j and j+4 (get_scale_min_k4); element e = 64j+l (+32) takes
+ * the low (high) nibble of qs[32j+l] and bit e%8 of qh[e/8] as bit 4. */
+void ora_dequant_q5k(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const uint8_t* blk = in + b * 176;
+        const float d = rd_h(blk), dmin = rd_h(blk + 2);
+        const uint8_t* scales = blk + 4;
+        const uint8_t* qh = blk + 16;
+        const uint8_t* qs = blk + 48;
+        float* vals = out + b * 256;
+        for (int j = 0; j < 4; ++j) {
+            uint8_t sc_lo, m_lo, sc_hi, m_hi;
+            scale_min_k4(j, scales, &sc_lo, &m_lo);
+            scale_min_k4(j + 4, scales, &sc_hi, &m_hi);
+            const float d_lo = d * (float)sc_lo, m_lo2 = dmin * (float)m_lo;
+            const float d_hi = d * (float)sc_hi, m_hi2 = dmin * (float)m_hi;
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t bv = qs[j * 32 + l];
+                const int elo = j * 64 + l, ehi = j * 64 + l + 32;
+                const unsigned hlo = (qh[elo / 8] >> (elo % 8)) & 1;
+                const unsigned hhi = (qh[ehi / 8] >> (ehi % 8)) & 1;
+                vals[elo] = d_lo * (float)((bv & 0x0Fu) | (hlo << 4)) - m_lo2;
+                vals[ehi] = d_hi * (float)((unsigned)(bv >> 4) | (hhi << 4)) - m_hi2;
+            }
+        }
+    }
+}
+
 void ora_dequant(int fmt, const uint8_t* in, size_t nblk, float* out) {
     switch (fmt) {
         case ORA_Q8_0: ora_dequant_q8_0(in, nblk, out); break;
         case ORA_Q4_0: ora_dequant_q4_0(in, nblk, out); break;
         case ORA_Q4K: ora_dequant_q4k(in, nblk, out); break;
         case ORA_Q6K: ora_dequant_q6k(in, nblk, out); break;
+        case ORA_Q5_0: ora_dequant_q5_0(in, nblk, out); break;
+        case ORA_Q5K: ora_dequant_q5k(in, nblk, out); break;
     }
 }
 
@@ -445,5 +500,79 @@ void ora_quantize_q6k(const float* w, size_t nblk, uint8_t* out) {
             p[192 + slot + 1] = 0x5A;
         }
         wr_h(p + 208, dh);
+    }
+}
+
+/* Test-data quantisers for the 5-bit formats (not in the reference, which
+ * only reads such files): Q5_0 d = x[amax]/−16, q = clamp(x/d + 16.5, 0, 31)
+ * in the reference's layout; Q5_K as the Q4_K quantiser with 31 levels and
+ * the reference's high-bit order (bit e%8 of qh[e/8]). */
+void ora_quantize_q5_0(const float* w, size_t nblk, uint8_t* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const float* x = w + b * 32;
+        float amax = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 32; ++i)
+            if (fabsf(x[i]) > amax) { amax = fabsf(x[i]); mx = x[i]; }
+        const float d = mx / -16.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint8_t* p = out + b * 22;
+        wr_h(p, ora_f2h(d));
+        uint32_t qh = 0;
+        for (int j = 0; j < 16; ++j) {
+            const int q0 = clampi((int)(x[j] * id + 16.5f), 0, 31);
+            const int q1 = clampi((int)(x[j + 16] * id + 16.5f), 0, 31);
+            p[6 + j] = (uint8_t)((q0 & 15) | ((q1 & 15) << 4));
+            qh |= (uint32_t)(q0 >> 4) << j;
+            qh |= (uint32_t)(q1 >> 4) << (j + 16);
+        }
+        for (int i = 0; i < 4; ++i) p[2 + i] = (uint8_t)(qh >> (8 * i));
+    }
+}
+
+void ora_quantize_q5k(const float* w, size_t nblk, uint8_t* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const float* x = w + b * 256;
+        float scl[8], mns[8], maxs = 0.0f, maxm = 0.0f;
+        for (int s = 0; s < 8; ++s) {
+            const int base = 64 * (s & 3) + 32 * (s >> 2);
+            float mn = 0.0f, mx = -3.0e38f;
+            for (int l = 0; l < 32; ++l) { mn = fminf(mn, x[base + l]); mx = fmaxf(mx, x[base + l]); }
+            mns[s] = -mn;
+            scl[s] = (mx - mn) / 31.0f;
+            maxs = fmaxf(maxs, scl[s]);
+            maxm = fmaxf(maxm, mns[s]);
+        }
+        const float d = maxs / 63.0f, dmin = maxm / 63.0f;
+        const uint16_t dh = ora_f2h(d), dmh = ora_f2h(dmin);
+        const float dq = ora_h2f(dh), dmq = ora_h2f(dmh);
+        int sc[8], m[8];
+        for (int s = 0; s < 8; ++s) {
+            sc[s] = clampi(d > 0.0f ? (int)roundf(scl[s] / d) : 0, 0, 63);
+            m[s] = clampi(dmin > 0.0f ? (int)roundf(mns[s] / dmin) : 0, 0, 63);
+        }
+        uint8_t* p = out + b * 176;
+        memset(p, 0, 176);
+        wr_h(p, dh);
+        wr_h(p + 2, dmh);
+        uint8_t* S = p + 4;
+        for (int j = 0; j < 4; ++j) {
+            S[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            S[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+            S[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+        }
+        uint8_t* qh = p + 16;
+        uint8_t* qs = p + 48;
+        for (int j = 0; j < 4; ++j)
+            for (int l = 0; l < 32; ++l) {
+                int qq[2];
+                for (int hi = 0; hi < 2; ++hi) {
+                    const int s = j + 4 * hi, e = 64 * j + 32 * hi + l;
+                    const float ds = dq * (float)sc[s], ms = dmq * (float)m[s];
+                    const int q = ds > 0.0f ? (int)roundf((x[e] + ms) / ds) : 0;
+                    qq[hi] = clampi(q, 0, 31);
+                    qh[e / 8] |= (uint8_t)((qq[hi] >> 4) << (e % 8));
+                }
+                qs[32 * j + l] = (uint8_t)((qq[0] & 15) | ((qq[1] & 15) << 4));
+            }
     }
 }

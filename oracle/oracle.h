@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-enum { ORA_Q8_0 = 0, ORA_Q4_0 = 1, ORA_Q4K = 2, ORA_Q6K = 3 };
+enum { ORA_Q8_0 = 0, ORA_Q4_0 = 1, ORA_Q4K = 2, ORA_Q6K = 3, ORA_Q5_0 = 4, ORA_Q5K = 5 };
 
 /* half 2.7.1 crate (Cargo.lock): f16::to_f32 (exact) and f16::from_f32
  * (IEEE binary16, round to nearest even) — used at forward.rs:958,577. */
@@ -34,6 +34,8 @@ void ora_dequant_q8_0(const uint8_t* in, size_t nblk, float* out); /* forward.rs
 void ora_dequant_q4_0(const uint8_t* in, size_t nblk, float* out); /* forward.rs:964-978 */
 void ora_dequant_q4k(const uint8_t* in, size_t nblk, float* out);  /* forward.rs:1026-1057, 359-369 */
 void ora_dequant_q6k(const uint8_t* in, size_t nblk, float* out);  /* forward.rs:921-950 */
+void ora_dequant_q5_0(const uint8_t* in, size_t nblk, float* out); /* forward.rs:900-920 */
+void ora_dequant_q5k(const uint8_t* in, size_t nblk, float* out);  /* forward.rs:979-1012, 359-369 */
 void ora_dequant(int fmt, const uint8_t* in, size_t nblk, float* out);
 /* dequant.metal:53-98 — Q4_K → f16 (f32 value, then RNE to half). */
 void ora_dequant_q4k_f16(const uint8_t* in, size_t nblk, uint16_t* out);
@@ -86,6 +88,8 @@ void ora_quantize_q8_0(const float* w, size_t nblk, uint8_t* out);
 void ora_quantize_q4_0(const float* w, size_t nblk, uint8_t* out);
 void ora_quantize_q4k(const float* w, size_t nblk, uint8_t* out);
 void ora_quantize_q6k(const float* w, size_t nblk, uint8_t* out);
+void ora_quantize_q5_0(const float* w, size_t nblk, uint8_t* out);
+void ora_quantize_q5k(const float* w, size_t nblk, uint8_t* out);
 
 #ifdef __cplusplus
 }

@@ -91,6 +91,44 @@ k_dequant_q6k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint6
     out[i] = __fmul_rn(__fmul_rn(d, s), (float)q);  // forward.rs:935-946
 }
 
+// Q5_0: d f16 @0, qh u32 @2, qs[16] @6; element j < 16 is the low nibble of
+// qs[j] with qh bit j on top, element 16 + j the high nibble with bit 16 + j;
+// value d·(q − 16) (forward.rs:900-920).
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q5_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_el) return;
+    const uint8_t* blk = in + (i >> 5) * 22;
+    const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    const uint32_t e = (uint32_t)(i & 31), j = e & 15;
+    const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                        ((uint32_t)blk[5] << 24);
+    const uint32_t byte = blk[6 + j];
+    const uint32_t nib = (e < 16) ? (byte & 15u) : (byte >> 4);
+    const int q = (int)(nib | (((qh >> e) & 1u) << 4));
+    out[i] = __fmul_rn(d, (float)(q - 16));
+}
+
+// Q5_K: d, dmin f16 @0, scales[12] @4, qh[32] @16, qs[128] @48; element
+// 64j + l (+32) takes the low (high) nibble of qs[32j + l], bit (e % 8) of
+// qh[e / 8] on top, and (sc, m) of sub-block j (j + 4) (forward.rs:979-1012).
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q5k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_el) return;
+    const uint8_t* blk = in + (i >> 8) * 176;
+    const uint32_t e = (uint32_t)(i & 255), j = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+    const float d = h2f(*(const uint16_t*)blk);
+    const float dmin = h2f(*(const uint16_t*)(blk + 2));
+    uint32_t sc, m;
+    q4k_scale_min(j + 4 * hi, blk + 4, sc, m);
+    const uint32_t byte = blk[48 + 32 * j + l];
+    const uint32_t q = (hi ? (byte >> 4) : (byte & 15u)) | (((blk[16 + e / 8] >> (e % 8)) & 1u) << 4);
+    const float dsc = __fmul_rn(d, (float)sc);
+    const float mm = __fmul_rn(dmin, (float)m);
+    out[i] = __fsub_rn(__fmul_rn(dsc, (float)q), mm);
+}
+
 // ───────────────────────────── argmax ─────────────────────────────
 // greedy_argmax_f32 (sampler.rs:111-116) folds with Rust's max_by: the
 // running best m is replaced by x unless m > x (partial_cmp None → Equal).
@@ -370,6 +408,93 @@ k_synth_q4k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
                 qs[32 * j + l] = (uint8_t)(qq[0] | (qq[1] << 4));
             }
         }
+    }
+}
+
+// Q5_0: d = m/−16 (m: signed value of largest magnitude), q = clamp(int(w/d
+// + 16.5), 0, 31); element j < 16 in the low nibble of qs[j] and qh bit j,
+// element 16 + j in the high nibble and qh bit 16 + j.
+extern "C" __global__ void __launch_bounds__(256)
+k_synth_q5_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * blockDim.x) {
+        float w[32];
+        float amax = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            w[i] = stdv * synth_normal(seed, b * 32 + i);
+            if (fabsf(w[i]) > amax) { amax = fabsf(w[i]); mx = w[i]; }
+        }
+        const float d = mx / -16.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint8_t* p = out + b * 22;
+        const uint16_t dh = f2h(d);
+        p[0] = dh & 255; p[1] = dh >> 8;
+        uint32_t qh = 0;
+        for (int j = 0; j < 16; ++j) {
+            int q0 = (int)(w[j] * id + 16.5f), q1 = (int)(w[j + 16] * id + 16.5f);
+            q0 = q0 < 0 ? 0 : (q0 > 31 ? 31 : q0);
+            q1 = q1 < 0 ? 0 : (q1 > 31 ? 31 : q1);
+            p[6 + j] = (uint8_t)((q0 & 15) | ((q1 & 15) << 4));
+            qh |= (uint32_t)(q0 >> 4) << j;
+            qh |= (uint32_t)(q1 >> 4) << (j + 16);
+        }
+        for (int i = 0; i < 4; ++i) p[2 + i] = (uint8_t)(qh >> (8 * i));
+    }
+}
+
+// Q5_K: the Q4_K construction with 31 levels; the high bit of element e goes
+// to bit e%8 of qh[e/8].
+extern "C" __global__ void __launch_bounds__(256)
+k_synth_q5k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * blockDim.x) {
+        float w[256];
+        for (int i = 0; i < 256; ++i) w[i] = stdv * synth_normal(seed, b * 256 + i);
+        float scl[8], mns[8], maxs = 0.0f, maxm = 0.0f;
+        for (int s = 0; s < 8; ++s) {
+            const int base = 64 * (s & 3) + 32 * (s >> 2);
+            float mn = 0.0f, mx = -3.0e38f;
+            for (int l = 0; l < 32; ++l) { mn = fminf(mn, w[base + l]); mx = fmaxf(mx, w[base + l]); }
+            mns[s] = -mn;
+            scl[s] = (mx - mn) / 31.0f;
+            maxs = fmaxf(maxs, scl[s]);
+            maxm = fmaxf(maxm, mns[s]);
+        }
+        const float d = maxs / 63.0f, dmin = maxm / 63.0f;
+        const uint16_t dh = f2h(d), dmh = f2h(dmin);
+        const float dq = h2f(dh), dmq = h2f(dmh);
+        uint32_t sc[8], m[8];
+        for (int s = 0; s < 8; ++s) {
+            int a = d > 0.0f ? (int)roundf(scl[s] / d) : 0;
+            int c = dmin > 0.0f ? (int)roundf(mns[s] / dmin) : 0;
+            sc[s] = a < 0 ? 0 : (a > 63 ? 63 : a);
+            m[s] = c < 0 ? 0 : (c > 63 ? 63 : c);
+        }
+        uint8_t* p = out + b * 176;
+        p[0] = dh & 255; p[1] = dh >> 8; p[2] = dmh & 255; p[3] = dmh >> 8;
+        uint8_t* S = p + 4;
+        for (int j = 0; j < 4; ++j) {
+            S[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            S[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+            S[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+        }
+        uint8_t qh[32];
+        for (int i = 0; i < 32; ++i) qh[i] = 0;
+        uint8_t* qs = p + 48;
+        for (int j = 0; j < 4; ++j) {
+            for (int l = 0; l < 32; ++l) {
+                uint32_t qq[2];
+                for (int hi = 0; hi < 2; ++hi) {
+                    const int s = j + 4 * hi, e = 64 * j + 32 * hi + l;
+                    const float ds = dq * (float)sc[s], ms = dmq * (float)m[s];
+                    int q = ds > 0.0f ? (int)roundf((w[e] + ms) / ds) : 0;
+                    qq[hi] = q < 0 ? 0 : (q > 31 ? 31 : q);
+                    qh[e / 8] |= (uint8_t)((qq[hi] >> 4) << (e % 8));
+                }
+                qs[32 * j + l] = (uint8_t)((qq[0] & 15) | ((qq[1] & 15) << 4));
+            }
+        }
+        for (int i = 0; i < 32; ++i) p[16 + i] = qh[i];
     }
 }
 

@@ -528,3 +528,195 @@ struct FmtQ6KB {
         return acc;
     }
 };
+
+// ───────────────────────────── Q5_0 / Q5_K ─────────────────────────────
+//
+// The reference runs these through CPU dequantisation to f16/f32 (forward.rs:
+// 900-920 Q5_0, 979-1012 Q5_K); these formats give them fused GEMVs with the
+// same values.  A 5-bit code is a 4-bit nibble plus one high bit taken from a
+// bit array; for four consecutive elements the four high bits are one
+// nibble of that array, spread to bit 4 of each byte by spread4.
+RT_DEV uint32_t spread4(uint32_t nib) {  // bit k of nib → bit 8k
+    return (nib * 0x00204081u) & 0x01010101u;
+}
+
+// Q5_0 block (22 B): d f16 @0, qh u32 @2, qs[16] @6.  Element j < 16 is
+// (qs[j] & 15) | (qh bit j) << 4, element 16 + j is (qs[j] >> 4) | (qh bit
+// 16+j) << 4; value d·(q − 16) (forward.rs:900-920).  q[i] = qs dword i.
+RT_DEV float q5_0_block_mdot(uint32_t d16, uint32_t qh, const uint32_t q[4], const XLimb& x) {
+    v4i c = {-16 * x.s[0], -16 * x.s[1], -16 * x.s[2], 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        c = mfma4(x.l[i], (q[i] & 0x0F0F0F0Fu) | (spread4((qh >> (4 * i)) & 15u) << 4), c);
+        c = mfma4(x.l[4 + i],
+                  ((q[i] >> 4) & 0x0F0F0F0Fu) | (spread4((qh >> (16 + 4 * i)) & 15u) << 4), c);
+    }
+    return __builtin_amdgcn_ldexpf(h2f(d16) * comb4(c), x.e - 22);
+}
+RT_DEV float q5_0_block_dot(uint32_t d16, uint32_t qh, const uint32_t q[4], const XRegs& x) {
+    int t0 = -16 * x.s[0], t1 = -16 * x.s[1], t2 = -16 * x.s[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = (q[i] & 0x0F0F0F0Fu) | (spread4((qh >> (4 * i)) & 15u) << 4);
+        const uint32_t hi = ((q[i] >> 4) & 0x0F0F0F0Fu) | (spread4((qh >> (16 + 4 * i)) & 15u) << 4);
+        t0 = sdot4(lo, x.l[0][i], t0);
+        t1 = sdot4(lo, x.l[1][i], t1);
+        t2 = sdot4(lo, x.l[2][i], t2);
+        t0 = sdot4(hi, x.l[0][4 + i], t0);
+        t1 = sdot4(hi, x.l[1][4 + i], t1);
+        t2 = sdot4(hi, x.l[2][4 + i], t2);
+    }
+    return __builtin_amdgcn_ldexpf(h2f(d16) * limb_combine(t0, t1, t2), x.e - 22);
+}
+
+// Unit = two consecutive Q5_0 blocks (44 bytes, 4-byte aligned when a row
+// holds an even number of blocks): 11 aligned dwords.
+struct FmtQ5_0 {
+    static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 22, UNIT_EL = 64;
+    static constexpr bool Q40PERM = false;
+    struct Raw { uint32_t w[11]; };
+    struct XU { XRegs x[2]; };
+    RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
+        load_dwords<11>(row + (size_t)u * 44, r.w);
+    }
+    RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) {
+        load_xregs(recs + 2 * uu, xu.x[0]);
+        load_xregs(recs + 2 * uu + 1, xu.x[1]);
+    }
+    // block A at byte 0 (d, qh @2, qs @6), block B at byte 22 (d, qh @24, qs @28)
+    RT_DEV static void split(const Raw& r, uint32_t& da, uint32_t& qha, uint32_t qa[4],
+                             uint32_t& db, uint32_t& qhb, uint32_t qb[4]) {
+        da = r.w[0];
+        qha = alignb(r.w[1], r.w[0], 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qa[i] = alignb(r.w[2 + i], r.w[1 + i], 2);
+        db = r.w[5] >> 16;
+        qhb = r.w[6];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qb[i] = r.w[7 + i];
+    }
+    RT_DEV static float dot(const Raw& r, const XU& xu) {
+        uint32_t da, qha, qa[4], db, qhb, qb[4];
+        split(r, da, qha, qa, db, qhb, qb);
+        return q5_0_block_dot(da, qha, qa, xu.x[0]) + q5_0_block_dot(db, qhb, qb, xu.x[1]);
+    }
+    RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
+        XLimb xa, xb;
+        load_xlimb(xs + 2 * uu, lq, xa);
+        load_xlimb(xs + 2 * uu + 1, lq, xb);
+        uint32_t da, qha, qa[4], db, qhb, qb[4];
+        split(r, da, qha, qa, db, qhb, qb);
+        return q5_0_block_mdot(da, qha, qa, xa) + q5_0_block_mdot(db, qhb, qb, xb);
+    }
+};
+
+// Single-block unit for rows with an odd number of blocks: 6 aligned dwords
+// from the block's floor (never wholly past the block).
+struct FmtQ5_0S {
+    static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 22, UNIT_EL = 32;
+    static constexpr bool Q40PERM = false;
+    struct Raw { uint32_t w[6]; uint32_t sh; };
+    struct XU { XRegs x; };
+    RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
+        const uintptr_t p = (uintptr_t)(row + (size_t)u * 22);
+        r.sh = (uint32_t)(p & 3);
+        load_dwords<6>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
+    }
+    RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) { load_xregs(recs + uu, xu.x); }
+    RT_DEV static void split(const Raw& r, uint32_t& d, uint32_t& qh, uint32_t q[4]) {
+        d = r.sh ? (r.w[0] >> 16) : r.w[0];
+        qh = r.sh ? r.w[1] : alignb(r.w[1], r.w[0], 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = r.sh ? r.w[2 + i] : alignb(r.w[2 + i], r.w[1 + i], 2);
+    }
+    RT_DEV static float dot(const Raw& r, const XU& xu) {
+        uint32_t d, qh, q[4];
+        split(r, d, qh, q);
+        return q5_0_block_dot(d, qh, q, xu.x);
+    }
+};
+
+// Q5_K (176 B, 16-byte aligned): d, dmin f16 @0, scales[12] @4 (Q4_K
+// packing), qh[32] @16, qs[128] @48.  Unit (block, pair j) = 64 elements:
+// sub-block j (low nibbles of qs[32j..32j+31]) and j+4 (high nibbles); the
+// high bit of element e is bit e%8 of qh[e/8] (forward.rs:979-1012), so the
+// unit's 64 high bits are qh bytes 8j..8j+7.  v = d·sc·q − dmin·m.
+struct FmtQ5K {
+    static constexpr uint32_t BLK_EL = 256, BLK_BYTES = 176, UNIT_EL = 64;
+    static constexpr bool Q40PERM = false;
+    struct Raw { uint32_t dd; uint32_t sc; uint32_t qh0, qh1; uint32_t q[8]; };
+    struct XU { XRegs lo, hi; };
+    RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
+        const uint32_t b = u >> 2, j = u & 3;
+        const uint8_t* p = row + (size_t)b * 176;
+        const u32x4 hdr = *(const u32x4*)p;
+        r.dd = hdr.x;
+        const uint32_t sh = 8 * j;
+        r.sc = ((hdr.y >> sh) & 255u) | (((hdr.z >> sh) & 255u) << 8) | (((hdr.w >> sh) & 255u) << 16);
+        const uint2 h = *(const uint2*)(p + 16 + 8 * j);
+        r.qh0 = h.x;
+        r.qh1 = h.y;
+        const u32x4* qp = (const u32x4*)(p + 48 + 32 * j);
+        const u32x4 a = qp[0], c = qp[1];
+        r.q[0] = a.x; r.q[1] = a.y; r.q[2] = a.z; r.q[3] = a.w;
+        r.q[4] = c.x; r.q[5] = c.y; r.q[6] = c.z; r.q[7] = c.w;
+    }
+    RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) {
+        load_xregs(recs + 2 * uu, xu.lo);
+        load_xregs(recs + 2 * uu + 1, xu.hi);
+    }
+    RT_DEV static uint32_t code_lo(const Raw& r, int i) {
+        return (r.q[i] & 0x0F0F0F0Fu) | (spread4((r.qh0 >> (4 * i)) & 15u) << 4);
+    }
+    RT_DEV static uint32_t code_hi(const Raw& r, int i) {
+        return ((r.q[i] >> 4) & 0x0F0F0F0Fu) | (spread4((r.qh1 >> (4 * i)) & 15u) << 4);
+    }
+    RT_DEV static void scales(const Raw& r, float& d_lo, float& m_lo, float& d_hi, float& m_hi) {
+        const uint32_t c0 = r.sc & 255u, c1 = (r.sc >> 8) & 255u, c2 = (r.sc >> 16) & 255u;
+        const uint32_t sc_lo = c0 & 63u, mn_lo = c1 & 63u;
+        const uint32_t sc_hi = (c2 & 15u) | ((c0 >> 6) << 4);
+        const uint32_t mn_hi = (c2 >> 4) | ((c1 >> 6) << 4);
+        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
+        d_lo = d * (float)sc_lo;
+        m_lo = dmin * (float)mn_lo;
+        d_hi = d * (float)sc_hi;
+        m_hi = dmin * (float)mn_hi;
+    }
+    RT_DEV static float dot(const Raw& r, const XU& xu) {
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lo = code_lo(r, i), hi = code_hi(r, i);
+            a0 = sdot4(lo, xu.lo.l[0][i], a0);
+            a1 = sdot4(lo, xu.lo.l[1][i], a1);
+            a2 = sdot4(lo, xu.lo.l[2][i], a2);
+            b0 = sdot4(hi, xu.hi.l[0][i], b0);
+            b1 = sdot4(hi, xu.hi.l[1][i], b1);
+            b2 = sdot4(hi, xu.hi.l[2][i], b2);
+        }
+        float d_lo, m_lo, d_hi, m_hi;
+        scales(r, d_lo, m_lo, d_hi, m_hi);
+        const float vlo = d_lo * limb_combine(a0, a1, a2) -
+                          m_lo * limb_combine(xu.lo.s[0], xu.lo.s[1], xu.lo.s[2]);
+        const float vhi = d_hi * limb_combine(b0, b1, b2) -
+                          m_hi * limb_combine(xu.hi.s[0], xu.hi.s[1], xu.hi.s[2]);
+        return __builtin_amdgcn_ldexpf(vlo, xu.lo.e - 22) +
+               __builtin_amdgcn_ldexpf(vhi, xu.hi.e - 22);
+    }
+    RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
+        XLimb xl, xh;
+        load_xlimb(xs + 2 * uu, lq, xl);
+        load_xlimb(xs + 2 * uu + 1, lq, xh);
+        v4i cl = {0, 0, 0, 0}, ch = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            cl = mfma4(xl.l[i], code_lo(r, i), cl);
+            ch = mfma4(xh.l[i], code_hi(r, i), ch);
+        }
+        float d_lo, m_lo, d_hi, m_hi;
+        scales(r, d_lo, m_lo, d_hi, m_hi);
+        const float vlo = d_lo * comb4(cl) - m_lo * limb_combine(xl.s[0], xl.s[1], xl.s[2]);
+        const float vhi = d_hi * comb4(ch) - m_hi * limb_combine(xh.s[0], xh.s[1], xh.s[2]);
+        return __builtin_amdgcn_ldexpf(vlo, xl.e - 22) + __builtin_amdgcn_ldexpf(vhi, xh.e - 22);
+    }
+};

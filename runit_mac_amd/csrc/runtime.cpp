@@ -86,10 +86,20 @@ const char* const kKernelNames[] = {
     "k_gemv_q4_0_f32_f32_s1", "k_gemv_q4_0_f32_f32add_s1", "k_gemv_q4_0_f32_f16_s1",
     "k_gemv_q4_0_f16_f16_s1", "k_gemv_q4_0_f16_f16add_s1", "k_qkv_bias_q4_0_s1", "k_ffn_q4_0_s1",
     "k_dequant_q8_0_f32", "k_dequant_q4_0_f32", "k_dequant_q4k_f32", "k_dequant_q4k_f16",
-    "k_dequant_q6k_f32",
+    "k_dequant_q6k_f32", "k_dequant_q5_0_f32", "k_dequant_q5k_f32",
+    "k_gemv_q5_0_f32_f32_r1", "k_gemv_q5_0_f32_f32_r2",
+    "k_gemv_q5_0_f32_f32add_r1", "k_gemv_q5_0_f32_f32add_r2",
+    "k_gemv_q5_0_f32_f16_r1", "k_gemv_q5_0_f32_f16_r2",
+    "k_qkv_bias_q5_0_r1", "k_qkv_bias_q5_0_r2", "k_ffn_q5_0_r1", "k_ffn_q5_0_r2",
+    "k_gemv_q5_0_f32_f32_s1", "k_gemv_q5_0_f32_f32add_s1", "k_gemv_q5_0_f32_f16_s1",
+    "k_qkv_bias_q5_0_s1", "k_ffn_q5_0_s1",
+    "k_gemv_q5k_f32_f32_r1", "k_gemv_q5k_f32_f32_r2",
+    "k_gemv_q5k_f32_f32add_r1", "k_gemv_q5k_f32_f32add_r2",
+    "k_gemv_q5k_f32_f16_r1", "k_gemv_q5k_f32_f16_r2",
+    "k_qkv_bias_q5k_r1", "k_qkv_bias_q5k_r2", "k_ffn_q5k_r1", "k_ffn_q5k_r2",
     "k_argmax_f32", "k_argmax_f16",
     "k_synth_normal_f32", "k_synth_normal_f16", "k_synth_q8_0", "k_synth_q4_0",
-    "k_synth_q4k", "k_synth_q6k",
+    "k_synth_q4k", "k_synth_q6k", "k_synth_q5_0", "k_synth_q5k",
     "k_stream_read", "k_stream_copy",
     "k_act_limbs_f32", "k_act_limbs_f32_q40", "k_act_limbs_f16", "k_act_limbs_f16_q40",
     "k_rms_norm_f32g", "k_rope_qk_f32", "k_kv_copy_f32",
@@ -118,6 +128,9 @@ constexpr Fmt kQ8_0{32, 34, 64, 1, "Q8_0", &kQ8_0S};
 constexpr Fmt kQ4_0{32, 18, 64, 2, "Q4_0", &kQ4_0S};
 constexpr Fmt kQ4K{256, 144, 64, 1, "Q4_K", nullptr};
 constexpr Fmt kQ6K{256, 210, 64, 1, "Q6_K", nullptr, 256};  // matrix-core: one block per lane
+constexpr Fmt kQ5_0S{32, 22, 32, 4, "Q5_0", nullptr};
+constexpr Fmt kQ5_0{32, 22, 64, 2, "Q5_0", &kQ5_0S};
+constexpr Fmt kQ5K{256, 176, 64, 1, "Q5_K", nullptr};
 
 thread_local std::string g_global_error = "no error";
 
@@ -807,6 +820,55 @@ int rt_gemv_q6k_f32in(rt_ctx* c, const void* w, const float* x, uint16_t* y, uin
     return gemv_plain(c, "k_gemv_q6k_f32_f16", kQ6K, w, x, y, nullptr, false, m, k, false);
 }
 
+// ───────────────────────────── Q5_0 / Q5_K ─────────────────────────────
+
+int rt_gemv_q5_0_f32in_f32out(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m,
+                              uint32_t k) {
+    return gemv_plain(c, "k_gemv_q5_0_f32_f32", kQ5_0, w, x, y, nullptr, false, m, k, false);
+}
+int rt_gemv_q5_0_add_f32_f32in(rt_ctx* c, const void* w, const float* x, float* y,
+                               const float* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q5_0_f32_f32add", kQ5_0, w, x, y, r, true, m, k, false);
+}
+int rt_gemv_q5_0_f32in(rt_ctx* c, const void* w, const float* x, uint16_t* y, uint32_t m,
+                       uint32_t k) {
+    return gemv_plain(c, "k_gemv_q5_0_f32_f16", kQ5_0, w, x, y, nullptr, false, m, k, false);
+}
+int rt_gemv_q5k_f32in_f32out(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m,
+                             uint32_t k) {
+    return gemv_plain(c, "k_gemv_q5k_f32_f32", kQ5K, w, x, y, nullptr, false, m, k, false);
+}
+int rt_gemv_q5k_add_f32_f32in(rt_ctx* c, const void* w, const float* x, float* y,
+                              const float* r, uint32_t m, uint32_t k) {
+    return gemv_plain(c, "k_gemv_q5k_f32_f32add", kQ5K, w, x, y, r, true, m, k, false);
+}
+int rt_gemv_q5k_f32in(rt_ctx* c, const void* w, const float* x, uint16_t* y, uint32_t m,
+                      uint32_t k) {
+    return gemv_plain(c, "k_gemv_q5k_f32_f16", kQ5K, w, x, y, nullptr, false, m, k, false);
+}
+int rt_fused_qkv_bias_q5_0_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                               const float* x, float* oq, float* ok, float* ov,
+                               const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                               uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    return qkv_launch(c, "k_qkv_bias_q5_0", kQ5_0, wq, wk, wv, x, oq, ok, ov, bq, bk, bv, true,
+                      q_dim, kv_dim, k);
+}
+int rt_fused_qkv_bias_q5k_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                              const float* x, float* oq, float* ok, float* ov,
+                              const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                              uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    return qkv_launch(c, "k_qkv_bias_q5k", kQ5K, wq, wk, wv, x, oq, ok, ov, bq, bk, bv, true,
+                      q_dim, kv_dim, k);
+}
+int rt_fused_ffn_q5_0_f32(rt_ctx* c, const void* wg, const void* wu, const float* x, float* act,
+                          uint32_t ff, uint32_t k) {
+    return ffn_launch(c, "k_ffn_q5_0", kQ5_0, wg, wu, x, act, ff, k);
+}
+int rt_fused_ffn_q5k_f32(rt_ctx* c, const void* wg, const void* wu, const float* x, float* act,
+                         uint32_t ff, uint32_t k) {
+    return ffn_launch(c, "k_ffn_q5k", kQ5K, wg, wu, x, act, ff, k);
+}
+
 // ───────────────────────────── fused ─────────────────────────────
 
 int rt_fused_qkv_q8_0_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
@@ -962,6 +1024,12 @@ int rt_dequant_q4k_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
 int rt_dequant_q6k_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
     return elementwise_launch(c, "k_dequant_q6k_f32", in, out, (uint64_t)nb * 256);
 }
+int rt_dequant_q5_0_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q5_0_f32", in, out, (uint64_t)nb * 32);
+}
+int rt_dequant_q5k_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q5k_f32", in, out, (uint64_t)nb * 256);
+}
 int rt_dequant_q4k_f16(rt_ctx* c, const void* in, uint16_t* out, uint32_t nb) {
     return elementwise_launch(c, "k_dequant_q4k_f16", in, out, (uint64_t)nb * 256);
 }
@@ -1007,6 +1075,12 @@ int rt_synth_q4k(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
 }
 int rt_synth_q6k(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
     return synth_launch(c, "k_synth_q6k", out, nb, seed, std, false, 0.0f);
+}
+int rt_synth_q5_0(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
+    return synth_launch(c, "k_synth_q5_0", out, nb, seed, std, false, 0.0f);
+}
+int rt_synth_q5k(rt_ctx* c, void* out, uint64_t nb, uint64_t seed, float std) {
+    return synth_launch(c, "k_synth_q5k", out, nb, seed, std, false, 0.0f);
 }
 
 // ───────────────────────────── calibration ─────────────────────────────

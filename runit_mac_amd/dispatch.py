@@ -86,21 +86,26 @@ _SIGS = {
         "rt_gemv_q8_0_f32in_f32out_mr",
         "rt_gemv_q4_0_f32in_f32out", "rt_gemv_q4_0_f32in", "rt_gemv_q4_0_f16",
         "rt_gemv_q4k_f32in_f32out", "rt_gemv_q4k_f16",
-        "rt_gemv_q6k_f32in_f32out", "rt_gemv_q6k_f32in")},
+        "rt_gemv_q6k_f32in_f32out", "rt_gemv_q6k_f32in",
+        "rt_gemv_q5_0_f32in_f32out", "rt_gemv_q5_0_f32in",
+        "rt_gemv_q5k_f32in_f32out", "rt_gemv_q5k_f32in")},
     **{n: [_P, _P, _P, _P, _P, _U32, _U32] for n in (
         "rt_gemv_q8_0_add_f32_f32in", "rt_gemv_q8_0_add_f16", "rt_gemv_q8_0_add_f32res_f16",
         "rt_gemv_q8_0_add_f32_f32in_mr",
         "rt_gemv_q4_0_add_f32_f32in", "rt_gemv_q4_0_add_f16",
         "rt_gemv_q4k_add_f32_f32in", "rt_gemv_q4k_add_f16", "rt_gemv_q4k_add_f32res_f16",
-        "rt_gemv_q6k_add_f32_f32in")},
+        "rt_gemv_q6k_add_f32_f32in", "rt_gemv_q5_0_add_f32_f32in", "rt_gemv_q5k_add_f32_f32in")},
     "rt_fused_qkv_q8_0_f32": [_P] + [_P] * 7 + [_U32] * 3,
     "rt_fused_qkv_bias_q8_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
     "rt_fused_qkv_bias_q4_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
+    "rt_fused_qkv_bias_q5_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
+    "rt_fused_qkv_bias_q5k_f32": [_P] + [_P] * 10 + [_U32] * 3,
     **{n: [_P, _P, _P, _P, _P, _U32, _U32] for n in (
-        "rt_fused_ffn_q8_0_f32", "rt_fused_ffn_q4_0_f32", "rt_fused_ffn_q4k_f32")},
+        "rt_fused_ffn_q8_0_f32", "rt_fused_ffn_q4_0_f32", "rt_fused_ffn_q4k_f32",
+        "rt_fused_ffn_q5_0_f32", "rt_fused_ffn_q5k_f32")},
     **{n: [_P, _P, _P, _U32] for n in (
         "rt_dequant_q8_0_f32", "rt_dequant_q4_0_f32", "rt_dequant_q4k_f32",
-        "rt_dequant_q6k_f32", "rt_dequant_q4k_f16", "rt_argmax_f32", "rt_argmax_f16")},
+        "rt_dequant_q6k_f32", "rt_dequant_q4k_f16", "rt_dequant_q5_0_f32", "rt_dequant_q5k_f32", "rt_argmax_f32", "rt_argmax_f16")},
     "rt_gemm_q8_0_f32": [_P, _P, _P, _P, _U32, _U32, _U32],
     "rt_rms_norm_f32_f32_f32g": [_P, _P, _P, _P, _F, _U32, _U32],
     "rt_fused_rope_qk_f32": [_P, _P, _P, _U32, _U32, _U32, _U32, _F],
@@ -116,7 +121,8 @@ _SIGS = {
     "rt_synth_normal_f32": [_P, _P, _U64, _U64, _F, _F],
     "rt_synth_normal_f16": [_P, _P, _U64, _U64, _F, _F],
     **{n: [_P, _P, _U64, _U64, _F] for n in (
-        "rt_synth_q8_0", "rt_synth_q4_0", "rt_synth_q4k", "rt_synth_q6k")},
+        "rt_synth_q8_0", "rt_synth_q4_0", "rt_synth_q4k", "rt_synth_q6k", "rt_synth_q5_0",
+        "rt_synth_q5k")},
 }
 
 
@@ -372,6 +378,13 @@ gemv_q4k_add_f32res_f16 = _gemv_add("gemv_q4k_add_f32res_f16")
 gemv_q6k_f32in_f32out = _gemv("gemv_q6k_f32in_f32out")
 gemv_q6k_f32in = _gemv("gemv_q6k_f32in")
 gemv_q6k_add_f32_f32in = _gemv_add("gemv_q6k_add_f32_f32in")
+# Q5_0 / Q5_K (new: the reference dequantises both on the CPU, forward.rs:900-920, 979-1012)
+gemv_q5_0_f32in_f32out = _gemv("gemv_q5_0_f32in_f32out")
+gemv_q5_0_f32in = _gemv("gemv_q5_0_f32in")
+gemv_q5_0_add_f32_f32in = _gemv_add("gemv_q5_0_add_f32_f32in")
+gemv_q5k_f32in_f32out = _gemv("gemv_q5k_f32in_f32out")
+gemv_q5k_f32in = _gemv("gemv_q5k_f32in")
+gemv_q5k_add_f32_f32in = _gemv_add("gemv_q5k_add_f32_f32in")
 
 
 def fused_qkv_q8_0_f32(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, q_dim, kv_dim, k):
@@ -396,6 +409,22 @@ def fused_qkv_bias_q4_0_f32(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias
           q_dim, kv_dim, k)
 
 
+def fused_qkv_bias_q5_0_f32(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k,
+                            bias_v, q_dim, kv_dim, k):
+    """Q5_0 twin of dispatch.rs:842-871 (new)."""
+    _call(ctx, "rt_fused_qkv_bias_q5_0_f32",
+          *map(_ptr, (w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k, bias_v)),
+          q_dim, kv_dim, k)
+
+
+def fused_qkv_bias_q5k_f32(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k,
+                           bias_v, q_dim, kv_dim, k):
+    """Q5_K twin of dispatch.rs:842-871 (new)."""
+    _call(ctx, "rt_fused_qkv_bias_q5k_f32",
+          *map(_ptr, (w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k, bias_v)),
+          q_dim, kv_dim, k)
+
+
 def fused_ffn_q8_0_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
     """dispatch.rs:903-921"""
     _call(ctx, "rt_fused_ffn_q8_0_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
@@ -411,13 +440,23 @@ def fused_ffn_q4k_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
     _call(ctx, "rt_fused_ffn_q4k_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
 
 
+def fused_ffn_q5_0_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
+    """Q5_0 twin of dispatch.rs:903-921 (new)."""
+    _call(ctx, "rt_fused_ffn_q5_0_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
+
+
+def fused_ffn_q5k_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
+    """Q5_K twin of dispatch.rs:903-921 (new)."""
+    _call(ctx, "rt_fused_ffn_q5k_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
+
+
 def dequant_q4k_f16(ctx, input, output, n_blocks):
     """dispatch.rs:756-772"""
     _call(ctx, "rt_dequant_q4k_f16", _ptr(input), _ptr(output), n_blocks)
 
 
 def dequant_f32(ctx, fmt: str, input, output, n_blocks):
-    """Bit-exact dequantisation to f32 for fmt in {q8_0, q4_0, q4k, q6k}."""
+    """Bit-exact dequantisation to f32 for fmt in {q8_0, q4_0, q4k, q6k, q5_0, q5k}."""
     _call(ctx, f"rt_dequant_{fmt}_f32", _ptr(input), _ptr(output), n_blocks)
 
 
@@ -445,7 +484,7 @@ def synth_normal_f16(ctx, out, n, seed, mean=0.0, std=1.0):
 
 
 def synth_weights(ctx, fmt: str, out, n_blocks, seed, std=0.02):
-    """Seeded N(0, std) weights quantised per block (fmt in q8_0/q4_0/q4k/q6k)."""
+    """Seeded N(0, std) weights quantised per block (fmt in q8_0/q4_0/q4k/q6k/q5_0/q5k)."""
     _call(ctx, f"rt_synth_{fmt}", _ptr(out), n_blocks, seed, std)
 
 
@@ -518,7 +557,8 @@ def stream_copy(ctx, dst, src, nbytes):
 
 
 # Block geometry (crates/gguf/src/types.rs:158-191).
-BLOCK = {"q8_0": (32, 34), "q4_0": (32, 18), "q4k": (256, 144), "q6k": (256, 210)}
+BLOCK = {"q8_0": (32, 34), "q4_0": (32, 18), "q4k": (256, 144), "q6k": (256, 210),
+         "q5_0": (32, 22), "q5k": (256, 176)}
 
 
 def weight_bytes(fmt: str, n: int, k: int) -> int:

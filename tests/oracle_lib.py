@@ -11,13 +11,14 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_DIR = os.path.join(REPO, "oracle")
 LIB = os.path.join(ORACLE_DIR, "liboracle.so")
 
-FMT = {"q8_0": 0, "q4_0": 1, "q4k": 2, "q6k": 3}
-BLOCK = {"q8_0": (32, 34), "q4_0": (32, 18), "q4k": (256, 144), "q6k": (256, 210)}
+FMT = {"q8_0": 0, "q4_0": 1, "q4k": 2, "q6k": 3, "q5_0": 4, "q5k": 5}
+BLOCK = {"q8_0": (32, 34), "q4_0": (32, 18), "q4k": (256, 144), "q6k": (256, 210),
+         "q5_0": (32, 22), "q5k": (256, 176)}
 
 
 def _load():
-    src = os.path.join(ORACLE_DIR, "oracle.c")
-    if not os.path.exists(LIB) or os.path.getmtime(LIB) < os.path.getmtime(src):
+    srcs = [os.path.join(ORACLE_DIR, f) for f in ("oracle.c", "oracle.h")]
+    if not os.path.exists(LIB) or os.path.getmtime(LIB) < max(map(os.path.getmtime, srcs)):
         subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
     return ctypes.CDLL(LIB)
 
@@ -41,7 +42,7 @@ _lib.ora_synth_normal.restype = ctypes.c_float
 _lib.ora_rms_norm.argtypes = [_P, _P, ctypes.c_double, _S, _S, _P]
 _lib.ora_rope.argtypes = [_P, _S, _S, ctypes.c_uint32, ctypes.c_float]
 _lib.ora_attention.argtypes = [_P, _P, _P, _S, _S, _S, _S, _S, ctypes.c_double, _P]
-for _n in ("q8_0", "q4_0", "q4k", "q6k"):
+for _n in FMT:
     getattr(_lib, f"ora_quantize_{_n}").argtypes = [_P, _S, _P]
 
 

@@ -47,6 +47,12 @@ def test_fused_qkv_bias_q4_0(ctx, q_dim, kv_dim, k):
     _qkv_case(ctx, "q4_0", q_dim, kv_dim, k, True, seed=q_dim + 1)
 
 
+@pytest.mark.parametrize("fmt,q_dim,kv_dim,k", [("q5_0", 3584, 512, 3584), ("q5_0", 100, 20, 96),
+                                              ("q5k", 896, 128, 1024), ("q5k", 256, 64, 512)])
+def test_fused_qkv_bias_q5(ctx, fmt, q_dim, kv_dim, k):
+    _qkv_case(ctx, fmt, q_dim, kv_dim, k, True, seed=q_dim + 7)
+
+
 def ffn_check(got, gate_ref, gate_s, up_ref, up_s, what):
     """act = silu(g)·u with |g−g_ref| ≤ eg, |u−u_ref| ≤ eu: |silu'| ≤ 1.1 gives
     |Δact| ≤ 1.1·eg·(|u|+eu) + (|silu(g)|+1.1·eg)·eu, plus f32 epilogue rounding."""
@@ -61,7 +67,9 @@ def ffn_check(got, gate_ref, gate_s, up_ref, up_s, what):
 
 @pytest.mark.parametrize("fmt,ff,k", [("q8_0", 4864, 896), ("q8_0", 300, 512),
                                       ("q4_0", 1000, 3584), ("q4_0", 77, 256),
-                                      ("q4k", 1000, 3584), ("q4k", 33, 512)])
+                                      ("q4k", 1000, 3584), ("q4k", 33, 512),
+                                      ("q5_0", 1000, 3584), ("q5_0", 45, 160),
+                                      ("q5k", 1000, 3584), ("q5k", 33, 512)])
 def test_fused_ffn(ctx, fmt, ff, k):
     wg, rg = device_weights(ctx, fmt, ff, k, seed=ff + 1)
     wu, ru = device_weights(ctx, fmt, ff, k, seed=ff + 2)

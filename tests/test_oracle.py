@@ -203,7 +203,7 @@ def test_gemv_all_ones_closed_form(fmt):
     assert np.all(s == k * (k + 1) / 2)
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k"])
 def test_gemv_brute_force(fmt):
     n, k = 7, 512
     w = ora.synth_weights(fmt, n, k, seed=11)
@@ -266,18 +266,20 @@ def test_argmax_rust_max_by_semantics():
 
 # ───────────────────────── quantiser invariants ─────────────────────────
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k"])
 def test_quantizer_round_trip_error_bounded(fmt):
     n_el = 256 * 16
     w = (0.02 * ora.synth_normal(99, n_el)).astype(np.float32)
     v = ora.dequant(fmt, ora.quantize(fmt, w))
     err = np.abs(v - w)
-    el = 32 if fmt in ("q8_0", "q4_0") else 256
+    el = 32 if fmt in ("q8_0", "q4_0", "q5_0") else 256
     amax = np.abs(w).reshape(-1, el).max(axis=1).repeat(el)
     # half a step plus the f16 rounding of the scale: Q8_0 step amax/127
     # (q uses the unrounded d, so up to 127·2^-11 steps more), Q4_0 amax/8
     # (plus one clamped step at +8), Q4_K ≈ range/15, Q6_K amax/32
-    bound = {"q8_0": 0.6 / 127, "q4_0": 1.01 / 8, "q4k": 0.2, "q6k": 0.08}[fmt]
+    # Q5_0 amax/16 (plus one clamped step at +16), Q5_K ≈ range/31
+    bound = {"q8_0": 0.6 / 127, "q4_0": 1.01 / 8, "q4k": 0.2, "q6k": 0.08, "q5_0": 1.01 / 16,
+             "q5k": 0.1}[fmt]
     assert np.all(err <= bound * amax + 1e-7)
 
 
@@ -336,3 +338,79 @@ def test_attention_closed_forms_and_gqa_mapping():
     assert np.allclose(o2[0], v[0, :L].astype(np.float64).mean(axis=0), atol=1e-12)
     # kv_len = 0 → zeros (the reference's l = 0 case)
     assert np.all(ora.attention(q, k, v, H, KVH, hd, 0, S) == 0)
+
+
+# ───────────────────────── Q5_0 / Q5_K ─────────────────────────
+
+def test_q5_0_layout_j_and_j_plus_16_with_high_bits():
+    # forward.rs:900-920: element j (j < 16) = low nibble of qs[j] + qh bit j,
+    # element j+16 = high nibble + qh bit 16+j.  This is also ggml's published
+    # Q5_0 layout (dequantize_row_q5_0), so both readings must agree.
+    q = [(7 * e + 3) % 32 for e in range(32)]
+    qs = bytes((q[j] & 15) | ((q[j + 16] & 15) << 4) for j in range(16))
+    qh = 0
+    for e in range(32):
+        qh |= (q[e] >> 4) << e
+    blk = h16(0.5) + qh.to_bytes(4, "little") + qs
+    v = ora.dequant("q5_0", np.frombuffer(blk, np.uint8))
+    assert np.array_equal(v, 0.5 * (np.array(q) - 16))
+    # a single set high bit (bit 20 → element 20) moves exactly one value by 16·d
+    blk0 = h16(1.0) + bytes(4) + bytes(16)
+    blk1 = h16(1.0) + (1 << 20).to_bytes(4, "little") + bytes(16)
+    v0 = ora.dequant("q5_0", np.frombuffer(blk0, np.uint8))
+    v1 = ora.dequant("q5_0", np.frombuffer(blk1, np.uint8))
+    assert np.all(v0 == -16)
+    assert np.nonzero(v1 - v0)[0].tolist() == [20] and v1[20] == 0.0
+
+
+def test_q5_0_without_high_bits_is_q4_offset_by_minus_8():
+    # with qh = 0 a code c reads c − 16; the same nibbles under the Q4_0 rule
+    # (c − 8) differ by exactly 8·d, element order aside (j / j+16 here,
+    # 2i / 2i+1 there)
+    rng = np.random.default_rng(3)
+    qs = rng.integers(0, 256, 16, dtype=np.uint8).tobytes()
+    v5 = ora.dequant("q5_0", np.frombuffer(h16(0.25) + bytes(4) + qs, np.uint8))
+    v4 = ora.dequant("q4_0", np.frombuffer(h16(0.25) + qs, np.uint8))
+    lo, hi = v4[0::2], v4[1::2]
+    assert np.array_equal(v5[:16], lo - 2.0) and np.array_equal(v5[16:], hi - 2.0)
+
+
+def _q5k_block(d, dmin, sc, m, q):
+    """Q5_K in the reference layout: Q4_K scale packing, qs[32j+l] holds the
+    low 4 bits of elements 64j+l (low nibble) and 64j+32+l (high nibble), the
+    fifth bit of element e is bit e%8 of qh[e/8]."""
+    b4 = bytearray(_q4k_block(d, dmin, sc, m, [c & 15 for c in q]))
+    qh = bytearray(32)
+    for e in range(256):
+        qh[e // 8] |= (q[e] >> 4) << (e % 8)
+    return bytes(b4[:16]) + bytes(qh) + bytes(b4[16:])
+
+
+def test_q5k_high_bit_order_and_scale_pairing():
+    sc = [1, 2, 3, 4, 63, 17, 48, 33]
+    m = [5, 6, 7, 8, 62, 31, 16, 47]
+    q = [((e * 11) + 5) % 32 for e in range(256)]
+    d, dmin = 0.0625, 0.03125
+    v = ora.dequant("q5k", np.frombuffer(_q5k_block(d, dmin, sc, m, q), np.uint8))
+    for e in range(256):
+        s = (e // 64) + 4 * ((e // 32) & 1)
+        expect = np.float32(np.float32(d * sc[s]) * np.float32(q[e])) - np.float32(dmin * m[s])
+        assert v[e] == expect, e
+    # one qh bit: bit 3 of qh[9] is element 75 (pair j=1, high half, l=11);
+    # ggml's Q5_K order would put that bit on a different element
+    blk = bytearray(_q5k_block(1.0, 0.0, [1] * 8, [0] * 8, [0] * 256))
+    base = ora.dequant("q5k", np.frombuffer(bytes(blk), np.uint8))
+    blk[16 + 9] |= 1 << 3
+    v = ora.dequant("q5k", np.frombuffer(bytes(blk), np.uint8))
+    assert np.nonzero(v - base)[0].tolist() == [75] and v[75] == 16.0
+
+
+def test_q5k_without_high_bits_equals_q4k():
+    # qh = 0: Q5_K reduces to Q4_K with the same header and qs
+    rng = np.random.default_rng(5)
+    hdr = bytearray(rng.integers(0, 256, 16, dtype=np.uint8).tobytes())
+    hdr[0:4] = h16(0.01) + h16(0.002)
+    qs = rng.integers(0, 256, 128, dtype=np.uint8).tobytes()
+    v5 = ora.dequant("q5k", np.frombuffer(bytes(hdr) + bytes(32) + qs, np.uint8))
+    v4 = ora.dequant("q4k", np.frombuffer(bytes(hdr) + qs, np.uint8))
+    assert np.array_equal(v5, v4)
