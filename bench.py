@@ -438,6 +438,12 @@ def gemv_specs(ctx, suite):
         ("c2_q8_0_ffn_2x4864x896", lambda: Workload(ctx, "c2_ffn", "q8_0", "ffn", 4864, 896, seed=10)),
     ]
     if suite in ("all", "gemv"):
+        # 5-bit formats (Q5_K_M / Q5_0 files) at the 7B shapes
+        specs += [
+            ("c6_q5k_ffn_2x18944x3584", lambda: Workload(ctx, "c6_ffn", "q5k", "ffn", 18944, 3584, seed=13)),
+            ("c6_q5k_down_3584x18944", lambda: Workload(ctx, "c6_down", "q5k", "add", 3584, 18944, seed=14)),
+            ("c6_q5_0_ffn_2x18944x3584", lambda: Workload(ctx, "c6_ffn0", "q5_0", "ffn", 18944, 3584, seed=15)),
+        ]
         for m in (1, 4, 8, 16, 32):
             specs.append((f"c5_gemm_q8_0_m{m}_18944x3584",
                           (lambda m=m: Workload(ctx, "c5", "q8_0", "gemm", 18944, 3584, m=m, seed=11))))

@@ -8,7 +8,7 @@
 
 extern "C" __global__ void __launch_bounds__(256)
 k_dequant_q8_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
     if (i >= n_el) return;
     const uint8_t* blk = in + (i >> 5) * 34;
     const float d = h2f(*(const uint16_t*)blk);
@@ -18,7 +18,7 @@ k_dequant_q8_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint
 
 extern "C" __global__ void __launch_bounds__(256)
 k_dequant_q4_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
     if (i >= n_el) return;
     const uint8_t* blk = in + (i >> 5) * 18;
     const float d = h2f(*(const uint16_t*)blk);
@@ -54,7 +54,7 @@ RT_DEV float q4k_value(const uint8_t* blk, uint32_t e) {
 
 extern "C" __global__ void __launch_bounds__(256)
 k_dequant_q4k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
     if (i >= n_el) return;
     out[i] = q4k_value(in + (i >> 8) * 144, (uint32_t)(i & 255));
 }
@@ -62,7 +62,7 @@ k_dequant_q4k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint6
 // dequant.metal:53-98 — Q4_K to f16 (value rounded to nearest-even half).
 extern "C" __global__ void __launch_bounds__(256)
 k_dequant_q4k_f16(const uint8_t* __restrict__ in, uint16_t* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
     if (i >= n_el) return;
     float v = q4k_value(in + (i >> 8) * 144, (uint32_t)(i & 255));
     // Materialise the f32 value before the f16 conversion: the reference
@@ -74,7 +74,7 @@ k_dequant_q4k_f16(const uint8_t* __restrict__ in, uint16_t* __restrict__ out, ui
 
 extern "C" __global__ void __launch_bounds__(256)
 k_dequant_q6k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
     if (i >= n_el) return;
     const uint8_t* blk = in + (i >> 8) * 210;
     const uint32_t e = (uint32_t)(i & 255);
@@ -96,7 +96,7 @@ k_dequant_q6k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint6
 // value d·(q − 16) (forward.rs:900-920).
 extern "C" __global__ void __launch_bounds__(256)
 k_dequant_q5_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
     if (i >= n_el) return;
     const uint8_t* blk = in + (i >> 5) * 22;
     const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
@@ -114,7 +114,7 @@ k_dequant_q5_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint
 // qh[e / 8] on top, and (sc, m) of sub-block j (j + 4) (forward.rs:979-1012).
 extern "C" __global__ void __launch_bounds__(256)
 k_dequant_q5k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
     if (i >= n_el) return;
     const uint8_t* blk = in + (i >> 8) * 176;
     const uint32_t e = (uint32_t)(i & 255), j = e >> 6, hi = (e >> 5) & 1, l = e & 31;
@@ -295,14 +295,14 @@ RT_DEV float synth_normal(uint64_t seed, uint64_t idx) {
 
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_normal_f32(float* out, uint64_t n, uint64_t seed, float mean, float stdv) {
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (uint64_t)gridDim.x * blockDim.x)
+    for (uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * wg_threads())
         out[i] = mean + stdv * synth_normal(seed, i);
 }
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, float mean, float stdv) {
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (uint64_t)gridDim.x * blockDim.x)
+    for (uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * wg_threads())
         out[i] = f2h(mean + stdv * synth_normal(seed, i));
 }
 
@@ -310,8 +310,8 @@ k_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, float mean, float s
 // the unrounded d (round half away from zero).
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q8_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
-    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
-         b += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * wg_threads()) {
         float w[32];
         float amax = 0.0f;
         for (int i = 0; i < 32; ++i) {
@@ -334,8 +334,8 @@ k_synth_q8_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // nib = clamp(int(w/d + 8.5), 0, 15); reference nibble order (2i low, 2i+1 high).
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q4_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
-    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
-         b += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * wg_threads()) {
         float w[32];
         float amax = 0.0f, mx = 0.0f;
         for (int i = 0; i < 32; ++i) {
@@ -363,8 +363,8 @@ k_synth_q4_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // q = clamp(round((w + dmin·m_s)/(d·sc_s)), 0, 15).
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q4k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
-    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
-         b += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * wg_threads()) {
         float w[256];
         for (int i = 0; i < 256; ++i) w[i] = stdv * synth_normal(seed, b * 256 + i);
         float scl[8], mns[8], maxs = 0.0f, maxm = 0.0f;
@@ -416,8 +416,8 @@ k_synth_q4k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // element 16 + j in the high nibble and qh bit 16 + j.
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q5_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
-    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
-         b += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * wg_threads()) {
         float w[32];
         float amax = 0.0f, mx = 0.0f;
         for (int i = 0; i < 32; ++i) {
@@ -446,8 +446,8 @@ k_synth_q5_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // to bit e%8 of qh[e/8].
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q5k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
-    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
-         b += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * wg_threads()) {
         float w[256];
         for (int i = 0; i < 256; ++i) w[i] = stdv * synth_normal(seed, b * 256 + i);
         float scl[8], mns[8], maxs = 0.0f, maxm = 0.0f;
@@ -505,8 +505,8 @@ k_synth_q5k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // The odd scale slots, which the reference ignores, hold 0x5A.
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q6k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
-    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
-         b += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
+         b += (uint64_t)gridDim.x * wg_threads()) {
         float w[256];
         for (int i = 0; i < 256; ++i) w[i] = stdv * synth_normal(seed, b * 256 + i);
         float scl[8], dmax = 0.0f;
@@ -565,8 +565,8 @@ k_synth_q6k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 extern "C" __global__ void __launch_bounds__(256)
 k_stream_read(const u32x4* __restrict__ src, uint64_t n16, uint32_t* __restrict__ sink) {
     uint32_t acc = 0;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t stride = (uint64_t)gridDim.x * wg_threads();
+    uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
     for (; i + 3 * stride < n16; i += 4 * stride) {
         u32x4 a = __builtin_nontemporal_load(src + i);
         u32x4 b = __builtin_nontemporal_load(src + i + stride);
@@ -580,12 +580,12 @@ k_stream_read(const u32x4* __restrict__ src, uint64_t n16, uint32_t* __restrict_
         acc ^= a.x ^ a.y ^ a.z ^ a.w;
     }
     for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o, 64);
-    if ((threadIdx.x & 63) == 0) sink[blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)] = acc;
+    if ((threadIdx.x & 63) == 0) sink[blockIdx.x * (wg_threads() / 64) + (threadIdx.x >> 6)] = acc;
 }
 
 extern "C" __global__ void __launch_bounds__(256)
 k_stream_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst, uint64_t n16) {
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+    const uint64_t stride = (uint64_t)gridDim.x * wg_threads();
+    for (uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; i < n16; i += stride)
         dst[i] = src[i];
 }

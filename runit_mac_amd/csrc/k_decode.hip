@@ -7,7 +7,7 @@
 // floats of LDS.  Every thread receives the total.
 RT_DEV float block_sum(float v, float* red) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    const uint32_t w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const uint32_t w = threadIdx.x >> 6, nw = wg_threads() >> 6;
     __syncthreads();  // previous users of `red` are done
     if ((threadIdx.x & 63) == 0) red[w] = v;
     __syncthreads();
@@ -17,7 +17,7 @@ RT_DEV float block_sum(float v, float* red) {
 }
 RT_DEV float block_max(float v, float* red) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    const uint32_t w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const uint32_t w = threadIdx.x >> 6, nw = wg_threads() >> 6;
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[w] = v;
     __syncthreads();
@@ -34,10 +34,10 @@ k_rms_norm_f32g(const float* x, float* y, const float* gamma, float eps, uint32_
     const float* xr = x + (size_t)blockIdx.x * hidden;
     float* yr = y + (size_t)blockIdx.x * hidden;
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) ss += xr[i] * xr[i];
+    for (uint32_t i = threadIdx.x; i < hidden; i += wg_threads()) ss += xr[i] * xr[i];
     ss = block_sum(ss, red);
     const float rms = rsqrtf(ss / (float)hidden + eps);
-    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) yr[i] = xr[i] * rms * gamma[i];
+    for (uint32_t i = threadIdx.x; i < hidden; i += wg_threads()) yr[i] = xr[i] * rms * gamma[i];
 }
 
 // RoPE angle for pair d (fused_rope.metal:34-38): freq = 1/θ^(2d/hd).
@@ -52,7 +52,7 @@ extern "C" __global__ void __launch_bounds__(256)
 k_rope_qk_f32(float* Q, float* K, uint32_t head_dim, uint32_t q_heads, uint32_t kv_heads,
               uint32_t pos, float theta) {
     const uint32_t half = head_dim / 2;
-    const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t d = blockIdx.x * wg_threads() + threadIdx.x;
     const uint32_t h = blockIdx.y;
     if (d >= half) return;
     float c, s;
@@ -75,7 +75,7 @@ k_rope_qk_f32(float* Q, float* K, uint32_t head_dim, uint32_t q_heads, uint32_t 
 extern "C" __global__ void __launch_bounds__(256)
 k_kv_copy_f32(const float* src, float* dst, uint32_t pos, uint32_t max_seq, uint32_t head_dim,
               uint32_t n) {
-    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t t = blockIdx.x * wg_threads() + threadIdx.x;
     if (t >= n) return;
     const uint32_t h = t / head_dim, d = t % head_dim;
     dst[((size_t)h * max_seq + pos) * head_dim + d] = src[t];
@@ -354,7 +354,7 @@ RT_ATTN_KERNELS(256)
 extern "C" __global__ void __launch_bounds__(256)
 k_embed_q8_0_f32(const uint8_t* table, const uint32_t* token, float* out, uint32_t k) {
     const size_t row = (size_t)token[0] * (k / 32) * 34;
-    for (uint32_t i = threadIdx.x + blockIdx.x * blockDim.x; i < k; i += blockDim.x * gridDim.x) {
+    for (uint32_t i = threadIdx.x + blockIdx.x * wg_threads(); i < k; i += wg_threads() * gridDim.x) {
         const uint8_t* blk = table + row + (i / 32) * 34;
         out[i] = __fmul_rn(h2f(*(const uint16_t*)blk), (float)(int8_t)blk[2 + (i & 31)]);
     }

@@ -40,8 +40,8 @@ RT_DEV void gemm_prep_body(const float* __restrict__ x, uint32_t M, uint32_t K, 
     const uint32_t nxb = K / 32;
     constexpr uint32_t ROWS = 4 * MG;
     const uint64_t total = (uint64_t)nchunks * ROWS * nxb * 8;
-    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
-         t += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t t = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; t < total;
+         t += (uint64_t)gridDim.x * wg_threads()) {
         const uint32_t q = t & 7;
         const uint64_t rb = t >> 3;  // (chunk row, block) pair
         const uint32_t b = (uint32_t)(rb % nxb);
@@ -231,9 +231,10 @@ struct Gemm2Args {
     const int* etab;
     float* y;
     float* part;          // [chunk][split][chunk rows][N] partial sums (splits > 1)
-    uint32_t* counters;   // [chunk][tile]
+    uint32_t* counters;   // [chunk][tile], cstride u32 slots apart
     uint32_t M, N, nxb, tiles, splits, kbs, nchunks;
     uint64_t row_bytes;
+    uint32_t cstride;
 };
 
 template <int MG, int NB>
@@ -354,7 +355,7 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
         }
         dev_stores_done();
         __syncthreads();
-        uint32_t* counter = a.counters + (size_t)ch * a.tiles + tile;
+        uint32_t* counter = a.counters + ((size_t)ch * a.tiles + tile) * a.cstride;
         if (tid == 0) last_flag = arrive(counter) == a.splits - 1;
         __syncthreads();
         if (!last_flag) continue;

@@ -34,6 +34,7 @@ struct GemvArgs {
     uint32_t kc_units;
     float* part;         // [ksplit][nvrows]
     uint32_t* counters;  // [tiles] arrival counters (reset by the last arriver)
+    uint32_t cstride;    // u32 slots between two tiles' counters (own cache lines)
 };
 
 // Tiles one workgroup may own in a K-split launch (the host keeps the grid's
@@ -219,7 +220,7 @@ RT_DEV void gemv_body_pipelined(const GemvArgs& a) {
     const uint32_t tid = threadIdx.x;
     const uint32_t TL = a.lpr;
     const uint32_t grp = tid / TL, kl = tid % TL;
-    const uint32_t vrows_per_wg = (blockDim.x / TL) * RPL;
+    const uint32_t vrows_per_wg = (wg_threads() / TL) * RPL;
     const uint32_t nxb = a.K / 32;
     const uint32_t ntiles = (a.nvrows + vrows_per_wg - 1) / vrows_per_wg;
     const uint32_t units = a.K / F::UNIT_EL;
@@ -304,7 +305,7 @@ RT_DEV void gemv_body_chunked(const GemvArgs& a) {
     const uint32_t tid = threadIdx.x;
     const uint32_t TL = a.lpr;
     const uint32_t grp = tid / TL, kl = tid % TL;
-    const uint32_t vrows_per_wg = (blockDim.x / TL) * RPL;
+    const uint32_t vrows_per_wg = (wg_threads() / TL) * RPL;
     const uint32_t nxb = a.K / 32;
     const uint32_t ntiles = (a.nvrows + vrows_per_wg - 1) / vrows_per_wg;
 
@@ -359,7 +360,7 @@ template <class F, int EPI, typename XT, int RQ, int PF>
 RT_DEV void gemv_mq_body(const GemvArgs& a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t lane = tid & 63, wave = tid >> 6, nwaves = wg_threads() >> 6;
     const uint32_t q = lane & 3, slot = lane >> 2;
     const uint32_t lq = q < 3 ? q : 2;  // the A row of lane q = 3 is a don't-care
     // K chunk of this workgroup (the whole K when ksplit = 1)
@@ -431,8 +432,10 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                          nxb, xp);
 #endif
     load_tile_aux(0);
+#ifndef RT_XFIRST
 #pragma unroll
     for (int h = 0; h < PF; ++h) issue(h, buf[h]);  // items past nitems load clamped addresses
+#endif
     RT_TP(1);
 #ifndef RT_PROBE_NO_STAGE
     // (the host launches whole-K kernels either with x records or with a K
@@ -442,8 +445,12 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     else
         copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
 #endif
+#ifdef RT_XFIRST
+#pragma unroll
+    for (int h = 0; h < PF; ++h) issue(h, buf[h]);
+#endif
     RT_TP(2);
-    __syncthreads();
+    lds_barrier();  // the records are in LDS; the weight loads stay in flight
     RT_TP(3);
     if (nitems == 0) return;
 
@@ -493,7 +500,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
 #pragma unroll
                             for (int rq = 0; rq < RQ; ++rq) red[(wave * RQ + rq) * 4 + q] = rsum[rq];
                         }
-                        __syncthreads();
+                        lds_barrier();
                         if (wk == 0) {
 #pragma unroll
                             for (int rq = 0; rq < RQ; ++rq) {
@@ -503,7 +510,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                                 rsum[rq] = t;
                             }
                         }
-                        __syncthreads();
+                        lds_barrier();
                     }
                     if (S > 1) {
                         // partial sums of this K chunk (the tiles are
@@ -541,15 +548,15 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
         __shared__ uint8_t last_of[kMaxSplitTiles];
         dev_stores_done();
         __syncthreads();
-        for (uint32_t t = tid; t < my_tiles; t += blockDim.x)
-            last_of[t] = arrive(a.counters + wg + t * nwg) == S - 1;
+        for (uint32_t t = tid; t < my_tiles; t += wg_threads())
+            last_of[t] = arrive(a.counters + (size_t)(wg + t * nwg) * a.cstride) == S - 1;
         __syncthreads();
         for (uint32_t t = 0; t < my_tiles; ++t) {
             if (!last_of[t]) continue;  // uniform
             const uint32_t tile = wg + t * nwg;
             const uint32_t vt = tile * vrows_per_wg;
             const uint32_t step_r = EPI == EPI_FFN ? 2 : 1;
-            for (uint32_t i = tid * step_r; i < vrows_per_wg; i += blockDim.x * step_r) {
+            for (uint32_t i = tid * step_r; i < vrows_per_wg; i += wg_threads() * step_r) {
                 const uint32_t vr = vt + i;
                 if (vr >= a.nvrows) break;
                 float v = 0.0f, v1 = 0.0f;
@@ -564,7 +571,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                     store_row<EPI>(a, vr, v);
                 }
             }
-            if (tid == 0) dev_store(a.counters + tile, 0u);  // ready for the next call
+            if (tid == 0) dev_store(a.counters + (size_t)tile * a.cstride, 0u);  // ready for the next call
         }
     }
 #ifdef RT_PROBE_TIMING
@@ -572,7 +579,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     __syncthreads();
     RT_TP(5);
     if (threadIdx.x == 0) {
-        uint32_t* o = (uint32_t*)a.out[0] + 5120 + blockIdx.x * 8;  // past the outputs
+        uint32_t* o = (uint32_t*)a.out[0] + 20480 + blockIdx.x * 8;  // past the outputs
         o[0] = (uint32_t)rt0;
         for (int i = 1; i < 6; ++i) o[i] = (uint32_t)(tp[i] - tp[0]);
         o[6] = (uint32_t)(__builtin_amdgcn_s_memrealtime() - rt0);
@@ -592,19 +599,34 @@ RT_DEV void gemv_body(const GemvArgs& a) {
 // MFMA kernels: whole-K (or K-split) launches use the matrix-core body with
 // unit format FM; launches whose K exceeds the LDS budget without a split use
 // the chunked v_dot4 body with unit format FC.
+// Items in flight per wave on the matrix-core path: a format may set PF.
+// Formats whose lanes each load a long unit (Q6_K: 212 bytes, Q8_0: 68) keep
+// one item in flight: with two, a wave's loads touch each cache line again
+// after it has left L1 (the lines of a unit are shared by the wave's
+// consecutive load instructions), and the stream slows down.
+template <class F>
+constexpr int fmt_pf_get(decltype(F::PF)*) { return F::PF; }
+template <class F>
+constexpr int fmt_pf_get(...) { return 0; }
+template <class F>
+constexpr int fmt_pf() { return fmt_pf_get<F>(nullptr); }
+
 template <class FM, class FC, int EPI, typename XT, int RQ, int RPL, int UNR>
 RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
     if (a.xb_chunk >= a.K / 32)
-        gemv_mq_body<FM, EPI, XT, RQ, (RQ == 1 ? GEMV_PF1 : GEMV_PF2)>(a);
+        gemv_mq_body<FM, EPI, XT, RQ, (fmt_pf<FM>() ? fmt_pf<FM>() : (RQ == 1 ? GEMV_PF1 : GEMV_PF2))>(a);
     else
         gemv_body_chunked<FC, EPI, XT, RPL, UNR>(a);
 }
 
+#ifndef RT_GEMV_LB
+#define RT_GEMV_LB 512
+#endif
 #define RT_GEMV_KERNEL2(NAME, FMTM, FMTC, EPI, XT, UNR)                                 \
-    extern "C" __global__ void __launch_bounds__(512) NAME##_r1(GemvArgs a) {         \
+    extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) NAME##_r1(GemvArgs a) {  \
         gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);  \
     }                                                                                   \
-    extern "C" __global__ void __launch_bounds__(512) NAME##_r2(GemvArgs a) {         \
+    extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) NAME##_r2(GemvArgs a) {  \
         gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);  \
     }
 #define RT_GEMV_KERNEL(NAME, FMT, EPI, XT, UNR) RT_GEMV_KERNEL2(NAME, FMT, FMT, EPI, XT, UNR)
@@ -685,8 +707,8 @@ RT_GEMV_KERNEL(k_ffn_q5k, FmtQ5K, EPI_FFN, float, 1)
 template <typename XT, bool Q40PERM>
 RT_DEV void act_limbs_body(const XT* __restrict__ x, XRec* __restrict__ out, uint32_t nxb) {
     const uint32_t total = nxb * 8;
-    for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < total;
-         t += gridDim.x * blockDim.x) {
+    for (uint32_t t = blockIdx.x * wg_threads() + threadIdx.x; t < total;
+         t += gridDim.x * wg_threads()) {
         float v[4];
         load_x4<XT>(x, (t >> 3) * 32 + (t & 7) * 4, v);
         limb_slice<Q40PERM>(v, t & 7, out + (t >> 3));

@@ -18,6 +18,24 @@
 
 #define RT_DEV __device__ __forceinline__
 
+// Threads per workgroup: one scalar load of the implicit-argument dword at
+// byte 12 (group_size_x in its low half), which arrives with the kernel
+// arguments.  blockDim.x compiles to a 16-bit vector load issued only after
+// the kernel arguments have arrived (a second round trip that every wave
+// waits for before its first load of real data).
+RT_DEV uint32_t wg_threads() {
+    const uint32_t* ia = (const uint32_t*)__builtin_amdgcn_implicitarg_ptr();
+    return ia[3] & 0xFFFFu;
+}
+
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS (and
+// scalar) operations, not for its global loads.  __syncthreads() also waits
+// for every outstanding global load, which stalls a kernel that has weight
+// loads in flight across the barrier until they all return.
+RT_DEV void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
@@ -266,7 +284,7 @@ template <typename XT, bool Q40PERM>
 RT_DEV void stage_x_limbs(const XT* __restrict__ x, uint32_t xb0, uint32_t nxb,
                           XRec* __restrict__ recs) {
     const uint32_t total = nxb * 8;
-    const uint32_t step = blockDim.x;
+    const uint32_t step = wg_threads();
     for (uint32_t t0 = threadIdx.x; t0 < total; t0 += XSTAGE_UNR * step) {
         float v[XSTAGE_UNR][4];
 #pragma unroll
@@ -288,7 +306,7 @@ RT_DEV void copy_x_limbs(const XRec* __restrict__ src, uint32_t xb0, uint32_t nx
     const u32x4* s = (const u32x4*)(src + xb0);
     u32x4* d = (u32x4*)recs;
     const uint32_t n16 = nxb * (sizeof(XRec) / 16);
-    for (uint32_t i = threadIdx.x; i < n16; i += blockDim.x) d[i] = s[i];
+    for (uint32_t i = threadIdx.x; i < n16; i += wg_threads()) d[i] = s[i];
 }
 
 // RMSNorm fused into the staging (rms_norm_f32_f32_f32g, norm.metal:126-154,
@@ -300,7 +318,7 @@ RT_DEV void stage_x_norm(const float* __restrict__ x, const float* __restrict__ 
                          uint32_t K, XRec* __restrict__ recs) {
     __shared__ float nred[16];
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x * 4; i < K; i += blockDim.x * 4) {
+    for (uint32_t i = threadIdx.x * 4; i < K; i += wg_threads() * 4) {
         const f32x4 v = *(const f32x4*)(x + i);
         ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
@@ -308,10 +326,10 @@ RT_DEV void stage_x_norm(const float* __restrict__ x, const float* __restrict__ 
     if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
-    for (uint32_t w = 0; w < (blockDim.x >> 6); ++w) tot += nred[w];
+    for (uint32_t w = 0; w < (wg_threads() >> 6); ++w) tot += nred[w];
     const float rms = rsqrtf(tot / (float)K + eps);
     const uint32_t total = (K / 32) * 8;
-    const uint32_t step = blockDim.x;
+    const uint32_t step = wg_threads();
     for (uint32_t t0 = threadIdx.x; t0 < total; t0 += XSTAGE_UNR * step) {
         float v[XSTAGE_UNR][4];
 #pragma unroll
@@ -340,19 +358,19 @@ RT_DEV void stage_x_norm(const float* __restrict__ x, const float* __restrict__ 
 // (and γ), the caller issues its weight loads, and stage_x_convert then
 // converts while those are in flight.
 //
-// Slice handled by this thread in round s: t = threadIdx.x + s·blockDim.x.
+// Slice handled by this thread in round s: t = threadIdx.x + s·wg_threads().
 // Threads past the end take slice q of block 0: their 8-lane groups rebuild
 // record 0 exactly as its owners do (the same values into the same words),
 // so no lane needs a branch.
 RT_DEV uint32_t stage_slice(int s, uint32_t total) {
-    const uint32_t t = threadIdx.x + s * blockDim.x;
+    const uint32_t t = threadIdx.x + s * wg_threads();
     return t < total ? t : (t & 7);
 }
 struct XPre {
     float v[XSTAGE_UNR][4];
     float g[XSTAGE_UNR][4];
 };
-RT_DEV bool stage_one_pass(uint32_t nxb) { return nxb * 8 <= XSTAGE_UNR * blockDim.x; }
+RT_DEV bool stage_one_pass(uint32_t nxb) { return nxb * 8 <= XSTAGE_UNR * wg_threads(); }
 
 template <typename XT>
 RT_DEV void stage_x_load(const XT* __restrict__ x, const float* __restrict__ gamma, uint32_t nxb,
@@ -362,7 +380,7 @@ RT_DEV void stage_x_load(const XT* __restrict__ x, const float* __restrict__ gam
     for (int s = 0; s < XSTAGE_UNR; ++s) {
         // rounds past the vector are skipped (workgroup-uniform: no lane of a
         // later load is conditional); lanes past the end load clamped addresses
-        if (s * blockDim.x >= total) break;
+        if (s * wg_threads() >= total) break;
         const uint32_t t = stage_slice(s, total);
         const uint32_t i = (t >> 3) * 32 + (t & 7) * 4;
         load_x4<XT>(x, i, p.v[s]);
@@ -386,13 +404,13 @@ RT_DEV void stage_x_convert(XPre& p, const float* gamma, float eps, uint32_t nxb
         for (int s = 0; s < XSTAGE_UNR; ++s) {
             const float sq = p.v[s][0] * p.v[s][0] + p.v[s][1] * p.v[s][1] +
                              p.v[s][2] * p.v[s][2] + p.v[s][3] * p.v[s][3];
-            ss += (threadIdx.x + s * blockDim.x < total) ? sq : 0.0f;
+            ss += (threadIdx.x + s * wg_threads() < total) ? sq : 0.0f;
         }
         ss = group_sum(ss, 64);
         if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
-        __syncthreads();
+        lds_barrier();
         float tot = 0.0f;
-        for (uint32_t w = 0; w < (blockDim.x >> 6); ++w) tot += nred[w];
+        for (uint32_t w = 0; w < (wg_threads() >> 6); ++w) tot += nred[w];
         const float rms = rsqrtf(tot / (float)(nxb * 32) + eps);
 #pragma unroll
         for (int s = 0; s < XSTAGE_UNR; ++s)
@@ -403,7 +421,7 @@ RT_DEV void stage_x_convert(XPre& p, const float* gamma, float eps, uint32_t nxb
     for (int s = 0; s < XSTAGE_UNR; ++s) {
         // rounds past the vector are skipped (workgroup-uniform); inside a
         // round, lanes past the end convert a copy of block 0 (see stage_slice)
-        if (s * blockDim.x < total) {
+        if (s * wg_threads() < total) {
             const uint32_t t = stage_slice(s, total);
             limb_slice<Q40PERM>(p.v[s], t & 7, recs + (t >> 3));
         }

@@ -98,6 +98,7 @@ RT_DEV float q8_0_block_dot(uint32_t d, const uint32_t q[8], const XRegs& x) {
 struct FmtQ8_0 {
     static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 34, UNIT_EL = 64;
     static constexpr bool Q40PERM = false;
+    static constexpr int PF = 1;  // matrix-core path: one item in flight per wave
     // held as whole dwordx4 tuples: element-wise copies out of a load's
     // destination would make the compiler wait for the load right away
     struct Raw {
@@ -472,6 +473,7 @@ struct FmtQ6K {
 struct FmtQ6KB {
     static constexpr uint32_t BLK_EL = 256, BLK_BYTES = 210, UNIT_EL = 256;
     static constexpr bool Q40PERM = false;
+    static constexpr int PF = 1;  // one item (212 bytes per lane) in flight per wave
     struct Raw { uint32_t w[53]; uint32_t sh; };
     RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
         const uintptr_t p = (uintptr_t)(row + (size_t)u * 210);

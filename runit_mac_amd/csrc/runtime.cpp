@@ -41,6 +41,7 @@ struct GemvArgs {
     uint32_t kc_units;
     float* part;
     uint32_t* counters;
+    uint32_t cstride;
 };
 
 constexpr uint32_t XREC_BYTES = 112;  // one activation record per 32 elements
@@ -348,7 +349,7 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         a.x = c->ws;
         a.x_rec = 1;
     }
-    const size_t red_bytes = 8 * 2 * 4 * sizeof(float);  // [waves ≤ 8][rows ≤ 2][4]
+    const size_t red_bytes = 16 * 2 * 4 * sizeof(float);  // [waves ≤ 16][rows ≤ 2][4]
     const size_t lds_cap = std::min<size_t>(c->max_lds, 80 * 1024) - red_bytes;
     // records staged per workgroup: the K chunk (split), else all of K if it
     // fits, else LDS-sized chunks (v_dot4 path)
@@ -392,6 +393,10 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
             if (st != RT_OK) return st;
             a.part = (float*)c->part;
             a.counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
+            // one 128-byte line per tile's counter while they fit: arrivals on
+            // one line serialise (≈11 ns each) at the end of the kernel
+            a.cstride = 32;
+            while (a.cstride > 1 && (size_t)ntiles * a.cstride > kAttnCounters) a.cstride >>= 1;
         }
     } else {
         // chunked (long-K) and single-block kernels: one row (FFN: one gate/up
@@ -529,7 +534,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
         c->max_lds = (size_t)lds;
     if (const char* ov = getenv("RUNIT_GEMV_PLAN")) {
         unsigned T = 0, TL = 0, r = 0;
-        if (sscanf(ov, "%u,%u,%u", &T, &TL, &r) == 3 && (T == 64 || T == 128 || T == 256 || T == 512) &&
+        if (sscanf(ov, "%u,%u,%u", &T, &TL, &r) == 3 && (T == 64 || T == 128 || T == 256 || T == 512 || T == 1024) &&
             TL >= 1 && TL <= T && (TL & (TL - 1)) == 0 && (r == 1 || r == 2))
             c->plan_override = Plan{T, TL, r};
     }
@@ -916,6 +921,7 @@ struct Gemm2Args {
     uint32_t* counters;
     uint32_t M, N, nxb, tiles, splits, kbs, nchunks;
     uint64_t row_bytes;
+    uint32_t cstride;
 };
 struct GemmArgs {
     const void* w;
@@ -992,8 +998,10 @@ int rt_gemm_q8_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_
         if (st != RT_OK) return st;
     }
     if (staged) {
+        uint32_t cstride = 32;  // counters on their own cache lines while they fit
+        while (cstride > 1 && (size_t)base * cstride > kAttnCounters) cstride >>= 1;
         Gemm2Args a2{w, aops, etab, y, part, (uint32_t*)((char*)c->aux + kAuxAttnOff),
-                     m_rows, n, nxb, tiles, splits, kbs, nchunks, (uint64_t)nxb * 34};
+                     m_rows, n, nxb, tiles, splits, kbs, nchunks, (uint64_t)nxb * 34, cstride};
         char kn2[48];
         snprintf(kn2, sizeof kn2, "k_gemm2_q8_0_mg%u", MG);
         void* p2[] = {&a2};
