@@ -122,13 +122,16 @@ struct AttnArgs {
     float scale, theta;
 };
 
-template <int HD, bool ROPE>
+template <int HD, bool ROPE, int HG>
 RT_DEV void attn_split(const AttnArgs& a) {
-    constexpr uint32_t GM = ATT_GM, SUB = ATT_SUB;
+    // HG groups of 256 threads share the block's query heads: group g takes
+    // heads g, g + HG, ... (shorter per-thread chains; every group reads the
+    // same K / V rows)
+    constexpr uint32_t GM = ATT_GM, SUB = ATT_SUB, NT = 256 * HG, HPT = GM / HG;
     constexpr uint32_t NQ = HD / 16;   // float4 per thread: K quarter row, V rows
     constexpr uint32_t C4 = HD / 4;    // float4 columns of a row
     constexpr uint32_t PG = 256 / C4;  // value position groups
-    static_assert(SUB == 64 && NQ * PG == SUB, "layout");
+    static_assert(SUB == 64 && NQ * PG == SUB && GM % HG == 0, "layout");
     __shared__ f32x4 qs4[GM][C4];
     __shared__ f32x4 ks4[C4], vs4[C4];
     __shared__ float sc[GM][SUB];
@@ -136,6 +139,7 @@ RT_DEV void attn_split(const AttnArgs& a) {
     __shared__ f32x4 ored[4][GM][C4];
     __shared__ uint32_t last_flag;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t hg = tid >> 8, lt = tid & 255, lw = w & 3;  // group, thread / wave in group
     const uint32_t s = blockIdx.x, nsp = gridDim.x, b = blockIdx.z;
     const uint32_t G = a.H / a.KVH, HB = (G + GM - 1) / GM;
     const uint32_t kvh = blockIdx.y / HB, hb = blockIdx.y % HB;
@@ -146,11 +150,29 @@ RT_DEV void attn_split(const AttnArgs& a) {
     float* vc = a.vc + kvb;
     const uint32_t p_begin = s * a.chunk, p_end = min(a.kv_len, p_begin + a.chunk);
     float* qsf = (float*)qs4;
+    const uint32_t kp = lt >> 2, kq = lt & 3;      // key layout
+    const uint32_t vcol = lt % C4, vg = lt / C4;  // value layout
+    // K / V rows of a step (rows past the range load row p_begin: in bounds,
+    // their scores are masked); the first step's loads are issued before the
+    // query staging, each later step's while the previous one computes
+    auto load_kv = [&](uint32_t p0, f32x4 (&kr)[NQ], f32x4 (&vr)[NQ]) {
+        const uint32_t pk = p0 + kp;
+        const f32x4* krow = (const f32x4*)(kc + (size_t)(pk < p_end ? pk : p_begin) * HD) + kq * NQ;
+#pragma unroll
+        for (uint32_t i = 0; i < NQ; ++i) kr[i] = krow[i];
+#pragma unroll
+        for (uint32_t i = 0; i < NQ; ++i) {
+            const uint32_t pv = p0 + vg + i * PG;
+            vr[i] = ((const f32x4*)(vc + (size_t)(pv < p_end ? pv : p_begin) * HD))[vcol];
+        }
+    };
+    f32x4 kr[NQ], vr[NQ];
+    if (p_begin < p_end) load_kv(p_begin, kr, vr);
     if constexpr (ROPE) {
         // fused_rope_qk_f32 (fused_rope.metal:28-55) on the block's query
         // heads and on the kv head's key
         constexpr uint32_t half = HD / 2;
-        for (uint32_t i = tid; i < (gh + 1) * half; i += 256) {
+        for (uint32_t i = tid; i < (gh + 1) * half; i += NT) {
             const uint32_t hh = i / half, d = i % half;
             float c, sn;
             rope_cs(d, HD, a.pos, a.theta, c, sn);
@@ -160,42 +182,33 @@ RT_DEV void attn_split(const AttnArgs& a) {
             dst[d] = r * c - im * sn;
             dst[d + half] = r * sn + im * c;
         }
-        for (uint32_t d = tid; d < HD; d += 256) ((float*)vs4)[d] = a.v_new[(size_t)kvh * HD + d];
+        for (uint32_t d = tid; d < HD; d += NT) ((float*)vs4)[d] = a.v_new[(size_t)kvh * HD + d];
     } else {
         const float* q = a.q + ((size_t)b * a.H + h0) * HD;
-        for (uint32_t i = tid; i < gh * HD; i += 256) qsf[i] = q[i];
+        for (uint32_t i = tid; i < gh * HD; i += NT) qsf[i] = q[i];
     }
     if (tid < GM) {
         m_run[tid] = -__builtin_huge_valf();
         l_run[tid] = 0.0f;
     }
-    __syncthreads();
+    lds_barrier();
     if constexpr (ROPE) {
         // kv_copy_to_cache_f32 (activation.metal:30-45) of the rotated key and
         // the value, by the one workgroup whose range holds `pos`
         if (hb == 0 && a.pos >= p_begin && a.pos < p_end)
-            for (uint32_t d = tid; d < HD; d += 256) {
+            for (uint32_t d = tid; d < HD; d += NT) {
                 kc[(size_t)a.pos * HD + d] = ((const float*)ks4)[d];
                 vc[(size_t)a.pos * HD + d] = ((const float*)vs4)[d];
             }
     }
-    f32x4 oacc[GM];
+    f32x4 oacc[HPT];  // heads hg + HG·j
 #pragma unroll
-    for (uint32_t h = 0; h < GM; ++h) oacc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const uint32_t kp = tid >> 2, kq = tid & 3;      // key layout
-    const uint32_t vcol = tid % C4, vg = tid / C4;  // value layout
+    for (uint32_t j = 0; j < HPT; ++j) oacc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t p0 = p_begin; p0 < p_end; p0 += SUB) {
-        f32x4 kr[NQ], vr[NQ];
         const uint32_t pk = p0 + kp;
         const bool kvalid = pk < p_end;
-        const f32x4* krow = (const f32x4*)(kc + (size_t)(kvalid ? pk : p_begin) * HD) + kq * NQ;
-#pragma unroll
-        for (uint32_t i = 0; i < NQ; ++i) kr[i] = krow[i];
-#pragma unroll
-        for (uint32_t i = 0; i < NQ; ++i) {
-            const uint32_t pv = p0 + vg + i * PG;
-            vr[i] = ((const f32x4*)(vc + (size_t)(pv < p_end ? pv : p_begin) * HD))[vcol];
-        }
+        f32x4 kn[NQ], vn[NQ];
+        if (p0 + SUB < p_end) load_kv(p0 + SUB, kn, vn);  // next step (workgroup-uniform)
         if constexpr (ROPE) {
             // position `pos` comes from LDS (the cache write above may not be
             // visible to this workgroup's loads, and other workgroups never
@@ -208,7 +221,8 @@ RT_DEV void attn_split(const AttnArgs& a) {
                 if (p0 + vg + i * PG == a.pos) vr[i] = vs4[vcol];
         }
 #pragma unroll
-        for (uint32_t h = 0; h < GM; ++h) {
+        for (uint32_t j = 0; j < HPT; ++j) {
+            const uint32_t h = hg + HG * j;
             if (h < gh) {
                 float dot = 0.0f;
 #pragma unroll
@@ -220,51 +234,56 @@ RT_DEV void attn_split(const AttnArgs& a) {
                 if (kq == 0) sc[h][kp] = kvalid ? dot * a.scale : -__builtin_huge_valf();
             }
         }
-        __syncthreads();
-        {
-            // wave w: query heads w and w + 4, interleaved
-            float sv[2], e[2], mx[2], sum[2];
+        lds_barrier();
+        // softmax: wave w takes query heads w, w + 4·HG (one or two per wave)
 #pragma unroll
-            for (uint32_t u = 0; u < 2; ++u) {
-                const uint32_t h = w + 4 * u;
-                sv[u] = h < gh ? sc[h][lane] : -__builtin_huge_valf();
-                mx[u] = group_max(sv[u], 64);
-            }
-#pragma unroll
-            for (uint32_t u = 0; u < 2; ++u) {
-                const uint32_t h = w + 4 * u;
-                const float m_old = h < gh ? m_run[h] : 0.0f, m_new = fmaxf(m_old, mx[u]);
-                e[u] = (sv[u] == -__builtin_huge_valf()) ? 0.0f : expf(sv[u] - m_new);
-                sum[u] = group_sum(e[u], 64);
+        for (uint32_t u = 0; u < (GM + 4 * HG - 1) / (4 * HG); ++u) {
+            const uint32_t h = w + 4 * HG * u;
+            if (h < GM) {  // wave-uniform
+                const float sv = h < gh ? sc[h][lane] : -__builtin_huge_valf();
+                const float mx = group_max(sv, 64);
+                const float m_old = h < gh ? m_run[h] : 0.0f, m_new = fmaxf(m_old, mx);
+                const float e = (sv == -__builtin_huge_valf()) ? 0.0f : expf(sv - m_new);
+                const float sum = group_sum(e, 64);
                 if (h < gh) {
-                    sc[h][lane] = e[u];
+                    sc[h][lane] = e;
                     if (lane == 0) {
                         const float r =
                             (m_old == -__builtin_huge_valf()) ? 0.0f : expf(m_old - m_new);
                         resc[h] = r;
-                        l_run[h] = l_run[h] * r + sum[u];
+                        l_run[h] = l_run[h] * r + sum;
                         m_run[h] = m_new;
                     }
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
-        for (uint32_t h = 0; h < GM; ++h) {
+        for (uint32_t j = 0; j < HPT; ++j) {
+            const uint32_t h = hg + HG * j;
             if (h < gh) {
-                f32x4 acc = oacc[h] * resc[h];
+                f32x4 acc = oacc[j] * resc[h];
 #pragma unroll
                 for (uint32_t i = 0; i < NQ; ++i) acc += sc[h][vg + i * PG] * vr[i];
-                oacc[h] = acc;
+                oacc[j] = acc;
             }
         }
-        __syncthreads();  // sc / resc reused by the next step
-    }
-    // sum the value position groups: within the wave, then over the 4 waves
+        lds_barrier();  // sc / resc reused by the next step
+        if (p0 + SUB < p_end) {
 #pragma unroll
-    for (uint32_t h = 0; h < GM; ++h) {
+            for (uint32_t i = 0; i < NQ; ++i) {
+                kr[i] = kn[i];
+                vr[i] = vn[i];
+            }
+        }
+    }
+    // sum the value position groups: within the wave, then over the group's
+    // 4 waves
+#pragma unroll
+    for (uint32_t j = 0; j < HPT; ++j) {
+        const uint32_t h = hg + HG * j;
         if (h < gh) {
-            f32x4 v = oacc[h];
+            f32x4 v = oacc[j];
             if constexpr (C4 == 16) {
                 v.x += swz_xor_f<16>(v.x);
                 v.y += swz_xor_f<16>(v.y);
@@ -277,11 +296,11 @@ RT_DEV void attn_split(const AttnArgs& a) {
                 v.z += __shfl_xor(v.z, 32, 64);
                 v.w += __shfl_xor(v.w, 32, 64);
             }
-            if (lane < C4) ored[w][h][lane] = v;
+            if (lane < C4) ored[lw][h][lane] = v;
         }
     }
-    __syncthreads();
-    for (uint32_t i = tid; i < gh * C4; i += 256) {
+    lds_barrier();
+    for (uint32_t i = tid; i < gh * C4; i += NT) {
         const uint32_t h = i / C4, c = i % C4;
         const f32x4 t = ored[0][h][c] + ored[1][h][c] + ored[2][h][c] + ored[3][h][c];
         if (nsp == 1) {
@@ -308,7 +327,7 @@ RT_DEV void attn_split(const AttnArgs& a) {
     __syncthreads();
     if (!last_flag) return;
     // merge the splits in split order: o = Σ o_s·e^(m_s−M) / Σ l_s·e^(m_s−M)
-    for (uint32_t i = tid; i < gh * C4; i += 256) {
+    for (uint32_t i = tid; i < gh * C4; i += NT) {
         const uint32_t h = i / C4, c = i % C4;
         const size_t row = ((size_t)b * a.H + h0 + h) * nsp;
         const float* mlv = a.ml + row * 2;
@@ -329,19 +348,17 @@ RT_DEV void attn_split(const AttnArgs& a) {
     if (tid == 0) dev_store(counter, 0u);  // ready for the next call (also under graph replay)
 }
 
-// decode_attention_f32 (attention.metal:248-308; dispatch.rs:1575-1612).
-// K/V cache: [batch][num_kv_heads][kv_head_stride][head_dim].  Instantiated
-// for head_dim 64, 128 and 256 (the host checks).
-//
-// k_attn_rope_f32_hd*: one new token at position `pos` (batch 1) — equivalent
-// to fused_rope_qk_f32 on (q, k), kv_copy_to_cache_f32 of k and v at `pos`,
-// then decode_attention_f32 with kv_len = pos + 1.
-#define RT_ATTN_KERNELS(HD)                                                                       \
-    extern "C" __global__ void __launch_bounds__(256) k_decode_attention_f32_hd##HD(AttnArgs a) { \
-        attn_split<HD, false>(a);                                                                  \
-    }                                                                                              \
-    extern "C" __global__ void __launch_bounds__(256) k_attn_rope_f32_hd##HD(AttnArgs a) {        \
-        attn_split<HD, true>(a);                                                                   \
+// Head groups per head size (threads = 256 · HG; registers bound HD 256 to one)
+template <int HD> constexpr int attn_hg() { return HD == 64 ? 4 : HD == 128 ? 2 : 1; }
+
+#define RT_ATTN_KERNELS(HD)                                                                \
+    extern "C" __global__ void __launch_bounds__(256 * attn_hg<HD>())                     \
+        k_decode_attention_f32_hd##HD(AttnArgs a) {                                        \
+        attn_split<HD, false, attn_hg<HD>()>(a);                                           \
+    }                                                                                      \
+    extern "C" __global__ void __launch_bounds__(256 * attn_hg<HD>())                     \
+        k_attn_rope_f32_hd##HD(AttnArgs a) {                                               \
+        attn_split<HD, true, attn_hg<HD>()>(a);                                            \
     }
 RT_ATTN_KERNELS(64)
 RT_ATTN_KERNELS(128)

@@ -155,6 +155,7 @@ struct rt_ctx {
     Plan plan_override{};
     uint32_t grid_per_cu = 0;  // RUNIT_GEMV_GRID_PER_CU: persistent-grid cap (sweeps only)
     uint32_t ksw_override = 0;  // RUNIT_GEMV_KSW: K-split waves (sweeps only)
+    uint32_t attn_split_override = 0;  // RUNIT_ATTN_SPLIT: most KV splits (sweeps only)
     bool gemm_direct = false;   // RUNIT_GEMM_DIRECT: force the unstaged GEMM kernel (tests)
     bool ksplit_enabled = true; // RUNIT_GEMV_KSPLIT=0: long K via the pre-pass instead (tests)
     // Workspace for activation records built by the long-K pre-pass; grows on
@@ -542,6 +543,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_PREPASS_K")) c->prepass_k = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_DIRECT")) c->gemm_direct = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_ATTN_SPLIT")) c->attn_split_override = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_KSW")) {
         const int v = atoi(g);
         if (v == 1 || v == 2 || v == 4 || v == 8) c->ksw_override = (uint32_t)v;
@@ -1215,7 +1217,8 @@ struct AttnArgs {
 static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch) {
     const uint32_t G = a.H / a.KVH, HB = (G + 7) / 8;
     const uint32_t groups = batch * a.KVH * HB;
-    const uint32_t max_split = std::max<uint32_t>(1, 2 * c->cu_count / groups);
+    uint32_t max_split = std::max<uint32_t>(1, 2 * c->cu_count / groups);
+    if (c->attn_split_override) max_split = c->attn_split_override;
     const uint32_t n64 = std::max<uint32_t>(1, (a.kv_len + 63) / 64);
     const uint32_t per = (n64 + max_split - 1) / max_split;
     a.chunk = per * 64;
@@ -1234,7 +1237,9 @@ static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch)
         a.counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
     }
     void* params[] = {&a};
-    return launch(c, kname, dim3(nsplit, a.KVH * HB, batch), dim3(256), 0, params);
+    // 256 threads per head group (the kernels' HG: 4 at head size 64, 2 at 128)
+    const uint32_t nt = strstr(kname, "hd64") ? 1024 : strstr(kname, "hd128") ? 512 : 256;
+    return launch(c, kname, dim3(nsplit, a.KVH * HB, batch), dim3(nt), 0, params);
 }
 
 int rt_decode_attention_f32(rt_ctx* c, const float* q, const float* k, const float* v, float* out,
