@@ -315,6 +315,19 @@ int rt_decode_attention_rope_f32(rt_ctx* ctx, const float* q_raw, const float* k
                                  const float* v_raw, float* k_cache, float* v_cache, float* out,
                                  uint32_t pos, uint32_t max_seq, uint32_t num_heads,
                                  uint32_t num_kv_heads, uint32_t head_dim, float theta);
+/* New: decode_attention_rope_f32 followed by gemv_q8_0_add_f32_f32in of the
+ * output projection (forward.rs:1588-1619), x_io += W_o · attention(...).
+ * When q_dim = num_heads·head_dim ≤ 1024 and the attention splits the KV
+ * range in 2..8 parts, each split writes its unnormalised output and
+ * (max, sum) and the projection merges them while staging its input (the
+ * attention's own merge, without its extra memory round trips); otherwise
+ * the two kernels run as in the unfused sequence.  w_o: [hidden, q_dim] Q8_0. */
+int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* ctx, const float* q_raw, const float* k_raw,
+                                            const float* v_raw, float* k_cache, float* v_cache,
+                                            const void* w_o, float* x_io, uint32_t pos,
+                                            uint32_t max_seq, uint32_t num_heads,
+                                            uint32_t num_kv_heads, uint32_t head_dim, float theta,
+                                            uint32_t hidden);
 /* New: out = dequant(table row *token) for a Q8_0 [vocab, k] table; the token
  * id is read from device memory (forward.rs:1494-1505 does this on the CPU). */
 int rt_embed_q8_0_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,

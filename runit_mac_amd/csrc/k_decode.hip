@@ -120,6 +120,8 @@ struct AttnArgs {
     uint32_t* counters;   //             [batch][KVH][HB] arrival counters
     uint32_t kv_len, stride, H, KVH, chunk, pos;
     float scale, theta;
+    uint32_t parts_only;  // write (o, m, l) of every split, merge nothing (the
+                          // consumer merges: k_gemv_q8_0_attn_f32add)
 };
 
 template <int HD, bool ROPE, int HG>
@@ -300,10 +302,11 @@ RT_DEV void attn_split(const AttnArgs& a) {
         }
     }
     lds_barrier();
+    const bool direct = nsp == 1 && !a.parts_only;
     for (uint32_t i = tid; i < gh * C4; i += NT) {
         const uint32_t h = i / C4, c = i % C4;
         const f32x4 t = ored[0][h][c] + ored[1][h][c] + ored[2][h][c] + ored[3][h][c];
-        if (nsp == 1) {
+        if (direct) {
             const float l = l_run[h];
             ((f32x4*)(a.out + ((size_t)b * a.H + h0 + h) * HD))[c] = t * (l > 0.0f ? 1.0f / l : 0.0f);
         } else {
@@ -314,12 +317,13 @@ RT_DEV void attn_split(const AttnArgs& a) {
             dev_store(pp + 3, t.w);
         }
     }
-    if (nsp == 1) return;
+    if (direct) return;
     if (tid < gh) {
         float* mlp = a.ml + (((size_t)b * a.H + h0 + tid) * nsp + s) * 2;
         dev_store(mlp + 0, m_run[tid]);
         dev_store(mlp + 1, l_run[tid]);
     }
+    if (a.parts_only) return;
     dev_stores_done();
     __syncthreads();
     uint32_t* counter = a.counters + ((size_t)b * a.KVH + kvh) * HB + hb;

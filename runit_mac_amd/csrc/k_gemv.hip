@@ -35,6 +35,10 @@ struct GemvArgs {
     float* part;         // [ksplit][nvrows]
     uint32_t* counters;  // [tiles] arrival counters (reset by the last arriver)
     uint32_t cstride;    // u32 slots between two tiles' counters (own cache lines)
+    // x given as split-attention partials (XT = AttnX): x = o[H][nsp][hd],
+    // xml = (m, l)[H][nsp]; staging merges them as the attention kernel does
+    const float* xml;
+    uint32_t xnsp, xhd;
 };
 
 // Tiles one workgroup may own in a K-split launch (the host keeps the grid's
@@ -426,25 +430,35 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     const uint32_t nxb = units * F::UNIT_EL / 32, xb0 = cu0 * F::UNIT_EL / 32;
     const bool one_pass = !a.x_rec && stage_one_pass(nxb);
     XPre xp;
+    XPreAttn xa;
+    if constexpr (is_attn_x<XT>()) {
+        // (the host launches this form with one slice round, whole K, nsp ≤ 8)
+        stage_attn_load(a.x, a.xml, a.xnsp, a.xhd, nxb, xa);
+    } else {
 #ifndef RT_PROBE_NO_STAGE
-    if (one_pass)
-        stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32, a.gamma ? a.gamma + (size_t)xb0 * 32 : nullptr,
-                         nxb, xp);
+        if (one_pass)
+            stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32,
+                             a.gamma ? a.gamma + (size_t)xb0 * 32 : nullptr, nxb, xp);
 #endif
+    }
     load_tile_aux(0);
 #ifndef RT_XFIRST
 #pragma unroll
     for (int h = 0; h < PF; ++h) issue(h, buf[h]);  // items past nitems load clamped addresses
 #endif
     RT_TP(1);
+    if constexpr (is_attn_x<XT>()) {
+        stage_attn_convert<F::Q40PERM>(xa, a.xnsp, nxb, xs);
+    } else {
 #ifndef RT_PROBE_NO_STAGE
-    // (the host launches whole-K kernels either with x records or with a K
-    // that one pass covers)
-    if (one_pass)
-        stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
-    else
-        copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
+        // (the host launches whole-K kernels either with x records or with a
+        // K that one pass covers)
+        if (one_pass)
+            stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
+        else
+            copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
 #endif
+    }
 #ifdef RT_XFIRST
 #pragma unroll
     for (int h = 0; h < PF; ++h) issue(h, buf[h]);
@@ -630,6 +644,17 @@ RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
         gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);  \
     }
 #define RT_GEMV_KERNEL(NAME, FMT, EPI, XT, UNR) RT_GEMV_KERNEL2(NAME, FMT, FMT, EPI, XT, UNR)
+// As RT_GEMV_KERNEL2, with a register budget for WPE waves per SIMD
+#define RT_GEMV_KERNEL2W(NAME, FMTM, FMTC, EPI, XT, UNR, WPE)                                \
+    extern "C" __global__ void __launch_bounds__(RT_GEMV_LB, WPE) NAME##_r1(GemvArgs a) {   \
+        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);      \
+    }                                                                                       \
+    extern "C" __global__ void __launch_bounds__(RT_GEMV_LB, WPE) NAME##_r2(GemvArgs a) {   \
+        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);      \
+    }
+#ifndef RT_Q6K_WPE
+#define RT_Q6K_WPE 2
+#endif
 
 // Single-block-unit fallback (rows with an odd number of 32-element blocks)
 #define RT_GEMV_KERNEL_S(NAME, FMT, EPI, XT, UNR)                                 \
@@ -680,9 +705,9 @@ RT_GEMV_KERNEL(k_gemv_q4k_f16_f32add, FmtQ4K, EPI_F32_ADD, uint16_t, 1)
 RT_GEMV_KERNEL(k_ffn_q4k, FmtQ4K, EPI_FFN, float, 1)
 // Q6_K (new: the reference runs Q6_K through f16-dequantised weights)
 // (matrix-core path: one super-block per lane; chunked path: 64-element units)
-RT_GEMV_KERNEL2(k_gemv_q6k_f32_f32, FmtQ6KB, FmtQ6K, EPI_F32, float, 1)
-RT_GEMV_KERNEL2(k_gemv_q6k_f32_f32add, FmtQ6KB, FmtQ6K, EPI_F32_ADD, float, 1)
-RT_GEMV_KERNEL2(k_gemv_q6k_f32_f16, FmtQ6KB, FmtQ6K, EPI_F16, float, 1)
+RT_GEMV_KERNEL2W(k_gemv_q6k_f32_f32, FmtQ6KB, FmtQ6K, EPI_F32, float, 1, RT_Q6K_WPE)
+RT_GEMV_KERNEL2W(k_gemv_q6k_f32_f32add, FmtQ6KB, FmtQ6K, EPI_F32_ADD, float, 1, RT_Q6K_WPE)
+RT_GEMV_KERNEL2W(k_gemv_q6k_f32_f16, FmtQ6KB, FmtQ6K, EPI_F16, float, 1, RT_Q6K_WPE)
 
 // Q5_0 / Q5_K (new: the reference dequantises both on the CPU,
 // forward.rs:900-920 and 979-1012)
@@ -701,6 +726,13 @@ RT_GEMV_KERNEL(k_gemv_q5k_f32_f32add, FmtQ5K, EPI_F32_ADD, float, 1)
 RT_GEMV_KERNEL(k_gemv_q5k_f32_f16, FmtQ5K, EPI_F16, float, 1)
 RT_GEMV_KERNEL(k_qkv_bias_q5k, FmtQ5K, EPI_QKV_BIAS, float, 1)
 RT_GEMV_KERNEL(k_ffn_q5k, FmtQ5K, EPI_FFN, float, 1)
+
+// Attention output projection with the split merge folded into the staging
+// (decode_attention's merge, then gemv_q8_0_add_f32_f32in: forward.rs:1588-
+// 1619); one workgroup form only (matrix-core body, whole K, one slice round).
+extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) k_gemv_q8_0_attn_f32add_r1(GemvArgs a) {
+    gemv_mq_body<FmtQ8_0, EPI_F32_ADD, AttnX, 1, fmt_pf<FmtQ8_0>()>(a);
+}
 
 // Activation pre-pass: builds the limb records of x (nxb records) in global
 // memory once, for launches whose K is too long to convert per workgroup.

@@ -428,6 +428,58 @@ RT_DEV void stage_x_convert(XPre& p, const float* gamma, float eps, uint32_t nxb
     }
 }
 
+// x as split-attention partials: the slice of round 0 (one round only) loads
+// (o, m, l) of up to 8 splits, and the conversion merges them exactly as the
+// attention kernel's last workgroup does (o = Σ o_s·e^(m_s−M) / Σ l_s·e^(m_s−M),
+// splits in order), then builds the slice's limbs.
+struct AttnX {};
+template <typename XT>
+constexpr bool is_attn_x() { return __is_same(XT, AttnX); }
+constexpr uint32_t kAttnXMaxSplits = 8;
+struct XPreAttn {
+    f32x4 o[kAttnXMaxSplits];
+    float m[kAttnXMaxSplits], l[kAttnXMaxSplits];
+};
+RT_DEV void stage_attn_load(const void* part, const float* ml, uint32_t nsp, uint32_t hd,
+                            uint32_t nxb, XPreAttn& p) {
+    const uint32_t t = stage_slice(0, nxb * 8);
+    const uint32_t i = (t >> 3) * 32 + (t & 7) * 4;  // 4 elements of one head
+    const uint32_t h = i / hd, d = i % hd;
+#pragma unroll
+    for (uint32_t j = 0; j < kAttnXMaxSplits; ++j) {
+        // splits past nsp load split nsp − 1 again (unconditional loads; the
+        // merge ignores them)
+        const uint32_t jj = j < nsp ? j : nsp - 1;
+        const size_t row = (size_t)h * nsp + jj;
+        p.o[j] = *(const f32x4*)((const float*)part + row * hd + d);
+        const float2 v = *(const float2*)(ml + row * 2);
+        p.m[j] = v.x;
+        p.l[j] = v.y;
+    }
+}
+template <bool Q40PERM>
+RT_DEV void stage_attn_convert(const XPreAttn& p, uint32_t nsp, uint32_t nxb,
+                               XRec* __restrict__ recs) {
+    const uint32_t t = stage_slice(0, nxb * 8);
+    float M = -__builtin_huge_valf();
+#pragma unroll
+    for (uint32_t j = 0; j < kAttnXMaxSplits; ++j)
+        if (j < nsp) M = fmaxf(M, p.m[j]);
+    float L = 0.0f;
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t j = 0; j < kAttnXMaxSplits; ++j) {
+        if (j < nsp) {
+            const float f = expf(p.m[j] - M);
+            L += p.l[j] * f;
+            o += p.o[j] * f;
+        }
+    }
+    o = o * (L > 0.0f ? 1.0f / L : 0.0f);
+    float v[4] = {o.x, o.y, o.z, o.w};
+    limb_slice<Q40PERM>(v, t & 7, recs + (t >> 3));
+}
+
 // Stages activations for x-blocks [xb0, xb0+nxb): from f32/f16 values, from
 // RMSNorm(x) (gamma != null, whole K only), or from records that an earlier
 // kernel already built (x_rec).

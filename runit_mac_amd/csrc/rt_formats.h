@@ -489,17 +489,13 @@ struct FmtQ6KB {
         const float d = h2f(r.w[52] >> (8 * r.sh));  // bytes 208-209
         float acc = 0.0f;
 #pragma unroll 1
-        for (int hs = 0; hs < 2; ++hs) {  // (rolled: one half's limbs live at a time)
+        for (int hs = 0; hs < 2; ++hs) {  // (rolled: one half's operands live at a time)
             const XRec* rec = xs + 8 * uu + 4 * hs;
             v4i c[4];
-            uint32_t xl[4][8];
             int e[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const u32x4* p = (const u32x4*)(rec + t);
-                const u32x4 a = p[2 * lq], b = p[2 * lq + 1], m = p[6];
-                xl[t][0] = a.x; xl[t][1] = a.y; xl[t][2] = a.z; xl[t][3] = a.w;
-                xl[t][4] = b.x; xl[t][5] = b.y; xl[t][6] = b.z; xl[t][7] = b.w;
+                const u32x4 m = ((const u32x4*)(rec + t))[6];
                 e[t] = (int)(int16_t)(m.x & 0xFFFF);
                 // codes are 0..63; −32·Σx over the record seeds the accumulators
                 const int s0 = (int16_t)(m.x >> 16) + (int16_t)(m.z & 0xFFFF);
@@ -509,14 +505,18 @@ struct FmtQ6KB {
             }
 #pragma unroll
             for (int g = 0; g < 8; ++g) {
+                // limb dword g of the four records, read where it is used
+                uint32_t xl[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xl[t] = ((const uint32_t*)(rec + t))[8 * lq + g];
                 // (both halves' offsets are constants; the rolled loop selects)
                 const uint32_t ql = hs ? get(r, 64 + 4 * g) : get(r, 4 * g);
                 const uint32_t ql32 = hs ? get(r, 96 + 4 * g) : get(r, 32 + 4 * g);
                 const uint32_t qh = hs ? get(r, 160 + 4 * g) : get(r, 128 + 4 * g);
-                c[0] = mfma4(xl[0][g], (ql & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u), c[0]);
-                c[1] = mfma4(xl[1][g], (ql32 & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u), c[1]);
-                c[2] = mfma4(xl[2][g], ((ql >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u), c[2]);
-                c[3] = mfma4(xl[3][g], ((ql32 >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u), c[3]);
+                c[0] = mfma4(xl[0], (ql & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u), c[0]);
+                c[1] = mfma4(xl[1], (ql32 & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u), c[1]);
+                c[2] = mfma4(xl[2], ((ql >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u), c[2]);
+                c[3] = mfma4(xl[3], ((ql32 >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u), c[3]);
             }
             // scales sc[8·hs + 2t]: bytes 192 + 8·hs + {0, 2, 4, 6}
             const uint32_t sa = hs ? get(r, 200) : get(r, 192);

@@ -42,9 +42,12 @@ struct GemvArgs {
     float* part;
     uint32_t* counters;
     uint32_t cstride;
+    const float* xml;
+    uint32_t xnsp, xhd;
 };
 
-constexpr uint32_t XREC_BYTES = 112;  // one activation record per 32 elements
+constexpr uint32_t XREC_BYTES = 112;
+constexpr uint32_t kAttnXMaxSplits = 8;  // splits the merging projection stages  // one activation record per 32 elements
 // argmax: 256 workgroup states of 12 bytes, then the arrival counter
 constexpr uint32_t kArgmaxWgs = 256;
 constexpr uint32_t kOnePassMaxK = 8192;  // 512 threads × 4 slices × 4 elements
@@ -56,7 +59,7 @@ constexpr size_t kAuxBytes = 65536;
 constexpr uint32_t kAttnCounters = (kAuxBytes - kAuxAttnOff) / 4;
 
 const char* const kKernelNames[] = {
-    "k_gemv_q8_0_f32_f32_r1", "k_gemv_q8_0_f32_f32_r2",
+    "k_gemv_q8_0_f32_f32_r1", "k_gemv_q8_0_f32_f32_r2", "k_gemv_q8_0_attn_f32add_r1",
     "k_gemv_q8_0_f32_f32add_r1", "k_gemv_q8_0_f32_f32add_r2",
     "k_gemv_q8_0_f32_f16_r1", "k_gemv_q8_0_f32_f16_r2",
     "k_gemv_q8_0_f16_f16_r1", "k_gemv_q8_0_f16_f16_r2",
@@ -165,6 +168,8 @@ struct rt_ctx {
     std::unordered_map<std::string, uint32_t> occ;  // occupancy cache
     void* part = nullptr;  // K-split GEMV partial sums
     size_t part_bytes = 0;
+    void* attn_out = nullptr;  // attention output between the two launches of
+    size_t attn_out_bytes = 0;  // the unmerged attention + o_proj sequence
     uint32_t prepass_k = 8192;  // RUNIT_PREPASS_K: K from which x is converted once
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
@@ -325,13 +330,13 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
     // workgroups in chunks of kKSplitElems, each staged in one pass; the
     // partial sums meet in the workspace.
     uint32_t S = 1, kcu = units;
-    if (mq_shape && c->ksplit_enabled && !a.x_rec && !a.gamma && a.K > kOnePassMaxK) {
+    if (mq_shape && c->ksplit_enabled && !a.x_rec && !a.gamma && !a.xnsp && a.K > kOnePassMaxK) {
         kcu = kKSplitElems / mq_el;
         S = (units + kcu - 1) / kcu;
     }
     a.ksplit = S;
     a.kc_units = kcu;
-    if (S == 1 && !a.x_rec && !a.gamma &&
+    if (S == 1 && !a.x_rec && !a.gamma && !a.xnsp &&
         (a.K >= c->prepass_k || (mq_shape && a.K > kOnePassMaxK))) {
         // convert the activations once into the context workspace
         const size_t need = (size_t)nxb * XREC_BYTES;
@@ -595,6 +600,7 @@ void rt_ctx_destroy(rt_ctx* c) {
     }
     if (c->ws) hipFree(c->ws);
     if (c->part) hipFree(c->part);
+    if (c->attn_out) hipFree(c->attn_out);
     if (c->aux) hipFree(c->aux);
     if (c->module) hipModuleUnload(c->module);
     delete c;
@@ -1210,20 +1216,32 @@ struct AttnArgs {
     uint32_t* counters;
     uint32_t kv_len, stride, H, KVH, chunk, pos;
     float scale, theta;
+    uint32_t parts_only;
 };
 
 // Splits kv_len into ranges of a multiple of 64 positions so that the grid
 // holds about two workgroups per CU; sizes the partial-output workspace.
-static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch) {
-    const uint32_t G = a.H / a.KVH, HB = (G + 7) / 8;
-    const uint32_t groups = batch * a.KVH * HB;
+// KV positions per split (a multiple of 64): as many splits as give the
+// head groups about two workgroups per CU
+static uint32_t attn_chunk(rt_ctx* c, uint32_t kv_len, uint32_t groups, uint32_t max_split_cap = 0) {
     uint32_t max_split = std::max<uint32_t>(1, 2 * c->cu_count / groups);
     if (c->attn_split_override) max_split = c->attn_split_override;
-    const uint32_t n64 = std::max<uint32_t>(1, (a.kv_len + 63) / 64);
-    const uint32_t per = (n64 + max_split - 1) / max_split;
-    a.chunk = per * 64;
+    if (max_split_cap) max_split = std::min(max_split, max_split_cap);
+    const uint32_t n64 = std::max<uint32_t>(1, (kv_len + 63) / 64);
+    return (n64 + max_split - 1) / max_split * 64;
+}
+static uint32_t attn_nsplit(rt_ctx* c, uint32_t kv_len, uint32_t groups) {
+    const uint32_t chunk = attn_chunk(c, kv_len, groups);
+    return kv_len ? (kv_len + chunk - 1) / chunk : 1;
+}
+
+static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch,
+                       uint32_t max_split_cap = 0, AttnArgs* used = nullptr) {
+    const uint32_t G = a.H / a.KVH, HB = (G + 7) / 8;
+    const uint32_t groups = batch * a.KVH * HB;
+    a.chunk = attn_chunk(c, a.kv_len, groups, max_split_cap);
     const uint32_t nsplit = a.kv_len ? (a.kv_len + a.chunk - 1) / a.chunk : 1;
-    if (nsplit > 1) {
+    if (nsplit > 1 || a.parts_only) {
         if (groups > kAttnCounters)
             return fail(c, RT_ERR_DISPATCH,
                         "kernel dispatch error: attention: %u head groups exceed %u", groups,
@@ -1236,6 +1254,7 @@ static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch)
         a.ml = a.part + rows * hd;
         a.counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
     }
+    if (used) *used = a;
     void* params[] = {&a};
     // 256 threads per head group (the kernels' HG: 4 at head size 64, 2 at 128)
     const uint32_t nt = strstr(kname, "hd64") ? 1024 : strstr(kname, "hd128") ? 512 : 256;
@@ -1300,6 +1319,72 @@ int rt_decode_attention_rope_f32(rt_ctx* c, const float* q_raw, const float* k_r
     char kn[64];
     snprintf(kn, sizeof kn, "k_attn_rope_f32_hd%u", head_dim);
     return attn_launch(c, kn, a, 1);
+}
+
+int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const float* k_raw,
+                                            const float* v_raw, float* k_cache, float* v_cache,
+                                            const void* w_o, float* x_io, uint32_t pos,
+                                            uint32_t max_seq, uint32_t num_heads,
+                                            uint32_t num_kv_heads, uint32_t head_dim, float theta,
+                                            uint32_t hidden) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (num_heads == 0 || hidden == 0) return RT_OK;
+    int st = attn_check(c, num_heads, num_kv_heads, head_dim);
+    if (st != RT_OK) return st;
+    if (!q_raw || !k_raw || !v_raw || !k_cache || !v_cache || !w_o || !x_io)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: attention_oproj: null buffer");
+    if (pos >= max_seq)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: attention: pos=%u ≥ max_seq=%u",
+                    pos, max_seq);
+    const uint32_t q_dim = num_heads * head_dim;
+    if (!aligned(x_io, 16))
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: attention_oproj: x must be 16-byte aligned");
+    // The merged form needs the projection to stage in one slice round of a
+    // 256-thread workgroup (q_dim ≤ 1024) and pays off while the attention
+    // splits the KV range in 2..8 (one split has no merge to save; more
+    // splits than the projection stages would slow the attention down);
+    // otherwise: attention, then the GEMV.
+    const uint32_t nsplit0 = attn_nsplit(c, pos + 1, num_kv_heads * ((num_heads / num_kv_heads + 7) / 8));
+    const bool merged = q_dim % 64 == 0 && q_dim / 32 * 8 <= 256 && !c->plan_override.T &&
+                        nsplit0 >= 2 && nsplit0 <= kAttnXMaxSplits;
+    AttnArgs a{};
+    a.q = q_raw;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.k_new = k_raw;
+    a.v_new = v_raw;
+    a.kv_len = pos + 1;
+    a.stride = max_seq;
+    a.H = num_heads;
+    a.KVH = num_kv_heads;
+    a.pos = pos;
+    a.scale = 1.0f / sqrtf((float)head_dim);
+    a.theta = theta;
+    char kn[64];
+    snprintf(kn, sizeof kn, "k_attn_rope_f32_hd%u", head_dim);
+    if (!merged) {
+        // attention (with its own merge) into a context buffer, then the
+        // plain projection
+        st = ensure_buf(c, c->attn_out, c->attn_out_bytes, (size_t)q_dim * sizeof(float),
+                        "attention_oproj");
+        if (st != RT_OK) return st;
+        a.out = (float*)c->attn_out;
+        st = attn_launch(c, kn, a, 1);
+        if (st != RT_OK) return st;
+        return rt_gemv_q8_0_add_f32_f32in(c, w_o, (const float*)c->attn_out, x_io, x_io, hidden,
+                                          q_dim);
+    }
+    a.parts_only = 1;
+    AttnArgs used{};
+    st = attn_launch(c, kn, a, 1, kAttnXMaxSplits, &used);
+    if (st != RT_OK) return st;
+    const uint32_t nsplit = (a.kv_len + used.chunk - 1) / used.chunk;
+    GemvArgs g = plain_args(w_o, used.part, x_io, x_io, hidden, q_dim);
+    g.xml = used.ml;
+    g.xnsp = nsplit;
+    g.xhd = head_dim;
+    return gemv_launch(c, "k_gemv_q8_0_attn_f32add", kQ8_0, g, false);
 }
 
 int rt_embed_q8_0_f32(rt_ctx* c, const void* table, const uint32_t* token, float* out, uint32_t k) {

@@ -250,9 +250,9 @@ class DecodeModel:
             d.rms_norm_fused_qkv_bias_q8_0_f32(ctx, L["wq"], L["wk"], L["wv"], self.x,
                                                L["attn_norm"], c.eps, self.q, self.k, self.v,
                                                L["bq"], L["bk"], L["bv"], q_dim, kv_dim, h)
-            d.decode_attention_rope_f32(ctx, self.q, self.k, self.v, L["kc"], L["vc"], self.attn,
-                                        pos, c.max_seq, c.heads, c.kv_heads, c.head_dim, c.theta)
-            d.gemv_q8_0_add_f32_f32in(ctx, L["wo"], self.attn, self.x, self.x, h, q_dim)
+            d.decode_attention_rope_oproj_q8_0_f32(ctx, self.q, self.k, self.v, L["kc"], L["vc"],
+                                                   L["wo"], self.x, pos, c.max_seq, c.heads,
+                                                   c.kv_heads, c.head_dim, c.theta, h)
             d.rms_norm_fused_ffn_q8_0_f32(ctx, L["wg"], L["wu"], self.x, L["ffn_norm"], c.eps,
                                           self.act, c.ff, h)
             d.gemv_q8_0_add_f32_f32in(ctx, L["wd"], self.act, self.x, self.x, h, c.ff)

@@ -112,6 +112,7 @@ _SIGS = {
     "rt_kv_copy_to_cache_f32": [_P, _P, _P, _U32, _U32, _U32, _U32],
     "rt_decode_attention_f32": [_P, _P, _P, _P, _P] + [_U32] * 6,
     "rt_decode_attention_rope_f32": [_P] + [_P] * 6 + [_U32] * 5 + [_F],
+    "rt_decode_attention_rope_oproj_q8_0_f32": [_P] + [_P] * 7 + [_U32] * 5 + [_F, _U32],
     "rt_embed_q8_0_f32": [_P, _P, _P, _P, _U32],
     "rt_rms_norm_fused_qkv_bias_q8_0_f32": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 + [_U32] * 3,
     "rt_rms_norm_fused_ffn_q8_0_f32": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32],
@@ -519,6 +520,16 @@ def decode_attention_rope_f32(ctx, q_raw, k_raw, v_raw, k_cache, v_cache, out, p
     _call(ctx, "rt_decode_attention_rope_f32", *map(_ptr, (q_raw, k_raw, v_raw, k_cache, v_cache,
                                                            out)),
           pos, max_seq, num_heads, num_kv_heads, head_dim, theta)
+
+
+def decode_attention_rope_oproj_q8_0_f32(ctx, q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io,
+                                         pos, max_seq, num_heads, num_kv_heads, head_dim, theta,
+                                         hidden):
+    """Attention (RoPE, KV write) and x_io += W_o·attention in two launches,
+    the split merge folded into the projection's staging (new)."""
+    _call(ctx, "rt_decode_attention_rope_oproj_q8_0_f32",
+          *map(_ptr, (q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io)), pos, max_seq,
+          num_heads, num_kv_heads, head_dim, theta, hidden)
 
 
 def embed_q8_0_f32(ctx, table, token, out, k):
