@@ -633,8 +633,12 @@ RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
         gemv_body_chunked<FC, EPI, XT, RPL, UNR>(a);
 }
 
+// Thread bound of the GEMV kernels: 1024-thread workgroups (one per CU) serve
+// the large whole-K launches, whose waves then issue their first loads
+// together instead of queueing behind the weight loads of earlier
+// workgroups on the CU (the register budget stays at 128 per lane).
 #ifndef RT_GEMV_LB
-#define RT_GEMV_LB 512
+#define RT_GEMV_LB 1024
 #endif
 #define RT_GEMV_KERNEL2(NAME, FMTM, FMTC, EPI, XT, UNR)                                 \
     extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) NAME##_r1(GemvArgs a) {  \
@@ -644,13 +648,22 @@ RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
         gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);  \
     }
 #define RT_GEMV_KERNEL(NAME, FMT, EPI, XT, UNR) RT_GEMV_KERNEL2(NAME, FMT, FMT, EPI, XT, UNR)
-// As RT_GEMV_KERNEL2, with a register budget for WPE waves per SIMD
+// As RT_GEMV_KERNEL2, for at most 512 threads with a register budget for WPE
+// waves per SIMD (Q6_K: a whole super-block per lane needs ~240 registers)
 #define RT_GEMV_KERNEL2W(NAME, FMTM, FMTC, EPI, XT, UNR, WPE)                                \
-    extern "C" __global__ void __launch_bounds__(RT_GEMV_LB, WPE) NAME##_r1(GemvArgs a) {   \
+    extern "C" __global__ void __launch_bounds__(512, WPE) NAME##_r1(GemvArgs a) {          \
         gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);      \
     }                                                                                       \
-    extern "C" __global__ void __launch_bounds__(RT_GEMV_LB, WPE) NAME##_r2(GemvArgs a) {   \
+    extern "C" __global__ void __launch_bounds__(512, WPE) NAME##_r2(GemvArgs a) {          \
         gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);      \
+    }
+// Formats that never take the 1024-thread form (Q8_0): built for 512 threads
+#define RT_GEMV_KERNEL512(NAME, FMT, EPI, XT, UNR)                                         \
+    extern "C" __global__ void __launch_bounds__(512) NAME##_r1(GemvArgs a) {              \
+        gemv_mq_or_chunked<FMT, FMT, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);        \
+    }                                                                                       \
+    extern "C" __global__ void __launch_bounds__(512) NAME##_r2(GemvArgs a) {              \
+        gemv_mq_or_chunked<FMT, FMT, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);        \
     }
 #ifndef RT_Q6K_WPE
 #define RT_Q6K_WPE 2
@@ -663,15 +676,15 @@ RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
     }
 
 // Q8_0 (gemv_q8_0.metal, gemv_multirow.metal, fused_qkv.metal, fused_ffn.metal)
-RT_GEMV_KERNEL(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float, 1)
-RT_GEMV_KERNEL(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float, 1)
-RT_GEMV_KERNEL(k_gemv_q8_0_f32_f16, FmtQ8_0, EPI_F16, float, 1)
-RT_GEMV_KERNEL(k_gemv_q8_0_f16_f16, FmtQ8_0, EPI_F16, uint16_t, 1)
-RT_GEMV_KERNEL(k_gemv_q8_0_f16_f16add, FmtQ8_0, EPI_F16_ADD, uint16_t, 1)
-RT_GEMV_KERNEL(k_gemv_q8_0_f16_f32add, FmtQ8_0, EPI_F32_ADD, uint16_t, 1)
-RT_GEMV_KERNEL(k_qkv_q8_0, FmtQ8_0, EPI_QKV, float, 1)
-RT_GEMV_KERNEL(k_qkv_bias_q8_0, FmtQ8_0, EPI_QKV_BIAS, float, 1)
-RT_GEMV_KERNEL(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float, 1)
+RT_GEMV_KERNEL512(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float, 1)
+RT_GEMV_KERNEL512(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float, 1)
+RT_GEMV_KERNEL512(k_gemv_q8_0_f32_f16, FmtQ8_0, EPI_F16, float, 1)
+RT_GEMV_KERNEL512(k_gemv_q8_0_f16_f16, FmtQ8_0, EPI_F16, uint16_t, 1)
+RT_GEMV_KERNEL512(k_gemv_q8_0_f16_f16add, FmtQ8_0, EPI_F16_ADD, uint16_t, 1)
+RT_GEMV_KERNEL512(k_gemv_q8_0_f16_f32add, FmtQ8_0, EPI_F32_ADD, uint16_t, 1)
+RT_GEMV_KERNEL512(k_qkv_q8_0, FmtQ8_0, EPI_QKV, float, 1)
+RT_GEMV_KERNEL512(k_qkv_bias_q8_0, FmtQ8_0, EPI_QKV_BIAS, float, 1)
+RT_GEMV_KERNEL512(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float, 1)
 // Q4_0 (gemv_q4_0.metal)
 RT_GEMV_KERNEL(k_gemv_q4_0_f32_f32, FmtQ4_0, EPI_F32, float, 2)
 RT_GEMV_KERNEL(k_gemv_q4_0_f32_f32add, FmtQ4_0, EPI_F32_ADD, float, 2)
@@ -730,7 +743,7 @@ RT_GEMV_KERNEL(k_ffn_q5k, FmtQ5K, EPI_FFN, float, 1)
 // Attention output projection with the split merge folded into the staging
 // (decode_attention's merge, then gemv_q8_0_add_f32_f32in: forward.rs:1588-
 // 1619); one workgroup form only (matrix-core body, whole K, one slice round).
-extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) k_gemv_q8_0_attn_f32add_r1(GemvArgs a) {
+extern "C" __global__ void __launch_bounds__(512) k_gemv_q8_0_attn_f32add_r1(GemvArgs a) {
     gemv_mq_body<FmtQ8_0, EPI_F32_ADD, AttnX, 1, fmt_pf<FmtQ8_0>()>(a);
 }
 

@@ -374,6 +374,13 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         p = Plan{256, 16, 1};
         if (c->plan_override.T) p = Plan{c->plan_override.T, 16, c->plan_override.rpl};
         if (!a.x_rec && recs * 8 > 4 * p.T) p.T = 512;  // one staging pass
+        // large whole-K launches of the two-items-in-flight formats (4- and
+        // 5-bit): one 1024-thread workgroup per CU, whose 16 waves issue
+        // their activation loads before any weight load of the CU.  (Q8_0
+        // and Q6_K keep one item in flight per wave and run slower so; Q6_K's
+        // ~240-register kernels are built for 512 threads.)
+        const bool one_item = f.blk_bytes == 34 || mq_el == 256;
+        if (!c->plan_override.T && S == 1 && a.K >= 2048 && !one_item && !a.xnsp) p.T = 1024;
         // split K over the waves of a workgroup while row-quad groups are
         // scarcer than the resident waves (latency-bound small problems)
         const uint32_t nwaves = p.T / 64;
