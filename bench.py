@@ -80,7 +80,10 @@ class Workload:
             mats = []
             for j in range(nmat):
                 b = self.arena.take(wbytes)
-                d.synth_weights(ctx, fmt, b, n * k // el, seed * 1000 + r * 2 + j)
+                # ggml layouts (…g) are timed on the reference layout's synthetic
+                # bytes: the same block sizes and byte statistics
+                sfmt = fmt[:-1] if fmt.endswith("g") else fmt
+                d.synth_weights(ctx, sfmt, b, n * k // el, seed * 1000 + r * 2 + j)
                 mats.append(b)
             self.w.append(mats)
         self.x = ctx.new_buffer(4 * m * k)
@@ -443,6 +446,11 @@ def gemv_specs(ctx, suite):
             ("c6_q5k_ffn_2x18944x3584", lambda: Workload(ctx, "c6_ffn", "q5k", "ffn", 18944, 3584, seed=13)),
             ("c6_q5k_down_3584x18944", lambda: Workload(ctx, "c6_down", "q5k", "add", 3584, 18944, seed=14)),
             ("c6_q5_0_ffn_2x18944x3584", lambda: Workload(ctx, "c6_ffn0", "q5_0", "ffn", 18944, 3584, seed=15)),
+            # ggml layouts of the config-4 mix (upstream Q4_K_M files)
+            ("c4g_q4kg_ffn_2x18944x3584", lambda: Workload(ctx, "c4g_ffn", "q4kg", "ffn", 18944, 3584, seed=16)),
+            ("c4g_q6kg_down_3584x18944", lambda: Workload(ctx, "c4g_down", "q6kg", "add", 3584, 18944, seed=17)),
+            ("c4g_q6kg_lmhead_152064x3584", lambda: Workload(ctx, "c4g_lm", "q6kg", "gemv", 152064, 3584, seed=18)),
+            ("c3g_q4_0g_ffn_2x18944x3584", lambda: Workload(ctx, "c3g_ffn", "q4_0g", "ffn", 18944, 3584, seed=19)),
         ]
         for m in (1, 4, 8, 16, 32):
             specs.append((f"c5_gemm_q8_0_m{m}_18944x3584",

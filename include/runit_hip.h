@@ -200,6 +200,51 @@ int rt_gemv_q5k_add_f32_f32in(rt_ctx* ctx, const void* weight_q5k, const float* 
 int rt_gemv_q5k_f32in(rt_ctx* ctx, const void* weight_q5k, const float* input,
                       uint16_t* output, uint32_t m, uint32_t k);
 
+/* ───────────────────── ggml layouts (new) ─────────────────────
+ * The reference decodes Q4_0, Q4_K and Q6_K (and Q5_K) in layouts that
+ * differ from upstream ggml (forward.rs:964-978 interleaved Q4_0 nibbles,
+ * :1026-1057 Q4_K sub-block pairs (j, j+4), :921-950 one Q6_K scale per 32,
+ * :979-1012 Q5_K high bit e%8 of qh[e/8]).  Real GGUF files use ggml's:
+ *   q4_0g: element j < 16 = low nibble of qs[j], 16 + j = its high nibble;
+ *   q4kg : 64-element chunk j uses sub-blocks 2j (low) and 2j+1 (high);
+ *   q5kg : as q4kg, fifth bit = bit 2j (low) / 2j+1 (high) of qh[l];
+ *   q6kg : element h + 32t + l uses sc[h/16 + l/16 + 2t] (16 scales).
+ * Same block sizes and arguments as the reference-layout entry points. */
+int rt_gemv_q4_0g_f32in_f32out(rt_ctx* ctx, const void* weight, const float* input,
+                               float* output, uint32_t m, uint32_t k);
+int rt_gemv_q4_0g_add_f32_f32in(rt_ctx* ctx, const void* weight, const float* input,
+                                float* output, const float* residual, uint32_t m, uint32_t k);
+int rt_gemv_q4_0g_f32in(rt_ctx* ctx, const void* weight, const float* input, uint16_t* output,
+                        uint32_t m, uint32_t k);
+int rt_gemv_q4kg_f32in_f32out(rt_ctx* ctx, const void* weight, const float* input,
+                              float* output, uint32_t m, uint32_t k);
+int rt_gemv_q4kg_add_f32_f32in(rt_ctx* ctx, const void* weight, const float* input,
+                               float* output, const float* residual, uint32_t m, uint32_t k);
+int rt_gemv_q4kg_f32in(rt_ctx* ctx, const void* weight, const float* input, uint16_t* output,
+                       uint32_t m, uint32_t k);
+int rt_gemv_q5kg_f32in_f32out(rt_ctx* ctx, const void* weight, const float* input,
+                              float* output, uint32_t m, uint32_t k);
+int rt_gemv_q5kg_add_f32_f32in(rt_ctx* ctx, const void* weight, const float* input,
+                               float* output, const float* residual, uint32_t m, uint32_t k);
+int rt_gemv_q5kg_f32in(rt_ctx* ctx, const void* weight, const float* input, uint16_t* output,
+                       uint32_t m, uint32_t k);
+int rt_gemv_q6kg_f32in_f32out(rt_ctx* ctx, const void* weight, const float* input,
+                              float* output, uint32_t m, uint32_t k);
+int rt_gemv_q6kg_add_f32_f32in(rt_ctx* ctx, const void* weight, const float* input,
+                               float* output, const float* residual, uint32_t m, uint32_t k);
+int rt_gemv_q6kg_f32in(rt_ctx* ctx, const void* weight, const float* input, uint16_t* output,
+                       uint32_t m, uint32_t k);
+int rt_fused_ffn_q4_0g_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                           const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);
+int rt_fused_ffn_q4kg_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                          const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);
+int rt_fused_ffn_q5kg_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                          const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);
+int rt_dequant_q4_0g_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+int rt_dequant_q4kg_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+int rt_dequant_q5kg_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+int rt_dequant_q6kg_f32(rt_ctx* ctx, const void* input, float* output, uint32_t n_blocks);
+
 /* ───────────────────────── fused kernels ───────────────────────── */
 
 /* dispatch.rs:813-838 → fused_qkv.metal:72-119 */

@@ -68,7 +68,8 @@ uint16_t ora_f2h(float f) {
 static float rd_h(const uint8_t* p) { return ora_h2f((uint16_t)(p[0] | (p[1] << 8))); }
 
 size_t ora_block_elems(int fmt) {
-    return (fmt == ORA_Q4K || fmt == ORA_Q6K || fmt == ORA_Q5K) ? 256 : 32;
+    return (fmt == ORA_Q4K || fmt == ORA_Q6K || fmt == ORA_Q5K || fmt == ORA_Q4KG ||
+            fmt == ORA_Q5KG || fmt == ORA_Q6KG) ? 256 : 32;
 }
 size_t ora_block_bytes(int fmt) {
     switch (fmt) {
@@ -78,6 +79,10 @@ size_t ora_block_bytes(int fmt) {
         case ORA_Q6K: return 210;
         case ORA_Q5_0: return 22;
         case ORA_Q5K: return 176;
+        case ORA_Q4_0G: return 18;
+        case ORA_Q4KG: return 144;
+        case ORA_Q5KG: return 176;
+        case ORA_Q6KG: return 210;
     }
     return 0;
 }
@@ -216,6 +221,81 @@ void ora_dequant_q5k(const uint8_t* in, size_t nblk, float* out) {
     }
 }
 
+/* ggml dequantize_row_q4_0: x0 = (qs[j] & 0x0F) − 8, x1 = (qs[j] >> 4) − 8,
+ * y[j] = x0·d, y[j + 16] = x1·d */
+void ora_dequant_q4_0g(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const uint8_t* blk = in + b * 18;
+        const float d = rd_h(blk);
+        for (int j = 0; j < 16; ++j) {
+            const int x0 = (blk[2 + j] & 0x0F) - 8, x1 = (blk[2 + j] >> 4) - 8;
+            out[b * 32 + j] = (float)x0 * d;
+            out[b * 32 + j + 16] = (float)x1 * d;
+        }
+    }
+}
+
+/* ggml dequantize_row_q4_K / _q5_K: for chunk j (64 elements, sub-blocks
+ * is = 2j, 2j+1): d1 = d·sc, m1 = min·m; y[l] = d1·q_lo − m1, y[32+l] = d2·q_hi − m2;
+ * Q5_K adds 16 when bit 2j (low) / 2j+1 (high) of qh[l] is set. */
+static void dequant_k_ggml(const uint8_t* blk, const uint8_t* qh, const uint8_t* qs, float* y) {
+    const float d = rd_h(blk), dmin = rd_h(blk + 2);
+    const uint8_t* scales = blk + 4;
+    for (int j = 0; j < 4; ++j) {
+        uint8_t sc, m;
+        scale_min_k4(2 * j, scales, &sc, &m);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        scale_min_k4(2 * j + 1, scales, &sc, &m);
+        const float d2 = d * (float)sc, m2 = dmin * (float)m;
+        for (int l = 0; l < 32; ++l) {
+            int q1 = qs[32 * j + l] & 0x0F, q2 = qs[32 * j + l] >> 4;
+            if (qh) {
+                q1 += (qh[l] >> (2 * j)) & 1 ? 16 : 0;
+                q2 += (qh[l] >> (2 * j + 1)) & 1 ? 16 : 0;
+            }
+            y[64 * j + l] = d1 * (float)q1 - m1;
+            y[64 * j + 32 + l] = d2 * (float)q2 - m2;
+        }
+    }
+}
+void ora_dequant_q4kg(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b) dequant_k_ggml(in + b * 144, NULL, in + b * 144 + 16, out + b * 256);
+}
+void ora_dequant_q5kg(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b)
+        dequant_k_ggml(in + b * 176, in + b * 176 + 16, in + b * 176 + 48, out + b * 256);
+}
+
+/* ggml dequantize_row_q6_K: is = l/16; y[l + 32t] = d·sc[is + 2t]·q_t, the
+ * scale pointer advancing by 8 per 128-element half */
+void ora_dequant_q6kg(const uint8_t* in, size_t nblk, float* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        const uint8_t* blk = in + b * 210;
+        const uint8_t* ql = blk;
+        const uint8_t* qh = blk + 128;
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        const float d = rd_h(blk + 208);
+        float* y = out + b * 256;
+        for (int n = 0; n < 2; ++n) {
+            for (int l = 0; l < 32; ++l) {
+                const int is = l / 16;
+                const int q1 = ((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int q2 = ((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[l + 0] = d * (float)sc[is + 0] * (float)q1;
+                y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+            }
+            y += 128;
+            ql += 64;
+            qh += 32;
+            sc += 8;
+        }
+    }
+}
+
 void ora_dequant(int fmt, const uint8_t* in, size_t nblk, float* out) {
     switch (fmt) {
         case ORA_Q8_0: ora_dequant_q8_0(in, nblk, out); break;
@@ -224,6 +304,10 @@ void ora_dequant(int fmt, const uint8_t* in, size_t nblk, float* out) {
         case ORA_Q6K: ora_dequant_q6k(in, nblk, out); break;
         case ORA_Q5_0: ora_dequant_q5_0(in, nblk, out); break;
         case ORA_Q5K: ora_dequant_q5k(in, nblk, out); break;
+        case ORA_Q4_0G: ora_dequant_q4_0g(in, nblk, out); break;
+        case ORA_Q4KG: ora_dequant_q4kg(in, nblk, out); break;
+        case ORA_Q5KG: ora_dequant_q5kg(in, nblk, out); break;
+        case ORA_Q6KG: ora_dequant_q6kg(in, nblk, out); break;
     }
 }
 
@@ -574,5 +658,94 @@ void ora_quantize_q5k(const float* w, size_t nblk, uint8_t* out) {
                 }
                 qs[32 * j + l] = (uint8_t)((qq[0] & 15) | ((qq[1] & 15) << 4));
             }
+    }
+}
+
+/* ───────────────── re-layout to ggml (test data) ───────────────── */
+
+static void pack_scales_k4(const int sc[8], const int m[8], uint8_t* S) {
+    for (int j = 0; j < 4; ++j) {
+        S[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+        S[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+        S[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+    }
+}
+/* reference sub-block j (chunk j low) = ggml 2j, reference j + 4 (chunk j
+ * high) = ggml 2j + 1 */
+static void relayout_k_scales(const uint8_t* S_ref, uint8_t* S_g) {
+    int sc[8], m[8];
+    for (int j = 0; j < 4; ++j) {
+        uint8_t a, b;
+        scale_min_k4(j, S_ref, &a, &b);
+        sc[2 * j] = a; m[2 * j] = b;
+        scale_min_k4(j + 4, S_ref, &a, &b);
+        sc[2 * j + 1] = a; m[2 * j + 1] = b;
+    }
+    pack_scales_k4(sc, m, S_g);
+}
+
+void ora_relayout_to_ggml(int fmt, const uint8_t* in, size_t nblk, uint8_t* out) {
+    for (size_t b = 0; b < nblk; ++b) {
+        if (fmt == ORA_Q4_0) {
+            const uint8_t* r = in + b * 18;
+            uint8_t* g = out + b * 18;
+            int c[32];
+            for (int i = 0; i < 16; ++i) { c[2 * i] = r[2 + i] & 15; c[2 * i + 1] = r[2 + i] >> 4; }
+            g[0] = r[0]; g[1] = r[1];
+            for (int j = 0; j < 16; ++j) g[2 + j] = (uint8_t)(c[j] | (c[j + 16] << 4));
+        } else if (fmt == ORA_Q4K) {
+            const uint8_t* r = in + b * 144;
+            uint8_t* g = out + b * 144;
+            memcpy(g, r, 144);
+            relayout_k_scales(r + 4, g + 4);
+        } else if (fmt == ORA_Q5K) {
+            const uint8_t* r = in + b * 176;
+            uint8_t* g = out + b * 176;
+            memcpy(g, r, 176);
+            relayout_k_scales(r + 4, g + 4);
+            uint8_t qh[32];
+            memset(qh, 0, 32);
+            for (int e = 0; e < 256; ++e) {
+                const int bit = (r[16 + e / 8] >> (e % 8)) & 1;
+                const int j = e / 64, hi = (e / 32) & 1, l = e % 32;
+                qh[l] |= (uint8_t)(bit << (2 * j + hi));
+            }
+            memcpy(g + 16, qh, 32);
+        }
+    }
+}
+
+void ora_quantize_q4_0g(const float* w, size_t nblk, uint8_t* out) {
+    ora_quantize_q4_0(w, nblk, out);
+    uint8_t tmp[18];
+    for (size_t b = 0; b < nblk; ++b) {
+        ora_relayout_to_ggml(ORA_Q4_0, out + b * 18, 1, tmp);
+        memcpy(out + b * 18, tmp, 18);
+    }
+}
+void ora_quantize_q4kg(const float* w, size_t nblk, uint8_t* out) {
+    ora_quantize_q4k(w, nblk, out);
+    uint8_t tmp[144];
+    for (size_t b = 0; b < nblk; ++b) {
+        ora_relayout_to_ggml(ORA_Q4K, out + b * 144, 1, tmp);
+        memcpy(out + b * 144, tmp, 144);
+    }
+}
+void ora_quantize_q5kg(const float* w, size_t nblk, uint8_t* out) {
+    ora_quantize_q5k(w, nblk, out);
+    uint8_t tmp[176];
+    for (size_t b = 0; b < nblk; ++b) {
+        ora_relayout_to_ggml(ORA_Q5K, out + b * 176, 1, tmp);
+        memcpy(out + b * 176, tmp, 176);
+    }
+}
+void ora_quantize_q6kg(const float* w, size_t nblk, uint8_t* out) {
+    ora_quantize_q6k(w, nblk, out);
+    for (size_t b = 0; b < nblk; ++b) {
+        int8_t* sc = (int8_t*)(out + b * 210 + 192);
+        for (int k = 0; k < 8; ++k) {
+            const int v = sc[2 * k] + (int)((b * 5 + (size_t)k * 3) % 5) - 2;
+            sc[2 * k + 1] = (int8_t)clampi(v, -127, 127);
+        }
     }
 }

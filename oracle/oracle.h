@@ -18,7 +18,11 @@
 extern "C" {
 #endif
 
-enum { ORA_Q8_0 = 0, ORA_Q4_0 = 1, ORA_Q4K = 2, ORA_Q6K = 3, ORA_Q5_0 = 4, ORA_Q5K = 5 };
+enum {
+    ORA_Q8_0 = 0, ORA_Q4_0 = 1, ORA_Q4K = 2, ORA_Q6K = 3, ORA_Q5_0 = 4, ORA_Q5K = 5,
+    /* ggml layouts of the same blocks (upstream GGUF files) */
+    ORA_Q4_0G = 6, ORA_Q4KG = 7, ORA_Q5KG = 8, ORA_Q6KG = 9
+};
 
 /* half 2.7.1 crate (Cargo.lock): f16::to_f32 (exact) and f16::from_f32
  * (IEEE binary16, round to nearest even) — used at forward.rs:958,577. */
@@ -36,6 +40,17 @@ void ora_dequant_q4k(const uint8_t* in, size_t nblk, float* out);  /* forward.rs
 void ora_dequant_q6k(const uint8_t* in, size_t nblk, float* out);  /* forward.rs:921-950 */
 void ora_dequant_q5_0(const uint8_t* in, size_t nblk, float* out); /* forward.rs:900-920 */
 void ora_dequant_q5k(const uint8_t* in, size_t nblk, float* out);  /* forward.rs:979-1012, 359-369 */
+/* ggml layouts, restated from ggml's published decoders (ggml-quants.c
+ * dequantize_row_q4_0 / _q4_K / _q5_K / _q6_K; no copy of ggml is vendored
+ * in the reference, which documents the divergence at docs/STATUS_REPORT.md:184):
+ *   Q4_0: element j < 16 = low nibble of qs[j], 16 + j = high nibble;
+ *   Q4_K: chunk j of 64 uses sub-blocks 2j, 2j+1 (get_scale_min_k4 packing);
+ *   Q5_K: as Q4_K, fifth bit = bit 2j (low) / 2j+1 (high) of qh[l];
+ *   Q6_K: element h + 32t + l uses sc[h/16 + l/16 + 2t]. */
+void ora_dequant_q4_0g(const uint8_t* in, size_t nblk, float* out);
+void ora_dequant_q4kg(const uint8_t* in, size_t nblk, float* out);
+void ora_dequant_q5kg(const uint8_t* in, size_t nblk, float* out);
+void ora_dequant_q6kg(const uint8_t* in, size_t nblk, float* out);
 void ora_dequant(int fmt, const uint8_t* in, size_t nblk, float* out);
 /* dequant.metal:53-98 — Q4_K → f16 (f32 value, then RNE to half). */
 void ora_dequant_q4k_f16(const uint8_t* in, size_t nblk, uint16_t* out);
@@ -90,6 +105,16 @@ void ora_quantize_q4k(const float* w, size_t nblk, uint8_t* out);
 void ora_quantize_q6k(const float* w, size_t nblk, uint8_t* out);
 void ora_quantize_q5_0(const float* w, size_t nblk, uint8_t* out);
 void ora_quantize_q5k(const float* w, size_t nblk, uint8_t* out);
+/* Test data in the ggml layouts: the reference-layout quantiser's blocks
+ * re-laid out value for value (Q6_K: the odd scale slots, unused by the
+ * reference layout, get a value near their even neighbour). */
+void ora_quantize_q4_0g(const float* w, size_t nblk, uint8_t* out);
+void ora_quantize_q4kg(const float* w, size_t nblk, uint8_t* out);
+void ora_quantize_q5kg(const float* w, size_t nblk, uint8_t* out);
+void ora_quantize_q6kg(const float* w, size_t nblk, uint8_t* out);
+/* Re-layout one block stream from the reference layout to ggml's (fmt =
+ * ORA_Q4_0 / ORA_Q4K / ORA_Q5K), values preserved. */
+void ora_relayout_to_ggml(int fmt, const uint8_t* in, size_t nblk, uint8_t* out);
 
 #ifdef __cplusplus
 }

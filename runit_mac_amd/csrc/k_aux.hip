@@ -129,6 +129,72 @@ k_dequant_q5k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint6
     out[i] = __fsub_rn(__fmul_rn(dsc, (float)q), mm);
 }
 
+// ggml layouts (upstream GGUF files), same rounding as the decoders above.
+// Q4_0: element j < 16 low nibble of qs[j], 16 + j its high nibble
+// (dequantize_row_q4_0).
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q4_0g_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
+    if (i >= n_el) return;
+    const uint8_t* blk = in + (i >> 5) * 18;
+    const float d = h2f(*(const uint16_t*)blk);
+    const uint32_t e = i & 31;
+    const uint8_t byte = blk[2 + (e & 15)];
+    const int nib = (e < 16) ? (byte & 15) : (byte >> 4);
+    out[i] = __fmul_rn(d, (float)(nib - 8));
+}
+
+// Q4_K: chunk j of 64 elements uses sub-blocks 2j (low nibbles) and 2j + 1
+// (high nibbles) (dequantize_row_q4_K).
+RT_DEV float q4kg_value(const uint8_t* blk, uint32_t e, uint32_t qs_off, bool five,
+                        const uint8_t* qh) {
+    const float d = h2f(*(const uint16_t*)blk);
+    const float dmin = h2f(*(const uint16_t*)(blk + 2));
+    const uint32_t j = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+    uint32_t sc, m;
+    q4k_scale_min(2 * j + hi, blk + 4, sc, m);
+    const uint8_t byte = blk[qs_off + 32 * j + l];
+    uint32_t q = hi ? (byte >> 4) : (byte & 15u);
+    if (five) q |= ((qh[l] >> (2 * j + hi)) & 1u) << 4;  // Q5_K: bit 2j(+1) of qh[l]
+    const float dsc = __fmul_rn(d, (float)sc);
+    const float mm = __fmul_rn(dmin, (float)m);
+    return __fsub_rn(__fmul_rn(dsc, (float)q), mm);
+}
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q4kg_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
+    if (i >= n_el) return;
+    const uint8_t* blk = in + (i >> 8) * 144;
+    out[i] = q4kg_value(blk, (uint32_t)(i & 255), 16, false, nullptr);
+}
+// Q5_K: as Q4_K (qs at 48) with the fifth bit from qh (dequantize_row_q5_K).
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q5kg_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
+    if (i >= n_el) return;
+    const uint8_t* blk = in + (i >> 8) * 176;
+    out[i] = q4kg_value(blk, (uint32_t)(i & 255), 48, true, blk + 16);
+}
+// Q6_K: element h + 32t + l uses sc[h/16 + l/16 + 2t] (dequantize_row_q6_K).
+extern "C" __global__ void __launch_bounds__(256)
+k_dequant_q6kg_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
+    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
+    if (i >= n_el) return;
+    const uint8_t* blk = in + (i >> 8) * 210;
+    const uint32_t e = (uint32_t)(i & 255);
+    const uint32_t h = e & 128u, t = (e >> 5) & 3, l = e & 31;
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    const float d = h2f(*(const uint16_t*)(blk + 208));
+    const uint32_t qlb = ql[h / 2 + l + ((t & 1) ? 32 : 0)];
+    const uint32_t lo4 = (t < 2) ? (qlb & 15u) : (qlb >> 4);
+    const uint32_t hi2 = (qh[h / 4 + l] >> (2 * t)) & 3u;
+    const int q = (int)(lo4 | (hi2 << 4)) - 32;
+    const float s = (float)sc[h / 16 + l / 16 + 2 * t];
+    out[i] = __fmul_rn(__fmul_rn(d, s), (float)q);
+}
+
 // ───────────────────────────── argmax ─────────────────────────────
 // greedy_argmax_f32 (sampler.rs:111-116) folds with Rust's max_by: the
 // running best m is replaced by x unless m > x (partial_cmp None → Equal).

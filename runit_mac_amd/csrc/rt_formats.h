@@ -251,11 +251,38 @@ struct FmtQ4_0S {
 };
 
 // ───────────────────────────── Q4_K ─────────────────────────────
+// 6-bit (scale, min) of sub-block `is` from the 12-byte table held as three
+// dwords y = bytes 0..3, z = 4..7, w = 8..11 (get_scale_min_k4,
+// forward.rs:359-369; ggml uses the same packing).
+RT_DEV void kq_scale_min(uint32_t is, uint32_t y, uint32_t z, uint32_t w, uint32_t& sc,
+                          uint32_t& m) {
+    const uint32_t b = 8 * (is & 3);
+    const uint32_t yb = (y >> b) & 255u, zb = (z >> b) & 255u, wb = (w >> b) & 255u;
+    if (is < 4) {
+        sc = yb & 63u;
+        m = zb & 63u;
+    } else {
+        sc = (wb & 15u) | ((yb >> 6) << 4);
+        m = (wb >> 4) | ((zb >> 6) << 4);
+    }
+}
+// (scale, min) of the unit's two sub-blocks packed as bytes (sc_lo, m_lo,
+// sc_hi, m_hi).  Reference layout: pair j uses sub-blocks j and j + 4
+// (forward.rs:1026-1057); ggml layout: 2j and 2j + 1 (dequantize_row_q4_K).
+template <bool G>
+RT_DEV uint32_t k_quant_scales(uint32_t j, uint32_t y, uint32_t z, uint32_t w) {
+    uint32_t a, b, c, d;
+    kq_scale_min(G ? 2 * j : j, y, z, w, a, b);
+    kq_scale_min(G ? 2 * j + 1 : j + 4, y, z, w, c, d);
+    return a | (b << 8) | (c << 16) | (d << 24);
+}
+
 // Super-block: d:f16 @0, dmin:f16 @2, scales:u8[12] @4, qs:u8[128] @16
-// (dequant.metal:9-16).  Pair j ∈ 0..3: element 64j+l = d·sc_j·(qs[32j+l]&0xF)
-// − dmin·m_j, element 64j+32+l uses the high nibble with (sc,m)_{j+4}
-// (forward.rs:1026-1057; 6-bit (sc,m) per get_scale_min_k4, forward.rs:359-369).
-struct FmtQ4K {
+// (dequant.metal:9-16).  Pair j ∈ 0..3: element 64j+l = d·sc·(qs[32j+l]&0xF)
+// − dmin·m of the pair's first sub-block, element 64j+32+l the high nibble
+// with the second sub-block's (sc, m).  Sub-blocks per k_quant_scales<G>.
+template <bool G>
+struct FmtQ4KT {
     static constexpr uint32_t BLK_EL = 256, BLK_BYTES = 144, UNIT_EL = 64;
     static constexpr bool Q40PERM = false;
     struct Raw { uint32_t dd; uint32_t sc; uint32_t q[8]; };
@@ -266,10 +293,7 @@ struct FmtQ4K {
         // 144-byte blocks keep 16-byte alignment: header = one dwordx4
         const u32x4 hdr = *(const u32x4*)p;
         r.dd = hdr.x;
-        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
-        // bytes j, j+4, j+8 of the scale table, packed as (b0 | b1<<8 | b2<<16)
-        const uint32_t sh = 8 * j;
-        r.sc = ((s0 >> sh) & 255u) | (((s1 >> sh) & 255u) << 8) | (((s2 >> sh) & 255u) << 16);
+        r.sc = k_quant_scales<G>(j, hdr.y, hdr.z, hdr.w);
         const u32x4* qp = (const u32x4*)(p + 16 + 32 * j);
         u32x4 a = qp[0], c = qp[1];
         r.q[0] = a.x; r.q[1] = a.y; r.q[2] = a.z; r.q[3] = a.w;
@@ -278,6 +302,13 @@ struct FmtQ4K {
     RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) {
         load_xregs(recs + 2 * uu, xu.lo);
         load_xregs(recs + 2 * uu + 1, xu.hi);
+    }
+    RT_DEV static void scales(const Raw& r, float& d_lo, float& m_lo, float& d_hi, float& m_hi) {
+        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
+        d_lo = d * (float)(r.sc & 255u);
+        m_lo = dmin * (float)((r.sc >> 8) & 255u);
+        d_hi = d * (float)((r.sc >> 16) & 255u);
+        m_hi = dmin * (float)(r.sc >> 24);
     }
     RT_DEV static float dot(const Raw& r, const XU& xu) {
         int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
@@ -292,13 +323,8 @@ struct FmtQ4K {
             b1 = sdot4(hi, xu.hi.l[1][i], b1);
             b2 = sdot4(hi, xu.hi.l[2][i], b2);
         }
-        const uint32_t c0 = r.sc & 255u, c1 = (r.sc >> 8) & 255u, c2 = (r.sc >> 16) & 255u;
-        const uint32_t sc_lo = c0 & 63u, m_lo = c1 & 63u;
-        const uint32_t sc_hi = (c2 & 15u) | ((c0 >> 6) << 4);
-        const uint32_t m_hi = (c2 >> 4) | ((c1 >> 6) << 4);
-        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
-        const float d_lo = d * (float)sc_lo, mm_lo = dmin * (float)m_lo;
-        const float d_hi = d * (float)sc_hi, mm_hi = dmin * (float)m_hi;
+        float d_lo, mm_lo, d_hi, mm_hi;
+        scales(r, d_lo, mm_lo, d_hi, mm_hi);
         const float vlo = d_lo * limb_combine(a0, a1, a2) -
                           mm_lo * limb_combine(xu.lo.s[0], xu.lo.s[1], xu.lo.s[2]);
         const float vhi = d_hi * limb_combine(b0, b1, b2) -
@@ -316,18 +342,15 @@ struct FmtQ4K {
             cl = mfma4(xl.l[i], r.q[i] & 0x0F0F0F0Fu, cl);
             ch = mfma4(xh.l[i], (r.q[i] >> 4) & 0x0F0F0F0Fu, ch);
         }
-        const uint32_t c0 = r.sc & 255u, c1 = (r.sc >> 8) & 255u, c2 = (r.sc >> 16) & 255u;
-        const uint32_t sc_lo = c0 & 63u, m_lo = c1 & 63u;
-        const uint32_t sc_hi = (c2 & 15u) | ((c0 >> 6) << 4);
-        const uint32_t m_hi = (c2 >> 4) | ((c1 >> 6) << 4);
-        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
-        const float vlo = d * (float)sc_lo * comb4(cl) -
-                          dmin * (float)m_lo * limb_combine(xl.s[0], xl.s[1], xl.s[2]);
-        const float vhi = d * (float)sc_hi * comb4(ch) -
-                          dmin * (float)m_hi * limb_combine(xh.s[0], xh.s[1], xh.s[2]);
+        float d_lo, mm_lo, d_hi, mm_hi;
+        scales(r, d_lo, mm_lo, d_hi, mm_hi);
+        const float vlo = d_lo * comb4(cl) - mm_lo * limb_combine(xl.s[0], xl.s[1], xl.s[2]);
+        const float vhi = d_hi * comb4(ch) - mm_hi * limb_combine(xh.s[0], xh.s[1], xh.s[2]);
         return __builtin_amdgcn_ldexpf(vlo, xl.e - 22) + __builtin_amdgcn_ldexpf(vhi, xh.e - 22);
     }
 };
+using FmtQ4K = FmtQ4KT<false>;
+using FmtQ4KG = FmtQ4KT<true>;
 
 // ───────────────────────────── Q6_K ─────────────────────────────
 // Super-block: ql:u8[128] @0, qh:u8[64] @128, sc:i8[16] @192, d:f16 @208.
@@ -335,7 +358,11 @@ struct FmtQ4K {
 //   d · sc[h/16 + 2t] · (code_t − 32), code_t from ql[h/2+l (+32 if t odd)]
 //   (low nibble for t<2, high for t≥2) and 2 bits (qh[h/4+l] >> 2t)
 // (forward.rs:921-950; only the even scale slots are read, forward.rs:935).
-struct FmtQ6K {
+// The ggml layout (G) gives every 16 elements their own scale: element
+// h + 32t + l uses sc[h/16 + 2t + l/16] instead of sc[h/16 + 2t]
+// (dequantize_row_q6_K); its unit's scale bytes are shifted by l-half.
+template <bool G>
+struct FmtQ6KT {
     static constexpr uint32_t BLK_EL = 256, BLK_BYTES = 210, UNIT_EL = 64;
     static constexpr bool Q40PERM = false;
     struct Raw { uint32_t ql0[4], ql1[4], qh[4]; uint32_t sc01, sc23; uint32_t d; };
@@ -372,6 +399,10 @@ struct FmtQ6K {
         }
         r.sc01 = alignb(w[1], w[0], sh);  // bytes 0..3: sc[is+0], (odd), sc[is+2], (odd)
         r.sc23 = alignb(w[2], w[1], sh);  // bytes 4..7: sc[is+4], (odd), sc[is+6], (odd)
+        if (G) {  // bytes 0 and 2 become sc[is + lh + 0|2] (and + 4|6)
+            r.sc01 >>= 8 * lh;
+            r.sc23 >>= 8 * lh;
+        }
         // d sits 16 (h = 0) or 8 (h = 128) bytes after the scale window start
         r.d = hsel ? alignb(w[3], w[2], sh) : alignb(w[4], w[4], sh);
     }
@@ -462,6 +493,9 @@ struct FmtQ6K {
     }
 };
 
+using FmtQ6K = FmtQ6KT<false>;
+using FmtQ6KG = FmtQ6KT<true>;
+
 // Q6_K for the matrix-core path: one whole 210-byte super-block (256
 // elements) per lane, loaded as 53 aligned dwords (13 dwordx4 + 1) from the
 // block's 4-byte floor.  The block starts 0 or 2 bytes past that floor (sh);
@@ -470,7 +504,10 @@ struct FmtQ6K {
 // for half h ∈ {0, 128} and l ∈ 0..31, element h + 32t + l (t = 0..3) is
 //   ((ql[h/2 + l + 32·(t&1)] >> 4·(t>>1)) & 15) | (((qh[h/4 + l] >> 2t) & 3) << 4),
 // minus 32, times d · int8(sc[h/16 + 2t]) — one scale per 32-element record.
-struct FmtQ6KB {
+// ggml layout (G): the two 16-element halves of each record accumulate
+// separately and take sc[h/16 + 2t] and sc[h/16 + 2t + 1].
+template <bool G>
+struct FmtQ6KBT {
     static constexpr uint32_t BLK_EL = 256, BLK_BYTES = 210, UNIT_EL = 256;
     static constexpr bool Q40PERM = false;
     static constexpr int PF = 1;  // one item (212 bytes per lane) in flight per wave
@@ -487,21 +524,29 @@ struct FmtQ6KB {
     }
     RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
         const float d = h2f(r.w[52] >> (8 * r.sh));  // bytes 208-209
+        constexpr int NH = G ? 2 : 1;  // accumulators per record
         float acc = 0.0f;
 #pragma unroll 1
         for (int hs = 0; hs < 2; ++hs) {  // (rolled: one half's operands live at a time)
             const XRec* rec = xs + 8 * uu + 4 * hs;
-            v4i c[4];
+            v4i c[4][NH];
             int e[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const u32x4 m = ((const u32x4*)(rec + t))[6];
                 e[t] = (int)(int16_t)(m.x & 0xFFFF);
-                // codes are 0..63; −32·Σx over the record seeds the accumulators
-                const int s0 = (int16_t)(m.x >> 16) + (int16_t)(m.z & 0xFFFF);
-                const int s1 = (int16_t)(m.y & 0xFFFF) + (int16_t)(m.z >> 16);
-                const int s2 = (int16_t)(m.y >> 16) + (int16_t)(m.w & 0xFFFF);
-                c[t] = v4i{-32 * s0, -32 * s1, -32 * s2, 0};
+                // codes are 0..63; −32·Σx over the record (G: over each half)
+                // seeds the accumulators
+                const int a0 = (int16_t)(m.x >> 16), a1 = (int16_t)(m.y & 0xFFFF),
+                          a2 = (int16_t)(m.y >> 16);
+                const int b0 = (int16_t)(m.z & 0xFFFF), b1 = (int16_t)(m.z >> 16),
+                          b2 = (int16_t)(m.w & 0xFFFF);
+                if (G) {
+                    c[t][0] = v4i{-32 * a0, -32 * a1, -32 * a2, 0};
+                    c[t][NH - 1] = v4i{-32 * b0, -32 * b1, -32 * b2, 0};
+                } else {
+                    c[t][0] = v4i{-32 * (a0 + b0), -32 * (a1 + b1), -32 * (a2 + b2), 0};
+                }
             }
 #pragma unroll
             for (int g = 0; g < 8; ++g) {
@@ -513,23 +558,33 @@ struct FmtQ6KB {
                 const uint32_t ql = hs ? get(r, 64 + 4 * g) : get(r, 4 * g);
                 const uint32_t ql32 = hs ? get(r, 96 + 4 * g) : get(r, 32 + 4 * g);
                 const uint32_t qh = hs ? get(r, 160 + 4 * g) : get(r, 128 + 4 * g);
-                c[0] = mfma4(xl[0], (ql & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u), c[0]);
-                c[1] = mfma4(xl[1], (ql32 & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u), c[1]);
-                c[2] = mfma4(xl[2], ((ql >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u), c[2]);
-                c[3] = mfma4(xl[3], ((ql32 >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u), c[3]);
+                const int k = (G && g >= 4) ? NH - 1 : 0;
+                c[0][k] = mfma4(xl[0], (ql & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u), c[0][k]);
+                c[1][k] = mfma4(xl[1], (ql32 & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u), c[1][k]);
+                c[2][k] = mfma4(xl[2], ((ql >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u), c[2][k]);
+                c[3][k] = mfma4(xl[3], ((ql32 >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u), c[3][k]);
             }
-            // scales sc[8·hs + 2t]: bytes 192 + 8·hs + {0, 2, 4, 6}
+            // scales sc[8·hs + 2t (+1)]: bytes 192 + 8·hs + 0..7
             const uint32_t sa = hs ? get(r, 200) : get(r, 192);
             const uint32_t sb = hs ? get(r, 204) : get(r, 196);
-            const int sc[4] = {(int8_t)(sa & 255u), (int8_t)((sa >> 16) & 255u),
-                               (int8_t)(sb & 255u), (int8_t)((sb >> 16) & 255u)};
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-                acc += __builtin_amdgcn_ldexpf(d * (float)sc[t] * comb4(c[t]), e[t] - 22);
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t sw = t < 2 ? sa : sb;
+                const int sh0 = 16 * (t & 1);
+                const int s0 = (int8_t)((sw >> sh0) & 255u);
+                float v = d * (float)s0 * comb4(c[t][0]);
+                if (G) {
+                    const int s1 = (int8_t)((sw >> (sh0 + 8)) & 255u);
+                    v += d * (float)s1 * comb4(c[t][NH - 1]);
+                }
+                acc += __builtin_amdgcn_ldexpf(v, e[t] - 22);
+            }
         }
         return acc;
     }
 };
+using FmtQ6KB = FmtQ6KBT<false>;
+using FmtQ6KGB = FmtQ6KBT<true>;
 
 // ───────────────────────────── Q5_0 / Q5_K ─────────────────────────────
 //
@@ -640,24 +695,36 @@ struct FmtQ5_0S {
 
 // Q5_K (176 B, 16-byte aligned): d, dmin f16 @0, scales[12] @4 (Q4_K
 // packing), qh[32] @16, qs[128] @48.  Unit (block, pair j) = 64 elements:
-// sub-block j (low nibbles of qs[32j..32j+31]) and j+4 (high nibbles); the
-// high bit of element e is bit e%8 of qh[e/8] (forward.rs:979-1012), so the
-// unit's 64 high bits are qh bytes 8j..8j+7.  v = d·sc·q − dmin·m.
-struct FmtQ5K {
+// the low nibbles of qs[32j..32j+31] (first sub-block of the pair) and the
+// high nibbles (second), v = d·sc·q − dmin·m.  The fifth bit of element e:
+//   reference layout: bit e%8 of qh[e/8] (forward.rs:979-1012), so the
+//     unit's 64 bits are qh bytes 8j..8j+7 and sub-blocks pair as (j, j+4);
+//   ggml layout (G): bit 2j (low half) / 2j+1 (high half) of qh[l] for
+//     element 64j(+32)+l (dequantize_row_q5_K), sub-blocks (2j, 2j+1).
+template <bool G>
+struct FmtQ5KT {
     static constexpr uint32_t BLK_EL = 256, BLK_BYTES = 176, UNIT_EL = 64;
     static constexpr bool Q40PERM = false;
-    struct Raw { uint32_t dd; uint32_t sc; uint32_t qh0, qh1; uint32_t q[8]; };
+    static constexpr int NQH = G ? 8 : 2;
+    struct Raw { uint32_t dd; uint32_t sc; uint32_t qh[NQH]; uint32_t q[8]; uint32_t j2; };
     struct XU { XRegs lo, hi; };
     RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
         const uint32_t b = u >> 2, j = u & 3;
         const uint8_t* p = row + (size_t)b * 176;
         const u32x4 hdr = *(const u32x4*)p;
         r.dd = hdr.x;
-        const uint32_t sh = 8 * j;
-        r.sc = ((hdr.y >> sh) & 255u) | (((hdr.z >> sh) & 255u) << 8) | (((hdr.w >> sh) & 255u) << 16);
-        const uint2 h = *(const uint2*)(p + 16 + 8 * j);
-        r.qh0 = h.x;
-        r.qh1 = h.y;
+        r.sc = k_quant_scales<G>(j, hdr.y, hdr.z, hdr.w);
+        r.j2 = 2 * j;
+        if (G) {
+            const u32x4* hp = (const u32x4*)(p + 16);
+            const u32x4 h0 = hp[0], h1 = hp[1];
+            r.qh[0] = h0.x; r.qh[1] = h0.y; r.qh[2] = h0.z; r.qh[3] = h0.w;
+            r.qh[NQH - 4] = h1.x; r.qh[NQH - 3] = h1.y; r.qh[NQH - 2] = h1.z; r.qh[NQH - 1] = h1.w;
+        } else {
+            const uint2 h = *(const uint2*)(p + 16 + 8 * j);
+            r.qh[0] = h.x;
+            r.qh[NQH - 1] = h.y;
+        }
         const u32x4* qp = (const u32x4*)(p + 48 + 32 * j);
         const u32x4 a = qp[0], c = qp[1];
         r.q[0] = a.x; r.q[1] = a.y; r.q[2] = a.z; r.q[3] = a.w;
@@ -667,22 +734,22 @@ struct FmtQ5K {
         load_xregs(recs + 2 * uu, xu.lo);
         load_xregs(recs + 2 * uu + 1, xu.hi);
     }
+    // 5-bit codes of elements 4i..4i+3 of the low / high half
     RT_DEV static uint32_t code_lo(const Raw& r, int i) {
-        return (r.q[i] & 0x0F0F0F0Fu) | (spread4((r.qh0 >> (4 * i)) & 15u) << 4);
+        const uint32_t hb = G ? ((r.qh[i] >> r.j2) & 0x01010101u) : spread4((r.qh[0] >> (4 * i)) & 15u);
+        return (r.q[i] & 0x0F0F0F0Fu) | (hb << 4);
     }
     RT_DEV static uint32_t code_hi(const Raw& r, int i) {
-        return ((r.q[i] >> 4) & 0x0F0F0F0Fu) | (spread4((r.qh1 >> (4 * i)) & 15u) << 4);
+        const uint32_t hb = G ? ((r.qh[i] >> (r.j2 + 1)) & 0x01010101u)
+                              : spread4((r.qh[NQH - 1] >> (4 * i)) & 15u);
+        return ((r.q[i] >> 4) & 0x0F0F0F0Fu) | (hb << 4);
     }
     RT_DEV static void scales(const Raw& r, float& d_lo, float& m_lo, float& d_hi, float& m_hi) {
-        const uint32_t c0 = r.sc & 255u, c1 = (r.sc >> 8) & 255u, c2 = (r.sc >> 16) & 255u;
-        const uint32_t sc_lo = c0 & 63u, mn_lo = c1 & 63u;
-        const uint32_t sc_hi = (c2 & 15u) | ((c0 >> 6) << 4);
-        const uint32_t mn_hi = (c2 >> 4) | ((c1 >> 6) << 4);
         const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
-        d_lo = d * (float)sc_lo;
-        m_lo = dmin * (float)mn_lo;
-        d_hi = d * (float)sc_hi;
-        m_hi = dmin * (float)mn_hi;
+        d_lo = d * (float)(r.sc & 255u);
+        m_lo = dmin * (float)((r.sc >> 8) & 255u);
+        d_hi = d * (float)((r.sc >> 16) & 255u);
+        m_hi = dmin * (float)(r.sc >> 24);
     }
     RT_DEV static float dot(const Raw& r, const XU& xu) {
         int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
@@ -720,5 +787,88 @@ struct FmtQ5K {
         const float vlo = d_lo * comb4(cl) - m_lo * limb_combine(xl.s[0], xl.s[1], xl.s[2]);
         const float vhi = d_hi * comb4(ch) - m_hi * limb_combine(xh.s[0], xh.s[1], xh.s[2]);
         return __builtin_amdgcn_ldexpf(vlo, xl.e - 22) + __builtin_amdgcn_ldexpf(vhi, xh.e - 22);
+    }
+};
+using FmtQ5K = FmtQ5KT<false>;
+using FmtQ5KG = FmtQ5KT<true>;
+
+// ─────────────────────── Q4_0, ggml layout ───────────────────────
+// Block as Q4_0, but element j < 16 is the low nibble of qs[j] and element
+// 16 + j its high nibble (dequantize_row_q4_0), value d·(nib − 8).  The
+// activation records stay in natural order (no Q4_0 permutation).
+RT_DEV float q4_0g_block_dot(uint32_t d16, const uint32_t q[4], const XRegs& x) {
+    int t0 = -8 * x.s[0], t1 = -8 * x.s[1], t2 = -8 * x.s[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = q[i] & 0x0F0F0F0Fu, hi = (q[i] >> 4) & 0x0F0F0F0Fu;
+        t0 = sdot4(lo, x.l[0][i], t0);
+        t1 = sdot4(lo, x.l[1][i], t1);
+        t2 = sdot4(lo, x.l[2][i], t2);
+        t0 = sdot4(hi, x.l[0][4 + i], t0);
+        t1 = sdot4(hi, x.l[1][4 + i], t1);
+        t2 = sdot4(hi, x.l[2][4 + i], t2);
+    }
+    return __builtin_amdgcn_ldexpf(h2f(d16) * limb_combine(t0, t1, t2), x.e - 22);
+}
+RT_DEV float q4_0g_block_mdot(uint32_t d16, const uint32_t q[4], const XLimb& x) {
+    v4i c = {-8 * x.s[0], -8 * x.s[1], -8 * x.s[2], 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        c = mfma4(x.l[i], q[i] & 0x0F0F0F0Fu, c);
+        c = mfma4(x.l[4 + i], (q[i] >> 4) & 0x0F0F0F0Fu, c);
+    }
+    return __builtin_amdgcn_ldexpf(h2f(d16) * comb4(c), x.e - 22);
+}
+// Unit = two consecutive blocks (36 bytes): 9 aligned dwords.
+struct FmtQ4_0G {
+    static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 18, UNIT_EL = 64;
+    static constexpr bool Q40PERM = false;
+    struct Raw { uint32_t w[9]; };
+    struct XU { XRegs x[2]; };
+    RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
+        load_dwords<9>(row + (size_t)u * 36, r.w);
+    }
+    RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) {
+        load_xregs(recs + 2 * uu, xu.x[0]);
+        load_xregs(recs + 2 * uu + 1, xu.x[1]);
+    }
+    RT_DEV static void split(const Raw& r, uint32_t qa[4], uint32_t qb[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qa[i] = alignb(r.w[i + 1], r.w[i], 2);  // bytes 2..17
+            qb[i] = r.w[5 + i];                     // bytes 20..35
+        }
+    }
+    RT_DEV static float dot(const Raw& r, const XU& xu) {
+        uint32_t qa[4], qb[4];
+        split(r, qa, qb);
+        return q4_0g_block_dot(r.w[0], qa, xu.x[0]) + q4_0g_block_dot(r.w[4] >> 16, qb, xu.x[1]);
+    }
+    RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
+        XLimb xa, xb;
+        load_xlimb(xs + 2 * uu, lq, xa);
+        load_xlimb(xs + 2 * uu + 1, lq, xb);
+        uint32_t qa[4], qb[4];
+        split(r, qa, qb);
+        return q4_0g_block_mdot(r.w[0], qa, xa) + q4_0g_block_mdot(r.w[4] >> 16, qb, xb);
+    }
+};
+// Single-block unit for rows with an odd number of blocks.
+struct FmtQ4_0GS {
+    static constexpr uint32_t BLK_EL = 32, BLK_BYTES = 18, UNIT_EL = 32;
+    static constexpr bool Q40PERM = false;
+    struct Raw { uint32_t w[5]; uint32_t sh; };
+    struct XU { XRegs x; };
+    RT_DEV static void load(const uint8_t* row, uint32_t u, Raw& r) {
+        const uintptr_t p = (uintptr_t)(row + (size_t)u * 18);
+        r.sh = (uint32_t)(p & 3);
+        load_dwords<5>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
+    }
+    RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) { load_xregs(recs + uu, xu.x); }
+    RT_DEV static float dot(const Raw& r, const XU& xu) {
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = r.sh ? r.w[i + 1] : alignb(r.w[i + 1], r.w[i], 2);
+        return q4_0g_block_dot(alignb(r.w[1], r.w[0], r.sh), q, xu.x);
     }
 };

@@ -91,6 +91,19 @@ const char* const kKernelNames[] = {
     "k_gemv_q4_0_f16_f16_s1", "k_gemv_q4_0_f16_f16add_s1", "k_qkv_bias_q4_0_s1", "k_ffn_q4_0_s1",
     "k_dequant_q8_0_f32", "k_dequant_q4_0_f32", "k_dequant_q4k_f32", "k_dequant_q4k_f16",
     "k_dequant_q6k_f32", "k_dequant_q5_0_f32", "k_dequant_q5k_f32",
+    "k_dequant_q4_0g_f32", "k_dequant_q4kg_f32", "k_dequant_q5kg_f32", "k_dequant_q6kg_f32",
+    "k_gemv_q4_0g_f32_f32_r1", "k_gemv_q4_0g_f32_f32_r2", "k_gemv_q4_0g_f32_f32add_r1",
+    "k_gemv_q4_0g_f32_f32add_r2", "k_gemv_q4_0g_f32_f16_r1", "k_gemv_q4_0g_f32_f16_r2",
+    "k_ffn_q4_0g_r1", "k_ffn_q4_0g_r2", "k_gemv_q4_0g_f32_f32_s1", "k_gemv_q4_0g_f32_f32add_s1",
+    "k_gemv_q4_0g_f32_f16_s1", "k_ffn_q4_0g_s1",
+    "k_gemv_q4kg_f32_f32_r1", "k_gemv_q4kg_f32_f32_r2", "k_gemv_q4kg_f32_f32add_r1",
+    "k_gemv_q4kg_f32_f32add_r2", "k_gemv_q4kg_f32_f16_r1", "k_gemv_q4kg_f32_f16_r2",
+    "k_ffn_q4kg_r1", "k_ffn_q4kg_r2",
+    "k_gemv_q5kg_f32_f32_r1", "k_gemv_q5kg_f32_f32_r2", "k_gemv_q5kg_f32_f32add_r1",
+    "k_gemv_q5kg_f32_f32add_r2", "k_gemv_q5kg_f32_f16_r1", "k_gemv_q5kg_f32_f16_r2",
+    "k_ffn_q5kg_r1", "k_ffn_q5kg_r2",
+    "k_gemv_q6kg_f32_f32_r1", "k_gemv_q6kg_f32_f32_r2", "k_gemv_q6kg_f32_f32add_r1",
+    "k_gemv_q6kg_f32_f32add_r2", "k_gemv_q6kg_f32_f16_r1", "k_gemv_q6kg_f32_f16_r2",
     "k_gemv_q5_0_f32_f32_r1", "k_gemv_q5_0_f32_f32_r2",
     "k_gemv_q5_0_f32_f32add_r1", "k_gemv_q5_0_f32_f32add_r2",
     "k_gemv_q5_0_f32_f16_r1", "k_gemv_q5_0_f32_f16_r2",
@@ -122,19 +135,26 @@ struct Fmt {
     const char* name;
     const Fmt* single;  // single-block-unit fallback for odd block counts
     uint32_t mq_unit_el = 0;  // matrix-core path unit, if it differs from unit_el
+    bool q40perm = false;     // activation records in the reference Q4_0 order
     uint32_t mq_units() const { return mq_unit_el ? mq_unit_el : unit_el; }
 };
 // Q8_0 / Q4_0 kernels take two blocks per unit (4-byte-aligned loads); rows
 // with an odd number of blocks use the one-block "_s1" kernels.
 constexpr Fmt kQ8_0S{32, 34, 32, 2, "Q8_0", nullptr};
-constexpr Fmt kQ4_0S{32, 18, 32, 4, "Q4_0", nullptr};
+constexpr Fmt kQ4_0S{32, 18, 32, 4, "Q4_0", nullptr, 0, true};
 constexpr Fmt kQ8_0{32, 34, 64, 1, "Q8_0", &kQ8_0S};
-constexpr Fmt kQ4_0{32, 18, 64, 2, "Q4_0", &kQ4_0S};
+constexpr Fmt kQ4_0{32, 18, 64, 2, "Q4_0", &kQ4_0S, 0, true};
 constexpr Fmt kQ4K{256, 144, 64, 1, "Q4_K", nullptr};
 constexpr Fmt kQ6K{256, 210, 64, 1, "Q6_K", nullptr, 256};  // matrix-core: one block per lane
 constexpr Fmt kQ5_0S{32, 22, 32, 4, "Q5_0", nullptr};
 constexpr Fmt kQ5_0{32, 22, 64, 2, "Q5_0", &kQ5_0S};
 constexpr Fmt kQ5K{256, 176, 64, 1, "Q5_K", nullptr};
+// ggml layouts (upstream GGUF files)
+constexpr Fmt kQ4_0GS{32, 18, 32, 4, "Q4_0 (ggml)", nullptr};
+constexpr Fmt kQ4_0G{32, 18, 64, 2, "Q4_0 (ggml)", &kQ4_0GS};
+constexpr Fmt kQ4KG{256, 144, 64, 1, "Q4_K (ggml)", nullptr};
+constexpr Fmt kQ5KG{256, 176, 64, 1, "Q5_K (ggml)", nullptr};
+constexpr Fmt kQ6KG{256, 210, 64, 1, "Q6_K (ggml)", nullptr, 256};
 
 thread_local std::string g_global_error = "no error";
 
@@ -342,7 +362,7 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         const size_t need = (size_t)nxb * XREC_BYTES;
         const int st0 = ensure_ws(c, need, kname);
         if (st0 != RT_OK) return st0;
-        const bool q40 = f.blk_bytes == 18;
+        const bool q40 = f.q40perm;
         const char* pk = x_f16 ? (q40 ? "k_act_limbs_f16_q40" : "k_act_limbs_f16")
                                : (q40 ? "k_act_limbs_f32_q40" : "k_act_limbs_f32");
         const void* xin = a.x;
@@ -889,6 +909,41 @@ int rt_fused_ffn_q5k_f32(rt_ctx* c, const void* wg, const void* wu, const float*
     return ffn_launch(c, "k_ffn_q5k", kQ5K, wg, wu, x, act, ff, k);
 }
 
+// ───────────────────────────── ggml layouts ─────────────────────────────
+
+#define RT_GGML_GEMVS(NAME, FMT)                                                                 \
+    int rt_gemv_##NAME##_f32in_f32out(rt_ctx* c, const void* w, const float* x, float* y,       \
+                                      uint32_t m, uint32_t k) {                                  \
+        return gemv_plain(c, "k_gemv_" #NAME "_f32_f32", FMT, w, x, y, nullptr, false, m, k,     \
+                          false);                                                                \
+    }                                                                                            \
+    int rt_gemv_##NAME##_add_f32_f32in(rt_ctx* c, const void* w, const float* x, float* y,      \
+                                       const float* r, uint32_t m, uint32_t k) {                 \
+        return gemv_plain(c, "k_gemv_" #NAME "_f32_f32add", FMT, w, x, y, r, true, m, k, false); \
+    }                                                                                            \
+    int rt_gemv_##NAME##_f32in(rt_ctx* c, const void* w, const float* x, uint16_t* y,           \
+                               uint32_t m, uint32_t k) {                                         \
+        return gemv_plain(c, "k_gemv_" #NAME "_f32_f16", FMT, w, x, y, nullptr, false, m, k,     \
+                          false);                                                                \
+    }
+RT_GGML_GEMVS(q4_0g, kQ4_0G)
+RT_GGML_GEMVS(q4kg, kQ4KG)
+RT_GGML_GEMVS(q5kg, kQ5KG)
+RT_GGML_GEMVS(q6kg, kQ6KG)
+#undef RT_GGML_GEMVS
+int rt_fused_ffn_q4_0g_f32(rt_ctx* c, const void* wg, const void* wu, const float* x, float* act,
+                           uint32_t ff, uint32_t k) {
+    return ffn_launch(c, "k_ffn_q4_0g", kQ4_0G, wg, wu, x, act, ff, k);
+}
+int rt_fused_ffn_q4kg_f32(rt_ctx* c, const void* wg, const void* wu, const float* x, float* act,
+                          uint32_t ff, uint32_t k) {
+    return ffn_launch(c, "k_ffn_q4kg", kQ4KG, wg, wu, x, act, ff, k);
+}
+int rt_fused_ffn_q5kg_f32(rt_ctx* c, const void* wg, const void* wu, const float* x, float* act,
+                          uint32_t ff, uint32_t k) {
+    return ffn_launch(c, "k_ffn_q5kg", kQ5KG, wg, wu, x, act, ff, k);
+}
+
 // ───────────────────────────── fused ─────────────────────────────
 
 int rt_fused_qkv_q8_0_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
@@ -1052,6 +1107,18 @@ int rt_dequant_q5_0_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
 }
 int rt_dequant_q5k_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
     return elementwise_launch(c, "k_dequant_q5k_f32", in, out, (uint64_t)nb * 256);
+}
+int rt_dequant_q4_0g_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q4_0g_f32", in, out, (uint64_t)nb * 32);
+}
+int rt_dequant_q4kg_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q4kg_f32", in, out, (uint64_t)nb * 256);
+}
+int rt_dequant_q5kg_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q5kg_f32", in, out, (uint64_t)nb * 256);
+}
+int rt_dequant_q6kg_f32(rt_ctx* c, const void* in, float* out, uint32_t nb) {
+    return elementwise_launch(c, "k_dequant_q6kg_f32", in, out, (uint64_t)nb * 256);
 }
 int rt_dequant_q4k_f16(rt_ctx* c, const void* in, uint16_t* out, uint32_t nb) {
     return elementwise_launch(c, "k_dequant_q4k_f16", in, out, (uint64_t)nb * 256);

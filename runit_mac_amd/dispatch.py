@@ -88,13 +88,17 @@ _SIGS = {
         "rt_gemv_q4k_f32in_f32out", "rt_gemv_q4k_f16",
         "rt_gemv_q6k_f32in_f32out", "rt_gemv_q6k_f32in",
         "rt_gemv_q5_0_f32in_f32out", "rt_gemv_q5_0_f32in",
-        "rt_gemv_q5k_f32in_f32out", "rt_gemv_q5k_f32in")},
+        "rt_gemv_q5k_f32in_f32out", "rt_gemv_q5k_f32in",
+        *[f"rt_gemv_{g}_{v}" for g in ("q4_0g", "q4kg", "q5kg", "q6kg")
+          for v in ("f32in_f32out", "f32in")])},
     **{n: [_P, _P, _P, _P, _P, _U32, _U32] for n in (
         "rt_gemv_q8_0_add_f32_f32in", "rt_gemv_q8_0_add_f16", "rt_gemv_q8_0_add_f32res_f16",
         "rt_gemv_q8_0_add_f32_f32in_mr",
         "rt_gemv_q4_0_add_f32_f32in", "rt_gemv_q4_0_add_f16",
         "rt_gemv_q4k_add_f32_f32in", "rt_gemv_q4k_add_f16", "rt_gemv_q4k_add_f32res_f16",
-        "rt_gemv_q6k_add_f32_f32in", "rt_gemv_q5_0_add_f32_f32in", "rt_gemv_q5k_add_f32_f32in")},
+        "rt_gemv_q6k_add_f32_f32in", "rt_gemv_q5_0_add_f32_f32in", "rt_gemv_q5k_add_f32_f32in",
+        "rt_gemv_q4_0g_add_f32_f32in", "rt_gemv_q4kg_add_f32_f32in", "rt_gemv_q5kg_add_f32_f32in",
+        "rt_gemv_q6kg_add_f32_f32in")},
     "rt_fused_qkv_q8_0_f32": [_P] + [_P] * 7 + [_U32] * 3,
     "rt_fused_qkv_bias_q8_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
     "rt_fused_qkv_bias_q4_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
@@ -102,10 +106,12 @@ _SIGS = {
     "rt_fused_qkv_bias_q5k_f32": [_P] + [_P] * 10 + [_U32] * 3,
     **{n: [_P, _P, _P, _P, _P, _U32, _U32] for n in (
         "rt_fused_ffn_q8_0_f32", "rt_fused_ffn_q4_0_f32", "rt_fused_ffn_q4k_f32",
-        "rt_fused_ffn_q5_0_f32", "rt_fused_ffn_q5k_f32")},
+        "rt_fused_ffn_q5_0_f32", "rt_fused_ffn_q5k_f32", "rt_fused_ffn_q4_0g_f32",
+        "rt_fused_ffn_q4kg_f32", "rt_fused_ffn_q5kg_f32")},
     **{n: [_P, _P, _P, _U32] for n in (
         "rt_dequant_q8_0_f32", "rt_dequant_q4_0_f32", "rt_dequant_q4k_f32",
-        "rt_dequant_q6k_f32", "rt_dequant_q4k_f16", "rt_dequant_q5_0_f32", "rt_dequant_q5k_f32", "rt_argmax_f32", "rt_argmax_f16")},
+        "rt_dequant_q6k_f32", "rt_dequant_q4k_f16", "rt_dequant_q5_0_f32", "rt_dequant_q5k_f32",
+        "rt_dequant_q4_0g_f32", "rt_dequant_q4kg_f32", "rt_dequant_q5kg_f32", "rt_dequant_q6kg_f32", "rt_argmax_f32", "rt_argmax_f16")},
     "rt_gemm_q8_0_f32": [_P, _P, _P, _P, _U32, _U32, _U32],
     "rt_rms_norm_f32_f32_f32g": [_P, _P, _P, _P, _F, _U32, _U32],
     "rt_fused_rope_qk_f32": [_P, _P, _P, _U32, _U32, _U32, _U32, _F],
@@ -386,6 +392,11 @@ gemv_q5_0_add_f32_f32in = _gemv_add("gemv_q5_0_add_f32_f32in")
 gemv_q5k_f32in_f32out = _gemv("gemv_q5k_f32in_f32out")
 gemv_q5k_f32in = _gemv("gemv_q5k_f32in")
 gemv_q5k_add_f32_f32in = _gemv_add("gemv_q5k_add_f32_f32in")
+# ggml layouts (upstream GGUF files): q4_0g, q4kg, q5kg, q6kg
+for _g in ("q4_0g", "q4kg", "q5kg", "q6kg"):
+    globals()[f"gemv_{_g}_f32in_f32out"] = _gemv(f"gemv_{_g}_f32in_f32out")
+    globals()[f"gemv_{_g}_f32in"] = _gemv(f"gemv_{_g}_f32in")
+    globals()[f"gemv_{_g}_add_f32_f32in"] = _gemv_add(f"gemv_{_g}_add_f32_f32in")
 
 
 def fused_qkv_q8_0_f32(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, q_dim, kv_dim, k):
@@ -449,6 +460,21 @@ def fused_ffn_q5_0_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
 def fused_ffn_q5k_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
     """Q5_K twin of dispatch.rs:903-921 (new)."""
     _call(ctx, "rt_fused_ffn_q5k_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
+
+
+def fused_ffn_q4_0g_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
+    """ggml-layout Q4_0 twin of dispatch.rs:903-921 (new)."""
+    _call(ctx, "rt_fused_ffn_q4_0g_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
+
+
+def fused_ffn_q4kg_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
+    """ggml-layout Q4_K twin of dispatch.rs:903-921 (new)."""
+    _call(ctx, "rt_fused_ffn_q4kg_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
+
+
+def fused_ffn_q5kg_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):
+    """ggml-layout Q5_K twin of dispatch.rs:903-921 (new)."""
+    _call(ctx, "rt_fused_ffn_q5kg_f32", *map(_ptr, (w_gate, w_up, x_vec, act_out)), ff_dim, k)
 
 
 def dequant_q4k_f16(ctx, input, output, n_blocks):
@@ -569,7 +595,8 @@ def stream_copy(ctx, dst, src, nbytes):
 
 # Block geometry (crates/gguf/src/types.rs:158-191).
 BLOCK = {"q8_0": (32, 34), "q4_0": (32, 18), "q4k": (256, 144), "q6k": (256, 210),
-         "q5_0": (32, 22), "q5k": (256, 176)}
+         "q5_0": (32, 22), "q5k": (256, 176),
+         "q4_0g": (32, 18), "q4kg": (256, 144), "q5kg": (256, 176), "q6kg": (256, 210)}
 
 
 def weight_bytes(fmt: str, n: int, k: int) -> int:

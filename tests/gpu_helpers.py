@@ -14,9 +14,32 @@ F16_SUB = 2.0 ** -25       # half the smallest binary16 subnormal
 F32_EPS = 2.0 ** -24
 
 
+GGML = ("q4_0g", "q4kg", "q5kg", "q6kg")
+
+
+def ggml_from_reference(fmt: str, raw: np.ndarray) -> np.ndarray:
+    """ggml-layout bytes for a reference-layout stream (values preserved;
+    Q6_K's odd scale slots, unused by the reference layout, get a value next
+    to their even neighbour so that the 16-scale indexing is exercised)."""
+    base = fmt[:-1]
+    if base != "q6k":
+        return ora.relayout_to_ggml(base, raw)
+    blk = raw.reshape(-1, 210).copy()
+    sc = blk[:, 192:208].view(np.int8)
+    delta = (np.arange(blk.shape[0])[:, None] + np.arange(8)[None, :]) % 5 - 2
+    sc[:, 1::2] = np.clip(sc[:, 0::2].astype(np.int32) + delta, -127, 127).astype(np.int8)
+    return blk.reshape(-1)
+
+
 def device_weights(ctx, fmt: str, n: int, k: int, seed: int, std: float = 0.02):
     """Generates N(0, std) weights quantised per block on the device and
-    returns (device buffer, host copy of the packed bytes)."""
+    returns (device buffer, host copy of the packed bytes).  ggml layouts:
+    the reference-layout stream re-laid out on the host."""
+    if fmt in GGML:
+        buf, raw = device_weights(ctx, fmt[:-1], n, k, seed, std)
+        g = ggml_from_reference(fmt, raw)
+        buf.write(g)
+        return buf, g
     nbytes = d.weight_bytes(fmt, n, k)
     buf = ctx.new_buffer(nbytes)
     el, _ = d.BLOCK[fmt]

@@ -11,9 +11,11 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_DIR = os.path.join(REPO, "oracle")
 LIB = os.path.join(ORACLE_DIR, "liboracle.so")
 
-FMT = {"q8_0": 0, "q4_0": 1, "q4k": 2, "q6k": 3, "q5_0": 4, "q5k": 5}
+FMT = {"q8_0": 0, "q4_0": 1, "q4k": 2, "q6k": 3, "q5_0": 4, "q5k": 5,
+       "q4_0g": 6, "q4kg": 7, "q5kg": 8, "q6kg": 9}  # …g: ggml layouts
 BLOCK = {"q8_0": (32, 34), "q4_0": (32, 18), "q4k": (256, 144), "q6k": (256, 210),
-         "q5_0": (32, 22), "q5k": (256, 176)}
+         "q5_0": (32, 22), "q5k": (256, 176),
+         "q4_0g": (32, 18), "q4kg": (256, 144), "q5kg": (256, 176), "q6kg": (256, 210)}
 
 
 def _load():
@@ -44,6 +46,7 @@ _lib.ora_rope.argtypes = [_P, _S, _S, ctypes.c_uint32, ctypes.c_float]
 _lib.ora_attention.argtypes = [_P, _P, _P, _S, _S, _S, _S, _S, ctypes.c_double, _P]
 for _n in FMT:
     getattr(_lib, f"ora_quantize_{_n}").argtypes = [_P, _S, _P]
+_lib.ora_relayout_to_ggml.argtypes = [ctypes.c_int, _P, _S, _P]
 
 
 def _p(a: np.ndarray):
@@ -115,6 +118,15 @@ def quantize(fmt: str, w: np.ndarray) -> np.ndarray:
     nblk = w.size // el
     out = np.zeros(nblk * by, dtype=np.uint8)
     getattr(_lib, f"ora_quantize_{fmt}")(_p(w), nblk, _p(out))
+    return out
+
+
+def relayout_to_ggml(fmt: str, packed: np.ndarray) -> np.ndarray:
+    """Reference-layout blocks (q4_0 / q4k / q5k) re-laid out in ggml's."""
+    el, by = BLOCK[fmt]
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.empty_like(packed)
+    _lib.ora_relayout_to_ggml(FMT[fmt], _p(packed), packed.size // by, _p(out))
     return out
 
 

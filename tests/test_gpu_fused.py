@@ -69,7 +69,9 @@ def ffn_check(got, gate_ref, gate_s, up_ref, up_s, what):
                                       ("q4_0", 1000, 3584), ("q4_0", 77, 256),
                                       ("q4k", 1000, 3584), ("q4k", 33, 512),
                                       ("q5_0", 1000, 3584), ("q5_0", 45, 160),
-                                      ("q5k", 1000, 3584), ("q5k", 33, 512)])
+                                      ("q5k", 1000, 3584), ("q5k", 33, 512),
+                                      ("q4_0g", 1000, 3584), ("q4_0g", 45, 160),
+                                      ("q4kg", 1000, 3584), ("q5kg", 300, 1024)])
 def test_fused_ffn(ctx, fmt, ff, k):
     wg, rg = device_weights(ctx, fmt, ff, k, seed=ff + 1)
     wu, ru = device_weights(ctx, fmt, ff, k, seed=ff + 2)

@@ -15,7 +15,7 @@ from runit_mac_amd import dispatch as d
 
 pytestmark = pytest.mark.gpu
 
-FMTS = ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k"]
+FMTS = ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg"]
 
 VARIANTS = {
     "q8_0": ["f32in_f32out", "add_f32_f32in", "f32in", "f16", "add_f16", "add_f32res_f16",
@@ -25,6 +25,7 @@ VARIANTS = {
     "q6k": ["f32in_f32out", "add_f32_f32in", "f32in"],
     "q5_0": ["f32in_f32out", "add_f32_f32in", "f32in"],
     "q5k": ["f32in_f32out", "add_f32_f32in", "f32in"],
+    **{g: ["f32in_f32out", "add_f32_f32in", "f32in"] for g in ("q4_0g", "q4kg", "q5kg", "q6kg")},
 }
 
 
@@ -123,7 +124,7 @@ def test_gemv_variants(ctx, fmt, n, k):
         run_variant(ctx, fmt, var, wbuf, raw, n, k, seed=17 * i + n)
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0", "q4_0g"])
 @pytest.mark.parametrize("k", [32, 64, 96, 160])
 def test_gemv_small_and_odd_block_counts(ctx, fmt, k):
     n = 77

@@ -203,7 +203,8 @@ def test_gemv_all_ones_closed_form(fmt):
     assert np.all(s == k * (k + 1) / 2)
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg",
+                                 "q5kg", "q6kg"])
 def test_gemv_brute_force(fmt):
     n, k = 7, 512
     w = ora.synth_weights(fmt, n, k, seed=11)
@@ -266,20 +267,21 @@ def test_argmax_rust_max_by_semantics():
 
 # ───────────────────────── quantiser invariants ─────────────────────────
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg",
+                                 "q5kg"])
 def test_quantizer_round_trip_error_bounded(fmt):
     n_el = 256 * 16
     w = (0.02 * ora.synth_normal(99, n_el)).astype(np.float32)
     v = ora.dequant(fmt, ora.quantize(fmt, w))
     err = np.abs(v - w)
-    el = 32 if fmt in ("q8_0", "q4_0", "q5_0") else 256
+    el = 32 if fmt in ("q8_0", "q4_0", "q5_0", "q4_0g") else 256
     amax = np.abs(w).reshape(-1, el).max(axis=1).repeat(el)
     # half a step plus the f16 rounding of the scale: Q8_0 step amax/127
     # (q uses the unrounded d, so up to 127·2^-11 steps more), Q4_0 amax/8
     # (plus one clamped step at +8), Q4_K ≈ range/15, Q6_K amax/32
     # Q5_0 amax/16 (plus one clamped step at +16), Q5_K ≈ range/31
     bound = {"q8_0": 0.6 / 127, "q4_0": 1.01 / 8, "q4k": 0.2, "q6k": 0.08, "q5_0": 1.01 / 16,
-             "q5k": 0.1}[fmt]
+             "q5k": 0.1, "q4_0g": 1.01 / 8, "q4kg": 0.2, "q5kg": 0.1}[fmt]
     assert np.all(err <= bound * amax + 1e-7)
 
 
@@ -414,3 +416,70 @@ def test_q5k_without_high_bits_equals_q4k():
     v5 = ora.dequant("q5k", np.frombuffer(bytes(hdr) + bytes(32) + qs, np.uint8))
     v4 = ora.dequant("q4k", np.frombuffer(bytes(hdr) + qs, np.uint8))
     assert np.array_equal(v5, v4)
+
+
+# ───────────────────────── ggml layouts ─────────────────────────
+# Known answers written from ggml's block definitions (not from the oracle):
+# they pin the element ↔ nibble/bit/scale maps that differ from the
+# reference's layouts.
+
+def test_q4_0g_byte_j_holds_elements_j_and_j_plus_16():
+    c = [(5 * e + 2) % 16 for e in range(32)]
+    qs = bytes(c[j] | (c[j + 16] << 4) for j in range(16))
+    v = ora.dequant("q4_0g", np.frombuffer(h16(0.5) + qs, np.uint8))
+    assert np.array_equal(v, 0.5 * (np.array(c) - 8))
+
+
+def _scale_table(sc, m):
+    S = [0] * 12
+    for j in range(4):
+        S[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        S[j + 4] = (m[j] & 63) | ((m[j + 4] >> 4) << 6)
+        S[j + 8] = (sc[j + 4] & 15) | ((m[j + 4] & 15) << 4)
+    return bytes(S)
+
+
+@pytest.mark.parametrize("s", range(8))
+def test_q4kg_sub_block_s_covers_elements_32s(s):
+    # ggml: sub-block s scales elements 32s..32s+31 (chunk s//2, low nibbles
+    # for even s, high for odd); the reference layout would light up
+    # 64·(s%4) + 32·(s//4) instead
+    sc = [0] * 8
+    sc[s] = 9
+    qs = bytes([0x53] * 128)  # low nibble 3, high nibble 5
+    blk = h16(0.25) + h16(0.0) + _scale_table(sc, [0] * 8) + qs
+    v = ora.dequant("q4kg", np.frombuffer(blk, np.uint8))
+    nz = np.nonzero(v)[0]
+    assert nz.min() == 32 * s and nz.max() == 32 * s + 31
+    assert np.all(v[nz] == 0.25 * 9 * (5 if s % 2 else 3))
+
+
+def test_q5kg_fifth_bit_is_bit_2j_plus_half_of_qh_l():
+    sc, m = [1] * 8, [0] * 8
+    base = h16(1.0) + h16(0.0) + _scale_table(sc, m)
+    qh = bytearray(32)
+    qh[11] = 1 << 3  # j = 1, high half, l = 11 → element 64 + 32 + 11 = 107
+    v0 = ora.dequant("q5kg", np.frombuffer(base + bytes(32) + bytes(128), np.uint8))
+    v1 = ora.dequant("q5kg", np.frombuffer(base + bytes(qh) + bytes(128), np.uint8))
+    assert np.all(v0 == 0)
+    assert np.nonzero(v1)[0].tolist() == [107] and v1[107] == 16.0
+
+
+def test_q6kg_every_16_elements_have_their_own_scale():
+    # only sc[1] non-zero: ggml applies it to l in 16..31 of t = 0, h = 0, i.e.
+    # elements 16..31; the reference layout never reads odd slots
+    ql, qh = bytes([0x11] * 128), bytes(64)  # codes 1 → q = 1 − 32 = −31
+    sc = bytearray(16)
+    sc[1] = 3
+    v = ora.dequant("q6kg", np.frombuffer(ql + qh + bytes(sc) + h16(2.0), np.uint8))
+    nz = np.nonzero(v)[0]
+    assert nz.tolist() == list(range(16, 32)) and np.all(v[nz] == 2.0 * 3 * -31)
+    vr = ora.dequant("q6k", np.frombuffer(ql + qh + bytes(sc) + h16(2.0), np.uint8))
+    assert np.all(vr == 0)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4k", "q5k"])
+def test_relayout_to_ggml_preserves_values(fmt):
+    w = (0.02 * ora.synth_normal(21, 256 * 8)).astype(np.float32)
+    r = ora.quantize(fmt, w)
+    assert np.array_equal(ora.dequant(fmt, r), ora.dequant(fmt + "g", ora.relayout_to_ggml(fmt, r)))
