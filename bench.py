@@ -125,7 +125,7 @@ class Workload:
         elif self.kind == "ffn":
             getattr(d, f"fused_ffn_{f}_f32")(ctx, w[0], w[1], self.x, self.y, n, k)
         elif self.kind == "gemm":
-            d.gemm_q8_0_f32(ctx, w[0], self.x, self.y, self.m, n, k)
+            getattr(d, f"gemm_{f}_f32")(ctx, w[0], self.x, self.y, self.m, n, k)
         else:
             raise ValueError(self.kind)
 
@@ -452,6 +452,11 @@ def gemv_specs(ctx, suite):
             ("c4g_q6kg_lmhead_152064x3584", lambda: Workload(ctx, "c4g_lm", "q6kg", "gemv", 152064, 3584, seed=18)),
             ("c3g_q4_0g_ffn_2x18944x3584", lambda: Workload(ctx, "c3g_ffn", "q4_0g", "ffn", 18944, 3584, seed=19)),
         ]
+        for fmt in ("q4_0", "q4k"):  # verify / prefill GEMM of the 4-bit 7B formats
+            for m in (4, 16, 32):
+                specs.append((f"c5q_gemm_{fmt}_m{m}_18944x3584",
+                              (lambda m=m, fmt=fmt: Workload(ctx, "c5q", fmt, "gemm", 18944, 3584,
+                                                             m=m, seed=20))))
         for m in (1, 4, 8, 16, 32):
             specs.append((f"c5_gemm_q8_0_m{m}_18944x3584",
                           (lambda m=m: Workload(ctx, "c5", "q8_0", "gemm", 18944, 3584, m=m, seed=11))))

@@ -310,6 +310,15 @@ int rt_dequant_q4k_f16(rt_ctx* ctx, const void* input, uint16_t* output, uint32_
  * weights in verify_draft (forward.rs:2193-2271, gemm.metal:39-190). */
 int rt_gemm_q8_0_f32(rt_ctx* ctx, const void* weight, const float* x, float* y,
                      uint32_t m_rows, uint32_t n, uint32_t k);
+/* New: the same batched GEMM on Q4_0 and Q4_K weights in the reference's
+ * layouts (7B verify / prefill of Q4_0 and Q4_K_M files; the reference
+ * dequantises to f16 for gemm_f16, forward.rs:2193-2271).  Q4_K needs k a
+ * multiple of 256.  Shapes whose row segments are not 8/16-byte aligned run
+ * as one GEMV per activation row. */
+int rt_gemm_q4_0_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k);
+int rt_gemm_q4k_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
+                    uint32_t n, uint32_t k);
 
 /* ───────────────────────── argmax ───────────────────────── */
 

@@ -36,7 +36,8 @@ struct GemmArgs {
 // Rows past M are zero.
 template <int MG>
 RT_DEV void gemm_prep_body(const float* __restrict__ x, uint32_t M, uint32_t K, uint32_t nchunks,
-                           uint32_t* __restrict__ aops, int* __restrict__ etab) {
+                           uint32_t* __restrict__ aops, int* __restrict__ etab,
+                           float* __restrict__ stab) {
     const uint32_t nxb = K / 32;
     constexpr uint32_t ROWS = 4 * MG;
     const uint64_t total = (uint64_t)nchunks * ROWS * nxb * 8;
@@ -65,12 +66,29 @@ RT_DEV void gemm_prep_body(const float* __restrict__ x, uint32_t M, uint32_t K, 
             base[lane * 2 + (q & 1)] = k < 3 ? pack_i8x4(l[k]) : 0u;
         }
         if (q == 0) etab[(((size_t)ch * nxb + b) * 4 + mm) * MG + g] = e;
+        if (stab) {
+            // Σx over the record as its limbs represent it (for formats with a
+            // per-sub-block min): the 8 lanes of the record reduce their sums
+            int sk[3];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                int v2 = l[k][0] + l[k][1] + l[k][2] + l[k][3];
+                v2 += __shfl_xor(v2, 1, 64);
+                v2 += __shfl_xor(v2, 2, 64);
+                v2 += __shfl_xor(v2, 4, 64);
+                sk[k] = v2;
+            }
+            if (q == 0)
+                stab[(((size_t)ch * nxb + b) * 4 + mm) * MG + g] =
+                    __builtin_amdgcn_ldexpf(limb_combine(sk[0], sk[1], sk[2]), e - 22);
+        }
     }
 }
 #define RT_GEMM_PREP(MG)                                                                       \
     extern "C" __global__ void __launch_bounds__(256) k_gemm_x_prep_mg##MG(                    \
-        const float* x, uint32_t M, uint32_t K, uint32_t nchunks, uint32_t* aops, int* etab) { \
-        gemm_prep_body<MG>(x, M, K, nchunks, aops, etab);                                      \
+        const float* x, uint32_t M, uint32_t K, uint32_t nchunks, uint32_t* aops, int* etab,   \
+        float* stab) {                                                                         \
+        gemm_prep_body<MG>(x, M, K, nchunks, aops, etab, stab);                                \
     }
 RT_GEMM_PREP(1)
 RT_GEMM_PREP(2)
@@ -229,29 +247,90 @@ struct Gemm2Args {
     const uint8_t* w;
     const uint2* aops;
     const int* etab;
+    const float* stab;    // per-record activation sums (formats with a min)
     float* y;
     float* part;          // [chunk][split][chunk rows][N] partial sums (splits > 1)
     uint32_t* counters;   // [chunk][tile], cstride u32 slots apart
-    uint32_t M, N, nxb, tiles, splits, kbs, nchunks;
+    uint32_t M, N, nxb, tiles, splits, kbs, nchunks;  // nxb, kbs: in weight blocks
     uint64_t row_bytes;
     uint32_t cstride;
 };
 
-template <int MG, int NB>
+// Block formats of the staged GEMM.  decode() gives, for record r of a
+// stage (32 elements) and lane group c (elements 8c..8c+7), the 8 int8
+// weight values in element order (the B operand), the record's scale and,
+// for formats with a per-sub-block min, dmin·m (y += dsc·q·x − mn·Σx).
+struct GemmQ8_0 {  // gemv_q8_0.metal:11-17
+    static constexpr uint32_t BLK_BYTES = 34, RECS = 1;
+    static constexpr bool HAS_MIN = false;
+    RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
+                              float& mn) {
+        const uint32_t o = r * 34 + 2 + 8 * c;  // (row is 4-byte aligned)
+        const uint32_t* pw = (const uint32_t*)(row + (o & ~3u));
+        const uint32_t sh = o & 3;
+        const uint32_t w0 = pw[0], w1 = pw[1], w2 = pw[sh ? 2 : 1];
+        const uint32_t q0 = alignb(w1, w0, sh), q1 = alignb(w2, w1, sh);
+        B = (i64_t)(((uint64_t)q1 << 32) | q0);
+        dsc = h2f(*(const uint16_t*)(row + r * 34));
+        mn = 0.0f;
+    }
+};
+struct GemmQ4_0 {  // reference layout: byte i = elements 2i (low), 2i+1 (high)
+    static constexpr uint32_t BLK_BYTES = 18, RECS = 1;
+    static constexpr bool HAS_MIN = false;
+    RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
+                              float& mn) {
+        const uint32_t off = r * 18 + 2 + 4 * c;  // bytes 4c..4c+3 of the quants
+        const uint32_t* pw = (const uint32_t*)(row + (off & ~3u));
+        const uint32_t w = alignb(pw[(off & 3) ? 1 : 0], pw[0], off & 3);
+        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        // interleave (lo0 hi0 lo1 hi1) (lo2 hi2 lo3 hi3), then nib − 8 per byte
+        const uint32_t e0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+        const uint32_t e1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+        const uint32_t q0 = (e0 + 0x78787878u) ^ 0x80808080u;
+        const uint32_t q1 = (e1 + 0x78787878u) ^ 0x80808080u;
+        B = (i64_t)(((uint64_t)q1 << 32) | q0);
+        dsc = h2f(*(const uint16_t*)(row + r * 18));
+        mn = 0.0f;
+    }
+};
+struct GemmQ4K {  // reference layout: record 2j (low nibbles of qs[32j..]) uses
+                  // sub-block j, record 2j+1 (high nibbles) sub-block j + 4
+    static constexpr uint32_t BLK_BYTES = 144, RECS = 8;
+    static constexpr bool HAS_MIN = true;
+    RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
+                              float& mn) {
+        const uint8_t* blk = row + (r / 8) * 144;
+        const uint32_t rec = r % 8, j = rec / 2, hi = rec & 1;
+        const uint2 q = *(const uint2*)(blk + 16 + 32 * j + 8 * c);
+        const uint32_t q0 = hi ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+        const uint32_t q1 = hi ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+        B = (i64_t)(((uint64_t)q1 << 32) | q0);
+        const u32x4 hdr = *(const u32x4*)blk;
+        uint32_t sc, m;
+        kq_scale_min(hi ? j + 4 : j, hdr.y, hdr.z, hdr.w, sc, m);
+        dsc = h2f(hdr.x) * (float)sc;
+        mn = h2f(hdr.x >> 16) * (float)m;
+    }
+};
+
+template <class P, int MG, int NB>
 RT_DEV void gemm2_body(const Gemm2Args& a) {
-    constexpr uint32_t SEG = NB * 34;                   // bytes of a row segment
-    constexpr uint32_t VB = NB == 8 ? 16 : 8;           // bytes per W load (alignment)
-    typedef typename std::conditional<NB == 8, u32x4, uint2>::type WV;
-    constexpr uint32_t WPR = SEG / VB;                  // W loads per row segment
-    constexpr uint32_t WV_N = GB_ROWS * WPR;            // W loads per stage
-    constexpr uint32_t AV4 = NB * MG * 64 * 8 / 16;     // dwordx4 of A per stage
-    constexpr uint32_t EV4 = NB * 4 * MG * 4 / 16;      // dwordx4 of E per stage
-    constexpr uint32_t WPT = (WV_N + 255) / 256;        // W loads per thread
+    constexpr uint32_t NR = NB * P::RECS;                  // records per stage
+    constexpr uint32_t SEG = NB * P::BLK_BYTES;            // bytes of a row segment
+    constexpr uint32_t VB = SEG % 16 == 0 ? 16 : 8;        // bytes per W load (alignment)
+    typedef typename std::conditional<VB == 16, u32x4, uint2>::type WV;
+    constexpr uint32_t WPR = SEG / VB;                     // W loads per row segment
+    constexpr uint32_t WV_N = GB_ROWS * WPR;               // W loads per stage
+    constexpr uint32_t AV4 = NR * MG * 64 * 8 / 16;        // dwordx4 of A per stage
+    constexpr uint32_t EV4 = NR * 4 * MG * 4 / 16;         // dwordx4 of E (and of S) per stage
+    constexpr uint32_t WPT = (WV_N + 255) / 256;           // W loads per thread
     constexpr uint32_t APT = (AV4 + 255) / 256;
-    static_assert(SEG % VB == 0, "segment alignment");
+    static_assert(SEG % VB == 0 && EV4 <= 256, "segment alignment");
     __shared__ WV lw[2][WV_N];
     __shared__ u32x4 la[2][AV4];
     __shared__ u32x4 le[2][EV4 > 0 ? EV4 : 1];
+    __shared__ u32x4 ls[P::HAS_MIN ? 2 : 1][P::HAS_MIN ? EV4 : 1];
     __shared__ uint32_t last_flag;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint32_t j = lane & 15, c = lane >> 4;
@@ -265,25 +344,29 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
         const uint32_t kb1 = min(a.nxb, kb0 + a.kbs);
         const uint32_t nst = (kb1 - kb0) / NB;
         const uint32_t row0 = tile * GB_ROWS;
-        const uint2* ap = a.aops + (size_t)ch * a.nxb * MG * 64;
-        const int* ep = a.etab + (size_t)ch * a.nxb * 4 * MG;
+        const uint32_t nrec = a.nxb * P::RECS;
+        const uint2* ap = a.aops + (size_t)ch * nrec * MG * 64;
+        const int* ep = a.etab + (size_t)ch * nrec * 4 * MG;
+        const float* sp = P::HAS_MIN ? a.stab + (size_t)ch * nrec * 4 * MG : nullptr;
 
         WV rw[WPT];
-        u32x4 ra[APT], re;
+        u32x4 ra[APT], re, rs;
         auto gload = [&](uint32_t st) {
-            const uint32_t b0 = kb0 + st * NB;
+            const uint32_t b0 = kb0 + st * NB;  // first block of the stage
+            const uint32_t r0 = b0 * P::RECS;   // its first record
 #pragma unroll
             for (uint32_t i = 0; i < WPT; ++i) {
                 uint32_t f = tid + 256 * i;
                 if (f >= WV_N) f = WV_N - 1;  // duplicate load, not stored
                 const uint32_t r = f / WPR, col = f % WPR;
                 const uint32_t n = min(row0 + r, a.N - 1);
-                rw[i] = *(const WV*)(a.w + (size_t)n * a.row_bytes + (size_t)b0 * 34 + col * VB);
+                rw[i] = *(const WV*)(a.w + (size_t)n * a.row_bytes + (size_t)b0 * P::BLK_BYTES + col * VB);
             }
-            const u32x4* as = (const u32x4*)(ap + (size_t)b0 * MG * 64);
+            const u32x4* as = (const u32x4*)(ap + (size_t)r0 * MG * 64);
 #pragma unroll
             for (uint32_t i = 0; i < APT; ++i) ra[i] = as[min(tid + 256 * i, AV4 - 1)];
-            re = ((const u32x4*)(ep + (size_t)b0 * 4 * MG))[min(tid, EV4 - 1)];
+            re = ((const u32x4*)(ep + (size_t)r0 * 4 * MG))[min(tid, EV4 - 1)];
+            if (P::HAS_MIN) rs = ((const u32x4*)(sp + (size_t)r0 * 4 * MG))[min(tid, EV4 - 1)];
         };
         auto lstore = [&](uint32_t buf) {
 #pragma unroll
@@ -293,36 +376,38 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
             for (uint32_t i = 0; i < APT; ++i)
                 if (tid + 256 * i < AV4) la[buf][tid + 256 * i] = ra[i];
             if (tid < EV4) le[buf][tid] = re;
+            if (P::HAS_MIN && tid < EV4) ls[P::HAS_MIN ? buf : 0][tid] = rs;
         };
         float acc[MG];
 #pragma unroll
         for (int g = 0; g < MG; ++g) acc[g] = 0.0f;
         const uint32_t wrow = (16 * wv + j) * SEG;  // this lane's row in a W buffer
         auto compute = [&](uint32_t buf) {
-            const uint8_t* wb = (const uint8_t*)lw[buf];
+            const uint8_t* wb = (const uint8_t*)lw[buf] + wrow;
             const uint2* ab = (const uint2*)la[buf];
             const int* eb = (const int*)le[buf];
+            const float* sb = (const float*)ls[P::HAS_MIN ? buf : 0];
 #pragma unroll 2
-            for (uint32_t blk = 0; blk < NB; ++blk) {
-                const uint32_t o = wrow + blk * 34 + 2 + 8 * c;  // LDS byte offset of the quants
-                const uint32_t* pw = (const uint32_t*)(wb + (o & ~3u));
-                const uint32_t sh = o & 3;
-                const uint32_t w0 = pw[0], w1 = pw[1], w2 = pw[(o & 3) ? 2 : 1];
-                const uint32_t q0 = alignb(w1, w0, sh), q1 = alignb(w2, w1, sh);
-                const i64_t B = (i64_t)(((uint64_t)q1 << 32) | q0);
-                const float d = h2f(*(const uint16_t*)(wb + wrow + blk * 34));
-                // all of the block's matrix-core products first, then their
+            for (uint32_t r = 0; r < NR; ++r) {
+                i64_t B;
+                float dsc, mn;
+                P::decode(wb, r, c, B, dsc, mn);
+                // all of the record's matrix-core products first, then their
                 // epilogues (independent MFMAs overlap in the pipeline)
                 v4i C[MG];
 #pragma unroll
                 for (int g = 0; g < MG; ++g) {
-                    const uint2 av = ab[(blk * MG + g) * 64 + lane];
+                    const uint2 av = ab[(r * MG + g) * 64 + lane];
                     const i64_t A = (i64_t)(((uint64_t)av.y << 32) | av.x);
                     C[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, v4i{0, 0, 0, 0}, 0, 0, 0);
                 }
 #pragma unroll
-                for (int g = 0; g < MG; ++g)
-                    acc[g] += __builtin_amdgcn_ldexpf(d * comb4(C[g]), eb[(blk * 4 + c) * MG + g] - 22);
+                for (int g = 0; g < MG; ++g) {
+                    const uint32_t ei = (r * 4 + c) * MG + g;
+                    float v = __builtin_amdgcn_ldexpf(dsc * comb4(C[g]), eb[ei] - 22);
+                    if (P::HAS_MIN) v -= mn * sb[ei];
+                    acc[g] += v;
+                }
             }
         };
         if (nst > 0) {
@@ -373,11 +458,22 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
         __syncthreads();
     }
 }
-#define RT_GEMM2_KERNEL(MG, NB)                                                                \
-    extern "C" __global__ void __launch_bounds__(256) k_gemm2_q8_0_mg##MG(Gemm2Args a) {      \
-        gemm2_body<MG, NB>(a);                                                                 \
+#define RT_GEMM2_KERNEL(FN, P, MG, NB)                                                        \
+    extern "C" __global__ void __launch_bounds__(256) k_gemm2_##FN##_mg##MG(Gemm2Args a) {    \
+        gemm2_body<P, MG, NB>(a);                                                              \
     }
-RT_GEMM2_KERNEL(1, 8)
-RT_GEMM2_KERNEL(2, 8)
-RT_GEMM2_KERNEL(4, 4)
-RT_GEMM2_KERNEL(8, 4)
+// NB: blocks per stage (Q8_0 / Q4_0: 8 records, or 4 for large batches so
+// that the stage's operands leave room for 2+ workgroups per CU; Q4_K: one
+// 256-element super-block = 8 records)
+RT_GEMM2_KERNEL(q8_0, GemmQ8_0, 1, 8)
+RT_GEMM2_KERNEL(q8_0, GemmQ8_0, 2, 8)
+RT_GEMM2_KERNEL(q8_0, GemmQ8_0, 4, 4)
+RT_GEMM2_KERNEL(q8_0, GemmQ8_0, 8, 4)
+RT_GEMM2_KERNEL(q4_0, GemmQ4_0, 1, 8)
+RT_GEMM2_KERNEL(q4_0, GemmQ4_0, 2, 8)
+RT_GEMM2_KERNEL(q4_0, GemmQ4_0, 4, 4)
+RT_GEMM2_KERNEL(q4_0, GemmQ4_0, 8, 4)
+RT_GEMM2_KERNEL(q4k, GemmQ4K, 1, 1)
+RT_GEMM2_KERNEL(q4k, GemmQ4K, 2, 1)
+RT_GEMM2_KERNEL(q4k, GemmQ4K, 4, 1)
+RT_GEMM2_KERNEL(q4k, GemmQ4K, 8, 1)

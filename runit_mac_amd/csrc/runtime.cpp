@@ -127,6 +127,8 @@ const char* const kKernelNames[] = {
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
     "k_gemm_q8_0_mg1_ct2", "k_gemm_q8_0_mg2_ct2", "k_gemm_q8_0_mg4_ct2", "k_gemm_q8_0_mg8_ct2",
     "k_gemm2_q8_0_mg1", "k_gemm2_q8_0_mg2", "k_gemm2_q8_0_mg4", "k_gemm2_q8_0_mg8",
+    "k_gemm2_q4_0_mg1", "k_gemm2_q4_0_mg2", "k_gemm2_q4_0_mg4", "k_gemm2_q4_0_mg8",
+    "k_gemm2_q4k_mg1", "k_gemm2_q4k_mg2", "k_gemm2_q4k_mg4", "k_gemm2_q4k_mg8",
 };
 
 struct Fmt {
@@ -986,6 +988,7 @@ struct Gemm2Args {
     const void* w;
     const void* aops;
     const int* etab;
+    const float* stab;
     float* y;
     float* part;
     uint32_t* counters;
@@ -1002,90 +1005,131 @@ struct GemmArgs {
     uint64_t row_bytes;
 };
 
-int rt_gemm_q8_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
-                     uint32_t n, uint32_t k) {
+// Block formats of the batched GEMM (the k_gemm2_<name>_mg* kernels)
+struct GemmFmt {
+    const char* name;
+    uint32_t blk_el, blk_bytes, recs;  // recs: 32-element records per block
+    uint32_t nb_small, nb_large;       // blocks per stage for MG ≤ 2 / MG ≥ 4
+    bool has_min;                      // needs per-record activation sums
+    int (*gemv)(rt_ctx*, const void*, const float*, float*, uint32_t, uint32_t);
+};
+
+int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, float* y,
+                uint32_t m_rows, uint32_t n, uint32_t k) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     if (m_rows == 0 || n == 0) return RT_OK;
     if (!w || !x || !y)
-        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_q8_0_f32: null buffer");
-    if (k == 0 || k % 32 != 0)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_%s_f32: null buffer", f.name);
+    if (k == 0 || k % f.blk_el != 0)
         return fail(c, RT_ERR_DISPATCH,
-                    "kernel dispatch error: gemm_q8_0_f32: k=%u must be a positive multiple of 32",
-                    k);
+                    "kernel dispatch error: gemm_%s_f32: k=%u must be a positive multiple of %u",
+                    f.name, k, f.blk_el);
     if (!aligned(x, 16))
         return fail(c, RT_ERR_DISPATCH,
-                    "kernel dispatch error: gemm_q8_0_f32: input must be 16-byte aligned");
-    if (m_rows == 1) return rt_gemv_q8_0_f32in_f32out(c, w, x, y, n, k);
+                    "kernel dispatch error: gemm_%s_f32: input must be 16-byte aligned", f.name);
+    if (m_rows == 1) return f.gemv(c, w, x, y, n, k);
     const uint32_t cu = (uint32_t)c->cu_count;
     // 4·MG activation rows per chunk (MG ∈ {1, 2, 4, 8}); longer batches
     // take several chunks, each streaming W once
     const uint32_t groups = (m_rows + 3) / 4;
     const uint32_t MG = groups <= 1 ? 1 : groups <= 2 ? 2 : groups <= 4 ? 4 : 8;
     const uint32_t nchunks = (m_rows + 4 * MG - 1) / (4 * MG);
-    const uint32_t nxb = k / 32;
-    const size_t a_bytes = (size_t)nchunks * nxb * MG * 64 * 8;
-    const size_t e_bytes = (size_t)nchunks * nxb * 4 * MG * sizeof(int);
+    const uint32_t nrec = k / 32;        // activation records
+    const uint32_t nblk = k / f.blk_el;  // weight blocks per row
+    const uint64_t row_bytes = (uint64_t)nblk * f.blk_bytes;
+    const uint32_t NB = MG <= 2 ? f.nb_small : f.nb_large;
+    const uint32_t seg = NB * f.blk_bytes, vb = seg % 16 == 0 ? 16 : 8;
 
-    // Plan.  LDS-staged kernel when rows stream in 272-byte, 16-byte-aligned
-    // segments: 64-row tiles, K in stages of 8 blocks, items (tile, K split,
-    // chunk) on a persistent grid of `cap` workgroups.  Otherwise the direct
-    // kernel: 16·CT weight rows per workgroup whose ksw waves split the blocks.
-    const bool staged = nxb % 8 == 0 && aligned(w, 16) && !c->gemm_direct;
+    // Plan.  LDS-staged kernel when every row's stage segments stay
+    // vb-aligned: 64-row tiles, K in stages of NB blocks, items (tile, K
+    // split, chunk) on a persistent grid of `cap` workgroups.  Otherwise Q8_0
+    // takes the direct kernel (16·CT weight rows per workgroup whose ksw
+    // waves split the blocks) and the other formats one GEMV per row.
+    const bool staged = nblk % NB == 0 && aligned(w, 16) && row_bytes % vb == 0 && !c->gemm_direct;
+    const bool direct = !staged && f.blk_bytes == 34;
+    if (!staged && !direct) {
+        for (uint32_t m = 0; m < m_rows; ++m) {
+            const int st = f.gemv(c, w, x + (size_t)m * k, y + (size_t)m * n, n, k);
+            if (st != RT_OK) return st;
+        }
+        return RT_OK;
+    }
     const uint32_t tiles = (n + 63) / 64;
     const uint32_t per_cu = MG == 4 ? 4 : 3;  // LDS-bound residency (34-52 KB per workgroup)
     const uint32_t cap = cu * per_cu;
     const uint32_t base = tiles * nchunks;
-    uint32_t splits = 1, kbs = nxb;
+    uint32_t splits = 1, kbs = nblk;
     if (staged) {
         double best = 1e30;
-        for (uint32_t sp = 1; sp <= std::min<uint32_t>(16, nxb / 8); ++sp) {
+        for (uint32_t sp = 1; sp <= std::min<uint32_t>(16, nblk / NB); ++sp) {
             // rounds of items, each 1/sp of the K range, plus a small cost per split
             const double rounds = (double)((base * sp + cap - 1) / cap);
             const double t = rounds / sp + 0.02 * sp;
             if (t < best - 1e-9) { best = t; splits = sp; }
         }
-        kbs = ((nxb + splits - 1) / splits + 7) / 8 * 8;
-        splits = (nxb + kbs - 1) / kbs;
+        kbs = ((nblk + splits - 1) / splits + NB - 1) / NB * NB;
+        splits = (nblk + kbs - 1) / kbs;
         if (splits > 1 && base > kAttnCounters)
             return fail(c, RT_ERR_DISPATCH,
-                        "kernel dispatch error: gemm_q8_0_f32: %u tiles exceed %u counters", base,
-                        kAttnCounters);
+                        "kernel dispatch error: gemm_%s_f32: %u tiles exceed %u counters", f.name,
+                        base, kAttnCounters);
     }
+    const size_t a_bytes = (size_t)nchunks * nrec * MG * 64 * 8;
+    const size_t e_bytes = (size_t)nchunks * nrec * 4 * MG * sizeof(int);
+    const size_t s_bytes = f.has_min ? e_bytes : 0;
     const size_t p_bytes = splits > 1 ? (size_t)splits * nchunks * 4 * MG * n * sizeof(float) : 0;
-    int st = ensure_ws(c, a_bytes + e_bytes + p_bytes, "gemm_q8_0_f32");
+    int st = ensure_ws(c, a_bytes + e_bytes + s_bytes + p_bytes, "gemm");
     if (st != RT_OK) return st;
     void* aops = c->ws;
     int* etab = (int*)((char*)c->ws + a_bytes);
-    float* part = p_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes) : nullptr;
+    float* stab = s_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes) : nullptr;
+    float* part = p_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes + s_bytes) : nullptr;
     {
         char pk[48];
         snprintf(pk, sizeof pk, "k_gemm_x_prep_mg%u", MG);
-        const uint64_t threads = (uint64_t)nchunks * 4 * MG * nxb * 8;
+        const uint64_t threads = (uint64_t)nchunks * 4 * MG * nrec * 8;
         const uint32_t grid = (uint32_t)std::min<uint64_t>((threads + 255) / 256, (uint64_t)cu * 16);
         uint32_t M = m_rows, K = k, nc = nchunks;
-        void* pp[] = {(void*)&x, &M, &K, &nc, &aops, &etab};
+        void* pp[] = {(void*)&x, &M, &K, &nc, &aops, &etab, &stab};
         st = launch(c, pk, dim3(grid), dim3(256), 0, pp);
         if (st != RT_OK) return st;
     }
     if (staged) {
         uint32_t cstride = 32;  // counters on their own cache lines while they fit
         while (cstride > 1 && (size_t)base * cstride > kAttnCounters) cstride >>= 1;
-        Gemm2Args a2{w, aops, etab, y, part, (uint32_t*)((char*)c->aux + kAuxAttnOff),
-                     m_rows, n, nxb, tiles, splits, kbs, nchunks, (uint64_t)nxb * 34, cstride};
+        Gemm2Args a2{w, aops, etab, stab, y, part, (uint32_t*)((char*)c->aux + kAuxAttnOff),
+                     m_rows, n, nblk, tiles, splits, kbs, nchunks, row_bytes, cstride};
         char kn2[48];
-        snprintf(kn2, sizeof kn2, "k_gemm2_q8_0_mg%u", MG);
+        snprintf(kn2, sizeof kn2, "k_gemm2_%s_mg%u", f.name, MG);
         void* p2[] = {&a2};
         return launch(c, kn2, dim3(std::min(base * splits, cap)), dim3(256), 0, p2);
     }
     const uint32_t CT = ((n + 31) / 32 >= 2 * cu) ? 2 : 1;
     const uint32_t gx = (n + 16 * CT - 1) / (16 * CT);
     uint32_t ksw = 1;
-    while (ksw < 8 && (uint64_t)gx * nchunks * ksw < 8ull * cu && ksw * 2 <= nxb) ksw *= 2;
-    GemmArgs a{w, aops, etab, y, m_rows, n, k, nxb, ksw, (uint64_t)nxb * 34};
+    while (ksw < 8 && (uint64_t)gx * nchunks * ksw < 8ull * cu && ksw * 2 <= nrec) ksw *= 2;
+    GemmArgs a{w, aops, etab, y, m_rows, n, k, nrec, ksw, row_bytes};
     char kn[48];
     snprintf(kn, sizeof kn, "k_gemm_q8_0_mg%u_ct%u", MG, CT);
     void* params[] = {&a};
     return launch(c, kn, dim3(gx, nchunks), dim3(64 * ksw), 0, params);
+}
+
+constexpr GemmFmt kGemmQ8_0{"q8_0", 32, 34, 1, 8, 4, false, rt_gemv_q8_0_f32in_f32out};
+constexpr GemmFmt kGemmQ4_0{"q4_0", 32, 18, 1, 8, 4, false, rt_gemv_q4_0_f32in_f32out};
+constexpr GemmFmt kGemmQ4K{"q4k", 256, 144, 8, 1, 1, true, rt_gemv_q4k_f32in_f32out};
+
+int rt_gemm_q8_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ8_0, w, x, y, m_rows, n, k);
+}
+int rt_gemm_q4_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ4_0, w, x, y, m_rows, n, k);
+}
+int rt_gemm_q4k_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                    uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ4K, w, x, y, m_rows, n, k);
 }
 
 // ───────────────────────────── dequant ─────────────────────────────

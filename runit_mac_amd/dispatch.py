@@ -112,7 +112,8 @@ _SIGS = {
         "rt_dequant_q8_0_f32", "rt_dequant_q4_0_f32", "rt_dequant_q4k_f32",
         "rt_dequant_q6k_f32", "rt_dequant_q4k_f16", "rt_dequant_q5_0_f32", "rt_dequant_q5k_f32",
         "rt_dequant_q4_0g_f32", "rt_dequant_q4kg_f32", "rt_dequant_q5kg_f32", "rt_dequant_q6kg_f32", "rt_argmax_f32", "rt_argmax_f16")},
-    "rt_gemm_q8_0_f32": [_P, _P, _P, _P, _U32, _U32, _U32],
+    **{n: [_P, _P, _P, _P, _U32, _U32, _U32] for n in (
+        "rt_gemm_q8_0_f32", "rt_gemm_q4_0_f32", "rt_gemm_q4k_f32")},
     "rt_rms_norm_f32_f32_f32g": [_P, _P, _P, _P, _F, _U32, _U32],
     "rt_fused_rope_qk_f32": [_P, _P, _P, _U32, _U32, _U32, _U32, _F],
     "rt_kv_copy_to_cache_f32": [_P, _P, _P, _U32, _U32, _U32, _U32],
@@ -490,6 +491,16 @@ def dequant_f32(ctx, fmt: str, input, output, n_blocks):
 def gemm_q8_0_f32(ctx, weight, x, y, m_rows, n, k):
     """Batched Y[M,N] = X[M,K]·W[N,K]ᵀ (new; replaces gemm_f16 in verify_draft)."""
     _call(ctx, "rt_gemm_q8_0_f32", _ptr(weight), _ptr(x), _ptr(y), m_rows, n, k)
+
+
+def gemm_q4_0_f32(ctx, weight, x, y, m_rows, n, k):
+    """Batched GEMM on reference-layout Q4_0 weights (new)."""
+    _call(ctx, "rt_gemm_q4_0_f32", _ptr(weight), _ptr(x), _ptr(y), m_rows, n, k)
+
+
+def gemm_q4k_f32(ctx, weight, x, y, m_rows, n, k):
+    """Batched GEMM on reference-layout Q4_K weights (new)."""
+    _call(ctx, "rt_gemm_q4k_f32", _ptr(weight), _ptr(x), _ptr(y), m_rows, n, k)
 
 
 def argmax_f32(ctx, input, result, n):

@@ -146,6 +146,40 @@ def test_gemm_q8_0(ctx, m, n, k):
         check_close(y2.read(np.float32, 2 * n), yref[:2].ravel(), sabs[:2].ravel(), "gemm m=2")
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q4k"])
+@pytest.mark.parametrize("m", [2, 4, 7, 16, 32, 37])
+@pytest.mark.parametrize("n,k", [(512, 1024), (130, 3584), (70, 8192)])
+def test_gemm_4bit(ctx, fmt, m, n, k):
+    """Batched GEMM on reference-layout Q4_0 / Q4_K weights: every output row
+    within the GEMV bound of the per-row oracle."""
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=m + n + 5)
+    x = np.random.default_rng(m + 1).standard_normal((m, k)).astype(np.float32)
+    y = ctx.new_buffer(4 * m * n)
+    getattr(d, f"gemm_{fmt}_f32")(ctx, wbuf, ctx.buffer_from(x), y, m, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm {fmt} m={m}")
+
+
+@pytest.mark.parametrize("m", [3, 9])
+def test_gemm_q4_0_unaligned_rows_fall_back_to_gemvs(ctx, m):
+    # k = 96: 3 blocks per row (54 bytes) — not a whole stage, so one GEMV per row
+    n, k = 77, 96
+    wbuf, raw = device_weights(ctx, "q4_0", n, k, seed=m)
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    y = ctx.new_buffer(4 * m * n)
+    d.gemm_q4_0_f32(ctx, wbuf, ctx.buffer_from(x), y, m, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv("q4_0", raw, x, n, k)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm fallback m={m}")
+
+
+def test_gemm_q4k_rejects_k_not_multiple_of_256(ctx):
+    w = ctx.new_buffer(4096)
+    with pytest.raises(d.Dispatch):
+        d.gemm_q4k_f32(ctx, w, ctx.new_buffer(4096), ctx.new_buffer(4096), 2, 4, 128)
+
+
 def test_gemm_q8_0_direct_kernel_matches_staged(ctx):
     """The unstaged kernel (any K) on a shape the staged kernel also takes."""
     import os
