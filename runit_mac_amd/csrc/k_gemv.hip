@@ -39,6 +39,7 @@ struct GemvArgs {
     // xml = (m, l)[H][nsp]; staging merges them as the attention kernel does
     const float* xml;
     uint32_t xnsp, xhd;
+    uint32_t ls_rs;      // LDS-streamed body: LDS bytes between two rows of a slot
 };
 
 // Tiles one workgroup may own in a K-split launch (the host keeps the grid's
@@ -383,16 +384,18 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     const uint32_t spw = (nsteps + ksw - 1) / ksw;  // steps per wave per tile
     const uint32_t my_tiles = wg < ntiles ? (ntiles - wg + nwg - 1) / nwg : 0;
     const uint32_t nitems = my_tiles * spw;
+    // first virtual row of the wave's rows in the workgroup's tile number t
+    auto rows_of = [&](uint32_t t) -> uint32_t { return (wg + t * nwg) * vrows_per_wg + wgrp * 4 * RQ; };
 
     typename F::Raw buf[PF][RQ];  // PF items in flight per wave
     auto issue = [&](uint32_t item, typename F::Raw (&dst)[RQ]) {
-        const uint32_t tile = wg + (item / spw) * nwg;
+        const uint32_t vb = rows_of(item / spw);
         const uint32_t step = wk + ksw * (item % spw);
         uint32_t u = slot + 16 * step;
         if (u >= units) u = 0;  // clamped: loads stay in bounds, result is discarded
 #pragma unroll
         for (int rq = 0; rq < RQ; ++rq) {
-            uint32_t vr = tile * vrows_per_wg + wgrp * 4 * RQ + 4 * rq + q;
+            uint32_t vr = vb + 4 * rq + q;
             if (vr >= a.nvrows) vr = a.nvrows - 1;
             uint32_t mat, r;
             vrow_map<EPI>(a, vr, mat, r);
@@ -407,10 +410,10 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     // would make the compiler's wait for the x loads a wait for all loads)
     auto load_tile_aux = [&](uint32_t item) {
         if (has_aux<EPI>()) {
-            const uint32_t tile = wg + (item / spw) * nwg;
+            const uint32_t vb = rows_of(item / spw);
 #pragma unroll
             for (int rq = 0; rq < RQ; ++rq) {
-                const uint32_t vr = tile * vrows_per_wg + wgrp * 4 * RQ + 4 * rq + q;
+                const uint32_t vr = vb + 4 * rq + q;
                 aux[rq] = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
             }
         }
@@ -494,8 +497,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                 }
                 if (item + PF < nitems) issue(item + PF, buf[half]);
                 if (item % spw == spw - 1) {
-                    const uint32_t tile = wg + (item / spw) * nwg;
-                    const uint32_t vbase = tile * vrows_per_wg + wgrp * 4 * RQ;
+                    const uint32_t vbase = rows_of(item / spw);
                     float rsum[RQ];
 #pragma unroll
                     for (int rq = 0; rq < RQ; ++rq) {

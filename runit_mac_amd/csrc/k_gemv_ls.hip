@@ -1,0 +1,275 @@
+// k_gemv_ls.hip — LDS-streamed M=1 GEMV body (matrix-core dots) for gfx950.
+//
+// What limits an M=1 GEMV on MI355X is how the weight bytes are requested.
+// Two properties set the achieved HBM rate:
+//   * coalescing: a wave load of 64 lanes × 16 consecutive bytes (1 KB) is
+//     served as 8 whole 128-byte lines; lanes that each walk their own 36..212
+//     byte block touch ~20 lines per load instruction and stream ~15% slower;
+//   * a compact front: all waves reading a window of the stream that moves
+//     through memory together run ~10% faster than waves that each own one
+//     long contiguous span (≥ 16 KB per wave).
+// This body therefore:
+//   1. splits the launch into items of one row quad (4 rows of one K chunk);
+//      item j of wave w in workgroup g is quad g + nwg·(w + nwaves·j), so the
+//      waves of the whole grid move through the quads together, and every
+//      workgroup gets the same number of items to within one;
+//   2. loads each row of an item with coalesced dwordx4 loads (lane l reads
+//      bytes 16l.. of each KB) into registers, two items ahead, and writes
+//      the item into a wave-private LDS slot just before computing it,
+//      keeping the row's address modulo 16 so the block formats' alignment
+//      assumptions hold (no workgroup barrier after the activation staging;
+//      the compiler places every wait, which it cannot do for global→LDS
+//      loads whose target it cannot tell apart from the slot being read);
+//   3. computes the row-quad dots with the formats' matrix-core unit code
+//      (F::load on the LDS copy, F::mdot against the activation records) and
+//      collects the results in LDS, stored after the last item.
+// Residual/bias operands are loaded once at the start (≤ 64 items per wave).
+// A K split (S > 1 chunks) writes partial sums; the last chunk to arrive at a
+// quad adds them in chunk order and runs the epilogue.
+
+constexpr uint32_t kLsGroup = 16;     // items per result store instruction
+constexpr uint32_t kLsMaxGroups = 4;  // ≤ 64 items per wave
+constexpr uint32_t kLsResBytes = kLsMaxGroups * kLsGroup * 4 * sizeof(float);  // per wave
+
+// Unit loader for a row in LDS: F::load_ls where a format has one (loaders
+// that round the address with integer arithmetic would lose the LDS address
+// space), else F::load.
+template <class F>
+RT_DEV auto ls_load(const uint8_t* row, uint32_t u, typename F::Raw& r, int) -> decltype(F::load_ls(row, u, r)) {
+    return F::load_ls(row, u, r);
+}
+template <class F>
+RT_DEV void ls_load(const uint8_t* row, uint32_t u, typename F::Raw& r, long) { F::load(row, u, r); }
+
+template <class F, int EPI, typename XT, int NI>
+RT_DEV void gemv_ls_body(const GemvArgs& a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nwaves = wg_threads() >> 6;
+    const uint32_t q = lane & 3, slot = lane >> 2;
+    const uint32_t lq = q < 3 ? q : 2;  // the A row of lane q = 3 is a don't-care
+    const uint32_t S = a.ksplit;
+    const uint32_t ks = blockIdx.x % S, wg = blockIdx.x / S, nwg = gridDim.x / S;
+    const uint32_t cu0 = ks * a.kc_units;  // first unit of this workgroup's K chunk
+    const uint32_t units = min(a.K / F::UNIT_EL - cu0, a.kc_units);
+    const uint32_t cbyte0 = cu0 * F::UNIT_EL / F::BLK_EL * F::BLK_BYTES;  // chunk offset in a row
+    const uint32_t cbytes = units * F::UNIT_EL / F::BLK_EL * F::BLK_BYTES;
+    const uint32_t nxb = units * F::UNIT_EL / 32, xb0 = cu0 * F::UNIT_EL / 32;
+    const uint32_t xcap = a.kc_units * F::UNIT_EL / 32 * XREC_BYTES;
+    XRec* xs = (XRec*)smem;
+    float* res = (float*)(smem + xcap) + wave * (kLsMaxGroups * kLsGroup * 4);
+    const uint32_t RS = a.ls_rs;  // LDS bytes between two rows of the slot
+    uint8_t* wslot = smem + xcap + nwaves * kLsResBytes + wave * (4 * RS);
+    const uint32_t nq = (a.nvrows + 3) / 4;
+    const uint32_t first = wg + nwg * wave, stride = nwg * nwaves;
+    const uint32_t nitems = first < nq ? (nq - first + stride - 1) / stride : 0;
+    auto quad_of = [&](uint32_t j) { return first + stride * j; };
+
+    // chunk start of virtual row vr (clamped into the launch)
+    auto row_src = [&](uint32_t vr) -> const uint8_t* {
+        if (vr >= a.nvrows) vr = a.nvrows - 1;
+        uint32_t mat, r;
+        vrow_map<EPI>(a, vr, mat, r);
+        return mat_w(a, mat) + (size_t)r * a.row_bytes + cbyte0;
+    };
+    // coalesced loads of item j's four row chunks: NI dwordx4 per lane and
+    // row from the chunk's 16-byte floor (lanes past the chunk re-read its
+    // last 16 bytes).  Buffer loads over each matrix (from its 16-byte floor):
+    // an item past the wave's last is issued at an out-of-range offset, which
+    // returns zeros without a memory access, so every loop iteration issues
+    // the same loads and the compiler's waits stay exact.
+    __amdgpu_buffer_rsrc_t mrs[3];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+        const uint8_t* mb = mat_w(a, m);
+        const uint32_t lo = (uint32_t)((uintptr_t)mb & 15);
+        const uint32_t nrows = (EPI == EPI_QKV || EPI == EPI_QKV_BIAS) ? a.n[m]
+                               : (EPI == EPI_FFN ? a.nvrows / 2 : a.nvrows);
+        // (the record size is rounded up to 16 bytes: a dwordx4 that reaches
+        // past the record reads as zeros as a whole, and the last row's last
+        // piece may end up to 15 bytes past the matrix, inside the 16-byte
+        // granule that holds its last byte)
+        mrs[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(mb - lo), (short)0,
+                                                   (int)((nrows * (uint32_t)a.row_bytes + lo + 15) & ~15u),
+                                                   0x00020000);
+    }
+    typedef u32x4 Item[4][NI];
+    auto issue = [&](uint32_t j, Item& dst) {
+        // (branch-free: bit 31 of the offset marks an item past the last)
+        const uint32_t oob = (uint32_t)(j >= nitems) << 31;
+        const uint32_t quad = quad_of(j);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t vr = min(quad * 4 + r, a.nvrows - 1);
+            uint32_t mat, rr;
+            vrow_map<EPI>(a, vr, mat, rr);
+            const uint8_t* mb = mat_w(a, mat);
+            const uint32_t lo = (uint32_t)((uintptr_t)mb & 15);
+            const uint32_t so = rr * (uint32_t)a.row_bytes + cbyte0 + lo;  // chunk start in the buffer
+            const uint32_t base = so & ~15u, last = ((so & 15) + cbytes - 1) & ~15u;
+            const __amdgpu_buffer_rsrc_t rs = pick3(mrs[0], mrs[1], mrs[2], mat);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t off = (base + min((uint32_t)(i * 64 + lane) * 16, last)) | oob;
+                dst[r][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0);
+            }
+        }
+    };
+    // the item's bytes into the wave's LDS slot (row r at r·RS, keeping the
+    // chunk's address modulo 16)
+    auto commit = [&](const Item& src) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < NI; ++i) *(u32x4*)(wslot + r * RS + (i * 64 + lane) * 16) = src[r][i];
+    };
+
+    // epilogue operands of the lanes' result slots (lane l of group g: item
+    // 16g + l/4, row l%4), loaded before any weight
+    float aux[kLsMaxGroups];
+#pragma unroll
+    for (uint32_t g = 0; g < kLsMaxGroups; ++g) {
+        aux[g] = 0.0f;
+        if (has_aux<EPI>()) {
+            const uint32_t jj = g * kLsGroup + slot;
+            const uint32_t vr = (jj < nitems ? quad_of(jj) : 0) * 4 + q;
+            aux[g] = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
+        }
+    }
+    auto pick_aux = [&](uint32_t g) {
+        return g == 0 ? aux[0] : (g == 1 ? aux[1] : (g == 2 ? aux[2] : aux[3]));
+    };
+
+    // activation loads, then the first two items' weights, then the
+    // conversion (which waits for the activations only)
+    const bool one_pass = !a.x_rec && stage_one_pass(nxb);
+    XPre xp;
+    if (one_pass)
+        stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32,
+                         a.gamma ? a.gamma + (size_t)xb0 * 32 : nullptr, nxb, xp);
+    Item buf[2];
+    issue(0, buf[0]);
+    issue(1, buf[1]);
+    if (one_pass)
+        stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
+    else
+        copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
+    lds_barrier();
+
+    // results of group g (items 16g .. 16g + n - 1): one store per lane
+    auto flush = [&](uint32_t g, uint32_t n) {
+        const uint32_t jj = g * kLsGroup + slot;
+        const float v = res[g * 64 + lane];
+        const uint32_t vr = (jj < nitems ? quad_of(jj) : 0) * 4 + q;
+        const bool ok = slot < n && vr < a.nvrows;
+        if (S > 1) {
+            if (ok) dev_store(a.part + (size_t)ks * a.nvrows + vr, v);
+        } else if (EPI == EPI_FFN) {
+            // quad rows (gate r, up r, gate r+1, up r+1)
+            const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
+            if (ok && (q & 1) == 0 && vr + 1 < a.nvrows)
+                ((float*)a.out[0])[vr >> 1] = silu_ref(v) * up;
+        } else {
+            if (ok) store_row_pre<EPI>(a, vr, v, pick_aux(g));
+        }
+    };
+
+    const uint32_t nsteps = (units + 15) / 16;
+    // two items in flight in registers; the loop is unrolled by two so the
+    // buffers are addressed statically, and both halves always run (a half
+    // past the wave's last item computes on zeros and records nothing), so
+    // that every path through the loop issues the same memory operations and
+    // the compiler's waits stay exact.  Results wait in LDS until the end.
+    for (uint32_t j0 = 0; j0 < nitems; j0 += 2) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t j = j0 + h;
+#ifndef RT_PROBE_LS_NOCOMMIT
+            commit(buf[h]);
+#else
+            if (buf[h][0][0].x == 0x9E3779B9u) commit(buf[h]);  // probe: commit skipped
+#endif
+            issue(j + 2, buf[h]);
+            // this lane's row in the slot
+            const uint8_t* rowl = wslot + q * RS + ((uintptr_t)row_src(quad_of(j) * 4 + q) & 15);
+            float acc = 0.0f;
+            for (uint32_t st = 0; st < nsteps; ++st) {
+                const uint32_t u = slot + 16 * st;
+                const bool valid = u < units;
+                const uint32_t uc = valid ? u : 0;
+#ifndef RT_PROBE_LS_NODOT
+                typename F::Raw raw;
+                ls_load<F>(rowl, uc, raw, 0);
+                const float v = F::mdot(raw, xs, uc, lq);
+#else
+                const float v = __builtin_bit_cast(float, *(const uint32_t*)(rowl + 4 * uc));  // probe
+#endif
+                acc += valid ? v : 0.0f;
+            }
+            // sum over the 16 slots of the row (lane bits 2..5)
+            acc += swz_xor_f<4>(acc);
+            acc += swz_xor_f<8>(acc);
+            acc += swz_xor_f<16>(acc);
+            acc += __shfl_xor(acc, 32, 64);
+            if (slot == 0 && j < nitems) res[j * 4 + q] = acc;
+        }
+    }
+#pragma unroll
+    for (uint32_t g = 0; g < kLsMaxGroups; ++g) {
+        if (g * kLsGroup >= nitems) break;  // uniform
+        flush(g, min(nitems - g * kLsGroup, kLsGroup));
+    }
+
+    if (S > 1) {
+        // K split: count this chunk in at each of the wave's quads (lane of
+        // row 0 of the item), then the last chunk to arrive sums the chunks
+        // in order and runs the epilogue
+        dev_stores_done();
+#pragma unroll
+        for (uint32_t g = 0; g < kLsMaxGroups; ++g) {
+            if (g * kLsGroup >= nitems) break;  // uniform
+            const uint32_t jj = g * kLsGroup + slot;
+            const bool have = jj < nitems;
+            const uint32_t quad = have ? quad_of(jj) : 0;
+            uint32_t last = 0;
+            if (have && q == 0) last = arrive(a.counters + (size_t)quad * a.cstride) == S - 1;
+            last = __shfl(last, lane & ~3u, 64);
+            if (!last) continue;
+            const uint32_t vr = quad * 4 + q;
+            float v = 0.0f;
+            for (uint32_t c = 0; c < S; ++c)
+                v += dev_load(a.part + (size_t)c * a.nvrows + (vr < a.nvrows ? vr : a.nvrows - 1));
+            if (EPI == EPI_FFN) {
+                const float up = __shfl_xor(v, 1, 64);
+                if ((q & 1) == 0 && vr + 1 < a.nvrows) ((float*)a.out[0])[vr >> 1] = silu_ref(v) * up;
+            } else if (vr < a.nvrows) {
+                store_row_pre<EPI>(a, vr, v, pick_aux(g));
+            }
+            if (q == 0) dev_store(a.counters + (size_t)quad * a.cstride, 0u);  // ready for the next call
+        }
+    }
+}
+
+// Kernels: one per (format, epilogue, activation type, loads per row NI).
+// Built for 256-thread workgroups (the host launches 128 or 256 threads).
+#define RT_GEMV_LS1(NAME, FMT, EPI, XT, NI) \
+    extern "C" __global__ void __launch_bounds__(256) NAME##_ls##NI(GemvArgs a) { gemv_ls_body<FMT, EPI, XT, NI>(a); }
+#define RT_GEMV_LS(NAME, FMT, EPI, XT) \
+    RT_GEMV_LS1(NAME, FMT, EPI, XT, 1) RT_GEMV_LS1(NAME, FMT, EPI, XT, 2) RT_GEMV_LS1(NAME, FMT, EPI, XT, 3)
+
+RT_GEMV_LS(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float)
+RT_GEMV_LS(k_gemv_q8_0_f32_f16, FmtQ8_0, EPI_F16, float)
+RT_GEMV_LS(k_qkv_bias_q8_0, FmtQ8_0, EPI_QKV_BIAS, float)
+RT_GEMV_LS(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float)
+RT_GEMV_LS(k_gemv_q4_0_f32_f32, FmtQ4_0, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q4_0_f32_f32add, FmtQ4_0, EPI_F32_ADD, float)
+RT_GEMV_LS(k_qkv_bias_q4_0, FmtQ4_0, EPI_QKV_BIAS, float)
+RT_GEMV_LS(k_ffn_q4_0, FmtQ4_0, EPI_FFN, float)
+RT_GEMV_LS(k_gemv_q4k_f32_f32, FmtQ4K, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q4k_f32_f32add, FmtQ4K, EPI_F32_ADD, float)
+RT_GEMV_LS(k_ffn_q4k, FmtQ4K, EPI_FFN, float)
+RT_GEMV_LS(k_gemv_q6k_f32_f32, FmtQ6KB, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q6k_f32_f32add, FmtQ6KB, EPI_F32_ADD, float)
+RT_GEMV_LS(k_gemv_q6kg_f32_f32, FmtQ6KGB, EPI_F32, float)

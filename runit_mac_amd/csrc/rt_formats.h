@@ -517,6 +517,13 @@ struct FmtQ6KBT {
         r.sh = (uint32_t)(p & 3);
         load_dwords<53>((const uint8_t*)(p & ~(uintptr_t)3), r.w);
     }
+    // the same from a row copied into LDS (offset arithmetic on the pointer
+    // keeps its address space, so the reads compile to LDS reads)
+    RT_DEV static void load_ls(const uint8_t* row, uint32_t u, Raw& r) {
+        const uint8_t* p = row + (size_t)u * 210;
+        r.sh = (uint32_t)((uintptr_t)p & 3);
+        load_dwords<53>(p - r.sh, r.w);
+    }
     // bytes [off, off+4) of the block, off a multiple of 4 below 208 (a
     // constant once the callers' loops are unrolled)
     RT_DEV static uint32_t get(const Raw& r, uint32_t off) {

@@ -16,6 +16,7 @@
 #include <cstring>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/runit_hip.h"
 
@@ -44,6 +45,7 @@ struct GemvArgs {
     uint32_t cstride;
     const float* xml;
     uint32_t xnsp, xhd;
+    uint32_t ls_rs;
 };
 
 constexpr uint32_t XREC_BYTES = 112;
@@ -131,6 +133,21 @@ const char* const kKernelNames[] = {
     "k_gemm2_q4k_mg1", "k_gemm2_q4k_mg2", "k_gemm2_q4k_mg4", "k_gemm2_q4k_mg8",
 };
 
+// Kernels of the LDS-streamed GEMV body: <base>_ls<NI>, NI = 1..3 global→LDS
+// loads of 1 KB per row chunk.
+const char* const kLsBases[] = {
+    "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_gemv_q8_0_f32_f16", "k_qkv_bias_q8_0",
+    "k_ffn_q8_0", "k_gemv_q4_0_f32_f32", "k_gemv_q4_0_f32_f32add", "k_qkv_bias_q4_0",
+    "k_ffn_q4_0", "k_gemv_q4k_f32_f32", "k_gemv_q4k_f32_f32add", "k_ffn_q4k",
+    "k_gemv_q6k_f32_f32", "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32",
+};
+constexpr uint32_t kLsMaxNI = 3;
+constexpr int kLsDecline = -1;
+constexpr uint32_t kLsThreads = 256;
+constexpr uint32_t kLsMaxItems = 64;    // items per wave (kernel: 4 groups of 16)
+constexpr uint32_t kLsResBytes = 1024;  // per-wave result buffer (64 items × 4 rows)
+constexpr uint32_t kLsRowPad = 48;      // LDS row stride = NI KB + pad (bank spread)
+
 struct Fmt {
     uint32_t blk_el, blk_bytes, unit_el;  // unit_el: elements per lane unit (v_dot4 path)
     uint32_t unroll;  // UNR template constant of the format's kernels
@@ -193,6 +210,9 @@ struct rt_ctx {
     void* attn_out = nullptr;  // attention output between the two launches of
     size_t attn_out_bytes = 0;  // the unmerged attention + o_proj sequence
     uint32_t prepass_k = 8192;  // RUNIT_PREPASS_K: K from which x is converted once
+    bool ls_enabled = true;      // RUNIT_GEMV_LS=0: the per-lane-load matrix-core body instead
+    uint32_t ls_pad = kLsRowPad; // RUNIT_GEMV_LS_PAD (sweeps only)
+    uint32_t ls_min_items = 8;   // RUNIT_GEMV_LS_MIN: quads per wave from which the LDS body runs
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
     void* aux = nullptr;
@@ -326,6 +346,91 @@ int ensure_part(rt_ctx* c, size_t need, const char* who) {
     return ensure_buf(c, c->part, c->part_bytes, need, who);
 }
 
+bool has_ls_kernel(const rt_ctx* c, const char* kname) {
+    return c->fns.count(std::string(kname) + "_ls1") != 0;
+}
+
+// LDS-streamed matrix-core launch (k_gemv_ls.hip).  Items are row quads of
+// one K chunk; a chunk's rows are read with NI ≤ 3 coalesced 1 KB loads
+// each, so rows longer than 3 KB (or K beyond one staging pass) are split
+// into S chunks whose partial sums meet in the workspace.  Returns 1 when the
+// shape does not suit the body (kLsDecline: the caller takes the other bodies).
+int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
+    const uint32_t ue = f.mq_units();
+    const uint32_t units_total = a.K / ue;
+    const uint32_t gu = f.blk_el > ue ? f.blk_el / ue : 1;  // units per whole block
+    const uint32_t ubytes_num = ue * f.blk_bytes;           // unit bytes × blk_el
+    auto chunk_bytes = [&](uint32_t u) { return (uint64_t)u * ubytes_num / f.blk_el; };
+    const uint32_t max_recs = 4 * kLsThreads / 8;  // one staging pass
+    uint32_t kc = units_total, S = 1, NI = 0;
+    const uint64_t rb = chunk_bytes(units_total);
+    if (rb + 15 <= kLsMaxNI * 1024 && (a.x_rec || a.gamma || a.K / 32 <= max_recs)) {
+        NI = (uint32_t)((rb + 15 + 1023) / 1024);
+    } else {
+        if (a.x_rec || a.gamma || !c->ksplit_enabled) return kLsDecline;
+        // chunks of ≤ 2 KB (NI = 2), a whole number of blocks, ≤ one staging pass
+        uint32_t cap = (uint32_t)((2048 - 15) * (uint64_t)f.blk_el / ubytes_num);
+        cap = std::min<uint32_t>(cap, max_recs * 32 / ue);
+        cap -= cap % gu;
+        if (cap == 0) return kLsDecline;
+        S = (units_total + cap - 1) / cap;
+        kc = (units_total + S - 1) / S;
+        kc = (kc + gu - 1) / gu * gu;
+        S = (units_total + kc - 1) / kc;
+        NI = (uint32_t)((chunk_bytes(kc) + 15 + 1023) / 1024);
+        if (NI > kLsMaxNI) return kLsDecline;
+    }
+    a.ksplit = S;
+    a.kc_units = kc;
+    a.ls_rs = NI * 1024 + c->ls_pad;
+    const uint32_t nw = kLsThreads / 64;
+    const size_t lds = (size_t)kc * ue / 32 * XREC_BYTES + nw * kLsResBytes + (size_t)nw * 4 * a.ls_rs;
+    if (lds > c->max_lds) return kLsDecline;
+    const uint32_t nq = (a.nvrows + 3) / 4;
+    // The body's per-item dot code runs at two waves per SIMD; it pays off
+    // where each wave has many items (vocabulary-sized N), while
+    // shorter launches run faster on the matrix-core body's 16 waves per CU.
+    if (nq < (uint32_t)c->cu_count * 8 * c->ls_min_items) return kLsDecline;
+    // buffer loads address each matrix with 32-bit offsets (out-of-range
+    // offsets ≥ 2^31 mark the loads of items past a wave's last)
+    if ((uint64_t)a.nvrows * a.row_bytes + 16 >= (1ull << 31)) return kLsDecline;
+    char name[96];
+    snprintf(name, sizeof name, "%s_ls%u", kname, NI);
+    const uint32_t occ = occupancy(c, name, kLsThreads, lds);
+    // One round of resident workgroups, k per CU (k ≤ occupancy), with the k
+    // whose busiest wave is closest to the average: a wave's last items run
+    // with few loads in flight on its CU, so a grid that leaves a fraction of
+    // the waves one extra item pays most of an item's time for it.
+    uint32_t nwg = 0;
+    double best = -1.0;
+    for (uint32_t k = 1; k <= occ; ++k) {
+        const uint32_t g = std::max<uint32_t>(1, (uint32_t)c->cu_count * k / S);
+        const uint64_t waves = (uint64_t)g * nw;
+        const uint64_t per = (nq + waves - 1) / waves;
+        const double eff = (double)nq / (double)(waves * per);
+        if (eff > best + 0.02) {
+            best = eff;
+            nwg = g;
+        }
+    }
+    if (c->grid_per_cu) nwg = std::max<uint32_t>(1, (uint32_t)c->cu_count * c->grid_per_cu / S);
+    nwg = std::min<uint32_t>(nwg, (nq + nw - 1) / nw);
+    nwg = std::max<uint32_t>(nwg, (nq + nw * kLsMaxItems - 1) / (nw * kLsMaxItems));
+    if (S > 1) {
+        if (nq > kAttnCounters)
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: %u row quads exceed %u",
+                        kname, nq, kAttnCounters);
+        const int st = ensure_part(c, (size_t)S * a.nvrows * sizeof(float), kname);
+        if (st != RT_OK) return st;
+        a.part = (float*)c->part;
+        a.counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
+        a.cstride = 32;
+        while (a.cstride > 1 && (size_t)nq * a.cstride > kAttnCounters) a.cstride >>= 1;
+    }
+    void* params[] = {&a};
+    return launch(c, name, dim3(nwg * S), dim3(kLsThreads), lds, params);
+}
+
 int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x_f16,
                 bool paired = false) {
     const bool single = fmt.single && (a.K % fmt.unit_el) != 0;
@@ -343,6 +448,10 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
                     "kernel dispatch error: %s: input must be %d-byte aligned", kname,
                     x_f16 ? 8 : 16);
     a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
+    if (c->ls_enabled && !single && !x_f16 && !a.xnsp && has_ls_kernel(c, kname)) {
+        const int st = gemv_launch_ls(c, kname, f, a);
+        if (st != kLsDecline) return st;
+    }
     const uint32_t nxb = a.K / 32;
     const bool mq_shape = !single;
     const uint32_t mq_el = f.mq_units();
@@ -578,6 +687,9 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_DIRECT")) c->gemm_direct = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_ATTN_SPLIT")) c->attn_split_override = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMV_LS_PAD")) c->ls_pad = (uint32_t)atoi(g) & ~15u;
     if (const char* g = getenv("RUNIT_GEMV_KSW")) {
         const int v = atoi(g);
         if (v == 1 || v == 2 || v == 4 || v == 8) c->ksw_override = (uint32_t)v;
@@ -591,7 +703,11 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
         return fail(nullptr, RT_ERR_LIBRARY_LOAD, "failed to load code object from '%s': %s",
                     path.c_str(), hipGetErrorString(e));
     }
-    for (const char* n : kKernelNames) {
+    std::vector<std::string> names(std::begin(kKernelNames), std::end(kKernelNames));
+    for (const char* b : kLsBases)
+        for (uint32_t ni = 1; ni <= kLsMaxNI; ++ni) names.push_back(std::string(b) + "_ls" + std::to_string(ni));
+    for (const std::string& ns : names) {
+        const char* n = ns.c_str();
         hipFunction_t f = nullptr;
         e = hipModuleGetFunction(&f, c->module, n);
         if (e != hipSuccess || !f) {
