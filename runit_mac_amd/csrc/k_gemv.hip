@@ -40,6 +40,7 @@ struct GemvArgs {
     const float* xml;
     uint32_t xnsp, xhd;
     uint32_t ls_rs;      // LDS-streamed body: LDS bytes between two rows of a slot
+    uint32_t ls_res;     // LDS-streamed body: result slots per wave (items)
 };
 
 // Tiles one workgroup may own in a K-split launch (the host keeps the grid's

@@ -14,7 +14,7 @@
 //      waves of the whole grid move through the quads together, and every
 //      workgroup gets the same number of items to within one;
 //   2. loads each row of an item with coalesced dwordx4 loads (lane l reads
-//      bytes 16l.. of each KB) into registers, two items ahead, and writes
+//      bytes 16l.. of each KB) into registers, one item ahead, and writes
 //      the item into a wave-private LDS slot just before computing it,
 //      keeping the row's address modulo 16 so the block formats' alignment
 //      assumptions hold (no workgroup barrier after the activation staging;
@@ -29,7 +29,6 @@
 
 constexpr uint32_t kLsGroup = 16;     // items per result store instruction
 constexpr uint32_t kLsMaxGroups = 4;  // ≤ 64 items per wave
-constexpr uint32_t kLsResBytes = kLsMaxGroups * kLsGroup * 4 * sizeof(float);  // per wave
 
 // Unit loader for a row in LDS: F::load_ls where a format has one (loaders
 // that round the address with integer arithmetic would lose the LDS address
@@ -58,9 +57,10 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     const uint32_t nxb = units * F::UNIT_EL / 32, xb0 = cu0 * F::UNIT_EL / 32;
     const uint32_t xcap = a.kc_units * F::UNIT_EL / 32 * XREC_BYTES;
     XRec* xs = (XRec*)smem;
-    float* res = (float*)(smem + xcap) + wave * (kLsMaxGroups * kLsGroup * 4);
+    // per wave: a result buffer of a.ls_res items (a multiple of 16, ≤ 64)
+    float* res = (float*)(smem + xcap) + wave * (a.ls_res * 4);
     const uint32_t RS = a.ls_rs;  // LDS bytes between two rows of the slot
-    uint8_t* wslot = smem + xcap + nwaves * kLsResBytes + wave * (4 * RS);
+    uint8_t* wslot = smem + xcap + nwaves * a.ls_res * 16 + wave * (4 * RS);
     const uint32_t nq = (a.nvrows + 3) / 4;
     const uint32_t first = wg + nwg * wave, stride = nwg * nwaves;
     const uint32_t nitems = first < nq ? (nq - first + stride - 1) / stride : 0;
@@ -75,44 +75,21 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     };
     // coalesced loads of item j's four row chunks: NI dwordx4 per lane and
     // row from the chunk's 16-byte floor (lanes past the chunk re-read its
-    // last 16 bytes).  Buffer loads over each matrix (from its 16-byte floor):
-    // an item past the wave's last is issued at an out-of-range offset, which
-    // returns zeros without a memory access, so every loop iteration issues
-    // the same loads and the compiler's waits stay exact.
-    __amdgpu_buffer_rsrc_t mrs[3];
-#pragma unroll
-    for (int m = 0; m < 3; ++m) {
-        const uint8_t* mb = mat_w(a, m);
-        const uint32_t lo = (uint32_t)((uintptr_t)mb & 15);
-        const uint32_t nrows = (EPI == EPI_QKV || EPI == EPI_QKV_BIAS) ? a.n[m]
-                               : (EPI == EPI_FFN ? a.nvrows / 2 : a.nvrows);
-        // (the record size is rounded up to 16 bytes: a dwordx4 that reaches
-        // past the record reads as zeros as a whole, and the last row's last
-        // piece may end up to 15 bytes past the matrix, inside the 16-byte
-        // granule that holds its last byte)
-        mrs[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(mb - lo), (short)0,
-                                                   (int)((nrows * (uint32_t)a.row_bytes + lo + 15) & ~15u),
-                                                   0x00020000);
-    }
+    // last 16 bytes).  An item past the wave's last re-reads the wave's last
+    // item (cache hits), computed without branches so that every loop
+    // iteration issues the same loads and the compiler's waits stay exact.
     typedef u32x4 Item[4][NI];
     auto issue = [&](uint32_t j, Item& dst) {
-        // (branch-free: bit 31 of the offset marks an item past the last)
-        const uint32_t oob = (uint32_t)(j >= nitems) << 31;
-        const uint32_t quad = quad_of(j);
+        const uint32_t quad = quad_of(min(j, nitems - 1));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t vr = min(quad * 4 + r, a.nvrows - 1);
-            uint32_t mat, rr;
-            vrow_map<EPI>(a, vr, mat, rr);
-            const uint8_t* mb = mat_w(a, mat);
-            const uint32_t lo = (uint32_t)((uintptr_t)mb & 15);
-            const uint32_t so = rr * (uint32_t)a.row_bytes + cbyte0 + lo;  // chunk start in the buffer
-            const uint32_t base = so & ~15u, last = ((so & 15) + cbytes - 1) & ~15u;
-            const __amdgpu_buffer_rsrc_t rs = pick3(mrs[0], mrs[1], mrs[2], mat);
+            const uint8_t* src = row_src(quad * 4 + r);
+            const uint8_t* base = src - ((uintptr_t)src & 15);
+            const uint32_t last = (uint32_t)(((uintptr_t)src & 15) + cbytes - 1) & ~15u;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const uint32_t off = (base + min((uint32_t)(i * 64 + lane) * 16, last)) | oob;
-                dst[r][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0);
+                const uint32_t off = min((uint32_t)(i * 64 + lane) * 16, last);
+                dst[r][i] = *(const u32x4*)(base + off);
             }
         }
     };
@@ -145,16 +122,19 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     // conversion (which waits for the activations only)
     const bool one_pass = !a.x_rec && stage_one_pass(nxb);
     XPre xp;
+#ifndef RT_PROBE_NO_STAGE
     if (one_pass)
         stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32,
                          a.gamma ? a.gamma + (size_t)xb0 * 32 : nullptr, nxb, xp);
-    Item buf[2];
-    issue(0, buf[0]);
-    issue(1, buf[1]);
+#endif
+    Item buf;
+    issue(0, buf);
+#ifndef RT_PROBE_NO_STAGE
     if (one_pass)
         stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
     else
         copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
+#endif
     lds_barrier();
 
     // results of group g (items 16g .. 16g + n - 1): one store per lane
@@ -176,44 +156,39 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     };
 
     const uint32_t nsteps = (units + 15) / 16;
-    // two items in flight in registers; the loop is unrolled by two so the
-    // buffers are addressed statically, and both halves always run (a half
-    // past the wave's last item computes on zeros and records nothing), so
-    // that every path through the loop issues the same memory operations and
-    // the compiler's waits stay exact.  Results wait in LDS until the end.
-    for (uint32_t j0 = 0; j0 < nitems; j0 += 2) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t j = j0 + h;
+    // One item in flight: item j is written to the slot, item j+1's loads
+    // are issued, item j is computed.  (Two items in flight per wave stream
+    // slower: the extra outstanding requests only queue.)  Results wait in
+    // LDS until the end.
+    for (uint32_t j = 0; j < nitems; ++j) {
 #ifndef RT_PROBE_LS_NOCOMMIT
-            commit(buf[h]);
+        commit(buf);
 #else
-            if (buf[h][0][0].x == 0x9E3779B9u) commit(buf[h]);  // probe: commit skipped
+        if (buf[0][0].x == 0x9E3779B9u) commit(buf);  // probe: commit skipped
 #endif
-            issue(j + 2, buf[h]);
-            // this lane's row in the slot
-            const uint8_t* rowl = wslot + q * RS + ((uintptr_t)row_src(quad_of(j) * 4 + q) & 15);
-            float acc = 0.0f;
-            for (uint32_t st = 0; st < nsteps; ++st) {
-                const uint32_t u = slot + 16 * st;
-                const bool valid = u < units;
-                const uint32_t uc = valid ? u : 0;
+        issue(j + 1, buf);
+        // this lane's row in the slot
+        const uint8_t* rowl = wslot + q * RS + ((uintptr_t)row_src(quad_of(j) * 4 + q) & 15);
+        float acc = 0.0f;
+        for (uint32_t st = 0; st < nsteps; ++st) {
+            const uint32_t u = slot + 16 * st;
+            const bool valid = u < units;
+            const uint32_t uc = valid ? u : 0;
 #ifndef RT_PROBE_LS_NODOT
-                typename F::Raw raw;
-                ls_load<F>(rowl, uc, raw, 0);
-                const float v = F::mdot(raw, xs, uc, lq);
+            typename F::Raw raw;
+            ls_load<F>(rowl, uc, raw, 0);
+            const float v = F::mdot(raw, xs, uc, lq);
 #else
-                const float v = __builtin_bit_cast(float, *(const uint32_t*)(rowl + 4 * uc));  // probe
+            const float v = __builtin_bit_cast(float, *(const uint32_t*)(rowl + 4 * uc));  // probe
 #endif
-                acc += valid ? v : 0.0f;
-            }
-            // sum over the 16 slots of the row (lane bits 2..5)
-            acc += swz_xor_f<4>(acc);
-            acc += swz_xor_f<8>(acc);
-            acc += swz_xor_f<16>(acc);
-            acc += __shfl_xor(acc, 32, 64);
-            if (slot == 0 && j < nitems) res[j * 4 + q] = acc;
+            acc += valid ? v : 0.0f;
         }
+        // sum over the 16 slots of the row (lane bits 2..5)
+        acc += swz_xor_f<4>(acc);
+        acc += swz_xor_f<8>(acc);
+        acc += swz_xor_f<16>(acc);
+        acc += __shfl_xor(acc, 32, 64);
+        if (slot == 0) res[j * 4 + q] = acc;
     }
 #pragma unroll
     for (uint32_t g = 0; g < kLsMaxGroups; ++g) {
@@ -252,11 +227,14 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
 }
 
 // Kernels: one per (format, epilogue, activation type, loads per row NI).
-// Built for 256-thread workgroups (the host launches 128 or 256 threads).
-#define RT_GEMV_LS1(NAME, FMT, EPI, XT, NI) \
-    extern "C" __global__ void __launch_bounds__(256) NAME##_ls##NI(GemvArgs a) { gemv_ls_body<FMT, EPI, XT, NI>(a); }
-#define RT_GEMV_LS(NAME, FMT, EPI, XT) \
-    RT_GEMV_LS1(NAME, FMT, EPI, XT, 1) RT_GEMV_LS1(NAME, FMT, EPI, XT, 2) RT_GEMV_LS1(NAME, FMT, EPI, XT, 3)
+// Built for up to 1024 threads (≤ 128 registers: 16 waves per CU share one
+// copy of the activation records), except Q6_K, whose whole-super-block
+// units need ~270 registers (256 threads).
+#define RT_GEMV_LS1(NAME, FMT, EPI, XT, NI, LB) \
+    extern "C" __global__ void __launch_bounds__(LB) NAME##_ls##NI(GemvArgs a) { gemv_ls_body<FMT, EPI, XT, NI>(a); }
+#define RT_GEMV_LSB(NAME, FMT, EPI, XT, LB) \
+    RT_GEMV_LS1(NAME, FMT, EPI, XT, 1, LB) RT_GEMV_LS1(NAME, FMT, EPI, XT, 2, LB) RT_GEMV_LS1(NAME, FMT, EPI, XT, 3, LB)
+#define RT_GEMV_LS(NAME, FMT, EPI, XT) RT_GEMV_LSB(NAME, FMT, EPI, XT, 1024)
 
 RT_GEMV_LS(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float)
 RT_GEMV_LS(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float)
@@ -270,6 +248,22 @@ RT_GEMV_LS(k_ffn_q4_0, FmtQ4_0, EPI_FFN, float)
 RT_GEMV_LS(k_gemv_q4k_f32_f32, FmtQ4K, EPI_F32, float)
 RT_GEMV_LS(k_gemv_q4k_f32_f32add, FmtQ4K, EPI_F32_ADD, float)
 RT_GEMV_LS(k_ffn_q4k, FmtQ4K, EPI_FFN, float)
-RT_GEMV_LS(k_gemv_q6k_f32_f32, FmtQ6KB, EPI_F32, float)
-RT_GEMV_LS(k_gemv_q6k_f32_f32add, FmtQ6KB, EPI_F32_ADD, float)
-RT_GEMV_LS(k_gemv_q6kg_f32_f32, FmtQ6KGB, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q5_0_f32_f32, FmtQ5_0, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q5_0_f32_f32add, FmtQ5_0, EPI_F32_ADD, float)
+RT_GEMV_LS(k_ffn_q5_0, FmtQ5_0, EPI_FFN, float)
+RT_GEMV_LS(k_gemv_q5k_f32_f32, FmtQ5K, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q5k_f32_f32add, FmtQ5K, EPI_F32_ADD, float)
+RT_GEMV_LS(k_ffn_q5k, FmtQ5K, EPI_FFN, float)
+RT_GEMV_LS(k_gemv_q4_0g_f32_f32, FmtQ4_0G, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q4_0g_f32_f32add, FmtQ4_0G, EPI_F32_ADD, float)
+RT_GEMV_LS(k_ffn_q4_0g, FmtQ4_0G, EPI_FFN, float)
+RT_GEMV_LS(k_gemv_q4kg_f32_f32, FmtQ4KG, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q4kg_f32_f32add, FmtQ4KG, EPI_F32_ADD, float)
+RT_GEMV_LS(k_ffn_q4kg, FmtQ4KG, EPI_FFN, float)
+RT_GEMV_LS(k_gemv_q5kg_f32_f32, FmtQ5KG, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q5kg_f32_f32add, FmtQ5KG, EPI_F32_ADD, float)
+RT_GEMV_LS(k_ffn_q5kg, FmtQ5KG, EPI_FFN, float)
+RT_GEMV_LSB(k_gemv_q6k_f32_f32, FmtQ6KB, EPI_F32, float, 256)
+RT_GEMV_LSB(k_gemv_q6k_f32_f32add, FmtQ6KB, EPI_F32_ADD, float, 256)
+RT_GEMV_LSB(k_gemv_q6kg_f32_f32, FmtQ6KGB, EPI_F32, float, 256)
+RT_GEMV_LSB(k_gemv_q6kg_f32_f32add, FmtQ6KGB, EPI_F32_ADD, float, 256)

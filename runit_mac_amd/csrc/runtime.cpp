@@ -46,6 +46,7 @@ struct GemvArgs {
     const float* xml;
     uint32_t xnsp, xhd;
     uint32_t ls_rs;
+    uint32_t ls_res;
 };
 
 constexpr uint32_t XREC_BYTES = 112;
@@ -139,13 +140,16 @@ const char* const kLsBases[] = {
     "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_gemv_q8_0_f32_f16", "k_qkv_bias_q8_0",
     "k_ffn_q8_0", "k_gemv_q4_0_f32_f32", "k_gemv_q4_0_f32_f32add", "k_qkv_bias_q4_0",
     "k_ffn_q4_0", "k_gemv_q4k_f32_f32", "k_gemv_q4k_f32_f32add", "k_ffn_q4k",
-    "k_gemv_q6k_f32_f32", "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32",
+    "k_gemv_q6k_f32_f32", "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32", "k_gemv_q6kg_f32_f32add",
+    "k_gemv_q5_0_f32_f32", "k_gemv_q5_0_f32_f32add", "k_ffn_q5_0",
+    "k_gemv_q5k_f32_f32", "k_gemv_q5k_f32_f32add", "k_ffn_q5k",
+    "k_gemv_q4_0g_f32_f32", "k_gemv_q4_0g_f32_f32add", "k_ffn_q4_0g",
+    "k_gemv_q4kg_f32_f32", "k_gemv_q4kg_f32_f32add", "k_ffn_q4kg",
+    "k_gemv_q5kg_f32_f32", "k_gemv_q5kg_f32_f32add", "k_ffn_q5kg",
 };
 constexpr uint32_t kLsMaxNI = 3;
 constexpr int kLsDecline = -1;
 constexpr uint32_t kLsThreads = 256;
-constexpr uint32_t kLsMaxItems = 64;    // items per wave (kernel: 4 groups of 16)
-constexpr uint32_t kLsResBytes = 1024;  // per-wave result buffer (64 items × 4 rows)
 constexpr uint32_t kLsRowPad = 48;      // LDS row stride = NI KB + pad (bank spread)
 
 struct Fmt {
@@ -212,7 +216,8 @@ struct rt_ctx {
     uint32_t prepass_k = 8192;  // RUNIT_PREPASS_K: K from which x is converted once
     bool ls_enabled = true;      // RUNIT_GEMV_LS=0: the per-lane-load matrix-core body instead
     uint32_t ls_pad = kLsRowPad; // RUNIT_GEMV_LS_PAD (sweeps only)
-    uint32_t ls_min_items = 8;   // RUNIT_GEMV_LS_MIN: quads per wave from which the LDS body runs
+    uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
+    uint32_t ls_threads = 0;     // RUNIT_GEMV_LS_THREADS: force the block size (sweeps)
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
     void* aux = nullptr;
@@ -383,39 +388,48 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     a.ksplit = S;
     a.kc_units = kc;
     a.ls_rs = NI * 1024 + c->ls_pad;
-    const uint32_t nw = kLsThreads / 64;
-    const size_t lds = (size_t)kc * ue / 32 * XREC_BYTES + nw * kLsResBytes + (size_t)nw * 4 * a.ls_rs;
-    if (lds > c->max_lds) return kLsDecline;
     const uint32_t nq = (a.nvrows + 3) / 4;
-    // The body's per-item dot code runs at two waves per SIMD; it pays off
-    // where each wave has many items (vocabulary-sized N), while
-    // shorter launches run faster on the matrix-core body's 16 waves per CU.
-    if (nq < (uint32_t)c->cu_count * 8 * c->ls_min_items) return kLsDecline;
-    // buffer loads address each matrix with 32-bit offsets (out-of-range
-    // offsets ≥ 2^31 mark the loads of items past a wave's last)
+    // The body pays off from ~16 items (row quads × K chunks) per CU: the
+    // 7B FFN / down / LM-head launches; launches with fewer items (the QKV
+    // and attention projections, the 0.5B model's GEMVs) run faster on the
+    // matrix-core body, whose per-lane loads start streaming sooner.
+    if ((uint64_t)nq * S < (uint64_t)c->cu_count * c->ls_min_items) return kLsDecline;
+    // buffer sizes address each matrix with 32-bit offsets
     if ((uint64_t)a.nvrows * a.row_bytes + 16 >= (1ull << 31)) return kLsDecline;
     char name[96];
     snprintf(name, sizeof name, "%s_ls%u", kname, NI);
-    const uint32_t occ = occupancy(c, name, kLsThreads, lds);
-    // One round of resident workgroups, k per CU (k ≤ occupancy), with the k
-    // whose busiest wave is closest to the average: a wave's last items run
-    // with few loads in flight on its CU, so a grid that leaves a fraction of
-    // the waves one extra item pays most of an item's time for it.
-    uint32_t nwg = 0;
-    double best = -1.0;
-    for (uint32_t k = 1; k <= occ; ++k) {
-        const uint32_t g = std::max<uint32_t>(1, (uint32_t)c->cu_count * k / S);
-        const uint64_t waves = (uint64_t)g * nw;
-        const uint64_t per = (nq + waves - 1) / waves;
-        const double eff = (double)nq / (double)(waves * per);
-        if (eff > best + 0.02) {
-            best = eff;
-            nwg = g;
+    // Block size: the one with the most resident waves per CU (larger
+    // blocks share one copy of the activation records), one round of
+    // resident workgroups, result buffers sized to the items per wave.
+    const uint32_t tmax = f.mq_unit_el == 256 ? 256 : 1024;  // Q6_K: register-heavy units
+    const size_t xbytes = (size_t)kc * ue / 32 * XREC_BYTES;
+    uint32_t bt = 0, bg = 0, bres = 0, bwaves = 0;
+    size_t blds = 0;
+    for (uint32_t t = 256; t <= tmax; t *= 2) {
+        if (c->ls_threads && t != c->ls_threads) continue;
+        const uint32_t nwv = t / 64;
+        uint32_t res = 16, g = 0, occ = 0;
+        size_t lds = 0;
+        for (int it = 0; it < 4; ++it) {  // result capacity ↔ grid size
+            lds = xbytes + (size_t)nwv * res * 16 + (size_t)nwv * 4 * a.ls_rs;
+            if (lds > c->max_lds) break;
+            occ = occupancy(c, name, t, lds);
+            g = std::max<uint32_t>(1, (uint32_t)c->cu_count * (c->grid_per_cu ? c->grid_per_cu : occ) / S);
+            g = std::min<uint32_t>(g, (nq + nwv - 1) / nwv);
+            const uint32_t per = (nq + g * nwv - 1) / (g * nwv);
+            const uint32_t need = std::min<uint32_t>(64, (per + 15) / 16 * 16);
+            if (need == res) break;
+            res = need;
+        }
+        if (lds > c->max_lds || g == 0) continue;
+        g = std::max<uint32_t>(g, (nq + nwv * res - 1) / (nwv * res));  // ≤ res items per wave
+        const uint32_t waves = std::min<uint32_t>(occ * nwv, g * nwv * S / std::max(1, c->cu_count));
+        if (waves > bwaves || (waves == bwaves && t > bt)) {
+            bt = t; bg = g; bres = res; bwaves = waves; blds = lds;
         }
     }
-    if (c->grid_per_cu) nwg = std::max<uint32_t>(1, (uint32_t)c->cu_count * c->grid_per_cu / S);
-    nwg = std::min<uint32_t>(nwg, (nq + nw - 1) / nw);
-    nwg = std::max<uint32_t>(nwg, (nq + nw * kLsMaxItems - 1) / (nw * kLsMaxItems));
+    if (!bt) return kLsDecline;
+    a.ls_res = bres;
     if (S > 1) {
         if (nq > kAttnCounters)
             return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: %u row quads exceed %u",
@@ -428,7 +442,7 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
         while (a.cstride > 1 && (size_t)nq * a.cstride > kAttnCounters) a.cstride >>= 1;
     }
     void* params[] = {&a};
-    return launch(c, name, dim3(nwg * S), dim3(kLsThreads), lds, params);
+    return launch(c, name, dim3(bg * S), dim3(bt), blds, params);
 }
 
 int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x_f16,
@@ -689,6 +703,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_ATTN_SPLIT")) c->attn_split_override = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMV_LS_THREADS")) c->ls_threads = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS_PAD")) c->ls_pad = (uint32_t)atoi(g) & ~15u;
     if (const char* g = getenv("RUNIT_GEMV_KSW")) {
         const int v = atoi(g);

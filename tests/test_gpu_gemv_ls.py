@@ -1,9 +1,9 @@
 """GPU parity of the LDS-streamed GEMV body (k_gemv_ls.hip) against the CPU
 oracle, through the C ABI.
 
-The library takes that body only for vocabulary-sized launches; a second
-context created with RUNIT_GEMV_LS_MIN=0 takes it for every shape it can
-serve, so the cases below cover its edges at small sizes: row counts that are
+The library takes that body only for launches with at least 16 items (row
+quads × K chunks) per CU; a second context created with RUNIT_GEMV_LS_MIN=0
+takes it for every shape it can serve, so the cases below cover its edges at small sizes: row counts that are
 not a multiple of 4, a weight base that is not 16-byte aligned, an output that
 aliases the residual, fused QKV (+bias) and gate+up+SiLU row mappings, a
 K split into chunks (rows longer than 3 KB), and a launch with more items per
@@ -49,16 +49,17 @@ def _weights_at(ctx, fmt, n, k, seed, offset):
     return buf.ptr + offset, raw, [wbuf, buf]
 
 
-LS_FMTS = ["q8_0", "q4_0", "q4k", "q6k"]
+LS_FMTS = ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg"]
+KQUANTS = ("q4k", "q6k", "q5k", "q4kg", "q5kg", "q6kg")
 
 
 @pytest.mark.parametrize("fmt", LS_FMTS)
 @pytest.mark.parametrize("n,k,offset", [(37, 512, 0), (300, 3584, 2), (1027, 896, 0),
                                         (5, 1024, 4), (2053, 256, 8)])
 def test_ls_gemv_plain_and_residual(lsctx, fmt, n, k, offset):
-    if fmt in ("q4k", "q6k") and k % 256:
+    if fmt in KQUANTS and k % 256:
         pytest.skip("K-quants need K % 256 == 0")
-    if fmt == "q8_0" and (k // 32) % 2:
+    if fmt in ("q8_0", "q4_0", "q5_0", "q4_0g") and (k // 32) % 2:
         pytest.skip("odd block count: single-block kernels")
     w, raw, keep = _weights_at(lsctx, fmt, n, k, seed=n + k, offset=offset)
     rng = np.random.default_rng(n * 7 + k)
@@ -105,7 +106,10 @@ def test_ls_gemv_q6kg(lsctx):
 
 
 @pytest.mark.parametrize("fmt,n,k", [("q4_0", 96, 18944), ("q6k", 70, 18944),
-                                     ("q8_0", 130, 8192), ("q4k", 33, 16384)])
+                                     ("q8_0", 130, 8192), ("q4k", 33, 16384),
+                                     ("q5k", 41, 18944), ("q5_0", 37, 9216),
+                                     ("q4kg", 29, 18944), ("q6kg", 22, 18944),
+                                     ("q4_0g", 31, 18944), ("q5kg", 19, 18944)])
 def test_ls_gemv_k_split(lsctx, fmt, n, k):
     # rows longer than 3 KB: K chunks whose partial sums meet in the workspace
     wbuf, raw = device_weights(lsctx, fmt, n, k, seed=n)
@@ -129,7 +133,9 @@ def test_ls_gemv_k_split(lsctx, fmt, n, k):
 
 @pytest.mark.parametrize("fmt,ff,k", [("q8_0", 4864, 896), ("q8_0", 301, 512),
                                       ("q4_0", 1000, 3584), ("q4k", 77, 512),
-                                      ("q4_0", 129, 18944)])
+                                      ("q4_0", 129, 18944), ("q5_0", 1000, 3584),
+                                      ("q5k", 333, 3584), ("q4_0g", 257, 3584),
+                                      ("q4kg", 1000, 3584), ("q5kg", 65, 1024)])
 def test_ls_fused_ffn(lsctx, fmt, ff, k):
     wg, rg = device_weights(lsctx, fmt, ff, k, seed=ff + 1)
     wu, ru = device_weights(lsctx, fmt, ff, k, seed=ff + 2)
