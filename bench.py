@@ -305,8 +305,9 @@ def profile_pass(ctx, launches: int = 24) -> None:
     """Eager (not graph-captured) launches for hardware-counter runs
     (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the dominant kernel of the
     decode step — the norm-fused gate+up+SiLU GEMV at the 0.5B shape — over
-    `launches` distinct weight replicas, then a plain copy kernel of known
-    size whose counters calibrate the byte counts."""
+    `launches` distinct weight replicas, the 7B Q4_K gate+up+SiLU over 8,
+    then a plain copy kernel of known size whose counters calibrate the byte
+    counts."""
     from runit_mac_amd.decode import DecodeConfig
     cfg = DecodeConfig()
     h, ff = cfg.hidden, cfg.ff
@@ -327,16 +328,34 @@ def profile_pass(ctx, launches: int = 24) -> None:
     for g, u in mats:
         d.rms_norm_fused_ffn_q8_0_f32(ctx, g, u, x, gamma, cfg.eps, act, ff, h)
     ctx.flush()
+    # the 7B Q4_K gate+up+SiLU (LDS-streamed body) over 8 replicas of 76 MB
+    ff7, h7 = 18944, 3584
+    wb7 = d.weight_bytes("q4k", ff7, h7)
+    arena7 = _arena_for(ctx, [wb7, wb7], 8)
+    mats7 = []
+    for r in range(8):
+        g, u = arena7.take(wb7), arena7.take(wb7)
+        d.synth_weights(ctx, "q4k", g, ff7 * h7 // 256, 300 + 2 * r)
+        d.synth_weights(ctx, "q4k", u, ff7 * h7 // 256, 301 + 2 * r)
+        mats7.append((g, u))
+    x7, act7 = ctx.new_buffer(4 * h7), ctx.new_buffer(4 * ff7)
+    d.synth_normal_f32(ctx, x7, h7, 7)
+    ctx.flush()
+    for g, u in mats7:
+        d.fused_ffn_q4k_f32(ctx, g, u, x7, act7, ff7, h7)
+    ctx.flush()
     copy_bytes = 256 << 20
     src, dst = ctx.new_buffer(copy_bytes), ctx.new_buffer(copy_bytes)
     for _ in range(3):
         d.stream_copy(ctx, dst, src, copy_bytes)
     ctx.flush()
     log(f"profile pass: {launches} x k_ffn_q8_0 ({2 * wb} weight bytes each), "
+        f"8 x k_ffn_q4k ({2 * wb7} weight bytes each), "
         f"3 x k_stream_copy ({copy_bytes} bytes each)")
-    for b in (src, dst, x, gamma, act):
+    for b in (src, dst, x, gamma, act, x7, act7):
         b.free()
     arena.free()
+    arena7.free()
 
 
 def main():
