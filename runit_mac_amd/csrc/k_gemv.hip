@@ -41,6 +41,7 @@ struct GemvArgs {
     uint32_t xnsp, xhd;
     uint32_t ls_rs;      // LDS-streamed body: LDS bytes between two rows of a slot
     uint32_t ls_res;     // LDS-streamed body: result slots per wave (items)
+    uint32_t ls_xcd;     // LDS-streamed body: neighbouring quads to workgroups of one XCD
 };
 
 // Tiles one workgroup may own in a K-split launch (the host keeps the grid's

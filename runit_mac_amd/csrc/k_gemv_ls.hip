@@ -49,7 +49,14 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     const uint32_t q = lane & 3, slot = lane >> 2;
     const uint32_t lq = q < 3 ? q : 2;  // the A row of lane q = 3 is a don't-care
     const uint32_t S = a.ksplit;
-    const uint32_t ks = blockIdx.x % S, wg = blockIdx.x / S, nwg = gridDim.x / S;
+    const uint32_t ks = blockIdx.x % S, nwg = gridDim.x / S;
+    // Workgroups are dealt to the 8 XCDs in turn (block b → XCD b mod 8).
+    // Without a K split, renumber them so that neighbouring row quads, which
+    // share the cache lines at their ends, go to workgroups on one XCD (one
+    // L2) instead of to eight.
+    const uint32_t wg = (S == 1 && a.ls_xcd && nwg % 8 == 0)
+                            ? (blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8
+                            : blockIdx.x / S;
     const uint32_t cu0 = ks * a.kc_units;  // first unit of this workgroup's K chunk
     const uint32_t units = min(a.K / F::UNIT_EL - cu0, a.kc_units);
     const uint32_t cbyte0 = cu0 * F::UNIT_EL / F::BLK_EL * F::BLK_BYTES;  // chunk offset in a row

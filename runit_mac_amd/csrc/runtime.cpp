@@ -47,6 +47,7 @@ struct GemvArgs {
     uint32_t xnsp, xhd;
     uint32_t ls_rs;
     uint32_t ls_res;
+    uint32_t ls_xcd;
 };
 
 constexpr uint32_t XREC_BYTES = 112;
@@ -218,6 +219,7 @@ struct rt_ctx {
     uint32_t ls_pad = kLsRowPad; // RUNIT_GEMV_LS_PAD (sweeps only)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     uint32_t ls_threads = 0;     // RUNIT_GEMV_LS_THREADS: force the block size (sweeps)
+    uint32_t ls_xcd = 1;         // RUNIT_GEMV_LS_XCD=0: plain workgroup order (sweeps)
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
     void* aux = nullptr;
@@ -430,6 +432,7 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     }
     if (!bt) return kLsDecline;
     a.ls_res = bres;
+    a.ls_xcd = c->ls_xcd;
     if (S > 1) {
         if (nq > kAttnCounters)
             return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: %u row quads exceed %u",
@@ -704,6 +707,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS_THREADS")) c->ls_threads = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMV_LS_XCD")) c->ls_xcd = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS_PAD")) c->ls_pad = (uint32_t)atoi(g) & ~15u;
     if (const char* g = getenv("RUNIT_GEMV_KSW")) {
         const int v = atoi(g);
