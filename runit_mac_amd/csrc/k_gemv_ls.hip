@@ -203,7 +203,11 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
         flush(g, min(nitems - g * kLsGroup, kLsGroup));
     }
 
+#ifdef RT_PROBE_LS_NOMERGE
+    if (false) {
+#else
     if (S > 1) {
+#endif
         // K split: count this chunk in at each of the wave's quads (lane of
         // row 0 of the item), then the last chunk to arrive sums the chunks
         // in order and runs the epilogue
@@ -233,6 +237,122 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     }
 }
 
+// Workgroup-local K split (rows longer than the slot, few row quads: the 7B
+// down projections).  Each workgroup owns row quads g, g + nwg, ... and all K
+// chunks of each; its waves take (quad, chunk) items in turn (item i: quad
+// i / S, chunk i % S), so the partial sums of a row meet in LDS instead of
+// through memory and arrival counters.  The activation records of the whole
+// K are staged once per workgroup.  After the last item a barrier, then the
+// chunks of each row are added in chunk order and the epilogue runs.
+template <class F, int EPI, typename XT, int NI>
+RT_DEV void gemv_lsk_body(const GemvArgs& a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nwaves = wg_threads() >> 6;
+    const uint32_t q = lane & 3, slot = lane >> 2;
+    const uint32_t lq = q < 3 ? q : 2;
+    const uint32_t S = a.ksplit;          // K chunks of a row (all in this workgroup)
+    const uint32_t kcu = a.kc_units;      // units per chunk (the last may be shorter)
+    const uint32_t wg = blockIdx.x, nwg = gridDim.x;
+    const uint32_t units_all = a.K / F::UNIT_EL;
+    const uint32_t nxb_all = a.K / 32;
+    XRec* xs = (XRec*)smem;
+    const uint32_t xcap = nxb_all * XREC_BYTES;
+    const uint32_t nq = (a.nvrows + 3) / 4;
+    const uint32_t nql = wg < nq ? (nq - wg + nwg - 1) / nwg : 0;  // this workgroup's quads
+    float* res = (float*)(smem + xcap);                              // [nql][S][4]
+    const uint32_t RS = a.ls_rs;
+    uint8_t* wslot = smem + xcap + a.ls_res * 16 + wave * (4 * RS);
+    const uint32_t nitems_wg = nql * S;
+    const uint32_t nitems = wave < nitems_wg ? (nitems_wg - wave + nwaves - 1) / nwaves : 0;
+    auto item_of = [&](uint32_t j) { return wave + nwaves * j; };  // workgroup item index
+
+    auto row_src = [&](uint32_t vr, uint32_t c) -> const uint8_t* {
+        if (vr >= a.nvrows) vr = a.nvrows - 1;
+        uint32_t mat, r;
+        vrow_map<EPI>(a, vr, mat, r);
+        return mat_w(a, mat) + (size_t)r * a.row_bytes + c * kcu * F::UNIT_EL / F::BLK_EL * F::BLK_BYTES;
+    };
+    auto chunk_units = [&](uint32_t c) { return min(units_all - c * kcu, kcu); };
+    typedef u32x4 Item[4][NI];
+    auto issue = [&](uint32_t j, Item& dst) {
+        const uint32_t it = item_of(min(j, nitems - 1));
+        const uint32_t quad = wg + nwg * (it / S), c = it % S;
+        const uint32_t cbytes = chunk_units(c) * F::UNIT_EL / F::BLK_EL * F::BLK_BYTES;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint8_t* src = row_src(quad * 4 + r, c);
+            const uint8_t* base = src - ((uintptr_t)src & 15);
+            const uint32_t last = (uint32_t)(((uintptr_t)src & 15) + cbytes - 1) & ~15u;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t off = min((uint32_t)(i * 64 + lane) * 16, last);
+                dst[r][i] = *(const u32x4*)(base + off);
+            }
+        }
+    };
+    auto commit = [&](const Item& src) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < NI; ++i) *(u32x4*)(wslot + r * RS + (i * 64 + lane) * 16) = src[r][i];
+    };
+
+    // epilogue operand of this thread's row (thread t < 4·nql: quad t/4, row t%4)
+    float aux = 0.0f;
+    if (has_aux<EPI>()) {
+        const uint32_t vr = (wg + nwg * min(tid >> 2, nql ? nql - 1 : 0)) * 4 + (tid & 3);
+        aux = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
+    }
+    Item buf;
+    issue(0, buf);
+    stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, nxb_all, xs);
+    lds_barrier();
+
+    for (uint32_t j = 0; j < nitems; ++j) {
+        commit(buf);
+        issue(j + 1, buf);
+        const uint32_t it = item_of(j);
+        const uint32_t ql = it / S, c = it % S;
+        const uint32_t units = chunk_units(c);
+        const uint8_t* rowl = wslot + q * RS + ((uintptr_t)row_src((wg + nwg * ql) * 4 + q, c) & 15);
+        const XRec* xc = xs + c * kcu * F::UNIT_EL / 32;
+        const uint32_t nsteps = (units + 15) / 16;
+        float acc = 0.0f;
+        for (uint32_t st = 0; st < nsteps; ++st) {
+            const uint32_t u = slot + 16 * st;
+            const bool valid = u < units;
+            const uint32_t uc = valid ? u : 0;
+            typename F::Raw raw;
+            ls_load<F>(rowl, uc, raw, 0);
+            const float v = F::mdot(raw, xc, uc, lq);
+            acc += valid ? v : 0.0f;
+        }
+        acc += swz_xor_f<4>(acc);
+        acc += swz_xor_f<8>(acc);
+        acc += swz_xor_f<16>(acc);
+        acc += __shfl_xor(acc, 32, 64);
+        if (slot == 0) res[it * 4 + q] = acc;
+    }
+    __syncthreads();
+    if (tid < 4 * nql) {
+        const uint32_t ql = tid >> 2, r = tid & 3;
+        const uint32_t vr = (wg + nwg * ql) * 4 + r;
+        float v = 0.0f, v1 = 0.0f;
+        for (uint32_t c = 0; c < S; ++c) {
+            v += res[(ql * S + c) * 4 + r];
+            if (EPI == EPI_FFN && r + 1 < 4) v1 += res[(ql * S + c) * 4 + r + 1];
+        }
+        if (EPI == EPI_FFN) {
+            // quad rows (gate r, up r, gate r+1, up r+1)
+            if ((r & 1) == 0 && vr + 1 < a.nvrows) ((float*)a.out[0])[vr >> 1] = silu_ref(v) * v1;
+        } else if (vr < a.nvrows) {
+            store_row_pre<EPI>(a, vr, v, aux);
+        }
+    }
+}
+
 // Kernels: one per (format, epilogue, activation type, loads per row NI).
 // Built for up to 1024 threads (≤ 128 registers: 16 waves per CU share one
 // copy of the activation records), except Q6_K, whose whole-super-block
@@ -241,6 +361,8 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     extern "C" __global__ void __launch_bounds__(LB) NAME##_ls##NI(GemvArgs a) { gemv_ls_body<FMT, EPI, XT, NI>(a); }
 #define RT_GEMV_LSB(NAME, FMT, EPI, XT, LB) \
     RT_GEMV_LS1(NAME, FMT, EPI, XT, 1, LB) RT_GEMV_LS1(NAME, FMT, EPI, XT, 2, LB) RT_GEMV_LS1(NAME, FMT, EPI, XT, 3, LB)
+#define RT_GEMV_LSK(NAME, FMT, EPI, XT, LB) \
+    extern "C" __global__ void __launch_bounds__(LB) NAME##_lsk1(GemvArgs a) { gemv_lsk_body<FMT, EPI, XT, 1>(a); }
 #define RT_GEMV_LS(NAME, FMT, EPI, XT) RT_GEMV_LSB(NAME, FMT, EPI, XT, 1024)
 
 RT_GEMV_LS(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float)
@@ -274,3 +396,19 @@ RT_GEMV_LSB(k_gemv_q6k_f32_f32, FmtQ6KB, EPI_F32, float, 256)
 RT_GEMV_LSB(k_gemv_q6k_f32_f32add, FmtQ6KB, EPI_F32_ADD, float, 256)
 RT_GEMV_LSB(k_gemv_q6kg_f32_f32, FmtQ6KGB, EPI_F32, float, 256)
 RT_GEMV_LSB(k_gemv_q6kg_f32_f32add, FmtQ6KGB, EPI_F32_ADD, float, 256)
+
+// Workgroup-local K split kernels (the residual / plain forms of the down
+// projections and the FFNs of long-K models)
+RT_GEMV_LSK(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float, 1024)
+RT_GEMV_LSK(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_gemv_q4_0_f32_f32, FmtQ4_0, EPI_F32, float, 1024)
+RT_GEMV_LSK(k_gemv_q4_0_f32_f32add, FmtQ4_0, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_ffn_q4_0, FmtQ4_0, EPI_FFN, float, 1024)
+RT_GEMV_LSK(k_gemv_q4k_f32_f32, FmtQ4K, EPI_F32, float, 1024)
+RT_GEMV_LSK(k_gemv_q4k_f32_f32add, FmtQ4K, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_gemv_q5k_f32_f32, FmtQ5K, EPI_F32, float, 1024)
+RT_GEMV_LSK(k_gemv_q5k_f32_f32add, FmtQ5K, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_gemv_q4kg_f32_f32add, FmtQ4KG, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_gemv_q5kg_f32_f32add, FmtQ5KG, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_gemv_q4_0g_f32_f32add, FmtQ4_0G, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_gemv_q5_0_f32_f32add, FmtQ5_0, EPI_F32_ADD, float, 1024)

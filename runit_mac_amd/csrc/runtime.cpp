@@ -148,6 +148,12 @@ const char* const kLsBases[] = {
     "k_gemv_q4kg_f32_f32", "k_gemv_q4kg_f32_f32add", "k_ffn_q4kg",
     "k_gemv_q5kg_f32_f32", "k_gemv_q5kg_f32_f32add", "k_ffn_q5kg",
 };
+// Kernels of the workgroup-local K split: <base>_lsk1.
+const char* const kLskBases[] = {
+    "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_gemv_q4_0_f32_f32", "k_gemv_q4_0_f32_f32add",
+    "k_ffn_q4_0", "k_gemv_q4k_f32_f32", "k_gemv_q4k_f32_f32add", "k_gemv_q5k_f32_f32",
+    "k_gemv_q5k_f32_f32add", "k_gemv_q4kg_f32_f32add", "k_gemv_q5kg_f32_f32add", "k_gemv_q4_0g_f32_f32add", "k_gemv_q5_0_f32_f32add",
+};
 constexpr uint32_t kLsMaxNI = 3;
 constexpr int kLsDecline = -1;
 constexpr uint32_t kLsThreads = 256;
@@ -220,6 +226,7 @@ struct rt_ctx {
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     uint32_t ls_threads = 0;     // RUNIT_GEMV_LS_THREADS: force the block size (sweeps)
     uint32_t ls_xcd = 1;         // RUNIT_GEMV_LS_XCD=0: plain workgroup order (sweeps)
+    bool lsk_enabled = true;     // RUNIT_GEMV_LSK=0: K splits over workgroups (through memory) instead
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
     void* aux = nullptr;
@@ -362,6 +369,57 @@ bool has_ls_kernel(const rt_ctx* c, const char* kname) {
 // each, so rows longer than 3 KB (or K beyond one staging pass) are split
 // into S chunks whose partial sums meet in the workspace.  Returns 1 when the
 // shape does not suit the body (kLsDecline: the caller takes the other bodies).
+// Workgroup-local K split (k_gemv_ls.hip, *_lsk1): every K chunk of a row
+// quad in one workgroup, 1 KB row chunks, the whole K's activation records in
+// LDS; the chunks' partial sums meet in LDS.
+int gemv_launch_lsk(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
+    char name[96];
+    snprintf(name, sizeof name, "%s_lsk1", kname);
+    if (!c->fns.count(name)) return kLsDecline;
+    const uint32_t ue = f.mq_units();
+    const uint32_t units = a.K / ue;
+    const uint32_t gu = f.blk_el > ue ? f.blk_el / ue : 1;
+    const uint64_t unum = (uint64_t)ue * f.blk_bytes;  // unit bytes × blk_el
+    uint32_t cap = (uint32_t)((1024 - 15) * (uint64_t)f.blk_el / unum);
+    cap -= cap % gu;
+    if (cap == 0) return kLsDecline;
+    uint32_t S = (units + cap - 1) / cap;
+    uint32_t kc = (units + S - 1) / S;
+    kc = (kc + gu - 1) / gu * gu;
+    S = (units + kc - 1) / kc;
+    const uint32_t nq = (a.nvrows + 3) / 4;
+    // Taken where the whole K's activation records stay small (≤ 32 KB, K ≤
+    // 9,362: the 0.5B model's down projection, 896×4864, runs 1.3 µs faster
+    // than with the K split through memory) and the units suit 1024-thread
+    // workgroups; longer K (the 7B down projections) keeps the split through
+    // memory, whose workgroups stage only their own chunk.
+    if (f.mq_unit_el == 256 || (size_t)(a.K / 32) * XREC_BYTES > 32 * 1024) return kLsDecline;
+    const uint32_t t = 1024;
+    const uint32_t nwv = t / 64;
+    a.ksplit = S;
+    a.kc_units = kc;
+    a.ls_rs = 1024 + c->ls_pad;
+    const size_t xbytes = (size_t)(a.K / 32) * XREC_BYTES;
+    uint32_t nwg = 0, occ = 1;
+    size_t lds = 0;
+    for (int it = 0; it < 3; ++it) {  // workgroups ↔ result buffer size
+        const uint32_t g = nwg ? nwg : std::min<uint32_t>(nq, (uint32_t)c->cu_count);
+        const uint32_t nql = (nq + g - 1) / g;
+        lds = xbytes + (size_t)nql * S * 16 + (size_t)nwv * 4 * a.ls_rs;
+        if (lds > c->max_lds) return kLsDecline;
+        occ = occupancy(c, name, t, lds);
+        const uint32_t want = std::min<uint32_t>(nq, (uint32_t)c->cu_count * (c->grid_per_cu ? c->grid_per_cu : occ));
+        if (want == g && nwg) break;
+        nwg = want;
+    }
+    const uint32_t nql = (nq + nwg - 1) / nwg;
+    a.ls_res = nql * S;
+    lds = xbytes + (size_t)a.ls_res * 16 + (size_t)nwv * 4 * a.ls_rs;
+    if (lds > c->max_lds) return kLsDecline;
+    void* params[] = {&a};
+    return launch(c, name, dim3(nwg), dim3(t), lds, params);
+}
+
 int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     const uint32_t ue = f.mq_units();
     const uint32_t units_total = a.K / ue;
@@ -387,10 +445,14 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
         NI = (uint32_t)((chunk_bytes(kc) + 15 + 1023) / 1024);
         if (NI > kLsMaxNI) return kLsDecline;
     }
+    const uint32_t nq = (a.nvrows + 3) / 4;
+    if (S > 1 && c->lsk_enabled && !a.gamma) {
+        const int st = gemv_launch_lsk(c, kname, f, a);
+        if (st != kLsDecline) return st;
+    }
     a.ksplit = S;
     a.kc_units = kc;
     a.ls_rs = NI * 1024 + c->ls_pad;
-    const uint32_t nq = (a.nvrows + 3) / 4;
     // The body pays off from ~16 items (row quads × K chunks) per CU: the
     // 7B FFN / down / LM-head launches; launches with fewer items (the QKV
     // and attention projections, the 0.5B model's GEMVs) run faster on the
@@ -708,6 +770,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS_THREADS")) c->ls_threads = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS_XCD")) c->ls_xcd = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMV_LSK")) c->lsk_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS_PAD")) c->ls_pad = (uint32_t)atoi(g) & ~15u;
     if (const char* g = getenv("RUNIT_GEMV_KSW")) {
         const int v = atoi(g);
@@ -725,6 +788,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     std::vector<std::string> names(std::begin(kKernelNames), std::end(kKernelNames));
     for (const char* b : kLsBases)
         for (uint32_t ni = 1; ni <= kLsMaxNI; ++ni) names.push_back(std::string(b) + "_ls" + std::to_string(ni));
+    for (const char* b : kLskBases) names.push_back(std::string(b) + "_lsk1");
     for (const std::string& ns : names) {
         const char* n = ns.c_str();
         hipFunction_t f = nullptr;

@@ -179,3 +179,43 @@ def test_ls_default_context_vocab_sized(ctx):
     d.gemv_q8_0_f32in_f32out(ctx, wbuf, ctx.buffer_from(x), y, n, k)
     ctx.flush()
     check_close(y.read(np.float32, n), yref, sabs, "vocab-sized q8_0", F32_EPS * np.abs(yref))
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q8_0", 896, 4864), ("q8_0", 37, 6144), ("q4_0", 301, 4864),
+                                     ("q4k", 130, 4608), ("q5k", 77, 8192), ("q4kg", 66, 4608),
+                                     ("q5kg", 9, 5120), ("q4_0g", 129, 4864), ("q5_0", 64, 4864)])
+def test_lsk_workgroup_k_split(ctx, fmt, n, k):
+    # rows longer than the LDS slot with the whole K's records ≤ 32 KB (the
+    # 0.5B down projection's shape): every K chunk of a row quad in one
+    # workgroup, partial sums added in LDS in chunk order
+    w, raw, keep = _weights_at(ctx, fmt, n, k, seed=n + 5, offset=2 if fmt == "q8_0" else 0)
+    rng = np.random.default_rng(n + k)
+    x = rng.standard_normal(k).astype(np.float32)
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    xb = ctx.buffer_from(x)
+    res = rng.standard_normal(n).astype(np.float32)
+    for rep in range(2):
+        y = ctx.new_buffer(4 * n)
+        getattr(d, f"gemv_{fmt}_f32in_f32out")(ctx, w, xb, y, n, k)
+        yr = ctx.buffer_from(res)
+        getattr(d, f"gemv_{fmt}_add_f32_f32in")(ctx, w, xb, yr, yr, n, k)
+        ctx.flush()
+        check_close(y.read(np.float32, n), yref, sabs, f"lsk {fmt} {n}x{k} rep {rep}",
+                    F32_EPS * np.abs(yref))
+        ref = yref + res
+        check_close(yr.read(np.float32, n), ref, sabs, f"lsk add {fmt} {n}x{k} rep {rep}",
+                    F32_EPS * np.abs(ref))
+    del keep
+
+
+def test_lsk_fused_ffn_q4_0(ctx):
+    ff, k = 257, 5120
+    wg, rg = device_weights(ctx, "q4_0", ff, k, seed=71)
+    wu, ru = device_weights(ctx, "q4_0", ff, k, seed=72)
+    x = np.random.default_rng(73).standard_normal(k).astype(np.float32)
+    act = ctx.new_buffer(4 * ff)
+    d.fused_ffn_q4_0_f32(ctx, wg, wu, ctx.buffer_from(x), act, ff, k)
+    ctx.flush()
+    g, gs = ora.gemv("q4_0", rg, x, ff, k)
+    u, us = ora.gemv("q4_0", ru, x, ff, k)
+    ffn_check(act.read(np.float32, ff), g, gs, u, us, "lsk ffn q4_0")
