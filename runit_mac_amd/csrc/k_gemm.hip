@@ -314,19 +314,21 @@ struct GemmQ4K {  // reference layout: record 2j (low nibbles of qs[32j..]) uses
     }
 };
 
-template <class P, int MG, int NB>
+template <class P, int MG, int NB, int WAVES = 4>
 RT_DEV void gemm2_body(const Gemm2Args& a) {
+    // WAVES waves of 16 weight rows each share one stage of activation operands
+    constexpr uint32_t T = 64 * WAVES, ROWS = 16 * WAVES;
     constexpr uint32_t NR = NB * P::RECS;                  // records per stage
     constexpr uint32_t SEG = NB * P::BLK_BYTES;            // bytes of a row segment
     constexpr uint32_t VB = SEG % 16 == 0 ? 16 : 8;        // bytes per W load (alignment)
     typedef typename std::conditional<VB == 16, u32x4, uint2>::type WV;
     constexpr uint32_t WPR = SEG / VB;                     // W loads per row segment
-    constexpr uint32_t WV_N = GB_ROWS * WPR;               // W loads per stage
+    constexpr uint32_t WV_N = ROWS * WPR;               // W loads per stage
     constexpr uint32_t AV4 = NR * MG * 64 * 8 / 16;        // dwordx4 of A per stage
     constexpr uint32_t EV4 = NR * 4 * MG * 4 / 16;         // dwordx4 of E (and of S) per stage
-    constexpr uint32_t WPT = (WV_N + 255) / 256;           // W loads per thread
-    constexpr uint32_t APT = (AV4 + 255) / 256;
-    static_assert(SEG % VB == 0 && EV4 <= 256, "segment alignment");
+    constexpr uint32_t WPT = (WV_N + T - 1) / T;           // W loads per thread
+    constexpr uint32_t APT = (AV4 + T - 1) / T;
+    static_assert(SEG % VB == 0 && EV4 <= T, "segment alignment");
     __shared__ WV lw[2][WV_N];
     __shared__ u32x4 la[2][AV4];
     __shared__ u32x4 le[2][EV4 > 0 ? EV4 : 1];
@@ -343,7 +345,7 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
         const uint32_t kb0 = split * a.kbs;
         const uint32_t kb1 = min(a.nxb, kb0 + a.kbs);
         const uint32_t nst = (kb1 - kb0) / NB;
-        const uint32_t row0 = tile * GB_ROWS;
+        const uint32_t row0 = tile * ROWS;
         const uint32_t nrec = a.nxb * P::RECS;
         const uint2* ap = a.aops + (size_t)ch * nrec * MG * 64;
         const int* ep = a.etab + (size_t)ch * nrec * 4 * MG;
@@ -356,7 +358,7 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
             const uint32_t r0 = b0 * P::RECS;   // its first record
 #pragma unroll
             for (uint32_t i = 0; i < WPT; ++i) {
-                uint32_t f = tid + 256 * i;
+                uint32_t f = tid + T * i;
                 if (f >= WV_N) f = WV_N - 1;  // duplicate load, not stored
                 const uint32_t r = f / WPR, col = f % WPR;
                 const uint32_t n = min(row0 + r, a.N - 1);
@@ -364,17 +366,17 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
             }
             const u32x4* as = (const u32x4*)(ap + (size_t)r0 * MG * 64);
 #pragma unroll
-            for (uint32_t i = 0; i < APT; ++i) ra[i] = as[min(tid + 256 * i, AV4 - 1)];
+            for (uint32_t i = 0; i < APT; ++i) ra[i] = as[min(tid + T * i, AV4 - 1)];
             re = ((const u32x4*)(ep + (size_t)r0 * 4 * MG))[min(tid, EV4 - 1)];
             if (P::HAS_MIN) rs = ((const u32x4*)(sp + (size_t)r0 * 4 * MG))[min(tid, EV4 - 1)];
         };
         auto lstore = [&](uint32_t buf) {
 #pragma unroll
             for (uint32_t i = 0; i < WPT; ++i)
-                if (tid + 256 * i < WV_N) lw[buf][tid + 256 * i] = rw[i];
+                if (tid + T * i < WV_N) lw[buf][tid + T * i] = rw[i];
 #pragma unroll
             for (uint32_t i = 0; i < APT; ++i)
-                if (tid + 256 * i < AV4) la[buf][tid + 256 * i] = ra[i];
+                if (tid + T * i < AV4) la[buf][tid + T * i] = ra[i];
             if (tid < EV4) le[buf][tid] = re;
             if (P::HAS_MIN && tid < EV4) ls[P::HAS_MIN ? buf : 0][tid] = rs;
         };
@@ -461,6 +463,9 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
 #define RT_GEMM2_KERNEL(FN, P, MG, NB)                                                        \
     extern "C" __global__ void __launch_bounds__(256) k_gemm2_##FN##_mg##MG(Gemm2Args a) {    \
         gemm2_body<P, MG, NB>(a);                                                              \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(512) k_gemm2_##FN##_mg##MG##_w8(Gemm2Args a) { \
+        gemm2_body<P, MG, NB, 8>(a);                                                           \
     }
 // NB: blocks per stage (Q8_0 / Q4_0: 8 records, or 4 for large batches so
 // that the stage's operands leave room for 2+ workgroups per CU; Q4_K: one
