@@ -476,6 +476,9 @@ def gemv_specs(ctx, suite):
                 specs.append((f"c5q_gemm_{fmt}_m{m}_18944x3584",
                               (lambda m=m, fmt=fmt: Workload(ctx, "c5q", fmt, "gemm", 18944, 3584,
                                                              m=m, seed=20))))
+        for m in (4, 16, 32):  # the Q4_K_M mix's Q6_K down projection, batched
+            specs.append((f"c5q_gemm_q6k_m{m}_3584x18944",
+                          (lambda m=m: Workload(ctx, "c5q", "q6k", "gemm", 3584, 18944, m=m, seed=21))))
         for m in (1, 4, 8, 16, 32):
             specs.append((f"c5_gemm_q8_0_m{m}_18944x3584",
                           (lambda m=m: Workload(ctx, "c5", "q8_0", "gemm", 18944, 3584, m=m, seed=11))))

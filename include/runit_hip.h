@@ -319,6 +319,25 @@ int rt_gemm_q4_0_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, 
                      uint32_t n, uint32_t k);
 int rt_gemm_q4k_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
                     uint32_t n, uint32_t k);
+/* New: the same batched GEMM on the remaining block formats of Q4_K_M /
+ * Q5_K_M files and on the ggml layouts: Q5_0 (reference: CPU dequant,
+ * forward.rs:900-920), Q5_K (forward.rs:979-1012), Q6_K (forward.rs:921-950;
+ * k a multiple of 512 for the staged kernel), and the ggml-layout families
+ * (rt_gemv_*g).  K-quants need k a multiple of 256. */
+int rt_gemm_q5_0_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k);
+int rt_gemm_q5k_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
+                    uint32_t n, uint32_t k);
+int rt_gemm_q6k_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
+                    uint32_t n, uint32_t k);
+int rt_gemm_q4_0g_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
+                      uint32_t n, uint32_t k);
+int rt_gemm_q4kg_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k);
+int rt_gemm_q5kg_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k);
+int rt_gemm_q6kg_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k);
 
 /* ───────────────────────── argmax ───────────────────────── */
 

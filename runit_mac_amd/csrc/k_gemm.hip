@@ -264,7 +264,7 @@ struct GemmQ8_0 {  // gemv_q8_0.metal:11-17
     static constexpr uint32_t BLK_BYTES = 34, RECS = 1;
     static constexpr bool HAS_MIN = false;
     RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
-                              float& mn) {
+                              float& mn, float&) {
         const uint32_t o = r * 34 + 2 + 8 * c;  // (row is 4-byte aligned)
         const uint32_t* pw = (const uint32_t*)(row + (o & ~3u));
         const uint32_t sh = o & 3;
@@ -279,7 +279,7 @@ struct GemmQ4_0 {  // reference layout: byte i = elements 2i (low), 2i+1 (high)
     static constexpr uint32_t BLK_BYTES = 18, RECS = 1;
     static constexpr bool HAS_MIN = false;
     RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
-                              float& mn) {
+                              float& mn, float&) {
         const uint32_t off = r * 18 + 2 + 4 * c;  // bytes 4c..4c+3 of the quants
         const uint32_t* pw = (const uint32_t*)(row + (off & ~3u));
         const uint32_t w = alignb(pw[(off & 3) ? 1 : 0], pw[0], off & 3);
@@ -294,12 +294,15 @@ struct GemmQ4_0 {  // reference layout: byte i = elements 2i (low), 2i+1 (high)
         mn = 0.0f;
     }
 };
-struct GemmQ4K {  // reference layout: record 2j (low nibbles of qs[32j..]) uses
-                  // sub-block j, record 2j+1 (high nibbles) sub-block j + 4
+// Q4_K: record 2j = low nibbles of qs[32j..32j+31], record 2j+1 = high
+// nibbles; reference layout: sub-blocks j and j + 4 (dequant.metal:77-95);
+// ggml layout (G): sub-blocks 2j and 2j + 1.
+template <bool G>
+struct GemmQ4KT {
     static constexpr uint32_t BLK_BYTES = 144, RECS = 8;
     static constexpr bool HAS_MIN = true;
     RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
-                              float& mn) {
+                              float& mn, float&) {
         const uint8_t* blk = row + (r / 8) * 144;
         const uint32_t rec = r % 8, j = rec / 2, hi = rec & 1;
         const uint2 q = *(const uint2*)(blk + 16 + 32 * j + 8 * c);
@@ -308,10 +311,148 @@ struct GemmQ4K {  // reference layout: record 2j (low nibbles of qs[32j..]) uses
         B = (i64_t)(((uint64_t)q1 << 32) | q0);
         const u32x4 hdr = *(const u32x4*)blk;
         uint32_t sc, m;
-        kq_scale_min(hi ? j + 4 : j, hdr.y, hdr.z, hdr.w, sc, m);
+        kq_scale_min(G ? 2 * j + hi : (hi ? j + 4 : j), hdr.y, hdr.z, hdr.w, sc, m);
         dsc = h2f(hdr.x) * (float)sc;
         mn = h2f(hdr.x >> 16) * (float)m;
     }
+};
+using GemmQ4K = GemmQ4KT<false>;
+using GemmQ4KG = GemmQ4KT<true>;
+
+// Eight consecutive bytes at any 2-byte-aligned offset o of a 4-byte-aligned
+// row (three aligned dwords and alignbyte).
+RT_DEV void gemm_bytes8(const uint8_t* row, uint32_t o, uint32_t& q0, uint32_t& q1) {
+    const uint32_t* pw = (const uint32_t*)(row + (o & ~3u));
+    const uint32_t sh = o & 3;
+    const uint32_t w0 = pw[0], w1 = pw[1], w2 = pw[sh ? 2 : 1];
+    q0 = alignb(w1, w0, sh);
+    q1 = alignb(w2, w1, sh);
+}
+
+// Q4_0, ggml layout: element j < 16 = qs[j] & 15, 16 + j = qs[j] >> 4 (d·(q − 8)).
+struct GemmQ4_0G {
+    static constexpr uint32_t BLK_BYTES = 18, RECS = 1;
+    static constexpr bool HAS_MIN = false;
+    RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
+                              float& mn, float&) {
+        uint32_t w0, w1;
+        gemm_bytes8(row, r * 18 + 2 + 8 * (c & 1), w0, w1);
+        const uint32_t s = 4 * (c >> 1);
+        const uint32_t q0 = (((w0 >> s) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+        const uint32_t q1 = (((w1 >> s) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+        B = (i64_t)(((uint64_t)q1 << 32) | q0);
+        dsc = h2f(*(const uint16_t*)(row + r * 18));
+        mn = 0.0f;
+    }
+};
+
+// Q5_0 (forward.rs:900-920): element j < 16 = (qs[j] & 15) | (qh bit j) << 4,
+// 16 + j = (qs[j] >> 4) | (qh bit 16 + j) << 4, value d·(q − 16).  Lane group c
+// holds elements 8c..8c+7, whose fifth bits are qh bits 8c..8c+7.
+struct GemmQ5_0 {
+    static constexpr uint32_t BLK_BYTES = 22, RECS = 1;
+    static constexpr bool HAS_MIN = false;
+    RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
+                              float& mn, float&) {
+        uint32_t w0, w1, qh, unused;
+        gemm_bytes8(row, r * 22 + 6 + 8 * (c & 1), w0, w1);
+        gemm_bytes8(row, r * 22 + 2, qh, unused);
+        const uint32_t s = 4 * (c >> 1);
+        const uint32_t hb = (qh >> (8 * c)) & 255u;
+        const uint32_t q0 = ((w0 >> s) & 0x0F0F0F0Fu) | (spread4(hb & 15u) << 4);
+        const uint32_t q1 = ((w1 >> s) & 0x0F0F0F0Fu) | (spread4(hb >> 4) << 4);
+        // q − 16 per byte (q ≤ 31: no carry between bytes)
+        B = (i64_t)(((uint64_t)((q1 + 0x70707070u) ^ 0x80808080u) << 32) |
+                    ((q0 + 0x70707070u) ^ 0x80808080u));
+        dsc = h2f(*(const uint16_t*)(row + r * 22));
+        mn = 0.0f;
+    }
+};
+
+// Q5_K (176 B: d, dmin @0, scales[12] @4, qh[32] @16, qs[128] @48): record
+// 2j = low nibbles of qs[32j..], 2j+1 = high nibbles, v = d·sc·q − dmin·m.
+// Fifth bit of element e = 64j + 32·hi + l: reference layout bit e%8 of
+// qh[e/8] (forward.rs:979-1012), sub-blocks (j, j+4); ggml layout (G) bit
+// 2j + hi of qh[l], sub-blocks (2j, 2j+1).
+template <bool G>
+struct GemmQ5KT {
+    static constexpr uint32_t BLK_BYTES = 176, RECS = 8;
+    static constexpr bool HAS_MIN = true;
+    RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
+                              float& mn, float&) {
+        const uint8_t* blk = row + (r / 8) * 176;
+        const uint32_t rec = r % 8, j = rec / 2, hi = rec & 1;
+        const uint2 q = *(const uint2*)(blk + 48 + 32 * j + 8 * c);
+        const uint32_t n0 = hi ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+        const uint32_t n1 = hi ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+        uint32_t h0, h1;
+        if (G) {
+            const uint2 h = *(const uint2*)(blk + 16 + 8 * c);  // qh[l], l = 8c..8c+7
+            h0 = ((h.x >> (2 * j + hi)) & 0x01010101u) << 4;
+            h1 = ((h.y >> (2 * j + hi)) & 0x01010101u) << 4;
+        } else {
+            const uint32_t hb = blk[16 + 8 * j + 4 * hi + c];  // bits of elements 8c..8c+7
+            h0 = spread4(hb & 15u) << 4;
+            h1 = spread4(hb >> 4) << 4;
+        }
+        B = (i64_t)(((uint64_t)(n1 | h1) << 32) | (n0 | h0));
+        const u32x4 hdr = *(const u32x4*)blk;
+        uint32_t sc, m;
+        kq_scale_min(G ? 2 * j + hi : (hi ? j + 4 : j), hdr.y, hdr.z, hdr.w, sc, m);
+        dsc = h2f(hdr.x) * (float)sc;
+        mn = h2f(hdr.x >> 16) * (float)m;
+    }
+};
+using GemmQ5K = GemmQ5KT<false>;
+using GemmQ5KG = GemmQ5KT<true>;
+
+// Q6_K (210 B: ql[128] @0, qh[64] @128, sc[16] @192, d @208), staged two
+// super-blocks at a time (420 bytes keep 4-byte alignment).  Record r = 4·hs
+// + t of a super-block holds elements 128·hs + 32t + l:
+//   ((ql[64hs + l + 32(t&1)] >> 4(t>>1)) & 15) | (((qh[32hs + l] >> 2t) & 3) << 4)
+// minus 32, times d·sc[8hs + 2t] (reference layout, forward.rs:921-950); the
+// ggml layout (G) scales elements 16..31 of the record by sc[8hs + 2t + 1].
+template <bool G>
+struct GemmQ6KT {
+    static constexpr uint32_t BLK_BYTES = 210, RECS = 8;
+    static constexpr bool HAS_MIN = false;
+    static constexpr bool SPLIT16 = G;
+    RT_DEV static void decode(const uint8_t* row, uint32_t r, uint32_t c, i64_t& B, float& dsc,
+                              float& mn, float& dsc2) {
+        const uint32_t b = r / 8, rec = r % 8, hs = rec / 4, t = rec % 4;
+        const uint32_t o = b * 210;  // block start (2-byte aligned)
+        uint32_t l0, l1, h0, h1;
+        gemm_bytes8(row, o + 64 * hs + 32 * (t & 1) + 8 * c, l0, l1);
+        gemm_bytes8(row, o + 128 + 32 * hs + 8 * c, h0, h1);
+        const uint32_t s = 4 * (t >> 1);
+        const uint32_t q0 = ((l0 >> s) & 0x0F0F0F0Fu) | (((h0 >> (2 * t)) & 0x03030303u) << 4);
+        const uint32_t q1 = ((l1 >> s) & 0x0F0F0F0Fu) | (((h1 >> (2 * t)) & 0x03030303u) << 4);
+        // q − 32 per byte (q ≤ 63: no carry between bytes)
+        B = (i64_t)(((uint64_t)((q1 + 0x60606060u) ^ 0x80808080u) << 32) |
+                    ((q0 + 0x60606060u) ^ 0x80808080u));
+        uint32_t sw, unused;
+        gemm_bytes8(row, o + 192 + 8 * hs + 2 * t, sw, unused);  // sc[8hs + 2t], sc[8hs + 2t + 1]
+        uint32_t dw;
+        gemm_bytes8(row, o + 208, dw, unused);
+        const float d = h2f(dw);
+        dsc = d * (float)(int8_t)(sw & 255u);
+        dsc2 = G ? d * (float)(int8_t)((sw >> 8) & 255u) : dsc;
+        mn = 0.0f;
+    }
+};
+using GemmQ6K = GemmQ6KT<false>;
+using GemmQ6KG = GemmQ6KT<true>;
+
+// Formats whose record carries one scale per 16 elements (ggml Q6_K) set
+// SPLIT16: the record then takes two MFMAs, each with the other half's
+// weights zeroed, scaled by dsc and dsc2.
+template <class P, class = void>
+struct GemmSplit16 {
+    static constexpr bool value = false;
+};
+template <class P>
+struct GemmSplit16<P, decltype((void)P::SPLIT16)> {
+    static constexpr bool value = P::SPLIT16;
 };
 
 template <class P, int MG, int NB, int WAVES = 4>
@@ -320,8 +461,9 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
     constexpr uint32_t T = 64 * WAVES, ROWS = 16 * WAVES;
     constexpr uint32_t NR = NB * P::RECS;                  // records per stage
     constexpr uint32_t SEG = NB * P::BLK_BYTES;            // bytes of a row segment
-    constexpr uint32_t VB = SEG % 16 == 0 ? 16 : 8;        // bytes per W load (alignment)
-    typedef typename std::conditional<VB == 16, u32x4, uint2>::type WV;
+    constexpr uint32_t VB = SEG % 16 == 0 ? 16 : (SEG % 8 == 0 ? 8 : 4);  // bytes per W load
+    typedef typename std::conditional<VB == 16, u32x4,
+                                      typename std::conditional<VB == 8, uint2, uint32_t>::type>::type WV;
     constexpr uint32_t WPR = SEG / VB;                     // W loads per row segment
     constexpr uint32_t WV_N = ROWS * WPR;               // W loads per stage
     constexpr uint32_t AV4 = NR * MG * 64 * 8 / 16;        // dwordx4 of A per stage
@@ -392,21 +534,27 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
 #pragma unroll 2
             for (uint32_t r = 0; r < NR; ++r) {
                 i64_t B;
-                float dsc, mn;
-                P::decode(wb, r, c, B, dsc, mn);
+                float dsc, mn, dsc2 = 0.0f;
+                P::decode(wb, r, c, B, dsc, mn, dsc2);
                 // all of the record's matrix-core products first, then their
                 // epilogues (independent MFMAs overlap in the pipeline)
-                v4i C[MG];
+                v4i C[MG], C2[GemmSplit16<P>::value ? MG : 1];
+                const i64_t Blo = (GemmSplit16<P>::value && c >= 2) ? 0 : B;  // elements 0..15
 #pragma unroll
                 for (int g = 0; g < MG; ++g) {
                     const uint2 av = ab[(r * MG + g) * 64 + lane];
                     const i64_t A = (i64_t)(((uint64_t)av.y << 32) | av.x);
-                    C[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    C[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, Blo, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    if (GemmSplit16<P>::value)
+                        C2[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, c >= 2 ? B : 0, v4i{0, 0, 0, 0},
+                                                                      0, 0, 0);
                 }
 #pragma unroll
                 for (int g = 0; g < MG; ++g) {
                     const uint32_t ei = (r * 4 + c) * MG + g;
-                    float v = __builtin_amdgcn_ldexpf(dsc * comb4(C[g]), eb[ei] - 22);
+                    float t = dsc * comb4(C[g]);
+                    if (GemmSplit16<P>::value) t += dsc2 * comb4(C2[GemmSplit16<P>::value ? g : 0]);
+                    float v = __builtin_amdgcn_ldexpf(t, eb[ei] - 22);
                     if (P::HAS_MIN) v -= mn * sb[ei];
                     acc[g] += v;
                 }
@@ -460,10 +608,12 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
         __syncthreads();
     }
 }
-#define RT_GEMM2_KERNEL(FN, P, MG, NB)                                                        \
+#define RT_GEMM2_KERNEL4(FN, P, MG, NB)                                                       \
     extern "C" __global__ void __launch_bounds__(256) k_gemm2_##FN##_mg##MG(Gemm2Args a) {    \
         gemm2_body<P, MG, NB>(a);                                                              \
-    }                                                                                          \
+    }
+#define RT_GEMM2_KERNEL(FN, P, MG, NB)                                                        \
+    RT_GEMM2_KERNEL4(FN, P, MG, NB)                                                            \
     extern "C" __global__ void __launch_bounds__(512) k_gemm2_##FN##_mg##MG##_w8(Gemm2Args a) { \
         gemm2_body<P, MG, NB, 8>(a);                                                           \
     }
@@ -482,3 +632,31 @@ RT_GEMM2_KERNEL(q4k, GemmQ4K, 1, 1)
 RT_GEMM2_KERNEL(q4k, GemmQ4K, 2, 1)
 RT_GEMM2_KERNEL(q4k, GemmQ4K, 4, 1)
 RT_GEMM2_KERNEL(q4k, GemmQ4K, 8, 1)
+RT_GEMM2_KERNEL(q4kg, GemmQ4KG, 1, 1)
+RT_GEMM2_KERNEL(q4kg, GemmQ4KG, 2, 1)
+RT_GEMM2_KERNEL(q4kg, GemmQ4KG, 4, 1)
+RT_GEMM2_KERNEL(q4kg, GemmQ4KG, 8, 1)
+RT_GEMM2_KERNEL(q4_0g, GemmQ4_0G, 1, 8)
+RT_GEMM2_KERNEL(q4_0g, GemmQ4_0G, 2, 8)
+RT_GEMM2_KERNEL(q4_0g, GemmQ4_0G, 4, 4)
+RT_GEMM2_KERNEL(q4_0g, GemmQ4_0G, 8, 4)
+RT_GEMM2_KERNEL(q5_0, GemmQ5_0, 1, 8)
+RT_GEMM2_KERNEL(q5_0, GemmQ5_0, 2, 8)
+RT_GEMM2_KERNEL(q5_0, GemmQ5_0, 4, 4)
+RT_GEMM2_KERNEL(q5_0, GemmQ5_0, 8, 4)
+RT_GEMM2_KERNEL(q5k, GemmQ5K, 1, 1)
+RT_GEMM2_KERNEL(q5k, GemmQ5K, 2, 1)
+RT_GEMM2_KERNEL(q5k, GemmQ5K, 4, 1)
+RT_GEMM2_KERNEL(q5k, GemmQ5K, 8, 1)
+RT_GEMM2_KERNEL(q5kg, GemmQ5KG, 1, 1)
+RT_GEMM2_KERNEL(q5kg, GemmQ5KG, 2, 1)
+RT_GEMM2_KERNEL(q5kg, GemmQ5KG, 4, 1)
+RT_GEMM2_KERNEL(q5kg, GemmQ5KG, 8, 1)
+// Q6_K: two super-blocks per stage; at most 4 activation-row groups (the
+// stage's 16 records of operands) and 4-wave workgroups (LDS)
+RT_GEMM2_KERNEL4(q6k, GemmQ6K, 1, 2)
+RT_GEMM2_KERNEL4(q6k, GemmQ6K, 2, 2)
+RT_GEMM2_KERNEL4(q6k, GemmQ6K, 4, 2)
+RT_GEMM2_KERNEL4(q6kg, GemmQ6KG, 1, 2)
+RT_GEMM2_KERNEL4(q6kg, GemmQ6KG, 2, 2)
+RT_GEMM2_KERNEL4(q6kg, GemmQ6KG, 4, 2)

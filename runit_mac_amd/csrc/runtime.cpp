@@ -136,6 +136,13 @@ const char* const kKernelNames[] = {
     "k_gemm2_q8_0_mg1_w8", "k_gemm2_q8_0_mg2_w8", "k_gemm2_q8_0_mg4_w8", "k_gemm2_q8_0_mg8_w8",
     "k_gemm2_q4_0_mg1_w8", "k_gemm2_q4_0_mg2_w8", "k_gemm2_q4_0_mg4_w8", "k_gemm2_q4_0_mg8_w8",
     "k_gemm2_q4k_mg1_w8", "k_gemm2_q4k_mg2_w8", "k_gemm2_q4k_mg4_w8", "k_gemm2_q4k_mg8_w8",
+    "k_gemm2_q4kg_mg1", "k_gemm2_q4kg_mg2", "k_gemm2_q4kg_mg4", "k_gemm2_q4kg_mg8", "k_gemm2_q4kg_mg1_w8", "k_gemm2_q4kg_mg2_w8", "k_gemm2_q4kg_mg4_w8", "k_gemm2_q4kg_mg8_w8",
+    "k_gemm2_q4_0g_mg1", "k_gemm2_q4_0g_mg2", "k_gemm2_q4_0g_mg4", "k_gemm2_q4_0g_mg8", "k_gemm2_q4_0g_mg1_w8", "k_gemm2_q4_0g_mg2_w8", "k_gemm2_q4_0g_mg4_w8", "k_gemm2_q4_0g_mg8_w8",
+    "k_gemm2_q5_0_mg1", "k_gemm2_q5_0_mg2", "k_gemm2_q5_0_mg4", "k_gemm2_q5_0_mg8", "k_gemm2_q5_0_mg1_w8", "k_gemm2_q5_0_mg2_w8", "k_gemm2_q5_0_mg4_w8", "k_gemm2_q5_0_mg8_w8",
+    "k_gemm2_q5k_mg1", "k_gemm2_q5k_mg2", "k_gemm2_q5k_mg4", "k_gemm2_q5k_mg8", "k_gemm2_q5k_mg1_w8", "k_gemm2_q5k_mg2_w8", "k_gemm2_q5k_mg4_w8", "k_gemm2_q5k_mg8_w8",
+    "k_gemm2_q5kg_mg1", "k_gemm2_q5kg_mg2", "k_gemm2_q5kg_mg4", "k_gemm2_q5kg_mg8", "k_gemm2_q5kg_mg1_w8", "k_gemm2_q5kg_mg2_w8", "k_gemm2_q5kg_mg4_w8", "k_gemm2_q5kg_mg8_w8",
+    "k_gemm2_q6k_mg1", "k_gemm2_q6k_mg2", "k_gemm2_q6k_mg4",
+    "k_gemm2_q6kg_mg1", "k_gemm2_q6kg_mg2", "k_gemm2_q6kg_mg4",
 };
 
 // Kernels of the LDS-streamed GEMV body: <base>_ls<NI>, NI = 1..3 global→LDS
@@ -1219,6 +1226,7 @@ struct GemmFmt {
     uint32_t nb_small, nb_large;       // blocks per stage for MG ≤ 2 / MG ≥ 4
     bool has_min;                      // needs per-record activation sums
     int (*gemv)(rt_ctx*, const void*, const float*, float*, uint32_t, uint32_t);
+    uint32_t max_mg = 8;               // activation-row groups per chunk (LDS budget)
 };
 
 int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, float* y,
@@ -1239,13 +1247,13 @@ int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, floa
     // 4·MG activation rows per chunk (MG ∈ {1, 2, 4, 8}); longer batches
     // take several chunks, each streaming W once
     const uint32_t groups = (m_rows + 3) / 4;
-    const uint32_t MG = groups <= 1 ? 1 : groups <= 2 ? 2 : groups <= 4 ? 4 : 8;
+    const uint32_t MG = std::min<uint32_t>(f.max_mg, groups <= 1 ? 1 : groups <= 2 ? 2 : groups <= 4 ? 4 : 8);
     const uint32_t nchunks = (m_rows + 4 * MG - 1) / (4 * MG);
     const uint32_t nrec = k / 32;        // activation records
     const uint32_t nblk = k / f.blk_el;  // weight blocks per row
     const uint64_t row_bytes = (uint64_t)nblk * f.blk_bytes;
     const uint32_t NB = MG <= 2 ? f.nb_small : f.nb_large;
-    const uint32_t seg = NB * f.blk_bytes, vb = seg % 16 == 0 ? 16 : 8;
+    const uint32_t seg = NB * f.blk_bytes, vb = seg % 16 == 0 ? 16 : (seg % 8 == 0 ? 8 : 4);
 
     // Plan.  LDS-staged kernel when every row's stage segments stay
     // vb-aligned: 64-row tiles, K in stages of NB blocks, items (tile, K
@@ -1265,8 +1273,11 @@ int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, floa
     // for the 4-bit formats at 16+ rows, whose activation operands per stage
     // are larger than the weights': the 8 waves share each staged operand
     // stage (Q4_K at M = 32: 90 → 61 µs; Q8_0 runs slower so: 55 → 66 µs).
-    const uint32_t waves =
-        c->gemm_waves ? c->gemm_waves : (MG >= 4 && f.blk_bytes != 34 ? 8 : 4);
+    // (Q6_K: 4-wave workgroups only, its two-super-block stages fill LDS)
+    const bool w8ok = f.blk_bytes != 210;
+    const uint32_t waves = (c->gemm_waves && (c->gemm_waves == 4 || w8ok))
+                               ? c->gemm_waves
+                               : (MG >= 4 && f.blk_bytes != 34 && w8ok ? 8 : 4);
     char kn2[48];
     if (waves == 8)
         snprintf(kn2, sizeof kn2, "k_gemm2_%s_mg%u_w8", f.name, MG);
@@ -1334,6 +1345,13 @@ int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, floa
 constexpr GemmFmt kGemmQ8_0{"q8_0", 32, 34, 1, 8, 4, false, rt_gemv_q8_0_f32in_f32out};
 constexpr GemmFmt kGemmQ4_0{"q4_0", 32, 18, 1, 8, 4, false, rt_gemv_q4_0_f32in_f32out};
 constexpr GemmFmt kGemmQ4K{"q4k", 256, 144, 8, 1, 1, true, rt_gemv_q4k_f32in_f32out};
+constexpr GemmFmt kGemmQ5_0{"q5_0", 32, 22, 1, 8, 4, false, rt_gemv_q5_0_f32in_f32out};
+constexpr GemmFmt kGemmQ5K{"q5k", 256, 176, 8, 1, 1, true, rt_gemv_q5k_f32in_f32out};
+constexpr GemmFmt kGemmQ6K{"q6k", 256, 210, 8, 2, 2, false, rt_gemv_q6k_f32in_f32out, 4};
+constexpr GemmFmt kGemmQ4_0G{"q4_0g", 32, 18, 1, 8, 4, false, rt_gemv_q4_0g_f32in_f32out};
+constexpr GemmFmt kGemmQ4KG{"q4kg", 256, 144, 8, 1, 1, true, rt_gemv_q4kg_f32in_f32out};
+constexpr GemmFmt kGemmQ5KG{"q5kg", 256, 176, 8, 1, 1, true, rt_gemv_q5kg_f32in_f32out};
+constexpr GemmFmt kGemmQ6KG{"q6kg", 256, 210, 8, 2, 2, false, rt_gemv_q6kg_f32in_f32out, 4};
 
 int rt_gemm_q8_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
                      uint32_t n, uint32_t k) {
@@ -1346,6 +1364,34 @@ int rt_gemm_q4_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_
 int rt_gemm_q4k_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
                     uint32_t n, uint32_t k) {
     return gemm_launch(c, kGemmQ4K, w, x, y, m_rows, n, k);
+}
+int rt_gemm_q5_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ5_0, w, x, y, m_rows, n, k);
+}
+int rt_gemm_q5k_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                    uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ5K, w, x, y, m_rows, n, k);
+}
+int rt_gemm_q6k_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                    uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ6K, w, x, y, m_rows, n, k);
+}
+int rt_gemm_q4_0g_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                      uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ4_0G, w, x, y, m_rows, n, k);
+}
+int rt_gemm_q4kg_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ4KG, w, x, y, m_rows, n, k);
+}
+int rt_gemm_q5kg_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ5KG, w, x, y, m_rows, n, k);
+}
+int rt_gemm_q6kg_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
+                     uint32_t n, uint32_t k) {
+    return gemm_launch(c, kGemmQ6KG, w, x, y, m_rows, n, k);
 }
 
 // ───────────────────────────── dequant ─────────────────────────────

@@ -113,7 +113,9 @@ _SIGS = {
         "rt_dequant_q6k_f32", "rt_dequant_q4k_f16", "rt_dequant_q5_0_f32", "rt_dequant_q5k_f32",
         "rt_dequant_q4_0g_f32", "rt_dequant_q4kg_f32", "rt_dequant_q5kg_f32", "rt_dequant_q6kg_f32", "rt_argmax_f32", "rt_argmax_f16")},
     **{n: [_P, _P, _P, _P, _U32, _U32, _U32] for n in (
-        "rt_gemm_q8_0_f32", "rt_gemm_q4_0_f32", "rt_gemm_q4k_f32")},
+        "rt_gemm_q8_0_f32", "rt_gemm_q4_0_f32", "rt_gemm_q4k_f32", "rt_gemm_q5_0_f32",
+        "rt_gemm_q5k_f32", "rt_gemm_q6k_f32", "rt_gemm_q4_0g_f32", "rt_gemm_q4kg_f32",
+        "rt_gemm_q5kg_f32", "rt_gemm_q6kg_f32")},
     "rt_rms_norm_f32_f32_f32g": [_P, _P, _P, _P, _F, _U32, _U32],
     "rt_fused_rope_qk_f32": [_P, _P, _P, _U32, _U32, _U32, _U32, _F],
     "rt_kv_copy_to_cache_f32": [_P, _P, _P, _U32, _U32, _U32, _U32],
@@ -501,6 +503,23 @@ def gemm_q4_0_f32(ctx, weight, x, y, m_rows, n, k):
 def gemm_q4k_f32(ctx, weight, x, y, m_rows, n, k):
     """Batched GEMM on reference-layout Q4_K weights (new)."""
     _call(ctx, "rt_gemm_q4k_f32", _ptr(weight), _ptr(x), _ptr(y), m_rows, n, k)
+
+
+def _gemm_fn(fmt, doc):
+    def fn(ctx, weight, x, y, m_rows, n, k):
+        _call(ctx, f"rt_gemm_{fmt}_f32", _ptr(weight), _ptr(x), _ptr(y), m_rows, n, k)
+    fn.__name__ = f"gemm_{fmt}_f32"
+    fn.__doc__ = doc
+    return fn
+
+
+gemm_q5_0_f32 = _gemm_fn("q5_0", "Batched GEMM on Q5_0 weights (new).")
+gemm_q5k_f32 = _gemm_fn("q5k", "Batched GEMM on reference-layout Q5_K weights (new).")
+gemm_q6k_f32 = _gemm_fn("q6k", "Batched GEMM on reference-layout Q6_K weights (new).")
+gemm_q4_0g_f32 = _gemm_fn("q4_0g", "Batched GEMM on ggml-layout Q4_0 weights (new).")
+gemm_q4kg_f32 = _gemm_fn("q4kg", "Batched GEMM on ggml-layout Q4_K weights (new).")
+gemm_q5kg_f32 = _gemm_fn("q5kg", "Batched GEMM on ggml-layout Q5_K weights (new).")
+gemm_q6kg_f32 = _gemm_fn("q6kg", "Batched GEMM on ggml-layout Q6_K weights (new).")
 
 
 def argmax_f32(ctx, input, result, n):

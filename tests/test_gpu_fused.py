@@ -200,3 +200,41 @@ def test_gemm_q8_0_direct_kernel_matches_staged(ctx):
         check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), "gemm direct")
     finally:
         c2.close()
+
+
+GEMM_MORE = ["q5_0", "q5k", "q6k", "q4_0g", "q4kg", "q5kg", "q6kg"]
+
+
+@pytest.mark.parametrize("fmt", GEMM_MORE)
+@pytest.mark.parametrize("m", [2, 5, 16, 32, 37])
+@pytest.mark.parametrize("n,k", [(512, 1024), (130, 3584), (70, 8192)])
+def test_gemm_more_formats(ctx, fmt, m, n, k):
+    """Batched GEMM on the Q5_0 / Q5_K / Q6_K and ggml-layout weights: every
+    output row within the GEMV bound of the per-row oracle; a second, smaller
+    batch reuses the workspace."""
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=m + n + 11)
+    x = np.random.default_rng(m + 3).standard_normal((m, k)).astype(np.float32)
+    y = ctx.new_buffer(4 * m * n)
+    getattr(d, f"gemm_{fmt}_f32")(ctx, wbuf, ctx.buffer_from(x), y, m, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm {fmt} m={m}")
+    if m > 2:
+        y2 = ctx.new_buffer(4 * 2 * n)
+        getattr(d, f"gemm_{fmt}_f32")(ctx, wbuf, ctx.buffer_from(x[:2]), y2, 2, n, k)
+        ctx.flush()
+        check_close(y2.read(np.float32, 2 * n), yref[:2].ravel(), sabs[:2].ravel(),
+                    f"gemm {fmt} m=2 after m={m}")
+
+
+@pytest.mark.parametrize("fmt", ["q6k", "q6kg"])
+def test_gemm_q6k_odd_block_count_falls_back_to_gemvs(ctx, fmt):
+    # k = 3840: 15 super-blocks per row, not a whole number of two-block stages
+    n, k, m = 66, 3840, 6
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=21)
+    x = np.random.default_rng(22).standard_normal((m, k)).astype(np.float32)
+    y = ctx.new_buffer(4 * m * n)
+    getattr(d, f"gemm_{fmt}_f32")(ctx, wbuf, ctx.buffer_from(x), y, m, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm {fmt} fallback")
