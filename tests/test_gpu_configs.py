@@ -94,3 +94,34 @@ def test_config5_gemm_q8_0_7b(ctx, m):
         ctx.flush()
         yref, sabs = ora.gemv("q8_0", raw, x, n, k)
         check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("fmt", ["q4kg", "q5k", "q5_0"])
+def test_7b_ffn_other_formats(ctx, fmt):
+    # the 7B gate+up+SiLU in the ggml Q4_K layout (upstream Q4_K_M files) and
+    # the Q5 formats (Q5_K_M / Q5_0 files): the LDS-streamed body at full size
+    ff, h = 18944, 3584
+    wg, rg = device_weights(ctx, fmt, ff, h, 81)
+    wu, ru = device_weights(ctx, fmt, ff, h, 82)
+    xb, x = device_normal(ctx, h, 83)
+    act = ctx.new_buffer(4 * ff)
+    getattr(d, f"fused_ffn_{fmt}_f32")(ctx, wg, wu, xb, act, ff, h)
+    ctx.flush()
+    g, gs = ora.gemv(fmt, rg, x, ff, h)
+    u, us = ora.gemv(fmt, ru, x, ff, h)
+    ffn_check(act.read(np.float32, ff), g, gs, u, us, f"7B {fmt} ffn")
+
+
+@pytest.mark.parametrize("fmt", ["q6kg", "q5k", "q4kg"])
+def test_7b_down_other_formats(ctx, fmt):
+    # down 3584×18944 (+ residual, aliased as in forward.rs:1702): K split
+    # into chunks whose partial sums meet through memory
+    n, k = 3584, 18944
+    wbuf, raw = device_weights(ctx, fmt, n, k, 91)
+    xb, x = device_normal(ctx, k, 92)
+    res = np.random.default_rng(93).standard_normal(n).astype(np.float32)
+    yr = ctx.buffer_from(res)
+    getattr(d, f"gemv_{fmt}_add_f32_f32in")(ctx, wbuf, xb, yr, yr, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    check_close(yr.read(np.float32, n), yref + res, sabs, f"7B {fmt} down")
