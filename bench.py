@@ -289,6 +289,78 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
             "launches_reference": 1 + 10 * cfg.layers + 3}
 
 
+def bench_q4km_step(ctx, steps: int, warmup: int) -> dict:
+    """Config 4: every GEMV of one Qwen2.5-7B-shape token in a Q4_K_M-style
+    mix — 28 layers of Q, K, O, gate+up (Q4_K) and V, down (Q6_K), the
+    output and down projections adding into the residual — plus the
+    152064×3584 Q6_K LM head, captured as one graph (169 launches) and
+    replayed; random-init weights of that shape, one activation vector."""
+    h, ff, kv, vocab, layers = 3584, 18944, 512, 152064, 28
+    sizes = {"q": d.weight_bytes("q4k", h, h), "k": d.weight_bytes("q4k", kv, h),
+             "v": d.weight_bytes("q6k", kv, h), "o": d.weight_bytes("q4k", h, h),
+             "g": d.weight_bytes("q4k", ff, h), "u": d.weight_bytes("q4k", ff, h),
+             "d": d.weight_bytes("q6k", h, ff)}
+    fmts = {"q": "q4k", "k": "q4k", "v": "q6k", "o": "q4k", "g": "q4k", "u": "q4k", "d": "q6k"}
+    shapes = {"q": (h, h), "k": (kv, h), "v": (kv, h), "o": (h, h), "g": (ff, h), "u": (ff, h),
+              "d": (h, ff)}
+    lm_bytes = d.weight_bytes("q6k", vocab, h)
+    total_w = layers * sum(sizes.values()) + lm_bytes
+    arena = Arena(ctx, total_w + 4096 * (layers * len(sizes) + 1))
+    L = []
+    for i in range(layers):
+        mats = {}
+        for key, nb in sizes.items():
+            b = arena.take(nb)
+            n, k = shapes[key]
+            el, _ = d.BLOCK[fmts[key]]
+            d.synth_weights(ctx, fmts[key], b, n * k // el, 4000 + 16 * i + len(mats))
+            mats[key] = b
+        L.append(mats)
+    lm = arena.take(lm_bytes)
+    d.synth_weights(ctx, "q6k", lm, vocab * h // 256, 4999)
+    x = ctx.new_buffer(4 * ff)
+    d.synth_normal_f32(ctx, x, ff, 77)
+    q, kb, vb = ctx.new_buffer(4 * h), ctx.new_buffer(4 * kv), ctx.new_buffer(4 * kv)
+    hres, act, logits = ctx.new_buffer(4 * h), ctx.new_buffer(4 * ff), ctx.new_buffer(4 * vocab)
+    d.synth_normal_f32(ctx, hres, h, 78)
+    ctx.flush()
+
+    def sequence():
+        for m in L:
+            d.gemv_q4k_f32in_f32out(ctx, m["q"], x, q, h, h)
+            d.gemv_q4k_f32in_f32out(ctx, m["k"], x, kb, kv, h)
+            d.gemv_q6k_f32in_f32out(ctx, m["v"], x, vb, kv, h)
+            d.gemv_q4k_add_f32_f32in(ctx, m["o"], x, hres, hres, h, h)
+            d.fused_ffn_q4k_f32(ctx, m["g"], m["u"], x, act, ff, h)
+            d.gemv_q6k_add_f32_f32in(ctx, m["d"], x, hres, hres, h, ff)
+        d.gemv_q6k_f32in_f32out(ctx, lm, x, logits, vocab, h)
+
+    sequence()  # eager first pass: sizes the context workspace before capture
+    ctx.flush()
+    ctx.capture_begin()
+    sequence()
+    g = ctx.capture_end()
+    for _ in range(max(1, warmup)):
+        g.launch()
+    ctx.flush()
+    e0, e1 = ctx.event(), ctx.event()
+    reps = max(5, steps // 5)
+    e0.record()
+    for _ in range(reps):
+        g.launch()
+    e1.record()
+    us = e0.elapsed_ms(e1) * 1e3 / reps
+    del g
+    # algorithmic bytes: every weight once, plus the activation reads and
+    # output writes (residual read and write for O and down)
+    act_bytes = layers * (4 * h * 5 + 4 * ff + 4 * (h + kv + kv + 2 * h + ff + 2 * h)) + 4 * h + 4 * vocab
+    step_bytes = total_w + act_bytes
+    for b in (x, q, kb, vb, hres, act, logits):
+        b.free()
+    arena.free()
+    return {"us": us, "bytes": step_bytes, "weight_bytes": total_w, "launches": 6 * layers + 1}
+
+
 def measured_traffic(summary: str):
     """HBM bytes per launch of a kernel, from its committed rocprofv3 --pmc
     summary (FETCH_SIZE and WRITE_SIZE, each scaled by a copy kernel's
@@ -419,6 +491,16 @@ def main():
                        "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / dec["step_bytes"], 0)},
         })
 
+    if args.suite in ("all", "gemv") and not args.only:
+        q4 = bench_q4km_step(ctx, args.steps, args.warmup)
+        gbs = q4["bytes"] / (q4["us"] * 1e-6) / 1e9
+        log(f"config 4 (7B Q4_K_M mix, all 28 layers' GEMVs + Q6_K LM head, {q4['launches']} "
+            f"launches): {q4['us']:.1f} us per token = {1e6 / q4['us']:.1f} tok/s of GEMVs; "
+            f"{q4['bytes'] / 1e9:.3f} GB → {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM)")
+        line["q4k_m_7b_gemv_step"] = {
+            "us_per_token": round(q4["us"], 1), "tok_s_gemv_only": round(1e6 / q4["us"], 1),
+            "bytes": q4["bytes"], "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "launches": q4["launches"]}
     specs = [] if args.suite == "decode" else gemv_specs(ctx, args.suite)
     if args.only:
         specs = [sp for sp in specs if args.only in sp[0]]
