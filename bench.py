@@ -135,21 +135,25 @@ class Workload:
 
 
 class QKVWorkload(Workload):
-    def __init__(self, ctx, name, fmt, q_dim, kv_dim, k, seed=1):
+    """Fused Q/K/V (+f16 bias) launches; fmt_v: V in another format (Q4_K_M)."""
+
+    def __init__(self, ctx, name, fmt, q_dim, kv_dim, k, seed=1, fmt_v=None):
         self.q_dim, self.kv_dim = q_dim, kv_dim
         self.ctx, self.name, self.fmt, self.kind, self.k, self.m = ctx, name, fmt, "qkv", k, 1
+        self.fmt_v = fmt_v or fmt
         self.n = q_dim + 2 * kv_dim
-        el, _ = d.BLOCK[fmt]
         dims = (q_dim, kv_dim, kv_dim)
-        self.wbytes_per_launch = sum(d.weight_bytes(fmt, n, k) for n in dims)
+        fmts = (fmt, fmt, self.fmt_v)
+        sizes = [d.weight_bytes(f, n, k) for f, n in zip(fmts, dims)]
+        self.wbytes_per_launch = sum(sizes)
         self.reps = max(2, min(512, -(-WORKSET_BYTES // self.wbytes_per_launch)))
-        self.arena = _arena_for(ctx, [d.weight_bytes(fmt, n, k) for n in dims], self.reps)
+        self.arena = _arena_for(ctx, sizes, self.reps)
         self.w = []
         for r in range(self.reps):
             mats = []
-            for j, n in enumerate(dims):
-                b = self.arena.take(d.weight_bytes(fmt, n, k))
-                d.synth_weights(ctx, fmt, b, n * k // el, seed * 1000 + r * 3 + j)
+            for j, (f, n) in enumerate(zip(fmts, dims)):
+                b = self.arena.take(sizes[j])
+                d.synth_weights(ctx, f, b, n * k // d.BLOCK[f][0], seed * 1000 + r * 3 + j)
                 mats.append(b)
             self.w.append(mats)
         self.x = ctx.new_buffer(4 * k)
@@ -159,12 +163,14 @@ class QKVWorkload(Workload):
         for i, (b, n) in enumerate(zip(self.bias, dims)):
             d.synth_normal_f16(ctx, b, n, seed + 20 + i, 0.0, 0.02)
         ctx.flush()
+        fn = (f"fused_qkv_bias_{fmt}_f32" if self.fmt_v == fmt
+              else f"fused_qkv_bias_{fmt}_{self.fmt_v}_f32")
+        self.fn = getattr(d, fn)
 
     def launch(self, r: int):
         w = self.w[r % self.reps]
-        getattr(d, f"fused_qkv_bias_{self.fmt}_f32")(
-            self.ctx, w[0], w[1], w[2], self.x, *self.outs, *self.bias,
-            self.q_dim, self.kv_dim, self.k)
+        self.fn(self.ctx, w[0], w[1], w[2], self.x, *self.outs, *self.bias,
+                self.q_dim, self.kv_dim, self.k)
 
 
 def time_workload(ctx, wl: Workload, steps: int, warmup: int) -> dict:
@@ -293,8 +299,11 @@ def bench_q4km_step(ctx, steps: int, warmup: int) -> dict:
     """Config 4: every GEMV of one Qwen2.5-7B-shape token in a Q4_K_M-style
     mix — 28 layers of Q, K, O, gate+up (Q4_K) and V, down (Q6_K), the
     output and down projections adding into the residual — plus the
-    152064×3584 Q6_K LM head, captured as one graph (169 launches) and
-    replayed; random-init weights of that shape, one activation vector."""
+    152064×3584 Q6_K LM head, captured as one graph and replayed; random-init
+    weights of that shape, one activation vector.  Q, K and V (+ their f16
+    biases, as Qwen2.5 has them) run as one mixed-format launch (113 launches
+    per token); the same step with three separate bias-free GEMVs instead
+    (169 launches) is timed beside it."""
     h, ff, kv, vocab, layers = 3584, 18944, 512, 152064, 28
     sizes = {"q": d.weight_bytes("q4k", h, h), "k": d.weight_bytes("q4k", kv, h),
              "v": d.weight_bytes("q6k", kv, h), "o": d.weight_bytes("q4k", h, h),
@@ -316,6 +325,13 @@ def bench_q4km_step(ctx, steps: int, warmup: int) -> dict:
             d.synth_weights(ctx, fmts[key], b, n * k // el, 4000 + 16 * i + len(mats))
             mats[key] = b
         L.append(mats)
+    bias_bytes = 2 * (h + 2 * kv)
+    biases = []
+    for i in range(layers):
+        bq, bk, bv = ctx.new_buffer(2 * h), ctx.new_buffer(2 * kv), ctx.new_buffer(2 * kv)
+        for j, (bb, n) in enumerate(((bq, h), (bk, kv), (bv, kv))):
+            d.synth_normal_f16(ctx, bb, n, 5000 + 3 * i + j, 0.0, 0.02)
+        biases.append((bq, bk, bv))
     lm = arena.take(lm_bytes)
     d.synth_weights(ctx, "q6k", lm, vocab * h // 256, 4999)
     x = ctx.new_buffer(4 * ff)
@@ -325,40 +341,51 @@ def bench_q4km_step(ctx, steps: int, warmup: int) -> dict:
     d.synth_normal_f32(ctx, hres, h, 78)
     ctx.flush()
 
-    def sequence():
-        for m in L:
-            d.gemv_q4k_f32in_f32out(ctx, m["q"], x, q, h, h)
-            d.gemv_q4k_f32in_f32out(ctx, m["k"], x, kb, kv, h)
-            d.gemv_q6k_f32in_f32out(ctx, m["v"], x, vb, kv, h)
+    def sequence(fused_qkv: bool):
+        for m, (bq, bk, bv) in zip(L, biases):
+            if fused_qkv:
+                d.fused_qkv_bias_q4k_q6k_f32(ctx, m["q"], m["k"], m["v"], x, q, kb, vb,
+                                             bq, bk, bv, h, kv, h)
+            else:
+                d.gemv_q4k_f32in_f32out(ctx, m["q"], x, q, h, h)
+                d.gemv_q4k_f32in_f32out(ctx, m["k"], x, kb, kv, h)
+                d.gemv_q6k_f32in_f32out(ctx, m["v"], x, vb, kv, h)
             d.gemv_q4k_add_f32_f32in(ctx, m["o"], x, hres, hres, h, h)
             d.fused_ffn_q4k_f32(ctx, m["g"], m["u"], x, act, ff, h)
             d.gemv_q6k_add_f32_f32in(ctx, m["d"], x, hres, hres, h, ff)
         d.gemv_q6k_f32in_f32out(ctx, lm, x, logits, vocab, h)
 
-    sequence()  # eager first pass: sizes the context workspace before capture
-    ctx.flush()
-    ctx.capture_begin()
-    sequence()
-    g = ctx.capture_end()
-    for _ in range(max(1, warmup)):
-        g.launch()
-    ctx.flush()
-    e0, e1 = ctx.event(), ctx.event()
-    reps = max(5, steps // 5)
-    e0.record()
-    for _ in range(reps):
-        g.launch()
-    e1.record()
-    us = e0.elapsed_ms(e1) * 1e3 / reps
-    del g
-    # algorithmic bytes: every weight once, plus the activation reads and
-    # output writes (residual read and write for O and down)
-    act_bytes = layers * (4 * h * 5 + 4 * ff + 4 * (h + kv + kv + 2 * h + ff + 2 * h)) + 4 * h + 4 * vocab
+    def timed(fused_qkv: bool) -> float:
+        sequence(fused_qkv)  # eager first pass: sizes the context workspace before capture
+        ctx.flush()
+        ctx.capture_begin()
+        sequence(fused_qkv)
+        g = ctx.capture_end()
+        for _ in range(max(1, warmup)):
+            g.launch()
+        ctx.flush()
+        e0, e1 = ctx.event(), ctx.event()
+        reps = max(5, steps // 5)
+        e0.record()
+        for _ in range(reps):
+            g.launch()
+        e1.record()
+        us = e0.elapsed_ms(e1) * 1e3 / reps
+        del g
+        return us
+
+    us = timed(True)
+    us_sep = timed(False)
+    # algorithmic bytes: every weight once, plus the activation reads, the
+    # biases and output writes (residual read and write for O and down)
+    act_bytes = layers * (4 * h * 5 + 4 * ff + 4 * (h + kv + kv + 2 * h + ff + 2 * h)
+                          + bias_bytes) + 4 * h + 4 * vocab
     step_bytes = total_w + act_bytes
-    for b in (x, q, kb, vb, hres, act, logits):
+    for b in (x, q, kb, vb, hres, act, logits, *[bb for t in biases for bb in t]):
         b.free()
     arena.free()
-    return {"us": us, "bytes": step_bytes, "weight_bytes": total_w, "launches": 6 * layers + 1}
+    return {"us": us, "us_separate_qkv": us_sep, "bytes": step_bytes, "weight_bytes": total_w,
+            "launches": 4 * layers + 1, "launches_separate_qkv": 6 * layers + 1}
 
 
 def measured_traffic(summary: str):
@@ -435,7 +462,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--suite", default="all", choices=["all", "gemv", "quick", "decode"])
+    ap.add_argument("--suite", default="all", choices=["all", "gemv", "quick", "decode", "step"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run only GEMV workloads whose label contains this")
     ap.add_argument("--profile-pass", action="store_true",
@@ -491,17 +518,20 @@ def main():
                        "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / dec["step_bytes"], 0)},
         })
 
-    if args.suite in ("all", "gemv") and not args.only:
+    if args.suite in ("all", "gemv", "step") and not args.only:
         q4 = bench_q4km_step(ctx, args.steps, args.warmup)
         gbs = q4["bytes"] / (q4["us"] * 1e-6) / 1e9
         log(f"config 4 (7B Q4_K_M mix, all 28 layers' GEMVs + Q6_K LM head, {q4['launches']} "
             f"launches): {q4['us']:.1f} us per token = {1e6 / q4['us']:.1f} tok/s of GEMVs; "
-            f"{q4['bytes'] / 1e9:.3f} GB → {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM)")
+            f"{q4['bytes'] / 1e9:.3f} GB → {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM); "
+            f"with separate bias-free Q/K/V GEMVs ({q4['launches_separate_qkv']} launches): "
+            f"{q4['us_separate_qkv']:.1f} us")
         line["q4k_m_7b_gemv_step"] = {
             "us_per_token": round(q4["us"], 1), "tok_s_gemv_only": round(1e6 / q4["us"], 1),
             "bytes": q4["bytes"], "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "launches": q4["launches"]}
-    specs = [] if args.suite == "decode" else gemv_specs(ctx, args.suite)
+            "launches": q4["launches"],
+            "us_per_token_separate_qkv": round(q4["us_separate_qkv"], 1)}
+    specs = [] if args.suite in ("decode", "step") else gemv_specs(ctx, args.suite)
     if args.only:
         specs = [sp for sp in specs if args.only in sp[0]]
     results = []
@@ -535,6 +565,11 @@ def gemv_specs(ctx, suite):
         ("c3_q4_0_down_3584x18944", lambda: Workload(ctx, "c3_down", "q4_0", "add", 3584, 18944, seed=3)),
         ("c3_q4_0_qkv_4608x3584", lambda: QKVWorkload(ctx, "c3_qkv", "q4_0", 3584, 512, 3584, seed=4)),
         ("c4_q4k_q_3584x3584", lambda: Workload(ctx, "c4_q", "q4k", "gemv", 3584, 3584, seed=5)),
+        ("c4_q4k_k_512x3584", lambda: Workload(ctx, "c4_k", "q4k", "gemv", 512, 3584, seed=21)),
+        ("c4_q6k_v_512x3584", lambda: Workload(ctx, "c4_v", "q6k", "gemv", 512, 3584, seed=22)),
+        ("c4_qkv_bias_q4k_q6k_4608x3584", lambda: QKVWorkload(ctx, "c4_qkv", "q4k", 3584, 512, 3584,
+                                                             seed=24, fmt_v="q6k")),
+        ("c4_q4k_o_add_3584x3584", lambda: Workload(ctx, "c4_o", "q4k", "add", 3584, 3584, seed=23)),
         ("c4_q4k_ffn_2x18944x3584", lambda: Workload(ctx, "c4_ffn", "q4k", "ffn", 18944, 3584, seed=6)),
         ("c4_q6k_down_3584x18944", lambda: Workload(ctx, "c4_down", "q6k", "add", 3584, 18944, seed=7)),
         ("c4_q6k_lmhead_152064x3584", lambda: Workload(ctx, "c4_lm", "q6k", "gemv", 152064, 3584, seed=8)),

@@ -263,6 +263,35 @@ int rt_fused_qkv_bias_q4_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k, co
                                const uint16_t* bias_q, const uint16_t* bias_k,
                                const uint16_t* bias_v, uint32_t q_dim, uint32_t kv_dim,
                                uint32_t k);
+/* New: Q/K/V projections of Q4_K / Q4_K_M files in one launch.  They replace
+ * the reference's fallback sequence for non-Q8_0 projections: three
+ * WeightBuf GEMVs, each followed by add_f16_into_f32 of its bias
+ * (forward.rs:1561-1568).  Arguments follow fused_qkv_bias_q8_0_f32.  The
+ * three bias pointers may all be NULL (no bias); giving only some of them is
+ * an error.
+ *   _q4k      : Q, K and V in Q4_K;
+ *   _q4k_q6k  : Q and K in Q4_K, V in Q6_K (the Q4_K_M mix);
+ *   _q4kg / _q4kg_q6kg : the same in the ggml layouts. */
+int rt_fused_qkv_bias_q4k_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                              const float* x_vec, float* out_q, float* out_k, float* out_v,
+                              const uint16_t* bias_q, const uint16_t* bias_k,
+                              const uint16_t* bias_v, uint32_t q_dim, uint32_t kv_dim,
+                              uint32_t k);
+int rt_fused_qkv_bias_q4k_q6k_f32(rt_ctx* ctx, const void* w_q, const void* w_k,
+                                  const void* w_v, const float* x_vec, float* out_q,
+                                  float* out_k, float* out_v, const uint16_t* bias_q,
+                                  const uint16_t* bias_k, const uint16_t* bias_v, uint32_t q_dim,
+                                  uint32_t kv_dim, uint32_t k);
+int rt_fused_qkv_bias_q4kg_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                               const float* x_vec, float* out_q, float* out_k, float* out_v,
+                               const uint16_t* bias_q, const uint16_t* bias_k,
+                               const uint16_t* bias_v, uint32_t q_dim, uint32_t kv_dim,
+                               uint32_t k);
+int rt_fused_qkv_bias_q4kg_q6kg_f32(rt_ctx* ctx, const void* w_q, const void* w_k,
+                                    const void* w_v, const float* x_vec, float* out_q,
+                                    float* out_k, float* out_v, const uint16_t* bias_q,
+                                    const uint16_t* bias_k, const uint16_t* bias_v,
+                                    uint32_t q_dim, uint32_t kv_dim, uint32_t k);
 /* dispatch.rs:903-921 → fused_ffn.metal:36-93; act = silu(Wg·x)·(Wu·x) */
 int rt_fused_ffn_q8_0_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
                           const float* x_vec, float* act_out, uint32_t ff_dim, uint32_t k);

@@ -42,6 +42,9 @@ struct GemvArgs {
     uint32_t ls_rs;      // LDS-streamed body: LDS bytes between two rows of a slot
     uint32_t ls_res;     // LDS-streamed body: result slots per wave (items)
     uint32_t ls_xcd;     // LDS-streamed body: neighbouring quads to workgroups of one XCD
+    // matrix-core body in a two-part launch: this part owns workgroups
+    // [blk0, blk0 + nblk) (nblk = 0: the whole grid)
+    uint32_t blk0, nblk;
 };
 
 // Tiles one workgroup may own in a K-split launch (the host keeps the grid's
@@ -372,7 +375,8 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     const uint32_t lq = q < 3 ? q : 2;  // the A row of lane q = 3 is a don't-care
     // K chunk of this workgroup (the whole K when ksplit = 1)
     const uint32_t S = a.ksplit;
-    const uint32_t ks = blockIdx.x % S, wg = blockIdx.x / S, nwg = gridDim.x / S;
+    const uint32_t bid = blockIdx.x - a.blk0, gdim = a.nblk ? a.nblk : gridDim.x;
+    const uint32_t ks = bid % S, wg = bid / S, nwg = gdim / S;
     const uint32_t cu0 = ks * a.kc_units;  // first unit of the chunk
     const uint32_t units = min(a.K / F::UNIT_EL - cu0, a.kc_units);
     XRec* xs = (XRec*)smem;  // the chunk's records
@@ -765,6 +769,32 @@ RT_GEMV_KERNEL(k_ffn_q5kg, FmtQ5KG, EPI_FFN, float, 1)
 RT_GEMV_KERNEL2W(k_gemv_q6kg_f32_f32, FmtQ6KGB, FmtQ6KG, EPI_F32, float, 1, RT_Q6K_WPE)
 RT_GEMV_KERNEL2W(k_gemv_q6kg_f32_f32add, FmtQ6KGB, FmtQ6KG, EPI_F32_ADD, float, 1, RT_Q6K_WPE)
 RT_GEMV_KERNEL2W(k_gemv_q6kg_f32_f16, FmtQ6KGB, FmtQ6KG, EPI_F16, float, 1, RT_Q6K_WPE)
+
+// Q, K and V projections whose matrices differ in format (Q4_K_M files keep
+// V in Q6_K) in one launch: workgroups [0, b.blk0) run Q and K (format FA),
+// the rest run V (format FB), each part with its own tiling of the
+// matrix-core body; the reference issues three GEMVs and three bias adds
+// for these (forward.rs:1561-1568).
+template <class FA, class FB, int EPI>
+RT_DEV void gemv_mq_pair(const GemvArgs& a, const GemvArgs& b) {
+    if (blockIdx.x < b.blk0)
+        gemv_mq_body<FA, EPI, float, 1, (fmt_pf<FA>() ? fmt_pf<FA>() : GEMV_PF1)>(a);
+    else
+        gemv_mq_body<FB, EPI, float, 1, (fmt_pf<FB>() ? fmt_pf<FB>() : GEMV_PF1)>(b);
+}
+#define RT_GEMV_PAIR(NAME, FA, FB, EPI)                                                        \
+    extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) NAME##_r1(GemvArgs a, GemvArgs b) { \
+        gemv_mq_pair<FA, FB, EPI>(a, b);                                                       \
+    }
+RT_GEMV_PAIR(k_qkv2_bias_q4k_q6k, FmtQ4K, FmtQ6K, EPI_QKV_BIAS)
+RT_GEMV_PAIR(k_qkv2_q4k_q6k, FmtQ4K, FmtQ6K, EPI_QKV)
+RT_GEMV_PAIR(k_qkv2_bias_q4kg_q6kg, FmtQ4KG, FmtQ6KG, EPI_QKV_BIAS)
+RT_GEMV_PAIR(k_qkv2_q4kg_q6kg, FmtQ4KG, FmtQ6KG, EPI_QKV)
+// all-Q4_K projections (the other layers of Q4_K_M files)
+RT_GEMV_KERNEL(k_qkv_bias_q4k, FmtQ4K, EPI_QKV_BIAS, float, 1)
+RT_GEMV_KERNEL(k_qkv_q4k, FmtQ4K, EPI_QKV, float, 1)
+RT_GEMV_KERNEL(k_qkv_bias_q4kg, FmtQ4KG, EPI_QKV_BIAS, float, 1)
+RT_GEMV_KERNEL(k_qkv_q4kg, FmtQ4KG, EPI_QKV, float, 1)
 
 // Attention output projection with the split merge folded into the staging
 // (decode_attention's merge, then gemv_q8_0_add_f32_f32in: forward.rs:1588-

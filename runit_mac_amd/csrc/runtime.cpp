@@ -48,6 +48,7 @@ struct GemvArgs {
     uint32_t ls_rs;
     uint32_t ls_res;
     uint32_t ls_xcd;
+    uint32_t blk0, nblk;
 };
 
 constexpr uint32_t XREC_BYTES = 112;
@@ -118,6 +119,9 @@ const char* const kKernelNames[] = {
     "k_gemv_q5k_f32_f32add_r1", "k_gemv_q5k_f32_f32add_r2",
     "k_gemv_q5k_f32_f16_r1", "k_gemv_q5k_f32_f16_r2",
     "k_qkv_bias_q5k_r1", "k_qkv_bias_q5k_r2", "k_ffn_q5k_r1", "k_ffn_q5k_r2",
+    "k_qkv_bias_q4k_r1", "k_qkv_bias_q4k_r2", "k_qkv_q4k_r1", "k_qkv_q4k_r2",
+    "k_qkv_bias_q4kg_r1", "k_qkv_bias_q4kg_r2", "k_qkv_q4kg_r1", "k_qkv_q4kg_r2",
+    "k_qkv2_bias_q4k_q6k_r1", "k_qkv2_q4k_q6k_r1", "k_qkv2_bias_q4kg_q6kg_r1", "k_qkv2_q4kg_q6kg_r1",
     "k_argmax_f32", "k_argmax_f16",
     "k_synth_normal_f32", "k_synth_normal_f16", "k_synth_q8_0", "k_synth_q4_0",
     "k_synth_q4k", "k_synth_q6k", "k_synth_q5_0", "k_synth_q5k",
@@ -195,6 +199,10 @@ constexpr Fmt kQ4_0G{32, 18, 64, 2, "Q4_0 (ggml)", &kQ4_0GS};
 constexpr Fmt kQ4KG{256, 144, 64, 1, "Q4_K (ggml)", nullptr};
 constexpr Fmt kQ5KG{256, 176, 64, 1, "Q5_K (ggml)", nullptr};
 constexpr Fmt kQ6KG{256, 210, 64, 1, "Q6_K (ggml)", nullptr, 256};
+// Q6_K on the matrix-core path with 64-element lane units (small launches:
+// four times the lanes of the one-super-block-per-lane form)
+constexpr Fmt kQ6KU{256, 210, 64, 1, "Q6_K", nullptr};
+constexpr Fmt kQ6KGU{256, 210, 64, 1, "Q6_K (ggml)", nullptr};
 
 thread_local std::string g_global_error = "no error";
 
@@ -236,6 +244,7 @@ struct rt_ctx {
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     uint32_t ls_threads = 0;     // RUNIT_GEMV_LS_THREADS: force the block size (sweeps)
     uint32_t ls_xcd = 1;         // RUNIT_GEMV_LS_XCD=0: plain workgroup order (sweeps)
+    uint32_t pair_threads = 0;   // RUNIT_GEMV_PAIR_THREADS: two-part launch block size (sweeps)
     uint32_t gemm_waves = 0;     // RUNIT_GEMM_WAVES=4|8: force the staged GEMM's block (sweeps)
     bool lsk_enabled = true;     // RUNIT_GEMV_LSK=0: K splits over workgroups (through memory) instead
     // Small per-context device buffer: argmax range states + arrival counter
@@ -602,14 +611,15 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         // ~240-register kernels are built for 512 threads.)
         const bool one_item = f.blk_bytes == 34 || mq_el == 256;
         if (!c->plan_override.T && S == 1 && a.K >= 2048 && !one_item && !a.xnsp) p.T = 1024;
-        // split K over the waves of a workgroup while row-quad groups are
-        // scarcer than the resident waves (latency-bound small problems)
+        // split K over the waves of a workgroup while the split waves still
+        // fit in the resident waves (latency-bound small problems; a split
+        // past that leaves a second round of workgroups as a tail)
         const uint32_t nwaves = p.T / 64;
         const uint32_t quads = (a.nvrows + 4 * p.rpl - 1) / (4 * p.rpl);
         const uint32_t nsteps = (kcu + 15) / 16;
         const uint32_t resident_waves = (uint32_t)c->cu_count * 16;
         uint32_t ksw = 1;
-        while (ksw < nwaves && quads * S * ksw < resident_waves && ksw * 2 <= nsteps) ksw *= 2;
+        while (ksw < nwaves && quads * S * ksw * 2 <= resident_waves && ksw * 2 <= nsteps) ksw *= 2;
         if (c->ksw_override) ksw = std::min<uint32_t>(c->ksw_override, nwaves);
         a.ksw = ksw;
         rows_per_wg = (nwaves / ksw) * 4 * p.rpl;
@@ -702,6 +712,119 @@ int qkv_launch(rt_ctx* c, const char* kname, const Fmt& f, const void* wq, const
     return gemv_launch(c, kname, f, a, false);
 }
 
+// One part of a two-part matrix-core launch: whole K, `ksw` waves per row
+// quad group; returns the part's workgroups (every tile in one round: the
+// caller keeps the two parts' waves within the resident capacity).
+uint32_t pair_part_grid(const Fmt& f, GemvArgs& a, uint32_t threads, uint32_t ksw) {
+    if (a.nvrows == 0) return 0;
+    a.ksw = ksw;
+    a.ksplit = 1;
+    a.kc_units = a.K / f.mq_units();
+    a.xb_chunk = a.K / 32;
+    a.lpr = 16;
+    a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
+    const uint32_t rows_per_wg = (threads / 64 / ksw) * 4;
+    return (a.nvrows + rows_per_wg - 1) / rows_per_wg;
+}
+
+// K-split waves of the two parts: the part whose waves stream the most bytes
+// (steps per wave × bytes per 64-element lane unit) doubles its split while
+// the two parts' waves stay within the resident waves of the device.
+void pair_ksw(const Fmt& fa, uint32_t nva, const Fmt& fb, uint32_t nvb, uint32_t K,
+              uint32_t nwaves, uint32_t budget, uint32_t& ka, uint32_t& kb) {
+    const uint32_t qa = (nva + 3) / 4, qb = (nvb + 3) / 4;
+    const uint32_t sa = (K / fa.mq_units() + 15) / 16, sb = (K / fb.mq_units() + 15) / 16;
+    const double ua = (double)fa.blk_bytes * fa.mq_units() / fa.blk_el;
+    const double ub = (double)fb.blk_bytes * fb.mq_units() / fb.blk_el;
+    ka = kb = 1;
+    for (;;) {
+        const double ta = qa ? ua * ((sa + ka - 1) / ka) : 0.0;
+        const double tb = qb ? ub * ((sb + kb - 1) / kb) : 0.0;
+        const bool pick_a = ta >= tb;
+        uint32_t& kk = pick_a ? ka : kb;
+        const uint32_t steps = pick_a ? sa : sb;
+        const uint32_t quads = pick_a ? qa : qb;
+        const uint64_t total = (uint64_t)qa * ka + (uint64_t)qb * kb + (uint64_t)quads * kk;
+        if (kk * 2 > nwaves || kk * 2 > steps || total > budget) break;
+        kk *= 2;
+    }
+}
+
+// Q and K in format fa, V in format fb, in one launch (kernel <kname>_r1 of
+// gemv_mq_pair).  Biases: all three or none.
+int qkv_pair_launch(rt_ctx* c, const char* kname_bias, const char* kname_nobias, const Fmt& fa,
+                    const Fmt& fb, const void* wq, const void* wk, const void* wv, const float* x,
+                    float* oq, float* ok, float* ov, const uint16_t* bq, const uint16_t* bk,
+                    const uint16_t* bv, uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    const char* kname = bq ? kname_bias : kname_nobias;
+    if (!wq || !wk || !wv || !x || !oq || !ok || !ov)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: null buffer", kname);
+    if ((bq == nullptr) != (bk == nullptr) || (bq == nullptr) != (bv == nullptr))
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: %s: give all three biases or none", kname);
+    if (k == 0 || k % fa.blk_el != 0 || k % fb.blk_el != 0)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: %s: k=%u must be a positive multiple of %u", kname, k,
+                    std::max(fa.blk_el, fb.blk_el));
+    if (!aligned(x, 16))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: input must be 16-byte aligned",
+                    kname);
+    if (q_dim + kv_dim == 0) return RT_OK;
+    const uint32_t nxb = k / 32;
+    const size_t red_bytes = 16 * 2 * 4 * sizeof(float);
+    const size_t lds = (size_t)nxb * XREC_BYTES + red_bytes;
+    if (lds > std::min<size_t>(c->max_lds, 80 * 1024))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: k=%u exceeds the staged %u",
+                    kname, k, (uint32_t)((std::min<size_t>(c->max_lds, 80 * 1024) - red_bytes) /
+                                         XREC_BYTES * 32));
+    uint32_t threads = c->pair_threads ? c->pair_threads : 512;
+    GemvArgs a{};  // Q and K
+    a.w[0] = (const uint8_t*)wq; a.w[1] = (const uint8_t*)wk; a.w[2] = (const uint8_t*)wk;
+    a.out[0] = oq; a.out[1] = ok; a.out[2] = ok;
+    a.aux[0] = bq; a.aux[1] = bk; a.aux[2] = bk;
+    a.n[0] = q_dim; a.n[1] = kv_dim; a.n[2] = 0;
+    a.nvrows = q_dim + kv_dim;
+    a.K = k;
+    a.x = x;
+    GemvArgs b{};  // V (matrix slot 2: virtual row = row)
+    b.w[0] = b.w[1] = b.w[2] = (const uint8_t*)wv;
+    b.out[0] = b.out[1] = b.out[2] = ov;
+    b.aux[0] = b.aux[1] = b.aux[2] = bv;
+    b.n[0] = 0; b.n[1] = 0; b.n[2] = kv_dim;
+    b.nvrows = kv_dim;
+    b.K = k;
+    b.x = x;
+    // x in one staging pass (4 slices of 4 elements per thread), else
+    // converted once into the workspace
+    if ((size_t)nxb * 8 > 4 * (size_t)threads) {
+        const int st0 = ensure_ws(c, (size_t)nxb * XREC_BYTES, kname);
+        if (st0 != RT_OK) return st0;
+        const void* xin = x;
+        void* xout = c->ws;
+        uint32_t nx = nxb;
+        void* pp[] = {&xin, &xout, &nx};
+        const int st = launch(c, "k_act_limbs_f32", dim3((nxb * 8 + 255) / 256), dim3(256), 0, pp);
+        if (st != RT_OK) return st;
+        a.x = b.x = c->ws;
+        a.x_rec = b.x_rec = 1;
+    }
+    char name[96];
+    snprintf(name, sizeof name, "%s_r1", kname);
+    const uint32_t nwaves = threads / 64;
+    const uint32_t budget = (uint32_t)c->cu_count * nwaves *
+                            std::max<uint32_t>(1, occupancy(c, name, threads, lds));
+    uint32_t ka, kb;
+    pair_ksw(fa, a.nvrows, fb, b.nvrows, k, nwaves, budget, ka, kb);
+    if (c->ksw_override) ka = kb = std::min<uint32_t>(c->ksw_override, nwaves);
+    const uint32_t ga = pair_part_grid(fa, a, threads, ka);
+    const uint32_t gb = pair_part_grid(fb, b, threads, kb);
+    a.blk0 = 0; a.nblk = ga;
+    b.blk0 = ga; b.nblk = gb;
+    void* params[] = {&a, &b};
+    return launch(c, name, dim3(ga + gb), dim3(threads), lds, params);
+}
+
 int ffn_launch(rt_ctx* c, const char* kname, const Fmt& f, const void* wg, const void* wu,
                const float* x, float* act, uint32_t ff, uint32_t k) {
     if (!wg || !wu || !act)
@@ -782,6 +905,10 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_LS_THREADS")) c->ls_threads = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS_XCD")) c->ls_xcd = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LSK")) c->lsk_enabled = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMV_PAIR_THREADS")) {
+        const uint32_t t = (uint32_t)atoi(g);
+        if (t == 256 || t == 512 || t == 1024) c->pair_threads = t;
+    }
     if (const char* g = getenv("RUNIT_GEMM_WAVES")) {
         const int v = atoi(g);
         if (v == 4 || v == 8) c->gemm_waves = (uint32_t)v;
@@ -1115,6 +1242,36 @@ int rt_fused_qkv_bias_q5k_f32(rt_ctx* c, const void* wq, const void* wk, const v
                               uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
     return qkv_launch(c, "k_qkv_bias_q5k", kQ5K, wq, wk, wv, x, oq, ok, ov, bq, bk, bv, true,
                       q_dim, kv_dim, k);
+}
+int rt_fused_qkv_bias_q4k_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                              const float* x, float* oq, float* ok, float* ov,
+                              const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                              uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    const bool bias = bq || bk || bv;
+    return qkv_launch(c, bias ? "k_qkv_bias_q4k" : "k_qkv_q4k", kQ4K, wq, wk, wv, x, oq, ok, ov,
+                      bq, bk, bv, bias, q_dim, kv_dim, k);
+}
+int rt_fused_qkv_bias_q4kg_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                               const float* x, float* oq, float* ok, float* ov,
+                               const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                               uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    const bool bias = bq || bk || bv;
+    return qkv_launch(c, bias ? "k_qkv_bias_q4kg" : "k_qkv_q4kg", kQ4KG, wq, wk, wv, x, oq, ok,
+                      ov, bq, bk, bv, bias, q_dim, kv_dim, k);
+}
+int rt_fused_qkv_bias_q4k_q6k_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                                  const float* x, float* oq, float* ok, float* ov,
+                                  const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                                  uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    return qkv_pair_launch(c, "k_qkv2_bias_q4k_q6k", "k_qkv2_q4k_q6k", kQ4K, kQ6KU, wq, wk, wv,
+                           x, oq, ok, ov, bq, bk, bv, q_dim, kv_dim, k);
+}
+int rt_fused_qkv_bias_q4kg_q6kg_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
+                                    const float* x, float* oq, float* ok, float* ov,
+                                    const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                                    uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+    return qkv_pair_launch(c, "k_qkv2_bias_q4kg_q6kg", "k_qkv2_q4kg_q6kg", kQ4KG, kQ6KGU, wq, wk,
+                           wv, x, oq, ok, ov, bq, bk, bv, q_dim, kv_dim, k);
 }
 int rt_fused_ffn_q5_0_f32(rt_ctx* c, const void* wg, const void* wu, const float* x, float* act,
                           uint32_t ff, uint32_t k) {

@@ -104,6 +104,9 @@ _SIGS = {
     "rt_fused_qkv_bias_q4_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
     "rt_fused_qkv_bias_q5_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
     "rt_fused_qkv_bias_q5k_f32": [_P] + [_P] * 10 + [_U32] * 3,
+    **{n: [_P] + [_P] * 10 + [_U32] * 3 for n in (
+        "rt_fused_qkv_bias_q4k_f32", "rt_fused_qkv_bias_q4kg_f32",
+        "rt_fused_qkv_bias_q4k_q6k_f32", "rt_fused_qkv_bias_q4kg_q6kg_f32")},
     **{n: [_P, _P, _P, _P, _P, _U32, _U32] for n in (
         "rt_fused_ffn_q8_0_f32", "rt_fused_ffn_q4_0_f32", "rt_fused_ffn_q4k_f32",
         "rt_fused_ffn_q5_0_f32", "rt_fused_ffn_q5k_f32", "rt_fused_ffn_q4_0g_f32",
@@ -438,6 +441,29 @@ def fused_qkv_bias_q5k_f32(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_
     _call(ctx, "rt_fused_qkv_bias_q5k_f32",
           *map(_ptr, (w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k, bias_v)),
           q_dim, kv_dim, k)
+
+
+def _qkv_mixed(sym, doc):
+    def fn(ctx, w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k, bias_v, q_dim,
+           kv_dim, k):
+        _call(ctx, sym,
+              *map(_ptr, (w_q, w_k, w_v, x_vec, out_q, out_k, out_v, bias_q, bias_k, bias_v)),
+              q_dim, kv_dim, k)
+    fn.__name__ = sym[3:]
+    fn.__doc__ = doc
+    return fn
+
+
+_QKV_FALLBACK = ("Replaces the reference's non-Q8_0 projection sequence (three GEMVs, each "
+                 "followed by add_f16_into_f32 of its bias, forward.rs:1561-1568) with one "
+                 "launch (new). Biases: all three or all None.")
+fused_qkv_bias_q4k_f32 = _qkv_mixed("rt_fused_qkv_bias_q4k_f32", "Q/K/V in Q4_K. " + _QKV_FALLBACK)
+fused_qkv_bias_q4kg_f32 = _qkv_mixed("rt_fused_qkv_bias_q4kg_f32",
+                                     "Q/K/V in ggml Q4_K. " + _QKV_FALLBACK)
+fused_qkv_bias_q4k_q6k_f32 = _qkv_mixed("rt_fused_qkv_bias_q4k_q6k_f32",
+                                        "Q/K in Q4_K, V in Q6_K. " + _QKV_FALLBACK)
+fused_qkv_bias_q4kg_q6kg_f32 = _qkv_mixed("rt_fused_qkv_bias_q4kg_q6kg_f32",
+                                          "Q/K in ggml Q4_K, V in ggml Q6_K. " + _QKV_FALLBACK)
 
 
 def fused_ffn_q8_0_f32(ctx, w_gate, w_up, x_vec, act_out, ff_dim, k):

@@ -53,6 +53,55 @@ def test_fused_qkv_bias_q5(ctx, fmt, q_dim, kv_dim, k):
     _qkv_case(ctx, fmt, q_dim, kv_dim, k, True, seed=q_dim + 7)
 
 
+def _qkv_mixed_case(ctx, fq, fv, q_dim, kv_dim, k, bias, seed):
+    """Q and K in format fq, V in fv, one launch; biases all given or all None."""
+    rng = np.random.default_rng(seed)
+    fmts = (fq, fq, fv)
+    ws = [device_weights(ctx, f, n, k, seed=seed + i) for i, (f, n) in
+          enumerate(zip(fmts, (q_dim, kv_dim, kv_dim)))]
+    x = rng.standard_normal(k).astype(np.float32)
+    outs = [ctx.new_buffer(4 * n) for n in (q_dim, kv_dim, kv_dim)]
+    biases = [(0.02 * rng.standard_normal(n)).astype(np.float16) for n in (q_dim, kv_dim, kv_dim)]
+    bb = [ctx.buffer_from(b) for b in biases] if bias else [None] * 3
+    name = f"fused_qkv_bias_{fq}_f32" if fq == fv else f"fused_qkv_bias_{fq}_{fv}_f32"
+    getattr(d, name)(ctx, ws[0][0], ws[1][0], ws[2][0], ctx.buffer_from(x), *outs, *bb,
+                     q_dim, kv_dim, k)
+    ctx.flush()
+    for i, n in enumerate((q_dim, kv_dim, kv_dim)):
+        yref, sabs = ora.gemv(fmts[i], ws[i][1], x, n, k)
+        if bias:
+            yref = yref + biases[i].astype(np.float64)  # add_f16_into_f32 after each GEMV
+        check_close(outs[i].read(np.float32, n), yref, sabs, f"qkv[{i}] {fmts[i]}",
+                    F32_EPS * np.abs(yref))
+
+
+@pytest.mark.parametrize("fq,fv,q_dim,kv_dim,k,bias", [
+    ("q4k", "q6k", 3584, 512, 3584, True),    # config 4 (7B Q4_K_M mix)
+    ("q4k", "q6k", 3584, 512, 3584, False),
+    ("q4k", "q6k", 896, 128, 1024, True),
+    ("q4k", "q6k", 100, 20, 256, True),       # ragged: tiles past the last row
+    ("q4k", "q6k", 256, 64, 9216, True),      # K past one staging pass: x converted once
+    ("q4k", "q6k", 4, 4, 256, True),          # one row quad per part
+    ("q4kg", "q6kg", 3584, 512, 3584, True),
+    ("q4kg", "q6kg", 256, 64, 512, False),
+    ("q4k", "q4k", 3584, 512, 3584, True),
+    ("q4k", "q4k", 256, 64, 512, False),
+    ("q4kg", "q4kg", 896, 128, 1024, True),
+])
+def test_fused_qkv_q4k_mix(ctx, fq, fv, q_dim, kv_dim, k, bias):
+    _qkv_mixed_case(ctx, fq, fv, q_dim, kv_dim, k, bias, seed=q_dim + kv_dim + k)
+
+
+def test_fused_qkv_q4k_mix_partial_bias_rejected(ctx):
+    ws = [device_weights(ctx, f, n, 256, seed=i)[0] for i, (f, n) in
+          enumerate((("q4k", 32), ("q4k", 16), ("q6k", 16)))]
+    x = ctx.buffer_from(np.ones(256, np.float32))
+    outs = [ctx.new_buffer(4 * n) for n in (32, 16, 16)]
+    b = ctx.buffer_from(np.zeros(32, np.float16))
+    with pytest.raises(Exception, match="biases"):
+        d.fused_qkv_bias_q4k_q6k_f32(ctx, *ws, x, *outs, b, None, None, 32, 16, 256)
+
+
 def ffn_check(got, gate_ref, gate_s, up_ref, up_s, what):
     """act = silu(g)·u with |g−g_ref| ≤ eg, |u−u_ref| ≤ eu: |silu'| ≤ 1.1 gives
     |Δact| ≤ 1.1·eg·(|u|+eu) + (|silu(g)|+1.1·eg)·eu, plus f32 epilogue rounding."""
