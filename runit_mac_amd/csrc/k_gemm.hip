@@ -608,6 +608,318 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
         __syncthreads();
     }
 }
+// ───────────── f16 matrix-core variant (v_mfma_f32_16x16x32_f16) ─────────────
+//
+// Same stages, tiles, splits and decode policies as gemm2_body; the dot runs
+// on f16 operands with f32 accumulation, 8 activation rows per MFMA:
+//   A (16×32): row 2·mm + part = part (0: hi, 1: lo) of activation row
+//              8g + mm, scaled by 2^-e per 32-element record so that the
+//              record's largest |x| lies in [2^14, 2^15): hi = f16(x·2^-e),
+//              lo = f16(x·2^-e − hi), which together carry ~22 bits of each
+//              element;
+//   B (32×16): the record's integer weight codes (|q| ≤ 128) as f16, exact;
+//   D (16×16): lane l holds D[4·(l/16) + r][l % 16]: hi and lo dots of
+//              activation rows 8g + 2·(l/16) (r = 0, 1) and 8g + 2·(l/16) + 1
+//              (r = 2, 3) against weight row l % 16.
+// Per record the lane adds 2^e·(dsc·(hi + lo) − mn·Σx) for its two
+// activation rows.
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// 8 signed int8 codes → 8 exact f16: byte u = q + 128 becomes the f16 bits
+// 0x64uu = 1024 + u, then 1152 is subtracted (both exact in f16).
+RT_DEV h8_t gemm_i8x8_to_h8(i64_t B) {
+    const uint32_t lo = (uint32_t)(uint64_t)B ^ 0x80808080u;
+    const uint32_t hi = (uint32_t)((uint64_t)B >> 32) ^ 0x80808080u;
+    uint32_t w[4];
+    w[0] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
+    w[1] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
+    w[2] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
+    w[3] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
+    h8_t r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h2_t v = __builtin_bit_cast(h2_t, w[i]) - h2_t{(_Float16)1152.0f, (_Float16)1152.0f};
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+
+// Activation preparation of the f16 variant: thread t → (padded activation
+// row, record, k-group of 8 elements); the 4 threads of a record are
+// neighbours.  Writes the hi/lo operands in the A order ([chunk][record]
+// [group][lane] 16-byte entries), the record exponents and, for formats with
+// a min, the records' sums of the scaled values ([chunk][record][row][group]).
+// Rows past M are zero.
+template <int MG>
+RT_DEV void gemm_xh_prep_body(const float* __restrict__ x, uint32_t M, uint32_t K, uint32_t nchunks,
+                              u32x4* __restrict__ aops, int* __restrict__ etab,
+                              float* __restrict__ stab) {
+    constexpr uint32_t ROWS = 8 * MG;
+    const uint32_t nrec = K / 32;
+    const uint64_t total = (uint64_t)nchunks * ROWS * nrec * 4;
+    for (uint64_t t = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; t < total;
+         t += (uint64_t)gridDim.x * wg_threads()) {
+        const uint32_t kc = (uint32_t)(t & 3);
+        const uint64_t rr_rec = t >> 2;
+        const uint32_t rec = (uint32_t)(rr_rec % nrec);
+        const uint32_t m = (uint32_t)(rr_rec / nrec);  // padded row
+        const uint32_t ch = m / ROWS, rr = m % ROWS, g = rr / 8, mm = rr % 8;
+        float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (m < M) {
+            const f32x4* xp = (const f32x4*)(x + (size_t)m * K + (size_t)rec * 32 + 8 * kc);
+            const f32x4 a = xp[0], b = xp[1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        // 2^-e brings the record's largest |x| into [2^14, 2^15)
+        const int e = mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) - 15 : 0;
+        h8_t hv, lv;
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float xs = __builtin_amdgcn_ldexpf(v[i], -e);
+            const _Float16 h = (_Float16)xs;
+            hv[i] = h;
+            lv[i] = (_Float16)(xs - (float)h);
+            sum += xs;
+        }
+        u32x4* base = aops + (((size_t)ch * nrec + rec) * MG + g) * 64;
+        base[2 * mm + 16 * kc] = __builtin_bit_cast(u32x4, hv);
+        base[2 * mm + 1 + 16 * kc] = __builtin_bit_cast(u32x4, lv);
+        const size_t ei = (((size_t)ch * nrec + rec) * 8 + mm) * MG + g;
+        if (kc == 0) etab[ei] = e;
+        if (stab) {
+            sum += __shfl_xor(sum, 1, 64);
+            sum += __shfl_xor(sum, 2, 64);
+            if (kc == 0) stab[ei] = sum;
+        }
+    }
+}
+#define RT_GEMM_XH_PREP(MG)                                                                    \
+    extern "C" __global__ void __launch_bounds__(256) k_gemm_xh_prep_mg##MG(                   \
+        const float* x, uint32_t M, uint32_t K, uint32_t nchunks, u32x4* aops, int* etab,      \
+        float* stab) {                                                                         \
+        gemm_xh_prep_body<MG>(x, M, K, nchunks, aops, etab, stab);                             \
+    }
+RT_GEMM_XH_PREP(1)
+RT_GEMM_XH_PREP(2)
+RT_GEMM_XH_PREP(4)
+
+template <class P, int MG, int NB, int WAVES = 4>
+RT_DEV void gemm3_body(const Gemm2Args& a) {
+    constexpr uint32_t T = 64 * WAVES, ROWS = 16 * WAVES;
+    constexpr uint32_t NR = NB * P::RECS;
+    constexpr uint32_t SEG = NB * P::BLK_BYTES;
+    constexpr uint32_t VB = SEG % 16 == 0 ? 16 : (SEG % 8 == 0 ? 8 : 4);
+    typedef typename std::conditional<VB == 16, u32x4,
+                                      typename std::conditional<VB == 8, uint2, uint32_t>::type>::type WV;
+    constexpr uint32_t WPR = SEG / VB;
+    constexpr uint32_t WV_N = ROWS * WPR;
+    constexpr uint32_t AV4 = NR * MG * 64;               // 16-byte A entries per stage
+    constexpr uint32_t SV4 = NR * 8 * MG / 4;            // dwordx4 of E (and of S) per stage
+    constexpr uint32_t WPT = (WV_N + T - 1) / T;
+    constexpr uint32_t APT = (AV4 + T - 1) / T;
+    static_assert(SEG % VB == 0 && SV4 <= T, "segment alignment");
+    __shared__ WV lw[2][WV_N];
+    __shared__ u32x4 la[2][AV4];
+    __shared__ u32x4 le[2][SV4];
+    __shared__ u32x4 ls[P::HAS_MIN ? 2 : 1][P::HAS_MIN ? SV4 : 1];
+    __shared__ uint32_t last_flag;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t j = lane & 15, c = lane >> 4;
+    const uint32_t nitems = a.tiles * a.splits * a.nchunks;
+
+    for (uint32_t item = blockIdx.x; item < nitems; item += gridDim.x) {
+        const uint32_t tile = item % a.tiles;
+        const uint32_t split = (item / a.tiles) % a.splits;
+        const uint32_t ch = item / (a.tiles * a.splits);
+        const uint32_t kb0 = split * a.kbs;
+        const uint32_t kb1 = min(a.nxb, kb0 + a.kbs);
+        const uint32_t nst = (kb1 - kb0) / NB;
+        const uint32_t row0 = tile * ROWS;
+        const uint32_t nrec = a.nxb * P::RECS;
+        const u32x4* ap = (const u32x4*)a.aops + (size_t)ch * nrec * MG * 64;
+        const int* ep = a.etab + (size_t)ch * nrec * 8 * MG;
+        const float* sp = P::HAS_MIN ? a.stab + (size_t)ch * nrec * 8 * MG : nullptr;
+
+        WV rw[WPT];
+        u32x4 ra[APT], re, rs;
+        auto gload = [&](uint32_t st) {
+            const uint32_t b0 = kb0 + st * NB;
+            const uint32_t r0 = b0 * P::RECS;
+#pragma unroll
+            for (uint32_t i = 0; i < WPT; ++i) {
+                uint32_t f = tid + T * i;
+                if (f >= WV_N) f = WV_N - 1;  // duplicate load, not stored
+                const uint32_t r = f / WPR, col = f % WPR;
+                const uint32_t n = min(row0 + r, a.N - 1);
+                rw[i] = *(const WV*)(a.w + (size_t)n * a.row_bytes + (size_t)b0 * P::BLK_BYTES + col * VB);
+            }
+            const u32x4* as = ap + (size_t)r0 * MG * 64;
+#pragma unroll
+            for (uint32_t i = 0; i < APT; ++i) ra[i] = as[min(tid + T * i, AV4 - 1)];
+            re = ((const u32x4*)(ep + (size_t)r0 * 8 * MG))[min(tid, SV4 - 1)];
+            if (P::HAS_MIN) rs = ((const u32x4*)(sp + (size_t)r0 * 8 * MG))[min(tid, SV4 - 1)];
+        };
+        auto lstore = [&](uint32_t buf) {
+#pragma unroll
+            for (uint32_t i = 0; i < WPT; ++i)
+                if (tid + T * i < WV_N) lw[buf][tid + T * i] = rw[i];
+#pragma unroll
+            for (uint32_t i = 0; i < APT; ++i)
+                if (tid + T * i < AV4) la[buf][tid + T * i] = ra[i];
+            if (tid < SV4) le[buf][tid] = re;
+            if (P::HAS_MIN && tid < SV4) ls[P::HAS_MIN ? buf : 0][tid] = rs;
+        };
+        float acc[MG][2];
+#pragma unroll
+        for (int g = 0; g < MG; ++g) acc[g][0] = acc[g][1] = 0.0f;
+        const uint32_t wrow = (16 * wv + j) * SEG;
+        auto compute = [&](uint32_t buf) {
+            const uint8_t* wb = (const uint8_t*)lw[buf] + wrow;
+            const u32x4* ab = la[buf];
+            const int* eb = (const int*)le[buf];
+            const float* sb = (const float*)ls[P::HAS_MIN ? buf : 0];
+#pragma unroll 2
+            for (uint32_t r = 0; r < NR; ++r) {
+                i64_t B;
+                float dsc, mn, dsc2 = 0.0f;
+                P::decode(wb, r, c, B, dsc, mn, dsc2);
+                const h8_t Bh = gemm_i8x8_to_h8(B);
+                const h8_t Z = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+                // ggml Q6_K: elements 0..15 (k-groups c < 2) and 16..31 take
+                // their own scales: one MFMA per half, the other half zeroed
+                const h8_t B1 = (GemmSplit16<P>::value && c >= 2) ? Z : Bh;
+                f4_t C[MG], C2[GemmSplit16<P>::value ? MG : 1];
+#pragma unroll
+                for (int g = 0; g < MG; ++g) {
+                    const h8_t A = __builtin_bit_cast(h8_t, ab[(r * MG + g) * 64 + lane]);
+                    C[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B1, f4_t{0, 0, 0, 0}, 0, 0, 0);
+                    if (GemmSplit16<P>::value)
+                        C2[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, c >= 2 ? Bh : Z,
+                                                                       f4_t{0, 0, 0, 0}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int g = 0; g < MG; ++g) {
+                    float t0 = dsc * (C[g][0] + C[g][1]);
+                    float t1 = dsc * (C[g][2] + C[g][3]);
+                    if (GemmSplit16<P>::value) {
+                        const f4_t& D = C2[GemmSplit16<P>::value ? g : 0];
+                        t0 += dsc2 * (D[0] + D[1]);
+                        t1 += dsc2 * (D[2] + D[3]);
+                    }
+                    const uint32_t i0 = (r * 8 + 2 * c) * MG + g, i1 = i0 + MG;
+                    if (P::HAS_MIN) {
+                        t0 -= mn * sb[i0];
+                        t1 -= mn * sb[i1];
+                    }
+                    acc[g][0] += __builtin_amdgcn_ldexpf(t0, eb[i0]);
+                    acc[g][1] += __builtin_amdgcn_ldexpf(t1, eb[i1]);
+                }
+            }
+        };
+        if (nst > 0) {
+            gload(0);
+            lstore(0);
+        }
+        __syncthreads();
+        for (uint32_t st = 0; st < nst; ++st) {
+            const bool more = st + 1 < nst;
+            if (more) gload(st + 1);
+            compute(st & 1);
+            if (more) lstore((st + 1) & 1);
+            __syncthreads();
+        }
+        // lane holds activation rows ch·8MG + 8g + 2c + {0, 1} of weight row n
+        const uint32_t n = row0 + 16 * wv + j;
+        if (a.splits == 1) {
+#pragma unroll
+            for (int g = 0; g < MG; ++g)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t m = ch * 8 * MG + 8 * g + 2 * c + i;
+                    if (m < a.M && n < a.N) a.y[(size_t)m * a.N + n] = acc[g][i];
+                }
+            continue;
+        }
+        const size_t crow = (size_t)8 * MG;  // rows of a chunk
+#pragma unroll
+        for (int g = 0; g < MG; ++g)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const size_t pr = ((size_t)(ch * a.splits + split) * crow + 8 * g + 2 * c + i);
+                if (n < a.N) dev_store(a.part + pr * a.N + n, acc[g][i]);
+            }
+        dev_stores_done();
+        __syncthreads();
+        uint32_t* counter = a.counters + ((size_t)ch * a.tiles + tile) * a.cstride;
+        if (tid == 0) last_flag = arrive(counter) == a.splits - 1;
+        __syncthreads();
+        if (!last_flag) continue;
+        if (n < a.N) {
+#pragma unroll
+            for (int g = 0; g < MG; ++g)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t m = ch * 8 * MG + 8 * g + 2 * c + i;
+                    float s = 0.0f;
+                    for (uint32_t sp2 = 0; sp2 < a.splits; ++sp2)
+                        s += dev_load(a.part + ((size_t)(ch * a.splits + sp2) * crow + 8 * g + 2 * c + i) * a.N + n);
+                    if (m < a.M) a.y[(size_t)m * a.N + n] = s;
+                }
+        }
+        if (tid == 0) dev_store(counter, 0u);  // ready for the next call (also under graph replay)
+        __syncthreads();
+    }
+}
+#define RT_GEMM3_KERNEL4(FN, P, MG, NB)                                                       \
+    extern "C" __global__ void __launch_bounds__(256) k_gemm3_##FN##_mg##MG(Gemm2Args a) {    \
+        gemm3_body<P, MG, NB>(a);                                                              \
+    }
+#define RT_GEMM3_KERNEL(FN, P, MG, NB)                                                        \
+    RT_GEMM3_KERNEL4(FN, P, MG, NB)                                                            \
+    extern "C" __global__ void __launch_bounds__(512) k_gemm3_##FN##_mg##MG##_w8(Gemm2Args a) { \
+        gemm3_body<P, MG, NB, 8>(a);                                                           \
+    }
+// (a group here is 8 activation rows: MG = 1, 2, 4 cover 8, 16, 32 rows with
+// the stage sizes of gemm2's 4-row groups MG = 2, 4, 8)
+RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 1, 8)
+RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 2, 4)
+RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 4, 4)
+RT_GEMM3_KERNEL(q4_0, GemmQ4_0, 1, 8)
+RT_GEMM3_KERNEL(q4_0, GemmQ4_0, 2, 4)
+RT_GEMM3_KERNEL(q4_0, GemmQ4_0, 4, 4)
+RT_GEMM3_KERNEL(q4k, GemmQ4K, 1, 1)
+RT_GEMM3_KERNEL(q4k, GemmQ4K, 2, 1)
+RT_GEMM3_KERNEL(q4k, GemmQ4K, 4, 1)
+RT_GEMM3_KERNEL(q4kg, GemmQ4KG, 1, 1)
+RT_GEMM3_KERNEL(q4kg, GemmQ4KG, 2, 1)
+RT_GEMM3_KERNEL(q4kg, GemmQ4KG, 4, 1)
+RT_GEMM3_KERNEL(q4_0g, GemmQ4_0G, 1, 8)
+RT_GEMM3_KERNEL(q4_0g, GemmQ4_0G, 2, 4)
+RT_GEMM3_KERNEL(q4_0g, GemmQ4_0G, 4, 4)
+RT_GEMM3_KERNEL(q5_0, GemmQ5_0, 1, 8)
+RT_GEMM3_KERNEL(q5_0, GemmQ5_0, 2, 4)
+RT_GEMM3_KERNEL(q5_0, GemmQ5_0, 4, 4)
+RT_GEMM3_KERNEL(q5k, GemmQ5K, 1, 1)
+RT_GEMM3_KERNEL(q5k, GemmQ5K, 2, 1)
+RT_GEMM3_KERNEL(q5k, GemmQ5K, 4, 1)
+RT_GEMM3_KERNEL(q5kg, GemmQ5KG, 1, 1)
+RT_GEMM3_KERNEL(q5kg, GemmQ5KG, 2, 1)
+RT_GEMM3_KERNEL(q5kg, GemmQ5KG, 4, 1)
+RT_GEMM3_KERNEL4(q6k, GemmQ6K, 1, 2)
+RT_GEMM3_KERNEL4(q6k, GemmQ6K, 2, 2)
+RT_GEMM3_KERNEL4(q6kg, GemmQ6KG, 1, 2)
+RT_GEMM3_KERNEL4(q6kg, GemmQ6KG, 2, 2)
+
 #define RT_GEMM2_KERNEL4(FN, P, MG, NB)                                                       \
     extern "C" __global__ void __launch_bounds__(256) k_gemm2_##FN##_mg##MG(Gemm2Args a) {    \
         gemm2_body<P, MG, NB>(a);                                                              \

@@ -147,6 +147,20 @@ const char* const kKernelNames[] = {
     "k_gemm2_q5kg_mg1", "k_gemm2_q5kg_mg2", "k_gemm2_q5kg_mg4", "k_gemm2_q5kg_mg8", "k_gemm2_q5kg_mg1_w8", "k_gemm2_q5kg_mg2_w8", "k_gemm2_q5kg_mg4_w8", "k_gemm2_q5kg_mg8_w8",
     "k_gemm2_q6k_mg1", "k_gemm2_q6k_mg2", "k_gemm2_q6k_mg4",
     "k_gemm2_q6kg_mg1", "k_gemm2_q6kg_mg2", "k_gemm2_q6kg_mg4",
+    "k_gemm3_q8_0_mg1", "k_gemm3_q8_0_mg1_w8", "k_gemm3_q8_0_mg2", "k_gemm3_q8_0_mg2_w8",
+    "k_gemm3_q8_0_mg4", "k_gemm3_q8_0_mg4_w8", "k_gemm3_q4_0_mg1", "k_gemm3_q4_0_mg1_w8",
+    "k_gemm3_q4_0_mg2", "k_gemm3_q4_0_mg2_w8", "k_gemm3_q4_0_mg4", "k_gemm3_q4_0_mg4_w8",
+    "k_gemm3_q4k_mg1", "k_gemm3_q4k_mg1_w8", "k_gemm3_q4k_mg2", "k_gemm3_q4k_mg2_w8",
+    "k_gemm3_q4k_mg4", "k_gemm3_q4k_mg4_w8", "k_gemm3_q4kg_mg1", "k_gemm3_q4kg_mg1_w8",
+    "k_gemm3_q4kg_mg2", "k_gemm3_q4kg_mg2_w8", "k_gemm3_q4kg_mg4", "k_gemm3_q4kg_mg4_w8",
+    "k_gemm3_q4_0g_mg1", "k_gemm3_q4_0g_mg1_w8", "k_gemm3_q4_0g_mg2", "k_gemm3_q4_0g_mg2_w8",
+    "k_gemm3_q4_0g_mg4", "k_gemm3_q4_0g_mg4_w8", "k_gemm3_q5_0_mg1", "k_gemm3_q5_0_mg1_w8",
+    "k_gemm3_q5_0_mg2", "k_gemm3_q5_0_mg2_w8", "k_gemm3_q5_0_mg4", "k_gemm3_q5_0_mg4_w8",
+    "k_gemm3_q5k_mg1", "k_gemm3_q5k_mg1_w8", "k_gemm3_q5k_mg2", "k_gemm3_q5k_mg2_w8",
+    "k_gemm3_q5k_mg4", "k_gemm3_q5k_mg4_w8", "k_gemm3_q5kg_mg1", "k_gemm3_q5kg_mg1_w8",
+    "k_gemm3_q5kg_mg2", "k_gemm3_q5kg_mg2_w8", "k_gemm3_q5kg_mg4", "k_gemm3_q5kg_mg4_w8",
+    "k_gemm3_q6k_mg1", "k_gemm3_q6k_mg2", "k_gemm3_q6kg_mg1", "k_gemm3_q6kg_mg2",
+    "k_gemm_xh_prep_mg1", "k_gemm_xh_prep_mg2", "k_gemm_xh_prep_mg4",
 };
 
 // Kernels of the LDS-streamed GEMV body: <base>_ls<NI>, NI = 1..3 global→LDS
@@ -246,6 +260,7 @@ struct rt_ctx {
     uint32_t ls_xcd = 1;         // RUNIT_GEMV_LS_XCD=0: plain workgroup order (sweeps)
     uint32_t pair_threads = 0;   // RUNIT_GEMV_PAIR_THREADS: two-part launch block size (sweeps)
     uint32_t gemm_waves = 0;     // RUNIT_GEMM_WAVES=4|8: force the staged GEMM's block (sweeps)
+    bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
     bool lsk_enabled = true;     // RUNIT_GEMV_LSK=0: K splits over workgroups (through memory) instead
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
@@ -898,6 +913,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_GRID_PER_CU")) c->grid_per_cu = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_PREPASS_K")) c->prepass_k = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_DIRECT")) c->gemm_direct = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_F16")) c->gemm_f16 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_ATTN_SPLIT")) c->attn_split_override = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
@@ -1386,6 +1402,74 @@ struct GemmFmt {
     uint32_t max_mg = 8;               // activation-row groups per chunk (LDS budget)
 };
 
+// f16 matrix-core form of the staged GEMM (k_gemm3_*): 8 activation rows
+// per group (MG ∈ {1, 2, 4}), hi/lo f16 operands prepared by
+// k_gemm_xh_prep_mg*.  Returns kLsDecline where the staged layout does not
+// apply (the caller then takes the other forms).
+int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, float* y,
+                 uint32_t m_rows, uint32_t n, uint32_t k) {
+    const uint32_t cu = (uint32_t)c->cu_count;
+    const uint32_t groups = (m_rows + 7) / 8;
+    const uint32_t MG = std::min<uint32_t>(f.max_mg / 2, groups <= 1 ? 1 : groups <= 2 ? 2 : 4);
+    const uint32_t nchunks = (m_rows + 8 * MG - 1) / (8 * MG);
+    const uint32_t nrec = k / 32;
+    const uint32_t nblk = k / f.blk_el;
+    const uint64_t row_bytes = (uint64_t)nblk * f.blk_bytes;
+    const uint32_t NB = MG <= 1 ? f.nb_small : f.nb_large;
+    const uint32_t seg = NB * f.blk_bytes, vb = seg % 16 == 0 ? 16 : (seg % 8 == 0 ? 8 : 4);
+    if (nblk % NB != 0 || !aligned(w, 16) || row_bytes % vb != 0 || c->gemm_direct)
+        return kLsDecline;
+    const bool w8ok = f.blk_bytes != 210;
+    const uint32_t waves = (c->gemm_waves && (c->gemm_waves == 4 || w8ok))
+                               ? c->gemm_waves
+                               : (MG >= 2 && f.blk_bytes != 34 && w8ok ? 8 : 4);
+    char kn[48];
+    snprintf(kn, sizeof kn, waves == 8 ? "k_gemm3_%s_mg%u_w8" : "k_gemm3_%s_mg%u", f.name, MG);
+    if (!c->fns.count(kn)) return kLsDecline;
+    const uint32_t tiles = (n + 16 * waves - 1) / (16 * waves);
+    const uint32_t per_cu = std::max<uint32_t>(1, occupancy(c, kn, 64 * waves, 0));
+    const uint32_t cap = cu * per_cu;
+    const uint32_t base = tiles * nchunks;
+    uint32_t splits = 1;
+    double best = 1e30;
+    for (uint32_t sp = 1; sp <= std::min<uint32_t>(16, nblk / NB); ++sp) {
+        const double rounds = (double)((base * sp + cap - 1) / cap);
+        const double t = rounds / sp + 0.02 * sp;
+        if (t < best - 1e-9) { best = t; splits = sp; }
+    }
+    const uint32_t kbs = ((nblk + splits - 1) / splits + NB - 1) / NB * NB;
+    splits = (nblk + kbs - 1) / kbs;
+    if (splits > 1 && base > kAttnCounters)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_%s_f32: %u tiles exceed %u counters",
+                    f.name, base, kAttnCounters);
+    const size_t a_bytes = (size_t)nchunks * nrec * MG * 64 * 16;
+    const size_t e_bytes = (size_t)nchunks * nrec * 8 * MG * sizeof(int);
+    const size_t s_bytes = f.has_min ? e_bytes : 0;
+    const size_t p_bytes = splits > 1 ? (size_t)splits * nchunks * 8 * MG * n * sizeof(float) : 0;
+    int st = ensure_ws(c, a_bytes + e_bytes + s_bytes + p_bytes, "gemm");
+    if (st != RT_OK) return st;
+    void* aops = c->ws;
+    int* erow = (int*)((char*)c->ws + a_bytes);
+    float* stab = s_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes) : nullptr;
+    float* part = p_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes + s_bytes) : nullptr;
+    {
+        char pk[48];
+        snprintf(pk, sizeof pk, "k_gemm_xh_prep_mg%u", MG);
+        uint32_t M = m_rows, K = k, nc = nchunks;
+        const uint64_t threads = (uint64_t)nchunks * 8 * MG * nrec * 4;
+        const uint32_t grid = (uint32_t)std::min<uint64_t>((threads + 255) / 256, (uint64_t)cu * 16);
+        void* pp[] = {(void*)&x, &M, &K, &nc, &aops, &erow, &stab};
+        st = launch(c, pk, dim3(grid), dim3(256), 0, pp);
+        if (st != RT_OK) return st;
+    }
+    uint32_t cstride = 32;
+    while (cstride > 1 && (size_t)base * cstride > kAttnCounters) cstride >>= 1;
+    Gemm2Args a2{w, aops, erow, stab, y, part, (uint32_t*)((char*)c->aux + kAuxAttnOff),
+                 m_rows, n, nblk, tiles, splits, kbs, nchunks, row_bytes, cstride};
+    void* p2[] = {&a2};
+    return launch(c, kn, dim3(std::min(base * splits, cap)), dim3(64 * waves), 0, p2);
+}
+
 int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, float* y,
                 uint32_t m_rows, uint32_t n, uint32_t k) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
@@ -1400,6 +1484,12 @@ int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, floa
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: gemm_%s_f32: input must be 16-byte aligned", f.name);
     if (m_rows == 1) return f.gemv(c, w, x, y, n, k);
+    // f16 form from 9 rows on (two or more 8-row groups; at M = 16 / 32 it
+    // runs 3-15% faster than the int8 limb form, at M ≤ 8 up to 25% slower)
+    if (c->gemm_f16 && m_rows > 8) {
+        const int st = gemm3_launch(c, f, w, x, y, m_rows, n, k);
+        if (st != kLsDecline) return st;
+    }
     const uint32_t cu = (uint32_t)c->cu_count;
     // 4·MG activation rows per chunk (MG ∈ {1, 2, 4, 8}); longer batches
     // take several chunks, each streaming W once

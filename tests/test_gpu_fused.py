@@ -251,6 +251,51 @@ def test_gemm_q8_0_direct_kernel_matches_staged(ctx):
         c2.close()
 
 
+@pytest.mark.parametrize("fmt", ["q8_0", "q4k", "q6kg"])
+@pytest.mark.parametrize("m", [16, 32])
+def test_gemm_int8_form_matches_oracle(fmt, m):
+    """The int8 limb form of the staged GEMM, which batches above 8 rows take
+    only with RUNIT_GEMM_F16=0 (they take the f16 form by default)."""
+    import os
+    n, k = 130, 3584
+    os.environ["RUNIT_GEMM_F16"] = "0"
+    try:
+        c2 = d.HipContext()
+    finally:
+        del os.environ["RUNIT_GEMM_F16"]
+    try:
+        wbuf, raw = device_weights(c2, fmt, n, k, seed=m + 40)
+        x = np.random.default_rng(m + 41).standard_normal((m, k)).astype(np.float32)
+        y = c2.new_buffer(4 * m * n)
+        getattr(d, f"gemm_{fmt}_f32")(c2, wbuf, c2.buffer_from(x), y, m, n, k)
+        c2.flush()
+        yref, sabs = ora.gemv(fmt, raw, x, n, k)
+        check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm int8 {fmt} m={m}")
+    finally:
+        c2.close()
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4k"])
+def test_gemm_f16_form_wide_range(ctx, fmt):
+    """f16 form: every 32-element record is scaled into f16's range on its
+    own, so rows of 1e-6-sized activations, rows of 1e4-sized ones and
+    records with one large outlier among tiny values all stay within the
+    bound."""
+    n, k, m = 200, 1024, 24
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=77)
+    rng = np.random.default_rng(78)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0:8] *= 1e-6
+    x[8:16] *= 1e4
+    x[16:24] *= 1e-3
+    x[16:24, ::32] = 3e3  # one outlier per record
+    y = ctx.new_buffer(4 * m * n)
+    getattr(d, f"gemm_{fmt}_f32")(ctx, wbuf, ctx.buffer_from(x), y, m, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm f16 range {fmt}")
+
+
 GEMM_MORE = ["q5_0", "q5k", "q6k", "q4_0g", "q4kg", "q5kg", "q6kg"]
 
 
