@@ -194,6 +194,7 @@ struct Fmt {
     const Fmt* single;  // single-block-unit fallback for odd block counts
     uint32_t mq_unit_el = 0;  // matrix-core path unit, if it differs from unit_el
     bool q40perm = false;     // activation records in the reference Q4_0 order
+    uint32_t ls_chunk = 3072;  // LDS-streamed K split: chunk bytes per row (at most)
     uint32_t mq_units() const { return mq_unit_el ? mq_unit_el : unit_el; }
 };
 // Q8_0 / Q4_0 kernels take two blocks per unit (4-byte-aligned loads); rows
@@ -206,12 +207,12 @@ constexpr Fmt kQ4K{256, 144, 64, 1, "Q4_K", nullptr};
 constexpr Fmt kQ6K{256, 210, 64, 1, "Q6_K", nullptr, 256};  // matrix-core: one block per lane
 constexpr Fmt kQ5_0S{32, 22, 32, 4, "Q5_0", nullptr};
 constexpr Fmt kQ5_0{32, 22, 64, 2, "Q5_0", &kQ5_0S};
-constexpr Fmt kQ5K{256, 176, 64, 1, "Q5_K", nullptr};
+constexpr Fmt kQ5K{256, 176, 64, 1, "Q5_K", nullptr, 0, false, 2048};  // (2 KB chunks: 18.0 against 19.4 µs for 3 KB)
 // ggml layouts (upstream GGUF files)
 constexpr Fmt kQ4_0GS{32, 18, 32, 4, "Q4_0 (ggml)", nullptr};
 constexpr Fmt kQ4_0G{32, 18, 64, 2, "Q4_0 (ggml)", &kQ4_0GS};
 constexpr Fmt kQ4KG{256, 144, 64, 1, "Q4_K (ggml)", nullptr};
-constexpr Fmt kQ5KG{256, 176, 64, 1, "Q5_K (ggml)", nullptr};
+constexpr Fmt kQ5KG{256, 176, 64, 1, "Q5_K (ggml)", nullptr, 0, false, 2048};
 constexpr Fmt kQ6KG{256, 210, 64, 1, "Q6_K (ggml)", nullptr, 256};
 // Q6_K on the matrix-core path with 64-element lane units (small launches:
 // four times the lanes of the one-super-block-per-lane form)
@@ -258,6 +259,7 @@ struct rt_ctx {
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     uint32_t ls_threads = 0;     // RUNIT_GEMV_LS_THREADS: force the block size (sweeps)
     uint32_t ls_xcd = 1;         // RUNIT_GEMV_LS_XCD=0: plain workgroup order (sweeps)
+    uint32_t ls_chunk = 0;       // RUNIT_GEMV_LS_CHUNK: K-split chunk bytes per row (sweeps)
     uint32_t pair_threads = 0;   // RUNIT_GEMV_PAIR_THREADS: two-part launch block size (sweeps)
     uint32_t gemm_waves = 0;     // RUNIT_GEMM_WAVES=4|8: force the staged GEMM's block (sweeps)
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
@@ -468,8 +470,12 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
         NI = (uint32_t)((rb + 15 + 1023) / 1024);
     } else {
         if (a.x_rec || a.gamma || !c->ksplit_enabled) return kLsDecline;
-        // chunks of ≤ 2 KB (NI = 2), a whole number of blocks, ≤ one staging pass
-        uint32_t cap = (uint32_t)((2048 - 15) * (uint64_t)f.blk_el / ubytes_num);
+        // chunks of ≤ f.ls_chunk bytes (3 KB, NI ≤ 3; Q5_K 2 KB), a whole
+        // number of blocks, ≤ one staging pass (the 7B down projections:
+        // Q6_K 21.5 → 19.9 µs, Q4_0 15.2 → 14.5 µs with 3 KB against 2 KB
+        // chunks; 1 KB chunks are slower still)
+        const uint32_t chunk = c->ls_chunk ? c->ls_chunk : f.ls_chunk;
+        uint32_t cap = (uint32_t)((chunk - 15) * (uint64_t)f.blk_el / ubytes_num);
         cap = std::min<uint32_t>(cap, max_recs * 32 / ue);
         cap -= cap % gu;
         if (cap == 0) return kLsDecline;
@@ -921,6 +927,10 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_LS_THREADS")) c->ls_threads = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS_XCD")) c->ls_xcd = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LSK")) c->lsk_enabled = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMV_LS_CHUNK")) {
+        const uint32_t v = (uint32_t)atoi(g);
+        if (v >= 512 && v <= 3072) c->ls_chunk = v;
+    }
     if (const char* g = getenv("RUNIT_GEMV_PAIR_THREADS")) {
         const uint32_t t = (uint32_t)atoi(g);
         if (t == 256 || t == 512 || t == 1024) c->pair_threads = t;
