@@ -295,6 +295,35 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
             "launches_reference": 1 + 10 * cfg.layers + 3}
 
 
+def bench_q4km_decode(ctx, steps: int, warmup: int) -> dict:
+    """Config 4 as a whole greedy decode step: Qwen2.5-7B shapes (28 layers,
+    hidden 3584, 28/4 heads × 128, ff 18944, vocab 152064) with the Q4_K_M
+    mix (Q/K/O/gate/up Q4_K; V, down and LM head Q6_K; Q8_0 embedding rows),
+    RMSNorm, RoPE, KV-cache write and attention at kv_len 512, one graph
+    replay per token; random-init weights of that shape."""
+    from runit_mac_amd.decode import Q4K_M, DecodeConfig, DecodeModel
+    cfg = DecodeConfig(layers=28, hidden=3584, heads=28, kv_heads=4, head_dim=128, ff=18944,
+                       vocab=152064, max_seq=1024)
+    m = DecodeModel(ctx, cfg, seed=9, quant=Q4K_M)
+    pos = 511
+    m.set_token(1)
+    g = m.capture(pos, fused=True)
+    for _ in range(max(1, warmup)):
+        g.launch()
+    ctx.flush()
+    e0, e1 = ctx.event(), ctx.event()
+    reps = max(5, steps // 2)
+    e0.record()
+    for _ in range(reps):
+        g.launch()
+    e1.record()
+    ms = e0.elapsed_ms(e1) / reps
+    del g
+    launches = m.launches_fused()
+    m.free()
+    return {"ms": ms, "step_bytes": cfg.step_bytes(pos + 1, Q4K_M), "launches": launches}
+
+
 def bench_q4km_step(ctx, steps: int, warmup: int) -> dict:
     """Config 4: every GEMV of one Qwen2.5-7B-shape token in a Q4_K_M-style
     mix — 28 layers of Q, K, O, gate+up (Q4_K) and V, down (Q6_K), the
@@ -526,6 +555,16 @@ def main():
             f"{q4['bytes'] / 1e9:.3f} GB → {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM); "
             f"with separate bias-free Q/K/V GEMVs ({q4['launches_separate_qkv']} launches): "
             f"{q4['us_separate_qkv']:.1f} us")
+        q4d = bench_q4km_decode(ctx, args.steps, args.warmup)
+        dgbs = q4d["step_bytes"] / (q4d["ms"] * 1e-3) / 1e9
+        log(f"config 4 as a decode step (7B Q4_K_M mix, kv_len 512, {q4d['launches']} launches): "
+            f"{q4d['ms'] * 1e3:.1f} us = {1e3 / q4d['ms']:.1f} tok/s; step bytes "
+            f"{q4d['step_bytes'] / 1e9:.3f} GB → {dgbs:.0f} GB/s ({100 * dgbs / HBM_PEAK_GBS:.1f}% HBM)")
+        line["q4k_m_7b_decode"] = {
+            "tok_s": round(1e3 / q4d["ms"], 2), "us_per_token": round(q4d["ms"] * 1e3, 1),
+            "step_bytes": q4d["step_bytes"], "gbs": round(dgbs, 1),
+            "frac": round(dgbs / HBM_PEAK_GBS, 4), "launches_per_token": q4d["launches"],
+            "kv_len": 512}
         line["q4k_m_7b_gemv_step"] = {
             "us_per_token": round(q4["us"], 1), "tok_s_gemv_only": round(1e6 / q4["us"], 1),
             "bytes": q4["bytes"], "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),

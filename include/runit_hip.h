@@ -448,6 +448,20 @@ int rt_rms_norm_fused_ffn_q8_0_f32(rt_ctx* ctx, const void* w_gate, const void* 
 int rt_rms_norm_gemv_q8_0_f32in_f32out(rt_ctx* ctx, const void* weight, const float* x,
                                        const float* gamma, float eps, float* output, uint32_t m,
                                        uint32_t k);
+/* The same for the Q4_K_M projections: Q/K (Q4_K) + V (Q6_K) with biases
+ * (k ≤ 8192), the Q4_K gate+up+SiLU, and a Q6_K GEMV (the LM head). */
+int rt_rms_norm_fused_qkv_bias_q4k_q6k_f32(rt_ctx* ctx, const void* w_q, const void* w_k,
+                                           const void* w_v, const float* x, const float* gamma,
+                                           float eps, float* out_q, float* out_k, float* out_v,
+                                           const uint16_t* bias_q, const uint16_t* bias_k,
+                                           const uint16_t* bias_v, uint32_t q_dim,
+                                           uint32_t kv_dim, uint32_t k);
+int rt_rms_norm_fused_ffn_q4k_f32(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                                  const float* x, const float* gamma, float eps, float* act_out,
+                                  uint32_t ff_dim, uint32_t k);
+int rt_rms_norm_gemv_q6k_f32in_f32out(rt_ctx* ctx, const void* weight, const float* x,
+                                      const float* gamma, float eps, float* output, uint32_t m,
+                                      uint32_t k);
 
 /* ───────────────────────── calibration (bench only) ─────────────────────────
  * Plain HBM streams of known size; no reference counterpart.  stream_read

@@ -28,16 +28,51 @@ RT_DEV float block_max(float v, float* red) {
 
 // rms_norm_f32_f32_f32g (norm.metal:126-154): one workgroup per row,
 // y = x · rsqrt(mean(x²) + eps) · γ.  y may alias x.
+// Rows of up to 8 float4 per thread (8192 elements at 256 threads) whose
+// start is 16-byte aligned are read in one round trip: every x and γ load is
+// issued before the first is used, and x stays in registers for the second
+// pass.  Other rows take the element loop.
 extern "C" __global__ void __launch_bounds__(256)
 k_rms_norm_f32g(const float* x, float* y, const float* gamma, float eps, uint32_t hidden) {
     __shared__ float red[16];
+    constexpr uint32_t MAXV = 8;
     const float* xr = x + (size_t)blockIdx.x * hidden;
     float* yr = y + (size_t)blockIdx.x * hidden;
+    const uint32_t tid = threadIdx.x, nt = wg_threads();
+    const uint32_t n4 = hidden / 4;
+    const bool vec = hidden % 4 == 0 && n4 <= MAXV * nt &&
+                     (((uintptr_t)xr | (uintptr_t)yr | (uintptr_t)gamma) & 15) == 0;
+    if (vec) {
+        const f32x4* x4 = (const f32x4*)xr;
+        const f32x4* g4 = (const f32x4*)gamma;
+        f32x4 xv[MAXV], gv[MAXV];
+#pragma unroll
+        for (uint32_t j = 0; j < MAXV; ++j) {
+            const uint32_t i = tid + j * nt;
+            xv[j] = i < n4 ? x4[i] : f32x4{0, 0, 0, 0};
+            gv[j] = i < n4 ? g4[i] : f32x4{0, 0, 0, 0};
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < MAXV; ++j)
+            ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+        ss = block_sum(ss, red);
+        const float rms = rsqrtf(ss / (float)hidden + eps);
+        f32x4* y4 = (f32x4*)yr;
+#pragma unroll
+        for (uint32_t j = 0; j < MAXV; ++j) {
+            const uint32_t i = tid + j * nt;
+            if (i < n4)
+                y4[i] = f32x4{xv[j].x * rms * gv[j].x, xv[j].y * rms * gv[j].y,
+                              xv[j].z * rms * gv[j].z, xv[j].w * rms * gv[j].w};
+        }
+        return;
+    }
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < hidden; i += wg_threads()) ss += xr[i] * xr[i];
+    for (uint32_t i = tid; i < hidden; i += nt) ss += xr[i] * xr[i];
     ss = block_sum(ss, red);
     const float rms = rsqrtf(ss / (float)hidden + eps);
-    for (uint32_t i = threadIdx.x; i < hidden; i += wg_threads()) yr[i] = xr[i] * rms * gamma[i];
+    for (uint32_t i = tid; i < hidden; i += nt) yr[i] = xr[i] * rms * gamma[i];
 }
 
 // RoPE angle for pair d (fused_rope.metal:34-38): freq = 1/θ^(2d/hd).

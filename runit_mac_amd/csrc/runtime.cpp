@@ -776,7 +776,8 @@ void pair_ksw(const Fmt& fa, uint32_t nva, const Fmt& fb, uint32_t nvb, uint32_t
 int qkv_pair_launch(rt_ctx* c, const char* kname_bias, const char* kname_nobias, const Fmt& fa,
                     const Fmt& fb, const void* wq, const void* wk, const void* wv, const float* x,
                     float* oq, float* ok, float* ov, const uint16_t* bq, const uint16_t* bk,
-                    const uint16_t* bv, uint32_t q_dim, uint32_t kv_dim, uint32_t k) {
+                    const uint16_t* bv, uint32_t q_dim, uint32_t kv_dim, uint32_t k,
+                    const float* gamma = nullptr, float eps = 0.0f) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     const char* kname = bq ? kname_bias : kname_nobias;
     if (!wq || !wk || !wv || !x || !oq || !ok || !ov)
@@ -792,6 +793,11 @@ int qkv_pair_launch(rt_ctx* c, const char* kname_bias, const char* kname_nobias,
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: input must be 16-byte aligned",
                     kname);
     if (q_dim + kv_dim == 0) return RT_OK;
+    // (RMSNorm folds into the staging of one pass over x: 4 slices of 4
+    // elements per thread at 512 threads)
+    if (gamma && k > 8192)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: %s: k=%u exceeds 8192 for the norm-fused form", kname, k);
     const uint32_t nxb = k / 32;
     const size_t red_bytes = 16 * 2 * 4 * sizeof(float);
     const size_t lds = (size_t)nxb * XREC_BYTES + red_bytes;
@@ -816,9 +822,12 @@ int qkv_pair_launch(rt_ctx* c, const char* kname_bias, const char* kname_nobias,
     b.nvrows = kv_dim;
     b.K = k;
     b.x = x;
+    a.gamma = b.gamma = gamma;
+    a.eps = b.eps = eps;
     // x in one staging pass (4 slices of 4 elements per thread), else
     // converted once into the workspace
-    if ((size_t)nxb * 8 > 4 * (size_t)threads) {
+    if (gamma && (size_t)nxb * 8 > 4 * (size_t)threads) threads = 512;
+    if (!gamma && (size_t)nxb * 8 > 4 * (size_t)threads) {
         const int st0 = ensure_ws(c, (size_t)nxb * XREC_BYTES, kname);
         if (st0 != RT_OK) return st0;
         const void* xin = x;
@@ -2068,6 +2077,37 @@ int rt_rms_norm_fused_ffn_q8_0_f32(rt_ctx* c, const void* wg, const void* wu, co
     return norm_then(c, "k_ffn_q8_0", kQ8_0, a, true, gamma, eps);
 }
 
+int rt_rms_norm_fused_qkv_bias_q4k_q6k_f32(rt_ctx* c, const void* wq, const void* wk,
+                                           const void* wv, const float* x, const float* gamma,
+                                           float eps, float* oq, float* ok, float* ov,
+                                           const uint16_t* bq, const uint16_t* bk,
+                                           const uint16_t* bv, uint32_t q_dim, uint32_t kv_dim,
+                                           uint32_t k) {
+    if (!gamma)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: k_qkv2_bias_q4k_q6k: null gamma");
+    return qkv_pair_launch(c, "k_qkv2_bias_q4k_q6k", "k_qkv2_q4k_q6k", kQ4K, kQ6KU, wq, wk, wv,
+                           x, oq, ok, ov, bq, bk, bv, q_dim, kv_dim, k, gamma, eps);
+}
+int rt_rms_norm_fused_ffn_q4k_f32(rt_ctx* c, const void* wg, const void* wu, const float* x,
+                                  const float* gamma, float eps, float* act, uint32_t ff,
+                                  uint32_t k) {
+    if (!wg || !wu || !act)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: k_ffn_q4k: null buffer");
+    GemvArgs a{};
+    a.w[0] = (const uint8_t*)wg; a.w[1] = (const uint8_t*)wu;
+    a.out[0] = act;
+    a.x = x;
+    a.n[0] = ff; a.n[1] = ff;
+    a.nvrows = 2 * ff;
+    a.K = k;
+    return norm_then(c, "k_ffn_q4k", kQ4K, a, true, gamma, eps);
+}
+int rt_rms_norm_gemv_q6k_f32in_f32out(rt_ctx* c, const void* w, const float* x,
+                                      const float* gamma, float eps, float* y, uint32_t m,
+                                      uint32_t k) {
+    return norm_then(c, "k_gemv_q6k_f32_f32", kQ6K, plain_args(w, x, y, nullptr, m, k), false,
+                     gamma, eps);
+}
 int rt_rms_norm_gemv_q8_0_f32in_f32out(rt_ctx* c, const void* w, const float* x,
                                        const float* gamma, float eps, float* y, uint32_t m,
                                        uint32_t k) {

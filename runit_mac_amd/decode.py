@@ -15,6 +15,13 @@ a whole decode step.  Two kernel sequences are provided:
 Weights are synthetic (seeded N(0, 0.02) quantised per block, f16 biases
 N(0, 0.02), norms 1 + N(0, 0.02)); the KV cache is pre-filled with N(0, 1)
 for the positions before the decoded one.
+
+Each projection may take its own block format (``quant``: a Q4_K_M-style mix
+keeps V and down in Q6_K): the fused sequence then routes every matrix to the
+kernels of its format, as the reference's WeightBuf dispatch does
+(forward.rs:70-248).  RMSNorm folds into the Q8_0 and Q4_K_M projections'
+activation staging; other formats take it as a launch of its own, and output
+projections that are not Q8_0 run after the attention as a second launch.
 """
 from __future__ import annotations
 
@@ -47,19 +54,31 @@ class DecodeConfig:
     def kv_dim(self) -> int:
         return self.kv_heads * self.head_dim
 
-    def weight_bytes(self) -> int:
-        """Q8_0 weight bytes read per token (each matrix once)."""
+    def weight_bytes(self, quant: dict | None = None) -> int:
+        """Weight bytes read per token (each matrix once), Q8_0 unless
+        `quant` names another format for a role."""
+        fq = dict(Q8_ALL, **(quant or {}))
         h, q, kv, ff = self.hidden, self.q_dim, self.kv_dim, self.ff
-        per_layer = sum(d.weight_bytes("q8_0", n, k) for n, k in
-                        ((q, h), (kv, h), (kv, h), (h, q), (ff, h), (ff, h), (h, ff)))
-        return self.layers * per_layer + d.weight_bytes("q8_0", self.vocab, h)
+        per_layer = sum(d.weight_bytes(fq[r], n, k) for r, n, k in
+                        (("q", q, h), ("k", kv, h), ("v", kv, h), ("o", h, q), ("gate", ff, h),
+                         ("up", ff, h), ("down", h, ff)))
+        return self.layers * per_layer + d.weight_bytes(fq["lm_head"], self.vocab, h)
 
-    def step_bytes(self, kv_len: int) -> int:
+    def step_bytes(self, kv_len: int, quant: dict | None = None) -> int:
         """Algorithmic bytes of one step: weights + KV reads + f16 biases and
         f32 norms (activations are a few KB and not counted)."""
         kv = self.layers * 2 * self.kv_heads * kv_len * self.head_dim * 4
         small = self.layers * ((self.q_dim + 2 * self.kv_dim) * 2 + 2 * self.hidden * 4)
-        return self.weight_bytes() + kv + small + self.hidden * 4
+        return self.weight_bytes(quant) + kv + small + self.hidden * 4
+
+
+# Block format per weight role; the embedding table stays Q8_0 (its row is
+# read by embed_q8_0_f32).
+ROLES = ("q", "k", "v", "o", "gate", "up", "down", "lm_head")
+Q8_ALL = {r: "q8_0" for r in ROLES}
+# Q4_K_M-style mix (BASELINE config 4): V and down (and the LM head) in Q6_K
+Q4K_M = dict(q="q4k", k="q4k", v="q6k", o="q4k", gate="q4k", up="q4k", down="q6k",
+             lm_head="q6k")
 
 
 class Arena:
@@ -82,7 +101,7 @@ class DecodeModel:
     """Synthetic Qwen2-shape model resident in one arena, plus the KV cache."""
 
     def __init__(self, ctx: d.HipContext, cfg: DecodeConfig = DecodeConfig(), seed: int = 7,
-                 gguf=None):
+                 gguf=None, quant: dict | None = None):
         """Synthetic weights, or (gguf: a runit_mac_amd.gguf.GgufFile) the
         file's tensors: Q8_0 matrices as stored, f32 norms, f32/f16 biases
         converted to f16 (RNE, as upload_weight converts F32, forward.rs:
@@ -90,13 +109,21 @@ class DecodeModel:
         output.weight is absent (forward.rs:1271-1276), and an empty KV cache."""
         self.ctx, self.cfg = ctx, cfg
         c = cfg
+        self.quant = fq = dict(Q8_ALL, **(quant or {}))
+        if set(fq) != set(ROLES):
+            raise ValueError(f"quant roles must be among {ROLES}")
+        if gguf is not None and any(f != "q8_0" for f in fq.values()):
+            raise ValueError("GGUF models load Q8_0 matrices")
         h, q, kv, ff = c.hidden, c.q_dim, c.kv_dim, c.ff
-        wb = lambda n, k: d.weight_bytes("q8_0", n, k)  # noqa: E731
-        per_layer = (wb(q, h) + 2 * wb(kv, h) + wb(h, q) + 2 * wb(ff, h) + wb(h, ff)
+        wb = lambda n, k, f="q8_0": d.weight_bytes(f, n, k)  # noqa: E731
+        per_layer = (wb(q, h, fq["q"]) + wb(kv, h, fq["k"]) + wb(kv, h, fq["v"])
+                     + wb(h, q, fq["o"]) + wb(ff, h, fq["gate"]) + wb(ff, h, fq["up"])
+                     + wb(h, ff, fq["down"])
                      + 2 * (q + 2 * kv) + 8 * h + 2 * 4 * c.kv_heads * c.max_seq * c.head_dim
                      + 16 * 256)
-        tied = gguf is None or "output.weight" not in gguf
-        total = c.layers * per_layer + wb(c.vocab, h) * (1 if tied else 2) + 16 * h + \
+        tied = (gguf is None or "output.weight" not in gguf) and fq["lm_head"] == "q8_0"
+        total = c.layers * per_layer + wb(c.vocab, h) + \
+            (0 if tied else wb(c.vocab, h, fq["lm_head"])) + 16 * h + \
             64 * 1024 + 4 * (c.vocab + 8 * ff + 8 * q)
         self.arena = Arena(ctx, total)
         a = self.arena
@@ -115,14 +142,14 @@ class DecodeModel:
                                  f"{shape}")
             return t
 
-        def qw(n, k, name=None):
+        def qw(n, k, name=None, fmt="q8_0"):
             nonlocal s
-            p = a.take(wb(n, k))
+            p = a.take(wb(n, k, fmt))
             if gguf is not None:
                 tensor(name, n, k, ("Q8_0",))
                 gguf.upload(ctx, name, p)
             else:
-                d.synth_weights(ctx, "q8_0", p, n * k // 32, s)
+                d.synth_weights(ctx, fmt, p, n * k // d.BLOCK[fmt][0], s)
                 s += 1
             return p
 
@@ -162,11 +189,15 @@ class DecodeModel:
         self.layers = []
         for i in range(c.layers):
             b = f"blk.{i}."
-            L = dict(wq=qw(q, h, b + "attn_q.weight"), wk=qw(kv, h, b + "attn_k.weight"),
-                     wv=qw(kv, h, b + "attn_v.weight"), bq=f16(q, 0.02, b + "attn_q.bias"),
+            L = dict(wq=qw(q, h, b + "attn_q.weight", fq["q"]),
+                     wk=qw(kv, h, b + "attn_k.weight", fq["k"]),
+                     wv=qw(kv, h, b + "attn_v.weight", fq["v"]),
+                     bq=f16(q, 0.02, b + "attn_q.bias"),
                      bk=f16(kv, 0.02, b + "attn_k.bias"), bv=f16(kv, 0.02, b + "attn_v.bias"),
-                     wo=qw(h, q, b + "attn_output.weight"), wg=qw(ff, h, b + "ffn_gate.weight"),
-                     wu=qw(ff, h, b + "ffn_up.weight"), wd=qw(h, ff, b + "ffn_down.weight"),
+                     wo=qw(h, q, b + "attn_output.weight", fq["o"]),
+                     wg=qw(ff, h, b + "ffn_gate.weight", fq["gate"]),
+                     wu=qw(ff, h, b + "ffn_up.weight", fq["up"]),
+                     wd=qw(h, ff, b + "ffn_down.weight", fq["down"]),
                      attn_norm=f32(h, 1.0, 0.02, b + "attn_norm.weight"),
                      ffn_norm=f32(h, 1.0, 0.02, b + "ffn_norm.weight"),
                      kc=f32(c.kv_heads * c.max_seq * c.head_dim, 0.0, 1.0),
@@ -175,7 +206,7 @@ class DecodeModel:
         self.final_norm = f32(h, 1.0, 0.02, "output_norm.weight")
         self.embd = qw(c.vocab, h, "token_embd.weight")
         # LM head: tied to token_embd unless the file has output.weight
-        self.lm_head = self.embd if tied else qw(c.vocab, h, "output.weight")
+        self.lm_head = self.embd if tied else qw(c.vocab, h, "output.weight", fq["lm_head"])
         # activations
         self.x = a.take(4 * h)
         self.xn = a.take(4 * h)
@@ -219,7 +250,9 @@ class DecodeModel:
     # ─────────────────────────── step sequences ───────────────────────────
 
     def step_reference(self, pos: int) -> None:
-        """forward.rs:1494-1771, the reference's kernel sequence."""
+        """forward.rs:1494-1771, the reference's kernel sequence (Q8_0 models)."""
+        if any(f != "q8_0" for f in self.quant.values()):
+            raise ValueError("the reference sequence is built for Q8_0 models")
         ctx, c = self.ctx, self.cfg
         h, q_dim, kv_dim = c.hidden, c.q_dim, c.kv_dim
         d.embed_q8_0_f32(ctx, self.embd, self.token, self.x, h)
@@ -241,24 +274,79 @@ class DecodeModel:
         d.gemv_q8_0_f32in_f32out_mr(ctx, self.lm_head, self.xn, self.logits, c.vocab, h)
         d.argmax_f32(ctx, self.logits, self.token, c.vocab)
 
+    def _qkv(self, L, x) -> None:
+        """Q/K/V (+ bias) of the input x, routed by the projections' formats."""
+        c, fq = self.cfg, self.quant
+        fqk, fv = fq["q"], fq["v"]
+        if fq["k"] != fqk:
+            raise ValueError("Q and K must share a format")
+        name = (f"fused_qkv_bias_{fqk}_f32" if fv == fqk else f"fused_qkv_bias_{fqk}_{fv}_f32")
+        fn = getattr(d, name, None)
+        if fn is None:
+            raise ValueError(f"no fused Q/K/V for Q/K in {fqk}, V in {fv}")
+        fn(self.ctx, L["wq"], L["wk"], L["wv"], x, self.q, self.k, self.v, L["bq"], L["bk"],
+           L["bv"], c.q_dim, c.kv_dim, c.hidden)
+
     def step_fused(self, pos: int) -> None:
-        """Same arithmetic, 5 launches per layer."""
-        ctx, c = self.ctx, self.cfg
+        """Same arithmetic, 5 launches per layer for Q8_0 (RMSNorm folded into
+        the staging of the next GEMV, attention merged into the output
+        projection); other formats add a launch for each RMSNorm and split
+        attention from the output projection."""
+        ctx, c, fq = self.ctx, self.cfg, self.quant
         h, q_dim, kv_dim = c.hidden, c.q_dim, c.kv_dim
         d.embed_q8_0_f32(ctx, self.embd, self.token, self.x, h)
         for L in self.layers:
-            d.rms_norm_fused_qkv_bias_q8_0_f32(ctx, L["wq"], L["wk"], L["wv"], self.x,
-                                               L["attn_norm"], c.eps, self.q, self.k, self.v,
-                                               L["bq"], L["bk"], L["bv"], q_dim, kv_dim, h)
-            d.decode_attention_rope_oproj_q8_0_f32(ctx, self.q, self.k, self.v, L["kc"], L["vc"],
-                                                   L["wo"], self.x, pos, c.max_seq, c.heads,
-                                                   c.kv_heads, c.head_dim, c.theta, h)
-            d.rms_norm_fused_ffn_q8_0_f32(ctx, L["wg"], L["wu"], self.x, L["ffn_norm"], c.eps,
-                                          self.act, c.ff, h)
-            d.gemv_q8_0_add_f32_f32in(ctx, L["wd"], self.act, self.x, self.x, h, c.ff)
-        d.rms_norm_gemv_q8_0_f32in_f32out(ctx, self.lm_head, self.x, self.final_norm, c.eps,
-                                          self.logits, c.vocab, h)
+            if fq["q"] == fq["k"] == fq["v"] == "q8_0":
+                d.rms_norm_fused_qkv_bias_q8_0_f32(ctx, L["wq"], L["wk"], L["wv"], self.x,
+                                                   L["attn_norm"], c.eps, self.q, self.k, self.v,
+                                                   L["bq"], L["bk"], L["bv"], q_dim, kv_dim, h)
+            elif (fq["q"], fq["k"], fq["v"]) == ("q4k", "q4k", "q6k") and h <= 8192:
+                d.rms_norm_fused_qkv_bias_q4k_q6k_f32(ctx, L["wq"], L["wk"], L["wv"], self.x,
+                                                      L["attn_norm"], c.eps, self.q, self.k,
+                                                      self.v, L["bq"], L["bk"], L["bv"], q_dim,
+                                                      kv_dim, h)
+            else:
+                d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, L["attn_norm"], c.eps, h, 1)
+                self._qkv(L, self.xn)
+            if fq["o"] == "q8_0":
+                d.decode_attention_rope_oproj_q8_0_f32(ctx, self.q, self.k, self.v, L["kc"],
+                                                       L["vc"], L["wo"], self.x, pos, c.max_seq,
+                                                       c.heads, c.kv_heads, c.head_dim,
+                                                       c.theta, h)
+            else:
+                d.decode_attention_rope_f32(ctx, self.q, self.k, self.v, L["kc"], L["vc"],
+                                            self.attn, pos, c.max_seq, c.heads, c.kv_heads,
+                                            c.head_dim, c.theta)
+                getattr(d, f"gemv_{fq['o']}_add_f32_f32in")(ctx, L["wo"], self.attn, self.x,
+                                                            self.x, h, q_dim)
+            if fq["gate"] != fq["up"]:
+                raise ValueError("gate and up must share a format")
+            if fq["gate"] in ("q8_0", "q4k"):
+                getattr(d, f"rms_norm_fused_ffn_{fq['gate']}_f32")(
+                    ctx, L["wg"], L["wu"], self.x, L["ffn_norm"], c.eps, self.act, c.ff, h)
+            else:
+                d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, L["ffn_norm"], c.eps, h, 1)
+                getattr(d, f"fused_ffn_{fq['gate']}_f32")(ctx, L["wg"], L["wu"], self.xn,
+                                                          self.act, c.ff, h)
+            getattr(d, f"gemv_{fq['down']}_add_f32_f32in")(ctx, L["wd"], self.act, self.x,
+                                                           self.x, h, c.ff)
+        if fq["lm_head"] in ("q8_0", "q6k"):
+            getattr(d, f"rms_norm_gemv_{fq['lm_head']}_f32in_f32out")(
+                ctx, self.lm_head, self.x, self.final_norm, c.eps, self.logits, c.vocab, h)
+        else:
+            d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, self.final_norm, c.eps, h, 1)
+            getattr(d, f"gemv_{fq['lm_head']}_f32in_f32out")(ctx, self.lm_head, self.xn,
+                                                             self.logits, c.vocab, h)
         d.argmax_f32(ctx, self.logits, self.token, c.vocab)
+
+    def launches_fused(self) -> int:
+        """Launches of one fused step."""
+        fq, h = self.quant, self.cfg.hidden
+        qkv_norm_fused = (fq["q"] == fq["k"] == fq["v"] == "q8_0" or
+                          ((fq["q"], fq["k"], fq["v"]) == ("q4k", "q4k", "q6k") and h <= 8192))
+        per = (1 if qkv_norm_fused else 2) + 2 + \
+            (1 if fq["gate"] in ("q8_0", "q4k") else 2) + 1
+        return 1 + self.cfg.layers * per + (1 if fq["lm_head"] in ("q8_0", "q6k") else 2) + 1
 
     def capture(self, pos: int, fused: bool = True) -> d.Graph:
         """One step captured as a HIP graph (the reference's single command

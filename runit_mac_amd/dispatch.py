@@ -129,6 +129,9 @@ _SIGS = {
     "rt_rms_norm_fused_qkv_bias_q8_0_f32": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 + [_U32] * 3,
     "rt_rms_norm_fused_ffn_q8_0_f32": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32],
     "rt_rms_norm_gemv_q8_0_f32in_f32out": [_P, _P, _P, _P, _F, _P, _U32, _U32],
+    "rt_rms_norm_fused_qkv_bias_q4k_q6k_f32": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 + [_U32] * 3,
+    "rt_rms_norm_fused_ffn_q4k_f32": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32],
+    "rt_rms_norm_gemv_q6k_f32in_f32out": [_P, _P, _P, _P, _F, _P, _U32, _U32],
     "rt_stream_read": [_P, _P, c_size_t, _P, c_size_t],
     "rt_stream_copy": [_P, _P, _P, c_size_t],
     "rt_synth_normal_f32": [_P, _P, _U64, _U64, _F, _F],
@@ -625,6 +628,26 @@ def rms_norm_fused_qkv_bias_q8_0_f32(ctx, w_q, w_k, w_v, x, gamma, eps, out_q, o
     _call(ctx, "rt_rms_norm_fused_qkv_bias_q8_0_f32", _ptr(w_q), _ptr(w_k), _ptr(w_v), _ptr(x),
           _ptr(gamma), eps, *map(_ptr, (out_q, out_k, out_v, bias_q, bias_k, bias_v)),
           q_dim, kv_dim, k)
+
+
+def rms_norm_fused_qkv_bias_q4k_q6k_f32(ctx, w_q, w_k, w_v, x, gamma, eps, out_q, out_k, out_v,
+                                       bias_q, bias_k, bias_v, q_dim, kv_dim, k):
+    """rms_norm_f32_f32_f32g + fused_qkv_bias_q4k_q6k_f32 in one launch (new)."""
+    _call(ctx, "rt_rms_norm_fused_qkv_bias_q4k_q6k_f32", _ptr(w_q), _ptr(w_k), _ptr(w_v), _ptr(x),
+          _ptr(gamma), eps, *map(_ptr, (out_q, out_k, out_v, bias_q, bias_k, bias_v)),
+          q_dim, kv_dim, k)
+
+
+def rms_norm_fused_ffn_q4k_f32(ctx, w_gate, w_up, x, gamma, eps, act_out, ff_dim, k):
+    """rms_norm_f32_f32_f32g + fused_ffn_q4k_f32 in one launch (new)."""
+    _call(ctx, "rt_rms_norm_fused_ffn_q4k_f32", _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(gamma),
+          eps, _ptr(act_out), ff_dim, k)
+
+
+def rms_norm_gemv_q6k_f32in_f32out(ctx, weight, x, gamma, eps, output, m, k):
+    """rms_norm_f32_f32_f32g + gemv_q6k_f32in_f32out in one launch (new)."""
+    _call(ctx, "rt_rms_norm_gemv_q6k_f32in_f32out", _ptr(weight), _ptr(x), _ptr(gamma), eps,
+          _ptr(output), m, k)
 
 
 def rms_norm_fused_ffn_q8_0_f32(ctx, w_gate, w_up, x, gamma, eps, act_out, ff_dim, k):

@@ -28,6 +28,24 @@ def test_rms_norm(ctx):
     assert np.all(np.abs(xb.read(np.float32, x.size) - ref) <= 4e-6 * np.abs(ref) + 1e-7)
 
 
+@pytest.mark.parametrize("hidden", [3584, 8192, 8196, 90, 12])
+def test_rms_norm_row_sizes(ctx, hidden):
+    """Rows the one-round-trip form takes (multiples of 4 up to 8192) and
+    rows it leaves to the element loop (8196, 90), in place and not."""
+    rng = np.random.default_rng(hidden)
+    x = rng.standard_normal((2, hidden)).astype(np.float32) * 2
+    g = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32)
+    ref = ora.rms_norm(x, g, 1e-6).ravel()
+    y = ctx.new_buffer(x.nbytes)
+    d.rms_norm_f32_f32_f32g(ctx, ctx.buffer_from(x), y, ctx.buffer_from(g), 1e-6, hidden, 2)
+    xb = ctx.buffer_from(x)
+    d.rms_norm_f32_f32_f32g(ctx, xb, xb, ctx.buffer_from(g), 1e-6, hidden, 2)
+    ctx.flush()
+    tol = 2e-5 * np.abs(ref) + 1e-7  # f32 Σx² over up to 8196 terms, one rsqrt
+    assert np.all(np.abs(y.read(np.float32, x.size) - ref) <= tol)
+    assert np.all(np.abs(xb.read(np.float32, x.size) - ref) <= tol)
+
+
 @pytest.mark.parametrize("pos", [0, 1, 511, 4095])
 def test_fused_rope(ctx, pos):
     rng = np.random.default_rng(pos)
@@ -217,3 +235,46 @@ def test_rms_norm_fused_gemvs(ctx):
     ffn_check(act.read(np.float32, ff), gr, gs, ur, us, "norm+ffn")
     y, s = ora.gemv("q8_0", rl, xn, 5000, h)
     check_close(yl.read(np.float32, 5000), y, s, "norm+lm head")
+
+
+def test_rms_norm_fused_q4k_m_gemvs(ctx):
+    """The Q4_K_M forms: norm + Q/K (Q4_K) + V (Q6_K) + biases, norm + Q4_K
+    gate+up+SiLU, norm + Q6_K LM head, at 7B widths (hidden 3584; the FFN
+    and LM head narrower than the model's, same code paths)."""
+    rng = np.random.default_rng(4)
+    h, q_dim, kv_dim, ff, vocab = 3584, 3584, 512, 4096, 20000
+    x = (3 * rng.standard_normal(h)).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(h)).astype(np.float32)
+    xn = ora.rms_norm(x, g, 1e-6).astype(np.float32)
+    xb, gb = ctx.buffer_from(x), ctx.buffer_from(g)
+    fmts = ("q4k", "q4k", "q6k")
+    ws = [device_weights(ctx, f, n, h, 30 + i) for i, (f, n) in
+          enumerate(zip(fmts, (q_dim, kv_dim, kv_dim)))]
+    bias = [(0.02 * rng.standard_normal(n)).astype(np.float16) for n in (q_dim, kv_dim, kv_dim)]
+    outs = [ctx.new_buffer(4 * n) for n in (q_dim, kv_dim, kv_dim)]
+    d.rms_norm_fused_qkv_bias_q4k_q6k_f32(ctx, ws[0][0], ws[1][0], ws[2][0], xb, gb, 1e-6, *outs,
+                                          *[ctx.buffer_from(b) for b in bias], q_dim, kv_dim, h)
+    wg, rg = device_weights(ctx, "q4k", ff, h, 40)
+    wu, ru = device_weights(ctx, "q4k", ff, h, 41)
+    act = ctx.new_buffer(4 * ff)
+    d.rms_norm_fused_ffn_q4k_f32(ctx, wg, wu, xb, gb, 1e-6, act, ff, h)
+    wl, rl = device_weights(ctx, "q6k", vocab, h, 42)
+    yl = ctx.new_buffer(4 * vocab)
+    d.rms_norm_gemv_q6k_f32in_f32out(ctx, wl, xb, gb, 1e-6, yl, vocab, h)
+    ctx.flush()
+    for i, n in enumerate((q_dim, kv_dim, kv_dim)):
+        y, s = ora.gemv(fmts[i], ws[i][1], xn, n, h)
+        ref = y + bias[i].astype(np.float64)
+        check_close(outs[i].read(np.float32, n), ref, s, f"norm+qkv[{i}] {fmts[i]}",
+                    F32_EPS * np.abs(ref))
+    from test_gpu_fused import ffn_check
+    gr, gs = ora.gemv("q4k", rg, xn, ff, h)
+    ur, us = ora.gemv("q4k", ru, xn, ff, h)
+    ffn_check(act.read(np.float32, ff), gr, gs, ur, us, "norm+ffn q4k")
+    y, s = ora.gemv("q6k", rl, xn, vocab, h)
+    check_close(yl.read(np.float32, vocab), y, s, "norm+lm head q6k")
+    # k past the norm-fused staging limit is refused, not run unnormalised
+    with pytest.raises(d.Dispatch):
+        d.rms_norm_fused_qkv_bias_q4k_q6k_f32(ctx, ws[0][0], ws[1][0], ws[2][0], xb, gb, 1e-6,
+                                              *outs, *[ctx.buffer_from(b) for b in bias], 4, 4,
+                                              8448)

@@ -6,16 +6,25 @@ import pytest
 
 import oracle_lib as ora
 from runit_mac_amd import dispatch as d
-from runit_mac_amd.decode import DecodeConfig, DecodeModel
+from runit_mac_amd.decode import Q4K_M, DecodeConfig, DecodeModel
 
 pytestmark = pytest.mark.gpu
 
 
 def cpu_step(m: DecodeModel, tok: int, pos: int) -> np.ndarray:
     """forward.rs:1494-1771 on the CPU with the oracle (f64 arithmetic)."""
-    c = m.cfg
+    c, fq = m.cfg, m.quant
     h, qd, kvd, hd = c.hidden, c.q_dim, c.kv_dim, c.head_dim
-    rd8 = lambda p, n, k: m.read(p, d.weight_bytes("q8_0", n, k) // 4).view(np.uint8)  # noqa
+
+    def rdw(p, n, k, fmt="q8_0"):
+        nb = d.weight_bytes(fmt, n, k)
+        return m.read(p, (nb + 3) // 4).view(np.uint8)[:nb]
+
+    def gemv(role, p, x, n, k):
+        y, _ = ora.gemv(fq[role], rdw(p, n, k, fq[role]), x.astype(np.float32), n, k)
+        return y
+
+    rd8 = lambda p, n, k: rdw(p, n, k)  # noqa: E731
     emb = rd8(m.embd, c.vocab, h)
     row = (h // 32) * 34
     x = ora.dequant("q8_0", emb[tok * row:(tok + 1) * row]).astype(np.float64)
@@ -23,8 +32,9 @@ def cpu_step(m: DecodeModel, tok: int, pos: int) -> np.ndarray:
         g = m.read(L["attn_norm"], h)
         xn = ora.rms_norm(x.astype(np.float32), g, c.eps)
         outs = []
-        for w, b, n in ((L["wq"], L["bq"], qd), (L["wk"], L["bk"], kvd), (L["wv"], L["bv"], kvd)):
-            y, _ = ora.gemv("q8_0", rd8(w, n, h), xn.astype(np.float32), n, h)
+        for role, w, b, n in (("q", L["wq"], L["bq"], qd), ("k", L["wk"], L["bk"], kvd),
+                              ("v", L["wv"], L["bv"], kvd)):
+            y = gemv(role, w, xn, n, h)
             bias = m.read(b, n // 2 + 1).view(np.float16)[:n].astype(np.float64)
             outs.append(y + bias)
         q, k, v = outs
@@ -35,17 +45,17 @@ def cpu_step(m: DecodeModel, tok: int, pos: int) -> np.ndarray:
         kc[:, pos] = k.reshape(c.kv_heads, hd)
         vc[:, pos] = v.reshape(c.kv_heads, hd)
         att = ora.attention(q, kc, vc, c.heads, c.kv_heads, hd, pos + 1, c.max_seq)
-        y, _ = ora.gemv("q8_0", rd8(L["wo"], h, qd), att.astype(np.float32), h, qd)
-        x = x + y
+        x = x + gemv("o", L["wo"], att, h, qd)
         xn = ora.rms_norm(x.astype(np.float32), m.read(L["ffn_norm"], h), c.eps)
-        gt, _ = ora.gemv("q8_0", rd8(L["wg"], c.ff, h), xn.astype(np.float32), c.ff, h)
-        up, _ = ora.gemv("q8_0", rd8(L["wu"], c.ff, h), xn.astype(np.float32), c.ff, h)
+        gt = gemv("gate", L["wg"], xn, c.ff, h)
+        up = gemv("up", L["wu"], xn, c.ff, h)
         act = gt / (1.0 + np.exp(-gt)) * up
-        y, _ = ora.gemv("q8_0", rd8(L["wd"], h, c.ff), act.astype(np.float32), h, c.ff)
-        x = x + y
+        x = x + gemv("down", L["wd"], act, h, c.ff)
     xn = ora.rms_norm(x.astype(np.float32), m.read(m.final_norm, h), c.eps)
-    head = emb if m.lm_head == m.embd else rd8(m.lm_head, c.vocab, h)
-    logits, _ = ora.gemv("q8_0", head, xn.astype(np.float32), c.vocab, h)
+    if m.lm_head == m.embd:
+        logits, _ = ora.gemv("q8_0", emb, xn.astype(np.float32), c.vocab, h)
+    else:
+        logits = gemv("lm_head", m.lm_head, xn, c.vocab, h)
     return logits
 
 
@@ -79,6 +89,36 @@ def test_step_matches_cpu_oracle(ctx, layers):
         assert np.max(np.abs(got - ref)) <= 1e-3 * (ref.max() - ref.min()), \
             (fused, np.max(np.abs(got - ref)))
         assert m.get_token() == int(np.argmax(ref)) == ora.argmax(got.astype(np.float32))
+    m.free()
+
+
+def test_q4k_m_mix_step_matches_cpu_oracle(ctx):
+    """A Q4_K_M-style model (Q/K/O/gate/up Q4_K; V, down and the LM head
+    Q6_K; head size 128): the fused step routes each matrix to its format's
+    kernels, eagerly and replayed as a graph."""
+    cfg = DecodeConfig(layers=2, hidden=512, heads=4, kv_heads=2, head_dim=128, ff=1024,
+                       vocab=1000, max_seq=300)
+    m = DecodeModel(ctx, cfg, seed=11, quant=Q4K_M)
+    with pytest.raises(ValueError):
+        m.step_reference(0)
+    tok, pos = 77, 257
+    snap = snapshot_cache(m)
+    ref = cpu_step(m, tok, pos)
+    restore_cache(m, snap)
+    m.set_token(tok)
+    g = m.capture(pos, fused=True)
+    for replay in range(3):
+        restore_cache(m, snap)
+        m.set_token(tok)
+        if replay == 0:
+            m.step_fused(pos)
+        else:
+            g.launch()
+        ctx.flush()
+        got = m.read(m.logits, cfg.vocab).astype(np.float64)
+        assert np.max(np.abs(got - ref)) <= 1e-3 * (ref.max() - ref.min()), \
+            (replay, np.max(np.abs(got - ref)))
+        assert m.get_token() == int(np.argmax(ref))
     m.free()
 
 
