@@ -491,7 +491,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--suite", default="all", choices=["all", "gemv", "quick", "decode", "step"])
+    ap.add_argument("--suite", default="all", choices=["all", "gemv", "quick", "decode", "step", "q4decode"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run only GEMV workloads whose label contains this")
     ap.add_argument("--profile-pass", action="store_true",
@@ -547,14 +547,7 @@ def main():
                        "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / dec["step_bytes"], 0)},
         })
 
-    if args.suite in ("all", "gemv", "step") and not args.only:
-        q4 = bench_q4km_step(ctx, args.steps, args.warmup)
-        gbs = q4["bytes"] / (q4["us"] * 1e-6) / 1e9
-        log(f"config 4 (7B Q4_K_M mix, all 28 layers' GEMVs + Q6_K LM head, {q4['launches']} "
-            f"launches): {q4['us']:.1f} us per token = {1e6 / q4['us']:.1f} tok/s of GEMVs; "
-            f"{q4['bytes'] / 1e9:.3f} GB → {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM); "
-            f"with separate bias-free Q/K/V GEMVs ({q4['launches_separate_qkv']} launches): "
-            f"{q4['us_separate_qkv']:.1f} us")
+    if args.suite in ("all", "gemv", "step", "q4decode") and not args.only:
         q4d = bench_q4km_decode(ctx, args.steps, args.warmup)
         dgbs = q4d["step_bytes"] / (q4d["ms"] * 1e-3) / 1e9
         log(f"config 4 as a decode step (7B Q4_K_M mix, kv_len 512, {q4d['launches']} launches): "
@@ -565,12 +558,20 @@ def main():
             "step_bytes": q4d["step_bytes"], "gbs": round(dgbs, 1),
             "frac": round(dgbs / HBM_PEAK_GBS, 4), "launches_per_token": q4d["launches"],
             "kv_len": 512}
+    if args.suite in ("all", "gemv", "step") and not args.only:
+        q4 = bench_q4km_step(ctx, args.steps, args.warmup)
+        gbs = q4["bytes"] / (q4["us"] * 1e-6) / 1e9
+        log(f"config 4 (7B Q4_K_M mix, all 28 layers' GEMVs + Q6_K LM head, {q4['launches']} "
+            f"launches): {q4['us']:.1f} us per token = {1e6 / q4['us']:.1f} tok/s of GEMVs; "
+            f"{q4['bytes'] / 1e9:.3f} GB → {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM); "
+            f"with separate bias-free Q/K/V GEMVs ({q4['launches_separate_qkv']} launches): "
+            f"{q4['us_separate_qkv']:.1f} us")
         line["q4k_m_7b_gemv_step"] = {
             "us_per_token": round(q4["us"], 1), "tok_s_gemv_only": round(1e6 / q4["us"], 1),
             "bytes": q4["bytes"], "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
             "launches": q4["launches"],
             "us_per_token_separate_qkv": round(q4["us_separate_qkv"], 1)}
-    specs = [] if args.suite in ("decode", "step") else gemv_specs(ctx, args.suite)
+    specs = [] if args.suite in ("decode", "step", "q4decode") else gemv_specs(ctx, args.suite)
     if args.only:
         specs = [sp for sp in specs if args.only in sp[0]]
     results = []
