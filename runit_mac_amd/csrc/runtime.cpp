@@ -1883,7 +1883,9 @@ static uint32_t attn_nsplit(rt_ctx* c, uint32_t kv_len, uint32_t groups) {
 
 static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch,
                        uint32_t max_split_cap = 0, AttnArgs* used = nullptr) {
-    const uint32_t G = a.H / a.KVH, HB = (G + 7) / 8;
+    // query heads per workgroup, as the kernels' attn_gm<HD>()
+    const uint32_t gm = strstr(kname, "hd128") ? 4 : 8;
+    const uint32_t G = a.H / a.KVH, HB = (G + gm - 1) / gm;
     const uint32_t groups = batch * a.KVH * HB;
     a.chunk = attn_chunk(c, a.kv_len, groups, max_split_cap);
     const uint32_t nsplit = a.kv_len ? (a.kv_len + a.chunk - 1) / a.chunk : 1;
@@ -1991,7 +1993,9 @@ int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const
     // splits the KV range in 2..8 (one split has no merge to save; more
     // splits than the projection stages would slow the attention down);
     // otherwise: attention, then the GEMV.
-    const uint32_t nsplit0 = attn_nsplit(c, pos + 1, num_kv_heads * ((num_heads / num_kv_heads + 7) / 8));
+    const uint32_t gm = head_dim == 128 ? 4 : 8;  // query heads per attention workgroup
+    const uint32_t nsplit0 =
+        attn_nsplit(c, pos + 1, num_kv_heads * ((num_heads / num_kv_heads + gm - 1) / gm));
     const bool merged = q_dim % 64 == 0 && q_dim / 32 * 8 <= 256 && !c->plan_override.T &&
                         nsplit0 >= 2 && nsplit0 <= kAttnXMaxSplits;
     AttnArgs a{};
