@@ -1,0 +1,39 @@
+"""Host-side logic that needs no GPU: the bench's one-GPU contract and the
+decode step's per-role weight accounting and format checks."""
+import os
+import subprocess
+import sys
+
+import pytest
+
+from runit_mac_amd import dispatch as d
+from runit_mac_amd.decode import Q4K_M, Q8_ALL, ROLES, DecodeConfig, DecodeModel
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    p = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert p.returncode != 0
+    assert "one GPU" in p.stderr
+
+
+def test_q4k_m_weight_accounting():
+    c = DecodeConfig(layers=28, hidden=3584, heads=28, kv_heads=4, head_dim=128, ff=18944,
+                     vocab=152064)
+    h, q, kv, ff = c.hidden, c.q_dim, c.kv_dim, c.ff
+    per_layer = (d.weight_bytes("q4k", q, h) + d.weight_bytes("q4k", kv, h)
+                 + d.weight_bytes("q6k", kv, h) + d.weight_bytes("q4k", h, q)
+                 + 2 * d.weight_bytes("q4k", ff, h) + d.weight_bytes("q6k", h, ff))
+    assert c.weight_bytes(Q4K_M) == 28 * per_layer + d.weight_bytes("q6k", c.vocab, h)
+    assert c.weight_bytes() == c.weight_bytes(Q8_ALL)
+    # KV reads grow with the cache length; the weights do not
+    assert c.step_bytes(1024, Q4K_M) - c.step_bytes(512, Q4K_M) == \
+        28 * 2 * c.kv_heads * 512 * c.head_dim * 4
+    assert set(Q4K_M) == set(ROLES)
+
+
+def test_decode_model_rejects_unknown_roles_before_allocating():
+    with pytest.raises(ValueError):
+        DecodeModel(None, DecodeConfig(layers=1), quant={"attn": "q4k"})
