@@ -455,11 +455,58 @@ static uint64_t splitmix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
+/* ln(u) for u in (0, 1] and cos(2π·v) for v in [0, 1), built from correctly
+ * rounded f32 operations only (+, −, ×, /, fmaf; no contraction), so that the
+ * device generator, which evaluates the same sequence, yields the same bits.
+ * ln: u = m·2^e with m in [√½, √2), ln m = 2·atanh(s), s = (m−1)/(m+1), odd
+ * series to s^11 (|s| ≤ 0.172).  cos: quadrant n = rint(4v), r = v − n/4 in
+ * [−1/8, 1/8] (exact), θ = 2π·r, Taylor series of sin / cos to degree 11 / 10. */
+static float synth_ln(float u) {
+    int e = 0;
+    float m = frexpf(u, &e); /* u = m·2^e, m in [0.5, 1) */
+    if (m < 0.70710678f) { m = m * 2.0f; e -= 1; }
+    const float s = (m - 1.0f) / (m + 1.0f);
+    const float z = s * s;
+    float p = fmaf(z, 1.0f / 11.0f, 1.0f / 9.0f);
+    p = fmaf(z, p, 1.0f / 7.0f);
+    p = fmaf(z, p, 1.0f / 5.0f);
+    p = fmaf(z, p, 1.0f / 3.0f);
+    const float lnm = fmaf(2.0f * s, z * p, 2.0f * s);
+    return fmaf((float)e, 0.693147182f, lnm);
+}
+static float synth_cos2pi(float v) {
+    const float n = rintf(4.0f * v);
+    const float r = v - 0.25f * n;
+    const float t = r * 6.28318548f;
+    const float z = t * t;
+    float c = fmaf(z, -2.75573192e-7f, 2.48015873e-5f);
+    c = fmaf(z, c, -1.38888889e-3f);
+    c = fmaf(z, c, 4.16666667e-2f);
+    c = fmaf(z, c, -0.5f);
+    c = fmaf(z, c, 1.0f);
+    float sn = fmaf(z, -2.50521084e-8f, 2.75573192e-6f);
+    sn = fmaf(z, sn, -1.98412698e-4f);
+    sn = fmaf(z, sn, 8.33333333e-3f);
+    sn = fmaf(z, sn, -1.66666667e-1f);
+    sn = fmaf(t * z, sn, t);
+    switch (((int)n) & 3) {
+    case 0: return c;
+    case 1: return -sn;
+    case 2: return -c;
+    default: return sn;
+    }
+}
+
 float ora_synth_normal(uint64_t seed, uint64_t idx) {
     const uint64_t h = splitmix64(seed ^ splitmix64(idx));
-    const float u1 = (float)((h >> 40) + 1) * 5.9604644775390625e-8f;
-    const float u2 = (float)(h & 0xFFFFFFull) * 5.9604644775390625e-8f;
-    return sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    const float u1 = (float)((h >> 40) + 1) * 5.9604644775390625e-8f;  /* (0, 1] */
+    const float u2 = (float)(h & 0xFFFFFFull) * 5.9604644775390625e-8f; /* [0, 1) */
+    return sqrtf(-2.0f * synth_ln(u1)) * synth_cos2pi(u2);
+}
+
+void ora_synth_normal_f32(uint64_t seed, uint64_t n, float mean, float stdv, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; ++i) out[i] = mean + stdv * ora_synth_normal(seed, (uint64_t)i);
 }
 
 static int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
@@ -747,5 +794,30 @@ void ora_quantize_q6kg(const float* w, size_t nblk, uint8_t* out) {
             const int v = sc[2 * k] + (int)((b * 5 + (size_t)k * 3) % 5) - 2;
             sc[2 * k + 1] = (int8_t)clampi(v, -127, 127);
         }
+    }
+}
+
+/* Seeded weights as the device generators build them (rt_synth_*): element i
+ * of the stream is w_i = stdv·N_i (f32 product), quantised per block with the
+ * quantisers above. */
+void ora_synth_weights(int fmt, uint64_t seed, float stdv, size_t nblk, uint8_t* out) {
+    const size_t el = ora_block_elems(fmt), by = ora_block_bytes(fmt);
+#pragma omp parallel
+    {
+        float* w = (float*)malloc(el * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t b = 0; b < (int64_t)nblk; ++b) {
+            for (size_t i = 0; i < el; ++i) w[i] = stdv * ora_synth_normal(seed, (uint64_t)b * el + i);
+            switch (fmt) {
+            case ORA_Q8_0: ora_quantize_q8_0(w, 1, out + b * by); break;
+            case ORA_Q4_0: ora_quantize_q4_0(w, 1, out + b * by); break;
+            case ORA_Q4K: ora_quantize_q4k(w, 1, out + b * by); break;
+            case ORA_Q6K: ora_quantize_q6k(w, 1, out + b * by); break;
+            case ORA_Q5_0: ora_quantize_q5_0(w, 1, out + b * by); break;
+            case ORA_Q5K: ora_quantize_q5k(w, 1, out + b * by); break;
+            default: memset(out + b * by, 0, by); break;
+            }
+        }
+        free(w);
     }
 }

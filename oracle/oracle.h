@@ -99,6 +99,11 @@ void ora_attention(const double* q, const float* k, const float* v, size_t num_h
 /* Seeded synthetic data with the same definitions as the device generators
  * (splitmix64 → Box–Muller), used to build golden fixtures on the CPU. */
 float ora_synth_normal(uint64_t seed, uint64_t idx);
+/* out[i] = mean + stdv·N(seed, i), i < n (f32 arithmetic). */
+void ora_synth_normal_f32(uint64_t seed, uint64_t n, float mean, float stdv, float* out);
+/* nblk blocks of fmt (reference layouts: Q8_0, Q4_0, Q4_K, Q6_K, Q5_0, Q5_K)
+ * from w_i = stdv·N(seed, i), exactly as the device generators build them. */
+void ora_synth_weights(int fmt, uint64_t seed, float stdv, size_t nblk, uint8_t* out);
 void ora_quantize_q8_0(const float* w, size_t nblk, uint8_t* out);
 void ora_quantize_q4_0(const float* w, size_t nblk, uint8_t* out);
 void ora_quantize_q4k(const float* w, size_t nblk, uint8_t* out);

@@ -352,21 +352,63 @@ RT_DEV uint64_t splitmix64(uint64_t z) {
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
     return z ^ (z >> 31);
 }
+// ln(u), u in (0, 1], and cos(2π·v), v in [0, 1), from correctly rounded f32
+// operations only (+, −, ×, /, fma; contraction off), so that every machine
+// that evaluates the same sequence gets the same bits.  ln: u = m·2^e with m
+// in [√½, √2), ln m = 2·atanh(s), s = (m−1)/(m+1), odd series to s^11
+// (|s| ≤ 0.172).  cos: quadrant n = rint(4v), r = v − n/4 in [−1/8, 1/8]
+// (exact), θ = 2π·r, Taylor series of sin / cos to degree 11 / 10.
+RT_DEV float synth_ln(float u) {
+#pragma clang fp contract(off)
+    int e = 0;
+    float m = frexpf(u, &e);  // u = m·2^e, m in [0.5, 1)
+    if (m < 0.70710678f) { m = m * 2.0f; e -= 1; }
+    const float s = (m - 1.0f) / (m + 1.0f);
+    const float z = s * s;
+    float p = __builtin_fmaf(z, 1.0f / 11.0f, 1.0f / 9.0f);
+    p = __builtin_fmaf(z, p, 1.0f / 7.0f);
+    p = __builtin_fmaf(z, p, 1.0f / 5.0f);
+    p = __builtin_fmaf(z, p, 1.0f / 3.0f);
+    const float lnm = __builtin_fmaf(2.0f * s, z * p, 2.0f * s);
+    return __builtin_fmaf((float)e, 0.693147182f, lnm);
+}
+RT_DEV float synth_cos2pi(float v) {
+#pragma clang fp contract(off)
+    const float n = rintf(4.0f * v);
+    const float r = v - 0.25f * n;
+    const float t = r * 6.28318548f;
+    const float z = t * t;
+    float c = __builtin_fmaf(z, -2.75573192e-7f, 2.48015873e-5f);
+    c = __builtin_fmaf(z, c, -1.38888889e-3f);
+    c = __builtin_fmaf(z, c, 4.16666667e-2f);
+    c = __builtin_fmaf(z, c, -0.5f);
+    c = __builtin_fmaf(z, c, 1.0f);
+    float sn = __builtin_fmaf(z, -2.50521084e-8f, 2.75573192e-6f);
+    sn = __builtin_fmaf(z, sn, -1.98412698e-4f);
+    sn = __builtin_fmaf(z, sn, 8.33333333e-3f);
+    sn = __builtin_fmaf(z, sn, -1.66666667e-1f);
+    sn = __builtin_fmaf(t * z, sn, t);
+    const int q = ((int)n) & 3;
+    return q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+}
 RT_DEV float synth_normal(uint64_t seed, uint64_t idx) {
+#pragma clang fp contract(off)
     const uint64_t h = splitmix64(seed ^ splitmix64(idx));
     const float u1 = (float)((h >> 40) + 1) * 5.9604644775390625e-8f;  // (0, 1]
     const float u2 = (float)(h & 0xFFFFFFull) * 5.9604644775390625e-8f;  // [0, 1)
-    return sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    return sqrtf(-2.0f * synth_ln(u1)) * synth_cos2pi(u2);  // sqrtf: correctly rounded
 }
 
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_normal_f32(float* out, uint64_t n, uint64_t seed, float mean, float stdv) {
+#pragma clang fp contract(off)
     for (uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * wg_threads())
         out[i] = mean + stdv * synth_normal(seed, i);
 }
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, float mean, float stdv) {
+#pragma clang fp contract(off)
     for (uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * wg_threads())
         out[i] = f2h(mean + stdv * synth_normal(seed, i));
@@ -376,6 +418,7 @@ k_synth_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, float mean, float s
 // the unrounded d (round half away from zero).
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q8_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+#pragma clang fp contract(off)
     for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
          b += (uint64_t)gridDim.x * wg_threads()) {
         float w[32];
@@ -400,6 +443,7 @@ k_synth_q8_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // nib = clamp(int(w/d + 8.5), 0, 15); reference nibble order (2i low, 2i+1 high).
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q4_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+#pragma clang fp contract(off)
     for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
          b += (uint64_t)gridDim.x * wg_threads()) {
         float w[32];
@@ -429,6 +473,7 @@ k_synth_q4_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // q = clamp(round((w + dmin·m_s)/(d·sc_s)), 0, 15).
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q4k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+#pragma clang fp contract(off)
     for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
          b += (uint64_t)gridDim.x * wg_threads()) {
         float w[256];
@@ -482,6 +527,7 @@ k_synth_q4k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // element 16 + j in the high nibble and qh bit 16 + j.
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q5_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+#pragma clang fp contract(off)
     for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
          b += (uint64_t)gridDim.x * wg_threads()) {
         float w[32];
@@ -512,6 +558,7 @@ k_synth_q5_0(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // to bit e%8 of qh[e/8].
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q5k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+#pragma clang fp contract(off)
     for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
          b += (uint64_t)gridDim.x * wg_threads()) {
         float w[256];
@@ -571,6 +618,7 @@ k_synth_q5k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
 // The odd scale slots, which the reference ignores, hold 0x5A.
 extern "C" __global__ void __launch_bounds__(256)
 k_synth_q6k(uint8_t* out, uint64_t nblk, uint64_t seed, float stdv) {
+#pragma clang fp contract(off)
     for (uint64_t b = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x; b < nblk;
          b += (uint64_t)gridDim.x * wg_threads()) {
         float w[256];

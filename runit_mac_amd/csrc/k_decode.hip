@@ -2,6 +2,7 @@
 // KV-cache scatter, decode attention (plain and fused with RoPE + cache
 // write) and the Q8_0 embedding lookup.
 #include "rt_device.h"
+#include "rt_shared.h"
 
 // Sum over a workgroup (any multiple of 64 threads ≤ 1024); `red` holds ≥ 16
 // floats of LDS.  Every thread receives the total.
@@ -125,7 +126,7 @@ k_kv_copy_f32(const float* src, float* dst, uint32_t pos, uint32_t max_seq, uint
 //
 // Grid (nsplit, num_kv_heads · head_blocks, batch), 256 threads.  Workgroup
 // (s, kvh·HB + hb, b) takes positions [s·chunk, min(kv_len, (s+1)·chunk)) of
-// kv head kvh for the (up to ATT_GM) query heads of head block hb of that kv
+// kv head kvh for the (up to rt_attn_gm(HD)) query heads of head block hb of that kv
 // head's group, so each K/V row is fetched once for all of them.  Per 64
 // positions:
 //   loads  : thread t holds a quarter of key row t/4 and HD/16 float4 of the
@@ -140,7 +141,6 @@ k_kv_copy_f32(const float* src, float* dst, uint32_t pos, uint32_t max_seq, uint
 // With nsplit > 1 each workgroup writes (m, l, o) for its heads; the last
 // workgroup of a (b, kvh, hb) group to arrive (arrival counter, reset by that
 // workgroup) merges the splits in split order.
-constexpr uint32_t ATT_GM = 8;    // query heads per workgroup
 constexpr uint32_t ATT_SUB = 64;  // positions per inner step
 
 struct AttnArgs {
@@ -387,21 +387,10 @@ RT_DEV void attn_split(const AttnArgs& a) {
     if (tid == 0) dev_store(counter, 0u);  // ready for the next call (also under graph replay)
 }
 
-// Head groups per head size (threads = 256 · HG; registers bound HD 256 to one)
-template <int HD> constexpr int attn_hg() { return HD == 64 ? 4 : HD == 128 ? 2 : 1; }
-// Query heads per workgroup: ATT_GM, or 4 at head size 128 (7B-class groups
-// of 7 query heads then take two workgroups per KV head and split, twice the
-// workgroups of one block of 8: 12.6 → ~11 µs per 7B layer at kv_len 512;
-// at head size 64 the 0.5B step runs the same either way)
-#ifndef RT_ATT_GM128
-#define RT_ATT_GM128 4
-#endif
-#ifndef RT_ATT_GM64
-#define RT_ATT_GM64 8
-#endif
-template <int HD> constexpr int attn_gm() {
-    return HD == 128 ? RT_ATT_GM128 : HD == 64 ? RT_ATT_GM64 : (int)ATT_GM;
-}
+// Head groups and query heads per workgroup: rt_attn_hg / rt_attn_gm
+// (rt_shared.h, shared with the host's grid sizing).
+template <int HD> constexpr int attn_hg() { return (int)rt_attn_hg(HD); }
+template <int HD> constexpr int attn_gm() { return (int)rt_attn_gm(HD); }
 
 #define RT_ATTN_KERNELS(HD)                                                                \
     extern "C" __global__ void __launch_bounds__(256 * attn_hg<HD>())                     \

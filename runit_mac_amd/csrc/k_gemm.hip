@@ -134,16 +134,11 @@ RT_DEV void gemm_body(const GemmArgs& a) {
             k.wq[t][2] = pq[(p & 3) ? 2 : 1];
             k.wd[t] = *(const uint32_t*)((uintptr_t)blk & ~(uintptr_t)3);
         }
-#ifdef RT_PROBE_GEMM_NOA
-#pragma unroll
-        for (int g = 0; g < MG; ++g) { k.A[g] = uint2{lane * 77u + b, b}; k.E[g] = (int)(b & 7); }
-#else
 #pragma unroll
         for (int g = 0; g < MG; ++g) k.A[g] = ap[((size_t)b * MG + g) * 64 + lane];
         const int* e = ep + ((size_t)b * 4 + c) * MG;
 #pragma unroll
         for (int g = 0; g < MG; ++g) k.E[g] = e[g];
-#endif
     };
     float acc[MG][CT];
 #pragma unroll
@@ -161,13 +156,9 @@ RT_DEV void gemm_body(const GemmArgs& a) {
             const float d = h2f((blk & 3) ? (k.wd[t] >> 16) : k.wd[t]);
 #pragma unroll
             for (int g = 0; g < MG; ++g) {
-#ifdef RT_PROBE_GEMM_NOMFMA
-                acc[g][t] += d * (float)(q0 ^ q1 ^ k.A[g].x ^ k.A[g].y) + (float)k.E[g];
-#else
                 const i64_t A = (i64_t)(((uint64_t)k.A[g].y << 32) | k.A[g].x);
                 const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, v4i{0, 0, 0, 0}, 0, 0, 0);
                 acc[g][t] += __builtin_amdgcn_ldexpf(d * comb4(C), k.E[g] - 22);
-#endif
             }
         }
     };

@@ -53,12 +53,8 @@ constexpr uint32_t kMaxSplitTiles = 256;
 
 // Items (weight loads of one step) in flight per wave in the matrix-core
 // body, for one and two row quads per wave.
-#ifndef GEMV_PF1
 #define GEMV_PF1 2
-#endif
-#ifndef GEMV_PF2
 #define GEMV_PF2 2
-#endif
 
 enum Epi : int {
     EPI_F32 = 0,      // y = v                     (f32 out)
@@ -258,9 +254,7 @@ RT_DEV void gemv_body_pipelined(const GemvArgs& a) {
     };
 
     if (nitems > 0) issue(0, buf[0]);
-#ifndef RT_PROBE_NO_STAGE
     stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, nxb, xs, a.gamma, a.eps);
-#endif
     __syncthreads();
     if (nitems == 0) return;
     (void)rowp;
@@ -283,15 +277,8 @@ RT_DEV void gemv_body_pipelined(const GemvArgs& a) {
                     if (uu < units) {
                         typename F::XU xu;
                         F::load_x(xs, uu, xu);
-#ifdef RT_PROBE_NO_DOT
-#pragma unroll
-                        for (int i = 0; i < RPL; ++i)
-                            acc[i] += __builtin_bit_cast(
-                                float, ((const uint32_t*)&buf[half][s][i])[1] ^ ((const uint32_t*)&xu)[0]);
-#else
 #pragma unroll
                         for (int i = 0; i < RPL; ++i) acc[i] += F::dot(buf[half][s][i], xu);
-#endif
                     }
                 }
                 if (step == nsteps - 1) {
@@ -428,14 +415,6 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     // Memory order of the prologue: x (and γ), the first tile's epilogue
     // operand, the weights of the first two items; the conversion of x then
     // waits only for x.
-#ifdef RT_PROBE_TIMING
-    uint64_t tp[6];
-    tp[0] = __builtin_amdgcn_s_memtime();
-    const uint64_t rt0 = __builtin_amdgcn_s_memrealtime();
-#define RT_TP(i) tp[i] = __builtin_amdgcn_s_memtime()
-#else
-#define RT_TP(i)
-#endif
     const uint32_t nxb = units * F::UNIT_EL / 32, xb0 = cu0 * F::UNIT_EL / 32;
     const bool one_pass = !a.x_rec && stage_one_pass(nxb);
     XPre xp;
@@ -444,37 +423,24 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
         // (the host launches this form with one slice round, whole K, nsp ≤ 8)
         stage_attn_load(a.x, a.xml, a.xnsp, a.xhd, nxb, xa);
     } else {
-#ifndef RT_PROBE_NO_STAGE
         if (one_pass)
             stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32,
                              a.gamma ? a.gamma + (size_t)xb0 * 32 : nullptr, nxb, xp);
-#endif
     }
     load_tile_aux(0);
-#ifndef RT_XFIRST
 #pragma unroll
     for (int h = 0; h < PF; ++h) issue(h, buf[h]);  // items past nitems load clamped addresses
-#endif
-    RT_TP(1);
     if constexpr (is_attn_x<XT>()) {
         stage_attn_convert<F::Q40PERM>(xa, a.xnsp, nxb, xs);
     } else {
-#ifndef RT_PROBE_NO_STAGE
         // (the host launches whole-K kernels either with x records or with a
         // K that one pass covers)
         if (one_pass)
             stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
         else
             copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
-#endif
     }
-#ifdef RT_XFIRST
-#pragma unroll
-    for (int h = 0; h < PF; ++h) issue(h, buf[h]);
-#endif
-    RT_TP(2);
     lds_barrier();  // the records are in LDS; the weight loads stay in flight
-    RT_TP(3);
     if (nitems == 0) return;
 
     for (uint32_t it = 0; it < nitems; it += PF) {
@@ -489,16 +455,7 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                 const uint32_t uc = valid ? u : 0;
 #pragma unroll
                 for (int rq = 0; rq < RQ; ++rq) {
-#ifdef RT_PROBE_MQ_NODOT
-                    // probe: consume the raw registers without the dot
-                    uint32_t fold = 0;
-                    const uint32_t* rw = (const uint32_t*)&buf[half][rq];
-#pragma unroll
-                    for (uint32_t i = 0; i < sizeof(typename F::Raw) / 4; ++i) fold ^= rw[i];
-                    const float v = (float)(fold & 0xFFFF);
-#else
                     const float v = F::mdot(buf[half][rq], xs, uc, lq);
-#endif
                     acc[rq] += valid ? v : 0.0f;
                 }
                 if (item + PF < nitems) issue(item + PF, buf[half]);
@@ -596,18 +553,6 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
             if (tid == 0) dev_store(a.counters + (size_t)tile * a.cstride, 0u);  // ready for the next call
         }
     }
-#ifdef RT_PROBE_TIMING
-    RT_TP(4);
-    __syncthreads();
-    RT_TP(5);
-    if (threadIdx.x == 0) {
-        uint32_t* o = (uint32_t*)a.out[0] + 20480 + blockIdx.x * 8;  // past the outputs
-        o[0] = (uint32_t)rt0;
-        for (int i = 1; i < 6; ++i) o[i] = (uint32_t)(tp[i] - tp[0]);
-        o[6] = (uint32_t)(__builtin_amdgcn_s_memrealtime() - rt0);
-        o[7] = nitems;
-    }
-#endif
 }
 
 template <class F, int EPI, typename XT, int RPL, int UNR>
@@ -645,9 +590,7 @@ RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
 // the large whole-K launches, whose waves then issue their first loads
 // together instead of queueing behind the weight loads of earlier
 // workgroups on the CU (the register budget stays at 128 per lane).
-#ifndef RT_GEMV_LB
 #define RT_GEMV_LB 1024
-#endif
 #define RT_GEMV_KERNEL2(NAME, FMTM, FMTC, EPI, XT, UNR)                                 \
     extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) NAME##_r1(GemvArgs a) {  \
         gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);  \
@@ -673,9 +616,7 @@ RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
     extern "C" __global__ void __launch_bounds__(512) NAME##_r2(GemvArgs a) {              \
         gemv_mq_or_chunked<FMT, FMT, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);        \
     }
-#ifndef RT_Q6K_WPE
 #define RT_Q6K_WPE 2
-#endif
 
 // Single-block-unit fallback (rows with an odd number of 32-element blocks)
 #define RT_GEMV_KERNEL_S(NAME, FMT, EPI, XT, UNR)                                 \

@@ -129,19 +129,15 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     // conversion (which waits for the activations only)
     const bool one_pass = !a.x_rec && stage_one_pass(nxb);
     XPre xp;
-#ifndef RT_PROBE_NO_STAGE
     if (one_pass)
         stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32,
                          a.gamma ? a.gamma + (size_t)xb0 * 32 : nullptr, nxb, xp);
-#endif
     Item buf;
     issue(0, buf);
-#ifndef RT_PROBE_NO_STAGE
     if (one_pass)
         stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
     else
         copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
-#endif
     lds_barrier();
 
     // results of group g (items 16g .. 16g + n - 1): one store per lane
@@ -168,11 +164,7 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     // slower: the extra outstanding requests only queue.)  Results wait in
     // LDS until the end.
     for (uint32_t j = 0; j < nitems; ++j) {
-#ifndef RT_PROBE_LS_NOCOMMIT
         commit(buf);
-#else
-        if (buf[0][0].x == 0x9E3779B9u) commit(buf);  // probe: commit skipped
-#endif
         issue(j + 1, buf);
         // this lane's row in the slot
         const uint8_t* rowl = wslot + q * RS + ((uintptr_t)row_src(quad_of(j) * 4 + q) & 15);
@@ -181,13 +173,9 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
             const uint32_t u = slot + 16 * st;
             const bool valid = u < units;
             const uint32_t uc = valid ? u : 0;
-#ifndef RT_PROBE_LS_NODOT
             typename F::Raw raw;
             ls_load<F>(rowl, uc, raw, 0);
             const float v = F::mdot(raw, xs, uc, lq);
-#else
-            const float v = __builtin_bit_cast(float, *(const uint32_t*)(rowl + 4 * uc));  // probe
-#endif
             acc += valid ? v : 0.0f;
         }
         // sum over the 16 slots of the row (lane bits 2..5)
@@ -203,11 +191,7 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
         flush(g, min(nitems - g * kLsGroup, kLsGroup));
     }
 
-#ifdef RT_PROBE_LS_NOMERGE
-    if (false) {
-#else
     if (S > 1) {
-#endif
         // K split: count this chunk in at each of the wave's quads (lane of
         // row 0 of the item), then the last chunk to arrive sums the chunks
         // in order and runs the epilogue

@@ -1,0 +1,15 @@
+// rt_shared.h — launch-shape constants that the kernels and the host runtime
+// must agree on.  Plain C++ (no HIP types): included by the device sources
+// and by runtime.cpp, so a grid and the kernel it launches cannot disagree.
+#pragma once
+#include <stdint.h>
+
+// Decode attention: query heads per workgroup at a head size.  Head size 128
+// takes 4 (7B-class groups of 7 query heads then take two workgroups per KV
+// head, twice the workgroups of one block of 8: 12.6 → ~11 µs per 7B layer
+// at kv_len 512); head sizes 64 and 256 take 8.
+constexpr uint32_t rt_attn_gm(uint32_t head_dim) { return head_dim == 128 ? 4u : 8u; }
+// Head groups of 256 threads per workgroup (registers bound head size 256 to one).
+constexpr uint32_t rt_attn_hg(uint32_t head_dim) {
+    return head_dim == 64 ? 4u : head_dim == 128 ? 2u : 1u;
+}

@@ -7,6 +7,7 @@
 // validate their arguments, pick a launch shape for the problem and enqueue;
 // nothing synchronises until rt_flush (context.rs:289-296).
 #include <hip/hip_runtime.h>
+#include "rt_shared.h"
 #include <dlfcn.h>
 
 #include <algorithm>
@@ -186,6 +187,7 @@ constexpr uint32_t kLsMaxNI = 3;
 constexpr int kLsDecline = -1;
 constexpr uint32_t kLsThreads = 256;
 constexpr uint32_t kLsRowPad = 48;      // LDS row stride = NI KB + pad (bank spread)
+constexpr uint32_t kPrepassK = 8192;    // K from which x is converted once by a pre-pass
 
 struct Fmt {
     uint32_t blk_el, blk_bytes, unit_el;  // unit_el: elements per lane unit (v_dot4 path)
@@ -236,12 +238,6 @@ struct rt_ctx {
     size_t max_lds = 65536;
     std::string err = "no error";
     bool capturing = false;
-    // Tuning knob: RUNIT_GEMV_PLAN="T,TL,rpl" forces one launch plan for
-    // every GEMV-family call (sweeps only; validated at context creation).
-    Plan plan_override{};
-    uint32_t grid_per_cu = 0;  // RUNIT_GEMV_GRID_PER_CU: persistent-grid cap (sweeps only)
-    uint32_t ksw_override = 0;  // RUNIT_GEMV_KSW: K-split waves (sweeps only)
-    uint32_t attn_split_override = 0;  // RUNIT_ATTN_SPLIT: most KV splits (sweeps only)
     bool gemm_direct = false;   // RUNIT_GEMM_DIRECT: force the unstaged GEMM kernel (tests)
     bool ksplit_enabled = true; // RUNIT_GEMV_KSPLIT=0: long K via the pre-pass instead (tests)
     // Workspace for activation records built by the long-K pre-pass; grows on
@@ -253,17 +249,9 @@ struct rt_ctx {
     size_t part_bytes = 0;
     void* attn_out = nullptr;  // attention output between the two launches of
     size_t attn_out_bytes = 0;  // the unmerged attention + o_proj sequence
-    uint32_t prepass_k = 8192;  // RUNIT_PREPASS_K: K from which x is converted once
     bool ls_enabled = true;      // RUNIT_GEMV_LS=0: the per-lane-load matrix-core body instead
-    uint32_t ls_pad = kLsRowPad; // RUNIT_GEMV_LS_PAD (sweeps only)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
-    uint32_t ls_threads = 0;     // RUNIT_GEMV_LS_THREADS: force the block size (sweeps)
-    uint32_t ls_xcd = 1;         // RUNIT_GEMV_LS_XCD=0: plain workgroup order (sweeps)
-    uint32_t ls_chunk = 0;       // RUNIT_GEMV_LS_CHUNK: K-split chunk bytes per row (sweeps)
-    uint32_t pair_threads = 0;   // RUNIT_GEMV_PAIR_THREADS: two-part launch block size (sweeps)
-    uint32_t gemm_waves = 0;     // RUNIT_GEMM_WAVES=4|8: force the staged GEMM's block (sweeps)
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
-    bool lsk_enabled = true;     // RUNIT_GEMV_LSK=0: K splits over workgroups (through memory) instead
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
     void* aux = nullptr;
@@ -339,7 +327,6 @@ uint32_t occupancy(rt_ctx* c, const char* name, uint32_t threads, size_t lds) {
 Plan plan_gemv(const rt_ctx* c, const Fmt& f, uint32_t nvrows, uint32_t K, bool paired) {
     const uint32_t units = K / f.unit_el;
     Plan p{};
-    if (c->plan_override.T) return c->plan_override;
     p.T = (K / 32 >= 256) ? 512 : 256;
     p.TL = 0;
     for (uint32_t tl = 16; tl <= p.T; tl *= 2) {
@@ -435,7 +422,7 @@ int gemv_launch_lsk(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     const uint32_t nwv = t / 64;
     a.ksplit = S;
     a.kc_units = kc;
-    a.ls_rs = 1024 + c->ls_pad;
+    a.ls_rs = 1024 + kLsRowPad;
     const size_t xbytes = (size_t)(a.K / 32) * XREC_BYTES;
     uint32_t nwg = 0, occ = 1;
     size_t lds = 0;
@@ -445,7 +432,7 @@ int gemv_launch_lsk(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
         lds = xbytes + (size_t)nql * S * 16 + (size_t)nwv * 4 * a.ls_rs;
         if (lds > c->max_lds) return kLsDecline;
         occ = occupancy(c, name, t, lds);
-        const uint32_t want = std::min<uint32_t>(nq, (uint32_t)c->cu_count * (c->grid_per_cu ? c->grid_per_cu : occ));
+        const uint32_t want = std::min<uint32_t>(nq, (uint32_t)c->cu_count * occ);
         if (want == g && nwg) break;
         nwg = want;
     }
@@ -474,7 +461,7 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
         // number of blocks, ≤ one staging pass (the 7B down projections:
         // Q6_K 21.5 → 19.9 µs, Q4_0 15.2 → 14.5 µs with 3 KB against 2 KB
         // chunks; 1 KB chunks are slower still)
-        const uint32_t chunk = c->ls_chunk ? c->ls_chunk : f.ls_chunk;
+        const uint32_t chunk = f.ls_chunk;
         uint32_t cap = (uint32_t)((chunk - 15) * (uint64_t)f.blk_el / ubytes_num);
         cap = std::min<uint32_t>(cap, max_recs * 32 / ue);
         cap -= cap % gu;
@@ -487,13 +474,13 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
         if (NI > kLsMaxNI) return kLsDecline;
     }
     const uint32_t nq = (a.nvrows + 3) / 4;
-    if (S > 1 && c->lsk_enabled && !a.gamma) {
+    if (S > 1 && !a.gamma) {
         const int st = gemv_launch_lsk(c, kname, f, a);
         if (st != kLsDecline) return st;
     }
     a.ksplit = S;
     a.kc_units = kc;
-    a.ls_rs = NI * 1024 + c->ls_pad;
+    a.ls_rs = NI * 1024 + kLsRowPad;
     // The body pays off from ~16 items (row quads × K chunks) per CU: the
     // 7B FFN / down / LM-head launches; launches with fewer items (the QKV
     // and attention projections, the 0.5B model's GEMVs) run faster on the
@@ -511,7 +498,6 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     uint32_t bt = 0, bg = 0, bres = 0, bwaves = 0;
     size_t blds = 0;
     for (uint32_t t = 256; t <= tmax; t *= 2) {
-        if (c->ls_threads && t != c->ls_threads) continue;
         const uint32_t nwv = t / 64;
         uint32_t res = 16, g = 0, occ = 0;
         size_t lds = 0;
@@ -519,7 +505,7 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
             lds = xbytes + (size_t)nwv * res * 16 + (size_t)nwv * 4 * a.ls_rs;
             if (lds > c->max_lds) break;
             occ = occupancy(c, name, t, lds);
-            g = std::max<uint32_t>(1, (uint32_t)c->cu_count * (c->grid_per_cu ? c->grid_per_cu : occ) / S);
+            g = std::max<uint32_t>(1, (uint32_t)c->cu_count * occ / S);
             g = std::min<uint32_t>(g, (nq + nwv - 1) / nwv);
             const uint32_t per = (nq + g * nwv - 1) / (g * nwv);
             const uint32_t need = std::min<uint32_t>(64, (per + 15) / 16 * 16);
@@ -535,7 +521,7 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     }
     if (!bt) return kLsDecline;
     a.ls_res = bres;
-    a.ls_xcd = c->ls_xcd;
+    a.ls_xcd = 1;
     if (S > 1) {
         if (nq > kAttnCounters)
             return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: %u row quads exceed %u",
@@ -588,7 +574,7 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
     a.ksplit = S;
     a.kc_units = kcu;
     if (S == 1 && !a.x_rec && !a.gamma && !a.xnsp &&
-        (a.K >= c->prepass_k || (mq_shape && a.K > kOnePassMaxK))) {
+        (a.K >= kPrepassK || (mq_shape && a.K > kOnePassMaxK))) {
         // convert the activations once into the context workspace
         const size_t need = (size_t)nxb * XREC_BYTES;
         const int st0 = ensure_ws(c, need, kname);
@@ -623,7 +609,6 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         // Matrix-core path: a wave covers RQ quads of 4 rows, 16 lanes per
         // row; persistent grid of `gpc` workgroups per CU.
         p = Plan{256, 16, 1};
-        if (c->plan_override.T) p = Plan{c->plan_override.T, 16, c->plan_override.rpl};
         if (!a.x_rec && recs * 8 > 4 * p.T) p.T = 512;  // one staging pass
         // large whole-K launches of the two-items-in-flight formats (4- and
         // 5-bit): one 1024-thread workgroup per CU, whose 16 waves issue
@@ -631,7 +616,7 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         // and Q6_K keep one item in flight per wave and run slower so; Q6_K's
         // ~240-register kernels are built for 512 threads.)
         const bool one_item = f.blk_bytes == 34 || mq_el == 256;
-        if (!c->plan_override.T && S == 1 && a.K >= 2048 && !one_item && !a.xnsp) p.T = 1024;
+        if (S == 1 && a.K >= 2048 && !one_item && !a.xnsp) p.T = 1024;
         // split K over the waves of a workgroup while the split waves still
         // fit in the resident waves (latency-bound small problems; a split
         // past that leaves a second round of workgroups as a tail)
@@ -641,10 +626,9 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         const uint32_t resident_waves = (uint32_t)c->cu_count * 16;
         uint32_t ksw = 1;
         while (ksw < nwaves && quads * S * ksw * 2 <= resident_waves && ksw * 2 <= nsteps) ksw *= 2;
-        if (c->ksw_override) ksw = std::min<uint32_t>(c->ksw_override, nwaves);
         a.ksw = ksw;
         rows_per_wg = (nwaves / ksw) * 4 * p.rpl;
-        resident = c->grid_per_cu ? c->grid_per_cu : 4;
+        resident = 4;
         // never more than the kernel's occupancy allows (registers / LDS)
         char rn[96];
         snprintf(rn, sizeof rn, "%s_r%u", kname, p.rpl);
@@ -671,7 +655,6 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         rows_per_wg = (p.T / p.TL) * (paired ? 2 * p.rpl : p.rpl);
         resident = std::min<uint32_t>(2048 / p.T, (uint32_t)(160 * 1024 / lds));
         resident = std::max<uint32_t>(resident, 1);
-        if (c->grid_per_cu) resident = std::min<uint32_t>(resident, c->grid_per_cu);
     }
     a.lpr = p.TL;
     const uint32_t ntiles = (a.nvrows + rows_per_wg - 1) / rows_per_wg;
@@ -805,7 +788,7 @@ int qkv_pair_launch(rt_ctx* c, const char* kname_bias, const char* kname_nobias,
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: k=%u exceeds the staged %u",
                     kname, k, (uint32_t)((std::min<size_t>(c->max_lds, 80 * 1024) - red_bytes) /
                                          XREC_BYTES * 32));
-    uint32_t threads = c->pair_threads ? c->pair_threads : 512;
+    uint32_t threads = 512;
     GemvArgs a{};  // Q and K
     a.w[0] = (const uint8_t*)wq; a.w[1] = (const uint8_t*)wk; a.w[2] = (const uint8_t*)wk;
     a.out[0] = oq; a.out[1] = ok; a.out[2] = ok;
@@ -846,7 +829,6 @@ int qkv_pair_launch(rt_ctx* c, const char* kname_bias, const char* kname_nobias,
                             std::max<uint32_t>(1, occupancy(c, name, threads, lds));
     uint32_t ka, kb;
     pair_ksw(fa, a.nvrows, fb, b.nvrows, k, nwaves, budget, ka, kb);
-    if (c->ksw_override) ka = kb = std::min<uint32_t>(c->ksw_override, nwaves);
     const uint32_t ga = pair_part_grid(fa, a, threads, ka);
     const uint32_t gb = pair_part_grid(fb, b, threads, kb);
     a.blk0 = 0; a.nblk = ga;
@@ -919,43 +901,13 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, 0) == hipSuccess &&
         lds > 0)
         c->max_lds = (size_t)lds;
-    if (const char* ov = getenv("RUNIT_GEMV_PLAN")) {
-        unsigned T = 0, TL = 0, r = 0;
-        if (sscanf(ov, "%u,%u,%u", &T, &TL, &r) == 3 && (T == 64 || T == 128 || T == 256 || T == 512 || T == 1024) &&
-            TL >= 1 && TL <= T && (TL & (TL - 1)) == 0 && (r == 1 || r == 2))
-            c->plan_override = Plan{T, TL, r};
-    }
-    if (const char* g = getenv("RUNIT_GEMV_GRID_PER_CU")) c->grid_per_cu = (uint32_t)atoi(g);
-    if (const char* g = getenv("RUNIT_PREPASS_K")) c->prepass_k = (uint32_t)atoi(g);
+    // A/B switches between the kernel bodies (tests and measurements)
     if (const char* g = getenv("RUNIT_GEMM_DIRECT")) c->gemm_direct = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_F16")) c->gemm_f16 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
-    if (const char* g = getenv("RUNIT_ATTN_SPLIT")) c->attn_split_override = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
-    if (const char* g = getenv("RUNIT_GEMV_LS_THREADS")) c->ls_threads = (uint32_t)atoi(g);
-    if (const char* g = getenv("RUNIT_GEMV_LS_XCD")) c->ls_xcd = (uint32_t)atoi(g);
-    if (const char* g = getenv("RUNIT_GEMV_LSK")) c->lsk_enabled = atoi(g) != 0;
-    if (const char* g = getenv("RUNIT_GEMV_LS_CHUNK")) {
-        const uint32_t v = (uint32_t)atoi(g);
-        if (v >= 512 && v <= 3072) c->ls_chunk = v;
-    }
-    if (const char* g = getenv("RUNIT_GEMV_PAIR_THREADS")) {
-        const uint32_t t = (uint32_t)atoi(g);
-        if (t == 256 || t == 512 || t == 1024) c->pair_threads = t;
-    }
-    if (const char* g = getenv("RUNIT_GEMM_WAVES")) {
-        const int v = atoi(g);
-        if (v == 4 || v == 8) c->gemm_waves = (uint32_t)v;
-    }
-    if (const char* g = getenv("RUNIT_GEMV_LS_PAD")) c->ls_pad = (uint32_t)atoi(g) & ~15u;
-    if (const char* g = getenv("RUNIT_GEMV_KSW")) {
-        const int v = atoi(g);
-        if (v == 1 || v == 2 || v == 4 || v == 8) c->ksw_override = (uint32_t)v;
-    }
-    const char* env_co = getenv("RUNIT_CODE_OBJECT");
-    std::string path = code_object_path ? std::string(code_object_path)
-                                        : (env_co ? std::string(env_co) : default_code_object_path());
+    std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
     e = hipModuleLoad(&c->module, path.c_str());
     if (e != hipSuccess) {
         delete c;
@@ -1439,9 +1391,7 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
     if (nblk % NB != 0 || !aligned(w, 16) || row_bytes % vb != 0 || c->gemm_direct)
         return kLsDecline;
     const bool w8ok = f.blk_bytes != 210;
-    const uint32_t waves = (c->gemm_waves && (c->gemm_waves == 4 || w8ok))
-                               ? c->gemm_waves
-                               : (MG >= 2 && f.blk_bytes != 34 && w8ok ? 8 : 4);
+    const uint32_t waves = (MG >= 2 && f.blk_bytes != 34 && w8ok ? 8 : 4);
     char kn[48];
     snprintf(kn, sizeof kn, waves == 8 ? "k_gemm3_%s_mg%u_w8" : "k_gemm3_%s_mg%u", f.name, MG);
     if (!c->fns.count(kn)) return kLsDecline;
@@ -1541,9 +1491,7 @@ int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, floa
     // stage (Q4_K at M = 32: 90 → 61 µs; Q8_0 runs slower so: 55 → 66 µs).
     // (Q6_K: 4-wave workgroups only, its two-super-block stages fill LDS)
     const bool w8ok = f.blk_bytes != 210;
-    const uint32_t waves = (c->gemm_waves && (c->gemm_waves == 4 || w8ok))
-                               ? c->gemm_waves
-                               : (MG >= 4 && f.blk_bytes != 34 && w8ok ? 8 : 4);
+    const uint32_t waves = (MG >= 4 && f.blk_bytes != 34 && w8ok ? 8 : 4);
     char kn2[48];
     if (waves == 8)
         snprintf(kn2, sizeof kn2, "k_gemm2_%s_mg%u_w8", f.name, MG);
@@ -1787,11 +1735,16 @@ int norm_then(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a, bool paire
         a.eps = eps;
         return gemv_launch(c, kname, f, a, false, paired);
     }
-    int st = ensure_ws(c, (size_t)a.K * sizeof(float), kname);
+    // The normalised x sits past the activation-record area at the start of
+    // the workspace: a pre-pass of the GEMV writes its records there, and
+    // must never overwrite input that other workgroups have not read yet.
+    const size_t rec_off = ((size_t)(a.K / 32) * XREC_BYTES + 255) & ~(size_t)255;
+    int st = ensure_ws(c, rec_off + (size_t)a.K * sizeof(float), kname);
     if (st != RT_OK) return st;
-    st = rt_rms_norm_f32_f32_f32g(c, (const float*)a.x, (float*)c->ws, gamma, eps, a.K, 1);
+    float* xn = (float*)((char*)c->ws + rec_off);
+    st = rt_rms_norm_f32_f32_f32g(c, (const float*)a.x, xn, gamma, eps, a.K, 1);
     if (st != RT_OK) return st;
-    a.x = c->ws;
+    a.x = xn;
     return gemv_launch(c, kname, f, a, false, paired);
 }
 
@@ -1871,7 +1824,6 @@ struct AttnArgs {
 // head groups about two workgroups per CU
 static uint32_t attn_chunk(rt_ctx* c, uint32_t kv_len, uint32_t groups, uint32_t max_split_cap = 0) {
     uint32_t max_split = std::max<uint32_t>(1, 2 * c->cu_count / groups);
-    if (c->attn_split_override) max_split = c->attn_split_override;
     if (max_split_cap) max_split = std::min(max_split, max_split_cap);
     const uint32_t n64 = std::max<uint32_t>(1, (kv_len + 63) / 64);
     return (n64 + max_split - 1) / max_split * 64;
@@ -1883,8 +1835,8 @@ static uint32_t attn_nsplit(rt_ctx* c, uint32_t kv_len, uint32_t groups) {
 
 static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch,
                        uint32_t max_split_cap = 0, AttnArgs* used = nullptr) {
-    // query heads per workgroup, as the kernels' attn_gm<HD>()
-    const uint32_t gm = strstr(kname, "hd128") ? 4 : 8;
+    const uint32_t hd = strstr(kname, "hd256") ? 256 : strstr(kname, "hd128") ? 128 : 64;
+    const uint32_t gm = rt_attn_gm(hd);  // query heads per workgroup, as the kernel's
     const uint32_t G = a.H / a.KVH, HB = (G + gm - 1) / gm;
     const uint32_t groups = batch * a.KVH * HB;
     a.chunk = attn_chunk(c, a.kv_len, groups, max_split_cap);
@@ -1895,7 +1847,6 @@ static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch,
                         "kernel dispatch error: attention: %u head groups exceed %u", groups,
                         kAttnCounters);
         const size_t rows = (size_t)batch * a.H * nsplit;
-        const size_t hd = (size_t)(strstr(kname, "hd256") ? 256 : strstr(kname, "hd128") ? 128 : 64);
         int st = ensure_ws(c, rows * (hd + 2) * sizeof(float), kname);
         if (st != RT_OK) return st;
         a.part = (float*)c->ws;
@@ -1904,8 +1855,7 @@ static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch,
     }
     if (used) *used = a;
     void* params[] = {&a};
-    // 256 threads per head group (the kernels' HG: 4 at head size 64, 2 at 128)
-    const uint32_t nt = strstr(kname, "hd64") ? 1024 : strstr(kname, "hd128") ? 512 : 256;
+    const uint32_t nt = 256 * rt_attn_hg(hd);  // 256 threads per head group
     return launch(c, kname, dim3(nsplit, a.KVH * HB, batch), dim3(nt), 0, params);
 }
 
@@ -1993,10 +1943,10 @@ int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const
     // splits the KV range in 2..8 (one split has no merge to save; more
     // splits than the projection stages would slow the attention down);
     // otherwise: attention, then the GEMV.
-    const uint32_t gm = head_dim == 128 ? 4 : 8;  // query heads per attention workgroup
+    const uint32_t gm = rt_attn_gm(head_dim);  // query heads per attention workgroup
     const uint32_t nsplit0 =
         attn_nsplit(c, pos + 1, num_kv_heads * ((num_heads / num_kv_heads + gm - 1) / gm));
-    const bool merged = q_dim % 64 == 0 && q_dim / 32 * 8 <= 256 && !c->plan_override.T &&
+    const bool merged = q_dim % 64 == 0 && q_dim / 32 * 8 <= 256 &&
                         nsplit0 >= 2 && nsplit0 <= kAttnXMaxSplits;
     AttnArgs a{};
     a.q = q_raw;

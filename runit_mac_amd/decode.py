@@ -232,8 +232,9 @@ class DecodeModel:
         return cls(ctx, cfg, gguf=gguf)
 
     def set_token(self, tok: int) -> None:
-        d.load_library().rt_upload(self.ctx.handle, self.token,
-                                   np.array([tok], np.uint32).ctypes.data, 4)
+        buf = np.array([tok], np.uint32)  # kept alive across the synchronous copy
+        self.ctx._check(d.load_library().rt_upload(self.ctx.handle, self.token,
+                                                   buf.ctypes.data, 4))
 
     def get_token(self) -> int:
         out = np.zeros(1, np.uint32)

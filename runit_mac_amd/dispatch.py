@@ -298,7 +298,7 @@ class HipContext:
     def __init__(self, code_object: str | None = None):
         self.lib = load_library()
         h = c_void_p()
-        path = (code_object or os.environ.get("RUNIT_CODE_OBJECT") or HSACO_PATH).encode()
+        path = (code_object or HSACO_PATH).encode()
         st = self.lib.rt_ctx_create(ctypes.byref(h), path)
         if st != 0:
             raise _STATUS.get(st, KernelError)(self.lib.rt_global_last_error().decode())

@@ -41,6 +41,9 @@ _lib.ora_argmax_f32.argtypes = [_P, _S]
 _lib.ora_argmax_f32.restype = ctypes.c_uint32
 _lib.ora_synth_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
 _lib.ora_synth_normal.restype = ctypes.c_float
+_lib.ora_synth_normal_f32.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float,
+                                      ctypes.c_float, _P]
+_lib.ora_synth_weights.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_float, _S, _P]
 _lib.ora_rms_norm.argtypes = [_P, _P, ctypes.c_double, _S, _S, _P]
 _lib.ora_rope.argtypes = [_P, _S, _S, ctypes.c_uint32, ctypes.c_float]
 _lib.ora_attention.argtypes = [_P, _P, _P, _S, _S, _S, _S, _S, ctypes.c_double, _P]
@@ -108,8 +111,12 @@ def argmax(v: np.ndarray) -> int:
     return int(_lib.ora_argmax_f32(_p(v), v.size))
 
 
-def synth_normal(seed: int, n: int, start: int = 0) -> np.ndarray:
-    return np.array([_lib.ora_synth_normal(seed, start + i) for i in range(n)], dtype=np.float32)
+def synth_normal(seed: int, n: int, start: int = 0, mean: float = 0.0,
+                 std: float = 1.0) -> np.ndarray:
+    """mean + std·N(seed, i) for i in [start, start + n), in f32 arithmetic."""
+    out = np.empty(start + n, dtype=np.float32)
+    _lib.ora_synth_normal_f32(seed, start + n, mean, std, _p(out))
+    return out[start:]
 
 
 def quantize(fmt: str, w: np.ndarray) -> np.ndarray:
@@ -131,9 +138,14 @@ def relayout_to_ggml(fmt: str, packed: np.ndarray) -> np.ndarray:
 
 
 def synth_weights(fmt: str, n: int, k: int, seed: int, std: float = 0.02) -> np.ndarray:
-    """Host twin of the device generator (libm transcendental functions)."""
-    w = (std * synth_normal(seed, n * k)).astype(np.float32)
-    return quantize(fmt, w)
+    """Host twin of the device generators (rt_synth_*): the same bytes."""
+    el, by = BLOCK[fmt]
+    nblk = n * k // el
+    if fmt.endswith("g"):  # ggml layouts: the reference-layout blocks re-laid out
+        return quantize(fmt, synth_normal(seed, n * k, std=std))
+    out = np.empty(nblk * by, dtype=np.uint8)
+    _lib.ora_synth_weights(FMT[fmt], seed, std, nblk, _p(out))
+    return out
 
 
 def rms_norm(x: np.ndarray, gamma: np.ndarray, eps: float) -> np.ndarray:

@@ -84,7 +84,7 @@ def test_config4_q6k_lm_head_argmax(ctx):
     assert int(res.read(np.uint32, 1)[0]) == ora.argmax(yref.astype(np.float32))
 
 
-@pytest.mark.parametrize("m", [1, 4, 16, 32])
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 32])
 def test_config5_gemm_q8_0_7b(ctx, m):
     for n, k, s in ((18944, 3584, 71), (3584, 18944, 72)):
         wbuf, raw = device_weights(ctx, "q8_0", n, k, s + m)

@@ -122,25 +122,45 @@ def test_q4k_m_mix_step_matches_cpu_oracle(ctx):
     m.free()
 
 
-def test_full_depth_fused_vs_reference_sequence_and_graph(ctx):
-    cfg = DecodeConfig()  # 24 layers, 0.5B shapes
+def check_logits(got, ref, what):
+    """Logits within 1e-3 of the oracle's spread; the greedy token equal to
+    the oracle's unless its top-2 gap is inside that tolerance (then the GPU's
+    token must be one of the tied candidates)."""
+    tol = 1e-3 * (ref.max() - ref.min())
+    err = np.max(np.abs(got - ref))
+    assert err <= tol, (what, err, tol)
+    top = int(np.argmax(ref))
+    tok = ora.argmax(got.astype(np.float32))
+    if tok != top:
+        assert ref[top] - ref[tok] <= 2 * tol, (what, tok, top, ref[top] - ref[tok])
+    return tok
+
+
+def test_full_depth_step_matches_cpu_oracle(ctx):
+    """BASELINE config 2 as specified: 24 layers at 0.5B shapes, kv_len 512.
+    The reference's 10-launch sequence (eager) and the fused 5-launch
+    sequence (captured graph, replayed 3 times with the cache restored) are
+    both compared with the f64 oracle composition of forward.rs:1494-1771."""
+    cfg = DecodeConfig()
     m = DecodeModel(ctx, cfg, seed=5)
-    pos = 511
+    tok, pos = 42, 511
     snap = snapshot_cache(m)
-    m.set_token(42)
+    ref = cpu_step(m, tok, pos)
+    restore_cache(m, snap)
+    m.set_token(tok)
     m.step_reference(pos)
     ctx.flush()
-    ref = m.read(m.logits, cfg.vocab).astype(np.float64)
-    tok_ref = m.get_token()
+    t_ref = check_logits(m.read(m.logits, cfg.vocab).astype(np.float64), ref, "reference seq")
+    assert m.get_token() == t_ref
     restore_cache(m, snap)
-    m.set_token(42)
+    m.set_token(tok)
     g = m.capture(pos, fused=True)
-    for _ in range(3):  # replays: each re-embeds token 42? no — the token buffer feeds back
+    for replay in range(3):
         restore_cache(m, snap)
-        m.set_token(42)
+        m.set_token(tok)
         g.launch()
         ctx.flush()
-        got = m.read(m.logits, cfg.vocab).astype(np.float64)
-        assert np.max(np.abs(got - ref)) <= 1e-3 * (ref.max() - ref.min())
-        assert m.get_token() == tok_ref
+        t = check_logits(m.read(m.logits, cfg.vocab).astype(np.float64), ref, f"replay {replay}")
+        assert m.get_token() == t
+    del g
     m.free()

@@ -290,6 +290,48 @@ def test_synth_normal_moments():
     assert abs(z.mean()) < 0.03 and abs(z.std() - 1.0) < 0.03
 
 
+def _splitmix64(z: int) -> int:
+    m = (1 << 64) - 1
+    z = (z + 0x9E3779B97F4A7C15) & m
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+    return z ^ (z >> 31)
+
+
+def test_synth_normal_is_box_muller_of_splitmix():
+    """The generator's definition, written independently with Python's
+    integers and libm in f64: u1 = (h>>40 + 1)·2^-24, u2 = (h & 2^24−1)·2^-24,
+    z = √(−2 ln u1)·cos(2π u2).  The oracle's own ln / cos (correctly rounded
+    f32 operations only, so that the device reproduces its bits) stay within
+    a few f32 ulps of it."""
+    import math
+    seed, n = 1234, 4000
+    got = ora.synth_normal(seed, n).astype(np.float64)
+    worst = 0.0
+    for i in range(n):
+        h = _splitmix64(seed ^ _splitmix64(i))
+        u1 = ((h >> 40) + 1) * 2.0 ** -24
+        u2 = (h & 0xFFFFFF) * 2.0 ** -24
+        z = math.sqrt(-2.0 * math.log(u1)) * math.cos(2.0 * math.pi * u2)
+        worst = max(worst, abs(got[i] - z) / max(1.0, abs(z)))
+    assert worst < 4e-6, worst
+    # shifted windows are slices of the same stream; mean / std scale in f32
+    assert np.array_equal(ora.synth_normal(seed, 10, start=100), ora.synth_normal(seed, 110)[100:])
+    z32 = ora.synth_normal(seed, 64)
+    assert np.array_equal(ora.synth_normal(seed, 64, mean=1.0, std=0.02),
+                          np.float32(1.0) + np.float32(0.02) * z32)
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k"])
+def test_synth_weights_are_the_quantised_stream(fmt):
+    """synth_weights(fmt) = the BASELINE quantiser applied to 0.02·N(seed, i)."""
+    el, _ = ora.BLOCK[fmt]
+    n, k = 8, 2 * 256
+    raw = ora.synth_weights(fmt, n, k, seed=77)
+    w = np.float32(0.02) * ora.synth_normal(77, n * k)
+    assert np.array_equal(raw, ora.quantize(fmt, w))
+
+
 # ───────────────────────── decode glue oracles ─────────────────────────
 
 def test_rms_norm_closed_forms():
