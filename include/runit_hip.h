@@ -180,6 +180,20 @@ int rt_gemv_q6k_add_f32_f32in(rt_ctx* ctx, const void* weight_q6k, const float* 
                               float* output, const float* residual, uint32_t m, uint32_t k);
 int rt_gemv_q6k_f32in(rt_ctx* ctx, const void* weight_q6k, const float* input,
                       uint16_t* output, uint32_t m, uint32_t k);
+/* No counterpart in the reference.  rt_gemv_q6k_add_f32_f32in for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops that forbid hipMalloc): it calls no hipMalloc / hipFree and takes its
+ * K-split partial sums, activation records and arrival counters from a fixed
+ * 4 MiB array in the code object (one per device, held until the process
+ * ends) instead of the context's on-demand workspace.  Same kernels and
+ * results as rt_gemv_q6k_add_f32_f32in.  Shapes needing more than the
+ * array's regions (K-split partials: ~2.9 MiB, i.e. chunks × m floats;
+ * activation records: 1 MiB) return RT_ERR_DISPATCH.  All calls on one
+ * device share the array, which keeps the last call's contents: calls that
+ * overlap on one device (two contexts or streams) race. */
+int rt_gemv_q6k_add_f32_f32in_noalloc(rt_ctx* ctx, const void* weight_q6k, const float* input,
+                                      float* output, const float* residual, uint32_t m,
+                                      uint32_t k);
 
 /* ───────────────────────── Q5_0 / Q5_K GEMV (new) ─────────────────────────
  * The reference has no Q5 GEMVs: the loader dequantises Q5_0 (forward.rs:

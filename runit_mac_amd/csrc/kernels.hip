@@ -5,3 +5,4 @@
 #include "k_aux.hip"
 #include "k_decode.hip"
 #include "k_gemm.hip"
+#include "k_scratch.hip"

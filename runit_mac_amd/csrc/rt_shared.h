@@ -13,3 +13,13 @@ constexpr uint32_t rt_attn_gm(uint32_t head_dim) { return head_dim == 128 ? 4u :
 constexpr uint32_t rt_attn_hg(uint32_t head_dim) {
     return head_dim == 64 ? 4u : head_dim == 128 ? 2u : 1u;
 }
+
+// Device scratch of the no-allocation entry points: one fixed array in the
+// code object (k_scratch.hip), laid out as [arrival counters | activation
+// workspace | K-split partial sums].
+constexpr uint64_t RT_SCRATCH_BYTES = 4ull << 20;
+constexpr uint64_t RT_SCRATCH_COUNTER_BYTES = 56ull << 10;  // as the context's counter area
+constexpr uint64_t RT_SCRATCH_WS_OFF = 64ull << 10;
+constexpr uint64_t RT_SCRATCH_WS_BYTES = 1ull << 20;
+constexpr uint64_t RT_SCRATCH_PART_OFF = RT_SCRATCH_WS_OFF + RT_SCRATCH_WS_BYTES;
+constexpr uint64_t RT_SCRATCH_PART_BYTES = RT_SCRATCH_BYTES - RT_SCRATCH_PART_OFF;

@@ -65,6 +65,7 @@ constexpr size_t kAuxBytes = 65536;
 constexpr uint32_t kAttnCounters = (kAuxBytes - kAuxAttnOff) / 4;
 
 const char* const kKernelNames[] = {
+    "k_fill_u32",
     "k_gemv_q8_0_f32_f32_r1", "k_gemv_q8_0_f32_f32_r2", "k_gemv_q8_0_attn_f32add_r1",
     "k_gemv_q8_0_f32_f32add_r1", "k_gemv_q8_0_f32_f32add_r2",
     "k_gemv_q8_0_f32_f16_r1", "k_gemv_q8_0_f32_f16_r2",
@@ -255,6 +256,15 @@ struct rt_ctx {
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
     void* aux = nullptr;
+    // Arrival counters of split launches: the aux buffer's counter area, or
+    // the scratch array's inside a no-allocation call.
+    uint32_t* counters = nullptr;
+    // This device's copy of the code object's `scratch` array (address taken
+    // from the loaded module at context creation), and whether a
+    // no-allocation call is running: then the workspace buffers point into
+    // the scratch array and never grow.
+    uint8_t* scratch = nullptr;
+    bool noalloc = false;
 };
 struct rt_event { hipEvent_t ev; };
 struct rt_graph { hipGraph_t graph; hipGraphExec_t exec; };
@@ -358,6 +368,11 @@ Plan plan_gemv(const rt_ctx* c, const Fmt& f, uint32_t nvrows, uint32_t K, bool 
 // Grows a context buffer to `need` bytes (not during graph capture).
 int ensure_buf(rt_ctx* c, void*& buf, size_t& bytes, size_t need, const char* who) {
     if (need <= bytes) return RT_OK;
+    if (c->noalloc)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: %s: needs %zu bytes of scratch, the no-allocation "
+                    "entry point has %zu",
+                    who, need, bytes);
     if (c->capturing)
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: %s: workspace must be sized before graph capture", who);
@@ -529,7 +544,7 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
         const int st = ensure_part(c, (size_t)S * a.nvrows * sizeof(float), kname);
         if (st != RT_OK) return st;
         a.part = (float*)c->part;
-        a.counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
+        a.counters = c->counters;
         a.cstride = 32;
         while (a.cstride > 1 && (size_t)nq * a.cstride > kAttnCounters) a.cstride >>= 1;
     }
@@ -641,7 +656,7 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
             const int st = ensure_part(c, (size_t)S * a.nvrows * sizeof(float), kname);
             if (st != RT_OK) return st;
             a.part = (float*)c->part;
-            a.counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
+            a.counters = c->counters;
             // one 128-byte line per tile's counter while they fit: arrivals on
             // one line serialise (≈11 ns each) at the end of the kernel
             a.cstride = 32;
@@ -938,6 +953,22 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
         return fail(nullptr, RT_ERR_PIPELINE_CREATE, "failed to allocate context buffer: %s",
                     hipGetErrorString(e));
     }
+    c->counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
+    {
+        // this device's copy of the code object's scratch array
+        hipDeviceptr_t p = nullptr;
+        size_t bytes = 0;
+        e = hipModuleGetGlobal(&p, &bytes, c->module, "scratch");
+        if (e != hipSuccess || !p || bytes != RT_SCRATCH_BYTES) {
+            hipFree(c->aux);
+            hipModuleUnload(c->module);
+            delete c;
+            return fail(nullptr, RT_ERR_PIPELINE_NOT_FOUND,
+                        "code object has no %llu-byte 'scratch' array (%s)",
+                        (unsigned long long)RT_SCRATCH_BYTES, hipGetErrorString(e));
+        }
+        c->scratch = (uint8_t*)p;
+    }
     e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         hipModuleUnload(c->module);
@@ -1190,6 +1221,41 @@ int rt_gemv_q6k_f32in(rt_ctx* c, const void* w, const float* x, uint16_t* y, uin
     return gemv_plain(c, "k_gemv_q6k_f32_f16", kQ6K, w, x, y, nullptr, false, m, k, false);
 }
 
+// rt_gemv_q6k_add_f32_f32in without any device allocation: the K-split
+// partial sums, activation records and arrival counters come from the code
+// object's scratch array instead of the context's workspace (see
+// k_scratch.hip).  The counters are cleared by a fill kernel first.  Shapes
+// whose launch needs more scratch than the array's regions fail with
+// RT_ERR_DISPATCH before their first use of it.
+int rt_gemv_q6k_add_f32_f32in_noalloc(rt_ctx* c, const void* w, const float* x, float* y,
+                                      const float* r, uint32_t m, uint32_t k) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!c->scratch) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: no scratch array");
+    uint32_t* cnt = (uint32_t*)c->scratch;
+    uint32_t zero = 0, ncnt = (uint32_t)(RT_SCRATCH_COUNTER_BYTES / 4);
+    void* fp[] = {&cnt, &zero, &ncnt};
+    int st = launch(c, "k_fill_u32", dim3((ncnt + 255) / 256), dim3(256), 0, fp);
+    if (st != RT_OK) return st;
+    void* const ws = c->ws;
+    void* const part = c->part;
+    uint32_t* const counters = c->counters;
+    const size_t ws_bytes = c->ws_bytes, part_bytes = c->part_bytes;
+    c->noalloc = true;
+    c->counters = cnt;
+    c->ws = c->scratch + RT_SCRATCH_WS_OFF;
+    c->ws_bytes = RT_SCRATCH_WS_BYTES;
+    c->part = c->scratch + RT_SCRATCH_PART_OFF;
+    c->part_bytes = RT_SCRATCH_PART_BYTES;
+    st = gemv_plain(c, "k_gemv_q6k_f32_f32add", kQ6K, w, x, y, r, true, m, k, false);
+    c->noalloc = false;
+    c->counters = counters;
+    c->ws = ws;
+    c->ws_bytes = ws_bytes;
+    c->part = part;
+    c->part_bytes = part_bytes;
+    return st;
+}
+
 // ───────────────────────────── Q5_0 / Q5_K ─────────────────────────────
 
 int rt_gemv_q5_0_f32in_f32out(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m,
@@ -1433,7 +1499,7 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
     }
     uint32_t cstride = 32;
     while (cstride > 1 && (size_t)base * cstride > kAttnCounters) cstride >>= 1;
-    Gemm2Args a2{w, aops, erow, stab, y, part, (uint32_t*)((char*)c->aux + kAuxAttnOff),
+    Gemm2Args a2{w, aops, erow, stab, y, part, c->counters,
                  m_rows, n, nblk, tiles, splits, kbs, nchunks, row_bytes, cstride};
     void* p2[] = {&a2};
     return launch(c, kn, dim3(std::min(base * splits, cap)), dim3(64 * waves), 0, p2);
@@ -1540,7 +1606,7 @@ int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, floa
     if (staged) {
         uint32_t cstride = 32;  // counters on their own cache lines while they fit
         while (cstride > 1 && (size_t)base * cstride > kAttnCounters) cstride >>= 1;
-        Gemm2Args a2{w, aops, etab, stab, y, part, (uint32_t*)((char*)c->aux + kAuxAttnOff),
+        Gemm2Args a2{w, aops, etab, stab, y, part, c->counters,
                      m_rows, n, nblk, tiles, splits, kbs, nchunks, row_bytes, cstride};
         void* p2[] = {&a2};
         return launch(c, kn2, dim3(std::min(base * splits, cap)), dim3(64 * waves), 0, p2);
@@ -1851,7 +1917,7 @@ static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch,
         if (st != RT_OK) return st;
         a.part = (float*)c->ws;
         a.ml = a.part + rows * hd;
-        a.counters = (uint32_t*)((char*)c->aux + kAuxAttnOff);
+        a.counters = c->counters;
     }
     if (used) *used = a;
     void* params[] = {&a};

@@ -98,7 +98,7 @@ _SIGS = {
         "rt_gemv_q4k_add_f32_f32in", "rt_gemv_q4k_add_f16", "rt_gemv_q4k_add_f32res_f16",
         "rt_gemv_q6k_add_f32_f32in", "rt_gemv_q5_0_add_f32_f32in", "rt_gemv_q5k_add_f32_f32in",
         "rt_gemv_q4_0g_add_f32_f32in", "rt_gemv_q4kg_add_f32_f32in", "rt_gemv_q5kg_add_f32_f32in",
-        "rt_gemv_q6kg_add_f32_f32in")},
+        "rt_gemv_q6kg_add_f32_f32in", "rt_gemv_q6k_add_f32_f32in_noalloc")},
     "rt_fused_qkv_q8_0_f32": [_P] + [_P] * 7 + [_U32] * 3,
     "rt_fused_qkv_bias_q8_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
     "rt_fused_qkv_bias_q4_0_f32": [_P] + [_P] * 10 + [_U32] * 3,
@@ -394,6 +394,9 @@ gemv_q4k_add_f32res_f16 = _gemv_add("gemv_q4k_add_f32res_f16")
 gemv_q6k_f32in_f32out = _gemv("gemv_q6k_f32in_f32out")
 gemv_q6k_f32in = _gemv("gemv_q6k_f32in")
 gemv_q6k_add_f32_f32in = _gemv_add("gemv_q6k_add_f32_f32in")
+# no reference counterpart: the same GEMV with no device allocation (a fixed
+# scratch array in the code object), for callers that cannot allocate
+gemv_q6k_add_f32_f32in_noalloc = _gemv_add("gemv_q6k_add_f32_f32in_noalloc")
 # Q5_0 / Q5_K (new: the reference dequantises both on the CPU, forward.rs:900-920, 979-1012)
 gemv_q5_0_f32in_f32out = _gemv("gemv_q5_0_f32in_f32out")
 gemv_q5_0_f32in = _gemv("gemv_q5_0_f32in")
