@@ -201,51 +201,41 @@ def time_workload(ctx, wl: Workload, steps: int, warmup: int) -> dict:
             "tflops": round(wl.flops() / (us * 1e-6) / 1e12, 3)}
 
 
-def cpu_baseline(cfg, seconds: float = 12.0) -> dict:
-    """The reference CPU path (oracle restatement: dequantise a row, then the
-    sequential f32 dot of cpu_gemv, dispatch.rs:1705-1709) on a bounded sample
-    of the decode step: every GEMV of one layer plus the LM head, repeated for
-    ~`seconds`; the per-token time is extrapolated to all layers.  The glue
-    (norm, RoPE, attention over 512 positions) is < 1% of the CPU work and is
-    not timed."""
+def cpu_baseline(model, token: int, pos: int, gpu_token: int, seconds: float = 16.0) -> dict:
+    """The reference CPU path on the config-2 step itself: the oracle's f32
+    restatement of the reference's CPU helpers composed into one greedy decode
+    step (dequantise row → sequential f32 dot of cpu_gemv, dispatch.rs:
+    1705-1709; cpu_rms_norm, RoPE, attention over kv_len 512, SiLU, LM head,
+    argmax) on a host model rebuilt from the GPU model's seeds, byte-identical
+    to the weights and KV cache the GPU step reads.  Timed as whole steps:
+    single-thread (the reference's CPU code is single-threaded) for about
+    3/4 of `seconds`, then with GEMV rows split over every host core."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
     import oracle_lib as ora  # noqa: E402  (test infrastructure: baseline only)
-    rng = np.random.default_rng(1)
-    h, q, kv, ff, vocab = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.ff, cfg.vocab
-
-    def q8(n, k):  # valid Q8_0 blocks with random codes (values do not affect timing)
-        raw = rng.integers(0, 256, size=(n * k // 32, 34), dtype=np.uint8)
-        sc = np.float16(0.0005).view(np.uint16)
-        raw[:, 0], raw[:, 1] = sc & 255, sc >> 8
-        return raw.ravel()
-
-    layer = [(q8(n, k), n, k) for n, k in ((q, h), (kv, h), (kv, h), (h, q), (ff, h), (ff, h),
-                                           (h, ff))]
-    head = (q8(vocab, h), vocab, h)
-    xs = {k: rng.standard_normal(k).astype(np.float32) for k in (h, q, ff)}
-    out, nreps = {}, {}
-    for threads in (1, os.cpu_count() or 1):
-        t_layer = t_head = 0.0
-        reps = 0
-        t0 = time.perf_counter()
-        while time.perf_counter() - t0 < seconds / 2:
-            t1 = time.perf_counter()
-            for w, n, k in layer:
-                ora.gemv_ref_f32("q8_0", w, xs[k], n, k, threads)
-            t2 = time.perf_counter()
-            ora.gemv_ref_f32("q8_0", head[0], xs[h], vocab, h, threads)
-            t3 = time.perf_counter()
-            t_layer += t2 - t1
-            t_head += t3 - t2
-            reps += 1
-        out[threads] = (cfg.layers * t_layer + t_head) / reps
-        nreps[threads] = reps
-    t1, tn = out[1], out[max(out)]
+    t0 = time.perf_counter()
+    host = ora.HostStepModel.from_recipe(model)
+    t_build = time.perf_counter() - t0
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    res = {}
+    for threads, budget in ((1, 0.75 * seconds), (cores, 0.25 * seconds)):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            tok, _ = host.step(token, pos, threads)
+            n += 1
+            if time.perf_counter() - t0 >= budget:
+                break
+        res[threads] = ((time.perf_counter() - t0) / n, n, tok)
+    (t1, n1, tok1), (tn, nn, _) = res[1], res[cores]
     return {"value": round(1.0 / t1, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": (f"config 2 GEMVs of 1 layer + LM head ({nreps[1]} reps, ~{seconds / 2:.0f} s), "
-                       f"extrapolated to {cfg.layers} layers: {t1 * 1e3:.0f} ms/token "
-                       f"single-thread; {max(out)}-thread OpenMP row split "
-                       f"{tn * 1e3:.1f} ms/token ({1.0 / tn:.2f} tok/s)")}
+            "ms_per_token": round(t1 * 1e3, 1), "token": tok1, "gpu_token": gpu_token,
+            "token_match": tok1 == gpu_token,
+            "all_cores": {"value": round(1.0 / tn, 3), "unit": "tok/s", "cores": cores,
+                          "ms_per_token": round(tn * 1e3, 1), "steps": nn},
+            "sample": (f"{n1} whole config-2 decode steps single-thread (token {token} at pos "
+                       f"{pos}, kv_len {pos + 1}, 24 layers + LM head + argmax) on the GPU "
+                       f"model's seeded weights and KV cache rebuilt on the host "
+                       f"({t_build:.1f} s to rebuild), then {nn} steps with GEMV rows over "
+                       f"{cores} threads")}
 
 
 def bench_decode(ctx, steps: int, warmup: int) -> dict:
@@ -255,6 +245,11 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
     cfg = DecodeConfig()
     m = DecodeModel(ctx, cfg, seed=7)
     pos = 511  # decoding position 511 → kv_len 512
+    # one eager step from token 1: the greedy token the CPU baseline must match
+    m.set_token(1)
+    m.step_fused(pos)
+    ctx.flush()
+    gpu_token = m.get_token()
     m.set_token(1)
     res = {}
     for name, fused in (("fused", True), ("reference_sequence", False)):
@@ -288,10 +283,9 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
     ffn_us = e0.elapsed_ms(e1) * 1e3 / (reps * cfg.layers)
     del g
     ffn_bytes = 2 * d.weight_bytes("q8_0", cfg.ff, cfg.hidden) + 4 * cfg.hidden * 2 + 4 * cfg.ff
-    m.free()
-    return {"cfg": cfg, "ms_fused": res["fused"], "ms_reference": res["reference_sequence"],
+    return {"cfg": cfg, "model": m, "pos": pos, "gpu_token": gpu_token, "ms_fused": res["fused"], "ms_reference": res["reference_sequence"],
             "step_bytes": cfg.step_bytes(pos + 1), "ffn_us": ffn_us, "ffn_bytes": ffn_bytes,
-            "launches_fused": 1 + 5 * cfg.layers + 2,
+            "launches_fused": m.launches_fused(),
             "launches_reference": 1 + 10 * cfg.layers + 3}
 
 
@@ -592,8 +586,14 @@ def main():
                      "dtype": "quant x f32", "config": {"workload": r0["label"]},
                      "roofline": {"bound": "hbm", "achieved": r0["gbs"], "peak": HBM_PEAK_GBS,
                                   "unit": "GB/s", "frac": r0["frac_hbm"], "traffic": None}})
-    if not args.no_cpu and dec is not None:
-        line["cpu_baseline"] = cpu_baseline(dec["cfg"])
+    if dec is not None:
+        if not args.no_cpu:
+            cb = cpu_baseline(dec["model"], 1, dec["pos"], dec["gpu_token"])
+            log(f"cpu baseline: {cb['ms_per_token']} ms/token single-thread, "
+                f"{cb['all_cores']['ms_per_token']} ms/token on {cb['all_cores']['cores']} "
+                f"threads; token {cb['token']} (GPU {cb['gpu_token']})")
+            line["cpu_baseline"] = cb
+        dec["model"].free()
     ctx.close()
     print(json.dumps(line), flush=True)
 

@@ -821,3 +821,93 @@ void ora_synth_weights(int fmt, uint64_t seed, float stdv, size_t nblk, uint8_t*
         free(w);
     }
 }
+
+/* ───────────────── whole decode step, f32 (CPU baseline) ───────────────── */
+
+static void rms_norm_f32(const float* x, const float* g, float eps, size_t n, float* y) {
+    float ss = 0.0f; /* cpu_rms_norm: f32 sum of squares, then /n + eps, sqrt */
+    for (size_t i = 0; i < n; ++i) ss += x[i] * x[i];
+    const float rms = sqrtf(ss / (float)n + eps);
+    for (size_t i = 0; i < n; ++i) y[i] = x[i] / rms * g[i];
+}
+
+static void rope_f32(float* v, size_t heads, size_t hd, uint32_t pos, float theta) {
+    const size_t half = hd / 2;
+    for (size_t d = 0; d < half; ++d) {
+        const float freq = 1.0f / powf(theta, (float)(2 * d) / (float)hd);
+        const float ang = (float)pos * freq, c = cosf(ang), s = sinf(ang);
+        for (size_t h = 0; h < heads; ++h) {
+            float* x = v + h * hd;
+            const float r = x[d], i = x[d + half];
+            x[d] = r * c - i * s;
+            x[d + half] = r * s + i * c;
+        }
+    }
+}
+
+uint32_t ora_decode_step_ref_f32(const ora_model_t* m, uint32_t token, uint32_t pos,
+                                 float* logits, int threads) {
+    const size_t h = m->hidden, hd = m->head_dim, H = m->heads, KVH = m->kv_heads;
+    const size_t qd = H * hd, kvd = KVH * hd, ff = m->ff, S = m->max_seq, kv_len = (size_t)pos + 1;
+    float* x = (float*)malloc(h * sizeof(float));
+    float* xn = (float*)malloc((h > ff ? h : ff) * sizeof(float));
+    float* q = (float*)malloc(qd * sizeof(float));
+    float* k = (float*)malloc(kvd * sizeof(float));
+    float* v = (float*)malloc(kvd * sizeof(float));
+    float* att = (float*)malloc(qd * sizeof(float));
+    float* g = (float*)malloc(ff * sizeof(float));
+    float* u = (float*)malloc(ff * sizeof(float));
+    float* t = (float*)malloc((h > ff ? h : ff) * sizeof(float));
+    float* sc = (float*)malloc(kv_len * sizeof(float));
+    ora_dequant_q8_0(m->embd + (size_t)token * (h / 32) * 34, h / 32, x);
+    const float scale = 1.0f / sqrtf((float)hd);
+    for (uint32_t li = 0; li < m->layers; ++li) {
+        const ora_layer_t* L = &m->layer[li];
+        rms_norm_f32(x, L->attn_norm, m->eps, h, xn);
+        ora_gemv_ref_f32(L->fq, L->wq, xn, qd, h, q, threads);
+        ora_gemv_ref_f32(L->fk, L->wk, xn, kvd, h, k, threads);
+        ora_gemv_ref_f32(L->fv, L->wv, xn, kvd, h, v, threads);
+        for (size_t i = 0; i < qd; ++i) q[i] += ora_h2f(L->bq[i]);
+        for (size_t i = 0; i < kvd; ++i) { k[i] += ora_h2f(L->bk[i]); v[i] += ora_h2f(L->bv[i]); }
+        rope_f32(q, H, hd, pos, m->theta);
+        rope_f32(k, KVH, hd, pos, m->theta);
+        for (size_t j = 0; j < KVH; ++j) {
+            memcpy(L->kc + (j * S + pos) * hd, k + j * hd, hd * sizeof(float));
+            memcpy(L->vc + (j * S + pos) * hd, v + j * hd, hd * sizeof(float));
+        }
+        for (size_t hh = 0; hh < H; ++hh) {
+            const size_t kvh = hh / (H / KVH);
+            const float* qh = q + hh * hd;
+            float mx = -INFINITY;
+            for (size_t j = 0; j < kv_len; ++j) {
+                const float* kr = L->kc + (kvh * S + j) * hd;
+                float dot = 0.0f;
+                for (size_t d = 0; d < hd; ++d) dot += qh[d] * kr[d];
+                sc[j] = dot * scale;
+                mx = fmaxf(mx, sc[j]);
+            }
+            float sum = 0.0f;
+            for (size_t j = 0; j < kv_len; ++j) { sc[j] = expf(sc[j] - mx); sum += sc[j]; }
+            float* o = att + hh * hd;
+            for (size_t d = 0; d < hd; ++d) o[d] = 0.0f;
+            for (size_t j = 0; j < kv_len; ++j) {
+                const float p = sc[j] / sum;
+                const float* vr = L->vc + (kvh * S + j) * hd;
+                for (size_t d = 0; d < hd; ++d) o[d] += p * vr[d];
+            }
+        }
+        ora_gemv_ref_f32(L->fo, L->wo, att, h, qd, t, threads);
+        for (size_t i = 0; i < h; ++i) x[i] += t[i];
+        rms_norm_f32(x, L->ffn_norm, m->eps, h, xn);
+        ora_gemv_ref_f32(L->fg, L->wg, xn, ff, h, g, threads);
+        ora_gemv_ref_f32(L->fu, L->wu, xn, ff, h, u, threads);
+        for (size_t i = 0; i < ff; ++i) g[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+        ora_gemv_ref_f32(L->fd, L->wd, g, h, ff, t, threads);
+        for (size_t i = 0; i < h; ++i) x[i] += t[i];
+    }
+    rms_norm_f32(x, m->final_norm, m->eps, h, xn);
+    ora_gemv_ref_f32(m->f_lm, m->lm_head, xn, m->vocab, h, logits, threads);
+    const uint32_t tok = ora_argmax_f32(logits, m->vocab);
+    free(x); free(xn); free(q); free(k); free(v); free(att); free(g); free(u); free(t); free(sc);
+    return tok;
+}

@@ -96,6 +96,38 @@ void ora_attention(const double* q, const float* k, const float* v, size_t num_h
                    size_t num_kv_heads, size_t head_dim, size_t kv_len, size_t kv_stride,
                    double scale, double* out);
 
+/* One greedy decode step of a Qwen2-shape model as the reference's CPU
+ * helpers compute it, in f32 (the timed CPU baseline): embedding row
+ * dequantised (forward.rs:1494-1505); per layer cpu_rms_norm
+ * (dispatch.rs:1699-1702), Q/K/V by dequantise-row + cpu_gemv's sequential
+ * f32 sum (dispatch.rs:1705-1709) plus the f16 bias (fused_qkv.metal:68),
+ * RoPE on (d, d + hd/2) pairs (fused_rope.metal:28-55), the new K/V row
+ * written to the cache at pos (kv_copy_to_cache), softmax attention over
+ * pos + 1 positions with GQA head h → kv head h/(H/KVH) (cpu_attention
+ * dispatch.rs:1712-1742), o_proj + residual, cpu_rms_norm, gate/up GEMVs,
+ * cpu_silu_mul (dispatch.rs:1684-1690), down + residual; final norm, LM head,
+ * greedy_argmax_f32.  `threads` splits GEMV rows over OpenMP threads (the
+ * reference's CPU code is single-threaded: threads = 1).  Updates the KV
+ * caches; writes the logits; returns the greedy token. */
+typedef struct {
+    const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd; /* packed blocks, formats below */
+    const uint16_t *bq, *bk, *bv;                     /* f16 biases */
+    const float *attn_norm, *ffn_norm;
+    float *kc, *vc;                                   /* [kv_heads][max_seq][head_dim] */
+    int32_t fq, fk, fv, fo, fg, fu, fd;               /* ORA_* formats */
+} ora_layer_t;
+typedef struct {
+    uint32_t layers, hidden, heads, kv_heads, head_dim, ff, vocab, max_seq;
+    float eps, theta;
+    const ora_layer_t* layer;
+    const float* final_norm;
+    const uint8_t* embd; /* Q8_0 [vocab][hidden] */
+    const uint8_t* lm_head;
+    int32_t f_lm;
+} ora_model_t;
+uint32_t ora_decode_step_ref_f32(const ora_model_t* m, uint32_t token, uint32_t pos,
+                                 float* logits, int threads);
+
 /* Seeded synthetic data with the same definitions as the device generators
  * (splitmix64 → Box–Muller), used to build golden fixtures on the CPU. */
 float ora_synth_normal(uint64_t seed, uint64_t idx);

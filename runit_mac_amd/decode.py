@@ -128,6 +128,10 @@ class DecodeModel:
         self.arena = Arena(ctx, total)
         a = self.arena
         s = seed * 1000
+        # how every synthetic tensor was generated, in order: (pointer, kind,
+        # seed, count, format or (mean, std)) — a host twin rebuilds the same
+        # bytes from it (the device generators are pinned to the oracle's)
+        self.recipe = []
         lib = d.load_library()
 
         def upload_host(p, arr):
@@ -150,6 +154,7 @@ class DecodeModel:
                 gguf.upload(ctx, name, p)
             else:
                 d.synth_weights(ctx, fmt, p, n * k // d.BLOCK[fmt][0], s)
+                self.recipe.append((p, "w", s, n * k, fmt))
                 s += 1
             return p
 
@@ -166,6 +171,7 @@ class DecodeModel:
                 ctx._check(lib.rt_memset(ctx.handle, p, 0, 4 * n))
             else:
                 d.synth_normal_f32(ctx, p, n, s, mean, std)
+                self.recipe.append((p, "f32", s, n, (mean, std)))
                 s += 1
             return p
 
@@ -183,6 +189,7 @@ class DecodeModel:
                 upload_host(p, v)
             else:
                 d.synth_normal_f16(ctx, p, n, s, 0.0, std)
+                self.recipe.append((p, "f16", s, n, (0.0, std)))
                 s += 1
             return p
 

@@ -174,3 +174,79 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, num_heads: int, num_k
     _lib.ora_attention(_p(q), _p(k), _p(v), num_heads, num_kv_heads, head_dim, kv_len,
                        kv_stride, scale, _p(out))
     return out
+
+
+# ───────────────────────── whole decode step (f32, CPU baseline) ─────────────────────────
+
+class _Layer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("wq", "wk", "wv", "wo", "wg", "wu", "wd", "bq", "bk", "bv", "attn_norm",
+                 "ffn_norm", "kc", "vc")] + \
+               [(n, ctypes.c_int32) for n in ("fq", "fk", "fv", "fo", "fg", "fu", "fd")]
+
+
+class _Model(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in
+                ("layers", "hidden", "heads", "kv_heads", "head_dim", "ff", "vocab", "max_seq")] + \
+               [("eps", ctypes.c_float), ("theta", ctypes.c_float),
+                ("layer", ctypes.POINTER(_Layer)), ("final_norm", ctypes.c_void_p),
+                ("embd", ctypes.c_void_p), ("lm_head", ctypes.c_void_p), ("f_lm", ctypes.c_int32)]
+
+
+_lib.ora_decode_step_ref_f32.argtypes = [ctypes.POINTER(_Model), ctypes.c_uint32, ctypes.c_uint32,
+                                         _P, ctypes.c_int]
+_lib.ora_decode_step_ref_f32.restype = ctypes.c_uint32
+
+_ROLE_KEYS = (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo"), ("gate", "wg"), ("up", "wu"),
+              ("down", "wd"))
+
+
+class HostStepModel:
+    """A Qwen2-shape model in host memory for ora_decode_step_ref_f32.
+
+    layers: list of dicts with the keys of runit_mac_amd.decode.DecodeModel's
+    layers (wq … wd packed uint8, bq/bk/bv float16, attn_norm/ffn_norm
+    float32, kc/vc float32 [kv_heads·max_seq·head_dim]); quant: format per
+    role as DecodeModel's."""
+
+    def __init__(self, cfg, layers, final_norm, embd, lm_head, quant):
+        self.cfg, self.layers, self.quant = cfg, layers, quant
+        self.keep = [final_norm, embd, lm_head]
+        arr = (_Layer * len(layers))()
+        for i, L in enumerate(layers):
+            for k, v in L.items():
+                setattr(arr[i], k, v.ctypes.data)
+            for role, key in _ROLE_KEYS:
+                setattr(arr[i], "f" + key[1], FMT[quant[role]])
+        self.m = _Model(cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ff,
+                        cfg.vocab, cfg.max_seq, cfg.eps, cfg.theta, arr, final_norm.ctypes.data,
+                        embd.ctypes.data, lm_head.ctypes.data, FMT[quant["lm_head"]])
+        self.arr = arr
+
+    def step(self, token: int, pos: int, threads: int = 1):
+        logits = np.empty(self.cfg.vocab, np.float32)
+        tok = _lib.ora_decode_step_ref_f32(ctypes.byref(self.m), token, pos, _p(logits), threads)
+        return int(tok), logits
+
+    @classmethod
+    def from_recipe(cls, dm) -> "HostStepModel":
+        """The host twin of a synthetic runit_mac_amd.decode.DecodeModel: every
+        tensor regenerated from the model's recipe with the oracle's
+        generators (byte-identical to the device's)."""
+        spec = {p: (kind, seed, n, extra) for p, kind, seed, n, extra in dm.recipe}
+
+        def make(ptr):
+            kind, seed, n, extra = spec[ptr]
+            if kind == "w":
+                el, _ = BLOCK[extra]
+                out = np.empty(n // el * BLOCK[extra][1], np.uint8)
+                _lib.ora_synth_weights(FMT[extra], seed, 0.02, n // el, _p(out))
+                return out
+            mean, std = extra
+            v = synth_normal(seed, n, mean=mean, std=std)
+            return v.astype(np.float16) if kind == "f16" else v
+
+        layers = [{k: make(v) for k, v in L.items()} for L in dm.layers]
+        embd = make(dm.embd)
+        lm = embd if dm.lm_head == dm.embd else make(dm.lm_head)
+        return cls(dm.cfg, layers, make(dm.final_norm), embd, lm, dm.quant)

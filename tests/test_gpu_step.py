@@ -163,4 +163,24 @@ def test_full_depth_step_matches_cpu_oracle(ctx):
         t = check_logits(m.read(m.logits, cfg.vocab).astype(np.float64), ref, f"replay {replay}")
         assert m.get_token() == t
     del g
+    # the CPU baseline's model (rebuilt on the host from the seeds) computes
+    # the same step: the f32 reference CPU path lands on the oracle too
+    host = ora.HostStepModel.from_recipe(m)
+    htok, hlog = host.step(tok, pos, threads=8)
+    assert check_logits(hlog.astype(np.float64), ref, "host f32 step") == htok == t
+    m.free()
+
+
+@pytest.mark.parametrize("quant", [None, Q4K_M])
+def test_host_twin_rebuilds_device_model_bytes(ctx, quant):
+    """Every tensor the CPU baseline's host model regenerates from the decode
+    model's recipe equals the device's bytes."""
+    cfg = DecodeConfig(layers=2, hidden=512, heads=4, kv_heads=2, head_dim=128, ff=1024,
+                       vocab=1000, max_seq=64)
+    m = DecodeModel(ctx, cfg, seed=4, quant=quant)
+    host = ora.HostStepModel.from_recipe(m)
+    for L, HL in zip(m.layers, host.layers):
+        for key, arr in HL.items():
+            dev = m.read(L[key], (arr.nbytes + 3) // 4).view(np.uint8)[:arr.nbytes]
+            assert np.array_equal(dev, arr.view(np.uint8)), key
     m.free()

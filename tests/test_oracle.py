@@ -525,3 +525,73 @@ def test_relayout_to_ggml_preserves_values(fmt):
     w = (0.02 * ora.synth_normal(21, 256 * 8)).astype(np.float32)
     r = ora.quantize(fmt, w)
     assert np.array_equal(ora.dequant(fmt, r), ora.dequant(fmt + "g", ora.relayout_to_ggml(fmt, r)))
+
+
+# ───────────────────────── whole-step CPU baseline ─────────────────────────
+
+def test_decode_step_ref_f32_matches_f64_composition():
+    """ora_decode_step_ref_f32 (the timed CPU baseline: the reference's f32
+    CPU helpers composed into a decode step) against the same step composed in
+    f64 from the oracle's checked pieces: logits within 1e-4 of their spread,
+    the same greedy token, the KV cache row at pos written."""
+    from types import SimpleNamespace
+    cfg = SimpleNamespace(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=32, ff=512,
+                          vocab=300, max_seq=40, eps=1e-6, theta=1e6)
+    q, kv = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    quant = dict(q="q8_0", k="q8_0", v="q4k", o="q4_0", gate="q4k", up="q4k", down="q6k",
+                 lm_head="q6k")
+    seed = iter(range(100, 1000))
+    cache = cfg.kv_heads * cfg.max_seq * cfg.head_dim
+
+    def w(role, n, k):
+        return synth_w(quant[role], n, k, next(seed))
+
+    def synth_w(fmt, n, k, s):
+        return ora.synth_weights(fmt, n, k, s)
+
+    layers = []
+    for _ in range(cfg.layers):
+        layers.append(dict(
+            wq=w("q", q, cfg.hidden), wk=w("k", kv, cfg.hidden), wv=w("v", kv, cfg.hidden),
+            wo=w("o", cfg.hidden, q), wg=w("gate", cfg.ff, cfg.hidden),
+            wu=w("up", cfg.ff, cfg.hidden), wd=w("down", cfg.hidden, cfg.ff),
+            bq=ora.synth_normal(next(seed), q, std=0.02).astype(np.float16),
+            bk=ora.synth_normal(next(seed), kv, std=0.02).astype(np.float16),
+            bv=ora.synth_normal(next(seed), kv, std=0.02).astype(np.float16),
+            attn_norm=ora.synth_normal(next(seed), cfg.hidden, mean=1.0, std=0.02),
+            ffn_norm=ora.synth_normal(next(seed), cfg.hidden, mean=1.0, std=0.02),
+            kc=ora.synth_normal(next(seed), cache), vc=ora.synth_normal(next(seed), cache)))
+    embd = synth_w("q8_0", cfg.vocab, cfg.hidden, next(seed))
+    lm = synth_w("q6k", cfg.vocab, cfg.hidden, next(seed))
+    fnorm = ora.synth_normal(next(seed), cfg.hidden, mean=1.0, std=0.02)
+    tok, pos = 17, 30
+    # f64 composition (before the f32 step updates the caches)
+    row = (cfg.hidden // 32) * 34
+    x = ora.dequant("q8_0", embd[tok * row:(tok + 1) * row]).astype(np.float64)
+    for L in layers:
+        xn = ora.rms_norm(x.astype(np.float32), L["attn_norm"], cfg.eps)
+        qv = ora.gemv(quant["q"], L["wq"], xn.astype(np.float32), q, cfg.hidden)[0] + L["bq"]
+        kk = ora.gemv(quant["k"], L["wk"], xn.astype(np.float32), kv, cfg.hidden)[0] + L["bk"]
+        vv = ora.gemv(quant["v"], L["wv"], xn.astype(np.float32), kv, cfg.hidden)[0] + L["bv"]
+        qv = ora.rope(qv, cfg.heads, cfg.head_dim, pos, cfg.theta)
+        kk = ora.rope(kk, cfg.kv_heads, cfg.head_dim, pos, cfg.theta)
+        kc = L["kc"].reshape(cfg.kv_heads, cfg.max_seq, cfg.head_dim).copy()
+        vc = L["vc"].reshape(cfg.kv_heads, cfg.max_seq, cfg.head_dim).copy()
+        kc[:, pos] = kk.reshape(cfg.kv_heads, -1)
+        vc[:, pos] = vv.reshape(cfg.kv_heads, -1)
+        att = ora.attention(qv, kc, vc, cfg.heads, cfg.kv_heads, cfg.head_dim, pos + 1, cfg.max_seq)
+        x = x + ora.gemv(quant["o"], L["wo"], att.astype(np.float32), cfg.hidden, q)[0]
+        xn = ora.rms_norm(x.astype(np.float32), L["ffn_norm"], cfg.eps).astype(np.float32)
+        g = ora.gemv(quant["gate"], L["wg"], xn, cfg.ff, cfg.hidden)[0]
+        u = ora.gemv(quant["up"], L["wu"], xn, cfg.ff, cfg.hidden)[0]
+        act = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+        x = x + ora.gemv(quant["down"], L["wd"], act, cfg.hidden, cfg.ff)[0]
+    xn = ora.rms_norm(x.astype(np.float32), fnorm, cfg.eps).astype(np.float32)
+    ref = ora.gemv("q6k", lm, xn, cfg.vocab, cfg.hidden)[0]
+    m = ora.HostStepModel(cfg, layers, fnorm, embd, lm, quant)
+    for threads in (1, 3):
+        got_tok, logits = m.step(tok, pos, threads)
+        assert np.max(np.abs(logits - ref)) <= 1e-4 * (ref.max() - ref.min())
+        assert got_tok == int(np.argmax(ref)) == ora.argmax(logits)
+    kc0 = layers[0]["kc"].reshape(cfg.kv_heads, cfg.max_seq, cfg.head_dim)
+    assert np.any(kc0[:, pos] != 0) and kc0.shape[1] == cfg.max_seq
