@@ -444,10 +444,38 @@ int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* ctx, const float* q_raw, con
                                             uint32_t max_seq, uint32_t num_heads,
                                             uint32_t num_kv_heads, uint32_t head_dim, float theta,
                                             uint32_t hidden);
-/* New: out = dequant(table row *token) for a Q8_0 [vocab, k] table; the token
- * id is read from device memory (forward.rs:1494-1505 does this on the CPU). */
+/* add_f16_into_f32 (dispatch.rs:316-330): acc[i] += f32(src[i]) for i < n
+ * (the bias add of the separate-dispatch Q/K/V fallback, forward.rs:1561-1568). */
+int rt_add_f16_into_f32(rt_ctx* ctx, const uint16_t* src, float* acc, uint32_t n);
+/* New: out = dequant(table row *token) for a [vocab, k] table in the named
+ * block format (reference or ggml layout, or plain f16 / f32 rows, as
+ * token_embd.weight is stored); the token id is read from device memory
+ * (forward.rs:1494-1505 dequantises the row on the CPU). */
 int rt_embed_q8_0_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
                       uint32_t k);
+int rt_embed_q4_0_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_q4k_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_q6k_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_q5_0_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_q5k_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_q4_0g_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_q4kg_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_q5kg_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_q6kg_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_f16_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+int rt_embed_f32_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
+                      uint32_t k);
+
 /* New: rms_norm_f32_f32_f32g(x → x̂) fused into the following GEMV's
  * activation staging (same arguments as the pair of calls, minus x̂). */
 int rt_rms_norm_fused_qkv_bias_q8_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k,

@@ -859,7 +859,10 @@ uint32_t ora_decode_step_ref_f32(const ora_model_t* m, uint32_t token, uint32_t 
     float* u = (float*)malloc(ff * sizeof(float));
     float* t = (float*)malloc((h > ff ? h : ff) * sizeof(float));
     float* sc = (float*)malloc(kv_len * sizeof(float));
-    ora_dequant_q8_0(m->embd + (size_t)token * (h / 32) * 34, h / 32, x);
+    {
+        const size_t nb = h / ora_block_elems(m->f_embd);
+        ora_dequant(m->f_embd, m->embd + (size_t)token * nb * ora_block_bytes(m->f_embd), nb, x);
+    }
     const float scale = 1.0f / sqrtf((float)hd);
     for (uint32_t li = 0; li < m->layers; ++li) {
         const ora_layer_t* L = &m->layer[li];

@@ -121,9 +121,9 @@ typedef struct {
     float eps, theta;
     const ora_layer_t* layer;
     const float* final_norm;
-    const uint8_t* embd; /* Q8_0 [vocab][hidden] */
+    const uint8_t* embd; /* [vocab][hidden] in format f_embd */
     const uint8_t* lm_head;
-    int32_t f_lm;
+    int32_t f_lm, f_embd;
 } ora_model_t;
 uint32_t ora_decode_step_ref_f32(const ora_model_t* m, uint32_t token, uint32_t pos,
                                  float* logits, int threads);

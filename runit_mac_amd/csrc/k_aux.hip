@@ -6,26 +6,17 @@
 // _rn intrinsics so no FMA contraction changes the rounding: the results are
 // bit-identical to the reference's f32 CPU decoders.
 
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q8_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    const uint8_t* blk = in + (i >> 5) * 34;
+// Element e of one block, per format.
+RT_DEV float q8_0_value(const uint8_t* blk, uint32_t e) {
     const float d = h2f(*(const uint16_t*)blk);
-    const int8_t q = (int8_t)blk[2 + (i & 31)];
-    out[i] = __fmul_rn(d, (float)q);  // forward.rs:951-963: d * qs[i] as i8 as f32
+    return __fmul_rn(d, (float)(int8_t)blk[2 + e]);  // forward.rs:951-963: d * qs[i] as i8 as f32
 }
 
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q4_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    const uint8_t* blk = in + (i >> 5) * 18;
+RT_DEV float q4_0_value(const uint8_t* blk, uint32_t e) {
     const float d = h2f(*(const uint16_t*)blk);
-    const uint32_t e = i & 31;
     const uint8_t byte = blk[2 + e / 2];
     const int nib = (e & 1) ? (byte >> 4) : (byte & 15);
-    out[i] = __fmul_rn(d, (float)(nib - 8));  // forward.rs:964-978
+    return __fmul_rn(d, (float)(nib - 8));  // forward.rs:964-978
 }
 
 RT_DEV void q4k_scale_min(uint32_t j, const uint8_t* s, uint32_t& sc, uint32_t& m) {
@@ -52,12 +43,123 @@ RT_DEV float q4k_value(const uint8_t* blk, uint32_t e) {
     return __fsub_rn(__fmul_rn(dsc, (float)q), mm);  // forward.rs:1043-1053
 }
 
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q4k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    out[i] = q4k_value(in + (i >> 8) * 144, (uint32_t)(i & 255));
+// Q6_K element h + 32t + l; the reference reads scale slot h/16 + 2t
+// (forward.rs:935-946), ggml slot h/16 + l/16 + 2t (dequantize_row_q6_K).
+template <bool GGML>
+RT_DEV float q6k_value(const uint8_t* blk, uint32_t e) {
+    const uint32_t h = e & 128u, t = (e >> 5) & 3, l = e & 31;
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    const float d = h2f(*(const uint16_t*)(blk + 208));
+    const uint32_t qlb = ql[h / 2 + l + ((t & 1) ? 32 : 0)];
+    const uint32_t lo4 = (t < 2) ? (qlb & 15u) : (qlb >> 4);
+    const uint32_t hi2 = (qh[h / 4 + l] >> (2 * t)) & 3u;
+    const int q = (int)(lo4 | (hi2 << 4)) - 32;
+    const float s = (float)sc[h / 16 + (GGML ? l / 16 : 0) + 2 * t];
+    return __fmul_rn(__fmul_rn(d, s), (float)q);
 }
+RT_DEV float q6k_ref_value(const uint8_t* blk, uint32_t e) { return q6k_value<false>(blk, e); }
+RT_DEV float q6kg_value(const uint8_t* blk, uint32_t e) { return q6k_value<true>(blk, e); }
+
+// Q5_0: d f16 @0, qh u32 @2, qs[16] @6; element j < 16 is the low nibble of
+// qs[j] with qh bit j on top, element 16 + j the high nibble with bit 16 + j;
+// value d·(q − 16) (forward.rs:900-920).
+RT_DEV float q5_0_value(const uint8_t* blk, uint32_t e) {
+    const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    const uint32_t j = e & 15;
+    const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                        ((uint32_t)blk[5] << 24);
+    const uint32_t byte = blk[6 + j];
+    const uint32_t nib = (e < 16) ? (byte & 15u) : (byte >> 4);
+    const int q = (int)(nib | (((qh >> e) & 1u) << 4));
+    return __fmul_rn(d, (float)(q - 16));
+}
+
+// Q5_K: d, dmin f16 @0, scales[12] @4, qh[32] @16, qs[128] @48; element
+// 64j + l (+32) takes the low (high) nibble of qs[32j + l], bit (e % 8) of
+// qh[e / 8] on top, and (sc, m) of sub-block j (j + 4) (forward.rs:979-1012).
+RT_DEV float q5k_value(const uint8_t* blk, uint32_t e) {
+    const uint32_t j = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+    const float d = h2f(*(const uint16_t*)blk);
+    const float dmin = h2f(*(const uint16_t*)(blk + 2));
+    uint32_t sc, m;
+    q4k_scale_min(j + 4 * hi, blk + 4, sc, m);
+    const uint32_t byte = blk[48 + 32 * j + l];
+    const uint32_t q = (hi ? (byte >> 4) : (byte & 15u)) | (((blk[16 + e / 8] >> (e % 8)) & 1u) << 4);
+    const float dsc = __fmul_rn(d, (float)sc);
+    const float mm = __fmul_rn(dmin, (float)m);
+    return __fsub_rn(__fmul_rn(dsc, (float)q), mm);
+}
+
+// ggml layouts (upstream GGUF files), same rounding as the decoders above.
+// Q4_0: element j < 16 low nibble of qs[j], 16 + j its high nibble
+// (dequantize_row_q4_0).
+RT_DEV float q4_0g_value(const uint8_t* blk, uint32_t e) {
+    const float d = h2f(*(const uint16_t*)blk);
+    const uint8_t byte = blk[2 + (e & 15)];
+    const int nib = (e < 16) ? (byte & 15) : (byte >> 4);
+    return __fmul_rn(d, (float)(nib - 8));
+}
+
+// Q4_K: chunk j of 64 elements uses sub-blocks 2j (low nibbles) and 2j + 1
+// (high nibbles) (dequantize_row_q4_K); Q5_K: as Q4_K (qs at 48) with the
+// fifth bit = bit 2j(+1) of qh[l] (dequantize_row_q5_K).
+RT_DEV float q4kg_value(const uint8_t* blk, uint32_t e, uint32_t qs_off, bool five,
+                        const uint8_t* qh) {
+    const float d = h2f(*(const uint16_t*)blk);
+    const float dmin = h2f(*(const uint16_t*)(blk + 2));
+    const uint32_t j = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+    uint32_t sc, m;
+    q4k_scale_min(2 * j + hi, blk + 4, sc, m);
+    const uint8_t byte = blk[qs_off + 32 * j + l];
+    uint32_t q = hi ? (byte >> 4) : (byte & 15u);
+    if (five) q |= ((qh[l] >> (2 * j + hi)) & 1u) << 4;
+    const float dsc = __fmul_rn(d, (float)sc);
+    const float mm = __fmul_rn(dmin, (float)m);
+    return __fsub_rn(__fmul_rn(dsc, (float)q), mm);
+}
+RT_DEV float q4kg_value(const uint8_t* blk, uint32_t e) { return q4kg_value(blk, e, 16, false, nullptr); }
+RT_DEV float q5kg_value(const uint8_t* blk, uint32_t e) { return q4kg_value(blk, e, 48, true, blk + 16); }
+
+// Plain f16 / f32 rows (one-element "blocks").
+RT_DEV float f16_value(const uint8_t* blk, uint32_t) { return h2f(*(const uint16_t*)blk); }
+RT_DEV float f32_value(const uint8_t* blk, uint32_t) { return *(const float*)blk; }
+
+// Per format: k_dequant_<fmt>_f32 — one thread per element of a block
+// stream — and k_embed_<fmt>_f32 — the table row of the token id read from
+// device memory (the reference copies a dequantised token_embd row into the
+// residual stream on the CPU, forward.rs:1494-1505; reading the id on the
+// device lets a captured decode step consume the previous step's argmax
+// without a host round trip).
+#define RT_DEQ_KERNELS(NAME, EL, BY, VALUE)                                                       \
+    extern "C" __global__ void __launch_bounds__(256)                                            \
+        k_dequant_##NAME##_f32(const uint8_t* __restrict__ in, float* __restrict__ out,          \
+                               uint64_t n_el) {                                                  \
+        const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;                    \
+        if (i >= n_el) return;                                                                   \
+        out[i] = VALUE(in + (i / (EL)) * (BY), (uint32_t)(i % (EL)));                            \
+    }                                                                                            \
+    extern "C" __global__ void __launch_bounds__(256)                                            \
+        k_embed_##NAME##_f32(const uint8_t* __restrict__ table, const uint32_t* token,           \
+                             float* __restrict__ out, uint32_t k) {                              \
+        const uint8_t* row = table + (size_t)token[0] * (k / (EL)) * (BY);                       \
+        for (uint32_t i = threadIdx.x + blockIdx.x * wg_threads(); i < k;                        \
+             i += wg_threads() * gridDim.x)                                                      \
+            out[i] = VALUE(row + (i / (EL)) * (BY), i % (EL));                                   \
+    }
+RT_DEQ_KERNELS(q8_0, 32, 34, q8_0_value)
+RT_DEQ_KERNELS(q4_0, 32, 18, q4_0_value)
+RT_DEQ_KERNELS(q4k, 256, 144, q4k_value)
+RT_DEQ_KERNELS(q6k, 256, 210, q6k_ref_value)
+RT_DEQ_KERNELS(q5_0, 32, 22, q5_0_value)
+RT_DEQ_KERNELS(q5k, 256, 176, q5k_value)
+RT_DEQ_KERNELS(q4_0g, 32, 18, q4_0g_value)
+RT_DEQ_KERNELS(q4kg, 256, 144, q4kg_value)
+RT_DEQ_KERNELS(q5kg, 256, 176, q5kg_value)
+RT_DEQ_KERNELS(q6kg, 256, 210, q6kg_value)
+RT_DEQ_KERNELS(f16, 1, 2, f16_value)
+RT_DEQ_KERNELS(f32, 1, 4, f32_value)
 
 // dequant.metal:53-98 — Q4_K to f16 (value rounded to nearest-even half).
 extern "C" __global__ void __launch_bounds__(256)
@@ -70,129 +172,6 @@ k_dequant_q4k_f16(const uint8_t* __restrict__ in, uint16_t* __restrict__ out, ui
     // barrier the compiler fuses d·q − m with the conversion (one rounding).
     asm volatile("" : "+v"(v));
     out[i] = f2h(v);
-}
-
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q6k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    const uint8_t* blk = in + (i >> 8) * 210;
-    const uint32_t e = (uint32_t)(i & 255);
-    const uint32_t h = e & 128u, t = (e >> 5) & 3, l = e & 31;
-    const uint8_t* ql = blk;
-    const uint8_t* qh = blk + 128;
-    const int8_t* sc = (const int8_t*)(blk + 192);
-    const float d = h2f(*(const uint16_t*)(blk + 208));
-    const uint32_t qlb = ql[h / 2 + l + ((t & 1) ? 32 : 0)];
-    const uint32_t lo4 = (t < 2) ? (qlb & 15u) : (qlb >> 4);
-    const uint32_t hi2 = (qh[h / 4 + l] >> (2 * t)) & 3u;
-    const int q = (int)(lo4 | (hi2 << 4)) - 32;
-    const float s = (float)sc[h / 16 + 2 * t];
-    out[i] = __fmul_rn(__fmul_rn(d, s), (float)q);  // forward.rs:935-946
-}
-
-// Q5_0: d f16 @0, qh u32 @2, qs[16] @6; element j < 16 is the low nibble of
-// qs[j] with qh bit j on top, element 16 + j the high nibble with bit 16 + j;
-// value d·(q − 16) (forward.rs:900-920).
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q5_0_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    const uint8_t* blk = in + (i >> 5) * 22;
-    const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    const uint32_t e = (uint32_t)(i & 31), j = e & 15;
-    const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
-                        ((uint32_t)blk[5] << 24);
-    const uint32_t byte = blk[6 + j];
-    const uint32_t nib = (e < 16) ? (byte & 15u) : (byte >> 4);
-    const int q = (int)(nib | (((qh >> e) & 1u) << 4));
-    out[i] = __fmul_rn(d, (float)(q - 16));
-}
-
-// Q5_K: d, dmin f16 @0, scales[12] @4, qh[32] @16, qs[128] @48; element
-// 64j + l (+32) takes the low (high) nibble of qs[32j + l], bit (e % 8) of
-// qh[e / 8] on top, and (sc, m) of sub-block j (j + 4) (forward.rs:979-1012).
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q5k_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    const uint8_t* blk = in + (i >> 8) * 176;
-    const uint32_t e = (uint32_t)(i & 255), j = e >> 6, hi = (e >> 5) & 1, l = e & 31;
-    const float d = h2f(*(const uint16_t*)blk);
-    const float dmin = h2f(*(const uint16_t*)(blk + 2));
-    uint32_t sc, m;
-    q4k_scale_min(j + 4 * hi, blk + 4, sc, m);
-    const uint32_t byte = blk[48 + 32 * j + l];
-    const uint32_t q = (hi ? (byte >> 4) : (byte & 15u)) | (((blk[16 + e / 8] >> (e % 8)) & 1u) << 4);
-    const float dsc = __fmul_rn(d, (float)sc);
-    const float mm = __fmul_rn(dmin, (float)m);
-    out[i] = __fsub_rn(__fmul_rn(dsc, (float)q), mm);
-}
-
-// ggml layouts (upstream GGUF files), same rounding as the decoders above.
-// Q4_0: element j < 16 low nibble of qs[j], 16 + j its high nibble
-// (dequantize_row_q4_0).
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q4_0g_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    const uint8_t* blk = in + (i >> 5) * 18;
-    const float d = h2f(*(const uint16_t*)blk);
-    const uint32_t e = i & 31;
-    const uint8_t byte = blk[2 + (e & 15)];
-    const int nib = (e < 16) ? (byte & 15) : (byte >> 4);
-    out[i] = __fmul_rn(d, (float)(nib - 8));
-}
-
-// Q4_K: chunk j of 64 elements uses sub-blocks 2j (low nibbles) and 2j + 1
-// (high nibbles) (dequantize_row_q4_K).
-RT_DEV float q4kg_value(const uint8_t* blk, uint32_t e, uint32_t qs_off, bool five,
-                        const uint8_t* qh) {
-    const float d = h2f(*(const uint16_t*)blk);
-    const float dmin = h2f(*(const uint16_t*)(blk + 2));
-    const uint32_t j = e >> 6, hi = (e >> 5) & 1, l = e & 31;
-    uint32_t sc, m;
-    q4k_scale_min(2 * j + hi, blk + 4, sc, m);
-    const uint8_t byte = blk[qs_off + 32 * j + l];
-    uint32_t q = hi ? (byte >> 4) : (byte & 15u);
-    if (five) q |= ((qh[l] >> (2 * j + hi)) & 1u) << 4;  // Q5_K: bit 2j(+1) of qh[l]
-    const float dsc = __fmul_rn(d, (float)sc);
-    const float mm = __fmul_rn(dmin, (float)m);
-    return __fsub_rn(__fmul_rn(dsc, (float)q), mm);
-}
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q4kg_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    const uint8_t* blk = in + (i >> 8) * 144;
-    out[i] = q4kg_value(blk, (uint32_t)(i & 255), 16, false, nullptr);
-}
-// Q5_K: as Q4_K (qs at 48) with the fifth bit from qh (dequantize_row_q5_K).
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q5kg_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    const uint8_t* blk = in + (i >> 8) * 176;
-    out[i] = q4kg_value(blk, (uint32_t)(i & 255), 48, true, blk + 16);
-}
-// Q6_K: element h + 32t + l uses sc[h/16 + l/16 + 2t] (dequantize_row_q6_K).
-extern "C" __global__ void __launch_bounds__(256)
-k_dequant_q6kg_f32(const uint8_t* __restrict__ in, float* __restrict__ out, uint64_t n_el) {
-    const uint64_t i = (uint64_t)blockIdx.x * wg_threads() + threadIdx.x;
-    if (i >= n_el) return;
-    const uint8_t* blk = in + (i >> 8) * 210;
-    const uint32_t e = (uint32_t)(i & 255);
-    const uint32_t h = e & 128u, t = (e >> 5) & 3, l = e & 31;
-    const uint8_t* ql = blk;
-    const uint8_t* qh = blk + 128;
-    const int8_t* sc = (const int8_t*)(blk + 192);
-    const float d = h2f(*(const uint16_t*)(blk + 208));
-    const uint32_t qlb = ql[h / 2 + l + ((t & 1) ? 32 : 0)];
-    const uint32_t lo4 = (t < 2) ? (qlb & 15u) : (qlb >> 4);
-    const uint32_t hi2 = (qh[h / 4 + l] >> (2 * t)) & 3u;
-    const int q = (int)(lo4 | (hi2 << 4)) - 32;
-    const float s = (float)sc[h / 16 + l / 16 + 2 * t];
-    out[i] = __fmul_rn(__fmul_rn(d, s), (float)q);
 }
 
 // ───────────────────────────── argmax ─────────────────────────────

@@ -405,15 +405,10 @@ RT_ATTN_KERNELS(64)
 RT_ATTN_KERNELS(128)
 RT_ATTN_KERNELS(256)
 
-// Q8_0 embedding row (the reference copies a dequantised token_embd row into
-// the residual stream on the CPU, forward.rs:1494-1505).  The token id is
-// read from device memory so a captured decode step can consume the previous
-// step's argmax without a host round trip.
+// add_f16_into_f32 (dispatch.rs:316-330): acc[i] += f32(src[i]), the bias add
+// of the reference's separate-dispatch Q/K/V fallback (forward.rs:1561-1568).
 extern "C" __global__ void __launch_bounds__(256)
-k_embed_q8_0_f32(const uint8_t* table, const uint32_t* token, float* out, uint32_t k) {
-    const size_t row = (size_t)token[0] * (k / 32) * 34;
-    for (uint32_t i = threadIdx.x + blockIdx.x * wg_threads(); i < k; i += wg_threads() * gridDim.x) {
-        const uint8_t* blk = table + row + (i / 32) * 34;
-        out[i] = __fmul_rn(h2f(*(const uint16_t*)blk), (float)(int8_t)blk[2 + (i & 31)]);
-    }
+k_add_f16_into_f32(const uint16_t* __restrict__ src, float* __restrict__ acc, uint32_t n) {
+    for (uint32_t i = threadIdx.x + blockIdx.x * wg_threads(); i < n; i += wg_threads() * gridDim.x)
+        acc[i] += h2f(src[i]);
 }

@@ -132,7 +132,8 @@ const char* const kKernelNames[] = {
     "k_rms_norm_f32g", "k_rope_qk_f32", "k_kv_copy_f32",
     "k_decode_attention_f32_hd64", "k_decode_attention_f32_hd128", "k_decode_attention_f32_hd256",
     "k_attn_rope_f32_hd64", "k_attn_rope_f32_hd128", "k_attn_rope_f32_hd256",
-    "k_embed_q8_0_f32",
+    "k_add_f16_into_f32",
+    "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
     "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
     "k_gemm_q8_0_mg1_ct2", "k_gemm_q8_0_mg2_ct2", "k_gemm_q8_0_mg4_ct2", "k_gemm_q8_0_mg8_ct2",
@@ -2053,16 +2054,45 @@ int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const
     return gemv_launch(c, "k_gemv_q8_0_attn_f32add", kQ8_0, g, false);
 }
 
-int rt_embed_q8_0_f32(rt_ctx* c, const void* table, const uint32_t* token, float* out, uint32_t k) {
+int rt_add_f16_into_f32(rt_ctx* c, const uint16_t* src, float* acc, uint32_t n) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (n == 0) return RT_OK;
+    if (!src || !acc)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: add_f16_into_f32: null buffer");
+    void* params[] = {&src, &acc, &n};
+    return launch(c, "k_add_f16_into_f32", dim3(std::min<uint32_t>((n + 255) / 256, 1024)),
+                  dim3(256), 0, params);
+}
+
+static int embed_launch(rt_ctx* c, const char* kname, uint32_t blk_el, const void* table,
+                        const uint32_t* token, float* out, uint32_t k) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     if (k == 0) return RT_OK;
-    if (k % 32)
-        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: embed: k=%u not a multiple of 32", k);
+    if (k % blk_el)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: embed: k=%u not a multiple of %u",
+                    k, blk_el);
     if (!table || !token || !out)
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: embed: null buffer");
     void* params[] = {&table, &token, &out, &k};
-    return launch(c, "k_embed_q8_0_f32", dim3((k + 255) / 256), dim3(256), 0, params);
+    return launch(c, kname, dim3((k + 255) / 256), dim3(256), 0, params);
 }
+#define RT_EMBED_ENTRY(NAME, EL)                                                               \
+    int rt_embed_##NAME##_f32(rt_ctx* c, const void* table, const uint32_t* token, float* out,  \
+                              uint32_t k) {                                                    \
+        return embed_launch(c, "k_embed_" #NAME "_f32", EL, table, token, out, k);             \
+    }
+RT_EMBED_ENTRY(q8_0, 32)
+RT_EMBED_ENTRY(q4_0, 32)
+RT_EMBED_ENTRY(q4k, 256)
+RT_EMBED_ENTRY(q6k, 256)
+RT_EMBED_ENTRY(q5_0, 32)
+RT_EMBED_ENTRY(q5k, 256)
+RT_EMBED_ENTRY(q4_0g, 32)
+RT_EMBED_ENTRY(q4kg, 256)
+RT_EMBED_ENTRY(q5kg, 256)
+RT_EMBED_ENTRY(q6kg, 256)
+RT_EMBED_ENTRY(f16, 1)
+RT_EMBED_ENTRY(f32, 1)
 
 int rt_rms_norm_fused_qkv_bias_q8_0_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,
                                         const float* x, const float* gamma, float eps, float* oq,

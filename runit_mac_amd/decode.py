@@ -97,33 +97,88 @@ class Arena:
         return p
 
 
+# GGUF tensor dtype → block format of the kernels, per layout: real files
+# (upstream quantisers) use ggml's layouts; "reference" reads Q4_0 / Q4_K /
+# Q5_K / Q6_K with the reference's own decoders (forward.rs:900-1057), which
+# differ from ggml's (docs/STATUS_REPORT.md:184).  Q8_0 and Q5_0 agree.
+GGUF_FORMATS = {
+    "ggml": {"Q8_0": "q8_0", "Q4_0": "q4_0g", "Q4_K": "q4kg", "Q5_0": "q5_0", "Q5_K": "q5kg",
+             "Q6_K": "q6kg"},
+    "reference": {"Q8_0": "q8_0", "Q4_0": "q4_0", "Q4_K": "q4k", "Q5_0": "q5_0", "Q5_K": "q5k",
+                  "Q6_K": "q6k"},
+}
+# embedding tables may also be plain rows
+EMBED_FORMATS = {"F16": "f16", "F32": "f32"}
+_MATRIX_ROLES = (("q", "wq", "attn_q"), ("k", "wk", "attn_k"), ("v", "wv", "attn_v"),
+                 ("o", "wo", "attn_output"), ("gate", "wg", "ffn_gate"), ("up", "wu", "ffn_up"),
+                 ("down", "wd", "ffn_down"))
+
+
+def _fmt_bytes(fmt: str, n: int, k: int) -> int:
+    if fmt in ("f16", "f32"):
+        return n * k * (2 if fmt == "f16" else 4)
+    return d.weight_bytes(fmt, n, k)
+
+
 class DecodeModel:
-    """Synthetic Qwen2-shape model resident in one arena, plus the KV cache."""
+    """Qwen2-shape model resident in one arena, plus the KV cache.
+
+    Every weight matrix carries its own block format (``layers[i]["fmt"]``,
+    ``embd_fmt``, ``lm_fmt``), and the step routes each matrix to its
+    format's kernels, as the reference's WeightBuf dispatch does per tensor
+    (forward.rs:70-248, chosen by dtype in upload_weight_wb, :1137-1222)."""
 
     def __init__(self, ctx: d.HipContext, cfg: DecodeConfig = DecodeConfig(), seed: int = 7,
-                 gguf=None, quant: dict | None = None):
-        """Synthetic weights, or (gguf: a runit_mac_amd.gguf.GgufFile) the
-        file's tensors: Q8_0 matrices as stored, f32 norms, f32/f16 biases
-        converted to f16 (RNE, as upload_weight converts F32, forward.rs:
-        442-455), an absent bias as zeros, the LM head tied to token_embd when
-        output.weight is absent (forward.rs:1271-1276), and an empty KV cache."""
+                 gguf=None, quant: dict | None = None, layout: str = "ggml"):
+        """Synthetic weights (seeded N(0, 0.02) quantised per block; `quant`:
+        format per role), or (gguf: a runit_mac_amd.gguf.GgufFile) the file's
+        tensors, each routed by its own dtype (Q8_0, Q4_0, Q4_K, Q5_0, Q5_K,
+        Q6_K read in `layout`: "ggml" for upstream files, "reference" for the
+        reference's decoders), f32 norms, f32/f16 biases converted to f16
+        (RNE, as upload_weight converts F32, forward.rs:442-455), an absent
+        bias as zeros, the LM head tied to token_embd when output.weight is
+        absent (forward.rs:1271-1276), and an empty KV cache."""
         self.ctx, self.cfg = ctx, cfg
         c = cfg
+        if gguf is not None and quant is not None:
+            raise ValueError("quant applies to synthetic weights; a GGUF file names its dtypes")
+        if layout not in GGUF_FORMATS:
+            raise ValueError(f"layout must be one of {tuple(GGUF_FORMATS)}")
         self.quant = fq = dict(Q8_ALL, **(quant or {}))
         if set(fq) != set(ROLES):
             raise ValueError(f"quant roles must be among {ROLES}")
-        if gguf is not None and any(f != "q8_0" for f in fq.values()):
-            raise ValueError("GGUF models load Q8_0 matrices")
         h, q, kv, ff = c.hidden, c.q_dim, c.kv_dim, c.ff
-        wb = lambda n, k, f="q8_0": d.weight_bytes(f, n, k)  # noqa: E731
-        per_layer = (wb(q, h, fq["q"]) + wb(kv, h, fq["k"]) + wb(kv, h, fq["v"])
-                     + wb(h, q, fq["o"]) + wb(ff, h, fq["gate"]) + wb(ff, h, fq["up"])
-                     + wb(h, ff, fq["down"])
-                     + 2 * (q + 2 * kv) + 8 * h + 2 * 4 * c.kv_heads * c.max_seq * c.head_dim
-                     + 16 * 256)
-        tied = (gguf is None or "output.weight" not in gguf) and fq["lm_head"] == "q8_0"
-        total = c.layers * per_layer + wb(c.vocab, h) + \
-            (0 if tied else wb(c.vocab, h, fq["lm_head"])) + 16 * h + \
+        shapes = {"q": (q, h), "k": (kv, h), "v": (kv, h), "o": (h, q), "gate": (ff, h),
+                  "up": (ff, h), "down": (h, ff)}
+
+        def file_fmt(name, n, k, embed=False):
+            t = gguf.tensor(name)
+            if t.shape != (k, n):
+                raise ValueError(f"{name}: shape {t.shape}, expected {(k, n)}")
+            table = dict(GGUF_FORMATS[layout], **(EMBED_FORMATS if embed else {}))
+            if t.dtype_name not in table:
+                raise ValueError(f"{name}: dtype {t.dtype_name} has no GPU path here "
+                                 f"(supported: {sorted(table)})")
+            return table[t.dtype_name]
+
+        # format of every matrix
+        if gguf is not None:
+            lfmts = [{role: file_fmt(f"blk.{i}.{base}.weight", *shapes[role])
+                      for role, _, base in _MATRIX_ROLES} for i in range(c.layers)]
+            self.embd_fmt = file_fmt("token_embd.weight", c.vocab, h, embed=True)
+            tied = "output.weight" not in gguf
+            self.lm_fmt = self.embd_fmt if tied else file_fmt("output.weight", c.vocab, h)
+            if self.lm_fmt in ("f16", "f32"):
+                raise ValueError(f"LM head in {self.lm_fmt}: no f16/f32-weight GEMV here")
+        else:
+            lfmts = [{role: fq[role] for role, _, _ in _MATRIX_ROLES} for _ in range(c.layers)]
+            self.embd_fmt = "q8_0"
+            tied = fq["lm_head"] == "q8_0"
+            self.lm_fmt = fq["lm_head"]
+        per_layer = [sum(_fmt_bytes(L[r], *shapes[r]) + 256 for r in shapes) for L in lfmts]
+        small = 2 * (q + 2 * kv) + 8 * h + 2 * 4 * c.kv_heads * c.max_seq * c.head_dim + 16 * 256
+        total = sum(per_layer) + c.layers * small + _fmt_bytes(self.embd_fmt, c.vocab, h) + \
+            (0 if tied else _fmt_bytes(self.lm_fmt, c.vocab, h)) + 16 * h + \
             64 * 1024 + 4 * (c.vocab + 8 * ff + 8 * q)
         self.arena = Arena(ctx, total)
         a = self.arena
@@ -138,19 +193,17 @@ class DecodeModel:
             arr = np.ascontiguousarray(arr)
             ctx._check(lib.rt_upload(ctx.handle, p, arr.ctypes.data, arr.nbytes))
 
-        def tensor(name, n, k=None, dtypes=()):
+        def tensor(name, n, dtypes=()):
             t = gguf.tensor(name)
-            shape = (k, n) if k is not None else (n,)
-            if t.shape != shape or t.dtype_name not in dtypes:
+            if t.shape != (n,) or t.dtype_name not in dtypes:
                 raise ValueError(f"{name}: {t.dtype_name} {t.shape}, expected one of {dtypes} "
-                                 f"{shape}")
+                                 f"{(n,)}")
             return t
 
-        def qw(n, k, name=None, fmt="q8_0"):
+        def qw(n, k, name, fmt):
             nonlocal s
-            p = a.take(wb(n, k, fmt))
+            p = a.take(_fmt_bytes(fmt, n, k))
             if gguf is not None:
-                tensor(name, n, k, ("Q8_0",))
                 gguf.upload(ctx, name, p)
             else:
                 d.synth_weights(ctx, fmt, p, n * k // d.BLOCK[fmt][0], s)
@@ -196,24 +249,26 @@ class DecodeModel:
         self.layers = []
         for i in range(c.layers):
             b = f"blk.{i}."
-            L = dict(wq=qw(q, h, b + "attn_q.weight", fq["q"]),
-                     wk=qw(kv, h, b + "attn_k.weight", fq["k"]),
-                     wv=qw(kv, h, b + "attn_v.weight", fq["v"]),
+            F = lfmts[i]
+            L = dict(wq=qw(q, h, b + "attn_q.weight", F["q"]),
+                     wk=qw(kv, h, b + "attn_k.weight", F["k"]),
+                     wv=qw(kv, h, b + "attn_v.weight", F["v"]),
                      bq=f16(q, 0.02, b + "attn_q.bias"),
                      bk=f16(kv, 0.02, b + "attn_k.bias"), bv=f16(kv, 0.02, b + "attn_v.bias"),
-                     wo=qw(h, q, b + "attn_output.weight", fq["o"]),
-                     wg=qw(ff, h, b + "ffn_gate.weight", fq["gate"]),
-                     wu=qw(ff, h, b + "ffn_up.weight", fq["up"]),
-                     wd=qw(h, ff, b + "ffn_down.weight", fq["down"]),
+                     wo=qw(h, q, b + "attn_output.weight", F["o"]),
+                     wg=qw(ff, h, b + "ffn_gate.weight", F["gate"]),
+                     wu=qw(ff, h, b + "ffn_up.weight", F["up"]),
+                     wd=qw(h, ff, b + "ffn_down.weight", F["down"]),
                      attn_norm=f32(h, 1.0, 0.02, b + "attn_norm.weight"),
                      ffn_norm=f32(h, 1.0, 0.02, b + "ffn_norm.weight"),
                      kc=f32(c.kv_heads * c.max_seq * c.head_dim, 0.0, 1.0),
                      vc=f32(c.kv_heads * c.max_seq * c.head_dim, 0.0, 1.0))
             self.layers.append(L)
+        self.fmts = lfmts
         self.final_norm = f32(h, 1.0, 0.02, "output_norm.weight")
-        self.embd = qw(c.vocab, h, "token_embd.weight")
+        self.embd = qw(c.vocab, h, "token_embd.weight", self.embd_fmt)
         # LM head: tied to token_embd unless the file has output.weight
-        self.lm_head = self.embd if tied else qw(c.vocab, h, "output.weight", fq["lm_head"])
+        self.lm_head = self.embd if tied else qw(c.vocab, h, "output.weight", self.lm_fmt)
         # activations
         self.x = a.take(4 * h)
         self.xn = a.take(4 * h)
@@ -224,19 +279,31 @@ class DecodeModel:
         self.act = a.take(4 * ff)
         self.logits = a.take(4 * c.vocab)
         self.token = a.take(256)
+        self._launches = None
         ctx.flush()
 
     @classmethod
-    def from_gguf(cls, ctx: d.HipContext, gguf, max_seq: int = 1024) -> "DecodeModel":
-        """A Qwen2-family model from a GGUF file (Q8_0 matrices), with the
-        dimensions of ModelConfig.from_metadata (config.rs:96-265)."""
+    def from_gguf(cls, ctx: d.HipContext, gguf, max_seq: int = 1024,
+                  layout: str = "ggml") -> "DecodeModel":
+        """A Qwen2-family model from a GGUF file, with the dimensions of
+        ModelConfig.from_metadata (config.rs:96-265); every matrix keeps the
+        file's dtype (in `layout`) and runs on that format's kernels."""
         from .gguf import ModelConfig
         mc = ModelConfig.from_metadata(gguf.metadata, gguf.metadata_types)
         cfg = DecodeConfig(layers=mc.num_hidden_layers, hidden=mc.hidden_size,
                            heads=mc.num_attention_heads, kv_heads=mc.num_key_value_heads,
                            head_dim=mc.head_dim, ff=mc.intermediate_size, vocab=mc.vocab_size,
                            eps=mc.rms_norm_eps, theta=mc.rope_theta, max_seq=max_seq)
-        return cls(ctx, cfg, gguf=gguf)
+        return cls(ctx, cfg, gguf=gguf, layout=layout)
+
+    def weight_bytes(self) -> int:
+        """Weight bytes read per token: every matrix once, in its own format."""
+        c = self.cfg
+        h, q, kv, ff = c.hidden, c.q_dim, c.kv_dim, c.ff
+        shapes = {"q": (q, h), "k": (kv, h), "v": (kv, h), "o": (h, q), "gate": (ff, h),
+                  "up": (ff, h), "down": (h, ff)}
+        return sum(_fmt_bytes(F[r], *shapes[r]) for F in self.fmts for r in shapes) + \
+            _fmt_bytes(self.lm_fmt, c.vocab, h)
 
     def set_token(self, tok: int) -> None:
         buf = np.array([tok], np.uint32)  # kept alive across the synchronous copy
@@ -259,7 +326,8 @@ class DecodeModel:
 
     def step_reference(self, pos: int) -> None:
         """forward.rs:1494-1771, the reference's kernel sequence (Q8_0 models)."""
-        if any(f != "q8_0" for f in self.quant.values()):
+        if self.embd_fmt != "q8_0" or self.lm_fmt != "q8_0" or \
+                any(f != "q8_0" for F in self.fmts for f in F.values()):
             raise ValueError("the reference sequence is built for Q8_0 models")
         ctx, c = self.ctx, self.cfg
         h, q_dim, kv_dim = c.hidden, c.q_dim, c.kv_dim
@@ -282,41 +350,71 @@ class DecodeModel:
         d.gemv_q8_0_f32in_f32out_mr(ctx, self.lm_head, self.xn, self.logits, c.vocab, h)
         d.argmax_f32(ctx, self.logits, self.token, c.vocab)
 
-    def _qkv(self, L, x) -> None:
-        """Q/K/V (+ bias) of the input x, routed by the projections' formats."""
-        c, fq = self.cfg, self.quant
-        fqk, fv = fq["q"], fq["v"]
-        if fq["k"] != fqk:
-            raise ValueError("Q and K must share a format")
-        name = (f"fused_qkv_bias_{fqk}_f32" if fv == fqk else f"fused_qkv_bias_{fqk}_{fv}_f32")
-        fn = getattr(d, name, None)
-        if fn is None:
-            raise ValueError(f"no fused Q/K/V for Q/K in {fqk}, V in {fv}")
-        fn(self.ctx, L["wq"], L["wk"], L["wv"], x, self.q, self.k, self.v, L["bq"], L["bk"],
-           L["bv"], c.q_dim, c.kv_dim, c.hidden)
+    # Routing of one layer's launches by its matrices' formats (the WeightBuf
+    # match arms of forward.rs:1543-1568, 1684-1702): each returns the number
+    # of launches it issues.
+    def _plan_qkv(self, F) -> str:
+        fqk, fk, fv = F["q"], F["k"], F["v"]
+        h = self.cfg.hidden
+        if fqk == fk == fv == "q8_0":
+            return "norm_q8_0"
+        if (fqk, fk, fv) == ("q4k", "q4k", "q6k") and h <= 8192:
+            return "norm_q4k_q6k"
+        if fqk == fk and hasattr(d, f"fused_qkv_bias_{fqk}_f32") and fv == fqk:
+            return "fused"
+        if fqk == fk and hasattr(d, f"fused_qkv_bias_{fqk}_{fv}_f32"):
+            return "fused_mixed"
+        return "separate"
 
-    def step_fused(self, pos: int) -> None:
-        """Same arithmetic, 5 launches per layer for Q8_0 (RMSNorm folded into
-        the staging of the next GEMV, attention merged into the output
-        projection); other formats add a launch for each RMSNorm and split
-        attention from the output projection."""
-        ctx, c, fq = self.ctx, self.cfg, self.quant
-        h, q_dim, kv_dim = c.hidden, c.q_dim, c.kv_dim
-        d.embed_q8_0_f32(ctx, self.embd, self.token, self.x, h)
-        for L in self.layers:
-            if fq["q"] == fq["k"] == fq["v"] == "q8_0":
+    def _qkv(self, L, F, x) -> int:
+        """Q/K/V (+ bias) of the normalised input x: one fused launch where a
+        kernel covers the formats, else the reference's fallback of three
+        GEMVs each followed by add_f16_into_f32 (forward.rs:1561-1568)."""
+        c, ctx = self.cfg, self.ctx
+        plan = self._plan_qkv(F)
+        args = (L["wq"], L["wk"], L["wv"], x, self.q, self.k, self.v, L["bq"], L["bk"], L["bv"],
+                c.q_dim, c.kv_dim, c.hidden)
+        if plan == "fused":
+            getattr(d, f"fused_qkv_bias_{F['q']}_f32")(ctx, *args)
+            return 1
+        if plan == "fused_mixed":
+            getattr(d, f"fused_qkv_bias_{F['q']}_{F['v']}_f32")(ctx, *args)
+            return 1
+        for role, w, b, out, n in (("q", "wq", "bq", self.q, c.q_dim),
+                                   ("k", "wk", "bk", self.k, c.kv_dim),
+                                   ("v", "wv", "bv", self.v, c.kv_dim)):
+            getattr(d, f"gemv_{F[role]}_f32in_f32out")(ctx, L[w], x, out, n, c.hidden)
+            d.add_f16_into_f32(ctx, L[b], out, n)
+        return 6
+
+    def step_fused(self, pos: int) -> int:
+        """One greedy step: embedding, per layer Q/K/V (+ bias), RoPE + KV
+        write + attention, O (+ residual), gate/up/SiLU, down (+ residual);
+        final norm, LM head, argmax.  RMSNorm folds into the next launch's
+        staging for the Q8_0 and Q4_K_M projections, attention into the Q8_0
+        output projection; other formats take them as launches of their own.
+        Returns the number of launches."""
+        ctx, c = self.ctx, self.cfg
+        h, q_dim = c.hidden, c.q_dim
+        n = 1
+        d.embed_f32(ctx, self.embd_fmt, self.embd, self.token, self.x, h)
+        for L, F in zip(self.layers, self.fmts):
+            plan = self._plan_qkv(F)
+            if plan == "norm_q8_0":
                 d.rms_norm_fused_qkv_bias_q8_0_f32(ctx, L["wq"], L["wk"], L["wv"], self.x,
                                                    L["attn_norm"], c.eps, self.q, self.k, self.v,
-                                                   L["bq"], L["bk"], L["bv"], q_dim, kv_dim, h)
-            elif (fq["q"], fq["k"], fq["v"]) == ("q4k", "q4k", "q6k") and h <= 8192:
+                                                   L["bq"], L["bk"], L["bv"], q_dim, c.kv_dim, h)
+                n += 1
+            elif plan == "norm_q4k_q6k":
                 d.rms_norm_fused_qkv_bias_q4k_q6k_f32(ctx, L["wq"], L["wk"], L["wv"], self.x,
                                                       L["attn_norm"], c.eps, self.q, self.k,
                                                       self.v, L["bq"], L["bk"], L["bv"], q_dim,
-                                                      kv_dim, h)
+                                                      c.kv_dim, h)
+                n += 1
             else:
                 d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, L["attn_norm"], c.eps, h, 1)
-                self._qkv(L, self.xn)
-            if fq["o"] == "q8_0":
+                n += 1 + self._qkv(L, F, self.xn)
+            if F["o"] == "q8_0":
                 d.decode_attention_rope_oproj_q8_0_f32(ctx, self.q, self.k, self.v, L["kc"],
                                                        L["vc"], L["wo"], self.x, pos, c.max_seq,
                                                        c.heads, c.kv_heads, c.head_dim,
@@ -325,36 +423,44 @@ class DecodeModel:
                 d.decode_attention_rope_f32(ctx, self.q, self.k, self.v, L["kc"], L["vc"],
                                             self.attn, pos, c.max_seq, c.heads, c.kv_heads,
                                             c.head_dim, c.theta)
-                getattr(d, f"gemv_{fq['o']}_add_f32_f32in")(ctx, L["wo"], self.attn, self.x,
-                                                            self.x, h, q_dim)
-            if fq["gate"] != fq["up"]:
-                raise ValueError("gate and up must share a format")
-            if fq["gate"] in ("q8_0", "q4k"):
-                getattr(d, f"rms_norm_fused_ffn_{fq['gate']}_f32")(
+                getattr(d, f"gemv_{F['o']}_add_f32_f32in")(ctx, L["wo"], self.attn, self.x,
+                                                           self.x, h, q_dim)
+            n += 2
+            if F["gate"] == F["up"] and F["gate"] in ("q8_0", "q4k"):
+                getattr(d, f"rms_norm_fused_ffn_{F['gate']}_f32")(
                     ctx, L["wg"], L["wu"], self.x, L["ffn_norm"], c.eps, self.act, c.ff, h)
+                n += 1
             else:
                 d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, L["ffn_norm"], c.eps, h, 1)
-                getattr(d, f"fused_ffn_{fq['gate']}_f32")(ctx, L["wg"], L["wu"], self.xn,
-                                                          self.act, c.ff, h)
-            getattr(d, f"gemv_{fq['down']}_add_f32_f32in")(ctx, L["wd"], self.act, self.x,
-                                                           self.x, h, c.ff)
-        if fq["lm_head"] in ("q8_0", "q6k"):
-            getattr(d, f"rms_norm_gemv_{fq['lm_head']}_f32in_f32out")(
+                n += 1
+                if F["gate"] == F["up"] and hasattr(d, f"fused_ffn_{F['gate']}_f32"):
+                    getattr(d, f"fused_ffn_{F['gate']}_f32")(ctx, L["wg"], L["wu"], self.xn,
+                                                              self.act, c.ff, h)
+                    n += 1
+                else:
+                    raise ValueError(f"gate {F['gate']} / up {F['up']}: no fused gate+up+SiLU")
+            getattr(d, f"gemv_{F['down']}_add_f32_f32in")(ctx, L["wd"], self.act, self.x,
+                                                          self.x, h, c.ff)
+            n += 1
+        if self.lm_fmt in ("q8_0", "q6k"):
+            getattr(d, f"rms_norm_gemv_{self.lm_fmt}_f32in_f32out")(
                 ctx, self.lm_head, self.x, self.final_norm, c.eps, self.logits, c.vocab, h)
+            n += 1
         else:
             d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, self.final_norm, c.eps, h, 1)
-            getattr(d, f"gemv_{fq['lm_head']}_f32in_f32out")(ctx, self.lm_head, self.xn,
-                                                             self.logits, c.vocab, h)
+            getattr(d, f"gemv_{self.lm_fmt}_f32in_f32out")(ctx, self.lm_head, self.xn,
+                                                           self.logits, c.vocab, h)
+            n += 2
         d.argmax_f32(ctx, self.logits, self.token, c.vocab)
+        self._launches = n + 1
+        return n + 1
 
     def launches_fused(self) -> int:
-        """Launches of one fused step."""
-        fq, h = self.quant, self.cfg.hidden
-        qkv_norm_fused = (fq["q"] == fq["k"] == fq["v"] == "q8_0" or
-                          ((fq["q"], fq["k"], fq["v"]) == ("q4k", "q4k", "q6k") and h <= 8192))
-        per = (1 if qkv_norm_fused else 2) + 2 + \
-            (1 if fq["gate"] in ("q8_0", "q4k") else 2) + 1
-        return 1 + self.cfg.layers * per + (1 if fq["lm_head"] in ("q8_0", "q6k") else 2) + 1
+        """Launches of one fused step, as the last step_fused issued them (the
+        attention + output projection pair counted as two)."""
+        if self._launches is None:
+            raise RuntimeError("no fused step has run yet")
+        return self._launches
 
     def capture(self, pos: int, fused: bool = True) -> d.Graph:
         """One step captured as a HIP graph (the reference's single command

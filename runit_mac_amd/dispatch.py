@@ -125,7 +125,9 @@ _SIGS = {
     "rt_decode_attention_f32": [_P, _P, _P, _P, _P] + [_U32] * 6,
     "rt_decode_attention_rope_f32": [_P] + [_P] * 6 + [_U32] * 5 + [_F],
     "rt_decode_attention_rope_oproj_q8_0_f32": [_P] + [_P] * 7 + [_U32] * 5 + [_F, _U32],
-    "rt_embed_q8_0_f32": [_P, _P, _P, _P, _U32],
+    "rt_add_f16_into_f32": [_P, _P, _P, _U32],
+    **{f"rt_embed_{_f}_f32": [_P, _P, _P, _P, _U32] for _f in (
+        "q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg", "f16", "f32")},
     "rt_rms_norm_fused_qkv_bias_q8_0_f32": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 + [_U32] * 3,
     "rt_rms_norm_fused_ffn_q8_0_f32": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32],
     "rt_rms_norm_gemv_q8_0_f32in_f32out": [_P, _P, _P, _P, _F, _P, _U32, _U32],
@@ -620,9 +622,20 @@ def decode_attention_rope_oproj_q8_0_f32(ctx, q_raw, k_raw, v_raw, k_cache, v_ca
           num_heads, num_kv_heads, head_dim, theta, hidden)
 
 
+def add_f16_into_f32(ctx, src, acc, n):
+    """dispatch.rs:316-330: acc += f32(src) (f16 bias into an f32 vector)."""
+    _call(ctx, "rt_add_f16_into_f32", _ptr(src), _ptr(acc), n)
+
+
+def embed_f32(ctx, fmt: str, table, token, out, k):
+    """Embedding row of the device-resident token id, dequantised from a
+    `fmt` table (q8_0 … q6kg, f16, f32) (new)."""
+    _call(ctx, f"rt_embed_{fmt}_f32", _ptr(table), _ptr(token), _ptr(out), k)
+
+
 def embed_q8_0_f32(ctx, table, token, out, k):
     """Q8_0 embedding row of the device-resident token id (new)."""
-    _call(ctx, "rt_embed_q8_0_f32", _ptr(table), _ptr(token), _ptr(out), k)
+    embed_f32(ctx, "q8_0", table, token, out, k)
 
 
 def rms_norm_fused_qkv_bias_q8_0_f32(ctx, w_q, w_k, w_v, x, gamma, eps, out_q, out_k, out_v,

@@ -190,7 +190,8 @@ class _Model(ctypes.Structure):
                 ("layers", "hidden", "heads", "kv_heads", "head_dim", "ff", "vocab", "max_seq")] + \
                [("eps", ctypes.c_float), ("theta", ctypes.c_float),
                 ("layer", ctypes.POINTER(_Layer)), ("final_norm", ctypes.c_void_p),
-                ("embd", ctypes.c_void_p), ("lm_head", ctypes.c_void_p), ("f_lm", ctypes.c_int32)]
+                ("embd", ctypes.c_void_p), ("lm_head", ctypes.c_void_p), ("f_lm", ctypes.c_int32),
+                ("f_embd", ctypes.c_int32)]
 
 
 _lib.ora_decode_step_ref_f32.argtypes = [ctypes.POINTER(_Model), ctypes.c_uint32, ctypes.c_uint32,
@@ -206,21 +207,24 @@ class HostStepModel:
 
     layers: list of dicts with the keys of runit_mac_amd.decode.DecodeModel's
     layers (wq … wd packed uint8, bq/bk/bv float16, attn_norm/ffn_norm
-    float32, kc/vc float32 [kv_heads·max_seq·head_dim]); quant: format per
-    role as DecodeModel's."""
+    float32, kc/vc float32 [kv_heads·max_seq·head_dim]); fmts: one dict per
+    layer giving each role's format (or one dict for every layer); lm_fmt /
+    embd_fmt: the LM head's and the embedding table's formats."""
 
-    def __init__(self, cfg, layers, final_norm, embd, lm_head, quant):
-        self.cfg, self.layers, self.quant = cfg, layers, quant
+    def __init__(self, cfg, layers, final_norm, embd, lm_head, fmts, lm_fmt, embd_fmt="q8_0"):
+        if isinstance(fmts, dict):
+            fmts = [fmts] * len(layers)
+        self.cfg, self.layers, self.fmts = cfg, layers, fmts
         self.keep = [final_norm, embd, lm_head]
         arr = (_Layer * len(layers))()
         for i, L in enumerate(layers):
             for k, v in L.items():
                 setattr(arr[i], k, v.ctypes.data)
             for role, key in _ROLE_KEYS:
-                setattr(arr[i], "f" + key[1], FMT[quant[role]])
+                setattr(arr[i], "f" + key[1], FMT[fmts[i][role]])
         self.m = _Model(cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ff,
                         cfg.vocab, cfg.max_seq, cfg.eps, cfg.theta, arr, final_norm.ctypes.data,
-                        embd.ctypes.data, lm_head.ctypes.data, FMT[quant["lm_head"]])
+                        embd.ctypes.data, lm_head.ctypes.data, FMT[lm_fmt], FMT[embd_fmt])
         self.arr = arr
 
     def step(self, token: int, pos: int, threads: int = 1):
@@ -249,4 +253,4 @@ class HostStepModel:
         layers = [{k: make(v) for k, v in L.items()} for L in dm.layers]
         embd = make(dm.embd)
         lm = embd if dm.lm_head == dm.embd else make(dm.lm_head)
-        return cls(dm.cfg, layers, make(dm.final_norm), embd, lm, dm.quant)
+        return cls(dm.cfg, layers, make(dm.final_norm), embd, lm, dm.fmts, dm.lm_fmt, dm.embd_fmt)

@@ -12,29 +12,45 @@ pytestmark = pytest.mark.gpu
 
 
 def cpu_step(m: DecodeModel, tok: int, pos: int) -> np.ndarray:
-    """forward.rs:1494-1771 on the CPU with the oracle (f64 arithmetic)."""
-    c, fq = m.cfg, m.quant
+    """forward.rs:1494-1771 on the CPU with the oracle (f64 arithmetic), every
+    matrix decoded in its own format (the model's per-layer routing)."""
+    c = m.cfg
     h, qd, kvd, hd = c.hidden, c.q_dim, c.kv_dim, c.head_dim
 
-    def rdw(p, n, k, fmt="q8_0"):
+    def rdw(p, n, k, fmt):
         nb = d.weight_bytes(fmt, n, k)
         return m.read(p, (nb + 3) // 4).view(np.uint8)[:nb]
 
-    def gemv(role, p, x, n, k):
-        y, _ = ora.gemv(fq[role], rdw(p, n, k, fq[role]), x.astype(np.float32), n, k)
+    def gemv(fmt, p, x, n, k):
+        y, _ = ora.gemv(fmt, rdw(p, n, k, fmt), x.astype(np.float32), n, k)
         return y
 
-    rd8 = lambda p, n, k: rdw(p, n, k)  # noqa: E731
-    emb = rd8(m.embd, c.vocab, h)
-    row = (h // 32) * 34
-    x = ora.dequant("q8_0", emb[tok * row:(tok + 1) * row]).astype(np.float64)
-    for L in m.layers:
+    emb = rdw(m.embd, c.vocab, h, m.embd_fmt)
+    row = len(emb) // c.vocab
+    x = ora.dequant(m.embd_fmt, emb[tok * row:(tok + 1) * row]).astype(np.float64)
+    return cpu_step_from(m, x, pos, emb)
+
+
+def cpu_step_from(m: DecodeModel, x: np.ndarray, pos: int, emb=None) -> np.ndarray:
+    """cpu_step from a given embedding row x (f64)."""
+    c = m.cfg
+    h, qd, kvd, hd = c.hidden, c.q_dim, c.kv_dim, c.head_dim
+
+    def rdw(p, n, k, fmt):
+        nb = d.weight_bytes(fmt, n, k)
+        return m.read(p, (nb + 3) // 4).view(np.uint8)[:nb]
+
+    def gemv(fmt, p, x, n, k):
+        y, _ = ora.gemv(fmt, rdw(p, n, k, fmt), x.astype(np.float32), n, k)
+        return y
+
+    for L, F in zip(m.layers, m.fmts):
         g = m.read(L["attn_norm"], h)
         xn = ora.rms_norm(x.astype(np.float32), g, c.eps)
         outs = []
         for role, w, b, n in (("q", L["wq"], L["bq"], qd), ("k", L["wk"], L["bk"], kvd),
                               ("v", L["wv"], L["bv"], kvd)):
-            y = gemv(role, w, xn, n, h)
+            y = gemv(F[role], w, xn, n, h)
             bias = m.read(b, n // 2 + 1).view(np.float16)[:n].astype(np.float64)
             outs.append(y + bias)
         q, k, v = outs
@@ -45,17 +61,17 @@ def cpu_step(m: DecodeModel, tok: int, pos: int) -> np.ndarray:
         kc[:, pos] = k.reshape(c.kv_heads, hd)
         vc[:, pos] = v.reshape(c.kv_heads, hd)
         att = ora.attention(q, kc, vc, c.heads, c.kv_heads, hd, pos + 1, c.max_seq)
-        x = x + gemv("o", L["wo"], att, h, qd)
+        x = x + gemv(F["o"], L["wo"], att, h, qd)
         xn = ora.rms_norm(x.astype(np.float32), m.read(L["ffn_norm"], h), c.eps)
-        gt = gemv("gate", L["wg"], xn, c.ff, h)
-        up = gemv("up", L["wu"], xn, c.ff, h)
+        gt = gemv(F["gate"], L["wg"], xn, c.ff, h)
+        up = gemv(F["up"], L["wu"], xn, c.ff, h)
         act = gt / (1.0 + np.exp(-gt)) * up
-        x = x + gemv("down", L["wd"], act, h, c.ff)
+        x = x + gemv(F["down"], L["wd"], act, h, c.ff)
     xn = ora.rms_norm(x.astype(np.float32), m.read(m.final_norm, h), c.eps)
     if m.lm_head == m.embd:
-        logits, _ = ora.gemv("q8_0", emb, xn.astype(np.float32), c.vocab, h)
+        logits, _ = ora.gemv(m.embd_fmt, emb, xn.astype(np.float32), c.vocab, h)
     else:
-        logits = gemv("lm_head", m.lm_head, xn, c.vocab, h)
+        logits = gemv(m.lm_fmt, m.lm_head, xn, c.vocab, h)
     return logits
 
 

@@ -588,7 +588,7 @@ def test_decode_step_ref_f32_matches_f64_composition():
         x = x + ora.gemv(quant["down"], L["wd"], act, cfg.hidden, cfg.ff)[0]
     xn = ora.rms_norm(x.astype(np.float32), fnorm, cfg.eps).astype(np.float32)
     ref = ora.gemv("q6k", lm, xn, cfg.vocab, cfg.hidden)[0]
-    m = ora.HostStepModel(cfg, layers, fnorm, embd, lm, quant)
+    m = ora.HostStepModel(cfg, layers, fnorm, embd, lm, quant, quant["lm_head"])
     for threads in (1, 3):
         got_tok, logits = m.step(tok, pos, threads)
         assert np.max(np.abs(logits - ref)) <= 1e-4 * (ref.max() - ref.min())
