@@ -252,6 +252,25 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
     gpu_token = m.get_token()
     m.set_token(1)
     res = {}
+    # the persistent step: one launch for the embedding and every layer, then
+    # the LM head and the argmax
+    step = m.plan_persistent(pos)
+    step.run()
+    step.check()
+    ctx.capture_begin()
+    step.run()
+    g = ctx.capture_end()
+    for _ in range(max(1, warmup)):
+        g.launch()
+    ctx.flush()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record()
+    for _ in range(steps):
+        g.launch()
+    e1.record()
+    res["persistent"] = e0.elapsed_ms(e1) / steps
+    step.check()
+    del g
     for name, fused in (("fused", True), ("reference_sequence", False)):
         g = m.capture(pos, fused=fused)
         for _ in range(max(1, warmup)):
@@ -283,7 +302,8 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
     ffn_us = e0.elapsed_ms(e1) * 1e3 / (reps * cfg.layers)
     del g
     ffn_bytes = 2 * d.weight_bytes("q8_0", cfg.ff, cfg.hidden) + 4 * cfg.hidden * 2 + 4 * cfg.ff
-    return {"cfg": cfg, "model": m, "pos": pos, "gpu_token": gpu_token, "ms_fused": res["fused"], "ms_reference": res["reference_sequence"],
+    return {"cfg": cfg, "model": m, "pos": pos, "gpu_token": gpu_token, "step": step,
+            "ms_persistent": res["persistent"], "ms_fused": res["fused"], "ms_reference": res["reference_sequence"],
             "step_bytes": cfg.step_bytes(pos + 1), "ffn_us": ffn_us, "ffn_bytes": ffn_bytes,
             "launches_fused": m.launches_fused(),
             "launches_reference": 1 + 10 * cfg.layers + 3}
@@ -518,6 +538,8 @@ def main():
             f"= {tok_s:.1f} tok/s; reference sequence ({dec['launches_reference']} launches): "
             f"{dec['ms_reference'] * 1e3:.1f} us; step bytes {dec['step_bytes'] / 1e6:.1f} MB "
             f"→ {dec['step_bytes'] / (ms * 1e-3) / 1e9:.0f} GB/s effective")
+        log(f"persistent step (1 launch for embedding + 24 layers, then LM head + argmax): "
+            f"{dec['ms_persistent'] * 1e3:.1f} us = {1e3 / dec['ms_persistent']:.1f} tok/s")
         log(f"dominant kernel rms_norm+fused_ffn_q8_0 4864x896x2: {dec['ffn_us']:.2f} us, "
             f"{ffn_gbs:.0f} GB/s")
         line.update({

@@ -550,6 +550,41 @@ int rt_gguf_meta_array_numbers(const rt_gguf* g, uint64_t i, double* out, uint64
 int rt_gguf_meta_array_string(const rt_gguf* g, uint64_t i, uint64_t k, const char** s,
                               uint64_t* len);
 
+/* ───────────────────────── persistent decode step (new) ─────────────────────────
+ * No counterpart in the reference, whose engine encodes one command buffer of
+ * ~10 dispatches per layer (forward.rs:1470-1787).  One greedy decode step of
+ * a Q8_0 Qwen2-shape model (head size 64) with the arithmetic of that
+ * sequence, as ONE persistent launch (token embedding and every layer: RMSNorm
+ * + Q/K/V + bias, RoPE + KV write + attention, O + residual, RMSNorm +
+ * gate/up + SiLU, down + residual), then the norm-fused LM head and the
+ * argmax (two more launches).  create() plans the step for one position `pos`
+ * (kv_len = pos + 1) and allocates its activation buffers; run() enqueues it
+ * (no allocation; capturable); status() flushes and reports a grid barrier
+ * that timed out (the kernel bounds every wait).  The token id is read from
+ * *token and the greedy next token written back there. */
+typedef struct rt_step rt_step;
+typedef struct {
+    const void *wq, *wk, *wv, *wo, *wg, *wu, *wd; /* Q8_0 [rows][k] */
+    const uint16_t *bq, *bk, *bv;                  /* f16 biases */
+    const float *attn_norm, *ffn_norm;
+    float *k_cache, *v_cache;                      /* f32 [kv_heads][max_seq][head_dim] */
+} rt_step_layer;
+typedef struct {
+    uint32_t layers, hidden, heads, kv_heads, head_dim, ff, vocab, max_seq;
+    float eps, theta;
+    const rt_step_layer* layer;
+    const void* token_embd;  /* Q8_0 [vocab][hidden] */
+    const void* lm_head;     /* Q8_0 [vocab][hidden] (may equal token_embd) */
+    const float* output_norm;
+    uint32_t* token;         /* device: the input token id; receives the next one */
+    float* logits;           /* device: [vocab] */
+} rt_step_model;
+int rt_decode_step_q8_0_create(rt_ctx* ctx, const rt_step_model* model, uint32_t pos,
+                               rt_step** out);
+int rt_decode_step_run(rt_ctx* ctx, rt_step* step);
+int rt_decode_step_status(rt_ctx* ctx, rt_step* step);
+void rt_decode_step_destroy(rt_step* step);
+
 #ifdef __cplusplus
 }
 #endif

@@ -159,8 +159,13 @@ struct AttnArgs {
                           // consumer merges: k_gemv_q8_0_attn_f32add)
 };
 
-template <int HD, bool ROPE, int HG, int GMT>
-RT_DEV void attn_split(const AttnArgs& a) {
+// (s, nsp, y, b): the split, the number of splits, the (kv head, head
+// block) index and the batch row — the grid position of a stand-alone launch,
+// or a persistent kernel's virtual one.  COH: q / k / v come from other
+// workgroups of the same launch (device-scope loads); Hook: see NoHook.
+template <int HD, bool ROPE, int HG, int GMT, bool COH = false, class Hook = NoHook>
+RT_DEV void attn_split(const AttnArgs& a, uint32_t s, uint32_t nsp, uint32_t y, uint32_t b,
+                       const Hook& hook = Hook()) {
     // HG groups of 256 threads share the block's query heads: group g takes
     // heads g, g + HG, ... (shorter per-thread chains; every group reads the
     // same K / V rows)
@@ -177,9 +182,8 @@ RT_DEV void attn_split(const AttnArgs& a) {
     __shared__ uint32_t last_flag;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t hg = tid >> 8, lt = tid & 255, lw = w & 3;  // group, thread / wave in group
-    const uint32_t s = blockIdx.x, nsp = gridDim.x, b = blockIdx.z;
     const uint32_t G = a.H / a.KVH, HB = (G + GM - 1) / GM;
-    const uint32_t kvh = blockIdx.y / HB, hb = blockIdx.y % HB;
+    const uint32_t kvh = y / HB, hb = y % HB;
     const uint32_t gh = min(GM, G - hb * GM);
     const uint32_t h0 = kvh * G + hb * GM;  // first query head of the block
     const size_t kvb = ((size_t)b * a.KVH + kvh) * a.stride * HD;
@@ -205,6 +209,8 @@ RT_DEV void attn_split(const AttnArgs& a) {
     };
     f32x4 kr[NQ], vr[NQ];
     if (p_begin < p_end) load_kv(p_begin, kr, vr);
+    hook();
+    auto act = [&](const float* p) { if constexpr (COH) return dev_load(p); else return *p; };
     if constexpr (ROPE) {
         // fused_rope_qk_f32 (fused_rope.metal:28-55) on the block's query
         // heads and on the kv head's key
@@ -215,14 +221,14 @@ RT_DEV void attn_split(const AttnArgs& a) {
             rope_cs(d, HD, a.pos, a.theta, c, sn);
             const float* src = hh < gh ? a.q + (size_t)(h0 + hh) * HD : a.k_new + (size_t)kvh * HD;
             float* dst = hh < gh ? qsf + hh * HD : (float*)ks4;
-            const float r = src[d], im = src[d + half];
+            const float r = act(src + d), im = act(src + d + half);
             dst[d] = r * c - im * sn;
             dst[d + half] = r * sn + im * c;
         }
-        for (uint32_t d = tid; d < HD; d += NT) ((float*)vs4)[d] = a.v_new[(size_t)kvh * HD + d];
+        for (uint32_t d = tid; d < HD; d += NT) ((float*)vs4)[d] = act(a.v_new + (size_t)kvh * HD + d);
     } else {
         const float* q = a.q + ((size_t)b * a.H + h0) * HD;
-        for (uint32_t i = tid; i < gh * HD; i += NT) qsf[i] = q[i];
+        for (uint32_t i = tid; i < gh * HD; i += NT) qsf[i] = act(q + i);
     }
     if (tid < GM) {
         m_run[tid] = -__builtin_huge_valf();
@@ -395,11 +401,13 @@ template <int HD> constexpr int attn_gm() { return (int)rt_attn_gm(HD); }
 #define RT_ATTN_KERNELS(HD)                                                                \
     extern "C" __global__ void __launch_bounds__(256 * attn_hg<HD>())                     \
         k_decode_attention_f32_hd##HD(AttnArgs a) {                                        \
-        attn_split<HD, false, attn_hg<HD>(), attn_gm<HD>()>(a);                            \
+        attn_split<HD, false, attn_hg<HD>(), attn_gm<HD>()>(a, blockIdx.x, gridDim.x,      \
+                                                           blockIdx.y, blockIdx.z);        \
     }                                                                                      \
     extern "C" __global__ void __launch_bounds__(256 * attn_hg<HD>())                     \
         k_attn_rope_f32_hd##HD(AttnArgs a) {                                               \
-        attn_split<HD, true, attn_hg<HD>(), attn_gm<HD>()>(a);                             \
+        attn_split<HD, true, attn_hg<HD>(), attn_gm<HD>()>(a, blockIdx.x, gridDim.x,       \
+                                                          blockIdx.y, blockIdx.z);         \
     }
 RT_ATTN_KERNELS(64)
 RT_ATTN_KERNELS(128)

@@ -64,14 +64,30 @@ enum Epi : int {
     EPI_QKV = 4,      // 3 matrices, no bias
     EPI_QKV_BIAS = 5, // 3 matrices, + float(bias16)
     EPI_FFN = 6,      // act = silu(gate)·up, rows interleaved
+    // EPI_COH | e: the same epilogue inside a persistent kernel, whose
+    // activations are produced and consumed by other workgroups of the same
+    // launch: the residual is read and the outputs are written at device
+    // scope (dev_load / dev_store), so no cache holds a stale copy
+    EPI_COH = 16,
 };
+constexpr int epi_base(int e) { return e & 15; }
+constexpr bool epi_coh(int e) { return (e & EPI_COH) != 0; }
+// f32 store of an epilogue output (device scope inside a persistent kernel)
+template <int EPI, typename T>
+RT_DEV void out_store(T* p, T v) {
+    if constexpr (epi_coh(EPI)) dev_store(p, v); else *p = v;
+}
+template <int EPI, typename T>
+RT_DEV T aux_load(const T* p) {
+    if constexpr (epi_coh(EPI)) return dev_load(p); else return *p;
+}
 
 template <int EPI>
 RT_DEV void vrow_map(const GemvArgs& a, uint32_t vr, uint32_t& mat, uint32_t& r) {
-    if (EPI == EPI_FFN) {
+    if (epi_base(EPI) == EPI_FFN) {
         mat = vr & 1;
         r = vr >> 1;
-    } else if (EPI == EPI_QKV || EPI == EPI_QKV_BIAS) {
+    } else if (epi_base(EPI) == EPI_QKV || epi_base(EPI) == EPI_QKV_BIAS) {
         if (vr < a.n[0]) {
             mat = 0; r = vr;
         } else if (vr < a.n[0] + a.n[1]) {
@@ -108,14 +124,14 @@ template <int EPI>
 RT_DEV float load_aux(const GemvArgs& a, uint32_t vr) {
     uint32_t mat, r;
     vrow_map<EPI>(a, vr, mat, r);
-    if (EPI == EPI_F32_ADD) return ((const float*)a.aux[0])[r];
-    if (EPI == EPI_F16_ADD) return h2f(((const uint16_t*)a.aux[0])[r]);
-    if (EPI == EPI_QKV_BIAS) return h2f(((const uint16_t*)mat_aux(a, mat))[r]);
+    if (epi_base(EPI) == EPI_F32_ADD) return aux_load<EPI>((const float*)a.aux[0] + r);
+    if (epi_base(EPI) == EPI_F16_ADD) return h2f(((const uint16_t*)a.aux[0])[r]);
+    if (epi_base(EPI) == EPI_QKV_BIAS) return h2f(((const uint16_t*)mat_aux(a, mat))[r]);
     return 0.0f;
 }
 template <int EPI>
 constexpr bool has_aux() {
-    return EPI == EPI_F32_ADD || EPI == EPI_F16_ADD || EPI == EPI_QKV_BIAS;
+    return epi_base(EPI) == EPI_F32_ADD || epi_base(EPI) == EPI_F16_ADD || epi_base(EPI) == EPI_QKV_BIAS;
 }
 // Stores v (+ the preloaded epilogue operand) for virtual row vr.  With an
 // output aliasing the residual, the value was read by this same lane first.
@@ -123,12 +139,12 @@ template <int EPI>
 RT_DEV void store_row_pre(const GemvArgs& a, uint32_t vr, float v, float aux) {
     uint32_t mat, r;
     vrow_map<EPI>(a, vr, mat, r);
-    if (EPI == EPI_F32_ADD) {
-        ((float*)a.out[0])[r] = v + aux;
-    } else if (EPI == EPI_F16_ADD) {
+    if (epi_base(EPI) == EPI_F32_ADD) {
+        out_store<EPI>((float*)a.out[0] + r, v + aux);
+    } else if (epi_base(EPI) == EPI_F16_ADD) {
         ((uint16_t*)a.out[0])[r] = f2h(v + aux);
-    } else if (EPI == EPI_QKV_BIAS) {
-        ((float*)mat_out(a, mat))[r] = v + aux;
+    } else if (epi_base(EPI) == EPI_QKV_BIAS) {
+        out_store<EPI>((float*)mat_out(a, mat) + r, v + aux);
     } else {
         store_row<EPI>(a, vr, v);
     }
@@ -138,21 +154,21 @@ template <int EPI>
 RT_DEV void store_row(const GemvArgs& a, uint32_t vr, float v) {
     uint32_t mat, r;
     vrow_map<EPI>(a, vr, mat, r);
-    if (EPI == EPI_F32) {
-        ((float*)a.out[0])[r] = v;
-    } else if (EPI == EPI_F32_ADD) {
+    if (epi_base(EPI) == EPI_F32) {
+        out_store<EPI>((float*)a.out[0] + r, v);
+    } else if (epi_base(EPI) == EPI_F32_ADD) {
         // read residual[r] then write y[r] in the same lane: y may alias res
-        const float res = ((const float*)a.aux[0])[r];
-        ((float*)a.out[0])[r] = v + res;
-    } else if (EPI == EPI_F16) {
+        const float res = aux_load<EPI>((const float*)a.aux[0] + r);
+        out_store<EPI>((float*)a.out[0] + r, v + res);
+    } else if (epi_base(EPI) == EPI_F16) {
         ((uint16_t*)a.out[0])[r] = f2h(v);
-    } else if (EPI == EPI_F16_ADD) {
+    } else if (epi_base(EPI) == EPI_F16_ADD) {
         const float res = h2f(((const uint16_t*)a.aux[0])[r]);
         ((uint16_t*)a.out[0])[r] = f2h(v + res);
-    } else if (EPI == EPI_QKV) {
+    } else if (epi_base(EPI) == EPI_QKV) {
         ((float*)mat_out(a, mat))[r] = v;
-    } else if (EPI == EPI_QKV_BIAS) {
-        ((float*)mat_out(a, mat))[r] = v + h2f(((const uint16_t*)mat_aux(a, mat))[r]);
+    } else if (epi_base(EPI) == EPI_QKV_BIAS) {
+        out_store<EPI>((float*)mat_out(a, mat) + r, v + h2f(((const uint16_t*)mat_aux(a, mat))[r]));
     }
 }
 
@@ -183,7 +199,7 @@ RT_DEV void finish_rows(const GemvArgs& a, float* red, uint32_t tid, uint32_t TL
         __syncthreads();
     }
     if (kl == 0) {
-        if (EPI == EPI_FFN) {
+        if (epi_base(EPI) == EPI_FFN) {
 #pragma unroll
             for (int i = 0; i + 1 < RPL; i += 2) {
                 const uint32_t vr = vr0 + i;
@@ -353,8 +369,8 @@ RT_DEV void gemv_body_chunked(const GemvArgs& a) {
 // Each lane walks a flat sequence of (tile, step) items and issues the loads
 // of item n+1 before computing item n; the first item's loads are issued
 // before the activation staging.
-template <class F, int EPI, typename XT, int RQ, int PF>
-RT_DEV void gemv_mq_body(const GemvArgs& a) {
+template <class F, int EPI, typename XT, int RQ, int PF, class Hook = NoHook>
+RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6, nwaves = wg_threads() >> 6;
@@ -402,7 +418,8 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     // (every lane loads, unconditionally: a load on only some control paths
     // would make the compiler's wait for the x loads a wait for all loads)
     auto load_tile_aux = [&](uint32_t item) {
-        if (has_aux<EPI>()) {
+        // (device-scope operands: only the waves that run the epilogue)
+        if (has_aux<EPI>() && (!epi_coh(EPI) || wk == 0)) {
             const uint32_t vb = rows_of(item / spw);
 #pragma unroll
             for (int rq = 0; rq < RQ; ++rq) {
@@ -419,24 +436,35 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
     const bool one_pass = !a.x_rec && stage_one_pass(nxb);
     XPre xp;
     XPreAttn xa;
-    if constexpr (is_attn_x<XT>()) {
-        // (the host launches this form with one slice round, whole K, nsp ≤ 8)
-        stage_attn_load(a.x, a.xml, a.xnsp, a.xhd, nxb, xa);
-    } else {
-        if (one_pass)
-            stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32,
-                             a.gamma ? a.gamma + (size_t)xb0 * 32 : nullptr, nxb, xp);
-    }
-    load_tile_aux(0);
+    auto load_x = [&] {
+        if constexpr (is_attn_x<XT>()) {
+            // (the host launches this form with one slice round, whole K, nsp ≤ 8)
+            stage_attn_load<__is_same(XT, AttnXC)>(a.x, a.xml, a.xnsp, a.xhd, nxb, xa);
+        } else {
+            if (one_pass)
+                stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32,
+                                 a.gamma ? a.gamma + (size_t)xb0 * 32 : nullptr, nxb, xp);
+        }
+        load_tile_aux(0);
+    };
+    if constexpr (is_hook<Hook>()) {
 #pragma unroll
-    for (int h = 0; h < PF; ++h) issue(h, buf[h]);  // items past nitems load clamped addresses
+        for (int h = 0; h < PF; ++h) issue(h, buf[h]);
+        hook();
+        load_x();
+    } else {
+        load_x();
+#pragma unroll
+        for (int h = 0; h < PF; ++h) issue(h, buf[h]);  // items past nitems load clamped addresses
+    }
+    constexpr bool coh_x = __is_same(XT, AttnXC) || __is_same(XT, CohF32);
     if constexpr (is_attn_x<XT>()) {
-        stage_attn_convert<F::Q40PERM>(xa, a.xnsp, nxb, xs);
+        stage_attn_convert<F::Q40PERM, coh_x>(xa, a.xnsp, nxb, xs);
     } else {
         // (the host launches whole-K kernels either with x records or with a
         // K that one pass covers)
         if (one_pass)
-            stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
+            stage_x_convert<F::Q40PERM, coh_x>(xp, a.gamma, a.eps, nxb, xs);
         else
             copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
     }
@@ -506,11 +534,11 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
                         for (int rq = 0; rq < RQ; ++rq) {
                             const float v = rsum[rq];
                             const uint32_t vr = vbase + 4 * rq + q;
-                            if (EPI == EPI_FFN) {
+                            if (epi_base(EPI) == EPI_FFN) {
                                 // quad holds (gate r, up r, gate r+1, up r+1)
                                 const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
                                 if (slot == 0 && (q & 1) == 0 && vr + 1 < a.nvrows)
-                                    ((float*)a.out[0])[vr >> 1] = silu_ref(v) * up;
+                                    out_store<EPI>((float*)a.out[0] + (vr >> 1), silu_ref(v) * up);
                             } else {
                                 if (slot == 0 && vr < a.nvrows) store_row_pre<EPI>(a, vr, v, aux[rq]);
                             }
@@ -534,18 +562,18 @@ RT_DEV void gemv_mq_body(const GemvArgs& a) {
             if (!last_of[t]) continue;  // uniform
             const uint32_t tile = wg + t * nwg;
             const uint32_t vt = tile * vrows_per_wg;
-            const uint32_t step_r = EPI == EPI_FFN ? 2 : 1;
+            const uint32_t step_r = epi_base(EPI) == EPI_FFN ? 2 : 1;
             for (uint32_t i = tid * step_r; i < vrows_per_wg; i += wg_threads() * step_r) {
                 const uint32_t vr = vt + i;
                 if (vr >= a.nvrows) break;
                 float v = 0.0f, v1 = 0.0f;
                 for (uint32_t c = 0; c < S; ++c) {
                     v += dev_load(a.part + (size_t)c * a.nvrows + vr);
-                    if (EPI == EPI_FFN && vr + 1 < a.nvrows)
+                    if (epi_base(EPI) == EPI_FFN && vr + 1 < a.nvrows)
                         v1 += dev_load(a.part + (size_t)c * a.nvrows + vr + 1);
                 }
-                if (EPI == EPI_FFN) {
-                    if (vr + 1 < a.nvrows) ((float*)a.out[0])[vr >> 1] = silu_ref(v) * v1;
+                if (epi_base(EPI) == EPI_FFN) {
+                    if (vr + 1 < a.nvrows) out_store<EPI>((float*)a.out[0] + (vr >> 1), silu_ref(v) * v1);
                 } else {
                     store_row<EPI>(a, vr, v);
                 }
@@ -593,35 +621,35 @@ RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
 #define RT_GEMV_LB 1024
 #define RT_GEMV_KERNEL2(NAME, FMTM, FMTC, EPI, XT, UNR)                                 \
     extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) NAME##_r1(GemvArgs a) {  \
-        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);  \
+        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 1, (epi_base(EPI) == EPI_FFN ? 2 : 1), UNR>(a);  \
     }                                                                                   \
     extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) NAME##_r2(GemvArgs a) {  \
-        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);  \
+        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (epi_base(EPI) == EPI_FFN ? 2 : 1), UNR>(a);  \
     }
 #define RT_GEMV_KERNEL(NAME, FMT, EPI, XT, UNR) RT_GEMV_KERNEL2(NAME, FMT, FMT, EPI, XT, UNR)
 // As RT_GEMV_KERNEL2, for at most 512 threads with a register budget for WPE
 // waves per SIMD (Q6_K: a whole super-block per lane needs ~240 registers)
 #define RT_GEMV_KERNEL2W(NAME, FMTM, FMTC, EPI, XT, UNR, WPE)                                \
     extern "C" __global__ void __launch_bounds__(512, WPE) NAME##_r1(GemvArgs a) {          \
-        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);      \
+        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 1, (epi_base(EPI) == EPI_FFN ? 2 : 1), UNR>(a);      \
     }                                                                                       \
     extern "C" __global__ void __launch_bounds__(512, WPE) NAME##_r2(GemvArgs a) {          \
-        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);      \
+        gemv_mq_or_chunked<FMTM, FMTC, EPI, XT, 2, (epi_base(EPI) == EPI_FFN ? 2 : 1), UNR>(a);      \
     }
 // Formats that never take the 1024-thread form (Q8_0): built for 512 threads
 #define RT_GEMV_KERNEL512(NAME, FMT, EPI, XT, UNR)                                         \
     extern "C" __global__ void __launch_bounds__(512) NAME##_r1(GemvArgs a) {              \
-        gemv_mq_or_chunked<FMT, FMT, EPI, XT, 1, (EPI == EPI_FFN ? 2 : 1), UNR>(a);        \
+        gemv_mq_or_chunked<FMT, FMT, EPI, XT, 1, (epi_base(EPI) == EPI_FFN ? 2 : 1), UNR>(a);        \
     }                                                                                       \
     extern "C" __global__ void __launch_bounds__(512) NAME##_r2(GemvArgs a) {              \
-        gemv_mq_or_chunked<FMT, FMT, EPI, XT, 2, (EPI == EPI_FFN ? 2 : 1), UNR>(a);        \
+        gemv_mq_or_chunked<FMT, FMT, EPI, XT, 2, (epi_base(EPI) == EPI_FFN ? 2 : 1), UNR>(a);        \
     }
 #define RT_Q6K_WPE 2
 
 // Single-block-unit fallback (rows with an odd number of 32-element blocks)
 #define RT_GEMV_KERNEL_S(NAME, FMT, EPI, XT, UNR)                                 \
     extern "C" __global__ void __launch_bounds__(512) NAME##_s1(GemvArgs a) {    \
-        gemv_body<FMT, EPI, XT, (EPI == EPI_FFN ? 2 : 1), UNR>(a);                \
+        gemv_body<FMT, EPI, XT, (epi_base(EPI) == EPI_FFN ? 2 : 1), UNR>(a);                \
     }
 
 // Q8_0 (gemv_q8_0.metal, gemv_multirow.metal, fused_qkv.metal, fused_ffn.metal)

@@ -6,3 +6,4 @@
 #include "k_decode.hip"
 #include "k_gemm.hip"
 #include "k_scratch.hip"
+#include "k_step.hip"

@@ -142,6 +142,17 @@ RT_DEV uint32_t arrive(uint32_t* counter) {
     return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Hook of a kernel body run as one phase of a persistent kernel: the wait
+// for the previous phase (grid barrier).  With one, a body issues the loads
+// that do not depend on the previous phase (weights, KV-cache rows) first,
+// then waits, then loads the activations: those loads arrive while the grid
+// waits.
+struct NoHook {
+    RT_DEV void operator()() const {}
+};
+template <class Hook>
+constexpr bool is_hook() { return !__is_same(Hook, NoHook); }
+
 // ───────────────────────────── activation limbs ─────────────────────────────
 //
 // One record per 32 activations, 112 bytes (a stride of 28 dwords keeps eight
@@ -178,6 +189,14 @@ template <>
 RT_DEV void load_x4<float>(const float* x, uint32_t idx, float v[4]) {
     f32x4 t = *(const f32x4*)(x + idx);
     v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+}
+// f32 activations written by other workgroups of the same (persistent)
+// launch: read at device scope, so no cache returns a stale copy
+struct CohF32 {};
+template <>
+RT_DEV void load_x4<CohF32>(const CohF32* x, uint32_t idx, float v[4]) {
+    const float* p = (const float*)x + idx;
+    v[0] = dev_load(p); v[1] = dev_load(p + 1); v[2] = dev_load(p + 2); v[3] = dev_load(p + 3);
 }
 template <>
 RT_DEV void load_x4<uint16_t>(const uint16_t* x, uint32_t idx, float v[4]) {
@@ -381,6 +400,10 @@ RT_DEV void stage_x_load(const XT* __restrict__ x, const float* __restrict__ gam
         // rounds past the vector are skipped (workgroup-uniform: no lane of a
         // later load is conditional); lanes past the end load clamped addresses
         if (s * wg_threads() >= total) break;
+        // device-scope activations (a persistent kernel's): lanes past the
+        // end load nothing (their clamped copies would all hit the same few
+        // addresses at device scope) and convert nothing
+        if (__is_same(XT, CohF32) && threadIdx.x + s * wg_threads() >= total) continue;
         const uint32_t t = stage_slice(s, total);
         const uint32_t i = (t >> 3) * 32 + (t & 7) * 4;
         load_x4<XT>(x, i, p.v[s]);
@@ -393,7 +416,7 @@ RT_DEV void stage_x_load(const XT* __restrict__ x, const float* __restrict__ gam
 
 // With γ: x̂ = x · rsqrt(Σx²/K + eps) · γ (rms_norm_f32_f32_f32g,
 // norm.metal:126-154), each product rounded in f32 as in stage_x_norm.
-template <bool Q40PERM>
+template <bool Q40PERM, bool SKIP = false>
 RT_DEV void stage_x_convert(XPre& p, const float* gamma, float eps, uint32_t nxb,
                             XRec* __restrict__ recs) {
     const uint32_t total = nxb * 8;
@@ -422,6 +445,8 @@ RT_DEV void stage_x_convert(XPre& p, const float* gamma, float eps, uint32_t nxb
         // rounds past the vector are skipped (workgroup-uniform); inside a
         // round, lanes past the end convert a copy of block 0 (see stage_slice)
         if (s * wg_threads() < total) {
+            // (SKIP: lanes past the end loaded nothing; whole 8-lane groups)
+            if (SKIP && threadIdx.x + s * wg_threads() >= total) continue;
             const uint32_t t = stage_slice(s, total);
             limb_slice<Q40PERM>(p.v[s], t & 7, recs + (t >> 3));
         }
@@ -433,15 +458,18 @@ RT_DEV void stage_x_convert(XPre& p, const float* gamma, float eps, uint32_t nxb
 // attention kernel's last workgroup does (o = Σ o_s·e^(m_s−M) / Σ l_s·e^(m_s−M),
 // splits in order), then builds the slice's limbs.
 struct AttnX {};
+struct AttnXC {};  // the same, produced inside a persistent launch (device-scope loads)
 template <typename XT>
-constexpr bool is_attn_x() { return __is_same(XT, AttnX); }
+constexpr bool is_attn_x() { return __is_same(XT, AttnX) || __is_same(XT, AttnXC); }
 constexpr uint32_t kAttnXMaxSplits = 8;
 struct XPreAttn {
     f32x4 o[kAttnXMaxSplits];
     float m[kAttnXMaxSplits], l[kAttnXMaxSplits];
 };
+template <bool COH = false>
 RT_DEV void stage_attn_load(const void* part, const float* ml, uint32_t nsp, uint32_t hd,
                             uint32_t nxb, XPreAttn& p) {
+    if (COH && threadIdx.x >= nxb * 8) return;  // (as stage_x_load for CohF32)
     const uint32_t t = stage_slice(0, nxb * 8);
     const uint32_t i = (t >> 3) * 32 + (t & 7) * 4;  // 4 elements of one head
     const uint32_t h = i / hd, d = i % hd;
@@ -451,15 +479,23 @@ RT_DEV void stage_attn_load(const void* part, const float* ml, uint32_t nsp, uin
         // merge ignores them)
         const uint32_t jj = j < nsp ? j : nsp - 1;
         const size_t row = (size_t)h * nsp + jj;
-        p.o[j] = *(const f32x4*)((const float*)part + row * hd + d);
-        const float2 v = *(const float2*)(ml + row * 2);
-        p.m[j] = v.x;
-        p.l[j] = v.y;
+        const float* po = (const float*)part + row * hd + d;
+        if constexpr (COH) {
+            p.o[j] = f32x4{dev_load(po), dev_load(po + 1), dev_load(po + 2), dev_load(po + 3)};
+            p.m[j] = dev_load(ml + row * 2);
+            p.l[j] = dev_load(ml + row * 2 + 1);
+        } else {
+            p.o[j] = *(const f32x4*)po;
+            const float2 v = *(const float2*)(ml + row * 2);
+            p.m[j] = v.x;
+            p.l[j] = v.y;
+        }
     }
 }
-template <bool Q40PERM>
+template <bool Q40PERM, bool SKIP = false>
 RT_DEV void stage_attn_convert(const XPreAttn& p, uint32_t nsp, uint32_t nxb,
                                XRec* __restrict__ recs) {
+    if (SKIP && threadIdx.x >= nxb * 8) return;
     const uint32_t t = stage_slice(0, nxb * 8);
     float M = -__builtin_huge_valf();
 #pragma unroll

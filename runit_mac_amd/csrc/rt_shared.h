@@ -23,3 +23,10 @@ constexpr uint64_t RT_SCRATCH_WS_OFF = 64ull << 10;
 constexpr uint64_t RT_SCRATCH_WS_BYTES = 1ull << 20;
 constexpr uint64_t RT_SCRATCH_PART_OFF = RT_SCRATCH_WS_OFF + RT_SCRATCH_WS_BYTES;
 constexpr uint64_t RT_SCRATCH_PART_BYTES = RT_SCRATCH_BYTES - RT_SCRATCH_PART_OFF;
+
+// Persistent decode step (k_step.hip): phase record size and the most
+// workgroups a step grid may have.
+constexpr uint32_t RT_STEP_PHASE_BYTES = 368;
+constexpr uint32_t RT_STEP_MAX_WGS = 1024;
+constexpr uint32_t RT_STEP_SYNC_BYTES = 2048;  // StepSync (k_step.hip)
+constexpr uint32_t RT_STEP_STATUS_OFF = 1280;  // its status word

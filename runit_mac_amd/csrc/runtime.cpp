@@ -65,7 +65,7 @@ constexpr size_t kAuxBytes = 65536;
 constexpr uint32_t kAttnCounters = (kAuxBytes - kAuxAttnOff) / 4;
 
 const char* const kKernelNames[] = {
-    "k_fill_u32",
+    "k_fill_u32", "k_decode_step_q8_0",
     "k_gemv_q8_0_f32_f32_r1", "k_gemv_q8_0_f32_f32_r2", "k_gemv_q8_0_attn_f32add_r1",
     "k_gemv_q8_0_f32_f32add_r1", "k_gemv_q8_0_f32_f32add_r2",
     "k_gemv_q8_0_f32_f16_r1", "k_gemv_q8_0_f32_f16_r2",
@@ -269,6 +269,22 @@ struct rt_ctx {
 };
 struct rt_event { hipEvent_t ev; };
 struct rt_graph { hipGraph_t graph; hipGraphExec_t exec; };
+struct rt_step {
+    void* phases = nullptr;  // StepPhase[nph] (device)
+    uint32_t nph = 0;
+    void* sync = nullptr;    // StepSync (device)
+    void* acts = nullptr;    // the step's activation buffers (device)
+    uint32_t grid = 0;
+    size_t lds = 0;
+    // after the persistent launch: RMSNorm + LM head, argmax
+    const void* lm_head = nullptr;
+    const float* final_norm = nullptr;
+    const float* x_final = nullptr;
+    float* logits = nullptr;
+    uint32_t* token = nullptr;
+    uint32_t vocab = 0, hidden = 0;
+    float eps = 0.0f;
+};
 
 namespace {
 
@@ -2163,6 +2179,266 @@ int rt_rms_norm_gemv_q8_0_f32in_f32out(rt_ctx* c, const void* w, const float* x,
                                        uint32_t k) {
     return norm_then(c, "k_gemv_q8_0_f32_f32", kQ8_0, plain_args(w, x, y, nullptr, m, k), false,
                      gamma, eps);
+}
+
+}  // extern "C"
+
+// ───────────────────────────── persistent decode step ─────────────────────────────
+
+namespace {
+
+// Mirrors the device-side StepPhase / StepSync (k_step.hip).
+struct StepPhaseH {
+    uint32_t kind, n0, n1, n2;
+    const void* p0;
+    const void* p1;
+    void* p2;
+    uint64_t pad;
+    GemvArgs g;
+    AttnArgs at;
+};
+static_assert(sizeof(StepPhaseH) == RT_STEP_PHASE_BYTES, "StepPhase layout");
+constexpr size_t kStepSyncBytes = RT_STEP_SYNC_BYTES;
+constexpr uint32_t kStepThreads = 1024;
+enum : uint32_t { SK_EMBED_Q8_0 = 0, SK_QKV_Q8_0 = 1, SK_ATTN_HD64 = 2, SK_OPROJ_Q8_0 = 3,
+                  SK_FFN_Q8_0 = 4, SK_DOWN_Q8_0 = 5 };
+
+// Matrix-core GEMV phase on a persistent grid of G workgroups × T threads:
+// whole K staged per workgroup, no K split through memory.  The waves that
+// share a row-quad group (ksw) split its K steps; ksw is chosen for the
+// fewest items per wave (all of which are then in flight before the grid
+// barrier), then for the most workgroups with work.
+GemvArgs step_gemv_args(const Fmt& f, uint32_t nvrows, uint32_t K, uint32_t G, uint32_t T) {
+    GemvArgs a{};
+    a.nvrows = nvrows;
+    a.K = K;
+    a.lpr = 16;
+    a.row_bytes = (uint64_t)(K / f.blk_el) * f.blk_bytes;
+    const uint32_t units = K / f.mq_units();
+    a.ksplit = 1;
+    a.kc_units = units;
+    a.xb_chunk = K / 32;
+    const uint32_t nwaves = T / 64, nsteps = (units + 15) / 16;
+    uint32_t best = 0, best_cost = ~0u, best_tiles = 0;
+    for (uint32_t ksw = 1; ksw <= nwaves; ksw *= 2) {
+        const uint32_t rows_per_wg = (nwaves / ksw) * 4;
+        const uint32_t ntiles = (nvrows + rows_per_wg - 1) / rows_per_wg;
+        const uint32_t rounds = (ntiles + G - 1) / G;
+        const uint32_t spw = (nsteps + ksw - 1) / ksw;
+        const uint32_t cost = rounds * spw;
+        const uint32_t used = std::min(ntiles, G);
+        if (cost < best_cost || (cost == best_cost && used > best_tiles)) {
+            best = ksw; best_cost = cost; best_tiles = used;
+        }
+    }
+    a.ksw = best;
+    return a;
+}
+size_t step_gemv_lds(uint32_t K) { return (size_t)(K / 32) * XREC_BYTES + 16 * 2 * 4 * sizeof(float); }
+
+}  // namespace
+
+extern "C" {
+
+int rt_decode_step_q8_0_create(rt_ctx* c, const rt_step_model* m, uint32_t pos, rt_step** out) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!m || !out || !m->layer || !m->token_embd || !m->lm_head || !m->output_norm || !m->token ||
+        !m->logits)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: decode_step: null argument");
+    const uint32_t L = m->layers, h = m->hidden, H = m->heads, KVH = m->kv_heads, hd = m->head_dim;
+    const uint32_t ff = m->ff, qd = H * hd, kvd = KVH * hd;
+    if (hd != 64 || H == 0 || KVH == 0 || H % KVH || L == 0)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: decode_step: head_dim %u, heads %u / %u (built for "
+                    "head size 64, heads a multiple of the KV heads)", hd, H, KVH);
+    if (h % 64 || ff % 64 || qd % 64 || qd / 32 * 8 > kStepThreads || 2 * ff / 32 * 8 > 4 * kStepThreads)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: decode_step: hidden %u / ff %u / q_dim %u must be "
+                    "multiples of 64 within one staging pass", h, ff, qd);
+    if (pos >= m->max_seq)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: decode_step: pos=%u ≥ max_seq=%u",
+                    pos, m->max_seq);
+    for (uint32_t l = 0; l < L; ++l) {
+        const rt_step_layer& y = m->layer[l];
+        if (!y.wq || !y.wk || !y.wv || !y.wo || !y.wg || !y.wu || !y.wd || !y.bq || !y.bk || !y.bv ||
+            !y.attn_norm || !y.ffn_norm || !y.k_cache || !y.v_cache)
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: decode_step: layer %u: null buffer", l);
+    }
+    // one workgroup per CU, all resident (the grid barrier needs every
+    // workgroup running at once)
+    const uint32_t G = std::min<uint32_t>((uint32_t)c->cu_count, RT_STEP_MAX_WGS);
+    // attention splits: ≤ 8 (the O projection's staging merges ≤ 8), ≥ 64
+    // positions each
+    const uint32_t kv_len = pos + 1;
+    const uint32_t nsp = std::min<uint32_t>(kAttnXMaxSplits, (kv_len + 63) / 64);
+    const uint32_t chunk = ((kv_len + nsp - 1) / nsp + 63) / 64 * 64;
+    const uint32_t nsp_used = (kv_len + chunk - 1) / chunk;
+    const uint32_t gm = rt_attn_gm(hd), HB = (H / KVH + gm - 1) / gm;
+    // activation buffers, each on its own 256-byte lines, fresh for every
+    // phase of the step
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t b_h = al(4 * h), b_q = al(4 * qd), b_kv = al(4 * kvd), b_ff = al(4 * ff);
+    const size_t b_part = al(4 * (size_t)H * nsp_used * hd), b_ml = al(8 * (size_t)H * nsp_used);
+    const size_t per_layer = b_q + 2 * b_kv + b_part + b_ml + b_h + b_ff + b_h;
+    const size_t acts_bytes = b_h + (size_t)L * per_layer;
+    rt_step* st = new rt_step();
+    auto cleanup = [&](int code) {
+        if (st->phases) hipFree(st->phases);
+        if (st->sync) hipFree(st->sync);
+        if (st->acts) hipFree(st->acts);
+        delete st;
+        return code;
+    };
+    hipError_t e = hipMalloc(&st->acts, acts_bytes);
+    if (e == hipSuccess) e = hipMalloc(&st->sync, kStepSyncBytes);
+    if (e == hipSuccess) e = hipMemset(st->sync, 0, kStepSyncBytes);
+    if (e != hipSuccess) return cleanup(hip_fail(c, e, "decode_step buffers"));
+    char* ap = (char*)st->acts;
+    auto take = [&](size_t b) { char* p = ap; ap += b; return (float*)p; };
+    std::vector<StepPhaseH> ph;
+    size_t lds = 0;
+    float* x = take(b_h);
+    {
+        StepPhaseH p{};
+        p.kind = SK_EMBED_Q8_0;
+        p.n0 = h;
+        p.p0 = m->token_embd;
+        p.p1 = m->token;
+        p.p2 = x;
+        ph.push_back(p);
+    }
+    for (uint32_t l = 0; l < L; ++l) {
+        const rt_step_layer& y = m->layer[l];
+        float* q = take(b_q);
+        float* k = take(b_kv);
+        float* v = take(b_kv);
+        float* part = take(b_part);
+        float* ml = take(b_ml);
+        float* x1 = take(b_h);
+        float* act = take(b_ff);
+        float* x2 = take(b_h);
+        StepPhaseH p{};
+        // RMSNorm + Q/K/V + bias
+        p.kind = SK_QKV_Q8_0;
+        p.g = step_gemv_args(kQ8_0, qd + 2 * kvd, h, G, kStepThreads);
+        p.g.w[0] = (const uint8_t*)y.wq; p.g.w[1] = (const uint8_t*)y.wk; p.g.w[2] = (const uint8_t*)y.wv;
+        p.g.out[0] = q; p.g.out[1] = k; p.g.out[2] = v;
+        p.g.aux[0] = y.bq; p.g.aux[1] = y.bk; p.g.aux[2] = y.bv;
+        p.g.n[0] = qd; p.g.n[1] = kvd; p.g.n[2] = kvd;
+        p.g.x = x;
+        p.g.gamma = y.attn_norm;
+        p.g.eps = m->eps;
+        lds = std::max(lds, step_gemv_lds(h));
+        ph.push_back(p);
+        // RoPE + KV write + split attention (partials only)
+        p = StepPhaseH{};
+        p.kind = SK_ATTN_HD64;
+        p.n0 = nsp_used;
+        p.n1 = KVH * HB;
+        p.at.q = q; p.at.kc = y.k_cache; p.at.vc = y.v_cache; p.at.out = nullptr;
+        p.at.k_new = k; p.at.v_new = v; p.at.part = part; p.at.ml = ml;
+        p.at.kv_len = kv_len; p.at.stride = m->max_seq; p.at.H = H; p.at.KVH = KVH;
+        p.at.chunk = chunk; p.at.pos = pos;
+        p.at.scale = 1.0f / sqrtf((float)hd);
+        p.at.theta = m->theta;
+        p.at.parts_only = 1;
+        ph.push_back(p);
+        // O (staging merges the partials) + residual
+        p = StepPhaseH{};
+        p.kind = SK_OPROJ_Q8_0;
+        p.g = step_gemv_args(kQ8_0, h, qd, G, kStepThreads);
+        p.g.w[0] = (const uint8_t*)y.wo;
+        p.g.out[0] = x1;
+        p.g.aux[0] = x;
+        p.g.n[0] = h;
+        p.g.x = part;
+        p.g.xml = ml;
+        p.g.xnsp = nsp_used;
+        p.g.xhd = hd;
+        lds = std::max(lds, step_gemv_lds(qd));
+        ph.push_back(p);
+        // RMSNorm + gate/up + SiLU
+        p = StepPhaseH{};
+        p.kind = SK_FFN_Q8_0;
+        p.g = step_gemv_args(kQ8_0, 2 * ff, h, G, kStepThreads);
+        p.g.w[0] = (const uint8_t*)y.wg; p.g.w[1] = (const uint8_t*)y.wu;
+        p.g.out[0] = act;
+        p.g.n[0] = ff; p.g.n[1] = ff;
+        p.g.x = x1;
+        p.g.gamma = y.ffn_norm;
+        p.g.eps = m->eps;
+        ph.push_back(p);
+        // down + residual
+        p = StepPhaseH{};
+        p.kind = SK_DOWN_Q8_0;
+        p.g = step_gemv_args(kQ8_0, h, ff, G, kStepThreads);
+        p.g.w[0] = (const uint8_t*)y.wd;
+        p.g.out[0] = x2;
+        p.g.aux[0] = x1;
+        p.g.n[0] = h;
+        p.g.x = act;
+        lds = std::max(lds, step_gemv_lds(ff));
+        ph.push_back(p);
+        x = x2;
+    }
+    // occupancy: one workgroup of kStepThreads per CU must fit
+    if (occupancy(c, "k_decode_step_q8_0", kStepThreads, lds) < 1)
+        return cleanup(fail(c, RT_ERR_DISPATCH,
+                            "kernel dispatch error: decode_step: %zu bytes of LDS leave no "
+                            "resident workgroup", lds));
+    e = hipMalloc(&st->phases, ph.size() * sizeof(StepPhaseH));
+    if (e == hipSuccess)
+        e = hipMemcpy(st->phases, ph.data(), ph.size() * sizeof(StepPhaseH), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return cleanup(hip_fail(c, e, "decode_step phases"));
+    st->nph = (uint32_t)ph.size();
+    st->grid = G;
+    st->lds = lds;
+    st->lm_head = m->lm_head;
+    st->final_norm = m->output_norm;
+    st->x_final = x;
+    st->logits = m->logits;
+    st->token = m->token;
+    st->vocab = m->vocab;
+    st->hidden = h;
+    st->eps = m->eps;
+    *out = st;
+    return RT_OK;
+}
+
+int rt_decode_step_run(rt_ctx* c, rt_step* st) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!st) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: decode_step: null step");
+    void* params[] = {&st->phases, &st->nph, &st->sync};
+    int rc = launch(c, "k_decode_step_q8_0", dim3(st->grid), dim3(kStepThreads), st->lds, params);
+    if (rc != RT_OK) return rc;
+    rc = rt_rms_norm_gemv_q8_0_f32in_f32out(c, st->lm_head, st->x_final, st->final_norm, st->eps,
+                                            st->logits, st->vocab, st->hidden);
+    if (rc != RT_OK) return rc;
+    return rt_argmax_f32(c, st->logits, st->token, st->vocab);
+}
+
+int rt_decode_step_status(rt_ctx* c, rt_step* st) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!st) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: decode_step: null step");
+    int rc = rt_flush(c);
+    if (rc != RT_OK) return rc;
+    uint32_t status = 0;
+    hipError_t e = hipMemcpy(&status, (char*)st->sync + RT_STEP_STATUS_OFF, 4,
+                             hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(c, e, "decode_step status");
+    if (status)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: decode_step: a grid barrier timed out (workgroups "
+                    "not all resident?)");
+    return RT_OK;
+}
+
+void rt_decode_step_destroy(rt_step* st) {
+    if (!st) return;
+    if (st->phases) hipFree(st->phases);
+    if (st->sync) hipFree(st->sync);
+    if (st->acts) hipFree(st->acts);
+    delete st;
 }
 
 }  // extern "C"

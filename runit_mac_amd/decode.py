@@ -462,6 +462,29 @@ class DecodeModel:
             raise RuntimeError("no fused step has run yet")
         return self._launches
 
+    def plan_persistent(self, pos: int) -> d.DecodeStep:
+        """The step at `pos` as one persistent launch (k_decode_step_q8_0:
+        embedding and every layer, weights of each phase requested before the
+        grid barrier that precedes it) + the norm-fused LM head + argmax.
+        Q8_0 models with head size 64."""
+        if self.embd_fmt != "q8_0" or self.lm_fmt != "q8_0" or \
+                any(f != "q8_0" for F in self.fmts for f in F.values()):
+            raise ValueError("the persistent step is built for Q8_0 models")
+        c = self.cfg
+        layers = (d.StepLayer * c.layers)()
+        for i, L in enumerate(self.layers):
+            for k_dev, k_c in (("wq", "wq"), ("wk", "wk"), ("wv", "wv"), ("wo", "wo"), ("wg", "wg"),
+                               ("wu", "wu"), ("wd", "wd"), ("bq", "bq"), ("bk", "bk"),
+                               ("bv", "bv"), ("attn_norm", "attn_norm"),
+                               ("ffn_norm", "ffn_norm"), ("kc", "k_cache"), ("vc", "v_cache")):
+                setattr(layers[i], k_c, L[k_dev])
+        model = d.StepModel(c.layers, c.hidden, c.heads, c.kv_heads, c.head_dim, c.ff, c.vocab,
+                            c.max_seq, c.eps, c.theta, layers, self.embd, self.lm_head,
+                            self.final_norm, self.token, self.logits)
+        step = d.DecodeStep(self.ctx, model, pos)
+        step._layers = layers
+        return step
+
     def capture(self, pos: int, fused: bool = True) -> d.Graph:
         """One step captured as a HIP graph (the reference's single command
         buffer per token, context.rs:248-296)."""

@@ -144,6 +144,45 @@ _SIGS = {
 }
 
 
+class StepLayer(ctypes.Structure):
+    """rt_step_layer (include/runit_hip.h)."""
+    _fields_ = [(n, c_void_p) for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd", "bq", "bk",
+                                        "bv", "attn_norm", "ffn_norm", "k_cache", "v_cache")]
+
+
+class StepModel(ctypes.Structure):
+    """rt_step_model (include/runit_hip.h)."""
+    _fields_ = [(n, c_uint32) for n in ("layers", "hidden", "heads", "kv_heads", "head_dim", "ff",
+                                        "vocab", "max_seq")] + \
+               [("eps", ctypes.c_float), ("theta", ctypes.c_float),
+                ("layer", POINTER(StepLayer))] + \
+               [(n, c_void_p) for n in ("token_embd", "lm_head", "output_norm", "token", "logits")]
+
+
+class DecodeStep:
+    """A planned persistent decode step (rt_decode_step_*): one launch for the
+    embedding and every layer, then the LM head and the argmax."""
+
+    def __init__(self, ctx: "HipContext", model: StepModel, pos: int):
+        self.ctx, self._model = ctx, model
+        h = c_void_p()
+        ctx._check(ctx.lib.rt_decode_step_q8_0_create(ctx.handle, ctypes.byref(model), pos,
+                                                      ctypes.byref(h)))
+        self.handle = h.value
+
+    def run(self) -> None:
+        self.ctx._check(self.ctx.lib.rt_decode_step_run(self.ctx.handle, self.handle))
+
+    def check(self) -> None:
+        """Flushes; raises Dispatch if a grid barrier of any run timed out."""
+        self.ctx._check(self.ctx.lib.rt_decode_step_status(self.ctx.handle, self.handle))
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            self.ctx.lib.rt_decode_step_destroy(self.handle)
+            self.handle = None
+
+
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     """Loads librunit_hip.so and declares every entry point's signature."""
     global _lib
@@ -166,6 +205,14 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.rt_event_destroy.restype = None
     lib.rt_graph_destroy.argtypes = [_P]
     lib.rt_graph_destroy.restype = None
+    lib.rt_decode_step_q8_0_create.argtypes = [_P, POINTER(StepModel), c_uint32, POINTER(c_void_p)]
+    lib.rt_decode_step_q8_0_create.restype = c_int
+    lib.rt_decode_step_run.argtypes = [_P, _P]
+    lib.rt_decode_step_run.restype = c_int
+    lib.rt_decode_step_status.argtypes = [_P, _P]
+    lib.rt_decode_step_status.restype = c_int
+    lib.rt_decode_step_destroy.argtypes = [_P]
+    lib.rt_decode_step_destroy.restype = None
     # GGUF reader: (name, argtypes, restype)
     PU64 = POINTER(c_uint64)
     for name, argtypes, restype in (
