@@ -1,31 +1,7 @@
 // k_decode.hip — the non-GEMV kernels of one decode step: RMSNorm, RoPE,
 // KV-cache scatter, decode attention (plain and fused with RoPE + cache
 // write) and the Q8_0 embedding lookup.
-#include "rt_device.h"
-#include "rt_shared.h"
-
-// Sum over a workgroup (any multiple of 64 threads ≤ 1024); `red` holds ≥ 16
-// floats of LDS.  Every thread receives the total.
-RT_DEV float block_sum(float v, float* red) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    const uint32_t w = threadIdx.x >> 6, nw = wg_threads() >> 6;
-    __syncthreads();  // previous users of `red` are done
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float t = 0.0f;
-    for (uint32_t i = 0; i < nw; ++i) t += red[i];
-    return t;
-}
-RT_DEV float block_max(float v, float* red) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    const uint32_t w = threadIdx.x >> 6, nw = wg_threads() >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float t = -__builtin_huge_valf();
-    for (uint32_t i = 0; i < nw; ++i) t = fmaxf(t, red[i]);
-    return t;
-}
+#include "rt_attn.h"
 
 // rms_norm_f32_f32_f32g (norm.metal:126-154): one workgroup per row,
 // y = x · rsqrt(mean(x²) + eps) · γ.  y may alias x.
@@ -76,13 +52,6 @@ k_rms_norm_f32g(const float* x, float* y, const float* gamma, float eps, uint32_
     for (uint32_t i = tid; i < hidden; i += nt) yr[i] = xr[i] * rms * gamma[i];
 }
 
-// RoPE angle for pair d (fused_rope.metal:34-38): freq = 1/θ^(2d/hd).
-RT_DEV void rope_cs(uint32_t d, uint32_t head_dim, uint32_t pos, float theta, float& c, float& s) {
-    const float freq = 1.0f / powf(theta, (float)(2 * d) / (float)head_dim);
-    const float angle = (float)pos * freq;
-    sincosf(angle, &s, &c);
-}
-
 // fused_rope_qk_f32 (fused_rope.metal:17-56): non-interleaved pairs (d, d+hd/2).
 extern "C" __global__ void __launch_bounds__(256)
 k_rope_qk_f32(float* Q, float* K, uint32_t head_dim, uint32_t q_heads, uint32_t kv_heads,
@@ -116,287 +85,6 @@ k_kv_copy_f32(const float* src, float* dst, uint32_t pos, uint32_t max_seq, uint
     const uint32_t h = t / head_dim, d = t % head_dim;
     dst[((size_t)h * max_seq + pos) * head_dim + d] = src[t];
 }
-
-// ───────────────────────────── attention ─────────────────────────────
-//
-// Split-KV decode attention.  Decode attention reads a few hundred KB per
-// layer, so it is bound by memory latency, not bandwidth: the design keeps the
-// number of dependent memory round trips per workgroup at one per 64
-// positions and spreads the positions over many workgroups.
-//
-// Grid (nsplit, num_kv_heads · head_blocks, batch), 256 threads.  Workgroup
-// (s, kvh·HB + hb, b) takes positions [s·chunk, min(kv_len, (s+1)·chunk)) of
-// kv head kvh for the (up to rt_attn_gm(HD)) query heads of head block hb of that kv
-// head's group, so each K/V row is fetched once for all of them.  Per 64
-// positions:
-//   loads  : thread t holds a quarter of key row t/4 and HD/16 float4 of the
-//            value rows ≡ t/(HD/4) (mod 1024/HD), column t % (HD/4) — all
-//            issued together;
-//   scores : quarter dots reduced over 4 lanes, written to LDS;
-//   softmax: one wave per query head (64 lanes = 64 positions), running
-//            max / sum with rescaling (the online softmax of
-//            attention.metal:248-308);
-//   output : each thread accumulates its value rows weighted by the
-//            probabilities.
-// With nsplit > 1 each workgroup writes (m, l, o) for its heads; the last
-// workgroup of a (b, kvh, hb) group to arrive (arrival counter, reset by that
-// workgroup) merges the splits in split order.
-constexpr uint32_t ATT_SUB = 64;  // positions per inner step
-
-struct AttnArgs {
-    const float* q;       // [batch][H][HD]; with rope: the raw query of the token
-    float* kc;            // cache [batch][KVH][stride][HD]
-    float* vc;
-    float* out;           // [batch][H][HD]
-    const float* k_new;   // rope: raw key / value of the token, [KVH][HD]
-    const float* v_new;
-    float* part;          // nsplit > 1: [batch][H][nsplit][HD] unnormalised outputs
-    float* ml;            //             [batch][H][nsplit][2] running max, sum
-    uint32_t* counters;   //             [batch][KVH][HB] arrival counters
-    uint32_t kv_len, stride, H, KVH, chunk, pos;
-    float scale, theta;
-    uint32_t parts_only;  // write (o, m, l) of every split, merge nothing (the
-                          // consumer merges: k_gemv_q8_0_attn_f32add)
-};
-
-// (s, nsp, y, b): the split, the number of splits, the (kv head, head
-// block) index and the batch row — the grid position of a stand-alone launch,
-// or a persistent kernel's virtual one.  COH: q / k / v come from other
-// workgroups of the same launch (device-scope loads); Hook: see NoHook.
-template <int HD, bool ROPE, int HG, int GMT, bool COH = false, class Hook = NoHook>
-RT_DEV void attn_split(const AttnArgs& a, uint32_t s, uint32_t nsp, uint32_t y, uint32_t b,
-                       const Hook& hook = Hook()) {
-    // HG groups of 256 threads share the block's query heads: group g takes
-    // heads g, g + HG, ... (shorter per-thread chains; every group reads the
-    // same K / V rows)
-    constexpr uint32_t GM = GMT, SUB = ATT_SUB, NT = 256 * HG, HPT = GM / HG;
-    constexpr uint32_t NQ = HD / 16;   // float4 per thread: K quarter row, V rows
-    constexpr uint32_t C4 = HD / 4;    // float4 columns of a row
-    constexpr uint32_t PG = 256 / C4;  // value position groups
-    static_assert(SUB == 64 && NQ * PG == SUB && GM % HG == 0, "layout");
-    __shared__ f32x4 qs4[GM][C4];
-    __shared__ f32x4 ks4[C4], vs4[C4];
-    __shared__ float sc[GM][SUB];
-    __shared__ float m_run[GM], l_run[GM], resc[GM];
-    __shared__ f32x4 ored[4][GM][C4];
-    __shared__ uint32_t last_flag;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const uint32_t hg = tid >> 8, lt = tid & 255, lw = w & 3;  // group, thread / wave in group
-    const uint32_t G = a.H / a.KVH, HB = (G + GM - 1) / GM;
-    const uint32_t kvh = y / HB, hb = y % HB;
-    const uint32_t gh = min(GM, G - hb * GM);
-    const uint32_t h0 = kvh * G + hb * GM;  // first query head of the block
-    const size_t kvb = ((size_t)b * a.KVH + kvh) * a.stride * HD;
-    float* kc = a.kc + kvb;
-    float* vc = a.vc + kvb;
-    const uint32_t p_begin = s * a.chunk, p_end = min(a.kv_len, p_begin + a.chunk);
-    float* qsf = (float*)qs4;
-    const uint32_t kp = lt >> 2, kq = lt & 3;      // key layout
-    const uint32_t vcol = lt % C4, vg = lt / C4;  // value layout
-    // K / V rows of a step (rows past the range load row p_begin: in bounds,
-    // their scores are masked); the first step's loads are issued before the
-    // query staging, each later step's while the previous one computes
-    auto load_kv = [&](uint32_t p0, f32x4 (&kr)[NQ], f32x4 (&vr)[NQ]) {
-        const uint32_t pk = p0 + kp;
-        const f32x4* krow = (const f32x4*)(kc + (size_t)(pk < p_end ? pk : p_begin) * HD) + kq * NQ;
-#pragma unroll
-        for (uint32_t i = 0; i < NQ; ++i) kr[i] = krow[i];
-#pragma unroll
-        for (uint32_t i = 0; i < NQ; ++i) {
-            const uint32_t pv = p0 + vg + i * PG;
-            vr[i] = ((const f32x4*)(vc + (size_t)(pv < p_end ? pv : p_begin) * HD))[vcol];
-        }
-    };
-    f32x4 kr[NQ], vr[NQ];
-    if (p_begin < p_end) load_kv(p_begin, kr, vr);
-    hook();
-    auto act = [&](const float* p) { if constexpr (COH) return dev_load(p); else return *p; };
-    if constexpr (ROPE) {
-        // fused_rope_qk_f32 (fused_rope.metal:28-55) on the block's query
-        // heads and on the kv head's key
-        constexpr uint32_t half = HD / 2;
-        for (uint32_t i = tid; i < (gh + 1) * half; i += NT) {
-            const uint32_t hh = i / half, d = i % half;
-            float c, sn;
-            rope_cs(d, HD, a.pos, a.theta, c, sn);
-            const float* src = hh < gh ? a.q + (size_t)(h0 + hh) * HD : a.k_new + (size_t)kvh * HD;
-            float* dst = hh < gh ? qsf + hh * HD : (float*)ks4;
-            const float r = act(src + d), im = act(src + d + half);
-            dst[d] = r * c - im * sn;
-            dst[d + half] = r * sn + im * c;
-        }
-        for (uint32_t d = tid; d < HD; d += NT) ((float*)vs4)[d] = act(a.v_new + (size_t)kvh * HD + d);
-    } else {
-        const float* q = a.q + ((size_t)b * a.H + h0) * HD;
-        for (uint32_t i = tid; i < gh * HD; i += NT) qsf[i] = act(q + i);
-    }
-    if (tid < GM) {
-        m_run[tid] = -__builtin_huge_valf();
-        l_run[tid] = 0.0f;
-    }
-    lds_barrier();
-    if constexpr (ROPE) {
-        // kv_copy_to_cache_f32 (activation.metal:30-45) of the rotated key and
-        // the value, by the one workgroup whose range holds `pos`
-        if (hb == 0 && a.pos >= p_begin && a.pos < p_end)
-            for (uint32_t d = tid; d < HD; d += NT) {
-                kc[(size_t)a.pos * HD + d] = ((const float*)ks4)[d];
-                vc[(size_t)a.pos * HD + d] = ((const float*)vs4)[d];
-            }
-    }
-    f32x4 oacc[HPT];  // heads hg + HG·j
-#pragma unroll
-    for (uint32_t j = 0; j < HPT; ++j) oacc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t p0 = p_begin; p0 < p_end; p0 += SUB) {
-        const uint32_t pk = p0 + kp;
-        const bool kvalid = pk < p_end;
-        f32x4 kn[NQ], vn[NQ];
-        if (p0 + SUB < p_end) load_kv(p0 + SUB, kn, vn);  // next step (workgroup-uniform)
-        if constexpr (ROPE) {
-            // position `pos` comes from LDS (the cache write above may not be
-            // visible to this workgroup's loads, and other workgroups never
-            // read it)
-            if (pk == a.pos)
-#pragma unroll
-                for (uint32_t i = 0; i < NQ; ++i) kr[i] = ks4[kq * NQ + i];
-#pragma unroll
-            for (uint32_t i = 0; i < NQ; ++i)
-                if (p0 + vg + i * PG == a.pos) vr[i] = vs4[vcol];
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < HPT; ++j) {
-            const uint32_t h = hg + HG * j;
-            if (h < gh) {
-                float dot = 0.0f;
-#pragma unroll
-                for (uint32_t i = 0; i < NQ; ++i) {
-                    const f32x4 qv = qs4[h][kq * NQ + i];
-                    dot += qv.x * kr[i].x + qv.y * kr[i].y + qv.z * kr[i].z + qv.w * kr[i].w;
-                }
-                dot = group_sum(dot, 4);
-                if (kq == 0) sc[h][kp] = kvalid ? dot * a.scale : -__builtin_huge_valf();
-            }
-        }
-        lds_barrier();
-        // softmax: wave w takes query heads w, w + 4·HG (one or two per wave)
-#pragma unroll
-        for (uint32_t u = 0; u < (GM + 4 * HG - 1) / (4 * HG); ++u) {
-            const uint32_t h = w + 4 * HG * u;
-            if (h < GM) {  // wave-uniform
-                const float sv = h < gh ? sc[h][lane] : -__builtin_huge_valf();
-                const float mx = group_max(sv, 64);
-                const float m_old = h < gh ? m_run[h] : 0.0f, m_new = fmaxf(m_old, mx);
-                const float e = (sv == -__builtin_huge_valf()) ? 0.0f : expf(sv - m_new);
-                const float sum = group_sum(e, 64);
-                if (h < gh) {
-                    sc[h][lane] = e;
-                    if (lane == 0) {
-                        const float r =
-                            (m_old == -__builtin_huge_valf()) ? 0.0f : expf(m_old - m_new);
-                        resc[h] = r;
-                        l_run[h] = l_run[h] * r + sum;
-                        m_run[h] = m_new;
-                    }
-                }
-            }
-        }
-        lds_barrier();
-#pragma unroll
-        for (uint32_t j = 0; j < HPT; ++j) {
-            const uint32_t h = hg + HG * j;
-            if (h < gh) {
-                f32x4 acc = oacc[j] * resc[h];
-#pragma unroll
-                for (uint32_t i = 0; i < NQ; ++i) acc += sc[h][vg + i * PG] * vr[i];
-                oacc[j] = acc;
-            }
-        }
-        lds_barrier();  // sc / resc reused by the next step
-        if (p0 + SUB < p_end) {
-#pragma unroll
-            for (uint32_t i = 0; i < NQ; ++i) {
-                kr[i] = kn[i];
-                vr[i] = vn[i];
-            }
-        }
-    }
-    // sum the value position groups: within the wave, then over the group's
-    // 4 waves
-#pragma unroll
-    for (uint32_t j = 0; j < HPT; ++j) {
-        const uint32_t h = hg + HG * j;
-        if (h < gh) {
-            f32x4 v = oacc[j];
-            if constexpr (C4 == 16) {
-                v.x += swz_xor_f<16>(v.x);
-                v.y += swz_xor_f<16>(v.y);
-                v.z += swz_xor_f<16>(v.z);
-                v.w += swz_xor_f<16>(v.w);
-            }
-            if constexpr (C4 <= 32) {
-                v.x += __shfl_xor(v.x, 32, 64);
-                v.y += __shfl_xor(v.y, 32, 64);
-                v.z += __shfl_xor(v.z, 32, 64);
-                v.w += __shfl_xor(v.w, 32, 64);
-            }
-            if (lane < C4) ored[lw][h][lane] = v;
-        }
-    }
-    lds_barrier();
-    const bool direct = nsp == 1 && !a.parts_only;
-    for (uint32_t i = tid; i < gh * C4; i += NT) {
-        const uint32_t h = i / C4, c = i % C4;
-        const f32x4 t = ored[0][h][c] + ored[1][h][c] + ored[2][h][c] + ored[3][h][c];
-        if (direct) {
-            const float l = l_run[h];
-            ((f32x4*)(a.out + ((size_t)b * a.H + h0 + h) * HD))[c] = t * (l > 0.0f ? 1.0f / l : 0.0f);
-        } else {
-            float* pp = a.part + (((size_t)b * a.H + h0 + h) * nsp + s) * HD + 4 * c;
-            dev_store(pp + 0, t.x);
-            dev_store(pp + 1, t.y);
-            dev_store(pp + 2, t.z);
-            dev_store(pp + 3, t.w);
-        }
-    }
-    if (direct) return;
-    if (tid < gh) {
-        float* mlp = a.ml + (((size_t)b * a.H + h0 + tid) * nsp + s) * 2;
-        dev_store(mlp + 0, m_run[tid]);
-        dev_store(mlp + 1, l_run[tid]);
-    }
-    if (a.parts_only) return;
-    dev_stores_done();
-    __syncthreads();
-    uint32_t* counter = a.counters + ((size_t)b * a.KVH + kvh) * HB + hb;
-    if (tid == 0) last_flag = arrive(counter) == nsp - 1;
-    __syncthreads();
-    if (!last_flag) return;
-    // merge the splits in split order: o = Σ o_s·e^(m_s−M) / Σ l_s·e^(m_s−M)
-    for (uint32_t i = tid; i < gh * C4; i += NT) {
-        const uint32_t h = i / C4, c = i % C4;
-        const size_t row = ((size_t)b * a.H + h0 + h) * nsp;
-        const float* mlv = a.ml + row * 2;
-        float M = -__builtin_huge_valf();
-#pragma unroll 8
-        for (uint32_t j = 0; j < nsp; ++j) M = fmaxf(M, dev_load(mlv + 2 * j));
-        float L = 0.0f;
-        f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-        for (uint32_t j = 0; j < nsp; ++j) {
-            const float f = expf(dev_load(mlv + 2 * j) - M);
-            L += dev_load(mlv + 2 * j + 1) * f;
-            const float* pj = a.part + (row + j) * HD + 4 * c;
-            o += f32x4{dev_load(pj), dev_load(pj + 1), dev_load(pj + 2), dev_load(pj + 3)} * f;
-        }
-        ((f32x4*)(a.out + ((size_t)b * a.H + h0 + h) * HD))[c] = o * (L > 0.0f ? 1.0f / L : 0.0f);
-    }
-    if (tid == 0) dev_store(counter, 0u);  // ready for the next call (also under graph replay)
-}
-
-// Head groups and query heads per workgroup: rt_attn_hg / rt_attn_gm
-// (rt_shared.h, shared with the host's grid sizing).
-template <int HD> constexpr int attn_hg() { return (int)rt_attn_hg(HD); }
-template <int HD> constexpr int attn_gm() { return (int)rt_attn_gm(HD); }
 
 #define RT_ATTN_KERNELS(HD)                                                                \
     extern "C" __global__ void __launch_bounds__(256 * attn_hg<HD>())                     \

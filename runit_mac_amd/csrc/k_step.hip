@@ -36,6 +36,8 @@
 // after kStepSpinTicks of the 100 MHz real-time clock (50 ms) the workgroup
 // records the timeout in the status word and goes on, so the launch always
 // ends; the host reports a set status as an error.
+#include "rt_attn.h"
+#include "rt_gemv.h"
 #include "rt_shared.h"
 
 enum StepKind : uint32_t {

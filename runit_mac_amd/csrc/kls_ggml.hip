@@ -1,0 +1,17 @@
+// kls_ggml.hip — LDS-streamed GEMV kernels of rt_gemv_ls.h (ggml).
+#include "rt_gemv_ls.h"
+
+RT_GEMV_LS(k_gemv_q4_0g_f32_f32, FmtQ4_0G, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q4_0g_f32_f32add, FmtQ4_0G, EPI_F32_ADD, float)
+RT_GEMV_LS(k_ffn_q4_0g, FmtQ4_0G, EPI_FFN, float)
+RT_GEMV_LS(k_gemv_q4kg_f32_f32, FmtQ4KG, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q4kg_f32_f32add, FmtQ4KG, EPI_F32_ADD, float)
+RT_GEMV_LS(k_ffn_q4kg, FmtQ4KG, EPI_FFN, float)
+RT_GEMV_LS(k_gemv_q5kg_f32_f32, FmtQ5KG, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q5kg_f32_f32add, FmtQ5KG, EPI_F32_ADD, float)
+RT_GEMV_LS(k_ffn_q5kg, FmtQ5KG, EPI_FFN, float)
+RT_GEMV_LSB(k_gemv_q6kg_f32_f32, FmtQ6KGB, EPI_F32, float, 256)
+RT_GEMV_LSB(k_gemv_q6kg_f32_f32add, FmtQ6KGB, EPI_F32_ADD, float, 256)
+RT_GEMV_LSK(k_gemv_q4kg_f32_f32add, FmtQ4KG, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_gemv_q5kg_f32_f32add, FmtQ5KG, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_gemv_q4_0g_f32_f32add, FmtQ4_0G, EPI_F32_ADD, float, 1024)

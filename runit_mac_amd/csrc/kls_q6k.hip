@@ -1,0 +1,5 @@
+// kls_q6k.hip — LDS-streamed GEMV kernels of rt_gemv_ls.h (q6k).
+#include "rt_gemv_ls.h"
+
+RT_GEMV_LSB(k_gemv_q6k_f32_f32, FmtQ6KB, EPI_F32, float, 256)
+RT_GEMV_LSB(k_gemv_q6k_f32_f32add, FmtQ6KB, EPI_F32_ADD, float, 256)

@@ -1,0 +1,13 @@
+// kls_q8_0.hip — LDS-streamed GEMV kernels of rt_gemv_ls.h (q8_0).
+#include "rt_gemv_ls.h"
+
+RT_GEMV_LS(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float)
+RT_GEMV_LS(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float)
+RT_GEMV_LS(k_gemv_q8_0_f32_f16, FmtQ8_0, EPI_F16, float)
+RT_GEMV_LS(k_qkv_bias_q8_0, FmtQ8_0, EPI_QKV_BIAS, float)
+RT_GEMV_LS(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float)
+
+// Workgroup-local K split kernels (the residual / plain forms of the down
+// projections and the FFNs of long-K models)
+RT_GEMV_LSK(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float, 1024)
+RT_GEMV_LSK(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float, 1024)

@@ -1,5 +1,5 @@
-// k_gemv.hip — M=1 quantized GEMV, fused QKV(+bias) and fused gate+up+SiLU
-// kernels for gfx950.
+// rt_gemv.h — M=1 quantized GEMV, fused QKV(+bias) and fused gate+up+SiLU
+// kernel bodies for gfx950 (instantiated by the kg_*.hip files).
 //
 // One kernel template serves every format and epilogue:
 //   1. the workgroup turns the activation vector into limb records in LDS
@@ -11,6 +11,7 @@
 // Virtual rows let one launch cover several matrices: fused QKV maps row r to
 // (Q|K|V, local row); fused FFN interleaves gate and up rows so both dots of
 // an output land in the same lane.
+#pragma once
 #include "rt_formats.h"
 
 struct GemvArgs {
@@ -653,91 +654,6 @@ RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
     }
 
 // Q8_0 (gemv_q8_0.metal, gemv_multirow.metal, fused_qkv.metal, fused_ffn.metal)
-RT_GEMV_KERNEL512(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float, 1)
-RT_GEMV_KERNEL512(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float, 1)
-RT_GEMV_KERNEL512(k_gemv_q8_0_f32_f16, FmtQ8_0, EPI_F16, float, 1)
-RT_GEMV_KERNEL512(k_gemv_q8_0_f16_f16, FmtQ8_0, EPI_F16, uint16_t, 1)
-RT_GEMV_KERNEL512(k_gemv_q8_0_f16_f16add, FmtQ8_0, EPI_F16_ADD, uint16_t, 1)
-RT_GEMV_KERNEL512(k_gemv_q8_0_f16_f32add, FmtQ8_0, EPI_F32_ADD, uint16_t, 1)
-RT_GEMV_KERNEL512(k_qkv_q8_0, FmtQ8_0, EPI_QKV, float, 1)
-RT_GEMV_KERNEL512(k_qkv_bias_q8_0, FmtQ8_0, EPI_QKV_BIAS, float, 1)
-RT_GEMV_KERNEL512(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float, 1)
-// Q4_0 (gemv_q4_0.metal)
-RT_GEMV_KERNEL(k_gemv_q4_0_f32_f32, FmtQ4_0, EPI_F32, float, 2)
-RT_GEMV_KERNEL(k_gemv_q4_0_f32_f32add, FmtQ4_0, EPI_F32_ADD, float, 2)
-RT_GEMV_KERNEL(k_gemv_q4_0_f32_f16, FmtQ4_0, EPI_F16, float, 2)
-RT_GEMV_KERNEL(k_gemv_q4_0_f16_f16, FmtQ4_0, EPI_F16, uint16_t, 2)
-RT_GEMV_KERNEL(k_gemv_q4_0_f16_f16add, FmtQ4_0, EPI_F16_ADD, uint16_t, 2)
-RT_GEMV_KERNEL(k_qkv_bias_q4_0, FmtQ4_0, EPI_QKV_BIAS, float, 2)
-RT_GEMV_KERNEL(k_ffn_q4_0, FmtQ4_0, EPI_FFN, float, 2)
-RT_GEMV_KERNEL_S(k_gemv_q8_0_f32_f32, FmtQ8_0S, EPI_F32, float, 2)
-RT_GEMV_KERNEL_S(k_gemv_q8_0_f32_f32add, FmtQ8_0S, EPI_F32_ADD, float, 2)
-RT_GEMV_KERNEL_S(k_gemv_q8_0_f32_f16, FmtQ8_0S, EPI_F16, float, 2)
-RT_GEMV_KERNEL_S(k_gemv_q8_0_f16_f16, FmtQ8_0S, EPI_F16, uint16_t, 2)
-RT_GEMV_KERNEL_S(k_gemv_q8_0_f16_f16add, FmtQ8_0S, EPI_F16_ADD, uint16_t, 2)
-RT_GEMV_KERNEL_S(k_gemv_q8_0_f16_f32add, FmtQ8_0S, EPI_F32_ADD, uint16_t, 2)
-RT_GEMV_KERNEL_S(k_qkv_q8_0, FmtQ8_0S, EPI_QKV, float, 2)
-RT_GEMV_KERNEL_S(k_qkv_bias_q8_0, FmtQ8_0S, EPI_QKV_BIAS, float, 2)
-RT_GEMV_KERNEL_S(k_ffn_q8_0, FmtQ8_0S, EPI_FFN, float, 2)
-RT_GEMV_KERNEL_S(k_gemv_q4_0_f32_f32, FmtQ4_0S, EPI_F32, float, 4)
-RT_GEMV_KERNEL_S(k_gemv_q4_0_f32_f32add, FmtQ4_0S, EPI_F32_ADD, float, 4)
-RT_GEMV_KERNEL_S(k_gemv_q4_0_f32_f16, FmtQ4_0S, EPI_F16, float, 4)
-RT_GEMV_KERNEL_S(k_gemv_q4_0_f16_f16, FmtQ4_0S, EPI_F16, uint16_t, 4)
-RT_GEMV_KERNEL_S(k_gemv_q4_0_f16_f16add, FmtQ4_0S, EPI_F16_ADD, uint16_t, 4)
-RT_GEMV_KERNEL_S(k_qkv_bias_q4_0, FmtQ4_0S, EPI_QKV_BIAS, float, 4)
-RT_GEMV_KERNEL_S(k_ffn_q4_0, FmtQ4_0S, EPI_FFN, float, 4)
-// Q4_K (gemv_q4k.metal)
-RT_GEMV_KERNEL(k_gemv_q4k_f32_f32, FmtQ4K, EPI_F32, float, 1)
-RT_GEMV_KERNEL(k_gemv_q4k_f32_f32add, FmtQ4K, EPI_F32_ADD, float, 1)
-RT_GEMV_KERNEL(k_gemv_q4k_f16_f16, FmtQ4K, EPI_F16, uint16_t, 1)
-RT_GEMV_KERNEL(k_gemv_q4k_f16_f16add, FmtQ4K, EPI_F16_ADD, uint16_t, 1)
-RT_GEMV_KERNEL(k_gemv_q4k_f16_f32add, FmtQ4K, EPI_F32_ADD, uint16_t, 1)
-RT_GEMV_KERNEL(k_ffn_q4k, FmtQ4K, EPI_FFN, float, 1)
-// Q6_K (new: the reference runs Q6_K through f16-dequantised weights)
-// (matrix-core path: one super-block per lane; chunked path: 64-element units)
-RT_GEMV_KERNEL2W(k_gemv_q6k_f32_f32, FmtQ6KB, FmtQ6K, EPI_F32, float, 1, RT_Q6K_WPE)
-RT_GEMV_KERNEL2W(k_gemv_q6k_f32_f32add, FmtQ6KB, FmtQ6K, EPI_F32_ADD, float, 1, RT_Q6K_WPE)
-RT_GEMV_KERNEL2W(k_gemv_q6k_f32_f16, FmtQ6KB, FmtQ6K, EPI_F16, float, 1, RT_Q6K_WPE)
-
-// Q5_0 / Q5_K (new: the reference dequantises both on the CPU,
-// forward.rs:900-920 and 979-1012)
-RT_GEMV_KERNEL(k_gemv_q5_0_f32_f32, FmtQ5_0, EPI_F32, float, 2)
-RT_GEMV_KERNEL(k_gemv_q5_0_f32_f32add, FmtQ5_0, EPI_F32_ADD, float, 2)
-RT_GEMV_KERNEL(k_gemv_q5_0_f32_f16, FmtQ5_0, EPI_F16, float, 2)
-RT_GEMV_KERNEL(k_qkv_bias_q5_0, FmtQ5_0, EPI_QKV_BIAS, float, 2)
-RT_GEMV_KERNEL(k_ffn_q5_0, FmtQ5_0, EPI_FFN, float, 2)
-RT_GEMV_KERNEL_S(k_gemv_q5_0_f32_f32, FmtQ5_0S, EPI_F32, float, 4)
-RT_GEMV_KERNEL_S(k_gemv_q5_0_f32_f32add, FmtQ5_0S, EPI_F32_ADD, float, 4)
-RT_GEMV_KERNEL_S(k_gemv_q5_0_f32_f16, FmtQ5_0S, EPI_F16, float, 4)
-RT_GEMV_KERNEL_S(k_qkv_bias_q5_0, FmtQ5_0S, EPI_QKV_BIAS, float, 4)
-RT_GEMV_KERNEL_S(k_ffn_q5_0, FmtQ5_0S, EPI_FFN, float, 4)
-RT_GEMV_KERNEL(k_gemv_q5k_f32_f32, FmtQ5K, EPI_F32, float, 1)
-RT_GEMV_KERNEL(k_gemv_q5k_f32_f32add, FmtQ5K, EPI_F32_ADD, float, 1)
-RT_GEMV_KERNEL(k_gemv_q5k_f32_f16, FmtQ5K, EPI_F16, float, 1)
-RT_GEMV_KERNEL(k_qkv_bias_q5k, FmtQ5K, EPI_QKV_BIAS, float, 1)
-RT_GEMV_KERNEL(k_ffn_q5k, FmtQ5K, EPI_FFN, float, 1)
-
-// ggml layouts of Q4_0, Q4_K, Q5_K and Q6_K (upstream GGUF files; the
-// reference's own layouts differ, see the formats)
-RT_GEMV_KERNEL(k_gemv_q4_0g_f32_f32, FmtQ4_0G, EPI_F32, float, 2)
-RT_GEMV_KERNEL(k_gemv_q4_0g_f32_f32add, FmtQ4_0G, EPI_F32_ADD, float, 2)
-RT_GEMV_KERNEL(k_gemv_q4_0g_f32_f16, FmtQ4_0G, EPI_F16, float, 2)
-RT_GEMV_KERNEL(k_ffn_q4_0g, FmtQ4_0G, EPI_FFN, float, 2)
-RT_GEMV_KERNEL_S(k_gemv_q4_0g_f32_f32, FmtQ4_0GS, EPI_F32, float, 4)
-RT_GEMV_KERNEL_S(k_gemv_q4_0g_f32_f32add, FmtQ4_0GS, EPI_F32_ADD, float, 4)
-RT_GEMV_KERNEL_S(k_gemv_q4_0g_f32_f16, FmtQ4_0GS, EPI_F16, float, 4)
-RT_GEMV_KERNEL_S(k_ffn_q4_0g, FmtQ4_0GS, EPI_FFN, float, 4)
-RT_GEMV_KERNEL(k_gemv_q4kg_f32_f32, FmtQ4KG, EPI_F32, float, 1)
-RT_GEMV_KERNEL(k_gemv_q4kg_f32_f32add, FmtQ4KG, EPI_F32_ADD, float, 1)
-RT_GEMV_KERNEL(k_gemv_q4kg_f32_f16, FmtQ4KG, EPI_F16, float, 1)
-RT_GEMV_KERNEL(k_ffn_q4kg, FmtQ4KG, EPI_FFN, float, 1)
-RT_GEMV_KERNEL(k_gemv_q5kg_f32_f32, FmtQ5KG, EPI_F32, float, 1)
-RT_GEMV_KERNEL(k_gemv_q5kg_f32_f32add, FmtQ5KG, EPI_F32_ADD, float, 1)
-RT_GEMV_KERNEL(k_gemv_q5kg_f32_f16, FmtQ5KG, EPI_F16, float, 1)
-RT_GEMV_KERNEL(k_ffn_q5kg, FmtQ5KG, EPI_FFN, float, 1)
-RT_GEMV_KERNEL2W(k_gemv_q6kg_f32_f32, FmtQ6KGB, FmtQ6KG, EPI_F32, float, 1, RT_Q6K_WPE)
-RT_GEMV_KERNEL2W(k_gemv_q6kg_f32_f32add, FmtQ6KGB, FmtQ6KG, EPI_F32_ADD, float, 1, RT_Q6K_WPE)
-RT_GEMV_KERNEL2W(k_gemv_q6kg_f32_f16, FmtQ6KGB, FmtQ6KG, EPI_F16, float, 1, RT_Q6K_WPE)
 
 // Q, K and V projections whose matrices differ in format (Q4_K_M files keep
 // V in Q6_K) in one launch: workgroups [0, b.blk0) run Q and K (format FA),
@@ -755,22 +671,6 @@ RT_DEV void gemv_mq_pair(const GemvArgs& a, const GemvArgs& b) {
     extern "C" __global__ void __launch_bounds__(RT_GEMV_LB) NAME##_r1(GemvArgs a, GemvArgs b) { \
         gemv_mq_pair<FA, FB, EPI>(a, b);                                                       \
     }
-RT_GEMV_PAIR(k_qkv2_bias_q4k_q6k, FmtQ4K, FmtQ6K, EPI_QKV_BIAS)
-RT_GEMV_PAIR(k_qkv2_q4k_q6k, FmtQ4K, FmtQ6K, EPI_QKV)
-RT_GEMV_PAIR(k_qkv2_bias_q4kg_q6kg, FmtQ4KG, FmtQ6KG, EPI_QKV_BIAS)
-RT_GEMV_PAIR(k_qkv2_q4kg_q6kg, FmtQ4KG, FmtQ6KG, EPI_QKV)
-// all-Q4_K projections (the other layers of Q4_K_M files)
-RT_GEMV_KERNEL(k_qkv_bias_q4k, FmtQ4K, EPI_QKV_BIAS, float, 1)
-RT_GEMV_KERNEL(k_qkv_q4k, FmtQ4K, EPI_QKV, float, 1)
-RT_GEMV_KERNEL(k_qkv_bias_q4kg, FmtQ4KG, EPI_QKV_BIAS, float, 1)
-RT_GEMV_KERNEL(k_qkv_q4kg, FmtQ4KG, EPI_QKV, float, 1)
-
-// Attention output projection with the split merge folded into the staging
-// (decode_attention's merge, then gemv_q8_0_add_f32_f32in: forward.rs:1588-
-// 1619); one workgroup form only (matrix-core body, whole K, one slice round).
-extern "C" __global__ void __launch_bounds__(512) k_gemv_q8_0_attn_f32add_r1(GemvArgs a) {
-    gemv_mq_body<FmtQ8_0, EPI_F32_ADD, AttnX, 1, fmt_pf<FmtQ8_0>()>(a);
-}
 
 // Activation pre-pass: builds the limb records of x (nxb records) in global
 // memory once, for launches whose K is too long to convert per workgroup.
@@ -784,11 +684,3 @@ RT_DEV void act_limbs_body(const XT* __restrict__ x, XRec* __restrict__ out, uin
         limb_slice<Q40PERM>(v, t & 7, out + (t >> 3));
     }
 }
-extern "C" __global__ void __launch_bounds__(256)
-k_act_limbs_f32(const float* x, XRec* out, uint32_t nxb) { act_limbs_body<float, false>(x, out, nxb); }
-extern "C" __global__ void __launch_bounds__(256)
-k_act_limbs_f32_q40(const float* x, XRec* out, uint32_t nxb) { act_limbs_body<float, true>(x, out, nxb); }
-extern "C" __global__ void __launch_bounds__(256)
-k_act_limbs_f16(const uint16_t* x, XRec* out, uint32_t nxb) { act_limbs_body<uint16_t, false>(x, out, nxb); }
-extern "C" __global__ void __launch_bounds__(256)
-k_act_limbs_f16_q40(const uint16_t* x, XRec* out, uint32_t nxb) { act_limbs_body<uint16_t, true>(x, out, nxb); }

@@ -1,4 +1,5 @@
-// k_gemv_ls.hip — LDS-streamed M=1 GEMV body (matrix-core dots) for gfx950.
+// rt_gemv_ls.h — LDS-streamed M=1 GEMV body (matrix-core dots) for gfx950
+// (instantiated by the kls_*.hip files).
 //
 // What limits an M=1 GEMV on MI355X is how the weight bytes are requested.
 // Two properties set the achieved HBM rate:
@@ -26,6 +27,8 @@
 // Residual/bias operands are loaded once at the start (≤ 64 items per wave).
 // A K split (S > 1 chunks) writes partial sums; the last chunk to arrive at a
 // quad adds them in chunk order and runs the epilogue.
+#pragma once
+#include "rt_gemv.h"
 
 constexpr uint32_t kLsGroup = 16;     // items per result store instruction
 constexpr uint32_t kLsMaxGroups = 4;  // ≤ 64 items per wave
@@ -349,50 +352,3 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
     extern "C" __global__ void __launch_bounds__(LB) NAME##_lsk1(GemvArgs a) { gemv_lsk_body<FMT, EPI, XT, 1>(a); }
 #define RT_GEMV_LS(NAME, FMT, EPI, XT) RT_GEMV_LSB(NAME, FMT, EPI, XT, 1024)
 
-RT_GEMV_LS(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float)
-RT_GEMV_LS(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float)
-RT_GEMV_LS(k_gemv_q8_0_f32_f16, FmtQ8_0, EPI_F16, float)
-RT_GEMV_LS(k_qkv_bias_q8_0, FmtQ8_0, EPI_QKV_BIAS, float)
-RT_GEMV_LS(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float)
-RT_GEMV_LS(k_gemv_q4_0_f32_f32, FmtQ4_0, EPI_F32, float)
-RT_GEMV_LS(k_gemv_q4_0_f32_f32add, FmtQ4_0, EPI_F32_ADD, float)
-RT_GEMV_LS(k_qkv_bias_q4_0, FmtQ4_0, EPI_QKV_BIAS, float)
-RT_GEMV_LS(k_ffn_q4_0, FmtQ4_0, EPI_FFN, float)
-RT_GEMV_LS(k_gemv_q4k_f32_f32, FmtQ4K, EPI_F32, float)
-RT_GEMV_LS(k_gemv_q4k_f32_f32add, FmtQ4K, EPI_F32_ADD, float)
-RT_GEMV_LS(k_ffn_q4k, FmtQ4K, EPI_FFN, float)
-RT_GEMV_LS(k_gemv_q5_0_f32_f32, FmtQ5_0, EPI_F32, float)
-RT_GEMV_LS(k_gemv_q5_0_f32_f32add, FmtQ5_0, EPI_F32_ADD, float)
-RT_GEMV_LS(k_ffn_q5_0, FmtQ5_0, EPI_FFN, float)
-RT_GEMV_LS(k_gemv_q5k_f32_f32, FmtQ5K, EPI_F32, float)
-RT_GEMV_LS(k_gemv_q5k_f32_f32add, FmtQ5K, EPI_F32_ADD, float)
-RT_GEMV_LS(k_ffn_q5k, FmtQ5K, EPI_FFN, float)
-RT_GEMV_LS(k_gemv_q4_0g_f32_f32, FmtQ4_0G, EPI_F32, float)
-RT_GEMV_LS(k_gemv_q4_0g_f32_f32add, FmtQ4_0G, EPI_F32_ADD, float)
-RT_GEMV_LS(k_ffn_q4_0g, FmtQ4_0G, EPI_FFN, float)
-RT_GEMV_LS(k_gemv_q4kg_f32_f32, FmtQ4KG, EPI_F32, float)
-RT_GEMV_LS(k_gemv_q4kg_f32_f32add, FmtQ4KG, EPI_F32_ADD, float)
-RT_GEMV_LS(k_ffn_q4kg, FmtQ4KG, EPI_FFN, float)
-RT_GEMV_LS(k_gemv_q5kg_f32_f32, FmtQ5KG, EPI_F32, float)
-RT_GEMV_LS(k_gemv_q5kg_f32_f32add, FmtQ5KG, EPI_F32_ADD, float)
-RT_GEMV_LS(k_ffn_q5kg, FmtQ5KG, EPI_FFN, float)
-RT_GEMV_LSB(k_gemv_q6k_f32_f32, FmtQ6KB, EPI_F32, float, 256)
-RT_GEMV_LSB(k_gemv_q6k_f32_f32add, FmtQ6KB, EPI_F32_ADD, float, 256)
-RT_GEMV_LSB(k_gemv_q6kg_f32_f32, FmtQ6KGB, EPI_F32, float, 256)
-RT_GEMV_LSB(k_gemv_q6kg_f32_f32add, FmtQ6KGB, EPI_F32_ADD, float, 256)
-
-// Workgroup-local K split kernels (the residual / plain forms of the down
-// projections and the FFNs of long-K models)
-RT_GEMV_LSK(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float, 1024)
-RT_GEMV_LSK(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float, 1024)
-RT_GEMV_LSK(k_gemv_q4_0_f32_f32, FmtQ4_0, EPI_F32, float, 1024)
-RT_GEMV_LSK(k_gemv_q4_0_f32_f32add, FmtQ4_0, EPI_F32_ADD, float, 1024)
-RT_GEMV_LSK(k_ffn_q4_0, FmtQ4_0, EPI_FFN, float, 1024)
-RT_GEMV_LSK(k_gemv_q4k_f32_f32, FmtQ4K, EPI_F32, float, 1024)
-RT_GEMV_LSK(k_gemv_q4k_f32_f32add, FmtQ4K, EPI_F32_ADD, float, 1024)
-RT_GEMV_LSK(k_gemv_q5k_f32_f32, FmtQ5K, EPI_F32, float, 1024)
-RT_GEMV_LSK(k_gemv_q5k_f32_f32add, FmtQ5K, EPI_F32_ADD, float, 1024)
-RT_GEMV_LSK(k_gemv_q4kg_f32_f32add, FmtQ4KG, EPI_F32_ADD, float, 1024)
-RT_GEMV_LSK(k_gemv_q5kg_f32_f32add, FmtQ5KG, EPI_F32_ADD, float, 1024)
-RT_GEMV_LSK(k_gemv_q4_0g_f32_f32add, FmtQ4_0G, EPI_F32_ADD, float, 1024)
-RT_GEMV_LSK(k_gemv_q5_0_f32_f32add, FmtQ5_0, EPI_F32_ADD, float, 1024)

@@ -8,6 +8,7 @@
 // nothing synchronises until rt_flush (context.rs:289-296).
 #include <hip/hip_runtime.h>
 #include "rt_shared.h"
+#include <dirent.h>
 #include <dlfcn.h>
 
 #include <algorithm>
@@ -233,7 +234,7 @@ struct Plan {
 
 struct rt_ctx {
     int device = 0;
-    hipModule_t module = nullptr;
+    std::vector<hipModule_t> modules;  // the loaded code objects
     hipStream_t stream = nullptr;
     std::unordered_map<std::string, hipFunction_t> fns;
     int cu_count = 0;
@@ -302,15 +303,32 @@ int hip_fail(rt_ctx* c, hipError_t e, const char* what) {
     return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s: %s", what, hipGetErrorString(e));
 }
 
+// lib/kernels/ next to the host library: one code object per kernel unit
 std::string default_code_object_path() {
     Dl_info info;
     if (dladdr((void*)&rt_ctx_create, &info) && info.dli_fname) {
         std::string p(info.dli_fname);
         size_t s = p.find_last_of('/');
-        return (s == std::string::npos ? std::string(".") : p.substr(0, s)) +
-               "/runit_kernels.hsaco";
+        return (s == std::string::npos ? std::string(".") : p.substr(0, s)) + "/kernels";
     }
-    return "runit_kernels.hsaco";
+    return "kernels";
+}
+
+// The code objects of a path: every *.hsaco of a directory (sorted), or the
+// one file named.
+std::vector<std::string> code_object_files(const std::string& path) {
+    std::vector<std::string> files;
+    if (DIR* d = opendir(path.c_str())) {
+        while (dirent* e = readdir(d)) {
+            const std::string n = e->d_name;
+            if (n.size() > 6 && n.compare(n.size() - 6, 6, ".hsaco") == 0) files.push_back(path + "/" + n);
+        }
+        closedir(d);
+        std::sort(files.begin(), files.end());
+    } else {
+        files.push_back(path);
+    }
+    return files;
 }
 
 int launch(rt_ctx* c, const char* name, dim3 grid, dim3 block, size_t lds, void** params) {
@@ -940,11 +958,24 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
     std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
-    e = hipModuleLoad(&c->module, path.c_str());
-    if (e != hipSuccess) {
+    auto unload = [](rt_ctx* cc) {
+        for (hipModule_t m : cc->modules) hipModuleUnload(m);
+        delete cc;
+    };
+    const std::vector<std::string> files = code_object_files(path);
+    if (files.empty()) {
         delete c;
-        return fail(nullptr, RT_ERR_LIBRARY_LOAD, "failed to load code object from '%s': %s",
-                    path.c_str(), hipGetErrorString(e));
+        return fail(nullptr, RT_ERR_LIBRARY_LOAD, "no code object in '%s'", path.c_str());
+    }
+    for (const std::string& f : files) {
+        hipModule_t m = nullptr;
+        e = hipModuleLoad(&m, f.c_str());
+        if (e != hipSuccess) {
+            unload(c);
+            return fail(nullptr, RT_ERR_LIBRARY_LOAD, "failed to load code object from '%s': %s",
+                        f.c_str(), hipGetErrorString(e));
+        }
+        c->modules.push_back(m);
     }
     std::vector<std::string> names(std::begin(kKernelNames), std::end(kKernelNames));
     for (const char* b : kLsBases)
@@ -953,10 +984,10 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     for (const std::string& ns : names) {
         const char* n = ns.c_str();
         hipFunction_t f = nullptr;
-        e = hipModuleGetFunction(&f, c->module, n);
-        if (e != hipSuccess || !f) {
-            hipModuleUnload(c->module);
-            delete c;
+        for (hipModule_t m : c->modules)
+            if (hipModuleGetFunction(&f, m, n) == hipSuccess && f) break;
+        if (!f) {
+            unload(c);
             return fail(nullptr, RT_ERR_PIPELINE_NOT_FOUND,
                         "pipeline function '%s' not found in code object", n);
         }
@@ -965,8 +996,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     e = hipMalloc(&c->aux, kAuxBytes);
     if (e == hipSuccess) e = hipMemset(c->aux, 0, kAuxBytes);
     if (e != hipSuccess) {
-        hipModuleUnload(c->module);
-        delete c;
+        unload(c);
         return fail(nullptr, RT_ERR_PIPELINE_CREATE, "failed to allocate context buffer: %s",
                     hipGetErrorString(e));
     }
@@ -975,11 +1005,13 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
         // this device's copy of the code object's scratch array
         hipDeviceptr_t p = nullptr;
         size_t bytes = 0;
-        e = hipModuleGetGlobal(&p, &bytes, c->module, "scratch");
+        for (hipModule_t m : c->modules) {
+            e = hipModuleGetGlobal(&p, &bytes, m, "scratch");
+            if (e == hipSuccess && p) break;
+        }
         if (e != hipSuccess || !p || bytes != RT_SCRATCH_BYTES) {
             hipFree(c->aux);
-            hipModuleUnload(c->module);
-            delete c;
+            unload(c);
             return fail(nullptr, RT_ERR_PIPELINE_NOT_FOUND,
                         "code object has no %llu-byte 'scratch' array (%s)",
                         (unsigned long long)RT_SCRATCH_BYTES, hipGetErrorString(e));
@@ -988,8 +1020,8 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     }
     e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
-        hipModuleUnload(c->module);
-        delete c;
+        hipFree(c->aux);
+        unload(c);
         return fail(nullptr, RT_ERR_PIPELINE_CREATE, "failed to create stream: %s",
                     hipGetErrorString(e));
     }
@@ -1007,7 +1039,7 @@ void rt_ctx_destroy(rt_ctx* c) {
     if (c->part) hipFree(c->part);
     if (c->attn_out) hipFree(c->attn_out);
     if (c->aux) hipFree(c->aux);
-    if (c->module) hipModuleUnload(c->module);
+    for (hipModule_t m : c->modules) hipModuleUnload(m);
     delete c;
 }
 

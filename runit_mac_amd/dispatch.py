@@ -20,7 +20,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "lib", "librunit_hip.so")
-HSACO_PATH = os.path.join(_PKG, "lib", "runit_kernels.hsaco")
+HSACO_PATH = os.path.join(_PKG, "lib", "kernels")  # one code object per kernel unit
 
 
 # ───────────────────────────── errors (error.rs:4-21) ─────────────────────────────
