@@ -15,3 +15,4 @@ RT_GEMV_LSB(k_gemv_q6kg_f32_f32add, FmtQ6KGB, EPI_F32_ADD, float, 256)
 RT_GEMV_LSK(k_gemv_q4kg_f32_f32add, FmtQ4KG, EPI_F32_ADD, float, 1024)
 RT_GEMV_LSK(k_gemv_q5kg_f32_f32add, FmtQ5KG, EPI_F32_ADD, float, 1024)
 RT_GEMV_LSK(k_gemv_q4_0g_f32_f32add, FmtQ4_0G, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_gemv_q6kg_f32_f32add, FmtQ6KG, EPI_F32_ADD, float, 1024)

@@ -406,6 +406,38 @@ struct FmtQ6KT {
         // d sits 16 (h = 0) or 8 (h = 128) bytes after the scale window start
         r.d = hsel ? alignb(w[3], w[2], sh) : alignb(w[4], w[4], sh);
     }
+    // the same from a row copied into LDS: the alignment is taken with
+    // pointer arithmetic (integer address arithmetic would lose the LDS
+    // address space and turn every read into a flat load)
+    RT_DEV static void load16_ls(const uint8_t* q, uint32_t out[4]) {
+        const uint32_t sh = (uint32_t)((uintptr_t)q & 3);
+        uint32_t w[5];
+        load_dwords<5>(q - sh, w);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[i] = alignb(w[i + 1], w[i], sh);
+    }
+    RT_DEV static void load_ls(const uint8_t* row, uint32_t u, Raw& r) {
+        const uint32_t b = u >> 2, hsel = (u >> 1) & 1, lh = u & 1;
+        const uint8_t* p = row + (size_t)b * 210;
+        const uint32_t h = hsel * 128;
+        load16_ls(p + h / 2 + 16 * lh, r.ql0);
+        load16_ls(p + h / 2 + 32 + 16 * lh, r.ql1);
+        load16_ls(p + 128 + h / 4 + 16 * lh, r.qh);
+        const uint8_t* ps = p + 192 + h / 16;
+        const uint32_t sh = (uint32_t)((uintptr_t)ps & 3);
+        const uint8_t* ps4 = ps - sh;
+        // (in LDS the slot holds whole 16-byte granules around the chunk, so
+        // the window's last dword never leaves the slot)
+        uint32_t w[5];
+        load_dwords<5>(ps4, w);
+        r.sc01 = alignb(w[1], w[0], sh);
+        r.sc23 = alignb(w[2], w[1], sh);
+        if (G) {
+            r.sc01 >>= 8 * lh;
+            r.sc23 >>= 8 * lh;
+        }
+        r.d = hsel ? alignb(w[3], w[2], sh) : alignb(w[4], w[4], sh);
+    }
     RT_DEV static void load_x(const XRec* recs, uint32_t uu, XU& xu) {
         // unit uu (chunk-relative) → super-block b = uu>>2, half, l-half
         const uint32_t b = uu >> 2, hsel = (uu >> 1) & 1, lh = uu & 1;

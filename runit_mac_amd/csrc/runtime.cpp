@@ -185,6 +185,7 @@ const char* const kLskBases[] = {
     "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_gemv_q4_0_f32_f32", "k_gemv_q4_0_f32_f32add",
     "k_ffn_q4_0", "k_gemv_q4k_f32_f32", "k_gemv_q4k_f32_f32add", "k_gemv_q5k_f32_f32",
     "k_gemv_q5k_f32_f32add", "k_gemv_q4kg_f32_f32add", "k_gemv_q5kg_f32_f32add", "k_gemv_q4_0g_f32_f32add", "k_gemv_q5_0_f32_f32add",
+    "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32add",
 };
 constexpr uint32_t kLsMaxNI = 3;
 constexpr int kLsDecline = -1;
@@ -450,7 +451,9 @@ int gemv_launch_lsk(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     char name[96];
     snprintf(name, sizeof name, "%s_lsk1", kname);
     if (!c->fns.count(name)) return kLsDecline;
-    const uint32_t ue = f.mq_units();
+    // lane units of this body: the format's 64-element units (Q6_K too,
+    // whose matrix-core unit is a whole super-block)
+    const uint32_t ue = f.unit_el;
     const uint32_t units = a.K / ue;
     const uint32_t gu = f.blk_el > ue ? f.blk_el / ue : 1;
     const uint64_t unum = (uint64_t)ue * f.blk_bytes;  // unit bytes × blk_el
@@ -467,7 +470,10 @@ int gemv_launch_lsk(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     // than with the K split through memory) and the units suit 1024-thread
     // workgroups; longer K (the 7B down projections) keeps the split through
     // memory, whose workgroups stage only their own chunk.
-    if (f.mq_unit_el == 256 || (size_t)(a.K / 32) * XREC_BYTES > 32 * 1024) return kLsDecline;
+    // Q6_K: the 7B down projection (K = 18944, 66 KB of records) too — the
+    // K split through memory costs it ~3 µs of hand-off at the end
+    const size_t rec_cap = f.mq_unit_el == 256 ? 80 * 1024 : 32 * 1024;
+    if ((size_t)(a.K / 32) * XREC_BYTES > rec_cap) return kLsDecline;
     const uint32_t t = 1024;
     const uint32_t nwv = t / 64;
     a.ksplit = S;
