@@ -447,6 +447,44 @@ int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* ctx, const float* q_raw, con
 /* add_f16_into_f32 (dispatch.rs:316-330): acc[i] += f32(src[i]) for i < n
  * (the bias add of the separate-dispatch Q/K/V fallback, forward.rs:1561-1568). */
 int rt_add_f16_into_f32(rt_ctx* ctx, const uint16_t* src, float* acc, uint32_t n);
+/* ─────────────── batched verify / prefill (verify_draft's M-row path) ───────────────
+ * The kernels between the GEMMs of verify_draft (forward.rs:2118-2309) on f32
+ * activations [seq][dim]; the GEMMs are rt_gemm_<fmt>_f32. */
+/* dispatch.rs:1660-1680 → activation.metal:211-227: x[s][i] += f32(bias[i]). */
+int rt_add_bias_broadcast_f32(rt_ctx* ctx, float* x, const uint16_t* bias, uint32_t seq,
+                              uint32_t dim);
+/* dispatch.rs:1125-1150 → rope.metal:92-121: x [seq][num_heads][head_dim],
+ * row s rotated at position start_pos + s. */
+int rt_rope_batch_inplace_f32(rt_ctx* ctx, float* x, uint32_t head_dim, uint32_t num_heads,
+                              uint32_t start_pos, float theta, uint32_t seq);
+/* KvCache::write_at (kv_cache.rs:132-150) for positions start_pos ..
+ * start_pos+seq-1 (forward.rs:2216-2231): k, v [seq][num_kv_heads][head_dim]
+ * → caches [num_kv_heads][max_seq][head_dim]. */
+int rt_kv_write_batch_f32(rt_ctx* ctx, const float* k, const float* v, float* k_cache,
+                          float* v_cache, uint32_t start_pos, uint32_t seq, uint32_t max_seq,
+                          uint32_t head_dim, uint32_t num_kv_heads);
+/* dispatch.rs:645-687 → attention.metal:36-160 (flash_attention_f16) on f32:
+ * q, out [batch][q_len][num_heads][head_dim], caches [batch][num_kv_heads]
+ * [kv_head_stride][head_dim], scale 1/sqrt(head_dim).  Query row r attends to
+ * cache positions j < kv_len with j <= q_start + r.  q_start = 0 is the
+ * reference kernel's mask (j <= r); verify_draft with history needs
+ * q_start = kv_len - q_len (row r sits at absolute position q_start + r).
+ * head_dim 64, 128 or 256; batch·q_len ≤ 65535. */
+int rt_flash_attention_f32(rt_ctx* ctx, const float* q, const float* k, const float* v, float* out,
+                           uint32_t batch, uint32_t q_len, uint32_t kv_len, uint32_t num_heads,
+                           uint32_t num_kv_heads, uint32_t head_dim, uint32_t kv_head_stride,
+                           uint32_t q_start);
+/* dispatch.rs:57-75 → activation.metal:175-185 on f32: out = a + b (out may
+ * alias a or b). */
+int rt_add_f32(rt_ctx* ctx, const float* a, const float* b, float* out, uint32_t n);
+/* dispatch.rs:35-55 → activation.metal:156-173: out = silu(gate)·up. */
+int rt_silu_mul_f32(rt_ctx* ctx, const float* gate, const float* up, float* out, uint32_t n);
+/* The per-row argmax of verify_draft (forward.rs:2283-2293), on the GPU:
+ * result[r] = the first index of row r's maximum (strictly-greater scan from
+ * −inf; NaN never wins; a row of −inf/NaN gives 0).  in [rows][n]. */
+int rt_argmax_rows_first_f32(rt_ctx* ctx, const float* in, uint32_t* result, uint32_t rows,
+                             uint32_t n);
+
 /* New: out = dequant(table row *token) for a [vocab, k] table in the named
  * block format (reference or ggml layout, or plain f16 / f32 rows, as
  * token_embd.weight is stored); the token id is read from device memory
@@ -475,6 +513,33 @@ int rt_embed_f16_f32(rt_ctx* ctx, const void* table, const uint32_t* token, floa
                       uint32_t k);
 int rt_embed_f32_f32(rt_ctx* ctx, const void* table, const uint32_t* token, float* out,
                       uint32_t k);
+
+/* New: rt_embed_<fmt>_f32 for `rows` tokens at once: out[r·k ..] = row of
+ * tokens[r] (verify_draft embeds its sequence on the CPU, forward.rs:2142-2162). */
+int rt_embed_rows_q8_0_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_q4_0_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_q4k_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_q6k_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_q5_0_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_q5k_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_q4_0g_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_q4kg_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_q5kg_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_q6kg_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_f16_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
+int rt_embed_rows_f32_f32(rt_ctx* ctx, const void* table, const uint32_t* tokens, float* out,
+                         uint32_t k, uint32_t rows);
 
 /* New: rms_norm_f32_f32_f32g(x → x̂) fused into the following GEMV's
  * activation staging (same arguments as the pair of calls, minus x̂). */

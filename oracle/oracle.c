@@ -416,6 +416,37 @@ void ora_rope(double* v, size_t heads, size_t head_dim, uint32_t pos, float thet
     }
 }
 
+void ora_rope_batch(double* v, size_t seq, size_t heads, size_t head_dim, uint32_t start_pos,
+                    float theta) {
+    const size_t half = head_dim / 2;
+    for (size_t s = 0; s < seq; ++s)
+        for (size_t d = 0; d < half; ++d) {
+            const float angle =
+                (float)(start_pos + (uint32_t)s) / powf(theta, (float)(2 * d) / (float)head_dim);
+            const double c = cos((double)angle), sn = sin((double)angle);
+            for (size_t h = 0; h < heads; ++h) {
+                double* x = v + (s * heads + h) * head_dim;
+                const double r = x[d], i = x[d + half];
+                x[d] = r * c - i * sn;
+                x[d + half] = i * c + r * sn;
+            }
+        }
+}
+
+void ora_argmax_rows_first_f32(const float* v, size_t rows, size_t n, uint32_t* out) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float* row = v + r * n;
+        uint32_t best = 0;
+        float best_val = -INFINITY;
+        for (size_t j = 0; j < n; ++j)
+            if (row[j] > best_val) {
+                best_val = row[j];
+                best = (uint32_t)j;
+            }
+        out[r] = best;
+    }
+}
+
 void ora_attention(const double* q, const float* k, const float* v, size_t num_heads,
                    size_t num_kv_heads, size_t head_dim, size_t kv_len, size_t kv_stride,
                    double scale, double* out) {

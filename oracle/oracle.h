@@ -89,6 +89,18 @@ void ora_rms_norm(const float* x, const float* gamma, double eps, size_t hidden,
  * evaluated in f64. */
 void ora_rope(double* v, size_t heads, size_t head_dim, uint32_t pos, float theta);
 
+/* rope_batch_inplace_f16 (rope.metal:92-121) on f64 data [seq][heads][hd]:
+ * row s at position start_pos + s, angle = f32(pos) / powf(θ, (2d)/hd) formed
+ * in f32 as the kernel forms it (a division, unlike ora_rope), the rotation
+ * in f64. */
+void ora_rope_batch(double* v, size_t seq, size_t heads, size_t head_dim, uint32_t start_pos,
+                    float theta);
+
+/* The per-row argmax of verify_draft (forward.rs:2283-2293): best = 0,
+ * best_val = −inf; for j in row: if v[j] > best_val {best = j; best_val = v[j]}
+ * — the first maximal index; NaN never compares greater. */
+void ora_argmax_rows_first_f32(const float* v, size_t rows, size_t n, uint32_t* out);
+
 /* Decode attention (attention.metal:248-308; cpu_attention dispatch.rs:
  * 1712-1742 generalised to GQA): per query head h, kv head h/(H/KVH),
  * softmax(q·k_j · scale) · v over j < kv_len, in f64.  K/V: [kvh][stride][hd]. */

@@ -143,10 +143,12 @@ RT_DEV float f32_value(const uint8_t* blk, uint32_t) { return *(const float*)blk
     extern "C" __global__ void __launch_bounds__(256)                                            \
         k_embed_##NAME##_f32(const uint8_t* __restrict__ table, const uint32_t* token,           \
                              float* __restrict__ out, uint32_t k) {                              \
-        const uint8_t* row = table + (size_t)token[0] * (k / (EL)) * (BY);                       \
+        /* grid row y embeds token[y] into out[y·k ..] */                                        \
+        const uint8_t* row = table + (size_t)token[blockIdx.y] * (k / (EL)) * (BY);              \
+        float* o = out + (size_t)blockIdx.y * k;                                                 \
         for (uint32_t i = threadIdx.x + blockIdx.x * wg_threads(); i < k;                        \
              i += wg_threads() * gridDim.x)                                                      \
-            out[i] = VALUE(row + (i / (EL)) * (BY), i % (EL));                                   \
+            o[i] = VALUE(row + (i / (EL)) * (BY), i % (EL));                                     \
     }
 RT_DEQ_KERNELS(q8_0, 32, 34, q8_0_value)
 RT_DEQ_KERNELS(q4_0, 32, 18, q4_0_value)

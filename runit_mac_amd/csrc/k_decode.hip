@@ -86,6 +86,104 @@ k_kv_copy_f32(const float* src, float* dst, uint32_t pos, uint32_t max_seq, uint
     dst[((size_t)h * max_seq + pos) * head_dim + d] = src[t];
 }
 
+// ───────────────────── batched verify / prefill glue ─────────────────────
+// The M-row kernels between the GEMMs of verify_draft (forward.rs:2186-2271),
+// on f32 activations [rows][dim].
+
+// add_bias_broadcast_f16 (activation.metal:211-227, called at forward.rs:2199-2207):
+// x[s][i] += f32(bias[i]).
+extern "C" __global__ void __launch_bounds__(256)
+k_add_bias_broadcast_f32(float* __restrict__ x, const uint16_t* __restrict__ bias, uint32_t seq,
+                         uint32_t dim) {
+    const uint64_t n = (uint64_t)seq * dim;
+    for (uint64_t t = blockIdx.x * (uint64_t)wg_threads() + threadIdx.x; t < n;
+         t += (uint64_t)gridDim.x * wg_threads())
+        x[t] += h2f(bias[t % dim]);
+}
+
+// rope_batch_inplace_f16 (rope.metal:92-121): row s of [seq][heads][hd] at
+// position start_pos + s, pairs (d, d + hd/2), angle = pos / θ^(2d/hd) (a
+// division, where the single-token fused_rope multiplies by the inverse).
+// Grid (⌈hd/2 / 64⌉, heads, seq).
+extern "C" __global__ void __launch_bounds__(64)
+k_rope_batch_f32(float* x, uint32_t head_dim, uint32_t heads, uint32_t start_pos, float theta) {
+    const uint32_t half = head_dim / 2;
+    const uint32_t d = blockIdx.x * wg_threads() + threadIdx.x;
+    if (d >= half) return;
+    const float angle = (float)(start_pos + blockIdx.z) / powf(theta, (float)(2 * d) / (float)head_dim);
+    float c, s;
+    sincosf(angle, &s, &c);
+    float* v = x + ((size_t)blockIdx.z * heads + blockIdx.y) * head_dim;
+    const float r = v[d], i = v[d + half];
+    v[d] = r * c - i * s;
+    v[d + half] = i * c + r * s;
+}
+
+// KvCache::write_at (kv_cache.rs:132-150) for rows start_pos .. start_pos+seq-1
+// (the loop of forward.rs:2216-2231):
+// k / v [seq][kv_heads][hd] → cache[h][start_pos + s][d], both caches in one launch.
+extern "C" __global__ void __launch_bounds__(256)
+k_kv_write_batch_f32(const float* __restrict__ k, const float* __restrict__ v, float* kc,
+                     float* vc, uint32_t start_pos, uint32_t max_seq, uint32_t head_dim,
+                     uint32_t kv_heads, uint32_t n) {
+    const uint32_t t = blockIdx.x * wg_threads() + threadIdx.x;
+    if (t >= n) return;
+    const uint32_t row = kv_heads * head_dim;
+    const uint32_t s = t / row, h = (t % row) / head_dim, d = t % head_dim;
+    const size_t o = ((size_t)h * max_seq + start_pos + s) * head_dim + d;
+    kc[o] = k[t];
+    vc[o] = v[t];
+}
+
+// add_f16 (activation.metal:175-185, forward.rs:2247) on f32: out = a + b
+// (out may alias a or b).
+extern "C" __global__ void __launch_bounds__(256)
+k_add_f32(const float* a, const float* b, float* out, uint32_t n) {
+    for (uint32_t i = blockIdx.x * wg_threads() + threadIdx.x; i < n; i += gridDim.x * wg_threads())
+        out[i] = a[i] + b[i];
+}
+
+// silu_mul_f32 (activation.metal:156-173; f16 form at forward.rs:2256):
+// out = silu(gate) · up, silu(g) = g / (1 + e^−g).
+extern "C" __global__ void __launch_bounds__(256)
+k_silu_mul_f32(const float* gate, const float* up, float* out, uint32_t n) {
+    for (uint32_t i = blockIdx.x * wg_threads() + threadIdx.x; i < n; i += gridDim.x * wg_threads()) {
+        const float g = gate[i];
+        out[i] = g / (1.0f + expf(-g)) * up[i];
+    }
+}
+
+// The per-row argmax of verify_draft (forward.rs:2283-2293): the FIRST index
+// whose value is strictly greater than every earlier one, starting from −∞
+// (NaN never wins; a row of −∞ / NaN gives 0).  One workgroup per row.
+extern "C" __global__ void __launch_bounds__(1024)
+k_argmax_rows_first_f32(const float* __restrict__ in, uint32_t* __restrict__ out, uint32_t n) {
+    __shared__ float bv_s[16];
+    __shared__ uint32_t bi_s[16];
+    const float* row = in + (size_t)blockIdx.x * n;
+    float bv = -__builtin_huge_valf();
+    uint32_t bi = 0xFFFFFFFFu;  // none yet
+    for (uint32_t i = threadIdx.x; i < n; i += wg_threads()) {
+        const float v = row[i];
+        if (v > bv) { bv = v; bi = i; }
+    }
+    // larger value wins; equal values: the smaller index (none = UINT_MAX)
+    auto better = [](float v, uint32_t i, float w, uint32_t j) { return w > v || (w == v && j < i); };
+    for (int o = 32; o > 0; o >>= 1) {
+        const float w = __shfl_xor(bv, o, 64);
+        const uint32_t j = __shfl_xor(bi, o, 64);
+        if (better(bv, bi, w, j)) { bv = w; bi = j; }
+    }
+    const uint32_t wv = threadIdx.x >> 6, nw = wg_threads() >> 6;
+    if ((threadIdx.x & 63) == 0) { bv_s[wv] = bv; bi_s[wv] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t k = 1; k < nw; ++k)
+            if (better(bv, bi, bv_s[k], bi_s[k])) { bv = bv_s[k]; bi = bi_s[k]; }
+        out[blockIdx.x] = bi == 0xFFFFFFFFu ? 0u : bi;
+    }
+}
+
 #define RT_ATTN_KERNELS(HD)                                                                \
     extern "C" __global__ void __launch_bounds__(256 * attn_hg<HD>())                     \
         k_decode_attention_f32_hd##HD(AttnArgs a) {                                        \

@@ -75,6 +75,12 @@ struct AttnArgs {
     float scale, theta;
     uint32_t parts_only;  // write (o, m, l) of every split, merge nothing (the
                           // consumer merges: k_gemv_q8_0_attn_f32add)
+    uint32_t q_len;       // > 0: causal multi-query rows (no rope): grid row b is
+                          // query r = b % q_len of sequence b / q_len, at
+                          // position q_start + r; it attends to the first
+                          // min(kv_len, q_start + r + 1) positions of its
+                          // sequence's cache
+    uint32_t q_start;
 };
 
 // (s, nsp, y, b): the split, the number of splits, the (kv head, head
@@ -104,10 +110,14 @@ RT_DEV void attn_split(const AttnArgs& a, uint32_t s, uint32_t nsp, uint32_t y, 
     const uint32_t kvh = y / HB, hb = y % HB;
     const uint32_t gh = min(GM, G - hb * GM);
     const uint32_t h0 = kvh * G + hb * GM;  // first query head of the block
-    const size_t kvb = ((size_t)b * a.KVH + kvh) * a.stride * HD;
+    // causal rows share their sequence's cache and see a prefix of it
+    const uint32_t seq = a.q_len ? b / a.q_len : b;
+    const uint32_t kv_len = a.q_len ? min(a.kv_len, a.q_start + b % a.q_len + 1) : a.kv_len;
+    const size_t kvb = ((size_t)seq * a.KVH + kvh) * a.stride * HD;
     float* kc = a.kc + kvb;
     float* vc = a.vc + kvb;
-    const uint32_t p_begin = s * a.chunk, p_end = min(a.kv_len, p_begin + a.chunk);
+    // (a split past a causal row's prefix is empty: it contributes m = −∞, l = 0)
+    const uint32_t p_begin = s * a.chunk, p_end = min(kv_len, p_begin + a.chunk);
     float* qsf = (float*)qs4;
     const uint32_t kp = lt >> 2, kq = lt & 3;      // key layout
     const uint32_t vcol = lt % C4, vg = lt / C4;  // value layout

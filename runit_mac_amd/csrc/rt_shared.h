@@ -26,7 +26,7 @@ constexpr uint64_t RT_SCRATCH_PART_BYTES = RT_SCRATCH_BYTES - RT_SCRATCH_PART_OF
 
 // Persistent decode step (k_step.hip): phase record size and the most
 // workgroups a step grid may have.
-constexpr uint32_t RT_STEP_PHASE_BYTES = 368;
+constexpr uint32_t RT_STEP_PHASE_BYTES = 376;
 constexpr uint32_t RT_STEP_MAX_WGS = 1024;
 constexpr uint32_t RT_STEP_SYNC_BYTES = 2048;  // StepSync (k_step.hip)
 constexpr uint32_t RT_STEP_STATUS_OFF = 1280;  // its status word

@@ -133,7 +133,8 @@ const char* const kKernelNames[] = {
     "k_rms_norm_f32g", "k_rope_qk_f32", "k_kv_copy_f32",
     "k_decode_attention_f32_hd64", "k_decode_attention_f32_hd128", "k_decode_attention_f32_hd256",
     "k_attn_rope_f32_hd64", "k_attn_rope_f32_hd128", "k_attn_rope_f32_hd256",
-    "k_add_f16_into_f32",
+    "k_add_f16_into_f32", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
+    "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
     "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
@@ -1937,6 +1938,7 @@ struct AttnArgs {
     uint32_t kv_len, stride, H, KVH, chunk, pos;
     float scale, theta;
     uint32_t parts_only;
+    uint32_t q_len, q_start;
 };
 
 // Splits kv_len into ranges of a multiple of 64 positions so that the grid
@@ -2118,22 +2120,145 @@ int rt_add_f16_into_f32(rt_ctx* c, const uint16_t* src, float* acc, uint32_t n) 
                   dim3(256), 0, params);
 }
 
-static int embed_launch(rt_ctx* c, const char* kname, uint32_t blk_el, const void* table,
-                        const uint32_t* token, float* out, uint32_t k) {
+// ───────────────────── batched verify / prefill glue ─────────────────────
+
+static uint32_t grid_1d(uint64_t n) {
+    return (uint32_t)std::min<uint64_t>((n + 255) / 256, 4096);
+}
+
+int rt_add_bias_broadcast_f32(rt_ctx* c, float* x, const uint16_t* bias, uint32_t seq,
+                              uint32_t dim) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
-    if (k == 0) return RT_OK;
+    if (seq == 0 || dim == 0) return RT_OK;
+    if (!x || !bias)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: add_bias_broadcast: null buffer");
+    void* params[] = {&x, &bias, &seq, &dim};
+    return launch(c, "k_add_bias_broadcast_f32", dim3(grid_1d((uint64_t)seq * dim)), dim3(256), 0,
+                  params);
+}
+
+int rt_rope_batch_inplace_f32(rt_ctx* c, float* x, uint32_t head_dim, uint32_t num_heads,
+                              uint32_t start_pos, float theta, uint32_t seq) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (head_dim < 2 || head_dim % 2)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: rope_batch: head_dim=%u must be even",
+                    head_dim);
+    if (seq == 0 || num_heads == 0) return RT_OK;
+    if (!x) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: rope_batch: null buffer");
+    if (seq > 65535 || num_heads > 65535)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: rope_batch: seq=%u heads=%u > 65535",
+                    seq, num_heads);
+    void* params[] = {&x, &head_dim, &num_heads, &start_pos, &theta};
+    return launch(c, "k_rope_batch_f32", dim3((head_dim / 2 + 63) / 64, num_heads, seq), dim3(64),
+                  0, params);
+}
+
+int rt_kv_write_batch_f32(rt_ctx* c, const float* k, const float* v, float* k_cache,
+                          float* v_cache, uint32_t start_pos, uint32_t seq, uint32_t max_seq,
+                          uint32_t head_dim, uint32_t num_kv_heads) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    const uint64_t n64 = (uint64_t)seq * num_kv_heads * head_dim;
+    if (n64 == 0) return RT_OK;
+    if (!k || !v || !k_cache || !v_cache)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: kv_write_batch: null buffer");
+    if ((uint64_t)start_pos + seq > max_seq)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: kv_write_batch: start_pos=%u + seq=%u > max_seq=%u",
+                    start_pos, seq, max_seq);
+    if (n64 > 0xFFFFFFFFull)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: kv_write_batch: too many elements");
+    const uint32_t n = (uint32_t)n64;
+    void* params[] = {&k, &v, &k_cache, &v_cache, &start_pos, &max_seq, &head_dim, &num_kv_heads,
+                      (void*)&n};
+    return launch(c, "k_kv_write_batch_f32", dim3((n + 255) / 256), dim3(256), 0, params);
+}
+
+int rt_add_f32(rt_ctx* c, const float* a, const float* b, float* out, uint32_t n) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (n == 0) return RT_OK;
+    if (!a || !b || !out) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: add: null buffer");
+    void* params[] = {&a, &b, &out, &n};
+    return launch(c, "k_add_f32", dim3(grid_1d(n)), dim3(256), 0, params);
+}
+
+int rt_silu_mul_f32(rt_ctx* c, const float* gate, const float* up, float* out, uint32_t n) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (n == 0) return RT_OK;
+    if (!gate || !up || !out)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: silu_mul: null buffer");
+    void* params[] = {&gate, &up, &out, &n};
+    return launch(c, "k_silu_mul_f32", dim3(grid_1d(n)), dim3(256), 0, params);
+}
+
+int rt_argmax_rows_first_f32(rt_ctx* c, const float* in, uint32_t* result, uint32_t rows,
+                             uint32_t n) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (rows == 0) return RT_OK;
+    if (!in || !result)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: argmax_rows: null buffer");
+    if (n == 0) return rt_memset(c, result, 0, (size_t)rows * 4);
+    void* params[] = {&in, &result, &n};
+    return launch(c, "k_argmax_rows_first_f32", dim3(rows), dim3(1024), 0, params);
+}
+
+int rt_flash_attention_f32(rt_ctx* c, const float* q, const float* k, const float* v, float* out,
+                           uint32_t batch, uint32_t q_len, uint32_t kv_len, uint32_t num_heads,
+                           uint32_t num_kv_heads, uint32_t head_dim, uint32_t kv_head_stride,
+                           uint32_t q_start) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (batch == 0 || q_len == 0 || num_heads == 0) return RT_OK;
+    int st = attn_check(c, num_heads, num_kv_heads, head_dim);
+    if (st != RT_OK) return st;
+    if (!q || !k || !v || !out)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: flash_attention: null buffer");
+    if (kv_len == 0 || kv_len > kv_head_stride)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: flash_attention: kv_len=%u (need 1..kv_head_stride=%u)",
+                    kv_len, kv_head_stride);
+    const uint64_t rows = (uint64_t)batch * q_len;
+    if (rows > 65535)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: flash_attention: batch·q_len=%llu > 65535",
+                    (unsigned long long)rows);
+    AttnArgs a{};
+    a.q = q;
+    a.kc = const_cast<float*>(k);  // read only without rope
+    a.vc = const_cast<float*>(v);
+    a.out = out;
+    a.kv_len = kv_len;
+    a.stride = kv_head_stride;
+    a.H = num_heads;
+    a.KVH = num_kv_heads;
+    a.scale = 1.0f / sqrtf((float)head_dim);  // dispatch.rs:659
+    a.q_len = q_len;
+    a.q_start = q_start;
+    char kn[64];
+    snprintf(kn, sizeof kn, "k_decode_attention_f32_hd%u", head_dim);
+    return attn_launch(c, kn, a, (uint32_t)rows);
+}
+
+static int embed_launch(rt_ctx* c, const char* kname, uint32_t blk_el, const void* table,
+                        const uint32_t* token, float* out, uint32_t k, uint32_t rows = 1) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (k == 0 || rows == 0) return RT_OK;
     if (k % blk_el)
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: embed: k=%u not a multiple of %u",
                     k, blk_el);
     if (!table || !token || !out)
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: embed: null buffer");
+    if (rows > 65535)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: embed: rows=%u > 65535", rows);
     void* params[] = {&table, &token, &out, &k};
-    return launch(c, kname, dim3((k + 255) / 256), dim3(256), 0, params);
+    return launch(c, kname, dim3((k + 255) / 256, rows), dim3(256), 0, params);
 }
 #define RT_EMBED_ENTRY(NAME, EL)                                                               \
     int rt_embed_##NAME##_f32(rt_ctx* c, const void* table, const uint32_t* token, float* out,  \
                               uint32_t k) {                                                    \
         return embed_launch(c, "k_embed_" #NAME "_f32", EL, table, token, out, k);             \
+    }                                                                                          \
+    int rt_embed_rows_##NAME##_f32(rt_ctx* c, const void* table, const uint32_t* tokens,        \
+                                   float* out, uint32_t k, uint32_t rows) {                    \
+        return embed_launch(c, "k_embed_" #NAME "_f32", EL, table, tokens, out, k, rows);      \
     }
 RT_EMBED_ENTRY(q8_0, 32)
 RT_EMBED_ENTRY(q4_0, 32)

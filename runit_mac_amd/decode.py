@@ -120,6 +120,24 @@ def _fmt_bytes(fmt: str, n: int, k: int) -> int:
     return d.weight_bytes(fmt, n, k)
 
 
+def accept_drafts(argmax_rows, drafts) -> tuple[int, int]:
+    """The acceptance loop of verify_draft (forward.rs:2279-2305): row r's
+    argmax must equal draft r; the first row that differs ends it with its
+    argmax as the correct next token; when every draft is accepted the last
+    row's argmax is the next token.  len(argmax_rows) = len(drafts) + 1."""
+    if len(argmax_rows) != len(drafts) + 1:
+        raise ValueError("one argmax per verified row (prompt token + drafts) expected")
+    accepted = 0
+    for r, best in enumerate(int(b) for b in argmax_rows):
+        if r < len(drafts):
+            if best != int(drafts[r]):
+                return accepted, best
+            accepted += 1
+        else:
+            return accepted, best
+    raise AssertionError("unreachable")
+
+
 class DecodeModel:
     """Qwen2-shape model resident in one arena, plus the KV cache.
 
@@ -485,6 +503,95 @@ class DecodeModel:
         step._layers = layers
         return step
 
+    # ───────────────────────── batched verify ─────────────────────────
+
+    def _verify_arena(self, rows: int) -> dict:
+        """Activation buffers of an M-row verify pass, [rows][dim] f32,
+        allocated once per largest M seen."""
+        v = getattr(self, "_vbufs", None)
+        if v is not None and v["rows"] >= rows:
+            return v
+        if v is not None:
+            v["arena"].buf.free()
+        c = self.cfg
+        dims = dict(x=c.hidden, xn=c.hidden, q=c.q_dim, k=c.kv_dim, v=c.kv_dim, att=c.q_dim,
+                    p=c.hidden, g=c.ff, u=c.ff, logits=c.vocab)
+        a = Arena(self.ctx, sum(((4 * rows * n + 255) & ~255) for n in dims.values()) + 2 * 1024)
+        v = {k: a.take(4 * rows * n) for k, n in dims.items()}
+        v.update(tok=a.take(4 * rows), idx=a.take(4 * rows), rows=rows, arena=a)
+        self._vbufs = v
+        return v
+
+    def verify_forward(self, tokens, start_pos: int) -> dict:
+        """verify_draft's batched forward (forward.rs:2141-2273) on the GPU:
+        the M tokens embedded together, every projection one batched GEMM in
+        the matrix's own format, bias broadcast, batched RoPE at start_pos..,
+        the M keys / values written to the cache, causal attention (row r at
+        position start_pos + r sees the cache up to there), residual adds,
+        SiLU·up, the final norm and the LM-head GEMM, and the per-row
+        first-max argmax.  Returns the activation buffers (``logits``:
+        [M][vocab], ``idx``: [M] argmax)."""
+        ctx, c = self.ctx, self.cfg
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        M = int(toks.size)
+        if M == 0:
+            raise ValueError("verify: empty sequence")
+        if start_pos + M > c.max_seq:
+            raise ValueError(f"verify: start_pos {start_pos} + {M} tokens exceed the KV cache "
+                             f"({c.max_seq})")
+        if self.lm_fmt in ("f16", "f32"):
+            raise ValueError(f"LM head in {self.lm_fmt}: no f16/f32-weight GEMM here")
+        B = self._verify_arena(M)
+        h, qd, kvd, hd, ff = c.hidden, c.q_dim, c.kv_dim, c.head_dim, c.ff
+        lib = d.load_library()
+        ctx._check(lib.rt_upload(ctx.handle, B["tok"], toks.ctypes.data, toks.nbytes))
+        X, XN = B["x"], B["xn"]
+        d.embed_rows_f32(ctx, self.embd_fmt, self.embd, B["tok"], X, h, M)
+
+        def gemm(fmt, w, x, y, n, k):
+            getattr(d, f"gemm_{fmt}_f32")(ctx, w, x, y, M, n, k)
+
+        for L, F in zip(self.layers, self.fmts):
+            d.rms_norm_f32_f32_f32g(ctx, X, XN, L["attn_norm"], c.eps, h, M)
+            for role, w, b, out, n in (("q", "wq", "bq", B["q"], qd), ("k", "wk", "bk", B["k"], kvd),
+                                       ("v", "wv", "bv", B["v"], kvd)):
+                gemm(F[role], L[w], XN, out, n, h)
+                d.add_bias_broadcast_f32(ctx, out, L[b], M, n)
+            d.rope_batch_inplace_f32(ctx, B["q"], hd, c.heads, start_pos, c.theta, M)
+            d.rope_batch_inplace_f32(ctx, B["k"], hd, c.kv_heads, start_pos, c.theta, M)
+            d.kv_write_batch_f32(ctx, B["k"], B["v"], L["kc"], L["vc"], start_pos, M, c.max_seq,
+                                 hd, c.kv_heads)
+            d.flash_attention_f32(ctx, B["q"], L["kc"], L["vc"], B["att"], 1, M, start_pos + M,
+                                  c.heads, c.kv_heads, hd, c.max_seq, q_start=start_pos)
+            gemm(F["o"], L["wo"], B["att"], B["p"], h, qd)
+            d.add_f32(ctx, X, B["p"], X, M * h)
+            d.rms_norm_f32_f32_f32g(ctx, X, XN, L["ffn_norm"], c.eps, h, M)
+            gemm(F["gate"], L["wg"], XN, B["g"], ff, h)
+            gemm(F["up"], L["wu"], XN, B["u"], ff, h)
+            d.silu_mul_f32(ctx, B["g"], B["u"], B["g"], M * ff)
+            gemm(F["down"], L["wd"], B["g"], B["p"], h, ff)
+            d.add_f32(ctx, X, B["p"], X, M * h)
+        d.rms_norm_f32_f32_f32g(ctx, X, XN, self.final_norm, c.eps, h, M)
+        gemm(self.lm_fmt, self.lm_head, XN, B["logits"], c.vocab, h)
+        d.argmax_rows_first_f32(ctx, B["logits"], B["idx"], M, c.vocab)
+        return B
+
+    def verify_draft(self, prompt_token: int, draft_tokens, start_pos: int):
+        """forward.rs:2118-2309: run [prompt_token, *draft_tokens] at
+        start_pos.. in one batched pass, then accept drafts while each equals
+        the argmax of the row before it.  Returns (accepted, correct_next):
+        the first rejected row's argmax, or the last row's when every draft
+        was accepted.  The cache holds the keys / values of all M rows; the
+        caller's next position is start_pos + accepted + 1 (the reference's
+        kv.set_seq_len)."""
+        drafts = [int(t) for t in draft_tokens]
+        B = self.verify_forward([int(prompt_token)] + drafts, start_pos)
+        M = len(drafts) + 1
+        idx = np.zeros(M, np.uint32)
+        self.ctx._check(d.load_library().rt_download(self.ctx.handle, idx.ctypes.data, B["idx"],
+                                                     idx.nbytes))
+        return accept_drafts(idx, drafts)
+
     def capture(self, pos: int, fused: bool = True) -> d.Graph:
         """One step captured as a HIP graph (the reference's single command
         buffer per token, context.rs:248-296)."""
@@ -496,4 +603,7 @@ class DecodeModel:
         return self.ctx.capture_end()
 
     def free(self) -> None:
+        if getattr(self, "_vbufs", None) is not None:
+            self._vbufs["arena"].buf.free()
+            self._vbufs = None
         self.arena.buf.free()

@@ -128,6 +128,15 @@ _SIGS = {
     "rt_add_f16_into_f32": [_P, _P, _P, _U32],
     **{f"rt_embed_{_f}_f32": [_P, _P, _P, _P, _U32] for _f in (
         "q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg", "f16", "f32")},
+    **{f"rt_embed_rows_{_f}_f32": [_P, _P, _P, _P, _U32, _U32] for _f in (
+        "q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg", "f16", "f32")},
+    "rt_add_bias_broadcast_f32": [_P, _P, _P, _U32, _U32],
+    "rt_rope_batch_inplace_f32": [_P, _P, _U32, _U32, _U32, _F, _U32],
+    "rt_kv_write_batch_f32": [_P] + [_P] * 4 + [_U32] * 5,
+    "rt_flash_attention_f32": [_P] + [_P] * 4 + [_U32] * 8,
+    "rt_add_f32": [_P, _P, _P, _P, _U32],
+    "rt_silu_mul_f32": [_P, _P, _P, _P, _U32],
+    "rt_argmax_rows_first_f32": [_P, _P, _P, _U32, _U32],
     "rt_rms_norm_fused_qkv_bias_q8_0_f32": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 + [_U32] * 3,
     "rt_rms_norm_fused_ffn_q8_0_f32": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32],
     "rt_rms_norm_gemv_q8_0_f32in_f32out": [_P, _P, _P, _P, _F, _P, _U32, _U32],
@@ -678,6 +687,52 @@ def embed_f32(ctx, fmt: str, table, token, out, k):
     """Embedding row of the device-resident token id, dequantised from a
     `fmt` table (q8_0 … q6kg, f16, f32) (new)."""
     _call(ctx, f"rt_embed_{fmt}_f32", _ptr(table), _ptr(token), _ptr(out), k)
+
+
+def embed_rows_f32(ctx, fmt: str, table, tokens, out, k, rows):
+    """embed_f32 for `rows` device-resident token ids at once (new)."""
+    _call(ctx, f"rt_embed_rows_{fmt}_f32", _ptr(table), _ptr(tokens), _ptr(out), k, rows)
+
+
+# ──────────────────── batched verify / prefill glue ────────────────────
+
+def add_bias_broadcast_f32(ctx, x, bias, seq, dim):
+    """dispatch.rs:1660-1680: x[s][i] += f32(bias[i])."""
+    _call(ctx, "rt_add_bias_broadcast_f32", _ptr(x), _ptr(bias), seq, dim)
+
+
+def rope_batch_inplace_f32(ctx, x, head_dim, num_heads, start_pos, theta, seq):
+    """dispatch.rs:1125-1150: row s of [seq][heads][hd] rotated at start_pos + s."""
+    _call(ctx, "rt_rope_batch_inplace_f32", _ptr(x), head_dim, num_heads, start_pos, theta, seq)
+
+
+def kv_write_batch_f32(ctx, k, v, k_cache, v_cache, start_pos, seq, max_seq, head_dim,
+                       num_kv_heads):
+    """KvCache::write_at (kv_cache.rs:132-150) for seq consecutive positions."""
+    _call(ctx, "rt_kv_write_batch_f32", *map(_ptr, (k, v, k_cache, v_cache)), start_pos, seq,
+          max_seq, head_dim, num_kv_heads)
+
+
+def flash_attention_f32(ctx, q, k, v, out, batch, q_len, kv_len, num_heads, num_kv_heads,
+                        head_dim, kv_head_stride, q_start=0):
+    """dispatch.rs:645-687 (causal; row r sees positions ≤ q_start + r)."""
+    _call(ctx, "rt_flash_attention_f32", *map(_ptr, (q, k, v, out)), batch, q_len, kv_len,
+          num_heads, num_kv_heads, head_dim, kv_head_stride, q_start)
+
+
+def add_f32(ctx, a, b, out, n):
+    """dispatch.rs:57-75 on f32: out = a + b."""
+    _call(ctx, "rt_add_f32", _ptr(a), _ptr(b), _ptr(out), n)
+
+
+def silu_mul_f32(ctx, gate, up, out, n):
+    """dispatch.rs:35-55: out = silu(gate)·up."""
+    _call(ctx, "rt_silu_mul_f32", _ptr(gate), _ptr(up), _ptr(out), n)
+
+
+def argmax_rows_first_f32(ctx, input, result, rows, n):
+    """verify_draft's per-row argmax (forward.rs:2283-2293): first max wins."""
+    _call(ctx, "rt_argmax_rows_first_f32", _ptr(input), _ptr(result), rows, n)
 
 
 def embed_q8_0_f32(ctx, table, token, out, k):

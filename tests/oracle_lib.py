@@ -148,6 +148,35 @@ def synth_weights(fmt: str, n: int, k: int, seed: int, std: float = 0.02) -> np.
     return out
 
 
+_lib.ora_rope_batch.argtypes = [_P, _S, _S, _S, ctypes.c_uint32, ctypes.c_float]
+_lib.ora_argmax_rows_first_f32.argtypes = [_P, _S, _S, _P]
+
+
+def rope_batch(v: np.ndarray, seq: int, heads: int, head_dim: int, start_pos: int,
+               theta: float) -> np.ndarray:
+    out = np.ascontiguousarray(v, dtype=np.float64).copy()
+    _lib.ora_rope_batch(_p(out), seq, heads, head_dim, start_pos, theta)
+    return out
+
+
+def argmax_rows_first(v: np.ndarray, rows: int) -> np.ndarray:
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.zeros(rows, np.uint32)
+    _lib.ora_argmax_rows_first_f32(_p(v), rows, v.size // max(rows, 1), _p(out))
+    return out
+
+
+def causal_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, q_len: int, num_heads: int,
+                     num_kv_heads: int, head_dim: int, kv_len: int, kv_stride: int,
+                     q_start: int) -> np.ndarray:
+    """flash_attention_f16 (attention.metal:36-160) for one sequence: query
+    row r attends to cache positions j < kv_len with j <= q_start + r — each
+    row is the decode attention over its prefix."""
+    q = np.asarray(q, dtype=np.float64).reshape(q_len, num_heads * head_dim)
+    return np.stack([attention(q[r], k, v, num_heads, num_kv_heads, head_dim,
+                               min(kv_len, q_start + r + 1), kv_stride) for r in range(q_len)])
+
+
 def rms_norm(x: np.ndarray, gamma: np.ndarray, eps: float) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     gamma = np.ascontiguousarray(gamma, dtype=np.float32)

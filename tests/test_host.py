@@ -37,3 +37,14 @@ def test_q4k_m_weight_accounting():
 def test_decode_model_rejects_unknown_roles_before_allocating():
     with pytest.raises(ValueError):
         DecodeModel(None, DecodeConfig(layers=1), quant={"attn": "q4k"})
+
+
+def test_accept_drafts_follows_verify_draft():
+    """forward.rs:2279-2305: accept while row r's argmax equals draft r."""
+    from runit_mac_amd.decode import accept_drafts
+    assert accept_drafts([5], []) == (0, 5)
+    assert accept_drafts([1, 2, 3, 9], [1, 2, 3]) == (3, 9)
+    assert accept_drafts([1, 7, 3, 9], [1, 2, 3]) == (1, 7)
+    assert accept_drafts([4, 2, 3, 9], [1, 2, 3]) == (0, 4)
+    with pytest.raises(ValueError):
+        accept_drafts([1, 2], [1, 2])

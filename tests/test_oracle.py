@@ -595,3 +595,66 @@ def test_decode_step_ref_f32_matches_f64_composition():
         assert got_tok == int(np.argmax(ref)) == ora.argmax(logits)
     kc0 = layers[0]["kc"].reshape(cfg.kv_heads, cfg.max_seq, cfg.head_dim)
     assert np.any(kc0[:, pos] != 0) and kc0.shape[1] == cfg.max_seq
+
+
+# ───────────────────────── verify_draft glue ─────────────────────────
+
+def test_rope_batch_rows_are_single_position_ropes():
+    """Row s of the batched rotation is the single-token rotation at
+    start_pos + s (the angle formed by division instead of multiplication by
+    the inverse: equal to f32 rounding), and position 0 is the identity."""
+    rng = np.random.default_rng(2)
+    seq, heads, hd, start = 5, 3, 64, 507
+    v = rng.standard_normal(seq * heads * hd)
+    r = ora.rope_batch(v, seq, heads, hd, start, 1e6).reshape(seq, heads * hd)
+    for s in range(seq):
+        one = ora.rope(v.reshape(seq, -1)[s], heads, hd, start + s, 1e6)
+        assert np.allclose(r[s], one, rtol=0, atol=1e-3 * np.abs(one).max()), s
+    assert np.array_equal(ora.rope_batch(v[:heads * hd], 1, heads, hd, 0, 1e6), v[:heads * hd])
+    # pair 0 has frequency 1: angle = position exactly
+    rr = r.reshape(seq, heads, hd)
+    vv = v.reshape(seq, heads, hd)
+    for s in range(seq):
+        c, sn = np.cos(float(start + s)), np.sin(float(start + s))
+        assert np.allclose(rr[s, :, 0], vv[s, :, 0] * c - vv[s, :, 32] * sn, rtol=1e-12)
+
+
+def test_argmax_rows_first_semantics():
+    """forward.rs:2283-2293: strictly-greater scan from −inf — the first
+    maximal index, NaN never wins, a row with nothing above −inf gives 0."""
+    nan, inf = np.float32("nan"), np.float32("inf")
+    cases = [
+        ([1.0, 3.0, 3.0, 2.0], 1),   # ties → first maximal index
+        ([3.0, 1.0, 3.0], 0),
+        ([-inf, -inf], 0),
+        ([nan, 2.0, 7.0, 7.0], 2),
+        ([1.0, nan, 0.5], 0),
+        ([nan, nan], 0),
+        ([-inf, -5.0], 1),
+        ([inf, inf], 0),
+    ]
+    for vals, expect in cases:
+        assert ora.argmax_rows_first(np.array(vals, np.float32), 1)[0] == expect, vals
+    # NaN-free rows: numpy's argmax also returns the first maximal index
+    rng = np.random.default_rng(3)
+    m = rng.integers(-4, 5, size=(7, 300)).astype(np.float32)
+    assert np.array_equal(ora.argmax_rows_first(m, 7), np.argmax(m, axis=1))
+
+
+def test_causal_attention_rows_are_prefix_decode_attention():
+    """Row r of the causal oracle is the decode attention over the first
+    q_start + r + 1 positions; a row that sees one position returns its value
+    row exactly."""
+    rng = np.random.default_rng(4)
+    H, KVH, hd, S, M, kv_len = 4, 2, 64, 40, 3, 20
+    q = rng.standard_normal(M * H * hd)
+    k = rng.standard_normal(KVH * S * hd).astype(np.float32)
+    v = rng.standard_normal(KVH * S * hd).astype(np.float32)
+    out = ora.causal_attention(q, k, v, M, H, KVH, hd, kv_len, S, 0)
+    vv = v.reshape(KVH, S, hd)
+    for h in range(H):
+        assert np.allclose(out[0, h * hd:(h + 1) * hd], vv[h // 2, 0], rtol=1e-12)
+    full = ora.causal_attention(q, k, v, M, H, KVH, hd, kv_len, S, kv_len - M)
+    for r in range(M):
+        ref = ora.attention(q.reshape(M, -1)[r], k, v, H, KVH, hd, kv_len - M + r + 1, S)
+        assert np.array_equal(full[r], ref)
