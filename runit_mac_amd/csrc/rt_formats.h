@@ -621,6 +621,68 @@ struct FmtQ6KBT {
         }
         return acc;
     }
+    // VALU form of mdot: every lane takes all three limbs of its records and
+    // accumulates them with v_dot4_i32_i8 (no matrix core); same integer
+    // sums, same f32 combination, so the same result bit for bit
+    RT_DEV static float vdot(const Raw& r, const XRec* xs, uint32_t uu) {
+        const float d = h2f(r.w[52] >> (8 * r.sh));
+        constexpr int NH = G ? 2 : 1;
+        float acc = 0.0f;
+#pragma unroll 1
+        for (int hs = 0; hs < 2; ++hs) {
+            const XRec* rec = xs + 8 * uu + 4 * hs;
+            int z[4][NH][3];
+            int e[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const u32x4 m = ((const u32x4*)(rec + t))[6];
+                e[t] = (int)(int16_t)(m.x & 0xFFFF);
+                const int a0 = (int16_t)(m.x >> 16), a1 = (int16_t)(m.y & 0xFFFF),
+                          a2 = (int16_t)(m.y >> 16);
+                const int b0 = (int16_t)(m.z & 0xFFFF), b1 = (int16_t)(m.z >> 16),
+                          b2 = (int16_t)(m.w & 0xFFFF);
+                if (G) {
+                    z[t][0][0] = -32 * a0; z[t][0][1] = -32 * a1; z[t][0][2] = -32 * a2;
+                    z[t][NH - 1][0] = -32 * b0; z[t][NH - 1][1] = -32 * b1; z[t][NH - 1][2] = -32 * b2;
+                } else {
+                    z[t][0][0] = -32 * (a0 + b0); z[t][0][1] = -32 * (a1 + b1);
+                    z[t][0][2] = -32 * (a2 + b2);
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                const uint32_t ql = hs ? get(r, 64 + 4 * g) : get(r, 4 * g);
+                const uint32_t ql32 = hs ? get(r, 96 + 4 * g) : get(r, 32 + 4 * g);
+                const uint32_t qh = hs ? get(r, 160 + 4 * g) : get(r, 128 + 4 * g);
+                const int k = (G && g >= 4) ? NH - 1 : 0;
+                const uint32_t code[4] = {
+                    (ql & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u),
+                    (ql32 & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u),
+                    ((ql >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u),
+                    ((ql32 >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u)};
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int l = 0; l < 3; ++l)
+                        z[t][k][l] = sdot4(code[t], ((const uint32_t*)(rec + t))[8 * l + g], z[t][k][l]);
+            }
+            const uint32_t sa = hs ? get(r, 200) : get(r, 192);
+            const uint32_t sb = hs ? get(r, 204) : get(r, 196);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t sw = t < 2 ? sa : sb;
+                const int sh0 = 16 * (t & 1);
+                const int s0 = (int8_t)((sw >> sh0) & 255u);
+                float v = d * (float)s0 * limb_combine(z[t][0][0], z[t][0][1], z[t][0][2]);
+                if (G) {
+                    const int s1 = (int8_t)((sw >> (sh0 + 8)) & 255u);
+                    v += d * (float)s1 * limb_combine(z[t][NH - 1][0], z[t][NH - 1][1], z[t][NH - 1][2]);
+                }
+                acc += __builtin_amdgcn_ldexpf(v, e[t] - 22);
+            }
+        }
+        return acc;
+    }
 };
 using FmtQ6KB = FmtQ6KBT<false>;
 using FmtQ6KGB = FmtQ6KBT<true>;

@@ -43,7 +43,28 @@ RT_DEV auto ls_load(const uint8_t* row, uint32_t u, typename F::Raw& r, int) -> 
 template <class F>
 RT_DEV void ls_load(const uint8_t* row, uint32_t u, typename F::Raw& r, long) { F::load(row, u, r); }
 
-template <class F, int EPI, typename XT, int NI>
+// The unit dot of this lane's row: matrix-core form (F::mdot, lane q feeds
+// limb lq of the quad's A operand), or, VALU, the format's v_dot4 form over
+// all three limbs of the records (F::vdot where the format has one, else
+// F::load_x + F::dot) — the same integer sums and the same result.
+template <class F>
+RT_DEV auto fmt_vdot(const typename F::Raw& r, const XRec* xs, uint32_t u, int)
+    -> decltype(F::vdot(r, xs, u)) {
+    return F::vdot(r, xs, u);
+}
+template <class F>
+RT_DEV float fmt_vdot(const typename F::Raw& r, const XRec* xs, uint32_t u, long) {
+    typename F::XU xu;
+    F::load_x(xs, u, xu);
+    return F::dot(r, xu);
+}
+template <class F, bool VALU>
+RT_DEV float ls_dot(const typename F::Raw& r, const XRec* xs, uint32_t u, uint32_t lq) {
+    if constexpr (VALU) return fmt_vdot<F>(r, xs, u, 0);
+    else return F::mdot(r, xs, u, lq);
+}
+
+template <class F, int EPI, typename XT, int NI, bool VALU = false>
 RT_DEV void gemv_ls_body(const GemvArgs& a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -178,7 +199,7 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
             const uint32_t uc = valid ? u : 0;
             typename F::Raw raw;
             ls_load<F>(rowl, uc, raw, 0);
-            const float v = F::mdot(raw, xs, uc, lq);
+            const float v = ls_dot<F, VALU>(raw, xs, uc, lq);
             acc += valid ? v : 0.0f;
         }
         // sum over the 16 slots of the row (lane bits 2..5)
@@ -231,7 +252,7 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
 // through memory and arrival counters.  The activation records of the whole
 // K are staged once per workgroup.  After the last item a barrier, then the
 // chunks of each row are added in chunk order and the epilogue runs.
-template <class F, int EPI, typename XT, int NI>
+template <class F, int EPI, typename XT, int NI, bool VALU = false>
 RT_DEV void gemv_lsk_body(const GemvArgs& a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -313,7 +334,7 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
             const uint32_t uc = valid ? u : 0;
             typename F::Raw raw;
             ls_load<F>(rowl, uc, raw, 0);
-            const float v = F::mdot(raw, xc, uc, lq);
+            const float v = ls_dot<F, VALU>(raw, xc, uc, lq);
             acc += valid ? v : 0.0f;
         }
         acc += swz_xor_f<4>(acc);
@@ -351,4 +372,12 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
 #define RT_GEMV_LSK(NAME, FMT, EPI, XT, LB) \
     extern "C" __global__ void __launch_bounds__(LB) NAME##_lsk1(GemvArgs a) { gemv_lsk_body<FMT, EPI, XT, 1>(a); }
 #define RT_GEMV_LS(NAME, FMT, EPI, XT) RT_GEMV_LSB(NAME, FMT, EPI, XT, 1024)
+// The VALU-dot twins (<name>_ls<NI>v) of a kernel set, for the A/B of the two
+// dot forms (selected by the context's gemv_valu switch)
+#define RT_GEMV_LS1V(NAME, FMT, EPI, XT, NI, LB)                                            \
+    extern "C" __global__ void __launch_bounds__(LB) NAME##_ls##NI##v(GemvArgs a) {        \
+        gemv_ls_body<FMT, EPI, XT, NI, true>(a);                                           \
+    }
+#define RT_GEMV_LSBV(NAME, FMT, EPI, XT, LB) \
+    RT_GEMV_LS1V(NAME, FMT, EPI, XT, 1, LB) RT_GEMV_LS1V(NAME, FMT, EPI, XT, 2, LB) RT_GEMV_LS1V(NAME, FMT, EPI, XT, 3, LB)
 

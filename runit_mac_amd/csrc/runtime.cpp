@@ -188,6 +188,8 @@ const char* const kLskBases[] = {
     "k_gemv_q5k_f32_f32add", "k_gemv_q4kg_f32_f32add", "k_gemv_q5kg_f32_f32add", "k_gemv_q4_0g_f32_f32add", "k_gemv_q5_0_f32_f32add",
     "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32add",
 };
+// Kernels with a VALU-dot twin <base>_ls<NI>v (the dot-form A/B).
+const char* const kLsValuBases[] = {"k_ffn_q4k", "k_gemv_q6k_f32_f32"};
 constexpr uint32_t kLsMaxNI = 3;
 constexpr int kLsDecline = -1;
 constexpr uint32_t kLsThreads = 256;
@@ -255,6 +257,7 @@ struct rt_ctx {
     void* attn_out = nullptr;  // attention output between the two launches of
     size_t attn_out_bytes = 0;  // the unmerged attention + o_proj sequence
     bool ls_enabled = true;      // RUNIT_GEMV_LS=0: the per-lane-load matrix-core body instead
+    bool gemv_valu = false;      // RUNIT_GEMV_VALU=1: VALU-dot twins of the LDS body (A/B)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
     // Small per-context device buffer: argmax range states + arrival counter
@@ -547,6 +550,7 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     if ((uint64_t)a.nvrows * a.row_bytes + 16 >= (1ull << 31)) return kLsDecline;
     char name[96];
     snprintf(name, sizeof name, "%s_ls%u", kname, NI);
+    if (c->gemv_valu && c->fns.count(std::string(name) + "v")) strcat(name, "v");
     // Block size: the one with the most resident waves per CU (larger
     // blocks share one copy of the activation records), one round of
     // resident workgroups, result buffers sized to the items per wave.
@@ -964,6 +968,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMV_VALU")) c->gemv_valu = atoi(g) != 0;
     std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
     auto unload = [](rt_ctx* cc) {
         for (hipModule_t m : cc->modules) hipModuleUnload(m);
@@ -988,6 +993,9 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     for (const char* b : kLsBases)
         for (uint32_t ni = 1; ni <= kLsMaxNI; ++ni) names.push_back(std::string(b) + "_ls" + std::to_string(ni));
     for (const char* b : kLskBases) names.push_back(std::string(b) + "_lsk1");
+    for (const char* b : kLsValuBases)
+        for (uint32_t ni = 1; ni <= kLsMaxNI; ++ni)
+            names.push_back(std::string(b) + "_ls" + std::to_string(ni) + "v");
     for (const std::string& ns : names) {
         const char* n = ns.c_str();
         hipFunction_t f = nullptr;

@@ -542,9 +542,16 @@ class DecodeModel:
         if self.lm_fmt in ("f16", "f32"):
             raise ValueError(f"LM head in {self.lm_fmt}: no f16/f32-weight GEMM here")
         B = self._verify_arena(M)
-        h, qd, kvd, hd, ff = c.hidden, c.q_dim, c.kv_dim, c.head_dim, c.ff
         lib = d.load_library()
         ctx._check(lib.rt_upload(ctx.handle, B["tok"], toks.ctypes.data, toks.nbytes))
+        return self.verify_pass(M, start_pos)
+
+    def verify_pass(self, M: int, start_pos: int) -> dict:
+        """The launches of verify_forward for the M token ids already in the
+        verify buffers (``tok``): no host transfer, so it can be captured."""
+        ctx, c = self.ctx, self.cfg
+        B = self._verify_arena(M)
+        h, qd, kvd, hd, ff = c.hidden, c.q_dim, c.kv_dim, c.head_dim, c.ff
         X, XN = B["x"], B["xn"]
         d.embed_rows_f32(ctx, self.embd_fmt, self.embd, B["tok"], X, h, M)
 

@@ -219,3 +219,59 @@ def test_lsk_fused_ffn_q4_0(ctx):
     g, gs = ora.gemv("q4_0", rg, x, ff, k)
     u, us = ora.gemv("q4_0", ru, x, ff, k)
     ffn_check(act.read(np.float32, ff), g, gs, u, us, "lsk ffn q4_0")
+
+
+@pytest.fixture(scope="module")
+def valuctx():
+    old = os.environ.get("RUNIT_GEMV_VALU")
+    os.environ["RUNIT_GEMV_VALU"] = "1"
+    try:
+        c = d.HipContext()
+    finally:
+        if old is None:
+            del os.environ["RUNIT_GEMV_VALU"]
+        else:
+            os.environ["RUNIT_GEMV_VALU"] = old
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("what", ["q4k_ffn_7b", "q6k_lm_head_7b"])
+def test_valu_dot_twin_equals_matrix_core_form(ctx, valuctx, what):
+    """The VALU-dot twins (v_dot4 over the three limbs) of the 7B Q4_K FFN
+    and the Q6_K LM head compute the same integer sums and the same f32
+    combination as the matrix-core form: equal bit for bit, and on the
+    oracle."""
+    outs = []
+    if what == "q4k_ffn_7b":
+        ff, k = 18944, 3584
+        for c in (ctx, valuctx):
+            wg, rg = device_weights(c, "q4k", ff, k, seed=31)
+            wu, ru = device_weights(c, "q4k", ff, k, seed=32)
+            xb = c.new_buffer(4 * k)
+            d.synth_normal_f32(c, xb, k, 33)
+            c.flush()
+            x = xb.read(np.float32, k)
+            ob = c.new_buffer(4 * ff)
+            d.fused_ffn_q4k_f32(c, wg, wu, xb, ob, ff, k)
+            c.flush()
+            outs.append(ob.read(np.float32, ff))
+        g_ref, g_s = ora.gemv("q4k", rg, x, ff, k)
+        u_ref, u_s = ora.gemv("q4k", ru, x, ff, k)
+        ffn_check(outs[1], g_ref, g_s, u_ref, u_s, "q4k valu ffn")
+    else:
+        n, k = 152064, 3584
+        for c in (ctx, valuctx):
+            wb, raw = device_weights(c, "q6k", n, k, seed=41)
+            xb = c.new_buffer(4 * k)
+            d.synth_normal_f32(c, xb, k, 42)
+            c.flush()
+            x = xb.read(np.float32, k)
+            ob = c.new_buffer(4 * n)
+            d.gemv_q6k_f32in_f32out(c, wb, xb, ob, n, k)
+            c.flush()
+            outs.append(ob.read(np.float32, n))
+        rows = slice(0, 4096)  # oracle on a slice of the rows (CPU time)
+        ref, sabs = ora.gemv("q6k", raw[:4096 * (k // 256) * 210], x, 4096, k)
+        check_close(outs[1][rows], ref, sabs, "q6k valu lm head")
+    assert np.array_equal(outs[0], outs[1])
