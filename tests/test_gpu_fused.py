@@ -275,12 +275,12 @@ def test_gemm_int8_form_matches_oracle(fmt, m):
         c2.close()
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4k"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4k", "q4_0", "q6k", "q6kg"])
 def test_gemm_f16_form_wide_range(ctx, fmt):
-    """f16 form: every 32-element record is scaled into f16's range on its
-    own, so rows of 1e-6-sized activations, rows of 1e4-sized ones and
-    records with one large outlier among tiny values all stay within the
-    bound."""
+    """f16 forms: each 32-element record (min formats) or each row (the
+    accumulate-in-matrix-core form) is scaled into f16's range on its own, so
+    rows of 1e-6-sized activations, rows of 1e4-sized ones and records with
+    one large outlier among tiny values all stay within the bound."""
     n, k, m = 200, 1024, 24
     wbuf, raw = device_weights(ctx, fmt, n, k, seed=77)
     rng = np.random.default_rng(78)
