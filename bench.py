@@ -287,11 +287,11 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
     # the batched GEMMs, causal attention over the cache + the M new rows),
     # captured as one graph; the cache is restored between replays
     verify = {}
-    for M in (4, 8, 16):
-        m.verify_forward([1] * M, pos)  # uploads the ids, sizes the buffers
+    for M, form in ((4, "rows"), (8, "rows"), (16, "rows"), (16, "gemm"), (32, "gemm")):
+        m.verify_forward([1] * M, pos, form)  # uploads the ids, sizes the buffers
         ctx.flush()
         ctx.capture_begin()
-        m.verify_pass(M, pos)
+        m.verify_pass(M, pos, form)
         g = ctx.capture_end()
         for _ in range(max(1, warmup)):
             g.launch()
@@ -301,7 +301,7 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
         for _ in range(steps):
             g.launch()
         e1.record()
-        verify[M] = e0.elapsed_ms(e1) / steps
+        verify[(M, form)] = e0.elapsed_ms(e1) / steps
         del g
     # dominant kernel of the fused step: the norm-fused gate+up+SiLU GEMV,
     # 24 launches per token.  Timed live over the model's own 24 layers.
@@ -560,8 +560,8 @@ def main():
             f"→ {dec['step_bytes'] / (ms * 1e-3) / 1e9:.0f} GB/s effective")
         log(f"persistent step (1 launch for embedding + 24 layers, then LM head + argmax): "
             f"{dec['ms_persistent'] * 1e3:.1f} us = {1e3 / dec['ms_persistent']:.1f} tok/s")
-        for M, vms in dec["verify_ms"].items():
-            log(f"verify pass, {M} tokens at kv 512..{512 + M - 1}: {vms * 1e3:.1f} us "
+        for (M, form), vms in dec["verify_ms"].items():
+            log(f"verify pass ({form}), {M} tokens at kv 512..{512 + M - 1}: {vms * 1e3:.1f} us "
                 f"({vms * 1e3 / M:.1f} us per token; {M} fused decode steps: {M * ms * 1e3:.1f} us)")
         log(f"dominant kernel rms_norm+fused_ffn_q8_0 4864x896x2: {dec['ffn_us']:.2f} us, "
             f"{ffn_gbs:.0f} GB/s")
@@ -584,8 +584,8 @@ def main():
                        "step_bytes": dec["step_bytes"],
                        "effective_gbs": round(dec["step_bytes"] / (ms * 1e-3) / 1e9, 1),
                        "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / dec["step_bytes"], 0)},
-            "verify": {str(M): {"us": round(v * 1e3, 1), "us_per_token": round(v * 1e3 / M, 1)}
-                       for M, v in dec["verify_ms"].items()},
+            "verify": {f"{form}_m{M}": {"us": round(v * 1e3, 1), "us_per_token": round(v * 1e3 / M, 1)}
+                       for (M, form), v in dec["verify_ms"].items()},
         })
 
     if args.suite in ("all", "gemv", "step", "q4decode") and not args.only:

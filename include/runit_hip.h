@@ -382,6 +382,140 @@ int rt_gemm_q5kg_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, 
 int rt_gemm_q6kg_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
                      uint32_t n, uint32_t k);
 
+/* ──────────────── multi-row GEMVs (batched verify / prefill) ────────────────
+ * New: the M-row projections of verify_draft (forward.rs:2186-2271, which
+ * dequantises to f16 and runs gemm_f16) on the quantized weights: rows
+ * activation rows x [rows][k] f32 (16-byte aligned), outputs [rows][n].  A
+ * pre-pass builds each row's activation records (RMS-normalised with gamma,
+ * x·rsqrt(mean(x²)+eps)·γ, when gamma is not NULL); the weights are read once
+ * per 8 rows.  k must be a multiple of 64 (K-quants: 256).
+ *   rt_gemv_rows_<f>_f32     y = (norm)x · Wᵀ
+ *   rt_gemv_rows_<f>_add_f32 y = res + x · Wᵀ   (y may alias res)
+ *   rt_qkv_bias_rows_<f>_f32 q/k/v = (norm)x · W_{q,k,v}ᵀ + f32(bias); a NULL
+ *                            weight skips that matrix (mixed-format Q/K/V:
+ *                            one call per format)
+ *   rt_fused_ffn_rows_<f>_f32 act = silu((norm)x·W_gᵀ) · ((norm)x·W_uᵀ) */
+int rt_gemv_rows_q8_0_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q8_0_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q8_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q8_0_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+int rt_gemv_rows_q4_0_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q4_0_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q4_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q4_0_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+int rt_gemv_rows_q4k_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q4k_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q4k_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q4k_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+int rt_gemv_rows_q6k_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q6k_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q6k_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q6k_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+int rt_gemv_rows_q5_0_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q5_0_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q5_0_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q5_0_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+int rt_gemv_rows_q5k_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q5k_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q5k_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q5k_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+int rt_gemv_rows_q4_0g_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q4_0g_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q4_0g_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q4_0g_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+int rt_gemv_rows_q4kg_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q4kg_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q4kg_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q4kg_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+int rt_gemv_rows_q5kg_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q5kg_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q5kg_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q5kg_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+int rt_gemv_rows_q6kg_f32(rt_ctx* ctx, const void* weight, const float* x, const float* gamma,
+                       float eps, float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_gemv_rows_q6kg_add_f32(rt_ctx* ctx, const void* weight, const float* x, const float* res,
+                           float* y, uint32_t rows, uint32_t n, uint32_t k);
+int rt_qkv_bias_rows_q6kg_f32(rt_ctx* ctx, const void* w_q, const void* w_k, const void* w_v,
+                           const float* x, const float* gamma, float eps, float* q, float* k_out,
+                           float* v, const uint16_t* bias_q, const uint16_t* bias_k,
+                           const uint16_t* bias_v, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                           uint32_t k);
+int rt_fused_ffn_rows_q6kg_f32(rt_ctx* ctx, const void* w_gate, const void* w_up, const float* x,
+                            const float* gamma, float eps, float* act, uint32_t rows, uint32_t ff,
+                            uint32_t k);
+
 /* ───────────────────────── argmax ───────────────────────── */
 
 /* greedy_argmax_f32 (crates/engine/src/sampler.rs:111-116) on the GPU:
@@ -457,6 +591,13 @@ int rt_add_bias_broadcast_f32(rt_ctx* ctx, float* x, const uint16_t* bias, uint3
  * row s rotated at position start_pos + s. */
 int rt_rope_batch_inplace_f32(rt_ctx* ctx, float* x, uint32_t head_dim, uint32_t num_heads,
                               uint32_t start_pos, float theta, uint32_t seq);
+/* New: rt_rope_batch_inplace_f32 of q (num_heads) and k (num_kv_heads) and
+ * rt_kv_write_batch_f32 of the rotated k and of v in one launch; q is rotated
+ * in place, k and v are read only. */
+int rt_rope_kv_write_batch_f32(rt_ctx* ctx, float* q, const float* k, const float* v,
+                               float* k_cache, float* v_cache, uint32_t head_dim,
+                               uint32_t num_heads, uint32_t num_kv_heads, uint32_t start_pos,
+                               float theta, uint32_t seq, uint32_t max_seq);
 /* KvCache::write_at (kv_cache.rs:132-150) for positions start_pos ..
  * start_pos+seq-1 (forward.rs:2216-2231): k, v [seq][num_kv_heads][head_dim]
  * → caches [num_kv_heads][max_seq][head_dim]. */

@@ -119,6 +119,38 @@ k_rope_batch_f32(float* x, uint32_t head_dim, uint32_t heads, uint32_t start_pos
     v[d + half] = i * c + r * s;
 }
 
+// rope_batch_inplace_f16 of q and k (rope.metal:92-121) and KvCache::write_at
+// of the rotated k and of v (forward.rs:2209-2231) in one launch: grid
+// (⌈hd/2 / 64⌉, max(heads, kv_heads), seq); q rotated in place, k and v
+// written to cache[h][start_pos + s].
+extern "C" __global__ void __launch_bounds__(64)
+k_rope_kv_write_batch_f32(float* q, const float* k, const float* v, float* kc, float* vc,
+                          uint32_t head_dim, uint32_t heads, uint32_t kv_heads, uint32_t start_pos,
+                          float theta, uint32_t max_seq) {
+    const uint32_t half = head_dim / 2;
+    const uint32_t d = blockIdx.x * wg_threads() + threadIdx.x;
+    if (d >= half) return;
+    const uint32_t h = blockIdx.y, s = blockIdx.z, pos = start_pos + s;
+    const float angle = (float)pos / powf(theta, (float)(2 * d) / (float)head_dim);
+    float c, sn;
+    sincosf(angle, &sn, &c);
+    if (h < heads) {
+        float* x = q + ((size_t)s * heads + h) * head_dim;
+        const float r = x[d], i = x[d + half];
+        x[d] = r * c - i * sn;
+        x[d + half] = i * c + r * sn;
+    }
+    if (h < kv_heads) {
+        const size_t src = ((size_t)s * kv_heads + h) * head_dim;
+        const size_t dst = ((size_t)h * max_seq + pos) * head_dim;
+        const float r = k[src + d], i = k[src + d + half];
+        kc[dst + d] = r * c - i * sn;
+        kc[dst + d + half] = i * c + r * sn;
+        vc[dst + d] = v[src + d];
+        vc[dst + d + half] = v[src + d + half];
+    }
+}
+
 // KvCache::write_at (kv_cache.rs:132-150) for rows start_pos .. start_pos+seq-1
 // (the loop of forward.rs:2216-2231):
 // k / v [seq][kv_heads][hd] → cache[h][start_pos + s][d], both caches in one launch.
@@ -155,16 +187,23 @@ k_silu_mul_f32(const float* gate, const float* up, float* out, uint32_t n) {
 
 // The per-row argmax of verify_draft (forward.rs:2283-2293): the FIRST index
 // whose value is strictly greater than every earlier one, starting from −∞
-// (NaN never wins; a row of −∞ / NaN gives 0).  One workgroup per row.
-extern "C" __global__ void __launch_bounds__(1024)
-k_argmax_rows_first_f32(const float* __restrict__ in, uint32_t* __restrict__ out, uint32_t n) {
-    __shared__ float bv_s[16];
-    __shared__ uint32_t bi_s[16];
-    const float* row = in + (size_t)blockIdx.x * n;
+// (NaN never wins; a row of −∞ / NaN gives 0).  Grid (G, rows): workgroup g
+// scans range g of row y and leaves (value, index) in `states`; the last
+// workgroup of the row to arrive (counter, reset by it) merges the G ranges
+// in order.
+extern "C" __global__ void __launch_bounds__(256)
+k_argmax_rows_first_f32(const float* __restrict__ in, uint32_t* __restrict__ out, uint32_t n,
+                        float2* __restrict__ states, uint32_t* __restrict__ counters) {
+    __shared__ float bv_s[4];
+    __shared__ uint32_t bi_s[4];
+    __shared__ bool last;
+    const uint32_t G = gridDim.x, g = blockIdx.x, row = blockIdx.y;
+    const uint32_t per = (n + G - 1) / G, b0 = g * per, b1 = min(n, b0 + per);
+    const float* r = in + (size_t)row * n;
     float bv = -__builtin_huge_valf();
     uint32_t bi = 0xFFFFFFFFu;  // none yet
-    for (uint32_t i = threadIdx.x; i < n; i += wg_threads()) {
-        const float v = row[i];
+    for (uint32_t i = b0 + threadIdx.x; i < b1; i += wg_threads()) {
+        const float v = r[i];
         if (v > bv) { bv = v; bi = i; }
     }
     // larger value wins; equal values: the smaller index (none = UINT_MAX)
@@ -180,7 +219,22 @@ k_argmax_rows_first_f32(const float* __restrict__ in, uint32_t* __restrict__ out
     if (threadIdx.x == 0) {
         for (uint32_t k = 1; k < nw; ++k)
             if (better(bv, bi, bv_s[k], bi_s[k])) { bv = bv_s[k]; bi = bi_s[k]; }
-        out[blockIdx.x] = bi == 0xFFFFFFFFu ? 0u : bi;
+        dev_store(&states[(size_t)row * G + g].x, bv);
+        dev_store(&states[(size_t)row * G + g].y, __uint_as_float(bi));
+        dev_stores_done();
+        last = arrive(&counters[row]) == G - 1;
+        if (last) {
+            // ranges in order: a later range wins only with a strictly greater value
+            float best = -__builtin_huge_valf();
+            uint32_t bidx = 0xFFFFFFFFu;
+            for (uint32_t k = 0; k < G; ++k) {
+                const float v = dev_load(&states[(size_t)row * G + k].x);
+                const uint32_t j = __float_as_uint(dev_load(&states[(size_t)row * G + k].y));
+                if (j != 0xFFFFFFFFu && v > best) { best = v; bidx = j; }
+            }
+            out[row] = bidx == 0xFFFFFFFFu ? 0u : bidx;
+            dev_store(&counters[row], 0u);  // ready for the next call (also under graph replay)
+        }
     }
 }
 

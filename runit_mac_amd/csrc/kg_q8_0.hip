@@ -35,3 +35,11 @@ extern "C" __global__ void __launch_bounds__(256)
 k_act_limbs_f16(const uint16_t* x, XRec* out, uint32_t nxb) { act_limbs_body<uint16_t, false>(x, out, nxb); }
 extern "C" __global__ void __launch_bounds__(256)
 k_act_limbs_f16_q40(const uint16_t* x, XRec* out, uint32_t nxb) { act_limbs_body<uint16_t, true>(x, out, nxb); }
+extern "C" __global__ void __launch_bounds__(256)
+k_act_limbs_rows_f32(const float* x, const float* gamma, float eps, uint32_t K, XRec* out) {
+    act_limbs_rows_body<false>(x, gamma, eps, K, out);
+}
+extern "C" __global__ void __launch_bounds__(256)
+k_act_limbs_rows_f32_q40(const float* x, const float* gamma, float eps, uint32_t K, XRec* out) {
+    act_limbs_rows_body<true>(x, gamma, eps, K, out);
+}

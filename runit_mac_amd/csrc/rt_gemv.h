@@ -46,6 +46,10 @@ struct GemvArgs {
     // matrix-core body in a two-part launch: this part owns workgroups
     // [blk0, blk0 + nblk) (nblk = 0: the whole grid)
     uint32_t blk0, nblk;
+    // activation rows of a multi-row launch (the _x8 kernels; 0 otherwise):
+    // x holds their limb records row after row, output / residual row m of
+    // a matrix starts m rows of that matrix's length further on
+    uint32_t nx;
 };
 
 // Tiles one workgroup may own in a K-split launch (the host keeps the grid's
@@ -119,13 +123,22 @@ RT_DEV float silu_ref(float g) {
     return g / (1.0f + expf(-g));
 }
 
-// Epilogue operand (residual or bias) of virtual row vr, loaded early so the
-// epilogue does not wait on a dependent load.
+// Output length of matrix `mat` (the distance between two activation rows'
+// outputs in a multi-row launch).
 template <int EPI>
-RT_DEV float load_aux(const GemvArgs& a, uint32_t vr) {
+RT_DEV uint32_t out_len(const GemvArgs& a, uint32_t mat) {
+    if (epi_base(EPI) == EPI_FFN) return a.nvrows >> 1;
+    if (epi_base(EPI) == EPI_QKV || epi_base(EPI) == EPI_QKV_BIAS) return pick3(a.n[0], a.n[1], a.n[2], mat);
+    return a.nvrows;
+}
+
+// Epilogue operand (residual or bias) of virtual row vr (activation row m),
+// loaded early so the epilogue does not wait on a dependent load.
+template <int EPI>
+RT_DEV float load_aux(const GemvArgs& a, uint32_t vr, uint32_t m = 0) {
     uint32_t mat, r;
     vrow_map<EPI>(a, vr, mat, r);
-    if (epi_base(EPI) == EPI_F32_ADD) return aux_load<EPI>((const float*)a.aux[0] + r);
+    if (epi_base(EPI) == EPI_F32_ADD) return aux_load<EPI>((const float*)a.aux[0] + r + (size_t)m * a.nvrows);
     if (epi_base(EPI) == EPI_F16_ADD) return h2f(((const uint16_t*)a.aux[0])[r]);
     if (epi_base(EPI) == EPI_QKV_BIAS) return h2f(((const uint16_t*)mat_aux(a, mat))[r]);
     return 0.0f;
@@ -137,24 +150,29 @@ constexpr bool has_aux() {
 // Stores v (+ the preloaded epilogue operand) for virtual row vr.  With an
 // output aliasing the residual, the value was read by this same lane first.
 template <int EPI>
-RT_DEV void store_row_pre(const GemvArgs& a, uint32_t vr, float v, float aux) {
+RT_DEV void store_row(const GemvArgs& a, uint32_t vr, float v, uint32_t m);
+// (m: activation row of a multi-row launch)
+template <int EPI>
+RT_DEV void store_row_pre(const GemvArgs& a, uint32_t vr, float v, float aux, uint32_t m = 0) {
     uint32_t mat, r;
     vrow_map<EPI>(a, vr, mat, r);
+    const size_t ro = (size_t)m * out_len<EPI>(a, mat);
     if (epi_base(EPI) == EPI_F32_ADD) {
-        out_store<EPI>((float*)a.out[0] + r, v + aux);
+        out_store<EPI>((float*)a.out[0] + ro + r, v + aux);
     } else if (epi_base(EPI) == EPI_F16_ADD) {
         ((uint16_t*)a.out[0])[r] = f2h(v + aux);
     } else if (epi_base(EPI) == EPI_QKV_BIAS) {
-        out_store<EPI>((float*)mat_out(a, mat) + r, v + aux);
+        out_store<EPI>((float*)mat_out(a, mat) + ro + r, v + aux);
     } else {
-        store_row<EPI>(a, vr, v);
+        store_row<EPI>(a, vr, v, m);
     }
 }
 
 template <int EPI>
-RT_DEV void store_row(const GemvArgs& a, uint32_t vr, float v) {
+RT_DEV void store_row(const GemvArgs& a, uint32_t vr, float v, uint32_t m) {
     uint32_t mat, r;
     vrow_map<EPI>(a, vr, mat, r);
+    r += (uint32_t)(m * out_len<EPI>(a, mat));  // multi-row launch: row m's outputs
     if (epi_base(EPI) == EPI_F32) {
         out_store<EPI>((float*)a.out[0] + r, v);
     } else if (epi_base(EPI) == EPI_F32_ADD) {
@@ -212,7 +230,7 @@ RT_DEV void finish_rows(const GemvArgs& a, float* red, uint32_t tid, uint32_t TL
         } else {
 #pragma unroll
             for (int i = 0; i < RPL; ++i) {
-                if (vr0 + i < a.nvrows) store_row<EPI>(a, vr0 + i, acc[i]);
+                if (vr0 + i < a.nvrows) store_row<EPI>(a, vr0 + i, acc[i], 0);
             }
         }
     }
@@ -363,6 +381,54 @@ RT_DEV void gemv_body_chunked(const GemvArgs& a) {
     }
 }
 
+// One activation row staged by one wave (multi-row launches with K ≤ 1024):
+// lane l takes slices l, l + 64, ... (≤ XSTAGE_UNR rounds), loads them (and
+// γ) before the caller issues its weight loads, then RMS-normalises the row
+// with a wave-wide sum (x̂ = x · rsqrt(Σx²/K + eps) · γ, products rounded in
+// f32 as stage_x_convert rounds them) and writes its limb records.
+RT_DEV void stage_row_load(const float* __restrict__ x, const float* __restrict__ gamma,
+                           uint32_t nxb, XPre& p) {
+    const uint32_t total = nxb * 8, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int s = 0; s < XSTAGE_UNR; ++s) {
+        const uint32_t t = lane + 64 * s;
+        if (64 * s >= total) break;  // uniform
+        const uint32_t i = t < total ? (t >> 3) * 32 + (t & 7) * 4 : 0;
+        const f32x4 v = *(const f32x4*)(x + i);
+        p.v[s][0] = v.x; p.v[s][1] = v.y; p.v[s][2] = v.z; p.v[s][3] = v.w;
+        if (gamma) {
+            const f32x4 g = *(const f32x4*)(gamma + i);
+            p.g[s][0] = g.x; p.g[s][1] = g.y; p.g[s][2] = g.z; p.g[s][3] = g.w;
+        }
+    }
+}
+RT_DEV void stage_row_convert(XPre& p, const float* gamma, float eps, uint32_t nxb,
+                              XRec* __restrict__ recs) {
+    const uint32_t total = nxb * 8, lane = threadIdx.x & 63;
+    if (gamma) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int s = 0; s < XSTAGE_UNR; ++s) {
+            if (64 * s >= total) break;
+            const float sq = p.v[s][0] * p.v[s][0] + p.v[s][1] * p.v[s][1] +
+                             p.v[s][2] * p.v[s][2] + p.v[s][3] * p.v[s][3];
+            ss += lane + 64 * s < total ? sq : 0.0f;
+        }
+        ss = group_sum(ss, 64);
+        const float rms = rsqrtf(ss / (float)(nxb * 32) + eps);
+#pragma unroll
+        for (int s = 0; s < XSTAGE_UNR; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p.v[s][i] = p.v[s][i] * rms * p.g[s][i];
+    }
+#pragma unroll
+    for (int s = 0; s < XSTAGE_UNR; ++s) {
+        const uint32_t t = lane + 64 * s;
+        if (64 * s >= total) break;
+        if (t < total) limb_slice<false>(p.v[s], t & 7, recs + (t >> 3));  // whole 8-lane groups
+    }
+}
+
 // Matrix-core path (whole K in LDS).  Lane 4·slot + q works on row q of the
 // wave's current row quad and on unit `slot` (+16 per step) of that row, so
 // the 16 lanes of a row read 16 consecutive units (coalesced) and the four
@@ -370,7 +436,10 @@ RT_DEV void gemv_body_chunked(const GemvArgs& a) {
 // Each lane walks a flat sequence of (tile, step) items and issues the loads
 // of item n+1 before computing item n; the first item's loads are issued
 // before the activation staging.
-template <class F, int EPI, typename XT, int RQ, int PF, class Hook = NoHook>
+// NX > 1: up to NX activation rows (a.nx of them) against each weight row:
+// x holds their limb records (k_act_limbs_rows), every loaded weight unit is
+// dotted with each row's records, and each row gets its own epilogue.
+template <class F, int EPI, typename XT, int RQ, int PF, class Hook = NoHook, int NX = 1>
 RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t tid = threadIdx.x;
@@ -383,8 +452,9 @@ RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
     const uint32_t ks = bid % S, wg = bid / S, nwg = gdim / S;
     const uint32_t cu0 = ks * a.kc_units;  // first unit of the chunk
     const uint32_t units = min(a.K / F::UNIT_EL - cu0, a.kc_units);
-    XRec* xs = (XRec*)smem;  // the chunk's records
-    float* red = (float*)(smem + (size_t)(a.kc_units * F::UNIT_EL / 32) * sizeof(XRec));
+    XRec* xs = (XRec*)smem;  // the chunk's records (NX rows: row after row)
+    float* red = (float*)(smem + (size_t)NX * (a.kc_units * F::UNIT_EL / 32) * sizeof(XRec));
+    const uint32_t nx = NX > 1 ? a.nx : 1;  // activation rows (uniform)
     // ksw waves share one group of RQ row quads and split its K steps
     const uint32_t ksw = a.ksw;
     const uint32_t wgrp = wave / ksw, wk = wave % ksw;
@@ -413,9 +483,11 @@ RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
         }
     };
 
-    float acc[RQ], aux[RQ];
+    float acc[RQ][NX], aux[RQ][NX];
 #pragma unroll
-    for (int rq = 0; rq < RQ; ++rq) acc[rq] = aux[rq] = 0.0f;
+    for (int rq = 0; rq < RQ; ++rq)
+#pragma unroll
+        for (int m = 0; m < NX; ++m) acc[rq][m] = aux[rq][m] = 0.0f;
     // (every lane loads, unconditionally: a load on only some control paths
     // would make the compiler's wait for the x loads a wait for all loads)
     auto load_tile_aux = [&](uint32_t item) {
@@ -425,7 +497,9 @@ RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
 #pragma unroll
             for (int rq = 0; rq < RQ; ++rq) {
                 const uint32_t vr = vb + 4 * rq + q;
-                aux[rq] = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
+#pragma unroll
+                for (int m = 0; m < NX; ++m)
+                    if (m < (int)nx) aux[rq][m] = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1, m);
             }
         }
     };
@@ -441,6 +515,10 @@ RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
         if constexpr (is_attn_x<XT>()) {
             // (the host launches this form with one slice round, whole K, nsp ≤ 8)
             stage_attn_load<__is_same(XT, AttnXC)>(a.x, a.xml, a.xnsp, a.xhd, nxb, xa);
+        } else if constexpr (NX > 1) {
+            // f32 rows staged here (K ≤ 1024): wave w takes activation row w
+            if (!a.x_rec && wave < nx)
+                stage_row_load((const float*)a.x + (size_t)wave * a.K, a.gamma, nxb, xp);
         } else {
             if (one_pass)
                 stage_x_load<XT>((const XT*)a.x + (size_t)xb0 * 32,
@@ -464,7 +542,18 @@ RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
     } else {
         // (the host launches whole-K kernels either with x records or with a
         // K that one pass covers)
-        if (one_pass)
+        if constexpr (NX > 1) {
+            if (!a.x_rec) {
+                if (wave < nx) stage_row_convert(xp, a.gamma, a.eps, nxb, xs + (size_t)wave * nxb);
+            } else {
+                // every row's records of the chunk, loads of all rows in flight
+                const uint32_t n16 = nxb * (sizeof(XRec) / 16), kr = a.K / 32;
+                for (uint32_t i = threadIdx.x; i < nx * n16; i += wg_threads()) {
+                    const uint32_t m = i / n16, j = i % n16;
+                    ((u32x4*)xs)[i] = ((const u32x4*)((const XRec*)a.x + (size_t)m * kr + xb0))[j];
+                }
+            }
+        } else if (one_pass)
             stage_x_convert<F::Q40PERM, coh_x>(xp, a.gamma, a.eps, nxb, xs);
         else
             copy_x_limbs((const XRec*)a.x, xb0, nxb, xs);
@@ -483,40 +572,52 @@ RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
                 const bool valid = u < units;
                 const uint32_t uc = valid ? u : 0;
 #pragma unroll
-                for (int rq = 0; rq < RQ; ++rq) {
-                    const float v = F::mdot(buf[half][rq], xs, uc, lq);
-                    acc[rq] += valid ? v : 0.0f;
-                }
+                for (int rq = 0; rq < RQ; ++rq)
+#pragma unroll
+                    for (int m = 0; m < NX; ++m)
+                        if (m < (int)nx) {
+                            const float v = F::mdot(buf[half][rq], xs + (size_t)m * nxb, uc, lq);
+                            acc[rq][m] += valid ? v : 0.0f;
+                        }
                 if (item + PF < nitems) issue(item + PF, buf[half]);
                 if (item % spw == spw - 1) {
                     const uint32_t vbase = rows_of(item / spw);
-                    float rsum[RQ];
+                    float rsum[RQ][NX];
 #pragma unroll
-                    for (int rq = 0; rq < RQ; ++rq) {
-                        // sum over the 16 slots of the row: lane bits 2..5
-                        float v = acc[rq];
-                        v += swz_xor_f<4>(v);
-                        v += swz_xor_f<8>(v);
-                        v += swz_xor_f<16>(v);
-                        v += __shfl_xor(v, 32, 64);
-                        rsum[rq] = v;
-                        acc[rq] = 0.0f;
-                    }
+                    for (int rq = 0; rq < RQ; ++rq)
+#pragma unroll
+                        for (int m = 0; m < NX; ++m) {
+                            if (m >= (int)nx) continue;
+                            // sum over the 16 slots of the row: lane bits 2..5
+                            float v = acc[rq][m];
+                            v += swz_xor_f<4>(v);
+                            v += swz_xor_f<8>(v);
+                            v += swz_xor_f<16>(v);
+                            v += __shfl_xor(v, 32, 64);
+                            rsum[rq][m] = v;
+                            acc[rq][m] = 0.0f;
+                        }
                     if (ksw > 1) {
                         // combine the K-split waves of the group in a fixed order
                         if (slot == 0) {
 #pragma unroll
-                            for (int rq = 0; rq < RQ; ++rq) red[(wave * RQ + rq) * 4 + q] = rsum[rq];
+                            for (int rq = 0; rq < RQ; ++rq)
+#pragma unroll
+                                for (int m = 0; m < NX; ++m)
+                                    if (m < (int)nx) red[((wave * RQ + rq) * NX + m) * 4 + q] = rsum[rq][m];
                         }
                         lds_barrier();
                         if (wk == 0) {
 #pragma unroll
-                            for (int rq = 0; rq < RQ; ++rq) {
-                                float t = 0.0f;
-                                for (uint32_t w = 0; w < ksw; ++w)
-                                    t += red[((wgrp * ksw + w) * RQ + rq) * 4 + q];
-                                rsum[rq] = t;
-                            }
+                            for (int rq = 0; rq < RQ; ++rq)
+#pragma unroll
+                                for (int m = 0; m < NX; ++m) {
+                                    if (m >= (int)nx) continue;
+                                    float t = 0.0f;
+                                    for (uint32_t w = 0; w < ksw; ++w)
+                                        t += red[(((wgrp * ksw + w) * RQ + rq) * NX + m) * 4 + q];
+                                    rsum[rq][m] = t;
+                                }
                         }
                         lds_barrier();
                     }
@@ -527,21 +628,29 @@ RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
 #pragma unroll
                             for (int rq = 0; rq < RQ; ++rq) {
                                 const uint32_t vr = vbase + 4 * rq + q;
-                                if (vr < a.nvrows) dev_store(a.part + (size_t)ks * a.nvrows + vr, rsum[rq]);
+#pragma unroll
+                                for (int m = 0; m < NX; ++m)
+                                    if (m < (int)nx && vr < a.nvrows)
+                                        dev_store(a.part + ((size_t)ks * nx + m) * a.nvrows + vr, rsum[rq][m]);
                             }
                         }
                     } else if (wk == 0) {
 #pragma unroll
                         for (int rq = 0; rq < RQ; ++rq) {
-                            const float v = rsum[rq];
                             const uint32_t vr = vbase + 4 * rq + q;
-                            if (epi_base(EPI) == EPI_FFN) {
-                                // quad holds (gate r, up r, gate r+1, up r+1)
-                                const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
-                                if (slot == 0 && (q & 1) == 0 && vr + 1 < a.nvrows)
-                                    out_store<EPI>((float*)a.out[0] + (vr >> 1), silu_ref(v) * up);
-                            } else {
-                                if (slot == 0 && vr < a.nvrows) store_row_pre<EPI>(a, vr, v, aux[rq]);
+#pragma unroll
+                            for (int m = 0; m < NX; ++m) {
+                                if (m >= (int)nx) continue;
+                                const float v = rsum[rq][m];
+                                if (epi_base(EPI) == EPI_FFN) {
+                                    // quad holds (gate r, up r, gate r+1, up r+1)
+                                    const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(v);
+                                    if (slot == 0 && (q & 1) == 0 && vr + 1 < a.nvrows)
+                                        out_store<EPI>((float*)a.out[0] + (size_t)m * (a.nvrows >> 1) + (vr >> 1),
+                                                       silu_ref(v) * up);
+                                } else {
+                                    if (slot == 0 && vr < a.nvrows) store_row_pre<EPI>(a, vr, v, aux[rq][m], m);
+                                }
                             }
                         }
                     }
@@ -564,19 +673,21 @@ RT_DEV void gemv_mq_body(const GemvArgs& a, const Hook& hook = Hook()) {
             const uint32_t tile = wg + t * nwg;
             const uint32_t vt = tile * vrows_per_wg;
             const uint32_t step_r = epi_base(EPI) == EPI_FFN ? 2 : 1;
+            for (uint32_t m = 0; m < nx; ++m)
             for (uint32_t i = tid * step_r; i < vrows_per_wg; i += wg_threads() * step_r) {
                 const uint32_t vr = vt + i;
                 if (vr >= a.nvrows) break;
                 float v = 0.0f, v1 = 0.0f;
                 for (uint32_t c = 0; c < S; ++c) {
-                    v += dev_load(a.part + (size_t)c * a.nvrows + vr);
-                    if (epi_base(EPI) == EPI_FFN && vr + 1 < a.nvrows)
-                        v1 += dev_load(a.part + (size_t)c * a.nvrows + vr + 1);
+                    const float* pc = a.part + ((size_t)c * nx + m) * a.nvrows;
+                    v += dev_load(pc + vr);
+                    if (epi_base(EPI) == EPI_FFN && vr + 1 < a.nvrows) v1 += dev_load(pc + vr + 1);
                 }
                 if (epi_base(EPI) == EPI_FFN) {
-                    if (vr + 1 < a.nvrows) out_store<EPI>((float*)a.out[0] + (vr >> 1), silu_ref(v) * v1);
+                    if (vr + 1 < a.nvrows)
+                        out_store<EPI>((float*)a.out[0] + (size_t)m * (a.nvrows >> 1) + (vr >> 1), silu_ref(v) * v1);
                 } else {
-                    store_row<EPI>(a, vr, v);
+                    store_row<EPI>(a, vr, v, m);
                 }
             }
             if (tid == 0) dev_store(a.counters + (size_t)tile * a.cstride, 0u);  // ready for the next call
@@ -646,6 +757,12 @@ RT_DEV void gemv_mq_or_chunked(const GemvArgs& a) {
         gemv_mq_or_chunked<FMT, FMT, EPI, XT, 2, (epi_base(EPI) == EPI_FFN ? 2 : 1), UNR>(a);        \
     }
 #define RT_Q6K_WPE 2
+// Multi-row kernels (<name>_x8): up to 8 activation rows (records prepared by
+// k_act_limbs_rows) through the matrix-core body, whole K or K split.
+#define RT_GEMV_ROWS(NAME, FMT, EPI, LB)                                                  \
+    extern "C" __global__ void __launch_bounds__(LB) NAME##_x8(GemvArgs a) {              \
+        gemv_mq_body<FMT, EPI, float, 1, (fmt_pf<FMT>() ? fmt_pf<FMT>() : GEMV_PF1), NoHook, 8>(a); \
+    }
 
 // Single-block-unit fallback (rows with an odd number of 32-element blocks)
 #define RT_GEMV_KERNEL_S(NAME, FMT, EPI, XT, UNR)                                 \
@@ -684,3 +801,42 @@ RT_DEV void act_limbs_body(const XT* __restrict__ x, XRec* __restrict__ out, uin
         limb_slice<Q40PERM>(v, t & 7, out + (t >> 3));
     }
 }
+
+// Multi-row pre-pass: the limb records of `rows` activation rows ([rows][K]
+// f32), one workgroup per row; with γ the row is RMS-normalised first,
+// x̂ = x · rsqrt(Σx²/K + eps) · γ, each product rounded in f32 as the fused
+// staging (stage_x_convert) computes it.
+template <bool Q40PERM>
+RT_DEV void act_limbs_rows_body(const float* __restrict__ x, const float* __restrict__ gamma,
+                                float eps, uint32_t K, XRec* __restrict__ out) {
+    const uint32_t nxb = K / 32, total = nxb * 8, nt = wg_threads();
+    const float* xr = x + (size_t)blockIdx.x * K;
+    XRec* o = out + (size_t)blockIdx.x * nxb;
+    float rms = 1.0f;
+    if (gamma) {
+        __shared__ float nred[16];
+        float ss = 0.0f;
+        for (uint32_t t = threadIdx.x; t < total; t += nt) {
+            const f32x4 v = *(const f32x4*)(xr + (t >> 3) * 32 + (t & 7) * 4);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = group_sum(ss, 64);
+        if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (uint32_t w = 0; w < (nt >> 6); ++w) tot += nred[w];
+        rms = rsqrtf(tot / (float)K + eps);
+    }
+    for (uint32_t t = threadIdx.x; t < total; t += nt) {
+        const uint32_t i = (t >> 3) * 32 + (t & 7) * 4;
+        const f32x4 xv = *(const f32x4*)(xr + i);
+        float v[4] = {xv.x, xv.y, xv.z, xv.w};
+        if (gamma) {
+            const f32x4 g = *(const f32x4*)(gamma + i);
+            v[0] = v[0] * rms * g.x; v[1] = v[1] * rms * g.y;
+            v[2] = v[2] * rms * g.z; v[3] = v[3] * rms * g.w;
+        }
+        limb_slice<Q40PERM>(v, t & 7, o + (t >> 3));
+    }
+}
+

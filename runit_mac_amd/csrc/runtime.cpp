@@ -51,6 +51,7 @@ struct GemvArgs {
     uint32_t ls_res;
     uint32_t ls_xcd;
     uint32_t blk0, nblk;
+    uint32_t nx;
 };
 
 constexpr uint32_t XREC_BYTES = 112;
@@ -134,7 +135,7 @@ const char* const kKernelNames[] = {
     "k_decode_attention_f32_hd64", "k_decode_attention_f32_hd128", "k_decode_attention_f32_hd256",
     "k_attn_rope_f32_hd64", "k_attn_rope_f32_hd128", "k_attn_rope_f32_hd256",
     "k_add_f16_into_f32", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
-    "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32",
+    "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32", "k_rope_kv_write_batch_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
     "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
@@ -188,6 +189,9 @@ const char* const kLskBases[] = {
     "k_gemv_q5k_f32_f32add", "k_gemv_q4kg_f32_f32add", "k_gemv_q5kg_f32_f32add", "k_gemv_q4_0g_f32_f32add", "k_gemv_q5_0_f32_f32add",
     "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32add",
 };
+// Multi-row kernels: <base>_x8 for each format's four epilogues.
+const char* const kRowsFmts[] = {"q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k",
+                                 "q4_0g", "q4kg", "q5kg", "q6kg"};
 // Kernels with a VALU-dot twin <base>_ls<NI>v (the dot-form A/B).
 const char* const kLsValuBases[] = {"k_ffn_q4k", "k_gemv_q6k_f32_f32"};
 constexpr uint32_t kLsMaxNI = 3;
@@ -740,6 +744,190 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
     return launch(c, name, dim3(grid), dim3(p.T), lds, params);
 }
 
+// ─────────────── multi-row launches (batched verify / prefill) ───────────────
+//
+// rows activation rows [rows][K] through one weight pass per 8 rows: a
+// pre-pass builds every row's limb records (RMS-normalised first when gamma
+// is given) into the workspace, then the <kname>_x8 kernel runs the
+// matrix-core body with up to 8 rows per launch, whole K per workgroup when
+// 8 rows' records fit in LDS, else split over workgroups (partials in `part`).
+constexpr uint32_t kRowsNX = 8;  // activation rows per launch (the kernels' NX)
+
+int gemv_rows_launch(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a, uint32_t rows,
+                     const float* gamma, float eps) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    const uint32_t mq_el = f.mq_units();
+    if (a.K == 0 || a.K % f.blk_el != 0 || a.K % mq_el != 0)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: %s rows: k=%u must be a positive multiple of %u (%s)",
+                    kname, a.K, std::max(f.blk_el, mq_el), f.name);
+    if (rows == 0 || a.nvrows == 0) return RT_OK;
+    if (!a.x || !a.out[0])
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s rows: null buffer", kname);
+    if (!aligned(a.x, 16) || (gamma && !aligned(gamma, 16)))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s rows: input must be 16-byte aligned",
+                    kname);
+    char name[96];
+    snprintf(name, sizeof name, "%s_x%u", kname, kRowsNX);
+    if (!c->fns.count(name))
+        return fail(c, RT_ERR_PIPELINE_NOT_FOUND, "pipeline function '%s' not found", name);
+    a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
+    const uint32_t nxb = a.K / 32;
+    // rows of at most 1024 elements are staged (and normalised) by the
+    // kernel itself, one wave per row; longer ones by the pre-pass
+    const bool in_kernel = nxb * 8 <= 4 * 64 && !f.q40perm;
+    int st = RT_OK;
+    if (!in_kernel) st = ensure_ws(c, (size_t)rows * nxb * XREC_BYTES, kname);
+    if (st != RT_OK) return st;
+    if (in_kernel) {
+        a.gamma = gamma;
+        a.eps = eps;
+    } else {
+        const char* pk = f.q40perm ? "k_act_limbs_rows_f32_q40" : "k_act_limbs_rows_f32";
+        const void* xin = a.x;
+        void* xout = c->ws;
+        uint32_t K = a.K;
+        void* pp[] = {&xin, (void*)&gamma, &eps, &K, &xout};
+        st = launch(c, pk, dim3(rows), dim3(256), 0, pp);
+        if (st != RT_OK) return st;
+        a.x_rec = 1;
+        a.gamma = nullptr;
+    }
+    // K chunk per workgroup: whole K when 8 rows' records fit in LDS
+    const uint32_t T = 512, nwaves = T / 64;
+    const size_t red_bytes = (size_t)16 * kRowsNX * 4 * sizeof(float);
+    const size_t lds_cap = std::min<size_t>(c->max_lds, 160 * 1024) - red_bytes;
+    const uint32_t units = a.K / mq_el, rec_per_unit = mq_el / 32;
+    uint32_t kcu = units;
+    if ((size_t)kRowsNX * nxb * XREC_BYTES > lds_cap) {
+        if (!c->ksplit_enabled)
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s rows: k=%u needs a K split",
+                        kname, a.K);
+        kcu = (uint32_t)(lds_cap / ((size_t)kRowsNX * XREC_BYTES * rec_per_unit));
+    }
+    const uint32_t S = (units + kcu - 1) / kcu;
+    kcu = (units + S - 1) / S;
+    a.ksplit = S;
+    a.kc_units = kcu;
+    a.xb_chunk = nxb;  // whole-K form of the kernel (matrix-core body)
+    const size_t lds = (size_t)kRowsNX * kcu * rec_per_unit * XREC_BYTES + red_bytes;
+    const uint32_t quads = (a.nvrows + 3) / 4;
+    const uint32_t nsteps = (kcu + 15) / 16;
+    const uint32_t resident_waves = (uint32_t)c->cu_count * 16;
+    uint32_t ksw = 1;
+    while (ksw < nwaves && quads * S * ksw * 2 <= resident_waves && ksw * 2 <= nsteps) ksw *= 2;
+    a.ksw = ksw;
+    a.lpr = 16;
+    const uint32_t rows_per_wg = (nwaves / ksw) * 4;
+    const uint32_t resident = std::max<uint32_t>(1, std::min<uint32_t>(4, occupancy(c, name, T, lds)));
+    const uint32_t ntiles = (a.nvrows + rows_per_wg - 1) / rows_per_wg;
+    const uint32_t cap = (uint32_t)c->cu_count * resident;
+    const uint32_t rounds = (ntiles * S + cap - 1) / cap;
+    const uint32_t grid = (ntiles + rounds - 1) / rounds * S;
+    if (S > 1) {
+        if (ntiles > kAttnCounters)
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s rows: %u row tiles exceed %u",
+                        kname, ntiles, kAttnCounters);
+        if (rounds > kMaxSplitTiles)
+            return fail(c, RT_ERR_DISPATCH,
+                        "kernel dispatch error: %s rows: %u tiles per workgroup exceed %u", kname,
+                        rounds, kMaxSplitTiles);
+        st = ensure_part(c, (size_t)S * kRowsNX * a.nvrows * sizeof(float), kname);
+        if (st != RT_OK) return st;
+        a.part = (float*)c->part;
+        a.counters = c->counters;
+        a.cstride = 32;
+        while (a.cstride > 1 && (size_t)ntiles * a.cstride > kAttnCounters) a.cstride >>= 1;
+    }
+    // outputs (and residual) of row r0 of a matrix lie r0 of its lengths on
+    const bool ffn = strstr(kname, "k_ffn_") == kname;
+    const bool qkv = strstr(kname, "k_qkv") == kname;
+    auto len = [&](uint32_t mat) -> size_t {
+        return ffn ? a.nvrows / 2 : qkv ? a.n[mat] : a.nvrows;
+    };
+    for (uint32_t r0 = 0; r0 < rows; r0 += kRowsNX) {
+        GemvArgs b = a;
+        b.nx = std::min(kRowsNX, rows - r0);
+        b.x = in_kernel ? (const void*)((const float*)a.x + (size_t)r0 * a.K)
+                        : (const void*)((const uint8_t*)c->ws + (size_t)r0 * nxb * XREC_BYTES);
+        for (uint32_t mat = 0; mat < 3; ++mat)
+            if (b.out[mat]) b.out[mat] = (float*)b.out[mat] + r0 * len(mat);
+        if (!qkv && b.aux[0]) b.aux[0] = (const float*)b.aux[0] + r0 * len(0);  // residual
+        void* params[] = {&b};
+        st = launch(c, name, dim3(grid), dim3(T), lds, params);
+        if (st != RT_OK) return st;
+    }
+    return RT_OK;
+}
+
+// Multi-row entry points per format: plain (optionally RMS-normalised input:
+// the LM head after the final norm), + residual (y may alias res), Q/K/V
+// (+ bias; a null weight skips that matrix, so a mixed-format Q/K/V takes
+// two calls) and gate+up+SiLU (optionally normalised input).
+static int rows_qkv(rt_ctx* c, const char* kname, const Fmt& f, const void* wq, const void* wk,
+                    const void* wv, const float* x, const float* gamma, float eps, float* oq,
+                    float* ok, float* ov, const uint16_t* bq, const uint16_t* bk,
+                    const uint16_t* bv, uint32_t rows, uint32_t q_dim, uint32_t kv_dim,
+                    uint32_t k) {
+    GemvArgs a{};
+    uint32_t nm = 0;
+    const void* w3[3] = {wq, wk, wv};
+    float* o3[3] = {oq, ok, ov};
+    const uint16_t* b3[3] = {bq, bk, bv};
+    const uint32_t n3[3] = {q_dim, kv_dim, kv_dim};
+    for (int i = 0; i < 3; ++i) {
+        if (!w3[i]) continue;
+        if (!o3[i] || !b3[i])
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: %s rows: null buffer", kname);
+        a.w[nm] = (const uint8_t*)w3[i];
+        a.out[nm] = o3[i];
+        a.aux[nm] = b3[i];
+        a.n[nm] = n3[i];
+        ++nm;
+    }
+    if (nm == 0) return RT_OK;
+    a.x = x;
+    a.nvrows = a.n[0] + a.n[1] + a.n[2];
+    a.K = k;
+    return gemv_rows_launch(c, kname, f, a, rows, gamma, eps);
+}
+#define RT_ROWS_ENTRIES(FN, FMT)                                                                 \
+    int rt_gemv_rows_##FN##_f32(rt_ctx* c, const void* w, const float* x, const float* gamma,      \
+                                float eps, float* y, uint32_t rows, uint32_t n, uint32_t k) {      \
+        if (!w) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemv_rows: null weight");  \
+        return gemv_rows_launch(c, "k_gemv_" #FN "_f32_f32", FMT, plain_args(w, x, y, nullptr, n, k), \
+                                rows, gamma, eps);                                                 \
+    }                                                                                              \
+    int rt_gemv_rows_##FN##_add_f32(rt_ctx* c, const void* w, const float* x, const float* res,    \
+                                    float* y, uint32_t rows, uint32_t n, uint32_t k) {             \
+        if (!w || !res)                                                                            \
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemv_rows_add: null buffer");  \
+        return gemv_rows_launch(c, "k_gemv_" #FN "_f32_f32add", FMT, plain_args(w, x, y, res, n, k), \
+                                rows, nullptr, 0.0f);                                              \
+    }                                                                                              \
+    int rt_qkv_bias_rows_##FN##_f32(rt_ctx* c, const void* wq, const void* wk, const void* wv,     \
+                                    const float* x, const float* gamma, float eps, float* q,       \
+                                    float* k_out, float* v, const uint16_t* bq,                    \
+                                    const uint16_t* bk, const uint16_t* bv, uint32_t rows,         \
+                                    uint32_t q_dim, uint32_t kv_dim, uint32_t k) {                 \
+        return rows_qkv(c, "k_qkv_bias_" #FN, FMT, wq, wk, wv, x, gamma, eps, q, k_out, v, bq, bk,   \
+                        bv, rows, q_dim, kv_dim, k);                                               \
+    }                                                                                              \
+    int rt_fused_ffn_rows_##FN##_f32(rt_ctx* c, const void* wg, const void* wu, const float* x,    \
+                                     const float* gamma, float eps, float* act, uint32_t rows,     \
+                                     uint32_t ff, uint32_t k) {                                    \
+        if (!wg || !wu)                                                                            \
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: ffn_rows: null weight");       \
+        GemvArgs a{};                                                                              \
+        a.w[0] = (const uint8_t*)wg; a.w[1] = (const uint8_t*)wu;                                  \
+        a.out[0] = act;                                                                            \
+        a.x = x;                                                                                   \
+        a.n[0] = ff; a.n[1] = ff;                                                                  \
+        a.nvrows = 2 * ff;                                                                         \
+        a.K = k;                                                                                   \
+        return gemv_rows_launch(c, "k_ffn_" #FN, FMT, a, rows, gamma, eps);                        \
+    }
+
 GemvArgs plain_args(const void* w, const void* x, void* y, const void* aux, uint32_t m,
                     uint32_t k) {
     GemvArgs a{};
@@ -993,6 +1181,15 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     for (const char* b : kLsBases)
         for (uint32_t ni = 1; ni <= kLsMaxNI; ++ni) names.push_back(std::string(b) + "_ls" + std::to_string(ni));
     for (const char* b : kLskBases) names.push_back(std::string(b) + "_lsk1");
+    for (const char* fm : kRowsFmts)
+        for (const char* pat : {"k_gemv_%s_f32_f32_x8", "k_gemv_%s_f32_f32add_x8", "k_qkv_bias_%s_x8",
+                                "k_ffn_%s_x8"}) {
+            char nb[64];
+            snprintf(nb, sizeof nb, pat, fm);
+            names.push_back(nb);
+        }
+    names.push_back("k_act_limbs_rows_f32");
+    names.push_back("k_act_limbs_rows_f32_q40");
     for (const char* b : kLsValuBases)
         for (uint32_t ni = 1; ni <= kLsMaxNI; ++ni)
             names.push_back(std::string(b) + "_ls" + std::to_string(ni) + "v");
@@ -1697,6 +1894,17 @@ constexpr GemmFmt kGemmQ4KG{"q4kg", 256, 144, 8, 1, 1, true, rt_gemv_q4kg_f32in_
 constexpr GemmFmt kGemmQ5KG{"q5kg", 256, 176, 8, 1, 1, true, rt_gemv_q5kg_f32in_f32out};
 constexpr GemmFmt kGemmQ6KG{"q6kg", 256, 210, 8, 2, 2, false, rt_gemv_q6kg_f32in_f32out, 4};
 
+RT_ROWS_ENTRIES(q8_0, kQ8_0)
+RT_ROWS_ENTRIES(q4_0, kQ4_0)
+RT_ROWS_ENTRIES(q4k, kQ4K)
+RT_ROWS_ENTRIES(q6k, kQ6KU)
+RT_ROWS_ENTRIES(q5_0, kQ5_0)
+RT_ROWS_ENTRIES(q5k, kQ5K)
+RT_ROWS_ENTRIES(q4_0g, kQ4_0G)
+RT_ROWS_ENTRIES(q4kg, kQ4KG)
+RT_ROWS_ENTRIES(q5kg, kQ5KG)
+RT_ROWS_ENTRIES(q6kg, kQ6KGU)
+
 int rt_gemm_q8_0_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
                      uint32_t n, uint32_t k) {
     return gemm_launch(c, kGemmQ8_0, w, x, y, m_rows, n, k);
@@ -2161,6 +2369,31 @@ int rt_rope_batch_inplace_f32(rt_ctx* c, float* x, uint32_t head_dim, uint32_t n
                   0, params);
 }
 
+int rt_rope_kv_write_batch_f32(rt_ctx* c, float* q, const float* k, const float* v,
+                               float* k_cache, float* v_cache, uint32_t head_dim,
+                               uint32_t num_heads, uint32_t num_kv_heads, uint32_t start_pos,
+                               float theta, uint32_t seq, uint32_t max_seq) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (head_dim < 2 || head_dim % 2)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: rope_kv: head_dim=%u must be even",
+                    head_dim);
+    const uint32_t heads = std::max(num_heads, num_kv_heads);
+    if (seq == 0 || heads == 0) return RT_OK;
+    if ((num_heads && !q) || (num_kv_heads && (!k || !v || !k_cache || !v_cache)))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: rope_kv: null buffer");
+    if ((uint64_t)start_pos + seq > max_seq)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: rope_kv: start_pos=%u + seq=%u > max_seq=%u", start_pos,
+                    seq, max_seq);
+    if (seq > 65535 || heads > 65535)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: rope_kv: seq=%u heads=%u > 65535",
+                    seq, heads);
+    void* params[] = {&q, (void*)&k, (void*)&v, &k_cache, &v_cache, &head_dim, &num_heads,
+                      &num_kv_heads, &start_pos, &theta, &max_seq};
+    return launch(c, "k_rope_kv_write_batch_f32", dim3((head_dim / 2 + 63) / 64, heads, seq),
+                  dim3(64), 0, params);
+}
+
 int rt_kv_write_batch_f32(rt_ctx* c, const float* k, const float* v, float* k_cache,
                           float* v_cache, uint32_t start_pos, uint32_t seq, uint32_t max_seq,
                           uint32_t head_dim, uint32_t num_kv_heads) {
@@ -2204,9 +2437,17 @@ int rt_argmax_rows_first_f32(rt_ctx* c, const float* in, uint32_t* result, uint3
     if (rows == 0) return RT_OK;
     if (!in || !result)
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: argmax_rows: null buffer");
-    if (n == 0) return rt_memset(c, result, 0, (size_t)rows * 4);
-    void* params[] = {&in, &result, &n};
-    return launch(c, "k_argmax_rows_first_f32", dim3(rows), dim3(1024), 0, params);
+    if (rows > kAttnCounters || rows > 65535)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: argmax_rows: rows=%u > %u", rows,
+                    std::min<uint32_t>(kAttnCounters, 65535));
+    // ranges of ≥ 4096 elements, at most 64 per row
+    const uint32_t G = std::max<uint32_t>(1, std::min<uint32_t>(64, (n + 4095) / 4096));
+    int st = ensure_ws(c, (size_t)rows * G * 8, "argmax_rows");
+    if (st != RT_OK) return st;
+    void* states = c->ws;
+    uint32_t* counters = c->counters;
+    void* params[] = {(void*)&in, &result, &n, &states, &counters};
+    return launch(c, "k_argmax_rows_first_f32", dim3(G, rows), dim3(256), 0, params);
 }
 
 int rt_flash_attention_f32(rt_ctx* c, const float* q, const float* k, const float* v, float* out,

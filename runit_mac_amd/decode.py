@@ -522,15 +522,16 @@ class DecodeModel:
         self._vbufs = v
         return v
 
-    def verify_forward(self, tokens, start_pos: int) -> dict:
+    def verify_forward(self, tokens, start_pos: int, form: str | None = None) -> dict:
         """verify_draft's batched forward (forward.rs:2141-2273) on the GPU:
-        the M tokens embedded together, every projection one batched GEMM in
-        the matrix's own format, bias broadcast, batched RoPE at start_pos..,
-        the M keys / values written to the cache, causal attention (row r at
-        position start_pos + r sees the cache up to there), residual adds,
-        SiLU·up, the final norm and the LM-head GEMM, and the per-row
-        first-max argmax.  Returns the activation buffers (``logits``:
-        [M][vocab], ``idx``: [M] argmax)."""
+        the M tokens embedded together; per layer Q/K/V (+ bias) of the
+        normalised rows, batched RoPE at start_pos.., the M keys / values
+        written to the cache, causal attention (row r at position
+        start_pos + r sees the cache up to there), O (+ residual), gate+up+SiLU
+        of the normalised rows, down (+ residual); the final norm and the LM
+        head, and the per-row first-max argmax.  Every projection runs in its
+        matrix's own format (see verify_pass for the two forms).  Returns the
+        activation buffers (``logits``: [M][vocab], ``idx``: [M] argmax)."""
         ctx, c = self.ctx, self.cfg
         toks = np.ascontiguousarray(tokens, dtype=np.uint32)
         M = int(toks.size)
@@ -544,42 +545,83 @@ class DecodeModel:
         B = self._verify_arena(M)
         lib = d.load_library()
         ctx._check(lib.rt_upload(ctx.handle, B["tok"], toks.ctypes.data, toks.nbytes))
-        return self.verify_pass(M, start_pos)
+        return self.verify_pass(M, start_pos, form)
 
-    def verify_pass(self, M: int, start_pos: int) -> dict:
+    # Batches of up to VERIFY_ROWS_MAX rows of a model with a hidden size of at
+    # most 1024 take the multi-row GEMVs (weights read once per 8 rows, norms /
+    # biases / SiLU / residuals fused in; at the 0.5B shapes, 8 rows: 12.4 µs
+    # for gate+up+SiLU, 9.1 µs for O + residual).  Larger models and longer
+    # batches take the batched GEMMs, which are faster there (the 7B Q4_K
+    # gate+up at 8 rows: 72.8 µs as multi-row GEMVs).
+    VERIFY_ROWS_MAX = 16
+    VERIFY_ROWS_MAX_HIDDEN = 1024
+
+    def verify_pass(self, M: int, start_pos: int, form: str | None = None) -> dict:
         """The launches of verify_forward for the M token ids already in the
-        verify buffers (``tok``): no host transfer, so it can be captured."""
+        verify buffers (``tok``): no host transfer, so it can be captured.
+        form: "rows" (multi-row GEMVs) or "gemm" (batched GEMMs + separate
+        norm / bias / SiLU / residual kernels, the reference's sequence);
+        default by M."""
         ctx, c = self.ctx, self.cfg
         B = self._verify_arena(M)
         h, qd, kvd, hd, ff = c.hidden, c.q_dim, c.kv_dim, c.head_dim, c.ff
         X, XN = B["x"], B["xn"]
+        form = form or ("rows" if M <= self.VERIFY_ROWS_MAX and h <= self.VERIFY_ROWS_MAX_HIDDEN
+                        else "gemm")
+        if form not in ("rows", "gemm"):
+            raise ValueError("form must be 'rows' or 'gemm'")
         d.embed_rows_f32(ctx, self.embd_fmt, self.embd, B["tok"], X, h, M)
 
         def gemm(fmt, w, x, y, n, k):
             getattr(d, f"gemm_{fmt}_f32")(ctx, w, x, y, M, n, k)
 
         for L, F in zip(self.layers, self.fmts):
-            d.rms_norm_f32_f32_f32g(ctx, X, XN, L["attn_norm"], c.eps, h, M)
-            for role, w, b, out, n in (("q", "wq", "bq", B["q"], qd), ("k", "wk", "bk", B["k"], kvd),
-                                       ("v", "wv", "bv", B["v"], kvd)):
-                gemm(F[role], L[w], XN, out, n, h)
-                d.add_bias_broadcast_f32(ctx, out, L[b], M, n)
-            d.rope_batch_inplace_f32(ctx, B["q"], hd, c.heads, start_pos, c.theta, M)
-            d.rope_batch_inplace_f32(ctx, B["k"], hd, c.kv_heads, start_pos, c.theta, M)
-            d.kv_write_batch_f32(ctx, B["k"], B["v"], L["kc"], L["vc"], start_pos, M, c.max_seq,
-                                 hd, c.kv_heads)
+            if form == "rows":
+                # Q/K/V (+ bias) of the normalised rows, one call per format
+                for fmt in dict.fromkeys((F["q"], F["k"], F["v"])):
+                    sel = lambda role, key: L[key] if F[role] == fmt else None
+                    d.qkv_bias_rows_f32(ctx, fmt, sel("q", "wq"), sel("k", "wk"), sel("v", "wv"), X,
+                                        B["q"] if F["q"] == fmt else None,
+                                        B["k"] if F["k"] == fmt else None,
+                                        B["v"] if F["v"] == fmt else None,
+                                        sel("q", "bq"), sel("k", "bk"), sel("v", "bv"), M, qd, kvd, h,
+                                        gamma=L["attn_norm"], eps=c.eps)
+                d.rope_kv_write_batch_f32(ctx, B["q"], B["k"], B["v"], L["kc"], L["vc"], hd, c.heads,
+                                          c.kv_heads, start_pos, c.theta, M, c.max_seq)
+            else:
+                d.rms_norm_f32_f32_f32g(ctx, X, XN, L["attn_norm"], c.eps, h, M)
+                for role, w, b, out, n in (("q", "wq", "bq", B["q"], qd), ("k", "wk", "bk", B["k"], kvd),
+                                           ("v", "wv", "bv", B["v"], kvd)):
+                    gemm(F[role], L[w], XN, out, n, h)
+                    d.add_bias_broadcast_f32(ctx, out, L[b], M, n)
+                d.rope_batch_inplace_f32(ctx, B["q"], hd, c.heads, start_pos, c.theta, M)
+                d.rope_batch_inplace_f32(ctx, B["k"], hd, c.kv_heads, start_pos, c.theta, M)
+                d.kv_write_batch_f32(ctx, B["k"], B["v"], L["kc"], L["vc"], start_pos, M, c.max_seq,
+                                     hd, c.kv_heads)
             d.flash_attention_f32(ctx, B["q"], L["kc"], L["vc"], B["att"], 1, M, start_pos + M,
                                   c.heads, c.kv_heads, hd, c.max_seq, q_start=start_pos)
-            gemm(F["o"], L["wo"], B["att"], B["p"], h, qd)
-            d.add_f32(ctx, X, B["p"], X, M * h)
-            d.rms_norm_f32_f32_f32g(ctx, X, XN, L["ffn_norm"], c.eps, h, M)
-            gemm(F["gate"], L["wg"], XN, B["g"], ff, h)
-            gemm(F["up"], L["wu"], XN, B["u"], ff, h)
-            d.silu_mul_f32(ctx, B["g"], B["u"], B["g"], M * ff)
-            gemm(F["down"], L["wd"], B["g"], B["p"], h, ff)
-            d.add_f32(ctx, X, B["p"], X, M * h)
-        d.rms_norm_f32_f32_f32g(ctx, X, XN, self.final_norm, c.eps, h, M)
-        gemm(self.lm_fmt, self.lm_head, XN, B["logits"], c.vocab, h)
+            if form == "rows":
+                d.gemv_rows_add_f32(ctx, F["o"], L["wo"], B["att"], X, X, M, h, qd)
+                if F["gate"] != F["up"]:
+                    raise ValueError(f"gate {F['gate']} / up {F['up']}: no fused gate+up+SiLU")
+                d.fused_ffn_rows_f32(ctx, F["gate"], L["wg"], L["wu"], X, B["g"], M, ff, h,
+                                     gamma=L["ffn_norm"], eps=c.eps)
+                d.gemv_rows_add_f32(ctx, F["down"], L["wd"], B["g"], X, X, M, h, ff)
+            else:
+                gemm(F["o"], L["wo"], B["att"], B["p"], h, qd)
+                d.add_f32(ctx, X, B["p"], X, M * h)
+                d.rms_norm_f32_f32_f32g(ctx, X, XN, L["ffn_norm"], c.eps, h, M)
+                gemm(F["gate"], L["wg"], XN, B["g"], ff, h)
+                gemm(F["up"], L["wu"], XN, B["u"], ff, h)
+                d.silu_mul_f32(ctx, B["g"], B["u"], B["g"], M * ff)
+                gemm(F["down"], L["wd"], B["g"], B["p"], h, ff)
+                d.add_f32(ctx, X, B["p"], X, M * h)
+        if form == "rows":
+            d.gemv_rows_f32(ctx, self.lm_fmt, self.lm_head, X, B["logits"], M, c.vocab, h,
+                            gamma=self.final_norm, eps=c.eps)
+        else:
+            d.rms_norm_f32_f32_f32g(ctx, X, XN, self.final_norm, c.eps, h, M)
+            gemm(self.lm_fmt, self.lm_head, XN, B["logits"], c.vocab, h)
         d.argmax_rows_first_f32(ctx, B["logits"], B["idx"], M, c.vocab)
         return B
 

@@ -63,6 +63,7 @@ _lib = None
 
 # (name, argtypes) for every exported symbol; restype is c_int unless noted.
 _P, _U32, _U64, _F = c_void_p, c_uint32, c_uint64, c_float
+_ROWS_FMTS = ("q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg")
 _SIGS = {
     "rt_ctx_create": [POINTER(c_void_p), c_char_p],
     "rt_flush": [_P],
@@ -130,9 +131,16 @@ _SIGS = {
         "q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg", "f16", "f32")},
     **{f"rt_embed_rows_{_f}_f32": [_P, _P, _P, _P, _U32, _U32] for _f in (
         "q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg", "f16", "f32")},
+    **{f"rt_gemv_rows_{_f}_f32": [_P, _P, _P, _P, _F, _P, _U32, _U32, _U32] for _f in _ROWS_FMTS},
+    **{f"rt_gemv_rows_{_f}_add_f32": [_P, _P, _P, _P, _P, _U32, _U32, _U32] for _f in _ROWS_FMTS},
+    **{f"rt_qkv_bias_rows_{_f}_f32": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 + [_U32] * 4
+       for _f in _ROWS_FMTS},
+    **{f"rt_fused_ffn_rows_{_f}_f32": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32, _U32]
+       for _f in _ROWS_FMTS},
     "rt_add_bias_broadcast_f32": [_P, _P, _P, _U32, _U32],
     "rt_rope_batch_inplace_f32": [_P, _P, _U32, _U32, _U32, _F, _U32],
     "rt_kv_write_batch_f32": [_P] + [_P] * 4 + [_U32] * 5,
+    "rt_rope_kv_write_batch_f32": [_P] + [_P] * 5 + [_U32] * 4 + [_F, _U32, _U32],
     "rt_flash_attention_f32": [_P] + [_P] * 4 + [_U32] * 8,
     "rt_add_f32": [_P, _P, _P, _P, _U32],
     "rt_silu_mul_f32": [_P, _P, _P, _P, _U32],
@@ -694,6 +702,33 @@ def embed_rows_f32(ctx, fmt: str, table, tokens, out, k, rows):
     _call(ctx, f"rt_embed_rows_{fmt}_f32", _ptr(table), _ptr(tokens), _ptr(out), k, rows)
 
 
+# ──────────────────── multi-row GEMVs (verify / prefill) ────────────────────
+
+def gemv_rows_f32(ctx, fmt, w, x, y, rows, n, k, gamma=None, eps=0.0):
+    """y[rows][n] = (RMSNorm(x)·γ if gamma) · Wᵀ, weights read once per 8 rows (new)."""
+    _call(ctx, f"rt_gemv_rows_{fmt}_f32", _ptr(w), _ptr(x), _ptr(gamma) if gamma else None, eps,
+          _ptr(y), rows, n, k)
+
+
+def gemv_rows_add_f32(ctx, fmt, w, x, res, y, rows, n, k):
+    """y = res + x·Wᵀ for rows activation rows (new)."""
+    _call(ctx, f"rt_gemv_rows_{fmt}_add_f32", _ptr(w), _ptr(x), _ptr(res), _ptr(y), rows, n, k)
+
+
+def qkv_bias_rows_f32(ctx, fmt, wq, wk, wv, x, q, k_out, v, bq, bk, bv, rows, q_dim, kv_dim, k,
+                      gamma=None, eps=0.0):
+    """Q/K/V (+ f16 bias) of rows activation rows; a None weight skips its matrix (new)."""
+    p = lambda b: _ptr(b) if b is not None else None
+    _call(ctx, f"rt_qkv_bias_rows_{fmt}_f32", p(wq), p(wk), p(wv), _ptr(x), p(gamma), eps,
+          p(q), p(k_out), p(v), p(bq), p(bk), p(bv), rows, q_dim, kv_dim, k)
+
+
+def fused_ffn_rows_f32(ctx, fmt, wg, wu, x, act, rows, ff, k, gamma=None, eps=0.0):
+    """act = silu(x̂·W_gᵀ)·(x̂·W_uᵀ) for rows activation rows (new)."""
+    _call(ctx, f"rt_fused_ffn_rows_{fmt}_f32", _ptr(wg), _ptr(wu), _ptr(x),
+          _ptr(gamma) if gamma is not None else None, eps, _ptr(act), rows, ff, k)
+
+
 # ──────────────────── batched verify / prefill glue ────────────────────
 
 def add_bias_broadcast_f32(ctx, x, bias, seq, dim):
@@ -711,6 +746,13 @@ def kv_write_batch_f32(ctx, k, v, k_cache, v_cache, start_pos, seq, max_seq, hea
     """KvCache::write_at (kv_cache.rs:132-150) for seq consecutive positions."""
     _call(ctx, "rt_kv_write_batch_f32", *map(_ptr, (k, v, k_cache, v_cache)), start_pos, seq,
           max_seq, head_dim, num_kv_heads)
+
+
+def rope_kv_write_batch_f32(ctx, q, k, v, k_cache, v_cache, head_dim, num_heads, num_kv_heads,
+                            start_pos, theta, seq, max_seq):
+    """Batched RoPE of q and k + KV-cache write of k and v in one launch (new)."""
+    _call(ctx, "rt_rope_kv_write_batch_f32", *map(_ptr, (q, k, v, k_cache, v_cache)), head_dim,
+          num_heads, num_kv_heads, start_pos, theta, seq, max_seq)
 
 
 def flash_attention_f32(ctx, q, k, v, out, batch, q_len, kv_len, num_heads, num_kv_heads,

@@ -139,12 +139,13 @@ def check_rows(got, ref, what):
         assert err <= tol, (what, r, err, tol)
 
 
+@pytest.mark.parametrize("form", ["rows", "gemm"])
 @pytest.mark.parametrize("quant,cfg_kw,start", [
     (None, dict(layers=2, max_seq=600), 500),
     (Q4K_M, dict(layers=2, hidden=512, heads=4, kv_heads=2, head_dim=128, ff=1024, vocab=1000,
                  max_seq=300), 130),
 ])
-def test_verify_forward_equals_sequential_steps(ctx, quant, cfg_kw, start):
+def test_verify_forward_equals_sequential_steps(ctx, quant, cfg_kw, start, form):
     """Each row of the batched pass equals the single-token step of the CPU
     reference model at its position (the host twin regenerated from the
     seeds, stepped once per row: its cache grows exactly as the batch's)."""
@@ -153,7 +154,7 @@ def test_verify_forward_equals_sequential_steps(ctx, quant, cfg_kw, start):
     host = ora.HostStepModel.from_recipe(m)
     toks = [11, 999 % cfg.vocab, 4242 % cfg.vocab, 7, 123 % cfg.vocab, 5]
     M = len(toks)
-    B = m.verify_forward(toks, start)
+    B = m.verify_forward(toks, start, form)
     ctx.flush()
     got = m.read(B["logits"], M * cfg.vocab).reshape(M, cfg.vocab).astype(np.float64)
     idx = np.zeros(M, np.uint32)
@@ -212,3 +213,76 @@ def test_verify_draft_accepts_greedy_continuation(ctx):
     wrong[2] = (wrong[2] + 1) % cfg.vocab
     assert m.verify_draft(prompt, wrong, start) == (2, seq[2])
     m.free()
+
+
+# ───────────────────────── multi-row GEMVs ─────────────────────────
+
+from gpu_helpers import check_close, device_weights  # noqa: E402
+from test_gpu_fused import ffn_check  # noqa: E402
+
+ROWS_FMTS = ["q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg"]
+
+
+@pytest.mark.parametrize("fmt", ROWS_FMTS)
+@pytest.mark.parametrize("rows,n,k", [(1, 300, 512), (5, 896, 896), (8, 130, 3584),
+                                      (13, 70, 1024), (3, 64, 18944)])
+def test_gemv_rows_plain_and_residual(ctx, fmt, rows, n, k):
+    """y = x·Wᵀ and y = res + x·Wᵀ for rows activation rows: every output
+    within the GEMV bound of the per-row oracle (13 rows: two launches; k =
+    18944: K split over workgroups)."""
+    if fmt in ("q4k", "q6k", "q5k", "q4kg", "q5kg", "q6kg") and k % 256:
+        k = 1024
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=rows + n)
+    x = np.random.default_rng(rows).standard_normal((rows, k)).astype(np.float32)
+    res = np.random.default_rng(rows + 1).standard_normal((rows, n)).astype(np.float32)
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    bx = ctx.buffer_from(x)
+    y = ctx.new_buffer(4 * rows * n)
+    d.gemv_rows_f32(ctx, fmt, wbuf, bx, y, rows, n, k)
+    ctx.flush()
+    check_close(y.read(np.float32, rows * n), yref.ravel(), sabs.ravel(), f"rows {fmt}")
+    br = ctx.buffer_from(res)
+    d.gemv_rows_add_f32(ctx, fmt, wbuf, bx, br, br, rows, n, k)  # in place
+    ctx.flush()
+    check_close(br.read(np.float32, rows * n), (yref + res).ravel(), sabs.ravel(),
+                f"rows add {fmt}", extra=2 ** -24 * np.abs(res).ravel() * 2)
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4k", "q6k", "q4kg", "q6kg", "q4_0"])
+@pytest.mark.parametrize("rows", [4, 8, 11])
+def test_qkv_bias_and_ffn_rows_with_norm(ctx, fmt, rows):
+    """Q/K/V (+ bias) and gate+up+SiLU of rows RMS-normalised activation
+    rows (0.5B head layout; K-quants at hidden 1024) against the oracle's
+    rms_norm + GEMVs; the Q/K/V call with V skipped leaves V untouched."""
+    h = 896 if fmt in ("q8_0", "q4_0") else 1024
+    qd, kvd, ff = h, 128, 2 * h
+    rng = np.random.default_rng(rows + 7)
+    x = rng.standard_normal((rows, h)).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(h)).astype(np.float32)
+    eps = 1e-6
+    xn = np.stack([ora.rms_norm(x[r], g, eps) for r in range(rows)]).astype(np.float32)
+    ws = [device_weights(ctx, fmt, n_, h, seed=s) for n_, s in ((qd, 1), (kvd, 2), (kvd, 3))]
+    bias = [rng.standard_normal(n_).astype(np.float16) * 0.1 for n_ in (qd, kvd, kvd)]
+    outs = [ctx.new_buffer(4 * rows * n_) for n_ in (qd, kvd, kvd)]
+    outs[2].write(np.full(rows * kvd, 7.0, np.float32))
+    bx, bg = ctx.buffer_from(x), ctx.buffer_from(g)
+    bb = [ctx.buffer_from(b) for b in bias]
+    d.qkv_bias_rows_f32(ctx, fmt, ws[0][0], ws[1][0], None, bx, outs[0], outs[1], None,
+                        bb[0], bb[1], None, rows, qd, kvd, h, gamma=bg, eps=eps)
+    ctx.flush()
+    for i, n_ in enumerate((qd, kvd)):
+        yref, sabs = ora.gemv(fmt, ws[i][1], xn, n_, h)
+        check_close(outs[i].read(np.float32, rows * n_),
+                    (yref + bias[i].astype(np.float64)).ravel(), sabs.ravel(),
+                    f"qkv rows {fmt} mat {i}")
+    assert np.all(outs[2].read(np.float32, rows * kvd) == 7.0)
+    wg, rg = device_weights(ctx, fmt, ff, h, seed=11)
+    wu, ru = device_weights(ctx, fmt, ff, h, seed=12)
+    act = ctx.new_buffer(4 * rows * ff)
+    d.fused_ffn_rows_f32(ctx, fmt, wg, wu, bx, act, rows, ff, h, gamma=bg, eps=eps)
+    ctx.flush()
+    got = act.read(np.float32, rows * ff).reshape(rows, ff)
+    for r in range(rows):
+        g_ref, g_s = ora.gemv(fmt, rg, xn[r], ff, h)
+        u_ref, u_s = ora.gemv(fmt, ru, xn[r], ff, h)
+        ffn_check(got[r], g_ref, g_s, u_ref, u_s, f"ffn rows {fmt} r={r}")
