@@ -460,15 +460,7 @@ class DecodeModel:
             getattr(d, f"gemv_{F['down']}_add_f32_f32in")(ctx, L["wd"], self.act, self.x,
                                                           self.x, h, c.ff)
             n += 1
-        if self.lm_fmt in ("q8_0", "q6k"):
-            getattr(d, f"rms_norm_gemv_{self.lm_fmt}_f32in_f32out")(
-                ctx, self.lm_head, self.x, self.final_norm, c.eps, self.logits, c.vocab, h)
-            n += 1
-        else:
-            d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, self.final_norm, c.eps, h, 1)
-            getattr(d, f"gemv_{self.lm_fmt}_f32in_f32out")(ctx, self.lm_head, self.xn,
-                                                           self.logits, c.vocab, h)
-            n += 2
+        n += self._lm_head(self.x)
         d.argmax_f32(ctx, self.logits, self.token, c.vocab)
         self._launches = n + 1
         return n + 1
@@ -505,20 +497,26 @@ class DecodeModel:
 
     # ───────────────────────── batched verify ─────────────────────────
 
-    def _verify_arena(self, rows: int) -> dict:
-        """Activation buffers of an M-row verify pass, [rows][dim] f32,
-        allocated once per largest M seen."""
+    def _verify_arena(self, rows: int, logits: bool = True) -> dict:
+        """Activation buffers of an M-row pass, [rows][dim] f32, allocated
+        once per largest M seen (with the [rows][vocab] logits only when a
+        caller needs every row's logits: not for prefill)."""
         v = getattr(self, "_vbufs", None)
-        if v is not None and v["rows"] >= rows:
+        if v is not None and v["rows"] >= rows and (v["has_logits"] or not logits):
             return v
         if v is not None:
+            logits = logits or v["has_logits"]
+            rows = max(rows, v["rows"])
             v["arena"].buf.free()
         c = self.cfg
         dims = dict(x=c.hidden, xn=c.hidden, q=c.q_dim, k=c.kv_dim, v=c.kv_dim, att=c.q_dim,
-                    p=c.hidden, g=c.ff, u=c.ff, logits=c.vocab)
+                    p=c.hidden, g=c.ff, u=c.ff)
+        if logits:
+            dims["logits"] = c.vocab
         a = Arena(self.ctx, sum(((4 * rows * n + 255) & ~255) for n in dims.values()) + 2 * 1024)
         v = {k: a.take(4 * rows * n) for k, n in dims.items()}
-        v.update(tok=a.take(4 * rows), idx=a.take(4 * rows), rows=rows, arena=a)
+        v.update(tok=a.take(4 * rows), idx=a.take(4 * rows), rows=rows, arena=a,
+                 has_logits=logits)
         self._vbufs = v
         return v
 
@@ -556,14 +554,15 @@ class DecodeModel:
     VERIFY_ROWS_MAX = 16
     VERIFY_ROWS_MAX_HIDDEN = 1024
 
-    def verify_pass(self, M: int, start_pos: int, form: str | None = None) -> dict:
+    def verify_pass(self, M: int, start_pos: int, form: str | None = None,
+                    last_only: bool = False) -> dict:
         """The launches of verify_forward for the M token ids already in the
         verify buffers (``tok``): no host transfer, so it can be captured.
         form: "rows" (multi-row GEMVs) or "gemm" (batched GEMMs + separate
         norm / bias / SiLU / residual kernels, the reference's sequence);
         default by M."""
         ctx, c = self.ctx, self.cfg
-        B = self._verify_arena(M)
+        B = self._verify_arena(M, logits=not last_only)
         h, qd, kvd, hd, ff = c.hidden, c.q_dim, c.kv_dim, c.head_dim, c.ff
         X, XN = B["x"], B["xn"]
         form = form or ("rows" if M <= self.VERIFY_ROWS_MAX and h <= self.VERIFY_ROWS_MAX_HIDDEN
@@ -616,14 +615,56 @@ class DecodeModel:
                 d.silu_mul_f32(ctx, B["g"], B["u"], B["g"], M * ff)
                 gemm(F["down"], L["wd"], B["g"], B["p"], h, ff)
                 d.add_f32(ctx, X, B["p"], X, M * h)
-        if form == "rows":
+        if last_only:
+            # prefill: the final norm and the LM head on the last row only, into
+            # the decode buffers (logits, token = its argmax) so that decoding
+            # continues at position start_pos + M
+            self._lm_head(X + 4 * (M - 1) * h)
+            d.argmax_f32(ctx, self.logits, self.token, c.vocab)
+        elif form == "rows":
             d.gemv_rows_f32(ctx, self.lm_fmt, self.lm_head, X, B["logits"], M, c.vocab, h,
                             gamma=self.final_norm, eps=c.eps)
         else:
             d.rms_norm_f32_f32_f32g(ctx, X, XN, self.final_norm, c.eps, h, M)
             gemm(self.lm_fmt, self.lm_head, XN, B["logits"], c.vocab, h)
-        d.argmax_rows_first_f32(ctx, B["logits"], B["idx"], M, c.vocab)
+        if not last_only:
+            d.argmax_rows_first_f32(ctx, B["logits"], B["idx"], M, c.vocab)
         return B
+
+    def _lm_head(self, x) -> int:
+        """Final RMSNorm + LM head of one hidden row x into self.logits (the
+        norm fused into the GEMV's staging for Q8_0 / Q6_K heads); returns the
+        number of launches."""
+        c, ctx = self.cfg, self.ctx
+        if self.lm_fmt in ("q8_0", "q6k"):
+            getattr(d, f"rms_norm_gemv_{self.lm_fmt}_f32in_f32out")(
+                ctx, self.lm_head, x, self.final_norm, c.eps, self.logits, c.vocab, c.hidden)
+            return 1
+        d.rms_norm_f32_f32_f32g(ctx, x, self.xn, self.final_norm, c.eps, c.hidden, 1)
+        getattr(d, f"gemv_{self.lm_fmt}_f32in_f32out")(ctx, self.lm_head, self.xn, self.logits,
+                                                       c.vocab, c.hidden)
+        return 2
+
+    def prefill(self, tokens) -> np.ndarray:
+        """prefill.rs:29-257: the whole prompt in one batched pass from
+        position 0 (every KV position written, causal attention), then the
+        final norm and the LM head on the last token only.  Returns that
+        token's logits; the greedy next token is left in the decode token
+        buffer, so step_fused(len(tokens)) continues the sequence."""
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        if toks.size == 0:
+            raise ValueError("prefill: empty prompt")
+        if np.any(toks >= self.cfg.vocab):
+            raise ValueError("prefill: token id out of range")
+        M = int(toks.size)
+        if M > self.cfg.max_seq:
+            raise ValueError(f"prefill: {M} tokens exceed the KV cache ({self.cfg.max_seq})")
+        B = self._verify_arena(M, logits=False)
+        self.ctx._check(d.load_library().rt_upload(self.ctx.handle, B["tok"], toks.ctypes.data,
+                                                   toks.nbytes))
+        self.verify_pass(M, 0, last_only=True)
+        self.ctx.flush()
+        return self.read(self.logits, self.cfg.vocab)
 
     def verify_draft(self, prompt_token: int, draft_tokens, start_pos: int):
         """forward.rs:2118-2309: run [prompt_token, *draft_tokens] at

@@ -268,6 +268,8 @@ def _ptr(b) -> int | None:
         return None
     if isinstance(b, Buffer):
         return b.ptr
+    if isinstance(b, bool) or not isinstance(b, (int, np.integer)):
+        raise TypeError(f"device pointer expected, got {type(b).__name__}")
     return int(b)
 
 

@@ -286,3 +286,34 @@ def test_qkv_bias_and_ffn_rows_with_norm(ctx, fmt, rows):
         g_ref, g_s = ora.gemv(fmt, rg, xn[r], ff, h)
         u_ref, u_s = ora.gemv(fmt, ru, xn[r], ff, h)
         ffn_check(got[r], g_ref, g_s, u_ref, u_s, f"ffn rows {fmt} r={r}")
+
+
+@pytest.mark.parametrize("quant,cfg_kw,M", [
+    (None, dict(layers=2, max_seq=600), 5),
+    (None, dict(layers=2, max_seq=600), 40),
+    (Q4K_M, dict(layers=2, hidden=512, heads=4, kv_heads=2, head_dim=128, ff=1024, vocab=1000,
+                 max_seq=300), 24),
+])
+def test_prefill_equals_sequential_steps(ctx, quant, cfg_kw, M):
+    """prefill.rs:29-257: the prompt's last logits equal the CPU reference
+    model's after stepping the prompt token by token from position 0, and
+    decoding continues from the prefilled cache: the next fused step equals
+    the reference's next step."""
+    cfg = DecodeConfig(**cfg_kw)
+    m = DecodeModel(ctx, cfg, seed=23, quant=quant)
+    host = ora.HostStepModel.from_recipe(m)
+    toks = [(37 * i + 11) % cfg.vocab for i in range(M)]
+    got = m.prefill(toks).astype(np.float64)
+    ref = None
+    for pos, t in enumerate(toks):
+        htok, ref = host.step(t, pos, threads=8)
+    check_rows(got[None], ref.astype(np.float64)[None], "prefill last logits")
+    tok = m.get_token()
+    assert tok == ora.argmax(got.astype(np.float32)) or \
+        ref[int(np.argmax(ref))] - ref[tok] <= 2e-3 * (ref.max() - ref.min())
+    m.step_fused(M)
+    ctx.flush()
+    _, ref2 = host.step(tok, M, threads=8)
+    check_rows(m.read(m.logits, cfg.vocab).astype(np.float64)[None], ref2.astype(np.float64)[None],
+               "decode after prefill")
+    m.free()

@@ -4,6 +4,7 @@ import os
 import subprocess
 import sys
 
+import numpy as np
 import pytest
 
 from runit_mac_amd import dispatch as d
@@ -48,3 +49,13 @@ def test_accept_drafts_follows_verify_draft():
     assert accept_drafts([4, 2, 3, 9], [1, 2, 3]) == (0, 4)
     with pytest.raises(ValueError):
         accept_drafts([1, 2], [1, 2])
+
+
+def test_device_pointer_arguments_reject_non_integers():
+    """A bool (or any non-integer) passed where a device pointer is expected
+    is an error on the host, not address 1 on the device."""
+    from runit_mac_amd.dispatch import _ptr
+    assert _ptr(None) is None and _ptr(4096) == 4096 and _ptr(np.uint64(64)) == 64
+    for bad in (True, False, 1.0, "0x10"):
+        with pytest.raises(TypeError):
+            _ptr(bad)
