@@ -303,6 +303,28 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
         e1.record()
         verify[(M, form)] = e0.elapsed_ms(e1) / steps
         del g
+    # prefill of a 512-token prompt (prefill.rs): one batched pass from
+    # position 0 on the batched GEMMs, the LM head on the last row
+    P = 512
+    m._verify_arena(P, logits=False)
+    toks = np.arange(P, dtype=np.uint32) % cfg.vocab
+    ctx._check(d.load_library().rt_upload(ctx.handle, m._vbufs["tok"], toks.ctypes.data,
+                                          toks.nbytes))
+    m.verify_pass(P, 0, last_only=True)
+    ctx.flush()
+    ctx.capture_begin()
+    m.verify_pass(P, 0, last_only=True)
+    g = ctx.capture_end()
+    g.launch()
+    ctx.flush()
+    e0, e1 = ctx.event(), ctx.event()
+    reps = max(3, steps // 10)
+    e0.record()
+    for _ in range(reps):
+        g.launch()
+    e1.record()
+    prefill_ms = e0.elapsed_ms(e1) / reps
+    del g
     # dominant kernel of the fused step: the norm-fused gate+up+SiLU GEMV,
     # 24 launches per token.  Timed live over the model's own 24 layers.
     ctx.capture_begin()
@@ -326,7 +348,8 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
             "ms_persistent": res["persistent"], "ms_fused": res["fused"], "ms_reference": res["reference_sequence"],
             "step_bytes": cfg.step_bytes(pos + 1), "ffn_us": ffn_us, "ffn_bytes": ffn_bytes,
             "launches_fused": m.launches_fused(),
-            "launches_reference": 1 + 10 * cfg.layers + 3, "verify_ms": verify}
+            "launches_reference": 1 + 10 * cfg.layers + 3, "verify_ms": verify,
+            "prefill_ms": prefill_ms, "prefill_tokens": P}
 
 
 def bench_q4km_decode(ctx, steps: int, warmup: int) -> dict:
@@ -563,6 +586,8 @@ def main():
         for (M, form), vms in dec["verify_ms"].items():
             log(f"verify pass ({form}), {M} tokens at kv 512..{512 + M - 1}: {vms * 1e3:.1f} us "
                 f"({vms * 1e3 / M:.1f} us per token; {M} fused decode steps: {M * ms * 1e3:.1f} us)")
+        log(f"prefill of {dec['prefill_tokens']} tokens: {dec['prefill_ms']:.2f} ms = "
+            f"{dec['prefill_tokens'] / dec['prefill_ms'] * 1e3:.0f} tok/s")
         log(f"dominant kernel rms_norm+fused_ffn_q8_0 4864x896x2: {dec['ffn_us']:.2f} us, "
             f"{ffn_gbs:.0f} GB/s")
         line.update({
@@ -584,6 +609,8 @@ def main():
                        "step_bytes": dec["step_bytes"],
                        "effective_gbs": round(dec["step_bytes"] / (ms * 1e-3) / 1e9, 1),
                        "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / dec["step_bytes"], 0)},
+            "prefill": {"tokens": dec["prefill_tokens"], "ms": round(dec["prefill_ms"], 3),
+                        "tok_s": round(dec["prefill_tokens"] / dec["prefill_ms"] * 1e3, 1)},
             "verify": {f"{form}_m{M}": {"us": round(v * 1e3, 1), "us_per_token": round(v * 1e3 / M, 1)}
                        for (M, form), v in dec["verify_ms"].items()},
         })

@@ -505,7 +505,6 @@ class DecodeModel:
         if v is not None and v["rows"] >= rows and (v["has_logits"] or not logits):
             return v
         if v is not None:
-            logits = logits or v["has_logits"]
             rows = max(rows, v["rows"])
             v["arena"].buf.free()
         c = self.cfg
@@ -513,10 +512,10 @@ class DecodeModel:
                     p=c.hidden, g=c.ff, u=c.ff)
         if logits:
             dims["logits"] = c.vocab
-        a = Arena(self.ctx, sum(((4 * rows * n + 255) & ~255) for n in dims.values()) + 2 * 1024)
+        dims.update(tok=1, idx=1)
+        a = Arena(self.ctx, sum(((4 * rows * n + 255) & ~255) for n in dims.values()))
         v = {k: a.take(4 * rows * n) for k, n in dims.items()}
-        v.update(tok=a.take(4 * rows), idx=a.take(4 * rows), rows=rows, arena=a,
-                 has_logits=logits)
+        v.update(rows=rows, arena=a, has_logits=logits)
         self._vbufs = v
         return v
 
