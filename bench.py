@@ -238,7 +238,30 @@ def cpu_baseline(model, token: int, pos: int, gpu_token: int, seconds: float = 1
                        f"{cores} threads")}
 
 
-def bench_decode(ctx, steps: int, warmup: int) -> dict:
+def _bench_prefill(ctx, m, cfg, P: int, steps: int) -> float:
+    """Milliseconds of one captured prefill of a P-token prompt."""
+    m._verify_arena(P, logits=False)
+    toks = np.arange(P, dtype=np.uint32) % cfg.vocab
+    ctx._check(d.load_library().rt_upload(ctx.handle, m._vbufs["tok"], toks.ctypes.data,
+                                          toks.nbytes))
+    m.verify_pass(P, 0, last_only=True)
+    ctx.flush()
+    ctx.capture_begin()
+    m.verify_pass(P, 0, last_only=True)
+    g = ctx.capture_end()
+    g.launch()
+    ctx.flush()
+    e0, e1 = ctx.event(), ctx.event()
+    reps = max(3, steps // 10)
+    e0.record()
+    for _ in range(reps):
+        g.launch()
+    e1.record()
+    del g
+    return e0.elapsed_ms(e1) / reps
+
+
+def bench_decode(ctx, steps: int, warmup: int, verify_forms: bool = True) -> dict:
     """Config 2: one greedy decode step of the 0.5B Q8_0 shape at kv_len 512,
     captured as one HIP graph and replayed (one replay = one token)."""
     from runit_mac_amd.decode import DecodeConfig, DecodeModel
@@ -287,7 +310,7 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
     # the batched GEMMs, causal attention over the cache + the M new rows),
     # captured as one graph; the cache is restored between replays
     verify = {}
-    for M, form in ((4, "rows"), (8, "rows"), (16, "rows"), (16, "gemm"), (32, "gemm")):
+    for M, form in ((4, "rows"), (8, "rows"), (16, "rows"), (16, "gemm"), (32, "gemm")) if verify_forms else ():
         m.verify_forward([1] * M, pos, form)  # uploads the ids, sizes the buffers
         ctx.flush()
         ctx.capture_begin()
@@ -306,25 +329,9 @@ def bench_decode(ctx, steps: int, warmup: int) -> dict:
     # prefill of a 512-token prompt (prefill.rs): one batched pass from
     # position 0 on the batched GEMMs, the LM head on the last row
     P = 512
-    m._verify_arena(P, logits=False)
-    toks = np.arange(P, dtype=np.uint32) % cfg.vocab
-    ctx._check(d.load_library().rt_upload(ctx.handle, m._vbufs["tok"], toks.ctypes.data,
-                                          toks.nbytes))
-    m.verify_pass(P, 0, last_only=True)
-    ctx.flush()
-    ctx.capture_begin()
-    m.verify_pass(P, 0, last_only=True)
-    g = ctx.capture_end()
-    g.launch()
-    ctx.flush()
-    e0, e1 = ctx.event(), ctx.event()
-    reps = max(3, steps // 10)
-    e0.record()
-    for _ in range(reps):
-        g.launch()
-    e1.record()
-    prefill_ms = e0.elapsed_ms(e1) / reps
-    del g
+    prefill_ms = float("nan")
+    if verify_forms:
+        prefill_ms = _bench_prefill(ctx, m, cfg, P, steps)
     # dominant kernel of the fused step: the norm-fused gate+up+SiLU GEMV,
     # 24 launches per token.  Timed live over the model's own 24 layers.
     ctx.capture_begin()
@@ -550,6 +557,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--suite", default="all", choices=["all", "gemv", "quick", "decode", "step", "q4decode"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-verify", action="store_true",
+                    help="skip the verify / prefill graphs (rocprofv3 --kernel-trace runs)")
     ap.add_argument("--only", default=None, help="run only GEMV workloads whose label contains this")
     ap.add_argument("--profile-pass", action="store_true",
                     help="eager launches of the dominant kernel + a calibration copy, for "
@@ -572,7 +581,7 @@ def main():
     }
     dec = None
     if args.suite in ("all", "decode") and not args.only:
-        dec = bench_decode(ctx, args.steps, args.warmup)
+        dec = bench_decode(ctx, args.steps, args.warmup, verify_forms=not args.no_verify)
         cfg = dec["cfg"]
         ms = dec["ms_fused"]
         tok_s = 1e3 / ms
@@ -586,8 +595,9 @@ def main():
         for (M, form), vms in dec["verify_ms"].items():
             log(f"verify pass ({form}), {M} tokens at kv 512..{512 + M - 1}: {vms * 1e3:.1f} us "
                 f"({vms * 1e3 / M:.1f} us per token; {M} fused decode steps: {M * ms * 1e3:.1f} us)")
-        log(f"prefill of {dec['prefill_tokens']} tokens: {dec['prefill_ms']:.2f} ms = "
-            f"{dec['prefill_tokens'] / dec['prefill_ms'] * 1e3:.0f} tok/s")
+        if dec["verify_ms"]:
+            log(f"prefill of {dec['prefill_tokens']} tokens: {dec['prefill_ms']:.2f} ms = "
+                f"{dec['prefill_tokens'] / dec['prefill_ms'] * 1e3:.0f} tok/s")
         log(f"dominant kernel rms_norm+fused_ffn_q8_0 4864x896x2: {dec['ffn_us']:.2f} us, "
             f"{ffn_gbs:.0f} GB/s")
         line.update({
@@ -609,8 +619,9 @@ def main():
                        "step_bytes": dec["step_bytes"],
                        "effective_gbs": round(dec["step_bytes"] / (ms * 1e-3) / 1e9, 1),
                        "roofline_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / dec["step_bytes"], 0)},
-            "prefill": {"tokens": dec["prefill_tokens"], "ms": round(dec["prefill_ms"], 3),
-                        "tok_s": round(dec["prefill_tokens"] / dec["prefill_ms"] * 1e3, 1)},
+            "prefill": ({"tokens": dec["prefill_tokens"], "ms": round(dec["prefill_ms"], 3),
+                         "tok_s": round(dec["prefill_tokens"] / dec["prefill_ms"] * 1e3, 1)}
+                        if dec["verify_ms"] else None),
             "verify": {f"{form}_m{M}": {"us": round(v * 1e3, 1), "us_per_token": round(v * 1e3 / M, 1)}
                        for (M, form), v in dec["verify_ms"].items()},
         })
