@@ -61,8 +61,9 @@ typedef struct rt_ctx rt_ctx;
 /* ───────────────────────── context / runtime ───────────────────────── */
 
 /* MetalContext::new() (context.rs:163-205): selects device 0, loads the
- * gfx950 code object at `code_object_path` (NULL → runit_kernels.hsaco next
- * to this library), resolves every kernel, creates one stream. */
+ * gfx950 code objects at `code_object_path` (one .hsaco file or a directory of
+ * them; NULL → the lib/kernels/ directory next to this library), resolves
+ * every kernel, creates one stream. */
 int rt_ctx_create(rt_ctx** out, const char* code_object_path);
 /* Drop for MetalContext (context.rs:299-304): flushes, then releases. */
 void rt_ctx_destroy(rt_ctx* ctx);

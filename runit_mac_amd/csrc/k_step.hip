@@ -17,8 +17,8 @@
 //
 // Phases are described by an array of StepPhase records built by the host
 // (runtime.cpp, rt_decode_step_*): the GEMV phases run the matrix-core body
-// of k_gemv.hip (gemv_mq_body) and attention runs attn_split of
-// k_decode.hip, with device-scope activation loads and stores (every
+// of rt_gemv.h (gemv_mq_body) and attention runs attn_split of
+// rt_attn.h, with device-scope activation loads and stores (every
 // activation is produced and consumed by different workgroups of the same
 // launch; no cache may return a stale copy, and no cache-wide write-back or
 // invalidate is needed).

@@ -1,6 +1,6 @@
 // runtime.cpp — host side of the C ABI declared in include/runit_hip.h.
 //
-// The context loads one prebuilt gfx950 code object (runit_kernels.hsaco)
+// The context loads the prebuilt gfx950 code objects (lib/kernels/*.hsaco)
 // with hipModuleLoad, resolves every kernel up front (the reference builds
 // every pipeline state at MetalContext::new, context.rs:163-205), owns one
 // HIP stream, and launches with hipModuleLaunchKernel.  Kernel entry points
@@ -24,7 +24,7 @@
 
 namespace {
 
-// Mirrors the kernel-side GemvArgs (k_gemv.hip); passed by value.
+// Mirrors the kernel-side GemvArgs (rt_gemv.h); passed by value.
 struct GemvArgs {
     const uint8_t* w[3];
     void* out[3];
@@ -447,12 +447,12 @@ bool has_ls_kernel(const rt_ctx* c, const char* kname) {
     return c->fns.count(std::string(kname) + "_ls1") != 0;
 }
 
-// LDS-streamed matrix-core launch (k_gemv_ls.hip).  Items are row quads of
+// LDS-streamed matrix-core launch (rt_gemv_ls.h).  Items are row quads of
 // one K chunk; a chunk's rows are read with NI ≤ 3 coalesced 1 KB loads
 // each, so rows longer than 3 KB (or K beyond one staging pass) are split
 // into S chunks whose partial sums meet in the workspace.  Returns 1 when the
 // shape does not suit the body (kLsDecline: the caller takes the other bodies).
-// Workgroup-local K split (k_gemv_ls.hip, *_lsk1): every K chunk of a row
+// Workgroup-local K split (rt_gemv_ls.h, *_lsk1): every K chunk of a row
 // quad in one workgroup, 1 KB row chunks, the whole K's activation records in
 // LDS; the chunks' partial sums meet in LDS.
 int gemv_launch_lsk(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {

@@ -1,4 +1,4 @@
-"""GPU parity of the LDS-streamed GEMV body (k_gemv_ls.hip) against the CPU
+"""GPU parity of the LDS-streamed GEMV body (rt_gemv_ls.h) against the CPU
 oracle, through the C ABI.
 
 The library takes that body only for launches with at least 16 items (row
