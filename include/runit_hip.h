@@ -579,6 +579,23 @@ int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* ctx, const float* q_raw, con
                                             uint32_t max_seq, uint32_t num_heads,
                                             uint32_t num_kv_heads, uint32_t head_dim, float theta,
                                             uint32_t hidden);
+/* The same for Q4_K output projections (reference layout; the 7B Q4_K_M
+ * models' attn_output), whose merging form stages q_dim ≤ 4096 in one round
+ * of up to 1024 threads; w_o: [hidden, q_dim] Q4_K.  New: the reference runs
+ * decode_attention_f32 then the Q4_K GEMV (forward.rs:1588-1619). */
+int rt_decode_attention_rope_oproj_q4k_f32(rt_ctx* ctx, const float* q_raw, const float* k_raw,
+                                           const float* v_raw, float* k_cache, float* v_cache,
+                                           const void* w_o, float* x_io, uint32_t pos,
+                                           uint32_t max_seq, uint32_t num_heads,
+                                           uint32_t num_kv_heads, uint32_t head_dim, float theta,
+                                           uint32_t hidden);
+/* The same for ggml-layout Q4_K output projections (upstream GGUF files). New. */
+int rt_decode_attention_rope_oproj_q4kg_f32(rt_ctx* ctx, const float* q_raw, const float* k_raw,
+                                            const float* v_raw, float* k_cache, float* v_cache,
+                                            const void* w_o, float* x_io, uint32_t pos,
+                                            uint32_t max_seq, uint32_t num_heads,
+                                            uint32_t num_kv_heads, uint32_t head_dim, float theta,
+                                            uint32_t hidden);
 /* add_f16_into_f32 (dispatch.rs:316-330): acc[i] += f32(src[i]) for i < n
  * (the bias add of the separate-dispatch Q/K/V fallback, forward.rs:1561-1568). */
 int rt_add_f16_into_f32(rt_ctx* ctx, const uint16_t* src, float* acc, uint32_t n);

@@ -26,3 +26,8 @@ RT_GEMV_PAIR(k_qkv2_bias_q4kg_q6kg, FmtQ4KG, FmtQ6KG, EPI_QKV_BIAS)
 RT_GEMV_PAIR(k_qkv2_q4kg_q6kg, FmtQ4KG, FmtQ6KG, EPI_QKV)
 RT_GEMV_KERNEL(k_qkv_bias_q4kg, FmtQ4KG, EPI_QKV_BIAS, float, 1)
 RT_GEMV_KERNEL(k_qkv_q4kg, FmtQ4KG, EPI_QKV, float, 1)
+
+// ggml-layout Q4_K form of k_gemv_q4k_attn_f32add (split merge in the staging)
+extern "C" __global__ void __launch_bounds__(1024) k_gemv_q4kg_attn_f32add_r1(GemvArgs a) {
+    gemv_mq_body<FmtQ4KG, EPI_F32_ADD, AttnX, 1, GEMV_PF1>(a);
+}

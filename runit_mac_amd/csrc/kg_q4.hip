@@ -26,3 +26,11 @@ RT_GEMV_KERNEL(k_ffn_q4k, FmtQ4K, EPI_FFN, float, 1)
 // all-Q4_K projections (the other layers of Q4_K_M files)
 RT_GEMV_KERNEL(k_qkv_bias_q4k, FmtQ4K, EPI_QKV_BIAS, float, 1)
 RT_GEMV_KERNEL(k_qkv_q4k, FmtQ4K, EPI_QKV, float, 1)
+
+// Attention output projection with the split merge folded into the staging
+// (the Q4_K form of k_gemv_q8_0_attn_f32add: decode_attention's merge, then
+// the projection + residual, forward.rs:1588-1619); whole K in one slice
+// round of up to 1024 threads (q_dim ≤ 4096).
+extern "C" __global__ void __launch_bounds__(1024) k_gemv_q4k_attn_f32add_r1(GemvArgs a) {
+    gemv_mq_body<FmtQ4K, EPI_F32_ADD, AttnX, 1, GEMV_PF1>(a);
+}

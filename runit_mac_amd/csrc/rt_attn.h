@@ -135,28 +135,77 @@ RT_DEV void attn_split(const AttnArgs& a, uint32_t s, uint32_t nsp, uint32_t y, 
             vr[i] = ((const f32x4*)(vc + (size_t)(pv < p_end ? pv : p_begin) * HD))[vcol];
         }
     };
-    f32x4 kr[NQ], vr[NQ];
-    if (p_begin < p_end) load_kv(p_begin, kr, vr);
-    hook();
+    // The token's raw query / key / value (or the queries) go to registers
+    // first: a stand-alone launch issues them ahead of the K / V rows, which
+    // would otherwise queue in front of them (the RoPE and the scores wait for
+    // the query); a persistent phase issues the K / V rows before its hook,
+    // since only the token's vectors depend on the previous phase.
     auto act = [&](const float* p) { if constexpr (COH) return dev_load(p); else return *p; };
+    constexpr uint32_t half = HD / 2;
+    constexpr uint32_t PPT = ((GM + 1) * half + NT - 1) / NT;  // (q heads + key) pairs per thread
+    constexpr uint32_t VPT = (HD + NT - 1) / NT;               // value elements per thread
+    constexpr uint32_t QPT = (GM * HD + NT - 1) / NT;          // query elements per thread (no rope)
+    const uint32_t npair = (gh + 1) * half;
+    float rre[ROPE ? PPT : 1], rim[ROPE ? PPT : 1], rv[ROPE ? VPT : 1], rq[ROPE ? 1 : QPT];
+    auto load_token = [&]() {
+        if constexpr (ROPE) {
+#pragma unroll
+            for (uint32_t j = 0; j < PPT; ++j) {
+                const uint32_t i = tid + j * NT, ii = i < npair ? i : 0;
+                const uint32_t hh = ii / half, d = ii % half;
+                const float* src = hh < gh ? a.q + (size_t)(h0 + hh) * HD : a.k_new + (size_t)kvh * HD;
+                rre[j] = act(src + d);
+                rim[j] = act(src + d + half);
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < VPT; ++j) {
+                const uint32_t dd = tid + j * NT;
+                rv[j] = act(a.v_new + (size_t)kvh * HD + (dd < HD ? dd : 0));
+            }
+        } else {
+            const float* q = a.q + ((size_t)b * a.H + h0) * HD;
+#pragma unroll
+            for (uint32_t j = 0; j < QPT; ++j) {
+                const uint32_t i = tid + j * NT;
+                rq[j] = act(q + (i < gh * HD ? i : 0));
+            }
+        }
+    };
+    f32x4 kr[NQ], vr[NQ];
+    if constexpr (is_hook<Hook>()) {
+        if (p_begin < p_end) load_kv(p_begin, kr, vr);
+        hook();
+        load_token();
+    } else {
+        load_token();
+        if (p_begin < p_end) load_kv(p_begin, kr, vr);
+    }
     if constexpr (ROPE) {
         // fused_rope_qk_f32 (fused_rope.metal:28-55) on the block's query
         // heads and on the kv head's key
-        constexpr uint32_t half = HD / 2;
-        for (uint32_t i = tid; i < (gh + 1) * half; i += NT) {
-            const uint32_t hh = i / half, d = i % half;
-            float c, sn;
-            rope_cs(d, HD, a.pos, a.theta, c, sn);
-            const float* src = hh < gh ? a.q + (size_t)(h0 + hh) * HD : a.k_new + (size_t)kvh * HD;
-            float* dst = hh < gh ? qsf + hh * HD : (float*)ks4;
-            const float r = act(src + d), im = act(src + d + half);
-            dst[d] = r * c - im * sn;
-            dst[d + half] = r * sn + im * c;
+#pragma unroll
+        for (uint32_t j = 0; j < PPT; ++j) {
+            const uint32_t i = tid + j * NT;
+            if (i < npair) {
+                const uint32_t hh = i / half, d = i % half;
+                float c, sn;
+                rope_cs(d, HD, a.pos, a.theta, c, sn);
+                float* dst = hh < gh ? qsf + hh * HD : (float*)ks4;
+                dst[d] = rre[j] * c - rim[j] * sn;
+                dst[d + half] = rre[j] * sn + rim[j] * c;
+            }
         }
-        for (uint32_t d = tid; d < HD; d += NT) ((float*)vs4)[d] = act(a.v_new + (size_t)kvh * HD + d);
+#pragma unroll
+        for (uint32_t j = 0; j < VPT; ++j) {
+            const uint32_t dd = tid + j * NT;
+            if (dd < HD) ((float*)vs4)[dd] = rv[j];
+        }
     } else {
-        const float* q = a.q + ((size_t)b * a.H + h0) * HD;
-        for (uint32_t i = tid; i < gh * HD; i += NT) qsf[i] = act(q + i);
+#pragma unroll
+        for (uint32_t j = 0; j < QPT; ++j) {
+            const uint32_t i = tid + j * NT;
+            if (i < gh * HD) qsf[i] = rq[j];
+        }
     }
     if (tid < GM) {
         m_run[tid] = -__builtin_huge_valf();

@@ -69,6 +69,7 @@ constexpr uint32_t kAttnCounters = (kAuxBytes - kAuxAttnOff) / 4;
 const char* const kKernelNames[] = {
     "k_fill_u32", "k_decode_step_q8_0",
     "k_gemv_q8_0_f32_f32_r1", "k_gemv_q8_0_f32_f32_r2", "k_gemv_q8_0_attn_f32add_r1",
+    "k_gemv_q4k_attn_f32add_r1", "k_gemv_q4kg_attn_f32add_r1",
     "k_gemv_q8_0_f32_f32add_r1", "k_gemv_q8_0_f32_f32add_r2",
     "k_gemv_q8_0_f32_f16_r1", "k_gemv_q8_0_f32_f16_r2",
     "k_gemv_q8_0_f16_f16_r1", "k_gemv_q8_0_f16_f16_r2",
@@ -682,6 +683,9 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
         // ~240-register kernels are built for 512 threads.)
         const bool one_item = f.blk_bytes == 34 || mq_el == 256;
         if (S == 1 && a.K >= 2048 && !one_item && !a.xnsp) p.T = 1024;
+        // a merging projection stages its whole input in one slice round
+        if (a.xnsp)
+            while (p.T < nxb * 8 && p.T < 1024) p.T *= 2;
         // split K over the waves of a workgroup while the split waves still
         // fit in the resident waves (latency-bound small problems; a split
         // past that leaves a second round of workgroups as a tail)
@@ -2258,12 +2262,20 @@ int rt_decode_attention_rope_f32(rt_ctx* c, const float* q_raw, const float* k_r
     return attn_launch(c, kn, a, 1);
 }
 
-int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const float* k_raw,
-                                            const float* v_raw, float* k_cache, float* v_cache,
-                                            const void* w_o, float* x_io, uint32_t pos,
-                                            uint32_t max_seq, uint32_t num_heads,
-                                            uint32_t num_kv_heads, uint32_t head_dim, float theta,
-                                            uint32_t hidden) {
+// Attention (RoPE, KV write) and x_io += W_o·attention as two launches: the
+// attention writes every split's (o, m, l) and the projection's staging
+// merges them (the attention's own merge without its memory round trips).
+// `gkern` is the projection's merging kernel, `max_t` its largest workgroup
+// (the staging takes one 4-element slice per thread, so q_dim ≤ 4·max_t);
+// `plain` is the unfused projection for the shapes the merged form does not
+// take (no KV split, more than 8 splits, or q_dim too long).
+typedef int (*GemvAddFn)(rt_ctx*, const void*, const float*, float*, const float*, uint32_t,
+                         uint32_t);
+static int attention_oproj(rt_ctx* c, const float* q_raw, const float* k_raw, const float* v_raw,
+                           float* k_cache, float* v_cache, const void* w_o, float* x_io,
+                           uint32_t pos, uint32_t max_seq, uint32_t num_heads,
+                           uint32_t num_kv_heads, uint32_t head_dim, float theta, uint32_t hidden,
+                           const char* gkern, const Fmt& fmt, uint32_t max_t, GemvAddFn plain) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     if (num_heads == 0 || hidden == 0) return RT_OK;
     int st = attn_check(c, num_heads, num_kv_heads, head_dim);
@@ -2277,16 +2289,19 @@ int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const
     if (!aligned(x_io, 16))
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: attention_oproj: x must be 16-byte aligned");
-    // The merged form needs the projection to stage in one slice round of a
-    // 256-thread workgroup (q_dim ≤ 1024) and pays off while the attention
-    // splits the KV range in 2..8 (one split has no merge to save; more
-    // splits than the projection stages would slow the attention down);
-    // otherwise: attention, then the GEMV.
+    if (q_dim % fmt.blk_el != 0)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: attention_oproj: q_dim=%u must be a multiple of %u (%s)",
+                    q_dim, fmt.blk_el, fmt.name);
+    // The merged form needs the projection to stage in one slice round and
+    // pays off while the attention splits the KV range in 2..8 (one split has
+    // no merge to save; more splits than the projection stages would slow the
+    // attention down); otherwise: attention, then the GEMV.
     const uint32_t gm = rt_attn_gm(head_dim);  // query heads per attention workgroup
     const uint32_t nsplit0 =
         attn_nsplit(c, pos + 1, num_kv_heads * ((num_heads / num_kv_heads + gm - 1) / gm));
-    const bool merged = q_dim % 64 == 0 && q_dim / 32 * 8 <= 256 &&
-                        nsplit0 >= 2 && nsplit0 <= kAttnXMaxSplits;
+    const bool merged = q_dim % 64 == 0 && q_dim / 32 * 8 <= max_t && nsplit0 >= 2 &&
+                        nsplit0 <= kAttnXMaxSplits && c->fns.count(std::string(gkern) + "_r1");
     AttnArgs a{};
     a.q = q_raw;
     a.kc = k_cache;
@@ -2311,8 +2326,7 @@ int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const
         a.out = (float*)c->attn_out;
         st = attn_launch(c, kn, a, 1);
         if (st != RT_OK) return st;
-        return rt_gemv_q8_0_add_f32_f32in(c, w_o, (const float*)c->attn_out, x_io, x_io, hidden,
-                                          q_dim);
+        return plain(c, w_o, (const float*)c->attn_out, x_io, x_io, hidden, q_dim);
     }
     a.parts_only = 1;
     AttnArgs used{};
@@ -2323,7 +2337,39 @@ int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const
     g.xml = used.ml;
     g.xnsp = nsplit;
     g.xhd = head_dim;
-    return gemv_launch(c, "k_gemv_q8_0_attn_f32add", kQ8_0, g, false);
+    return gemv_launch(c, gkern, fmt, g, false);
+}
+
+int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const float* k_raw,
+                                            const float* v_raw, float* k_cache, float* v_cache,
+                                            const void* w_o, float* x_io, uint32_t pos,
+                                            uint32_t max_seq, uint32_t num_heads,
+                                            uint32_t num_kv_heads, uint32_t head_dim, float theta,
+                                            uint32_t hidden) {
+    // (512-thread body: the 0.5B shapes' q_dim = 896 stage in 224 slices)
+    return attention_oproj(c, q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io, pos, max_seq,
+                           num_heads, num_kv_heads, head_dim, theta, hidden,
+                           "k_gemv_q8_0_attn_f32add", kQ8_0, 256, rt_gemv_q8_0_add_f32_f32in);
+}
+int rt_decode_attention_rope_oproj_q4k_f32(rt_ctx* c, const float* q_raw, const float* k_raw,
+                                           const float* v_raw, float* k_cache, float* v_cache,
+                                           const void* w_o, float* x_io, uint32_t pos,
+                                           uint32_t max_seq, uint32_t num_heads,
+                                           uint32_t num_kv_heads, uint32_t head_dim, float theta,
+                                           uint32_t hidden) {
+    return attention_oproj(c, q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io, pos, max_seq,
+                           num_heads, num_kv_heads, head_dim, theta, hidden,
+                           "k_gemv_q4k_attn_f32add", kQ4K, 1024, rt_gemv_q4k_add_f32_f32in);
+}
+int rt_decode_attention_rope_oproj_q4kg_f32(rt_ctx* c, const float* q_raw, const float* k_raw,
+                                            const float* v_raw, float* k_cache, float* v_cache,
+                                            const void* w_o, float* x_io, uint32_t pos,
+                                            uint32_t max_seq, uint32_t num_heads,
+                                            uint32_t num_kv_heads, uint32_t head_dim, float theta,
+                                            uint32_t hidden) {
+    return attention_oproj(c, q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io, pos, max_seq,
+                           num_heads, num_kv_heads, head_dim, theta, hidden,
+                           "k_gemv_q4kg_attn_f32add", kQ4KG, 1024, rt_gemv_q4kg_add_f32_f32in);
 }
 
 int rt_add_f16_into_f32(rt_ctx* c, const uint16_t* src, float* acc, uint32_t n) {

@@ -409,9 +409,9 @@ class DecodeModel:
         """One greedy step: embedding, per layer Q/K/V (+ bias), RoPE + KV
         write + attention, O (+ residual), gate/up/SiLU, down (+ residual);
         final norm, LM head, argmax.  RMSNorm folds into the next launch's
-        staging for the Q8_0 and Q4_K_M projections, attention into the Q8_0
-        output projection; other formats take them as launches of their own.
-        Returns the number of launches."""
+        staging for the Q8_0 and Q4_K_M projections, the attention's split
+        merge into the Q8_0 and Q4_K output projections; other formats take
+        them as launches of their own.  Returns the number of launches."""
         ctx, c = self.ctx, self.cfg
         h, q_dim = c.hidden, c.q_dim
         n = 1
@@ -432,11 +432,10 @@ class DecodeModel:
             else:
                 d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, L["attn_norm"], c.eps, h, 1)
                 n += 1 + self._qkv(L, F, self.xn)
-            if F["o"] == "q8_0":
-                d.decode_attention_rope_oproj_q8_0_f32(ctx, self.q, self.k, self.v, L["kc"],
-                                                       L["vc"], L["wo"], self.x, pos, c.max_seq,
-                                                       c.heads, c.kv_heads, c.head_dim,
-                                                       c.theta, h)
+            if F["o"] in ("q8_0", "q4k", "q4kg"):
+                getattr(d, f"decode_attention_rope_oproj_{F['o']}_f32")(
+                    ctx, self.q, self.k, self.v, L["kc"], L["vc"], L["wo"], self.x, pos,
+                    c.max_seq, c.heads, c.kv_heads, c.head_dim, c.theta, h)
             else:
                 d.decode_attention_rope_f32(ctx, self.q, self.k, self.v, L["kc"], L["vc"],
                                             self.attn, pos, c.max_seq, c.heads, c.kv_heads,

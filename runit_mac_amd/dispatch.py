@@ -126,6 +126,8 @@ _SIGS = {
     "rt_decode_attention_f32": [_P, _P, _P, _P, _P] + [_U32] * 6,
     "rt_decode_attention_rope_f32": [_P] + [_P] * 6 + [_U32] * 5 + [_F],
     "rt_decode_attention_rope_oproj_q8_0_f32": [_P] + [_P] * 7 + [_U32] * 5 + [_F, _U32],
+    "rt_decode_attention_rope_oproj_q4k_f32": [_P] + [_P] * 7 + [_U32] * 5 + [_F, _U32],
+    "rt_decode_attention_rope_oproj_q4kg_f32": [_P] + [_P] * 7 + [_U32] * 5 + [_F, _U32],
     "rt_add_f16_into_f32": [_P, _P, _P, _U32],
     **{f"rt_embed_{_f}_f32": [_P, _P, _P, _P, _U32] for _f in (
         "q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg", "f16", "f32")},
@@ -686,6 +688,21 @@ def decode_attention_rope_oproj_q8_0_f32(ctx, q_raw, k_raw, v_raw, k_cache, v_ca
     _call(ctx, "rt_decode_attention_rope_oproj_q8_0_f32",
           *map(_ptr, (q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io)), pos, max_seq,
           num_heads, num_kv_heads, head_dim, theta, hidden)
+
+
+def _attention_oproj(fmt):
+    def fn(ctx, q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io, pos, max_seq, num_heads,
+           num_kv_heads, head_dim, theta, hidden):
+        _call(ctx, f"rt_decode_attention_rope_oproj_{fmt}_f32",
+              *map(_ptr, (q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io)), pos, max_seq,
+              num_heads, num_kv_heads, head_dim, theta, hidden)
+    fn.__name__ = f"decode_attention_rope_oproj_{fmt}_f32"
+    fn.__doc__ = (f"decode_attention_rope_oproj_q8_0_f32 for a {fmt} output projection (new).")
+    return fn
+
+
+decode_attention_rope_oproj_q4k_f32 = _attention_oproj("q4k")
+decode_attention_rope_oproj_q4kg_f32 = _attention_oproj("q4kg")
 
 
 def add_f16_into_f32(ctx, src, acc, n):

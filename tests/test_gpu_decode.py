@@ -153,13 +153,19 @@ def test_decode_attention_rope_fused(ctx, pos):
     assert np.all(np.abs(got - ref) <= 2e-3 * np.abs(vc2).max() + 1e-6), np.abs(got - ref).max()
 
 
-@pytest.mark.parametrize("H,KVH,hd,hidden,pos", [(14, 2, 64, 896, 0), (14, 2, 64, 896, 63),
-                                                  (14, 2, 64, 896, 511), (14, 2, 64, 896, 4200),
-                                                  (8, 8, 128, 512, 300), (28, 4, 128, 3584, 511)])
-def test_attention_oproj_matches_the_two_call_sequence(ctx, H, KVH, hd, hidden, pos):
-    """decode_attention_rope_oproj_q8_0_f32 (split merge inside the projection
-    when q_dim ≤ 1024, else the two kernels) against decode_attention_rope_f32
-    followed by gemv_q8_0_add_f32_f32in on copies of the same inputs."""
+@pytest.mark.parametrize("fmt,H,KVH,hd,hidden,pos", [
+    ("q8_0", 14, 2, 64, 896, 0), ("q8_0", 14, 2, 64, 896, 63), ("q8_0", 14, 2, 64, 896, 511),
+    ("q8_0", 14, 2, 64, 896, 4200), ("q8_0", 8, 8, 128, 512, 300), ("q8_0", 28, 4, 128, 3584, 511),
+    # Q4_K projections (q_dim a multiple of 256): merged at 2..8 KV splits
+    # (pos 63..511), the two kernels at one split (pos 0) and past 8 (pos 1000)
+    ("q4k", 28, 4, 128, 3584, 0), ("q4k", 28, 4, 128, 3584, 63), ("q4k", 28, 4, 128, 3584, 511),
+    ("q4k", 28, 4, 128, 3584, 1000), ("q4k", 8, 8, 128, 512, 300), ("q4k", 16, 2, 64, 1024, 200),
+    ("q4kg", 28, 4, 128, 3584, 511), ("q4kg", 8, 8, 128, 512, 300)])
+def test_attention_oproj_matches_the_two_call_sequence(ctx, fmt, H, KVH, hd, hidden, pos):
+    """decode_attention_rope_oproj_<fmt>_f32 (split merge inside the
+    projection's staging when the attention splits the KV range in 2..8,
+    else the two kernels) against decode_attention_rope_f32 followed by
+    gemv_<fmt>_add_f32_f32in on copies of the same inputs."""
     rng = np.random.default_rng(pos + hd)
     max_seq, theta, q_dim = 4300, 1e6, H * hd
     q = rng.standard_normal(q_dim).astype(np.float32)
@@ -168,17 +174,17 @@ def test_attention_oproj_matches_the_two_call_sequence(ctx, H, KVH, hd, hidden, 
     kc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float32)
     vc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float32)
     x0 = rng.standard_normal(hidden).astype(np.float32)
-    wo, raw = device_weights(ctx, "q8_0", hidden, q_dim, seed=pos + 3)
+    wo, raw = device_weights(ctx, fmt, hidden, q_dim, seed=pos + 3)
     qb, kb, vb = ctx.buffer_from(q), ctx.buffer_from(k_new), ctx.buffer_from(v_new)
     # the two-call sequence
     kc1, vc1, x1 = ctx.buffer_from(kc), ctx.buffer_from(vc), ctx.buffer_from(x0)
     att = ctx.new_buffer(4 * q_dim)
     d.decode_attention_rope_f32(ctx, qb, kb, vb, kc1, vc1, att, pos, max_seq, H, KVH, hd, theta)
-    d.gemv_q8_0_add_f32_f32in(ctx, wo, att, x1, x1, hidden, q_dim)
+    getattr(d, f"gemv_{fmt}_add_f32_f32in")(ctx, wo, att, x1, x1, hidden, q_dim)
     # the merged call
     kc2, vc2, x2 = ctx.buffer_from(kc), ctx.buffer_from(vc), ctx.buffer_from(x0)
-    d.decode_attention_rope_oproj_q8_0_f32(ctx, qb, kb, vb, kc2, vc2, wo, x2, pos, max_seq, H, KVH,
-                                           hd, theta, hidden)
+    getattr(d, f"decode_attention_rope_oproj_{fmt}_f32")(ctx, qb, kb, vb, kc2, vc2, wo, x2, pos,
+                                                         max_seq, H, KVH, hd, theta, hidden)
     ctx.flush()
     assert np.array_equal(kc1.read(np.float32, kc.size), kc2.read(np.float32, kc.size))
     assert np.array_equal(vc1.read(np.float32, vc.size), vc2.read(np.float32, vc.size))
@@ -187,7 +193,7 @@ def test_attention_oproj_matches_the_two_call_sequence(ctx, H, KVH, hd, hidden, 
     # same merge formula and order; the only freedom is the compiler's
     # contraction of the merge's multiply-adds, well inside the GEMV tolerance
     a = att.read(np.float32, q_dim).astype(np.float64)
-    W = ora.dequant("q8_0", raw).reshape(hidden, q_dim).astype(np.float64)
+    W = ora.dequant(fmt, raw).reshape(hidden, q_dim).astype(np.float64)
     sabs = np.abs(W) @ np.abs(a)
     assert np.all(np.abs(y1 - y2) <= 1e-5 * sabs + 1e-6), np.abs(y1 - y2).max()
 
