@@ -153,7 +153,7 @@ struct StepHook {
     }
 };
 
-extern "C" __global__ void __launch_bounds__(1024)
+extern "C" __global__ void __launch_bounds__(RT_STEP_THREADS)
 k_decode_step_q8_0(const StepPhase* __restrict__ ph, uint32_t nph, StepSync* sy) {
     constexpr int PF = fmt_pf<FmtQ8_0>() ? fmt_pf<FmtQ8_0>() : GEMV_PF1;
     __shared__ uint32_t base_s;
@@ -182,7 +182,7 @@ k_decode_step_q8_0(const StepPhase* __restrict__ ph, uint32_t nph, StepSync* sy)
         case SK_ATTN_HD64: {
             const uint32_t nsp = f.n0, ny = f.n1;
             if (blockIdx.x < nsp * ny)
-                attn_split<64, true, rt_attn_hg(64), rt_attn_gm(64), true>(
+                attn_split<64, true, RT_STEP_THREADS / 256, rt_attn_gm(64), true>(
                     step_attn_args(f.at), blockIdx.x % nsp, nsp, blockIdx.x / nsp, 0, hook);
             else
                 hook();

@@ -361,6 +361,121 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
     }
 }
 
+// Small-launch body (M = 1, whole K in one staging pass, about one row quad
+// per wave: the 0.5B model's norm-fused Q/K/V, attention-merging O and
+// norm-fused gate+up launches).  These launches are bound by the chain
+// before their first dot, not by their 1-9 MB of weights, and per-workgroup
+// timestamps show where that chain goes on the matrix-core body: its lanes'
+// strided 68-byte units touch ~34 cache lines per load instruction, so
+// issuing a workgroup's weight loads backs up the CU's address unit for
+// ~0.7 µs, and the staging barriers then wait ~1.9 µs for the slowest wave.
+// Here every row of a quad is read with NI coalesced 1 KB loads (8 lines per
+// instruction), the activation loads go out first, the quad goes through the
+// wave's LDS slot (as in gemv_ls_body), and the result is stored right after
+// the dot: no result buffer, no second item in flight.
+template <class F, int EPI, typename XT, int NI>
+RT_DEV void gemv_sm_body(const GemvArgs& a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nwaves = wg_threads() >> 6;
+    const uint32_t q = lane & 3, slot = lane >> 2;
+    const uint32_t lq = q < 3 ? q : 2;  // the A row of lane q = 3 is a don't-care
+    const uint32_t units = a.K / F::UNIT_EL;
+    const uint32_t cbytes = units * F::UNIT_EL / F::BLK_EL * F::BLK_BYTES;  // a whole row
+    const uint32_t nxb = a.K / 32;
+    XRec* xs = (XRec*)smem;
+    const uint32_t RS = a.ls_rs;
+    uint8_t* wslot = smem + nxb * XREC_BYTES + wave * (4 * RS);
+    const uint32_t nq = (a.nvrows + 3) / 4;
+    // the waves of a workgroup take neighbouring quads (one contiguous run
+    // of rows per workgroup), then the next run of the grid
+    const uint32_t first = blockIdx.x * nwaves + wave, stride = gridDim.x * nwaves;
+    const uint32_t nitems = first < nq ? (nq - first + stride - 1) / stride : 0;
+    auto row_src = [&](uint32_t vr) -> const uint8_t* {
+        if (vr >= a.nvrows) vr = a.nvrows - 1;
+        uint32_t mat, r;
+        vrow_map<EPI>(a, vr, mat, r);
+        return mat_w(a, mat) + (size_t)r * a.row_bytes;
+    };
+    typedef u32x4 Item[4][NI];
+    auto issue = [&](uint32_t j, Item& dst) {
+        const uint32_t quad = first + stride * min(j, nitems ? nitems - 1 : 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint8_t* src = row_src(quad * 4 + r);
+            const uint8_t* base = src - ((uintptr_t)src & 15);
+            const uint32_t last = (uint32_t)(((uintptr_t)src & 15) + cbytes - 1) & ~15u;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t off = min((uint32_t)(i * 64 + lane) * 16, last);
+                dst[r][i] = *(const u32x4*)(base + off);
+            }
+        }
+    };
+    auto commit = [&](const Item& src) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < NI; ++i) *(u32x4*)(wslot + r * RS + (i * 64 + lane) * 16) = src[r][i];
+    };
+    // activations first, then the weights and the epilogue operand of the
+    // lane's row of the first quad, then the conversion (which waits for the
+    // activations only)
+    XPre xp;
+    XPreAttn xa;
+    if constexpr (is_attn_x<XT>())
+        stage_attn_load<false>(a.x, a.xml, a.xnsp, a.xhd, nxb, xa);
+    else
+        stage_x_load<XT>((const XT*)a.x, a.gamma, nxb, xp);
+    Item buf;
+    issue(0, buf);
+    float aux = 0.0f;
+    if (has_aux<EPI>() && nitems) {
+        const uint32_t vr = first * 4 + q;
+        aux = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
+    }
+    if constexpr (is_attn_x<XT>())
+        stage_attn_convert<F::Q40PERM>(xa, a.xnsp, nxb, xs);
+    else
+        stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
+    lds_barrier();
+
+    const uint32_t nsteps = (units + 15) / 16;
+    for (uint32_t j = 0; j < nitems; ++j) {
+        commit(buf);
+        const uint32_t quad = first + stride * j;
+        if (j + 1 < nitems) issue(j + 1, buf);
+        const uint8_t* rowl = wslot + q * RS + ((uintptr_t)row_src(quad * 4 + q) & 15);
+        float acc = 0.0f;
+        for (uint32_t st = 0; st < nsteps; ++st) {
+            const uint32_t u = slot + 16 * st;
+            const bool valid = u < units;
+            const uint32_t uc = valid ? u : 0;
+            typename F::Raw raw;
+            ls_load<F>(rowl, uc, raw, 0);
+            const float v = F::mdot(raw, xs, uc, lq);
+            acc += valid ? v : 0.0f;
+        }
+        // sum over the 16 slots of the row (lane bits 2..5): every lane of
+        // the row gets the total
+        acc += swz_xor_f<4>(acc);
+        acc += swz_xor_f<8>(acc);
+        acc += swz_xor_f<16>(acc);
+        acc += __shfl_xor(acc, 32, 64);
+        const uint32_t vr = quad * 4 + q;
+        if (j > 0 && has_aux<EPI>()) aux = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
+        if (EPI == EPI_FFN) {
+            // quad rows (gate r, up r, gate r+1, up r+1)
+            const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(acc);
+            if (slot == 0 && (q & 1) == 0 && vr + 1 < a.nvrows)
+                ((float*)a.out[0])[vr >> 1] = silu_ref(acc) * up;
+        } else if (slot == 0 && vr < a.nvrows) {
+            store_row_pre<EPI>(a, vr, acc, aux);
+        }
+    }
+}
+
 // Kernels: one per (format, epilogue, activation type, loads per row NI).
 // Built for up to 1024 threads (≤ 128 registers: 16 waves per CU share one
 // copy of the activation records), except Q6_K, whose whole-super-block
@@ -381,3 +496,8 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
 #define RT_GEMV_LSBV(NAME, FMT, EPI, XT, LB) \
     RT_GEMV_LS1V(NAME, FMT, EPI, XT, 1, LB) RT_GEMV_LS1V(NAME, FMT, EPI, XT, 2, LB) RT_GEMV_LS1V(NAME, FMT, EPI, XT, 3, LB)
 
+
+// Small-launch kernels (gemv_sm_body): <name>_sm<NI>, 256 threads.
+#define RT_GEMV_SM1(NAME, FMT, EPI, XT, NI) \
+    extern "C" __global__ void __launch_bounds__(256) NAME##_sm##NI(GemvArgs a) { gemv_sm_body<FMT, EPI, XT, NI>(a); }
+#define RT_GEMV_SM(NAME, FMT, EPI, XT) RT_GEMV_SM1(NAME, FMT, EPI, XT, 1) RT_GEMV_SM1(NAME, FMT, EPI, XT, 2)

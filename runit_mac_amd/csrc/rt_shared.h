@@ -28,5 +28,8 @@ constexpr uint64_t RT_SCRATCH_PART_BYTES = RT_SCRATCH_BYTES - RT_SCRATCH_PART_OF
 // workgroups a step grid may have.
 constexpr uint32_t RT_STEP_PHASE_BYTES = 376;
 constexpr uint32_t RT_STEP_MAX_WGS = 1024;
+// threads per workgroup of the persistent step (its attention phase runs
+// RT_STEP_THREADS / 256 head groups)
+#define RT_STEP_THREADS 512
 constexpr uint32_t RT_STEP_SYNC_BYTES = 2048;  // StepSync (k_step.hip)
 constexpr uint32_t RT_STEP_STATUS_OFF = 1280;  // its status word

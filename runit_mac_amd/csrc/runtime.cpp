@@ -190,6 +190,11 @@ const char* const kLskBases[] = {
     "k_gemv_q5k_f32_f32add", "k_gemv_q4kg_f32_f32add", "k_gemv_q5kg_f32_f32add", "k_gemv_q4_0g_f32_f32add", "k_gemv_q5_0_f32_f32add",
     "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32add",
 };
+// Small-launch kernels: <base>_sm1, <base>_sm2.
+const char* const kSmBases[] = {
+    "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_qkv_bias_q8_0", "k_ffn_q8_0",
+    "k_gemv_q8_0_attn_f32add",
+};
 // Multi-row kernels: <base>_x8 for each format's four epilogues.
 const char* const kRowsFmts[] = {"q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k",
                                  "q4_0g", "q4kg", "q5kg", "q6kg"};
@@ -262,6 +267,7 @@ struct rt_ctx {
     void* attn_out = nullptr;  // attention output between the two launches of
     size_t attn_out_bytes = 0;  // the unmerged attention + o_proj sequence
     bool ls_enabled = true;      // RUNIT_GEMV_LS=0: the per-lane-load matrix-core body instead
+    bool sm_enabled = true;      // RUNIT_GEMV_SM=0: no small-launch body (A/B)
     bool gemv_valu = false;      // RUNIT_GEMV_VALU=1: VALU-dot twins of the LDS body (A/B)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
@@ -603,6 +609,39 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     return launch(c, name, dim3(bg * S), dim3(bt), blds, params);
 }
 
+// Small-launch body (rt_gemv_ls.h, *_sm<NI>): whole K in one staging pass,
+// rows of ≤ 2 KB read with coalesced 1 KB loads, about one row quad per wave
+// (256-thread workgroups).  Taken for launches of at most kSmMaxQuadsPerCu
+// row quads per CU (the 0.5B model's Q/K/V, O and gate+up launches: 72, 56
+// and 608 workgroups), where the chain before the first dot, not the weight
+// stream, bounds the launch.
+constexpr uint32_t kSmThreads = 256;
+constexpr uint32_t kSmMaxQuadsPerCu = 12;
+int gemv_launch_sm(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
+    const uint64_t rb = a.row_bytes;
+    const uint32_t NI = (uint32_t)((rb + 15 + 1023) / 1024);
+    if (NI > 2) return kLsDecline;
+    const uint32_t nxb = a.K / 32;
+    // one staging pass of ≤ 4 slices per thread (a merged attention input: one)
+    if (nxb * 8 > (a.xnsp ? 1u : 4u) * kSmThreads) return kLsDecline;
+    if (a.K % f.mq_units() != 0 || a.x_rec) return kLsDecline;
+    const uint32_t nq = (a.nvrows + 3) / 4;
+    if (nq > (uint64_t)c->cu_count * kSmMaxQuadsPerCu) return kLsDecline;
+    char name[96];
+    snprintf(name, sizeof name, "%s_sm%u", kname, NI);
+    if (!c->fns.count(name)) return kLsDecline;
+    a.ksplit = 1;
+    a.kc_units = a.K / f.mq_units();
+    a.ls_rs = NI * 1024 + kLsRowPad;
+    const uint32_t nwv = kSmThreads / 64;
+    const size_t lds = (size_t)nxb * XREC_BYTES + (size_t)nwv * 4 * a.ls_rs;
+    if (lds > c->max_lds) return kLsDecline;
+    const uint32_t occ = std::max<uint32_t>(1, occupancy(c, name, kSmThreads, lds));
+    const uint32_t grid = std::min<uint32_t>((nq + nwv - 1) / nwv, (uint32_t)c->cu_count * occ);
+    void* params[] = {&a};
+    return launch(c, name, dim3(grid), dim3(kSmThreads), lds, params);
+}
+
 int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x_f16,
                 bool paired = false) {
     const bool single = fmt.single && (a.K % fmt.unit_el) != 0;
@@ -620,6 +659,10 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
                     "kernel dispatch error: %s: input must be %d-byte aligned", kname,
                     x_f16 ? 8 : 16);
     a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
+    if (c->sm_enabled && !single && !x_f16 && a.nx <= 1 && a.nblk == 0) {
+        const int st = gemv_launch_sm(c, kname, f, a);
+        if (st != kLsDecline) return st;
+    }
     if (c->ls_enabled && !single && !x_f16 && !a.xnsp && has_ls_kernel(c, kname)) {
         const int st = gemv_launch_ls(c, kname, f, a);
         if (st != kLsDecline) return st;
@@ -1159,6 +1202,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_F16")) c->gemm_f16 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMV_SM")) c->sm_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_VALU")) c->gemv_valu = atoi(g) != 0;
     std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
@@ -1185,6 +1229,8 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     for (const char* b : kLsBases)
         for (uint32_t ni = 1; ni <= kLsMaxNI; ++ni) names.push_back(std::string(b) + "_ls" + std::to_string(ni));
     for (const char* b : kLskBases) names.push_back(std::string(b) + "_lsk1");
+    for (const char* b : kSmBases)
+        for (uint32_t ni = 1; ni <= 2; ++ni) names.push_back(std::string(b) + "_sm" + std::to_string(ni));
     for (const char* fm : kRowsFmts)
         for (const char* pat : {"k_gemv_%s_f32_f32_x8", "k_gemv_%s_f32_f32add_x8", "k_qkv_bias_%s_x8",
                                 "k_ffn_%s_x8"}) {
@@ -2657,7 +2703,7 @@ struct StepPhaseH {
 };
 static_assert(sizeof(StepPhaseH) == RT_STEP_PHASE_BYTES, "StepPhase layout");
 constexpr size_t kStepSyncBytes = RT_STEP_SYNC_BYTES;
-constexpr uint32_t kStepThreads = 1024;
+constexpr uint32_t kStepThreads = RT_STEP_THREADS;
 enum : uint32_t { SK_EMBED_Q8_0 = 0, SK_QKV_Q8_0 = 1, SK_ATTN_HD64 = 2, SK_OPROJ_Q8_0 = 3,
                   SK_FFN_Q8_0 = 4, SK_DOWN_Q8_0 = 5 };
 
@@ -2709,7 +2755,7 @@ int rt_decode_step_q8_0_create(rt_ctx* c, const rt_step_model* m, uint32_t pos, 
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: decode_step: head_dim %u, heads %u / %u (built for "
                     "head size 64, heads a multiple of the KV heads)", hd, H, KVH);
-    if (h % 64 || ff % 64 || qd % 64 || qd / 32 * 8 > kStepThreads || 2 * ff / 32 * 8 > 4 * kStepThreads)
+    if (h % 64 || ff % 64 || qd % 64 || qd / 32 * 8 > kStepThreads || ff / 32 * 8 > 4 * kStepThreads)
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: decode_step: hidden %u / ff %u / q_dim %u must be "
                     "multiples of 64 within one staging pass", h, ff, qd);
