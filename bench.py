@@ -607,7 +607,7 @@ def main():
                                    "batch 1, kv_len 512 (24 layers, hidden 896, 14/2 heads x 64, "
                                    "ff 4864, vocab 151936), one HIP-graph replay per token",
                        "global_batch": 1, "kv_len": 512},
-            "roofline": {"bound": "hbm", "kernel": "k_ffn_q8_0 (rms_norm + gate/up + SiLU)",
+            "roofline": {"bound": "hbm", "kernel": "k_ffn_q8_0_sm1 (rms_norm + gate/up + SiLU, small-launch body)",
                          "achieved": round(ffn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ffn_gbs / HBM_PEAK_GBS, 4),
                          "traffic": measured_traffic("ffn_q8_0_0p5b_pmc_traffic.md"),
