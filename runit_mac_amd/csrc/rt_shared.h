@@ -9,9 +9,12 @@
 // head, twice the workgroups of one block of 8: 12.6 → ~11 µs per 7B layer
 // at kv_len 512); head sizes 64 and 256 take 8.
 constexpr uint32_t rt_attn_gm(uint32_t head_dim) { return head_dim == 128 ? 4u : 8u; }
-// Head groups of 256 threads per workgroup (registers bound head size 256 to one).
+// Head groups of 256 threads per workgroup (registers bound head size 256 to
+// one).  Every group reads the workgroup's K / V rows, so more groups mean
+// more repeated loads through the CU against shorter per-thread chains;
+// head size 64 takes two (0.5B step: 706 → 701 µs against four).
 constexpr uint32_t rt_attn_hg(uint32_t head_dim) {
-    return head_dim == 64 ? 4u : head_dim == 128 ? 2u : 1u;
+    return head_dim == 256 ? 1u : 2u;
 }
 
 // Device scratch of the no-allocation entry points: one fixed array in the
