@@ -268,6 +268,7 @@ struct rt_ctx {
     size_t attn_out_bytes = 0;  // the unmerged attention + o_proj sequence
     bool ls_enabled = true;      // RUNIT_GEMV_LS=0: the per-lane-load matrix-core body instead
     bool sm_enabled = true;      // RUNIT_GEMV_SM=0: no small-launch body (A/B)
+    uint64_t launches = 0;       // kernel launches enqueued so far (rt_launch_count)
     bool gemv_valu = false;      // RUNIT_GEMV_VALU=1: VALU-dot twins of the LDS body (A/B)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
@@ -355,6 +356,7 @@ int launch(rt_ctx* c, const char* name, dim3 grid, dim3 block, size_t lds, void*
     hipError_t e = hipModuleLaunchKernel(it->second, grid.x, grid.y, grid.z, block.x, block.y,
                                          block.z, (unsigned)lds, c->stream, params, nullptr);
     if (e != hipSuccess) return hip_fail(c, e, name);
+    ++c->launches;
     return RT_OK;
 }
 
@@ -2417,6 +2419,8 @@ int rt_decode_attention_rope_oproj_q4kg_f32(rt_ctx* c, const float* q_raw, const
                            num_heads, num_kv_heads, head_dim, theta, hidden,
                            "k_gemv_q4kg_attn_f32add", kQ4KG, 1024, rt_gemv_q4kg_add_f32_f32in);
 }
+
+uint64_t rt_launch_count(const rt_ctx* c) { return c ? c->launches : 0; }
 
 int rt_add_f16_into_f32(rt_ctx* c, const uint16_t* src, float* acc, uint32_t n) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");

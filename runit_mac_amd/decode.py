@@ -411,9 +411,11 @@ class DecodeModel:
         final norm, LM head, argmax.  RMSNorm folds into the next launch's
         staging for the Q8_0 and Q4_K_M projections, the attention's split
         merge into the Q8_0 and Q4_K output projections; other formats take
-        them as launches of their own.  Returns the number of launches."""
+        them as launches of their own.  Returns the number of launches (as
+        the library counted them)."""
         ctx, c = self.ctx, self.cfg
         h, q_dim = c.hidden, c.q_dim
+        n0 = d.launch_count(ctx)
         n = 1
         d.embed_f32(ctx, self.embd_fmt, self.embd, self.token, self.x, h)
         for L, F in zip(self.layers, self.fmts):
@@ -461,8 +463,10 @@ class DecodeModel:
             n += 1
         n += self._lm_head(self.x)
         d.argmax_f32(ctx, self.logits, self.token, c.vocab)
-        self._launches = n + 1
-        return n + 1
+        # launches as the library counted them (a fused call may fall back to
+        # its unfused sequence)
+        self._launches = d.launch_count(ctx) - n0
+        return self._launches
 
     def launches_fused(self) -> int:
         """Launches of one fused step, as the last step_fused issued them (the

@@ -127,6 +127,7 @@ _SIGS = {
     "rt_decode_attention_rope_f32": [_P] + [_P] * 6 + [_U32] * 5 + [_F],
     "rt_decode_attention_rope_oproj_q8_0_f32": [_P] + [_P] * 7 + [_U32] * 5 + [_F, _U32],
     "rt_decode_attention_rope_oproj_q4k_f32": [_P] + [_P] * 7 + [_U32] * 5 + [_F, _U32],
+    "rt_launch_count": [_P],
     "rt_decode_attention_rope_oproj_q4kg_f32": [_P] + [_P] * 7 + [_U32] * 5 + [_F, _U32],
     "rt_add_f16_into_f32": [_P, _P, _P, _U32],
     **{f"rt_embed_{_f}_f32": [_P, _P, _P, _P, _U32] for _f in (
@@ -232,6 +233,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.rt_decode_step_status.restype = c_int
     lib.rt_decode_step_destroy.argtypes = [_P]
     lib.rt_decode_step_destroy.restype = None
+    lib.rt_launch_count.restype = c_uint64
     # GGUF reader: (name, argtypes, restype)
     PU64 = POINTER(c_uint64)
     for name, argtypes, restype in (
@@ -699,6 +701,11 @@ def _attention_oproj(fmt):
     fn.__name__ = f"decode_attention_rope_oproj_{fmt}_f32"
     fn.__doc__ = (f"decode_attention_rope_oproj_q8_0_f32 for a {fmt} output projection (new).")
     return fn
+
+
+def launch_count(ctx) -> int:
+    """Kernel launches enqueued on the context so far (new)."""
+    return int(ctx.lib.rt_launch_count(ctx.handle))
 
 
 decode_attention_rope_oproj_q4k_f32 = _attention_oproj("q4k")

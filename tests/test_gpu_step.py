@@ -200,3 +200,17 @@ def test_host_twin_rebuilds_device_model_bytes(ctx, quant):
             dev = m.read(L[key], (arr.nbytes + 3) // 4).view(np.uint8)[:arr.nbytes]
             assert np.array_equal(dev, arr.view(np.uint8)), key
     m.free()
+
+
+@pytest.mark.gpu
+def test_step_fused_counts_its_launches(ctx):
+    """step_fused reports the launches the library enqueued (rt_launch_count):
+    for the 2-layer 0.5B-shape model, 1 embedding + 5 per layer + norm-fused
+    LM head + argmax."""
+    from runit_mac_amd.decode import DecodeConfig, DecodeModel
+    m = DecodeModel(ctx, DecodeConfig(layers=2), seed=3)
+    m.set_token(1)
+    before = d.launch_count(ctx)
+    n = m.step_fused(5)
+    ctx.flush()
+    assert n == d.launch_count(ctx) - before == 1 + 5 * 2 + 2
