@@ -193,7 +193,7 @@ const char* const kLskBases[] = {
 // Small-launch kernels: <base>_sm1, <base>_sm2.
 const char* const kSmBases[] = {
     "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_qkv_bias_q8_0", "k_ffn_q8_0",
-    "k_gemv_q8_0_attn_f32add",
+    "k_gemv_q8_0_attn_f32add", "k_gemv_q4k_f32_f32", "k_gemv_q4k_f32_f32add",
 };
 // Multi-row kernels: <base>_x8 for each format's four epilogues.
 const char* const kRowsFmts[] = {"q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k",
