@@ -385,25 +385,31 @@ RT_DEV uint32_t stage_slice(int s, uint32_t total) {
     const uint32_t t = threadIdx.x + s * wg_threads();
     return t < total ? t : (t & 7);
 }
-struct XPre {
-    float v[XSTAGE_UNR][4];
-    float g[XSTAGE_UNR][4];
+// U slices per thread (XSTAGE_UNR unless a body holds more registers for it)
+template <int U>
+struct XPreU {
+    float v[U][4];
+    float g[U][4];
 };
-RT_DEV bool stage_one_pass(uint32_t nxb) { return nxb * 8 <= XSTAGE_UNR * wg_threads(); }
+using XPre = XPreU<XSTAGE_UNR>;
+template <int U = XSTAGE_UNR>
+RT_DEV bool stage_one_pass(uint32_t nxb) { return nxb * 8 <= U * wg_threads(); }
 
-template <typename XT>
+// SKIP: lanes past the end load and convert nothing (whole 8-lane groups; a
+// workgroup of many such lanes otherwise rebuilds record 0 many times over)
+template <typename XT, int U, bool SKIP = false>
 RT_DEV void stage_x_load(const XT* __restrict__ x, const float* __restrict__ gamma, uint32_t nxb,
-                         XPre& p) {
+                         XPreU<U>& p) {
     const uint32_t total = nxb * 8;
 #pragma unroll
-    for (int s = 0; s < XSTAGE_UNR; ++s) {
+    for (int s = 0; s < U; ++s) {
         // rounds past the vector are skipped (workgroup-uniform: no lane of a
         // later load is conditional); lanes past the end load clamped addresses
         if (s * wg_threads() >= total) break;
         // device-scope activations (a persistent kernel's): lanes past the
         // end load nothing (their clamped copies would all hit the same few
         // addresses at device scope) and convert nothing
-        if (__is_same(XT, CohF32) && threadIdx.x + s * wg_threads() >= total) continue;
+        if ((SKIP || __is_same(XT, CohF32)) && threadIdx.x + s * wg_threads() >= total) continue;
         const uint32_t t = stage_slice(s, total);
         const uint32_t i = (t >> 3) * 32 + (t & 7) * 4;
         load_x4<XT>(x, i, p.v[s]);
@@ -416,15 +422,15 @@ RT_DEV void stage_x_load(const XT* __restrict__ x, const float* __restrict__ gam
 
 // With γ: x̂ = x · rsqrt(Σx²/K + eps) · γ (rms_norm_f32_f32_f32g,
 // norm.metal:126-154), each product rounded in f32 as in stage_x_norm.
-template <bool Q40PERM, bool SKIP = false>
-RT_DEV void stage_x_convert(XPre& p, const float* gamma, float eps, uint32_t nxb,
+template <bool Q40PERM, bool SKIP = false, int U>
+RT_DEV void stage_x_convert(XPreU<U>& p, const float* gamma, float eps, uint32_t nxb,
                             XRec* __restrict__ recs) {
     const uint32_t total = nxb * 8;
     if (gamma) {
         __shared__ float nred[16];
         float ss = 0.0f;
 #pragma unroll
-        for (int s = 0; s < XSTAGE_UNR; ++s) {
+        for (int s = 0; s < U; ++s) {
             const float sq = p.v[s][0] * p.v[s][0] + p.v[s][1] * p.v[s][1] +
                              p.v[s][2] * p.v[s][2] + p.v[s][3] * p.v[s][3];
             ss += (threadIdx.x + s * wg_threads() < total) ? sq : 0.0f;
@@ -436,12 +442,12 @@ RT_DEV void stage_x_convert(XPre& p, const float* gamma, float eps, uint32_t nxb
         for (uint32_t w = 0; w < (wg_threads() >> 6); ++w) tot += nred[w];
         const float rms = rsqrtf(tot / (float)(nxb * 32) + eps);
 #pragma unroll
-        for (int s = 0; s < XSTAGE_UNR; ++s)
+        for (int s = 0; s < U; ++s)
 #pragma unroll
             for (int i = 0; i < 4; ++i) p.v[s][i] = p.v[s][i] * rms * p.g[s][i];
     }
 #pragma unroll
-    for (int s = 0; s < XSTAGE_UNR; ++s) {
+    for (int s = 0; s < U; ++s) {
         // rounds past the vector are skipped (workgroup-uniform); inside a
         // round, lanes past the end convert a copy of block 0 (see stage_slice)
         if (s * wg_threads() < total) {

@@ -313,9 +313,19 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
         const uint32_t vr = (wg + nwg * min(tid >> 2, nql ? nql - 1 : 0)) * 4 + (tid & 3);
         aux = load_aux<EPI>(a, vr < a.nvrows ? vr : a.nvrows - 1);
     }
+    // activation loads, then the first item's weights, then the conversion
+    // (which waits for the activations only: loads complete in issue order,
+    // so staging behind the weight loads would wait for HBM)
+    constexpr int XU = 5;  // slices per thread: K ≤ 20,480 at 1024 threads
+    const bool one_pass = !a.x_rec && stage_one_pass<XU>(nxb_all);
+    XPreU<XU> xp;
+    if (one_pass) stage_x_load<XT, XU, true>((const XT*)a.x, nullptr, nxb_all, xp);
     Item buf;
     issue(0, buf);
-    stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, nxb_all, xs);
+    if (one_pass)
+        stage_x_convert<F::Q40PERM, true>(xp, nullptr, 0.0f, nxb_all, xs);
+    else
+        stage_x<XT, F::Q40PERM>(a.x, a.x_rec != 0, 0, nxb_all, xs);
     lds_barrier();
 
     for (uint32_t j = 0; j < nitems; ++j) {
