@@ -106,11 +106,14 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
     };
     // coalesced loads of item j's four row chunks: NI dwordx4 per lane and
     // row from the chunk's 16-byte floor (lanes past the chunk re-read its
-    // last 16 bytes).  An item past the wave's last re-reads the wave's last
-    // item (cache hits), computed without branches so that every loop
-    // iteration issues the same loads and the compiler's waits stay exact.
+    // last 16 bytes).  An item past the wave's last issues the same loads
+    // with no records in their descriptor (dropped, no memory access), so
+    // that every loop iteration issues the same loads and the compiler's
+    // waits stay exact.  (Re-reading the last item instead fetched 7% more
+    // than the weight bytes: some of those lines had left the L2.)
     typedef u32x4 Item[4][NI];
     auto issue = [&](uint32_t j, Item& dst) {
+        const bool none = j >= nitems;
         const uint32_t quad = quad_of(min(j, nitems - 1));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -120,7 +123,7 @@ RT_DEV void gemv_ls_body(const GemvArgs& a) {
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const uint32_t off = min((uint32_t)(i * 64 + lane) * 16, last);
-                dst[r][i] = *(const u32x4*)(base + off);
+                dst[r][i] = load16_or_none(base, off, none);
             }
         }
     };
@@ -284,7 +287,8 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
     };
     auto chunk_units = [&](uint32_t c) { return min(units_all - c * kcu, kcu); };
     typedef u32x4 Item[4][NI];
-    auto issue = [&](uint32_t j, Item& dst) {
+    auto issue = [&](uint32_t j, Item& dst) {  // (past the last item: dropped loads)
+        const bool none = j >= nitems;
         const uint32_t it = item_of(min(j, nitems - 1));
         const uint32_t quad = wg + nwg * (it / S), c = it % S;
         const uint32_t cbytes = chunk_units(c) * F::UNIT_EL / F::BLK_EL * F::BLK_BYTES;
@@ -296,7 +300,7 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const uint32_t off = min((uint32_t)(i * 64 + lane) * 16, last);
-                dst[r][i] = *(const u32x4*)(base + off);
+                dst[r][i] = load16_or_none(base, off, none);
             }
         }
     };
