@@ -183,12 +183,10 @@ k_dequant_q4k_f16(const uint8_t* __restrict__ in, uint16_t* __restrict__ out, ui
 //   * the index of the last NaN, if the last element is NaN;
 //   * otherwise the LAST index of the maximum of the elements after the last
 //     NaN (of all elements when there is no NaN).
-// Both parts are order-independent reductions inside a range, so each
-// workgroup reduces its contiguous range with coalesced loads to a state
-// (last NaN index P, best (value, index) after P), and the ranges are merged
-// in index order: merge(L, R) = R if R has a NaN, else (L.P, later-wins max of
-// L.best and R.best).  The last workgroup to finish (arrival counter, reset by
-// that workgroup) merges all states and writes the result.
+// Both parts are order-independent reductions, so each workgroup reduces its
+// contiguous range with coalesced loads to a state (last NaN index, best
+// (value, index) after it), and the last workgroup to finish (arrival
+// counter, reset by that workgroup) reduces the states and writes the result.
 struct AmState {
     int32_t nan_idx;  // last NaN index in the range, -1 if none
     int32_t idx;      // index of the best element after nan_idx, -1 if none
@@ -208,30 +206,29 @@ RT_DEV float am_load<float>(const float* p, uint32_t i) { return p[i]; }
 template <>
 RT_DEV float am_load<uint16_t>(const uint16_t* p, uint32_t i) { return h2f(p[i]); }
 
-RT_DEV AmState am_merge(AmState L, AmState R) {
-    // R's range follows L's: a NaN in R makes everything before it irrelevant
-    if (R.nan_idx >= 0) return R;
-    if (R.idx >= 0 && am_better(R.v, R.idx, L.v, L.idx)) return AmState{L.nan_idx, R.idx, R.v};
-    return L;
-}
-
 constexpr int AM_PER = 4;  // elements per thread per workgroup range
 
+// The states reduce in any order: with P the largest NaN index over all of
+// them, the result is the later-wins maximum over the states whose best
+// index exceeds P (ranges before P hold only indices below it, and the range
+// holding P reports its best after P).
 template <typename T>
 RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result, uint32_t n,
                         AmState* __restrict__ states, uint32_t* __restrict__ counter) {
     __shared__ int32_t sn[AM_T / 64];
-    __shared__ AmState sb[AM_T];
+    __shared__ AmState sb[AM_T / 64];
     __shared__ bool last;
     const uint32_t per = (n + gridDim.x - 1) / gridDim.x;
     const uint32_t b0 = blockIdx.x * per, b1 = min(n, b0 + per);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Ranges up to AM_PER·AM_T elements take one pass with all loads issued
-    // up front; longer ranges loop over such chunks.
+    // up front and the values kept for the second reduction; longer ranges
+    // loop over such chunks, reading the range twice.
     constexpr uint32_t CH = AM_PER * AM_T;
+    const bool one = b1 - b0 <= CH;  // workgroup-uniform
+    float xv[AM_PER];
     int32_t nl = -1;
     for (uint32_t c0 = b0; c0 < b1; c0 += CH) {
-        float xv[AM_PER];
 #pragma unroll
         for (int u = 0; u < AM_PER; ++u) {
             const uint32_t i = c0 + tid + u * AM_T;
@@ -248,16 +245,16 @@ RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result,
     __syncthreads();
     int32_t P = -1;
     for (uint32_t w = 0; w < AM_T / 64; ++w) P = max(P, sn[w]);
-    // best element after P (later index wins ties); the second read of the
-    // range hits the cache
+    // best element after P (later index wins ties)
     float bv = 0.0f;
     int32_t bi = -1;
     for (uint32_t c0 = b0; c0 < b1; c0 += CH) {
-        float xv[AM_PER];
+        if (!one) {
 #pragma unroll
-        for (int u = 0; u < AM_PER; ++u) {
-            const uint32_t i = c0 + tid + u * AM_T;
-            xv[u] = i < b1 ? am_load<T>(in, i) : 0.0f;
+            for (int u = 0; u < AM_PER; ++u) {
+                const uint32_t i = c0 + tid + u * AM_T;
+                xv[u] = i < b1 ? am_load<T>(in, i) : 0.0f;
+            }
         }
 #pragma unroll
         for (int u = 0; u < AM_PER; ++u) {
@@ -287,26 +284,39 @@ RT_DEV void argmax_body(const T* __restrict__ in, uint32_t* __restrict__ result,
         last = arrive(counter) == gridDim.x - 1;
     }
     __syncthreads();
-    if (!last) return;
-    // ordered tree merge of the workgroup states (merge is associative)
+    if (!last || wave != 0) return;
+    // the last workgroup's first wave: up to AM_T states, AM_T / 64 per lane
     const uint32_t G = gridDim.x;
-    if (tid < G) {
-        const AmState* vs = &states[tid];
-        sb[tid] = AmState{dev_load(&vs->nan_idx), dev_load(&vs->idx), dev_load(&vs->v)};
+    AmState s[AM_T / 64];
+    int32_t gp = -1;
+#pragma unroll
+    for (uint32_t r = 0; r < AM_T / 64; ++r) {
+        const uint32_t g = lane + 64 * r;
+        s[r] = AmState{-1, -1, 0.0f};
+        if (g < G) {
+            const AmState* vs = &states[g];
+            s[r] = AmState{dev_load(&vs->nan_idx), dev_load(&vs->idx), dev_load(&vs->v)};
+        }
+        gp = max(gp, s[r].nan_idx);
     }
-    __syncthreads();
-    for (uint32_t st = 1; st < G; st <<= 1) {
-        if ((tid % (2 * st)) == 0 && tid + st < G) sb[tid] = am_merge(sb[tid], sb[tid + st]);
-        __syncthreads();
+    for (int o = 32; o > 0; o >>= 1) gp = max(gp, __shfl_xor(gp, o, 64));
+    bv = 0.0f;
+    bi = -1;
+#pragma unroll
+    for (uint32_t r = 0; r < AM_T / 64; ++r)
+        if (s[r].idx > gp && am_better(s[r].v, s[r].idx, bv, bi)) { bv = s[r].v; bi = s[r].idx; }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int32_t oi = __shfl_xor(bi, o, 64);
+        if (oi >= 0 && am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
     }
-    if (tid == 0) {
-        const AmState acc = sb[0];
+    if (lane == 0) {
         uint32_t res = 0;
         if (n > 0) {
-            if (acc.nan_idx == (int32_t)n - 1 || acc.idx < 0)
-                res = acc.nan_idx >= 0 ? (uint32_t)acc.nan_idx : 0u;
+            if (gp == (int32_t)n - 1 || bi < 0)
+                res = gp >= 0 ? (uint32_t)gp : 0u;
             else
-                res = (uint32_t)acc.idx;
+                res = (uint32_t)bi;
         }
         result[0] = res;
         dev_store(counter, 0u);  // ready for the next call (also under graph replay)

@@ -167,6 +167,26 @@ def test_argmax_ties_and_nan_follow_rust_max_by(ctx):
         assert int(res.read(np.uint32, 1)[0]) == ora.argmax(c)
 
 
+def test_argmax_nan_ranges_at_vocab_size(ctx):
+    """NaNs in several workgroup ranges, the maximum before, inside and after
+    the range holding the last NaN, and ties across ranges (later wins)."""
+    rng = np.random.default_rng(11)
+    n = 151936
+    res = ctx.new_buffer(4)
+    for case in range(24):
+        v = rng.standard_normal(n).astype(np.float32)
+        k = int(rng.integers(0, 4))
+        if k:
+            v[rng.integers(0, n, size=k)] = np.float32("nan")
+        for pos in rng.integers(0, n, size=int(rng.integers(1, 4))):
+            v[pos] = 6.0  # equal maxima, possibly on both sides of a NaN
+        if case == 0:
+            v[-1] = np.float32("nan")
+        d.argmax_f32(ctx, ctx.buffer_from(v), res, n)
+        ctx.flush()
+        assert int(res.read(np.uint32, 1)[0]) == ora.argmax(v), case
+
+
 def test_argmax_f16(ctx):
     v = np.random.default_rng(9).standard_normal(151936).astype(np.float16)
     res = ctx.new_buffer(4)
