@@ -182,7 +182,7 @@ k_decode_step_q8_0(const StepPhase* __restrict__ ph, uint32_t nph, StepSync* sy)
         case SK_ATTN_HD64: {
             const uint32_t nsp = f.n0, ny = f.n1;
             if (blockIdx.x < nsp * ny)
-                attn_split<64, true, RT_STEP_THREADS / 256, rt_attn_gm(64), true>(
+                attn_split<64, true, RT_STEP_THREADS / 256, rt_step_attn_gm(64), true>(
                     step_attn_args(f.at), blockIdx.x % nsp, nsp, blockIdx.x / nsp, 0, hook);
             else
                 hook();

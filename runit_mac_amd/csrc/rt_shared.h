@@ -4,18 +4,19 @@
 #pragma once
 #include <stdint.h>
 
-// Decode attention: query heads per workgroup at a head size.  Head size 128
-// takes 4 (7B-class groups of 7 query heads then take two workgroups per KV
-// head, twice the workgroups of one block of 8: 12.6 → ~11 µs per 7B layer
-// at kv_len 512); head sizes 64 and 256 take 8.
-constexpr uint32_t rt_attn_gm(uint32_t head_dim) { return head_dim == 128 ? 4u : 8u; }
-// Head groups of 256 threads per workgroup (registers bound head size 256 to
-// one).  Every group reads the workgroup's K / V rows, so more groups mean
-// more repeated loads through the CU against shorter per-thread chains;
-// head size 64 takes two (0.5B step: 706 → 701 µs against four).
-constexpr uint32_t rt_attn_hg(uint32_t head_dim) {
-    return head_dim == 256 ? 1u : 2u;
-}
+// Decode attention: query heads per workgroup at a head size.  Head sizes 64
+// and 128 take 1: a group of 7 query heads spreads over 7 workgroups per KV
+// head and split, each thread's score chain one head long (0.5B step: 690 →
+// 667 µs, 7B step: 1889 → 1846 µs against 8 and 4 heads per workgroup);
+// head size 256 takes 8.
+constexpr uint32_t rt_attn_gm(uint32_t head_dim) { return head_dim == 256 ? 8u : 1u; }
+// Head groups of 256 threads per workgroup: one (groups share the query heads
+// of their workgroup, so one head leaves one group; head size 256 is bound to
+// one by its registers).
+constexpr uint32_t rt_attn_hg(uint32_t) { return 1u; }
+// The persistent step's attention phase runs RT_STEP_THREADS / 256 = 2 head
+// groups, so its workgroups take 2 query heads (step 772 → 753 µs against 8).
+constexpr uint32_t rt_step_attn_gm(uint32_t) { return 2u; }
 
 // Device scratch of the no-allocation entry points: one fixed array in the
 // code object (k_scratch.hip), laid out as [arrival counters | activation

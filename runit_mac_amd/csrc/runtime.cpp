@@ -2781,7 +2781,7 @@ int rt_decode_step_q8_0_create(rt_ctx* c, const rt_step_model* m, uint32_t pos, 
     const uint32_t nsp = std::min<uint32_t>(kAttnXMaxSplits, (kv_len + 63) / 64);
     const uint32_t chunk = ((kv_len + nsp - 1) / nsp + 63) / 64 * 64;
     const uint32_t nsp_used = (kv_len + chunk - 1) / chunk;
-    const uint32_t gm = rt_attn_gm(hd), HB = (H / KVH + gm - 1) / gm;
+    const uint32_t gm = rt_step_attn_gm(hd), HB = (H / KVH + gm - 1) / gm;
     // activation buffers, each on its own 256-byte lines, fresh for every
     // phase of the step
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
