@@ -704,7 +704,10 @@ RT_GEMM_XH_PREP(1)
 RT_GEMM_XH_PREP(2)
 RT_GEMM_XH_PREP(4)
 
-template <class P, int MG, int NB, int WAVES = 4>
+// ABUF = 1: the activation operands of a stage in one LDS buffer (the
+// weights keep two), refilled after a barrier that ends every wave's reads —
+// the Q6_K form at 32 rows, whose two buffers would not fit the LDS.
+template <class P, int MG, int NB, int WAVES = 4, int ABUF = 2>
 RT_DEV void gemm3_body(const Gemm2Args& a) {
     constexpr uint32_t T = 64 * WAVES, ROWS = 16 * WAVES;
     constexpr uint32_t NR = NB * P::RECS;
@@ -720,7 +723,7 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
     constexpr uint32_t APT = (AV4 + T - 1) / T;
     static_assert(SEG % VB == 0 && SV4 <= T, "segment alignment");
     __shared__ WV lw[2][WV_N];
-    __shared__ u32x4 la[2][AV4];
+    __shared__ u32x4 la[ABUF][AV4];
     __shared__ u32x4 le[2][SV4];
     __shared__ u32x4 ls[P::HAS_MIN ? 2 : 1][P::HAS_MIN ? SV4 : 1];
     __shared__ uint32_t last_flag;
@@ -766,7 +769,7 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
                 if (tid + T * i < WV_N) lw[buf][tid + T * i] = rw[i];
 #pragma unroll
             for (uint32_t i = 0; i < APT; ++i)
-                if (tid + T * i < AV4) la[buf][tid + T * i] = ra[i];
+                if (tid + T * i < AV4) la[ABUF == 2 ? buf : 0][tid + T * i] = ra[i];
             if (tid < SV4) le[buf][tid] = re;
             if (P::HAS_MIN && tid < SV4) ls[P::HAS_MIN ? buf : 0][tid] = rs;
         };
@@ -776,7 +779,7 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
         const uint32_t wrow = (16 * wv + j) * SEG;
         auto compute = [&](uint32_t buf) {
             const uint8_t* wb = (const uint8_t*)lw[buf] + wrow;
-            const u32x4* ab = la[buf];
+            const u32x4* ab = la[ABUF == 2 ? buf : 0];
             const int* eb = (const int*)le[buf];
             const float* sb = (const float*)ls[P::HAS_MIN ? buf : 0];
 #pragma unroll 2
@@ -826,6 +829,7 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
             const bool more = st + 1 < nst;
             if (more) gload(st + 1);
             compute(st & 1);
+            if (ABUF == 1) __syncthreads();  // every wave done with the one operand buffer
             if (more) lstore((st + 1) & 1);
             __syncthreads();
         }
@@ -910,6 +914,14 @@ RT_GEMM3_KERNEL4(q6k, GemmQ6K, 1, 2)
 RT_GEMM3_KERNEL4(q6k, GemmQ6K, 2, 2)
 RT_GEMM3_KERNEL4(q6kg, GemmQ6KG, 1, 2)
 RT_GEMM3_KERNEL4(q6kg, GemmQ6KG, 2, 2)
+// 32 rows in one chunk (one pass over the weights): 64 KB of activation
+// operands per stage, single-buffered
+#define RT_GEMM3_KERNEL4A1(FN, P, MG, NB)                                                     \
+    extern "C" __global__ void __launch_bounds__(256) k_gemm3_##FN##_mg##MG(Gemm2Args a) {    \
+        gemm3_body<P, MG, NB, 4, 1>(a);                                                        \
+    }
+RT_GEMM3_KERNEL4A1(q6k, GemmQ6K, 4, 2)
+RT_GEMM3_KERNEL4A1(q6kg, GemmQ6KG, 4, 2)
 
 #define RT_GEMM2_KERNEL4(FN, P, MG, NB)                                                       \
     extern "C" __global__ void __launch_bounds__(256) k_gemm2_##FN##_mg##MG(Gemm2Args a) {    \

@@ -166,7 +166,8 @@ const char* const kKernelNames[] = {
     "k_gemm3_q5k_mg1", "k_gemm3_q5k_mg1_w8", "k_gemm3_q5k_mg2", "k_gemm3_q5k_mg2_w8",
     "k_gemm3_q5k_mg4", "k_gemm3_q5k_mg4_w8", "k_gemm3_q5kg_mg1", "k_gemm3_q5kg_mg1_w8",
     "k_gemm3_q5kg_mg2", "k_gemm3_q5kg_mg2_w8", "k_gemm3_q5kg_mg4", "k_gemm3_q5kg_mg4_w8",
-    "k_gemm3_q6k_mg1", "k_gemm3_q6k_mg2", "k_gemm3_q6kg_mg1", "k_gemm3_q6kg_mg2",
+    "k_gemm3_q6k_mg1", "k_gemm3_q6k_mg2", "k_gemm3_q6k_mg4", "k_gemm3_q6kg_mg1", "k_gemm3_q6kg_mg2",
+    "k_gemm3_q6kg_mg4",
     "k_gemm_xh_prep_mg1", "k_gemm_xh_prep_mg2", "k_gemm_xh_prep_mg4",
 };
 
@@ -1750,6 +1751,7 @@ struct GemmFmt {
     bool has_min;                      // needs per-record activation sums
     int (*gemv)(rt_ctx*, const void*, const float*, float*, uint32_t, uint32_t);
     uint32_t max_mg = 8;               // activation-row groups per chunk (LDS budget)
+    uint32_t max_mg_f16 = 4;           // the f16 form's 8-row groups per chunk
 };
 
 // f16 matrix-core form of the staged GEMM (k_gemm3_*): 8 activation rows
@@ -1760,7 +1762,7 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
                  uint32_t m_rows, uint32_t n, uint32_t k) {
     const uint32_t cu = (uint32_t)c->cu_count;
     const uint32_t groups = (m_rows + 7) / 8;
-    const uint32_t MG = std::min<uint32_t>(f.max_mg / 2, groups <= 1 ? 1 : groups <= 2 ? 2 : 4);
+    const uint32_t MG = std::min<uint32_t>(f.max_mg_f16, groups <= 1 ? 1 : groups <= 2 ? 2 : 4);
     const uint32_t nchunks = (m_rows + 8 * MG - 1) / (8 * MG);
     const uint32_t nrec = k / 32;
     const uint32_t nblk = k / f.blk_el;
@@ -1940,11 +1942,11 @@ constexpr GemmFmt kGemmQ4_0{"q4_0", 32, 18, 1, 8, 4, false, rt_gemv_q4_0_f32in_f
 constexpr GemmFmt kGemmQ4K{"q4k", 256, 144, 8, 1, 1, true, rt_gemv_q4k_f32in_f32out};
 constexpr GemmFmt kGemmQ5_0{"q5_0", 32, 22, 1, 8, 4, false, rt_gemv_q5_0_f32in_f32out};
 constexpr GemmFmt kGemmQ5K{"q5k", 256, 176, 8, 1, 1, true, rt_gemv_q5k_f32in_f32out};
-constexpr GemmFmt kGemmQ6K{"q6k", 256, 210, 8, 2, 2, false, rt_gemv_q6k_f32in_f32out, 4};
+constexpr GemmFmt kGemmQ6K{"q6k", 256, 210, 8, 2, 2, false, rt_gemv_q6k_f32in_f32out, 4, 4};
 constexpr GemmFmt kGemmQ4_0G{"q4_0g", 32, 18, 1, 8, 4, false, rt_gemv_q4_0g_f32in_f32out};
 constexpr GemmFmt kGemmQ4KG{"q4kg", 256, 144, 8, 1, 1, true, rt_gemv_q4kg_f32in_f32out};
 constexpr GemmFmt kGemmQ5KG{"q5kg", 256, 176, 8, 1, 1, true, rt_gemv_q5kg_f32in_f32out};
-constexpr GemmFmt kGemmQ6KG{"q6kg", 256, 210, 8, 2, 2, false, rt_gemv_q6kg_f32in_f32out, 4};
+constexpr GemmFmt kGemmQ6KG{"q6kg", 256, 210, 8, 2, 2, false, rt_gemv_q6kg_f32in_f32out, 4, 4};
 
 RT_ROWS_ENTRIES(q8_0, kQ8_0)
 RT_ROWS_ENTRIES(q4_0, kQ4_0)
