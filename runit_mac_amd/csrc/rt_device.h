@@ -39,6 +39,9 @@ RT_DEV void lds_barrier() {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // 16 bytes at base + off through a raw buffer descriptor.  none = true gives
 // the descriptor no records: the hardware's range check then drops the
@@ -49,9 +52,6 @@ RT_DEV u32x4 load16_or_none(const void* base, uint32_t off, bool none) {
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, none ? 0 : 0x7FFFFFFF, 0x00020000);
     return (u32x4)__builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
 }
-typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
-typedef uint32_t u32_a2 __attribute__((aligned(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ───────────────────────────── f16 ─────────────────────────────
 
