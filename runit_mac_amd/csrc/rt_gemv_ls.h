@@ -403,8 +403,11 @@ RT_DEV void gemv_sm_body(const GemvArgs& a) {
     uint8_t* wslot = smem + nxb * XREC_BYTES + wave * (4 * RS);
     const uint32_t nq = (a.nvrows + 3) / 4;
     // the waves of a workgroup take neighbouring quads (one contiguous run
-    // of rows per workgroup), then the next run of the grid
-    const uint32_t first = blockIdx.x * nwaves + wave, stride = gridDim.x * nwaves;
+    // of rows per workgroup), then the next run of the grid (in a two-part
+    // launch: of this part's workgroups [blk0, blk0 + nblk))
+    const uint32_t bid = a.nblk ? blockIdx.x - a.blk0 : blockIdx.x;
+    const uint32_t nbid = a.nblk ? a.nblk : gridDim.x;
+    const uint32_t first = bid * nwaves + wave, stride = nbid * nwaves;
     const uint32_t nitems = first < nq ? (nq - first + stride - 1) / stride : 0;
     auto row_src = [&](uint32_t vr) -> const uint8_t* {
         if (vr >= a.nvrows) vr = a.nvrows - 1;
