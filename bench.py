@@ -498,8 +498,8 @@ def profile_pass(ctx, launches: int = 24) -> None:
     (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the dominant kernel of the
     decode step — the norm-fused gate+up+SiLU GEMV at the 0.5B shape — over
     `launches` distinct weight replicas, the 7B Q4_K gate+up+SiLU over 8,
-    then a plain copy kernel of known size whose counters calibrate the byte
-    counts."""
+    the 7B Q6_K down projection over 8, then a plain copy kernel of known
+    size whose counters calibrate the byte counts."""
     from runit_mac_amd.decode import DecodeConfig
     cfg = DecodeConfig()
     h, ff = cfg.hidden, cfg.ff
@@ -535,6 +535,21 @@ def profile_pass(ctx, launches: int = 24) -> None:
     ctx.flush()
     for g, u in mats7:
         d.fused_ffn_q4k_f32(ctx, g, u, x7, act7, ff7, h7)
+    ctx.flush()
+    # the 7B Q6_K down projection + residual (workgroup-local K split) over 8
+    # replicas of 56 MB
+    wd7 = d.weight_bytes("q6k", h7, ff7)
+    arena_d = _arena_for(ctx, [wd7], 8)
+    downs = []
+    for r in range(8):
+        w = arena_d.take(wd7)
+        d.synth_weights(ctx, "q6k", w, h7 * ff7 // 256, 400 + r)
+        downs.append(w)
+    y7 = ctx.new_buffer(4 * h7)
+    d.synth_normal_f32(ctx, y7, h7, 8)
+    ctx.flush()
+    for w in downs:
+        d.gemv_q6k_add_f32_f32in(ctx, w, act7, y7, y7, h7, ff7)
     ctx.flush()
     copy_bytes = 256 << 20
     src, dst = ctx.new_buffer(copy_bytes), ctx.new_buffer(copy_bytes)
