@@ -17,6 +17,7 @@ pub mod ffi;
 
 use std::ffi::{CStr, CString};
 use std::os::raw::{c_int, c_void};
+use std::rc::Rc;
 use thiserror::Error;
 
 /// crates/kernels/src/error.rs:4-21, variant for variant.
@@ -67,8 +68,24 @@ fn status_at(ctx: *const ffi::RtCtx, st: c_int, path: &str) -> Result<()> {
 /// `MetalContext` analogue (crates/kernels/src/context.rs:150-304): device 0,
 /// the gfx950 code objects, every kernel resolved up front, one stream.
 /// Not `Sync`, like `MetalContext` (context.rs:158).
+///
+/// The native context is reference-counted: every [`Buffer`] and [`Graph`]
+/// holds a count, so the context is destroyed only when the `HipContext` and
+/// everything allocated from it are gone (dropping the `HipContext` first is
+/// safe; its buffers stay usable for read / write / free).
 pub struct HipContext {
+    inner: Rc<CtxHandle>,
     raw: *mut ffi::RtCtx,
+}
+
+/// Owner of the native context: destroyed with the last reference.
+struct CtxHandle(*mut ffi::RtCtx);
+
+impl Drop for CtxHandle {
+    /// context.rs:299-304: flushes, then releases everything.
+    fn drop(&mut self) {
+        unsafe { ffi::rt_ctx_destroy(self.0) }
+    }
 }
 
 impl HipContext {
@@ -77,14 +94,14 @@ impl HipContext {
         let mut raw = std::ptr::null_mut();
         status_at(std::ptr::null(), unsafe { ffi::rt_ctx_create(&mut raw, std::ptr::null()) },
                   "<librunit_hip.so dir>/kernels")?;
-        Ok(Self { raw })
+        Ok(Self { inner: Rc::new(CtxHandle(raw)), raw })
     }
     /// The same with a given code object (a file, or a directory of them).
     pub fn with_code_object(path: &str) -> Result<Self> {
         let c = CString::new(path).map_err(|e| KernelError::Dispatch(e.to_string()))?;
         let mut raw = std::ptr::null_mut();
         status_at(std::ptr::null(), unsafe { ffi::rt_ctx_create(&mut raw, c.as_ptr()) }, path)?;
-        Ok(Self { raw })
+        Ok(Self { inner: Rc::new(CtxHandle(raw)), raw })
     }
     pub(crate) fn raw(&self) -> *mut ffi::RtCtx {
         self.raw
@@ -93,7 +110,7 @@ impl HipContext {
     pub fn new_buffer(&self, size: usize) -> Result<Buffer> {
         let mut p = std::ptr::null_mut();
         status(self.raw, unsafe { ffi::rt_malloc(self.raw, size.max(1), &mut p) })?;
-        Ok(Buffer { ptr: p, len: size, ctx: self.raw })
+        Ok(Buffer { ptr: p, len: size, ctx: self.raw, _owner: Rc::clone(&self.inner) })
     }
     /// A new buffer holding `data` (the engine's `new_buffer` + `contents()` copy).
     pub fn buffer_from<T: Copy>(&self, data: &[T]) -> Result<Buffer> {
@@ -112,14 +129,7 @@ impl HipContext {
     pub fn capture_end(&self) -> Result<Graph> {
         let mut g = std::ptr::null_mut();
         status(self.raw, unsafe { ffi::rt_capture_end(self.raw, &mut g) })?;
-        Ok(Graph { raw: g, ctx: self.raw })
-    }
-}
-
-impl Drop for HipContext {
-    /// context.rs:299-304: flushes, then releases everything.
-    fn drop(&mut self) {
-        unsafe { ffi::rt_ctx_destroy(self.raw) }
+        Ok(Graph { raw: g, ctx: self.raw, _owner: Rc::clone(&self.inner) })
     }
 }
 
@@ -129,6 +139,7 @@ pub struct Buffer {
     ptr: *mut c_void,
     len: usize,
     ctx: *mut ffi::RtCtx,
+    _owner: Rc<CtxHandle>, // keeps the context alive until this buffer is freed
 }
 
 impl Buffer {
@@ -169,6 +180,7 @@ impl Drop for Buffer {
 pub struct Graph {
     raw: *mut ffi::RtGraph,
     ctx: *mut ffi::RtCtx,
+    _owner: Rc<CtxHandle>, // keeps the context alive until the graph is destroyed
 }
 
 impl Graph {

@@ -786,7 +786,9 @@ int rt_gguf_meta_array_string(const rt_gguf* g, uint64_t i, uint64_t k, const ch
  * argmax (two more launches).  create() plans the step for one position `pos`
  * (kv_len = pos + 1) and allocates its activation buffers; run() enqueues it
  * (no allocation; capturable); status() flushes and reports a grid barrier
- * that timed out (the kernel bounds every wait).  The token id is read from
+ * that timed out (the kernel bounds every wait) since the last status() call,
+ * then clears the report: a run that timed out left an invalid token and
+ * invalid activations, so check status() before using a token.  The token id is read from
  * *token and the greedy next token written back there. */
 typedef struct rt_step rt_step;
 typedef struct {

@@ -508,8 +508,10 @@ class DecodeModel:
         if v is not None and v["rows"] >= rows and (v["has_logits"] or not logits):
             return v
         if v is not None:
+            # the old arena stays allocated until free(): a graph captured
+            # over it (verify_pass is capturable) keeps valid pointers
             rows = max(rows, v["rows"])
-            v["arena"].buf.free()
+            self._retired_arenas = getattr(self, "_retired_arenas", []) + [v["arena"]]
         c = self.cfg
         dims = dict(x=c.hidden, xn=c.hidden, q=c.q_dim, k=c.kv_dim, v=c.kv_dim, att=c.q_dim,
                     p=c.hidden, g=c.ff, u=c.ff)
@@ -533,10 +535,15 @@ class DecodeModel:
         matrix's own format (see verify_pass for the two forms).  Returns the
         activation buffers (``logits``: [M][vocab], ``idx``: [M] argmax)."""
         ctx, c = self.ctx, self.cfg
-        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
-        M = int(toks.size)
-        if M == 0:
+        ids = np.asarray(tokens).astype(np.int64, casting="same_kind").ravel()
+        if ids.size == 0:
             raise ValueError("verify: empty sequence")
+        # the embedding kernel indexes the table with the id unchecked: a
+        # negative or past-the-vocabulary id is refused before any upload
+        if np.any(ids < 0) or np.any(ids >= c.vocab):
+            raise ValueError(f"verify: token id out of range [0, {c.vocab})")
+        toks = ids.astype(np.uint32)
+        M = int(toks.size)
         if start_pos + M > c.max_seq:
             raise ValueError(f"verify: start_pos {start_pos} + {M} tokens exceed the KV cache "
                              f"({c.max_seq})")
@@ -653,11 +660,12 @@ class DecodeModel:
         final norm and the LM head on the last token only.  Returns that
         token's logits; the greedy next token is left in the decode token
         buffer, so step_fused(len(tokens)) continues the sequence."""
-        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
-        if toks.size == 0:
+        ids = np.asarray(tokens).astype(np.int64, casting="same_kind").ravel()
+        if ids.size == 0:
             raise ValueError("prefill: empty prompt")
-        if np.any(toks >= self.cfg.vocab):
+        if np.any(ids < 0) or np.any(ids >= self.cfg.vocab):
             raise ValueError("prefill: token id out of range")
+        toks = ids.astype(np.uint32)
         M = int(toks.size)
         if M > self.cfg.max_seq:
             raise ValueError(f"prefill: {M} tokens exceed the KV cache ({self.cfg.max_seq})")
@@ -698,4 +706,7 @@ class DecodeModel:
         if getattr(self, "_vbufs", None) is not None:
             self._vbufs["arena"].buf.free()
             self._vbufs = None
+        for a in getattr(self, "_retired_arenas", []):
+            a.buf.free()
+        self._retired_arenas = []
         self.arena.buf.free()

@@ -284,3 +284,55 @@ def test_rms_norm_fused_q4k_m_gemvs(ctx):
         d.rms_norm_fused_qkv_bias_q4k_q6k_f32(ctx, ws[0][0], ws[1][0], ws[2][0], xb, gb, 1e-6,
                                               *outs, *[ctx.buffer_from(b) for b in bias], 4, 4,
                                               8448)
+
+
+@pytest.mark.parametrize("fmt,H,KVH,hd,hidden,pos", [
+    ("q4k", 28, 4, 128, 3584, 511), ("q4k", 28, 4, 128, 3584, 200),
+    ("q4kg", 28, 4, 128, 3584, 511), ("q8_0", 14, 2, 64, 896, 511)])
+def test_attention_oproj_matches_oracle(ctx, fmt, H, KVH, hd, hidden, pos):
+    """decode_attention_rope_oproj_<fmt>_f32 at the 7B head count (28/4 heads
+    of 128, hidden 3584: 8 KV splits merged in the O projection's staging at
+    pos 511, 4 at pos 200) against the f64 oracle: RoPE, the cache write,
+    attention over pos + 1 positions (attention.metal:248-308) and
+    x + W_o·att (gemv_multirow.metal:205-243).
+
+    theta = 1 makes every RoPE frequency exactly 1 (1/powf(1, ·) = 1), so
+    every angle is the integer pos, exact in f32, and the device's f32
+    rotation differs from the oracle's only by its sincosf rounding (~1e-7
+    relative).  The tolerance is then the GEMV bound on the oracle's
+    attention output plus the f32 attention error carried through |W_o|:
+        |y − y_ref| ≤ 1e-4·Σ_j|w_ij·a_j| + Σ_j|w_ij|·ε_a,
+        ε_a = 1e-5·max|v|  (f32 scores, exp and the ≤ 64-position partial
+                             sums of each split, then an 8-way merge)."""
+    rng = np.random.default_rng(pos + 7 * hd)
+    max_seq, theta, q_dim = 1024, 1.0, H * hd
+    q = rng.standard_normal(q_dim).astype(np.float32)
+    k_new = rng.standard_normal(KVH * hd).astype(np.float32)
+    v_new = rng.standard_normal(KVH * hd).astype(np.float32)
+    kc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float32)
+    vc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float32)
+    x0 = rng.standard_normal(hidden).astype(np.float32)
+    wo, raw = device_weights(ctx, fmt, hidden, q_dim, seed=pos + 11)
+    qb, kb, vb = ctx.buffer_from(q), ctx.buffer_from(k_new), ctx.buffer_from(v_new)
+    kcb, vcb, xb = ctx.buffer_from(kc), ctx.buffer_from(vc), ctx.buffer_from(x0)
+    getattr(d, f"decode_attention_rope_oproj_{fmt}_f32")(ctx, qb, kb, vb, kcb, vcb, wo, xb, pos,
+                                                         max_seq, H, KVH, hd, theta, hidden)
+    ctx.flush()
+    # oracle: rotate, write position pos, attend, project, add
+    q_r = ora.rope(q.astype(np.float64), H, hd, pos, theta)
+    k_r = ora.rope(k_new.astype(np.float64), KVH, hd, pos, theta)
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[:, pos] = k_r.reshape(KVH, hd).astype(np.float32)
+    vc2[:, pos] = v_new.reshape(KVH, hd)
+    att = ora.attention(q_r, kc2, vc2, H, KVH, hd, pos + 1, max_seq)
+    y, sabs = ora.gemv(fmt, raw, att.astype(np.float32), hidden, q_dim)
+    ref = x0.astype(np.float64) + y
+    W = np.abs(ora.dequant(fmt, raw).reshape(hidden, q_dim).astype(np.float64))
+    eps_a = 1e-5 * np.abs(vc2[:, :pos + 1]).max()
+    got = xb.read(np.float32, hidden)
+    check_close(got, ref, sabs, f"attention+O {fmt} {H}/{KVH}x{hd} pos {pos}",
+                W.sum(axis=1) * eps_a + F32_EPS * np.abs(ref))
+    # the cache row the call wrote: v exact, k the rotated key
+    assert np.array_equal(vcb.read(np.float32, vc.size).reshape(vc.shape)[:, pos], vc2[:, pos])
+    got_k = kcb.read(np.float32, kc.size).reshape(kc.shape)[:, pos].astype(np.float64)
+    assert np.all(np.abs(got_k - kc2[:, pos]) <= 1e-6 * np.abs(k_new).max())

@@ -214,3 +214,32 @@ def test_step_fused_counts_its_launches(ctx):
     n = m.step_fused(5)
     ctx.flush()
     assert n == d.launch_count(ctx) - before == 1 + 5 * 2 + 2
+
+
+def test_full_depth_q4k_m_7b_step_matches_cpu_oracle(ctx):
+    """BASELINE config 4 as one decode step at its real shapes: 28 layers of
+    Qwen2.5-7B (hidden 3584, 28/4 heads × 128, ff 18944, vocab 152064) in the
+    Q4_K_M mix (Q/K/O/gate/up Q4_K; V, down and the LM head Q6_K), kv_len
+    512 — the model, position and graph that bench.py's q4k_m_7b_decode
+    times — against the f64 oracle composition of forward.rs:1470-1787.
+    The captured graph is replayed twice with the cache restored."""
+    cfg = DecodeConfig(layers=28, hidden=3584, heads=28, kv_heads=4, head_dim=128, ff=18944,
+                       vocab=152064, max_seq=1024)
+    m = DecodeModel(ctx, cfg, seed=9, quant=Q4K_M)
+    tok, pos = 1, 511
+    snap = snapshot_cache(m)
+    print(f"[7B Q4_K_M step] oracle, {cfg.layers} layers", flush=True)
+    ref = cpu_step(m, tok, pos)
+    restore_cache(m, snap)
+    m.set_token(tok)
+    g = m.capture(pos, fused=True)
+    for replay in range(2):
+        restore_cache(m, snap)
+        m.set_token(tok)
+        print(f"[7B Q4_K_M step] replay {replay}", flush=True)
+        g.launch()
+        ctx.flush()
+        t = check_logits(m.read(m.logits, cfg.vocab).astype(np.float64), ref, f"7B replay {replay}")
+        assert m.get_token() == t
+    del g
+    m.free()

@@ -59,3 +59,18 @@ def test_device_pointer_arguments_reject_non_integers():
     for bad in (True, False, 1.0, "0x10"):
         with pytest.raises(TypeError):
             _ptr(bad)
+
+
+@pytest.mark.parametrize("ids", [[1, 2, 1000], [5, -1], [1000]])
+def test_verify_and_prefill_reject_ids_outside_the_vocabulary(ids):
+    """The embedding kernel indexes the table with each id unchecked, so ids
+    outside [0, vocab) are refused on the host, before any upload or launch
+    (the model has no context here: a launch would fail differently)."""
+    m = DecodeModel.__new__(DecodeModel)
+    m.ctx, m.cfg, m.lm_fmt = None, DecodeConfig(layers=1, vocab=1000, max_seq=64), "q8_0"
+    with pytest.raises(ValueError, match="out of range"):
+        m.verify_forward(ids, 0)
+    with pytest.raises(ValueError, match="out of range"):
+        m.prefill(ids)
+    with pytest.raises(ValueError, match="out of range"):
+        m.verify_draft(ids[0], ids[1:], 0)
