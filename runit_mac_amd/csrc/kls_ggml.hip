@@ -16,6 +16,12 @@ RT_GEMV_LSK(k_gemv_q4kg_f32_f32add, FmtQ4KG, EPI_F32_ADD, float, 1024)
 RT_GEMV_LSK(k_gemv_q5kg_f32_f32add, FmtQ5KG, EPI_F32_ADD, float, 1024)
 RT_GEMV_LSK(k_gemv_q4_0g_f32_f32add, FmtQ4_0G, EPI_F32_ADD, float, 1024)
 RT_GEMV_LSK(k_gemv_q6kg_f32_f32add, FmtQ6KG, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_ffn_q4kg, FmtQ4KG, EPI_FFN, float, 1024)
+RT_GEMV_LSK(k_ffn_q4_0g, FmtQ4_0G, EPI_FFN, float, 1024)
+RT_GEMV_LSK(k_ffn_q5kg, FmtQ5KG, EPI_FFN, float, 1024)
+RT_GEMV_LSK(k_gemv_q4kg_f32_f32, FmtQ4KG, EPI_F32, float, 1024)
+RT_GEMV_LSK(k_gemv_q4_0g_f32_f32, FmtQ4_0G, EPI_F32, float, 1024)
+RT_GEMV_LSK(k_gemv_q5kg_f32_f32, FmtQ5KG, EPI_F32, float, 1024)
 
 // Q/K (Q4_K) on the small-launch body and V (Q6_K) on the matrix-core body,
 // ggml layouts, in one launch

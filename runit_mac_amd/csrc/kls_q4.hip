@@ -13,6 +13,7 @@ RT_GEMV_LSK(k_gemv_q4_0_f32_f32add, FmtQ4_0, EPI_F32_ADD, float, 1024)
 RT_GEMV_LSK(k_ffn_q4_0, FmtQ4_0, EPI_FFN, float, 1024)
 RT_GEMV_LSK(k_gemv_q4k_f32_f32, FmtQ4K, EPI_F32, float, 1024)
 RT_GEMV_LSK(k_gemv_q4k_f32_f32add, FmtQ4K, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_ffn_q4k, FmtQ4K, EPI_FFN, float, 1024)
 RT_GEMV_LSBV(k_ffn_q4k, FmtQ4K, EPI_FFN, float, 1024)
 
 // Small-launch kernels for Q4_K rows of ≤ 2 KB (the 7B-shape Q and K

@@ -11,6 +11,7 @@ RT_GEMV_LS(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float)
 // projections and the FFNs of long-K models)
 RT_GEMV_LSK(k_gemv_q8_0_f32_f32, FmtQ8_0, EPI_F32, float, 1024)
 RT_GEMV_LSK(k_gemv_q8_0_f32_f32add, FmtQ8_0, EPI_F32_ADD, float, 1024)
+RT_GEMV_LSK(k_ffn_q8_0, FmtQ8_0, EPI_FFN, float, 1024)
 
 // Small-launch kernels (the 0.5B model's norm-fused Q/K/V, O with the
 // attention merge, norm-fused gate+up; plain and residual forms)

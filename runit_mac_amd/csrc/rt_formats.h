@@ -127,10 +127,14 @@ struct FmtQ8_0 {
         return q8_0_block_dot(r[0], qa, xu.x[0]) + q8_0_block_dot(r[8] >> 16, qb, xu.x[1]);
     }
     // matrix-core form: recs = the unit's two records, lq = this lane's limb
+    static constexpr bool XPAIR = true;  // mdotx: the unit's two records' limbs given
     RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
         XLimb xa, xb;
         load_xlimb(xs + 2 * uu, lq, xa);
         load_xlimb(xs + 2 * uu + 1, lq, xb);
+        return mdotx(r, xa, xb);
+    }
+    RT_DEV static float mdotx(const Raw& r, const XLimb& xa, const XLimb& xb) {
         v4i ca = {0, 0, 0, 0}, cb = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -208,10 +212,14 @@ struct FmtQ4_0 {
         }
         return q4_0_block_dot(r.w[0], qa, xu.x[0]) + q4_0_block_dot(r.w[4] >> 16, qb, xu.x[1]);
     }
+    static constexpr bool XPAIR = true;
     RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
         XLimb xa, xb;
         load_xlimb(xs + 2 * uu, lq, xa);
         load_xlimb(xs + 2 * uu + 1, lq, xb);
+        return mdotx(r, xa, xb);
+    }
+    RT_DEV static float mdotx(const Raw& r, const XLimb& xa, const XLimb& xb) {
         // −8·Σx folded into the accumulators' start values
         v4i ca = {-8 * xa.s[0], -8 * xa.s[1], -8 * xa.s[2], 0};
         v4i cb = {-8 * xb.s[0], -8 * xb.s[1], -8 * xb.s[2], 0};
@@ -332,10 +340,14 @@ struct FmtQ4KT {
         return __builtin_amdgcn_ldexpf(vlo, xu.lo.e - 22) +
                __builtin_amdgcn_ldexpf(vhi, xu.hi.e - 22);
     }
+    static constexpr bool XPAIR = true;
     RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
         XLimb xl, xh;
         load_xlimb(xs + 2 * uu, lq, xl);
         load_xlimb(xs + 2 * uu + 1, lq, xh);
+        return mdotx(r, xl, xh);
+    }
+    RT_DEV static float mdotx(const Raw& r, const XLimb& xl, const XLimb& xh) {
         v4i cl = {0, 0, 0, 0}, ch = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -758,10 +770,14 @@ struct FmtQ5_0 {
         split(r, da, qha, qa, db, qhb, qb);
         return q5_0_block_dot(da, qha, qa, xu.x[0]) + q5_0_block_dot(db, qhb, qb, xu.x[1]);
     }
+    static constexpr bool XPAIR = true;
     RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
         XLimb xa, xb;
         load_xlimb(xs + 2 * uu, lq, xa);
         load_xlimb(xs + 2 * uu + 1, lq, xb);
+        return mdotx(r, xa, xb);
+    }
+    RT_DEV static float mdotx(const Raw& r, const XLimb& xa, const XLimb& xb) {
         uint32_t da, qha, qa[4], db, qhb, qb[4];
         split(r, da, qha, qa, db, qhb, qb);
         return q5_0_block_mdot(da, qha, qa, xa) + q5_0_block_mdot(db, qhb, qb, xb);
@@ -873,10 +889,14 @@ struct FmtQ5KT {
         return __builtin_amdgcn_ldexpf(vlo, xu.lo.e - 22) +
                __builtin_amdgcn_ldexpf(vhi, xu.hi.e - 22);
     }
+    static constexpr bool XPAIR = true;
     RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
         XLimb xl, xh;
         load_xlimb(xs + 2 * uu, lq, xl);
         load_xlimb(xs + 2 * uu + 1, lq, xh);
+        return mdotx(r, xl, xh);
+    }
+    RT_DEV static float mdotx(const Raw& r, const XLimb& xl, const XLimb& xh) {
         v4i cl = {0, 0, 0, 0}, ch = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -945,10 +965,14 @@ struct FmtQ4_0G {
         split(r, qa, qb);
         return q4_0g_block_dot(r.w[0], qa, xu.x[0]) + q4_0g_block_dot(r.w[4] >> 16, qb, xu.x[1]);
     }
+    static constexpr bool XPAIR = true;
     RT_DEV static float mdot(const Raw& r, const XRec* xs, uint32_t uu, uint32_t lq) {
         XLimb xa, xb;
         load_xlimb(xs + 2 * uu, lq, xa);
         load_xlimb(xs + 2 * uu + 1, lq, xb);
+        return mdotx(r, xa, xb);
+    }
+    RT_DEV static float mdotx(const Raw& r, const XLimb& xa, const XLimb& xb) {
         uint32_t qa[4], qb[4];
         split(r, qa, qb);
         return q4_0g_block_mdot(r.w[0], qa, xa) + q4_0g_block_mdot(r.w[4] >> 16, qb, xb);

@@ -186,10 +186,13 @@ const char* const kLsBases[] = {
 };
 // Kernels of the workgroup-local K split: <base>_lsk1.
 const char* const kLskBases[] = {
-    "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_gemv_q4_0_f32_f32", "k_gemv_q4_0_f32_f32add",
-    "k_ffn_q4_0", "k_gemv_q4k_f32_f32", "k_gemv_q4k_f32_f32add", "k_gemv_q5k_f32_f32",
-    "k_gemv_q5k_f32_f32add", "k_gemv_q4kg_f32_f32add", "k_gemv_q5kg_f32_f32add", "k_gemv_q4_0g_f32_f32add", "k_gemv_q5_0_f32_f32add",
-    "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32add",
+    "k_ffn_q4_0", "k_ffn_q4_0g", "k_ffn_q4k", "k_ffn_q4kg", "k_ffn_q5_0", "k_ffn_q5k", "k_ffn_q5kg",
+    "k_ffn_q8_0", "k_gemv_q4_0_f32_f32", "k_gemv_q4_0_f32_f32add", "k_gemv_q4_0g_f32_f32",
+    "k_gemv_q4_0g_f32_f32add", "k_gemv_q4k_f32_f32", "k_gemv_q4k_f32_f32add", "k_gemv_q4kg_f32_f32",
+    "k_gemv_q4kg_f32_f32add", "k_gemv_q5_0_f32_f32", "k_gemv_q5_0_f32_f32add", "k_gemv_q5k_f32_f32",
+    "k_gemv_q5k_f32_f32add", "k_gemv_q5kg_f32_f32", "k_gemv_q5kg_f32_f32add",
+    "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32add", "k_gemv_q8_0_f32_f32",
+    "k_gemv_q8_0_f32_f32add",
 };
 // Small-launch kernels: <base>_sm1, <base>_sm2.
 const char* const kSmBases[] = {
@@ -215,24 +218,25 @@ struct Fmt {
     uint32_t mq_unit_el = 0;  // matrix-core path unit, if it differs from unit_el
     bool q40perm = false;     // activation records in the reference Q4_0 order
     uint32_t ls_chunk = 3072;  // LDS-streamed K split: chunk bytes per row (at most)
+    bool xpair = false;        // units of two whole records (the K-split body can hold their limbs)
     uint32_t mq_units() const { return mq_unit_el ? mq_unit_el : unit_el; }
 };
 // Q8_0 / Q4_0 kernels take two blocks per unit (4-byte-aligned loads); rows
 // with an odd number of blocks use the one-block "_s1" kernels.
 constexpr Fmt kQ8_0S{32, 34, 32, 2, "Q8_0", nullptr};
 constexpr Fmt kQ4_0S{32, 18, 32, 4, "Q4_0", nullptr, 0, true};
-constexpr Fmt kQ8_0{32, 34, 64, 1, "Q8_0", &kQ8_0S};
-constexpr Fmt kQ4_0{32, 18, 64, 2, "Q4_0", &kQ4_0S, 0, true};
-constexpr Fmt kQ4K{256, 144, 64, 1, "Q4_K", nullptr};
+constexpr Fmt kQ8_0{32, 34, 64, 1, "Q8_0", &kQ8_0S, 0, false, 3072, true};
+constexpr Fmt kQ4_0{32, 18, 64, 2, "Q4_0", &kQ4_0S, 0, true, 3072, true};
+constexpr Fmt kQ4K{256, 144, 64, 1, "Q4_K", nullptr, 0, false, 3072, true};
 constexpr Fmt kQ6K{256, 210, 64, 1, "Q6_K", nullptr, 256};  // matrix-core: one block per lane
 constexpr Fmt kQ5_0S{32, 22, 32, 4, "Q5_0", nullptr};
-constexpr Fmt kQ5_0{32, 22, 64, 2, "Q5_0", &kQ5_0S};
-constexpr Fmt kQ5K{256, 176, 64, 1, "Q5_K", nullptr, 0, false, 2048};  // (2 KB chunks: 18.0 against 19.4 µs for 3 KB)
+constexpr Fmt kQ5_0{32, 22, 64, 2, "Q5_0", &kQ5_0S, 0, false, 3072, true};
+constexpr Fmt kQ5K{256, 176, 64, 1, "Q5_K", nullptr, 0, false, 2048, true};  // (2 KB chunks: 18.0 against 19.4 µs for 3 KB)
 // ggml layouts (upstream GGUF files)
 constexpr Fmt kQ4_0GS{32, 18, 32, 4, "Q4_0 (ggml)", nullptr};
-constexpr Fmt kQ4_0G{32, 18, 64, 2, "Q4_0 (ggml)", &kQ4_0GS};
-constexpr Fmt kQ4KG{256, 144, 64, 1, "Q4_K (ggml)", nullptr};
-constexpr Fmt kQ5KG{256, 176, 64, 1, "Q5_K (ggml)", nullptr, 0, false, 2048};
+constexpr Fmt kQ4_0G{32, 18, 64, 2, "Q4_0 (ggml)", &kQ4_0GS, 0, false, 3072, true};
+constexpr Fmt kQ4KG{256, 144, 64, 1, "Q4_K (ggml)", nullptr, 0, false, 3072, true};
+constexpr Fmt kQ5KG{256, 176, 64, 1, "Q5_K (ggml)", nullptr, 0, false, 2048, true};
 constexpr Fmt kQ6KG{256, 210, 64, 1, "Q6_K (ggml)", nullptr, 256};
 // Q6_K on the matrix-core path with 64-element lane units (small launches:
 // four times the lanes of the one-super-block-per-lane form)
@@ -272,6 +276,7 @@ struct rt_ctx {
     uint64_t launches = 0;       // kernel launches enqueued so far (rt_launch_count)
     bool gemv_valu = false;      // RUNIT_GEMV_VALU=1: VALU-dot twins of the LDS body (A/B)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
+    bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
@@ -465,7 +470,7 @@ bool has_ls_kernel(const rt_ctx* c, const char* kname) {
 // Workgroup-local K split (rt_gemv_ls.h, *_lsk1): every K chunk of a row
 // quad in one workgroup, 1 KB row chunks, the whole K's activation records in
 // LDS; the chunks' partial sums meet in LDS.
-int gemv_launch_lsk(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
+int gemv_launch_lsk(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a, bool whole = false) {
     char name[96];
     snprintf(name, sizeof name, "%s_lsk1", kname);
     if (!c->fns.count(name)) return kLsDecline;
@@ -483,6 +488,10 @@ int gemv_launch_lsk(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     kc = (kc + gu - 1) / gu * gu;
     S = (units + kc - 1) / kc;
     const uint32_t nq = (a.nvrows + 3) / 4;
+    // A whole-K launch takes this body only where each wave keeps one chunk
+    // (16 waves a multiple of S) of ≤ 2 steps of 16 units, whose activation
+    // limbs it then holds in registers (formats with two-record units)
+    if (whole && !(f.xpair && 16 % S == 0 && kc <= 32)) return kLsDecline;
     // Taken where the whole K's activation records stay small (≤ 32 KB, K ≤
     // 9,362: the 0.5B model's down projection, 896×4864, runs 1.3 µs faster
     // than with the K split through memory) and the units suit 1024-thread
@@ -548,6 +557,16 @@ int gemv_launch_ls(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
         if (NI > kLsMaxNI) return kLsDecline;
     }
     const uint32_t nq = (a.nvrows + 3) / 4;
+    // Whole-K launches of ≥ 16 row quads per CU (the 7B FFNs) on the
+    // K-split body: every workgroup owns nq / nwg whole quads, its waves
+    // take (quad, 1 KB chunk) items, so waves differ by at most one 4 KB
+    // item (dealt whole quads of 8 KB left 30% of the 7B FFN's waves a third
+    // item), and the activation limbs stay in registers.  Q4_K FFN 2×18944
+    // ×3584: 21.0 → 18.3 µs, Q4_0: 19.5 → 17.3 µs.
+    if (S == 1 && c->lsk_whole && (uint64_t)nq >= (uint64_t)c->cu_count * c->ls_min_items) {
+        const int st = gemv_launch_lsk(c, kname, f, a, true);
+        if (st != kLsDecline) return st;
+    }
     if (S > 1 && !a.gamma) {
         const int st = gemv_launch_lsk(c, kname, f, a);
         if (st != kLsDecline) return st;
@@ -1235,6 +1254,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_SM")) c->sm_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_VALU")) c->gemv_valu = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMV_LSK_WHOLE")) c->lsk_whole = atoi(g) != 0;
     std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
     auto unload = [](rt_ctx* cc) {
         for (hipModule_t m : cc->modules) hipModuleUnload(m);
@@ -2965,10 +2985,16 @@ int rt_decode_step_status(rt_ctx* c, rt_step* st) {
     hipError_t e = hipMemcpy(&status, (char*)st->sync + RT_STEP_STATUS_OFF, 4,
                              hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(c, e, "decode_step status");
-    if (status)
+    if (status) {
+        // reported once: cleared so that the next runs report their own
+        // outcome (the token of the run that timed out is not valid)
+        const uint32_t zero = 0;
+        e = hipMemcpy((char*)st->sync + RT_STEP_STATUS_OFF, &zero, 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(c, e, "decode_step status reset");
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: decode_step: a grid barrier timed out (workgroups "
                     "not all resident?)");
+    }
     return RT_OK;
 }
 
