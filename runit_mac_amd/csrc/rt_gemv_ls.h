@@ -337,6 +337,8 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
     // registers for all its items.
     constexpr bool XP = fmt_xpair<F>(0) && !VALU;
     const bool xreg = XP && nwaves % S == 0 && kcu <= 32;
+    __shared__ uint32_t qcnt[16];  // per chunk: quads taken past the dealt ones
+    if (tid < 16) qcnt[tid] = 0;   // (ordered before use by the staging barrier)
     Item buf;
     issue(0, buf);
     if (one_pass)
@@ -359,10 +361,35 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
                 load_xlimb(xc + 2 * uc + 1, lq, xb[st]);
             }
             const uint32_t nsteps = (units + 15) / 16;
-            // item j from the wave's slot
-            auto work = [&](uint32_t j) {
-                const uint32_t it = item_of(j);
-                const uint32_t ql = it / S;
+            // quad ql of this wave's chunk: loads of its four row chunks
+            // (ql ≥ nql: dropped)
+            auto issue_q = [&](uint32_t ql, Item& dst) {
+                const bool none = ql >= nql;
+                const uint32_t quad = wg + nwg * min(ql, nql - 1);
+                const uint32_t cbytes = units * F::UNIT_EL / F::BLK_EL * F::BLK_BYTES;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint8_t* src = row_src(quad * 4 + r, c);
+                    const uint8_t* base = src - ((uintptr_t)src & 15);
+                    const uint32_t last = (uint32_t)(((uintptr_t)src & 15) + cbytes - 1) & ~15u;
+#pragma unroll
+                    for (int i = 0; i < NI; ++i) {
+                        const uint32_t off = min((uint32_t)(i * 64 + lane) * 16, last);
+                        dst[r][i] = load16_or_none(base, off, none);
+                    }
+                }
+            };
+            // the next quad of the wave's chunk from the workgroup's counter
+            // (the first nwaves / S quads of each chunk are dealt statically)
+            auto draw = [&]() -> uint32_t {
+                uint32_t v = 0;
+                if (lane == 0) v = __hip_atomic_fetch_add(&qcnt[c], 1u, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_WORKGROUP);
+                return nwaves / S + __builtin_amdgcn_readfirstlane(v);
+            };
+            // quad ql from the wave's slot
+            auto work = [&](uint32_t ql) {
+                const uint32_t it = ql * S + c;
                 const uint8_t* rowl =
                     wslot + q * RS + ((uintptr_t)row_src((wg + nwg * ql) * 4 + q, c) & 15);
                 float acc = 0.0f;
@@ -383,12 +410,21 @@ RT_DEV void gemv_lsk_body(const GemvArgs& a) {
                 acc += __shfl_xor(acc, 32, 64);
                 if (slot == 0) res[it * 4 + q] = acc;
             };
-            // one item in flight (two per wave streamed slower: 7B Q4_K FFN
-            // 18.3 → 19.8 µs, Q4_0 17.3 → 18.7 µs)
-            for (uint32_t j = 0; j < nitems; ++j) {
+            // One item in flight (two per wave streamed slower: 7B Q4_K FFN
+            // 18.3 → 19.8 µs, Q4_0 17.3 → 18.7 µs).  After its first quad a
+            // wave takes the next quad of its chunk from the workgroup's
+            // counter, drawn one item ahead: waves whose data comes back
+            // sooner take more quads, instead of the workgroup waiting for
+            // its slowest wave's fixed share.
+            uint32_t qcur = wave / S;
+            uint32_t qnext = qcur < nql ? draw() : nql;
+            while (qcur < nql) {
                 commit(buf);
-                issue(j + 1, buf);
-                work(j);
+                issue_q(qnext, buf);
+                const uint32_t qnn = qnext < nql ? draw() : nql;
+                work(qcur);
+                qcur = qnext;
+                qnext = qnn;
             }
             goto combine;
         }
