@@ -332,28 +332,60 @@ def bench_decode(ctx, steps: int, warmup: int, verify_forms: bool = True) -> dic
     prefill_ms = float("nan")
     if verify_forms:
         prefill_ms = _bench_prefill(ctx, m, cfg, P, steps)
-    # dominant kernel of the fused step: the norm-fused gate+up+SiLU GEMV,
-    # 24 launches per token.  Timed live over the model's own 24 layers.
-    ctx.capture_begin()
-    for L in m.layers:
-        d.rms_norm_fused_ffn_q8_0_f32(ctx, L["wg"], L["wu"], m.x, L["ffn_norm"], cfg.eps, m.act,
-                                      cfg.ff, cfg.hidden)
-    g = ctx.capture_end()
-    for _ in range(max(1, warmup)):
-        g.launch()
-    ctx.flush()
-    e0, e1 = ctx.event(), ctx.event()
-    reps = max(20, steps)
-    e0.record()
-    for _ in range(reps):
-        g.launch()
-    e1.record()
-    ffn_us = e0.elapsed_ms(e1) * 1e3 / (reps * cfg.layers)
-    del g
-    ffn_bytes = 2 * d.weight_bytes("q8_0", cfg.ff, cfg.hidden) + 4 * cfg.hidden * 2 + 4 * cfg.ff
+    # the step's single-kernel launches, each timed live over the model's own
+    # 24 layers (a graph of 24 launches on the library stream, HIP events
+    # around its replays): norm-fused Q/K/V + bias, norm-fused gate+up+SiLU,
+    # down + residual.  The roofline reports the one with the most time per
+    # token.
+    h, ff, kvd = cfg.hidden, cfg.ff, cfg.kv_dim
+
+    def live_us(launch) -> float:
+        ctx.capture_begin()
+        for L in m.layers:
+            launch(L)
+        g = ctx.capture_end()
+        for _ in range(max(1, warmup)):
+            g.launch()
+        ctx.flush()
+        e0, e1 = ctx.event(), ctx.event()
+        reps = max(20, steps)
+        e0.record()
+        for _ in range(reps):
+            g.launch()
+        e1.record()
+        us = e0.elapsed_ms(e1) * 1e3 / (reps * cfg.layers)
+        del g
+        return us
+
+    wq = d.weight_bytes("q8_0", cfg.q_dim + 2 * kvd, h)
+    kernels = {
+        "k_ffn_q8_0_sm1": {
+            "role": "rms_norm + gate/up 2x4864x896 + SiLU (small-launch body)",
+            "us": live_us(lambda L: d.rms_norm_fused_ffn_q8_0_f32(
+                ctx, L["wg"], L["wu"], m.x, L["ffn_norm"], cfg.eps, m.act, ff, h)),
+            # weights + x + gamma + act
+            "bytes": 2 * d.weight_bytes("q8_0", ff, h) + 4 * h * 2 + 4 * ff,
+            "pmc": "ffn_q8_0_0p5b_pmc_traffic.md"},
+        "k_gemv_q8_0_f32_f32add_lsk1": {
+            "role": "down 896x4864 + residual (workgroup-local K split)",
+            "us": live_us(lambda L: d.gemv_q8_0_add_f32_f32in(ctx, L["wd"], m.act, m.x, m.x, h, ff)),
+            # weights + act + residual read + output write
+            "bytes": d.weight_bytes("q8_0", h, ff) + 4 * ff + 4 * h + 4 * h,
+            "pmc": "down_q8_0_0p5b_pmc_traffic.md"},
+        "k_qkv_bias_q8_0_sm1": {
+            "role": "rms_norm + Q/K/V 1152x896 + bias (small-launch body)",
+            "us": live_us(lambda L: d.rms_norm_fused_qkv_bias_q8_0_f32(
+                ctx, L["wq"], L["wk"], L["wv"], m.x, L["attn_norm"], cfg.eps, m.q, m.k, m.v,
+                L["bq"], L["bk"], L["bv"], cfg.q_dim, kvd, h)),
+            # weights + x + gamma + f16 biases + outputs
+            "bytes": wq + 4 * h * 2 + 2 * (cfg.q_dim + 2 * kvd) + 4 * (cfg.q_dim + 2 * kvd),
+            "pmc": None},
+    }
+    for kk in kernels.values():
+        kk["us_per_token"] = kk["us"] * cfg.layers
     return {"cfg": cfg, "model": m, "pos": pos, "gpu_token": gpu_token, "step": step,
             "ms_persistent": res["persistent"], "ms_fused": res["fused"], "ms_reference": res["reference_sequence"],
-            "step_bytes": cfg.step_bytes(pos + 1), "ffn_us": ffn_us, "ffn_bytes": ffn_bytes,
+            "step_bytes": cfg.step_bytes(pos + 1), "kernels": kernels,
             "launches_fused": m.launches_fused(),
             "launches_reference": 1 + 10 * cfg.layers + 3, "verify_ms": verify,
             "prefill_ms": prefill_ms, "prefill_tokens": P}
@@ -520,6 +552,21 @@ def profile_pass(ctx, launches: int = 24) -> None:
     for g, u in mats:
         d.rms_norm_fused_ffn_q8_0_f32(ctx, g, u, x, gamma, cfg.eps, act, ff, h)
     ctx.flush()
+    # the 0.5B down projection + residual (896x4864, workgroup-local K split)
+    # over the same number of replicas
+    wd5 = d.weight_bytes("q8_0", h, ff)
+    arena_d5 = _arena_for(ctx, [wd5], launches)
+    downs5 = []
+    for r in range(launches):
+        w = arena_d5.take(wd5)
+        d.synth_weights(ctx, "q8_0", w, h * ff // 32, 200 + r)
+        downs5.append(w)
+    y5 = ctx.new_buffer(4 * h)
+    d.synth_normal_f32(ctx, y5, h, 9)
+    ctx.flush()
+    for w in downs5:
+        d.gemv_q8_0_add_f32_f32in(ctx, w, act, y5, y5, h, ff)
+    ctx.flush()
     # the 7B Q4_K gate+up+SiLU (LDS-streamed body) over 8 replicas of 76 MB
     ff7, h7 = 18944, 3584
     wb7 = d.weight_bytes("q4k", ff7, h7)
@@ -557,10 +604,12 @@ def profile_pass(ctx, launches: int = 24) -> None:
         d.stream_copy(ctx, dst, src, copy_bytes)
     ctx.flush()
     log(f"profile pass: {launches} x k_ffn_q8_0 ({2 * wb} weight bytes each), "
+        f"{launches} x k_gemv_q8_0_f32_f32add ({wd5} weight bytes each), "
         f"8 x k_ffn_q4k ({2 * wb7} weight bytes each), "
         f"3 x k_stream_copy ({copy_bytes} bytes each)")
-    for b in (src, dst, x, gamma, act, x7, act7):
+    for b in (src, dst, x, gamma, act, x7, act7, y5):
         b.free()
+    arena_d5.free()
     arena.free()
     arena7.free()
 
@@ -600,7 +649,11 @@ def main():
         cfg = dec["cfg"]
         ms = dec["ms_fused"]
         tok_s = 1e3 / ms
-        ffn_gbs = dec["ffn_bytes"] / (dec["ffn_us"] * 1e-6) / 1e9
+        # the roofline kernel: the step's single-kernel launch with the most
+        # time per token (all three are 24 launches per token)
+        kname = max(dec["kernels"], key=lambda k: dec["kernels"][k]["us_per_token"])
+        kern = dec["kernels"][kname]
+        kern_gbs = kern["bytes"] / (kern["us"] * 1e-6) / 1e9
         log(f"decode step (fused graph, {dec['launches_fused']} launches): {ms * 1e3:.1f} us "
             f"= {tok_s:.1f} tok/s; reference sequence ({dec['launches_reference']} launches): "
             f"{dec['ms_reference'] * 1e3:.1f} us; step bytes {dec['step_bytes'] / 1e6:.1f} MB "
@@ -613,8 +666,10 @@ def main():
         if dec["verify_ms"]:
             log(f"prefill of {dec['prefill_tokens']} tokens: {dec['prefill_ms']:.2f} ms = "
                 f"{dec['prefill_tokens'] / dec['prefill_ms'] * 1e3:.0f} tok/s")
-        log(f"dominant kernel rms_norm+fused_ffn_q8_0 4864x896x2: {dec['ffn_us']:.2f} us, "
-            f"{ffn_gbs:.0f} GB/s")
+        for kn, kk in dec["kernels"].items():
+            log(f"live kernel {kn} ({kk['role']}): {kk['us']:.2f} us x {cfg.layers} per token, "
+                f"{kk['bytes'] / (kk['us'] * 1e-6) / 1e9:.0f} GB/s"
+                + ("  <- roofline kernel" if kn == kname else ""))
         line.update({
             "value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms, 5),
             "dtype": "q8_0 x f32 (int8 matrix-core dots, f32 scales/accumulate)",
@@ -622,12 +677,19 @@ def main():
                                    "batch 1, kv_len 512 (24 layers, hidden 896, 14/2 heads x 64, "
                                    "ff 4864, vocab 151936), one HIP-graph replay per token",
                        "global_batch": 1, "kv_len": 512},
-            "roofline": {"bound": "hbm", "kernel": "k_ffn_q8_0_sm1 (rms_norm + gate/up + SiLU, small-launch body)",
-                         "achieved": round(ffn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(ffn_gbs / HBM_PEAK_GBS, 4),
-                         "traffic": measured_traffic("ffn_q8_0_0p5b_pmc_traffic.md"),
-                         "bytes_per_launch": dec["ffn_bytes"],
-                         "avg_launch_us": round(dec["ffn_us"], 3)},
+            "roofline": {"bound": "hbm", "kernel": f"{kname} ({kern['role']})",
+                         "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic(kern["pmc"]) if kern["pmc"] else None,
+                         "bytes_per_launch": kern["bytes"],
+                         "avg_launch_us": round(kern["us"], 3),
+                         "us_per_token": round(kern["us_per_token"], 1),
+                         "others": {kn: {"us": round(kk["us"], 3), "bytes_per_launch": kk["bytes"],
+                                         "frac": round(kk["bytes"] / (kk["us"] * 1e-6) / 1e9
+                                                       / HBM_PEAK_GBS, 4),
+                                         "traffic": (measured_traffic(kk["pmc"]) if kk["pmc"]
+                                                     else None)}
+                                    for kn, kk in dec["kernels"].items() if kn != kname}},
             "decode": {"tok_s": round(tok_s, 2), "us_per_token": round(ms * 1e3, 1),
                        "reference_sequence_us_per_token": round(dec["ms_reference"] * 1e3, 1),
                        "launches_per_token": dec["launches_fused"],

@@ -26,7 +26,7 @@ KERNEL_DIR = os.path.join(LIB_DIR, "kernels")
 # kernel translation units (csrc/<name>.hip → lib/kernels/<name>.hsaco)
 KERNEL_UNITS = ("kg_q8_0", "kg_q4", "kg_q5", "kg_q6k", "kg_ggml", "kls_q8_0", "kls_q4", "kls_q5",
                 "kls_q6k", "kls_ggml", "kgx_rows", "k_gemm", "k_aux", "k_decode", "k_step",
-                "k_scratch")
+                "k_scratch", "kvs")
 HOST_LIB = os.path.join(LIB_DIR, "librunit_hip.so")
 
 # -packed-fp32-ops: no v_pk_*_f32 (their results have been unreliable on the

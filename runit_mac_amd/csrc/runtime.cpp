@@ -194,6 +194,10 @@ const char* const kLskBases[] = {
     "k_gemv_q6k_f32_f32add", "k_gemv_q6kg_f32_f32add", "k_gemv_q8_0_f32_f32",
     "k_gemv_q8_0_f32_f32add",
 };
+// VALU small-launch kernels: <base>_vs, and with the norm in the body <base>_vsn.
+const char* const kVsBases[] = {"k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_qkv_bias_q8_0",
+                                "k_ffn_q8_0"};
+const char* const kVsnBases[] = {"k_gemv_q8_0_f32_f32", "k_qkv_bias_q8_0", "k_ffn_q8_0"};
 // Small-launch kernels: <base>_sm1, <base>_sm2.
 const char* const kSmBases[] = {
     "k_gemv_q8_0_f32_f32", "k_gemv_q8_0_f32_f32add", "k_qkv_bias_q8_0", "k_ffn_q8_0",
@@ -277,6 +281,7 @@ struct rt_ctx {
     bool gemv_valu = false;      // RUNIT_GEMV_VALU=1: VALU-dot twins of the LDS body (A/B)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
+    bool vs_enabled = true;      // RUNIT_GEMV_VS=0: no VALU small-launch body (A/B)
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
@@ -290,6 +295,8 @@ struct rt_ctx {
     // the scratch array and never grow.
     uint8_t* scratch = nullptr;
     bool noalloc = false;
+    // workspace buffers replaced by larger ones (freed with the context)
+    std::vector<void*> retired;
 };
 struct rt_event { hipEvent_t ev; };
 struct rt_graph { hipGraph_t graph; hipGraphExec_t exec; };
@@ -436,9 +443,10 @@ int ensure_buf(rt_ctx* c, void*& buf, size_t& bytes, size_t need, const char* wh
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: %s: workspace must be sized before graph capture", who);
     if (buf) {
-        hipError_t e = hipStreamSynchronize(c->stream);
-        if (e != hipSuccess) return hip_fail(c, e, "workspace sync");
-        (void)hipFree(buf);
+        // the old buffer stays allocated until the context is destroyed: a
+        // graph captured before this growth holds its address in its kernel
+        // arguments and may still be replayed
+        c->retired.push_back(buf);
         buf = nullptr;
         bytes = 0;
     }
@@ -664,6 +672,37 @@ int gemv_launch_sm(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     return launch(c, name, dim3(grid), dim3(kSmThreads), lds, params);
 }
 
+// VALU small-launch body (rt_gemv_vs.h, *_vs / *_vsn): Q8_0, whole K, f32
+// activations (no merged attention input), a lane per (row, 32-element
+// block), ⌈K/32/16⌉ waves per row quad, the norm in the body for K ≤ 1024.
+// Taken for launches of at most kVsMaxQuadsPerCu row quads per CU: the 0.5B
+// model's norm-fused Q/K/V (1152×896: 4.07 → 3.65 µs) and down + residual
+// (896×4864: 5.64 → 4.02 µs).  Its per-lane 34-byte block loads and
+// per-lane activation reads cost more than they save on larger launches
+// (0.5B norm-fused gate+up 2×4864×896: 5.57 → 11.1 µs).
+constexpr uint32_t kVsMaxQuadsPerCu = 2;
+int gemv_launch_vs(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
+    // (a merged attention input stays on the small-launch body: merging 8
+    // splits per lane made the 0.5B attention + O pair 8.9 → 9.1 µs)
+    if (f.blk_bytes != 34 || f.blk_el != 32 || a.x_rec || a.xnsp || a.nx > 1) return kLsDecline;
+    if (a.gamma && a.K > 1024) return kLsDecline;
+    const uint32_t nb = a.K / 32;
+    const uint32_t wpq = (nb + 15) / 16;
+    if (wpq > 16) return kLsDecline;  // (K ≤ 8192: the quad's waves in one workgroup)
+    const uint32_t nq = (a.nvrows + 3) / 4;
+    if (nq > (uint64_t)c->cu_count * kVsMaxQuadsPerCu) return kLsDecline;
+    char name[96];
+    snprintf(name, sizeof name, "%s_%s", kname, a.gamma ? "vsn" : "vs");
+    if (!c->fns.count(name)) return kLsDecline;
+    // quads per workgroup: enough workgroups for every CU, ≤ 1024 threads
+    const uint32_t qmax = 16 / wpq;
+    const uint32_t qpw = std::max<uint32_t>(
+        1, std::min<uint32_t>(qmax, (nq + (uint32_t)c->cu_count - 1) / (uint32_t)c->cu_count));
+    const uint32_t grid = (nq + qpw - 1) / qpw;
+    void* params[] = {&a};
+    return launch(c, name, dim3(grid), dim3(qpw * wpq * 64), 0, params);
+}
+
 int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x_f16,
                 bool paired = false) {
     const bool single = fmt.single && (a.K % fmt.unit_el) != 0;
@@ -681,6 +720,10 @@ int gemv_launch(rt_ctx* c, const char* kname, const Fmt& fmt, GemvArgs a, bool x
                     "kernel dispatch error: %s: input must be %d-byte aligned", kname,
                     x_f16 ? 8 : 16);
     a.row_bytes = (uint64_t)(a.K / f.blk_el) * f.blk_bytes;
+    if (c->vs_enabled && !x_f16 && a.nblk == 0) {
+        const int st = gemv_launch_vs(c, kname, f, a);
+        if (st != kLsDecline) return st;
+    }
     if (c->sm_enabled && !single && !x_f16 && a.nx <= 1 && a.nblk == 0) {
         const int st = gemv_launch_sm(c, kname, f, a);
         if (st != kLsDecline) return st;
@@ -1255,6 +1298,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_VALU")) c->gemv_valu = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LSK_WHOLE")) c->lsk_whole = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMV_VS")) c->vs_enabled = atoi(g) != 0;
     std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
     auto unload = [](rt_ctx* cc) {
         for (hipModule_t m : cc->modules) hipModuleUnload(m);
@@ -1279,6 +1323,8 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     for (const char* b : kLsBases)
         for (uint32_t ni = 1; ni <= kLsMaxNI; ++ni) names.push_back(std::string(b) + "_ls" + std::to_string(ni));
     for (const char* b : kLskBases) names.push_back(std::string(b) + "_lsk1");
+    for (const char* b : kVsBases) names.push_back(std::string(b) + "_vs");
+    for (const char* b : kVsnBases) names.push_back(std::string(b) + "_vsn");
     for (const char* b : kSmBases)
         for (uint32_t ni = 1; ni <= 2; ++ni) names.push_back(std::string(b) + "_sm" + std::to_string(ni));
     for (const char* b : {"k_qkv2_bias_q4k_q6k", "k_qkv2_q4k_q6k", "k_qkv2_bias_q4kg_q6kg", "k_qkv2_q4kg_q6kg"})
@@ -1353,6 +1399,7 @@ void rt_ctx_destroy(rt_ctx* c) {
     if (c->part) hipFree(c->part);
     if (c->attn_out) hipFree(c->attn_out);
     if (c->aux) hipFree(c->aux);
+    for (void* p : c->retired) hipFree(p);
     for (hipModule_t m : c->modules) hipModuleUnload(m);
     delete c;
 }
