@@ -261,6 +261,44 @@ def _bench_prefill(ctx, m, cfg, P: int, steps: int) -> float:
     return e0.elapsed_ms(e1) / reps
 
 
+def bench_verify_eager(ctx, steps: int) -> dict:
+    """The batched verify passes (M = 4, 8, 16 on the multi-row GEMVs; 16, 32
+    on the GEMMs) and a 512-token prefill of the 0.5B model, launched eagerly
+    (no graph), for kernel traces of their kernels: rocprofv3 --kernel-trace
+    ends in a host-side fault when it traces the replay of their graphs."""
+    from runit_mac_amd.decode import DecodeConfig, DecodeModel
+    cfg = DecodeConfig()
+    m = DecodeModel(ctx, cfg, seed=7)
+    pos, out = 511, {}
+    for M, form in ((4, "rows"), (8, "rows"), (16, "rows"), (16, "gemm"), (32, "gemm")):
+        m.verify_forward([1] * M, pos, form)  # uploads the ids, sizes the buffers
+        ctx.flush()
+        e0, e1 = ctx.event(), ctx.event()
+        e0.record()
+        for _ in range(steps):
+            m.verify_pass(M, pos, form)
+        e1.record()
+        out[f"{form}_m{M}"] = e0.elapsed_ms(e1) * 1e3 / steps
+        log(f"verify pass ({form}, eager launches), {M} tokens: {out[f'{form}_m{M}']:.1f} us")
+    P = 512
+    m._verify_arena(P, logits=False)
+    toks = np.arange(P, dtype=np.uint32) % cfg.vocab
+    ctx._check(d.load_library().rt_upload(ctx.handle, m._vbufs["tok"], toks.ctypes.data,
+                                          toks.nbytes))
+    m.verify_pass(P, 0, last_only=True)
+    ctx.flush()
+    e0, e1 = ctx.event(), ctx.event()
+    reps = max(3, steps // 10)
+    e0.record()
+    for _ in range(reps):
+        m.verify_pass(P, 0, last_only=True)
+    e1.record()
+    out["prefill_512"] = e0.elapsed_ms(e1) * 1e3 / reps
+    log(f"prefill of {P} tokens (eager launches): {out['prefill_512'] / 1e3:.2f} ms")
+    m.free()
+    return out
+
+
 def bench_decode(ctx, steps: int, warmup: int, verify_forms: bool = True) -> dict:
     """Config 2: one greedy decode step of the 0.5B Q8_0 shape at kv_len 512,
     captured as one HIP graph and replayed (one replay = one token)."""
@@ -340,6 +378,9 @@ def bench_decode(ctx, steps: int, warmup: int, verify_forms: bool = True) -> dic
     h, ff, kvd = cfg.hidden, cfg.ff, cfg.kv_dim
 
     def live_us(launch) -> float:
+        launch(m.layers[0])  # eager: names the kernel the library chose
+        ctx.flush()
+        names.append(d.last_launch_name(ctx))
         ctx.capture_begin()
         for L in m.layers:
             launch(L)
@@ -358,22 +399,23 @@ def bench_decode(ctx, steps: int, warmup: int, verify_forms: bool = True) -> dic
         return us
 
     wq = d.weight_bytes("q8_0", cfg.q_dim + 2 * kvd, h)
+    names = []
     kernels = {
-        "k_ffn_q8_0_sm1": {
-            "role": "rms_norm + gate/up 2x4864x896 + SiLU (small-launch body)",
+        "ffn": {
+            "role": "rms_norm + gate/up 2x4864x896 + SiLU",
             "us": live_us(lambda L: d.rms_norm_fused_ffn_q8_0_f32(
                 ctx, L["wg"], L["wu"], m.x, L["ffn_norm"], cfg.eps, m.act, ff, h)),
             # weights + x + gamma + act
             "bytes": 2 * d.weight_bytes("q8_0", ff, h) + 4 * h * 2 + 4 * ff,
             "pmc": "ffn_q8_0_0p5b_pmc_traffic.md"},
-        "k_gemv_q8_0_f32_f32add_lsk1": {
-            "role": "down 896x4864 + residual (workgroup-local K split)",
+        "down": {
+            "role": "down 896x4864 + residual",
             "us": live_us(lambda L: d.gemv_q8_0_add_f32_f32in(ctx, L["wd"], m.act, m.x, m.x, h, ff)),
             # weights + act + residual read + output write
             "bytes": d.weight_bytes("q8_0", h, ff) + 4 * ff + 4 * h + 4 * h,
             "pmc": "down_q8_0_0p5b_pmc_traffic.md"},
-        "k_qkv_bias_q8_0_sm1": {
-            "role": "rms_norm + Q/K/V 1152x896 + bias (small-launch body)",
+        "qkv": {
+            "role": "rms_norm + Q/K/V 1152x896 + bias",
             "us": live_us(lambda L: d.rms_norm_fused_qkv_bias_q8_0_f32(
                 ctx, L["wq"], L["wk"], L["wv"], m.x, L["attn_norm"], cfg.eps, m.q, m.k, m.v,
                 L["bq"], L["bk"], L["bv"], cfg.q_dim, kvd, h)),
@@ -381,6 +423,8 @@ def bench_decode(ctx, steps: int, warmup: int, verify_forms: bool = True) -> dic
             "bytes": wq + 4 * h * 2 + 2 * (cfg.q_dim + 2 * kvd) + 4 * (cfg.q_dim + 2 * kvd),
             "pmc": None},
     }
+    # keyed by the kernel the library launched for each
+    kernels = {nm: dict(kk, launch=key) for nm, (key, kk) in zip(names, kernels.items())}
     for kk in kernels.values():
         kk["us_per_token"] = kk["us"] * cfg.layers
     return {"cfg": cfg, "model": m, "pos": pos, "gpu_token": gpu_token, "step": step,
@@ -619,7 +663,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--suite", default="all", choices=["all", "gemv", "quick", "decode", "step", "q4decode"])
+    ap.add_argument("--suite", default="all",
+                    choices=["all", "gemv", "quick", "decode", "step", "q4decode", "verify"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-verify", action="store_true",
                     help="skip the verify / prefill graphs (rocprofv3 --kernel-trace runs)")
@@ -635,6 +680,11 @@ def main():
     ctx = d.HipContext()
     if args.profile_pass:
         profile_pass(ctx)
+        return
+    if args.suite == "verify":
+        # eager verify / prefill passes for kernel traces; prints no JSON
+        bench_verify_eager(ctx, args.steps)
+        ctx.close()
         return
     line = {
         "metric": "quant GEMV HBM GB/s (% of peak) + decode tok/s, 0.5B Q8_0 & 7B Q4_K",

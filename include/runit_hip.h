@@ -598,6 +598,10 @@ int rt_decode_attention_rope_oproj_q4kg_f32(rt_ctx* ctx, const float* q_raw, con
                                             uint32_t hidden);
 /* Kernel launches enqueued on the context so far (graph capture included). New. */
 uint64_t rt_launch_count(const rt_ctx* ctx);
+/* Name of the kernel the context launched last ("" before the first launch;
+ * valid until the next call on the context).  New: for profiles and
+ * benchmarks that label a launch by the kernel the library chose. */
+const char* rt_last_launch_name(const rt_ctx* ctx);
 /* add_f16_into_f32 (dispatch.rs:316-330): acc[i] += f32(src[i]) for i < n
  * (the bias add of the separate-dispatch Q/K/V fallback, forward.rs:1561-1568). */
 int rt_add_f16_into_f32(rt_ctx* ctx, const uint16_t* src, float* acc, uint32_t n);

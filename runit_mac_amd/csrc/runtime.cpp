@@ -278,6 +278,7 @@ struct rt_ctx {
     bool ls_enabled = true;      // RUNIT_GEMV_LS=0: the per-lane-load matrix-core body instead
     bool sm_enabled = true;      // RUNIT_GEMV_SM=0: no small-launch body (A/B)
     uint64_t launches = 0;       // kernel launches enqueued so far (rt_launch_count)
+    const char* last_name = "";  // the last launched kernel (rt_last_launch_name)
     bool gemv_valu = false;      // RUNIT_GEMV_VALU=1: VALU-dot twins of the LDS body (A/B)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
@@ -370,6 +371,7 @@ int launch(rt_ctx* c, const char* name, dim3 grid, dim3 block, size_t lds, void*
                                          block.z, (unsigned)lds, c->stream, params, nullptr);
     if (e != hipSuccess) return hip_fail(c, e, name);
     ++c->launches;
+    c->last_name = it->first.c_str();
     return RT_OK;
 }
 
@@ -2519,6 +2521,7 @@ int rt_decode_attention_rope_oproj_q4kg_f32(rt_ctx* c, const float* q_raw, const
 }
 
 uint64_t rt_launch_count(const rt_ctx* c) { return c ? c->launches : 0; }
+const char* rt_last_launch_name(const rt_ctx* c) { return c ? c->last_name : ""; }
 
 int rt_add_f16_into_f32(rt_ctx* c, const uint16_t* src, float* acc, uint32_t n) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");

@@ -234,6 +234,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.rt_decode_step_destroy.argtypes = [_P]
     lib.rt_decode_step_destroy.restype = None
     lib.rt_launch_count.restype = c_uint64
+    lib.rt_last_launch_name.argtypes = [_P]
+    lib.rt_last_launch_name.restype = c_char_p
     # GGUF reader: (name, argtypes, restype)
     PU64 = POINTER(c_uint64)
     for name, argtypes, restype in (
@@ -706,6 +708,11 @@ def _attention_oproj(fmt):
 def launch_count(ctx) -> int:
     """Kernel launches enqueued on the context so far (new)."""
     return int(ctx.lib.rt_launch_count(ctx.handle))
+
+
+def last_launch_name(ctx) -> str:
+    """Name of the kernel the context launched last (new)."""
+    return ctx.lib.rt_last_launch_name(ctx.handle).decode()
 
 
 decode_attention_rope_oproj_q4k_f32 = _attention_oproj("q4k")
