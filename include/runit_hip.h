@@ -720,6 +720,35 @@ int rt_rms_norm_fused_ffn_q8_0_f32(rt_ctx* ctx, const void* w_gate, const void* 
 int rt_rms_norm_gemv_q8_0_f32in_f32out(rt_ctx* ctx, const void* weight, const float* x,
                                        const float* gamma, float eps, float* output, uint32_t m,
                                        uint32_t k);
+/* New: a decode step's RMSNorm factor handed from the launch that produces
+ * x to the norm-fused launch that consumes it.  The producing forms (down
+ * projection + residual, attention + output projection + residual) also
+ * write ssq[i] = Σ y² over output rows 4i..4i+3 (⌈m/4⌉ floats); the
+ * consuming forms take Σx² as those nparts partial sums instead of reducing
+ * x inside every workgroup (nparts ≤ 256; more: x is reduced as in the forms
+ * above).  The partial sums must be those of the x passed.  Results equal the
+ * forms without _ssq to f32 rounding of Σx². */
+int rt_gemv_q8_0_add_f32_f32in_ssq(rt_ctx* ctx, const void* weight, const float* input,
+                                   float* output, const float* residual, uint32_t m, uint32_t k,
+                                   float* ssq);
+int rt_decode_attention_rope_oproj_q8_0_f32_ssq(rt_ctx* ctx, const float* q_raw,
+                                                const float* k_raw, const float* v_raw,
+                                                float* k_cache, float* v_cache, const void* w_o,
+                                                float* x_io, uint32_t pos, uint32_t max_seq,
+                                                uint32_t num_heads, uint32_t num_kv_heads,
+                                                uint32_t head_dim, float theta, uint32_t hidden,
+                                                float* ssq);
+int rt_rms_norm_fused_qkv_bias_q8_0_f32_ssq(rt_ctx* ctx, const void* w_q, const void* w_k,
+                                            const void* w_v, const float* x, const float* gamma,
+                                            float eps, float* out_q, float* out_k, float* out_v,
+                                            const uint16_t* bias_q, const uint16_t* bias_k,
+                                            const uint16_t* bias_v, uint32_t q_dim,
+                                            uint32_t kv_dim, uint32_t k, const float* ssq,
+                                            uint32_t nparts);
+int rt_rms_norm_fused_ffn_q8_0_f32_ssq(rt_ctx* ctx, const void* w_gate, const void* w_up,
+                                       const float* x, const float* gamma, float eps,
+                                       float* act_out, uint32_t ff_dim, uint32_t k,
+                                       const float* ssq, uint32_t nparts);
 /* The same for the Q4_K_M projections: Q/K (Q4_K) + V (Q6_K) with biases
  * (k ≤ 8192), the Q4_K gate+up+SiLU, and a Q6_K GEMV (the LM head). */
 int rt_rms_norm_fused_qkv_bias_q4k_q6k_f32(rt_ctx* ctx, const void* w_q, const void* w_k,

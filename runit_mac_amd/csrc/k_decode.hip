@@ -260,3 +260,19 @@ k_add_f16_into_f32(const uint16_t* __restrict__ src, float* __restrict__ acc, ui
     for (uint32_t i = threadIdx.x + blockIdx.x * wg_threads(); i < n; i += wg_threads() * gridDim.x)
         acc[i] += h2f(src[i]);
 }
+
+// Σ y² over rows 4i..4i+3 of y (m rows), one thread per row quad: the
+// partial sums a norm-fused launch reads instead of reducing y itself, for
+// a producing launch whose body does not write them.
+extern "C" __global__ void __launch_bounds__(256)
+k_ssq_quads(const float* __restrict__ y, uint32_t m, float* __restrict__ out) {
+    const uint32_t qd = blockIdx.x * 256 + threadIdx.x;
+    if (qd * 4 >= m) return;
+    float s = 0.0f;
+    for (uint32_t r = 0; r < 4; ++r) {
+        const uint32_t i = qd * 4 + r;
+        const float v = i < m ? y[i] : 0.0f;
+        s += v * v;
+    }
+    out[qd] = s;
+}

@@ -400,17 +400,29 @@ template <int U>
 struct XPreU {
     float v[U][4];
     float g[U][4];
+    float sq[4];  // Σx² partials of the producing launch (≤ 256, 4 per lane)
 };
+constexpr uint32_t kMaxSsqParts = 256;
 using XPre = XPreU<XSTAGE_UNR>;
 template <int U = XSTAGE_UNR>
 RT_DEV bool stage_one_pass(uint32_t nxb) { return nxb * 8 <= U * wg_threads(); }
 
 // SKIP: lanes past the end load and convert nothing (whole 8-lane groups; a
 // workgroup of many such lanes otherwise rebuilds record 0 many times over)
+// ssq: the Σx² of x as nssq partial sums written by the launch that
+// produced x (≤ kMaxSsqParts; null: the staging reduces x itself).
 template <typename XT, int U, bool SKIP = false>
 RT_DEV void stage_x_load(const XT* __restrict__ x, const float* __restrict__ gamma, uint32_t nxb,
-                         XPreU<U>& p) {
+                         XPreU<U>& p, const float* __restrict__ ssq = nullptr, uint32_t nssq = 0) {
     const uint32_t total = nxb * 8;
+    if (ssq) {
+        const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t k = lane + 64 * i;
+            p.sq[i] = k < nssq ? ssq[k] : 0.0f;
+        }
+    }
 #pragma unroll
     for (int s = 0; s < U; ++s) {
         // rounds past the vector are skipped (workgroup-uniform: no lane of a
@@ -434,22 +446,29 @@ RT_DEV void stage_x_load(const XT* __restrict__ x, const float* __restrict__ gam
 // norm.metal:126-154), each product rounded in f32 as in stage_x_norm.
 template <bool Q40PERM, bool SKIP = false, int U>
 RT_DEV void stage_x_convert(XPreU<U>& p, const float* gamma, float eps, uint32_t nxb,
-                            XRec* __restrict__ recs) {
+                            XRec* __restrict__ recs, bool have_ssq = false) {
     const uint32_t total = nxb * 8;
     if (gamma) {
-        __shared__ float nred[16];
-        float ss = 0.0f;
+        float tot;
+        if (have_ssq) {
+            // the producer's partial sums: every wave adds them itself, in
+            // the same order, so no wave waits at a barrier for the others
+            tot = group_sum(p.sq[0] + p.sq[1] + p.sq[2] + p.sq[3], 64);
+        } else {
+            __shared__ float nred[16];
+            float ss = 0.0f;
 #pragma unroll
-        for (int s = 0; s < U; ++s) {
-            const float sq = p.v[s][0] * p.v[s][0] + p.v[s][1] * p.v[s][1] +
-                             p.v[s][2] * p.v[s][2] + p.v[s][3] * p.v[s][3];
-            ss += (threadIdx.x + s * wg_threads() < total) ? sq : 0.0f;
+            for (int s = 0; s < U; ++s) {
+                const float sq = p.v[s][0] * p.v[s][0] + p.v[s][1] * p.v[s][1] +
+                                 p.v[s][2] * p.v[s][2] + p.v[s][3] * p.v[s][3];
+                ss += (threadIdx.x + s * wg_threads() < total) ? sq : 0.0f;
+            }
+            ss = group_sum(ss, 64);
+            if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
+            lds_barrier();
+            tot = 0.0f;
+            for (uint32_t w = 0; w < (wg_threads() >> 6); ++w) tot += nred[w];
         }
-        ss = group_sum(ss, 64);
-        if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
-        lds_barrier();
-        float tot = 0.0f;
-        for (uint32_t w = 0; w < (wg_threads() >> 6); ++w) tot += nred[w];
         const float rms = rsqrtf(tot / (float)(nxb * 32) + eps);
 #pragma unroll
         for (int s = 0; s < U; ++s)

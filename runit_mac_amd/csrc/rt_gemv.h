@@ -50,7 +50,24 @@ struct GemvArgs {
     // x holds their limb records row after row, output / residual row m of
     // a matrix starts m rows of that matrix's length further on
     uint32_t nx;
+    // Σy² of the outputs, one float per row quad, for the next launch's
+    // RMSNorm (null: not written) ...
+    float* ssq_out;
+    // ... and the same as input: Σx² of x as ssq_n partial sums (null: the
+    // staging reduces x itself)
+    const float* ssq_in;
+    uint32_t ssq_n;
 };
+
+// Σ over the four rows of a row quad of the stored outputs' squares, written
+// to ssq_out[quad] by the quad's first lane (lanes 4b..4b+3 hold rows 0..3;
+// rows past the launch count 0).
+RT_DEV void quad_ssq_store(float* ssq_out, uint32_t quad, float y, bool valid, uint32_t q) {
+    float sq = valid ? y * y : 0.0f;
+    sq += dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(sq);
+    sq += dpp_f<DPP_QUAD_PERM(2, 3, 0, 1)>(sq);
+    if (q == 0) ssq_out[quad] = sq;
+}
 
 // Tiles one workgroup may own in a K-split launch (the host keeps the grid's
 // rounds below this).

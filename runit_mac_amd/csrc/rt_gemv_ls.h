@@ -542,7 +542,7 @@ RT_DEV void gemv_sm_body(const GemvArgs& a) {
     if constexpr (is_attn_x<XT>())
         stage_attn_load<false>(a.x, a.xml, a.xnsp, a.xhd, nxb, xa);
     else
-        stage_x_load<XT>((const XT*)a.x, a.gamma, nxb, xp);
+        stage_x_load<XT>((const XT*)a.x, a.gamma, nxb, xp, a.ssq_in, a.ssq_n);
     Item buf;
     issue(0, buf);
     float aux = 0.0f;
@@ -553,7 +553,7 @@ RT_DEV void gemv_sm_body(const GemvArgs& a) {
     if constexpr (is_attn_x<XT>())
         stage_attn_convert<F::Q40PERM>(xa, a.xnsp, nxb, xs);
     else
-        stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs);
+        stage_x_convert<F::Q40PERM>(xp, a.gamma, a.eps, nxb, xs, a.ssq_in != nullptr);
     lds_barrier();
 
     const uint32_t nsteps = (units + 15) / 16;
@@ -585,8 +585,10 @@ RT_DEV void gemv_sm_body(const GemvArgs& a) {
             const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(acc);
             if (slot == 0 && (q & 1) == 0 && vr + 1 < a.nvrows)
                 ((float*)a.out[0])[vr >> 1] = silu_ref(acc) * up;
-        } else if (slot == 0 && vr < a.nvrows) {
-            store_row_pre<EPI>(a, vr, acc, aux);
+        } else {
+            if (slot == 0 && vr < a.nvrows) store_row_pre<EPI>(a, vr, acc, aux);
+            if (epi_base(EPI) == EPI_F32_ADD && a.ssq_out && slot == 0)
+                quad_ssq_store(a.ssq_out, quad, acc + aux, vr < a.nvrows, q);
         }
     }
 }

@@ -71,14 +71,24 @@ RT_DEV void gemv_vs_body(const GemvArgs& a) {
     for (int i = 0; i < 8; ++i) y[i] = *(const f32x4*)(x + bc * 32 + 4 * i);
     f32x4 g[8];
     f32x4 xn[4];
+    float sqp[4];
     if constexpr (NORM) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) g[i] = *(const f32x4*)(a.gamma + bc * 32 + 4 * i);
-        // the whole x for Σx² (K ≤ 1024: 4 float4 per lane)
+        if (a.ssq_in) {
+            // Σx² as the producing launch's partial sums (≤ 256)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t e = (lane + 64 * i) * 4;
-            xn[i] = e < a.K ? *(const f32x4*)(x + e) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t k = lane + 64 * i;
+                sqp[i] = k < a.ssq_n ? a.ssq_in[k] : 0.0f;
+            }
+        } else {
+            // the whole x for Σx² (K ≤ 1024: 4 float4 per lane)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t e = (lane + 64 * i) * 4;
+                xn[i] = e < a.K ? *(const f32x4*)(x + e) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
         }
     }
     float aux = 0.0f;
@@ -86,9 +96,13 @@ RT_DEV void gemv_vs_body(const GemvArgs& a) {
     if constexpr (NORM) {
         // rms_norm_f32_f32_f32g (norm.metal:126-154): y = x·rsqrt(Σx²/K + eps)·γ
         float ss = 0.0f;
+        if (a.ssq_in) {
+            ss = sqp[0] + sqp[1] + sqp[2] + sqp[3];
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            ss += xn[i].x * xn[i].x + xn[i].y * xn[i].y + xn[i].z * xn[i].z + xn[i].w * xn[i].w;
+            for (int i = 0; i < 4; ++i)
+                ss += xn[i].x * xn[i].x + xn[i].y * xn[i].y + xn[i].z * xn[i].z + xn[i].w * xn[i].w;
+        }
         ss = group_sum(ss, 64);
         const float rms = rsqrtf(ss / (float)a.K + a.eps);
 #pragma unroll
@@ -117,8 +131,10 @@ RT_DEV void gemv_vs_body(const GemvArgs& a) {
         // quad rows (gate r, up r, gate r+1, up r+1)
         const float up = dpp_f<DPP_QUAD_PERM(1, 0, 3, 2)>(acc);
         if ((r & 1) == 0 && vr0 + 1 < a.nvrows) ((float*)a.out[0])[vr0 >> 1] = silu_ref(acc) * up;
-    } else if (vr0 < a.nvrows) {
-        store_row_pre<EPI>(a, vr0, acc, aux);
+    } else {
+        if (vr0 < a.nvrows) store_row_pre<EPI>(a, vr0, acc, aux);
+        if (epi_base(EPI) == EPI_F32_ADD && a.ssq_out)
+            quad_ssq_store(a.ssq_out, quad, acc + aux, vr0 < a.nvrows, r);
     }
 }
 

@@ -30,7 +30,7 @@ constexpr uint64_t RT_SCRATCH_PART_BYTES = RT_SCRATCH_BYTES - RT_SCRATCH_PART_OF
 
 // Persistent decode step (k_step.hip): phase record size and the most
 // workgroups a step grid may have.
-constexpr uint32_t RT_STEP_PHASE_BYTES = 376;
+constexpr uint32_t RT_STEP_PHASE_BYTES = 400;
 constexpr uint32_t RT_STEP_MAX_WGS = 1024;
 // threads per workgroup of the persistent step (its attention phase runs
 // RT_STEP_THREADS / 256 head groups)

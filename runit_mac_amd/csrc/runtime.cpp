@@ -52,6 +52,9 @@ struct GemvArgs {
     uint32_t ls_xcd;
     uint32_t blk0, nblk;
     uint32_t nx;
+    float* ssq_out;        // Σy² per output row quad (for the next RMSNorm), or null
+    const float* ssq_in;   // Σx² of x as ssq_n partial sums, or null
+    uint32_t ssq_n;
 };
 
 constexpr uint32_t XREC_BYTES = 112;
@@ -135,7 +138,7 @@ const char* const kKernelNames[] = {
     "k_rms_norm_f32g", "k_rope_qk_f32", "k_kv_copy_f32",
     "k_decode_attention_f32_hd64", "k_decode_attention_f32_hd128", "k_decode_attention_f32_hd256",
     "k_attn_rope_f32_hd64", "k_attn_rope_f32_hd128", "k_attn_rope_f32_hd256",
-    "k_add_f16_into_f32", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
+    "k_add_f16_into_f32", "k_ssq_quads", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
     "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32", "k_rope_kv_write_batch_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
     "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
@@ -209,6 +212,8 @@ const char* const kRowsFmts[] = {"q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k",
 // Kernels with a VALU-dot twin <base>_ls<NI>v (the dot-form A/B).
 const char* const kLsValuBases[] = {"k_ffn_q4k", "k_gemv_q6k_f32_f32"};
 constexpr uint32_t kLsMaxNI = 3;
+constexpr uint32_t kVsMaxQuadsPerCu = 2;  // VALU small-launch body: row quads per CU (at most)
+constexpr uint32_t kMaxSsqParts = 256;    // Σx² partial sums a norm-fused staging reads (at most)
 constexpr int kLsDecline = -1;
 constexpr uint32_t kLsThreads = 256;
 constexpr uint32_t kLsRowPad = 48;      // LDS row stride = NI KB + pad (bank spread)
@@ -283,6 +288,7 @@ struct rt_ctx {
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
     bool vs_enabled = true;      // RUNIT_GEMV_VS=0: no VALU small-launch body (A/B)
+    uint32_t vs_max_q = kVsMaxQuadsPerCu;  // RUNIT_GEMV_VS_MAXQ: row quads per CU up to which it runs
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
@@ -682,7 +688,6 @@ int gemv_launch_sm(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
 // (896×4864: 5.64 → 4.02 µs).  Its per-lane 34-byte block loads and
 // per-lane activation reads cost more than they save on larger launches
 // (0.5B norm-fused gate+up 2×4864×896: 5.57 → 11.1 µs).
-constexpr uint32_t kVsMaxQuadsPerCu = 2;
 int gemv_launch_vs(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     // (a merged attention input stays on the small-launch body: merging 8
     // splits per lane made the 0.5B attention + O pair 8.9 → 9.1 µs)
@@ -692,7 +697,7 @@ int gemv_launch_vs(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a) {
     const uint32_t wpq = (nb + 15) / 16;
     if (wpq > 16) return kLsDecline;  // (K ≤ 8192: the quad's waves in one workgroup)
     const uint32_t nq = (a.nvrows + 3) / 4;
-    if (nq > (uint64_t)c->cu_count * kVsMaxQuadsPerCu) return kLsDecline;
+    if (nq > (uint64_t)c->cu_count * c->vs_max_q) return kLsDecline;
     char name[96];
     snprintf(name, sizeof name, "%s_%s", kname, a.gamma ? "vsn" : "vs");
     if (!c->fns.count(name)) return kLsDecline;
@@ -1301,6 +1306,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_VALU")) c->gemv_valu = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LSK_WHOLE")) c->lsk_whole = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_VS")) c->vs_enabled = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMV_VS_MAXQ")) c->vs_max_q = (uint32_t)atoi(g);
     std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
     auto unload = [](rt_ctx* cc) {
         for (hipModule_t m : cc->modules) hipModuleUnload(m);
@@ -2238,6 +2244,23 @@ int norm_then(rt_ctx* c, const char* kname, const Fmt& f, GemvArgs a, bool paire
     return gemv_launch(c, kname, f, a, false, paired);
 }
 
+// Σy² partial sums for the next norm-fused launch (rt_*_ssq): one float per
+// row quad of y, by a kernel of their own ...
+int ssq_quads(rt_ctx* c, const float* y, uint32_t m, float* ssq) {
+    if (!ssq) return RT_OK;
+    const uint32_t nq = (m + 3) / 4;
+    void* params[] = {&y, &m, &ssq};
+    return launch(c, "k_ssq_quads", dim3((nq + 255) / 256), dim3(256), 0, params);
+}
+// ... unless the launch just made was one whose epilogue writes them (the
+// small-launch and VALU small-launch bodies, with a + residual epilogue)
+int ssq_after(rt_ctx* c, const float* y, uint32_t m, float* ssq) {
+    const std::string n = c->last_name;
+    const bool written = (n.size() > 3 && n.compare(n.size() - 3, 3, "_vs") == 0) ||
+                         n.find("_sm1") != std::string::npos || n.find("_sm2") != std::string::npos;
+    return written ? RT_OK : ssq_quads(c, y, m, ssq);
+}
+
 }  // namespace
 
 extern "C" {
@@ -2423,7 +2446,8 @@ static int attention_oproj(rt_ctx* c, const float* q_raw, const float* k_raw, co
                            float* k_cache, float* v_cache, const void* w_o, float* x_io,
                            uint32_t pos, uint32_t max_seq, uint32_t num_heads,
                            uint32_t num_kv_heads, uint32_t head_dim, float theta, uint32_t hidden,
-                           const char* gkern, const Fmt& fmt, uint32_t max_t, GemvAddFn plain) {
+                           const char* gkern, const Fmt& fmt, uint32_t max_t, GemvAddFn plain,
+                           float* ssq = nullptr) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     if (num_heads == 0 || hidden == 0) return RT_OK;
     int st = attn_check(c, num_heads, num_kv_heads, head_dim);
@@ -2474,6 +2498,11 @@ static int attention_oproj(rt_ctx* c, const float* q_raw, const float* k_raw, co
         a.out = (float*)c->attn_out;
         st = attn_launch(c, kn, a, 1);
         if (st != RT_OK) return st;
+        // (ssq is given by the Q8_0 form only, whose plain projection also
+        // writes the partial sums)
+        if (ssq)
+            return rt_gemv_q8_0_add_f32_f32in_ssq(c, w_o, (const float*)c->attn_out, x_io, x_io,
+                                                  hidden, q_dim, ssq);
         return plain(c, w_o, (const float*)c->attn_out, x_io, x_io, hidden, q_dim);
     }
     a.parts_only = 1;
@@ -2485,7 +2514,10 @@ static int attention_oproj(rt_ctx* c, const float* q_raw, const float* k_raw, co
     g.xml = used.ml;
     g.xnsp = nsplit;
     g.xhd = head_dim;
-    return gemv_launch(c, gkern, fmt, g, false);
+    g.ssq_out = ssq;
+    st = gemv_launch(c, gkern, fmt, g, false);
+    if (st != RT_OK || !ssq) return st;
+    return ssq_after(c, x_io, hidden, ssq);
 }
 
 int rt_decode_attention_rope_oproj_q8_0_f32(rt_ctx* c, const float* q_raw, const float* k_raw,
@@ -2518,6 +2550,70 @@ int rt_decode_attention_rope_oproj_q4kg_f32(rt_ctx* c, const float* q_raw, const
     return attention_oproj(c, q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io, pos, max_seq,
                            num_heads, num_kv_heads, head_dim, theta, hidden,
                            "k_gemv_q4kg_attn_f32add", kQ4KG, 1024, rt_gemv_q4kg_add_f32_f32in);
+}
+
+// The decode step's RMSNorm factor handed from producer to consumer: the
+// producing launches also write Σy² per output row quad, the consuming
+// norm-fused launches read those partial sums instead of reducing x.
+int rt_gemv_q8_0_add_f32_f32in_ssq(rt_ctx* c, const void* w, const float* x, float* y,
+                                   const float* r, uint32_t m, uint32_t k, float* ssq) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (!r) return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: k_gemv_q8_0_f32_f32add: null residual");
+    GemvArgs a = plain_args(w, x, y, r, m, k);
+    a.ssq_out = ssq;
+    int st = gemv_launch(c, "k_gemv_q8_0_f32_f32add", kQ8_0, a, false);
+    if (st != RT_OK || !ssq || m == 0) return st;
+    return ssq_after(c, y, m, ssq);
+}
+int rt_decode_attention_rope_oproj_q8_0_f32_ssq(rt_ctx* c, const float* q_raw, const float* k_raw,
+                                                const float* v_raw, float* k_cache, float* v_cache,
+                                                const void* w_o, float* x_io, uint32_t pos,
+                                                uint32_t max_seq, uint32_t num_heads,
+                                                uint32_t num_kv_heads, uint32_t head_dim,
+                                                float theta, uint32_t hidden, float* ssq) {
+    return attention_oproj(c, q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io, pos, max_seq,
+                           num_heads, num_kv_heads, head_dim, theta, hidden,
+                           "k_gemv_q8_0_attn_f32add", kQ8_0, 256, rt_gemv_q8_0_add_f32_f32in, ssq);
+}
+int rt_rms_norm_fused_qkv_bias_q8_0_f32_ssq(rt_ctx* c, const void* wq, const void* wk,
+                                            const void* wv, const float* x, const float* gamma,
+                                            float eps, float* oq, float* ok, float* ov,
+                                            const uint16_t* bq, const uint16_t* bk,
+                                            const uint16_t* bv, uint32_t q_dim, uint32_t kv_dim,
+                                            uint32_t k, const float* ssq, uint32_t nparts) {
+    if (!wq || !wk || !wv || !oq || !ok || !ov || !bq || !bk || !bv)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: k_qkv_bias_q8_0: null buffer");
+    GemvArgs a{};
+    a.w[0] = (const uint8_t*)wq; a.w[1] = (const uint8_t*)wk; a.w[2] = (const uint8_t*)wv;
+    a.out[0] = oq; a.out[1] = ok; a.out[2] = ov;
+    a.aux[0] = bq; a.aux[1] = bk; a.aux[2] = bv;
+    a.x = x;
+    a.n[0] = q_dim; a.n[1] = kv_dim; a.n[2] = kv_dim;
+    a.nvrows = q_dim + 2 * kv_dim;
+    a.K = k;
+    if (ssq && nparts && nparts <= kMaxSsqParts) {
+        a.ssq_in = ssq;
+        a.ssq_n = nparts;
+    }
+    return norm_then(c, "k_qkv_bias_q8_0", kQ8_0, a, false, gamma, eps);
+}
+int rt_rms_norm_fused_ffn_q8_0_f32_ssq(rt_ctx* c, const void* wg, const void* wu, const float* x,
+                                       const float* gamma, float eps, float* act, uint32_t ff,
+                                       uint32_t k, const float* ssq, uint32_t nparts) {
+    if (!wg || !wu || !act)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: k_ffn_q8_0: null buffer");
+    GemvArgs a{};
+    a.w[0] = (const uint8_t*)wg; a.w[1] = (const uint8_t*)wu;
+    a.out[0] = act;
+    a.x = x;
+    a.n[0] = ff; a.n[1] = ff;
+    a.nvrows = 2 * ff;
+    a.K = k;
+    if (ssq && nparts && nparts <= kMaxSsqParts) {
+        a.ssq_in = ssq;
+        a.ssq_n = nparts;
+    }
+    return norm_then(c, "k_ffn_q8_0", kQ8_0, a, true, gamma, eps);
 }
 
 uint64_t rt_launch_count(const rt_ctx* c) { return c ? c->launches : 0; }

@@ -297,6 +297,10 @@ class DecodeModel:
         self.act = a.take(4 * ff)
         self.logits = a.take(4 * c.vocab)
         self.token = a.take(256)
+        # Σx² partial sums (one per 4 elements of x) handed from the launch
+        # that updates x to the norm-fused launch that reads it
+        self.ssq = [a.take(4 * ((h + 3) // 4)) for _ in range(2)]
+        self.hand_off_norm = True  # (False: every norm-fused launch reduces x itself)
         self._launches = None
         ctx.flush()
 
@@ -418,9 +422,21 @@ class DecodeModel:
         n0 = d.launch_count(ctx)
         n = 1
         d.embed_f32(ctx, self.embd_fmt, self.embd, self.token, self.x, h)
+        # Q8_0 layers of a model whose x fits 256 partial sums hand the RMSNorm
+        # factor from the launch that updates x (O, down) to the norm-fused
+        # launch after it (gate+up, the next layer's Q/K/V)
+        nparts = (h + 3) // 4
+        ssq_x = None  # partial sums of the current x, if a launch wrote them
         for L, F in zip(self.layers, self.fmts):
             plan = self._plan_qkv(F)
-            if plan == "norm_q8_0":
+            q8 = (self.hand_off_norm and nparts <= 256
+                  and F["o"] == F["gate"] == F["up"] == F["down"] == "q8_0")
+            if plan == "norm_q8_0" and ssq_x is not None:
+                d.rms_norm_fused_qkv_bias_q8_0_f32_ssq(
+                    ctx, L["wq"], L["wk"], L["wv"], self.x, L["attn_norm"], c.eps, self.q,
+                    self.k, self.v, L["bq"], L["bk"], L["bv"], q_dim, c.kv_dim, h, ssq_x, nparts)
+                n += 1
+            elif plan == "norm_q8_0":
                 d.rms_norm_fused_qkv_bias_q8_0_f32(ctx, L["wq"], L["wk"], L["wv"], self.x,
                                                    L["attn_norm"], c.eps, self.q, self.k, self.v,
                                                    L["bq"], L["bk"], L["bv"], q_dim, c.kv_dim, h)
@@ -434,7 +450,13 @@ class DecodeModel:
             else:
                 d.rms_norm_f32_f32_f32g(ctx, self.x, self.xn, L["attn_norm"], c.eps, h, 1)
                 n += 1 + self._qkv(L, F, self.xn)
-            if F["o"] in ("q8_0", "q4k", "q4kg"):
+            ssq_x = None
+            if q8:
+                d.decode_attention_rope_oproj_q8_0_f32_ssq(
+                    ctx, self.q, self.k, self.v, L["kc"], L["vc"], L["wo"], self.x, pos,
+                    c.max_seq, c.heads, c.kv_heads, c.head_dim, c.theta, h, self.ssq[0])
+                ssq_x = self.ssq[0]
+            elif F["o"] in ("q8_0", "q4k", "q4kg"):
                 getattr(d, f"decode_attention_rope_oproj_{F['o']}_f32")(
                     ctx, self.q, self.k, self.v, L["kc"], L["vc"], L["wo"], self.x, pos,
                     c.max_seq, c.heads, c.kv_heads, c.head_dim, c.theta, h)
@@ -445,7 +467,11 @@ class DecodeModel:
                 getattr(d, f"gemv_{F['o']}_add_f32_f32in")(ctx, L["wo"], self.attn, self.x,
                                                            self.x, h, q_dim)
             n += 2
-            if F["gate"] == F["up"] and F["gate"] in ("q8_0", "q4k"):
+            if q8 and ssq_x is not None:
+                d.rms_norm_fused_ffn_q8_0_f32_ssq(ctx, L["wg"], L["wu"], self.x, L["ffn_norm"],
+                                                  c.eps, self.act, c.ff, h, ssq_x, nparts)
+                n += 1
+            elif F["gate"] == F["up"] and F["gate"] in ("q8_0", "q4k"):
                 getattr(d, f"rms_norm_fused_ffn_{F['gate']}_f32")(
                     ctx, L["wg"], L["wu"], self.x, L["ffn_norm"], c.eps, self.act, c.ff, h)
                 n += 1
@@ -458,8 +484,14 @@ class DecodeModel:
                     n += 1
                 else:
                     raise ValueError(f"gate {F['gate']} / up {F['up']}: no fused gate+up+SiLU")
-            getattr(d, f"gemv_{F['down']}_add_f32_f32in")(ctx, L["wd"], self.act, self.x,
-                                                          self.x, h, c.ff)
+            if q8:
+                d.gemv_q8_0_add_f32_f32in_ssq(ctx, L["wd"], self.act, self.x, self.x, h, c.ff,
+                                              self.ssq[1])
+                ssq_x = self.ssq[1]
+            else:
+                getattr(d, f"gemv_{F['down']}_add_f32_f32in")(ctx, L["wd"], self.act, self.x,
+                                                              self.x, h, c.ff)
+                ssq_x = None
             n += 1
         n += self._lm_head(self.x)
         d.argmax_f32(ctx, self.logits, self.token, c.vocab)

@@ -150,6 +150,11 @@ _SIGS = {
     "rt_argmax_rows_first_f32": [_P, _P, _P, _U32, _U32],
     "rt_rms_norm_fused_qkv_bias_q8_0_f32": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 + [_U32] * 3,
     "rt_rms_norm_fused_ffn_q8_0_f32": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32],
+    "rt_rms_norm_fused_ffn_q8_0_f32_ssq": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32, _P, _U32],
+    "rt_rms_norm_fused_qkv_bias_q8_0_f32_ssq": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 +
+                                               [_U32] * 3 + [_P, _U32],
+    "rt_gemv_q8_0_add_f32_f32in_ssq": [_P, _P, _P, _P, _P, _U32, _U32, _P],
+    "rt_decode_attention_rope_oproj_q8_0_f32_ssq": [_P] + [_P] * 7 + [_U32] * 5 + [_F, _U32, _P],
     "rt_rms_norm_gemv_q8_0_f32in_f32out": [_P, _P, _P, _P, _F, _P, _U32, _U32],
     "rt_rms_norm_fused_qkv_bias_q4k_q6k_f32": [_P, _P, _P, _P, _P, _P, _F] + [_P] * 6 + [_U32] * 3,
     "rt_rms_norm_fused_ffn_q4k_f32": [_P, _P, _P, _P, _P, _F, _P, _U32, _U32],
@@ -821,6 +826,38 @@ def rms_norm_fused_qkv_bias_q8_0_f32(ctx, w_q, w_k, w_v, x, gamma, eps, out_q, o
     _call(ctx, "rt_rms_norm_fused_qkv_bias_q8_0_f32", _ptr(w_q), _ptr(w_k), _ptr(w_v), _ptr(x),
           _ptr(gamma), eps, *map(_ptr, (out_q, out_k, out_v, bias_q, bias_k, bias_v)),
           q_dim, kv_dim, k)
+
+
+def rms_norm_fused_qkv_bias_q8_0_f32_ssq(ctx, w_q, w_k, w_v, x, gamma, eps, out_q, out_k, out_v,
+                                         bias_q, bias_k, bias_v, q_dim, kv_dim, k, ssq, nparts):
+    """rms_norm_fused_qkv_bias_q8_0_f32 with Σx² given as the producing
+    launch's nparts partial sums (new)."""
+    _call(ctx, "rt_rms_norm_fused_qkv_bias_q8_0_f32_ssq", _ptr(w_q), _ptr(w_k), _ptr(w_v),
+          _ptr(x), _ptr(gamma), eps, *map(_ptr, (out_q, out_k, out_v, bias_q, bias_k, bias_v)),
+          q_dim, kv_dim, k, _ptr(ssq), nparts)
+
+
+def rms_norm_fused_ffn_q8_0_f32_ssq(ctx, w_gate, w_up, x, gamma, eps, act_out, ff_dim, k, ssq,
+                                    nparts):
+    """rms_norm_fused_ffn_q8_0_f32 with Σx² given as partial sums (new)."""
+    _call(ctx, "rt_rms_norm_fused_ffn_q8_0_f32_ssq", _ptr(w_gate), _ptr(w_up), _ptr(x),
+          _ptr(gamma), eps, _ptr(act_out), ff_dim, k, _ptr(ssq), nparts)
+
+
+def gemv_q8_0_add_f32_f32in_ssq(ctx, weight, input, output, residual, m, k, ssq):
+    """gemv_q8_0_add_f32_f32in that also writes Σy² per 4 output rows (new)."""
+    _call(ctx, "rt_gemv_q8_0_add_f32_f32in_ssq", *map(_ptr, (weight, input, output, residual)),
+          m, k, _ptr(ssq))
+
+
+def decode_attention_rope_oproj_q8_0_f32_ssq(ctx, q_raw, k_raw, v_raw, k_cache, v_cache, w_o,
+                                             x_io, pos, max_seq, num_heads, num_kv_heads,
+                                             head_dim, theta, hidden, ssq):
+    """decode_attention_rope_oproj_q8_0_f32 that also writes Σy² per 4 rows
+    of the updated x (new)."""
+    _call(ctx, "rt_decode_attention_rope_oproj_q8_0_f32_ssq",
+          *map(_ptr, (q_raw, k_raw, v_raw, k_cache, v_cache, w_o, x_io)), pos, max_seq,
+          num_heads, num_kv_heads, head_dim, theta, hidden, _ptr(ssq))
 
 
 def rms_norm_fused_qkv_bias_q4k_q6k_f32(ctx, w_q, w_k, w_v, x, gamma, eps, out_q, out_k, out_v,

@@ -336,3 +336,82 @@ def test_attention_oproj_matches_oracle(ctx, fmt, H, KVH, hd, hidden, pos):
     assert np.array_equal(vcb.read(np.float32, vc.size).reshape(vc.shape)[:, pos], vc2[:, pos])
     got_k = kcb.read(np.float32, kc.size).reshape(kc.shape)[:, pos].astype(np.float64)
     assert np.all(np.abs(got_k - kc2[:, pos]) <= 1e-6 * np.abs(k_new).max())
+
+
+@pytest.mark.parametrize("m,k", [(896, 4864), (4864, 896), (900, 896)])
+def test_gemv_add_ssq_writes_quad_sums(ctx, m, k):
+    """gemv_q8_0_add_f32_f32in_ssq: the same output as gemv_q8_0_add_f32_f32in
+    (bit for bit) plus Σy² over every 4 output rows — written by the
+    launch's own epilogue (896 rows: VALU small-launch body) or by a kernel
+    of its own where the chosen body has no such epilogue (4864 rows)."""
+    rng = np.random.default_rng(m + k)
+    w, raw = device_weights(ctx, "q8_0", m, k, seed=m)
+    x = rng.standard_normal(k).astype(np.float32)
+    r = rng.standard_normal(m).astype(np.float32)
+    y1, y2 = ctx.buffer_from(r), ctx.buffer_from(r)
+    nq = (m + 3) // 4
+    ssq = ctx.new_buffer(4 * nq)
+    xb = ctx.buffer_from(x)
+    d.gemv_q8_0_add_f32_f32in(ctx, w, xb, y1, y1, m, k)
+    d.gemv_q8_0_add_f32_f32in_ssq(ctx, w, xb, y2, y2, m, k, ssq)
+    ctx.flush()
+    a, b = y1.read(np.float32, m), y2.read(np.float32, m)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    yy = np.zeros(4 * nq)
+    yy[:m] = b.astype(np.float64) ** 2
+    ref = yy.reshape(nq, 4).sum(axis=1)
+    assert np.allclose(ssq.read(np.float32, nq), ref, rtol=4 * F32_EPS, atol=0)
+
+
+def test_attention_oproj_and_norm_fused_ssq(ctx):
+    """The 0.5B layer's hand-off: attention + O projection writing Σy² per
+    quad (ssq), then norm-fused gate+up and Q/K/V reading them.  Producer:
+    x bit-identical to the form without ssq; consumers: within 1e-6 relative
+    of the forms that reduce x themselves (the only difference is the order
+    of the f32 Σx²)."""
+    rng = np.random.default_rng(9)
+    H, KVH, hd, h, ff, pos, max_seq = 14, 2, 64, 896, 4864, 511, 1024
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kn = rng.standard_normal(KVH * hd).astype(np.float32)
+    vn = rng.standard_normal(KVH * hd).astype(np.float32)
+    kc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float32)
+    vc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float32)
+    x0 = rng.standard_normal(h).astype(np.float32)
+    wo, _ = device_weights(ctx, "q8_0", h, H * hd, seed=1)
+    qb, kb, vb = ctx.buffer_from(q), ctx.buffer_from(kn), ctx.buffer_from(vn)
+    outs = []
+    ssq = ctx.new_buffer(4 * (h // 4))
+    for with_ssq in (False, True):
+        kcb, vcb, xb = ctx.buffer_from(kc), ctx.buffer_from(vc), ctx.buffer_from(x0)
+        args = (ctx, qb, kb, vb, kcb, vcb, wo, xb, pos, max_seq, H, KVH, hd, 1e6, h)
+        if with_ssq:
+            d.decode_attention_rope_oproj_q8_0_f32_ssq(*args, ssq)
+        else:
+            d.decode_attention_rope_oproj_q8_0_f32(*args)
+        ctx.flush()
+        outs.append(xb)
+    x1 = outs[0].read(np.float32, h)
+    assert np.array_equal(x1.view(np.uint32), outs[1].read(np.float32, h).view(np.uint32))
+    ref = (x1.astype(np.float64) ** 2).reshape(-1, 4).sum(axis=1)
+    assert np.allclose(ssq.read(np.float32, h // 4), ref, rtol=4 * F32_EPS, atol=0)
+    # consumers
+    xb = outs[1]
+    g = ctx.buffer_from((1 + 0.02 * rng.standard_normal(h)).astype(np.float32))
+    wg, _ = device_weights(ctx, "q8_0", ff, h, seed=2)
+    wu, _ = device_weights(ctx, "q8_0", ff, h, seed=3)
+    a1, a2 = ctx.new_buffer(4 * ff), ctx.new_buffer(4 * ff)
+    d.rms_norm_fused_ffn_q8_0_f32(ctx, wg, wu, xb, g, 1e-6, a1, ff, h)
+    d.rms_norm_fused_ffn_q8_0_f32_ssq(ctx, wg, wu, xb, g, 1e-6, a2, ff, h, ssq, h // 4)
+    qkv = [(d.weight_bytes("q8_0", n, h), n) for n in (896, 128, 128)]
+    ws = [device_weights(ctx, "q8_0", n, h, seed=10 + i)[0] for i, (_, n) in enumerate(qkv)]
+    bias = [ctx.buffer_from((0.02 * rng.standard_normal(n)).astype(np.float16)) for _, n in qkv]
+    o1 = [ctx.new_buffer(4 * n) for _, n in qkv]
+    o2 = [ctx.new_buffer(4 * n) for _, n in qkv]
+    d.rms_norm_fused_qkv_bias_q8_0_f32(ctx, *ws, xb, g, 1e-6, *o1, *bias, 896, 128, h)
+    d.rms_norm_fused_qkv_bias_q8_0_f32_ssq(ctx, *ws, xb, g, 1e-6, *o2, *bias, 896, 128, h, ssq,
+                                           h // 4)
+    ctx.flush()
+    for u, v, n in [(a1, a2, ff)] + [(o1[i], o2[i], qkv[i][1]) for i in range(3)]:
+        p1 = u.read(np.float32, n).astype(np.float64)
+        p2 = v.read(np.float32, n).astype(np.float64)
+        assert np.all(np.abs(p1 - p2) <= 1e-6 * np.abs(p1).max() + 1e-30), np.abs(p1 - p2).max()
