@@ -889,6 +889,10 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
 RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 1, 8)
 RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 2, 4)
 RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 4, 4)
+// 256-row tiles (16 waves share each stage of activation operands)
+extern "C" __global__ void __launch_bounds__(1024) k_gemm3_q8_0_mg4_w16(Gemm2Args a) {
+    gemm3_body<GemmQ8_0, 4, 4, 16>(a);
+}
 RT_GEMM3_KERNEL(q4_0, GemmQ4_0, 1, 8)
 RT_GEMM3_KERNEL(q4_0, GemmQ4_0, 2, 4)
 RT_GEMM3_KERNEL(q4_0, GemmQ4_0, 4, 4)

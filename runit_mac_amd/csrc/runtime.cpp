@@ -158,7 +158,7 @@ const char* const kKernelNames[] = {
     "k_gemm2_q6k_mg1", "k_gemm2_q6k_mg2", "k_gemm2_q6k_mg4",
     "k_gemm2_q6kg_mg1", "k_gemm2_q6kg_mg2", "k_gemm2_q6kg_mg4",
     "k_gemm3_q8_0_mg1", "k_gemm3_q8_0_mg1_w8", "k_gemm3_q8_0_mg2", "k_gemm3_q8_0_mg2_w8",
-    "k_gemm3_q8_0_mg4", "k_gemm3_q8_0_mg4_w8", "k_gemm3_q4_0_mg1", "k_gemm3_q4_0_mg1_w8",
+    "k_gemm3_q8_0_mg4", "k_gemm3_q8_0_mg4_w8", "k_gemm3_q8_0_mg4_w16", "k_gemm3_q4_0_mg1", "k_gemm3_q4_0_mg1_w8",
     "k_gemm3_q4_0_mg2", "k_gemm3_q4_0_mg2_w8", "k_gemm3_q4_0_mg4", "k_gemm3_q4_0_mg4_w8",
     "k_gemm3_q4k_mg1", "k_gemm3_q4k_mg1_w8", "k_gemm3_q4k_mg2", "k_gemm3_q4k_mg2_w8",
     "k_gemm3_q4k_mg4", "k_gemm3_q4k_mg4_w8", "k_gemm3_q4kg_mg1", "k_gemm3_q4kg_mg1_w8",
@@ -289,6 +289,7 @@ struct rt_ctx {
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
     bool vs_enabled = true;      // RUNIT_GEMV_VS=0: no VALU small-launch body (A/B)
     uint32_t vs_max_q = kVsMaxQuadsPerCu;  // RUNIT_GEMV_VS_MAXQ: row quads per CU up to which it runs
+    bool gemm_w16 = true;        // RUNIT_GEMM_W16=0: no 256-row tiles (A/B)
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
@@ -1299,6 +1300,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     // A/B switches between the kernel bodies (tests and measurements)
     if (const char* g = getenv("RUNIT_GEMM_DIRECT")) c->gemm_direct = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_F16")) c->gemm_f16 = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_W16")) c->gemm_w16 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_SM")) c->sm_enabled = atoi(g) != 0;
@@ -1876,9 +1878,21 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
     if (nblk % NB != 0 || !aligned(w, 16) || row_bytes % vb != 0 || c->gemm_direct)
         return kLsDecline;
     const bool w8ok = f.blk_bytes != 210;
-    const uint32_t waves = (MG >= 2 && f.blk_bytes != 34 && w8ok ? 8 : 4);
+    uint32_t waves = (MG >= 2 && f.blk_bytes != 34 && w8ok ? 8 : 4);
     char kn[48];
     snprintf(kn, sizeof kn, waves == 8 ? "k_gemm3_%s_mg%u_w8" : "k_gemm3_%s_mg%u", f.name, MG);
+    // 256-row tiles (16 waves share each stage of activation operands: a
+    // quarter of the operand reads from L2) where they leave ≥ 1/4 of the CUs
+    // a tile without a K split: Q8_0 18944×3584 at M = 32 51.0 → 44.6 µs
+    // (3584×18944, 14 such tiles, 64.3 → 85.4 µs)
+    if (c->gemm_w16 && MG == 4 && (n + 255) / 256 >= cu / 4) {
+        char k16[48];
+        snprintf(k16, sizeof k16, "k_gemm3_%s_mg%u_w16", f.name, MG);
+        if (c->fns.count(k16)) {
+            strcpy(kn, k16);
+            waves = 16;
+        }
+    }
     if (!c->fns.count(kn)) return kLsDecline;
     const uint32_t tiles = (n + 16 * waves - 1) / (16 * waves);
     const uint32_t per_cu = std::max<uint32_t>(1, occupancy(c, kn, 64 * waves, 0));
