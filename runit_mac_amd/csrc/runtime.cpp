@@ -1911,8 +1911,8 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_%s_f32: %u tiles exceed %u counters",
                     f.name, base, kAttnCounters);
     const size_t a_bytes = (size_t)nchunks * nrec * MG * 64 * 16;
-    const size_t e_bytes = (size_t)nchunks * nrec * 8 * MG * sizeof(int);
-    const size_t s_bytes = f.has_min ? e_bytes : 0;
+    const size_t e_bytes = (size_t)nchunks * 8 * MG * sizeof(int);  // per padded row
+    const size_t s_bytes = f.has_min ? (size_t)nchunks * nrec * 8 * MG * sizeof(float) : 0;
     const size_t p_bytes = splits > 1 ? (size_t)splits * nchunks * 8 * MG * n * sizeof(float) : 0;
     int st = ensure_ws(c, a_bytes + e_bytes + s_bytes + p_bytes, "gemm");
     if (st != RT_OK) return st;
@@ -1924,10 +1924,10 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
         char pk[48];
         snprintf(pk, sizeof pk, "k_gemm_xh_prep_mg%u", MG);
         uint32_t M = m_rows, K = k, nc = nchunks;
-        const uint64_t threads = (uint64_t)nchunks * 8 * MG * nrec * 4;
-        const uint32_t grid = (uint32_t)std::min<uint64_t>((threads + 255) / 256, (uint64_t)cu * 16);
+        // one workgroup per padded activation row
+        const uint32_t threads = std::min<uint32_t>(1024, (nrec * 4 + 63) / 64 * 64);
         void* pp[] = {(void*)&x, &M, &K, &nc, &aops, &erow, &stab};
-        st = launch(c, pk, dim3(grid), dim3(256), 0, pp);
+        st = launch(c, pk, dim3(nchunks * 8 * MG), dim3(threads), 0, pp);
         if (st != RT_OK) return st;
     }
     uint32_t cstride = 32;

@@ -297,10 +297,11 @@ def test_gemm_int8_form_matches_oracle(fmt, m):
 
 @pytest.mark.parametrize("fmt", ["q8_0", "q4k", "q4_0", "q6k", "q6kg"])
 def test_gemm_f16_form_wide_range(ctx, fmt):
-    """f16 forms: each 32-element record (min formats) or each row (the
-    accumulate-in-matrix-core form) is scaled into f16's range on its own, so
-    rows of 1e-6-sized activations, rows of 1e4-sized ones and records with
-    one large outlier among tiny values all stay within the bound."""
+    """f16 forms: each activation row is scaled into f16's range on its own
+    (hi/lo pairs carry ~22 bits of every element down to 2^-24 of the row's
+    scale), so rows of 1e-6-sized activations, rows of 1e4-sized ones and rows
+    of 1e-3-sized values with an outlier of 3e3 in every record (a range of
+    ~1e7 inside the row) all stay within the bound."""
     n, k, m = 200, 1024, 24
     wbuf, raw = device_weights(ctx, fmt, n, k, seed=77)
     rng = np.random.default_rng(78)
