@@ -577,8 +577,12 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
 #pragma unroll
         for (int g = 0; g < MG; ++g) {
             const size_t pr = ((size_t)(ch * a.splits + split) * crow + 4 * g + c);
-            if (n < a.N) dev_store(a.part + pr * a.N + n, acc[g]);
+            if (n < a.N) {
+                if (a.counters) dev_store(a.part + pr * a.N + n, acc[g]);
+                else a.part[pr * a.N + n] = acc[g];
+            }
         }
+        if (!a.counters) continue;  // partial sums only: k_gemm_split_sum adds them
         dev_stores_done();
         __syncthreads();
         uint32_t* counter = a.counters + ((size_t)ch * a.tiles + tile) * a.cstride;
@@ -641,13 +645,15 @@ RT_DEV h8_t gemm_i8x8_to_h8(i64_t B) {
     return r;
 }
 
-// Activation preparation of the f16 variant: one workgroup per padded
-// activation row m.  The row's largest |x| sets its exponent e (etab[m]):
-// 2^-e brings it into [2^14, 2^15).  Then thread t → (record, k-group of 8
-// elements), the 4 threads of a record neighbours: hi = f16(x·2^-e), lo =
-// f16(x·2^-e − hi) in the A order ([chunk][record][group][lane] 16-byte
-// entries) and, for formats with a min, the records' sums of the scaled
-// values ([chunk][record][row][group]).  Rows past M are zero (e = 0).
+// Activation preparation of the f16 variant: workgroup (m, q) takes padded
+// activation row m and the q-th of its gridDim.y record ranges.  The row's
+// largest |x| (read whole by every workgroup of the row) sets its exponent e
+// (etab[m], written by q = 0): 2^-e brings it into [2^14, 2^15).  Then thread
+// t → (record, k-group of 8 elements), the 4 threads of a record neighbours:
+// hi = f16(x·2^-e), lo = f16(x·2^-e − hi) in the A order ([chunk][record]
+// [group][lane] 16-byte entries) and, for formats with a min, the records'
+// sums of the scaled values ([chunk][record][row][group]).  Rows past M are
+// zero (e = 0).
 template <int MG>
 RT_DEV void gemm_xh_prep_body(const float* __restrict__ x, uint32_t M, uint32_t K, uint32_t nchunks,
                               u32x4* __restrict__ aops, int* __restrict__ etab,
@@ -661,9 +667,16 @@ RT_DEV void gemm_xh_prep_body(const float* __restrict__ x, uint32_t M, uint32_t 
     const float* xr = x + (size_t)(m < M ? m : 0) * K;
     float mx = 0.0f;
     if (m < M)
-        for (uint32_t i = tid * 4; i < K; i += T * 4) {
-            const f32x4 v = *(const f32x4*)(xr + i);
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        for (uint32_t i0 = tid * 4; i0 < K; i0 += T * 32) {  // 8 loads in flight per thread
+            f32x4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t i = i0 + u * T * 4;
+                v[u] = i < K ? *(const f32x4*)(xr + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
         }
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     if ((tid & 63) == 0) red[tid >> 6] = mx;
@@ -671,8 +684,10 @@ RT_DEV void gemm_xh_prep_body(const float* __restrict__ x, uint32_t M, uint32_t 
     mx = 0.0f;
     for (uint32_t w = 0; w < (T >> 6); ++w) mx = fmaxf(mx, red[w]);
     const int e = mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) - 15 : 0;
-    if (tid == 0) etab[m] = e;
-    for (uint32_t t = tid; t < nrec * 4; t += T) {  // (groups of 4 lanes share a trip count)
+    if (tid == 0 && blockIdx.y == 0) etab[m] = e;
+    const uint32_t per = (nrec + gridDim.y - 1) / gridDim.y;
+    const uint32_t r0 = blockIdx.y * per, r1 = min(nrec, r0 + per);
+    for (uint32_t t = r0 * 4 + tid; t < r1 * 4; t += T) {  // (groups of 4 lanes share a trip count)
         const uint32_t kc = t & 3, rec = t >> 2;
         float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         if (m < M) {
@@ -729,8 +744,11 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
     constexpr uint32_t WPT = (WV_N + T - 1) / T;
     constexpr uint32_t APT = (AV4 + T - 1) / T;
     static_assert(SEG % VB == 0 && SV4 <= T, "segment alignment");
-    __shared__ WV lw[2][WV_N];
-    __shared__ u32x4 la[ABUF][AV4];
+    // one LDS block, activation operands first: their reads then take
+    // 16-bit immediate offsets
+    __shared__ u32x4 g3lds[ABUF * AV4 + (2 * WV_N * sizeof(WV) + 15) / 16];
+    u32x4 (*la)[AV4] = (u32x4 (*)[AV4])g3lds;
+    WV (*lw)[WV_N] = (WV (*)[WV_N])(g3lds + ABUF * AV4);
     __shared__ u32x4 ls[P::HAS_MIN ? 2 : 1][P::HAS_MIN ? SV4 : 1];
     __shared__ uint32_t last_flag;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -805,20 +823,25 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
                 }
 #pragma unroll
                 for (int g = 0; g < MG; ++g) {
-                    float t0 = dsc * (C[g][0] + C[g][1]);
-                    float t1 = dsc * (C[g][2] + C[g][3]);
+                    // acc += dsc·(hi + lo) − mn·Σx, as fused multiply-adds
+                    float a0 = __builtin_fmaf(dsc, C[g][0], acc[g][0]);
+                    float a1 = __builtin_fmaf(dsc, C[g][2], acc[g][1]);
+                    a0 = __builtin_fmaf(dsc, C[g][1], a0);
+                    a1 = __builtin_fmaf(dsc, C[g][3], a1);
                     if (GemmSplit16<P>::value) {
                         const f4_t& D = C2[GemmSplit16<P>::value ? g : 0];
-                        t0 += dsc2 * (D[0] + D[1]);
-                        t1 += dsc2 * (D[2] + D[3]);
+                        a0 = __builtin_fmaf(dsc2, D[0], a0);
+                        a1 = __builtin_fmaf(dsc2, D[2], a1);
+                        a0 = __builtin_fmaf(dsc2, D[1], a0);
+                        a1 = __builtin_fmaf(dsc2, D[3], a1);
                     }
-                    const uint32_t i0 = (r * 8 + 2 * c) * MG + g, i1 = i0 + MG;
                     if (P::HAS_MIN) {
-                        t0 -= mn * sb[i0];
-                        t1 -= mn * sb[i1];
+                        const uint32_t i0 = (r * 8 + 2 * c) * MG + g, i1 = i0 + MG;
+                        a0 = __builtin_fmaf(-mn, sb[i0], a0);
+                        a1 = __builtin_fmaf(-mn, sb[i1], a1);
                     }
-                    acc[g][0] += t0;
-                    acc[g][1] += t1;
+                    acc[g][0] = a0;
+                    acc[g][1] = a1;
                 }
             }
         };
@@ -859,8 +882,12 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const size_t pr = ((size_t)(ch * a.splits + split) * crow + 8 * g + 2 * c + i);
-                if (n < a.N) dev_store(a.part + pr * a.N + n, acc[g][i]);
+                if (n < a.N) {
+                    if (a.counters) dev_store(a.part + pr * a.N + n, acc[g][i]);
+                    else a.part[pr * a.N + n] = acc[g][i];
+                }
             }
+        if (!a.counters) continue;  // partial sums only: k_gemm_split_sum adds them
         dev_stores_done();
         __syncthreads();
         uint32_t* counter = a.counters + ((size_t)ch * a.tiles + tile) * a.cstride;
@@ -881,6 +908,24 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
         }
         if (tid == 0) dev_store(counter, 0u);  // ready for the next call (also under graph replay)
         __syncthreads();
+    }
+}
+// Sum of the K splits' partial sums ([chunk][split][crow][N]) into
+// Y[M][N], split by split in split order.  A launch of its own after the
+// GEMM: the kernel boundary makes the partials visible, where an in-kernel
+// hand-off (device-scope stores, an arrival counter, device-scope loads by
+// the last split) cost ~9 µs of a 40 µs GEMM.
+extern "C" __global__ void __launch_bounds__(256) k_gemm_split_sum(const float* __restrict__ part, float* __restrict__ y,
+                                                                 uint32_t M, uint32_t N, uint32_t splits,
+                                                                 uint32_t crow) {
+    const uint64_t total = (uint64_t)M * N;
+    for (uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (uint64_t)gridDim.x * 256) {
+        const uint32_t m = (uint32_t)(idx / N), n = (uint32_t)(idx % N);
+        const uint32_t ch = m / crow, r = m % crow;
+        const float* p = part + ((size_t)ch * splits * crow + r) * N + n;
+        float v = 0.0f;
+        for (uint32_t sp = 0; sp < splits; ++sp) v += p[(size_t)sp * crow * N];
+        y[idx] = v;
     }
 }
 #define RT_GEMM3_KERNEL4(FN, P, MG, NB)                                                       \

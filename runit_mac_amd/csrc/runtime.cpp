@@ -141,7 +141,7 @@ const char* const kKernelNames[] = {
     "k_add_f16_into_f32", "k_ssq_quads", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
     "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32", "k_rope_kv_write_batch_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
-    "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
+    "k_gemm_split_sum", "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
     "k_gemm_q8_0_mg1_ct2", "k_gemm_q8_0_mg2_ct2", "k_gemm_q8_0_mg4_ct2", "k_gemm_q8_0_mg8_ct2",
     "k_gemm2_q8_0_mg1", "k_gemm2_q8_0_mg2", "k_gemm2_q8_0_mg4", "k_gemm2_q8_0_mg8",
@@ -286,6 +286,8 @@ struct rt_ctx {
     const char* last_name = "";  // the last launched kernel (rt_last_launch_name)
     bool gemv_valu = false;      // RUNIT_GEMV_VALU=1: VALU-dot twins of the LDS body (A/B)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
+    bool gemm_sum_kernel = true;  // RUNIT_GEMM_SUM_KERNEL=0: K splits meet in the GEMM (arrival counters)
+    uint32_t gemm_splits = 0;    // RUNIT_GEMM_SPLITS=n: the f16 GEMM's K splits forced (A/B)
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
     bool vs_enabled = true;      // RUNIT_GEMV_VS=0: no VALU small-launch body (A/B)
     uint32_t vs_max_q = kVsMaxQuadsPerCu;  // RUNIT_GEMV_VS_MAXQ: row quads per CU up to which it runs
@@ -1301,6 +1303,8 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_DIRECT")) c->gemm_direct = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_F16")) c->gemm_f16 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_W16")) c->gemm_w16 = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_SPLITS")) c->gemm_splits = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMM_SUM_KERNEL")) c->gemm_sum_kernel = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_SM")) c->sm_enabled = atoi(g) != 0;
@@ -1860,6 +1864,16 @@ struct GemmFmt {
     uint32_t max_mg_f16 = 4;           // the f16 form's 8-row groups per chunk
 };
 
+// Y = the sum of the K splits' partial sums ([chunk][split][crow][N]),
+// in split order (k_gemm_split_sum).
+static int gemm_split_sum(rt_ctx* c, float* part, float* y, uint32_t m, uint32_t n, uint32_t splits,
+                          uint32_t crow) {
+    const uint64_t total = (uint64_t)m * n;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>((total + 255) / 256, (uint64_t)c->cu_count * 8);
+    void* pp[] = {&part, &y, &m, &n, &splits, &crow};
+    return launch(c, "k_gemm_split_sum", dim3(grid), dim3(256), 0, pp);
+}
+
 // f16 matrix-core form of the staged GEMM (k_gemm3_*): 8 activation rows
 // per group (MG ∈ {1, 2, 4}), hi/lo f16 operands prepared by
 // k_gemm_xh_prep_mg*.  Returns kLsDecline where the staged layout does not
@@ -1905,6 +1919,7 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
         const double t = rounds / sp + 0.02 * sp;
         if (t < best - 1e-9) { best = t; splits = sp; }
     }
+    if (c->gemm_splits) splits = std::min<uint32_t>(c->gemm_splits, nblk / NB);
     const uint32_t kbs = ((nblk + splits - 1) / splits + NB - 1) / NB * NB;
     splits = (nblk + kbs - 1) / kbs;
     if (splits > 1 && base > kAttnCounters)
@@ -1924,18 +1939,26 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
         char pk[48];
         snprintf(pk, sizeof pk, "k_gemm_xh_prep_mg%u", MG);
         uint32_t M = m_rows, K = k, nc = nchunks;
-        // one workgroup per padded activation row
-        const uint32_t threads = std::min<uint32_t>(1024, (nrec * 4 + 63) / 64 * 64);
+        // workgroups (padded row, record range): ~2 per CU, ranges of ≥ 16
+        // records; each workgroup also reads its whole row for the row's
+        // exponent (Q8_0 3584-wide rows at M = 32: 5.0 µs with one
+        // workgroup per row)
+        const uint32_t rows = nchunks * 8 * MG;
+        const uint32_t parts = std::max<uint32_t>(1, std::min<uint32_t>((2 * cu + rows - 1) / rows, nrec / 16));
+        const uint32_t threads = k <= 8192 ? 256 : 512;
         void* pp[] = {(void*)&x, &M, &K, &nc, &aops, &erow, &stab};
-        st = launch(c, pk, dim3(nchunks * 8 * MG), dim3(threads), 0, pp);
+        st = launch(c, pk, dim3(rows, parts), dim3(threads), 0, pp);
         if (st != RT_OK) return st;
     }
     uint32_t cstride = 32;
     while (cstride > 1 && (size_t)base * cstride > kAttnCounters) cstride >>= 1;
-    Gemm2Args a2{w, aops, erow, stab, y, part, c->counters,
+    const bool sum_kernel = splits > 1 && c->gemm_sum_kernel;
+    Gemm2Args a2{w, aops, erow, stab, y, part, sum_kernel ? nullptr : c->counters,
                  m_rows, n, nblk, tiles, splits, kbs, nchunks, row_bytes, cstride};
     void* p2[] = {&a2};
-    return launch(c, kn, dim3(std::min(base * splits, cap)), dim3(64 * waves), 0, p2);
+    st = launch(c, kn, dim3(std::min(base * splits, cap)), dim3(64 * waves), 0, p2);
+    if (st != RT_OK || !sum_kernel) return st;
+    return gemm_split_sum(c, part, y, m_rows, n, splits, 8 * MG);
 }
 
 int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, float* y,
@@ -2039,10 +2062,13 @@ int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, floa
     if (staged) {
         uint32_t cstride = 32;  // counters on their own cache lines while they fit
         while (cstride > 1 && (size_t)base * cstride > kAttnCounters) cstride >>= 1;
-        Gemm2Args a2{w, aops, etab, stab, y, part, c->counters,
+        const bool sum_kernel = splits > 1 && c->gemm_sum_kernel;
+        Gemm2Args a2{w, aops, etab, stab, y, part, sum_kernel ? nullptr : c->counters,
                      m_rows, n, nblk, tiles, splits, kbs, nchunks, row_bytes, cstride};
         void* p2[] = {&a2};
-        return launch(c, kn2, dim3(std::min(base * splits, cap)), dim3(64 * waves), 0, p2);
+        st = launch(c, kn2, dim3(std::min(base * splits, cap)), dim3(64 * waves), 0, p2);
+        if (st != RT_OK || !sum_kernel) return st;
+        return gemm_split_sum(c, part, y, m_rows, n, splits, 4 * MG);
     }
     const uint32_t CT = ((n + 31) / 32 >= 2 * cu) ? 2 : 1;
     const uint32_t gx = (n + 16 * CT - 1) / (16 * CT);
