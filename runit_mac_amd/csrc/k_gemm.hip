@@ -722,6 +722,76 @@ RT_DEV void gemm_xh_prep_body(const float* __restrict__ x, uint32_t M, uint32_t 
         float* stab) {                                                                         \
         gemm_xh_prep_body<MG>(x, M, K, nchunks, aops, etab, stab);                             \
     }
+// One-pass form (K ≤ 20,480): workgroup m holds its row in registers
+// (thread t: float4s t, t + 1024, ...), reduces the row's largest |x|, then
+// writes each float4 as half of a 16-byte A entry (hi, lo) — one round trip
+// to memory instead of three.
+template <int MG>
+RT_DEV void gemm_xh_prep1_body(const float* __restrict__ x, uint32_t M, uint32_t K,
+                               uint2* __restrict__ aops, int* __restrict__ etab,
+                               float* __restrict__ stab) {
+    constexpr uint32_t ROWS = 8 * MG, T = 1024, NPT = 5;
+    __shared__ float red[16];
+    const uint32_t nrec = K / 32, nf = K / 4;
+    const uint32_t m = blockIdx.x;
+    const uint32_t ch = m / ROWS, rr = m % ROWS, g = rr / 8, mm = rr % 8;
+    const uint32_t tid = threadIdx.x;
+    const float* xr = x + (size_t)(m < M ? m : 0) * K;
+    f32x4 v[NPT];
+    float mx = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < NPT; ++i) {
+        const uint32_t f = tid + T * i;
+        v[i] = (m < M && f < nf) ? *(const f32x4*)(xr + 4 * f) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < NPT; ++i)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = 0.0f;
+#pragma unroll
+    for (uint32_t w = 0; w < T / 64; ++w) mx = fmaxf(mx, red[w]);
+    const int e = mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) - 15 : 0;
+    if (tid == 0) etab[m] = e;
+#pragma unroll
+    for (uint32_t i = 0; i < NPT; ++i) {
+        const uint32_t f = tid + T * i;
+        if (f >= nf) break;  // (the 8 lanes of a record share this)
+        const uint32_t rec = f >> 3, qf = f & 7, kc = qf >> 1, half = qf & 1;
+        const float xs[4] = {__builtin_amdgcn_ldexpf(v[i].x, -e), __builtin_amdgcn_ldexpf(v[i].y, -e),
+                             __builtin_amdgcn_ldexpf(v[i].z, -e), __builtin_amdgcn_ldexpf(v[i].w, -e)};
+        _Float16 h[4], l[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            h[u] = (_Float16)xs[u];
+            l[u] = (_Float16)(xs[u] - (float)h[u]);
+        }
+        // 16-byte entries 2·mm (hi) and 2·mm + 1 (lo) of k-group kc: this
+        // float4 is their half `half`
+        uint2* base = aops + ((((size_t)ch * nrec + rec) * MG + g) * 64 + 16 * kc + 2 * mm) * 2 + half;
+        base[0] = uint2{(uint32_t)__builtin_bit_cast(uint16_t, h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[1]) << 16),
+                        (uint32_t)__builtin_bit_cast(uint16_t, h[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[3]) << 16)};
+        base[2] = uint2{(uint32_t)__builtin_bit_cast(uint16_t, l[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, l[1]) << 16),
+                        (uint32_t)__builtin_bit_cast(uint16_t, l[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, l[3]) << 16)};
+        if (stab) {
+            float sum = xs[0] + xs[1] + xs[2] + xs[3];
+            sum += __shfl_xor(sum, 1, 64);
+            sum += __shfl_xor(sum, 2, 64);
+            sum += __shfl_xor(sum, 4, 64);
+            if (qf == 0) stab[(((size_t)ch * nrec + rec) * 8 + mm) * MG + g] = sum;
+        }
+    }
+}
+#define RT_GEMM_XH_PREP1(MG)                                                                   \
+    extern "C" __global__ void __launch_bounds__(1024) k_gemm_xh_prep1_mg##MG(                 \
+        const float* x, uint32_t M, uint32_t K, uint2* aops, int* etab, float* stab) {         \
+        gemm_xh_prep1_body<MG>(x, M, K, aops, etab, stab);                                     \
+    }
+RT_GEMM_XH_PREP1(1)
+RT_GEMM_XH_PREP1(2)
+RT_GEMM_XH_PREP1(4)
 RT_GEMM_XH_PREP(1)
 RT_GEMM_XH_PREP(2)
 RT_GEMM_XH_PREP(4)
@@ -918,14 +988,22 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
 extern "C" __global__ void __launch_bounds__(256) k_gemm_split_sum(const float* __restrict__ part, float* __restrict__ y,
                                                                  uint32_t M, uint32_t N, uint32_t splits,
                                                                  uint32_t crow) {
-    const uint64_t total = (uint64_t)M * N;
-    for (uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (uint64_t)gridDim.x * 256) {
-        const uint32_t m = (uint32_t)(idx / N), n = (uint32_t)(idx % N);
-        const uint32_t ch = m / crow, r = m % crow;
-        const float* p = part + ((size_t)ch * splits * crow + r) * N + n;
-        float v = 0.0f;
-        for (uint32_t sp = 0; sp < splits; ++sp) v += p[(size_t)sp * crow * N];
-        y[idx] = v;
+    // grid (⌈N / 1024⌉, M): thread → 4 consecutive outputs of row m
+    const uint32_t m = blockIdx.y, n = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (n >= N) return;
+    const uint32_t ch = m / crow, r = m % crow;
+    const float* p = part + ((size_t)ch * splits * crow + r) * N + n;
+    const size_t ss = (size_t)crow * N;
+    if (n + 4 <= N && N % 4 == 0) {
+        f32x4 v = *(const f32x4*)p;
+        for (uint32_t sp = 1; sp < splits; ++sp) v += *(const f32x4*)(p + sp * ss);
+        *(f32x4*)(y + (size_t)m * N + n) = v;
+    } else {
+        for (uint32_t i = 0; i < 4 && n + i < N; ++i) {
+            float v = p[i];
+            for (uint32_t sp = 1; sp < splits; ++sp) v += p[sp * ss + i];
+            y[(size_t)m * N + n + i] = v;
+        }
     }
 }
 #define RT_GEMM3_KERNEL4(FN, P, MG, NB)                                                       \

@@ -141,7 +141,7 @@ const char* const kKernelNames[] = {
     "k_add_f16_into_f32", "k_ssq_quads", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
     "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32", "k_rope_kv_write_batch_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
-    "k_gemm_split_sum", "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
+    "k_gemm_split_sum", "k_gemm_xh_prep1_mg1", "k_gemm_xh_prep1_mg2", "k_gemm_xh_prep1_mg4", "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
     "k_gemm_q8_0_mg1_ct2", "k_gemm_q8_0_mg2_ct2", "k_gemm_q8_0_mg4_ct2", "k_gemm_q8_0_mg8_ct2",
     "k_gemm2_q8_0_mg1", "k_gemm2_q8_0_mg2", "k_gemm2_q8_0_mg4", "k_gemm2_q8_0_mg8",
@@ -1868,10 +1868,8 @@ struct GemmFmt {
 // in split order (k_gemm_split_sum).
 static int gemm_split_sum(rt_ctx* c, float* part, float* y, uint32_t m, uint32_t n, uint32_t splits,
                           uint32_t crow) {
-    const uint64_t total = (uint64_t)m * n;
-    const uint32_t grid = (uint32_t)std::min<uint64_t>((total + 255) / 256, (uint64_t)c->cu_count * 8);
     void* pp[] = {&part, &y, &m, &n, &splits, &crow};
-    return launch(c, "k_gemm_split_sum", dim3(grid), dim3(256), 0, pp);
+    return launch(c, "k_gemm_split_sum", dim3((n + 1023) / 1024, m), dim3(256), 0, pp);
 }
 
 // f16 matrix-core form of the staged GEMM (k_gemm3_*): 8 activation rows
@@ -1935,7 +1933,15 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
     int* erow = (int*)((char*)c->ws + a_bytes);
     float* stab = s_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes) : nullptr;
     float* part = p_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes + s_bytes) : nullptr;
-    {
+    if (k <= 20480) {
+        // one workgroup per padded row, the row held in registers
+        char pk[48];
+        snprintf(pk, sizeof pk, "k_gemm_xh_prep1_mg%u", MG);
+        uint32_t M = m_rows, K = k;
+        void* pp[] = {(void*)&x, &M, &K, &aops, &erow, &stab};
+        st = launch(c, pk, dim3(nchunks * 8 * MG), dim3(1024), 0, pp);
+        if (st != RT_OK) return st;
+    } else {
         char pk[48];
         snprintf(pk, sizeof pk, "k_gemm_xh_prep_mg%u", MG);
         uint32_t M = m_rows, K = k, nc = nchunks;
