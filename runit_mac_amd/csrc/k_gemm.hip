@@ -430,6 +430,36 @@ struct GemmQ6KT {
         dsc2 = G ? d * (float)(int8_t)((sw >> 8) & 255u) : dsc;
         mn = 0.0f;
     }
+    // Records 4·r4 .. 4·r4 + 3 (super-block r4 / 2, half r4 % 2, t = 0..3) at
+    // once: they share their qh bytes, t and t + 2 their ql bytes, and all
+    // four their scale window and d, so the bytes are read once (5 reads of
+    // 8 bytes instead of 16).
+    static constexpr bool DECODE4 = true;
+    RT_DEV static void decode4(const uint8_t* row, uint32_t r4, uint32_t c, i64_t B[4], float dsc[4],
+                               float dsc2[4]) {
+        const uint32_t b = r4 / 2, hs = r4 % 2;
+        const uint32_t o = b * 210;
+        uint32_t la0, la1, lb0, lb1, h0, h1, sw0, sw1, dw, unused;
+        gemm_bytes8(row, o + 64 * hs + 8 * c, la0, la1);        // ql of t = 0, 2
+        gemm_bytes8(row, o + 64 * hs + 32 + 8 * c, lb0, lb1);   // ql of t = 1, 3
+        gemm_bytes8(row, o + 128 + 32 * hs + 8 * c, h0, h1);    // qh of t = 0..3
+        gemm_bytes8(row, o + 192 + 8 * hs, sw0, sw1);           // sc[8hs .. 8hs + 7]
+        gemm_bytes8(row, o + 208, dw, unused);
+        const float d = h2f(dw);
+#pragma unroll
+        for (uint32_t t = 0; t < 4; ++t) {
+            const uint32_t l0 = (t & 1) ? lb0 : la0, l1 = (t & 1) ? lb1 : la1;
+            const uint32_t s = 4 * (t >> 1);
+            const uint32_t q0 = ((l0 >> s) & 0x0F0F0F0Fu) | (((h0 >> (2 * t)) & 0x03030303u) << 4);
+            const uint32_t q1 = ((l1 >> s) & 0x0F0F0F0Fu) | (((h1 >> (2 * t)) & 0x03030303u) << 4);
+            B[t] = (i64_t)(((uint64_t)((q1 + 0x60606060u) ^ 0x80808080u) << 32) |
+                           ((q0 + 0x60606060u) ^ 0x80808080u));
+            const uint32_t sw = (t >> 1) ? sw1 : sw0;           // sc[8hs + 2t] at byte 2(t & 1)
+            const uint32_t sb = sw >> (16 * (t & 1));
+            dsc[t] = d * (float)(int8_t)(sb & 255u);
+            dsc2[t] = G ? d * (float)(int8_t)((sb >> 8) & 255u) : dsc[t];
+        }
+    }
 };
 using GemmQ6K = GemmQ6KT<false>;
 using GemmQ6KG = GemmQ6KT<true>;
@@ -444,6 +474,15 @@ struct GemmSplit16 {
 template <class P>
 struct GemmSplit16<P, decltype((void)P::SPLIT16)> {
     static constexpr bool value = P::SPLIT16;
+};
+// formats whose records come four at a time from shared bytes (decode4)
+template <class P, class = void>
+struct GemmDecode4 {
+    static constexpr bool value = false;
+};
+template <class P>
+struct GemmDecode4<P, decltype((void)P::DECODE4)> {
+    static constexpr bool value = P::DECODE4;
 };
 
 template <class P, int MG, int NB, int WAVES = 4>
@@ -522,11 +561,8 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
             const uint2* ab = (const uint2*)la[buf];
             const int* eb = (const int*)le[buf];
             const float* sb = (const float*)ls[P::HAS_MIN ? buf : 0];
-#pragma unroll 2
-            for (uint32_t r = 0; r < NR; ++r) {
-                i64_t B;
-                float dsc, mn, dsc2 = 0.0f;
-                P::decode(wb, r, c, B, dsc, mn, dsc2);
+            // record r of the stage from its decoded codes B and scales
+            auto record = [&](uint32_t r, i64_t B, float dsc, float mn, float dsc2) {
                 // all of the record's matrix-core products first, then their
                 // epilogues (independent MFMAs overlap in the pipeline)
                 v4i C[MG], C2[GemmSplit16<P>::value ? MG : 1];
@@ -548,6 +584,24 @@ RT_DEV void gemm2_body(const Gemm2Args& a) {
                     float v = __builtin_amdgcn_ldexpf(t, eb[ei] - 22);
                     if (P::HAS_MIN) v -= mn * sb[ei];
                     acc[g] += v;
+                }
+            };
+            if constexpr (GemmDecode4<P>::value) {
+#pragma unroll 1
+                for (uint32_t r4 = 0; r4 < NR / 4; ++r4) {
+                    i64_t B4[4];
+                    float ds4[4], ds24[4];
+                    P::decode4(wb, r4, c, B4, ds4, ds24);
+#pragma unroll
+                    for (uint32_t q = 0; q < 4; ++q) record(4 * r4 + q, B4[q], ds4[q], 0.0f, ds24[q]);
+                }
+            } else {
+#pragma unroll 2
+                for (uint32_t r = 0; r < NR; ++r) {
+                    i64_t B;
+                    float dsc, mn, dsc2 = 0.0f;
+                    P::decode(wb, r, c, B, dsc, mn, dsc2);
+                    record(r, B, dsc, mn, dsc2);
                 }
             }
         };
@@ -872,11 +926,8 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
             const uint8_t* wb = (const uint8_t*)lw[buf] + wrow;
             const u32x4* ab = la[ABUF == 2 ? buf : 0];
             const float* sb = (const float*)ls[P::HAS_MIN ? buf : 0];
-#pragma unroll 2
-            for (uint32_t r = 0; r < NR; ++r) {
-                i64_t B;
-                float dsc, mn, dsc2 = 0.0f;
-                P::decode(wb, r, c, B, dsc, mn, dsc2);
+            // record r of the stage from its decoded codes B and scales
+            auto record = [&](uint32_t r, i64_t B, float dsc, float mn, float dsc2) {
                 const h8_t Bh = gemm_i8x8_to_h8(B);
                 const h8_t Z = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
                 // ggml Q6_K: elements 0..15 (k-groups c < 2) and 16..31 take
@@ -912,6 +963,24 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
                     }
                     acc[g][0] = a0;
                     acc[g][1] = a1;
+                }
+            };
+            if constexpr (GemmDecode4<P>::value) {
+#pragma unroll 1
+                for (uint32_t r4 = 0; r4 < NR / 4; ++r4) {
+                    i64_t B4[4];
+                    float ds4[4], ds24[4];
+                    P::decode4(wb, r4, c, B4, ds4, ds24);
+#pragma unroll
+                    for (uint32_t q = 0; q < 4; ++q) record(4 * r4 + q, B4[q], ds4[q], 0.0f, ds24[q]);
+                }
+            } else {
+#pragma unroll 2
+                for (uint32_t r = 0; r < NR; ++r) {
+                    i64_t B;
+                    float dsc, mn, dsc2 = 0.0f;
+                    P::decode(wb, r, c, B, dsc, mn, dsc2);
+                    record(r, B, dsc, mn, dsc2);
                 }
             }
         };
