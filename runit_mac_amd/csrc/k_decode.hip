@@ -252,6 +252,14 @@ k_argmax_rows_first_f32(const float* __restrict__ in, uint32_t* __restrict__ out
 RT_ATTN_KERNELS(64)
 RT_ATTN_KERNELS(128)
 RT_ATTN_KERNELS(256)
+// wave form of the RoPE attention (attn_split_w): one query head per
+// workgroup, parts-only or single-split launches
+#define RT_ATTN_W_KERNEL(HD)                                                                \
+    extern "C" __global__ void __launch_bounds__(256) k_attn_rope_w_f32_hd##HD(AttnArgs a) { \
+        attn_split_w<HD>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z);                  \
+    }
+RT_ATTN_W_KERNEL(64)
+RT_ATTN_W_KERNEL(128)
 
 // add_f16_into_f32 (dispatch.rs:316-330): acc[i] += f32(src[i]), the bias add
 // of the reference's separate-dispatch Q/K/V fallback (forward.rs:1561-1568).

@@ -375,3 +375,166 @@ RT_DEV void attn_split(const AttnArgs& a, uint32_t s, uint32_t nsp, uint32_t y, 
 template <int HD> constexpr int attn_hg() { return (int)rt_attn_hg(HD); }
 template <int HD> constexpr int attn_gm() { return (int)rt_attn_gm(HD); }
 
+
+// ───────────── decode attention, wave form (one query head, RoPE) ─────────────
+//
+// The token's attention for one query head over one split of the KV range,
+// with the split's positions spread over the 4 waves of a 256-thread
+// workgroup: lane l of wave w holds dims [16·(l mod LPP), +16) of position
+// p0 + PPW·w + l / LPP (LPP = HD/16 lanes per position, PPW = 64/LPP
+// positions per wave), with the next step's K / V rows in flight.  Scores,
+// the running max, the exponentials and the probability-weighted values are
+// reduced inside the wave (cross-lane adds), each wave keeps its own running
+// (m, l, o), and the 4 waves' states meet in LDS once, at the end — one
+// barrier after the query staging and one for that merge, where attn_split
+// takes three per 64 positions.  Output as attn_split's: the normalised o
+// (one split) or the split's (o, m, l) for the consumer to merge.
+template <int HD>
+RT_DEV void attn_split_w(const AttnArgs& a, uint32_t s, uint32_t nsp, uint32_t y, uint32_t b) {
+    constexpr uint32_t LPP = HD / 16, PPW = 64 / LPP, PPS = 4 * PPW, C4 = HD / 4, half = HD / 2;
+    static_assert(HD == 64 || HD == 128, "head size");
+    __shared__ f32x4 qs4[C4], ks4[C4], vs4[C4];
+    __shared__ f32x4 wo[4][C4];
+    __shared__ float wm[4], wl[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t G = a.H / a.KVH;
+    const uint32_t kvh = y / G, hb = y % G;  // one query head per workgroup
+    const uint32_t h = kvh * G + hb;
+    const size_t kvb = ((size_t)b * a.KVH + kvh) * a.stride * HD;
+    float* kc = a.kc + kvb;
+    float* vc = a.vc + kvb;
+    const uint32_t p_begin = s * a.chunk, p_end = min(a.kv_len, p_begin + a.chunk);
+    const uint32_t kq = lane % LPP, pl = lane / LPP;
+    auto load_kv = [&](uint32_t p0, f32x4 (&kr)[4], f32x4 (&vr)[4]) {
+        const uint32_t p = p0 + PPW * w + pl;
+        const size_t pc = p < p_end ? p : p_begin;
+        const f32x4* kp = (const f32x4*)(kc + pc * HD) + 4 * kq;
+        const f32x4* vp = (const f32x4*)(vc + pc * HD) + 4 * kq;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = kp[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vr[i] = vp[i];
+    };
+    // the token's raw q / k (one RoPE pair per thread: threads [0, half) the
+    // query, [half, HD) the key) and v (threads [HD, 2·HD)), loaded ahead of
+    // the K / V rows
+    const bool pair = tid < HD, isv = tid >= HD && tid < 2 * HD;
+    const uint32_t d = tid % half;
+    const float* src = tid < half ? a.q + (size_t)(b * a.H + h) * HD : a.k_new + (size_t)kvh * HD;
+    float re = 0.0f, im = 0.0f, vv = 0.0f;
+    if (pair) {
+        re = src[d];
+        im = src[d + half];
+    }
+    if (isv) vv = a.v_new[(size_t)kvh * HD + (tid - HD)];
+    f32x4 kr[4], vr[4];
+    if (p_begin < p_end) load_kv(p_begin, kr, vr);
+    if (pair) {
+        // fused_rope_qk_f32 (fused_rope.metal:28-55)
+        float c, sn;
+        rope_cs(d, HD, a.pos, a.theta, c, sn);
+        float* dst = tid < half ? (float*)qs4 : (float*)ks4;
+        dst[d] = re * c - im * sn;
+        dst[d + half] = re * sn + im * c;
+    }
+    if (isv) ((float*)vs4)[tid - HD] = vv;
+    lds_barrier();
+    // kv_copy_to_cache_f32 (activation.metal:30-45) of the rotated key and the
+    // value, by the first head's workgroup whose range holds `pos`
+    if (hb == 0 && a.pos >= p_begin && a.pos < p_end && tid < C4) {
+        ((f32x4*)(kc + (size_t)a.pos * HD))[tid] = ks4[tid];
+        ((f32x4*)(vc + (size_t)a.pos * HD))[tid] = vs4[tid];
+    }
+    f32x4 qv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qv[i] = qs4[4 * kq + i];
+    float m = -__builtin_huge_valf(), l = 0.0f;
+    f32x4 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // sum / max over the wave's positions (lanes ≡ kq mod LPP)
+    auto pos_sum = [&](float v) {
+#pragma unroll
+        for (uint32_t x = LPP; x < 32; x <<= 1) v += __shfl_xor(v, x, 64);
+        return v + __shfl_xor(v, 32, 64);
+    };
+    auto pos_max = [&](float v) {
+#pragma unroll
+        for (uint32_t x = LPP; x < 32; x <<= 1) v = fmaxf(v, __shfl_xor(v, x, 64));
+        return fmaxf(v, __shfl_xor(v, 32, 64));
+    };
+    for (uint32_t p0 = p_begin; p0 < p_end; p0 += PPS) {
+        f32x4 kn[4], vn[4];
+        if (p0 + PPS < p_end) load_kv(p0 + PPS, kn, vn);  // next step (workgroup-uniform)
+        const uint32_t p = p0 + PPW * w + pl;
+        const bool valid = p < p_end;
+        if (p == a.pos) {  // the token's own row (the cache write may not be visible yet)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kr[i] = ks4[4 * kq + i];
+                vr[i] = vs4[4 * kq + i];
+            }
+        }
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            dot += qv[i].x * kr[i].x + qv[i].y * kr[i].y + qv[i].z * kr[i].z + qv[i].w * kr[i].w;
+        dot = group_sum(dot, LPP);
+        const float sc = valid ? dot * a.scale : -__builtin_huge_valf();
+        const float m_new = fmaxf(m, pos_max(sc));
+        // (a wave whose positions are all past the range keeps m = −∞)
+        const float e = valid ? expf(sc - m_new) : 0.0f;
+        const float r = (m == -__builtin_huge_valf()) ? 0.0f : expf(m - m_new);
+        l = l * r + pos_sum(e);  // (e is the same in the LPP lanes of a position)
+        m = m_new;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = o[i] * r + e * vr[i];
+        if (p0 + PPS < p_end) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kr[i] = kn[i];
+                vr[i] = vn[i];
+            }
+        }
+    }
+    // the wave's o over its positions, then the 4 waves' states in LDS
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        o[i].x = pos_sum(o[i].x);
+        o[i].y = pos_sum(o[i].y);
+        o[i].z = pos_sum(o[i].z);
+        o[i].w = pos_sum(o[i].w);
+    }
+    if (lane < LPP) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wo[w][4 * kq + i] = o[i];
+    }
+    if (lane == 0) {
+        wm[w] = m;
+        wl[w] = l;
+    }
+    lds_barrier();
+    if (tid < C4) {
+        float M = -__builtin_huge_valf();
+#pragma unroll
+        for (int v = 0; v < 4; ++v) M = fmaxf(M, wm[v]);
+        float L = 0.0f;
+        f32x4 O = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float f = wm[v] == -__builtin_huge_valf() ? 0.0f : expf(wm[v] - M);
+            L += wl[v] * f;
+            O += wo[v][tid] * f;
+        }
+        if (nsp == 1 && !a.parts_only) {
+            ((f32x4*)(a.out + ((size_t)b * a.H + h) * HD))[tid] = O * (L > 0.0f ? 1.0f / L : 0.0f);
+        } else {
+            const size_t row = ((size_t)b * a.H + h) * nsp + s;
+            ((f32x4*)(a.part + row * HD))[tid] = O;
+            if (tid == 0) {
+                a.ml[row * 2] = M;
+                a.ml[row * 2 + 1] = L;
+            }
+        }
+    }
+}

@@ -138,6 +138,7 @@ const char* const kKernelNames[] = {
     "k_rms_norm_f32g", "k_rope_qk_f32", "k_kv_copy_f32",
     "k_decode_attention_f32_hd64", "k_decode_attention_f32_hd128", "k_decode_attention_f32_hd256",
     "k_attn_rope_f32_hd64", "k_attn_rope_f32_hd128", "k_attn_rope_f32_hd256",
+    "k_attn_rope_w_f32_hd64", "k_attn_rope_w_f32_hd128",
     "k_add_f16_into_f32", "k_ssq_quads", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
     "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32", "k_rope_kv_write_batch_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
@@ -288,6 +289,7 @@ struct rt_ctx {
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool gemm_sum_kernel = true;  // RUNIT_GEMM_SUM_KERNEL=0: K splits meet in the GEMM (arrival counters)
     uint32_t gemm_splits = 0;    // RUNIT_GEMM_SPLITS=n: the f16 GEMM's K splits forced (A/B)
+    bool attn_w = true;          // RUNIT_ATTN_W=0: the token's RoPE attention on attn_split (A/B)
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
     bool vs_enabled = true;      // RUNIT_GEMV_VS=0: no VALU small-launch body (A/B)
     uint32_t vs_max_q = kVsMaxQuadsPerCu;  // RUNIT_GEMV_VS_MAXQ: row quads per CU up to which it runs
@@ -1311,6 +1313,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_VALU")) c->gemv_valu = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LSK_WHOLE")) c->lsk_whole = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_ATTN_W")) c->attn_w = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_VS")) c->vs_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_VS_MAXQ")) c->vs_max_q = (uint32_t)atoi(g);
     std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
@@ -2416,6 +2419,14 @@ static int attn_launch(rt_ctx* c, const char* kname, AttnArgs a, uint32_t batch,
     if (used) *used = a;
     void* params[] = {&a};
     const uint32_t nt = 256 * rt_attn_hg(hd);  // 256 threads per head group
+    // the wave form for the token's RoPE attention at head sizes 64 / 128
+    // when no split merge is needed in the launch
+    if (c->attn_w && gm == 1 && a.q_len == 0 && (a.parts_only || nsplit == 1) &&
+        strncmp(kname, "k_attn_rope_f32_hd", 18) == 0 && (hd == 64 || hd == 128)) {
+        char wn[48];
+        snprintf(wn, sizeof wn, "k_attn_rope_w_f32_hd%u", hd);
+        if (c->fns.count(wn)) return launch(c, wn, dim3(nsplit, a.KVH * HB, batch), dim3(256), 0, params);
+    }
     return launch(c, kname, dim3(nsplit, a.KVH * HB, batch), dim3(nt), 0, params);
 }
 
