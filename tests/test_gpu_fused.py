@@ -215,6 +215,23 @@ def test_gemm_q8_0(ctx, m, n, k):
         check_close(y2.read(np.float32, 2 * n), yref[:2].ravel(), sabs[:2].ravel(), "gemm m=2")
 
 
+@pytest.mark.parametrize("m", [12, 32])
+def test_gemm_f16_form_long_rows(ctx, m):
+    """Rows longer than 20,480 elements: the f16 form's activations are
+    prepared by the multi-workgroup pass (record ranges, every workgroup
+    reducing its row's maximum), the K range split over workgroups and the
+    splits summed by their own launch."""
+    n, k = 96, 24576
+    wbuf, raw = device_weights(ctx, "q8_0", n, k, seed=m + 91)
+    x = np.random.default_rng(m + 92).standard_normal((m, k)).astype(np.float32)
+    x[:, ::997] *= 50.0  # a wider range inside each row
+    y = ctx.new_buffer(4 * m * n)
+    d.gemm_q8_0_f32(ctx, wbuf, ctx.buffer_from(x), y, m, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv("q8_0", raw, x, n, k)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm long rows m={m}")
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "q4k"])
 @pytest.mark.parametrize("m", [2, 4, 7, 16, 32, 37])
 @pytest.mark.parametrize("n,k", [(512, 1024), (130, 3584), (70, 8192)])
