@@ -421,7 +421,7 @@ def bench_decode(ctx, steps: int, warmup: int, verify_forms: bool = True) -> dic
                 L["bq"], L["bk"], L["bv"], cfg.q_dim, kvd, h)),
             # weights + x + gamma + f16 biases + outputs
             "bytes": wq + 4 * h * 2 + 2 * (cfg.q_dim + 2 * kvd) + 4 * (cfg.q_dim + 2 * kvd),
-            "pmc": None},
+            "pmc": "qkv_q8_0_0p5b_pmc_traffic.md"},
     }
     # keyed by the kernel the library launched for each
     kernels = {nm: dict(kk, launch=key) for nm, (key, kk) in zip(names, kernels.items())}
@@ -611,6 +611,27 @@ def profile_pass(ctx, launches: int = 24) -> None:
     for w in downs5:
         d.gemv_q8_0_add_f32_f32in(ctx, w, act, y5, y5, h, ff)
     ctx.flush()
+    # the 0.5B norm-fused Q/K/V + biases (1152x896) over the same number of
+    # replicas
+    qd, kvd = cfg.q_dim, cfg.kv_dim
+    wqb, wkb = d.weight_bytes("q8_0", qd, h), d.weight_bytes("q8_0", kvd, h)
+    arena_q = _arena_for(ctx, [wqb, wkb, wkb], launches)
+    qkvs = []
+    for r in range(launches):
+        wq_, wk_, wv_ = arena_q.take(wqb), arena_q.take(wkb), arena_q.take(wkb)
+        d.synth_weights(ctx, "q8_0", wq_, qd * h // 32, 500 + 3 * r)
+        d.synth_weights(ctx, "q8_0", wk_, kvd * h // 32, 501 + 3 * r)
+        d.synth_weights(ctx, "q8_0", wv_, kvd * h // 32, 502 + 3 * r)
+        qkvs.append((wq_, wk_, wv_))
+    bq, bk, bv = (ctx.new_buffer(2 * n + 4) for n in (qd, kvd, kvd))
+    for b_, n in ((bq, qd), (bk, kvd), (bv, kvd)):
+        d.synth_normal_f16(ctx, b_, n, 11 + n, 0.0, 0.02)
+    oq, ok_, ov = ctx.new_buffer(4 * qd), ctx.new_buffer(4 * kvd), ctx.new_buffer(4 * kvd)
+    ctx.flush()
+    for wq_, wk_, wv_ in qkvs:
+        d.rms_norm_fused_qkv_bias_q8_0_f32(ctx, wq_, wk_, wv_, x, gamma, cfg.eps, oq, ok_, ov,
+                                           bq, bk, bv, qd, kvd, h)
+    ctx.flush()
     # the 7B Q4_K gate+up+SiLU (LDS-streamed body) over 8 replicas of 76 MB
     ff7, h7 = 18944, 3584
     wb7 = d.weight_bytes("q4k", ff7, h7)
@@ -649,10 +670,12 @@ def profile_pass(ctx, launches: int = 24) -> None:
     ctx.flush()
     log(f"profile pass: {launches} x k_ffn_q8_0 ({2 * wb} weight bytes each), "
         f"{launches} x k_gemv_q8_0_f32_f32add ({wd5} weight bytes each), "
+        f"{launches} x k_qkv_bias_q8_0 ({wqb + 2 * wkb} weight bytes each), "
         f"8 x k_ffn_q4k ({2 * wb7} weight bytes each), "
         f"3 x k_stream_copy ({copy_bytes} bytes each)")
-    for b in (src, dst, x, gamma, act, x7, act7, y5):
+    for b in (src, dst, x, gamma, act, x7, act7, y5, bq, bk, bv, oq, ok_, ov):
         b.free()
+    arena_q.free()
     arena_d5.free()
     arena.free()
     arena7.free()
