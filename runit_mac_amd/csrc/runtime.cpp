@@ -290,6 +290,7 @@ struct rt_ctx {
     bool gemm_sum_kernel = true;  // RUNIT_GEMM_SUM_KERNEL=0: K splits meet in the GEMM (arrival counters)
     uint32_t gemm_splits = 0;    // RUNIT_GEMM_SPLITS=n: the f16 GEMM's K splits forced (A/B)
     bool attn_w = true;          // RUNIT_ATTN_W=0: the token's RoPE attention on attn_split (A/B)
+    uint32_t gemm_f16_min = 4;   // RUNIT_GEMM_F16_MIN: batches above this many rows run the f16 form
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
     bool vs_enabled = true;      // RUNIT_GEMV_VS=0: no VALU small-launch body (A/B)
     uint32_t vs_max_q = kVsMaxQuadsPerCu;  // RUNIT_GEMV_VS_MAXQ: row quads per CU up to which it runs
@@ -1313,6 +1314,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_LS_MIN")) c->ls_min_items = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_VALU")) c->gemv_valu = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LSK_WHOLE")) c->lsk_whole = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_F16_MIN")) c->gemm_f16_min = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_ATTN_W")) c->attn_w = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_VS")) c->vs_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_VS_MAXQ")) c->vs_max_q = (uint32_t)atoi(g);
@@ -1984,9 +1986,11 @@ int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, floa
         return fail(c, RT_ERR_DISPATCH,
                     "kernel dispatch error: gemm_%s_f32: input must be 16-byte aligned", f.name);
     if (m_rows == 1) return f.gemv(c, w, x, y, n, k);
-    // f16 form from 9 rows on (two or more 8-row groups; at M = 16 / 32 it
-    // runs 3-15% faster than the int8 limb form, at M ≤ 8 up to 25% slower)
-    if (c->gemm_f16 && m_rows > 8) {
+    // f16 form from 5 rows on (with one exponent per activation row it runs
+    // M = 8 faster than the int8 limb form: Q8_0 18944×3584 27.7 → 25.9 µs,
+    // Q6_K 3584×18944 51.0 → 42.6 µs; at M = 4 the int8 form stays ahead:
+    // 24.1 against 25.8 µs)
+    if (c->gemm_f16 && m_rows > c->gemm_f16_min) {
         const int st = gemm3_launch(c, f, w, x, y, m_rows, n, k);
         if (st != kLsDecline) return st;
     }
