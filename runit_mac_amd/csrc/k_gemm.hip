@@ -853,8 +853,11 @@ RT_GEMM_XH_PREP(4)
 // ABUF = 1: the activation operands of a stage in one LDS buffer (the
 // weights keep two), refilled after a barrier that ends every wave's reads —
 // the Q6_K form at 32 rows, whose two buffers would not fit the LDS.
-template <class P, int MG, int NB, int WAVES = 4, int ABUF = 2>
+// WBUF = 1: the weights in one LDS buffer as well (the same barrier ends
+// the stage's reads of both) — the Q6_K 128-row tiles at 32 rows.
+template <class P, int MG, int NB, int WAVES = 4, int ABUF = 2, int WBUF = 2>
 RT_DEV void gemm3_body(const Gemm2Args& a) {
+    static_assert(WBUF == 2 || ABUF == 1, "one weight buffer needs the operand barrier");
     constexpr uint32_t T = 64 * WAVES, ROWS = 16 * WAVES;
     constexpr uint32_t NR = NB * P::RECS;
     constexpr uint32_t SEG = NB * P::BLK_BYTES;
@@ -870,7 +873,7 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
     static_assert(SEG % VB == 0 && SV4 <= T, "segment alignment");
     // one LDS block, activation operands first: their reads then take
     // 16-bit immediate offsets
-    __shared__ u32x4 g3lds[ABUF * AV4 + (2 * WV_N * sizeof(WV) + 15) / 16];
+    __shared__ u32x4 g3lds[ABUF * AV4 + (WBUF * WV_N * sizeof(WV) + 15) / 16];
     u32x4 (*la)[AV4] = (u32x4 (*)[AV4])g3lds;
     WV (*lw)[WV_N] = (WV (*)[WV_N])(g3lds + ABUF * AV4);
     __shared__ u32x4 ls[P::HAS_MIN ? 2 : 1][P::HAS_MIN ? SV4 : 1];
@@ -896,9 +899,14 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
         auto gload = [&](uint32_t st) {
             const uint32_t b0 = kb0 + st * NB;
             const uint32_t r0 = b0 * P::RECS;
+            // many loads per thread at 8 waves (Q6_K: 27): the load offsets
+            // recomputed per stage, not held in registers across the item
+            // loop (held, they spilled: Q6_K M = 32 74 µs against 50 µs)
+            uint32_t tidw = tid;
+            if (WAVES >= 8 && WPT > 16) asm volatile("" : "+v"(tidw));
 #pragma unroll
             for (uint32_t i = 0; i < WPT; ++i) {
-                uint32_t f = tid + T * i;
+                uint32_t f = tidw + T * i;
                 if (f >= WV_N) f = WV_N - 1;  // duplicate load, not stored
                 const uint32_t r = f / WPR, col = f % WPR;
                 const uint32_t n = min(row0 + r, a.N - 1);
@@ -912,7 +920,7 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
         auto lstore = [&](uint32_t buf) {
 #pragma unroll
             for (uint32_t i = 0; i < WPT; ++i)
-                if (tid + T * i < WV_N) lw[buf][tid + T * i] = rw[i];
+                if (tid + T * i < WV_N) lw[WBUF == 2 ? buf : 0][tid + T * i] = rw[i];
 #pragma unroll
             for (uint32_t i = 0; i < APT; ++i)
                 if (tid + T * i < AV4) la[ABUF == 2 ? buf : 0][tid + T * i] = ra[i];
@@ -923,7 +931,7 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
         for (int g = 0; g < MG; ++g) acc[g][0] = acc[g][1] = 0.0f;
         const uint32_t wrow = (16 * wv + j) * SEG;
         auto compute = [&](uint32_t buf) {
-            const uint8_t* wb = (const uint8_t*)lw[buf] + wrow;
+            const uint8_t* wb = (const uint8_t*)lw[WBUF == 2 ? buf : 0] + wrow;
             const u32x4* ab = la[ABUF == 2 ? buf : 0];
             const float* sb = (const float*)ls[P::HAS_MIN ? buf : 0];
             // record r of the stage from its decoded codes B and scales
@@ -1126,6 +1134,23 @@ RT_GEMM3_KERNEL4(q6kg, GemmQ6KG, 2, 2)
     }
 RT_GEMM3_KERNEL4A1(q6k, GemmQ6K, 4, 2)
 RT_GEMM3_KERNEL4A1(q6kg, GemmQ6KG, 4, 2)
+// 128-row tiles at 8 rows, both buffers doubled (137 KB)
+extern "C" __global__ void __launch_bounds__(512) k_gemm3_q6k_mg1_w8(Gemm2Args a) {
+    gemm3_body<GemmQ6K, 1, 2, 8>(a);
+}
+extern "C" __global__ void __launch_bounds__(512) k_gemm3_q6kg_mg1_w8(Gemm2Args a) {
+    gemm3_body<GemmQ6KG, 1, 2, 8>(a);
+}
+// 128-row tiles at 16 / 32 rows: one operand and one weight buffer (84.5 /
+// 116.5 KB)
+#define RT_GEMM3_KERNEL8A1(FN, P, MG, NB)                                                     \
+    extern "C" __global__ void __launch_bounds__(512) k_gemm3_##FN##_mg##MG##_w8(Gemm2Args a) { \
+        gemm3_body<P, MG, NB, 8, 1, 1>(a);                                                     \
+    }
+RT_GEMM3_KERNEL8A1(q6k, GemmQ6K, 4, 2)
+RT_GEMM3_KERNEL8A1(q6kg, GemmQ6KG, 4, 2)
+RT_GEMM3_KERNEL8A1(q6k, GemmQ6K, 2, 2)
+RT_GEMM3_KERNEL8A1(q6kg, GemmQ6KG, 2, 2)
 
 #define RT_GEMM2_KERNEL4(FN, P, MG, NB)                                                       \
     extern "C" __global__ void __launch_bounds__(256) k_gemm2_##FN##_mg##MG(Gemm2Args a) {    \

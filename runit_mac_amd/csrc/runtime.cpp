@@ -171,7 +171,8 @@ const char* const kKernelNames[] = {
     "k_gemm3_q5k_mg4", "k_gemm3_q5k_mg4_w8", "k_gemm3_q5kg_mg1", "k_gemm3_q5kg_mg1_w8",
     "k_gemm3_q5kg_mg2", "k_gemm3_q5kg_mg2_w8", "k_gemm3_q5kg_mg4", "k_gemm3_q5kg_mg4_w8",
     "k_gemm3_q6k_mg1", "k_gemm3_q6k_mg2", "k_gemm3_q6k_mg4", "k_gemm3_q6kg_mg1", "k_gemm3_q6kg_mg2",
-    "k_gemm3_q6kg_mg4",
+    "k_gemm3_q6kg_mg4", "k_gemm3_q6k_mg1_w8", "k_gemm3_q6kg_mg1_w8", "k_gemm3_q6k_mg2_w8", "k_gemm3_q6k_mg4_w8", "k_gemm3_q6kg_mg2_w8",
+    "k_gemm3_q6kg_mg4_w8",
     "k_gemm_xh_prep_mg1", "k_gemm_xh_prep_mg2", "k_gemm_xh_prep_mg4",
 };
 
@@ -291,10 +292,12 @@ struct rt_ctx {
     uint32_t gemm_splits = 0;    // RUNIT_GEMM_SPLITS=n: the f16 GEMM's K splits forced (A/B)
     bool attn_w = true;          // RUNIT_ATTN_W=0: the token's RoPE attention on attn_split (A/B)
     uint32_t gemm_f16_min = 4;   // RUNIT_GEMM_F16_MIN: batches above this many rows run the f16 form
+    uint32_t gemm_f16_min_q6 = 1;  // RUNIT_GEMM_F16_MIN_Q6: the same for Q6_K
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
     bool vs_enabled = true;      // RUNIT_GEMV_VS=0: no VALU small-launch body (A/B)
     uint32_t vs_max_q = kVsMaxQuadsPerCu;  // RUNIT_GEMV_VS_MAXQ: row quads per CU up to which it runs
     bool gemm_w16 = true;        // RUNIT_GEMM_W16=0: no 256-row tiles (A/B)
+    int gemm_q6w8 = 7;           // RUNIT_GEMM_Q6W8: Q6_K f16 form on 128-row tiles at MG = 4 / 2 / 1 (bits 0 / 1 / 2)
     bool gemm_f16 = true;        // RUNIT_GEMM_F16=0: the int8 limb form of the staged GEMM at every M
     // Small per-context device buffer: argmax range states + arrival counter
     // (the counter is reset by the kernel that consumes it).
@@ -1306,6 +1309,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_DIRECT")) c->gemm_direct = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_F16")) c->gemm_f16 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_W16")) c->gemm_w16 = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_Q6W8")) c->gemm_q6w8 = atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_SPLITS")) c->gemm_splits = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_SUM_KERNEL")) c->gemm_sum_kernel = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
@@ -1315,6 +1319,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMV_VALU")) c->gemv_valu = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LSK_WHOLE")) c->lsk_whole = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_F16_MIN")) c->gemm_f16_min = (uint32_t)atoi(g);
+    if (const char* g = getenv("RUNIT_GEMM_F16_MIN_Q6")) c->gemm_f16_min_q6 = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_ATTN_W")) c->attn_w = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_VS")) c->vs_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_VS_MAXQ")) c->vs_max_q = (uint32_t)atoi(g);
@@ -1894,8 +1899,10 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
     const uint32_t seg = NB * f.blk_bytes, vb = seg % 16 == 0 ? 16 : (seg % 8 == 0 ? 8 : 4);
     if (nblk % NB != 0 || !aligned(w, 16) || row_bytes % vb != 0 || c->gemm_direct)
         return kLsDecline;
-    const bool w8ok = f.blk_bytes != 210;
-    uint32_t waves = (MG >= 2 && f.blk_bytes != 34 && w8ok ? 8 : 4);
+    // Q6_K: 128-row tiles with one operand and one weight buffer
+    const bool q6 = f.blk_bytes == 210;
+    const bool w8ok = !q6 || (c->gemm_q6w8 >> (MG == 4 ? 0 : MG == 2 ? 1 : 2) & 1);
+    uint32_t waves = ((MG >= 2 || q6) && f.blk_bytes != 34 && w8ok ? 8 : 4);
     char kn[48];
     snprintf(kn, sizeof kn, waves == 8 ? "k_gemm3_%s_mg%u_w8" : "k_gemm3_%s_mg%u", f.name, MG);
     // 256-row tiles (16 waves share each stage of activation operands: a
@@ -1989,8 +1996,9 @@ int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, floa
     // f16 form from 5 rows on (with one exponent per activation row it runs
     // M = 8 faster than the int8 limb form: Q8_0 18944×3584 27.7 → 25.9 µs,
     // Q6_K 3584×18944 51.0 → 42.6 µs; at M = 4 the int8 form stays ahead:
-    // 24.1 against 25.8 µs)
-    if (c->gemm_f16 && m_rows > c->gemm_f16_min) {
+    // 24.1 against 25.8 µs); Q6_K from 2 rows on (its 128-row f16 tiles:
+    // M = 2 / 4 on 3584×18944 42.8 / 43.0 → 36.5 / 36.7 µs)
+    if (c->gemm_f16 && m_rows > (f.blk_bytes == 210 ? c->gemm_f16_min_q6 : c->gemm_f16_min)) {
         const int st = gemm3_launch(c, f, w, x, y, m_rows, n, k);
         if (st != kLsDecline) return st;
     }
