@@ -159,7 +159,8 @@ const char* const kKernelNames[] = {
     "k_gemm2_q6k_mg1", "k_gemm2_q6k_mg2", "k_gemm2_q6k_mg4",
     "k_gemm2_q6kg_mg1", "k_gemm2_q6kg_mg2", "k_gemm2_q6kg_mg4",
     "k_gemm3_q8_0_mg1", "k_gemm3_q8_0_mg1_w8", "k_gemm3_q8_0_mg2", "k_gemm3_q8_0_mg2_w8",
-    "k_gemm3_q8_0_mg4", "k_gemm3_q8_0_mg4_w8", "k_gemm3_q8_0_mg4_w16", "k_gemm3_q4_0_mg1", "k_gemm3_q4_0_mg1_w8",
+    "k_gemm3_q8_0_mg4", "k_gemm3_q8_0_mg4_w8", "k_gemm3_q8_0_mg4_w16", "k_gemm3_q4k_mg4_w16", "k_gemm3_q4kg_mg4_w16",
+    "k_gemm3_q5k_mg4_w16", "k_gemm3_q5kg_mg4_w16", "k_gemm3_q4_0_mg1", "k_gemm3_q4_0_mg1_w8",
     "k_gemm3_q4_0_mg2", "k_gemm3_q4_0_mg2_w8", "k_gemm3_q4_0_mg4", "k_gemm3_q4_0_mg4_w8",
     "k_gemm3_q4k_mg1", "k_gemm3_q4k_mg1_w8", "k_gemm3_q4k_mg2", "k_gemm3_q4k_mg2_w8",
     "k_gemm3_q4k_mg4", "k_gemm3_q4k_mg4_w8", "k_gemm3_q4kg_mg1", "k_gemm3_q4kg_mg1_w8",
