@@ -1930,6 +1930,24 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
         const double t = rounds / sp + 0.02 * sp;
         if (t < best - 1e-9) { best = t; splits = sp; }
     }
+    // splits as launched: K ranges of whole stages
+    auto eff = [&](uint32_t sp) {
+        const uint32_t kb = ((nblk + sp - 1) / sp + NB - 1) / NB * NB;
+        return (nblk + kb - 1) / kb;
+    };
+    // One workgroup per CU: where the chosen split leaves more than a tenth of
+    // the CUs idle, the next larger split whose items still fit 1.15 rounds
+    // (Q6_K 3584×18944 at M = 8 / 16 / 32: 8 splits of 5 stages for 7 of 6,
+    // 37.1 / 41.9 / 50.0 → 33.9 / 38.4 / 45.2 µs, where 10 of 4 took 35.6 /
+    // 40.2 / 47.7; Q4_K 18944×3584 keeps 3, where 4 took 34.0 → 41.8 µs, and
+    // Q6_K 18944×3584 keeps 1, 45.1 against 53.1 µs)
+    if (per_cu == 1 && (uint64_t)base * eff(splits) * 10 < (uint64_t)cap * 9) {
+        for (uint32_t sp = splits + 1; sp <= std::min<uint32_t>(16, nblk / NB); ++sp) {
+            if (eff(sp) <= eff(splits)) continue;
+            if ((uint64_t)base * eff(sp) * 100 <= (uint64_t)cap * 115) splits = sp;
+            break;
+        }
+    }
     if (c->gemm_splits) splits = std::min<uint32_t>(c->gemm_splits, nblk / NB);
     const uint32_t kbs = ((nblk + splits - 1) / splits + NB - 1) / NB * NB;
     splits = (nblk + kbs - 1) / kbs;
