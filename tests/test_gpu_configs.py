@@ -96,6 +96,23 @@ def test_config5_gemm_q8_0_7b(ctx, m):
         check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("fmt,n,k,m", [("q6k", 3584, 18944, 2), ("q6k", 3584, 18944, 8),
+                                       ("q6k", 3584, 18944, 32), ("q6kg", 3584, 18944, 32),
+                                       ("q4k", 18944, 3584, 4), ("q4k", 18944, 3584, 32),
+                                       ("q4_0", 18944, 3584, 32)])
+def test_config5_gemm_4bit_q6k_7b(ctx, fmt, n, k, m):
+    # the bench's batched 4-bit / Q6_K lines at full size: Q6_K on 128-row
+    # tiles with the planner's K splits filling the CUs (28 tiles × 8
+    # splits), Q4_K on 256-row tiles at 32 rows, the int8 form at 4
+    wbuf, raw = device_weights(ctx, fmt, n, k, 170 + m)
+    x = np.random.default_rng(m + 1).standard_normal((m, k)).astype(np.float32)
+    y = ctx.new_buffer(4 * m * n)
+    getattr(d, f"gemm_{fmt}_f32")(ctx, wbuf, ctx.buffer_from(x), y, m, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm {fmt} {m}x{n}x{k}")
+
+
 @pytest.mark.parametrize("fmt", ["q4kg", "q5k", "q5_0"])
 def test_7b_ffn_other_formats(ctx, fmt):
     # the 7B gate+up+SiLU in the ggml Q4_K layout (upstream Q4_K_M files) and
