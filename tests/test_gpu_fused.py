@@ -359,6 +359,22 @@ def test_gemm_more_formats(ctx, fmt, m, n, k):
                     f"gemm {fmt} m=2 after m={m}")
 
 
+@pytest.mark.parametrize("fmt", ["q8_0", "q4k", "q5k"])
+@pytest.mark.parametrize("m", [32, 27])
+def test_gemm_256_row_tiles_partial_last_tile(ctx, fmt, m):
+    # n = 16500 rows: enough 256-row tiles (≥ a quarter of the CUs) for the
+    # 16-wave form at 32 rows, the last tile 116 rows short; m = 27 pads the
+    # activation rows of the last 8-row group
+    n, k = 16500, 512
+    wbuf, raw = device_weights(ctx, fmt, n, k, seed=m + 31)
+    x = np.random.default_rng(m + 32).standard_normal((m, k)).astype(np.float32)
+    y = ctx.new_buffer(4 * m * n)
+    getattr(d, f"gemm_{fmt}_f32")(ctx, wbuf, ctx.buffer_from(x), y, m, n, k)
+    ctx.flush()
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm {fmt} {m}x{n}x{k}")
+
+
 @pytest.mark.parametrize("fmt", ["q6k", "q6kg"])
 def test_gemm_q6k_odd_block_count_falls_back_to_gemvs(ctx, fmt):
     # k = 3840: 15 super-blocks per row, not a whole number of two-block stages
