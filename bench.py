@@ -261,16 +261,25 @@ def _bench_prefill(ctx, m, cfg, P: int, steps: int) -> float:
     return e0.elapsed_ms(e1) / reps
 
 
-def bench_verify_eager(ctx, steps: int) -> dict:
+def bench_verify_eager(ctx, steps: int, q4k_7b: bool = False) -> dict:
     """The batched verify passes (M = 4, 8, 16 on the multi-row GEMVs; 16, 32
-    on the GEMMs) and a 512-token prefill of the 0.5B model, launched eagerly
-    (no graph), for kernel traces of their kernels: rocprofv3 --kernel-trace
-    ends in a host-side fault when it traces the replay of their graphs."""
-    from runit_mac_amd.decode import DecodeConfig, DecodeModel
-    cfg = DecodeConfig()
-    m = DecodeModel(ctx, cfg, seed=7)
+    on the GEMMs) and a 512-token prefill of the 0.5B model — or, with
+    q4k_7b, of the 7B Q4_K_M-mix model on the GEMMs at M = 8, 16, 32 —
+    launched eagerly (no graph), for kernel traces of their kernels:
+    rocprofv3 --kernel-trace ends in a host-side fault when it traces the
+    replay of their graphs."""
+    from runit_mac_amd.decode import Q4K_M, DecodeConfig, DecodeModel
+    if q4k_7b:
+        cfg = DecodeConfig(layers=28, hidden=3584, heads=28, kv_heads=4, head_dim=128, ff=18944,
+                           vocab=152064, max_seq=1024)
+        m = DecodeModel(ctx, cfg, seed=9, quant=Q4K_M)
+        forms = ((8, "gemm"), (16, "gemm"), (32, "gemm"))
+    else:
+        cfg = DecodeConfig()
+        m = DecodeModel(ctx, cfg, seed=7)
+        forms = ((4, "rows"), (8, "rows"), (16, "rows"), (16, "gemm"), (32, "gemm"))
     pos, out = 511, {}
-    for M, form in ((4, "rows"), (8, "rows"), (16, "rows"), (16, "gemm"), (32, "gemm")):
+    for M, form in forms:
         m.verify_forward([1] * M, pos, form)  # uploads the ids, sizes the buffers
         ctx.flush()
         e0, e1 = ctx.event(), ctx.event()
@@ -460,8 +469,28 @@ def bench_q4km_decode(ctx, steps: int, warmup: int) -> dict:
     ms = e0.elapsed_ms(e1) / reps
     del g
     launches = m.launches_fused()
+    # the batched verify pass at these shapes (M draft tokens through all 28
+    # layers on the Q4_K / Q6_K GEMMs, the form verify_draft takes at this
+    # hidden size), one graph per M, replayed over the same cache positions
+    verify = {}
+    for M, form in ((4, "gemm"), (8, "gemm"), (16, "gemm"), (32, "gemm")):
+        m.verify_forward([1] * M, pos, form)
+        ctx.flush()
+        ctx.capture_begin()
+        m.verify_pass(M, pos, form)
+        gv = ctx.capture_end()
+        gv.launch()
+        ctx.flush()
+        e0.record()
+        for _ in range(reps):
+            gv.launch()
+        e1.record()
+        verify[(M, form)] = e0.elapsed_ms(e1) / reps
+        del gv
+    prefill_ms = _bench_prefill(ctx, m, cfg, 512, steps)
     m.free()
-    return {"ms": ms, "step_bytes": cfg.step_bytes(pos + 1, Q4K_M), "launches": launches}
+    return {"ms": ms, "step_bytes": cfg.step_bytes(pos + 1, Q4K_M), "launches": launches,
+            "verify_ms": verify, "prefill_ms": prefill_ms, "prefill_tokens": 512}
 
 
 def bench_q4km_step(ctx, steps: int, warmup: int) -> dict:
@@ -687,7 +716,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--suite", default="all",
-                    choices=["all", "gemv", "quick", "decode", "step", "q4decode", "verify"])
+                    choices=["all", "gemv", "quick", "decode", "step", "q4decode", "verify", "verify7b"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-verify", action="store_true",
                     help="skip the verify / prefill graphs (rocprofv3 --kernel-trace runs)")
@@ -704,9 +733,9 @@ def main():
     if args.profile_pass:
         profile_pass(ctx)
         return
-    if args.suite == "verify":
+    if args.suite in ("verify", "verify7b"):
         # eager verify / prefill passes for kernel traces; prints no JSON
-        bench_verify_eager(ctx, args.steps)
+        bench_verify_eager(ctx, args.steps, q4k_7b=args.suite == "verify7b")
         ctx.close()
         return
     line = {
@@ -786,7 +815,16 @@ def main():
             "tok_s": round(1e3 / q4d["ms"], 2), "us_per_token": round(q4d["ms"] * 1e3, 1),
             "step_bytes": q4d["step_bytes"], "gbs": round(dgbs, 1),
             "frac": round(dgbs / HBM_PEAK_GBS, 4), "launches_per_token": q4d["launches"],
-            "kv_len": 512}
+            "kv_len": 512,
+            "verify": {f"{form}_m{M}": {"us": round(v * 1e3, 1), "us_per_token": round(v * 1e3 / M, 1)}
+                       for (M, form), v in q4d["verify_ms"].items()}}
+        line["q4k_m_7b_decode"]["prefill"] = {
+            "tokens": q4d["prefill_tokens"], "ms": round(q4d["prefill_ms"], 3),
+            "tok_s": round(q4d["prefill_tokens"] / (q4d["prefill_ms"] * 1e-3), 1)}
+        for (M, form), v in q4d["verify_ms"].items():
+            log(f"config 4 verify pass, {M} tokens ({form}): {v * 1e3:.1f} us = "
+                f"{v * 1e3 / M:.1f} us per token")
+        log(f"config 4 prefill of {q4d['prefill_tokens']} tokens: {q4d['prefill_ms']:.2f} ms")
     if args.suite in ("all", "gemv", "step") and not args.only:
         q4 = bench_q4km_step(ctx, args.steps, args.warmup)
         gbs = q4["bytes"] / (q4["us"] * 1e-6) / 1e9

@@ -284,3 +284,233 @@ k_ssq_quads(const float* __restrict__ y, uint32_t m, float* __restrict__ out) {
     }
     out[qd] = s;
 }
+
+// Causal multi-query attention on the matrix cores (f32 MFMA 16x16x4): one
+// workgroup takes 16 query columns — consecutive (row, head) pairs of one KV
+// head's query-head group, flattened row-major — and one of nsp ranges of
+// a.chunk key tiles (16 positions each) of the positions the columns see;
+// its W waves split the range's tiles (wave w: tiles w, w + W, ...).  Per
+// tile a wave computes Sᵀ = K·Qᵀ (16 positions × 16 columns), the online
+// softmax per column, and Oᵀ += Vᵀ·Pᵀ, the next tile's K and V already in
+// flight; the waves' partial (O, max, sum) meet in LDS.  With one range the
+// workgroup writes the normalised rows; with several it writes its partial
+// and the last of the column group's workgroups to arrive merges them in
+// range order.  The sums over d and over positions are taken in orders of
+// the layout's choosing:
+//   Sᵀ k-step s, lane group g (lane / 16) supplies d = (HD/4)·g + s, so a lane
+//   reads one contiguous quarter row of K and of its query (four
+//   accumulators, one per s mod 4, summed at the end);
+//   Oᵀ k-step i, lane group g supplies position 4g + i of the tile (the
+//   lane's own i-th score), block b, lane row n supplies d = (HD/16)·n + b.
+// Positions past a column's causal limit score -inf; rows past the last
+// position any column sees are never read (indices clamp to it).
+template <int HD>
+RT_DEV void attn_mq(const AttnArgs& a) {
+    constexpr uint32_t QC = HD / 4, NB = HD / 16;
+    extern __shared__ f32x4 mq_lds[];
+    __shared__ uint32_t last_flag;
+    float* lds = (float*)mq_lds;
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = wg_threads() >> 6;
+    const uint32_t n = lane & 15, g = lane >> 4;
+    const uint32_t G = a.H / a.KVH, kvh = blockIdx.y, bt = blockIdx.z;
+    const uint32_t R = a.q_len * G, cgs = (R + 15) / 16, nsp = gridDim.x / cgs;
+    const uint32_t cg = blockIdx.x / nsp, sp = blockIdx.x % nsp, c0 = cg * 16;
+    const uint32_t qi = c0 + n;
+    const bool valid = qi < R;
+    const uint32_t r = valid ? qi / G : 0, h = kvh * G + (valid ? qi % G : 0);
+    const uint32_t lim = valid ? min(a.kv_len, a.q_start + r + 1) : 0;
+    const uint32_t Lmax = min(a.kv_len, a.q_start + (min(R, c0 + 16) - 1) / G + 1);
+    const size_t qrow = (size_t)(bt * a.q_len + r) * a.H + h;
+    float qv[QC];
+    {
+        const f32x4* q4 = (const f32x4*)(a.q + qrow * HD + QC * g);
+#pragma unroll
+        for (uint32_t j = 0; j < QC / 4; ++j) {
+            const f32x4 t = q4[j];
+            qv[4 * j] = t.x; qv[4 * j + 1] = t.y; qv[4 * j + 2] = t.z; qv[4 * j + 3] = t.w;
+        }
+    }
+    const size_t cb = ((size_t)bt * a.KVH + kvh) * a.stride * HD;
+    const float* kb = a.kc + cb;
+    const float* vb = a.vc + cb;
+    f32x4 acc[NB];
+#pragma unroll
+    for (uint32_t j = 0; j < NB; ++j) acc[j] = f32x4{0, 0, 0, 0};
+    const float NEG = -__builtin_huge_valf();
+    float m = NEG, l = 0.0f;
+    const uint32_t T = min((Lmax + 15) / 16, (sp + 1) * a.chunk);
+    f32x4 kk[QC / 4], vv[4][NB / 4];
+    auto load = [&](uint32_t t, f32x4 (&kd)[QC / 4], f32x4 (&vd)[4][NB / 4]) {
+        const uint32_t p0 = t * 16;
+        const f32x4* kr = (const f32x4*)(kb + (size_t)min(p0 + n, Lmax - 1) * HD + QC * g);
+#pragma unroll
+        for (uint32_t j = 0; j < QC / 4; ++j) kd[j] = kr[j];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const f32x4* vr = (const f32x4*)(vb + (size_t)min(p0 + 4 * g + i, Lmax - 1) * HD + NB * n);
+#pragma unroll
+            for (uint32_t j = 0; j < NB / 4; ++j) vd[i][j] = vr[j];
+        }
+    };
+    auto tile = [&](uint32_t t, const f32x4 (&kd)[QC / 4], const f32x4 (&vd)[4][NB / 4]) {
+        const uint32_t p0 = t * 16;
+        f32x4 s4[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+        for (uint32_t j = 0; j < QC / 4; ++j) {
+            s4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(kd[j].x, qv[4 * j], s4[0], 0, 0, 0);
+            s4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kd[j].y, qv[4 * j + 1], s4[1], 0, 0, 0);
+            s4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(kd[j].z, qv[4 * j + 2], s4[2], 0, 0, 0);
+            s4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(kd[j].w, qv[4 * j + 3], s4[3], 0, 0, 0);
+        }
+        const f32x4 s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        float sv[4], tmax = NEG;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            sv[i] = p0 + 4 * g + i < lim ? s[i] * a.scale : NEG;
+            tmax = fmaxf(tmax, sv[i]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m, tmax);
+        const float alpha = m == NEG ? 0.0f : expf(m - m_new);
+        float p[4], ps = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            p[i] = sv[i] == NEG ? 0.0f : expf(sv[i] - m_new);
+            ps += p[i];
+        }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        l = l * alpha + ps;
+        m = m_new;
+#pragma unroll
+        for (uint32_t j = 0; j < NB; ++j) acc[j] *= alpha;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+            for (uint32_t j = 0; j < NB / 4; ++j) {
+                acc[4 * j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[i][j].x, p[i], acc[4 * j], 0, 0, 0);
+                acc[4 * j + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[i][j].y, p[i], acc[4 * j + 1], 0, 0, 0);
+                acc[4 * j + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[i][j].z, p[i], acc[4 * j + 2], 0, 0, 0);
+                acc[4 * j + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[i][j].w, p[i], acc[4 * j + 3], 0, 0, 0);
+            }
+    };
+    // two register sets in turn: the next tile's loads (unconditional, the
+    // last tile again at the end) issue ahead of this tile's matrix work.
+    // Head size 256 has the registers for one set only.
+    uint32_t t = sp * a.chunk + w;
+    if constexpr (HD > 128) {
+        for (; t < T; t += W) {
+            load(t, kk, vv);
+            tile(t, kk, vv);
+        }
+    }
+    f32x4 k2[QC / 4], v2[4][NB / 4];
+    if (t < T) load(t, kk, vv);
+    for (; t < T; t += 2 * W) {
+        load(min(t + W, T - 1), k2, v2);
+        __builtin_amdgcn_sched_barrier(0);
+        tile(t, kk, vv);
+        if (t + W >= T) break;
+        load(min(t + 2 * W, T - 1), kk, vv);
+        __builtin_amdgcn_sched_barrier(0);
+        tile(t + W, k2, v2);
+    }
+    // the wave's partial: O[column][d] unnormalised, then max and sum per column
+    constexpr uint32_t WS = 16 * HD + 32;
+    float* wo = lds + w * WS;
+#pragma unroll
+    for (uint32_t rr = 0; rr < 4; ++rr)
+#pragma unroll
+        for (uint32_t j = 0; j < NB / 4; ++j)
+            *(f32x4*)(wo + n * HD + NB * (4 * g + rr) + 4 * j) =
+                f32x4{acc[4 * j][rr], acc[4 * j + 1][rr], acc[4 * j + 2][rr], acc[4 * j + 3][rr]};
+    if (g == 0) {
+        wo[16 * HD + n] = m;
+        wo[16 * HD + 16 + n] = l;
+    }
+    __syncthreads();
+    // partials of a multi-range column group: [pair][range][16][HD] and
+    // [pair][range][16][max, sum], pair = (batch · KVH + kvh) · cgs + cg
+    const size_t pair = ((size_t)bt * a.KVH + kvh) * cgs + cg;
+    for (uint32_t e = threadIdx.x; e < 16 * (HD / 4); e += wg_threads()) {
+        const uint32_t col = e / (HD / 4), d4 = e % (HD / 4);
+        const uint32_t qc = c0 + col;
+        if (qc >= R) continue;
+        float M = NEG;
+        for (uint32_t v = 0; v < W; ++v) M = fmaxf(M, lds[v * WS + 16 * HD + col]);
+        f32x4 o = {0, 0, 0, 0};
+        float den = 0.0f;
+        for (uint32_t v = 0; v < W; ++v) {
+            const float mv = lds[v * WS + 16 * HD + col];
+            const float f = mv == NEG ? 0.0f : expf(mv - M);
+            den += f * lds[v * WS + 16 * HD + 16 + col];
+            o += f * *(const f32x4*)(lds + v * WS + col * HD + 4 * d4);
+        }
+        if (nsp == 1) {
+            const uint32_t orow = qc / G, oh = kvh * G + qc % G;
+            *(f32x4*)(a.out + ((size_t)(bt * a.q_len + orow) * a.H + oh) * HD + 4 * d4) = o / den;
+        } else {
+            float* pp = a.part + ((pair * nsp + sp) * 16 + col) * HD + 4 * d4;
+            dev_store(pp + 0, o.x);
+            dev_store(pp + 1, o.y);
+            dev_store(pp + 2, o.z);
+            dev_store(pp + 3, o.w);
+            if (d4 == 0) {
+                float* mlp = a.ml + ((pair * nsp + sp) * 16 + col) * 2;
+                dev_store(mlp + 0, M);
+                dev_store(mlp + 1, den);
+            }
+        }
+    }
+    if (nsp == 1) return;
+    dev_stores_done();
+    __syncthreads();
+    uint32_t* counter = a.counters + pair;
+    if (threadIdx.x == 0) last_flag = arrive(counter) == nsp - 1;
+    __syncthreads();
+    if (!last_flag) return;
+    // o = Σ o_s·e^(m_s−M) / Σ l_s·e^(m_s−M) over the ranges, in range order;
+    // every range's loads are issued before the first is used (indices past
+    // nsp repeat the last range, weighted 0), so the merge waits once
+    for (uint32_t e = threadIdx.x; e < 16 * (HD / 4); e += wg_threads()) {
+        const uint32_t col = e / (HD / 4), d4 = e % (HD / 4);
+        const uint32_t qc = c0 + col;
+        if (qc >= R) continue;
+        const float* mlv = a.ml + (pair * nsp * 16 + col) * 2;
+        float mj[RT_ATTN_MQ_NSP_MAX], lj[RT_ATTN_MQ_NSP_MAX];
+        f32x4 oj[RT_ATTN_MQ_NSP_MAX];
+#pragma unroll
+        for (uint32_t j = 0; j < RT_ATTN_MQ_NSP_MAX; ++j) {
+            const uint32_t jj = min(j, nsp - 1);
+            mj[j] = dev_load(mlv + 32 * jj);
+            lj[j] = dev_load(mlv + 32 * jj + 1);
+            const float* pj = a.part + ((pair * nsp + jj) * 16 + col) * HD + 4 * d4;
+            oj[j] = f32x4{dev_load(pj), dev_load(pj + 1), dev_load(pj + 2), dev_load(pj + 3)};
+        }
+        float M = NEG;
+#pragma unroll
+        for (uint32_t j = 0; j < RT_ATTN_MQ_NSP_MAX; ++j) M = fmaxf(M, mj[j]);
+        float L = 0.0f;
+        f32x4 o = {0, 0, 0, 0};
+#pragma unroll
+        for (uint32_t j = 0; j < RT_ATTN_MQ_NSP_MAX; ++j) {
+            const float f = (j >= nsp || mj[j] == NEG) ? 0.0f : expf(mj[j] - M);
+            L += f * lj[j];
+            o += f * oj[j];
+        }
+        const uint32_t orow = qc / G, oh = kvh * G + qc % G;
+        *(f32x4*)(a.out + ((size_t)(bt * a.q_len + orow) * a.H + oh) * HD + 4 * d4) = o / L;
+    }
+    if (threadIdx.x == 0) dev_store(counter, 0u);  // ready for the next call (also under graph replay)
+}
+// at most 8 / 8 / 4 waves at head size 64 / 128 / 256 (the registers of two
+// tiles' K and V, the query and the output slices)
+#define RT_ATTN_MQ_KERNEL(HD)                                                                  \
+    extern "C" __global__ void __launch_bounds__(64 * rt_attn_mq_wmax(HD))                    \
+        k_attn_mq_f32_hd##HD(AttnArgs a) {                                                     \
+        attn_mq<HD>(a);                                                                          \
+    }
+RT_ATTN_MQ_KERNEL(64)
+RT_ATTN_MQ_KERNEL(128)
+RT_ATTN_MQ_KERNEL(256)

@@ -17,6 +17,14 @@ constexpr uint32_t rt_attn_hg(uint32_t) { return 1u; }
 // The persistent step's attention phase runs RT_STEP_THREADS / 256 = 2 head
 // groups, so its workgroups take 2 query heads (step 772 → 753 µs against 8).
 constexpr uint32_t rt_step_attn_gm(uint32_t) { return 2u; }
+// Multi-query (verify / prefill) attention on the matrix cores: the most
+// waves a workgroup of 16 query columns may have at a head size.
+constexpr uint32_t rt_attn_mq_wmax(uint32_t head_dim) { return head_dim == 256 ? 4u : 8u; }
+// Key ranges of one column group merged by its last workgroup (at most).
+constexpr uint32_t RT_ATTN_MQ_NSP_MAX = 8;
+// LDS bytes of such a workgroup of w waves: per wave 16 columns × head_dim
+// outputs + 16 maxima + 16 sums.
+constexpr uint32_t rt_attn_mq_lds(uint32_t head_dim, uint32_t w) { return w * (16u * head_dim + 32u) * 4u; }
 
 // Device scratch of the no-allocation entry points: one fixed array in the
 // code object (k_scratch.hip), laid out as [arrival counters | activation

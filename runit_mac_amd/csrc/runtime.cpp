@@ -137,6 +137,7 @@ const char* const kKernelNames[] = {
     "k_act_limbs_f32", "k_act_limbs_f32_q40", "k_act_limbs_f16", "k_act_limbs_f16_q40",
     "k_rms_norm_f32g", "k_rope_qk_f32", "k_kv_copy_f32",
     "k_decode_attention_f32_hd64", "k_decode_attention_f32_hd128", "k_decode_attention_f32_hd256",
+    "k_attn_mq_f32_hd64", "k_attn_mq_f32_hd128", "k_attn_mq_f32_hd256",
     "k_attn_rope_f32_hd64", "k_attn_rope_f32_hd128", "k_attn_rope_f32_hd256",
     "k_attn_rope_w_f32_hd64", "k_attn_rope_w_f32_hd128",
     "k_add_f16_into_f32", "k_ssq_quads", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
@@ -292,6 +293,8 @@ struct rt_ctx {
     bool gemm_sum_kernel = true;  // RUNIT_GEMM_SUM_KERNEL=0: K splits meet in the GEMM (arrival counters)
     uint32_t gemm_splits = 0;    // RUNIT_GEMM_SPLITS=n: the f16 GEMM's K splits forced (A/B)
     bool attn_w = true;          // RUNIT_ATTN_W=0: the token's RoPE attention on attn_split (A/B)
+    bool attn_mq = true;         // RUNIT_ATTN_MQ=0: multi-query attention on attn_split per row (A/B)
+    uint32_t attn_mq_nsp = 0, attn_mq_w = 0;  // probe: forced ranges / waves (0: planned)
     uint32_t gemm_f16_min = 4;   // RUNIT_GEMM_F16_MIN: batches above this many rows run the f16 form
     uint32_t gemm_f16_min_q6 = 1;  // RUNIT_GEMM_F16_MIN_Q6: the same for Q6_K
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
@@ -1322,6 +1325,9 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_F16_MIN")) c->gemm_f16_min = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_F16_MIN_Q6")) c->gemm_f16_min_q6 = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_ATTN_W")) c->attn_w = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_ATTN_MQ")) c->attn_mq = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_ATTN_MQ_NSP")) c->attn_mq_nsp = atoi(g);
+    if (const char* g = getenv("RUNIT_ATTN_MQ_W")) c->attn_mq_w = atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_VS")) c->vs_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_VS_MAXQ")) c->vs_max_q = (uint32_t)atoi(g);
     std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
@@ -2863,6 +2869,52 @@ int rt_flash_attention_f32(rt_ctx* c, const float* q, const float* k, const floa
     a.q_len = q_len;
     a.q_start = q_start;
     char kn[64];
+    snprintf(kn, sizeof kn, "k_attn_mq_f32_hd%u", head_dim);
+    if (c->attn_mq && c->fns.count(kn)) {
+        // workgroups of 16 (row, head) columns per KV head and range of key
+        // tiles.  Fewer than 256 column groups (verify): the key range split
+        // so that the grid holds about 1024 waves of 4 per range, ranges of
+        // at least 4 tiles, at most RT_ATTN_MQ_NSP_MAX of them (the last
+        // workgroup of a group merges them).  Otherwise (prefill) one range,
+        // W waves doubled while the grid stays under 4096 waves and each
+        // wave keeps 2 tiles of the longest range.
+        const uint32_t G = num_heads / num_kv_heads;
+        const uint64_t cols = ((uint64_t)q_len * G + 15) / 16;
+        const uint64_t pairs = cols * num_kv_heads * batch;
+        const uint32_t tiles = (std::min<uint32_t>(kv_len, q_start + q_len) + 15) / 16;
+        const uint32_t wmax = rt_attn_mq_wmax(head_dim);
+        uint32_t nsp = 1;
+        if (pairs < 256)
+            nsp = std::max<uint32_t>(1, std::min<uint32_t>({(uint32_t)(256 / pairs), tiles / 4,
+                                                            RT_ATTN_MQ_NSP_MAX}));
+        if (c->attn_mq_nsp) nsp = std::min({c->attn_mq_nsp, tiles, RT_ATTN_MQ_NSP_MAX});
+        const uint32_t chunk = (tiles + nsp - 1) / nsp;
+        nsp = (tiles + chunk - 1) / chunk;
+        uint32_t w = 1;
+        if (nsp > 1)
+            while (w < 4 && w * 2 <= chunk) w *= 2;
+        else
+            while (w < wmax && w * 2 * pairs <= 4096 && w * 4 <= chunk) w *= 2;
+        if (c->attn_mq_w) w = std::min(c->attn_mq_w, wmax);
+        if (cols * nsp > 0x7FFFFFFFull || batch > 65535)
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: flash_attention: %llu column "
+                        "groups, batch %u", (unsigned long long)cols, batch);
+        if (nsp > 1) {
+            if (pairs > kAttnCounters)
+                return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: flash_attention: %llu "
+                            "column groups exceed %u", (unsigned long long)pairs, kAttnCounters);
+            const size_t parts = (size_t)pairs * nsp * 16;
+            int st = ensure_ws(c, parts * (head_dim + 2) * sizeof(float), kn);
+            if (st != RT_OK) return st;
+            a.part = (float*)c->ws;
+            a.ml = a.part + parts * head_dim;
+            a.counters = c->counters;
+        }
+        a.chunk = chunk;
+        void* params[] = {&a};
+        return launch(c, kn, dim3((uint32_t)(cols * nsp), num_kv_heads, batch), dim3(64 * w),
+                      rt_attn_mq_lds(head_dim, w), params);
+    }
     snprintf(kn, sizeof kn, "k_decode_attention_f32_hd%u", head_dim);
     return attn_launch(c, kn, a, (uint32_t)rows);
 }

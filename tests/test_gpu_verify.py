@@ -94,6 +94,10 @@ def test_argmax_rows_first(ctx):
     (64, 14, 2, 8, 8, 0),         # prefill from position 0
     (128, 28, 4, 5, 300, 0),      # the reference kernel's mask (q_start 0) with history
     (128, 28, 4, 16, 1040, 1024),
+    (128, 28, 4, 200, 200, 0),    # prefill-length: many column groups, a few waves each
+    (256, 8, 2, 6, 40, 34),       # head size 256
+    (64, 12, 4, 7, 23, 16),       # 3 heads per KV head: column groups straddle rows
+    (128, 28, 4, 1, 1, 0),        # one row, one position
 ])
 def test_flash_attention_causal_matches_oracle(ctx, hd, H, KVH, M, kv_len, q_start):
     rng = np.random.default_rng(hd + M + kv_len)
@@ -111,10 +115,12 @@ def test_flash_attention_causal_matches_oracle(ctx, hd, H, KVH, M, kv_len, q_sta
     assert np.max(np.abs(got - ref)) <= 1e-5 * np.abs(vc).max() * 8
 
 
-def test_flash_attention_batch_of_sequences(ctx):
-    """batch 2: each sequence reads its own cache [b][kvh][stride][hd]."""
+@pytest.mark.parametrize("kv_len", [70, 300])
+def test_flash_attention_batch_of_sequences(ctx, kv_len):
+    """batch 2: each sequence reads its own cache [b][kvh][stride][hd] (at
+    kv_len 300 the key range is split over workgroups and merged)."""
     rng = np.random.default_rng(9)
-    hd, H, KVH, M, kv_len, S = 64, 4, 2, 3, 70, 80
+    hd, H, KVH, M, S = 64, 4, 2, 3, kv_len + 10
     q = rng.standard_normal(2 * M * H * hd).astype(np.float32)
     kc = rng.standard_normal(2 * KVH * S * hd).astype(np.float32)
     vc = rng.standard_normal(2 * KVH * S * hd).astype(np.float32)
