@@ -382,6 +382,26 @@ int rt_gemm_q5kg_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, 
                      uint32_t n, uint32_t k);
 int rt_gemm_q6kg_f32(rt_ctx* ctx, const void* weight, const float* x, float* y, uint32_t m_rows,
                      uint32_t n, uint32_t k);
+/* New: the batched GEMMs of verify_draft that share one activation matrix,
+ * with the kernels between them folded in (forward.rs:2186-2271: the Q/K/V
+ * projections of the normalised rows + their f16 biases; gate and up + SiLU;
+ * O and down + the residual).  count (1..4) weight matrices, fmts[i] the
+ * block format of weight[i] ("q8_0", "q4_0", "q4k", "q5_0", "q5k", "q6k",
+ * "q4_0g", "q4kg", "q5kg", "q6kg"), y[i] [m_rows][n[i]]:
+ *   X = x, or RMSNorm(x)·gamma (eps) when gamma is given, written to xn
+ *       ([m_rows][k], required with gamma);
+ *   y[i] = X·weight[i]ᵀ (+ f32(bias[i]) on every row, bias and bias[i] may
+ *       be NULL);
+ *   res (count 1, not y[0]): y[0] = res + X·weight[0]ᵀ;
+ *   silu_pair (count 2, one shape, no bias / res): y[0] = silu(X·weight[0]ᵀ)
+ *       · (X·weight[1]ᵀ), y[1] left unspecified.
+ * Where every matrix takes the f16 matrix-core form with one row grouping,
+ * x is prepared once (the norm in the preparation) and the bias / residual /
+ * SiLU run in the K-split sums; otherwise as the separate launches. */
+int rt_gemm_set_f32(rt_ctx* ctx, uint32_t count, const char* const* fmts, const void* const* weight,
+                    float* const* y, const uint32_t* n, const uint16_t* const* bias,
+                    const float* res, const float* x, uint32_t m_rows, uint32_t k,
+                    const float* gamma, float eps, float* xn, uint32_t silu_pair);
 
 /* ──────────────── multi-row GEMVs (batched verify / prefill) ────────────────
  * New: the M-row projections of verify_draft (forward.rs:2186-2271, which

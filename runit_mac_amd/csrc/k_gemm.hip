@@ -780,10 +780,11 @@ RT_DEV void gemm_xh_prep_body(const float* __restrict__ x, uint32_t M, uint32_t 
 // (thread t: float4s t, t + 1024, ...), reduces the row's largest |x|, then
 // writes each float4 as half of a 16-byte A entry (hi, lo) — one round trip
 // to memory instead of three.
-template <int MG>
+template <int MG, bool NORM = false>
 RT_DEV void gemm_xh_prep1_body(const float* __restrict__ x, uint32_t M, uint32_t K,
                                uint2* __restrict__ aops, int* __restrict__ etab,
-                               float* __restrict__ stab) {
+                               float* __restrict__ stab, const float* __restrict__ gamma = nullptr,
+                               float eps = 0.0f, float* __restrict__ xn = nullptr) {
     constexpr uint32_t ROWS = 8 * MG, T = 1024, NPT = 5;
     __shared__ float red[16];
     const uint32_t nrec = K / 32, nf = K / 4;
@@ -797,6 +798,32 @@ RT_DEV void gemm_xh_prep1_body(const float* __restrict__ x, uint32_t M, uint32_t
     for (uint32_t i = 0; i < NPT; ++i) {
         const uint32_t f = tid + T * i;
         v[i] = (m < M && f < nf) ? *(const f32x4*)(xr + 4 * f) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    if constexpr (NORM) {
+        // rms_norm_f32_f32_f32g of the row first: x · rsqrt(mean(x²) + eps) · γ,
+        // also written to xn (the rows past M stay zero)
+        __shared__ float red2[16];
+        float ss = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < NPT; ++i)
+            ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((tid & 63) == 0) red2[tid >> 6] = ss;
+        __syncthreads();
+        ss = 0.0f;
+#pragma unroll
+        for (uint32_t w = 0; w < T / 64; ++w) ss += red2[w];
+        const float rms = rsqrtf(ss / (float)K + eps);
+#pragma unroll
+        for (uint32_t i = 0; i < NPT; ++i) {
+            const uint32_t f = tid + T * i;
+            if (m < M && f < nf) {
+                const f32x4 gv = *(const f32x4*)(gamma + 4 * f);
+                v[i] = f32x4{v[i].x * rms * gv.x, v[i].y * rms * gv.y, v[i].z * rms * gv.z,
+                             v[i].w * rms * gv.w};
+                if (xn) *(f32x4*)(xn + (size_t)m * K + 4 * f) = v[i];
+            }
+        }
     }
 #pragma unroll
     for (uint32_t i = 0; i < NPT; ++i)
@@ -846,6 +873,17 @@ RT_DEV void gemm_xh_prep1_body(const float* __restrict__ x, uint32_t M, uint32_t
 RT_GEMM_XH_PREP1(1)
 RT_GEMM_XH_PREP1(2)
 RT_GEMM_XH_PREP1(4)
+// the same preparation of RMSNorm(x)·γ, the normalised rows also written to
+// xn (when given)
+#define RT_GEMM_XH_PREP1N(MG)                                                                  \
+    extern "C" __global__ void __launch_bounds__(1024) k_gemm_xh_prep1n_mg##MG(                \
+        const float* x, uint32_t M, uint32_t K, uint2* aops, int* etab, float* stab,           \
+        const float* gamma, float eps, float* xn) {                                            \
+        gemm_xh_prep1_body<MG, true>(x, M, K, aops, etab, stab, gamma, eps, xn);               \
+    }
+RT_GEMM_XH_PREP1N(1)
+RT_GEMM_XH_PREP1N(2)
+RT_GEMM_XH_PREP1N(4)
 RT_GEMM_XH_PREP(1)
 RT_GEMM_XH_PREP(2)
 RT_GEMM_XH_PREP(4)
@@ -1081,6 +1119,53 @@ extern "C" __global__ void __launch_bounds__(256) k_gemm_split_sum(const float* 
             for (uint32_t sp = 1; sp < splits; ++sp) v += p[sp * ss + i];
             y[(size_t)m * N + n + i] = v;
         }
+    }
+}
+// k_gemm_split_sum with the epilogues of verify_draft's GEMMs
+// (forward.rs:2199-2271) folded in: Y = Σ part, then
+//   part2 given (the up projection's partial sums, same splits and layout):
+//     Y = silu(Σ part) · Σ part2, silu(g) = g / (1 + e^−g)  (silu_mul_f32);
+//   bias given: Y += f32(bias[n])  (add_bias_broadcast_f16);
+//   res given:  Y = res + Y         (add_f32; Y may alias res).
+extern "C" __global__ void __launch_bounds__(256)
+k_gemm_split_sum_ep(const float* __restrict__ part, const float* __restrict__ part2, float* y,
+                    uint32_t M, uint32_t N, uint32_t splits, uint32_t crow,
+                    const uint16_t* __restrict__ bias, const float* res) {
+    const uint32_t m = blockIdx.y, n0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (n0 >= N) return;
+    const uint32_t ch = m / crow, r = m % crow;
+    const size_t off = ((size_t)ch * splits * crow + r) * N, ss = (size_t)crow * N;
+    if (N % 4 == 0 && (((uintptr_t)part | (uintptr_t)part2 | (uintptr_t)y | (uintptr_t)res) & 15) == 0 &&
+        ((uintptr_t)bias & 7) == 0) {
+        // four consecutive outputs in 16-byte loads and stores (rows of a
+        // multiple of 4 keep every row aligned)
+        f32x4 v = *(const f32x4*)(part + off + n0);
+        for (uint32_t sp = 1; sp < splits; ++sp) v += *(const f32x4*)(part + off + sp * ss + n0);
+        if (part2) {
+            f32x4 u = *(const f32x4*)(part2 + off + n0);
+            for (uint32_t sp = 1; sp < splits; ++sp) u += *(const f32x4*)(part2 + off + sp * ss + n0);
+            v = f32x4{v.x / (1.0f + expf(-v.x)) * u.x, v.y / (1.0f + expf(-v.y)) * u.y,
+                      v.z / (1.0f + expf(-v.z)) * u.z, v.w / (1.0f + expf(-v.w)) * u.w};
+        }
+        if (bias) {
+            const uint2 b = *(const uint2*)(bias + n0);
+            v += f32x4{h2f(b.x), h2f(b.x >> 16), h2f(b.y), h2f(b.y >> 16)};
+        }
+        if (res) v = *(const f32x4*)(res + (size_t)m * N + n0) + v;
+        *(f32x4*)(y + (size_t)m * N + n0) = v;
+        return;
+    }
+    for (uint32_t n = n0; n < n0 + 4 && n < N; ++n) {
+        float v = part[off + n];
+        for (uint32_t sp = 1; sp < splits; ++sp) v += part[off + sp * ss + n];
+        if (part2) {
+            float u = part2[off + n];
+            for (uint32_t sp = 1; sp < splits; ++sp) u += part2[off + sp * ss + n];
+            v = v / (1.0f + expf(-v)) * u;
+        }
+        if (bias) v += h2f(bias[n]);
+        if (res) v = res[(size_t)m * N + n] + v;
+        y[(size_t)m * N + n] = v;
     }
 }
 #define RT_GEMM3_KERNEL4(FN, P, MG, NB)                                                       \

@@ -143,7 +143,8 @@ const char* const kKernelNames[] = {
     "k_add_f16_into_f32", "k_ssq_quads", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
     "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32", "k_rope_kv_write_batch_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
-    "k_gemm_split_sum", "k_gemm_xh_prep1_mg1", "k_gemm_xh_prep1_mg2", "k_gemm_xh_prep1_mg4", "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
+    "k_gemm_split_sum", "k_gemm_split_sum_ep", "k_gemm_xh_prep1n_mg1", "k_gemm_xh_prep1n_mg2",
+    "k_gemm_xh_prep1n_mg4", "k_gemm_xh_prep1_mg1", "k_gemm_xh_prep1_mg2", "k_gemm_xh_prep1_mg4", "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
     "k_gemm_q8_0_mg1_ct2", "k_gemm_q8_0_mg2_ct2", "k_gemm_q8_0_mg4_ct2", "k_gemm_q8_0_mg8_ct2",
     "k_gemm2_q8_0_mg1", "k_gemm2_q8_0_mg2", "k_gemm2_q8_0_mg4", "k_gemm2_q8_0_mg8",
@@ -290,6 +291,7 @@ struct rt_ctx {
     const char* last_name = "";  // the last launched kernel (rt_last_launch_name)
     bool gemv_valu = false;      // RUNIT_GEMV_VALU=1: VALU-dot twins of the LDS body (A/B)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
+    bool gemm_set = true;  // RUNIT_GEMM_SET=0: rt_gemm_set_f32 as separate launches (A/B)
     bool gemm_sum_kernel = true;  // RUNIT_GEMM_SUM_KERNEL=0: K splits meet in the GEMM (arrival counters)
     uint32_t gemm_splits = 0;    // RUNIT_GEMM_SPLITS=n: the f16 GEMM's K splits forced (A/B)
     bool attn_w = true;          // RUNIT_ATTN_W=0: the token's RoPE attention on attn_split (A/B)
@@ -1316,6 +1318,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_Q6W8")) c->gemm_q6w8 = atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_SPLITS")) c->gemm_splits = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_SUM_KERNEL")) c->gemm_sum_kernel = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_SET")) c->gemm_set = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_SM")) c->sm_enabled = atoi(g) != 0;
@@ -1889,12 +1892,20 @@ static int gemm_split_sum(rt_ctx* c, float* part, float* y, uint32_t m, uint32_t
     return launch(c, "k_gemm_split_sum", dim3((n + 1023) / 1024, m), dim3(256), 0, pp);
 }
 
-// f16 matrix-core form of the staged GEMM (k_gemm3_*): 8 activation rows
-// per group (MG ∈ {1, 2, 4}), hi/lo f16 operands prepared by
-// k_gemm_xh_prep_mg*.  Returns kLsDecline where the staged layout does not
-// apply (the caller then takes the other forms).
-int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, float* y,
-                 uint32_t m_rows, uint32_t n, uint32_t k) {
+// Launch plan of the f16 matrix-core form (k_gemm3_*) for one weight matrix.
+struct Gemm3Plan {
+    char kn[48];
+    uint32_t waves, MG, nchunks, nrec, nblk, tiles, base, cap, splits, kbs;
+    uint64_t row_bytes;
+    size_t a_bytes, e_bytes, s_bytes;  // prepared operands, row exponents, record sums
+    size_t p_bytes;                    // K-split partial sums (splits > 1)
+};
+
+// Plans the f16 form: 8 activation rows per group (MG ∈ {1, 2, 4}), hi/lo
+// f16 operands prepared by k_gemm_xh_prep*_mg*.  Returns kLsDecline where
+// the staged layout does not apply (the caller then takes the other forms).
+static int gemm3_plan(rt_ctx* c, const GemmFmt& f, const void* w, uint32_t m_rows, uint32_t n,
+                      uint32_t k, Gemm3Plan& p) {
     const uint32_t cu = (uint32_t)c->cu_count;
     const uint32_t groups = (m_rows + 7) / 8;
     const uint32_t MG = std::min<uint32_t>(f.max_mg_f16, groups <= 1 ? 1 : groups <= 2 ? 2 : 4);
@@ -1960,48 +1971,93 @@ int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, flo
     if (splits > 1 && base > kAttnCounters)
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_%s_f32: %u tiles exceed %u counters",
                     f.name, base, kAttnCounters);
-    const size_t a_bytes = (size_t)nchunks * nrec * MG * 64 * 16;
-    const size_t e_bytes = (size_t)nchunks * 8 * MG * sizeof(int);  // per padded row
-    const size_t s_bytes = f.has_min ? (size_t)nchunks * nrec * 8 * MG * sizeof(float) : 0;
-    const size_t p_bytes = splits > 1 ? (size_t)splits * nchunks * 8 * MG * n * sizeof(float) : 0;
-    int st = ensure_ws(c, a_bytes + e_bytes + s_bytes + p_bytes, "gemm");
-    if (st != RT_OK) return st;
-    void* aops = c->ws;
-    int* erow = (int*)((char*)c->ws + a_bytes);
-    float* stab = s_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes) : nullptr;
-    float* part = p_bytes ? (float*)((char*)c->ws + a_bytes + e_bytes + s_bytes) : nullptr;
+    memcpy(p.kn, kn, sizeof kn);
+    p.waves = waves;
+    p.MG = MG;
+    p.nchunks = nchunks;
+    p.nrec = nrec;
+    p.nblk = nblk;
+    p.tiles = tiles;
+    p.base = base;
+    p.cap = cap;
+    p.splits = splits;
+    p.kbs = kbs;
+    p.row_bytes = row_bytes;
+    p.a_bytes = (size_t)nchunks * nrec * MG * 64 * 16;
+    p.e_bytes = (size_t)nchunks * 8 * MG * sizeof(int);  // per padded row
+    p.s_bytes = f.has_min ? (size_t)nchunks * nrec * 8 * MG * sizeof(float) : 0;
+    p.p_bytes = splits > 1 ? (size_t)splits * nchunks * 8 * MG * n * sizeof(float) : 0;
+    return RT_OK;
+}
+
+// The activation preparation of a plan: x (or RMSNorm(x)·γ with gamma, the
+// normalised rows also into xn when given) into aops / erow / stab.
+static int gemm3_prep(rt_ctx* c, const Gemm3Plan& p, const float* x, uint32_t m_rows, uint32_t k,
+                      void* aops, int* erow, float* stab, const float* gamma = nullptr,
+                      float eps = 0.0f, float* xn = nullptr) {
+    const uint32_t MG = p.MG, nchunks = p.nchunks, cu = (uint32_t)c->cu_count;
+    uint32_t M = m_rows, K = k;
+    char pk[48];
+    if (gamma) {
+        if (k > 20480)
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm: norm-fused preparation "
+                        "of k=%u > 20480", k);
+        snprintf(pk, sizeof pk, "k_gemm_xh_prep1n_mg%u", MG);
+        void* pp[] = {(void*)&x, &M, &K, &aops, &erow, &stab, (void*)&gamma, &eps, &xn};
+        return launch(c, pk, dim3(nchunks * 8 * MG), dim3(1024), 0, pp);
+    }
     if (k <= 20480) {
         // one workgroup per padded row, the row held in registers
-        char pk[48];
         snprintf(pk, sizeof pk, "k_gemm_xh_prep1_mg%u", MG);
-        uint32_t M = m_rows, K = k;
         void* pp[] = {(void*)&x, &M, &K, &aops, &erow, &stab};
-        st = launch(c, pk, dim3(nchunks * 8 * MG), dim3(1024), 0, pp);
-        if (st != RT_OK) return st;
-    } else {
-        char pk[48];
-        snprintf(pk, sizeof pk, "k_gemm_xh_prep_mg%u", MG);
-        uint32_t M = m_rows, K = k, nc = nchunks;
-        // workgroups (padded row, record range): ~2 per CU, ranges of ≥ 16
-        // records; each workgroup also reads its whole row for the row's
-        // exponent (Q8_0 3584-wide rows at M = 32: 5.0 µs with one
-        // workgroup per row)
-        const uint32_t rows = nchunks * 8 * MG;
-        const uint32_t parts = std::max<uint32_t>(1, std::min<uint32_t>((2 * cu + rows - 1) / rows, nrec / 16));
-        const uint32_t threads = k <= 8192 ? 256 : 512;
-        void* pp[] = {(void*)&x, &M, &K, &nc, &aops, &erow, &stab};
-        st = launch(c, pk, dim3(rows, parts), dim3(threads), 0, pp);
-        if (st != RT_OK) return st;
+        return launch(c, pk, dim3(nchunks * 8 * MG), dim3(1024), 0, pp);
     }
+    snprintf(pk, sizeof pk, "k_gemm_xh_prep_mg%u", MG);
+    uint32_t nc = nchunks;
+    // workgroups (padded row, record range): ~2 per CU, ranges of ≥ 16
+    // records; each workgroup also reads its whole row for the row's
+    // exponent (Q8_0 3584-wide rows at M = 32: 5.0 µs with one
+    // workgroup per row)
+    const uint32_t rows = nchunks * 8 * MG;
+    const uint32_t parts = std::max<uint32_t>(1, std::min<uint32_t>((2 * cu + rows - 1) / rows, p.nrec / 16));
+    const uint32_t threads = k <= 8192 ? 256 : 512;
+    void* pp[] = {(void*)&x, &M, &K, &nc, &aops, &erow, &stab};
+    return launch(c, pk, dim3(rows, parts), dim3(threads), 0, pp);
+}
+
+// The GEMM of a plan over prepared operands.  part: the partial sums
+// (splits > 1), left for the caller's sum when `leave_parts`; otherwise
+// summed here (k_gemm_split_sum, or in the GEMM with arrival counters).
+static int gemm3_run(rt_ctx* c, const Gemm3Plan& p, const void* w, void* aops, int* erow,
+                     float* stab, float* y, float* part, uint32_t m_rows, uint32_t n,
+                     bool leave_parts = false) {
     uint32_t cstride = 32;
-    while (cstride > 1 && (size_t)base * cstride > kAttnCounters) cstride >>= 1;
-    const bool sum_kernel = splits > 1 && c->gemm_sum_kernel;
+    while (cstride > 1 && (size_t)p.base * cstride > kAttnCounters) cstride >>= 1;
+    const bool sum_kernel = p.splits > 1 && (c->gemm_sum_kernel || leave_parts);
     Gemm2Args a2{w, aops, erow, stab, y, part, sum_kernel ? nullptr : c->counters,
-                 m_rows, n, nblk, tiles, splits, kbs, nchunks, row_bytes, cstride};
+                 m_rows, n, p.nblk, p.tiles, p.splits, p.kbs, p.nchunks, p.row_bytes, cstride};
     void* p2[] = {&a2};
-    st = launch(c, kn, dim3(std::min(base * splits, cap)), dim3(64 * waves), 0, p2);
-    if (st != RT_OK || !sum_kernel) return st;
-    return gemm_split_sum(c, part, y, m_rows, n, splits, 8 * MG);
+    int st = launch(c, p.kn, dim3(std::min(p.base * p.splits, p.cap)), dim3(64 * p.waves), 0, p2);
+    if (st != RT_OK || !sum_kernel || leave_parts) return st;
+    return gemm_split_sum(c, part, y, m_rows, n, p.splits, 8 * p.MG);
+}
+
+// f16 matrix-core form of the staged GEMM for one weight matrix: plan,
+// workspace, preparation, GEMM.
+int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, float* y,
+                 uint32_t m_rows, uint32_t n, uint32_t k) {
+    Gemm3Plan p;
+    int st = gemm3_plan(c, f, w, m_rows, n, k, p);
+    if (st != RT_OK) return st;
+    st = ensure_ws(c, p.a_bytes + p.e_bytes + p.s_bytes + p.p_bytes, "gemm");
+    if (st != RT_OK) return st;
+    void* aops = c->ws;
+    int* erow = (int*)((char*)c->ws + p.a_bytes);
+    float* stab = p.s_bytes ? (float*)((char*)c->ws + p.a_bytes + p.e_bytes) : nullptr;
+    float* part = p.p_bytes ? (float*)((char*)c->ws + p.a_bytes + p.e_bytes + p.s_bytes) : nullptr;
+    st = gemm3_prep(c, p, x, m_rows, k, aops, erow, stab);
+    if (st != RT_OK) return st;
+    return gemm3_run(c, p, w, aops, erow, stab, y, part, m_rows, n);
 }
 
 int gemm_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, float* y,
@@ -2188,6 +2244,126 @@ int rt_gemm_q5kg_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_
 int rt_gemm_q6kg_f32(rt_ctx* c, const void* w, const float* x, float* y, uint32_t m_rows,
                      uint32_t n, uint32_t k) {
     return gemm_launch(c, kGemmQ6KG, w, x, y, m_rows, n, k);
+}
+
+static const GemmFmt* gemm_fmt_named(const char* name) {
+    static const GemmFmt* const all[] = {&kGemmQ8_0, &kGemmQ4_0, &kGemmQ4K, &kGemmQ5_0, &kGemmQ5K,
+                                         &kGemmQ6K, &kGemmQ4_0G, &kGemmQ4KG, &kGemmQ5KG, &kGemmQ6KG};
+    for (const GemmFmt* f : all)
+        if (name && strcmp(name, f->name) == 0) return f;
+    return nullptr;
+}
+
+static int gemm_split_sum_ep(rt_ctx* c, const float* part, const float* part2, float* y, uint32_t m,
+                             uint32_t n, uint32_t splits, uint32_t crow, const uint16_t* bias,
+                             const float* res) {
+    void* pp[] = {(void*)&part, (void*)&part2, &y, &m, &n, &splits, &crow, (void*)&bias, (void*)&res};
+    return launch(c, "k_gemm_split_sum_ep", dim3((n + 1023) / 1024, m), dim3(256), 0, pp);
+}
+
+int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const void* const* w,
+                    float* const* y, const uint32_t* n, const uint16_t* const* bias,
+                    const float* res, const float* x, uint32_t m_rows, uint32_t k,
+                    const float* gamma, float eps, float* xn, uint32_t silu_pair) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (count == 0 || count > 4 || !fmts || !w || !y || !n)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_set: count=%u (1..4) or null "
+                    "array", count);
+    if (m_rows == 0) return RT_OK;
+    if (!x || (gamma && !xn))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_set: null x, or gamma without xn");
+    if (silu_pair && (count != 2 || bias || res || n[0] != n[1]))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_set: the SiLU pair takes two "
+                    "matrices of one shape, no bias or residual");
+    if (res && (count != 1 || res == y[0]))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_set: the residual takes one "
+                    "matrix and an output apart from it");
+    const GemmFmt* f[4];
+    for (uint32_t i = 0; i < count; ++i) {
+        f[i] = gemm_fmt_named(fmts[i]);
+        if (!f[i] || !w[i] || !y[i] || n[i] == 0)
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_set: matrix %u: format "
+                        "'%s', null buffer or n = 0", i, fmts[i] ? fmts[i] : "(null)");
+        if (k == 0 || k % f[i]->blk_el != 0)
+            return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_set: k=%u must be a "
+                        "positive multiple of %u", k, f[i]->blk_el);
+    }
+    // The shared form: every matrix on the f16 form with one row grouping,
+    // one preparation (norm-fused when gamma), epilogues in the split sums.
+    Gemm3Plan pl[4];
+    bool shared = c->gemm_set && c->gemm_f16 && m_rows >= 2 && k <= 20480 && aligned(x, 16);
+    for (uint32_t i = 0; shared && i < count; ++i) {
+        shared = m_rows > (f[i]->blk_bytes == 210 ? c->gemm_f16_min_q6 : c->gemm_f16_min);
+        if (!shared) break;
+        const int st = gemm3_plan(c, *f[i], w[i], m_rows, n[i], k, pl[i]);
+        if (st != RT_OK && st != kLsDecline) return st;
+        shared = st == RT_OK && pl[i].MG == pl[0].MG;
+    }
+    if (!shared) {
+        // the separate launches: norm, one GEMM per matrix, then the
+        // bias / residual / SiLU kernels
+        const float* X = x;
+        if (gamma) {
+            int st = rt_rms_norm_f32_f32_f32g(c, x, xn, gamma, eps, k, m_rows);
+            if (st != RT_OK) return st;
+            X = xn;
+        }
+        for (uint32_t i = 0; i < count; ++i) {
+            int st = gemm_launch(c, *f[i], w[i], X, y[i], m_rows, n[i], k);
+            if (st == RT_OK && bias && bias[i]) st = rt_add_bias_broadcast_f32(c, y[i], bias[i], m_rows, n[i]);
+            if (st != RT_OK) return st;
+        }
+        if (res) return rt_add_f32(c, res, y[0], y[0], m_rows * n[0]);
+        if (silu_pair) return rt_silu_mul_f32(c, y[0], y[1], y[0], m_rows * n[0]);
+        return RT_OK;
+    }
+    // workspace: [operands | row exponents | record sums | partials of each matrix]
+    bool any_min = false;
+    for (uint32_t i = 0; i < count; ++i) any_min |= f[i]->has_min;
+    const Gemm3Plan& p0 = pl[0];
+    const size_t s_bytes = any_min ? (size_t)p0.nchunks * p0.nrec * 8 * p0.MG * sizeof(float) : 0;
+    const uint32_t crow = 8 * p0.MG;
+    size_t poff[4], total = p0.a_bytes + p0.e_bytes + s_bytes;
+    bool ep[4];
+    for (uint32_t i = 0; i < count; ++i) {
+        ep[i] = silu_pair || res || (bias && bias[i]);
+        poff[i] = total;
+        // a matrix with an epilogue leaves its partial sums (one "split"
+        // when unsplit) for k_gemm_split_sum_ep
+        total += ep[i] ? (size_t)std::max<uint32_t>(1, pl[i].splits) * p0.nchunks * crow * n[i] * sizeof(float)
+                       : pl[i].p_bytes;
+        total = (total + 255) & ~(size_t)255;
+    }
+    int st = ensure_ws(c, total, "gemm_set");
+    if (st != RT_OK) return st;
+    char* ws = (char*)c->ws;
+    void* aops = ws;
+    int* erow = (int*)(ws + p0.a_bytes);
+    float* stab = s_bytes ? (float*)(ws + p0.a_bytes + p0.e_bytes) : nullptr;
+    st = gemm3_prep(c, p0, x, m_rows, k, aops, erow, stab, gamma, eps, gamma ? xn : nullptr);
+    if (st != RT_OK) return st;
+    for (uint32_t i = 0; i < count; ++i) {
+        float* part = (float*)(ws + poff[i]);
+        // unsplit with an epilogue: the GEMM writes its rows into the partials
+        float* yi = ep[i] && pl[i].splits == 1 ? part : y[i];
+        st = gemm3_run(c, pl[i], w[i], aops, erow, f[i]->has_min ? stab : nullptr, yi, part, m_rows,
+                       n[i], ep[i]);
+        if (st != RT_OK) return st;
+        if (ep[i] && !silu_pair)
+            st = gemm_split_sum_ep(c, part, nullptr, y[i], m_rows, n[i], pl[i].splits, crow,
+                                   bias ? bias[i] : nullptr, res);
+        if (st != RT_OK) return st;
+    }
+    if (!silu_pair) return RT_OK;
+    float* pg = (float*)(ws + poff[0]);
+    float* pu = (float*)(ws + poff[1]);
+    if (pl[0].splits == pl[1].splits)
+        return gemm_split_sum_ep(c, pg, pu, y[0], m_rows, n[0], pl[0].splits, crow, nullptr, nullptr);
+    st = gemm_split_sum_ep(c, pu, nullptr, y[1], m_rows, n[1], pl[1].splits, crow, nullptr, nullptr);
+    if (st == RT_OK)
+        st = gemm_split_sum_ep(c, pg, nullptr, y[0], m_rows, n[0], pl[0].splits, crow, nullptr, nullptr);
+    if (st != RT_OK) return st;
+    return rt_silu_mul_f32(c, y[0], y[1], y[0], m_rows * n[0]);
 }
 
 // ───────────────────────────── dequant ─────────────────────────────

@@ -591,8 +591,10 @@ class DecodeModel:
     # biases / SiLU / residuals fused in; at the 0.5B shapes, 8 rows: 12.4 µs
     # for gate+up+SiLU, 9.1 µs for O + residual).  Larger models and longer
     # batches take the batched GEMMs, which are faster there (the 7B Q4_K
-    # gate+up at 8 rows: 72.8 µs as multi-row GEMVs).
-    VERIFY_ROWS_MAX = 16
+    # gate+up at 8 rows: 72.8 µs as multi-row GEMVs; the whole 0.5B pass at
+    # 16 rows: 2.20 ms on the GEMMs, 3.01 ms on the multi-row GEMVs, at 8
+    # rows 3.22 against 1.75 ms).
+    VERIFY_ROWS_MAX = 8
     VERIFY_ROWS_MAX_HIDDEN = 1024
 
     def verify_pass(self, M: int, start_pos: int, form: str | None = None,
@@ -605,15 +607,12 @@ class DecodeModel:
         ctx, c = self.ctx, self.cfg
         B = self._verify_arena(M, logits=not last_only)
         h, qd, kvd, hd, ff = c.hidden, c.q_dim, c.kv_dim, c.head_dim, c.ff
-        X, XN = B["x"], B["xn"]
+        X, XN, Xo = B["x"], B["xn"], B["p"]
         form = form or ("rows" if M <= self.VERIFY_ROWS_MAX and h <= self.VERIFY_ROWS_MAX_HIDDEN
                         else "gemm")
         if form not in ("rows", "gemm"):
             raise ValueError("form must be 'rows' or 'gemm'")
         d.embed_rows_f32(ctx, self.embd_fmt, self.embd, B["tok"], X, h, M)
-
-        def gemm(fmt, w, x, y, n, k):
-            getattr(d, f"gemm_{fmt}_f32")(ctx, w, x, y, M, n, k)
 
         for L, F in zip(self.layers, self.fmts):
             if form == "rows":
@@ -629,15 +628,14 @@ class DecodeModel:
                 d.rope_kv_write_batch_f32(ctx, B["q"], B["k"], B["v"], L["kc"], L["vc"], hd, c.heads,
                                           c.kv_heads, start_pos, c.theta, M, c.max_seq)
             else:
-                d.rms_norm_f32_f32_f32g(ctx, X, XN, L["attn_norm"], c.eps, h, M)
-                for role, w, b, out, n in (("q", "wq", "bq", B["q"], qd), ("k", "wk", "bk", B["k"], kvd),
-                                           ("v", "wv", "bv", B["v"], kvd)):
-                    gemm(F[role], L[w], XN, out, n, h)
-                    d.add_bias_broadcast_f32(ctx, out, L[b], M, n)
-                d.rope_batch_inplace_f32(ctx, B["q"], hd, c.heads, start_pos, c.theta, M)
-                d.rope_batch_inplace_f32(ctx, B["k"], hd, c.kv_heads, start_pos, c.theta, M)
-                d.kv_write_batch_f32(ctx, B["k"], B["v"], L["kc"], L["vc"], start_pos, M, c.max_seq,
-                                     hd, c.kv_heads)
+                # Q/K/V (+ bias) of the normalised rows: one preparation of
+                # RMSNorm(X)·γ for the three GEMMs, the biases in their sums
+                d.gemm_set_f32(ctx, [F["q"], F["k"], F["v"]], [L["wq"], L["wk"], L["wv"]],
+                               [B["q"], B["k"], B["v"]], [qd, kvd, kvd], X, M, h,
+                               biases=[L["bq"], L["bk"], L["bv"]], gamma=L["attn_norm"], eps=c.eps,
+                               xn=XN)
+                d.rope_kv_write_batch_f32(ctx, B["q"], B["k"], B["v"], L["kc"], L["vc"], hd, c.heads,
+                                          c.kv_heads, start_pos, c.theta, M, c.max_seq)
             d.flash_attention_f32(ctx, B["q"], L["kc"], L["vc"], B["att"], 1, M, start_pos + M,
                                   c.heads, c.kv_heads, hd, c.max_seq, q_start=start_pos)
             if form == "rows":
@@ -648,14 +646,16 @@ class DecodeModel:
                                      gamma=L["ffn_norm"], eps=c.eps)
                 d.gemv_rows_add_f32(ctx, F["down"], L["wd"], B["g"], X, X, M, h, ff)
             else:
-                gemm(F["o"], L["wo"], B["att"], B["p"], h, qd)
-                d.add_f32(ctx, X, B["p"], X, M * h)
-                d.rms_norm_f32_f32_f32g(ctx, X, XN, L["ffn_norm"], c.eps, h, M)
-                gemm(F["gate"], L["wg"], XN, B["g"], ff, h)
-                gemm(F["up"], L["wu"], XN, B["u"], ff, h)
-                d.silu_mul_f32(ctx, B["g"], B["u"], B["g"], M * ff)
-                gemm(F["down"], L["wd"], B["g"], B["p"], h, ff)
-                d.add_f32(ctx, X, B["p"], X, M * h)
+                # O (+ the residual, into the other residual buffer), gate and
+                # up of the normalised rows with SiLU(gate)·up in their sums,
+                # down (+ the residual, back into the first)
+                d.gemm_set_f32(ctx, [F["o"]], [L["wo"]], [Xo], [h], B["att"], M, qd, res=X)
+                X, Xo = Xo, X
+                d.gemm_set_f32(ctx, [F["gate"], F["up"]], [L["wg"], L["wu"]], [B["g"], B["u"]],
+                               [ff, ff], X, M, h, gamma=L["ffn_norm"], eps=c.eps, xn=XN,
+                               silu_pair=True)
+                d.gemm_set_f32(ctx, [F["down"]], [L["wd"]], [Xo], [h], B["g"], M, ff, res=X)
+                X, Xo = Xo, X
         if last_only:
             # prefill: the final norm and the LM head on the last row only, into
             # the decode buffers (logits, token = its argmax) so that decoding
@@ -666,8 +666,8 @@ class DecodeModel:
             d.gemv_rows_f32(ctx, self.lm_fmt, self.lm_head, X, B["logits"], M, c.vocab, h,
                             gamma=self.final_norm, eps=c.eps)
         else:
-            d.rms_norm_f32_f32_f32g(ctx, X, XN, self.final_norm, c.eps, h, M)
-            gemm(self.lm_fmt, self.lm_head, XN, B["logits"], c.vocab, h)
+            d.gemm_set_f32(ctx, [self.lm_fmt], [self.lm_head], [B["logits"]], [c.vocab], X, M, h,
+                           gamma=self.final_norm, eps=c.eps, xn=XN)
         if not last_only:
             d.argmax_rows_first_f32(ctx, B["logits"], B["idx"], M, c.vocab)
         return B

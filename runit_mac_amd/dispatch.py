@@ -66,6 +66,7 @@ _P, _U32, _U64, _F = c_void_p, c_uint32, c_uint64, c_float
 _ROWS_FMTS = ("q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5kg", "q6kg")
 _SIGS = {
     "rt_ctx_create": [POINTER(c_void_p), c_char_p],
+    "rt_gemm_set_f32": [_P, _U32, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _P, _F, _P, _U32],
     "rt_flush": [_P],
     "rt_device_cu_count": [_P],
     "rt_has_kernel": [_P, c_char_p],
@@ -599,6 +600,27 @@ def dequant_q4k_f16(ctx, input, output, n_blocks):
 def dequant_f32(ctx, fmt: str, input, output, n_blocks):
     """Bit-exact dequantisation to f32 for fmt in {q8_0, q4_0, q4k, q6k, q5_0, q5k}."""
     _call(ctx, f"rt_dequant_{fmt}_f32", _ptr(input), _ptr(output), n_blocks)
+
+
+def gemm_set_f32(ctx, fmts, weights, ys, ns, x, m_rows, k, biases=None, res=None, gamma=None,
+                 eps=0.0, xn=None, silu_pair=False):
+    """The batched GEMMs of verify_draft over one activation matrix with the
+    kernels between them folded in (new; forward.rs:2186-2271): y[i] =
+    X·W[i]ᵀ (+ f16 bias[i]), X = x or RMSNorm(x)·γ (also written to xn);
+    res: y[0] = res + X·W[0]ᵀ; silu_pair: y[0] = silu(X·W[0]ᵀ)·(X·W[1]ᵀ)."""
+    cnt = len(fmts)
+    if not (len(weights) == len(ys) == len(ns) == cnt) or (biases is not None and len(biases) != cnt):
+        raise ValueError("gemm_set_f32: one weight, output and n per format")
+    names = (c_char_p * cnt)(*[f.encode() for f in fmts])
+    wv = (c_void_p * cnt)(*[_ptr(w) for w in weights])
+    yv = (c_void_p * cnt)(*[_ptr(y) for y in ys])
+    nv = (c_uint32 * cnt)(*ns)
+    bv = (c_void_p * cnt)(*[_ptr(b) if b is not None else None for b in biases]) if biases else None
+    adr = ctypes.addressof
+    _call(ctx, "rt_gemm_set_f32", cnt, adr(names), adr(wv), adr(yv), adr(nv),
+          adr(bv) if bv is not None else None, _ptr(res) if res is not None else None,
+          _ptr(x), m_rows, k, _ptr(gamma) if gamma is not None else None, eps,
+          _ptr(xn) if xn is not None else None, int(bool(silu_pair)))
 
 
 def gemm_q8_0_f32(ctx, weight, x, y, m_rows, n, k):

@@ -1,0 +1,99 @@
+"""rt_gemm_set_f32: the batched GEMMs of one activation matrix with the
+RMSNorm in the activation preparation and the bias / residual / SiLU in the
+K-split sums (verify_draft's projections, forward.rs:2186-2271), against the
+oracle: the normalised rows against ora.rms_norm, each projection against the
+per-row f64 GEMV of the same packed blocks over the rows the GPU normalised.
+Row counts cover the shared f16 form (8, 27, 32 rows; 27 leaves padded rows
+in the last group) and its fallbacks (1 row: GEMVs; 4 rows: the int8 form of
+the 4-bit formats, separate launches)."""
+import numpy as np
+import pytest
+
+import oracle_lib as ora
+from runit_mac_amd import dispatch as d
+from gpu_helpers import check_close, device_weights
+from test_gpu_fused import ffn_check
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+
+
+def _x(m, k, seed):
+    return np.random.default_rng(seed).standard_normal((m, k)).astype(np.float32)
+
+
+def _norm_checked(ctx, xn, x, gamma, m, h):
+    got = xn.read(np.float32, m * h).reshape(m, h)
+    ref = ora.rms_norm(x, gamma, EPS).reshape(m, h)
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.abs(ref).max(), "rms_norm rows"
+    return got
+
+
+@pytest.mark.parametrize("fmts", [("q4k", "q4k", "q6k"), ("q8_0", "q8_0", "q8_0")])
+@pytest.mark.parametrize("m", [1, 4, 8, 27, 32])
+def test_gemm_set_qkv_norm_bias(ctx, fmts, m):
+    h, ns = 1024, [1024, 256, 256]
+    W = [device_weights(ctx, f, n, h, 300 + i) for i, (f, n) in enumerate(zip(fmts, ns))]
+    rng = np.random.default_rng(m)
+    x = _x(m, h, m + 10)
+    gamma = (1 + 0.1 * rng.standard_normal(h)).astype(np.float32)
+    biases = [(0.1 * rng.standard_normal(n)).astype(np.float16) for n in ns]
+    ys = [ctx.new_buffer(4 * m * n) for n in ns]
+    xn = ctx.new_buffer(4 * m * h)
+    d.gemm_set_f32(ctx, list(fmts), [w for w, _ in W], ys, ns, ctx.buffer_from(x), m, h,
+                   biases=[ctx.buffer_from(b.view(np.uint16)) for b in biases],
+                   gamma=ctx.buffer_from(gamma), eps=EPS, xn=xn)
+    ctx.flush()
+    xr = _norm_checked(ctx, xn, x, gamma, m, h)
+    for i, (f, n) in enumerate(zip(fmts, ns)):
+        yref, sabs = ora.gemv(f, W[i][1], xr, n, h)
+        yref = yref + biases[i].astype(np.float64)[None, :]
+        check_close(ys[i].read(np.float32, m * n), yref.ravel(), sabs.ravel(),
+                    f"gemm_set {f} m={m} matrix {i}", extra=1e-6 * np.abs(yref.ravel()))
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q8_0"])
+@pytest.mark.parametrize("m", [1, 4, 8, 32])
+def test_gemm_set_silu_pair(ctx, fmt, m):
+    h, ff = 1024, 2048
+    (wg, rg), (wu, ru) = device_weights(ctx, fmt, ff, h, 311), device_weights(ctx, fmt, ff, h, 312)
+    x = _x(m, h, 40 + m)
+    gamma = np.linspace(0.5, 1.5, h, dtype=np.float32)
+    g, u, xn = ctx.new_buffer(4 * m * ff), ctx.new_buffer(4 * m * ff), ctx.new_buffer(4 * m * h)
+    d.gemm_set_f32(ctx, [fmt, fmt], [wg, wu], [g, u], [ff, ff], ctx.buffer_from(x), m, h,
+                   gamma=ctx.buffer_from(gamma), eps=EPS, xn=xn, silu_pair=True)
+    ctx.flush()
+    xr = _norm_checked(ctx, xn, x, gamma, m, h)
+    gr, gs = ora.gemv(fmt, rg, xr, ff, h)
+    ur, us = ora.gemv(fmt, ru, xr, ff, h)
+    ffn_check(g.read(np.float32, m * ff), gr.ravel(), gs.ravel(), ur.ravel(), us.ravel(),
+              f"gemm_set silu {fmt} m={m}")
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q6k", 1024, 2048), ("q4k", 1024, 3072), ("q8_0", 896, 4864)])
+@pytest.mark.parametrize("m", [1, 4, 8, 32])
+def test_gemm_set_residual(ctx, fmt, n, k, m):
+    w, raw = device_weights(ctx, fmt, n, k, 320)
+    x = _x(m, k, 50 + m)
+    res = _x(m, n, 60 + m)
+    y = ctx.new_buffer(4 * m * n)
+    d.gemm_set_f32(ctx, [fmt], [w], [y], [n], ctx.buffer_from(x), m, k, res=ctx.buffer_from(res))
+    ctx.flush()
+    yref, sabs = ora.gemv(fmt, raw, x, n, k)
+    yref = yref + res.astype(np.float64)
+    check_close(y.read(np.float32, m * n), yref.ravel(), sabs.ravel(), f"gemm_set res {fmt} m={m}",
+                extra=1e-6 * np.abs(yref.ravel()))
+
+
+def test_gemm_set_rejects_bad_sets(ctx):
+    w, _ = device_weights(ctx, "q8_0", 64, 256, 330)
+    x, y, y2 = ctx.new_buffer(4 * 8 * 256), ctx.new_buffer(4 * 8 * 64), ctx.new_buffer(4 * 8 * 64)
+    with pytest.raises(d.KernelError, match="residual"):
+        d.gemm_set_f32(ctx, ["q8_0"], [w], [y], [64], x, 8, 256, res=y)  # res aliases y[0]
+    with pytest.raises(d.KernelError, match="SiLU pair"):
+        d.gemm_set_f32(ctx, ["q8_0"], [w], [y], [64], x, 8, 256, silu_pair=True)
+    with pytest.raises(d.KernelError, match="format"):
+        d.gemm_set_f32(ctx, ["q9"], [w], [y], [64], x, 8, 256)
+    with pytest.raises(d.KernelError, match="gamma without xn"):
+        d.gemm_set_f32(ctx, ["q8_0", "q8_0"], [w, w], [y, y2], [64, 64], x, 8, 256, gamma=x)
