@@ -292,6 +292,7 @@ struct rt_ctx {
     bool gemv_valu = false;      // RUNIT_GEMV_VALU=1: VALU-dot twins of the LDS body (A/B)
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool gemm_set = true;  // RUNIT_GEMM_SET=0: rt_gemm_set_f32 as separate launches (A/B)
+    uint32_t gemm_set_min = 1;  // RUNIT_GEMM_SET_MIN: rows above which a set takes the shared f16 form
     bool gemm_sum_kernel = true;  // RUNIT_GEMM_SUM_KERNEL=0: K splits meet in the GEMM (arrival counters)
     uint32_t gemm_splits = 0;    // RUNIT_GEMM_SPLITS=n: the f16 GEMM's K splits forced (A/B)
     bool attn_w = true;          // RUNIT_ATTN_W=0: the token's RoPE attention on attn_split (A/B)
@@ -1319,6 +1320,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_SPLITS")) c->gemm_splits = (uint32_t)atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_SUM_KERNEL")) c->gemm_sum_kernel = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_SET")) c->gemm_set = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_SET_MIN")) c->gemm_set_min = atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_SM")) c->sm_enabled = atoi(g) != 0;
@@ -2291,10 +2293,9 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
     // The shared form: every matrix on the f16 form with one row grouping,
     // one preparation (norm-fused when gamma), epilogues in the split sums.
     Gemm3Plan pl[4];
-    bool shared = c->gemm_set && c->gemm_f16 && m_rows >= 2 && k <= 20480 && aligned(x, 16);
+    bool shared = c->gemm_set && c->gemm_f16 && m_rows >= 2 && m_rows > c->gemm_set_min &&
+                  k <= 20480 && aligned(x, 16);
     for (uint32_t i = 0; shared && i < count; ++i) {
-        shared = m_rows > (f[i]->blk_bytes == 210 ? c->gemm_f16_min_q6 : c->gemm_f16_min);
-        if (!shared) break;
         const int st = gemm3_plan(c, *f[i], w[i], m_rows, n[i], k, pl[i]);
         if (st != RT_OK && st != kLsDecline) return st;
         shared = st == RT_OK && pl[i].MG == pl[0].MG;
