@@ -245,6 +245,9 @@ struct Gemm2Args {
     uint32_t M, N, nxb, tiles, splits, kbs, nchunks;  // nxb, kbs: in weight blocks
     uint64_t row_bytes;
     uint32_t cstride;
+    // f16 form, unsplit launches: y = acc (+ f32(bias[n])) (+ res as res + y)
+    const uint16_t* bias;
+    const float* res;
 };
 
 // Block formats of the staged GEMM.  decode() gives, for record r of a
@@ -1052,12 +1055,18 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
                 acc[g][i] = __builtin_amdgcn_ldexpf(acc[g][i], a.etab[ch * 8 * MG + 8 * g + 2 * c + i]);
         const uint32_t n = row0 + 16 * wv + j;
         if (a.splits == 1) {
+            const float b = (a.bias && n < a.N) ? h2f(a.bias[n]) : 0.0f;
 #pragma unroll
             for (int g = 0; g < MG; ++g)
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
                     const uint32_t m = ch * 8 * MG + 8 * g + 2 * c + i;
-                    if (m < a.M && n < a.N) a.y[(size_t)m * a.N + n] = acc[g][i];
+                    if (m < a.M && n < a.N) {
+                        float v = acc[g][i];
+                        if (a.bias) v += b;
+                        if (a.res) v = a.res[(size_t)m * a.N + n] + v;
+                        a.y[(size_t)m * a.N + n] = v;
+                    }
                 }
             continue;
         }

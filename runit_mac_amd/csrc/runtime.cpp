@@ -1865,6 +1865,8 @@ struct Gemm2Args {
     uint32_t M, N, nxb, tiles, splits, kbs, nchunks;
     uint64_t row_bytes;
     uint32_t cstride;
+    const uint16_t* bias;
+    const float* res;
 };
 struct GemmArgs {
     const void* w;
@@ -2030,14 +2032,18 @@ static int gemm3_prep(rt_ctx* c, const Gemm3Plan& p, const float* x, uint32_t m_
 // The GEMM of a plan over prepared operands.  part: the partial sums
 // (splits > 1), left for the caller's sum when `leave_parts`; otherwise
 // summed here (k_gemm_split_sum, or in the GEMM with arrival counters).
+// Unsplit launches apply bias / res in their stores (y = acc + bias, then
+// res + y).
 static int gemm3_run(rt_ctx* c, const Gemm3Plan& p, const void* w, void* aops, int* erow,
                      float* stab, float* y, float* part, uint32_t m_rows, uint32_t n,
-                     bool leave_parts = false) {
+                     bool leave_parts = false, const uint16_t* bias = nullptr,
+                     const float* res = nullptr) {
     uint32_t cstride = 32;
     while (cstride > 1 && (size_t)p.base * cstride > kAttnCounters) cstride >>= 1;
     const bool sum_kernel = p.splits > 1 && (c->gemm_sum_kernel || leave_parts);
     Gemm2Args a2{w, aops, erow, stab, y, part, sum_kernel ? nullptr : c->counters,
-                 m_rows, n, p.nblk, p.tiles, p.splits, p.kbs, p.nchunks, p.row_bytes, cstride};
+                 m_rows, n, p.nblk, p.tiles, p.splits, p.kbs, p.nchunks, p.row_bytes, cstride,
+                 p.splits == 1 ? bias : nullptr, p.splits == 1 ? res : nullptr};
     void* p2[] = {&a2};
     int st = launch(c, p.kn, dim3(std::min(p.base * p.splits, p.cap)), dim3(64 * p.waves), 0, p2);
     if (st != RT_OK || !sum_kernel || leave_parts) return st;
@@ -2327,7 +2333,9 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
     size_t poff[4], total = p0.a_bytes + p0.e_bytes + s_bytes;
     bool ep[4];
     for (uint32_t i = 0; i < count; ++i) {
-        ep[i] = silu_pair || res || (bias && bias[i]);
+        // epilogue in the split sum: split launches, and the SiLU pair (an
+        // unsplit launch adds its bias / residual in its own stores)
+        ep[i] = (silu_pair || res || (bias && bias[i])) && (silu_pair || pl[i].splits > 1);
         poff[i] = total;
         // a matrix with an epilogue leaves its partial sums (one "split"
         // when unsplit) for k_gemm_split_sum_ep
@@ -2348,7 +2356,7 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
         // unsplit with an epilogue: the GEMM writes its rows into the partials
         float* yi = ep[i] && pl[i].splits == 1 ? part : y[i];
         st = gemm3_run(c, pl[i], w[i], aops, erow, f[i]->has_min ? stab : nullptr, yi, part, m_rows,
-                       n[i], ep[i]);
+                       n[i], ep[i], ep[i] || !bias ? nullptr : bias[i], ep[i] ? nullptr : res);
         if (st != RT_OK) return st;
         if (ep[i] && !silu_pair)
             st = gemm_split_sum_ep(c, part, nullptr, y[i], m_rows, n[i], pl[i].splits, crow,
