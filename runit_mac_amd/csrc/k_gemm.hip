@@ -1136,11 +1136,10 @@ extern "C" __global__ void __launch_bounds__(256) k_gemm_split_sum(const float* 
 //     Y = silu(Σ part) · Σ part2, silu(g) = g / (1 + e^−g)  (silu_mul_f32);
 //   bias given: Y += f32(bias[n])  (add_bias_broadcast_f16);
 //   res given:  Y = res + Y         (add_f32; Y may alias res).
-extern "C" __global__ void __launch_bounds__(256)
-k_gemm_split_sum_ep(const float* __restrict__ part, const float* __restrict__ part2, float* y,
-                    uint32_t M, uint32_t N, uint32_t splits, uint32_t crow,
-                    const uint16_t* __restrict__ bias, const float* res) {
-    const uint32_t m = blockIdx.y, n0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+RT_DEV void split_sum_ep(const float* __restrict__ part, const float* __restrict__ part2, float* y,
+                         uint32_t N, uint32_t splits, uint32_t crow,
+                         const uint16_t* __restrict__ bias, const float* res, uint32_t bx) {
+    const uint32_t m = blockIdx.y, n0 = (bx * 256 + threadIdx.x) * 4;
     if (n0 >= N) return;
     const uint32_t ch = m / crow, r = m % crow;
     const size_t off = ((size_t)ch * splits * crow + r) * N, ss = (size_t)crow * N;
@@ -1176,6 +1175,30 @@ k_gemm_split_sum_ep(const float* __restrict__ part, const float* __restrict__ pa
         if (res) v = res[(size_t)m * N + n] + v;
         y[(size_t)m * N + n] = v;
     }
+}
+extern "C" __global__ void __launch_bounds__(256)
+k_gemm_split_sum_ep(const float* __restrict__ part, const float* __restrict__ part2, float* y,
+                    uint32_t M, uint32_t N, uint32_t splits, uint32_t crow,
+                    const uint16_t* __restrict__ bias, const float* res) {
+    split_sum_ep(part, part2, y, N, splits, crow, bias, res, blockIdx.x);
+}
+// The split sums (+ bias) of up to three GEMMs of one set in one launch
+// (Q/K/V): workgroup columns [blk0[i], blk0[i + 1]) take output i.
+struct EpSeg {
+    const float* part;
+    float* y;
+    const uint16_t* bias;
+    uint32_t n, splits, blk0;
+};
+struct EpSegs {
+    EpSeg s[3];
+    uint32_t count, crow;
+};
+extern "C" __global__ void __launch_bounds__(256) k_gemm_split_sum_ep3(EpSegs a) {
+    uint32_t i = 0;
+    while (i + 1 < a.count && blockIdx.x >= a.s[i + 1].blk0) ++i;
+    const EpSeg& g = a.s[i];
+    split_sum_ep(g.part, nullptr, g.y, g.n, g.splits, a.crow, g.bias, nullptr, blockIdx.x - g.blk0);
 }
 #define RT_GEMM3_KERNEL4(FN, P, MG, NB)                                                       \
     extern "C" __global__ void __launch_bounds__(256) k_gemm3_##FN##_mg##MG(Gemm2Args a) {    \

@@ -143,7 +143,7 @@ const char* const kKernelNames[] = {
     "k_add_f16_into_f32", "k_ssq_quads", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
     "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32", "k_rope_kv_write_batch_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
-    "k_gemm_split_sum", "k_gemm_split_sum_ep", "k_gemm_xh_prep1n_mg1", "k_gemm_xh_prep1n_mg2",
+    "k_gemm_split_sum", "k_gemm_split_sum_ep", "k_gemm_split_sum_ep3", "k_gemm_xh_prep1n_mg1", "k_gemm_xh_prep1n_mg2",
     "k_gemm_xh_prep1n_mg4", "k_gemm_xh_prep1_mg1", "k_gemm_xh_prep1_mg2", "k_gemm_xh_prep1_mg4", "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
     "k_gemm_q8_0_mg1_ct2", "k_gemm_q8_0_mg2_ct2", "k_gemm_q8_0_mg4_ct2", "k_gemm_q8_0_mg8_ct2",
@@ -293,6 +293,7 @@ struct rt_ctx {
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool gemm_set = true;  // RUNIT_GEMM_SET=0: rt_gemm_set_f32 as separate launches (A/B)
     uint32_t gemm_set_min = 1;  // RUNIT_GEMM_SET_MIN: rows above which a set takes the shared f16 form
+    bool gemm_set_sum1 = true;  // RUNIT_GEMM_SET_SUM1=0: a set's split sums one launch per matrix (A/B)
     bool gemm_sum_kernel = true;  // RUNIT_GEMM_SUM_KERNEL=0: K splits meet in the GEMM (arrival counters)
     uint32_t gemm_splits = 0;    // RUNIT_GEMM_SPLITS=n: the f16 GEMM's K splits forced (A/B)
     bool attn_w = true;          // RUNIT_ATTN_W=0: the token's RoPE attention on attn_split (A/B)
@@ -1321,6 +1322,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_SUM_KERNEL")) c->gemm_sum_kernel = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_SET")) c->gemm_set = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_SET_MIN")) c->gemm_set_min = atoi(g);
+    if (const char* g = getenv("RUNIT_GEMM_SET_SUM1")) c->gemm_set_sum1 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_SM")) c->sm_enabled = atoi(g) != 0;
@@ -2262,6 +2264,18 @@ static const GemmFmt* gemm_fmt_named(const char* name) {
     return nullptr;
 }
 
+// Mirrors the device-side EpSeg / EpSegs (k_gemm.hip).
+struct EpSeg {
+    const float* part;
+    float* y;
+    const uint16_t* bias;
+    uint32_t n, splits, blk0;
+};
+struct EpSegs {
+    EpSeg s[3];
+    uint32_t count, crow;
+};
+
 static int gemm_split_sum_ep(rt_ctx* c, const float* part, const float* part2, float* y, uint32_t m,
                              uint32_t n, uint32_t splits, uint32_t crow, const uint16_t* bias,
                              const float* res) {
@@ -2351,6 +2365,11 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
     float* stab = s_bytes ? (float*)(ws + p0.a_bytes + p0.e_bytes) : nullptr;
     st = gemm3_prep(c, p0, x, m_rows, k, aops, erow, stab, gamma, eps, gamma ? xn : nullptr);
     if (st != RT_OK) return st;
+    // the sums (+ bias) of the matrices of a set without residual or SiLU
+    // pair: one launch for all of them (k_gemm_split_sum_ep3)
+    EpSegs es{};
+    es.crow = crow;
+    const bool one_sum = !silu_pair && !res && c->gemm_set_sum1 && count <= 3;
     for (uint32_t i = 0; i < count; ++i) {
         float* part = (float*)(ws + poff[i]);
         // unsplit with an epilogue: the GEMM writes its rows into the partials
@@ -2358,11 +2377,31 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
         st = gemm3_run(c, pl[i], w[i], aops, erow, f[i]->has_min ? stab : nullptr, yi, part, m_rows,
                        n[i], ep[i], ep[i] || !bias ? nullptr : bias[i], ep[i] ? nullptr : res);
         if (st != RT_OK) return st;
-        if (ep[i] && !silu_pair)
+        if (ep[i] && one_sum) {
+            EpSeg& g = es.s[es.count];
+            g.blk0 = es.count ? es.s[es.count - 1].blk0 + (es.s[es.count - 1].n + 1023) / 1024 : 0;
+            g.part = part;
+            g.y = y[i];
+            g.bias = bias ? bias[i] : nullptr;
+            g.n = n[i];
+            g.splits = pl[i].splits;
+            ++es.count;
+        } else if (ep[i] && !silu_pair) {
             st = gemm_split_sum_ep(c, part, nullptr, y[i], m_rows, n[i], pl[i].splits, crow,
                                    bias ? bias[i] : nullptr, res);
+        }
         if (st != RT_OK) return st;
     }
+    if (es.count == 1) {
+        const EpSeg& g = es.s[0];
+        st = gemm_split_sum_ep(c, g.part, nullptr, g.y, m_rows, g.n, g.splits, crow, g.bias, nullptr);
+    } else if (es.count > 1) {
+        const EpSeg& g = es.s[es.count - 1];
+        void* pp[] = {&es};
+        st = launch(c, "k_gemm_split_sum_ep3", dim3(g.blk0 + (g.n + 1023) / 1024, m_rows), dim3(256),
+                    0, pp);
+    }
+    if (st != RT_OK) return st;
     if (!silu_pair) return RT_OK;
     float* pg = (float*)(ws + poff[0]);
     float* pu = (float*)(ws + poff[1]);
