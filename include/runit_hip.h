@@ -402,6 +402,22 @@ int rt_gemm_set_f32(rt_ctx* ctx, uint32_t count, const char* const* fmts, const 
                     float* const* y, const uint32_t* n, const uint16_t* const* bias,
                     const float* res, const float* x, uint32_t m_rows, uint32_t k,
                     const float* gamma, float eps, float* xn, uint32_t silu_pair);
+/* New: the part of a verify_draft layer after the attention
+ * (forward.rs:2227-2271) over M rows as one call: O + residual, RMSNorm,
+ * gate / up + SiLU, down + residual, each projection in its own block format:
+ *   x_mid = x + att·w_oᵀ;  X2 = RMSNorm(x_mid)·gamma;
+ *   g = silu(X2·w_gateᵀ) · (X2·w_upᵀ);  x = x_mid + g·w_downᵀ
+ * (att [m_rows][qd], x and x_mid [m_rows][h], x_mid apart from x).  Where all
+ * four take the f16 matrix-core form with one row grouping, each sum of K
+ * splits is folded into the next projection's activation preparation
+ * (8 launches); otherwise it runs as three rt_gemm_set_f32 calls, which also
+ * write g, u ([m_rows][ff]) and xn ([m_rows][h], X2); the shared form leaves
+ * them unspecified. */
+int rt_gemm_ffn_block_f32(rt_ctx* ctx, const char* fmt_o, const void* w_o, const char* fmt_gate,
+                          const void* w_gate, const char* fmt_up, const void* w_up,
+                          const char* fmt_down, const void* w_down, const float* att, float* x,
+                          float* x_mid, const float* gamma, float eps, float* g, float* u,
+                          float* xn, uint32_t m_rows, uint32_t h, uint32_t qd, uint32_t ff);
 
 /* ──────────────── multi-row GEMVs (batched verify / prefill) ────────────────
  * New: the M-row projections of verify_draft (forward.rs:2186-2271, which

@@ -783,24 +783,61 @@ RT_DEV void gemm_xh_prep_body(const float* __restrict__ x, uint32_t M, uint32_t 
 // (thread t: float4s t, t + 1024, ...), reduces the row's largest |x|, then
 // writes each float4 as half of a 16-byte A entry (hi, lo) — one round trip
 // to memory instead of three.
-template <int MG, bool NORM = false>
+// The row of a preparation given as the K-split partial sums of the GEMM
+// that produced it ([chunk][split][crow][K], as k_gemm_split_sum reads
+// them): x = Σ part (SILU: silu(Σ part)·Σ part2), then res + x; written to y
+// when given.
+struct PrepSum {
+    const float* part;
+    const float* part2;
+    const float* res;
+    float* y;
+    uint32_t splits, crow;
+};
+
+template <int MG, bool NORM = false, bool SUM = false>
 RT_DEV void gemm_xh_prep1_body(const float* __restrict__ x, uint32_t M, uint32_t K,
                                uint2* __restrict__ aops, int* __restrict__ etab,
                                float* __restrict__ stab, const float* __restrict__ gamma = nullptr,
-                               float eps = 0.0f, float* __restrict__ xn = nullptr) {
+                               float eps = 0.0f, float* __restrict__ xn = nullptr,
+                               const PrepSum* ps = nullptr) {
     constexpr uint32_t ROWS = 8 * MG, T = 1024, NPT = 5;
     __shared__ float red[16];
     const uint32_t nrec = K / 32, nf = K / 4;
     const uint32_t m = blockIdx.x;
     const uint32_t ch = m / ROWS, rr = m % ROWS, g = rr / 8, mm = rr % 8;
     const uint32_t tid = threadIdx.x;
-    const float* xr = x + (size_t)(m < M ? m : 0) * K;
     f32x4 v[NPT];
     float mx = 0.0f;
+    if constexpr (SUM) {
+        const uint32_t mc = m < M ? m : 0, sch = mc / ps->crow, sr = mc % ps->crow;
+        const size_t off = ((size_t)sch * ps->splits * ps->crow + sr) * K, ss = (size_t)ps->crow * K;
 #pragma unroll
-    for (uint32_t i = 0; i < NPT; ++i) {
-        const uint32_t f = tid + T * i;
-        v[i] = (m < M && f < nf) ? *(const f32x4*)(xr + 4 * f) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t i = 0; i < NPT; ++i) {
+            const uint32_t f = tid + T * i;
+            f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (m < M && f < nf) {
+                t = *(const f32x4*)(ps->part + off + 4 * f);
+                for (uint32_t sp = 1; sp < ps->splits; ++sp) t += *(const f32x4*)(ps->part + off + sp * ss + 4 * f);
+                if (ps->part2) {
+                    f32x4 u = *(const f32x4*)(ps->part2 + off + 4 * f);
+                    for (uint32_t sp = 1; sp < ps->splits; ++sp)
+                        u += *(const f32x4*)(ps->part2 + off + sp * ss + 4 * f);
+                    t = f32x4{t.x / (1.0f + expf(-t.x)) * u.x, t.y / (1.0f + expf(-t.y)) * u.y,
+                              t.z / (1.0f + expf(-t.z)) * u.z, t.w / (1.0f + expf(-t.w)) * u.w};
+                }
+                if (ps->res) t = *(const f32x4*)(ps->res + (size_t)m * K + 4 * f) + t;
+                if (ps->y) *(f32x4*)(ps->y + (size_t)m * K + 4 * f) = t;
+            }
+            v[i] = t;
+        }
+    } else {
+        const float* xr = x + (size_t)(m < M ? m : 0) * K;
+#pragma unroll
+        for (uint32_t i = 0; i < NPT; ++i) {
+            const uint32_t f = tid + T * i;
+            v[i] = (m < M && f < nf) ? *(const f32x4*)(xr + 4 * f) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
     }
     if constexpr (NORM) {
         // rms_norm_f32_f32_f32g of the row first: x · rsqrt(mean(x²) + eps) · γ,
@@ -887,6 +924,23 @@ RT_GEMM_XH_PREP1(4)
 RT_GEMM_XH_PREP1N(1)
 RT_GEMM_XH_PREP1N(2)
 RT_GEMM_XH_PREP1N(4)
+// the preparation of a row given as a GEMM's partial sums (PrepSum), plain or
+// RMS-normalised
+#define RT_GEMM_XH_PREP1S(MG)                                                                  \
+    extern "C" __global__ void __launch_bounds__(1024) k_gemm_xh_prep1s_mg##MG(                \
+        PrepSum ps, uint32_t M, uint32_t K, uint2* aops, int* etab, float* stab) {             \
+        gemm_xh_prep1_body<MG, false, true>(nullptr, M, K, aops, etab, stab, nullptr, 0.0f,    \
+                                            nullptr, &ps);                                     \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(1024) k_gemm_xh_prep1sn_mg##MG(               \
+        PrepSum ps, uint32_t M, uint32_t K, uint2* aops, int* etab, float* stab,               \
+        const float* gamma, float eps) {                                                       \
+        gemm_xh_prep1_body<MG, true, true>(nullptr, M, K, aops, etab, stab, gamma, eps,        \
+                                           nullptr, &ps);                                      \
+    }
+RT_GEMM_XH_PREP1S(1)
+RT_GEMM_XH_PREP1S(2)
+RT_GEMM_XH_PREP1S(4)
 RT_GEMM_XH_PREP(1)
 RT_GEMM_XH_PREP(2)
 RT_GEMM_XH_PREP(4)

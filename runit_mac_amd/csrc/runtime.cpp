@@ -18,6 +18,7 @@
 #include <cstring>
 #include <string>
 #include <unordered_map>
+#include <array>
 #include <vector>
 
 #include "../../include/runit_hip.h"
@@ -143,7 +144,9 @@ const char* const kKernelNames[] = {
     "k_add_f16_into_f32", "k_ssq_quads", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
     "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32", "k_rope_kv_write_batch_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
-    "k_gemm_split_sum", "k_gemm_split_sum_ep", "k_gemm_split_sum_ep3", "k_gemm_xh_prep1n_mg1", "k_gemm_xh_prep1n_mg2",
+    "k_gemm_split_sum", "k_gemm_split_sum_ep", "k_gemm_split_sum_ep3", "k_gemm_xh_prep1s_mg1",
+    "k_gemm_xh_prep1s_mg2", "k_gemm_xh_prep1s_mg4", "k_gemm_xh_prep1sn_mg1", "k_gemm_xh_prep1sn_mg2",
+    "k_gemm_xh_prep1sn_mg4", "k_gemm_xh_prep1n_mg1", "k_gemm_xh_prep1n_mg2",
     "k_gemm_xh_prep1n_mg4", "k_gemm_xh_prep1_mg1", "k_gemm_xh_prep1_mg2", "k_gemm_xh_prep1_mg4", "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
     "k_gemm_q8_0_mg1_ct2", "k_gemm_q8_0_mg2_ct2", "k_gemm_q8_0_mg4_ct2", "k_gemm_q8_0_mg8_ct2",
@@ -294,6 +297,9 @@ struct rt_ctx {
     bool gemm_set = true;  // RUNIT_GEMM_SET=0: rt_gemm_set_f32 as separate launches (A/B)
     uint32_t gemm_set_min = 1;  // RUNIT_GEMM_SET_MIN: rows above which a set takes the shared f16 form
     bool gemm_set_sum1 = true;  // RUNIT_GEMM_SET_SUM1=0: a set's split sums one launch per matrix (A/B)
+    bool gemm_block = true;     // RUNIT_GEMM_BLOCK=0: rt_gemm_ffn_block_f32 as three sets (A/B)
+    uint32_t gemm_block_silu_min = 64;  // RUNIT_GEMM_BLOCK_SILU_MIN: rows from which the block
+                                        // sums the SiLU pair in the down preparation
     bool gemm_sum_kernel = true;  // RUNIT_GEMM_SUM_KERNEL=0: K splits meet in the GEMM (arrival counters)
     uint32_t gemm_splits = 0;    // RUNIT_GEMM_SPLITS=n: the f16 GEMM's K splits forced (A/B)
     bool attn_w = true;          // RUNIT_ATTN_W=0: the token's RoPE attention on attn_split (A/B)
@@ -1323,6 +1329,8 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_SET")) c->gemm_set = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_SET_MIN")) c->gemm_set_min = atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_SET_SUM1")) c->gemm_set_sum1 = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_BLOCK")) c->gemm_block = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_BLOCK_SILU_MIN")) c->gemm_block_silu_min = atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_SM")) c->sm_enabled = atoi(g) != 0;
@@ -2412,6 +2420,146 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
         st = gemm_split_sum_ep(c, pg, nullptr, y[0], m_rows, n[0], pl[0].splits, crow, nullptr, nullptr);
     if (st != RT_OK) return st;
     return rt_silu_mul_f32(c, y[0], y[1], y[0], m_rows * n[0]);
+}
+
+// Mirrors the device-side PrepSum (k_gemm.hip).
+struct PrepSum {
+    const float* part;
+    const float* part2;
+    const float* res;
+    float* y;
+    uint32_t splits, crow;
+};
+
+int rt_gemm_ffn_block_f32(rt_ctx* c, const char* fmt_o, const void* w_o, const char* fmt_gate,
+                          const void* w_gate, const char* fmt_up, const void* w_up,
+                          const char* fmt_down, const void* w_down, const float* att, float* x,
+                          float* x_mid, const float* gamma, float eps, float* g, float* u,
+                          float* xn, uint32_t m_rows, uint32_t h, uint32_t qd, uint32_t ff) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (m_rows == 0) return RT_OK;
+    if (!att || !x || !x_mid || !gamma || !g || !u || !xn || x_mid == x)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_ffn_block: null buffer, or "
+                    "x_mid the same as x");
+    const GemmFmt* fo = gemm_fmt_named(fmt_o);
+    const GemmFmt* fg = gemm_fmt_named(fmt_gate);
+    const GemmFmt* fu = gemm_fmt_named(fmt_up);
+    const GemmFmt* fd = gemm_fmt_named(fmt_down);
+    // the separate sets: O + residual, gate/up + SiLU of the normalised
+    // rows, down + residual (every argument check is theirs)
+    auto sets = [&]() {
+        const char* f1[] = {fmt_o};
+        const void* w1[] = {w_o};
+        float* y1[] = {x_mid};
+        const uint32_t n1[] = {h};
+        int st = rt_gemm_set_f32(c, 1, f1, w1, y1, n1, nullptr, x, att, m_rows, qd, nullptr, 0.0f,
+                                 nullptr, 0);
+        if (st != RT_OK) return st;
+        const char* f2[] = {fmt_gate, fmt_up};
+        const void* w2[] = {w_gate, w_up};
+        float* y2[] = {g, u};
+        const uint32_t n2[] = {ff, ff};
+        st = rt_gemm_set_f32(c, 2, f2, w2, y2, n2, nullptr, nullptr, x_mid, m_rows, h, gamma, eps,
+                             xn, 1);
+        if (st != RT_OK) return st;
+        const char* f3[] = {fmt_down};
+        const void* w3[] = {w_down};
+        float* y3[] = {x};
+        const uint32_t n3[] = {h};
+        return rt_gemm_set_f32(c, 1, f3, w3, y3, n3, nullptr, x_mid, g, m_rows, ff, nullptr, 0.0f,
+                               nullptr, 0);
+    };
+    if (!fo || !fg || !fu || !fd || !c->gemm_set || !c->gemm_block || !c->gemm_f16 || m_rows < 2 ||
+        m_rows <= c->gemm_set_min || qd > 20480 || h > 20480 || ff > 20480 || !aligned(att, 16) ||
+        qd % fo->blk_el || h % fg->blk_el || h % fu->blk_el || ff % fd->blk_el)
+        return sets();
+    Gemm3Plan po, pg, pu, pd;
+    int st = gemm3_plan(c, *fo, w_o, m_rows, h, qd, po);
+    if (st == RT_OK) st = gemm3_plan(c, *fg, w_gate, m_rows, ff, h, pg);
+    if (st == RT_OK) st = gemm3_plan(c, *fu, w_up, m_rows, ff, h, pu);
+    if (st == RT_OK) st = gemm3_plan(c, *fd, w_down, m_rows, h, ff, pd);
+    if (st == kLsDecline || (st == RT_OK && (pg.MG != po.MG || pu.MG != po.MG || pd.MG != po.MG ||
+                                             pg.splits != pu.splits)))
+        return sets();
+    if (st != RT_OK) return st;
+    // workspace: operands of att (K = qd), of the normalised x_mid (K = h),
+    // of the SiLU product (K = ff), then the partial sums of O, gate, up, down
+    const uint32_t MG = po.MG, nch = po.nchunks, crow = 8 * MG;
+    auto ops = [&](uint32_t k, bool mins) {
+        const size_t a = (size_t)nch * (k / 32) * MG * 64 * 16, e = (size_t)nch * 8 * MG * sizeof(int);
+        const size_t sb = mins ? (size_t)nch * (k / 32) * 8 * MG * sizeof(float) : 0;
+        return std::array<size_t, 3>{a, e, sb};
+    };
+    auto parts = [&](const Gemm3Plan& p, uint32_t n) {
+        return (size_t)std::max<uint32_t>(1, p.splits) * nch * crow * n * sizeof(float);
+    };
+    const auto oa = ops(qd, fo->has_min), oh = ops(h, fg->has_min || fu->has_min), of = ops(ff, fd->has_min);
+    size_t off[12], total = 0;
+    const size_t sizes[12] = {oa[0], oa[1], oa[2], oh[0], oh[1], oh[2], of[0], of[1], of[2],
+                              parts(po, h), parts(pg, ff), parts(pu, ff)};
+    for (int i = 0; i < 12; ++i) {
+        off[i] = total;
+        total = (total + sizes[i] + 255) & ~(size_t)255;
+    }
+    const size_t off_pd = total;
+    total += parts(pd, h);
+    st = ensure_ws(c, total, "gemm_ffn_block");
+    if (st != RT_OK) return st;
+    char* ws = (char*)c->ws;
+    auto at = [&](int i) { return sizes[i] ? (void*)(ws + off[i]) : nullptr; };
+    float* part_o = (float*)at(9);
+    float* part_g = (float*)at(10);
+    float* part_u = (float*)at(11);
+    float* part_d = (float*)(ws + off_pd);
+    // O over att, its partials left; x_mid = x + Σ, normalised and prepared
+    st = gemm3_prep(c, po, att, m_rows, qd, at(0), (int*)at(1), (float*)at(2));
+    if (st == RT_OK)
+        st = gemm3_run(c, po, w_o, at(0), (int*)at(1), fo->has_min ? (float*)at(2) : nullptr,
+                       po.splits == 1 ? part_o : x_mid, part_o, m_rows, h, true);
+    if (st != RT_OK) return st;
+    char pk[48];
+    uint32_t M = m_rows, K = h;
+    {
+        PrepSum ps{part_o, nullptr, x, x_mid, po.splits, crow};
+        void* aops = at(3);
+        int* erow = (int*)at(4);
+        float* stab = (float*)at(5);
+        snprintf(pk, sizeof pk, "k_gemm_xh_prep1sn_mg%u", MG);
+        void* pp[] = {&ps, &M, &K, &aops, &erow, &stab, (void*)&gamma, &eps};
+        st = launch(c, pk, dim3(nch * 8 * MG), dim3(1024), 0, pp);
+    }
+    // gate and up, their partials left; silu(Σ gate)·Σ up prepared for down
+    if (st == RT_OK)
+        st = gemm3_run(c, pg, w_gate, at(3), (int*)at(4), fg->has_min ? (float*)at(5) : nullptr,
+                       part_g, part_g, m_rows, ff, true);
+    if (st == RT_OK)
+        st = gemm3_run(c, pu, w_up, at(3), (int*)at(4), fu->has_min ? (float*)at(5) : nullptr,
+                       part_u, part_u, m_rows, ff, true);
+    if (st != RT_OK) return st;
+    if (m_rows >= c->gemm_block_silu_min) {
+        // the SiLU sum in the preparation (one workgroup per row reads the
+        // row's partials of gate and up)
+        PrepSum ps{part_g, part_u, nullptr, nullptr, pg.splits, crow};
+        void* aops = at(6);
+        int* erow = (int*)at(7);
+        float* stab = (float*)at(8);
+        K = ff;
+        snprintf(pk, sizeof pk, "k_gemm_xh_prep1s_mg%u", MG);
+        void* pp[] = {&ps, &M, &K, &aops, &erow, &stab};
+        st = launch(c, pk, dim3(nch * 8 * MG), dim3(1024), 0, pp);
+    } else {
+        // few rows: the sum over the whole grid into g, then g prepared (8
+        // rows of 18944 summed in their 8 preparation workgroups made the 7B
+        // verify pass 50-60 µs slower)
+        st = gemm_split_sum_ep(c, part_g, part_u, g, m_rows, ff, pg.splits, crow, nullptr, nullptr);
+        if (st == RT_OK) st = gemm3_prep(c, pd, g, m_rows, ff, at(6), (int*)at(7), (float*)at(8));
+    }
+    // down, then x = x_mid + Σ
+    if (st == RT_OK)
+        st = gemm3_run(c, pd, w_down, at(6), (int*)at(7), fd->has_min ? (float*)at(8) : nullptr,
+                       part_d, part_d, m_rows, h, true);
+    if (st != RT_OK) return st;
+    return gemm_split_sum_ep(c, part_d, nullptr, x, m_rows, h, pd.splits, crow, nullptr, x_mid);
 }
 
 // ───────────────────────────── dequant ─────────────────────────────

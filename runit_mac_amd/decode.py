@@ -646,16 +646,12 @@ class DecodeModel:
                                      gamma=L["ffn_norm"], eps=c.eps)
                 d.gemv_rows_add_f32(ctx, F["down"], L["wd"], B["g"], X, X, M, h, ff)
             else:
-                # O (+ the residual, into the other residual buffer), gate and
-                # up of the normalised rows with SiLU(gate)·up in their sums,
-                # down (+ the residual, back into the first)
-                d.gemm_set_f32(ctx, [F["o"]], [L["wo"]], [Xo], [h], B["att"], M, qd, res=X)
-                X, Xo = Xo, X
-                d.gemm_set_f32(ctx, [F["gate"], F["up"]], [L["wg"], L["wu"]], [B["g"], B["u"]],
-                               [ff, ff], X, M, h, gamma=L["ffn_norm"], eps=c.eps, xn=XN,
-                               silu_pair=True)
-                d.gemm_set_f32(ctx, [F["down"]], [L["wd"]], [Xo], [h], B["g"], M, ff, res=X)
-                X, Xo = Xo, X
+                # O + residual (into Xo), norm, gate/up + SiLU, down +
+                # residual (back into X): each K-split sum folded into the
+                # next projection's operand preparation
+                d.gemm_ffn_block_f32(ctx, (F["o"], F["gate"], F["up"], F["down"]), L["wo"], L["wg"],
+                                     L["wu"], L["wd"], B["att"], X, Xo, L["ffn_norm"], c.eps,
+                                     B["g"], B["u"], XN, M, h, qd, ff)
         if last_only:
             # prefill: the final norm and the LM head on the last row only, into
             # the decode buffers (logits, token = its argmax) so that decoding

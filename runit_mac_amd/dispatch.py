@@ -67,6 +67,8 @@ _ROWS_FMTS = ("q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5k
 _SIGS = {
     "rt_ctx_create": [POINTER(c_void_p), c_char_p],
     "rt_gemm_set_f32": [_P, _U32, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _P, _F, _P, _U32],
+    "rt_gemm_ffn_block_f32": [_P, c_char_p, _P, c_char_p, _P, c_char_p, _P, c_char_p, _P, _P, _P,
+                              _P, _P, _F, _P, _P, _P, _U32, _U32, _U32, _U32],
     "rt_flush": [_P],
     "rt_device_cu_count": [_P],
     "rt_has_kernel": [_P, c_char_p],
@@ -621,6 +623,18 @@ def gemm_set_f32(ctx, fmts, weights, ys, ns, x, m_rows, k, biases=None, res=None
           adr(bv) if bv is not None else None, _ptr(res) if res is not None else None,
           _ptr(x), m_rows, k, _ptr(gamma) if gamma is not None else None, eps,
           _ptr(xn) if xn is not None else None, int(bool(silu_pair)))
+
+
+def gemm_ffn_block_f32(ctx, fmts, w_o, w_gate, w_up, w_down, att, x, x_mid, gamma, eps, g, u, xn,
+                       m_rows, h, qd, ff):
+    """The part of a verify_draft layer after the attention (new;
+    forward.rs:2227-2271): x_mid = x + att·W_oᵀ, then x = x_mid +
+    (silu(X2·W_gᵀ)·(X2·W_uᵀ))·W_dᵀ with X2 = RMSNorm(x_mid)·γ.  fmts: the
+    formats of (o, gate, up, down)."""
+    fo, fg, fu, fd = (f.encode() for f in fmts)
+    _call(ctx, "rt_gemm_ffn_block_f32", fo, _ptr(w_o), fg, _ptr(w_gate), fu, _ptr(w_up), fd,
+          _ptr(w_down), _ptr(att), _ptr(x), _ptr(x_mid), _ptr(gamma), eps, _ptr(g), _ptr(u),
+          _ptr(xn), m_rows, h, qd, ff)
 
 
 def gemm_q8_0_f32(ctx, weight, x, y, m_rows, n, k):

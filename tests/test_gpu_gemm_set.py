@@ -97,3 +97,38 @@ def test_gemm_set_rejects_bad_sets(ctx):
         d.gemm_set_f32(ctx, ["q9"], [w], [y], [64], x, 8, 256)
     with pytest.raises(d.KernelError, match="gamma without xn"):
         d.gemm_set_f32(ctx, ["q8_0", "q8_0"], [w, w], [y, y2], [64, 64], x, 8, 256, gamma=x)
+
+
+@pytest.mark.parametrize("fmts", [("q4k", "q4k", "q4k", "q6k"), ("q8_0", "q8_0", "q8_0", "q8_0")])
+@pytest.mark.parametrize("m", [1, 4, 8, 27, 32, 70])
+def test_gemm_ffn_block_equals_the_three_sets(ctx, fmts, m):
+    """rt_gemm_ffn_block_f32 against the same layer part as three GEMM sets
+    (each pinned to the oracle above): the folded sums add the same terms in
+    the same order, so x_mid and x are bit-identical.  70 rows: the SiLU sum
+    folded into the down projection's preparation as well (64 rows on)."""
+    h, qd, ff = 1024, 1024, 2048
+    fo, fg, fu, fd = fmts
+    wo, _ = device_weights(ctx, fo, h, qd, 340)
+    wg, _ = device_weights(ctx, fg, ff, h, 341)
+    wu, _ = device_weights(ctx, fu, ff, h, 342)
+    wd, _ = device_weights(ctx, fd, h, ff, 343)
+    att = ctx.buffer_from(_x(m, qd, 70 + m))
+    x0 = _x(m, h, 80 + m)
+    gamma = ctx.buffer_from(np.linspace(0.5, 1.5, h, dtype=np.float32))
+    outs = []
+    for block in (True, False):
+        x, xm = ctx.buffer_from(x0), ctx.new_buffer(4 * m * h)
+        g, u, xn = ctx.new_buffer(4 * m * ff), ctx.new_buffer(4 * m * ff), ctx.new_buffer(4 * m * h)
+        if block:
+            d.gemm_ffn_block_f32(ctx, fmts, wo, wg, wu, wd, att, x, xm, gamma, EPS, g, u, xn,
+                                 m, h, qd, ff)
+        else:
+            d.gemm_set_f32(ctx, [fo], [wo], [xm], [h], att, m, qd, res=x)
+            d.gemm_set_f32(ctx, [fg, fu], [wg, wu], [g, u], [ff, ff], xm, m, h, gamma=gamma,
+                           eps=EPS, xn=xn, silu_pair=True)
+            d.gemm_set_f32(ctx, [fd], [wd], [x], [h], g, m, ff, res=xm)
+        ctx.flush()
+        outs.append((xm.read(np.float32, m * h), x.read(np.float32, m * h)))
+    assert np.array_equal(outs[0][0], outs[1][0]), "x_mid"
+    assert np.array_equal(outs[0][1], outs[1][1]), "x"
+    assert np.all(np.isfinite(outs[0][1]))
