@@ -402,6 +402,20 @@ int rt_gemm_set_f32(rt_ctx* ctx, uint32_t count, const char* const* fmts, const 
                     float* const* y, const uint32_t* n, const uint16_t* const* bias,
                     const float* res, const float* x, uint32_t m_rows, uint32_t k,
                     const float* gamma, float eps, float* xn, uint32_t silu_pair);
+/* New: the Q/K/V projections of verify_draft (forward.rs:2186-2231) as one
+ * call: rt_gemm_set_f32 of the three matrices with their f16 biases over
+ * RMSNorm(x)·gamma (written to xn), then RoPE of q and k at positions
+ * start_pos + r (rt_rope_kv_write_batch_f32) and k / v written to the caches
+ * ([kv_dim / head_dim][max_seq][head_dim]).  q receives the rotated rows;
+ * k and v ([m_rows][kv_dim]) are left unspecified.  On the shared f16 form
+ * the rotation and the cache writes run in the K-split sum launch. */
+int rt_gemm_qkv_rope_f32(rt_ctx* ctx, const char* fmt_q, const void* w_q, const char* fmt_k,
+                         const void* w_k, const char* fmt_v, const void* w_v, const uint16_t* b_q,
+                         const uint16_t* b_k, const uint16_t* b_v, const float* x,
+                         const float* gamma, float eps, float* xn, float* q, float* k, float* v,
+                         float* k_cache, float* v_cache, uint32_t m_rows, uint32_t hidden,
+                         uint32_t q_dim, uint32_t kv_dim, uint32_t head_dim, uint32_t start_pos,
+                         float theta, uint32_t max_seq);
 /* New: the part of a verify_draft layer after the attention
  * (forward.rs:2227-2271) over M rows as one call: O + residual, RMSNorm,
  * gate / up + SiLU, down + residual, each projection in its own block format:

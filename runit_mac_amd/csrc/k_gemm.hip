@@ -1254,6 +1254,74 @@ extern "C" __global__ void __launch_bounds__(256) k_gemm_split_sum_ep3(EpSegs a)
     const EpSeg& g = a.s[i];
     split_sum_ep(g.part, nullptr, g.y, g.n, g.splits, a.crow, g.bias, nullptr, blockIdx.x - g.blk0);
 }
+// k_gemm_split_sum_ep3 of the Q/K/V set with rope_kv_write_batch folded in:
+// segment 0 (q) rotated and written to q, segment 1 (k) rotated and written
+// to the key cache at position start_pos + row, segment 2 (v) written to the
+// value cache.  A workgroup's 1024 outputs are whole heads (head_dim divides
+// 1024), so each pair (d, d + hd/2) meets in the workgroup's LDS; the angle
+// is rope_kv_write_batch's, pos / θ^(2d/hd).
+struct RopeKv {
+    float* kc;
+    float* vc;
+    uint32_t head_dim, start_pos, max_seq;
+    float theta;
+};
+extern "C" __global__ void __launch_bounds__(256) k_gemm_split_sum_qkv_rope(EpSegs a, RopeKv rk) {
+    __shared__ float row[1024];
+    uint32_t si = 0;
+    while (si + 1 < a.count && blockIdx.x >= a.s[si + 1].blk0) ++si;
+    const EpSeg& g = a.s[si];
+    const uint32_t m = blockIdx.y, bx = blockIdx.x - g.blk0, tid = threadIdx.x;
+    const uint32_t n0 = (bx * 256 + tid) * 4;
+    const bool live = n0 < g.n;
+    f32x4 v = {0, 0, 0, 0};
+    if (live) {
+        const uint32_t ch = m / a.crow, r = m % a.crow;
+        const size_t off = ((size_t)ch * g.splits * a.crow + r) * g.n, ss = (size_t)a.crow * g.n;
+        v = *(const f32x4*)(g.part + off + n0);
+        for (uint32_t sp = 1; sp < g.splits; ++sp) v += *(const f32x4*)(g.part + off + sp * ss + n0);
+        if (g.bias) {
+            const uint2 b = *(const uint2*)(g.bias + n0);
+            v += f32x4{h2f(b.x), h2f(b.x >> 16), h2f(b.y), h2f(b.y >> 16)};
+        }
+    }
+    const uint32_t hd = rk.head_dim, half = hd / 2, pos = rk.start_pos + m;
+    if (si == 2) {  // v: straight to the cache
+        if (live) {
+            const uint32_t h = n0 / hd, d = n0 % hd;
+            *(f32x4*)(rk.vc + ((size_t)h * rk.max_seq + pos) * hd + d) = v;
+        }
+        return;
+    }
+    // the row's cos / sin per pair index, once per workgroup (head_dim ≤ 512)
+    __shared__ float cs[256], sn_[256];
+    if (tid < half) {
+        const float angle = (float)pos / powf(rk.theta, (float)(2 * tid) / (float)hd);
+        sincosf(angle, &sn_[tid], &cs[tid]);
+    }
+    *(f32x4*)(row + 4 * tid) = v;
+    __syncthreads();
+    if (!live) return;
+    const uint32_t h = n0 / hd, d0 = n0 % hd;
+    float o[4];
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e) {
+        const uint32_t d = d0 + e, dd = d % half, lo = 4 * tid + e;
+        const float c = cs[dd], sn = sn_[dd];
+        if (d < half) {
+            const float r = v[e], i = row[lo + half];
+            o[e] = r * c - i * sn;
+        } else {
+            const float r = row[lo - half], i = v[e];
+            o[e] = i * c + r * sn;
+        }
+    }
+    const f32x4 ov = {o[0], o[1], o[2], o[3]};
+    if (si == 0)
+        *(f32x4*)(g.y + (size_t)m * g.n + n0) = ov;
+    else
+        *(f32x4*)(rk.kc + ((size_t)h * rk.max_seq + pos) * hd + d0) = ov;
+}
 #define RT_GEMM3_KERNEL4(FN, P, MG, NB)                                                       \
     extern "C" __global__ void __launch_bounds__(256) k_gemm3_##FN##_mg##MG(Gemm2Args a) {    \
         gemm3_body<P, MG, NB>(a);                                                              \

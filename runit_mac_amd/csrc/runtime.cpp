@@ -144,7 +144,7 @@ const char* const kKernelNames[] = {
     "k_add_f16_into_f32", "k_ssq_quads", "k_add_bias_broadcast_f32", "k_rope_batch_f32", "k_kv_write_batch_f32",
     "k_add_f32", "k_silu_mul_f32", "k_argmax_rows_first_f32", "k_rope_kv_write_batch_f32",
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
-    "k_gemm_split_sum", "k_gemm_split_sum_ep", "k_gemm_split_sum_ep3", "k_gemm_xh_prep1s_mg1",
+    "k_gemm_split_sum", "k_gemm_split_sum_ep", "k_gemm_split_sum_ep3", "k_gemm_split_sum_qkv_rope", "k_gemm_xh_prep1s_mg1",
     "k_gemm_xh_prep1s_mg2", "k_gemm_xh_prep1s_mg4", "k_gemm_xh_prep1sn_mg1", "k_gemm_xh_prep1sn_mg2",
     "k_gemm_xh_prep1sn_mg4", "k_gemm_xh_prep1n_mg1", "k_gemm_xh_prep1n_mg2",
     "k_gemm_xh_prep1n_mg4", "k_gemm_xh_prep1_mg1", "k_gemm_xh_prep1_mg2", "k_gemm_xh_prep1_mg4", "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
@@ -298,6 +298,7 @@ struct rt_ctx {
     uint32_t gemm_set_min = 1;  // RUNIT_GEMM_SET_MIN: rows above which a set takes the shared f16 form
     bool gemm_set_sum1 = true;  // RUNIT_GEMM_SET_SUM1=0: a set's split sums one launch per matrix (A/B)
     bool gemm_block = true;     // RUNIT_GEMM_BLOCK=0: rt_gemm_ffn_block_f32 as three sets (A/B)
+    bool gemm_rope = true;      // RUNIT_GEMM_ROPE=0: rt_gemm_qkv_rope_f32 with a separate RoPE launch (A/B)
     uint32_t gemm_block_silu_min = 64;  // RUNIT_GEMM_BLOCK_SILU_MIN: rows from which the block
                                         // sums the SiLU pair in the down preparation
     bool gemm_sum_kernel = true;  // RUNIT_GEMM_SUM_KERNEL=0: K splits meet in the GEMM (arrival counters)
@@ -1330,6 +1331,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_SET_MIN")) c->gemm_set_min = atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_SET_SUM1")) c->gemm_set_sum1 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_BLOCK")) c->gemm_block = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_ROPE")) c->gemm_rope = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_BLOCK_SILU_MIN")) c->gemm_block_silu_min = atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_LS")) c->ls_enabled = atoi(g) != 0;
@@ -2291,10 +2293,22 @@ static int gemm_split_sum_ep(rt_ctx* c, const float* part, const float* part2, f
     return launch(c, "k_gemm_split_sum_ep", dim3((n + 1023) / 1024, m), dim3(256), 0, pp);
 }
 
-int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const void* const* w,
-                    float* const* y, const uint32_t* n, const uint16_t* const* bias,
-                    const float* res, const float* x, uint32_t m_rows, uint32_t k,
-                    const float* gamma, float eps, float* xn, uint32_t silu_pair) {
+// Mirrors the device-side RopeKv (k_gemm.hip).
+struct RopeKv {
+    float* kc;
+    float* vc;
+    uint32_t head_dim, start_pos, max_seq;
+    float theta;
+};
+
+// rt_gemm_set_f32; with `rope` (count 3: q, k, v) the sums also rotate q and
+// k and write k and v to the caches (k_gemm_split_sum_qkv_rope), or, on the
+// separate launches, rope_kv_write_batch runs after them.
+static int gemm_set_impl(rt_ctx* c, uint32_t count, const char* const* fmts, const void* const* w,
+                         float* const* y, const uint32_t* n, const uint16_t* const* bias,
+                         const float* res, const float* x, uint32_t m_rows, uint32_t k,
+                         const float* gamma, float eps, float* xn, uint32_t silu_pair,
+                         const RopeKv* rope) {
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     if (count == 0 || count > 4 || !fmts || !w || !y || !n)
         return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_set: count=%u (1..4) or null "
@@ -2318,11 +2332,17 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
             return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_set: k=%u must be a "
                         "positive multiple of %u", k, f[i]->blk_el);
     }
+    if (rope && (count != 3 || silu_pair || res || n[1] != n[2] || rope->head_dim == 0 ||
+                 n[0] % rope->head_dim || n[1] % rope->head_dim))
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_qkv_rope: q_dim / kv_dim "
+                    "not multiples of head_dim");
     // The shared form: every matrix on the f16 form with one row grouping,
     // one preparation (norm-fused when gamma), epilogues in the split sums.
     Gemm3Plan pl[4];
     bool shared = c->gemm_set && c->gemm_f16 && m_rows >= 2 && m_rows > c->gemm_set_min &&
-                  k <= 20480 && aligned(x, 16);
+                  k <= 20480 && aligned(x, 16) &&
+                  (!rope || (1024 % rope->head_dim == 0 && rope->head_dim <= 512 && n[0] % 4 == 0 && n[1] % 4 == 0 &&
+                             c->gemm_rope));
     for (uint32_t i = 0; shared && i < count; ++i) {
         const int st = gemm3_plan(c, *f[i], w[i], m_rows, n[i], k, pl[i]);
         if (st != RT_OK && st != kLsDecline) return st;
@@ -2344,6 +2364,11 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
         }
         if (res) return rt_add_f32(c, res, y[0], y[0], m_rows * n[0]);
         if (silu_pair) return rt_silu_mul_f32(c, y[0], y[1], y[0], m_rows * n[0]);
+        if (rope)
+            return rt_rope_kv_write_batch_f32(c, y[0], y[1], y[2], rope->kc, rope->vc,
+                                              rope->head_dim, n[0] / rope->head_dim,
+                                              n[1] / rope->head_dim, rope->start_pos, rope->theta,
+                                              m_rows, rope->max_seq);
         return RT_OK;
     }
     // workspace: [operands | row exponents | record sums | partials of each matrix]
@@ -2357,7 +2382,7 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
     for (uint32_t i = 0; i < count; ++i) {
         // epilogue in the split sum: split launches, and the SiLU pair (an
         // unsplit launch adds its bias / residual in its own stores)
-        ep[i] = (silu_pair || res || (bias && bias[i])) && (silu_pair || pl[i].splits > 1);
+        ep[i] = rope || ((silu_pair || res || (bias && bias[i])) && (silu_pair || pl[i].splits > 1));
         poff[i] = total;
         // a matrix with an epilogue leaves its partial sums (one "split"
         // when unsplit) for k_gemm_split_sum_ep
@@ -2377,7 +2402,7 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
     // pair: one launch for all of them (k_gemm_split_sum_ep3)
     EpSegs es{};
     es.crow = crow;
-    const bool one_sum = !silu_pair && !res && c->gemm_set_sum1 && count <= 3;
+    const bool one_sum = !silu_pair && !res && (c->gemm_set_sum1 || rope) && count <= 3;
     for (uint32_t i = 0; i < count; ++i) {
         float* part = (float*)(ws + poff[i]);
         // unsplit with an epilogue: the GEMM writes its rows into the partials
@@ -2405,9 +2430,10 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
         st = gemm_split_sum_ep(c, g.part, nullptr, g.y, m_rows, g.n, g.splits, crow, g.bias, nullptr);
     } else if (es.count > 1) {
         const EpSeg& g = es.s[es.count - 1];
-        void* pp[] = {&es};
-        st = launch(c, "k_gemm_split_sum_ep3", dim3(g.blk0 + (g.n + 1023) / 1024, m_rows), dim3(256),
-                    0, pp);
+        RopeKv rk = rope ? *rope : RopeKv{};
+        void* pp[] = {&es, &rk};
+        st = launch(c, rope ? "k_gemm_split_sum_qkv_rope" : "k_gemm_split_sum_ep3",
+                    dim3(g.blk0 + (g.n + 1023) / 1024, m_rows), dim3(256), 0, pp);
     }
     if (st != RT_OK) return st;
     if (!silu_pair) return RT_OK;
@@ -2420,6 +2446,36 @@ int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const vo
         st = gemm_split_sum_ep(c, pg, nullptr, y[0], m_rows, n[0], pl[0].splits, crow, nullptr, nullptr);
     if (st != RT_OK) return st;
     return rt_silu_mul_f32(c, y[0], y[1], y[0], m_rows * n[0]);
+}
+
+int rt_gemm_set_f32(rt_ctx* c, uint32_t count, const char* const* fmts, const void* const* w,
+                    float* const* y, const uint32_t* n, const uint16_t* const* bias,
+                    const float* res, const float* x, uint32_t m_rows, uint32_t k,
+                    const float* gamma, float eps, float* xn, uint32_t silu_pair) {
+    return gemm_set_impl(c, count, fmts, w, y, n, bias, res, x, m_rows, k, gamma, eps, xn,
+                         silu_pair, nullptr);
+}
+
+int rt_gemm_qkv_rope_f32(rt_ctx* c, const char* fmt_q, const void* w_q, const char* fmt_k,
+                         const void* w_k, const char* fmt_v, const void* w_v, const uint16_t* b_q,
+                         const uint16_t* b_k, const uint16_t* b_v, const float* x,
+                         const float* gamma, float eps, float* xn, float* q, float* k, float* v,
+                         float* k_cache, float* v_cache, uint32_t m_rows, uint32_t hidden,
+                         uint32_t q_dim, uint32_t kv_dim, uint32_t head_dim, uint32_t start_pos,
+                         float theta, uint32_t max_seq) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (m_rows == 0) return RT_OK;
+    if (!k_cache || !v_cache || (uint64_t)start_pos + m_rows > max_seq)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: gemm_qkv_rope: null cache, or "
+                    "start_pos=%u + %u rows > max_seq=%u", start_pos, m_rows, max_seq);
+    const char* fm[] = {fmt_q, fmt_k, fmt_v};
+    const void* wv[] = {w_q, w_k, w_v};
+    float* yv[] = {q, k, v};
+    const uint32_t nv[] = {q_dim, kv_dim, kv_dim};
+    const uint16_t* bv[] = {b_q, b_k, b_v};
+    const RopeKv rk{k_cache, v_cache, head_dim, start_pos, max_seq, theta};
+    return gemm_set_impl(c, 3, fm, wv, yv, nv, bv, nullptr, x, m_rows, hidden, gamma, eps, xn, 0,
+                         &rk);
 }
 
 // Mirrors the device-side PrepSum (k_gemm.hip).

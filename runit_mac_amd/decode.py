@@ -629,13 +629,12 @@ class DecodeModel:
                                           c.kv_heads, start_pos, c.theta, M, c.max_seq)
             else:
                 # Q/K/V (+ bias) of the normalised rows: one preparation of
-                # RMSNorm(X)·γ for the three GEMMs, the biases in their sums
-                d.gemm_set_f32(ctx, [F["q"], F["k"], F["v"]], [L["wq"], L["wk"], L["wv"]],
-                               [B["q"], B["k"], B["v"]], [qd, kvd, kvd], X, M, h,
-                               biases=[L["bq"], L["bk"], L["bv"]], gamma=L["attn_norm"], eps=c.eps,
-                               xn=XN)
-                d.rope_kv_write_batch_f32(ctx, B["q"], B["k"], B["v"], L["kc"], L["vc"], hd, c.heads,
-                                          c.kv_heads, start_pos, c.theta, M, c.max_seq)
+                # RMSNorm(X)·γ for the three GEMMs; the biases, RoPE and the
+                # cache writes in their sums
+                d.gemm_qkv_rope_f32(ctx, (F["q"], F["k"], F["v"]), L["wq"], L["wk"], L["wv"],
+                                    L["bq"], L["bk"], L["bv"], X, L["attn_norm"], c.eps, XN,
+                                    B["q"], B["k"], B["v"], L["kc"], L["vc"], M, h, qd, kvd, hd,
+                                    start_pos, c.theta, c.max_seq)
             d.flash_attention_f32(ctx, B["q"], L["kc"], L["vc"], B["att"], 1, M, start_pos + M,
                                   c.heads, c.kv_heads, hd, c.max_seq, q_start=start_pos)
             if form == "rows":

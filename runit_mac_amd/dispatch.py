@@ -67,6 +67,8 @@ _ROWS_FMTS = ("q8_0", "q4_0", "q4k", "q6k", "q5_0", "q5k", "q4_0g", "q4kg", "q5k
 _SIGS = {
     "rt_ctx_create": [POINTER(c_void_p), c_char_p],
     "rt_gemm_set_f32": [_P, _U32, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _P, _F, _P, _U32],
+    "rt_gemm_qkv_rope_f32": [_P, c_char_p, _P, c_char_p, _P, c_char_p, _P, _P, _P, _P, _P, _P, _F,
+                             _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F, _U32],
     "rt_gemm_ffn_block_f32": [_P, c_char_p, _P, c_char_p, _P, c_char_p, _P, c_char_p, _P, _P, _P,
                               _P, _P, _F, _P, _P, _P, _U32, _U32, _U32, _U32],
     "rt_flush": [_P],
@@ -623,6 +625,19 @@ def gemm_set_f32(ctx, fmts, weights, ys, ns, x, m_rows, k, biases=None, res=None
           adr(bv) if bv is not None else None, _ptr(res) if res is not None else None,
           _ptr(x), m_rows, k, _ptr(gamma) if gamma is not None else None, eps,
           _ptr(xn) if xn is not None else None, int(bool(silu_pair)))
+
+
+def gemm_qkv_rope_f32(ctx, fmts, w_q, w_k, w_v, b_q, b_k, b_v, x, gamma, eps, xn, q, k, v,
+                      k_cache, v_cache, m_rows, hidden, q_dim, kv_dim, head_dim, start_pos, theta,
+                      max_seq):
+    """verify_draft's Q/K/V of RMSNorm(x)·γ + biases, RoPE of q and k at
+    start_pos + r, k / v into the caches, in one call (new;
+    forward.rs:2186-2231).  fmts: the formats of (q, k, v)."""
+    fq, fk, fv = (f.encode() for f in fmts)
+    _call(ctx, "rt_gemm_qkv_rope_f32", fq, _ptr(w_q), fk, _ptr(w_k), fv, _ptr(w_v), _ptr(b_q),
+          _ptr(b_k), _ptr(b_v), _ptr(x), _ptr(gamma), eps, _ptr(xn), _ptr(q), _ptr(k), _ptr(v),
+          _ptr(k_cache), _ptr(v_cache), m_rows, hidden, q_dim, kv_dim, head_dim, start_pos, theta,
+          max_seq)
 
 
 def gemm_ffn_block_f32(ctx, fmts, w_o, w_gate, w_up, w_down, att, x, x_mid, gamma, eps, g, u, xn,

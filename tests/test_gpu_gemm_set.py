@@ -132,3 +132,45 @@ def test_gemm_ffn_block_equals_the_three_sets(ctx, fmts, m):
     assert np.array_equal(outs[0][0], outs[1][0]), "x_mid"
     assert np.array_equal(outs[0][1], outs[1][1]), "x"
     assert np.all(np.isfinite(outs[0][1]))
+
+
+@pytest.mark.parametrize("fmts,hd,heads,kvh", [(("q4k", "q4k", "q6k"), 128, 8, 2),
+                                               (("q8_0", "q8_0", "q8_0"), 64, 14, 2)])
+@pytest.mark.parametrize("m", [1, 4, 8, 27, 32])
+def test_gemm_qkv_rope_equals_set_then_rope(ctx, fmts, hd, heads, kvh, m):
+    """rt_gemm_qkv_rope_f32 against the Q/K/V set followed by
+    rt_rope_kv_write_batch_f32 (each pinned to the oracle elsewhere): the
+    same sums and angles; the rotation's r·c − i·s may contract to a fused
+    multiply-add differently in the two kernels, so the rotated q and keys
+    agree to 2e-6 of their range and the values exactly; the cache outside
+    rows start_pos .. start_pos + m stays untouched."""
+    h, qd, kvd, S, start = 1024, heads * hd, kvh * hd, 64, 20
+    W = [device_weights(ctx, f, n, h, 350 + i) for i, (f, n) in enumerate(zip(fmts, (qd, kvd, kvd)))]
+    rng = np.random.default_rng(90 + m)
+    x = ctx.buffer_from(_x(m, h, 91 + m))
+    gamma = ctx.buffer_from((1 + 0.1 * rng.standard_normal(h)).astype(np.float32))
+    biases = [ctx.buffer_from((0.1 * rng.standard_normal(n)).astype(np.float16).view(np.uint16))
+              for n in (qd, kvd, kvd)]
+    cache0 = rng.standard_normal(kvh * S * hd).astype(np.float32)
+    outs = []
+    for fused in (True, False):
+        q, k, v = (ctx.new_buffer(4 * m * n) for n in (qd, kvd, kvd))
+        xn = ctx.new_buffer(4 * m * h)
+        kc, vc = ctx.buffer_from(cache0), ctx.buffer_from(cache0)
+        if fused:
+            d.gemm_qkv_rope_f32(ctx, fmts, W[0][0], W[1][0], W[2][0], *biases, x, gamma, EPS, xn,
+                                q, k, v, kc, vc, m, h, qd, kvd, hd, start, 10000.0, S)
+        else:
+            d.gemm_set_f32(ctx, list(fmts), [w for w, _ in W], [q, k, v], [qd, kvd, kvd], x, m, h,
+                           biases=biases, gamma=gamma, eps=EPS, xn=xn)
+            d.rope_kv_write_batch_f32(ctx, q, k, v, kc, vc, hd, heads, kvh, start, 10000.0, m, S)
+        ctx.flush()
+        outs.append([b.read(np.float32, n) for b, n in ((q, m * qd), (kc, cache0.size),
+                                                        (vc, cache0.size))])
+    for a, b, what in zip(outs[0][:2], outs[1][:2], ("q", "k cache")):
+        assert np.max(np.abs(a - b)) <= 2e-6 * np.abs(b).max(), what
+    assert np.array_equal(outs[0][2], outs[1][2]), "v cache"
+    kc = outs[0][1].reshape(kvh, S, hd)
+    keep = np.ones(S, bool)
+    keep[start:start + m] = False
+    assert np.array_equal(kc[:, keep], cache0.reshape(kvh, S, hd)[:, keep]), "rows outside"
