@@ -95,8 +95,10 @@ def test_argmax_rows_first(ctx):
     (128, 28, 4, 5, 300, 0),      # the reference kernel's mask (q_start 0) with history
     (128, 28, 4, 16, 1040, 1024),
     (128, 28, 4, 200, 200, 0),    # prefill-length: many column groups, a few waves each
-    (256, 8, 2, 6, 40, 34),       # head size 256
+    (256, 8, 2, 6, 40, 34),       # head size 256 (4 column groups: the per-row kernel)
+    (256, 8, 2, 40, 80, 40),      # head size 256 on the matrix cores
     (64, 12, 4, 7, 23, 16),       # 3 heads per KV head: column groups straddle rows
+    (64, 12, 4, 11, 40, 29),      # the same on the matrix cores (12 column groups)
     (128, 28, 4, 1, 1, 0),        # one row, one position
 ])
 def test_flash_attention_causal_matches_oracle(ctx, hd, H, KVH, M, kv_len, q_start):
