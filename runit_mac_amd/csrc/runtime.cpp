@@ -2339,11 +2339,19 @@ static int gemm_set_impl(rt_ctx* c, uint32_t count, const char* const* fmts, con
     // The shared form: every matrix on the f16 form with one row grouping,
     // one preparation (norm-fused when gamma), epilogues in the split sums.
     Gemm3Plan pl[4];
+    // (the shared form's kernels move x, γ, the normalised rows, the
+    // residual and the rotated / cached rows in 16-byte, biases in 8-byte units)
     bool shared = c->gemm_set && c->gemm_f16 && m_rows >= 2 && m_rows > c->gemm_set_min &&
-                  k <= 20480 && aligned(x, 16) &&
-                  (!rope || (1024 % rope->head_dim == 0 && rope->head_dim <= 512 && n[0] % 4 == 0 && n[1] % 4 == 0 &&
+                  k <= 20480 && aligned(x, 16) && (!gamma || (aligned(gamma, 16) && aligned(xn, 16))) &&
+                  (!res || aligned(res, 16)) &&
+                  (!rope || (aligned(y[0], 16) && aligned(rope->kc, 16) && aligned(rope->vc, 16))) &&
+                  (!rope || (1024 % rope->head_dim == 0 && rope->head_dim % 4 == 0 && rope->head_dim <= 512 && n[0] % 4 == 0 && n[1] % 4 == 0 &&
                              c->gemm_rope));
     for (uint32_t i = 0; shared && i < count; ++i) {
+        if (bias && bias[i] && !aligned(bias[i], 8)) {
+            shared = false;
+            break;
+        }
         const int st = gemm3_plan(c, *f[i], w[i], m_rows, n[i], k, pl[i]);
         if (st != RT_OK && st != kLsDecline) return st;
         shared = st == RT_OK && pl[i].MG == pl[0].MG;
@@ -2527,6 +2535,7 @@ int rt_gemm_ffn_block_f32(rt_ctx* c, const char* fmt_o, const void* w_o, const c
     };
     if (!fo || !fg || !fu || !fd || !c->gemm_set || !c->gemm_block || !c->gemm_f16 || m_rows < 2 ||
         m_rows <= c->gemm_set_min || qd > 20480 || h > 20480 || ff > 20480 || !aligned(att, 16) ||
+        !aligned(x, 16) || !aligned(x_mid, 16) || !aligned(gamma, 16) ||
         qd % fo->blk_el || h % fg->blk_el || h % fu->blk_el || ff % fd->blk_el)
         return sets();
     Gemm3Plan po, pg, pu, pd;

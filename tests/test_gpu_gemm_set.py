@@ -174,3 +174,23 @@ def test_gemm_qkv_rope_equals_set_then_rope(ctx, fmts, hd, heads, kvh, m):
     keep = np.ones(S, bool)
     keep[start:start + m] = False
     assert np.array_equal(kc[:, keep], cache0.reshape(kvh, S, hd)[:, keep]), "rows outside"
+
+
+def test_gemm_set_unaligned_operands_take_the_separate_launches(ctx):
+    """A γ that is not 16-byte aligned (the shared form loads it in 16-byte
+    units) makes the set run as the separate launches; the result matches
+    the aligned call to rounding."""
+    m, h, n = 8, 1024, 512
+    w, _ = device_weights(ctx, "q4k", n, h, 360)
+    x = ctx.buffer_from(_x(m, h, 361))
+    gamma = np.linspace(0.5, 1.5, h, dtype=np.float32)
+    ga = ctx.buffer_from(gamma)
+    gu = ctx.new_buffer(4 * (h + 1))
+    gu.write(gamma, offset=4)
+    outs = []
+    for gptr in (ga, gu.ptr + 4):
+        y, xn = ctx.new_buffer(4 * m * n), ctx.new_buffer(4 * m * h)
+        d.gemm_set_f32(ctx, ["q4k"], [w], [y], [n], x, m, h, gamma=gptr, eps=EPS, xn=xn)
+        ctx.flush()
+        outs.append(y.read(np.float32, m * n))
+    assert np.max(np.abs(outs[0] - outs[1])) <= 1e-5 * np.abs(outs[1]).max()
