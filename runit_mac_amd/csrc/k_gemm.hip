@@ -950,8 +950,10 @@ RT_GEMM_XH_PREP(4)
 // the Q6_K form at 32 rows, whose two buffers would not fit the LDS.
 // WBUF = 1: the weights in one LDS buffer as well (the same barrier ends
 // the stage's reads of both) — the Q6_K 128-row tiles at 32 rows.
+// bid / nbk: the workgroup's index and the number of workgroups working on
+// this GEMM (the whole grid, or its range of a multi-matrix launch).
 template <class P, int MG, int NB, int WAVES = 4, int ABUF = 2, int WBUF = 2>
-RT_DEV void gemm3_body(const Gemm2Args& a) {
+RT_DEV void gemm3_body(const Gemm2Args& a, uint32_t bid = blockIdx.x, uint32_t nbk = gridDim.x) {
     static_assert(WBUF == 2 || ABUF == 1, "one weight buffer needs the operand barrier");
     constexpr uint32_t T = 64 * WAVES, ROWS = 16 * WAVES;
     constexpr uint32_t NR = NB * P::RECS;
@@ -977,7 +979,7 @@ RT_DEV void gemm3_body(const Gemm2Args& a) {
     const uint32_t j = lane & 15, c = lane >> 4;
     const uint32_t nitems = a.tiles * a.splits * a.nchunks;
 
-    for (uint32_t item = blockIdx.x; item < nitems; item += gridDim.x) {
+    for (uint32_t item = bid; item < nitems; item += nbk) {
         const uint32_t tile = item % a.tiles;
         const uint32_t split = (item / a.tiles) % a.splits;
         const uint32_t ch = item / (a.tiles * a.splits);
@@ -1322,15 +1324,30 @@ extern "C" __global__ void __launch_bounds__(256) k_gemm_split_sum_qkv_rope(EpSe
     else
         *(f32x4*)(rk.kc + ((size_t)h * rk.max_seq + pos) * hd + d0) = ov;
 }
+// Up to three GEMMs of one kernel shape over the same prepared activations
+// in one launch: workgroups [g0[i], g0[i + 1]) run matrix i.
+struct Gemm3Multi {
+    Gemm2Args a[3];
+    uint32_t g0[4];
+    uint32_t count;
+};
+#define RT_GEMM3_MULTI(NAME, THREADS, ...)                                                    \
+    extern "C" __global__ void __launch_bounds__(THREADS) NAME##_x3(Gemm3Multi m) {          \
+        uint32_t i = 0;                                                                        \
+        while (i + 1 < m.count && blockIdx.x >= m.g0[i + 1]) ++i;                             \
+        gemm3_body<__VA_ARGS__>(m.a[i], blockIdx.x - m.g0[i], m.g0[i + 1] - m.g0[i]);         \
+    }
 #define RT_GEMM3_KERNEL4(FN, P, MG, NB)                                                       \
     extern "C" __global__ void __launch_bounds__(256) k_gemm3_##FN##_mg##MG(Gemm2Args a) {    \
         gemm3_body<P, MG, NB>(a);                                                              \
-    }
+    }                                                                                          \
+    RT_GEMM3_MULTI(k_gemm3_##FN##_mg##MG, 256, P, MG, NB)
 #define RT_GEMM3_KERNEL(FN, P, MG, NB)                                                        \
     RT_GEMM3_KERNEL4(FN, P, MG, NB)                                                            \
     extern "C" __global__ void __launch_bounds__(512) k_gemm3_##FN##_mg##MG##_w8(Gemm2Args a) { \
         gemm3_body<P, MG, NB, 8>(a);                                                           \
-    }
+    }                                                                                          \
+    RT_GEMM3_MULTI(k_gemm3_##FN##_mg##MG##_w8, 512, P, MG, NB, 8)
 // (a group here is 8 activation rows: MG = 1, 2, 4 cover 8, 16, 32 rows with
 // the stage sizes of gemm2's 4-row groups MG = 2, 4, 8)
 RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 1, 8)
@@ -1340,12 +1357,14 @@ RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 4, 4)
 extern "C" __global__ void __launch_bounds__(1024) k_gemm3_q8_0_mg4_w16(Gemm2Args a) {
     gemm3_body<GemmQ8_0, 4, 4, 16>(a);
 }
+RT_GEMM3_MULTI(k_gemm3_q8_0_mg4_w16, 1024, GemmQ8_0, 4, 4, 16)
 // and for the super-block formats at 32 rows (Q4_K 18944×3584 40.7 → 33.2 µs,
 // Q5_K 42.2 → 35.8; Q4_0 unchanged, Q5_0 32.3 → 33.5, so they keep 128 rows)
 #define RT_GEMM3_W16(FN, P, NB)                                                               \
     extern "C" __global__ void __launch_bounds__(1024) k_gemm3_##FN##_mg4_w16(Gemm2Args a) {  \
         gemm3_body<P, 4, NB, 16>(a);                                                           \
-    }
+    }                                                                                          \
+    RT_GEMM3_MULTI(k_gemm3_##FN##_mg4_w16, 1024, P, 4, NB, 16)
 RT_GEMM3_W16(q4k, GemmQ4K, 1)
 RT_GEMM3_W16(q4kg, GemmQ4KG, 1)
 RT_GEMM3_W16(q5k, GemmQ5K, 1)

@@ -296,6 +296,7 @@ struct rt_ctx {
     uint32_t ls_min_items = 16;  // RUNIT_GEMV_LS_MIN: items per CU from which the LDS body runs
     bool gemm_set = true;  // RUNIT_GEMM_SET=0: rt_gemm_set_f32 as separate launches (A/B)
     uint32_t gemm_set_min = 1;  // RUNIT_GEMM_SET_MIN: rows above which a set takes the shared f16 form
+    bool gemm_multi = true;     // RUNIT_GEMM_MULTI=0: a set's GEMMs one launch each (A/B)
     bool gemm_set_sum1 = true;  // RUNIT_GEMM_SET_SUM1=0: a set's split sums one launch per matrix (A/B)
     bool gemm_block = true;     // RUNIT_GEMM_BLOCK=0: rt_gemm_ffn_block_f32 as three sets (A/B)
     bool gemm_rope = true;      // RUNIT_GEMM_ROPE=0: rt_gemm_qkv_rope_f32 with a separate RoPE launch (A/B)
@@ -1329,6 +1330,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_SUM_KERNEL")) c->gemm_sum_kernel = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_SET")) c->gemm_set = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_SET_MIN")) c->gemm_set_min = atoi(g);
+    if (const char* g = getenv("RUNIT_GEMM_MULTI")) c->gemm_multi = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_SET_SUM1")) c->gemm_set_sum1 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_BLOCK")) c->gemm_block = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_ROPE")) c->gemm_rope = atoi(g) != 0;
@@ -1401,6 +1403,16 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
         }
         c->fns[n] = f;
     }
+    // the multi-matrix twins of the f16 GEMM kernels (where built)
+    for (const std::string& ns : names) {
+        if (ns.compare(0, 8, "k_gemm3_") != 0) continue;
+        const std::string x3 = ns + "_x3";
+        hipFunction_t f = nullptr;
+        for (hipModule_t m : c->modules)
+            if (hipModuleGetFunction(&f, m, x3.c_str()) == hipSuccess && f) break;
+        if (f) c->fns[x3] = f;
+    }
+    (void)hipGetLastError();  // the lookups of absent twins
     e = hipMalloc(&c->aux, kAuxBytes);
     if (e == hipSuccess) e = hipMemset(c->aux, 0, kAuxBytes);
     if (e != hipSuccess) {
@@ -2062,6 +2074,84 @@ static int gemm3_run(rt_ctx* c, const Gemm3Plan& p, const void* w, void* aops, i
     return gemm_split_sum(c, part, y, m_rows, n, p.splits, 8 * p.MG);
 }
 
+// Mirrors the device-side Gemm3Multi (k_gemm.hip).
+struct Gemm3Multi {
+    Gemm2Args a[3];
+    uint32_t g0[4];
+    uint32_t count;
+};
+
+// One GEMM of a multi-matrix launch (gemm3_many): its plan, weights, output,
+// partial sums and the store epilogue of an unsplit launch.
+struct Gemm3Job {
+    const Gemm3Plan* p;
+    const void* w;
+    float* stab;
+    float* y;
+    float* part;
+    uint32_t n;
+    bool leave_parts;
+    const uint16_t* bias;
+    const float* res;
+};
+
+// The GEMMs of `jobs` over the same prepared operands: those that share a
+// kernel run in one launch of its _x3 twin (up to three), each on its own
+// range of workgroups; then the K-split sums the jobs do not leave.
+static int gemm3_many(rt_ctx* c, const Gemm3Job* jobs, uint32_t count, void* aops, int* erow,
+                      uint32_t m_rows) {
+    bool done[4] = {false, false, false, false};
+    int st = RT_OK;
+    for (uint32_t i = 0; i < count && st == RT_OK; ++i) {
+        if (done[i]) continue;
+        // group the jobs of one kernel that each take at most two rounds of
+        // resident workgroups (at the 7B prefill's 512 rows gate and up take
+        // five each, and one launch of both took 36.8 against 36.4 ms; a
+        // grouping that fits one round in all left out gate + up at 8 rows:
+        // 7B verify 3.55 against 3.75 ms)
+        auto short_job = [&](const Gemm3Job& b) {
+            return (uint64_t)b.p->base * b.p->splits <= 2ull * b.p->cap;
+        };
+        uint32_t grp[3] = {i, 0, 0}, ng = 1;
+        for (uint32_t j = i + 1; j < count && ng < 3 && c->gemm_multi && short_job(jobs[i]); ++j)
+            if (!done[j] && strcmp(jobs[j].p->kn, jobs[i].p->kn) == 0 && short_job(jobs[j]))
+                grp[ng++] = j;
+        char x3[56];
+        snprintf(x3, sizeof x3, "%s_x3", jobs[i].p->kn);
+        if (ng == 1 || !c->fns.count(x3)) {
+            const Gemm3Job& b = jobs[i];
+            st = gemm3_run(c, *b.p, b.w, aops, erow, b.stab, b.y, b.part, m_rows, b.n, b.leave_parts,
+                           b.bias, b.res);
+            done[i] = true;
+            continue;
+        }
+        Gemm3Multi mm{};
+        uint32_t g = 0;
+        for (uint32_t q = 0; q < ng; ++q) {
+            const Gemm3Job& b = jobs[grp[q]];
+            const Gemm3Plan& p = *b.p;
+            uint32_t cstride = 32;
+            while (cstride > 1 && (size_t)p.base * cstride > kAttnCounters) cstride >>= 1;
+            mm.a[q] = Gemm2Args{b.w, aops, erow, b.stab, b.y, b.part, nullptr, m_rows, b.n, p.nblk,
+                                p.tiles, p.splits, p.kbs, p.nchunks, p.row_bytes, cstride,
+                                p.splits == 1 ? b.bias : nullptr, p.splits == 1 ? b.res : nullptr};
+            mm.g0[q] = g;
+            g += std::min(p.base * p.splits, p.cap);
+            done[grp[q]] = true;
+        }
+        mm.g0[ng] = g;
+        mm.count = ng;
+        void* pp[] = {&mm};
+        st = launch(c, x3, dim3(g), dim3(64 * jobs[i].p->waves), 0, pp);
+        for (uint32_t q = 0; q < ng && st == RT_OK; ++q) {
+            const Gemm3Job& b = jobs[grp[q]];
+            if (b.p->splits > 1 && !b.leave_parts)
+                st = gemm_split_sum(c, b.part, b.y, m_rows, b.n, b.p->splits, 8 * b.p->MG);
+        }
+    }
+    return st;
+}
+
 // f16 matrix-core form of the staged GEMM for one weight matrix: plan,
 // workspace, preparation, GEMM.
 int gemm3_launch(rt_ctx* c, const GemmFmt& f, const void* w, const float* x, float* y,
@@ -2411,13 +2501,18 @@ static int gemm_set_impl(rt_ctx* c, uint32_t count, const char* const* fmts, con
     EpSegs es{};
     es.crow = crow;
     const bool one_sum = !silu_pair && !res && (c->gemm_set_sum1 || rope) && count <= 3;
+    Gemm3Job jobs[4];
     for (uint32_t i = 0; i < count; ++i) {
         float* part = (float*)(ws + poff[i]);
         // unsplit with an epilogue: the GEMM writes its rows into the partials
-        float* yi = ep[i] && pl[i].splits == 1 ? part : y[i];
-        st = gemm3_run(c, pl[i], w[i], aops, erow, f[i]->has_min ? stab : nullptr, yi, part, m_rows,
-                       n[i], ep[i], ep[i] || !bias ? nullptr : bias[i], ep[i] ? nullptr : res);
-        if (st != RT_OK) return st;
+        jobs[i] = Gemm3Job{&pl[i], w[i], f[i]->has_min ? stab : nullptr,
+                           ep[i] && pl[i].splits == 1 ? part : y[i], part, n[i], ep[i],
+                           ep[i] || !bias ? nullptr : bias[i], ep[i] ? nullptr : res};
+    }
+    st = gemm3_many(c, jobs, count, aops, erow, m_rows);
+    if (st != RT_OK) return st;
+    for (uint32_t i = 0; i < count; ++i) {
+        float* part = (float*)(ws + poff[i]);
         if (ep[i] && one_sum) {
             EpSeg& g = es.s[es.count];
             g.blk0 = es.count ? es.s[es.count - 1].blk0 + (es.s[es.count - 1].n + 1023) / 1024 : 0;
@@ -2593,13 +2688,14 @@ int rt_gemm_ffn_block_f32(rt_ctx* c, const char* fmt_o, const void* w_o, const c
         void* pp[] = {&ps, &M, &K, &aops, &erow, &stab, (void*)&gamma, &eps};
         st = launch(c, pk, dim3(nch * 8 * MG), dim3(1024), 0, pp);
     }
-    // gate and up, their partials left; silu(Σ gate)·Σ up prepared for down
-    if (st == RT_OK)
-        st = gemm3_run(c, pg, w_gate, at(3), (int*)at(4), fg->has_min ? (float*)at(5) : nullptr,
-                       part_g, part_g, m_rows, ff, true);
-    if (st == RT_OK)
-        st = gemm3_run(c, pu, w_up, at(3), (int*)at(4), fu->has_min ? (float*)at(5) : nullptr,
-                       part_u, part_u, m_rows, ff, true);
+    // gate and up (one launch where they share a kernel), their partials
+    // left; silu(Σ gate)·Σ up prepared for down
+    if (st == RT_OK) {
+        const Gemm3Job gu[2] = {
+            {&pg, w_gate, fg->has_min ? (float*)at(5) : nullptr, part_g, part_g, ff, true, nullptr, nullptr},
+            {&pu, w_up, fu->has_min ? (float*)at(5) : nullptr, part_u, part_u, ff, true, nullptr, nullptr}};
+        st = gemm3_many(c, gu, 2, at(3), (int*)at(4), m_rows);
+    }
     if (st != RT_OK) return st;
     if (m_rows >= c->gemm_block_silu_min) {
         // the SiLU sum in the preparation (one workgroup per row reads the
