@@ -357,7 +357,7 @@ def bench_decode(ctx, steps: int, warmup: int, verify_forms: bool = True) -> dic
     # the batched GEMMs, causal attention over the cache + the M new rows),
     # captured as one graph; the cache is restored between replays
     verify = {}
-    for M, form in ((4, "rows"), (8, "rows"), (16, "rows"), (16, "gemm"), (32, "gemm")) if verify_forms else ():
+    for M, form in ((4, "rows"), (8, "rows"), (16, "rows"), (8, "gemm"), (16, "gemm"), (32, "gemm")) if verify_forms else ():
         m.verify_forward([1] * M, pos, form)  # uploads the ids, sizes the buffers
         ctx.flush()
         ctx.capture_begin()

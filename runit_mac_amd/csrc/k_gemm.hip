@@ -1353,6 +1353,10 @@ struct Gemm3Multi {
 RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 1, 8)
 RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 2, 4)
 RT_GEMM3_KERNEL(q8_0, GemmQ8_0, 4, 4)
+// 8 rows with 4-block stages, for K of a multiple of 4 but not of 8 blocks
+// (the 0.5B hidden size 896: 28 blocks)
+RT_GEMM3_KERNEL4(q8_0_nb4, GemmQ8_0, 1, 4)
+RT_GEMM3_KERNEL4(q4_0_nb4, GemmQ4_0, 1, 4)
 // 256-row tiles (16 waves share each stage of activation operands)
 extern "C" __global__ void __launch_bounds__(1024) k_gemm3_q8_0_mg4_w16(Gemm2Args a) {
     gemm3_body<GemmQ8_0, 4, 4, 16>(a);

@@ -297,6 +297,7 @@ struct rt_ctx {
     bool gemm_set = true;  // RUNIT_GEMM_SET=0: rt_gemm_set_f32 as separate launches (A/B)
     uint32_t gemm_set_min = 1;  // RUNIT_GEMM_SET_MIN: rows above which a set takes the shared f16 form
     bool gemm_multi = true;     // RUNIT_GEMM_MULTI=0: a set's GEMMs one launch each (A/B)
+    bool gemm_nb4 = true;       // RUNIT_GEMM_NB4=0: no 4-block-stage 8-row variant (A/B)
     bool gemm_set_sum1 = true;  // RUNIT_GEMM_SET_SUM1=0: a set's split sums one launch per matrix (A/B)
     bool gemm_block = true;     // RUNIT_GEMM_BLOCK=0: rt_gemm_ffn_block_f32 as three sets (A/B)
     bool gemm_rope = true;      // RUNIT_GEMM_ROPE=0: rt_gemm_qkv_rope_f32 with a separate RoPE launch (A/B)
@@ -1331,6 +1332,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_SET")) c->gemm_set = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_SET_MIN")) c->gemm_set_min = atoi(g);
     if (const char* g = getenv("RUNIT_GEMM_MULTI")) c->gemm_multi = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_NB4")) c->gemm_nb4 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_SET_SUM1")) c->gemm_set_sum1 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_BLOCK")) c->gemm_block = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_ROPE")) c->gemm_rope = atoi(g) != 0;
@@ -1388,6 +1390,8 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
         }
     names.push_back("k_act_limbs_rows_f32");
     names.push_back("k_act_limbs_rows_f32_q40");
+    names.push_back("k_gemm3_q8_0_nb4_mg1");
+    names.push_back("k_gemm3_q4_0_nb4_mg1");
     for (const char* b : kLsValuBases)
         for (uint32_t ni = 1; ni <= kLsMaxNI; ++ni)
             names.push_back(std::string(b) + "_ls" + std::to_string(ni) + "v");
@@ -1941,7 +1945,18 @@ static int gemm3_plan(rt_ctx* c, const GemmFmt& f, const void* w, uint32_t m_row
     const uint32_t nrec = k / 32;
     const uint32_t nblk = k / f.blk_el;
     const uint64_t row_bytes = (uint64_t)nblk * f.blk_bytes;
-    const uint32_t NB = MG <= 1 ? f.nb_small : f.nb_large;
+    uint32_t NB = MG <= 1 ? f.nb_small : f.nb_large;
+    // 8 rows whose blocks do not fill the 8-row stages: the 4-block stage
+    // variant (k_gemm3_<fmt>_nb4_mg1) where there is one
+    bool nb4 = false;
+    if (MG == 1 && nblk % NB != 0 && NB == 8 && nblk % 4 == 0 && c->gemm_nb4) {
+        char kb[48];
+        snprintf(kb, sizeof kb, "k_gemm3_%s_nb4_mg1", f.name);
+        if (c->fns.count(kb)) {
+            NB = 4;
+            nb4 = true;
+        }
+    }
     const uint32_t seg = NB * f.blk_bytes, vb = seg % 16 == 0 ? 16 : (seg % 8 == 0 ? 8 : 4);
     if (nblk % NB != 0 || !aligned(w, 16) || row_bytes % vb != 0 || c->gemm_direct)
         return kLsDecline;
@@ -1951,6 +1966,10 @@ static int gemm3_plan(rt_ctx* c, const GemmFmt& f, const void* w, uint32_t m_row
     uint32_t waves = ((MG >= 2 || q6) && f.blk_bytes != 34 && w8ok ? 8 : 4);
     char kn[48];
     snprintf(kn, sizeof kn, waves == 8 ? "k_gemm3_%s_mg%u_w8" : "k_gemm3_%s_mg%u", f.name, MG);
+    if (nb4) {
+        snprintf(kn, sizeof kn, "k_gemm3_%s_nb4_mg1", f.name);
+        waves = 4;
+    }
     // 256-row tiles (16 waves share each stage of activation operands: a
     // quarter of the operand reads from L2) where they leave ≥ 1/4 of the CUs
     // a tile without a K split: Q8_0 18944×3584 at M = 32 51.0 → 44.6 µs

@@ -592,9 +592,9 @@ class DecodeModel:
     # for gate+up+SiLU, 9.1 µs for O + residual).  Larger models and longer
     # batches take the batched GEMMs, which are faster there (the 7B Q4_K
     # gate+up at 8 rows: 72.8 µs as multi-row GEMVs; the whole 0.5B pass at
-    # 16 rows: 2.20 ms on the GEMMs, 3.01 ms on the multi-row GEMVs, at 8
-    # rows 3.22 against 1.75 ms).
-    VERIFY_ROWS_MAX = 8
+    # 4 / 8 / 16 rows: 1.54 / 1.59 / 1.71 ms on the GEMMs, 1.37 / 1.75 / 3.01
+    # ms on the multi-row GEMVs, even at about 6).
+    VERIFY_ROWS_MAX = 5
     VERIFY_ROWS_MAX_HIDDEN = 1024
 
     def verify_pass(self, M: int, start_pos: int, form: str | None = None,

@@ -71,7 +71,8 @@ def test_gemm_set_silu_pair(ctx, fmt, m):
               f"gemm_set silu {fmt} m={m}")
 
 
-@pytest.mark.parametrize("fmt,n,k", [("q6k", 1024, 2048), ("q4k", 1024, 3072), ("q8_0", 896, 4864)])
+@pytest.mark.parametrize("fmt,n,k", [("q6k", 1024, 2048), ("q4k", 1024, 3072), ("q8_0", 896, 4864),
+                                     ("q8_0", 4864, 896), ("q4_0", 1000, 896)])
 @pytest.mark.parametrize("m", [1, 4, 8, 32])
 def test_gemm_set_residual(ctx, fmt, n, k, m):
     w, raw = device_weights(ctx, fmt, n, k, 320)
