@@ -299,6 +299,7 @@ struct rt_ctx {
     bool gemm_multi = true;     // RUNIT_GEMM_MULTI=0: a set's GEMMs one launch each (A/B)
     bool gemm_nb4 = true;       // RUNIT_GEMM_NB4=0: no 4-block-stage 8-row variant (A/B)
     bool gemm_bigm_split = true;  // RUNIT_GEMM_BIGM_SPLIT=0: 256+ rows split as short launches (A/B)
+    uint32_t gemm_bigm_chunks = 2;  // RUNIT_GEMM_BIGM_CHUNKS: activation chunks from which that holds
     bool gemm_set_sum1 = true;  // RUNIT_GEMM_SET_SUM1=0: a set's split sums one launch per matrix (A/B)
     bool gemm_block = true;     // RUNIT_GEMM_BLOCK=0: rt_gemm_ffn_block_f32 as three sets (A/B)
     bool gemm_rope = true;      // RUNIT_GEMM_ROPE=0: rt_gemm_qkv_rope_f32 with a separate RoPE launch (A/B)
@@ -1335,6 +1336,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_MULTI")) c->gemm_multi = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_NB4")) c->gemm_nb4 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_BIGM_SPLIT")) c->gemm_bigm_split = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_GEMM_BIGM_CHUNKS")) c->gemm_bigm_chunks = std::max(1, atoi(g));
     if (const char* g = getenv("RUNIT_GEMM_SET_SUM1")) c->gemm_set_sum1 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_BLOCK")) c->gemm_block = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_ROPE")) c->gemm_rope = atoi(g) != 0;
@@ -2014,11 +2016,12 @@ static int gemm3_plan(rt_ctx* c, const GemmFmt& f, const void* w, uint32_t m_row
             break;
         }
     }
-    // 8+ activation chunks (256+ rows): the chunks already fill the grid, and
-    // each split adds its partial sums; split only as far as half the
-    // resident grid (7B prefill 38.9 → 37.9 ms, 0.5B 4.49 → 4.20 ms against
-    // the rounds model above, whose splits are for short launches)
-    if (nchunks >= 8 && c->gemm_bigm_split) {
+    // 2+ activation chunks (64+ rows at 32 per chunk): the chunks fill the
+    // grid, and each split adds its partial sums; split only as far as half
+    // the resident grid (against the rounds model above, whose splits are for
+    // short launches: 0.5B prefill 4.49 → 3.81 ms, 128-row pass 2.56 → 2.35
+    // ms; 7B 128 rows 13.80 → 13.00 ms, 256 rows 23.43 → 23.63 ms)
+    if (nchunks >= c->gemm_bigm_chunks && c->gemm_bigm_split) {
         splits = 1;
         while ((uint64_t)base * splits * 2 <= cap && splits < nblk / NB) ++splits;
     }
