@@ -432,6 +432,22 @@ int rt_gemm_ffn_block_f32(rt_ctx* ctx, const char* fmt_o, const void* w_o, const
                           const char* fmt_down, const void* w_down, const float* att, float* x,
                           float* x_mid, const float* gamma, float eps, float* g, float* u,
                           float* xn, uint32_t m_rows, uint32_t h, uint32_t qd, uint32_t ff);
+/* New: the attention of a verify_draft layer (forward.rs:2225-2226,
+ * rt_flash_attention_f32 with batch 1, q_len = m_rows) followed by
+ * rt_gemm_ffn_block_f32 over its output, as one call (qd = num_heads ·
+ * head_dim).  Where the block takes its shared form and the attention its
+ * multi-range matrix-core form, the attention leaves per-range partials and
+ * the O projection's operand preparation merges them, as the attention's own
+ * last workgroup would; att is then left unspecified.  Otherwise att receives
+ * the attention output and the two calls run in turn. */
+int rt_gemm_attn_ffn_block_f32(rt_ctx* ctx, const float* q, const float* k_cache,
+                               const float* v_cache, uint32_t kv_len, uint32_t num_heads,
+                               uint32_t num_kv_heads, uint32_t head_dim, uint32_t kv_head_stride,
+                               uint32_t q_start, float* att, const char* fmt_o, const void* w_o,
+                               const char* fmt_gate, const void* w_gate, const char* fmt_up,
+                               const void* w_up, const char* fmt_down, const void* w_down, float* x,
+                               float* x_mid, const float* gamma, float eps, float* g, float* u,
+                               float* xn, uint32_t m_rows, uint32_t h, uint32_t ff);
 
 /* ──────────────── multi-row GEMVs (batched verify / prefill) ────────────────
  * New: the M-row projections of verify_draft (forward.rs:2186-2271, which

@@ -463,7 +463,8 @@ RT_DEV void attn_mq(const AttnArgs& a) {
             }
         }
     }
-    if (nsp == 1) return;
+    // parts only: the consumer merges (k_gemm_xh_prep1a_mg*)
+    if (nsp == 1 || a.parts_only) return;
     dev_stores_done();
     __syncthreads();
     uint32_t* counter = a.counters + pair;

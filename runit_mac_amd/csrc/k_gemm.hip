@@ -19,6 +19,7 @@
 // operand order ([chunk][block][group][lane] 8-byte entries, one coalesced
 // dwordx2 per lane) plus the block exponents ([chunk][block][mm][group]).
 #include "rt_formats.h"
+#include "rt_shared.h"
 
 typedef long i64_t;
 
@@ -795,12 +796,22 @@ struct PrepSum {
     uint32_t splits, crow;
 };
 
-template <int MG, bool NORM = false, bool SUM = false>
+// The row of a preparation given as the split partials of the multi-query
+// attention (k_attn_mq_f32_hd*, parts-only, one sequence): element (head h,
+// d) of row r is column qi = r·G + h mod G of KV head h / G, merged over the
+// nsp key ranges as that kernel's last workgroup merges them.
+struct PrepAttn {
+    const float* part;
+    const float* ml;
+    uint32_t nsp, G, hd, cgs;
+};
+
+template <int MG, bool NORM = false, bool SUM = false, bool ATT = false>
 RT_DEV void gemm_xh_prep1_body(const float* __restrict__ x, uint32_t M, uint32_t K,
                                uint2* __restrict__ aops, int* __restrict__ etab,
                                float* __restrict__ stab, const float* __restrict__ gamma = nullptr,
                                float eps = 0.0f, float* __restrict__ xn = nullptr,
-                               const PrepSum* ps = nullptr) {
+                               const PrepSum* ps = nullptr, const PrepAttn* pa = nullptr) {
     constexpr uint32_t ROWS = 8 * MG, T = 1024, NPT = 5;
     __shared__ float red[16];
     const uint32_t nrec = K / 32, nf = K / 4;
@@ -809,7 +820,43 @@ RT_DEV void gemm_xh_prep1_body(const float* __restrict__ x, uint32_t M, uint32_t
     const uint32_t tid = threadIdx.x;
     f32x4 v[NPT];
     float mx = 0.0f;
-    if constexpr (SUM) {
+    if constexpr (ATT) {
+        const float NEG = -__builtin_huge_valf();
+#pragma unroll
+        for (uint32_t i = 0; i < NPT; ++i) {
+            const uint32_t f = tid + T * i;
+            f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (m < M && f < nf) {
+                const uint32_t h = 4 * f / pa->hd, d = 4 * f % pa->hd, kvh = h / pa->G;
+                const uint32_t qi = m * pa->G + h % pa->G, cg = qi / 16, col = qi % 16;
+                const size_t pair = (size_t)kvh * pa->cgs + cg;
+                const float* mlv = pa->ml + (pair * pa->nsp * 16 + col) * 2;
+                // every range's (max, sum) and partial issued before the
+                // first is used (ranges past nsp read range 0, weight 0)
+                float mj[RT_ATTN_MQ_NSP_MAX], lj[RT_ATTN_MQ_NSP_MAX];
+                f32x4 pj[RT_ATTN_MQ_NSP_MAX];
+#pragma unroll
+                for (uint32_t j = 0; j < RT_ATTN_MQ_NSP_MAX; ++j) {
+                    const uint32_t jj = j < pa->nsp ? j : 0;
+                    mj[j] = mlv[32 * jj];
+                    lj[j] = mlv[32 * jj + 1];
+                    pj[j] = *(const f32x4*)(pa->part + ((pair * pa->nsp + jj) * 16 + col) * pa->hd + d);
+                }
+                float Mx = NEG;
+#pragma unroll
+                for (uint32_t j = 0; j < RT_ATTN_MQ_NSP_MAX; ++j) Mx = fmaxf(Mx, mj[j]);
+                float L = 0.0f;
+#pragma unroll
+                for (uint32_t j = 0; j < RT_ATTN_MQ_NSP_MAX; ++j) {
+                    const float w = (j >= pa->nsp || mj[j] == NEG) ? 0.0f : expf(mj[j] - Mx);
+                    L += w * lj[j];
+                    o += w * pj[j];
+                }
+                o = o / L;
+            }
+            v[i] = o;
+        }
+    } else if constexpr (SUM) {
         const uint32_t mc = m < M ? m : 0, sch = mc / ps->crow, sr = mc % ps->crow;
         const size_t off = ((size_t)sch * ps->splits * ps->crow + sr) * K, ss = (size_t)ps->crow * K;
 #pragma unroll
@@ -941,6 +988,16 @@ RT_GEMM_XH_PREP1N(4)
 RT_GEMM_XH_PREP1S(1)
 RT_GEMM_XH_PREP1S(2)
 RT_GEMM_XH_PREP1S(4)
+// the preparation of rows given as multi-query attention partials (PrepAttn)
+#define RT_GEMM_XH_PREP1A(MG)                                                                  \
+    extern "C" __global__ void __launch_bounds__(1024) k_gemm_xh_prep1a_mg##MG(                \
+        PrepAttn pa, uint32_t M, uint32_t K, uint2* aops, int* etab, float* stab) {            \
+        gemm_xh_prep1_body<MG, false, false, true>(nullptr, M, K, aops, etab, stab, nullptr,   \
+                                                   0.0f, nullptr, nullptr, &pa);               \
+    }
+RT_GEMM_XH_PREP1A(1)
+RT_GEMM_XH_PREP1A(2)
+RT_GEMM_XH_PREP1A(4)
 RT_GEMM_XH_PREP(1)
 RT_GEMM_XH_PREP(2)
 RT_GEMM_XH_PREP(4)

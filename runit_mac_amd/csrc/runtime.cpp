@@ -146,7 +146,7 @@ const char* const kKernelNames[] = {
     "k_embed_q8_0_f32", "k_embed_q4_0_f32", "k_embed_q4k_f32", "k_embed_q6k_f32", "k_embed_q5_0_f32", "k_embed_q5k_f32", "k_embed_q4_0g_f32", "k_embed_q4kg_f32", "k_embed_q5kg_f32", "k_embed_q6kg_f32", "k_embed_f16_f32", "k_embed_f32_f32",
     "k_gemm_split_sum", "k_gemm_split_sum_ep", "k_gemm_split_sum_ep3", "k_gemm_split_sum_qkv_rope", "k_gemm_xh_prep1s_mg1",
     "k_gemm_xh_prep1s_mg2", "k_gemm_xh_prep1s_mg4", "k_gemm_xh_prep1sn_mg1", "k_gemm_xh_prep1sn_mg2",
-    "k_gemm_xh_prep1sn_mg4", "k_gemm_xh_prep1n_mg1", "k_gemm_xh_prep1n_mg2",
+    "k_gemm_xh_prep1sn_mg4", "k_gemm_xh_prep1a_mg1", "k_gemm_xh_prep1a_mg2", "k_gemm_xh_prep1a_mg4", "k_gemm_xh_prep1n_mg1", "k_gemm_xh_prep1n_mg2",
     "k_gemm_xh_prep1n_mg4", "k_gemm_xh_prep1_mg1", "k_gemm_xh_prep1_mg2", "k_gemm_xh_prep1_mg4", "k_gemm_x_prep_mg1", "k_gemm_x_prep_mg2", "k_gemm_x_prep_mg4", "k_gemm_x_prep_mg8",
     "k_gemm_q8_0_mg1_ct1", "k_gemm_q8_0_mg2_ct1", "k_gemm_q8_0_mg4_ct1", "k_gemm_q8_0_mg8_ct1",
     "k_gemm_q8_0_mg1_ct2", "k_gemm_q8_0_mg2_ct2", "k_gemm_q8_0_mg4_ct2", "k_gemm_q8_0_mg8_ct2",
@@ -302,6 +302,7 @@ struct rt_ctx {
     uint32_t gemm_bigm_chunks = 2;  // RUNIT_GEMM_BIGM_CHUNKS: activation chunks from which that holds
     bool gemm_set_sum1 = true;  // RUNIT_GEMM_SET_SUM1=0: a set's split sums one launch per matrix (A/B)
     bool gemm_block = true;     // RUNIT_GEMM_BLOCK=0: rt_gemm_ffn_block_f32 as three sets (A/B)
+    bool attn_fold = true;      // RUNIT_ATTN_FOLD=0: rt_gemm_attn_ffn_block_f32 merges in the attention (A/B)
     bool gemm_rope = true;      // RUNIT_GEMM_ROPE=0: rt_gemm_qkv_rope_f32 with a separate RoPE launch (A/B)
     uint32_t gemm_block_silu_min = 64;  // RUNIT_GEMM_BLOCK_SILU_MIN: rows from which the block
                                         // sums the SiLU pair in the down preparation
@@ -1339,6 +1340,7 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_GEMM_BIGM_CHUNKS")) c->gemm_bigm_chunks = std::max(1, atoi(g));
     if (const char* g = getenv("RUNIT_GEMM_SET_SUM1")) c->gemm_set_sum1 = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_BLOCK")) c->gemm_block = atoi(g) != 0;
+    if (const char* g = getenv("RUNIT_ATTN_FOLD")) c->attn_fold = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_ROPE")) c->gemm_rope = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMM_BLOCK_SILU_MIN")) c->gemm_block_silu_min = atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_KSPLIT")) c->ksplit_enabled = atoi(g) != 0;
@@ -2622,11 +2624,24 @@ struct PrepSum {
     uint32_t splits, crow;
 };
 
-int rt_gemm_ffn_block_f32(rt_ctx* c, const char* fmt_o, const void* w_o, const char* fmt_gate,
+// Mirrors the device-side PrepAttn (k_gemm.hip).
+struct PrepAttnHost {
+    const float* part;
+    const float* ml;
+    uint32_t nsp, G, hd, cgs;
+};
+
+// rt_gemm_ffn_block_f32.  plan_only: report in *shared whether the shared
+// form applies, launching nothing; pa: the O projection's input given as
+// multi-query attention partials (merged in its operand preparation) instead
+// of att (shared form only).
+static int ffn_block_impl(rt_ctx* c, const char* fmt_o, const void* w_o, const char* fmt_gate,
                           const void* w_gate, const char* fmt_up, const void* w_up,
                           const char* fmt_down, const void* w_down, const float* att, float* x,
                           float* x_mid, const float* gamma, float eps, float* g, float* u,
-                          float* xn, uint32_t m_rows, uint32_t h, uint32_t qd, uint32_t ff) {
+                          float* xn, uint32_t m_rows, uint32_t h, uint32_t qd, uint32_t ff,
+                          bool plan_only, bool* shared, const PrepAttnHost* pa) {
+    if (shared) *shared = false;
     if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
     if (m_rows == 0) return RT_OK;
     if (!att || !x || !x_mid || !gamma || !g || !u || !xn || x_mid == x)
@@ -2664,7 +2679,7 @@ int rt_gemm_ffn_block_f32(rt_ctx* c, const char* fmt_o, const void* w_o, const c
         m_rows <= c->gemm_set_min || qd > 20480 || h > 20480 || ff > 20480 || !aligned(att, 16) ||
         !aligned(x, 16) || !aligned(x_mid, 16) || !aligned(gamma, 16) ||
         qd % fo->blk_el || h % fg->blk_el || h % fu->blk_el || ff % fd->blk_el)
-        return sets();
+        return plan_only ? RT_OK : sets();
     Gemm3Plan po, pg, pu, pd;
     int st = gemm3_plan(c, *fo, w_o, m_rows, h, qd, po);
     if (st == RT_OK) st = gemm3_plan(c, *fg, w_gate, m_rows, ff, h, pg);
@@ -2672,8 +2687,12 @@ int rt_gemm_ffn_block_f32(rt_ctx* c, const char* fmt_o, const void* w_o, const c
     if (st == RT_OK) st = gemm3_plan(c, *fd, w_down, m_rows, h, ff, pd);
     if (st == kLsDecline || (st == RT_OK && (pg.MG != po.MG || pu.MG != po.MG || pd.MG != po.MG ||
                                              pg.splits != pu.splits)))
-        return sets();
+        return plan_only ? RT_OK : sets();
     if (st != RT_OK) return st;
+    if (plan_only) {
+        if (shared) *shared = true;
+        return RT_OK;
+    }
     // workspace: operands of att (K = qd), of the normalised x_mid (K = h),
     // of the SiLU product (K = ff), then the partial sums of O, gate, up, down
     const uint32_t MG = po.MG, nch = po.nchunks, crow = 8 * MG;
@@ -2703,8 +2722,21 @@ int rt_gemm_ffn_block_f32(rt_ctx* c, const char* fmt_o, const void* w_o, const c
     float* part_g = (float*)at(10);
     float* part_u = (float*)at(11);
     float* part_d = (float*)(ws + off_pd);
-    // O over att, its partials left; x_mid = x + Σ, normalised and prepared
-    st = gemm3_prep(c, po, att, m_rows, qd, at(0), (int*)at(1), (float*)at(2));
+    // O over att (or over the attention partials, merged per row in the
+    // preparation), its partials left; x_mid = x + Σ, normalised and prepared
+    if (pa) {
+        PrepAttnHost pah = *pa;
+        uint32_t Mr = m_rows, Kq = qd;
+        void* aops = at(0);
+        int* erow = (int*)at(1);
+        float* stab = (float*)at(2);
+        char pk0[48];
+        snprintf(pk0, sizeof pk0, "k_gemm_xh_prep1a_mg%u", po.MG);
+        void* pp0[] = {&pah, &Mr, &Kq, &aops, &erow, &stab};
+        st = launch(c, pk0, dim3(po.nchunks * 8 * po.MG), dim3(1024), 0, pp0);
+    } else {
+        st = gemm3_prep(c, po, att, m_rows, qd, at(0), (int*)at(1), (float*)at(2));
+    }
     if (st == RT_OK)
         st = gemm3_run(c, po, w_o, at(0), (int*)at(1), fo->has_min ? (float*)at(2) : nullptr,
                        po.splits == 1 ? part_o : x_mid, part_o, m_rows, h, true);
@@ -2754,6 +2786,16 @@ int rt_gemm_ffn_block_f32(rt_ctx* c, const char* fmt_o, const void* w_o, const c
     if (st != RT_OK) return st;
     return gemm_split_sum_ep(c, part_d, nullptr, x, m_rows, h, pd.splits, crow, nullptr, x_mid);
 }
+
+int rt_gemm_ffn_block_f32(rt_ctx* c, const char* fmt_o, const void* w_o, const char* fmt_gate,
+                          const void* w_gate, const char* fmt_up, const void* w_up,
+                          const char* fmt_down, const void* w_down, const float* att, float* x,
+                          float* x_mid, const float* gamma, float eps, float* g, float* u,
+                          float* xn, uint32_t m_rows, uint32_t h, uint32_t qd, uint32_t ff) {
+    return ffn_block_impl(c, fmt_o, w_o, fmt_gate, w_gate, fmt_up, w_up, fmt_down, w_down, att, x,
+                          x_mid, gamma, eps, g, u, xn, m_rows, h, qd, ff, false, nullptr, nullptr);
+}
+
 
 // ───────────────────────────── dequant ─────────────────────────────
 
@@ -3402,37 +3444,16 @@ int rt_argmax_rows_first_f32(rt_ctx* c, const float* in, uint32_t* result, uint3
     return launch(c, "k_argmax_rows_first_f32", dim3(G, rows), dim3(256), 0, params);
 }
 
-int rt_flash_attention_f32(rt_ctx* c, const float* q, const float* k, const float* v, float* out,
-                           uint32_t batch, uint32_t q_len, uint32_t kv_len, uint32_t num_heads,
-                           uint32_t num_kv_heads, uint32_t head_dim, uint32_t kv_head_stride,
-                           uint32_t q_start) {
-    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
-    if (batch == 0 || q_len == 0 || num_heads == 0) return RT_OK;
-    int st = attn_check(c, num_heads, num_kv_heads, head_dim);
-    if (st != RT_OK) return st;
-    if (!q || !k || !v || !out)
-        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: flash_attention: null buffer");
-    if (kv_len == 0 || kv_len > kv_head_stride)
-        return fail(c, RT_ERR_DISPATCH,
-                    "kernel dispatch error: flash_attention: kv_len=%u (need 1..kv_head_stride=%u)",
-                    kv_len, kv_head_stride);
-    const uint64_t rows = (uint64_t)batch * q_len;
-    if (rows > 65535)
-        return fail(c, RT_ERR_DISPATCH,
-                    "kernel dispatch error: flash_attention: batch·q_len=%llu > 65535",
-                    (unsigned long long)rows);
-    AttnArgs a{};
-    a.q = q;
-    a.kc = const_cast<float*>(k);  // read only without rope
-    a.vc = const_cast<float*>(v);
-    a.out = out;
-    a.kv_len = kv_len;
-    a.stride = kv_head_stride;
-    a.H = num_heads;
-    a.KVH = num_kv_heads;
-    a.scale = 1.0f / sqrtf((float)head_dim);  // dispatch.rs:659
-    a.q_len = q_len;
-    a.q_start = q_start;
+
+// The multi-query attention on the matrix cores (k_attn_mq_f32_hd*): plan and
+// launch; kLsDecline where the per-row kernel is the better one.  in_part:
+// the split partials in the context's second scratch buffer (c->part) instead
+// of the workspace; parts_only: no merge in the launch (declined when the
+// plan has a single key range), the partials' layout returned in *pa.
+static int attn_mq_launch(rt_ctx* c, AttnArgs a, uint32_t batch, uint32_t q_len, uint32_t kv_len,
+                          uint32_t num_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                          uint32_t q_start, bool in_part, bool parts_only,
+                          PrepAttnHost* pa) {
     char kn[64];
     snprintf(kn, sizeof kn, "k_attn_mq_f32_hd%u", head_dim);
     // up to 8 column groups the per-row kernel below (7B at 2 rows: 14.3
@@ -3467,22 +3488,117 @@ int rt_flash_attention_f32(rt_ctx* c, const float* q, const float* k, const floa
         if (cols * nsp > 0x7FFFFFFFull || batch > 65535)
             return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: flash_attention: %llu column "
                         "groups, batch %u", (unsigned long long)cols, batch);
+        if (parts_only && nsp == 1) return kLsDecline;
         if (nsp > 1) {
             if (pairs > kAttnCounters)
                 return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: flash_attention: %llu "
                             "column groups exceed %u", (unsigned long long)pairs, kAttnCounters);
             const size_t parts = (size_t)pairs * nsp * 16;
-            int st = ensure_ws(c, parts * (head_dim + 2) * sizeof(float), kn);
+            const size_t bytes = parts * (head_dim + 2) * sizeof(float);
+            int st = in_part ? ensure_part(c, bytes, kn) : ensure_ws(c, bytes, kn);
             if (st != RT_OK) return st;
-            a.part = (float*)c->ws;
+            a.part = (float*)(in_part ? c->part : c->ws);
             a.ml = a.part + parts * head_dim;
             a.counters = c->counters;
+            a.parts_only = parts_only ? 1u : 0u;
+            if (pa) *pa = PrepAttnHost{a.part, a.ml, nsp, num_heads / num_kv_heads, head_dim,
+                                       (uint32_t)cols};
         }
         a.chunk = chunk;
         void* params[] = {&a};
         return launch(c, kn, dim3((uint32_t)(cols * nsp), num_kv_heads, batch), dim3(64 * w),
                       rt_attn_mq_lds(head_dim, w), params);
     }
+    return kLsDecline;
+}
+
+int rt_gemm_attn_ffn_block_f32(rt_ctx* c, const float* q, const float* k_cache,
+                               const float* v_cache, uint32_t kv_len, uint32_t num_heads,
+                               uint32_t num_kv_heads, uint32_t head_dim, uint32_t kv_head_stride,
+                               uint32_t q_start, float* att, const char* fmt_o, const void* w_o,
+                               const char* fmt_gate, const void* w_gate, const char* fmt_up,
+                               const void* w_up, const char* fmt_down, const void* w_down, float* x,
+                               float* x_mid, const float* gamma, float eps, float* g, float* u,
+                               float* xn, uint32_t m_rows, uint32_t h, uint32_t ff) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (m_rows == 0) return RT_OK;
+    const uint32_t qd = num_heads * head_dim;
+    // the attention's split partials merged in the O projection's operand
+    // preparation, where the FFN block takes its shared form and the
+    // attention its multi-range matrix-core form
+    bool shared = false;
+    int st = RT_OK;
+    if (c->attn_fold && q && k_cache && v_cache && num_kv_heads && num_heads % num_kv_heads == 0 &&
+        kv_len >= 1 && kv_len <= kv_head_stride && aligned(q, 16) &&
+        attn_check(c, num_heads, num_kv_heads, head_dim) == RT_OK) {
+        st = ffn_block_impl(c, fmt_o, w_o, fmt_gate, w_gate, fmt_up, w_up, fmt_down, w_down, att, x,
+                            x_mid, gamma, eps, g, u, xn, m_rows, h, qd, ff, true, &shared, nullptr);
+        if (st != RT_OK) return st;
+    }
+    if (shared) {
+        AttnArgs a{};
+        a.q = q;
+        a.kc = const_cast<float*>(k_cache);
+        a.vc = const_cast<float*>(v_cache);
+        a.out = att;
+        a.kv_len = kv_len;
+        a.stride = kv_head_stride;
+        a.H = num_heads;
+        a.KVH = num_kv_heads;
+        a.scale = 1.0f / sqrtf((float)head_dim);  // dispatch.rs:659
+        a.q_len = m_rows;
+        a.q_start = q_start;
+        PrepAttnHost pa{};
+        st = attn_mq_launch(c, a, 1, m_rows, kv_len, num_heads, num_kv_heads, head_dim, q_start,
+                            true, true, &pa);
+        if (st == RT_OK)
+            return ffn_block_impl(c, fmt_o, w_o, fmt_gate, w_gate, fmt_up, w_up, fmt_down, w_down,
+                                  att, x, x_mid, gamma, eps, g, u, xn, m_rows, h, qd, ff, false,
+                                  nullptr, &pa);
+        if (st != kLsDecline) return st;
+    }
+    st = rt_flash_attention_f32(c, q, k_cache, v_cache, att, 1, m_rows, kv_len, num_heads,
+                                num_kv_heads, head_dim, kv_head_stride, q_start);
+    if (st != RT_OK) return st;
+    return rt_gemm_ffn_block_f32(c, fmt_o, w_o, fmt_gate, w_gate, fmt_up, w_up, fmt_down, w_down,
+                                 att, x, x_mid, gamma, eps, g, u, xn, m_rows, h, qd, ff);
+}
+
+int rt_flash_attention_f32(rt_ctx* c, const float* q, const float* k, const float* v, float* out,
+                           uint32_t batch, uint32_t q_len, uint32_t kv_len, uint32_t num_heads,
+                           uint32_t num_kv_heads, uint32_t head_dim, uint32_t kv_head_stride,
+                           uint32_t q_start) {
+    if (!c) return fail(nullptr, RT_ERR_DISPATCH, "kernel dispatch error: null context");
+    if (batch == 0 || q_len == 0 || num_heads == 0) return RT_OK;
+    int st = attn_check(c, num_heads, num_kv_heads, head_dim);
+    if (st != RT_OK) return st;
+    if (!q || !k || !v || !out)
+        return fail(c, RT_ERR_DISPATCH, "kernel dispatch error: flash_attention: null buffer");
+    if (kv_len == 0 || kv_len > kv_head_stride)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: flash_attention: kv_len=%u (need 1..kv_head_stride=%u)",
+                    kv_len, kv_head_stride);
+    const uint64_t rows = (uint64_t)batch * q_len;
+    if (rows > 65535)
+        return fail(c, RT_ERR_DISPATCH,
+                    "kernel dispatch error: flash_attention: batch·q_len=%llu > 65535",
+                    (unsigned long long)rows);
+    AttnArgs a{};
+    a.q = q;
+    a.kc = const_cast<float*>(k);  // read only without rope
+    a.vc = const_cast<float*>(v);
+    a.out = out;
+    a.kv_len = kv_len;
+    a.stride = kv_head_stride;
+    a.H = num_heads;
+    a.KVH = num_kv_heads;
+    a.scale = 1.0f / sqrtf((float)head_dim);  // dispatch.rs:659
+    a.q_len = q_len;
+    a.q_start = q_start;
+    char kn[64];
+    const int mq = attn_mq_launch(c, a, batch, q_len, kv_len, num_heads, num_kv_heads, head_dim,
+                                  q_start, false, false, nullptr);
+    if (mq != kLsDecline) return mq;
     snprintf(kn, sizeof kn, "k_decode_attention_f32_hd%u", head_dim);
     return attn_launch(c, kn, a, (uint32_t)rows);
 }

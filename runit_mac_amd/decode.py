@@ -635,9 +635,9 @@ class DecodeModel:
                                     L["bq"], L["bk"], L["bv"], X, L["attn_norm"], c.eps, XN,
                                     B["q"], B["k"], B["v"], L["kc"], L["vc"], M, h, qd, kvd, hd,
                                     start_pos, c.theta, c.max_seq)
-            d.flash_attention_f32(ctx, B["q"], L["kc"], L["vc"], B["att"], 1, M, start_pos + M,
-                                  c.heads, c.kv_heads, hd, c.max_seq, q_start=start_pos)
             if form == "rows":
+                d.flash_attention_f32(ctx, B["q"], L["kc"], L["vc"], B["att"], 1, M, start_pos + M,
+                                      c.heads, c.kv_heads, hd, c.max_seq, q_start=start_pos)
                 d.gemv_rows_add_f32(ctx, F["o"], L["wo"], B["att"], X, X, M, h, qd)
                 if F["gate"] != F["up"]:
                     raise ValueError(f"gate {F['gate']} / up {F['up']}: no fused gate+up+SiLU")
@@ -645,12 +645,15 @@ class DecodeModel:
                                      gamma=L["ffn_norm"], eps=c.eps)
                 d.gemv_rows_add_f32(ctx, F["down"], L["wd"], B["g"], X, X, M, h, ff)
             else:
-                # O + residual (into Xo), norm, gate/up + SiLU, down +
-                # residual (back into X): each K-split sum folded into the
-                # next projection's operand preparation
-                d.gemm_ffn_block_f32(ctx, (F["o"], F["gate"], F["up"], F["down"]), L["wo"], L["wg"],
-                                     L["wu"], L["wd"], B["att"], X, Xo, L["ffn_norm"], c.eps,
-                                     B["g"], B["u"], XN, M, h, qd, ff)
+                # the attention, O + residual (into Xo), norm, gate/up + SiLU,
+                # down + residual (back into X): the attention's key-range
+                # partials merged and each K-split sum folded into the next
+                # projection's operand preparation
+                d.gemm_attn_ffn_block_f32(ctx, B["q"], L["kc"], L["vc"], start_pos + M, c.heads,
+                                          c.kv_heads, hd, c.max_seq, start_pos, B["att"],
+                                          (F["o"], F["gate"], F["up"], F["down"]), L["wo"],
+                                          L["wg"], L["wu"], L["wd"], X, Xo, L["ffn_norm"], c.eps,
+                                          B["g"], B["u"], XN, M, h, ff)
         if last_only:
             # prefill: the final norm and the LM head on the last row only, into
             # the decode buffers (logits, token = its argmax) so that decoding

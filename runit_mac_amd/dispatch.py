@@ -71,6 +71,9 @@ _SIGS = {
                              _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F, _U32],
     "rt_gemm_ffn_block_f32": [_P, c_char_p, _P, c_char_p, _P, c_char_p, _P, c_char_p, _P, _P, _P,
                               _P, _P, _F, _P, _P, _P, _U32, _U32, _U32, _U32],
+    "rt_gemm_attn_ffn_block_f32": [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _P,
+                                   c_char_p, _P, c_char_p, _P, c_char_p, _P, c_char_p, _P, _P, _P,
+                                   _P, _F, _P, _P, _P, _U32, _U32, _U32],
     "rt_flush": [_P],
     "rt_device_cu_count": [_P],
     "rt_has_kernel": [_P, c_char_p],
@@ -650,6 +653,18 @@ def gemm_ffn_block_f32(ctx, fmts, w_o, w_gate, w_up, w_down, att, x, x_mid, gamm
     _call(ctx, "rt_gemm_ffn_block_f32", fo, _ptr(w_o), fg, _ptr(w_gate), fu, _ptr(w_up), fd,
           _ptr(w_down), _ptr(att), _ptr(x), _ptr(x_mid), _ptr(gamma), eps, _ptr(g), _ptr(u),
           _ptr(xn), m_rows, h, qd, ff)
+
+
+def gemm_attn_ffn_block_f32(ctx, q, k_cache, v_cache, kv_len, num_heads, num_kv_heads, head_dim,
+                            kv_head_stride, q_start, att, fmts, w_o, w_gate, w_up, w_down, x, x_mid,
+                            gamma, eps, g, u, xn, m_rows, h, ff):
+    """flash_attention_f32 (batch 1, q_len = m_rows) then gemm_ffn_block_f32
+    over its output as one call (new; forward.rs:2225-2271)."""
+    fo, fg, fu, fd = (f.encode() for f in fmts)
+    _call(ctx, "rt_gemm_attn_ffn_block_f32", _ptr(q), _ptr(k_cache), _ptr(v_cache), kv_len,
+          num_heads, num_kv_heads, head_dim, kv_head_stride, q_start, _ptr(att), fo, _ptr(w_o), fg,
+          _ptr(w_gate), fu, _ptr(w_up), fd, _ptr(w_down), _ptr(x), _ptr(x_mid), _ptr(gamma), eps,
+          _ptr(g), _ptr(u), _ptr(xn), m_rows, h, ff)
 
 
 def gemm_q8_0_f32(ctx, weight, x, y, m_rows, n, k):

@@ -195,3 +195,48 @@ def test_gemm_set_unaligned_operands_take_the_separate_launches(ctx):
         ctx.flush()
         outs.append(y.read(np.float32, m * n))
     assert np.max(np.abs(outs[0] - outs[1])) <= 1e-5 * np.abs(outs[1]).max()
+
+
+@pytest.mark.parametrize("fmts", [("q4k", "q4k", "q4k", "q6k"), ("q8_0", "q8_0", "q8_0", "q8_0")])
+@pytest.mark.parametrize("hd,heads,kvh", [(128, 8, 2), (64, 16, 2)])
+@pytest.mark.parametrize("m,start", [(8, 40), (27, 200), (32, 0), (70, 200)])
+def test_gemm_attn_ffn_block_equals_attention_then_block(ctx, fmts, hd, heads, kvh, m, start):
+    """rt_gemm_attn_ffn_block_f32 against rt_flash_attention_f32 then
+    rt_gemm_ffn_block_f32 (both pinned above and in the attention tests).
+    27 / 70 rows after 200 cached positions take the folded form (the
+    attention's key-range partials merged in the O preparation, 3-4 ranges);
+    8 rows and 32 rows from position 0 the two calls.  The merge adds the
+    same terms as the attention's last workgroup, up to the rounding of the
+    division: x within 1e-5 of its largest magnitude."""
+    h, qd, ff, max_seq = 1024, heads * hd, 2048, 512
+    fo, fg, fu, fd = fmts
+    wo, _ = device_weights(ctx, fo, h, qd, 350)
+    wg, _ = device_weights(ctx, fg, ff, h, 351)
+    wu, _ = device_weights(ctx, fu, ff, h, 352)
+    wd, _ = device_weights(ctx, fd, h, ff, 353)
+    rng = np.random.default_rng(90 + m)
+    q = ctx.buffer_from(rng.standard_normal((m, qd)).astype(np.float32))
+    kc = ctx.buffer_from(rng.standard_normal((kvh, max_seq, hd)).astype(np.float32))
+    vc = ctx.buffer_from(rng.standard_normal((kvh, max_seq, hd)).astype(np.float32))
+    x0 = _x(m, h, 95 + m)
+    gamma = ctx.buffer_from(np.linspace(0.5, 1.5, h, dtype=np.float32))
+    outs = []
+    for fused in (True, False):
+        att = ctx.new_buffer(4 * m * qd)
+        x, xm = ctx.buffer_from(x0), ctx.new_buffer(4 * m * h)
+        g, u, xn = ctx.new_buffer(4 * m * ff), ctx.new_buffer(4 * m * ff), ctx.new_buffer(4 * m * h)
+        if fused:
+            d.gemm_attn_ffn_block_f32(ctx, q, kc, vc, start + m, heads, kvh, hd, max_seq, start,
+                                      att, fmts, wo, wg, wu, wd, x, xm, gamma, EPS, g, u, xn,
+                                      m, h, ff)
+        else:
+            d.flash_attention_f32(ctx, q, kc, vc, att, 1, m, start + m, heads, kvh, hd, max_seq,
+                                  q_start=start)
+            d.gemm_ffn_block_f32(ctx, fmts, wo, wg, wu, wd, att, x, xm, gamma, EPS, g, u, xn,
+                                 m, h, qd, ff)
+        ctx.flush()
+        outs.append((xm.read(np.float32, m * h), x.read(np.float32, m * h)))
+    for i, name in enumerate(("x_mid", "x")):
+        a, b = outs[0][i], outs[1][i]
+        assert np.all(np.isfinite(a)), name
+        assert np.max(np.abs(a - b)) <= 1e-5 * np.abs(b).max(), name
