@@ -311,6 +311,9 @@ struct rt_ctx {
     bool attn_w = true;          // RUNIT_ATTN_W=0: the token's RoPE attention on attn_split (A/B)
     bool attn_mq = true;         // RUNIT_ATTN_MQ=0: multi-query attention on attn_split per row (A/B)
     uint32_t attn_mq_nsp = 0, attn_mq_w = 0;  // probe: forced ranges / waves (0: planned)
+    // RUNIT_ATTN_MQ_MIN / _FOLD_MIN: column-group pairs up to which the
+    // per-row kernel runs (rt_flash_attention_f32 / rt_gemm_attn_ffn_block_f32)
+    uint32_t attn_mq_min = 8, attn_mq_fold_min = 0;
     uint32_t gemm_f16_min = 4;   // RUNIT_GEMM_F16_MIN: batches above this many rows run the f16 form
     uint32_t gemm_f16_min_q6 = 1;  // RUNIT_GEMM_F16_MIN_Q6: the same for Q6_K
     bool lsk_whole = true;       // RUNIT_GEMV_LSK_WHOLE=0: whole-K launches off the K-split body (A/B)
@@ -1354,6 +1357,8 @@ int rt_ctx_create(rt_ctx** out, const char* code_object_path) {
     if (const char* g = getenv("RUNIT_ATTN_W")) c->attn_w = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_ATTN_MQ")) c->attn_mq = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_ATTN_MQ_NSP")) c->attn_mq_nsp = atoi(g);
+    if (const char* g = getenv("RUNIT_ATTN_MQ_MIN")) c->attn_mq_min = atoi(g);
+    if (const char* g = getenv("RUNIT_ATTN_MQ_FOLD_MIN")) c->attn_mq_fold_min = atoi(g);
     if (const char* g = getenv("RUNIT_ATTN_MQ_W")) c->attn_mq_w = atoi(g);
     if (const char* g = getenv("RUNIT_GEMV_VS")) c->vs_enabled = atoi(g) != 0;
     if (const char* g = getenv("RUNIT_GEMV_VS_MAXQ")) c->vs_max_q = (uint32_t)atoi(g);
@@ -3452,14 +3457,17 @@ int rt_argmax_rows_first_f32(rt_ctx* c, const float* in, uint32_t* result, uint3
 // plan has a single key range), the partials' layout returned in *pa.
 static int attn_mq_launch(rt_ctx* c, AttnArgs a, uint32_t batch, uint32_t q_len, uint32_t kv_len,
                           uint32_t num_heads, uint32_t num_kv_heads, uint32_t head_dim,
-                          uint32_t q_start, bool in_part, bool parts_only,
+                          uint32_t q_start, uint32_t min_pairs, bool in_part, bool parts_only,
                           PrepAttnHost* pa) {
     char kn[64];
     snprintf(kn, sizeof kn, "k_attn_mq_f32_hd%u", head_dim);
-    // up to 8 column groups the per-row kernel below (7B at 2 rows: 14.3
-    // against 10.2 µs, 0.5B at 4 rows 9.5 against 8.9; at 8 groups even)
+    // up to min_pairs column groups the per-row kernel below.  Alone
+    // (rt_flash_attention_f32) up to 8 (7B at 2 rows: 14.3 against 10.2 µs,
+    // 0.5B at 4 rows 9.5 against 8.9; at 8 groups even); with the range
+    // merge in the O preparation none (0.5B at 8 rows 1583 -> 1521 µs per
+    // verify pass, 7B at 4 rows 3510 -> 3418 µs)
     const uint64_t mq_pairs = ((uint64_t)q_len * (num_heads / num_kv_heads) + 15) / 16 * num_kv_heads * batch;
-    if (c->attn_mq && c->fns.count(kn) && mq_pairs > 8) {
+    if (c->attn_mq && c->fns.count(kn) && mq_pairs > min_pairs) {
         // workgroups of 16 (row, head) columns per KV head and range of key
         // tiles.  Fewer than 256 column groups (verify): the key range split
         // so that the grid holds about 1024 waves of 4 per range, ranges of
@@ -3550,7 +3558,7 @@ int rt_gemm_attn_ffn_block_f32(rt_ctx* c, const float* q, const float* k_cache,
         a.q_start = q_start;
         PrepAttnHost pa{};
         st = attn_mq_launch(c, a, 1, m_rows, kv_len, num_heads, num_kv_heads, head_dim, q_start,
-                            true, true, &pa);
+                            c->attn_mq_fold_min, true, true, &pa);
         if (st == RT_OK)
             return ffn_block_impl(c, fmt_o, w_o, fmt_gate, w_gate, fmt_up, w_up, fmt_down, w_down,
                                   att, x, x_mid, gamma, eps, g, u, xn, m_rows, h, qd, ff, false,
@@ -3597,7 +3605,7 @@ int rt_flash_attention_f32(rt_ctx* c, const float* q, const float* k, const floa
     a.q_start = q_start;
     char kn[64];
     const int mq = attn_mq_launch(c, a, batch, q_len, kv_len, num_heads, num_kv_heads, head_dim,
-                                  q_start, false, false, nullptr);
+                                  q_start, c->attn_mq_min, false, false, nullptr);
     if (mq != kLsDecline) return mq;
     snprintf(kn, sizeof kn, "k_decode_attention_f32_hd%u", head_dim);
     return attn_launch(c, kn, a, (uint32_t)rows);

@@ -199,13 +199,14 @@ def test_gemm_set_unaligned_operands_take_the_separate_launches(ctx):
 
 @pytest.mark.parametrize("fmts", [("q4k", "q4k", "q4k", "q6k"), ("q8_0", "q8_0", "q8_0", "q8_0")])
 @pytest.mark.parametrize("hd,heads,kvh", [(128, 8, 2), (64, 16, 2)])
-@pytest.mark.parametrize("m,start", [(8, 40), (27, 200), (32, 0), (70, 200)])
+@pytest.mark.parametrize("m,start", [(4, 300), (8, 40), (8, 300), (27, 200), (32, 0), (70, 200)])
 def test_gemm_attn_ffn_block_equals_attention_then_block(ctx, fmts, hd, heads, kvh, m, start):
     """rt_gemm_attn_ffn_block_f32 against rt_flash_attention_f32 then
     rt_gemm_ffn_block_f32 (both pinned above and in the attention tests).
-    27 / 70 rows after 200 cached positions take the folded form (the
-    attention's key-range partials merged in the O preparation, 3-4 ranges);
-    8 rows and 32 rows from position 0 the two calls.  The merge adds the
+    8 rows after 300 cached positions and 27 / 70 rows after 200 take the
+    folded form (the attention's key-range partials merged in the O
+    preparation, 3-8 ranges); 8 rows after 40 and 32 rows from position 0
+    (one key range) and 4 rows (int8 form of Q4_K) the two calls.  The merge adds the
     same terms as the attention's last workgroup, up to the rounding of the
     division: x within 1e-5 of its largest magnitude."""
     h, qd, ff, max_seq = 1024, heads * hd, 2048, 512
